@@ -1,0 +1,254 @@
+/*
+ * lq_api.h -- C ABI of the MI355X (gfx950) int8 quantized-inference backend.
+ *
+ * Every entry point is `extern "C"`, takes plain pointers and sizes, returns an
+ * int status (LQ_OK == 0, negative on error; the message is in lq_last_error(),
+ * thread-local) and never throws.  Compute entry points are asynchronous on the
+ * HIP stream passed as `void* stream` (NULL = the null stream).  Device pointers
+ * are marked `d_`; the caller owns every buffer.  Entry points that need
+ * scratch memory take an explicit workspace whose size comes from the matching
+ * `*_workspace_size` query.
+ *
+ * Reference seams this ABI replaces (paths relative to lucid-official/lucid):
+ *   - the pybind op seam `_C_engine.quantized.{quantize,dequantize,quantized_matmul}`
+ *     lucid/_C/bindings/bind_quantized.cpp:17-27, lucid/_C/engine.pyi:741-748,
+ *     implemented by lucid/_C/ops/quantized/QuantizedMatmul.cpp:111-207;
+ *   - the CPU backend calls the sidecar modules bottom out in
+ *     (lucid/_C/backend/IBackend.h:228 via Dispatcher::for_device,
+ *     lucid/_C/backend/Dispatcher.h:101-140): min/max reductions
+ *     (backend/cpu/Reduce.cpp:54-135), round/clip/mul/add elementwise passes
+ *     (methods/Unary.cpp:143-147, methods/Binary.cpp:24-104,481-523), the saturating
+ *     float->int cast (methods/Factory.cpp:103-146), `linear` = sgemm + bias
+ *     (methods/Matmul.cpp:80-122) and conv = im2col + sgemm (methods/Conv.cpp:271-360).
+ *
+ * Arithmetic contract (float32, no FMA contraction, round-half-to-even):
+ *   quantize     c = satcast(clip(rne(fl32(x * inv)) + z, qmin, qmax))
+ *   dequantize   y = fl32(fl32(float(c) - z) * s)
+ *   fake-quant   y = fl32(fl32(clip(rne(fl32(x * inv)) + z, qmin, qmax) - z) * s)
+ *   inv          = fl32(1.0f / s) when s comes from device memory (a tensor scale),
+ *                  or the caller-supplied value (fl32(1.0 / double(s)) for a host scalar).
+ *   following lucid/quantization/_functional.py:59-69,195-197,293,326-328.
+ */
+#ifndef LQ_API_H
+#define LQ_API_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LQ_ABI_VERSION 1
+
+/* ---- status codes -------------------------------------------------------- */
+enum {
+    LQ_OK = 0,
+    LQ_ERR_INVALID = -1,     /* bad argument (shape, dtype, NULL pointer, alignment) */
+    LQ_ERR_HIP = -2,         /* a HIP runtime call failed */
+    LQ_ERR_UNSUPPORTED = -3, /* valid request this build does not implement */
+    LQ_ERR_NOMEM = -4        /* device allocation failed */
+};
+
+/* ---- element types of code / output buffers ------------------------------ */
+enum {
+    LQ_I8 = 1,    /* int8 codes (qint8 / qint4 grids) */
+    LQ_U8 = 2,    /* uint8 codes */
+    LQ_I16 = 3,   /* int16 codes (Lucid stores quint8 as int16, _qscheme.py:243) */
+    LQ_I32 = 4,   /* int32 (accumulators) */
+    LQ_F16 = 5,   /* IEEE half */
+    LQ_F32 = 6,   /* IEEE single */
+    LQ_U8S8 = 7   /* an unsigned-grid code c stored as int8 (c - 128): MFMA operand form */
+};
+
+/* ---- runtime -------------------------------------------------------------- */
+/* Version of this ABI (LQ_ABI_VERSION).  No reference counterpart. */
+int lq_abi_version(void);
+/* Message of the last failed call on this thread ("" if none). */
+const char* lq_last_error(void);
+/* Name of the backend ("hip-gfx950"); replaces the backend registration of
+ * lucid/_C/backend/BackendInit.cpp:25-38. */
+const char* lq_backend_name(void);
+/* Number of visible HIP devices (0 when no GPU is present; not an error). */
+int lq_device_count(int* count);
+int lq_set_device(int device);
+int lq_get_device(int* device);
+/* Device allocations come from a per-device caching allocator: lq_free returns
+ * the block to the cache (no implicit device synchronisation).  lq_empty_cache
+ * releases cached blocks back to HIP.  Stands in for the engine allocator
+ * (lucid/_C/core/Allocator.h) for device storage. */
+int lq_malloc(void** d_ptr, size_t bytes);
+int lq_free(void* d_ptr);
+int lq_empty_cache(void);
+/* Bytes currently handed out / held in the cache by the allocator. */
+int lq_memory_stats(size_t* allocated, size_t* cached);
+int lq_memcpy_h2d(void* d_dst, const void* h_src, size_t bytes, void* stream);
+int lq_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes, void* stream);
+int lq_memcpy_d2d(void* d_dst, const void* d_src, size_t bytes, void* stream);
+/* Fill `count` 32-bit words with `value` using a kernel (graph-capture safe). */
+int lq_fill_u32(void* d_dst, uint32_t value, size_t count, void* stream);
+int lq_stream_create(void** stream);
+int lq_stream_destroy(void* stream);
+int lq_stream_synchronize(void* stream);
+int lq_device_synchronize(void);
+int lq_event_create(void** event);
+int lq_event_destroy(void* event);
+int lq_event_record(void* event, void* stream);
+int lq_event_synchronize(void* event);
+int lq_event_elapsed_ms(float* ms, void* start, void* stop);
+
+/* ---- observers ------------------------------------------------------------ */
+/* Observer update modes. */
+enum {
+    LQ_OBS_MINMAX = 0, /* running = minimum(running, batch) (MinMaxObserver, observer.py:408-414) */
+    LQ_OBS_EMA = 1,    /* running = isinf(running_min) ? batch : running + c*(batch - running)
+                          (MovingAverageMinMaxObserver, observer.py:527-544) */
+    LQ_OBS_REPLACE = 2 /* running = batch (plain x.min()/x.max(), dynamic/linear.py:87) */
+};
+
+/* Per-tensor min/max of x[n] (NaN-propagating, -0 < +0, Reduce.cpp:54-105),
+ * folded into the running 0-d buffers d_running_min / d_running_max by `mode`.  `ema_c` is the float32
+ * averaging constant (LQ_OBS_EMA only).  n == 0 leaves the batch extrema at
+ * {+inf, -inf}.  Two launches; workspace from lq_minmax_workspace_size. */
+size_t lq_minmax_workspace_size(int64_t n);
+int lq_minmax_f32(const float* d_x, int64_t n, float* d_running_min, float* d_running_max,
+                  int mode, float ema_c, void* d_workspace, size_t workspace_bytes, void* stream);
+
+/* Per-channel min/max of x viewed as [outer, C, inner] (channel axis in the
+ * middle; PerChannelMinMaxObserver moveaxis+reshape+amin/amax, observer.py:672-685),
+ * folded into d_running_min[C] / d_running_max[C] by `mode`.  For LQ_OBS_EMA the
+ * seed test is "all of running_min is inf" (observer.py:1039-1044). */
+size_t lq_minmax_per_channel_workspace_size(int64_t outer, int64_t C, int64_t inner);
+int lq_minmax_per_channel_f32(const float* d_x, int64_t outer, int64_t C, int64_t inner,
+                              float* d_running_min, float* d_running_max, int mode,
+                              float ema_c, void* d_workspace, size_t workspace_bytes,
+                              void* stream);
+
+/* calculate_qparams (lucid/quantization/_qparams.py:186-205) over n ranges:
+ * scale[i], zero_point[i] from min[i], max[i].  symmetric != 0 selects the
+ * symmetric branch; is_signed picks its zero point (0 or (qmax+qmin+1)//2). */
+int lq_calc_qparams_f32(const float* d_min, const float* d_max, int64_t n, int symmetric,
+                        int is_signed, int qmin, int qmax, float eps, float* d_scale,
+                        float* d_zero_point, void* stream);
+
+/* ---- quantize / dequantize / fake-quantize --------------------------------- */
+/* Per-tensor quantize of x[n] to codes q[n] of type q_dtype (LQ_I8, LQ_U8,
+ * LQ_I16, LQ_I32 or LQ_U8S8).  Scale: if d_scale != NULL the kernel uses
+ * inv = fl32(1.0f / d_scale[0]); else inv = inv_scale_value.  Zero point:
+ * d_zero_point[0] if non-NULL, else zero_point_value.
+ * Replaces quantize(..., ch_axis=None), _functional.py:179-197. */
+int lq_quantize_per_tensor_f32(const float* d_x, void* d_q, int64_t n, int q_dtype,
+                               const float* d_scale, const float* d_zero_point,
+                               float inv_scale_value, float zero_point_value, int qmin,
+                               int qmax, void* stream);
+/* Per-channel quantize, x viewed as [outer, C, inner]; inv = fl32(1.0f/scale[c]),
+ * zero point d_zero_point[c] (or zero_point_value if NULL).
+ * Replaces quantize(..., ch_axis=k) with _reshape_for_channel, _functional.py:47-56,190-197. */
+int lq_quantize_per_channel_f32(const float* d_x, void* d_q, int64_t outer, int64_t C,
+                                int64_t inner, int q_dtype, const float* d_scale,
+                                const float* d_zero_point, float zero_point_value, int qmin,
+                                int qmax, void* stream);
+/* Per-tensor dequantize of codes q[n] (q_dtype LQ_I8/LQ_U8/LQ_I16/LQ_I32/LQ_U8S8)
+ * to y[n] of y_dtype LQ_F32 or LQ_F16 (fl16 of the float32 result).
+ * s = d_scale[0] or scale_value; z = d_zero_point[0] or zero_point_value.
+ * Replaces dequantize(..., ch_axis=None), _functional.py:281-293. */
+int lq_dequantize_per_tensor(const void* d_q, int q_dtype, void* d_y, int y_dtype, int64_t n,
+                             const float* d_scale, const float* d_zero_point, float scale_value,
+                             float zero_point_value, void* stream);
+/* Per-channel dequantize ([outer, C, inner]); replaces dequantize(..., ch_axis=k). */
+int lq_dequantize_per_channel(const void* d_q, int q_dtype, void* d_y, int y_dtype,
+                              int64_t outer, int64_t C, int64_t inner, const float* d_scale,
+                              const float* d_zero_point, float zero_point_value, void* stream);
+/* Per-tensor fake-quantize forward (_FakeQuantizeAffine.forward, _functional.py:314-333):
+ * y = fl32(fl32(clip(rne(fl32(x*inv)) + z) - z) * s).  With d_scale == NULL the
+ * caller passes both inv_scale_value and scale_value.  d_mask (may be NULL)
+ * receives the straight-through mask as float 1/0 (_functional.py:330-332). */
+int lq_fake_quantize_per_tensor_f32(const float* d_x, float* d_y, int64_t n,
+                                    const float* d_scale, const float* d_zero_point,
+                                    float inv_scale_value, float scale_value,
+                                    float zero_point_value, int qmin, int qmax, float* d_mask,
+                                    void* stream);
+/* Per-channel fake-quantize ([outer, C, inner]). */
+int lq_fake_quantize_per_channel_f32(const float* d_x, float* d_y, int64_t outer, int64_t C,
+                                     int64_t inner, const float* d_scale,
+                                     const float* d_zero_point, float zero_point_value, int qmin,
+                                     int qmax, float* d_mask, void* stream);
+
+/* ---- W8A8 int8 GEMM with fused requantize epilogue -------------------------- */
+/* Epilogue output kinds of lq_gemm_w8a8. */
+enum {
+    LQ_OUT_I32 = 0,  /* raw int32 accumulator */
+    LQ_OUT_F32 = 1,  /* y */
+    LQ_OUT_F16 = 2,  /* fl16(y) */
+    LQ_OUT_Q8 = 3,   /* codes of y on the output grid, stored int8 (signed grid) */
+    LQ_OUT_QU8 = 4,  /* codes of y on the output grid, stored uint8 (unsigned grid) */
+    LQ_OUT_FQ32 = 5, /* fake-quantized y on the output grid, float32 (the sidecar module output) */
+    LQ_OUT_Q16 = 6   /* codes of y on the output grid, stored int16 (Lucid quint8 storage) */
+};
+/* Epilogue flag bits. */
+enum { LQ_EPI_RELU = 1 };
+
+/* C[m,n] epilogue of acc[m,n] = sum_k (A[m,k] - za) * (B[n,k] - zb[n])  (exact int32),
+ * A int8 [M,K] row-major (lda), B int8 [N,K] row-major (ldb; Lucid's weight_int8 [out,in]).
+ *   s  = fl32(a_scale[m * a_scale_stride] * b_scale[n * b_scale_stride])
+ *   y  = fl32(float(acc) * s); y = fl32(y + bias[n]) (bias may be NULL); ReLU if flagged
+ *        (y <= 0 -> +0, NaN passes; Vdsp.cpp vrelu_f32);
+ *   out by out_kind, requantized with inv = fl32(1.0f / out_scale[0]), z = out_zp[0].
+ * za = d_a_zero_point[0] (integer-valued float, NULL = 0); zb = d_b_zero_point[n] (NULL = 0).
+ * Replaces the nnq.Linear / nnqd.Linear compute: dequantize(W) -> F.linear -> act ->
+ * fake_quantize (lucid/nn/quantized/linear.py:206-215, dynamic/linear.py:85-92,
+ * Linear.cpp:199 -> Matmul.cpp:80-122).  Workspace holds the row/column code sums
+ * for the zero-point correction (lq_gemm_w8a8_workspace_size). */
+size_t lq_gemm_w8a8_workspace_size(int64_t M, int64_t N, int64_t K);
+int lq_gemm_w8a8(const int8_t* d_A, int64_t lda, const int8_t* d_B, int64_t ldb, void* d_C,
+                 int64_t ldc, int64_t M, int64_t N, int64_t K, const float* d_a_scale,
+                 int64_t a_scale_stride, const float* d_b_scale, int64_t b_scale_stride,
+                 const float* d_a_zero_point, const float* d_b_zero_point, const float* d_bias,
+                 const float* d_out_scale, const float* d_out_zero_point, int out_qmin,
+                 int out_qmax, int out_kind, int flags, void* d_workspace,
+                 size_t workspace_bytes, void* stream);
+
+/* ---- weight-only int8 GEMV / skinny GEMM (M <= 64) ----------------------------- */
+/* y[m,n] = sum_k x[m,k] * w_hat[n,k] + bias[n], w_hat = fl32(fl32(W[n,k] - zb[n]) * sb[n]),
+ * x / y of x_dtype (LQ_F32 or LQ_F16, accumulation in float32).  W int8 [N,K] row-major.
+ * The dequantize-then-linear of the sidecar Linear with a float input
+ * (linear.py:206-210) evaluated without materialising w_hat. */
+int lq_gemv_w8(const void* d_x, int x_dtype, int64_t ldx, const int8_t* d_W, int64_t ldw,
+               const float* d_w_scale, const float* d_w_zero_point, const float* d_bias,
+               void* d_y, int64_t ldy, int64_t M, int64_t N, int64_t K, int flags, void* stream);
+
+/* ---- group-wise packed weights (QuantizedLinearMLX layout) ------------------------ */
+/* Group-wise affine quantize of W[N,K] (float32) with groups of `group_size` along K:
+ * s_g = (max_g - min_g) / (2^bits - 1), b_g = min_g, c = clip(rne((w - b_g) / s_g), 0, 2^bits-1),
+ * 32/bits codes per uint32 little-end first.  packed [N, K*bits/32] uint32,
+ * scales/biases [N, K/group_size] float32.  Replaces quantize_op
+ * (QuantizedMatmul.cpp:111-121, formula _qgemm.py:84-97). */
+int lq_group_quantize_f32(const float* d_w, int64_t N, int64_t K, int group_size, int bits,
+                          uint32_t* d_packed, float* d_scales, float* d_biases, void* stream);
+/* w_hat = fl32(fl32(c * s_g) + b_g) as float32 [N, K]; replaces dequantize_op
+ * (QuantizedMatmul.cpp:123-141, _qgemm.py:167-170).  d_biases may be NULL (b_g = 0). */
+int lq_group_dequantize_f32(const uint32_t* d_packed, const float* d_scales,
+                            const float* d_biases, int64_t N, int64_t K, int group_size,
+                            int bits, float* d_w, void* stream);
+/* y[m,n] = sum_k x[m,k] * w_hat[n,k] (+ bias[n]) with x/y of x_dtype (LQ_F32/LQ_F16);
+ * replaces quantized_matmul_op with transpose=true (QuantizedMatmul.cpp:143-163). */
+int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d_packed,
+                    const float* d_scales, const float* d_biases, const float* d_bias, void* d_y,
+                    int64_t ldy, int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                    int flags, void* stream);
+
+/* ---- float helpers around the quantized path ----------------------------------- */
+/* y = (x <= 0) ? +0 : x, NaN passes (the CPU relu of backend/cpu/Vdsp.cpp vrelu_f32,
+ * reached from nn.ReLU between quantized layers). */
+int lq_relu_f32(const float* d_x, float* d_y, int64_t n, void* stream);
+/* Float Linear y[M,N] = x[M,K] W[N,K]^T + bias (linear_op, lucid/_C/nn/Linear.cpp:199 ->
+ * backend/cpu/methods/Matmul.cpp:80-122); runs the float model during calibration. */
+int lq_linear_f32(const float* d_x, int64_t ldx, const float* d_w, int64_t ldw,
+                  const float* d_bias, float* d_y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                  void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* LQ_API_H */

@@ -1,0 +1,148 @@
+"""ctypes binding of the HIP backend library (``include/lq_api.h``).
+
+This is the thin shim between Lucid's Python op/module surface and the gfx950
+kernels, in the place of Lucid's pybind seam ``_C_engine.quantized``
+(lucid/_C/bindings/bind_quantized.cpp:17-27).  Loading fails loudly: there is
+no CPU fallback, so a missing or unloadable ``liblucid_amd.so`` raises
+:class:`BackendUnavailable` and a device call without a GPU raises
+:class:`LucidError`.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "_lib", "liblucid_amd.so")
+
+# Status and type codes of include/lq_api.h.
+OK = 0
+I8, U8, I16, I32, F16, F32, U8S8 = 1, 2, 3, 4, 5, 6, 7
+OBS_MINMAX, OBS_EMA, OBS_REPLACE = 0, 1, 2
+OUT_I32, OUT_F32, OUT_F16, OUT_Q8, OUT_QU8, OUT_FQ32, OUT_Q16 = 0, 1, 2, 3, 4, 5, 6
+EPI_RELU = 1
+
+
+class LucidError(RuntimeError):
+    """Error raised by the backend (the role of Lucid's ``LucidError``, bind_errors.cpp:6-71)."""
+
+
+class BackendUnavailable(LucidError):
+    """The HIP backend library is missing or cannot be loaded."""
+
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+_I = ctypes.c_int
+_SZ = ctypes.c_size_t
+
+# name -> (restype, argtypes)
+_SIGNATURES: dict[str, tuple] = {
+    "lq_abi_version": (_I, []),
+    "lq_last_error": (ctypes.c_char_p, []),
+    "lq_backend_name": (ctypes.c_char_p, []),
+    "lq_device_count": (_I, [ctypes.POINTER(_I)]),
+    "lq_set_device": (_I, [_I]),
+    "lq_get_device": (_I, [ctypes.POINTER(_I)]),
+    "lq_malloc": (_I, [ctypes.POINTER(_P), _SZ]),
+    "lq_free": (_I, [_P]),
+    "lq_empty_cache": (_I, []),
+    "lq_memory_stats": (_I, [ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
+    "lq_memcpy_h2d": (_I, [_P, _P, _SZ, _P]),
+    "lq_memcpy_d2h": (_I, [_P, _P, _SZ, _P]),
+    "lq_memcpy_d2d": (_I, [_P, _P, _SZ, _P]),
+    "lq_fill_u32": (_I, [_P, ctypes.c_uint32, _SZ, _P]),
+    "lq_stream_create": (_I, [ctypes.POINTER(_P)]),
+    "lq_stream_destroy": (_I, [_P]),
+    "lq_stream_synchronize": (_I, [_P]),
+    "lq_device_synchronize": (_I, []),
+    "lq_event_create": (_I, [ctypes.POINTER(_P)]),
+    "lq_event_destroy": (_I, [_P]),
+    "lq_event_record": (_I, [_P, _P]),
+    "lq_event_synchronize": (_I, [_P]),
+    "lq_event_elapsed_ms": (_I, [ctypes.POINTER(_F), _P, _P]),
+    "lq_minmax_workspace_size": (_SZ, [_I64]),
+    "lq_minmax_f32": (_I, [_P, _I64, _P, _P, _I, _F, _P, _SZ, _P]),
+    "lq_minmax_per_channel_workspace_size": (_SZ, [_I64, _I64, _I64]),
+    "lq_minmax_per_channel_f32": (_I, [_P, _I64, _I64, _I64, _P, _P, _I, _F, _P, _SZ, _P]),
+    "lq_calc_qparams_f32": (_I, [_P, _P, _I64, _I, _I, _I, _I, _F, _P, _P, _P]),
+    "lq_quantize_per_tensor_f32": (_I, [_P, _P, _I64, _I, _P, _P, _F, _F, _I, _I, _P]),
+    "lq_quantize_per_channel_f32": (_I, [_P, _P, _I64, _I64, _I64, _I, _P, _P, _F, _I, _I, _P]),
+    "lq_dequantize_per_tensor": (_I, [_P, _I, _P, _I, _I64, _P, _P, _F, _F, _P]),
+    "lq_dequantize_per_channel": (_I, [_P, _I, _P, _I, _I64, _I64, _I64, _P, _P, _F, _P]),
+    "lq_fake_quantize_per_tensor_f32": (_I, [_P, _P, _I64, _P, _P, _F, _F, _F, _I, _I, _P, _P]),
+    "lq_fake_quantize_per_channel_f32": (_I, [_P, _P, _I64, _I64, _I64, _P, _P, _F, _I, _I, _P, _P]),
+}
+
+_lib = None
+_lib_lock = threading.Lock()
+
+
+def _declare(L: ctypes.CDLL, sigs: dict[str, tuple]) -> None:
+    for name, (res, args) in sigs.items():
+        fn = getattr(L, name, None)
+        if fn is None:
+            raise BackendUnavailable(f"{LIB_PATH} does not export {name}")
+        fn.restype = res
+        fn.argtypes = args
+
+
+def register_signatures(sigs: dict[str, tuple]) -> None:
+    """Add entry points declared by another module (kept beside their wrappers)."""
+    _SIGNATURES.update(sigs)
+    if _lib is not None:
+        _declare(_lib, sigs)
+
+
+def lib() -> ctypes.CDLL:
+    """The loaded backend library; raises :class:`BackendUnavailable` if absent."""
+    global _lib
+    if _lib is None:
+        with _lib_lock:
+            if _lib is None:
+                if not os.path.exists(LIB_PATH):
+                    raise BackendUnavailable(
+                        f"HIP backend library not built: {LIB_PATH} is missing "
+                        "(run `python -m lucid_amd.build`)"
+                    )
+                try:
+                    L = ctypes.CDLL(LIB_PATH)
+                except OSError as e:
+                    raise BackendUnavailable(f"cannot load {LIB_PATH}: {e}") from e
+                _declare(L, _SIGNATURES)
+                if L.lq_abi_version() != 1:
+                    raise BackendUnavailable("ABI version mismatch")
+                _lib = L
+    return _lib
+
+
+def check(rc: int, what: str = "") -> None:
+    if rc != OK:
+        msg = lib().lq_last_error().decode(errors="replace")
+        raise LucidError(f"{what}: {msg}" if what else msg)
+
+
+def call(name: str, *args) -> None:
+    """Call an int-status entry point and raise on failure."""
+    check(getattr(lib(), name)(*args), name)
+
+
+def device_count() -> int:
+    n = _I(0)
+    check(lib().lq_device_count(ctypes.byref(n)), "lq_device_count")
+    return n.value
+
+
+def is_available() -> bool:
+    """True when the library loads and a GPU is visible."""
+    try:
+        return device_count() > 0
+    except LucidError:
+        return False
+
+
+def synchronize() -> None:
+    check(lib().lq_device_synchronize(), "lq_device_synchronize")

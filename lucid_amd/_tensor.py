@@ -1,0 +1,372 @@
+"""Minimal tensor of the HIP backend: host (numpy) or device (HBM) storage.
+
+Lucid's quantized path needs only a small part of ``lucid.Tensor``: shape,
+dtype, device, ``.to(device)``, ``.numpy()``, ``.item()``, ``reshape`` and
+buffer bookkeeping for ``state_dict``.  This class provides exactly that.  Device
+memory comes from the backend's caching allocator (``lq_malloc``/``lq_free``);
+there is no arithmetic on this class -- compute goes through the quantization
+ops, which call the HIP kernels.
+
+A device float tensor may be *code-backed*: produced by a fake-quantize on a
+known grid, it carries the integer codes and ``(scale, zero_point)`` instead of
+float storage.  Its float values are ``fl32(fl32(code - zero_point) * scale)``,
+bit-identical to the fake-quantize output, and are materialised (one dequantize
+launch) only when read as floats.  Quantized modules consume the codes directly,
+which is how an int8 GEMM can sit behind Lucid's float-in/float-out sidecar
+modules (lucid/nn/quantized/linear.py:206-215).
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Any, Sequence
+
+import numpy as np
+
+from lucid_amd import _C
+
+float32 = np.dtype(np.float32)
+float16 = np.dtype(np.float16)
+float64 = np.dtype(np.float64)
+int8 = np.dtype(np.int8)
+uint8 = np.dtype(np.uint8)
+int16 = np.dtype(np.int16)
+int32 = np.dtype(np.int32)
+int64 = np.dtype(np.int64)
+uint32 = np.dtype(np.uint32)
+bool_ = np.dtype(np.bool_)
+
+dtype = np.dtype
+
+_DEVICE_ALIASES = {"cpu": "cpu", "gpu": "gpu", "hip": "gpu", "metal": "gpu"}
+
+
+def normalize_device(device: Any) -> str:
+    if device is None:
+        return "cpu"
+    d = str(device).split(":")[0].lower()
+    if d not in _DEVICE_ALIASES:
+        raise ValueError(f"unknown device {device!r} (expected 'cpu' or 'gpu')")
+    return _DEVICE_ALIASES[d]
+
+
+class _DeviceBuffer:
+    """An ``lq_malloc`` allocation, returned to the cache when collected."""
+
+    __slots__ = ("ptr", "nbytes", "__weakref__")
+
+    def __init__(self, nbytes: int) -> None:
+        p = ctypes.c_void_p()
+        _C.check(_C.lib().lq_malloc(ctypes.byref(p), max(int(nbytes), 1)), "lq_malloc")
+        self.ptr = p.value
+        self.nbytes = int(nbytes)
+
+    def __del__(self) -> None:
+        ptr = getattr(self, "ptr", None)
+        if ptr and _C._lib is not None:
+            _C._lib.lq_free(ptr)
+            self.ptr = None
+
+
+@dataclass
+class QuantSource:
+    """Integer codes behind a code-backed float tensor (see module docstring)."""
+
+    codes: "Tensor"  # device integer tensor, same shape as the float tensor
+    code_type: int  # _C code dtype of `codes` (I8, U8, I16, U8S8, ...)
+    scale: "Tensor"  # 0-d float32 device tensor
+    zero_point: "Tensor"  # 0-d float32 device tensor (integer valued)
+    quant_min: int
+    quant_max: int
+
+
+class Tensor:
+    __slots__ = ("_host", "_buf", "_offset", "_shape", "_dtype", "_device", "_qsrc",
+                 "requires_grad", "__weakref__")
+
+    def __init__(self) -> None:  # use the factories
+        self._host: np.ndarray | None = None
+        self._buf: _DeviceBuffer | None = None
+        self._offset = 0
+        self._shape: tuple[int, ...] = ()
+        self._dtype = float32
+        self._device = "cpu"
+        self._qsrc: QuantSource | None = None
+        self.requires_grad = False
+
+    # ------------------------------------------------------------ construction
+    @classmethod
+    def _from_numpy(cls, arr: np.ndarray, device: str = "cpu") -> "Tensor":
+        arr = np.asarray(arr, order="C")  # keeps 0-d arrays 0-d (ascontiguousarray does not)
+        t = cls()
+        t._shape = tuple(int(s) for s in arr.shape)
+        t._dtype = arr.dtype
+        if device == "cpu":
+            t._host = arr.copy()
+            t._device = "cpu"
+        else:
+            t._device = "gpu"
+            t._buf = _DeviceBuffer(arr.nbytes)
+            _C.call("lq_memcpy_h2d", t._buf.ptr, arr.ctypes.data, arr.nbytes, None)
+        return t
+
+    @classmethod
+    def _empty(cls, shape: Sequence[int], dt: np.dtype, device: str) -> "Tensor":
+        t = cls()
+        t._shape = tuple(int(s) for s in shape)
+        t._dtype = np.dtype(dt)
+        if device == "cpu":
+            t._host = np.empty(t._shape, t._dtype)
+            t._device = "cpu"
+        else:
+            t._device = "gpu"
+            t._buf = _DeviceBuffer(t.nbytes)
+        return t
+
+    @classmethod
+    def _code_backed(cls, q: QuantSource, shape: Sequence[int]) -> "Tensor":
+        t = cls()
+        t._shape = tuple(int(s) for s in shape)
+        t._dtype = float32
+        t._device = "gpu"
+        t._qsrc = q
+        return t
+
+    # ----------------------------------------------------------------- metadata
+    @property
+    def shape(self) -> tuple[int, ...]:
+        return self._shape
+
+    @property
+    def dtype(self) -> np.dtype:
+        return self._dtype
+
+    @property
+    def device(self) -> str:
+        return self._device
+
+    @property
+    def ndim(self) -> int:
+        return len(self._shape)
+
+    def dim(self) -> int:
+        return len(self._shape)
+
+    def numel(self) -> int:
+        return int(np.prod(self._shape, dtype=np.int64))
+
+    @property
+    def size(self) -> int:
+        return self.numel()
+
+    @property
+    def nbytes(self) -> int:
+        return self.numel() * self._dtype.itemsize
+
+    @property
+    def is_code_backed(self) -> bool:
+        return self._qsrc is not None
+
+    @property
+    def quant_source(self) -> QuantSource | None:
+        return self._qsrc
+
+    def data_ptr(self) -> int:
+        """Device address of the float/integer storage (materialising codes if needed)."""
+        if self._device != "gpu":
+            raise _C.LucidError("data_ptr() of a CPU tensor; move it with .to('gpu')")
+        if self._buf is None:
+            self._materialize()
+        return self._buf.ptr + self._offset
+
+    def _materialize(self) -> None:
+        q = self._qsrc
+        assert q is not None
+        self._buf = _DeviceBuffer(self.nbytes)
+        self._offset = 0
+        _C.call("lq_dequantize_per_tensor", q.codes.data_ptr(), q.code_type, self._buf.ptr, _C.F32,
+                self.numel(), q.scale.data_ptr(), q.zero_point.data_ptr(), 0.0, 0.0, None)
+
+    # -------------------------------------------------------------- conversion
+    def numpy(self) -> np.ndarray:
+        if self._device == "cpu":
+            return self._host.copy()
+        out = np.empty(self._shape, self._dtype)
+        if out.nbytes:
+            _C.call("lq_memcpy_d2h", out.ctypes.data, self.data_ptr(), out.nbytes, None)
+        return out
+
+    def item(self) -> Any:
+        if self.numel() != 1:
+            raise ValueError("item() needs a one-element tensor")
+        return self.numpy().reshape(()).item()
+
+    def tolist(self) -> Any:
+        return self.numpy().tolist()
+
+    def to(self, device: Any = None, dtype: Any = None) -> "Tensor":
+        t = self
+        if device is not None:
+            dev = normalize_device(device)
+            if dev != self._device:
+                t = Tensor._from_numpy(self.numpy(), dev)
+        if dtype is not None and np.dtype(dtype) != t._dtype:
+            if t._device != "cpu":
+                raise _C.LucidError("dtype conversion of a device tensor is not part of this backend")
+            t = Tensor._from_numpy(t._host.astype(dtype), "cpu")
+        return t
+
+    def cpu(self) -> "Tensor":
+        return self.to("cpu")
+
+    def gpu(self) -> "Tensor":
+        return self.to("gpu")
+
+    def detach(self) -> "Tensor":
+        return self
+
+    def contiguous(self) -> "Tensor":
+        return self
+
+    def clone(self) -> "Tensor":
+        if self._device == "cpu":
+            return Tensor._from_numpy(self._host, "cpu")
+        t = Tensor._empty(self._shape, self._dtype, "gpu")
+        if self.nbytes:
+            _C.call("lq_memcpy_d2d", t._buf.ptr, self.data_ptr(), self.nbytes, None)
+        return t
+
+    def copy_(self, src: "Tensor") -> "Tensor":
+        if tuple(src.shape) != self._shape:
+            raise ValueError(f"copy_ shape mismatch {src.shape} vs {self._shape}")
+        if src.dtype != self._dtype:
+            raise ValueError(f"copy_ dtype mismatch {src.dtype} vs {self._dtype}")
+        if self._device == "cpu":
+            self._host[...] = src.numpy()
+        elif self.nbytes:
+            dst = self.data_ptr()
+            if src.device == "cpu":
+                arr = np.ascontiguousarray(src._host)
+                _C.call("lq_memcpy_h2d", dst, arr.ctypes.data, arr.nbytes, None)
+            else:
+                _C.call("lq_memcpy_d2d", dst, src.data_ptr(), self.nbytes, None)
+        self._qsrc = None
+        return self
+
+    def reshape(self, *shape: Any) -> "Tensor":
+        if len(shape) == 1 and isinstance(shape[0], (tuple, list)):
+            shape = tuple(shape[0])
+        shape = tuple(int(s) for s in shape)
+        n = self.numel()
+        if -1 in shape:
+            known = int(np.prod([s for s in shape if s != -1], dtype=np.int64))
+            shape = tuple(n // known if s == -1 else s for s in shape)
+        if int(np.prod(shape, dtype=np.int64)) != n:
+            raise ValueError(f"cannot reshape {self._shape} to {shape}")
+        t = Tensor()
+        t._shape = shape
+        t._dtype = self._dtype
+        t._device = self._device
+        t.requires_grad = self.requires_grad
+        if self._device == "cpu":
+            t._host = self._host.reshape(shape)
+        else:
+            if self._buf is None and self._qsrc is not None:
+                q = self._qsrc
+                t._qsrc = QuantSource(q.codes.reshape(shape), q.code_type, q.scale, q.zero_point,
+                                      q.quant_min, q.quant_max)
+            else:
+                t._buf = self._buf
+                t._offset = self._offset
+                t._qsrc = self._qsrc
+        return t
+
+    def view(self, *shape: Any) -> "Tensor":
+        return self.reshape(*shape)
+
+    def flatten(self) -> "Tensor":
+        return self.reshape(-1)
+
+    def __len__(self) -> int:
+        if not self._shape:
+            raise TypeError("len() of a 0-d tensor")
+        return self._shape[0]
+
+    def __repr__(self) -> str:
+        tag = ", code-backed" if self._qsrc is not None and self._buf is None else ""
+        return f"Tensor(shape={self._shape}, dtype={self._dtype}, device='{self._device}'{tag})"
+
+    def __deepcopy__(self, memo: dict) -> "Tensor":
+        if self._device == "cpu":
+            t = Tensor._from_numpy(self._host, "cpu")
+        else:
+            t = self.clone()
+        t.requires_grad = self.requires_grad
+        if type(self) is not Tensor:
+            t.__class__ = type(self)
+        return t
+
+    def __reduce_ex__(self, protocol: int):
+        return (_rebuild, (self.numpy(), self._device, type(self), self.requires_grad))
+
+
+def _rebuild(arr: np.ndarray, device: str, cls: type, requires_grad: bool) -> Tensor:
+    t = Tensor._from_numpy(arr, device)
+    t.__class__ = cls
+    t.requires_grad = requires_grad
+    return t
+
+
+# -------------------------------------------------------------------- factories
+
+
+def tensor(data: Any, dtype: Any = None, device: Any = "cpu", requires_grad: bool = False) -> Tensor:
+    if isinstance(data, Tensor):
+        arr = data.numpy()
+    else:
+        arr = np.asarray(data)
+    if dtype is not None:
+        arr = arr.astype(dtype)
+    elif arr.dtype == np.float64:
+        arr = arr.astype(np.float32)
+    elif arr.dtype == np.int64 and not isinstance(data, np.ndarray):
+        arr = arr.astype(np.int64)
+    t = Tensor._from_numpy(arr, normalize_device(device))
+    t.requires_grad = requires_grad
+    return t
+
+
+def from_numpy(arr: np.ndarray, device: Any = "cpu") -> Tensor:
+    return Tensor._from_numpy(arr, normalize_device(device))
+
+
+def empty(shape: Sequence[int] | int, dtype: Any = float32, device: Any = "cpu") -> Tensor:
+    if isinstance(shape, int):
+        shape = (shape,)
+    return Tensor._empty(shape, np.dtype(dtype), normalize_device(device))
+
+
+def full(shape: Sequence[int] | int, value: float, dtype: Any = float32, device: Any = "cpu") -> Tensor:
+    if isinstance(shape, int):
+        shape = (shape,)
+    return tensor(np.full(shape, value, dtype=np.dtype(dtype)), device=device)
+
+
+def zeros(shape: Sequence[int] | int, dtype: Any = float32, device: Any = "cpu") -> Tensor:
+    return full(shape, 0, dtype, device)
+
+
+def ones(shape: Sequence[int] | int, dtype: Any = float32, device: Any = "cpu") -> Tensor:
+    return full(shape, 1, dtype, device)
+
+
+def zeros_like(t: Tensor) -> Tensor:
+    return zeros(t.shape, t.dtype, t.device)
+
+
+def randn(*shape: Any, device: Any = "cpu", seed: int | None = None) -> Tensor:
+    if len(shape) == 1 and isinstance(shape[0], (tuple, list)):
+        shape = tuple(shape[0])
+    rng = np.random.default_rng(seed)
+    return tensor(rng.standard_normal(shape, dtype=np.float32), device=device)

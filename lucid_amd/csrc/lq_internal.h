@@ -1,0 +1,157 @@
+// lq_internal.h -- shared host/device helpers of the gfx950 backend.
+//
+// Every translation unit is compiled with -ffp-contract=off (see lucid_amd/build.py):
+// each float expression below is the IEEE binary32 operation it names, never an FMA,
+// so the kernels compute the same bits as Lucid's one-op-per-pass CPU composition.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "lq_api.h"
+
+namespace lq {
+
+// ---------------------------------------------------------------- errors (host)
+int set_error(int code, const std::string& msg);
+int check_hip(hipError_t e, const char* what);
+
+#define LQ_HIP(call)                                      \
+    do {                                                  \
+        hipError_t _e = (call);                           \
+        if (_e != hipSuccess) return ::lq::check_hip(_e, #call); \
+    } while (0)
+
+#define LQ_REQUIRE(cond, msg)                                   \
+    do {                                                        \
+        if (!(cond)) return ::lq::set_error(LQ_ERR_INVALID, msg); \
+    } while (0)
+
+inline int launch_status(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return check_hip(e, what);
+    return LQ_OK;
+}
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+inline hipStream_t as_stream(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+// Native clang vector types (HIP's float4/uint4 are wrapper structs, which the
+// nontemporal builtins do not accept).
+typedef float vf4 __attribute__((ext_vector_type(4)));
+typedef uint32_t vu4 __attribute__((ext_vector_type(4)));
+
+// ------------------------------------------------------------- device scalar rules
+
+// round half to even (v_rndne_f32): Lucid's lucid.round = vvnintf.
+__device__ __forceinline__ float rne(float x) { return __builtin_rintf(x); }
+
+// clip with NaN pass-through and Lucid's signed-zero tie rule (backend/cpu/Vdsp.cpp:33-62).
+__device__ __forceinline__ float clip_tie(float v, float lo, float hi, bool lo_ties, bool hi_ties) {
+    if (lo_ties ? v <= lo : v < lo) return lo;
+    if (hi_ties ? v >= hi : v > hi) return hi;
+    return v;
+}
+
+struct Grid {
+    float lo, hi;
+    bool lo_ties, hi_ties;
+};
+
+inline Grid make_grid(int qmin, int qmax) {
+    Grid g;
+    g.lo = (float)qmin;
+    g.hi = (float)qmax;
+    g.lo_ties = (qmin == 0);  // a +0 floor
+    g.hi_ties = false;        // an integer cap is never -0
+    return g;
+}
+
+__device__ __forceinline__ float clip_grid(float v, const Grid& g) {
+    return clip_tie(v, g.lo, g.hi, g.lo_ties, g.hi_ties);
+}
+
+// float -> integer storage: saturating, NaN -> 0 (backend/cpu/methods/Factory.cpp:127-146).
+template <typename T>
+__device__ __forceinline__ T satcast(float v, float lo, float hi, int lo_i, int hi_i) {
+    if (v != v) return (T)0;
+    if (v <= lo) return (T)lo_i;
+    if (v >= hi) return (T)hi_i;
+    return (T)(int)v;
+}
+
+// Code storage types.  store(c) writes the clipped float code c.
+struct CodeI8 {
+    typedef int8_t T;
+    static __device__ __forceinline__ T store(float c) { return satcast<int8_t>(c, -128.f, 127.f, -128, 127); }
+    static __device__ __forceinline__ float load(T v) { return (float)v; }
+};
+struct CodeU8 {
+    typedef uint8_t T;
+    static __device__ __forceinline__ T store(float c) { return satcast<uint8_t>(c, 0.f, 255.f, 0, 255); }
+    static __device__ __forceinline__ float load(T v) { return (float)v; }
+};
+struct CodeI16 {
+    typedef int16_t T;
+    static __device__ __forceinline__ T store(float c) {
+        return satcast<int16_t>(c, -32768.f, 32767.f, -32768, 32767);
+    }
+    static __device__ __forceinline__ float load(T v) { return (float)v; }
+};
+struct CodeI32 {
+    typedef int32_t T;
+    static __device__ __forceinline__ T store(float c) {
+        if (c != c) return 0;
+        if (c <= -2147483648.f) return INT32_MIN;
+        if (c >= 2147483648.f) return INT32_MAX;
+        return (int32_t)c;
+    }
+    static __device__ __forceinline__ float load(T v) { return (float)v; }
+};
+// Unsigned-grid code c kept as int8 (c - 128): the signed MFMA operand form.
+struct CodeU8S8 {
+    typedef int8_t T;
+    static __device__ __forceinline__ T store(float c) {
+        return (int8_t)((int)satcast<uint8_t>(c, 0.f, 255.f, 0, 255) - 128);
+    }
+    static __device__ __forceinline__ float load(T v) { return (float)((int)v + 128); }
+};
+
+// Order-preserving int32 key of a float: integer order of keys is the float order with
+// -0 below +0; a NaN with the sign bit clear keys above +inf, one with it set below -inf.
+__device__ __forceinline__ int32_t fkey(float f) {
+    int32_t b = __float_as_int(f);
+    return b ^ ((b >> 31) & 0x7fffffff);
+}
+__device__ __forceinline__ float unkey(int32_t k) {
+    return __int_as_float(k ^ ((k >> 31) & 0x7fffffff));
+}
+constexpr int32_t KEY_POS_INF = 0x7f800000;
+constexpr int32_t KEY_NEG_INF = (int32_t)(0xff800000u ^ 0x7fffffffu);
+
+// NaN-propagating extreme with -0 < +0 (backend/cpu/Reduce.cpp:54-72).
+__device__ __forceinline__ float extreme_min(float a, float b) {
+    if (a != a || b != b) return __int_as_float(0x7fc00000);
+    return unkey(min(fkey(a), fkey(b)));
+}
+__device__ __forceinline__ float extreme_max(float a, float b) {
+    if (a != a || b != b) return __int_as_float(0x7fc00000);
+    return unkey(max(fkey(a), fkey(b)));
+}
+
+// Wave64 reductions over int32.
+__device__ __forceinline__ int32_t wave_min(int32_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = min(v, __shfl_xor(v, off, 64));
+    return v;
+}
+__device__ __forceinline__ int32_t wave_max(int32_t v) {
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
+    return v;
+}
+
+}  // namespace lq

@@ -1,0 +1,856 @@
+// lq_quant.hip -- bandwidth-bound kernels of the quantized path on gfx950:
+// min/max observers, calculate_qparams, quantize, dequantize and fake-quantize.
+//
+// Reference compute each kernel replaces (lucid-official/lucid):
+//   observers     observer.py:408-414 (MinMax), 527-544 (EMA), 672-685 (per channel),
+//                 1031-1048 (per-channel EMA); NaN-propagating min/max Reduce.cpp:54-135
+//   qparams       quantization/_qparams.py:186-205
+//   quantize      quantization/_functional.py:59-69,179-197 (five Accelerate passes)
+//   dequantize    quantization/_functional.py:281-293 (three passes)
+//   fake-quant    quantization/_functional.py:314-333 (about ten passes incl. the mask)
+// Here each is one pass: 128-bit loads and stores, 16 elements per lane, results
+// identical bit-for-bit to the one-op-per-pass composition (no FMA contraction).
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include "lq_internal.h"
+
+namespace lq {
+
+constexpr int kBlock = 256;
+constexpr int kVec = 16;  // elements per lane in the vector paths
+
+// ------------------------------------------------------------ qparam sources
+// A per-tensor parameter is either a device scalar (a Lucid tensor scale: its
+// reciprocal is the float32 division 1.0f / s) or a host value passed by value
+// (a Python-float scale: its reciprocal was rounded on the host from a double).
+struct PtParams {
+    const float* d_scale;
+    const float* d_zp;
+    float inv_value;
+    float scale_value;
+    float zp_value;
+    __device__ __forceinline__ void load(float& inv, float& s, float& z) const {
+        if (d_scale) {
+            s = d_scale[0];
+            inv = 1.0f / s;
+        } else {
+            inv = inv_value;
+            s = scale_value;
+        }
+        z = d_zp ? d_zp[0] : zp_value;
+    }
+};
+
+// ----------------------------------------------------------------- observers
+
+__device__ __forceinline__ void key_accum(int32_t& kmin, int32_t& kmax, float v) {
+    int32_t k = fkey(v);
+    kmin = min(kmin, k);
+    kmax = max(kmax, k);
+}
+
+// Block-wide min/max of keys; result valid in thread 0.
+__device__ __forceinline__ void block_reduce_keys(int32_t& kmin, int32_t& kmax) {
+    __shared__ int32_t smin[kBlock / 64], smax[kBlock / 64];
+    kmin = wave_min(kmin);
+    kmax = wave_max(kmax);
+    int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+    if (lane == 0) {
+        smin[wid] = kmin;
+        smax[wid] = kmax;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); ++w) {
+            kmin = min(kmin, smin[w]);
+            kmax = max(kmax, smax[w]);
+        }
+    }
+}
+
+// Stage 1: per-block extrema keys of x[n], grid-stride over vf4 quads.
+__global__ __launch_bounds__(kBlock) void minmax_partial_kernel(const float* __restrict__ x,
+                                                                int64_t n, int2* __restrict__ part,
+                                                                bool vec_ok) {
+    int32_t kmin = KEY_POS_INF, kmax = KEY_NEG_INF;
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t nthreads = (int64_t)gridDim.x * blockDim.x;
+    int64_t done = 0;
+    if (vec_ok) {
+        const vf4* x4 = reinterpret_cast<const vf4*>(x);
+        const int64_t nq = n >> 2;
+        int64_t i = tid;
+        // Four independent 128-bit loads in flight per iteration.
+        for (; i + 3 * nthreads < nq; i += 4 * nthreads) {
+            vf4 a = __builtin_nontemporal_load(&x4[i]);
+            vf4 b = __builtin_nontemporal_load(&x4[i + nthreads]);
+            vf4 c = __builtin_nontemporal_load(&x4[i + 2 * nthreads]);
+            vf4 d = __builtin_nontemporal_load(&x4[i + 3 * nthreads]);
+            key_accum(kmin, kmax, a.x); key_accum(kmin, kmax, a.y);
+            key_accum(kmin, kmax, a.z); key_accum(kmin, kmax, a.w);
+            key_accum(kmin, kmax, b.x); key_accum(kmin, kmax, b.y);
+            key_accum(kmin, kmax, b.z); key_accum(kmin, kmax, b.w);
+            key_accum(kmin, kmax, c.x); key_accum(kmin, kmax, c.y);
+            key_accum(kmin, kmax, c.z); key_accum(kmin, kmax, c.w);
+            key_accum(kmin, kmax, d.x); key_accum(kmin, kmax, d.y);
+            key_accum(kmin, kmax, d.z); key_accum(kmin, kmax, d.w);
+        }
+        for (; i < nq; i += nthreads) {
+            vf4 a = x4[i];
+            key_accum(kmin, kmax, a.x); key_accum(kmin, kmax, a.y);
+            key_accum(kmin, kmax, a.z); key_accum(kmin, kmax, a.w);
+        }
+        done = nq << 2;
+    }
+    for (int64_t i = done + tid; i < n; i += nthreads) key_accum(kmin, kmax, x[i]);
+    block_reduce_keys(kmin, kmax);
+    if (threadIdx.x == 0) part[blockIdx.x] = make_int2(kmin, kmax);
+}
+
+// Decode an extrema key pair: NaN in the data (keyed outside [-inf, +inf]) makes both NaN.
+__device__ __forceinline__ void decode_keys(int32_t kmin, int32_t kmax, float& mn, float& mx) {
+    if (kmax > KEY_POS_INF || kmin < KEY_NEG_INF) {
+        mn = mx = __int_as_float(0x7fc00000);
+    } else {
+        mn = unkey(kmin);
+        mx = unkey(kmax);
+    }
+}
+
+// Fold batch extrema into a running pair by mode (observer.py:408-414, 527-544).
+__device__ __forceinline__ void fold_running(float& rmin, float& rmax, float cmin, float cmax,
+                                             int mode, float c, bool first) {
+    if (mode == LQ_OBS_REPLACE) {
+        rmin = cmin;
+        rmax = cmax;
+    } else if (mode == LQ_OBS_MINMAX) {
+        rmin = extreme_min(rmin, cmin);
+        rmax = extreme_max(rmax, cmax);
+    } else {
+        if (first) {
+            rmin = cmin;
+            rmax = cmax;
+        } else {
+            float dmin = cmin - rmin;
+            float dmax = cmax - rmax;
+            float tmin = c * dmin;
+            float tmax = c * dmax;
+            rmin = rmin + tmin;
+            rmax = rmax + tmax;
+        }
+    }
+}
+
+// Stage 2: one block folds the partials into the running {min, max}.
+__global__ __launch_bounds__(kBlock) void minmax_finalize_kernel(const int2* __restrict__ part,
+                                                                 int nparts, float* rmin_p,
+                                                                 float* rmax_p, int mode, float c) {
+    int32_t kmin = KEY_POS_INF, kmax = KEY_NEG_INF;
+    for (int i = threadIdx.x; i < nparts; i += blockDim.x) {
+        int2 p = part[i];
+        kmin = min(kmin, p.x);
+        kmax = max(kmax, p.y);
+    }
+    block_reduce_keys(kmin, kmax);
+    if (threadIdx.x == 0) {
+        float cmin, cmax;
+        decode_keys(kmin, kmax, cmin, cmax);
+        float rmin = *rmin_p, rmax = *rmax_p;
+        bool first = __builtin_isinf(rmin);
+        fold_running(rmin, rmax, cmin, cmax, mode, c, first);
+        *rmin_p = rmin;
+        *rmax_p = rmax;
+    }
+}
+
+static int minmax_grid(int64_t n) {
+    int64_t g = (n + (int64_t)kBlock * kVec - 1) / ((int64_t)kBlock * kVec);
+    if (g < 1) g = 1;
+    if (g > 4096) g = 4096;
+    return (int)g;
+}
+
+// ---- per channel, x as [outer, C, inner]
+// Row form (inner >= 64): block (c, split) reduces channel c over its share of `outer`.
+__global__ __launch_bounds__(kBlock) void minmax_pc_rows_kernel(const float* __restrict__ x,
+                                                                int64_t outer, int64_t C,
+                                                                int64_t inner, int splits,
+                                                                int2* __restrict__ part,
+                                                                bool vec_ok) {
+    const int64_t c = blockIdx.x;
+    const int split = blockIdx.y;
+    int32_t kmin = KEY_POS_INF, kmax = KEY_NEG_INF;
+    for (int64_t o = split; o < outer; o += splits) {
+        const float* row = x + (o * C + c) * inner;
+        int64_t done = 0;
+        if (vec_ok) {
+            const vf4* r4 = reinterpret_cast<const vf4*>(row);
+            const int64_t nq = inner >> 2;
+            int64_t i = threadIdx.x;
+            for (; i + 3 * kBlock < nq; i += 4 * kBlock) {
+                vf4 a = __builtin_nontemporal_load(&r4[i]);
+                vf4 b = __builtin_nontemporal_load(&r4[i + kBlock]);
+                vf4 cc = __builtin_nontemporal_load(&r4[i + 2 * kBlock]);
+                vf4 d = __builtin_nontemporal_load(&r4[i + 3 * kBlock]);
+                key_accum(kmin, kmax, a.x); key_accum(kmin, kmax, a.y);
+                key_accum(kmin, kmax, a.z); key_accum(kmin, kmax, a.w);
+                key_accum(kmin, kmax, b.x); key_accum(kmin, kmax, b.y);
+                key_accum(kmin, kmax, b.z); key_accum(kmin, kmax, b.w);
+                key_accum(kmin, kmax, cc.x); key_accum(kmin, kmax, cc.y);
+                key_accum(kmin, kmax, cc.z); key_accum(kmin, kmax, cc.w);
+                key_accum(kmin, kmax, d.x); key_accum(kmin, kmax, d.y);
+                key_accum(kmin, kmax, d.z); key_accum(kmin, kmax, d.w);
+            }
+            for (; i < nq; i += kBlock) {
+                vf4 a = r4[i];
+                key_accum(kmin, kmax, a.x); key_accum(kmin, kmax, a.y);
+                key_accum(kmin, kmax, a.z); key_accum(kmin, kmax, a.w);
+            }
+            done = nq << 2;
+        }
+        for (int64_t i = done + threadIdx.x; i < inner; i += kBlock) key_accum(kmin, kmax, row[i]);
+    }
+    block_reduce_keys(kmin, kmax);
+    if (threadIdx.x == 0) part[(int64_t)split * C + c] = make_int2(kmin, kmax);
+}
+
+// Column form (inner < 64): lane j of block (tile, split) owns column j of the
+// [outer, C*inner] matrix and walks its share of the rows (coalesced across lanes).
+__global__ __launch_bounds__(kBlock) void minmax_pc_cols_kernel(const float* __restrict__ x,
+                                                                int64_t outer, int64_t width,
+                                                                int splits,
+                                                                int2* __restrict__ part) {
+    const int64_t j = (int64_t)blockIdx.x * kBlock + threadIdx.x;
+    const int split = blockIdx.y;
+    if (j >= width) return;
+    int32_t kmin = KEY_POS_INF, kmax = KEY_NEG_INF;
+    for (int64_t o = split; o < outer; o += splits) key_accum(kmin, kmax, x[o * width + j]);
+    part[(int64_t)split * width + j] = make_int2(kmin, kmax);
+}
+
+// Fold per-channel partials: part is [splits, C * per_c] key pairs (per_c = inner for the
+// column form, 1 for the row form).  One block; the per-channel EMA seed test reads the
+// whole running_min first (observer.py:1039-1044).
+__global__ __launch_bounds__(1024) void minmax_pc_finalize_kernel(const int2* __restrict__ part,
+                                                                  int splits, int64_t C,
+                                                                  int64_t per_c, float* rmin,
+                                                                  float* rmax, int mode,
+                                                                  float c) {
+    __shared__ int all_inf;
+    if (threadIdx.x == 0) all_inf = 1;
+    __syncthreads();
+    if (mode == LQ_OBS_EMA) {
+        for (int64_t ch = threadIdx.x; ch < C; ch += blockDim.x)
+            if (!__builtin_isinf(rmin[ch])) all_inf = 0;  // benign race: all writers store 0
+        __syncthreads();
+    }
+    const bool first = all_inf != 0;
+    for (int64_t ch = threadIdx.x; ch < C; ch += blockDim.x) {
+        int32_t kmin = KEY_POS_INF, kmax = KEY_NEG_INF;
+        for (int s = 0; s < splits; ++s)
+            for (int64_t i = 0; i < per_c; ++i) {
+                int2 p = part[(int64_t)s * C * per_c + ch * per_c + i];
+                kmin = min(kmin, p.x);
+                kmax = max(kmax, p.y);
+            }
+        float cmin, cmax;
+        decode_keys(kmin, kmax, cmin, cmax);
+        float a = rmin[ch], b = rmax[ch];
+        fold_running(a, b, cmin, cmax, mode, c, first);
+        rmin[ch] = a;
+        rmax[ch] = b;
+    }
+}
+
+struct PcPlan {
+    bool rows;
+    int splits;
+    int64_t per_c;
+    size_t bytes;
+};
+
+static PcPlan pc_plan(int64_t outer, int64_t C, int64_t inner) {
+    PcPlan p;
+    p.rows = inner >= 64;
+    if (p.rows) {
+        // Enough blocks to fill the chip, each with at least ~16K elements.
+        int64_t want = (C >= 1024) ? 1 : (1024 + C - 1) / C;
+        int64_t max_by_work = (outer * inner) / 16384;
+        if (want > max_by_work) want = max_by_work;
+        if (want > outer) want = outer;
+        if (want < 1) want = 1;
+        p.splits = (int)want;
+        p.per_c = 1;
+        p.bytes = sizeof(int2) * (size_t)(p.splits * C);
+    } else {
+        int64_t width = C * inner;
+        int64_t tiles = (width + kBlock - 1) / kBlock;
+        int64_t want = (tiles >= 1024) ? 1 : (1024 + tiles - 1) / tiles;
+        int64_t max_by_work = outer / 64;
+        if (want > max_by_work) want = max_by_work;
+        if (want < 1) want = 1;
+        p.splits = (int)want;
+        p.per_c = inner;
+        p.bytes = sizeof(int2) * (size_t)(p.splits * width);
+    }
+    return p;
+}
+
+// ------------------------------------------------------------------ qparams
+// calculate_qparams (_qparams.py:186-205), one lane per range.
+__global__ void calc_qparams_kernel(const float* __restrict__ mn_in, const float* __restrict__ mx_in,
+                                    int64_t n, int symmetric, int is_signed, int qmin, int qmax,
+                                    float eps, float* __restrict__ scale,
+                                    float* __restrict__ zero_point, float half_range,
+                                    float width_f, float mid_zp, Grid g) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float mn = extreme_min(mn_in[i], 0.0f);  // lucid.minimum(min, zeros_like)
+    float mx = extreme_max(mx_in[i], 0.0f);
+    if (symmetric) {
+        float ma = extreme_max(__builtin_fabsf(mn), __builtin_fabsf(mx));
+        float q = ma / half_range;
+        scale[i] = extreme_max(q, eps);
+        zero_point[i] = is_signed ? 0.0f : mid_zp;
+    } else {
+        float w = mx - mn;
+        float q = w / width_f;
+        float s = extreme_max(q, eps);
+        float r = rne(mn / s);
+        float z = (float)qmin - r;
+        scale[i] = s;
+        zero_point[i] = clip_grid(z, g);
+    }
+}
+
+// -------------------------------------------------------- quantize kernels
+
+template <class Code, int N>
+struct CodeVec {
+    typename Code::T v[N];
+};
+
+template <class Code>
+__device__ __forceinline__ float quant_one(float x, float inv, float z, const Grid& g) {
+    float t = x * inv;
+    float r = rne(t);
+    float u = r + z;
+    return clip_grid(u, g);
+}
+
+template <class Code>
+__device__ __forceinline__ void store16(typename Code::T* dst, const float* c) {
+    CodeVec<Code, kVec> out;
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) out.v[j] = Code::store(c[j]);
+    constexpr int bytes = sizeof(out);
+    static_assert(bytes % 16 == 0, "16-element code vector is a multiple of 16 bytes");
+    const vu4* s = reinterpret_cast<const vu4*>(&out);
+    vu4* d = reinterpret_cast<vu4*>(dst);
+#pragma unroll
+    for (int j = 0; j < bytes / 16; ++j) __builtin_nontemporal_store(s[j], &d[j]);
+}
+
+__device__ __forceinline__ void load16(const float* src, float* v) {
+    const vf4* s = reinterpret_cast<const vf4*>(src);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        vf4 a = __builtin_nontemporal_load(&s[j]);
+        v[4 * j + 0] = a.x;
+        v[4 * j + 1] = a.y;
+        v[4 * j + 2] = a.z;
+        v[4 * j + 3] = a.w;
+    }
+}
+
+// Per-tensor: lane t handles elements [16t, 16t+16) when the vector path applies.
+template <class Code>
+__global__ __launch_bounds__(kBlock) void quantize_pt_kernel(const float* __restrict__ x,
+                                                             typename Code::T* __restrict__ q,
+                                                             int64_t n, PtParams pp, Grid g,
+                                                             bool vec_ok) {
+    float inv, s, z;
+    pp.load(inv, s, z);
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (vec_ok) {
+        const int64_t base = t * kVec;
+        if (base + kVec <= n) {
+            float v[kVec], c[kVec];
+            load16(x + base, v);
+#pragma unroll
+            for (int j = 0; j < kVec; ++j) c[j] = quant_one<Code>(v[j], inv, z, g);
+            store16<Code>(q + base, c);
+        } else {
+            for (int64_t i = base; i < n; ++i) q[i] = Code::store(quant_one<Code>(x[i], inv, z, g));
+        }
+    } else {
+        const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+        for (int64_t i = t; i < n; i += stride) q[i] = Code::store(quant_one<Code>(x[i], inv, z, g));
+    }
+}
+
+// Channel of flat element i in [outer, C, inner].
+__device__ __forceinline__ int64_t channel_of(int64_t i, int64_t C, int64_t inner) {
+    if (inner == 1) return i % C;
+    return (i / inner) % C;
+}
+
+template <class Code>
+__global__ __launch_bounds__(kBlock) void quantize_pc_kernel(
+    const float* __restrict__ x, typename Code::T* __restrict__ q, int64_t n, int64_t C,
+    int64_t inner, const float* __restrict__ scale, const float* __restrict__ zp, float zp_value,
+    Grid g, bool vec_ok) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (vec_ok) {  // inner % 16 == 0: the 16 elements share one channel
+        const int64_t base = t * kVec;
+        if (base >= n) return;
+        const int64_t ch = channel_of(base, C, inner);
+        const float inv = 1.0f / scale[ch];
+        const float z = zp ? zp[ch] : zp_value;
+        float v[kVec], c[kVec];
+        load16(x + base, v);
+#pragma unroll
+        for (int j = 0; j < kVec; ++j) c[j] = quant_one<Code>(v[j], inv, z, g);
+        store16<Code>(q + base, c);
+    } else {
+        const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+        for (int64_t i = t; i < n; i += stride) {
+            const int64_t ch = channel_of(i, C, inner);
+            const float inv = 1.0f / scale[ch];
+            const float z = zp ? zp[ch] : zp_value;
+            q[i] = Code::store(quant_one<Code>(x[i], inv, z, g));
+        }
+    }
+}
+
+// ------------------------------------------------------- dequantize kernels
+
+template <typename Y>
+__device__ __forceinline__ Y to_out(float v);
+template <>
+__device__ __forceinline__ float to_out<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ __half to_out<__half>(float v) { return __float2half_rn(v); }
+
+template <class Code, typename Y>
+__device__ __forceinline__ void dequant16(const typename Code::T* src, Y* dst, float s, float z) {
+    CodeVec<Code, kVec> in;
+    constexpr int inb = sizeof(in);
+    const vu4* sp = reinterpret_cast<const vu4*>(src);
+    vu4* ip = reinterpret_cast<vu4*>(&in);
+#pragma unroll
+    for (int j = 0; j < inb / 16; ++j) ip[j] = __builtin_nontemporal_load(&sp[j]);
+    Y out[kVec];
+#pragma unroll
+    for (int j = 0; j < kVec; ++j) {
+        float f = Code::load(in.v[j]);
+        float d = f - z;
+        out[j] = to_out<Y>(d * s);
+    }
+    constexpr int outb = sizeof(out);
+    const vu4* op = reinterpret_cast<const vu4*>(out);
+    vu4* dp = reinterpret_cast<vu4*>(dst);
+#pragma unroll
+    for (int j = 0; j < outb / 16; ++j) __builtin_nontemporal_store(op[j], &dp[j]);
+}
+
+template <class Code, typename Y>
+__global__ __launch_bounds__(kBlock) void dequantize_pt_kernel(const typename Code::T* __restrict__ q,
+                                                               Y* __restrict__ y, int64_t n,
+                                                               PtParams pp, bool vec_ok) {
+    float inv, s, z;
+    pp.load(inv, s, z);
+    (void)inv;
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (vec_ok) {
+        const int64_t base = t * kVec;
+        if (base + kVec <= n) {
+            dequant16<Code, Y>(q + base, y + base, s, z);
+        } else {
+            for (int64_t i = base; i < n; ++i) {
+                float d = Code::load(q[i]) - z;
+                y[i] = to_out<Y>(d * s);
+            }
+        }
+    } else {
+        const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+        for (int64_t i = t; i < n; i += stride) {
+            float d = Code::load(q[i]) - z;
+            y[i] = to_out<Y>(d * s);
+        }
+    }
+}
+
+template <class Code, typename Y>
+__global__ __launch_bounds__(kBlock) void dequantize_pc_kernel(
+    const typename Code::T* __restrict__ q, Y* __restrict__ y, int64_t n, int64_t C, int64_t inner,
+    const float* __restrict__ scale, const float* __restrict__ zp, float zp_value, bool vec_ok) {
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (vec_ok) {
+        const int64_t base = t * kVec;
+        if (base >= n) return;
+        const int64_t ch = channel_of(base, C, inner);
+        dequant16<Code, Y>(q + base, y + base, scale[ch], zp ? zp[ch] : zp_value);
+    } else {
+        const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+        for (int64_t i = t; i < n; i += stride) {
+            const int64_t ch = channel_of(i, C, inner);
+            float d = Code::load(q[i]) - (zp ? zp[ch] : zp_value);
+            y[i] = to_out<Y>(d * scale[ch]);
+        }
+    }
+}
+
+// ---------------------------------------------------- fake-quantize kernels
+
+__device__ __forceinline__ float fq_one(float x, float inv, float s, float z, const Grid& g,
+                                        float& m) {
+    float t = x * inv;
+    float r = rne(t);
+    float qpre = r + z;
+    float qc = clip_grid(qpre, g);
+    float d = qc - z;
+    float lo = (qpre >= g.lo) ? 1.0f : 0.0f;
+    float hi = (qpre <= g.hi) ? 1.0f : 0.0f;
+    m = lo * hi;
+    return d * s;
+}
+
+__device__ __forceinline__ void store16f(float* dst, const float* v) {
+    vf4* d = reinterpret_cast<vf4*>(dst);
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        __builtin_nontemporal_store(vf4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]}, &d[j]);
+}
+
+__global__ __launch_bounds__(kBlock) void fake_quant_kernel(const float* __restrict__ x,
+                                                            float* __restrict__ y,
+                                                            float* __restrict__ mask, int64_t n,
+                                                            int64_t C, int64_t inner, PtParams pp,
+                                                            const float* __restrict__ scale,
+                                                            const float* __restrict__ zp,
+                                                            float zp_value, Grid g, bool per_channel,
+                                                            bool vec_ok) {
+    float inv = 0.f, s = 0.f, z = 0.f;
+    if (!per_channel) pp.load(inv, s, z);
+    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (vec_ok) {
+        const int64_t base = t * kVec;
+        if (base + kVec <= n) {
+            if (per_channel) {
+                const int64_t ch = channel_of(base, C, inner);
+                s = scale[ch];
+                inv = 1.0f / s;
+                z = zp ? zp[ch] : zp_value;
+            }
+            float v[kVec], o[kVec], m[kVec];
+            load16(x + base, v);
+#pragma unroll
+            for (int j = 0; j < kVec; ++j) o[j] = fq_one(v[j], inv, s, z, g, m[j]);
+            store16f(y + base, o);
+            if (mask) store16f(mask + base, m);
+            return;
+        }
+        for (int64_t i = base; i < n; ++i) {
+            if (per_channel) {
+                const int64_t ch = channel_of(i, C, inner);
+                s = scale[ch];
+                inv = 1.0f / s;
+                z = zp ? zp[ch] : zp_value;
+            }
+            float m;
+            y[i] = fq_one(x[i], inv, s, z, g, m);
+            if (mask) mask[i] = m;
+        }
+    } else {
+        const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+        for (int64_t i = t; i < n; i += stride) {
+            if (per_channel) {
+                const int64_t ch = channel_of(i, C, inner);
+                s = scale[ch];
+                inv = 1.0f / s;
+                z = zp ? zp[ch] : zp_value;
+            }
+            float m;
+            y[i] = fq_one(x[i], inv, s, z, g, m);
+            if (mask) mask[i] = m;
+        }
+    }
+}
+
+// ------------------------------------------------------------------- launch helpers
+
+static dim3 vec_grid(int64_t n) {
+    int64_t lanes = (n + kVec - 1) / kVec;
+    int64_t blocks = (lanes + kBlock - 1) / kBlock;
+    if (blocks < 1) blocks = 1;
+    return dim3((unsigned)blocks);
+}
+
+static dim3 scalar_grid(int64_t n) {
+    int64_t blocks = (n + kBlock - 1) / kBlock;
+    if (blocks > 65536) blocks = 65536;
+    if (blocks < 1) blocks = 1;
+    return dim3((unsigned)blocks);
+}
+
+static bool valid_code(int t) {
+    return t == LQ_I8 || t == LQ_U8 || t == LQ_I16 || t == LQ_I32 || t == LQ_U8S8;
+}
+
+template <template <class> class F, typename... Args>
+static int dispatch_code(int q_dtype, Args&&... args) {
+    switch (q_dtype) {
+    case LQ_I8: return F<CodeI8>::run(args...);
+    case LQ_U8: return F<CodeU8>::run(args...);
+    case LQ_I16: return F<CodeI16>::run(args...);
+    case LQ_I32: return F<CodeI32>::run(args...);
+    case LQ_U8S8: return F<CodeU8S8>::run(args...);
+    default: return set_error(LQ_ERR_INVALID, "unsupported code dtype");
+    }
+}
+
+template <class Code>
+struct QuantPt {
+    static int run(const float* x, void* q, int64_t n, PtParams pp, Grid g, hipStream_t st) {
+        typedef typename Code::T T;
+        bool vec = aligned16(x) && aligned16(q);
+        dim3 grid = vec ? vec_grid(n) : scalar_grid(n);
+        hipLaunchKernelGGL(quantize_pt_kernel<Code>, grid, dim3(kBlock), 0, st, x, (T*)q, n, pp, g, vec);
+        return launch_status("lq_quantize_per_tensor_f32");
+    }
+};
+
+template <class Code>
+struct QuantPc {
+    static int run(const float* x, void* q, int64_t n, int64_t C, int64_t inner, const float* scale,
+                   const float* zp, float zp_value, Grid g, hipStream_t st) {
+        typedef typename Code::T T;
+        bool vec = aligned16(x) && aligned16(q) && (inner % kVec == 0);
+        dim3 grid = vec ? vec_grid(n) : scalar_grid(n);
+        hipLaunchKernelGGL(quantize_pc_kernel<Code>, grid, dim3(kBlock), 0, st, x, (T*)q, n, C, inner,
+                           scale, zp, zp_value, g, vec);
+        return launch_status("lq_quantize_per_channel_f32");
+    }
+};
+
+template <class Code>
+struct DequantPt {
+    static int run(const void* q, void* y, int y_dtype, int64_t n, PtParams pp, hipStream_t st) {
+        typedef typename Code::T T;
+        bool vec = aligned16(q) && aligned16(y);
+        dim3 grid = vec ? vec_grid(n) : scalar_grid(n);
+        if (y_dtype == LQ_F32)
+            hipLaunchKernelGGL((dequantize_pt_kernel<Code, float>), grid, dim3(kBlock), 0, st,
+                               (const T*)q, (float*)y, n, pp, vec);
+        else
+            hipLaunchKernelGGL((dequantize_pt_kernel<Code, __half>), grid, dim3(kBlock), 0, st,
+                               (const T*)q, (__half*)y, n, pp, vec);
+        return launch_status("lq_dequantize_per_tensor");
+    }
+};
+
+template <class Code>
+struct DequantPc {
+    static int run(const void* q, void* y, int y_dtype, int64_t n, int64_t C, int64_t inner,
+                   const float* scale, const float* zp, float zp_value, hipStream_t st) {
+        typedef typename Code::T T;
+        bool vec = aligned16(q) && aligned16(y) && (inner % kVec == 0);
+        dim3 grid = vec ? vec_grid(n) : scalar_grid(n);
+        if (y_dtype == LQ_F32)
+            hipLaunchKernelGGL((dequantize_pc_kernel<Code, float>), grid, dim3(kBlock), 0, st,
+                               (const T*)q, (float*)y, n, C, inner, scale, zp, zp_value, vec);
+        else
+            hipLaunchKernelGGL((dequantize_pc_kernel<Code, __half>), grid, dim3(kBlock), 0, st,
+                               (const T*)q, (__half*)y, n, C, inner, scale, zp, zp_value, vec);
+        return launch_status("lq_dequantize_per_channel");
+    }
+};
+
+static int check_ocl(int64_t outer, int64_t C, int64_t inner) {
+    LQ_REQUIRE(outer >= 0 && C >= 1 && inner >= 0, "invalid [outer, C, inner] layout");
+    return LQ_OK;
+}
+
+}  // namespace lq
+
+using namespace lq;
+
+extern "C" {
+
+size_t lq_minmax_workspace_size(int64_t n) { return sizeof(int2) * (size_t)minmax_grid(n); }
+
+int lq_minmax_f32(const float* d_x, int64_t n, float* d_running_min, float* d_running_max,
+                  int mode, float ema_c, void* d_workspace, size_t workspace_bytes, void* stream) {
+    LQ_REQUIRE(n >= 0, "lq_minmax_f32: n < 0");
+    LQ_REQUIRE(d_running_min && d_running_max, "lq_minmax_f32: NULL running buffer");
+    LQ_REQUIRE(n == 0 || d_x, "lq_minmax_f32: NULL input");
+    LQ_REQUIRE(mode >= 0 && mode <= 2, "lq_minmax_f32: bad mode");
+    const int grid = minmax_grid(n);
+    LQ_REQUIRE(d_workspace && workspace_bytes >= sizeof(int2) * (size_t)grid,
+               "lq_minmax_f32: workspace too small");
+    hipStream_t st = as_stream(stream);
+    int2* part = (int2*)d_workspace;
+    hipLaunchKernelGGL(minmax_partial_kernel, dim3(grid), dim3(kBlock), 0, st, d_x, n, part,
+                       aligned16(d_x));
+    int rc = launch_status("lq_minmax_f32 partial");
+    if (rc) return rc;
+    hipLaunchKernelGGL(minmax_finalize_kernel, dim3(1), dim3(kBlock), 0, st, part, grid,
+                       d_running_min, d_running_max, mode, ema_c);
+    return launch_status("lq_minmax_f32 finalize");
+}
+
+size_t lq_minmax_per_channel_workspace_size(int64_t outer, int64_t C, int64_t inner) {
+    if (C < 1 || outer < 0 || inner < 0) return 0;
+    return pc_plan(outer, C, inner).bytes;
+}
+
+int lq_minmax_per_channel_f32(const float* d_x, int64_t outer, int64_t C, int64_t inner,
+                              float* d_running_min, float* d_running_max, int mode, float ema_c,
+                              void* d_workspace, size_t workspace_bytes, void* stream) {
+    int rc = check_ocl(outer, C, inner);
+    if (rc) return rc;
+    LQ_REQUIRE(d_running_min && d_running_max, "lq_minmax_per_channel_f32: NULL running buffer");
+    LQ_REQUIRE(outer * inner == 0 || d_x, "lq_minmax_per_channel_f32: NULL input");
+    LQ_REQUIRE(mode >= 0 && mode <= 2, "lq_minmax_per_channel_f32: bad mode");
+    PcPlan p = pc_plan(outer, C, inner);
+    LQ_REQUIRE(d_workspace && workspace_bytes >= p.bytes,
+               "lq_minmax_per_channel_f32: workspace too small");
+    LQ_REQUIRE(C <= 0x7fffffff, "lq_minmax_per_channel_f32: too many channels");
+    hipStream_t st = as_stream(stream);
+    int2* part = (int2*)d_workspace;
+    if (p.rows) {
+        bool vec = aligned16(d_x) && (inner % 4 == 0);
+        hipLaunchKernelGGL(minmax_pc_rows_kernel, dim3((unsigned)C, (unsigned)p.splits), dim3(kBlock),
+                           0, st, d_x, outer, C, inner, p.splits, part, vec);
+    } else {
+        int64_t width = C * inner;
+        if (width > 0) {
+            int64_t tiles = (width + kBlock - 1) / kBlock;
+            LQ_REQUIRE(tiles <= 0x7fffffff, "lq_minmax_per_channel_f32: too wide");
+            hipLaunchKernelGGL(minmax_pc_cols_kernel, dim3((unsigned)tiles, (unsigned)p.splits),
+                               dim3(kBlock), 0, st, d_x, outer, width, p.splits, part);
+        }
+    }
+    rc = launch_status("lq_minmax_per_channel_f32 partial");
+    if (rc) return rc;
+    // inner == 0 leaves per_c == 0: the finalize reads no partials and folds the
+    // identity extrema {+inf, -inf}.
+    hipLaunchKernelGGL(minmax_pc_finalize_kernel, dim3(1), dim3(1024), 0, st, part, p.splits, C,
+                       p.per_c, d_running_min, d_running_max, mode, ema_c);
+    return launch_status("lq_minmax_per_channel_f32 finalize");
+}
+
+int lq_calc_qparams_f32(const float* d_min, const float* d_max, int64_t n, int symmetric,
+                        int is_signed, int qmin, int qmax, float eps, float* d_scale,
+                        float* d_zero_point, void* stream) {
+    LQ_REQUIRE(n >= 0, "lq_calc_qparams_f32: n < 0");
+    if (n == 0) return LQ_OK;
+    LQ_REQUIRE(d_min && d_max && d_scale && d_zero_point, "lq_calc_qparams_f32: NULL pointer");
+    LQ_REQUIRE(qmax > qmin, "lq_calc_qparams_f32: qmax <= qmin");
+    // Python-side constants of _qparams.py:197-204, rounded to float32 as the scalars are.
+    const float half_range = (float)((double)(qmax - qmin) / 2.0);
+    const float width_f = (float)(qmax - qmin);
+    // (qmax + qmin + 1) // 2 with Python's floor division.
+    const long long sum = (long long)qmax + qmin + 1;
+    const long long half = (sum >= 0 || sum % 2 == 0) ? sum / 2 : sum / 2 - 1;
+    const float mid_zp = (float)half;
+    unsigned blocks = (unsigned)((n + kBlock - 1) / kBlock);
+    hipLaunchKernelGGL(calc_qparams_kernel, dim3(blocks), dim3(kBlock), 0, as_stream(stream), d_min,
+                       d_max, n, symmetric, is_signed, qmin, qmax, eps, d_scale, d_zero_point,
+                       half_range, width_f, mid_zp, make_grid(qmin, qmax));
+    return launch_status("lq_calc_qparams_f32");
+}
+
+int lq_quantize_per_tensor_f32(const float* d_x, void* d_q, int64_t n, int q_dtype,
+                               const float* d_scale, const float* d_zero_point,
+                               float inv_scale_value, float zero_point_value, int qmin, int qmax,
+                               void* stream) {
+    LQ_REQUIRE(n >= 0, "lq_quantize_per_tensor_f32: n < 0");
+    if (n == 0) return LQ_OK;
+    LQ_REQUIRE(d_x && d_q, "lq_quantize_per_tensor_f32: NULL pointer");
+    LQ_REQUIRE(valid_code(q_dtype), "lq_quantize_per_tensor_f32: bad code dtype");
+    LQ_REQUIRE(qmax >= qmin, "lq_quantize_per_tensor_f32: qmax < qmin");
+    PtParams pp{d_scale, d_zero_point, inv_scale_value, 0.0f, zero_point_value};
+    return dispatch_code<QuantPt>(q_dtype, d_x, d_q, n, pp, make_grid(qmin, qmax), as_stream(stream));
+}
+
+int lq_quantize_per_channel_f32(const float* d_x, void* d_q, int64_t outer, int64_t C,
+                                int64_t inner, int q_dtype, const float* d_scale,
+                                const float* d_zero_point, float zero_point_value, int qmin,
+                                int qmax, void* stream) {
+    int rc = check_ocl(outer, C, inner);
+    if (rc) return rc;
+    const int64_t n = outer * C * inner;
+    if (n == 0) return LQ_OK;
+    LQ_REQUIRE(d_x && d_q && d_scale, "lq_quantize_per_channel_f32: NULL pointer");
+    LQ_REQUIRE(valid_code(q_dtype), "lq_quantize_per_channel_f32: bad code dtype");
+    LQ_REQUIRE(qmax >= qmin, "lq_quantize_per_channel_f32: qmax < qmin");
+    return dispatch_code<QuantPc>(q_dtype, d_x, d_q, n, C, inner, d_scale, d_zero_point,
+                                  zero_point_value, make_grid(qmin, qmax), as_stream(stream));
+}
+
+int lq_dequantize_per_tensor(const void* d_q, int q_dtype, void* d_y, int y_dtype, int64_t n,
+                             const float* d_scale, const float* d_zero_point, float scale_value,
+                             float zero_point_value, void* stream) {
+    LQ_REQUIRE(n >= 0, "lq_dequantize_per_tensor: n < 0");
+    if (n == 0) return LQ_OK;
+    LQ_REQUIRE(d_q && d_y, "lq_dequantize_per_tensor: NULL pointer");
+    LQ_REQUIRE(valid_code(q_dtype), "lq_dequantize_per_tensor: bad code dtype");
+    LQ_REQUIRE(y_dtype == LQ_F32 || y_dtype == LQ_F16, "lq_dequantize_per_tensor: bad output dtype");
+    PtParams pp{d_scale, d_zero_point, 0.0f, scale_value, zero_point_value};
+    return dispatch_code<DequantPt>(q_dtype, d_q, d_y, y_dtype, n, pp, as_stream(stream));
+}
+
+int lq_dequantize_per_channel(const void* d_q, int q_dtype, void* d_y, int y_dtype, int64_t outer,
+                              int64_t C, int64_t inner, const float* d_scale,
+                              const float* d_zero_point, float zero_point_value, void* stream) {
+    int rc = check_ocl(outer, C, inner);
+    if (rc) return rc;
+    const int64_t n = outer * C * inner;
+    if (n == 0) return LQ_OK;
+    LQ_REQUIRE(d_q && d_y && d_scale, "lq_dequantize_per_channel: NULL pointer");
+    LQ_REQUIRE(valid_code(q_dtype), "lq_dequantize_per_channel: bad code dtype");
+    LQ_REQUIRE(y_dtype == LQ_F32 || y_dtype == LQ_F16, "lq_dequantize_per_channel: bad output dtype");
+    return dispatch_code<DequantPc>(q_dtype, d_q, d_y, y_dtype, n, C, inner, d_scale, d_zero_point,
+                                    zero_point_value, as_stream(stream));
+}
+
+int lq_fake_quantize_per_tensor_f32(const float* d_x, float* d_y, int64_t n, const float* d_scale,
+                                    const float* d_zero_point, float inv_scale_value,
+                                    float scale_value, float zero_point_value, int qmin, int qmax,
+                                    float* d_mask, void* stream) {
+    LQ_REQUIRE(n >= 0, "lq_fake_quantize_per_tensor_f32: n < 0");
+    if (n == 0) return LQ_OK;
+    LQ_REQUIRE(d_x && d_y, "lq_fake_quantize_per_tensor_f32: NULL pointer");
+    LQ_REQUIRE(qmax >= qmin, "lq_fake_quantize_per_tensor_f32: qmax < qmin");
+    PtParams pp{d_scale, d_zero_point, inv_scale_value, scale_value, zero_point_value};
+    bool vec = aligned16(d_x) && aligned16(d_y) && (!d_mask || aligned16(d_mask));
+    dim3 grid = vec ? vec_grid(n) : scalar_grid(n);
+    hipLaunchKernelGGL(fake_quant_kernel, grid, dim3(kBlock), 0, as_stream(stream), d_x, d_y, d_mask,
+                       n, (int64_t)1, n, pp, (const float*)nullptr, (const float*)nullptr, 0.0f,
+                       make_grid(qmin, qmax), false, vec);
+    return launch_status("lq_fake_quantize_per_tensor_f32");
+}
+
+int lq_fake_quantize_per_channel_f32(const float* d_x, float* d_y, int64_t outer, int64_t C,
+                                     int64_t inner, const float* d_scale,
+                                     const float* d_zero_point, float zero_point_value, int qmin,
+                                     int qmax, float* d_mask, void* stream) {
+    int rc = check_ocl(outer, C, inner);
+    if (rc) return rc;
+    const int64_t n = outer * C * inner;
+    if (n == 0) return LQ_OK;
+    LQ_REQUIRE(d_x && d_y && d_scale, "lq_fake_quantize_per_channel_f32: NULL pointer");
+    LQ_REQUIRE(qmax >= qmin, "lq_fake_quantize_per_channel_f32: qmax < qmin");
+    bool vec = aligned16(d_x) && aligned16(d_y) && (!d_mask || aligned16(d_mask)) && (inner % kVec == 0);
+    dim3 grid = vec ? vec_grid(n) : scalar_grid(n);
+    PtParams pp{nullptr, nullptr, 0.f, 0.f, 0.f};
+    hipLaunchKernelGGL(fake_quant_kernel, grid, dim3(kBlock), 0, as_stream(stream), d_x, d_y, d_mask,
+                       n, C, inner, pp, d_scale, d_zero_point, zero_point_value,
+                       make_grid(qmin, qmax), true, vec);
+    return launch_status("lq_fake_quantize_per_channel_f32");
+}
+
+}  // extern "C"

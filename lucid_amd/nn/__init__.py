@@ -1,0 +1,23 @@
+"""``lucid_amd.nn``: the module system and the float layers a quantized model is built from."""
+
+from lucid_amd.nn.module import Module, Parameter
+from lucid_amd.nn.layers import (
+    BatchNorm2d,
+    Conv2d,
+    Flatten,
+    Identity,
+    Linear,
+    ReLU,
+    Sequential,
+)
+
+__all__ = ["Module", "Parameter", "Linear", "Conv2d", "ReLU", "Sequential", "Identity",
+           "BatchNorm2d", "Flatten"]
+
+
+def __getattr__(name: str):
+    import importlib
+
+    if name in ("quantized", "intrinsic", "functional"):
+        return importlib.import_module(f"lucid_amd.nn.{name}")
+    raise AttributeError(f"module 'lucid_amd.nn' has no attribute {name!r}")

@@ -1,0 +1,186 @@
+"""Float layers a quantized model starts from (the ``nn.Linear`` / ``nn.Conv2d`` /
+``nn.ReLU`` / ``nn.BatchNorm2d`` / ``nn.Sequential`` inputs of ``prepare``, ``convert``
+and ``quantize_dynamic``).
+
+Attribute names and parameter shapes follow Lucid's float modules (``weight``
+``[out, in]`` / ``[Cout, Cin/groups, kh, kw]``, ``bias``, BatchNorm's ``running_mean`` /
+``running_var`` / ``num_batches_tracked``) so ``from_float`` and ``fuse_modules`` read
+them unchanged.  Their forward runs the float HIP kernels of ``lucid_amd.nn.functional``
+(used for calibration and as the float reference of a quantized model).
+"""
+
+from __future__ import annotations
+
+import math
+from collections import OrderedDict
+from typing import Any, Iterator
+
+import numpy as np
+
+from lucid_amd._tensor import Tensor, tensor
+from lucid_amd.nn import functional as F
+from lucid_amd.nn.module import Module, Parameter
+
+
+def _pair(v: Any) -> tuple[int, int]:
+    if isinstance(v, (tuple, list)):
+        return int(v[0]), int(v[1])
+    return int(v), int(v)
+
+
+_init_rng = np.random.default_rng(0)
+
+
+def manual_seed(seed: int) -> None:
+    """Seed the host generator that initialises float layer parameters."""
+    global _init_rng
+    _init_rng = np.random.default_rng(seed)
+
+
+def _uniform(shape: tuple[int, ...], bound: float) -> Tensor:
+    return tensor(_init_rng.uniform(-bound, bound, size=shape).astype(np.float32))
+
+
+class Linear(Module):
+    def __init__(self, in_features: int, out_features: int, bias: bool = True) -> None:
+        super().__init__()
+        self.in_features = in_features
+        self.out_features = out_features
+        bound = 1.0 / math.sqrt(in_features) if in_features > 0 else 0.0
+        self.weight = Parameter(_uniform((out_features, in_features), bound))
+        if bias:
+            self.bias = Parameter(_uniform((out_features,), bound))
+        else:
+            self.register_parameter("bias", None)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return F.linear(x, self.weight, self.bias)
+
+    def extra_repr(self) -> str:
+        return (f"in_features={self.in_features}, out_features={self.out_features}, "
+                f"bias={self.bias is not None}")
+
+
+class Conv2d(Module):
+    def __init__(self, in_channels: int, out_channels: int, kernel_size: Any, stride: Any = 1,
+                 padding: Any = 0, dilation: Any = 1, groups: int = 1, bias: bool = True,
+                 padding_mode: str = "zeros") -> None:
+        super().__init__()
+        if in_channels % groups or out_channels % groups:
+            raise ValueError("in_channels and out_channels must be divisible by groups")
+        self.in_channels = in_channels
+        self.out_channels = out_channels
+        self.kernel_size = _pair(kernel_size)
+        self.stride = _pair(stride)
+        if isinstance(padding, str):
+            self.padding_str = padding
+            self.padding = (0, 0)
+        else:
+            self.padding_str = None
+            self.padding = _pair(padding)
+        self.dilation = _pair(dilation)
+        self.groups = groups
+        self.padding_mode = padding_mode
+        fan_in = (in_channels // groups) * self.kernel_size[0] * self.kernel_size[1]
+        bound = 1.0 / math.sqrt(fan_in) if fan_in > 0 else 0.0
+        self.weight = Parameter(_uniform((out_channels, in_channels // groups, *self.kernel_size),
+                                         bound))
+        if bias:
+            self.bias = Parameter(_uniform((out_channels,), bound))
+        else:
+            self.register_parameter("bias", None)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return F.conv2d(x, self.weight, self.bias, self.stride, self._resolved_padding(),
+                        self.dilation, self.groups)
+
+    def _resolved_padding(self) -> tuple[int, int]:
+        if self.padding_str is None or self.padding_str == "valid":
+            return self.padding
+        if self.padding_str == "same":
+            kh, kw = self.kernel_size
+            dh, dw = self.dilation
+            return ((dh * (kh - 1)) // 2, (dw * (kw - 1)) // 2)
+        raise ValueError(f"unknown padding {self.padding_str!r}")
+
+    def extra_repr(self) -> str:
+        return (f"{self.in_channels}, {self.out_channels}, kernel_size={self.kernel_size}, "
+                f"stride={self.stride}, padding={self.padding_str or self.padding}")
+
+
+class ReLU(Module):
+    def forward(self, x: Tensor) -> Tensor:
+        return F.relu(x)
+
+
+class Identity(Module):
+    def forward(self, x: Tensor) -> Tensor:
+        return x
+
+
+class Flatten(Module):
+    def __init__(self, start_dim: int = 1, end_dim: int = -1) -> None:
+        super().__init__()
+        self.start_dim = start_dim
+        self.end_dim = end_dim
+
+    def forward(self, x: Tensor) -> Tensor:
+        shape = list(x.shape)
+        s = self.start_dim % len(shape)
+        e = self.end_dim % len(shape)
+        new = shape[:s] + [int(np.prod(shape[s:e + 1]))] + shape[e + 1:]
+        return x.reshape(new)
+
+
+class BatchNorm2d(Module):
+    def __init__(self, num_features: int, eps: float = 1e-5, momentum: float = 0.1,
+                 affine: bool = True, track_running_stats: bool = True) -> None:
+        super().__init__()
+        self.num_features = num_features
+        self.eps = eps
+        self.momentum = momentum
+        self.affine = affine
+        self.track_running_stats = track_running_stats
+        if affine:
+            self.weight = Parameter(tensor(np.ones(num_features, np.float32)))
+            self.bias = Parameter(tensor(np.zeros(num_features, np.float32)))
+        else:
+            self.register_parameter("weight", None)
+            self.register_parameter("bias", None)
+        self.register_buffer("running_mean", tensor(np.zeros(num_features, np.float32)))
+        self.register_buffer("running_var", tensor(np.ones(num_features, np.float32)))
+        self.register_buffer("num_batches_tracked", tensor(np.array(0, np.int64)))
+
+    def forward(self, x: Tensor) -> Tensor:
+        return F.batch_norm_eval(x, self.running_mean, self.running_var, self.weight, self.bias,
+                                 self.eps)
+
+    def extra_repr(self) -> str:
+        return f"{self.num_features}, eps={self.eps}"
+
+
+class Sequential(Module):
+    def __init__(self, *args: Any) -> None:
+        super().__init__()
+        if len(args) == 1 and isinstance(args[0], OrderedDict):
+            for name, m in args[0].items():
+                self.add_module(name, m)
+        else:
+            for i, m in enumerate(args):
+                self.add_module(str(i), m)
+
+    def __getitem__(self, idx: int) -> Module:
+        mods = list(self._modules.values())
+        return mods[idx]
+
+    def __len__(self) -> int:
+        return len(self._modules)
+
+    def __iter__(self) -> Iterator[Module]:
+        return iter(self._modules.values())
+
+    def forward(self, x: Any) -> Any:
+        for m in self._modules.values():
+            if m is not None:
+                x = m(x)
+        return x

@@ -1,0 +1,333 @@
+"""CPU oracle for the int8 quantized-inference path -- TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s ``cpu_baseline`` leg
+may import this package, and only as the checker / the timed CPU baseline.  The
+product package ``lucid_amd`` never imports it.
+
+Thin numpy wrappers over ``liblq_oracle.so`` (built from ``lq_oracle.c`` by
+``oracle/Makefile``), a plain-C restatement of Lucid's arithmetic:
+
+============================  ==========================================================
+function                      follows (lucid-official/lucid)
+============================  ==========================================================
+``rne``                       ``lucid.round`` = vvnintf (backend/cpu/methods/Unary.cpp:143-147)
+``clip``                      backend/cpu/Vdsp.cpp:33-62 (NaN passes, signed-zero ties)
+``minmax`` / ``_per_channel``  observer.py:408-414, 527-544, 672-685, 1031-1048;
+                              backend/cpu/Reduce.cpp:54-105
+``calc_qparams``              quantization/_qparams.py:186-205
+``quantize``                  quantization/_functional.py:59-69, 179-197
+``dequantize``                quantization/_functional.py:281-293
+``fake_quantize``             quantization/_functional.py:314-333
+``gemm_w8a8``                 build-defined integer contract (no reference counterpart):
+                              exact int32 sum, then the epilogue documented in
+                              include/lq_api.h; int32 core checked by brute force
+``gemv_w8``                   nn/quantized/linear.py:206-210 (dequantize -> F.linear) with
+                              float64 accumulation (tolerance reference)
+``group_*``                   quantization/_qgemm.py:84-97, 167-170 (MLX 0.32.3 internals:
+                              parity unpinned beyond this documented formula)
+``lucid_*``                   the multi-pass CPU composition timed as the CPU baseline
+============================  ==========================================================
+
+Pins (tests/test_oracle.py): the reference's known-answer tests, torch's
+``quantize_per_tensor`` / ``fake_quantize_per_*`` (the independent oracle the
+reference's own parity suite uses), closed forms and brute force.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "liblq_oracle.so")
+
+# Element-type codes shared with include/lq_api.h.
+I8, U8, I16, I32, F16, F32, U8S8 = 1, 2, 3, 4, 5, 6, 7
+OBS_MINMAX, OBS_EMA, OBS_REPLACE = 0, 1, 2
+OUT_I32, OUT_F32, OUT_F16, OUT_Q8, OUT_QU8, OUT_FQ32, OUT_Q16 = 0, 1, 2, 3, 4, 5, 6
+
+_CODE_NP = {I8: np.int8, U8: np.uint8, I16: np.int16, I32: np.int32, U8S8: np.int8}
+
+_lib = None
+
+
+def build() -> None:
+    """Compile ``liblq_oracle.so`` with the committed Makefile."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        _lib = ctypes.CDLL(_LIB_PATH)
+        _declare(_lib)
+    return _lib
+
+
+_P = ctypes.c_void_p
+_I64 = ctypes.c_int64
+_F = ctypes.c_float
+_I = ctypes.c_int
+
+
+def _declare(L: ctypes.CDLL) -> None:
+    L.lqo_rne.argtypes, L.lqo_rne.restype = [_F], _F
+    L.lqo_clip.argtypes, L.lqo_clip.restype = [_F, _F, _F], _F
+    L.lqo_extreme.argtypes, L.lqo_extreme.restype = [_F, _F, _I], _F
+    L.lqo_f32_to_f16.argtypes, L.lqo_f32_to_f16.restype = [_F], ctypes.c_uint16
+    L.lqo_recip_f32.argtypes, L.lqo_recip_f32.restype = [_F], _F
+    L.lqo_recip_f64.argtypes, L.lqo_recip_f64.restype = [ctypes.c_double], _F
+    L.lqo_minmax.argtypes = [_P, _I64, _P, _I, _F]
+    L.lqo_minmax_per_channel.argtypes = [_P, _I64, _I64, _I64, _P, _P, _I, _F]
+    L.lqo_calc_qparams.argtypes = [_P, _P, _I64, _I, _I, _I, _I, _F, _P, _P]
+    L.lqo_quantize.argtypes = [_P, _I64, _I64, _I64, _P, _P, _I, _I, _P, _I]
+    L.lqo_dequantize.argtypes = [_P, _I, _I64, _I64, _I64, _P, _P, _P, _I]
+    L.lqo_fake_quantize.argtypes = [_P, _I64, _I64, _I64, _P, _P, _P, _I, _I, _P, _P]
+    L.lqo_gemm_acc.argtypes = [_P, _I64, _P, _I64, _I64, _I64, _I64, ctypes.c_int32, _P, _P]
+    L.lqo_gemm_acc.restype = _I
+    L.lqo_gemm_w8a8.argtypes = [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P,
+                                _I64, _F, _P, _P, _F, _F, _I, _I, _I, _I]
+    L.lqo_gemm_w8a8.restype = _I
+    L.lqo_gemv_w8.argtypes = [_P, _I64, _I64, _P, _I64, _P, _P, _P, _I, _P]
+    L.lqo_group_quantize.argtypes = [_P, _I64, _I64, _I, _I, _P, _P, _P]
+    L.lqo_group_dequantize.argtypes = [_P, _P, _P, _I64, _I64, _I, _I, _P]
+    L.lqo_lucid_minmax.argtypes = [_P, _I64, _P, _P]
+    L.lqo_lucid_quantize.argtypes = [_P, _I64, _F, _F, _I, _I, _P, _P, _P]
+    L.lqo_lucid_dequantize.argtypes = [_P, _I64, _F, _F, _P, _P]
+    L.lqo_set_threads.argtypes, L.lqo_set_threads.restype = [_I], _I
+
+
+def _ptr(a: np.ndarray | None) -> int | None:
+    return None if a is None else a.ctypes.data
+
+
+def _f32(a) -> np.ndarray:
+    return np.asarray(a, dtype=np.float32, order="C")
+
+
+# ---------------------------------------------------------------- scalar rules
+
+
+def rne(x: float) -> float:
+    return lib().lqo_rne(x)
+
+
+def clip(v: float, lo: float, hi: float) -> float:
+    return lib().lqo_clip(v, lo, hi)
+
+
+def f32_to_f16_bits(x: np.ndarray) -> np.ndarray:
+    L = lib()
+    x = _f32(x).ravel()
+    return np.array([L.lqo_f32_to_f16(float(v)) for v in x], dtype=np.uint16)
+
+
+def recip_tensor(s) -> np.ndarray:
+    """Reciprocal of a float32 tensor scale: 1.0f / s in float32."""
+    s = _f32(s)
+    return (np.float32(1.0) / s).astype(np.float32)
+
+
+def recip_scalar(s: float) -> np.float32:
+    """Reciprocal of a Python-float scale: fl32(1.0 / s) computed in double."""
+    return np.float32(lib().lqo_recip_f64(float(s)))
+
+
+# ------------------------------------------------------------------ observers
+
+
+def minmax(x: np.ndarray, running=(np.inf, -np.inf), mode: int = OBS_MINMAX, c: float = 0.0):
+    x = _f32(x).ravel()
+    r = _f32(running).copy()
+    lib().lqo_minmax(_ptr(x), x.size, _ptr(r), mode, np.float32(c))
+    return r
+
+
+def _ocl(shape, ch_axis):
+    shape = tuple(shape)
+    outer = int(np.prod(shape[:ch_axis], dtype=np.int64))
+    C = int(shape[ch_axis])
+    inner = int(np.prod(shape[ch_axis + 1 :], dtype=np.int64))
+    return outer, C, inner
+
+
+def minmax_per_channel(x: np.ndarray, ch_axis: int, rmin=None, rmax=None,
+                       mode: int = OBS_MINMAX, c: float = 0.0):
+    x = _f32(x)
+    outer, C, inner = _ocl(x.shape, ch_axis)
+    rmin = np.full(C, np.inf, np.float32) if rmin is None else _f32(np.broadcast_to(rmin, (C,))).copy()
+    rmax = np.full(C, -np.inf, np.float32) if rmax is None else _f32(np.broadcast_to(rmax, (C,))).copy()
+    lib().lqo_minmax_per_channel(_ptr(x), outer, C, inner, _ptr(rmin), _ptr(rmax), mode,
+                                 np.float32(c))
+    return rmin, rmax
+
+
+def calc_qparams(mn, mx, symmetric: bool, signed: bool, qmin: int, qmax: int, eps: float = 1e-8):
+    mn = _f32(mn)
+    mx = _f32(mx)
+    shape = mn.shape
+    mn, mx = mn.ravel().copy(), mx.ravel().copy()
+    s = np.empty_like(mn)
+    z = np.empty_like(mn)
+    lib().lqo_calc_qparams(_ptr(mn), _ptr(mx), mn.size, int(symmetric), int(signed), qmin, qmax,
+                           np.float32(eps), _ptr(s), _ptr(z))
+    return s.reshape(shape), z.reshape(shape)
+
+
+# ----------------------------------------------------- quantize / dequantize
+
+
+def _qp_vectors(C, inv, zp):
+    inv = _f32(np.broadcast_to(np.asarray(inv, np.float32), (C,))).copy()
+    zp = _f32(np.broadcast_to(np.asarray(zp, np.float32), (C,))).copy()
+    return inv, zp
+
+
+def quantize(x: np.ndarray, inv, zp, qmin: int, qmax: int, q_dtype: int = I8,
+             ch_axis: int | None = None) -> np.ndarray:
+    """Codes of ``x``; ``inv`` is the reciprocal already rounded to float32."""
+    x = _f32(x)
+    if ch_axis is None:
+        outer, C, inner = 1, 1, x.size
+    else:
+        outer, C, inner = _ocl(x.shape, ch_axis)
+    inv, zp = _qp_vectors(C, inv, zp)
+    q = np.empty(x.shape, dtype=_CODE_NP[q_dtype])
+    lib().lqo_quantize(_ptr(x), outer, C, inner, _ptr(inv), _ptr(zp), qmin, qmax, _ptr(q), q_dtype)
+    return q
+
+
+def dequantize(q: np.ndarray, q_dtype: int, s, zp, ch_axis: int | None = None,
+               y_dtype: int = F32) -> np.ndarray:
+    q = np.ascontiguousarray(q)
+    if ch_axis is None:
+        outer, C, inner = 1, 1, q.size
+    else:
+        outer, C, inner = _ocl(q.shape, ch_axis)
+    s, zp = _qp_vectors(C, s, zp)
+    if y_dtype == F16:
+        y = np.empty(q.shape, np.uint16)
+    else:
+        y = np.empty(q.shape, np.float32)
+    lib().lqo_dequantize(_ptr(q), q_dtype, outer, C, inner, _ptr(s), _ptr(zp), _ptr(y), y_dtype)
+    return y.view(np.float16) if y_dtype == F16 else y
+
+
+def fake_quantize(x: np.ndarray, inv, s, zp, qmin: int, qmax: int, ch_axis: int | None = None):
+    x = _f32(x)
+    if ch_axis is None:
+        outer, C, inner = 1, 1, x.size
+    else:
+        outer, C, inner = _ocl(x.shape, ch_axis)
+    inv, zp2 = _qp_vectors(C, inv, zp)
+    s, _ = _qp_vectors(C, s, zp)
+    y = np.empty_like(x)
+    mask = np.empty_like(x)
+    lib().lqo_fake_quantize(_ptr(x), outer, C, inner, _ptr(inv), _ptr(s), _ptr(zp2), qmin, qmax,
+                            _ptr(y), _ptr(mask))
+    return y, mask
+
+
+# --------------------------------------------------------------------- GEMM
+
+
+def gemm_acc(A: np.ndarray, B: np.ndarray, za: int = 0, zb=None) -> np.ndarray:
+    """Exact int32 accumulator of sum_k (A[m,k]-za)(B[n,k]-zb[n]); B is [N,K]."""
+    A = np.ascontiguousarray(A, np.int8)
+    B = np.ascontiguousarray(B, np.int8)
+    M, K = A.shape
+    N = B.shape[0]
+    zbv = None if zb is None else np.ascontiguousarray(np.broadcast_to(zb, (N,)), np.int32)
+    acc = np.empty((M, N), np.int32)
+    ovf = lib().lqo_gemm_acc(_ptr(A), K, _ptr(B), K, M, N, K, int(za), _ptr(zbv), _ptr(acc))
+    if ovf:
+        raise OverflowError("int32 accumulator overflow")
+    return acc
+
+
+_OUT_NP = {OUT_I32: np.int32, OUT_F32: np.float32, OUT_F16: np.uint16, OUT_Q8: np.int8,
+           OUT_QU8: np.uint8, OUT_FQ32: np.float32, OUT_Q16: np.int16}
+
+
+def gemm_w8a8(A, B, a_scale, b_scale, za=0.0, zb=None, bias=None, out_scale=1.0, out_zp=0.0,
+              qmin=-128, qmax=127, out_kind=OUT_F32, relu=False) -> np.ndarray:
+    A = np.ascontiguousarray(A, np.int8)
+    B = np.ascontiguousarray(B, np.int8)
+    M, K = A.shape
+    N = B.shape[0]
+    a_scale = _f32(np.atleast_1d(a_scale))
+    b_scale = _f32(np.atleast_1d(b_scale))
+    a_stride = 0 if a_scale.size == 1 else 1
+    b_stride = 0 if b_scale.size == 1 else 1
+    zbv = None if zb is None else _f32(np.broadcast_to(zb, (N,)))
+    bias = None if bias is None else _f32(bias)
+    C = np.empty((M, N), _OUT_NP[out_kind])
+    ovf = lib().lqo_gemm_w8a8(_ptr(A), K, _ptr(B), K, _ptr(C), N, M, N, K, _ptr(a_scale),
+                              a_stride, _ptr(b_scale), b_stride, np.float32(za), _ptr(zbv),
+                              _ptr(bias), np.float32(out_scale), np.float32(out_zp), qmin, qmax,
+                              out_kind, int(relu))
+    if ovf:
+        raise OverflowError("int32 accumulator overflow")
+    return C.view(np.float16) if out_kind == OUT_F16 else C
+
+
+def gemv_w8(x, W, w_scale, w_zp=None, bias=None, relu=False) -> np.ndarray:
+    x = _f32(x)
+    W = np.ascontiguousarray(W, np.int8)
+    M, K = x.shape
+    N = W.shape[0]
+    zb = None if w_zp is None else _f32(np.broadcast_to(w_zp, (N,)))
+    y = np.empty((M, N), np.float64)
+    lib().lqo_gemv_w8(_ptr(x), M, K, _ptr(W), N, _ptr(_f32(w_scale)), _ptr(zb),
+                      _ptr(None if bias is None else _f32(bias)), int(relu), _ptr(y))
+    return y
+
+
+def group_quantize(w, group_size: int, bits: int):
+    w = _f32(w)
+    N, K = w.shape
+    packed = np.empty((N, K * bits // 32), np.uint32)
+    scales = np.empty((N, K // group_size), np.float32)
+    biases = np.empty((N, K // group_size), np.float32)
+    lib().lqo_group_quantize(_ptr(w), N, K, group_size, bits, _ptr(packed), _ptr(scales),
+                             _ptr(biases))
+    return packed, scales, biases
+
+
+def group_dequantize(packed, scales, biases, group_size: int, bits: int) -> np.ndarray:
+    packed = np.ascontiguousarray(packed, np.uint32)
+    N = packed.shape[0]
+    K = packed.shape[1] * 32 // bits
+    w = np.empty((N, K), np.float32)
+    lib().lqo_group_dequantize(_ptr(packed), _ptr(_f32(scales)),
+                               _ptr(None if biases is None else _f32(biases)), N, K, group_size,
+                               bits, _ptr(w))
+    return w
+
+
+# ------------------------------------------- Lucid's multi-pass CPU composition
+
+
+def set_threads(n: int) -> int:
+    return lib().lqo_set_threads(int(n))
+
+
+def lucid_minmax(x: np.ndarray):
+    mn = ctypes.c_float()
+    mx = ctypes.c_float()
+    lib().lqo_lucid_minmax(_ptr(x), x.size, ctypes.byref(mn), ctypes.byref(mx))
+    return mn.value, mx.value
+
+
+def lucid_quantize(x, inv, z, qmin, qmax, q, t0, t1) -> None:
+    lib().lqo_lucid_quantize(_ptr(x), x.size, np.float32(inv), np.float32(z), qmin, qmax, _ptr(q),
+                             _ptr(t0), _ptr(t1))
+
+
+def lucid_dequantize(q, s, z, y, t0) -> None:
+    lib().lqo_lucid_dequantize(_ptr(q), q.size, np.float32(s), np.float32(z), _ptr(y), _ptr(t0))

@@ -1,0 +1,319 @@
+"""Pins of the CPU oracle (no GPU): the reference's known-answer tests, PyTorch's
+implementation of the same primitives (the independent oracle of Lucid's own parity
+suite, committed as tests/golden/torch_quant.npz), closed forms and brute force.
+
+Each check is chosen so a plausible slip in the oracle (dropped zero point, divide
+instead of multiply-by-reciprocal, wrong rounding mode, transposed operand, wrong pack
+order) fails at least one of them.
+"""
+
+from __future__ import annotations
+
+import os
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "torch_quant.npz")
+
+
+@pytest.fixture(scope="module")
+def g():
+    return np.load(GOLDEN)
+
+
+# ------------------------------------------------------------ reference KATs
+# lucid/test/unit/quantization/test_functional.py
+
+
+def test_kat_round_trip_on_grid():
+    x = np.array([-1.0, -0.3, 0.0, 0.7, 2.0], np.float32)
+    q = O.quantize(x, O.recip_scalar(0.05), 0.0, -128, 127, O.I8)
+    assert q.tolist() == [-20, -6, 0, 14, 40]
+    dq = O.dequantize(q, O.I8, np.float32(0.05), 0.0)
+    assert np.allclose(dq, x, atol=1e-6)
+
+
+def test_kat_saturation():
+    q = O.quantize(np.array([-1000.0, 1000.0], np.float32), O.recip_scalar(0.1), 0.0, -128, 127)
+    assert q.tolist() == [-128, 127]
+
+
+def test_kat_docstring_saturation():
+    # _functional.py:161-163: 100.0 at s=0.05 saturates to 127, not 2000
+    assert O.quantize(np.array([100.0], np.float32), O.recip_scalar(0.05), 0, -128, 127)[0] == 127
+
+
+def test_kat_affine_zero_point():
+    q = O.quantize(np.array([0.0], np.float32), O.recip_scalar(0.02), 128.0, 0, 255, O.I16)
+    assert q.tolist() == [128]
+
+
+def test_kat_fake_equals_dequant_of_quant():
+    x = np.array([-1.0, -0.31, 0.0, 0.72, 2.0], np.float32)
+    inv = O.recip_scalar(0.05)
+    fq, _ = O.fake_quantize(x, inv, np.float32(0.05), 0.0, -128, 127)
+    dq = O.dequantize(O.quantize(x, inv, 0.0, -128, 127), O.I8, np.float32(0.05), 0.0)
+    assert np.array_equal(fq, dq)
+
+
+def test_kat_ste_mask_per_tensor():
+    x = np.array([-100.0, 0.2, 0.5, 100.0], np.float32)
+    _, m = O.fake_quantize(x, O.recip_scalar(0.05), np.float32(0.05), 0.0, -128, 127)
+    assert m.tolist() == [0.0, 1.0, 1.0, 0.0]
+
+
+def test_kat_ste_mask_per_channel():
+    w = np.array([[1.0, 2.0, 300.0], [-400.0, 0.5, 0.1]], np.float32)
+    s = np.array([0.02, 0.03], np.float32)
+    _, m = O.fake_quantize(w, O.recip_tensor(s), s, 0.0, -128, 127, ch_axis=0)
+    assert m.tolist() == [[1.0, 1.0, 0.0], [0.0, 1.0, 1.0]]
+
+
+def test_kat_per_channel_half_step():
+    w = np.array([[1.0, 2.0, 3.0], [-4.0, 0.5, 0.1]], np.float32)
+    s = np.array([0.03, 0.05], np.float32)
+    q = O.quantize(w, O.recip_tensor(s), 0.0, -128, 127, ch_axis=0)
+    dq = O.dequantize(q, O.I8, s, 0.0, ch_axis=0)
+    bound = np.array([[0.03 / 2], [0.05 / 2]]) + 1e-6
+    assert (np.abs(dq - w) <= bound).all()
+
+
+def test_kat_qparams():
+    s, z = O.calc_qparams(-1.0, 3.0, False, False, 0, 255)
+    assert s.item() == pytest.approx(4.0 / 255.0, rel=1e-5) and 0 <= z.item() <= 255
+    s, z = O.calc_qparams(-2.5, 2.0, True, True, -128, 127)
+    assert z.item() == 0.0 and s.item() > 0
+    s, _ = O.calc_qparams(0.0, 0.0, False, True, -128, 127)
+    assert s.item() > 0
+    # docstring examples, _qparams.py:165-177
+    s, z = O.calc_qparams(-2.0, 6.0, False, False, 0, 255)
+    assert round(s.item(), 4) == 0.0314 and int(z.item()) == 64
+    s, z = O.calc_qparams(-0.8, 0.5, True, True, -128, 127)
+    assert int(z.item()) == 0
+    s, _ = O.calc_qparams(3.0, 3.0, False, True, -128, 127)
+    assert s.item() > 0
+
+
+def test_kat_symmetric_extremum_reciprocal_rounding():
+    """test_functional.py:114-139: codes are round(x * (1/s)) with the float32 reciprocal;
+    at each channel's extremum x/s is exactly 127.5, so a divide would round differently."""
+    data = np.random.default_rng(0).standard_normal((64, 256)).astype(np.float32)
+    mn, mx = O.minmax_per_channel(data, 1)
+    scale, zp = O.calc_qparams(mn, mx, True, True, -128, 127)
+    inv = np.float32(1.0) / scale
+    codes = np.round(data * inv)
+    expected_mask = ((codes >= -128) & (codes <= 127)).astype(np.float32)
+    assert (expected_mask == 0.0).any()
+    _, mask = O.fake_quantize(data, O.recip_tensor(scale), scale, zp, -128, 127, ch_axis=1)
+    np.testing.assert_array_equal(mask, expected_mask)
+    q = O.quantize(data, O.recip_tensor(scale), zp, -128, 127, ch_axis=1)
+    np.testing.assert_array_equal(q, np.clip(codes, -128, 127))
+    # dividing instead would differ at the extrema
+    divided = np.clip(np.round(data / scale), -128, 127)
+    assert (divided != q).any()
+
+
+# lucid/test/unit/quantization/test_observer.py
+
+
+def test_kat_observers():
+    r = O.minmax(np.array([[-1.0, 2.0], [0.5, 3.0]], np.float32))
+    r = O.minmax(np.array([[-2.0, 1.0]], np.float32), r)
+    assert r.tolist() == [-2.0, 3.0]
+    r = O.minmax(np.array([-1.0, 3.0], np.float32))
+    s, z = O.calc_qparams(r[0], r[1], False, False, 0, 255)
+    assert s.item() == pytest.approx(4.0 / 255.0, rel=1e-5)
+    r = O.minmax(np.array([-2.0, 2.0], np.float32), mode=O.OBS_EMA, c=0.5)
+    r = O.minmax(np.array([-4.0, 4.0], np.float32), r, mode=O.OBS_EMA, c=0.5)
+    assert r.tolist() == [-3.0, 3.0]
+    mn, mx = O.minmax_per_channel(np.array([[1.0, 2.0, 3.0], [-4.0, 0.5, 0.1]], np.float32), 0)
+    assert mn.tolist() == [1.0, -4.0] and mx.tolist() == [3.0, 0.5]
+    _, z = O.calc_qparams(mn, mx, True, True, -128, 127)
+    assert z.tolist() == [0.0, 0.0]
+    # EMA docstring, observer.py:506-512: a spike moves the smoothed max by ~1%
+    r = O.minmax(np.zeros(4, np.float32), mode=O.OBS_EMA, c=0.01)
+    r = O.minmax(np.full(4, 1000.0, np.float32), r, mode=O.OBS_EMA, c=0.01)
+    assert r[1] < 20.0
+
+
+# -------------------------------------------------------- PyTorch fixtures
+
+
+def test_torch_per_tensor_codes_fake_dequant(g):
+    x = g["pt_x"]
+    for i, (s, z, signed) in enumerate(zip(g["pt_scale"], g["pt_zp"], g["pt_signed"])):
+        lo, hi = (-128, 127) if signed else (0, 255)
+        inv = O.recip_scalar(float(s))
+        np.testing.assert_array_equal(O.quantize(x, inv, z, lo, hi, O.I16), g["pt_codes"][i])
+        fq, _ = O.fake_quantize(x, inv, np.float32(s), z, lo, hi)
+        np.testing.assert_array_equal(fq, g["pt_fake"][i])
+        dq = O.dequantize(g["pt_codes"][i], O.I16, np.float32(s), z)
+        np.testing.assert_array_equal(dq, g["pt_dequant"][i])
+
+
+def test_torch_per_channel(g):
+    for ax in (0, 1):
+        sc = g[f"pc{ax}_scale"]
+        q = O.quantize(g["pc_w"], O.recip_tensor(sc), 0.0, -128, 127, O.I8, ch_axis=ax)
+        np.testing.assert_array_equal(q, g[f"pc{ax}_codes"])
+        fq, _ = O.fake_quantize(g["pc_w"], O.recip_tensor(sc), sc, 0.0, -128, 127, ch_axis=ax)
+        np.testing.assert_array_equal(fq, g[f"pc{ax}_fake"])
+
+
+def test_torch_observers(g):
+    """Observer parity tolerances of lucid/test/parity/quantization/test_observer_parity.py."""
+    r = np.array([np.inf, -np.inf], np.float32)
+    e = r.copy()
+    for b in g["obs_batches"]:
+        r = O.minmax(b, r)
+        e = O.minmax(b, e, mode=O.OBS_EMA, c=0.1)
+    np.testing.assert_array_equal(r, g["obs_minmax_range"])
+    s, z = O.calc_qparams(r[0], r[1], False, False, 0, 255)
+    assert s.item() == pytest.approx(float(g["obs_minmax_scale"][0]), abs=1e-6)
+    assert abs(z.item() - float(g["obs_minmax_zp"][0])) <= 1
+    s, _ = O.calc_qparams(e[0], e[1], False, False, 0, 255)
+    assert s.item() == pytest.approx(float(g["obs_ema_scale"][0]), abs=1e-6)
+    mn, mx = O.minmax_per_channel(g["obs_pc_x"], 0)
+    s, _ = O.calc_qparams(mn, mx, True, True, -128, 127)
+    np.testing.assert_allclose(s, g["obs_pc_scale"], atol=1e-6)
+
+
+# ---------------------------------------------------- closed forms, invariants
+
+
+def test_minmax_matches_numpy_and_propagates_nan():
+    rng = np.random.default_rng(1)
+    x = rng.standard_normal(10007).astype(np.float32)
+    assert O.minmax(x).tolist() == [x.min(), x.max()]
+    x[777] = np.nan
+    assert np.isnan(O.minmax(x)).all()
+    assert np.isnan(O.minmax(np.array([1.0], np.float32), (np.nan, 2.0))[0])
+
+
+def test_minmax_signed_zero_order():
+    r = O.minmax(np.array([0.0, -0.0], np.float32))
+    assert np.signbit(r[0]) and not np.signbit(r[1])
+    r = O.minmax(np.array([-0.0, 0.0], np.float32))
+    assert np.signbit(r[0]) and not np.signbit(r[1])
+
+
+def test_minmax_per_channel_matches_numpy_any_axis():
+    x = np.random.default_rng(2).standard_normal((5, 7, 9)).astype(np.float32)
+    for ax in range(3):
+        mn, mx = O.minmax_per_channel(x, ax)
+        axes = tuple(a for a in range(3) if a != ax)
+        np.testing.assert_array_equal(mn, x.min(axis=axes))
+        np.testing.assert_array_equal(mx, x.max(axis=axes))
+
+
+def test_quantize_nan_inf_edge_cases():
+    x = np.array([np.nan, np.inf, -np.inf, 0.0, -0.0], np.float32)
+    q = O.quantize(x, O.recip_scalar(0.1), 5.0, -128, 127)
+    assert q.tolist() == [0, 127, -128, 5, 5]  # NaN passes clip, then casts to 0
+    q = O.quantize(x, O.recip_scalar(0.1), 0.0, 0, 255, O.I16)
+    assert q.tolist() == [0, 255, 0, 0, 0]
+
+
+def test_round_half_even():
+    x = np.array([0.5, 1.5, 2.5, -0.5, -1.5, -2.5], np.float32)
+    q = O.quantize(x, 1.0, 0.0, -128, 127)
+    assert q.tolist() == [0, 2, 2, 0, -2, -2]
+
+
+def test_f16_conversion_matches_numpy():
+    rng = np.random.default_rng(3)
+    vals = np.concatenate([
+        rng.standard_normal(4000).astype(np.float32) * 1000,
+        rng.standard_normal(2000).astype(np.float32) * 1e-5,  # subnormal halves
+        np.array([65504, 65519.99, 65520, 1e6, -1e6, np.inf, -np.inf, 0.0, -0.0,
+                  2.0 ** -25, 2.0 ** -24 * 1.5, 6.1e-5, 1.0009765625 + 2 ** -12], np.float32),
+    ])
+    bits = O.f32_to_f16_bits(vals)
+    with np.errstate(over="ignore"):
+        ref = vals.astype(np.float16).view(np.uint16)
+    np.testing.assert_array_equal(bits, ref)
+
+
+def test_gemm_acc_brute_force():
+    rng = np.random.default_rng(4)
+    for M, N, K in [(1, 1, 1), (3, 5, 7), (17, 33, 129), (64, 48, 256)]:
+        A = rng.integers(-128, 128, (M, K), dtype=np.int8)
+        B = rng.integers(-128, 128, (N, K), dtype=np.int8)
+        za, zb = int(rng.integers(-5, 6)), rng.integers(-3, 4, N)
+        want = (A.astype(np.int64) - za) @ (B.astype(np.int64) - zb[:, None]).T
+        np.testing.assert_array_equal(O.gemm_acc(A, B, za, zb), want)
+
+
+def test_gemm_epilogue_structure():
+    rng = np.random.default_rng(5)
+    A = rng.integers(-127, 128, (8, 64), dtype=np.int8)
+    B = rng.integers(-127, 128, (16, 64), dtype=np.int8)
+    acc = O.gemm_acc(A, B)
+    # unit scales, no bias: y is the accumulator converted exactly (|acc| < 2^24)
+    y = O.gemm_w8a8(A, B, 1.0, 1.0)
+    np.testing.assert_array_equal(y, acc.astype(np.float32))
+    sa = rng.uniform(1e-3, 1e-1, 8).astype(np.float32)
+    sb = rng.uniform(1e-3, 1e-1, 16).astype(np.float32)
+    bias = rng.standard_normal(16).astype(np.float32)
+    y = O.gemm_w8a8(A, B, sa, sb, bias=bias)
+    ref = acc.astype(np.float64) * sa[:, None] * sb[None, :] + bias
+    np.testing.assert_allclose(y, ref, rtol=1e-6, atol=1e-6)
+    # requantized codes are the oracle quantize of the float output; FQ32 its dequantize
+    for relu in (False, True):
+        yf = O.gemm_w8a8(A, B, sa, sb, bias=bias, relu=relu)
+        if relu:
+            assert (yf >= 0).all()
+        q = O.gemm_w8a8(A, B, sa, sb, bias=bias, out_scale=0.05, out_zp=3, qmin=-128, qmax=127,
+                        out_kind=O.OUT_Q8, relu=relu)
+        np.testing.assert_array_equal(q, O.quantize(yf, O.recip_tensor(np.float32(0.05)), 3.0,
+                                                    -128, 127))
+        fq = O.gemm_w8a8(A, B, sa, sb, bias=bias, out_scale=0.05, out_zp=3, qmin=-128,
+                         qmax=127, out_kind=O.OUT_FQ32, relu=relu)
+        np.testing.assert_array_equal(fq, O.dequantize(q, O.I8, np.float32(0.05), 3.0))
+    h = O.gemm_w8a8(A, B, sa, sb, bias=bias, out_kind=O.OUT_F16)
+    np.testing.assert_array_equal(h, O.gemm_w8a8(A, B, sa, sb, bias=bias).astype(np.float16))
+
+
+def test_gemv_w8_vs_float64_dequantized():
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((4, 96)).astype(np.float32)
+    W = rng.integers(-127, 128, (40, 96), dtype=np.int8)
+    s = rng.uniform(1e-3, 1e-1, 40).astype(np.float32)
+    b = rng.standard_normal(40).astype(np.float32)
+    what = (W.astype(np.float32) * s[:, None]).astype(np.float32)
+    want = x.astype(np.float64) @ what.T.astype(np.float64) + b
+    np.testing.assert_allclose(O.gemv_w8(x, W, s, bias=b), want, rtol=1e-12, atol=1e-12)
+
+
+def test_group_pack_closed_form():
+    # one row, gs=16, bits=4: w = 0..15 gives min 0, s = 1, codes = w
+    w = np.arange(16, dtype=np.float32)[None, :]
+    packed, scales, biases = O.group_quantize(w, 16, 4)
+    assert scales.tolist() == [[1.0]] and biases.tolist() == [[0.0]]
+    want = [sum(int(c) << (4 * j) for j, c in enumerate(range(i * 8, i * 8 + 8))) for i in range(2)]
+    assert packed.tolist() == [want]
+    np.testing.assert_array_equal(O.group_dequantize(packed, scales, biases, 16, 4), w)
+    # bits=8, gs=4: codes 0..255 spread, little end first
+    w8 = np.array([[0.0, 255.0, 1.0, 128.0]], np.float32)
+    p8, s8, b8 = O.group_quantize(w8, 4, 8)
+    assert p8.tolist() == [[0 | (255 << 8) | (1 << 16) | (128 << 24)]]
+
+
+def test_group_round_trip_half_step():
+    rng = np.random.default_rng(7)
+    w = rng.standard_normal((8, 256)).astype(np.float32)
+    for bits in (4, 8):
+        for gs in (32, 64, 128):
+            p, s, b = O.group_quantize(w, gs, bits)
+            wh = O.group_dequantize(p, s, b, gs, bits)
+            step = np.repeat(s, gs, axis=1)
+            assert (np.abs(wh - w) <= step / 2 + 1e-6).all()
+
+
+def test_group_constant_group_exact():
+    w = np.full((2, 64), 0.375, np.float32)
+    p, s, b = O.group_quantize(w, 64, 4)
+    np.testing.assert_array_equal(O.group_dequantize(p, s, b, 64, 4), w)
