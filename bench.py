@@ -1,0 +1,282 @@
+"""Benchmark of the int8 quantized-inference hot path on one MI355X.
+
+``python bench.py [--gpus 1] [--steps K] [--warmup W] [--components/--no-components]``
+
+Headline (``value``): the W8A8 int8 GEMM of BASELINE config 3 at M = N = K = 4096 --
+int8 A[M,K] x int8 B[N,K] on MFMA, exact int32 accumulation, per-row activation scale
+and per-column weight scale in [1e-3, 1e-1], fp32 bias, fused requantize to int8 --
+in TOPS (2*M*N*K per step).  A step is one launch of that GEMM over inputs already
+resident in HBM; K steps are timed between HIP events on the launch stream, bracketed
+by device synchronizations.
+
+The same JSON line carries:
+  * ``roofline``: the GEMM kernel's achieved TOPS against the 5.0 POPS dense int8 MFMA
+    peak (algorithmic ops / average launch time from the events);
+  * ``components``: the rest of BASELINE configs 2 and 3 -- the GEMM M-sweep and the
+    4096x11008 / 11008x4096 shapes, and the bandwidth kernels (min/max observer,
+    quantize, dequantize) over 2^28 fp32 elements, each with its roofline fraction;
+  * ``cpu_baseline``: Lucid's CPU composition for the same GEMM (dequantize both
+    operands every call, fp32 sgemm on all host BLAS threads, bias add, multi-pass
+    requantize), restated by the oracle package and timed on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+INT8_PEAK_TOPS = 5000.0
+
+
+def _parse() -> argparse.Namespace:
+    p = argparse.ArgumentParser()
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=50)
+    p.add_argument("--warmup", type=int, default=10)
+    p.add_argument("--components", dest="components", action="store_true", default=True)
+    p.add_argument("--no-components", dest="components", action="store_false")
+    p.add_argument("--cpu-seconds", type=float, default=12.0,
+                   help="bound on the CPU-baseline sample's wall time")
+    return p.parse_args()
+
+
+class Timer:
+    """HIP events on the launch stream (the null stream) around a block of launches."""
+
+    def __init__(self, C) -> None:
+        self.C = C
+        self.start = ctypes.c_void_p()
+        self.stop = ctypes.c_void_p()
+        C.call("lq_event_create", ctypes.byref(self.start))
+        C.call("lq_event_create", ctypes.byref(self.stop))
+
+    def time_ms(self, fn, steps: int, warmup: int) -> float:
+        C = self.C
+        for _ in range(warmup):
+            fn()
+        C.synchronize()
+        C.call("lq_event_record", self.start, None)
+        for _ in range(steps):
+            fn()
+        C.call("lq_event_record", self.stop, None)
+        C.call("lq_event_synchronize", self.stop)
+        C.synchronize()
+        ms = ctypes.c_float()
+        C.call("lq_event_elapsed_ms", ctypes.byref(ms), self.start, self.stop)
+        return ms.value / steps
+
+
+class Gemm:
+    """One configured lq_gemm_w8a8 call on device-resident synthetic inputs."""
+
+    def __init__(self, L, C, M, N, K, out_kind, seed=0):
+        rng = np.random.default_rng(seed)
+        self.M, self.N, self.K = M, N, K
+        self.A = L.tensor(rng.integers(-127, 128, (M, K), dtype=np.int64).astype(np.int8), device="gpu")
+        self.B = L.tensor(rng.integers(-127, 128, (N, K), dtype=np.int64).astype(np.int8), device="gpu")
+        self.sa = L.tensor(rng.uniform(1e-3, 1e-1, M).astype(np.float32), device="gpu")
+        self.sb = L.tensor(rng.uniform(1e-3, 1e-1, N).astype(np.float32), device="gpu")
+        self.bias = L.tensor(rng.standard_normal(N).astype(np.float32), device="gpu")
+        self.os = L.tensor(np.float32(64.0), device="gpu")
+        self.oz = L.tensor(np.float32(0.0), device="gpu")
+        self.out_kind = out_kind
+        dt = {C.OUT_Q8: np.int8, C.OUT_F16: np.float16, C.OUT_F32: np.float32}[out_kind]
+        self.Cm = L.empty((M, N), dt, "gpu")
+        self.ws_bytes = C.lib().lq_gemm_w8a8_workspace_size(M, N, K)
+        self.ws = L.empty((max(self.ws_bytes, 1),), np.uint8, "gpu")
+        f = C.lib().lq_gemm_w8a8
+        args = (self.A.data_ptr(), K, self.B.data_ptr(), K, self.Cm.data_ptr(), N, M, N, K,
+                self.sa.data_ptr(), 1, self.sb.data_ptr(), 1, None, None, None,
+                self.bias.data_ptr(), self.os.data_ptr(), self.oz.data_ptr(), -128, 127,
+                out_kind, 0, self.ws.data_ptr(), self.ws_bytes, None)
+
+        def run() -> None:
+            rc = f(*args)
+            if rc:
+                C.check(rc, "lq_gemm_w8a8")
+
+        self.run = run
+
+    @property
+    def ops(self) -> float:
+        return 2.0 * self.M * self.N * self.K
+
+    @property
+    def bytes(self) -> float:
+        ob = self.Cm.dtype.itemsize
+        return self.M * self.K + self.K * self.N + self.M * self.N * ob + 4.0 * (self.M + 2 * self.N)
+
+
+def gemm_line(L, C, timer, M, N, K, out_kind, steps, warmup):
+    g = Gemm(L, C, M, N, K, out_kind, seed=M + N + K)
+    ms = timer.time_ms(g.run, steps, warmup)
+    tops = g.ops / (ms * 1e-3) / 1e12
+    gbs = g.bytes / (ms * 1e-3) / 1e9
+    ai = g.ops / g.bytes
+    bound_tops = min(INT8_PEAK_TOPS, HBM_PEAK_GBS * ai / 1e3)
+    return {"M": M, "N": N, "K": K, "out": {C.OUT_Q8: "int8", C.OUT_F16: "f16", C.OUT_F32: "f32"}[out_kind],
+            "us": round(ms * 1e3, 2), "TOPS": round(tops, 1), "GB/s": round(gbs, 1),
+            "bound": "mfma" if bound_tops >= INT8_PEAK_TOPS else "hbm",
+            "frac": round(tops / bound_tops, 3)}
+
+
+def bandwidth_lines(L, C, timer, steps, warmup):
+    """Observer / quantize / dequantize over 2^28 fp32 (1 GiB: larger than the 256 MB
+    Infinity Cache, so every pass streams HBM)."""
+    n = 1 << 28
+    rng = np.random.default_rng(7)
+    host = rng.standard_normal(n, dtype=np.float32)
+    idx = rng.choice(n, n // 1000, replace=False)
+    host[idx] *= 20.0
+    x = L.tensor(host, device="gpu")
+    del host
+    q = L.empty((n,), np.int8, "gpu")
+    y = L.empty((n,), np.float32, "gpu")
+    rmin = L.tensor(np.float32(np.inf), device="gpu")
+    rmax = L.tensor(np.float32(-np.inf), device="gpu")
+    scale = L.tensor(np.float32(0.05), device="gpu")
+    zp = L.tensor(np.float32(0.0), device="gpu")
+    lib = C.lib()
+    ws_bytes = lib.lq_minmax_workspace_size(n)
+    ws = L.empty((ws_bytes,), np.uint8, "gpu")
+    xp, qp, yp = x.data_ptr(), q.data_ptr(), y.data_ptr()
+    out = {}
+
+    def obs():
+        lib.lq_minmax_f32(xp, n, rmin.data_ptr(), rmax.data_ptr(), C.OBS_MINMAX, 0.0, ws.data_ptr(),
+                          ws_bytes, None)
+
+    def quant():
+        lib.lq_quantize_per_tensor_f32(xp, qp, n, C.I8, scale.data_ptr(), zp.data_ptr(), 0.0, 0.0,
+                                       -128, 127, None)
+
+    def dequant():
+        lib.lq_dequantize_per_tensor(qp, C.I8, yp, C.F32, n, scale.data_ptr(), zp.data_ptr(), 0.0,
+                                     0.0, None)
+
+    for name, fn, bpe in (("minmax_observer", obs, 4), ("quantize_f32_to_i8", quant, 5),
+                          ("dequantize_i8_to_f32", dequant, 5)):
+        ms = timer.time_ms(fn, max(steps // 5, 5), max(warmup // 5, 2))
+        gbs = n * bpe / (ms * 1e-3) / 1e9
+        out[name] = {"n": n, "bytes_per_elem": bpe, "us": round(ms * 1e3, 1),
+                     "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3)}
+    C.call("lq_device_synchronize")
+    return out
+
+
+def cpu_baseline(M, N, K, seconds):
+    """Lucid's CPU composition of the W8A8 Linear (lucid/nn/quantized/linear.py:206-215):
+    dequantize activations and weights (separate passes), fp32 sgemm (numpy's OpenBLAS on
+    every host BLAS thread, standing in for Accelerate's cblas_sgemm), bias add, then the
+    multi-pass requantize (mul by reciprocal, round, add zp, clip, cast).  Timed on a
+    bounded sample of the same workload; reported in TOPS like the headline."""
+    import oracle  # noqa: F401  (CPU-baseline leg: the oracle package provides the restatement)
+
+    try:
+        from threadpoolctl import threadpool_info
+
+        threads = max([int(i.get("num_threads", 1)) for i in threadpool_info()
+                       if i.get("internal_api") in ("openblas", "mkl", "blis")] or [1])
+    except Exception:  # pragma: no cover
+        threads = os.cpu_count() or 1
+    rng = np.random.default_rng(1)
+    A = rng.integers(-127, 128, (M, K), dtype=np.int64).astype(np.int8)
+    B = rng.integers(-127, 128, (N, K), dtype=np.int64).astype(np.int8)
+    sa = rng.uniform(1e-3, 1e-1, (M, 1)).astype(np.float32)
+    sb = rng.uniform(1e-3, 1e-1, (N, 1)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    inv = np.float32(1.0) / np.float32(64.0)
+
+    def step():
+        xa = A.astype(np.float32)
+        xa = xa - np.float32(0.0)
+        xa = xa * sa
+        wb = B.astype(np.float32)
+        wb = wb - np.float32(0.0)
+        wb = wb * sb
+        y = xa @ wb.T
+        y = y + bias
+        t = y * inv
+        t = np.rint(t)
+        t = t + np.float32(0.0)
+        t = np.clip(t, -128, 127)
+        return t.astype(np.int8)
+
+    step()  # warm
+    t0 = time.perf_counter()
+    iters = 0
+    while True:
+        step()
+        iters += 1
+        if time.perf_counter() - t0 > seconds or iters >= 20:
+            break
+    dt = (time.perf_counter() - t0) / iters
+    return {"value": round(2.0 * M * N * K / dt / 1e12, 4), "unit": "TOPS", "cores": threads,
+            "kind": "port",
+            "sample": f"{iters} steps of the {M}x{N}x{K} W8A8 Linear (dequantize A and B, fp32 "
+                      f"sgemm, bias, requantize to int8) in {dt * iters:.1f} s; "
+                      f"{os.cpu_count()} host CPUs visible"}
+
+
+def main() -> None:
+    args = _parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only: the hot path has no "
+                                   "collective (see DESIGN.md for how it would shard); "
+                                   "run with --gpus 1"}))
+        sys.exit(2)
+    import lucid_amd as L
+    from lucid_amd import _C as C
+
+    if not L.is_available():
+        print(json.dumps({"error": "no HIP device visible"}))
+        sys.exit(1)
+    timer = Timer(C)
+    M = N = K = 4096
+    head = Gemm(L, C, M, N, K, C.OUT_Q8, seed=0)
+    ms = timer.time_ms(head.run, args.steps, args.warmup)
+    tops = head.ops / (ms * 1e-3) / 1e12
+    line = {
+        "metric": "int8 GEMM TOPS + quant/dequant/GEMV GB/s (% roofline), 1xMI355X",
+        "value": round(tops, 2),
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int8",
+        "data": "synthetic (uniform int8 codes in [-127,127], scales U[1e-3,1e-1], bias N(0,1))",
+        "config": {"workload": "W8A8 int8 GEMM M=N=K=4096, per-row/per-col fp32 scales, "
+                               "fp32 bias, fused requantize to int8 (BASELINE config 3)",
+                   "M": M, "N": N, "K": K, "out": "int8"},
+        "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS,
+                     "unit": "TFLOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None},
+    }
+    if args.components:
+        comps = {"gemm_sweep": []}
+        for (m, n, k) in ((1, 4096, 4096), (16, 4096, 4096), (128, 4096, 4096), (1024, 4096, 4096),
+                          (4096, 4096, 4096), (4096, 11008, 4096), (4096, 4096, 11008)):
+            for kind in (C.OUT_Q8, C.OUT_F16):
+                comps["gemm_sweep"].append(gemm_line(L, C, timer, m, n, k, kind, 20, 5))
+        comps.update(bandwidth_lines(L, C, timer, 50, 10))
+        line["components"] = comps
+    line["cpu_baseline"] = cpu_baseline(M, N, K, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

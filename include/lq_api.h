@@ -183,59 +183,43 @@ enum {
     LQ_OUT_Q8 = 3,   /* codes of y on the output grid, stored int8 (signed grid) */
     LQ_OUT_QU8 = 4,  /* codes of y on the output grid, stored uint8 (unsigned grid) */
     LQ_OUT_FQ32 = 5, /* fake-quantized y on the output grid, float32 (the sidecar module output) */
-    LQ_OUT_Q16 = 6   /* codes of y on the output grid, stored int16 (Lucid quint8 storage) */
+    LQ_OUT_Q16 = 6,  /* codes of y on the output grid, stored int16 (Lucid quint8 storage) */
+    LQ_OUT_QU8S8 = 7 /* unsigned-grid codes c of y stored as int8 (c - 128): the next layer's
+                        MFMA operand (LQ_U8S8) */
 };
 /* Epilogue flag bits. */
 enum { LQ_EPI_RELU = 1 };
 
 /* C[m,n] epilogue of acc[m,n] = sum_k (A[m,k] - za) * (B[n,k] - zb[n])  (exact int32),
  * A int8 [M,K] row-major (lda), B int8 [N,K] row-major (ldb; Lucid's weight_int8 [out,in]).
- *   s  = fl32(a_scale[m * a_scale_stride] * b_scale[n * b_scale_stride])
+ *   s  = fl32(a_scale[m * a_scale_stride] * b_scale[n * b_scale_stride])   (NULL scale = 1)
  *   y  = fl32(float(acc) * s); y = fl32(y + bias[n]) (bias may be NULL); ReLU if flagged
  *        (y <= 0 -> +0, NaN passes; Vdsp.cpp vrelu_f32);
- *   out by out_kind, requantized with inv = fl32(1.0f / out_scale[0]), z = out_zp[0].
+ *   out by out_kind, requantized with inv = fl32(1.0f / out_scale[0]), z = out_zp[0]
+ *   (c = clip(rne(fl32(y * inv)) + z, out_qmin, out_qmax), saturating store).
  * za = d_a_zero_point[0] (integer-valued float, NULL = 0); zb = d_b_zero_point[n] (NULL = 0).
+ * The zero points enter as sum_k A*B - za*bsum[n] - zb[n]*asum[m] + K*za*zb[n] with
+ * bsum[n] = sum_k B[n,k] (d_b_sums, e.g. cached by the module from lq_row_sums_i8; NULL =
+ * computed into the workspace) and asum[m] = sum_k A[m,k] (computed when zb is given).
+ * Fast paths need 16-byte aligned A/B, lda/ldb/K multiples of 16; other shapes run a
+ * generic kernel with the same results.
  * Replaces the nnq.Linear / nnqd.Linear compute: dequantize(W) -> F.linear -> act ->
  * fake_quantize (lucid/nn/quantized/linear.py:206-215, dynamic/linear.py:85-92,
- * Linear.cpp:199 -> Matmul.cpp:80-122).  Workspace holds the row/column code sums
- * for the zero-point correction (lq_gemm_w8a8_workspace_size). */
+ * Linear.cpp:199 -> Matmul.cpp:80-122).  The workspace (lq_gemm_w8a8_workspace_size)
+ * holds the code sums and, for mid-size M, split-K partial sums; with a smaller (or NULL)
+ * workspace the call still succeeds when no zero-point sums must be computed, without split-K. */
 size_t lq_gemm_w8a8_workspace_size(int64_t M, int64_t N, int64_t K);
 int lq_gemm_w8a8(const int8_t* d_A, int64_t lda, const int8_t* d_B, int64_t ldb, void* d_C,
                  int64_t ldc, int64_t M, int64_t N, int64_t K, const float* d_a_scale,
                  int64_t a_scale_stride, const float* d_b_scale, int64_t b_scale_stride,
-                 const float* d_a_zero_point, const float* d_b_zero_point, const float* d_bias,
-                 const float* d_out_scale, const float* d_out_zero_point, int out_qmin,
-                 int out_qmax, int out_kind, int flags, void* d_workspace,
-                 size_t workspace_bytes, void* stream);
-
-/* ---- weight-only int8 GEMV / skinny GEMM (M <= 64) ----------------------------- */
-/* y[m,n] = sum_k x[m,k] * w_hat[n,k] + bias[n], w_hat = fl32(fl32(W[n,k] - zb[n]) * sb[n]),
- * x / y of x_dtype (LQ_F32 or LQ_F16, accumulation in float32).  W int8 [N,K] row-major.
- * The dequantize-then-linear of the sidecar Linear with a float input
- * (linear.py:206-210) evaluated without materialising w_hat. */
-int lq_gemv_w8(const void* d_x, int x_dtype, int64_t ldx, const int8_t* d_W, int64_t ldw,
-               const float* d_w_scale, const float* d_w_zero_point, const float* d_bias,
-               void* d_y, int64_t ldy, int64_t M, int64_t N, int64_t K, int flags, void* stream);
-
-/* ---- group-wise packed weights (QuantizedLinearMLX layout) ------------------------ */
-/* Group-wise affine quantize of W[N,K] (float32) with groups of `group_size` along K:
- * s_g = (max_g - min_g) / (2^bits - 1), b_g = min_g, c = clip(rne((w - b_g) / s_g), 0, 2^bits-1),
- * 32/bits codes per uint32 little-end first.  packed [N, K*bits/32] uint32,
- * scales/biases [N, K/group_size] float32.  Replaces quantize_op
- * (QuantizedMatmul.cpp:111-121, formula _qgemm.py:84-97). */
-int lq_group_quantize_f32(const float* d_w, int64_t N, int64_t K, int group_size, int bits,
-                          uint32_t* d_packed, float* d_scales, float* d_biases, void* stream);
-/* w_hat = fl32(fl32(c * s_g) + b_g) as float32 [N, K]; replaces dequantize_op
- * (QuantizedMatmul.cpp:123-141, _qgemm.py:167-170).  d_biases may be NULL (b_g = 0). */
-int lq_group_dequantize_f32(const uint32_t* d_packed, const float* d_scales,
-                            const float* d_biases, int64_t N, int64_t K, int group_size,
-                            int bits, float* d_w, void* stream);
-/* y[m,n] = sum_k x[m,k] * w_hat[n,k] (+ bias[n]) with x/y of x_dtype (LQ_F32/LQ_F16);
- * replaces quantized_matmul_op with transpose=true (QuantizedMatmul.cpp:143-163). */
-int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d_packed,
-                    const float* d_scales, const float* d_biases, const float* d_bias, void* d_y,
-                    int64_t ldy, int64_t M, int64_t N, int64_t K, int group_size, int bits,
-                    int flags, void* stream);
+                 const float* d_a_zero_point, const float* d_b_zero_point,
+                 const int32_t* d_b_sums, const float* d_bias, const float* d_out_scale,
+                 const float* d_out_zero_point, int out_qmin, int out_qmax, int out_kind,
+                 int flags, void* d_workspace, size_t workspace_bytes, void* stream);
+/* sums[r] = sum_k X[r,k] over int8 rows (the weight code sums a module caches for the
+ * activation zero-point correction).  No reference counterpart (Lucid has no integer GEMM). */
+int lq_row_sums_i8(const int8_t* d_X, int64_t ld, int64_t rows, int64_t K, int32_t* d_sums,
+                   void* stream);
 
 /* ---- float helpers around the quantized path ----------------------------------- */
 /* y = (x <= 0) ? +0 : x, NaN passes (the CPU relu of backend/cpu/Vdsp.cpp vrelu_f32,

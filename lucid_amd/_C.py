@@ -21,7 +21,7 @@ LIB_PATH = os.path.join(_HERE, "_lib", "liblucid_amd.so")
 OK = 0
 I8, U8, I16, I32, F16, F32, U8S8 = 1, 2, 3, 4, 5, 6, 7
 OBS_MINMAX, OBS_EMA, OBS_REPLACE = 0, 1, 2
-OUT_I32, OUT_F32, OUT_F16, OUT_Q8, OUT_QU8, OUT_FQ32, OUT_Q16 = 0, 1, 2, 3, 4, 5, 6
+OUT_I32, OUT_F32, OUT_F16, OUT_Q8, OUT_QU8, OUT_FQ32, OUT_Q16, OUT_QU8S8 = 0, 1, 2, 3, 4, 5, 6, 7
 EPI_RELU = 1
 
 
@@ -75,6 +75,10 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_dequantize_per_channel": (_I, [_P, _I, _P, _I, _I64, _I64, _I64, _P, _P, _F, _P]),
     "lq_fake_quantize_per_tensor_f32": (_I, [_P, _P, _I64, _P, _P, _F, _F, _F, _I, _I, _P, _P]),
     "lq_fake_quantize_per_channel_f32": (_I, [_P, _P, _I64, _I64, _I64, _P, _P, _F, _I, _I, _P, _P]),
+    "lq_row_sums_i8": (_I, [_P, _I64, _I64, _I64, _P, _P]),
+    "lq_gemm_w8a8_workspace_size": (_SZ, [_I64, _I64, _I64]),
+    "lq_gemm_w8a8": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64,
+                          _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _SZ, _P]),
 }
 
 _lib = None

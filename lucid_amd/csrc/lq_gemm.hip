@@ -1,0 +1,898 @@
+// lq_gemm.hip -- W8A8 int8 GEMM on CDNA4 MFMA (v_mfma_i32_16x16x64_i8) with a fused
+// zero-point / scale / bias / ReLU / requantize epilogue.
+//
+// Replaces the compute of Lucid's sidecar quantized Linear, which dequantizes the int8
+// weight and runs an fp32 sgemm every call (lucid/nn/quantized/linear.py:206-215,
+// lucid/nn/quantized/dynamic/linear.py:85-92 -> lucid/_C/nn/Linear.cpp:199 ->
+// lucid/_C/backend/cpu/methods/Matmul.cpp:80-122).  Here the integer product is exact:
+//
+//   acc[m,n] = sum_k (A[m,k] - za) * (B[n,k] - zb[n])          (int32, wrap-free when it fits)
+//            = sum_k A*B - za*bsum[n] - zb[n]*asum[m] + K*za*zb[n]
+//   y        = fl32(fl32(float(acc) * fl32(sa[m] * sb[n])) + bias[n]), ReLU, then the output
+//              kind (int32 / f32 / f16 / requantized codes / fake-quantized f32).
+//
+// Integer addition is associative, so the MFMA k-order, the tile split and split-K
+// partial sums all give the same bits; the float epilogue is one IEEE op per step
+// (compiled with -ffp-contract=off).
+//
+// Layout: A [M,K] and B [N,K] are both K-contiguous (Lucid's weight_int8 is [out, in]).
+// The MFMA is fed B as its row operand and A as its column operand, so it produces C^T
+// tiles: lane l holds four consecutive n of one m, which the epilogue stores as one vector.
+#include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
+
+#include <type_traits>
+
+#include "lq_internal.h"
+
+namespace lq {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct GemmArgs {
+    const int8_t* A;
+    const int8_t* B;
+    void* C;
+    int64_t lda, ldb, ldc;
+    int M, N, K;
+    const float* a_scale;
+    const float* b_scale;
+    int a_stride, b_stride;
+    const float* a_zp;       // device scalar (integer valued) or null
+    const float* b_zp;       // [N] (integer valued) or null
+    const int32_t* b_sums;   // [N] sum_k B[n,k]; required when a_zp is set
+    const int32_t* a_sums;   // [M] sum_k A[m,k]; required when b_zp is set
+    const float* bias;       // [N] or null
+    const float* out_scale;  // device scalar (requantizing kinds)
+    const float* out_zp;     // device scalar or null
+    int qmin, qmax;
+    int out_kind;
+    int relu;
+    int32_t* partial;        // split-K: [M,N] int32 accumulation buffer (zeroed)
+    uint32_t* counters;      // split-K: one arrival counter per output tile (zeroed)
+    int splits;              // split-K factor (1 = none)
+};
+
+// ------------------------------------------------------------------ epilogue
+
+struct EpiParams {
+    int za;
+    float out_inv, out_s, out_z;
+    Grid g;
+};
+
+__device__ __forceinline__ EpiParams epi_params(const GemmArgs& a) {
+    EpiParams p;
+    p.za = a.a_zp ? (int)a.a_zp[0] : 0;
+    p.out_s = a.out_scale ? a.out_scale[0] : 1.0f;
+    p.out_inv = 1.0f / p.out_s;
+    p.out_z = a.out_zp ? a.out_zp[0] : 0.0f;
+    p.g.lo = (float)a.qmin;
+    p.g.hi = (float)a.qmax;
+    p.g.lo_ties = (a.qmin == 0);
+    p.g.hi_ties = false;
+    return p;
+}
+
+// Zero-point corrected accumulator (two's-complement wrap; exact whenever it fits int32).
+__device__ __forceinline__ int32_t corrected(int32_t raw, int m, int n, const GemmArgs& a,
+                                             const EpiParams& p) {
+    uint32_t acc = (uint32_t)raw;
+    if (a.a_zp) acc -= (uint32_t)p.za * (uint32_t)a.b_sums[n];
+    if (a.b_zp) {
+        const uint32_t zb = (uint32_t)(int)a.b_zp[n];
+        acc -= zb * (uint32_t)a.a_sums[m];
+        acc += (uint32_t)a.K * (uint32_t)p.za * zb;
+    }
+    return (int32_t)acc;
+}
+
+__device__ __forceinline__ float requant_code(float y, const EpiParams& p) {
+    float t = y * p.out_inv;
+    float r = rne(t);
+    float u = r + p.out_z;
+    return clip_grid(u, p.g);
+}
+
+// Epilogue value of one element, as the bits of the output element type.
+template <int KIND>
+__device__ __forceinline__ uint32_t epi_one(int32_t acc, float sa, float sb, const float* bias_p,
+                                            bool relu, const EpiParams& p) {
+    if (KIND == LQ_OUT_I32) return (uint32_t)acc;
+    float s = sa * sb;
+    float y = (float)acc * s;
+    if (bias_p) y = y + *bias_p;  // no add without a bias: -0 stays -0
+    if (relu) y = (y <= 0.0f) ? 0.0f : y;
+    if (KIND == LQ_OUT_F32) return __float_as_uint(y);
+    if (KIND == LQ_OUT_F16) return (uint32_t)__half_as_ushort(__float2half_rn(y));
+    float c = requant_code(y, p);
+    if (KIND == LQ_OUT_Q8) return (uint32_t)(uint8_t)CodeI8::store(c);
+    if (KIND == LQ_OUT_QU8) return (uint32_t)CodeU8::store(c);
+    if (KIND == LQ_OUT_Q16) return (uint32_t)(uint16_t)CodeI16::store(c);
+    if (KIND == LQ_OUT_QU8S8) return (uint32_t)(uint8_t)CodeU8S8::store(c);
+    // LQ_OUT_FQ32
+    float d = c - p.out_z;
+    return __float_as_uint(d * p.out_s);
+}
+
+template <int KIND>
+struct OutTraits {
+    static constexpr int bytes = (KIND == LQ_OUT_I32 || KIND == LQ_OUT_F32 || KIND == LQ_OUT_FQ32) ? 4
+                                 : (KIND == LQ_OUT_F16 || KIND == LQ_OUT_Q16)                        ? 2
+                                                                                                     : 1;
+};
+
+template <int KIND>
+__device__ __forceinline__ void store_elem(void* C, int64_t idx, uint32_t v) {
+    constexpr int b = OutTraits<KIND>::bytes;
+    if (b == 4) reinterpret_cast<uint32_t*>(C)[idx] = v;
+    else if (b == 2) reinterpret_cast<uint16_t*>(C)[idx] = (uint16_t)v;
+    else reinterpret_cast<uint8_t*>(C)[idx] = (uint8_t)v;
+}
+
+// Epilogue inputs of the four consecutive columns n..n+3 a lane owns, loaded once.
+struct ColCtx {
+    float sb[4], bias[4];
+    int32_t bsum[4], zb[4];
+    int n;
+    bool vec;  // the four are in range and aligned for one vector store
+};
+
+// Epilogue inputs of one row m.
+struct RowCtx {
+    float sa;
+    int32_t asum;
+};
+
+// Whether four consecutive outputs starting at column n can be one vector store.
+__device__ __forceinline__ bool vec_store_ok(const GemmArgs& a, int n, int elem_bytes) {
+    const bool base_ok = ((reinterpret_cast<uintptr_t>(a.C) & (uintptr_t)(4 * elem_bytes - 1)) == 0) &&
+                         ((a.ldc & 3) == 0);
+    return base_ok && (n + 3 < a.N);
+}
+
+template <int KIND>
+__device__ __forceinline__ ColCtx load_cols(const GemmArgs& a, int n) {
+    ColCtx c;
+    c.n = n;
+    c.vec = vec_store_ok(a, n, OutTraits<KIND>::bytes);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int nn = min(n + r, a.N - 1);  // clamped: out-of-range columns are never stored
+        c.sb[r] = a.b_scale ? a.b_scale[(int64_t)nn * a.b_stride] : 1.0f;
+        c.bias[r] = a.bias ? a.bias[nn] : 0.0f;
+        c.bsum[r] = a.a_zp ? a.b_sums[nn] : 0;
+        c.zb[r] = a.b_zp ? (int)a.b_zp[nn] : 0;
+    }
+    return c;
+}
+
+__device__ __forceinline__ RowCtx load_row(const GemmArgs& a, int m) {
+    RowCtx r;
+    const int mm = min(m, a.M - 1);  // clamped: rows past M are never stored
+    r.sa = a.a_scale ? a.a_scale[(int64_t)mm * a.a_stride] : 1.0f;
+    r.asum = a.b_zp ? a.a_sums[mm] : 0;
+    return r;
+}
+
+// Four consecutive outputs C[m, c.n .. c.n+3] from raw accumulators.
+template <int KIND>
+__device__ __forceinline__ void epilogue4c(const GemmArgs& a, const EpiParams& p, const RowCtx& row,
+                                           const ColCtx& c, int m, v4i raw) {
+    if (m >= a.M) return;
+    uint32_t out[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        uint32_t acc = (uint32_t)raw[r];  // zero-point correction, two's-complement wrap
+        if (a.a_zp) acc -= (uint32_t)p.za * (uint32_t)c.bsum[r];
+        if (a.b_zp) {
+            acc -= (uint32_t)c.zb[r] * (uint32_t)row.asum;
+            acc += (uint32_t)a.K * (uint32_t)p.za * (uint32_t)c.zb[r];
+        }
+        out[r] = epi_one<KIND>((int32_t)acc, row.sa, c.sb[r], a.bias ? &c.bias[r] : nullptr, a.relu != 0, p);
+    }
+    const int64_t base = (int64_t)m * a.ldc + c.n;
+    constexpr int b = OutTraits<KIND>::bytes;
+    if (c.vec) {
+        if (b == 4) {
+            *reinterpret_cast<v4i*>(reinterpret_cast<uint32_t*>(a.C) + base) =
+                v4i{(int)out[0], (int)out[1], (int)out[2], (int)out[3]};
+        } else if (b == 2) {
+            typedef int v2i __attribute__((ext_vector_type(2)));
+            *reinterpret_cast<v2i*>(reinterpret_cast<uint16_t*>(a.C) + base) =
+                v2i{(int)(out[0] | (out[1] << 16)), (int)(out[2] | (out[3] << 16))};
+        } else {
+            *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(a.C) + base) =
+                out[0] | (out[1] << 8) | (out[2] << 16) | (out[3] << 24);
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            if (c.n + r < a.N) store_elem<KIND>(a.C, base + r, out[r]);
+    }
+}
+
+template <int KIND>
+__device__ __forceinline__ void epilogue4(const GemmArgs& a, const EpiParams& p, int m, int n, v4i raw) {
+    if (m >= a.M) return;
+    epilogue4c<KIND>(a, p, load_row(a, m), load_cols<KIND>(a, n), m, raw);
+}
+
+
+// ------------------------------------------------------------ tile scheduling
+
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2): block b
+// runs on XCD b % 8.  Renumber so each XCD works on a contiguous run of tiles, then walk
+// tiles in GROUP_M-tall bands so that run covers a compact block of A rows and B columns.
+__device__ __forceinline__ void tile_of_block(int bid, int nblk, int tiles_m, int tiles_n, int& tm,
+                                              int& tn) {
+    constexpr int XCDS = 8, GROUP_M = 4;
+    const int xcd = bid % XCDS, local = bid / XCDS;
+    const int per = nblk / XCDS, rem = nblk % XCDS;
+    const int t = xcd * per + (xcd < rem ? xcd : rem) + local;
+    const int band = GROUP_M * tiles_n;
+    const int first_m = (t / band) * GROUP_M;
+    const int gsize = min(tiles_m - first_m, GROUP_M);
+    const int in_band = t % band;
+    tm = first_m + in_band % gsize;
+    tn = in_band / gsize;
+}
+
+// ------------------------------------------------------- tiled MFMA main loop
+//
+// Block tile BM x BN, K staged 128 bytes at a time through double-buffered LDS.  Each LDS
+// row holds the 128 K-bytes of one A (or B) row as eight 16-byte chunks, chunk c stored at
+// slot c ^ (row & 7): the sixteen lanes that read one MFMA fragment (rows r..r+15, same
+// chunk) then hit eight different 16-byte bank groups per half, and the eight lanes that
+// write one row's chunks hit eight different slots.  One barrier per K stage: stage k+1
+// is written into the other buffer while stage k is consumed.
+
+constexpr int BK = 128;
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, int KIND>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_tiled_kernel(GemmArgs a) {
+    constexpr int T = 64 * WAVES_M * WAVES_N;
+    constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+    constexpr int FM = WM / 16, FN = WN / 16;
+    constexpr int A_CH = BM * (BK / 16) / T;  // 16-byte chunks per thread per stage
+    constexpr int B_CH = BN * (BK / 16) / T;
+    static_assert(A_CH * T == BM * (BK / 16) && B_CH * T == BN * (BK / 16), "tile/threads mismatch");
+    static_assert(FM >= 1 && FN >= 1, "wave tile smaller than one MFMA");
+
+    __shared__ __attribute__((aligned(16))) int8_t As[2][BM * BK];
+    __shared__ __attribute__((aligned(16))) int8_t Bs[2][BN * BK];
+
+    const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
+    const int ntiles = tiles_m * tiles_n;
+    int tile_id = blockIdx.x, split = 0;
+    if (a.splits > 1) {
+        split = blockIdx.x / ntiles;
+        tile_id = blockIdx.x % ntiles;
+    }
+    int tm, tn;
+    tile_of_block(tile_id, ntiles, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+
+    // K range of this split (whole BK stages).
+    const int nk_total = (a.K + BK - 1) / BK;
+    const int per_split = (nk_total + a.splits - 1) / a.splits;
+    const int kt_begin = split * per_split;
+    const int kt_end = min(nk_total, kt_begin + per_split);
+
+    v4i ra[A_CH], rb[B_CH];
+    auto gload = [&](int kt) {
+        const int k0 = kt * BK;
+#pragma unroll
+        for (int j = 0; j < A_CH; ++j) {
+            const int q = tid + T * j, row = q >> 3, c = q & 7;
+            const int gm = m0 + row, gk = k0 + c * 16;
+            ra[j] = (gm < a.M && gk < a.K)
+                        ? *reinterpret_cast<const v4i*>(a.A + (int64_t)gm * a.lda + gk)
+                        : v4i{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int j = 0; j < B_CH; ++j) {
+            const int q = tid + T * j, row = q >> 3, c = q & 7;
+            const int gn = n0 + row, gk = k0 + c * 16;
+            rb[j] = (gn < a.N && gk < a.K)
+                        ? *reinterpret_cast<const v4i*>(a.B + (int64_t)gn * a.ldb + gk)
+                        : v4i{0, 0, 0, 0};
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int j = 0; j < A_CH; ++j) {
+            const int q = tid + T * j, row = q >> 3, c = q & 7;
+            *reinterpret_cast<v4i*>(&As[buf][row * BK + ((c ^ (row & 7)) << 4)]) = ra[j];
+        }
+#pragma unroll
+        for (int j = 0; j < B_CH; ++j) {
+            const int q = tid + T * j, row = q >> 3, c = q & 7;
+            *reinterpret_cast<v4i*>(&Bs[buf][row * BK + ((c ^ (row & 7)) << 4)]) = rb[j];
+        }
+    };
+
+    v4i acc[FN][FM];
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+    if (kt_begin < kt_end) {
+        gload(kt_begin);
+        lstore(0);
+        __syncthreads();
+        const int a_row0 = wm * WM + (lane & 15);
+        const int b_row0 = wn * WN + (lane & 15);
+        for (int kt = kt_begin; kt < kt_end; ++kt) {
+            const int buf = (kt - kt_begin) & 1;
+            const bool more = kt + 1 < kt_end;
+            if (more) gload(kt + 1);
+#pragma unroll
+            for (int s = 0; s < BK / 64; ++s) {
+                const int c = s * 4 + (lane >> 4);
+                const int off = (c ^ (lane & 7)) << 4;
+                v4i af[FM], bf[FN];
+#pragma unroll
+                for (int j = 0; j < FM; ++j)
+                    af[j] = *reinterpret_cast<const v4i*>(&As[buf][(a_row0 + j * 16) * BK + off]);
+#pragma unroll
+                for (int i = 0; i < FN; ++i)
+                    bf[i] = *reinterpret_cast<const v4i*>(&Bs[buf][(b_row0 + i * 16) * BK + off]);
+#pragma unroll
+                for (int i = 0; i < FN; ++i)
+#pragma unroll
+                    for (int j = 0; j < FM; ++j)
+                        acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[i], af[j], acc[i][j], 0, 0, 0);
+            }
+            if (more) lstore(buf ^ 1);
+            __syncthreads();
+        }
+    }
+
+    if (a.splits > 1) {
+        // Exact int32 partial sums: atomics commute, so the total is the same bits in any order.
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+            for (int j = 0; j < FM; ++j) {
+                const int m = m0 + wm * WM + j * 16 + (lane & 15);
+                const int n = n0 + wn * WN + i * 16 + (lane >> 4) * 4;
+                if (m < a.M)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        if (n + r < a.N) atomicAdd(&a.partial[(int64_t)m * a.N + n + r], acc[i][j][r]);
+            }
+        // The last split to arrive at this tile runs the epilogue on the complete sums.
+        __threadfence();
+        __syncthreads();
+        __shared__ int last;
+        if (tid == 0) last = (atomicAdd(&a.counters[tile_id], 1u) == (unsigned)(a.splits - 1));
+        __syncthreads();
+        if (!last) return;
+        __threadfence();
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+            for (int j = 0; j < FM; ++j) {
+                const int m = m0 + wm * WM + j * 16 + (lane & 15);
+                const int n = n0 + wn * WN + i * 16 + (lane >> 4) * 4;
+                if (m < a.M)
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        acc[i][j][r] = (n + r < a.N)
+                                           ? __hip_atomic_load(&a.partial[(int64_t)m * a.N + n + r],
+                                                               __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                           : 0;
+            }
+    }
+
+    const EpiParams p = epi_params(a);
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+            const int m = m0 + wm * WM + j * 16 + (lane & 15);
+            const int n = n0 + wn * WN + i * 16 + (lane >> 4) * 4;
+            epilogue4<KIND>(a, p, m, n, acc[i][j]);
+        }
+}
+
+// --------------------------------------------- LDS-DMA MFMA main loop (large M)
+//
+// The production path for M > 64 when K % 128 == 0.  Global -> LDS copies use the LDS-DMA
+// form of buffer_load_dwordx4 (data goes straight to LDS, no staging registers): each wave
+// instruction moves 1 KB = 8 rows x 128 K-bytes of A or B into the next stage's buffer.
+// Buffer descriptors bound A and B to M*lda and N*ldb bytes, so rows past M or N read as
+// zero (their outputs are never stored) and no per-row predicates are needed.
+//
+// Two LDS stages of BK = 128: stage kt+2 is issued right after the barrier that retires
+// stage kt, and waited for (vmcnt) one stage later.  Inside a stage the two 64-byte K steps
+// ping-pong fragment registers: step s+1's fragments are read while step s's MFMAs run.
+// The copy is issued from inline asm so the compiler neither tracks it nor inserts its own
+// conservative vmcnt(0) in front of every LDS read (it cannot tell the stage buffers apart);
+// the explicit vmcnt waits below are the synchronization.  Copies of stages past the end
+// are clamped to the last stage (a valid address, landing in a buffer never read again),
+// which keeps the steady-state loop free of branches.
+
+// s_waitcnt vmcnt(N) only (lgkmcnt and expcnt fields at their no-wait maximum).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// Workgroup barrier without the memory-model fence __syncthreads() adds (that fence waits
+// for every outstanding copy).  It first waits for this wave's own LDS reads (lgkmcnt(0)):
+// after the barrier another wave may copy into the buffer those reads came from.  The
+// copies themselves are covered by wait_vmcnt.  The empty asm keeps the compiler from
+// moving memory accesses across the barrier.
+__device__ __forceinline__ void block_barrier() {
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt fields at maximum
+    __builtin_amdgcn_s_barrier();
+    asm volatile("" ::: "memory");
+}
+
+// Raw buffer descriptor (base, num_records = bytes, stride 0).
+__device__ __forceinline__ v4i buffer_rsrc(const void* base, uint32_t bytes) {
+    const uint64_t b = reinterpret_cast<uint64_t>(base);
+    return v4i{__builtin_amdgcn_readfirstlane((int)(uint32_t)b),
+               __builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)),
+               __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
+}
+
+// 16 bytes per lane from rsrc + voff + soff into LDS at lds_addr + 16 * lane.
+__device__ __forceinline__ void lds_dma16(v4i rsrc, uint32_t voff, uint32_t soff, uint32_t lds_addr) {
+    asm volatile(
+        "s_mov_b32 m0, %0\n\t"
+        "buffer_load_dwordx4 %1, %2, %3 offen lds"
+        :
+        : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
+        : "memory", "m0");
+}
+
+template <int BM, int BN, int WAVES_M, int WAVES_N>
+struct DmaTile {
+    static constexpr int BK = 128, CPR = 8, KS = 2, NBUF = 2;
+    static constexpr int NW = WAVES_M * WAVES_N;
+    static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+    static constexpr int FM = WM / 16, FN = WN / 16;
+    static constexpr int ROWS_PER_INSTR = 64 / CPR;
+    static constexpr int A_I = BM / ROWS_PER_INSTR / NW;
+    static constexpr int B_I = BN / ROWS_PER_INSTR / NW;
+    static constexpr int LPS = A_I + B_I;  // copy instructions per wave per stage
+    static constexpr int SB = (BM + BN) * BK;
+    // epilogue staging: each wave's WM x WN int32 tile, rows padded by 16 bytes
+    static constexpr int EPI_STRIDE = WN * 4 + 16;
+    static constexpr int EPI_BYTES = NW * WM * EPI_STRIDE;
+    static constexpr int LDS_BYTES = (NBUF * SB > EPI_BYTES) ? NBUF * SB : EPI_BYTES;
+    static_assert(A_I * ROWS_PER_INSTR * NW == BM && B_I * ROWS_PER_INSTR * NW == BN, "copy split");
+    static_assert(WN % 64 == 0, "epilogue writes 64-column row segments");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+};
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, int KIND>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_dma_kernel(GemmArgs a) {
+    typedef DmaTile<BM, BN, WAVES_M, WAVES_N> P;
+    constexpr int BK = P::BK, NW = P::NW, WM = P::WM, WN = P::WN, FM = P::FM, FN = P::FN;
+    constexpr int RPI = P::ROWS_PER_INSTR, A_I = P::A_I, B_I = P::B_I, SB = P::SB;
+    __shared__ __attribute__((aligned(1024))) int8_t lds[P::LDS_BYTES];
+
+    const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
+    int tm, tn;
+    tile_of_block(blockIdx.x, gridDim.x, tiles_m, tiles_n, tm, tn);
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const int nk = a.K / BK;
+
+    const v4i ra = buffer_rsrc(a.A, (uint32_t)((int64_t)a.M * a.lda));
+    const v4i rb = buffer_rsrc(a.B, (uint32_t)((int64_t)a.N * a.ldb));
+    // Lane l of a copy moves chunk p = l % 8 of row l / 8 of its 8-row block: the global
+    // chunk p ^ (row & 7), so LDS holds logical chunk c at slot c ^ (row & 7).
+    uint32_t a_off[A_I], b_off[B_I];
+    {
+        const int rl = lane >> 3;
+        const int cb = ((lane & 7) ^ rl) * 16;
+#pragma unroll
+        for (int j = 0; j < A_I; ++j) a_off[j] = (uint32_t)(m0 + (j * NW + wave) * RPI + rl) * (uint32_t)a.lda + cb;
+#pragma unroll
+        for (int j = 0; j < B_I; ++j) b_off[j] = (uint32_t)(n0 + (j * NW + wave) * RPI + rl) * (uint32_t)a.ldb + cb;
+    }
+    const uint32_t lds_base = (uint32_t)reinterpret_cast<uintptr_t>(lds);
+    auto issue = [&](int buf, int kt) __attribute__((always_inline)) {
+        const uint32_t k0 = (uint32_t)(min(kt, nk - 1) * BK);
+        const uint32_t sb = lds_base + buf * SB;
+#pragma unroll
+        for (int j = 0; j < A_I; ++j) lds_dma16(ra, a_off[j], k0, sb + (j * NW + wave) * RPI * BK);
+#pragma unroll
+        for (int j = 0; j < B_I; ++j) lds_dma16(rb, b_off[j], k0, sb + BM * BK + (j * NW + wave) * RPI * BK);
+    };
+    const int a_frag0 = (wm * WM + (lane & 15)) * BK;
+    const int b_frag0 = BM * BK + (wn * WN + (lane & 15)) * BK;
+    const int fsw = lane & 7;
+    v4i F0[FM + FN], F1[FM + FN];
+    auto read_frags = [&](v4i* f, int buf, int s) __attribute__((always_inline)) {
+        const int8_t* sbuf = lds + buf * SB;
+        const int off = ((s * 4 + (lane >> 4)) ^ fsw) << 4;
+#pragma unroll
+        for (int j = 0; j < FM; ++j) f[j] = *reinterpret_cast<const v4i*>(sbuf + a_frag0 + j * 16 * BK + off);
+#pragma unroll
+        for (int i = 0; i < FN; ++i) f[FM + i] = *reinterpret_cast<const v4i*>(sbuf + b_frag0 + i * 16 * BK + off);
+    };
+    v4i acc[FN][FM];
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    auto mfmas = [&](const v4i* f) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+            for (int j = 0; j < FM; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f[FM + i], f[j], acc[i][j], 0, 0, 0);
+    };
+    // One stage in buffer B (compile time), ending with the switch to the other buffer.
+    auto stage = [&](auto bc, int kt, bool last) __attribute__((always_inline)) {
+        constexpr int B = decltype(bc)::value;
+        read_frags(F1, B, 1);
+        mfmas(F0);
+        if (!last) {
+            wait_vmcnt<0>();  // stage kt+1 (the only copy in flight) has landed
+            block_barrier();  // ... in every wave, and every wave is done reading stage kt
+            issue(B, kt + 2);
+            read_frags(F0, B ^ 1, 0);
+        }
+        mfmas(F1);
+    };
+
+    if (nk > 0) {
+        issue(0, 0);
+        issue(1, 1);
+        wait_vmcnt<P::LPS>();
+        block_barrier();
+        read_frags(F0, 0, 0);
+        int kt = 0;
+        for (; kt + 2 < nk; kt += 2) {
+            stage(std::integral_constant<int, 0>(), kt, false);
+            stage(std::integral_constant<int, 1>(), kt + 1, false);
+        }
+        stage(std::integral_constant<int, 0>(), kt, kt + 1 == nk);
+        if (kt + 1 < nk) stage(std::integral_constant<int, 1>(), kt + 1, true);
+    }
+    // Epilogue through LDS: every copy has landed and every wave is done with the stage
+    // buffers before they are reused.  Each wave stages its own WM x WN tile and reads it
+    // back as 64-column row segments, so stores are contiguous along n.
+    wait_vmcnt<0>();
+    block_barrier();
+    constexpr int ES = P::EPI_STRIDE;
+    int8_t* stile = lds + wave * WM * ES;
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+            *reinterpret_cast<v4i*>(stile + (j * 16 + (lane & 15)) * ES + (i * 16 + (lane >> 4) * 4) * 4) = acc[i][j];
+    const EpiParams p = epi_params(a);
+    // Lane l owns columns (l % 16) * 4 .. +3 of each 64-column segment and rows l / 16 + 4 i:
+    // its column parameters are loaded once per segment, its WM / 4 row parameters up front.
+    RowCtx rows[WM / 4];
+#pragma unroll
+    for (int i = 0; i < WM / 4; ++i) rows[i] = load_row(a, m0 + wm * WM + i * 4 + (lane >> 4));
+    for (int seg = 0; seg < WN / 64; ++seg) {
+        const int cc = seg * 64 + (lane & 15) * 4;
+        const ColCtx cols = load_cols<KIND>(a, n0 + wn * WN + cc);
+#pragma unroll
+        for (int i = 0; i < WM / 4; ++i) {
+            const int rr = i * 4 + (lane >> 4);
+            const v4i raw = *reinterpret_cast<const v4i*>(stile + rr * ES + cc * 4);
+            epilogue4c<KIND>(a, p, rows[i], cols, m0 + wm * WM + rr, raw);
+        }
+    }
+}
+
+// ------------------------------------------------------ skinny-M (decode) kernel
+//
+// M <= 16*MT.  One workgroup owns 16 output columns n and all M rows; its W waves split K
+// into W contiguous ranges and stream their share of the 16 B rows straight from HBM into
+// MFMA registers (every B byte is read once), UNROLL k-steps of 64 in flight per wave.
+// A (M x K, a few KB) stays L2-resident.  Partial accumulators are summed through LDS.
+
+template <int MT, int W, int KIND>
+__global__ __launch_bounds__(64 * W) void gemm_i8_skinny_kernel(GemmArgs a) {
+    constexpr int UNROLL = 8;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int n0 = blockIdx.x * 16;
+    const int nrow = n0 + (lane & 15);
+    const int kg = (lane >> 4) * 16;
+
+    const int ksteps = (a.K + 63) / 64;
+    const int per_wave = (ksteps + W - 1) / W;
+    const int ks_begin = wave * per_wave;
+    const int ks_end = min(ksteps, ks_begin + per_wave);
+
+    v4i acc[MT];
+#pragma unroll
+    for (int t = 0; t < MT; ++t) acc[t] = v4i{0, 0, 0, 0};
+
+    const int8_t* brow = a.B + (int64_t)nrow * a.ldb;
+    const bool nrow_ok = nrow < a.N;
+    for (int ks = ks_begin; ks < ks_end; ks += UNROLL) {
+        v4i bf[UNROLL], af[UNROLL][MT];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const int k = (ks + u) * 64 + kg;
+            const bool ok = (ks + u < ks_end) && k < a.K;
+            bf[u] = (ok && nrow_ok) ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(brow + k))
+                                    : v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int t = 0; t < MT; ++t) {
+                const int m = t * 16 + (lane & 15);
+                af[u][t] = (ok && m < a.M) ? *reinterpret_cast<const v4i*>(a.A + (int64_t)m * a.lda + k)
+                                           : v4i{0, 0, 0, 0};
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+            for (int t = 0; t < MT; ++t)
+                acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[u], af[u][t], acc[t], 0, 0, 0);
+    }
+
+    if (W > 1) {
+        __shared__ v4i red[W][MT][64];
+#pragma unroll
+        for (int t = 0; t < MT; ++t) red[wave][t][lane] = acc[t];
+        __syncthreads();
+        if (wave != 0) return;
+#pragma unroll
+        for (int t = 0; t < MT; ++t) {
+            v4i s = red[0][t][lane];
+            for (int w = 1; w < W; ++w) s += red[w][t][lane];
+            acc[t] = s;
+        }
+    }
+
+    const EpiParams p = epi_params(a);
+#pragma unroll
+    for (int t = 0; t < MT; ++t) {
+        const int m = t * 16 + (lane & 15);
+        const int n = n0 + (lane >> 4) * 4;
+        epilogue4<KIND>(a, p, m, n, acc[t]);
+    }
+}
+
+// ------------------------------------------------------------ generic kernel
+// Any K, alignment and leading dimensions (byte loads, dot4 on the fly): the fallback for
+// shapes the vector paths do not take.  One thread per output.
+template <int KIND>
+__global__ __launch_bounds__(256) void gemm_i8_generic_kernel(GemmArgs a) {
+    const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= (int64_t)a.M * a.N) return;
+    const int m = (int)(idx / a.N), n = (int)(idx % a.N);
+    const int8_t* ar = a.A + (int64_t)m * a.lda;
+    const int8_t* br = a.B + (int64_t)n * a.ldb;
+    uint32_t s = 0;
+    for (int k = 0; k < a.K; ++k) s += (uint32_t)((int)ar[k] * (int)br[k]);
+    const EpiParams p = epi_params(a);
+    int32_t acc = corrected((int32_t)s, m, n, a, p);
+    const float sa = a.a_scale ? a.a_scale[(int64_t)m * a.a_stride] : 1.0f;
+    const float sb = a.b_scale ? a.b_scale[(int64_t)n * a.b_stride] : 1.0f;
+    store_elem<KIND>(a.C, (int64_t)m * a.ldc + n,
+                     epi_one<KIND>(acc, sa, sb, a.bias ? a.bias + n : nullptr, a.relu != 0, p));
+}
+
+// ------------------------------------------------------------------ row sums
+// sums[r] = sum_k X[r,k] (int8), one wave per row.
+__global__ __launch_bounds__(256) void row_sums_i8_kernel(const int8_t* __restrict__ X, int64_t ld,
+                                                          int64_t rows, int64_t K,
+                                                          int32_t* __restrict__ sums) {
+    const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    const int8_t* x = X + r * ld;
+    int s = 0;
+    for (int64_t k = lane; k < K; k += 64) s += x[k];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if (lane == 0) sums[r] = s;
+}
+
+// ------------------------------------------------------------------- dispatch
+
+template <int KIND>
+struct GemmLaunch {
+    static int run(const GemmArgs& a0, hipStream_t st, int64_t workspace_split_bytes) {
+        GemmArgs a = a0;
+        const bool vec = aligned16(a.A) && aligned16(a.B) && (a.lda % 16 == 0) && (a.ldb % 16 == 0) &&
+                         (a.K % 16 == 0);
+        if (!vec) {
+            const int64_t total = (int64_t)a.M * a.N;
+            hipLaunchKernelGGL(gemm_i8_generic_kernel<KIND>, dim3((unsigned)((total + 255) / 256)),
+                               dim3(256), 0, st, a);
+            return launch_status("lq_gemm_w8a8 (generic)");
+        }
+        if (a.M <= 16) {
+            hipLaunchKernelGGL((gemm_i8_skinny_kernel<1, 8, KIND>), dim3((unsigned)((a.N + 15) / 16)),
+                               dim3(512), 0, st, a);
+            return launch_status("lq_gemm_w8a8 (skinny)");
+        }
+        if (a.M <= 32) {
+            hipLaunchKernelGGL((gemm_i8_skinny_kernel<2, 8, KIND>), dim3((unsigned)((a.N + 15) / 16)),
+                               dim3(512), 0, st, a);
+            return launch_status("lq_gemm_w8a8 (skinny)");
+        }
+        if (a.M <= 64) {
+            hipLaunchKernelGGL((gemm_i8_skinny_kernel<4, 8, KIND>), dim3((unsigned)((a.N + 15) / 16)),
+                               dim3(512), 0, st, a);
+            return launch_status("lq_gemm_w8a8 (skinny)");
+        }
+        // LDS-DMA path: whole 128-byte K stages, 32-bit buffer offsets.
+        const bool dma_ok = (a.K % 128 == 0) && ((int64_t)(a.M + 256) * a.lda < (int64_t)1 << 31) &&
+                            ((int64_t)(a.N + 256) * a.ldb < (int64_t)1 << 31);
+        const int64_t dma_tiles = ((int64_t)(a.M + 255) / 256) * ((a.N + 127) / 128);
+        if (dma_ok && dma_tiles >= 256) {
+            hipLaunchKernelGGL((gemm_i8_dma_kernel<256, 128, 4, 2, KIND>), dim3((unsigned)dma_tiles),
+                               dim3(512), 0, st, a);
+            return launch_status("lq_gemm_w8a8 (dma 256x128)");
+        }
+        const int64_t dma_tiles_128 = ((int64_t)(a.M + 127) / 128) * ((a.N + 127) / 128);
+        if (dma_ok && dma_tiles_128 >= 128) {
+            hipLaunchKernelGGL((gemm_i8_dma_kernel<128, 128, 4, 2, KIND>), dim3((unsigned)dma_tiles_128),
+                               dim3(512), 0, st, a);
+            return launch_status("lq_gemm_w8a8 (dma 128x128)");
+        }
+        const int64_t mid_tiles = ((int64_t)(a.M + 127) / 128) * ((a.N + 127) / 128);
+        int splits = 1;
+        const int nk = (a.K + BK - 1) / BK;
+        if (mid_tiles < 256 && workspace_split_bytes > 0) {
+            splits = (int)((256 + mid_tiles - 1) / mid_tiles);
+            if (splits > nk / 4) splits = nk / 4;  // keep at least 4 stages per split
+            if (splits < 1) splits = 1;
+        }
+        a.splits = splits;
+        if (splits > 1) {
+            int rc = lq_fill_u32(a.partial, 0u, (size_t)a.M * a.N, st);
+            if (rc) return rc;
+            rc = lq_fill_u32(a.counters, 0u, (size_t)mid_tiles, st);
+            if (rc) return rc;
+        }
+        hipLaunchKernelGGL((gemm_i8_tiled_kernel<128, 128, 2, 2, KIND>),
+                           dim3((unsigned)(mid_tiles * splits)), dim3(256), 0, st, a);
+        return launch_status("lq_gemm_w8a8 (128x128)");
+    }
+};
+
+static bool valid_out_kind(int k) { return k >= LQ_OUT_I32 && k <= LQ_OUT_QU8S8; }
+
+// Workspace layout: [a_sums M][b_sums N][split partial M*N][tile counters], 256-byte aligned parts.
+struct GemmWs {
+    size_t a_sums, b_sums, partial, counters, total;
+};
+static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+static GemmWs gemm_ws(int64_t M, int64_t N) {
+    GemmWs w;
+    w.a_sums = 0;
+    w.b_sums = w.a_sums + align256(sizeof(int32_t) * (size_t)M);
+    w.partial = w.b_sums + align256(sizeof(int32_t) * (size_t)N);
+    const bool may_split = M > 64 && ((M + 127) / 128) * ((N + 127) / 128) < 256;
+    w.counters = w.partial + (may_split ? align256(sizeof(int32_t) * (size_t)(M * N)) : 0);
+    const size_t tiles = (size_t)(((M + 127) / 128) * ((N + 127) / 128));
+    w.total = w.counters + (may_split ? align256(sizeof(uint32_t) * tiles) : 0);
+    return w;
+}
+
+}  // namespace lq
+
+using namespace lq;
+
+extern "C" {
+
+int lq_row_sums_i8(const int8_t* d_X, int64_t ld, int64_t rows, int64_t K, int32_t* d_sums,
+                   void* stream) {
+    LQ_REQUIRE(rows >= 0 && K >= 0 && ld >= K, "lq_row_sums_i8: bad shape");
+    if (rows == 0) return LQ_OK;
+    LQ_REQUIRE(d_sums && (K == 0 || d_X), "lq_row_sums_i8: NULL pointer");
+    hipLaunchKernelGGL(row_sums_i8_kernel, dim3((unsigned)((rows + 3) / 4)), dim3(256), 0,
+                       as_stream(stream), d_X, ld, rows, K, d_sums);
+    return launch_status("lq_row_sums_i8");
+}
+
+size_t lq_gemm_w8a8_workspace_size(int64_t M, int64_t N, int64_t K) {
+    (void)K;
+    if (M < 0 || N < 0) return 0;
+    return gemm_ws(M, N).total;
+}
+
+int lq_gemm_w8a8(const int8_t* d_A, int64_t lda, const int8_t* d_B, int64_t ldb, void* d_C,
+                 int64_t ldc, int64_t M, int64_t N, int64_t K, const float* d_a_scale,
+                 int64_t a_scale_stride, const float* d_b_scale, int64_t b_scale_stride,
+                 const float* d_a_zero_point, const float* d_b_zero_point, const int32_t* d_b_sums,
+                 const float* d_bias, const float* d_out_scale, const float* d_out_zero_point,
+                 int out_qmin, int out_qmax, int out_kind, int flags, void* d_workspace,
+                 size_t workspace_bytes, void* stream) {
+    LQ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "lq_gemm_w8a8: negative size");
+    LQ_REQUIRE(M <= 0x7fffffff && N <= 0x7fffffff && K <= 0x7fffffff, "lq_gemm_w8a8: size too large");
+    if (M == 0 || N == 0) return LQ_OK;
+    LQ_REQUIRE(d_C, "lq_gemm_w8a8: NULL output");
+    LQ_REQUIRE(K == 0 || (d_A && d_B), "lq_gemm_w8a8: NULL operand");
+    LQ_REQUIRE(lda >= K && ldb >= K && ldc >= N, "lq_gemm_w8a8: leading dimension too small");
+    LQ_REQUIRE(valid_out_kind(out_kind), "lq_gemm_w8a8: bad out_kind");
+    LQ_REQUIRE(a_scale_stride == 0 || a_scale_stride == 1, "lq_gemm_w8a8: a_scale_stride must be 0 or 1");
+    LQ_REQUIRE(b_scale_stride == 0 || b_scale_stride == 1, "lq_gemm_w8a8: b_scale_stride must be 0 or 1");
+    const bool requant = out_kind == LQ_OUT_Q8 || out_kind == LQ_OUT_QU8 || out_kind == LQ_OUT_Q16 ||
+                         out_kind == LQ_OUT_QU8S8 || out_kind == LQ_OUT_FQ32;
+    LQ_REQUIRE(!requant || d_out_scale, "lq_gemm_w8a8: requantizing output needs d_out_scale");
+    LQ_REQUIRE(!requant || out_qmax >= out_qmin, "lq_gemm_w8a8: out_qmax < out_qmin");
+    LQ_REQUIRE((flags & ~LQ_EPI_RELU) == 0, "lq_gemm_w8a8: unknown flags");
+    const GemmWs ws = gemm_ws(M, N);
+    LQ_REQUIRE(d_workspace || workspace_bytes == 0, "lq_gemm_w8a8: NULL workspace with nonzero size");
+    const bool need_asums = d_b_zero_point != nullptr;
+    const bool need_bsums = d_a_zero_point != nullptr && d_b_sums == nullptr;
+    if (need_asums || need_bsums)
+        LQ_REQUIRE(d_workspace && workspace_bytes >= ws.partial,
+                   "lq_gemm_w8a8: zero-point correction needs the workspace (lq_gemm_w8a8_workspace_size)");
+
+    hipStream_t st = as_stream(stream);
+    GemmArgs a{};
+    a.A = d_A;
+    a.B = d_B;
+    a.C = d_C;
+    a.lda = lda;
+    a.ldb = ldb;
+    a.ldc = ldc;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.a_scale = d_a_scale;
+    a.b_scale = d_b_scale;
+    a.a_stride = (int)a_scale_stride;
+    a.b_stride = (int)b_scale_stride;
+    a.a_zp = d_a_zero_point;
+    a.b_zp = d_b_zero_point;
+    a.bias = d_bias;
+    a.out_scale = d_out_scale;
+    a.out_zp = d_out_zero_point;
+    a.qmin = out_qmin;
+    a.qmax = out_qmax;
+    a.out_kind = out_kind;
+    a.relu = (flags & LQ_EPI_RELU) ? 1 : 0;
+    a.splits = 1;
+    char* wsb = (char*)d_workspace;
+    int rc;
+    if (need_asums) {
+        a.a_sums = (int32_t*)(wsb + ws.a_sums);
+        if ((rc = lq_row_sums_i8(d_A, lda, M, K, (int32_t*)a.a_sums, stream))) return rc;
+    }
+    if (d_a_zero_point) {
+        if (d_b_sums) {
+            a.b_sums = d_b_sums;
+        } else {
+            a.b_sums = (int32_t*)(wsb + ws.b_sums);
+            if ((rc = lq_row_sums_i8(d_B, ldb, N, K, (int32_t*)a.b_sums, stream))) return rc;
+        }
+    }
+    int64_t split_bytes = 0;
+    if (d_workspace && workspace_bytes >= ws.total && ws.total > ws.counters) {
+        a.partial = (int32_t*)(wsb + ws.partial);
+        a.counters = (uint32_t*)(wsb + ws.counters);
+        split_bytes = (int64_t)(ws.total - ws.partial);
+    }
+    switch (out_kind) {
+    case LQ_OUT_I32: return GemmLaunch<LQ_OUT_I32>::run(a, st, split_bytes);
+    case LQ_OUT_F32: return GemmLaunch<LQ_OUT_F32>::run(a, st, split_bytes);
+    case LQ_OUT_F16: return GemmLaunch<LQ_OUT_F16>::run(a, st, split_bytes);
+    case LQ_OUT_Q8: return GemmLaunch<LQ_OUT_Q8>::run(a, st, split_bytes);
+    case LQ_OUT_QU8: return GemmLaunch<LQ_OUT_QU8>::run(a, st, split_bytes);
+    case LQ_OUT_FQ32: return GemmLaunch<LQ_OUT_FQ32>::run(a, st, split_bytes);
+    case LQ_OUT_Q16: return GemmLaunch<LQ_OUT_Q16>::run(a, st, split_bytes);
+    case LQ_OUT_QU8S8: return GemmLaunch<LQ_OUT_QU8S8>::run(a, st, split_bytes);
+    default: return set_error(LQ_ERR_INVALID, "lq_gemm_w8a8: bad out_kind");
+    }
+}
+
+}  // extern "C"

@@ -286,7 +286,7 @@ static PcPlan pc_plan(int64_t outer, int64_t C, int64_t inner) {
     } else {
         int64_t width = C * inner;
         int64_t tiles = (width + kBlock - 1) / kBlock;
-        int64_t want = (tiles >= 1024) ? 1 : (1024 + tiles - 1) / tiles;
+        int64_t want = (tiles >= 1024 || tiles == 0) ? 1 : (1024 + tiles - 1) / tiles;
         int64_t max_by_work = outer / 64;
         if (want > max_by_work) want = max_by_work;
         if (want < 1) want = 1;

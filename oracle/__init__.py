@@ -47,7 +47,7 @@ _LIB_PATH = os.path.join(_HERE, "liblq_oracle.so")
 # Element-type codes shared with include/lq_api.h.
 I8, U8, I16, I32, F16, F32, U8S8 = 1, 2, 3, 4, 5, 6, 7
 OBS_MINMAX, OBS_EMA, OBS_REPLACE = 0, 1, 2
-OUT_I32, OUT_F32, OUT_F16, OUT_Q8, OUT_QU8, OUT_FQ32, OUT_Q16 = 0, 1, 2, 3, 4, 5, 6
+OUT_I32, OUT_F32, OUT_F16, OUT_Q8, OUT_QU8, OUT_FQ32, OUT_Q16, OUT_QU8S8 = 0, 1, 2, 3, 4, 5, 6, 7
 
 _CODE_NP = {I8: np.int8, U8: np.uint8, I16: np.int16, I32: np.int32, U8S8: np.int8}
 
@@ -93,6 +93,8 @@ def _declare(L: ctypes.CDLL) -> None:
     L.lqo_gemm_w8a8.argtypes = [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P,
                                 _I64, _F, _P, _P, _F, _F, _I, _I, _I, _I]
     L.lqo_gemm_w8a8.restype = _I
+    L.lqo_gemm_epilogue.argtypes = [_P, _I64, _I64, _P, _I64, _P, _I64, _P, _F, _F, _I, _I, _I, _I,
+                                    _P, _I64]
     L.lqo_gemv_w8.argtypes = [_P, _I64, _I64, _P, _I64, _P, _P, _P, _I, _P]
     L.lqo_group_quantize.argtypes = [_P, _I64, _I64, _I, _I, _P, _P, _P]
     L.lqo_group_dequantize.argtypes = [_P, _P, _P, _I64, _I64, _I, _I, _P]
@@ -251,7 +253,7 @@ def gemm_acc(A: np.ndarray, B: np.ndarray, za: int = 0, zb=None) -> np.ndarray:
 
 
 _OUT_NP = {OUT_I32: np.int32, OUT_F32: np.float32, OUT_F16: np.uint16, OUT_Q8: np.int8,
-           OUT_QU8: np.uint8, OUT_FQ32: np.float32, OUT_Q16: np.int16}
+           OUT_QU8: np.uint8, OUT_FQ32: np.float32, OUT_Q16: np.int16, OUT_QU8S8: np.int8}
 
 
 def gemm_w8a8(A, B, a_scale, b_scale, za=0.0, zb=None, bias=None, out_scale=1.0, out_zp=0.0,
@@ -273,6 +275,21 @@ def gemm_w8a8(A, B, a_scale, b_scale, za=0.0, zb=None, bias=None, out_scale=1.0,
                               out_kind, int(relu))
     if ovf:
         raise OverflowError("int32 accumulator overflow")
+    return C.view(np.float16) if out_kind == OUT_F16 else C
+
+
+def gemm_epilogue(acc, a_scale, b_scale, bias=None, out_scale=1.0, out_zp=0.0, qmin=-128,
+                  qmax=127, out_kind=OUT_F32, relu=False) -> np.ndarray:
+    """The W8A8 epilogue applied to a precomputed int32 accumulator [M, N]."""
+    acc = np.ascontiguousarray(acc, np.int32)
+    M, N = acc.shape
+    a_scale = _f32(np.atleast_1d(a_scale))
+    b_scale = _f32(np.atleast_1d(b_scale))
+    C = np.empty((M, N), _OUT_NP[out_kind])
+    lib().lqo_gemm_epilogue(_ptr(acc), M, N, _ptr(a_scale), 0 if a_scale.size == 1 else 1,
+                            _ptr(b_scale), 0 if b_scale.size == 1 else 1,
+                            _ptr(None if bias is None else _f32(bias)), np.float32(out_scale),
+                            np.float32(out_zp), qmin, qmax, out_kind, int(relu), _ptr(C), N)
     return C.view(np.float16) if out_kind == OUT_F16 else C
 
 

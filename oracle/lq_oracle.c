@@ -24,7 +24,7 @@
 enum { O_I8 = 1, O_U8 = 2, O_I16 = 3, O_I32 = 4, O_F16 = 5, O_F32 = 6, O_U8S8 = 7 };
 enum { O_OBS_MINMAX = 0, O_OBS_EMA = 1, O_OBS_REPLACE = 2 };
 enum { O_OUT_I32 = 0, O_OUT_F32 = 1, O_OUT_F16 = 2, O_OUT_Q8 = 3, O_OUT_QU8 = 4,
-       O_OUT_FQ32 = 5, O_OUT_Q16 = 6 };
+       O_OUT_FQ32 = 5, O_OUT_Q16 = 6, O_OUT_QU8S8 = 7 };
 
 /* ---------------------------------------------------------------- scalar rules */
 
@@ -320,6 +320,7 @@ static void gemm_epilogue_one(int32_t acc, float sa, float sb, const float* bias
         if (out_kind == O_OUT_Q8) ((int8_t*)C)[idx] = (int8_t)satcast(c, -128, 127);
         else if (out_kind == O_OUT_QU8) ((uint8_t*)C)[idx] = (uint8_t)satcast(c, 0, 255);
         else if (out_kind == O_OUT_Q16) ((int16_t*)C)[idx] = (int16_t)satcast(c, -32768, 32767);
+        else if (out_kind == O_OUT_QU8S8) ((int8_t*)C)[idx] = (int8_t)(satcast(c, 0, 255) - 128);
         else { /* FQ32 */
             float d = c - out_z;
             ((float*)C)[idx] = d * out_s;
@@ -351,6 +352,20 @@ int lqo_gemm_w8a8(const int8_t* A, int64_t lda, const int8_t* B, int64_t ldb, vo
     free(acc);
     free(zb);
     return ovf;
+}
+
+/* Epilogue of the W8A8 contract over a precomputed (already zero-point corrected) int32
+ * accumulator acc[M,N]: the same per-element steps as lqo_gemm_w8a8. */
+void lqo_gemm_epilogue(const int32_t* acc, int64_t M, int64_t N, const float* a_scale,
+                       int64_t a_stride, const float* b_scale, int64_t b_stride,
+                       const float* bias, float out_scale, float out_zp, int qmin, int qmax,
+                       int out_kind, int relu, void* C, int64_t ldc) {
+    float out_inv = 1.0f / out_scale;
+    for (int64_t m = 0; m < M; ++m)
+        for (int64_t n = 0; n < N; ++n)
+            gemm_epilogue_one(acc[m * N + n], a_scale[m * a_stride], b_scale[n * b_stride], bias,
+                              n, out_inv, out_scale, out_zp, qmin, qmax, out_kind, relu, C,
+                              m * ldc + n);
 }
 
 /* ------------------------------------------------- weight-only GEMV (fp64 sum) */

@@ -58,3 +58,18 @@ def test_cpu_tensor_ops_fail_loudly():
         Q.quantize(x, 0.1, 0, Q.qint8)
     with pytest.raises(L.LucidError, match="GPU tensors"):
         Q.MinMaxObserver()(x)
+
+
+def test_workspace_queries_on_degenerate_shapes():
+    """Host-side planning of empty / tiny shapes (no GPU call): sizes are finite and the
+    query does not divide by zero for an empty channel extent."""
+    from lucid_amd import _C
+
+    L = _C.lib()
+    for outer, C, inner in ((1, 2, 0), (0, 3, 5), (0, 1, 100), (4, 1, 0), (2, 4096, 1)):
+        assert L.lq_minmax_per_channel_workspace_size(outer, C, inner) >= 0
+    assert L.lq_minmax_workspace_size(0) > 0
+    for M, N, K in ((0, 0, 0), (1, 1, 1), (4096, 4096, 4096), (128, 4096, 4096)):
+        assert L.lq_gemm_w8a8_workspace_size(M, N, K) >= 0
+    # split-K partials are only planned for mid-size M with few 128x128 tiles
+    assert L.lq_gemm_w8a8_workspace_size(128, 4096, 4096) >= 128 * 4096 * 4

@@ -1,0 +1,231 @@
+"""GPU parity of the W8A8 int8 MFMA GEMM (lq_gemm_w8a8) through the C ABI.
+
+* int32 accumulators: bit-exact against the oracle's int64 brute force on every kernel
+  path (skinny M <= 64; LDS-DMA 256x128 and 128x128 tiles; register-staged 128x128 tiles
+  with and without split-K; generic);
+* every epilogue kind (f32, f16, requantized int8 / uint8 / int16 / uint8-as-int8,
+  fake-quantized f32) with activation and weight zero points, bias and ReLU: bit-exact
+  against the oracle's epilogue (same op order, no FMA);
+* BASELINE sizes (4096^3, 4096x11008): size-independent properties -- every row sum and
+  column sum of C against A @ colsum(B) and B @ colsum(A) in int64, plus sampled rows
+  exactly.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _dev(L, arr):
+    return L.tensor(np.ascontiguousarray(arr), device="gpu")
+
+
+_OUT_DT = {O.OUT_I32: np.int32, O.OUT_F32: np.float32, O.OUT_F16: np.float16, O.OUT_Q8: np.int8,
+           O.OUT_QU8: np.uint8, O.OUT_FQ32: np.float32, O.OUT_Q16: np.int16, O.OUT_QU8S8: np.int8}
+
+
+def run_gemm(L, A, B, out_kind=O.OUT_I32, a_scale=None, b_scale=None, za=None, zb=None,
+             b_sums=None, bias=None, out_scale=None, out_zp=None, qmin=-128, qmax=127,
+             relu=False, lda=None, ldb=None, ldc=None, workspace=True):
+    """Run lq_gemm_w8a8 on host arrays; returns C [M, N] as numpy."""
+    from lucid_amd import _C
+
+    M, K = A.shape
+    N = B.shape[0]
+    lda = lda or K
+    ldb = ldb or K
+    ldc = ldc or N
+    Ap = np.zeros((M, lda), np.int8)
+    Ap[:, :K] = A
+    Bp = np.zeros((N, ldb), np.int8)
+    Bp[:, :K] = B
+    dA, dB = _dev(L, Ap), _dev(L, Bp)
+    dC = L.empty((M, ldc), _OUT_DT[out_kind], "gpu")
+    keep = []
+
+    def opt(a, dt=np.float32):
+        if a is None:
+            return None
+        t = _dev(L, np.asarray(a, dt))
+        keep.append(t)
+        return t.data_ptr()
+
+    sa = None if a_scale is None else np.atleast_1d(np.asarray(a_scale, np.float32))
+    sb = None if b_scale is None else np.atleast_1d(np.asarray(b_scale, np.float32))
+    ws_bytes = _C.lib().lq_gemm_w8a8_workspace_size(M, N, K) if workspace else 0
+    ws = L.empty((max(ws_bytes, 1),), np.uint8, "gpu") if workspace else None
+    _C.call("lq_gemm_w8a8", dA.data_ptr(), lda, dB.data_ptr(), ldb, dC.data_ptr(), ldc, M, N, K,
+            opt(sa), 0 if sa is None or sa.size == 1 else 1, opt(sb),
+            0 if sb is None or sb.size == 1 else 1,
+            opt(None if za is None else [za]), opt(zb), opt(b_sums, np.int32), opt(bias),
+            opt(None if out_scale is None else [out_scale]),
+            opt(None if out_zp is None else [out_zp]), qmin, qmax, out_kind, 1 if relu else 0,
+            ws.data_ptr() if ws is not None else None, ws_bytes, None)
+    return dC.numpy()[:, :N]
+
+
+KINDS = [O.OUT_F32, O.OUT_F16, O.OUT_Q8, O.OUT_QU8, O.OUT_FQ32, O.OUT_Q16, O.OUT_QU8S8, O.OUT_I32]
+GRID = {O.OUT_Q8: (-128, 127), O.OUT_QU8: (0, 255), O.OUT_FQ32: (0, 255), O.OUT_Q16: (0, 255),
+        O.OUT_QU8S8: (0, 255)}
+
+
+def _codes(rng, shape, lo=-127, hi=127):
+    return rng.integers(lo, hi + 1, size=shape, dtype=np.int64).astype(np.int8)
+
+
+# Shapes chosen to hit every dispatch path of the kernel selector:
+#   M <= 16 / 32 / 64 -> skinny (1, 2, 4 m-tiles); K % 128 == 0 with enough tiles -> LDS-DMA
+#   256x128 / 128x128; otherwise register-staged 128x128 (split-K when tiles are few);
+#   K % 16 != 0 or unaligned -> generic.
+ACC_SHAPES = [
+    (1, 64, 64), (1, 1000, 784), (3, 4096, 512), (16, 256, 4096), (17, 100, 256),
+    (32, 48, 1024), (33, 160, 640), (64, 10, 256), (64, 256, 784), (65, 130, 96),
+    (128, 4096, 2048), (300, 520, 1040), (200, 300, 16), (5, 7, 13), (33, 40, 30),
+    (1, 1, 1), (7, 9, 0),
+]
+
+
+@pytest.mark.parametrize("M,N,K", ACC_SHAPES)
+def test_int32_accumulator_exact(gpu, M, N, K):
+    rng = np.random.default_rng(M * 7919 + N * 31 + K)
+    A = _codes(rng, (M, K), -128, 127)
+    B = _codes(rng, (N, K), -128, 127)
+    print(f"gemm acc M={M} N={N} K={K}", flush=True)
+    C = run_gemm(gpu, A, B)
+    np.testing.assert_array_equal(C, O.gemm_acc(A, B))
+
+
+def test_int32_accumulator_staged_many_tiles(gpu):
+    """Many tiles with K % 128 != 0 (register-staged path) and ragged M, N and K."""
+    rng = np.random.default_rng(5)
+    M, N, K = 2000, 6400, 400
+    A = _codes(rng, (M, K))
+    B = _codes(rng, (N, K))
+    C = run_gemm(gpu, A, B)
+    np.testing.assert_array_equal(C, O.gemm_acc(A, B))
+
+
+@pytest.mark.parametrize("M,N,K", [(1500, 2900, 256), (2000, 6400, 384), (257, 16384, 128),
+                                   (4096, 4100, 128), (1000, 2100, 256), (300, 7000, 128)])
+def test_int32_accumulator_dma_path(gpu, M, N, K):
+    """The LDS-DMA 256x128 path (K % 128 == 0, >= 128 tiles) with ragged M and N: rows past
+    M or N come in as zeros through the buffer bounds and are never stored."""
+    rng = np.random.default_rng(M + N + K)
+    A = _codes(rng, (M, K), -128, 127)
+    B = _codes(rng, (N, K), -128, 127)
+    print(f"gemm dma acc M={M} N={N} K={K}", flush=True)
+    C = run_gemm(gpu, A, B)
+    np.testing.assert_array_equal(C, O.gemm_acc(A, B))
+
+
+@pytest.mark.parametrize("kind", KINDS)
+def test_epilogue_kinds_dma_path(gpu, kind):
+    """Every output kind through the LDS-staged epilogue of the DMA path (ragged N)."""
+    rng = np.random.default_rng(1000 + kind)
+    M, N, K = 600, 8200, 128
+    A = _codes(rng, (M, K), -128, 127)
+    B = _codes(rng, (N, K), -127, 127)
+    a_scale = rng.uniform(1e-3, 1e-1, M).astype(np.float32)
+    b_scale = rng.uniform(1e-3, 1e-1, N).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    qmin, qmax = GRID.get(kind, (-128, 127))
+    out_scale, out_zp = 0.37, (128.0 if qmin == 0 else -3.0)
+    zb = rng.integers(-3, 4, N).astype(np.float32)
+    for za, zbv, with_bias, relu in ((None, None, True, False), (-5.0, zb, False, True)):
+        acc = O.gemm_acc(A, B, 0 if za is None else int(za), None if zbv is None else zbv.astype(np.int32))
+        got = run_gemm(gpu, A, B, kind, a_scale, b_scale, za, zbv, None,
+                       bias if with_bias else None, out_scale, out_zp, qmin, qmax, relu)
+        want = O.gemm_epilogue(acc, a_scale, b_scale, bias if with_bias else None, out_scale,
+                               out_zp, qmin, qmax, kind, relu)
+        if kind == O.OUT_F16:
+            np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+        else:
+            np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8))
+
+
+def test_leading_dimensions(gpu):
+    rng = np.random.default_rng(9)
+    for (M, N, K) in ((8, 70, 256), (100, 200, 512), (600, 900, 256)):
+        A = _codes(rng, (M, K))
+        B = _codes(rng, (N, K))
+        C = run_gemm(gpu, A, B, lda=K + 32, ldb=K + 48, ldc=N + 4)
+        np.testing.assert_array_equal(C, O.gemm_acc(A, B))
+        C = run_gemm(gpu, A, B, lda=K + 3, ldc=N + 1)  # unaligned rows -> generic path
+        np.testing.assert_array_equal(C, O.gemm_acc(A, B))
+
+
+
+
+@pytest.mark.parametrize("M,N,K", [(8, 200, 512), (96, 200, 512), (7, 9, 20), (300, 1000, 256)])
+@pytest.mark.parametrize("kind", KINDS)
+def test_epilogue_kinds_exact(gpu, M, N, K, kind):
+    rng = np.random.default_rng(M + N + K + kind)
+    # activations on an unsigned grid kept as (c - 128) int8 with za' = za - 128
+    A = _codes(rng, (M, K), -128, 127)
+    B = _codes(rng, (N, K), -127, 127)
+    a_scale = rng.uniform(1e-3, 1e-1, M).astype(np.float32)
+    b_scale = rng.uniform(1e-3, 1e-1, N).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    qmin, qmax = GRID.get(kind, (-128, 127))
+    for za, zb, with_bias, relu in ((None, None, True, False), (-5.0, None, True, True),
+                                    (3.0, rng.integers(-4, 5, N).astype(np.float32), False, True),
+                                    (None, rng.integers(-2, 3, N).astype(np.float32), True, False)):
+        out_scale, out_zp = 0.37, (128.0 if qmin == 0 else -3.0)
+        got = run_gemm(gpu, A, B, kind, a_scale, b_scale, za, zb, None,
+                       bias if with_bias else None, out_scale, out_zp, qmin, qmax, relu)
+        want = O.gemm_w8a8(A, B, a_scale, b_scale, za=0.0 if za is None else za, zb=zb,
+                           bias=bias if with_bias else None, out_scale=out_scale, out_zp=out_zp,
+                           qmin=qmin, qmax=qmax, out_kind=kind, relu=relu)
+        if kind == O.OUT_F16:
+            np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+        else:
+            np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8))
+
+
+def test_cached_weight_sums_and_scalar_scales(gpu):
+    """A caller-supplied sum_k B[n,k] (as a module caches it) and per-tensor scales."""
+    rng = np.random.default_rng(3)
+    M, N, K = 64, 256, 784
+    A = _codes(rng, (M, K))
+    B = _codes(rng, (N, K))
+    sums = B.astype(np.int64).sum(axis=1).astype(np.int32)
+    got = run_gemm(gpu, A, B, O.OUT_F32, np.float32(0.02), np.float32(0.03), za=7.0, b_sums=sums)
+    want = O.gemm_w8a8(A, B, np.float32(0.02), np.float32(0.03), za=7.0, out_kind=O.OUT_F32)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    # the library's own row sums
+    from lucid_amd import _C
+
+    dB = _dev(gpu, B)
+    out = gpu.empty((N,), np.int32, "gpu")
+    _C.call("lq_row_sums_i8", dB.data_ptr(), K, N, K, out.data_ptr(), None)
+    np.testing.assert_array_equal(out.numpy(), sums)
+
+
+def test_zero_point_needs_workspace(gpu):
+    from lucid_amd import _C
+
+    rng = np.random.default_rng(1)
+    A = _codes(rng, (4, 64))
+    B = _codes(rng, (8, 64))
+    with pytest.raises(_C.LucidError, match="workspace"):
+        run_gemm(gpu, A, B, O.OUT_F32, 1.0, 1.0, za=3.0, workspace=False)
+
+
+@pytest.mark.parametrize("M,N,K", [(4096, 4096, 4096), (4096, 11008, 4096), (4096, 4096, 11008),
+                                   (1024, 4096, 4096), (128, 4096, 4096), (16, 11008, 4096)])
+def test_baseline_sizes_checksums(gpu, M, N, K):
+    rng = np.random.default_rng(M + N + K)
+    A = _codes(rng, (M, K))
+    B = _codes(rng, (N, K))
+    print(f"gemm checksum M={M} N={N} K={K}", flush=True)
+    C = run_gemm(gpu, A, B).astype(np.int64)
+    A64, B64 = A.astype(np.int64), B.astype(np.int64)
+    np.testing.assert_array_equal(C.sum(axis=1), A64 @ B64.sum(axis=0))
+    np.testing.assert_array_equal(C.sum(axis=0), B64 @ A64.sum(axis=0))
+    rows = rng.choice(M, min(M, 24), replace=False)
+    np.testing.assert_array_equal(C[rows], A64[rows] @ B64.T)
