@@ -579,11 +579,222 @@ __global__ __launch_bounds__(kBlock) void fake_quant_kernel(const float* __restr
     }
 }
 
+// ------------------------------------------------ grouped (4-wide) vector kernels
+//
+// The aligned path of quantize / dequantize / fake-quantize.  Work is split into groups of
+// four consecutive elements, and every memory instruction is contiguous across the lanes
+// of a wave: float groups move as 16-byte vectors, code groups as 4 / 8 / 16-byte vectors
+// (1 / 2 / 4-byte codes).  Each thread keeps four groups in flight (grid-stride, unrolled
+// by four).  Qparams: per tensor (PT), one channel per group (PCG, inner % 4 == 0) or a
+// channel per element (PCE).  Elements past the last whole group are handled one by one.
+
+enum { PT = 0, PCG = 1, PCE = 2 };
+constexpr int kGrpUnroll = 4;
+
+template <int BYTES> struct RawVec;
+template <> struct RawVec<4> { typedef uint32_t T; };
+template <> struct RawVec<8> { typedef uint32_t T __attribute__((ext_vector_type(2))); };
+template <> struct RawVec<16> { typedef vu4 T; };
+
+template <class Code>
+struct Group4 {
+    typedef typename Code::T T;
+    typedef typename RawVec<4 * sizeof(T)>::T Raw;
+    union U {
+        Raw raw;
+        T v[4];
+    };
+};
+
+// Channel of element e of an [outer, C, inner] tensor (32-bit indices: n < 2^32).
+__device__ __forceinline__ uint32_t chan_of(uint32_t e, uint32_t C, uint32_t inner) {
+    return (e / inner) % C;
+}
+
+struct QArgs {
+    const float* d_scale;  // per tensor: [1] or NULL (then inv_value / scale_value); per channel: [C]
+    const float* d_zp;     // [1] / [C] or NULL (then zp_value)
+    float inv_value, scale_value, zp_value;
+    uint32_t C, inner;
+    __device__ __forceinline__ void tensor(float& inv, float& s, float& z) const {
+        if (d_scale) {
+            s = d_scale[0];
+            inv = 1.0f / s;
+        } else {
+            inv = inv_value;
+            s = scale_value;
+        }
+        z = d_zp ? d_zp[0] : zp_value;
+    }
+    __device__ __forceinline__ void channel(uint32_t c, float& inv, float& s, float& z) const {
+        s = d_scale[c];
+        inv = 1.0f / s;
+        z = d_zp ? d_zp[c] : zp_value;
+    }
+};
+
+template <int MODE>
+__device__ __forceinline__ void group_params(const QArgs& q, uint32_t e0, int j, float t_inv, float t_s,
+                                             float t_z, float& inv, float& s, float& z) {
+    if (MODE == PT) {
+        inv = t_inv;
+        s = t_s;
+        z = t_z;
+    } else {
+        q.channel(chan_of(e0 + (MODE == PCE ? j : 0), q.C, q.inner), inv, s, z);
+    }
+}
+
+template <class Code, int MODE>
+__global__ __launch_bounds__(kBlock) void quantize_g4_kernel(const float* __restrict__ x,
+                                                             typename Code::T* __restrict__ q,
+                                                             uint32_t n, QArgs qa, Grid g) {
+    typedef Group4<Code> G;
+    const uint32_t ng = n >> 2;
+    const uint32_t stride = gridDim.x * kBlock;
+    float t_inv = 0.f, t_s = 0.f, t_z = 0.f;
+    if (MODE == PT) qa.tensor(t_inv, t_s, t_z);
+    const vf4* x4 = reinterpret_cast<const vf4*>(x);
+    typename G::Raw* q4 = reinterpret_cast<typename G::Raw*>(q);
+    uint32_t i = blockIdx.x * kBlock + threadIdx.x;
+    auto one = [&](uint32_t gi, vf4 v) __attribute__((always_inline)) {
+        typename G::U o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float inv, s, z;
+            group_params<MODE>(qa, gi * 4, j, t_inv, t_s, t_z, inv, s, z);
+            o.v[j] = Code::store(quant_one<Code>(v[j], inv, z, g));
+        }
+        __builtin_nontemporal_store(o.raw, &q4[gi]);
+    };
+    for (; i + (kGrpUnroll - 1) * stride < ng; i += kGrpUnroll * stride) {
+        vf4 v[kGrpUnroll];
+#pragma unroll
+        for (int u = 0; u < kGrpUnroll; ++u) v[u] = __builtin_nontemporal_load(&x4[i + u * stride]);
+#pragma unroll
+        for (int u = 0; u < kGrpUnroll; ++u) one(i + u * stride, v[u]);
+    }
+    for (; i < ng; i += stride) one(i, __builtin_nontemporal_load(&x4[i]));
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
+        const uint32_t e = ng * 4 + threadIdx.x;
+        float inv, s, z;
+        if (MODE == PT) {
+            inv = t_inv;
+            z = t_z;
+        } else {
+            qa.channel(chan_of(e, qa.C, qa.inner), inv, s, z);
+        }
+        q[e] = Code::store(quant_one<Code>(x[e], inv, z, g));
+    }
+}
+
+template <class Code, typename Y, int MODE>
+__global__ __launch_bounds__(kBlock) void dequantize_g4_kernel(const typename Code::T* __restrict__ q,
+                                                               Y* __restrict__ y, uint32_t n, QArgs qa) {
+    typedef Group4<Code> G;
+    typedef typename RawVec<4 * sizeof(Y)>::T YRaw;
+    union YU {
+        YRaw raw;
+        Y v[4];
+    };
+    const uint32_t ng = n >> 2;
+    const uint32_t stride = gridDim.x * kBlock;
+    float t_inv = 0.f, t_s = 0.f, t_z = 0.f;
+    if (MODE == PT) qa.tensor(t_inv, t_s, t_z);
+    const typename G::Raw* q4 = reinterpret_cast<const typename G::Raw*>(q);
+    YRaw* y4 = reinterpret_cast<YRaw*>(y);
+    uint32_t i = blockIdx.x * kBlock + threadIdx.x;
+    auto one = [&](uint32_t gi, typename G::Raw raw) __attribute__((always_inline)) {
+        typename G::U in;
+        in.raw = raw;
+        YU o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float inv, s, z;
+            group_params<MODE>(qa, gi * 4, j, t_inv, t_s, t_z, inv, s, z);
+            const float d = Code::load(in.v[j]) - z;
+            o.v[j] = to_out<Y>(d * s);
+        }
+        __builtin_nontemporal_store(o.raw, &y4[gi]);
+    };
+    for (; i + (kGrpUnroll - 1) * stride < ng; i += kGrpUnroll * stride) {
+        typename G::Raw r[kGrpUnroll];
+#pragma unroll
+        for (int u = 0; u < kGrpUnroll; ++u) r[u] = __builtin_nontemporal_load(&q4[i + u * stride]);
+#pragma unroll
+        for (int u = 0; u < kGrpUnroll; ++u) one(i + u * stride, r[u]);
+    }
+    for (; i < ng; i += stride) one(i, __builtin_nontemporal_load(&q4[i]));
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
+        const uint32_t e = ng * 4 + threadIdx.x;
+        float inv, s, z;
+        if (MODE == PT) {
+            s = t_s;
+            z = t_z;
+        } else {
+            qa.channel(chan_of(e, qa.C, qa.inner), inv, s, z);
+        }
+        const float d = Code::load(q[e]) - z;
+        y[e] = to_out<Y>(d * s);
+    }
+}
+
+template <int MODE, bool MASK>
+__global__ __launch_bounds__(kBlock) void fake_quant_g4_kernel(const float* __restrict__ x,
+                                                               float* __restrict__ y,
+                                                               float* __restrict__ mask, uint32_t n,
+                                                               QArgs qa, Grid g) {
+    const uint32_t ng = n >> 2;
+    const uint32_t stride = gridDim.x * kBlock;
+    float t_inv = 0.f, t_s = 0.f, t_z = 0.f;
+    if (MODE == PT) qa.tensor(t_inv, t_s, t_z);
+    const vf4* x4 = reinterpret_cast<const vf4*>(x);
+    vf4* y4 = reinterpret_cast<vf4*>(y);
+    vf4* m4 = reinterpret_cast<vf4*>(mask);
+    uint32_t i = blockIdx.x * kBlock + threadIdx.x;
+    auto one = [&](uint32_t gi, vf4 v) __attribute__((always_inline)) {
+        vf4 o, mk;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            float inv, s, z, m;
+            group_params<MODE>(qa, gi * 4, j, t_inv, t_s, t_z, inv, s, z);
+            o[j] = fq_one(v[j], inv, s, z, g, m);
+            mk[j] = m;
+        }
+        __builtin_nontemporal_store(o, &y4[gi]);
+        if (MASK) __builtin_nontemporal_store(mk, &m4[gi]);
+    };
+    for (; i + (kGrpUnroll - 1) * stride < ng; i += kGrpUnroll * stride) {
+        vf4 v[kGrpUnroll];
+#pragma unroll
+        for (int u = 0; u < kGrpUnroll; ++u) v[u] = __builtin_nontemporal_load(&x4[i + u * stride]);
+#pragma unroll
+        for (int u = 0; u < kGrpUnroll; ++u) one(i + u * stride, v[u]);
+    }
+    for (; i < ng; i += stride) one(i, __builtin_nontemporal_load(&x4[i]));
+    if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
+        const uint32_t e = ng * 4 + threadIdx.x;
+        float inv, s, z, m;
+        if (MODE == PT) {
+            inv = t_inv;
+            s = t_s;
+            z = t_z;
+        } else {
+            qa.channel(chan_of(e, qa.C, qa.inner), inv, s, z);
+        }
+        y[e] = fq_one(x[e], inv, s, z, g, m);
+        if (MASK) mask[e] = m;
+    }
+}
+
 // ------------------------------------------------------------------- launch helpers
 
-static dim3 vec_grid(int64_t n) {
-    int64_t lanes = (n + kVec - 1) / kVec;
-    int64_t blocks = (lanes + kBlock - 1) / kBlock;
+// Grouped kernels: enough blocks to keep every CU streaming (8 blocks of 256 per CU),
+// never more than one group per thread.
+static dim3 g4_grid(int64_t n) {
+    int64_t groups = (n + 3) / 4;
+    int64_t blocks = (groups + kBlock - 1) / kBlock;
+    if (blocks > 2048) blocks = 2048;
     if (blocks < 1) blocks = 1;
     return dim3((unsigned)blocks);
 }
@@ -611,13 +822,26 @@ static int dispatch_code(int q_dtype, Args&&... args) {
     }
 }
 
+// Grouped path applies: 16-byte aligned float side, code side aligned for its group vector,
+// 32-bit element indices.
+template <class Code>
+static bool g4_ok(const void* f, const void* c, int64_t n) {
+    const uintptr_t ca = 4 * sizeof(typename Code::T) - 1;
+    return aligned16(f) && ((reinterpret_cast<uintptr_t>(c) & ca) == 0) && n < ((int64_t)1 << 32);
+}
+
 template <class Code>
 struct QuantPt {
     static int run(const float* x, void* q, int64_t n, PtParams pp, Grid g, hipStream_t st) {
         typedef typename Code::T T;
-        bool vec = aligned16(x) && aligned16(q);
-        dim3 grid = vec ? vec_grid(n) : scalar_grid(n);
-        hipLaunchKernelGGL(quantize_pt_kernel<Code>, grid, dim3(kBlock), 0, st, x, (T*)q, n, pp, g, vec);
+        if (g4_ok<Code>(x, q, n)) {
+            QArgs qa{pp.d_scale, pp.d_zp, pp.inv_value, pp.scale_value, pp.zp_value, 1u, 1u};
+            hipLaunchKernelGGL((quantize_g4_kernel<Code, PT>), g4_grid(n), dim3(kBlock), 0, st, x, (T*)q,
+                               (uint32_t)n, qa, g);
+        } else {
+            hipLaunchKernelGGL(quantize_pt_kernel<Code>, scalar_grid(n), dim3(kBlock), 0, st, x, (T*)q, n,
+                               pp, g, false);
+        }
         return launch_status("lq_quantize_per_tensor_f32");
     }
 };
@@ -627,10 +851,18 @@ struct QuantPc {
     static int run(const float* x, void* q, int64_t n, int64_t C, int64_t inner, const float* scale,
                    const float* zp, float zp_value, Grid g, hipStream_t st) {
         typedef typename Code::T T;
-        bool vec = aligned16(x) && aligned16(q) && (inner % kVec == 0);
-        dim3 grid = vec ? vec_grid(n) : scalar_grid(n);
-        hipLaunchKernelGGL(quantize_pc_kernel<Code>, grid, dim3(kBlock), 0, st, x, (T*)q, n, C, inner,
-                           scale, zp, zp_value, g, vec);
+        if (g4_ok<Code>(x, q, n)) {
+            QArgs qa{scale, zp, 0.f, 0.f, zp_value, (uint32_t)C, (uint32_t)inner};
+            if (inner % 4 == 0)
+                hipLaunchKernelGGL((quantize_g4_kernel<Code, PCG>), g4_grid(n), dim3(kBlock), 0, st, x,
+                                   (T*)q, (uint32_t)n, qa, g);
+            else
+                hipLaunchKernelGGL((quantize_g4_kernel<Code, PCE>), g4_grid(n), dim3(kBlock), 0, st, x,
+                                   (T*)q, (uint32_t)n, qa, g);
+        } else {
+            hipLaunchKernelGGL(quantize_pc_kernel<Code>, scalar_grid(n), dim3(kBlock), 0, st, x, (T*)q, n,
+                               C, inner, scale, zp, zp_value, g, false);
+        }
         return launch_status("lq_quantize_per_channel_f32");
     }
 };
@@ -639,14 +871,23 @@ template <class Code>
 struct DequantPt {
     static int run(const void* q, void* y, int y_dtype, int64_t n, PtParams pp, hipStream_t st) {
         typedef typename Code::T T;
-        bool vec = aligned16(q) && aligned16(y);
-        dim3 grid = vec ? vec_grid(n) : scalar_grid(n);
-        if (y_dtype == LQ_F32)
-            hipLaunchKernelGGL((dequantize_pt_kernel<Code, float>), grid, dim3(kBlock), 0, st,
-                               (const T*)q, (float*)y, n, pp, vec);
-        else
-            hipLaunchKernelGGL((dequantize_pt_kernel<Code, __half>), grid, dim3(kBlock), 0, st,
-                               (const T*)q, (__half*)y, n, pp, vec);
+        const bool y_ok = (y_dtype == LQ_F32) ? aligned16(y) : (((uintptr_t)y & 7) == 0);
+        const uintptr_t ca = 4 * sizeof(T) - 1;
+        if (y_ok && ((reinterpret_cast<uintptr_t>(q) & ca) == 0) && n < ((int64_t)1 << 32)) {
+            QArgs qa{pp.d_scale, pp.d_zp, pp.inv_value, pp.scale_value, pp.zp_value, 1u, 1u};
+            if (y_dtype == LQ_F32)
+                hipLaunchKernelGGL((dequantize_g4_kernel<Code, float, PT>), g4_grid(n), dim3(kBlock), 0, st,
+                                   (const T*)q, (float*)y, (uint32_t)n, qa);
+            else
+                hipLaunchKernelGGL((dequantize_g4_kernel<Code, __half, PT>), g4_grid(n), dim3(kBlock), 0,
+                                   st, (const T*)q, (__half*)y, (uint32_t)n, qa);
+        } else if (y_dtype == LQ_F32) {
+            hipLaunchKernelGGL((dequantize_pt_kernel<Code, float>), scalar_grid(n), dim3(kBlock), 0, st,
+                               (const T*)q, (float*)y, n, pp, false);
+        } else {
+            hipLaunchKernelGGL((dequantize_pt_kernel<Code, __half>), scalar_grid(n), dim3(kBlock), 0, st,
+                               (const T*)q, (__half*)y, n, pp, false);
+        }
         return launch_status("lq_dequantize_per_tensor");
     }
 };
@@ -656,17 +897,47 @@ struct DequantPc {
     static int run(const void* q, void* y, int y_dtype, int64_t n, int64_t C, int64_t inner,
                    const float* scale, const float* zp, float zp_value, hipStream_t st) {
         typedef typename Code::T T;
-        bool vec = aligned16(q) && aligned16(y) && (inner % kVec == 0);
-        dim3 grid = vec ? vec_grid(n) : scalar_grid(n);
-        if (y_dtype == LQ_F32)
-            hipLaunchKernelGGL((dequantize_pc_kernel<Code, float>), grid, dim3(kBlock), 0, st,
-                               (const T*)q, (float*)y, n, C, inner, scale, zp, zp_value, vec);
-        else
-            hipLaunchKernelGGL((dequantize_pc_kernel<Code, __half>), grid, dim3(kBlock), 0, st,
-                               (const T*)q, (__half*)y, n, C, inner, scale, zp, zp_value, vec);
+        const bool y_ok = (y_dtype == LQ_F32) ? aligned16(y) : (((uintptr_t)y & 7) == 0);
+        const uintptr_t ca = 4 * sizeof(T) - 1;
+        if (y_ok && ((reinterpret_cast<uintptr_t>(q) & ca) == 0) && n < ((int64_t)1 << 32)) {
+            QArgs qa{scale, zp, 0.f, 0.f, zp_value, (uint32_t)C, (uint32_t)inner};
+            const bool grp = inner % 4 == 0;
+            if (y_dtype == LQ_F32) {
+                if (grp)
+                    hipLaunchKernelGGL((dequantize_g4_kernel<Code, float, PCG>), g4_grid(n), dim3(kBlock), 0,
+                                       st, (const T*)q, (float*)y, (uint32_t)n, qa);
+                else
+                    hipLaunchKernelGGL((dequantize_g4_kernel<Code, float, PCE>), g4_grid(n), dim3(kBlock), 0,
+                                       st, (const T*)q, (float*)y, (uint32_t)n, qa);
+            } else {
+                if (grp)
+                    hipLaunchKernelGGL((dequantize_g4_kernel<Code, __half, PCG>), g4_grid(n), dim3(kBlock),
+                                       0, st, (const T*)q, (__half*)y, (uint32_t)n, qa);
+                else
+                    hipLaunchKernelGGL((dequantize_g4_kernel<Code, __half, PCE>), g4_grid(n), dim3(kBlock),
+                                       0, st, (const T*)q, (__half*)y, (uint32_t)n, qa);
+            }
+        } else if (y_dtype == LQ_F32) {
+            hipLaunchKernelGGL((dequantize_pc_kernel<Code, float>), scalar_grid(n), dim3(kBlock), 0, st,
+                               (const T*)q, (float*)y, n, C, inner, scale, zp, zp_value, false);
+        } else {
+            hipLaunchKernelGGL((dequantize_pc_kernel<Code, __half>), scalar_grid(n), dim3(kBlock), 0, st,
+                               (const T*)q, (__half*)y, n, C, inner, scale, zp, zp_value, false);
+        }
         return launch_status("lq_dequantize_per_channel");
     }
 };
+
+template <int MODE>
+static void launch_fq(const float* x, float* y, float* mask, int64_t n, const QArgs& qa, Grid g,
+                      hipStream_t st) {
+    if (mask)
+        hipLaunchKernelGGL((fake_quant_g4_kernel<MODE, true>), g4_grid(n), dim3(kBlock), 0, st, x, y, mask,
+                           (uint32_t)n, qa, g);
+    else
+        hipLaunchKernelGGL((fake_quant_g4_kernel<MODE, false>), g4_grid(n), dim3(kBlock), 0, st, x, y, mask,
+                           (uint32_t)n, qa, g);
+}
 
 static int check_ocl(int64_t outer, int64_t C, int64_t inner) {
     LQ_REQUIRE(outer >= 0 && C >= 1 && inner >= 0, "invalid [outer, C, inner] layout");
@@ -826,11 +1097,15 @@ int lq_fake_quantize_per_tensor_f32(const float* d_x, float* d_y, int64_t n, con
     LQ_REQUIRE(d_x && d_y, "lq_fake_quantize_per_tensor_f32: NULL pointer");
     LQ_REQUIRE(qmax >= qmin, "lq_fake_quantize_per_tensor_f32: qmax < qmin");
     PtParams pp{d_scale, d_zero_point, inv_scale_value, scale_value, zero_point_value};
-    bool vec = aligned16(d_x) && aligned16(d_y) && (!d_mask || aligned16(d_mask));
-    dim3 grid = vec ? vec_grid(n) : scalar_grid(n);
-    hipLaunchKernelGGL(fake_quant_kernel, grid, dim3(kBlock), 0, as_stream(stream), d_x, d_y, d_mask,
-                       n, (int64_t)1, n, pp, (const float*)nullptr, (const float*)nullptr, 0.0f,
-                       make_grid(qmin, qmax), false, vec);
+    const bool vec = aligned16(d_x) && aligned16(d_y) && (!d_mask || aligned16(d_mask)) && n < ((int64_t)1 << 32);
+    if (vec) {
+        QArgs qa{d_scale, d_zero_point, inv_scale_value, scale_value, zero_point_value, 1u, 1u};
+        launch_fq<PT>(d_x, d_y, d_mask, n, qa, make_grid(qmin, qmax), as_stream(stream));
+    } else {
+        hipLaunchKernelGGL(fake_quant_kernel, scalar_grid(n), dim3(kBlock), 0, as_stream(stream), d_x, d_y,
+                           d_mask, n, (int64_t)1, n, pp, (const float*)nullptr, (const float*)nullptr, 0.0f,
+                           make_grid(qmin, qmax), false, false);
+    }
     return launch_status("lq_fake_quantize_per_tensor_f32");
 }
 
@@ -844,12 +1119,19 @@ int lq_fake_quantize_per_channel_f32(const float* d_x, float* d_y, int64_t outer
     if (n == 0) return LQ_OK;
     LQ_REQUIRE(d_x && d_y && d_scale, "lq_fake_quantize_per_channel_f32: NULL pointer");
     LQ_REQUIRE(qmax >= qmin, "lq_fake_quantize_per_channel_f32: qmax < qmin");
-    bool vec = aligned16(d_x) && aligned16(d_y) && (!d_mask || aligned16(d_mask)) && (inner % kVec == 0);
-    dim3 grid = vec ? vec_grid(n) : scalar_grid(n);
-    PtParams pp{nullptr, nullptr, 0.f, 0.f, 0.f};
-    hipLaunchKernelGGL(fake_quant_kernel, grid, dim3(kBlock), 0, as_stream(stream), d_x, d_y, d_mask,
-                       n, C, inner, pp, d_scale, d_zero_point, zero_point_value,
-                       make_grid(qmin, qmax), true, vec);
+    const bool vec = aligned16(d_x) && aligned16(d_y) && (!d_mask || aligned16(d_mask)) && n < ((int64_t)1 << 32);
+    if (vec) {
+        QArgs qa{d_scale, d_zero_point, 0.f, 0.f, zero_point_value, (uint32_t)C, (uint32_t)inner};
+        if (inner % 4 == 0)
+            launch_fq<PCG>(d_x, d_y, d_mask, n, qa, make_grid(qmin, qmax), as_stream(stream));
+        else
+            launch_fq<PCE>(d_x, d_y, d_mask, n, qa, make_grid(qmin, qmax), as_stream(stream));
+    } else {
+        PtParams pp{nullptr, nullptr, 0.f, 0.f, 0.f};
+        hipLaunchKernelGGL(fake_quant_kernel, scalar_grid(n), dim3(kBlock), 0, as_stream(stream), d_x, d_y,
+                           d_mask, n, C, inner, pp, d_scale, d_zero_point, zero_point_value,
+                           make_grid(qmin, qmax), true, false);
+    }
     return launch_status("lq_fake_quantize_per_channel_f32");
 }
 
