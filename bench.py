@@ -48,7 +48,23 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--no-components", dest="components", action="store_false")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="bound on the CPU-baseline sample's wall time")
+    p.add_argument("--copy-mb", type=int, default=0,
+                   help="also run one device-to-device copy of this many MiB (the known-size "
+                        "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
     return p.parse_args()
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_w8a8_4096_traffic.json")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the headline GEMM kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE summary (scaled by the copy-kernel calibration), or None."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return json.load(f).get("hbm_bytes_per_launch")
+    except (OSError, ValueError):
+        return None
 
 
 class Timer:
@@ -243,6 +259,13 @@ def main() -> None:
         print(json.dumps({"error": "no HIP device visible"}))
         sys.exit(1)
     timer = Timer(C)
+    if args.copy_mb > 0:
+        nbytes = args.copy_mb << 20
+        src = L.empty((nbytes,), np.uint8, "gpu")
+        dst = L.empty((nbytes,), np.uint8, "gpu")
+        C.call("lq_memcpy_d2d", dst.data_ptr(), src.data_ptr(), nbytes, None)
+        C.synchronize()
+        del src, dst
     M = N = K = 4096
     head = Gemm(L, C, M, N, K, C.OUT_Q8, seed=0)
     ms = timer.time_ms(head.run, args.steps, args.warmup)
@@ -264,7 +287,8 @@ def main() -> None:
                                "fp32 bias, fused requantize to int8 (BASELINE config 3)",
                    "M": M, "N": N, "K": K, "out": "int8"},
         "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS,
-                     "unit": "TFLOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4), "traffic": None},
+                     "unit": "TFLOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
+                     "traffic": measured_traffic()},
     }
     if args.components:
         comps = {"gemm_sweep": []}
