@@ -216,6 +216,27 @@ int lq_gemm_w8a8(const int8_t* d_A, int64_t lda, const int8_t* d_B, int64_t ldb,
                  const int32_t* d_b_sums, const float* d_bias, const float* d_out_scale,
                  const float* d_out_zero_point, int out_qmin, int out_qmax, int out_kind,
                  int flags, void* d_workspace, size_t workspace_bytes, void* stream);
+/* ---- MFMA-packed weights for decode (M <= 128) ------------------------------ */
+/* Bytes of the packed form of an int8 weight B [N, K]: ceil(N/16) x ceil(K/64) tiles of
+ * 1 KB.  Tile (t, s) sits at byte (t * ceil(K/64) + s) * 1024; its 16-byte chunk l holds
+ * row 16 t + l % 16, K-bytes 64 s + 16 (l / 16) .. +15 (zero past N and K), i.e. the
+ * A-operand fragment of v_mfma_i32_16x16x64_i8, so a wave load is 1 KB contiguous.
+ * No reference counterpart: a device layout of Lucid's weight_int8 [out, in]
+ * (lucid/nn/quantized/linear.py:183-199), which stays the state_dict form. */
+size_t lq_packed_weights_size(int64_t N, int64_t K);
+int lq_pack_weights_i8(const int8_t* d_B, int64_t ldb, int64_t N, int64_t K, int8_t* d_packed,
+                       void* stream);
+/* lq_gemm_w8a8 with B in the packed form, for M <= 128 (decode); LQ_ERR_UNSUPPORTED above.
+ * Needs K and lda multiples of 16, 16-byte aligned A and packed B, and the cached weight
+ * sums d_b_sums whenever d_a_zero_point is given.  Same results as lq_gemm_w8a8. */
+int lq_gemm_w8a8_packed(const int8_t* d_A, int64_t lda, const int8_t* d_B_packed, void* d_C,
+                        int64_t ldc, int64_t M, int64_t N, int64_t K, const float* d_a_scale,
+                        int64_t a_scale_stride, const float* d_b_scale, int64_t b_scale_stride,
+                        const float* d_a_zero_point, const float* d_b_zero_point,
+                        const int32_t* d_b_sums, const float* d_bias, const float* d_out_scale,
+                        const float* d_out_zero_point, int out_qmin, int out_qmax, int out_kind,
+                        int flags, void* d_workspace, size_t workspace_bytes, void* stream);
+
 /* sums[r] = sum_k X[r,k] over int8 rows (the weight code sums a module caches for the
  * activation zero-point correction).  No reference counterpart (Lucid has no integer GEMM). */
 int lq_row_sums_i8(const int8_t* d_X, int64_t ld, int64_t rows, int64_t K, int32_t* d_sums,

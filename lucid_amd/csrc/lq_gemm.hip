@@ -602,9 +602,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_dma_kernel(Gem
 // MFMA registers (every B byte is read once), UNROLL k-steps of 64 in flight per wave.
 // A (M x K, a few KB) stays L2-resident.  Partial accumulators are summed through LDS.
 
-template <int MT, int W, int KIND>
+template <int MT, int W, int KIND, int UNROLL = 8>
 __global__ __launch_bounds__(64 * W) void gemm_i8_skinny_kernel(GemmArgs a) {
-    constexpr int UNROLL = 8;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int n0 = blockIdx.x * 16;
     const int nrow = n0 + (lane & 15);
@@ -664,6 +663,98 @@ __global__ __launch_bounds__(64 * W) void gemm_i8_skinny_kernel(GemmArgs a) {
         const int n = n0 + (lane >> 4) * 4;
         epilogue4<KIND>(a, p, m, n, acc[t]);
     }
+}
+
+// --------------------------------------------- packed weights (decode, M <= 64)
+//
+// MFMA-packed weight layout: B [N, K] int8 cut into tiles of 16 rows x 64 K-bytes; tile
+// (t, s) occupies bytes [(t * KS + s) * 1024, +1024) with KS = ceil(K / 64), and its lane-l
+// 16-byte chunk holds row 16 t + l % 16, K-bytes 64 s + 16 (l / 16) .. +15: exactly the
+// A-operand fragment of v_mfma_i32_16x16x64_i8.  Rows past N and bytes past K are zero.
+// One wave load is then 1 KB contiguous, where a row-major weight gives 16 rows x 64 bytes.
+
+constexpr int PACK_TILE = 1024;
+
+__global__ __launch_bounds__(256) void pack_weights_i8_kernel(const int8_t* __restrict__ B, int64_t ldb, int N,
+                                                              int K, int KS, int64_t chunks,
+                                                              int8_t* __restrict__ P) {
+    const int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= chunks) return;
+    const int l = (int)(c & 63);
+    const int64_t tile = c >> 6;
+    const int t = (int)(tile / KS), s = (int)(tile % KS);
+    const int row = t * 16 + (l & 15);
+    const int k0 = s * 64 + (l >> 4) * 16;
+    int8_t v[16];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) v[j] = (row < N && k0 + j < K) ? B[(int64_t)row * ldb + k0 + j] : (int8_t)0;
+    *reinterpret_cast<v4i*>(P + c * 16) = *reinterpret_cast<const v4i*>(v);
+}
+
+// One workgroup per 16-row n-tile, its W waves splitting the K steps; every tile byte is
+// read once, UNROLL steps (16 KB per wave) in flight.  A (M x K, a few KB) stays in L2.
+template <int MT, int W, int UNROLL, int KIND>
+__global__ __launch_bounds__(64 * W) void gemm_i8_packed_skinny_kernel(GemmArgs a) {
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int t = blockIdx.x;
+    const int KS = (a.K + 63) / 64;
+    const int per = (KS + W - 1) / W;
+    const int kb = wave * per, ke = min(KS, kb + per);
+    const int kg = (lane >> 4) * 16;
+    v4i acc[MT];
+#pragma unroll
+    for (int u = 0; u < MT; ++u) acc[u] = v4i{0, 0, 0, 0};
+    const int8_t* bt = a.B + (int64_t)t * KS * PACK_TILE + lane * 16;
+    for (int ks = kb; ks < ke; ks += UNROLL) {
+        v4i bf[UNROLL], af[UNROLL][MT];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) {
+            const bool ok = ks + u < ke;
+            const int k = (ks + u) * 64 + kg;
+            bf[u] = ok ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(bt + (int64_t)(ks + u) * PACK_TILE))
+                       : v4i{0, 0, 0, 0};
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int m = mt * 16 + (lane & 15);
+                af[u][mt] = (ok && k < a.K && m < a.M) ? *reinterpret_cast<const v4i*>(a.A + (int64_t)m * a.lda + k)
+                                                       : v4i{0, 0, 0, 0};
+            }
+        }
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u)
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+                acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[u], af[u][mt], acc[mt], 0, 0, 0);
+    }
+    __shared__ v4i red[W][MT][64];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) red[wave][mt][lane] = acc[mt];
+    __syncthreads();
+    if (wave != 0) return;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        v4i sum = red[0][mt][lane];
+        for (int w = 1; w < W; ++w) sum += red[w][mt][lane];
+        acc[mt] = sum;
+    }
+    const EpiParams p = epi_params(a);
+    const int n = t * 16 + (lane >> 4) * 4;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) epilogue4<KIND>(a, p, mt * 16 + (lane & 15), n, acc[mt]);
+}
+
+template <int KIND>
+static int launch_packed_skinny(const GemmArgs& a, hipStream_t st) {
+    const unsigned tiles = (unsigned)((a.N + 15) / 16);
+    if (a.M <= 16)
+        hipLaunchKernelGGL((gemm_i8_packed_skinny_kernel<1, 4, 16, KIND>), dim3(tiles), dim3(256), 0, st, a);
+    else if (a.M <= 32)
+        hipLaunchKernelGGL((gemm_i8_packed_skinny_kernel<2, 4, 8, KIND>), dim3(tiles), dim3(256), 0, st, a);
+    else if (a.M <= 64)
+        hipLaunchKernelGGL((gemm_i8_packed_skinny_kernel<4, 4, 4, KIND>), dim3(tiles), dim3(256), 0, st, a);
+    else
+        hipLaunchKernelGGL((gemm_i8_packed_skinny_kernel<8, 4, 2, KIND>), dim3(tiles), dim3(256), 0, st, a);
+    return launch_status("lq_gemm_w8a8_packed");
 }
 
 // ------------------------------------------------------------ generic kernel
@@ -728,6 +819,12 @@ struct GemmLaunch {
         }
         if (a.M <= 64) {
             hipLaunchKernelGGL((gemm_i8_skinny_kernel<4, 8, KIND>), dim3((unsigned)((a.N + 15) / 16)),
+                               dim3(512), 0, st, a);
+            return launch_status("lq_gemm_w8a8 (skinny)");
+        }
+        const int64_t tiles128 = ((int64_t)(a.M + 127) / 128) * ((a.N + 127) / 128);
+        if (a.M <= 128 && tiles128 < 128) {
+            hipLaunchKernelGGL((gemm_i8_skinny_kernel<8, 8, KIND, 2>), dim3((unsigned)((a.N + 15) / 16)),
                                dim3(512), 0, st, a);
             return launch_status("lq_gemm_w8a8 (skinny)");
         }
@@ -802,25 +899,49 @@ int lq_row_sums_i8(const int8_t* d_X, int64_t ld, int64_t rows, int64_t K, int32
     return launch_status("lq_row_sums_i8");
 }
 
+size_t lq_packed_weights_size(int64_t N, int64_t K) {
+    if (N < 0 || K < 0) return 0;
+    return (size_t)((N + 15) / 16) * (size_t)((K + 63) / 64) * PACK_TILE;
+}
+
+int lq_pack_weights_i8(const int8_t* d_B, int64_t ldb, int64_t N, int64_t K, int8_t* d_packed,
+                       void* stream) {
+    LQ_REQUIRE(N >= 0 && K >= 0 && ldb >= K, "lq_pack_weights_i8: bad shape");
+    LQ_REQUIRE(N <= 0x7fffffff && K <= 0x7fffffff, "lq_pack_weights_i8: size too large");
+    const int64_t chunks = (int64_t)lq_packed_weights_size(N, K) / 16;
+    if (chunks == 0) return LQ_OK;
+    LQ_REQUIRE(d_B && d_packed, "lq_pack_weights_i8: NULL pointer");
+    LQ_REQUIRE(aligned16(d_packed), "lq_pack_weights_i8: packed buffer must be 16-byte aligned");
+    hipLaunchKernelGGL(pack_weights_i8_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0,
+                       as_stream(stream), d_B, ldb, (int)N, (int)K, (int)((K + 63) / 64), chunks,
+                       d_packed);
+    return launch_status("lq_pack_weights_i8");
+}
+
 size_t lq_gemm_w8a8_workspace_size(int64_t M, int64_t N, int64_t K) {
     (void)K;
     if (M < 0 || N < 0) return 0;
     return gemm_ws(M, N).total;
 }
 
-int lq_gemm_w8a8(const int8_t* d_A, int64_t lda, const int8_t* d_B, int64_t ldb, void* d_C,
-                 int64_t ldc, int64_t M, int64_t N, int64_t K, const float* d_a_scale,
-                 int64_t a_scale_stride, const float* d_b_scale, int64_t b_scale_stride,
-                 const float* d_a_zero_point, const float* d_b_zero_point, const int32_t* d_b_sums,
-                 const float* d_bias, const float* d_out_scale, const float* d_out_zero_point,
-                 int out_qmin, int out_qmax, int out_kind, int flags, void* d_workspace,
-                 size_t workspace_bytes, void* stream) {
+}  // extern "C"
+
+namespace lq {
+
+// Shared validation / setup of lq_gemm_w8a8 and lq_gemm_w8a8_packed.
+static int gemm_entry(bool packed, const int8_t* d_A, int64_t lda, const int8_t* d_B, int64_t ldb,
+                      void* d_C, int64_t ldc, int64_t M, int64_t N, int64_t K, const float* d_a_scale,
+                      int64_t a_scale_stride, const float* d_b_scale, int64_t b_scale_stride,
+                      const float* d_a_zero_point, const float* d_b_zero_point, const int32_t* d_b_sums,
+                      const float* d_bias, const float* d_out_scale, const float* d_out_zero_point,
+                      int out_qmin, int out_qmax, int out_kind, int flags, void* d_workspace,
+                      size_t workspace_bytes, void* stream) {
     LQ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "lq_gemm_w8a8: negative size");
     LQ_REQUIRE(M <= 0x7fffffff && N <= 0x7fffffff && K <= 0x7fffffff, "lq_gemm_w8a8: size too large");
     if (M == 0 || N == 0) return LQ_OK;
     LQ_REQUIRE(d_C, "lq_gemm_w8a8: NULL output");
     LQ_REQUIRE(K == 0 || (d_A && d_B), "lq_gemm_w8a8: NULL operand");
-    LQ_REQUIRE(lda >= K && ldb >= K && ldc >= N, "lq_gemm_w8a8: leading dimension too small");
+    LQ_REQUIRE(lda >= K && ldc >= N && (packed || ldb >= K), "lq_gemm_w8a8: leading dimension too small");
     LQ_REQUIRE(valid_out_kind(out_kind), "lq_gemm_w8a8: bad out_kind");
     LQ_REQUIRE(a_scale_stride == 0 || a_scale_stride == 1, "lq_gemm_w8a8: a_scale_stride must be 0 or 1");
     LQ_REQUIRE(b_scale_stride == 0 || b_scale_stride == 1, "lq_gemm_w8a8: b_scale_stride must be 0 or 1");
@@ -829,6 +950,13 @@ int lq_gemm_w8a8(const int8_t* d_A, int64_t lda, const int8_t* d_B, int64_t ldb,
     LQ_REQUIRE(!requant || d_out_scale, "lq_gemm_w8a8: requantizing output needs d_out_scale");
     LQ_REQUIRE(!requant || out_qmax >= out_qmin, "lq_gemm_w8a8: out_qmax < out_qmin");
     LQ_REQUIRE((flags & ~LQ_EPI_RELU) == 0, "lq_gemm_w8a8: unknown flags");
+    if (packed) {
+        if (M > 128) return set_error(LQ_ERR_UNSUPPORTED, "lq_gemm_w8a8_packed: M > 128 (use lq_gemm_w8a8)");
+        LQ_REQUIRE(K % 16 == 0 && lda % 16 == 0 && aligned16(d_A) && aligned16(d_B),
+                   "lq_gemm_w8a8_packed: needs K and lda multiples of 16 and 16-byte aligned A / packed B");
+        LQ_REQUIRE(!d_a_zero_point || d_b_sums,
+                   "lq_gemm_w8a8_packed: an activation zero point needs the cached weight sums d_b_sums");
+    }
     const GemmWs ws = gemm_ws(M, N);
     LQ_REQUIRE(d_workspace || workspace_bytes == 0, "lq_gemm_w8a8: NULL workspace with nonzero size");
     const bool need_asums = d_b_zero_point != nullptr;
@@ -843,7 +971,7 @@ int lq_gemm_w8a8(const int8_t* d_A, int64_t lda, const int8_t* d_B, int64_t ldb,
     a.B = d_B;
     a.C = d_C;
     a.lda = lda;
-    a.ldb = ldb;
+    a.ldb = packed ? K : ldb;
     a.ldc = ldc;
     a.M = (int)M;
     a.N = (int)N;
@@ -876,6 +1004,19 @@ int lq_gemm_w8a8(const int8_t* d_A, int64_t lda, const int8_t* d_B, int64_t ldb,
             if ((rc = lq_row_sums_i8(d_B, ldb, N, K, (int32_t*)a.b_sums, stream))) return rc;
         }
     }
+    if (packed) {
+        switch (out_kind) {
+        case LQ_OUT_I32: return launch_packed_skinny<LQ_OUT_I32>(a, st);
+        case LQ_OUT_F32: return launch_packed_skinny<LQ_OUT_F32>(a, st);
+        case LQ_OUT_F16: return launch_packed_skinny<LQ_OUT_F16>(a, st);
+        case LQ_OUT_Q8: return launch_packed_skinny<LQ_OUT_Q8>(a, st);
+        case LQ_OUT_QU8: return launch_packed_skinny<LQ_OUT_QU8>(a, st);
+        case LQ_OUT_FQ32: return launch_packed_skinny<LQ_OUT_FQ32>(a, st);
+        case LQ_OUT_Q16: return launch_packed_skinny<LQ_OUT_Q16>(a, st);
+        case LQ_OUT_QU8S8: return launch_packed_skinny<LQ_OUT_QU8S8>(a, st);
+        default: return set_error(LQ_ERR_INVALID, "lq_gemm_w8a8: bad out_kind");
+        }
+    }
     int64_t split_bytes = 0;
     if (d_workspace && workspace_bytes >= ws.total && ws.total > ws.counters) {
         a.partial = (int32_t*)(wsb + ws.partial);
@@ -893,6 +1034,36 @@ int lq_gemm_w8a8(const int8_t* d_A, int64_t lda, const int8_t* d_B, int64_t ldb,
     case LQ_OUT_QU8S8: return GemmLaunch<LQ_OUT_QU8S8>::run(a, st, split_bytes);
     default: return set_error(LQ_ERR_INVALID, "lq_gemm_w8a8: bad out_kind");
     }
+}
+
+}  // namespace lq
+
+extern "C" {
+
+int lq_gemm_w8a8(const int8_t* d_A, int64_t lda, const int8_t* d_B, int64_t ldb, void* d_C,
+                 int64_t ldc, int64_t M, int64_t N, int64_t K, const float* d_a_scale,
+                 int64_t a_scale_stride, const float* d_b_scale, int64_t b_scale_stride,
+                 const float* d_a_zero_point, const float* d_b_zero_point, const int32_t* d_b_sums,
+                 const float* d_bias, const float* d_out_scale, const float* d_out_zero_point,
+                 int out_qmin, int out_qmax, int out_kind, int flags, void* d_workspace,
+                 size_t workspace_bytes, void* stream) {
+    return gemm_entry(false, d_A, lda, d_B, ldb, d_C, ldc, M, N, K, d_a_scale, a_scale_stride, d_b_scale,
+                      b_scale_stride, d_a_zero_point, d_b_zero_point, d_b_sums, d_bias, d_out_scale,
+                      d_out_zero_point, out_qmin, out_qmax, out_kind, flags, d_workspace, workspace_bytes,
+                      stream);
+}
+
+int lq_gemm_w8a8_packed(const int8_t* d_A, int64_t lda, const int8_t* d_B_packed, void* d_C, int64_t ldc,
+                        int64_t M, int64_t N, int64_t K, const float* d_a_scale, int64_t a_scale_stride,
+                        const float* d_b_scale, int64_t b_scale_stride, const float* d_a_zero_point,
+                        const float* d_b_zero_point, const int32_t* d_b_sums, const float* d_bias,
+                        const float* d_out_scale, const float* d_out_zero_point, int out_qmin,
+                        int out_qmax, int out_kind, int flags, void* d_workspace, size_t workspace_bytes,
+                        void* stream) {
+    return gemm_entry(true, d_A, lda, d_B_packed, K, d_C, ldc, M, N, K, d_a_scale, a_scale_stride,
+                      d_b_scale, b_scale_stride, d_a_zero_point, d_b_zero_point, d_b_sums, d_bias,
+                      d_out_scale, d_out_zero_point, out_qmin, out_qmax, out_kind, flags, d_workspace,
+                      workspace_bytes, stream);
 }
 
 }  // extern "C"

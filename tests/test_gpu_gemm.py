@@ -29,10 +29,33 @@ _OUT_DT = {O.OUT_I32: np.int32, O.OUT_F32: np.float32, O.OUT_F16: np.float16, O.
            O.OUT_QU8: np.uint8, O.OUT_FQ32: np.float32, O.OUT_Q16: np.int16, O.OUT_QU8S8: np.int8}
 
 
+def pack_weights(L, B):
+    """B [N, K] int8 -> device buffer in the MFMA-packed layout (lq_pack_weights_i8)."""
+    from lucid_amd import _C
+
+    N, K = B.shape
+    dB = _dev(L, B)
+    nbytes = _C.lib().lq_packed_weights_size(N, K)
+    dP = L.empty((max(nbytes, 16),), np.int8, "gpu")
+    _C.call("lq_pack_weights_i8", dB.data_ptr(), K, N, K, dP.data_ptr(), None)
+    return dP
+
+
+def packed_layout_oracle(B):
+    """The packed layout restated in numpy (tile (t, s), chunk l = row 16t + l%16,
+    K-bytes 64s + 16(l//16) .. +15, zero padded)."""
+    N, K = B.shape
+    NT, KS = -(-N // 16), -(-K // 64)
+    Bp = np.zeros((NT * 16, KS * 64), np.int8)
+    Bp[:N, :K] = B
+    t = Bp.reshape(NT, 16, KS, 4, 16)            # [t, row, s, g, byte]
+    return np.ascontiguousarray(t.transpose(0, 2, 3, 1, 4)).reshape(-1)  # [t, s, g, row, byte]
+
+
 def run_gemm(L, A, B, out_kind=O.OUT_I32, a_scale=None, b_scale=None, za=None, zb=None,
              b_sums=None, bias=None, out_scale=None, out_zp=None, qmin=-128, qmax=127,
-             relu=False, lda=None, ldb=None, ldc=None, workspace=True):
-    """Run lq_gemm_w8a8 on host arrays; returns C [M, N] as numpy."""
+             relu=False, lda=None, ldb=None, ldc=None, workspace=True, packed=False):
+    """Run lq_gemm_w8a8 (or lq_gemm_w8a8_packed) on host arrays; returns C [M, N]."""
     from lucid_amd import _C
 
     M, K = A.shape
@@ -59,6 +82,16 @@ def run_gemm(L, A, B, out_kind=O.OUT_I32, a_scale=None, b_scale=None, za=None, z
     sb = None if b_scale is None else np.atleast_1d(np.asarray(b_scale, np.float32))
     ws_bytes = _C.lib().lq_gemm_w8a8_workspace_size(M, N, K) if workspace else 0
     ws = L.empty((max(ws_bytes, 1),), np.uint8, "gpu") if workspace else None
+    if packed:
+        dP = pack_weights(L, B)
+        _C.call("lq_gemm_w8a8_packed", dA.data_ptr(), lda, dP.data_ptr(), dC.data_ptr(), ldc, M, N,
+                K, opt(sa), 0 if sa is None or sa.size == 1 else 1, opt(sb),
+                0 if sb is None or sb.size == 1 else 1,
+                opt(None if za is None else [za]), opt(zb), opt(b_sums, np.int32), opt(bias),
+                opt(None if out_scale is None else [out_scale]),
+                opt(None if out_zp is None else [out_zp]), qmin, qmax, out_kind, 1 if relu else 0,
+                ws.data_ptr() if ws is not None else None, ws_bytes, None)
+        return dC.numpy()[:, :N]
     _C.call("lq_gemm_w8a8", dA.data_ptr(), lda, dB.data_ptr(), ldb, dC.data_ptr(), ldc, M, N, K,
             opt(sa), 0 if sa is None or sa.size == 1 else 1, opt(sb),
             0 if sb is None or sb.size == 1 else 1,
@@ -85,7 +118,8 @@ def _codes(rng, shape, lo=-127, hi=127):
 ACC_SHAPES = [
     (1, 64, 64), (1, 1000, 784), (3, 4096, 512), (16, 256, 4096), (17, 100, 256),
     (32, 48, 1024), (33, 160, 640), (64, 10, 256), (64, 256, 784), (65, 130, 96),
-    (128, 4096, 2048), (300, 520, 1040), (200, 300, 16), (5, 7, 13), (33, 40, 30),
+    (128, 4096, 2048), (100, 4096, 1024), (128, 2048, 2048), (300, 520, 1040), (200, 300, 16),
+    (5, 7, 13), (33, 40, 30),
     (1, 1, 1), (7, 9, 0),
 ]
 
@@ -146,6 +180,48 @@ def test_epilogue_kinds_dma_path(gpu, kind):
             np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
         else:
             np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8))
+
+
+@pytest.mark.parametrize("N,K", [(4096, 4096), (100, 96), (17, 80), (1000, 784), (11008, 128)])
+def test_packed_weight_layout(gpu, N, K):
+    rng = np.random.default_rng(N + K)
+    B = _codes(rng, (N, K), -128, 127)
+    np.testing.assert_array_equal(pack_weights(gpu, B).numpy()[: packed_layout_oracle(B).size],
+                                  packed_layout_oracle(B))
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (16, 4096, 4096), (8, 11008, 4096), (1, 4096, 11008),
+                                   (17, 1000, 784), (32, 100, 96), (64, 256, 784), (3, 17, 80),
+                                   (100, 300, 256), (128, 4096, 4096)])
+def test_packed_skinny_exact(gpu, M, N, K):
+    rng = np.random.default_rng(M + N + K)
+    A = _codes(rng, (M, K), -128, 127)
+    B = _codes(rng, (N, K), -127, 127)
+    np.testing.assert_array_equal(run_gemm(gpu, A, B, packed=True), O.gemm_acc(A, B))
+    a_scale = rng.uniform(1e-3, 1e-1, M).astype(np.float32)
+    b_scale = rng.uniform(1e-3, 1e-1, N).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    sums = B.astype(np.int64).sum(axis=1).astype(np.int32)
+    for kind in KINDS:
+        qmin, qmax = GRID.get(kind, (-128, 127))
+        got = run_gemm(gpu, A, B, kind, a_scale, b_scale, za=-7.0, b_sums=sums, bias=bias,
+                       out_scale=0.37, out_zp=(128.0 if qmin == 0 else 3.0), qmin=qmin, qmax=qmax,
+                       relu=True, packed=True)
+        want = O.gemm_w8a8(A, B, a_scale, b_scale, za=-7.0, bias=bias, out_scale=0.37,
+                           out_zp=(128.0 if qmin == 0 else 3.0), qmin=qmin, qmax=qmax,
+                           out_kind=kind, relu=True)
+        if kind == O.OUT_F16:
+            np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+        else:
+            np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8))
+
+
+def test_packed_rejects_large_m(gpu):
+    from lucid_amd import _C
+
+    rng = np.random.default_rng(2)
+    with pytest.raises(_C.LucidError, match="M > 128"):
+        run_gemm(gpu, _codes(rng, (129, 64)), _codes(rng, (16, 64)), packed=True)
 
 
 def test_leading_dimensions(gpu):
