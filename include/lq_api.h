@@ -187,8 +187,10 @@ enum {
     LQ_OUT_QU8S8 = 7 /* unsigned-grid codes c of y stored as int8 (c - 128): the next layer's
                         MFMA operand (LQ_U8S8) */
 };
-/* Epilogue flag bits. */
-enum { LQ_EPI_RELU = 1 };
+/* Flag bits of lq_gemm_w8a8.  LQ_EPI_A_U8S8: A holds unsigned-grid codes c stored as int8
+ * (c - 128, the LQ_U8S8 form); d_a_zero_point (NULL = 0) is the grid's own zero point and
+ * the kernel applies the 128 shift. */
+enum { LQ_EPI_RELU = 1, LQ_EPI_A_U8S8 = 2 };
 
 /* C[m,n] epilogue of acc[m,n] = sum_k (A[m,k] - za) * (B[n,k] - zb[n])  (exact int32),
  * A int8 [M,K] row-major (lda), B int8 [N,K] row-major (ldb; Lucid's weight_int8 [out,in]).

@@ -48,6 +48,7 @@ struct GemmArgs {
     int qmin, qmax;
     int out_kind;
     int relu;
+    int a_u8s8;              // A holds unsigned codes c as int8 (c - 128): the zero point shifts by 128
     int32_t* partial;        // split-K: [M,N] int32 accumulation buffer (zeroed)
     uint32_t* counters;      // split-K: one arrival counter per output tile (zeroed)
     int splits;              // split-K factor (1 = none)
@@ -56,14 +57,16 @@ struct GemmArgs {
 // ------------------------------------------------------------------ epilogue
 
 struct EpiParams {
-    int za;
+    int za;       // effective activation zero point in A's stored units
+    bool has_za;
     float out_inv, out_s, out_z;
     Grid g;
 };
 
 __device__ __forceinline__ EpiParams epi_params(const GemmArgs& a) {
     EpiParams p;
-    p.za = a.a_zp ? (int)a.a_zp[0] : 0;
+    p.za = (a.a_zp ? (int)a.a_zp[0] : 0) - (a.a_u8s8 ? 128 : 0);
+    p.has_za = a.a_zp != nullptr || a.a_u8s8;
     p.out_s = a.out_scale ? a.out_scale[0] : 1.0f;
     p.out_inv = 1.0f / p.out_s;
     p.out_z = a.out_zp ? a.out_zp[0] : 0.0f;
@@ -78,7 +81,7 @@ __device__ __forceinline__ EpiParams epi_params(const GemmArgs& a) {
 __device__ __forceinline__ int32_t corrected(int32_t raw, int m, int n, const GemmArgs& a,
                                              const EpiParams& p) {
     uint32_t acc = (uint32_t)raw;
-    if (a.a_zp) acc -= (uint32_t)p.za * (uint32_t)a.b_sums[n];
+    if (p.has_za) acc -= (uint32_t)p.za * (uint32_t)a.b_sums[n];
     if (a.b_zp) {
         const uint32_t zb = (uint32_t)(int)a.b_zp[n];
         acc -= zb * (uint32_t)a.a_sums[m];
@@ -161,7 +164,7 @@ __device__ __forceinline__ ColCtx load_cols(const GemmArgs& a, int n) {
         const int nn = min(n + r, a.N - 1);  // clamped: out-of-range columns are never stored
         c.sb[r] = a.b_scale ? a.b_scale[(int64_t)nn * a.b_stride] : 1.0f;
         c.bias[r] = a.bias ? a.bias[nn] : 0.0f;
-        c.bsum[r] = a.a_zp ? a.b_sums[nn] : 0;
+        c.bsum[r] = a.b_sums ? a.b_sums[nn] : 0;
         c.zb[r] = a.b_zp ? (int)a.b_zp[nn] : 0;
     }
     return c;
@@ -184,7 +187,7 @@ __device__ __forceinline__ void epilogue4c(const GemmArgs& a, const EpiParams& p
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
         uint32_t acc = (uint32_t)raw[r];  // zero-point correction, two's-complement wrap
-        if (a.a_zp) acc -= (uint32_t)p.za * (uint32_t)c.bsum[r];
+        if (p.has_za) acc -= (uint32_t)p.za * (uint32_t)c.bsum[r];
         if (a.b_zp) {
             acc -= (uint32_t)c.zb[r] * (uint32_t)row.asum;
             acc += (uint32_t)a.K * (uint32_t)p.za * (uint32_t)c.zb[r];
@@ -949,18 +952,19 @@ static int gemm_entry(bool packed, const int8_t* d_A, int64_t lda, const int8_t*
                          out_kind == LQ_OUT_QU8S8 || out_kind == LQ_OUT_FQ32;
     LQ_REQUIRE(!requant || d_out_scale, "lq_gemm_w8a8: requantizing output needs d_out_scale");
     LQ_REQUIRE(!requant || out_qmax >= out_qmin, "lq_gemm_w8a8: out_qmax < out_qmin");
-    LQ_REQUIRE((flags & ~LQ_EPI_RELU) == 0, "lq_gemm_w8a8: unknown flags");
+    LQ_REQUIRE((flags & ~(LQ_EPI_RELU | LQ_EPI_A_U8S8)) == 0, "lq_gemm_w8a8: unknown flags");
+    const bool has_za = d_a_zero_point != nullptr || (flags & LQ_EPI_A_U8S8);
     if (packed) {
         if (M > 128) return set_error(LQ_ERR_UNSUPPORTED, "lq_gemm_w8a8_packed: M > 128 (use lq_gemm_w8a8)");
         LQ_REQUIRE(K % 16 == 0 && lda % 16 == 0 && aligned16(d_A) && aligned16(d_B),
                    "lq_gemm_w8a8_packed: needs K and lda multiples of 16 and 16-byte aligned A / packed B");
-        LQ_REQUIRE(!d_a_zero_point || d_b_sums,
+        LQ_REQUIRE(!has_za || d_b_sums,
                    "lq_gemm_w8a8_packed: an activation zero point needs the cached weight sums d_b_sums");
     }
     const GemmWs ws = gemm_ws(M, N);
     LQ_REQUIRE(d_workspace || workspace_bytes == 0, "lq_gemm_w8a8: NULL workspace with nonzero size");
     const bool need_asums = d_b_zero_point != nullptr;
-    const bool need_bsums = d_a_zero_point != nullptr && d_b_sums == nullptr;
+    const bool need_bsums = has_za && d_b_sums == nullptr;
     if (need_asums || need_bsums)
         LQ_REQUIRE(d_workspace && workspace_bytes >= ws.partial,
                    "lq_gemm_w8a8: zero-point correction needs the workspace (lq_gemm_w8a8_workspace_size)");
@@ -989,6 +993,7 @@ static int gemm_entry(bool packed, const int8_t* d_A, int64_t lda, const int8_t*
     a.qmax = out_qmax;
     a.out_kind = out_kind;
     a.relu = (flags & LQ_EPI_RELU) ? 1 : 0;
+    a.a_u8s8 = (flags & LQ_EPI_A_U8S8) ? 1 : 0;
     a.splits = 1;
     char* wsb = (char*)d_workspace;
     int rc;
@@ -996,7 +1001,7 @@ static int gemm_entry(bool packed, const int8_t* d_A, int64_t lda, const int8_t*
         a.a_sums = (int32_t*)(wsb + ws.a_sums);
         if ((rc = lq_row_sums_i8(d_A, lda, M, K, (int32_t*)a.a_sums, stream))) return rc;
     }
-    if (d_a_zero_point) {
+    if (has_za) {
         if (d_b_sums) {
             a.b_sums = d_b_sums;
         } else {

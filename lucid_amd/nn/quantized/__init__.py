@@ -1,0 +1,23 @@
+"""``lucid_amd.nn.quantized``: Lucid's quantized inference modules
+(lucid/nn/quantized/__init__.py) on the HIP backend.
+
+The int8 layers keep Lucid's buffers and ``state_dict`` layout and run the gfx950 W8A8
+MFMA GEMM over integer codes; ``QuantStub`` / ``DeQuantStub`` / ``Quantize`` /
+``DeQuantize`` / ``QuantWrapper`` mark the quantized region.
+"""
+
+from lucid_amd.nn.quantized.intrinsic import LinearReLU
+from lucid_amd.nn.quantized.linear import Linear
+from lucid_amd.nn.quantized.modules import (DeQuantize, DeQuantStub, Quantize, QuantStub,
+                                            QuantWrapper)
+
+__all__ = ["Linear", "LinearReLU", "QuantStub", "DeQuantStub", "Quantize", "DeQuantize",
+           "QuantWrapper"]
+
+
+def __getattr__(name: str):
+    import importlib
+
+    if name == "dynamic":
+        return importlib.import_module("lucid_amd.nn.quantized.dynamic")
+    raise AttributeError(f"module 'lucid_amd.nn.quantized' has no attribute {name!r}")

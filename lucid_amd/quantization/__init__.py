@@ -26,6 +26,15 @@ from lucid_amd.quantization.observer import (
     PerChannelMinMaxObserver,
     PlaceholderObserver,
 )
+from lucid_amd.quantization.qconfig import (
+    QConfig,
+    QConfigMapping,
+    get_default_qconfig,
+    get_default_qconfig_mapping,
+    get_minmax_qconfig,
+)
+from lucid_amd.quantization._quantize import convert, prepare, quantize_dynamic
+from lucid_amd.quantization.fuse_modules import fuse_modules
 
 __all__ = [
     "QScheme", "per_tensor_affine", "per_tensor_symmetric", "per_channel_affine",
@@ -33,5 +42,7 @@ __all__ = [
     "calculate_qparams", "quantize", "dequantize", "fake_quantize", "ObserverBase",
     "MinMaxObserver", "MovingAverageMinMaxObserver", "PerChannelMinMaxObserver",
     "MovingAveragePerChannelMinMaxObserver", "HistogramObserver", "FixedQParamsObserver",
-    "PlaceholderObserver", "NoopObserver",
+    "PlaceholderObserver", "NoopObserver", "QConfig", "QConfigMapping", "get_default_qconfig",
+    "get_default_qconfig_mapping", "get_minmax_qconfig", "prepare", "convert", "quantize_dynamic",
+    "fuse_modules",
 ]

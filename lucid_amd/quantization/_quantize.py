@@ -1,0 +1,242 @@
+"""Dispatch registration: ``prepare`` / ``convert`` / ``quantize_dynamic``
+(lucid/quantization/_quantize.py:46-778).
+
+* ``prepare`` resolves every module's ``QConfig``, gives each observed type (Linear,
+  Conv2d, the fused blocks, ``QuantStub``) an ``activation_post_process`` observer fed by a
+  forward hook (_quantize.py:199-304);
+* ``convert`` swaps each calibrated module for its quantized form through the
+  ``type -> from_float`` mapping (``_quant_mapping``, _quantize.py:74-121), depth first, in
+  place of the child so a ``Sequential`` keeps its order (_quantize.py:759-778);
+* ``quantize_dynamic`` swaps ``Linear`` for the dynamic int8 layer per ``qconfig_spec``
+  (_quantize.py:429-620).
+
+With ``lucid_amd.backends.quantized.use_mlx()`` the Linear family is routed to the
+group-wise weight-only layer instead, when ``in_features`` is divisible by a supported
+group size (``_mlx_group_size``: 64, then 128, then 32; _quantize.py:134-185).
+"""
+
+from __future__ import annotations
+
+import copy
+import warnings
+from typing import Callable
+
+from lucid_amd.nn.module import Module
+from lucid_amd.quantization._propagate import (QConfigResolver, normalize_dynamic_spec,
+                                               weight_dtype)
+from lucid_amd.quantization._qscheme import QDtype, qint8
+from lucid_amd.quantization.qconfig import QConfig, QConfigMapping, get_default_qconfig_mapping
+
+_FromFloat = Callable[[Module], Module]
+
+
+def _observed_types() -> tuple[type, ...]:
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.intrinsic as nni
+    import lucid_amd.nn.quantized as nnq
+
+    return (nn.Linear, nn.Conv2d, nni.ConvReLU2d, nni.LinearReLU, nnq.QuantStub)
+
+
+def _quant_mapping() -> dict[type, _FromFloat]:
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.intrinsic as nni
+    import lucid_amd.nn.quantized as nnq
+
+    mapping: dict[type, _FromFloat] = {
+        nn.Linear: nnq.Linear.from_float,
+        nni.LinearReLU: nnq.LinearReLU.from_float,
+        nnq.QuantStub: nnq.Quantize.from_float,
+        nnq.DeQuantStub: nnq.DeQuantize.from_float,
+    }
+    if hasattr(nnq, "Conv2d"):
+        mapping[nn.Conv2d] = nnq.Conv2d.from_float
+        mapping[nni.ConvReLU2d] = nnq.ConvReLU2d.from_float
+    return mapping
+
+
+def _mlx_weight_bits(mod: Module) -> int:
+    """Weight bit width (4 / 8) for the group-wise path, from the module's qconfig."""
+    qcfg = getattr(mod, "qconfig", None)
+    if qcfg is not None:
+        bits = getattr(getattr(qcfg.weight(), "qdtype", None), "bits", None)
+        if isinstance(bits, int) and bits in (4, 8):
+            return bits
+    return 8
+
+
+def _mlx_group_size(in_features: int) -> int | None:
+    """Largest supported group size (64, 128, 32 in that order) dividing ``in_features``."""
+    for gs in (64, 128, 32):
+        if in_features % gs == 0:
+            return gs
+    return None
+
+
+def _group_layer():
+    import lucid_amd.nn.quantized as nnq
+
+    cls = getattr(nnq, "QuantizedLinearMLX", None)
+    if cls is None:
+        raise NotImplementedError("the group-wise weight-only Linear is not built into this "
+                                  "backend; set lucid_amd.backends.quantized.engine = 'reference'")
+    return cls
+
+
+def _mlx_linear_builder(relu: bool) -> _FromFloat:
+    import lucid_amd.nn.quantized as nnq
+
+    dequant = nnq.LinearReLU.from_float if relu else nnq.Linear.from_float
+
+    def build(child: Module) -> Module:
+        inner = child[0] if relu else child
+        gs = _mlx_group_size(inner.in_features)
+        if gs is None:
+            return dequant(child)
+        return _group_layer().from_float(inner, bits=_mlx_weight_bits(child), group_size=gs,
+                                         relu=relu)
+
+    return build
+
+
+def _mlx_dynamic_builder():
+    import lucid_amd.nn.quantized.dynamic as nnqd
+
+    def build(child: Module, dtype: QDtype) -> Module:
+        gs = _mlx_group_size(child.in_features)
+        if gs is None:
+            return nnqd.Linear.from_float(child, dtype)
+        return _group_layer().from_float(child, bits=dtype.bits, group_size=gs, relu=False)
+
+    return build
+
+
+def _make_observer_hook(obs: Module):
+    def hook(_module, _args, output):
+        obs(output)
+
+    return hook
+
+
+def prepare(model: Module, qconfig: QConfig | QConfigMapping | None = None,
+            inplace: bool = False) -> Module:
+    """Attach activation observers to every quantizable module (static PTQ)."""
+    resolver = QConfigResolver.from_argument(qconfig, get_default_qconfig_mapping)
+    model = model if inplace else copy.deepcopy(model)
+    model.eval()
+    observed = _observed_types()
+    n_matched = 0
+    for _name, mod, _path, qcfg in map(resolver.stamp, resolver.walk(model)):
+        if qcfg is None or not isinstance(mod, observed):
+            continue
+        obs = qcfg.activation()
+        mod.activation_post_process = obs
+        mod.register_forward_hook(_make_observer_hook(obs))
+        n_matched += 1
+    if n_matched == 0:
+        warnings.warn("prepare(): the QConfigMapping matched no quantizable modules -- "
+                      "convert() will leave this model unchanged.", stacklevel=2)
+    return model
+
+
+def _convert_recursive(module: Module, mapping: dict, always: tuple) -> None:
+    for name, child in list(module.named_children()):
+        build = mapping.get(type(child))
+        excluded = "qconfig" in child.__dict__ and child.__dict__["qconfig"] is None
+        convertible = build is not None and (
+            (isinstance(child, always) and not excluded)
+            or "activation_post_process" in child._modules
+        )
+        if convertible:
+            setattr(module, name, build(child))
+        else:
+            _convert_recursive(child, mapping, always)
+
+
+def convert(model: Module, inplace: bool = False) -> Module:
+    """Swap calibrated modules for their quantized forms."""
+    import lucid_amd.backends as backends
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.intrinsic as nni
+    import lucid_amd.nn.quantized as nnq
+
+    model = model if inplace else copy.deepcopy(model)
+    mapping = _quant_mapping()
+    if backends.quantized.use_mlx():
+        mapping = dict(mapping)
+        mapping[nn.Linear] = _mlx_linear_builder(relu=False)
+        mapping[nni.LinearReLU] = _mlx_linear_builder(relu=True)
+    _convert_recursive(model, mapping, always=(nnq.DeQuantStub,))
+    QConfigResolver.strip(model)
+    model.eval()
+    return model
+
+
+def _dynamic_builders() -> dict:
+    import lucid_amd.backends as backends
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized.dynamic as nnqd
+
+    builders = {nn.Linear: nnqd.Linear.from_float}
+    if backends.quantized.use_mlx():
+        builders[nn.Linear] = _mlx_dynamic_builder()
+    return builders
+
+
+class _DynamicSwapper:
+    def __init__(self, spec, mapping: dict, dtype: QDtype) -> None:
+        self.resolver = QConfigResolver(spec.mapping)
+        self._targets = spec.targets
+        self._mapping = mapping
+        self._dtype = dtype
+        self._swapped = 0
+        self._unmapped: set[type] = set()
+
+    def apply(self, model: Module) -> Module:
+        swapped = self._swap(model)
+        QConfigResolver.strip(swapped)
+        return swapped
+
+    def _swap(self, model: Module) -> Module:
+        root = self.resolver.root(model)
+        if root.qconfig is not None and type(model) in self._mapping:
+            return self.build(model, root.qconfig)
+        self.swap_children(root)
+        self._warn_if_left_float()
+        return model
+
+    def build(self, module: Module, qconfig: QConfig) -> Module:
+        self._swapped += 1
+        return self._mapping[type(module)](module, weight_dtype(qconfig, self._dtype))
+
+    def swap_children(self, parent) -> None:
+        for entry in self.resolver.children(parent.module, parent.path, parent.qconfig):
+            if entry.qconfig is not None and type(entry.module) in self._mapping:
+                setattr(parent.module, entry.name, self.build(entry.module, entry.qconfig))
+                continue
+            if (entry.qconfig is not None and self.resolver.is_targeted(entry.module, entry.path)
+                    and next(entry.module.children(), None) is None):
+                self._unmapped.add(type(entry.module))
+            self.swap_children(entry)
+
+    def _warn_if_left_float(self) -> None:
+        if self._unmapped:
+            mapped = sorted(t.__name__ for t in self._mapping)
+            warnings.warn(
+                f"quantize_dynamic(): {', '.join(sorted(t.__name__ for t in self._unmapped))} "
+                "has no dynamically quantized form and stays float; dynamic quantization "
+                f"covers {', '.join(mapped)}.", stacklevel=5)
+        elif self._swapped == 0:
+            warnings.warn("quantize_dynamic(): no module of a targeted type "
+                          f"({', '.join(self._targets) or 'none'}) found -- the model is "
+                          "returned unchanged.", stacklevel=5)
+
+
+def quantize_dynamic(model: Module, qconfig_spec=None, dtype: QDtype = qint8,
+                     inplace: bool = False) -> Module:
+    """Replace ``Linear`` layers with dynamically quantized int8 layers."""
+    model = model if inplace else copy.deepcopy(model)
+    model.eval()
+    builders = _dynamic_builders()
+    spec = normalize_dynamic_spec(qconfig_spec, dtype, tuple(builders))
+    return _DynamicSwapper(spec, builders, dtype).apply(model)

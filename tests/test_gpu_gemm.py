@@ -54,7 +54,8 @@ def packed_layout_oracle(B):
 
 def run_gemm(L, A, B, out_kind=O.OUT_I32, a_scale=None, b_scale=None, za=None, zb=None,
              b_sums=None, bias=None, out_scale=None, out_zp=None, qmin=-128, qmax=127,
-             relu=False, lda=None, ldb=None, ldc=None, workspace=True, packed=False):
+             relu=False, lda=None, ldb=None, ldc=None, workspace=True, packed=False,
+             flags=0):
     """Run lq_gemm_w8a8 (or lq_gemm_w8a8_packed) on host arrays; returns C [M, N]."""
     from lucid_amd import _C
 
@@ -89,7 +90,7 @@ def run_gemm(L, A, B, out_kind=O.OUT_I32, a_scale=None, b_scale=None, za=None, z
                 0 if sb is None or sb.size == 1 else 1,
                 opt(None if za is None else [za]), opt(zb), opt(b_sums, np.int32), opt(bias),
                 opt(None if out_scale is None else [out_scale]),
-                opt(None if out_zp is None else [out_zp]), qmin, qmax, out_kind, 1 if relu else 0,
+                opt(None if out_zp is None else [out_zp]), qmin, qmax, out_kind, (1 if relu else 0) | flags,
                 ws.data_ptr() if ws is not None else None, ws_bytes, None)
         return dC.numpy()[:, :N]
     _C.call("lq_gemm_w8a8", dA.data_ptr(), lda, dB.data_ptr(), ldb, dC.data_ptr(), ldc, M, N, K,
@@ -97,7 +98,7 @@ def run_gemm(L, A, B, out_kind=O.OUT_I32, a_scale=None, b_scale=None, za=None, z
             0 if sb is None or sb.size == 1 else 1,
             opt(None if za is None else [za]), opt(zb), opt(b_sums, np.int32), opt(bias),
             opt(None if out_scale is None else [out_scale]),
-            opt(None if out_zp is None else [out_zp]), qmin, qmax, out_kind, 1 if relu else 0,
+            opt(None if out_zp is None else [out_zp]), qmin, qmax, out_kind, (1 if relu else 0) | flags,
             ws.data_ptr() if ws is not None else None, ws_bytes, None)
     return dC.numpy()[:, :N]
 
@@ -280,6 +281,33 @@ def test_cached_weight_sums_and_scalar_scales(gpu):
     out = gpu.empty((N,), np.int32, "gpu")
     _C.call("lq_row_sums_i8", dB.data_ptr(), K, N, K, out.data_ptr(), None)
     np.testing.assert_array_equal(out.numpy(), sums)
+
+
+@pytest.mark.parametrize("M,N,K,packed", [(8, 200, 512, False), (8, 200, 512, True),
+                                            (100, 300, 256, True), (96, 200, 512, False),
+                                            (300, 1000, 256, False), (7, 9, 20, False),
+                                            (512, 1024, 1024, False)])
+def test_unsigned_activation_flag(gpu, M, N, K, packed):
+    """LQ_EPI_A_U8S8: A holds unsigned codes u as u - 128 and the zero point passed is the
+    unsigned grid's own; the kernel's result equals the signed form with za - 128."""
+    from lucid_amd import _C
+
+    rng = np.random.default_rng(M * 7 + N + K)
+    U = rng.integers(0, 256, size=(M, K))
+    A = (U - 128).astype(np.int8)
+    B = _codes(rng, (N, K))
+    b_scale = rng.uniform(1e-3, 1e-1, N).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    for zu, kind, relu in ((131.0, O.OUT_F32, False), (None, O.OUT_F32, True),
+                           (0.0, O.OUT_QU8S8, True), (255.0, O.OUT_F16, False)):
+        qmin, qmax = GRID.get(kind, (-128, 127))
+        sums = B.astype(np.int64).sum(axis=1).astype(np.int32) if packed else None
+        got = run_gemm(gpu, A, B, kind, np.float32(0.011), b_scale, zu, None, sums, bias, 0.05,
+                       128.0, qmin, qmax, relu, packed=packed, flags=_C.EPI_A_U8S8)
+        want = O.gemm_w8a8(A, B, np.float32(0.011), b_scale, za=(zu or 0.0) - 128.0, bias=bias,
+                           out_scale=0.05, out_zp=128.0, qmin=qmin, qmax=qmax, out_kind=kind,
+                           relu=relu)
+        np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8))
 
 
 def test_zero_point_needs_workspace(gpu):

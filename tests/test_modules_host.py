@@ -1,0 +1,191 @@
+"""Host-side logic of the module layer (no GPU): config resolution, prepare's observer
+wiring, fusion and the BatchNorm fold, the engine selector, state_dict layouts."""
+
+from __future__ import annotations
+
+import warnings
+
+import numpy as np
+import pytest
+
+
+def _model():
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized as nnq
+
+    return nn.Sequential(nnq.QuantStub(), nn.Linear(16, 8), nn.ReLU(), nn.Linear(8, 4),
+                         nnq.DeQuantStub())
+
+
+def test_qconfig_mapping_precedence():
+    import lucid_amd.nn as nn
+    from lucid_amd.quantization import QConfigMapping, get_default_qconfig, get_minmax_qconfig
+
+    a, b = get_default_qconfig(), get_minmax_qconfig()
+    m = QConfigMapping().set_global(a).set_object_type(nn.Linear, b).set_module_name("3", None)
+    assert m.get_qconfig(nn.Linear, "1") is b
+    assert m.get_qconfig(nn.Linear, "3") is None
+    assert m.get_qconfig(nn.ReLU, "2") is a
+
+
+def test_prepare_attaches_observers_and_hooks():
+    import lucid_amd.nn as nn
+    import lucid_amd.quantization as Q
+    from lucid_amd.quantization.observer import MinMaxObserver
+
+    model = _model()
+    prepared = Q.prepare(model, Q.get_minmax_qconfig())
+    assert prepared is not model
+    for idx in ("0", "1", "3"):
+        mod = getattr(prepared, idx)
+        assert isinstance(mod.activation_post_process, MinMaxObserver)
+        assert len(mod._forward_hooks) == 1
+    assert not hasattr(prepared[2], "activation_post_process")
+    assert isinstance(prepared[1], nn.Linear) and prepared.training is False
+    # the observer buffers join the state dict under the module's prefix
+    assert "1.activation_post_process.min_val" in prepared.state_dict()
+
+
+def test_prepare_respects_none_and_warns_on_no_match():
+    import lucid_amd.nn as nn
+    import lucid_amd.quantization as Q
+
+    model = _model()
+    mapping = Q.QConfigMapping().set_global(Q.get_minmax_qconfig()).set_module_name("3", None)
+    prepared = Q.prepare(model, mapping)
+    assert hasattr(prepared[1], "activation_post_process")
+    assert not hasattr(prepared[3], "activation_post_process")
+    with pytest.warns(UserWarning, match="matched no quantizable modules"):
+        Q.prepare(nn.Sequential(nn.ReLU()), Q.get_minmax_qconfig())
+    with pytest.raises(TypeError):
+        Q.prepare(model, qconfig="not a qconfig")
+
+
+def test_fuse_linear_relu_and_identity_slots():
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.intrinsic as nni
+    import lucid_amd.quantization as Q
+
+    fused = Q.fuse_modules(_model(), [["1", "2"]])
+    assert isinstance(fused[1], nni.LinearReLU) and isinstance(fused[2], nn.Identity)
+    assert isinstance(fused[1][0], nn.Linear) and isinstance(fused[1][1], nn.ReLU)
+    with pytest.raises(ValueError, match="unsupported fusion pattern"):
+        Q.fuse_modules(_model(), [["2", "3"]])
+
+
+def test_bn_fold_closed_form():
+    """w' = w * gamma / sqrt(var + eps), b' = (b - mean) * gamma / sqrt(var + eps) + beta,
+    against float64 (fusion.py:52-106; the reference checks the fold at atol 1e-4)."""
+    import lucid_amd.nn as nn
+    from lucid_amd._tensor import tensor
+    from lucid_amd.quantization.fuse_modules import fuse_conv_bn_eval
+
+    rng = np.random.default_rng(0)
+    conv = nn.Conv2d(3, 6, 3)
+    bn = nn.BatchNorm2d(6)
+    bn.running_mean = tensor(rng.normal(0, 1, 6).astype(np.float32))
+    bn.running_var = tensor(rng.uniform(0.5, 2, 6).astype(np.float32))
+    bn.weight = nn.Parameter(tensor(rng.normal(1, 0.1, 6).astype(np.float32)))
+    bn.bias = nn.Parameter(tensor(rng.normal(0, 0.1, 6).astype(np.float32)))
+    conv.eval(), bn.eval()
+    fused = fuse_conv_bn_eval(conv, bn)
+    w = conv.weight.numpy().astype(np.float64)
+    g = bn.weight.numpy() / np.sqrt(bn.running_var.numpy().astype(np.float64) + bn.eps)
+    np.testing.assert_allclose(fused.weight.numpy(), w * g[:, None, None, None], rtol=1e-6)
+    want_b = (conv.bias.numpy() - bn.running_mean.numpy()) * g + bn.bias.numpy()
+    np.testing.assert_allclose(fused.bias.numpy(), want_b, rtol=1e-6, atol=1e-7)
+    assert isinstance(fused, nn.Conv2d) and fused is not conv
+    bn.train()
+    with pytest.raises(AssertionError, match="eval"):
+        fuse_conv_bn_eval(conv, bn)
+
+
+def test_fuse_conv_bn_relu_run():
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.intrinsic as nni
+    import lucid_amd.quantization as Q
+
+    model = nn.Sequential(nn.Conv2d(3, 4, 3), nn.BatchNorm2d(4), nn.ReLU()).eval()
+    fused = Q.fuse_modules(model, [["0", "1", "2"]])
+    assert isinstance(fused[0], nni.ConvReLU2d)
+    assert isinstance(fused[1], nn.Identity) and isinstance(fused[2], nn.Identity)
+
+
+def test_engine_selector():
+    import lucid_amd.backends as backends
+    from lucid_amd.quantization._quantize import _mlx_group_size
+
+    q = backends.quantized
+    assert q.engine == "auto"
+    with pytest.raises(ValueError):
+        q.engine = "cuda"
+    try:
+        q.engine = "reference"
+        assert q.use_mlx() is False
+        q.engine = "mlx_group"
+        assert q.use_mlx() is True
+    finally:
+        q.engine = "auto"
+    assert _mlx_group_size(784) is None and _mlx_group_size(256) == 64
+    assert _mlx_group_size(128 + 256) == 64 and _mlx_group_size(96) == 32
+    assert _mlx_group_size(128 * 3) == 64
+
+
+def test_dynamic_spec_normalisation():
+    import lucid_amd.nn as nn
+    from lucid_amd.quantization import qint8
+    from lucid_amd.quantization._propagate import normalize_dynamic_spec, weight_dtype
+
+    spec = normalize_dynamic_spec({nn.Linear: qint8, "head": None}, qint8, (nn.Linear,))
+    assert spec.targets == ("Linear",)
+    assert spec.mapping.get_qconfig(nn.Linear, "x") is not None
+    assert spec.mapping.get_qconfig(nn.Linear, "head") is None
+    assert weight_dtype(spec.mapping.get_qconfig(nn.Linear, "x"), None) is qint8
+    with pytest.raises(TypeError):
+        normalize_dynamic_spec("Linear", qint8, (nn.Linear,))
+    with pytest.raises(TypeError):
+        normalize_dynamic_spec({3: qint8}, qint8, (nn.Linear,))
+
+
+def test_quantized_module_state_dict_layouts():
+    """Lucid's buffer names, dtypes and shapes (lucid/nn/quantized/linear.py:190-203,
+    dynamic/linear.py:68-83, modules.py:229-278)."""
+    import lucid_amd.nn.quantized as nnq
+    import lucid_amd.nn.quantized.dynamic as nnqd
+
+    sd = nnq.Linear(16, 8).state_dict()
+    assert list(sd) == ["weight_int8", "weight_scale", "weight_zero_point", "bias", "scale",
+                        "zero_point"]
+    assert sd["weight_int8"].dtype == np.int8 and sd["weight_int8"].shape == (8, 16)
+    assert sd["weight_scale"].dtype == np.float32 and sd["weight_scale"].shape == (8,)
+    assert sd["scale"].shape == () and sd["zero_point"].shape == ()
+    assert "bias" not in nnq.Linear(16, 8, bias=False).state_dict()
+    assert list(nnqd.Linear(16, 8).state_dict()) == ["weight_int8", "weight_scale",
+                                                     "weight_zero_point", "bias"]
+    assert list(nnq.Quantize(0.1, 3).state_dict()) == ["scale", "zero_point"]
+    assert nnq.DeQuantize().state_dict() == {}
+    w = nnq.QuantWrapper(nnq.Linear(4, 2))
+    assert [n for n, _ in w.named_children()] == ["quant", "module", "dequant"]
+
+
+def test_quantized_ops_refuse_cpu_tensors():
+    """No CPU fallback: the quantized modules raise on host tensors."""
+    import lucid_amd as L
+    import lucid_amd.nn.quantized as nnq
+    import lucid_amd.nn.quantized.dynamic as nnqd
+
+    x = L.tensor(np.zeros((2, 16), np.float32))
+    for mod in (nnq.Linear(16, 8), nnqd.Linear(16, 8)):
+        with pytest.raises(L.LucidError, match="GPU"):
+            mod(x)
+
+
+def test_stubs_are_identity_before_prepare():
+    import lucid_amd as L
+    import lucid_amd.nn.quantized as nnq
+
+    x = L.tensor(np.arange(3, dtype=np.float32))
+    assert nnq.QuantStub()(x) is x and nnq.DeQuantStub()(x) is x and nnq.DeQuantize()(x) is x
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        assert nnq.Quantize(0.1, 0)(L.tensor(np.arange(3, dtype=np.int32))).dtype == np.int32
