@@ -244,6 +244,46 @@ int lq_gemm_w8a8_packed(const int8_t* d_A, int64_t lda, const int8_t* d_B_packed
 int lq_row_sums_i8(const int8_t* d_X, int64_t ld, int64_t rows, int64_t K, int32_t* d_sums,
                    void* stream);
 
+/* ---- weight-only int8 GEMV / skinny GEMM -------------------------------------------- */
+/* y[m,n] = w_scale[n] * (sum_k W[n,k] x[m,k] - zb[n] sum_k x[m,k]) + bias[n] (ReLU with
+ * LQ_EPI_RELU): Lucid's sidecar Linear on a float input, dequantize -> F.linear
+ * (lucid/nn/quantized/linear.py:206-210 -> lucid/_C/nn/Linear.cpp:199), without forming
+ * the float weight.  x / y of x_dtype (LQ_F32 or LQ_F16), W int8 [N, ldw] row-major,
+ * d_w_zero_point / d_bias may be NULL.  Float32 accumulation (tolerance parity: the float
+ * GEMM's summation order is the reference's own).  Any M; tuned for M <= 16.  Needs
+ * lq_gemv_w8_workspace_size(M, N, K) bytes of device workspace. */
+size_t lq_gemv_w8_workspace_size(int64_t M, int64_t N, int64_t K);
+int lq_gemv_w8(const void* d_x, int x_dtype, int64_t ldx, const int8_t* d_W, int64_t ldw,
+               const float* d_w_scale, const float* d_w_zero_point, const float* d_bias,
+               void* d_y, int64_t ldy, int64_t M, int64_t N, int64_t K, int flags,
+               void* d_workspace, size_t workspace_bytes, void* stream);
+
+/* ---- group-wise packed weights (QuantizedLinearMLX layout) -------------------------- */
+/* Group-wise affine quantize of W[N,K] (float32) with groups of group_size (32/64/128) along K:
+ * s_g = (max_g - min_g) / (2^bits - 1), b_g = min_g, c = clip(rne((w - b_g) / s_g), 0, 2^bits-1)
+ * (codes 0 when s_g is not > 0), 32/bits codes per uint32 little-end first.  packed
+ * [N, K*bits/32] uint32, scales/biases [N, K/group_size] float32.  Replaces
+ * _C_engine.quantized.quantize (lucid/_C/bindings/bind_quantized.cpp:17-27 ->
+ * lucid/_C/ops/quantized/QuantizedMatmul.cpp:111-121; formula lucid/quantization/_qgemm.py:84-97). */
+int lq_group_quantize_f32(const float* d_w, int64_t N, int64_t K, int group_size, int bits,
+                          uint32_t* d_packed, float* d_scales, float* d_biases, void* stream);
+/* w_hat = fl32(fl32(c * s_g) + b_g) as float32 [N, K] (d_biases NULL: b_g = 0).  Replaces
+ * _C_engine.quantized.dequantize (QuantizedMatmul.cpp:123-141, _qgemm.py:167-170). */
+int lq_group_dequantize_f32(const uint32_t* d_packed, const float* d_scales,
+                            const float* d_biases, int64_t N, int64_t K, int group_size,
+                            int bits, float* d_w, void* stream);
+/* y[m,n] = sum_k x[m,k] w_hat[n,k] (+ bias[n]) (ReLU with LQ_EPI_RELU), x / y of x_dtype
+ * (LQ_F32 or LQ_F16), float32 accumulation, without forming w_hat.  Replaces
+ * _C_engine.quantized.quantized_matmul (QuantizedMatmul.cpp:143-163) for transpose = 1;
+ * transpose = 0 returns LQ_ERR_UNSUPPORTED.  d_biases (group offsets) and d_bias (layer
+ * bias) may be NULL.  Needs lq_group_matmul_workspace_size(M, N, K, group_size) bytes. */
+size_t lq_group_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int group_size);
+int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d_packed,
+                    const float* d_scales, const float* d_biases, const float* d_bias, void* d_y,
+                    int64_t ldy, int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                    int transpose, int flags, void* d_workspace, size_t workspace_bytes,
+                    void* stream);
+
 /* ---- float helpers around the quantized path ----------------------------------- */
 /* y = (x <= 0) ? +0 : x, NaN passes (the CPU relu of backend/cpu/Vdsp.cpp vrelu_f32,
  * reached from nn.ReLU between quantized layers). */

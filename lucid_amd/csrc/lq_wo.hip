@@ -1,0 +1,864 @@
+// lq_wo.hip -- weight-only quantized GEMV / skinny GEMM on CDNA4 MFMA (v_mfma_f32_16x16x32_f16).
+//
+// Two weight formats, one kernel:
+//  * per-channel int8 weights (the sidecar Linear's weight_int8 [N,K], weight_scale [N],
+//    weight_zero_point [N]):  y = s[n] * (sum_k c[n,k] x[m,k] - z[n] sum_k x[m,k]) + bias[n]
+//    -- Lucid's dequantize -> F.linear for a float input (lucid/nn/quantized/linear.py:206-210);
+//  * group-wise packed 4/8-bit weights (QuantizedLinearMLX layout: uint32 words holding
+//    32/bits codes little-end first, scales/biases [N, K/gs]):
+//    y = sum_g (s[n,g] sum_{k in g} c[n,k] x[m,k] + b[n,g] sum_{k in g} x[m,k]) + bias[n]
+//    -- quantized_matmul with transpose=true (lucid/_C/ops/quantized/QuantizedMatmul.cpp:143-163,
+//    formula lucid/quantization/_qgemm.py:167-170).
+//
+// Operands.  The codes enter the MFMA as exact fp16 values: a code c of 8 or fewer bits is
+// placed under the exponent of 1024 (fp16 1024 + c, by v_perm byte placement or nibble
+// masks) and 1024 is subtracted in packed fp16.  A float32 activation enters as two fp16
+// terms hi + lo after an exact power-of-two pre-scale chosen per (row, k-block) so that the
+// block's max |x| lies in [2^14, 2^15): hi = fl16(x 2^e), lo = fl16(x 2^e - hi), ~22
+// significant bits per product, fp32 accumulation, and 2^-e applied to the block's sum.  A
+// float16 activation is its own hi term.
+//
+// Work split.  A workgroup of W waves owns 16 weight rows and one 16-row block of the
+// activations; its waves split K into equal runs of k-blocks (32*S k each, S = MFMA steps
+// per block) and stream their weight bytes with two blocks in flight.  The W partial sums
+// meet in LDS and are added in wave order (deterministic), then the epilogue runs.  One
+// launch per call, no workspace, no cross-workgroup synchronisation.
+//
+// K order inside a k-block: lane q (= l/16) of every step covers 8 consecutive k of its own
+// 8*S-wide quarter, so a block stays inside one weight group (group size 32*S) and a lane's
+// weight bytes for the block are one contiguous load.  Nibble pairs of a 4-bit word unpack
+// in the order 0,4,1,5,2,6,3,7 and the activation halves follow the same order.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+
+#include "lq_internal.h"
+
+namespace lq {
+namespace {
+
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u2v __attribute__((ext_vector_type(2)));
+
+constexpr int WO_MAX_WAVES = 16;
+constexpr int WO_RING = 4;  // k-blocks in flight per wave
+
+// Waves per workgroup: 16, or 8 for the group-wise variants whose ring of in-flight chunks
+// does not fit the 128 registers per lane of a 16-wave workgroup.
+constexpr int wo_max_waves(int S, bool xf32, bool grouped) {
+    return (grouped && S * (xf32 ? 2 : 1) >= 4) ? 8 : WO_MAX_WAVES;
+}
+
+__device__ __forceinline__ h2 bits_h2(uint32_t v) { return __builtin_bit_cast(h2, v); }
+
+// k offset of half h within a lane's 8-element step for a code width.
+template <int BITS>
+__device__ __forceinline__ int korder(int h) {
+    return BITS == 4 ? ((h & 1) * 4 + (h >> 1)) : h;
+}
+
+// Four bytes -> four halves (byte - off) in byte order.
+__device__ __forceinline__ void bytes_to_h2(uint32_t w, _Float16 off, h2& a, h2& b) {
+    const uint32_t p0 = __builtin_amdgcn_perm(0x64646464u, w, 0x04010400u);
+    const uint32_t p1 = __builtin_amdgcn_perm(0x64646464u, w, 0x04030402u);
+    const h2 o = {off, off};
+    a = bits_h2(p0) - o;
+    b = bits_h2(p1) - o;
+}
+
+// One MFMA step's 8 codes as fp16: 8-bit from two words (signed codes are xor'ed with
+// 0x80 so the byte is c + 128), 4-bit from one word.
+template <int BITS, bool SIGNED>
+__device__ __forceinline__ h8 unpack_step(const uint32_t* w) {
+    if constexpr (BITS == 8) {
+        const uint32_t x0 = SIGNED ? (w[0] ^ 0x80808080u) : w[0];
+        const uint32_t x1 = SIGNED ? (w[1] ^ 0x80808080u) : w[1];
+        const _Float16 off = SIGNED ? (_Float16)1152.0f : (_Float16)1024.0f;
+        h2 a, b, c, d;
+        bytes_to_h2(x0, off, a, b);
+        bytes_to_h2(x1, off, c, d);
+        return h8{a.x, a.y, b.x, b.y, c.x, c.y, d.x, d.y};
+    } else {
+        const h2 o = {(_Float16)1024.0f, (_Float16)1024.0f};
+        h2 r[4];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) r[s] = bits_h2(((w[0] >> (4 * s)) & 0x000F000Fu) | 0x64006400u) - o;
+        return h8{r[0].x, r[0].y, r[1].x, r[1].y, r[2].x, r[2].y, r[3].x, r[3].y};
+    }
+}
+
+__device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// ------------------------------------------------------------------ kernel
+
+struct WoArgs {
+    const void* x;
+    int64_t ldx;
+    const uint8_t* w;        // weight rows (int8 codes, or packed uint32 words as bytes)
+    int64_t ldw_bytes;
+    const float* w_scale;    // per-channel [N] or group [N][G]
+    const float* w_zp;       // per-channel zero points [N] or null
+    const float* g_bias;     // group biases [N][G] or null
+    const float* bias;       // layer bias [N] or null
+    void* y;
+    int64_t ldy;
+    int relu;
+    int M, N, K;
+    int G;                   // groups per row (group-wise)
+    int bpw;                 // k-blocks per wave (even; blocks past the last are zero work)
+};
+
+// A lane's weight bytes for one k-block: 8*S codes from k = kc.
+template <int BITS, int S>
+struct WChunk {
+    static constexpr int NW = S * BITS / 4;  // 32-bit words
+    uint32_t w[NW];
+};
+
+// A lane's activations for one k-block: 8*S values of one row from k = kc, raw.
+template <int S, bool XF32>
+struct XChunk {
+    static constexpr int NV = XF32 ? 2 * S : S;  // 16-byte units
+    vu4 v[NV];
+};
+
+// VEC loads are unconditional vector loads (the number in flight stays static, so the
+// compiler's wait counts are exact): weight rows past N are clamped to a valid row (their
+// outputs are never stored), activation rows past M to the last row, and a chunk at or past
+// K re-reads in-row bytes; the activation values of such lanes are replaced by 0 once
+// loaded, and an unpacked code is always a finite fp16, so the product is exactly 0.
+// Needs 16-byte aligned rows, K % (8S) == 0, K >= 8S.
+// !VEC: predicated scalar loads (unaligned rows or a ragged K).
+template <int BITS, int S, bool VEC>
+__device__ __forceinline__ void load_w(WChunk<BITS, S>& ch, const uint8_t* row, int kc, int K) {
+    constexpr int NW = WChunk<BITS, S>::NW;
+    constexpr int nk = 8 * S;
+    if constexpr (VEC) {
+        const uint8_t* p = row + (int64_t)min(kc, K - nk) * BITS / 8;
+        if constexpr (NW == 1) {
+            ch.w[0] = __builtin_nontemporal_load(reinterpret_cast<const uint32_t*>(p));
+        } else if constexpr (NW == 2) {
+            const u2v v = __builtin_nontemporal_load(reinterpret_cast<const u2v*>(p));
+            ch.w[0] = v.x; ch.w[1] = v.y;
+        } else {
+#pragma unroll
+            for (int i = 0; i < NW / 4; ++i) {
+                const vu4 v = __builtin_nontemporal_load(reinterpret_cast<const vu4*>(p) + i);
+                ch.w[4 * i] = v.x; ch.w[4 * i + 1] = v.y; ch.w[4 * i + 2] = v.z; ch.w[4 * i + 3] = v.w;
+            }
+        }
+    } else {
+        const uint8_t* p = row + (int64_t)kc * BITS / 8;
+#pragma unroll
+        for (int i = 0; i < NW; ++i) {
+            uint32_t v = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int k = kc + (i * 4 + b) * 8 / BITS;
+                if (k < K) v |= (uint32_t)p[i * 4 + b] << (8 * b);
+            }
+            ch.w[i] = v;
+        }
+    }
+}
+
+template <int S, bool XF32, bool VEC>
+__device__ __forceinline__ void load_x(XChunk<S, XF32>& xc, const void* xrow, bool row_ok, int kc, int K) {
+    constexpr int NV = XChunk<S, XF32>::NV;
+    constexpr int ES = XF32 ? 4 : 2;  // element bytes
+    if constexpr (VEC) {
+        // always a valid in-row address; rows past M and chunks past K are zeroed after the
+        // wait, in compute (a select here would pull the wait forward)
+        const vu4* p = reinterpret_cast<const vu4*>(static_cast<const uint8_t*>(xrow) +
+                                                    (int64_t)min(kc, K - 8 * S) * ES);
+#pragma unroll
+        for (int i = 0; i < NV; ++i) xc.v[i] = p[i];
+    } else {
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            uint32_t w4[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                uint32_t word = 0;
+                if constexpr (XF32) {
+                    const int k = kc + i * 4 + e;
+                    if (row_ok && k < K) word = static_cast<const uint32_t*>(xrow)[k];
+                } else {
+#pragma unroll
+                    for (int hh = 0; hh < 2; ++hh) {
+                        const int k = kc + i * 8 + e * 2 + hh;
+                        if (row_ok && k < K)
+                            word |= (uint32_t)static_cast<const uint16_t*>(xrow)[k] << (16 * hh);
+                    }
+                }
+                w4[e] = word;
+            }
+            xc.v[i] = vu4{w4[0], w4[1], w4[2], w4[3]};
+        }
+    }
+}
+
+template <int S, bool XF32>
+__device__ __forceinline__ float x_at(const XChunk<S, XF32>& xc, int i) {
+    if constexpr (XF32) {
+        return __uint_as_float(xc.v[i >> 2][i & 3]);
+    } else {
+        const uint32_t w = xc.v[i >> 3][(i >> 1) & 3];
+        return (float)bits_h2(w)[i & 1];
+    }
+}
+
+template <int BITS, bool SIGNED, int S, bool XF32, bool GROUPED, bool VEC>
+__global__ __launch_bounds__((64 * wo_max_waves(S, XF32, GROUPED))) void wo_gemv_kernel(WoArgs a) {
+    constexpr int NW = WChunk<BITS, S>::NW;
+    constexpr int NX = 8 * S;
+    extern __shared__ __attribute__((aligned(16))) float wo_lds[];
+    const int W = blockDim.x >> 6;
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int q = lane >> 4, l16 = lane & 15;
+    const int n0 = blockIdx.x * 16;
+    const int m = blockIdx.y * 16 + l16;  // this lane's activation row / output column
+    const int TW = W * a.bpw;             // k-blocks over all waves (padded)
+
+    // LDS: [reduction W x 64 x 4][x sums W x 64][group scales 16 x TW][group biases 16 x TW]
+    float* red = wo_lds;
+    float* redx = red + W * 256;
+    float* sc_lds = redx + W * 64;
+    float* bi_lds = sc_lds + 16 * TW;
+    if constexpr (GROUPED) {
+        for (int i = tid; i < 16 * TW; i += blockDim.x) {
+            const int n = min(n0 + i / TW, a.N - 1);
+            const int64_t gi = (int64_t)n * a.G + min(i % TW, a.G - 1);
+            sc_lds[i] = a.w_scale[gi];
+            bi_lds[i] = a.g_bias ? a.g_bias[gi] : 0.0f;
+        }
+        __syncthreads();
+    }
+
+    const bool row_ok = m < a.M;
+    const void* xrow = static_cast<const uint8_t*>(a.x) + (int64_t)min(m, a.M - 1) * a.ldx * (XF32 ? 4 : 2);
+    const uint8_t* wrow = a.w + (int64_t)min(n0 + l16, a.N - 1) * a.ldw_bytes;
+
+    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+    float xtot = 0.0f;
+
+    auto load_block = [&](WChunk<BITS, S>& wc, XChunk<S, XF32>& xc, int t) {
+        const int kc = t * 32 * S + q * 8 * S;
+        load_w<BITS, S, VEC>(wc, wrow, kc, a.K);
+        load_x<S, XF32, VEC>(xc, xrow, row_ok, kc, a.K);
+        // keep the prefetch where it is: the scheduler would otherwise sink these loads to
+        // their first use and wait on them at once
+        __builtin_amdgcn_sched_barrier(0);
+    };
+    auto compute_block = [&](const WChunk<BITS, S>& wc, const XChunk<S, XF32>& xc, int t) {
+        // the block's pre-scale for this lane's row, shared by the 4 lanes of the row
+        float xs[NX];
+        float amax = 0.0f, bsum = 0.0f;
+        const bool live = row_ok && t * 32 * S + q * 8 * S < a.K;
+#pragma unroll
+        for (int i = 0; i < NX; ++i) {
+            xs[i] = live ? x_at<S, XF32>(xc, i) : 0.0f;
+            amax = fmaxf(amax, fabsf(xs[i]));
+            bsum += xs[i];
+        }
+        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+        bsum += __shfl_xor(bsum, 16, 64);
+        bsum += __shfl_xor(bsum, 32, 64);
+        int e = 0;
+        if (XF32 && amax > 0.0f && amax <= 3.0e38f) e = min(max(14 - ilogbf(amax), -120), 120);
+        const float up = XF32 ? ldexpf(1.0f, e) : 1.0f;
+        f4 blk = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < S; ++j) {
+            h8 hi, lo;
+#pragma unroll
+            for (int h = 0; h < 8; ++h) {
+                const float v = xs[8 * j + korder<BITS>(h)] * up;
+                const _Float16 vh = (_Float16)v;
+                hi[h] = vh;
+                if constexpr (XF32) lo[h] = (_Float16)(v - (float)vh);
+            }
+            const h8 wa = unpack_step<BITS, SIGNED>(&wc.w[j * NW / S]);
+            blk = mfma16(wa, hi, blk);
+            if constexpr (XF32) blk = mfma16(wa, lo, blk);
+        }
+        const float down = XF32 ? ldexpf(1.0f, -e) : 1.0f;
+        if constexpr (GROUPED) {
+            const int tw = t;  // block index within the padded run of this workgroup
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int rl = 4 * q + i;
+                acc[i] += sc_lds[rl * TW + tw] * (blk[i] * down) + bi_lds[rl * TW + tw] * bsum;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += blk[i] * down;
+            xtot += bsum;
+        }
+    };
+
+    // a ring of WO_RING blocks in flight: bpw is a multiple of WO_RING and the last round is
+    // peeled, so every load is unconditional and used, and each block's wait leaves the
+    // WO_RING - 1 younger blocks in flight
+    // (the predicated scalar loads of !VEC keep one block at a time: their registers would
+    // not fit a ring)
+    constexpr int RING = VEC ? WO_RING : 1;
+    const int t0 = wave * a.bpw;
+    WChunk<BITS, S> wr[RING];
+    XChunk<S, XF32> xr[RING];
+#pragma unroll
+    for (int j = 0; j < RING; ++j) load_block(wr[j], xr[j], t0 + j);
+    int g = 0;
+    for (; g + RING < a.bpw; g += RING) {
+#pragma unroll
+        for (int j = 0; j < RING; ++j) {
+            compute_block(wr[j], xr[j], t0 + g + j);
+            load_block(wr[j], xr[j], t0 + g + RING + j);
+        }
+    }
+#pragma unroll
+    for (int j = 0; j < RING; ++j) compute_block(wr[j], xr[j], t0 + g + j);
+
+    // partial sums meet in LDS; each output is summed in wave order
+    *reinterpret_cast<f4*>(red + (wave * 64 + lane) * 4) = acc;
+    if (!GROUPED && q == 0) redx[wave * 64 + l16] = xtot;
+    __syncthreads();
+    for (int o = tid; o < 256; o += blockDim.x) {  // W may be as small as 1
+        const int ol = o >> 2, oi = o & 3;  // output of lane ol, register oi
+        const int on = n0 + 4 * (ol >> 4) + oi;
+        const int om = blockIdx.y * 16 + (ol & 15);
+        if (on < a.N && om < a.M) {
+            float v = 0.0f;
+            for (int w = 0; w < W; ++w) v += red[(w * 64 + ol) * 4 + oi];
+            if constexpr (!GROUPED) {
+                if (a.w_zp) {
+                    float xt = 0.0f;
+                    for (int w = 0; w < W; ++w) xt += redx[w * 64 + (ol & 15)];
+                    v = v - a.w_zp[on] * xt;
+                }
+                v = a.w_scale[on] * v;
+            }
+            if (a.bias) v = v + a.bias[on];
+            if (a.relu && v <= 0.0f) v = 0.0f;
+            if constexpr (XF32)
+                reinterpret_cast<float*>(a.y)[(int64_t)om * a.ldy + on] = v;
+            else
+                reinterpret_cast<_Float16*>(a.y)[(int64_t)om * a.ldy + on] = (_Float16)v;
+        }
+    }
+}
+
+// ------------------------------------------------- one or two activation rows (VALU)
+//
+// For M <= 2 the MFMA's 16 activation columns are mostly empty and the per-block hi/lo split
+// of x would dominate; a classic GEMV is cheaper.  The workgroup stages its (at most two)
+// activation rows in LDS as fp32 once; each wave then owns whole weight rows: lane l takes
+// the 16-byte chunks l, l + 64, ... of its row, issues all of them at once (J chunks in flight,
+// J a template step), converts each code with one instruction (v_cvt_f32_i32 / ubyte with a
+// byte select) and accumulates in fp32 with FMA.  A 64-lane shuffle reduction finishes each
+// row.  The LDS copy of x is swizzled (16-byte slot f of a 256-byte row stored at
+// f ^ ... rotated by f >> 4) so the 64 lanes' float4 reads of their chunks are conflict-free.
+
+struct WvArgs {
+    const void* x;
+    int64_t ldx;
+    const uint8_t* w;
+    int64_t ldw_bytes;
+    const float* w_scale;    // per-channel [N] or group [N][G]
+    const float* w_zp;       // per-channel zero points [N] or null
+    const float* g_bias;     // group biases [N][G] or null
+    const float* bias;       // layer bias [N] or null
+    void* y;
+    int64_t ldy;
+    int relu;
+    int M, N, K;
+    int G, gs;
+    int NC;                  // 16-byte chunks per weight row
+    int Kpad;                // staged activation length (J * 64 chunks of codes)
+};
+
+__device__ __forceinline__ int wv_slot(int k) {
+    // float index k -> swizzled float index: 16-byte slot f = k / 4 rotated within its
+    // 256-byte LDS row by f >> 4
+    const int f = k >> 2;
+    return (((f & ~15) | ((f + (f >> 4)) & 15)) << 2) | (k & 3);
+}
+
+__device__ __forceinline__ uint32_t opaque_and(uint32_t v, uint32_t m) {
+    uint32_t r;
+    __asm__("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(v), "v"(m));
+    return r;
+}
+
+template <int BITS, bool SIGNED, bool GROUPED, int MX, bool XF32, int J>
+__global__ __launch_bounds__(1024) void wo_gemv_valu_kernel(WvArgs a) {
+    constexpr int CK = 16 * 8 / BITS;  // codes per 16-byte chunk
+    extern __shared__ __attribute__((aligned(16))) float wv_lds[];
+    float* xs = wv_lds;                                   // [MX][Kpad], swizzled
+    float* gsum = xs + MX * a.Kpad;                       // [MX][G] (group-wise) or [MX] totals
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int waves = blockDim.x >> 6;
+    const int n = blockIdx.x * waves + wave;
+    const bool n_ok = n < a.N;
+    const uint8_t* row = a.w + (int64_t)min(n, a.N - 1) * a.ldw_bytes;
+
+    // every chunk load at once, before the activation staging so the two latencies overlap
+    // (clamped to the row; chunks past the row meet zero x)
+    vu4 wc[J];
+    float sg[GROUPED ? J : 1], bg[GROUPED ? J : 1];
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int c = min(lane + 64 * j, a.NC - 1);
+        wc[j] = __builtin_nontemporal_load(reinterpret_cast<const vu4*>(row) + c);
+        if constexpr (GROUPED) {
+            const int64_t gi = (int64_t)min(n, a.N - 1) * a.G + min((lane + 64 * j) * CK / a.gs, a.G - 1);
+            sg[j] = a.w_scale[gi];
+            bg[j] = a.g_bias ? a.g_bias[gi] : 0.0f;
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+
+    for (int i = tid; i < MX * a.Kpad; i += blockDim.x) {
+        const int m = i / a.Kpad, k = i - m * a.Kpad;
+        float v = 0.0f;
+        if (m < a.M && k < a.K) {
+            if constexpr (XF32) v = static_cast<const float*>(a.x)[(int64_t)m * a.ldx + k];
+            else v = (float)static_cast<const _Float16*>(a.x)[(int64_t)m * a.ldx + k];
+        }
+        xs[m * a.Kpad + wv_slot(k)] = v;
+    }
+    __syncthreads();
+    if constexpr (GROUPED) {
+        for (int i = tid; i < MX * a.G; i += blockDim.x) {
+            const int m = i / a.G, g = i - m * a.G;
+            float sum = 0.0f;
+            for (int k = g * a.gs; k < (g + 1) * a.gs; ++k) sum += xs[m * a.Kpad + wv_slot(k)];
+            gsum[i] = sum;
+        }
+        __syncthreads();
+    } else if (a.w_zp) {
+        if (wave == 0) {
+#pragma unroll
+            for (int m = 0; m < MX; ++m) {
+                float sum = 0.0f;
+                for (int k = lane; k < a.K; k += 64) sum += xs[m * a.Kpad + wv_slot(k)];
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+                if (lane == 0) gsum[m] = sum;
+            }
+        }
+        __syncthreads();
+    }
+    if (!n_ok) return;
+
+    float acc[MX];
+#pragma unroll
+    for (int m = 0; m < MX; ++m) acc[m] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; ++j) {
+        const int c = lane + 64 * j;
+        const int k0 = c * CK;
+        float p[MX];
+#pragma unroll
+        for (int m = 0; m < MX; ++m) p[m] = 0.0f;
+#pragma unroll
+        for (int wi = 0; wi < 4; ++wi) {
+            const uint32_t wd = wc[j][wi];
+            float code[32 / BITS];
+            if constexpr (BITS == 8) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    code[e] = SIGNED ? (float)(signed char)(wd >> (8 * e)) : (float)((wd >> (8 * e)) & 0xFFu);
+            } else {
+                const uint32_t lo = opaque_and(wd, 0x0F0F0F0Fu);
+                const uint32_t hi = opaque_and(wd >> 4, 0x0F0F0F0Fu);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    code[2 * e] = (float)((lo >> (8 * e)) & 0xFFu);
+                    code[2 * e + 1] = (float)((hi >> (8 * e)) & 0xFFu);
+                }
+            }
+            const int kw = k0 + wi * (32 / BITS);
+#pragma unroll
+            for (int m = 0; m < MX; ++m) {
+#pragma unroll
+                for (int f = 0; f < 32 / BITS; f += 4) {
+                    const vf4 xv = *reinterpret_cast<const vf4*>(xs + m * a.Kpad + wv_slot(kw + f));
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) p[m] = fmaf(code[f + e], xv[e], p[m]);
+                }
+            }
+        }
+        if constexpr (GROUPED) {
+            const bool first = c < a.NC && (k0 % a.gs) == 0;
+            const int g = min(k0 / a.gs, a.G - 1);
+#pragma unroll
+            for (int m = 0; m < MX; ++m) {
+                acc[m] = fmaf(sg[j], p[m], acc[m]);
+                if (first) acc[m] = fmaf(bg[j], gsum[m * a.G + g], acc[m]);
+            }
+        } else {
+#pragma unroll
+            for (int m = 0; m < MX; ++m) acc[m] += p[m];
+        }
+    }
+#pragma unroll
+    for (int m = 0; m < MX; ++m) {
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) acc[m] += __shfl_xor(acc[m], off, 64);
+    }
+    if (lane == 0) {
+#pragma unroll
+        for (int m = 0; m < MX; ++m) {
+            if (m >= a.M) break;
+            float v = acc[m];
+            if constexpr (!GROUPED) {
+                if (a.w_zp) v = v - a.w_zp[n] * gsum[m];
+                v = a.w_scale[n] * v;
+            }
+            if (a.bias) v = v + a.bias[n];
+            if (a.relu && v <= 0.0f) v = 0.0f;
+            if constexpr (XF32)
+                reinterpret_cast<float*>(a.y)[(int64_t)m * a.ldy + n] = v;
+            else
+                reinterpret_cast<_Float16*>(a.y)[(int64_t)m * a.ldy + n] = (_Float16)v;
+        }
+    }
+}
+
+// ------------------------------------------------- group-wise quantize / dequantize
+
+// One thread per (row, group): s = (max - min) / (2^bits - 1), b = min,
+// c = clip(rne((w - b) / s), 0, 2^bits - 1) (formula lucid/quantization/_qgemm.py:84-97; a
+// group with max == min, or a NaN range, keeps s as computed and codes 0).  Codes are packed
+// 32/bits per uint32, little-end first.
+template <int BITS>
+__global__ __launch_bounds__(256) void group_quantize_kernel(const float* __restrict__ w, int64_t N, int64_t K,
+                                                             int gs, uint32_t* __restrict__ packed,
+                                                             float* __restrict__ scales,
+                                                             float* __restrict__ biases) {
+    const int64_t G = K / gs;
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= N * G) return;
+    const int64_t n = id / G, g = id - n * G;
+    const float* p = w + n * K + g * gs;
+    float mn = __int_as_float(0x7f800000), mx = -__int_as_float(0x7f800000);
+    for (int i = 0; i < gs; i += 4) {
+        const vf4 v = *reinterpret_cast<const vf4*>(p + i);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            mn = extreme_min(mn, v[e]);
+            mx = extreme_max(mx, v[e]);
+        }
+    }
+    constexpr uint32_t L = (1u << BITS) - 1u;
+    constexpr int PER = 32 / BITS;
+    const float s = (mx - mn) / (float)L;
+    scales[id] = s;
+    biases[id] = mn;
+    uint32_t* out = packed + (n * K + g * gs) / PER;
+    for (int i = 0; i < gs; i += PER) {
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            uint32_t c = 0;
+            if (s > 0.0f) {
+                const float d = p[i + e] - mn;
+                const float t = d / s;
+                c = (uint32_t)satcast<int32_t>(clip_tie(rne(t), 0.0f, (float)L, true, false), 0.0f,
+                                               (float)L, 0, (int)L);
+            }
+            word |= c << (e * BITS);
+        }
+        out[i / PER] = word;
+    }
+}
+
+// w_hat = fl32(fl32(c * s) + b) (lucid/quantization/_qgemm.py:167-170); one thread per word.
+template <int BITS>
+__global__ __launch_bounds__(256) void group_dequantize_kernel(const uint32_t* __restrict__ packed,
+                                                               const float* __restrict__ scales,
+                                                               const float* __restrict__ biases, int64_t N,
+                                                               int64_t K, int gs, float* __restrict__ w) {
+    constexpr int PER = 32 / BITS;
+    constexpr uint32_t L = (1u << BITS) - 1u;
+    const int64_t words = N * K / PER;
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= words) return;
+    const int64_t k0 = (id * PER) % K, n = (id * PER) / K;
+    const int64_t gi = n * (K / gs) + k0 / gs;
+    const float s = scales[gi];
+    const float b = biases ? biases[gi] : 0.0f;
+    const uint32_t word = packed[id];
+    float out[PER];
+#pragma unroll
+    for (int e = 0; e < PER; ++e) {
+        const float t = (float)((word >> (e * BITS)) & L) * s;
+        out[e] = biases ? t + b : t;
+    }
+#pragma unroll
+    for (int e = 0; e < PER; e += 4)
+        *reinterpret_cast<vf4*>(w + id * PER + e) = vf4{out[e], out[e + 1], out[e + 2], out[e + 3]};
+}
+
+// ------------------------------------------------------------------ host side
+
+struct WoPlan {
+    int W, bpw;
+    size_t lds;
+};
+
+// W waves split the T real k-blocks into equal runs of bpw blocks, bpw a multiple of the
+// ring depth: the largest W (at most maxw) whose padded slots W * bpw stay within 1/8 of the
+// fewest possible.
+WoPlan wo_plan(int64_t K, int S, bool grouped, int maxw) {
+    const int T = (int)((K + 32 * S - 1) / (32 * S));
+    auto slots = [&](int W) {
+        const int b = ((T + W - 1) / W + WO_RING - 1) / WO_RING * WO_RING;
+        return (long)W * b;
+    };
+    long fewest = slots(1);
+    for (int W = 2; W <= maxw; ++W) fewest = std::min(fewest, slots(W));
+    int bestW = 1;
+    for (int W = maxw; W >= 1; --W)
+        if (slots(W) * 8 <= fewest * 9) {
+            bestW = W;
+            break;
+        }
+    const int bestB = (int)(slots(bestW) / bestW);
+    WoPlan p{bestW, bestB, 0};
+    const int TW = bestW * bestB;
+    p.lds = sizeof(float) * ((size_t)bestW * 256 + (size_t)bestW * 64 + (grouped ? 2 * 16 * (size_t)TW : 0));
+    return p;
+}
+
+template <int BITS, bool SIGNED, int S, bool GROUPED, bool VEC>
+int launch_wo(const WoPlan& p, const WoArgs& a, bool xf32, hipStream_t st) {
+    const dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)((a.M + 15) / 16));
+    const dim3 block(64 * p.W);
+    if (xf32)
+        hipLaunchKernelGGL((wo_gemv_kernel<BITS, SIGNED, S, true, GROUPED, VEC>), grid, block, p.lds, st, a);
+    else
+        hipLaunchKernelGGL((wo_gemv_kernel<BITS, SIGNED, S, false, GROUPED, VEC>), grid, block, p.lds, st, a);
+    return LQ_OK;
+}
+
+// The VALU path: M <= 2, 16-byte aligned rows, at most 16 chunks per lane, staged rows fit
+// 64 KB of LDS.  Returns false when the shape does not qualify.
+template <int BITS, bool SIGNED, bool GROUPED>
+bool launch_wv(WvArgs a, bool xf32, hipStream_t st) {
+    constexpr int CK = 16 * 8 / BITS;
+    if (a.M > 2) return false;
+    const int64_t row_bytes = (int64_t)a.K * BITS / 8;
+    if (row_bytes % 16) return false;
+    a.NC = (int)(row_bytes / 16);
+    const int Jn = (a.NC + 63) / 64;
+    const int J = Jn <= 1 ? 1 : Jn <= 2 ? 2 : Jn <= 4 ? 4 : Jn <= 8 ? 8 : Jn <= 12 ? 12 : Jn <= 16 ? 16 : 0;
+    if (J == 0 || (GROUPED && J > 8)) return false;  // (group scales of 12+ chunks spill)
+    a.Kpad = J * 64 * CK;
+    const int MX = a.M;
+    const size_t lds = sizeof(float) * ((size_t)MX * a.Kpad + (GROUPED ? (size_t)MX * a.G : (size_t)MX));
+    if (lds > 64 * 1024) return false;
+    const int waves = a.N >= 4096 ? 16 : std::max(1, (a.N + 255) / 256);
+    const dim3 grid((unsigned)((a.N + waves - 1) / waves));
+    const dim3 block(64 * waves);
+#define LQ_WV(MXV, XV, JV) \
+    hipLaunchKernelGGL((wo_gemv_valu_kernel<BITS, SIGNED, GROUPED, MXV, XV, JV>), grid, block, lds, st, a)
+#define LQ_WVJ(MXV, XV)                                                                    \
+    switch (J) {                                                                           \
+        case 1: LQ_WV(MXV, XV, 1); break;                                                  \
+        case 2: LQ_WV(MXV, XV, 2); break;                                                  \
+        case 4: LQ_WV(MXV, XV, 4); break;                                                  \
+        case 8: LQ_WV(MXV, XV, 8); break;                                                  \
+        case 12: LQ_WV(MXV, XV, 12); break;                                                \
+        default: LQ_WV(MXV, XV, 16); break;                                                \
+    }
+    if (MX == 1) {
+        if (xf32) { LQ_WVJ(1, true) } else { LQ_WVJ(1, false) }
+    } else {
+        if (xf32) { LQ_WVJ(2, true) } else { LQ_WVJ(2, false) }
+    }
+#undef LQ_WVJ
+#undef LQ_WV
+    return true;
+}
+
+constexpr int64_t WO_MAX_DIM = (int64_t)1 << 30;
+constexpr size_t WO_MAX_LDS = 64 * 1024;
+
+}  // namespace
+}  // namespace lq
+
+using namespace lq;
+
+extern "C" {
+
+size_t lq_gemv_w8_workspace_size(int64_t M, int64_t N, int64_t K) {
+    (void)M; (void)N; (void)K;
+    return 0;
+}
+
+int lq_gemv_w8(const void* d_x, int x_dtype, int64_t ldx, const int8_t* d_W, int64_t ldw,
+               const float* d_w_scale, const float* d_w_zero_point, const float* d_bias,
+               void* d_y, int64_t ldy, int64_t M, int64_t N, int64_t K, int flags,
+               void* d_workspace, size_t workspace_bytes, void* stream) {
+    (void)d_workspace; (void)workspace_bytes;
+    LQ_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M < WO_MAX_DIM && N < WO_MAX_DIM && K < WO_MAX_DIM,
+               "lq_gemv_w8: bad shape");
+    LQ_REQUIRE(x_dtype == LQ_F32 || x_dtype == LQ_F16, "lq_gemv_w8: x_dtype must be LQ_F32 or LQ_F16");
+    LQ_REQUIRE((flags & ~LQ_EPI_RELU) == 0, "lq_gemv_w8: unknown flags");
+    if (M == 0 || N == 0) return LQ_OK;
+    LQ_REQUIRE(d_x && d_W && d_y && d_w_scale, "lq_gemv_w8: NULL pointer");
+    LQ_REQUIRE(ldx >= K && ldw >= K && ldy >= N, "lq_gemv_w8: leading dimension too small");
+    const bool xf32 = x_dtype == LQ_F32;
+    const WoPlan p = wo_plan(std::max<int64_t>(K, 1), 2, false, wo_max_waves(2, xf32, false));
+    WoArgs a{};
+    a.x = d_x;
+    a.ldx = ldx;
+    a.w = reinterpret_cast<const uint8_t*>(d_W);
+    a.ldw_bytes = ldw;
+    a.w_scale = d_w_scale;
+    a.w_zp = d_w_zero_point;
+    a.bias = d_bias;
+    a.y = d_y;
+    a.ldy = ldy;
+    a.relu = (flags & LQ_EPI_RELU) ? 1 : 0;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.bpw = p.bpw;
+    hipStream_t st = as_stream(stream);
+    if (M <= 2 && aligned16(d_W) && ldw % 16 == 0) {
+        WvArgs v{};
+        v.x = d_x; v.ldx = ldx; v.w = a.w; v.ldw_bytes = ldw; v.w_scale = d_w_scale;
+        v.w_zp = d_w_zero_point; v.bias = d_bias; v.y = d_y; v.ldy = ldy; v.relu = a.relu;
+        v.M = (int)M; v.N = (int)N; v.K = (int)K;
+        if (launch_wv<8, true, false>(v, xf32, st)) return launch_status("lq_gemv_w8");
+    }
+    const bool vec = aligned16(d_W) && ldw % 16 == 0 && K % 16 == 0 && K >= 16 && aligned16(d_x) &&
+                     ldx % (xf32 ? 4 : 8) == 0;
+    if (vec) launch_wo<8, true, 2, false, true>(p, a, xf32, st);
+    else launch_wo<8, true, 2, false, false>(p, a, xf32, st);
+    return launch_status("lq_gemv_w8");
+}
+
+size_t lq_group_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int group_size) {
+    (void)M; (void)N; (void)K; (void)group_size;
+    return 0;
+}
+
+int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d_packed,
+                    const float* d_scales, const float* d_biases, const float* d_bias, void* d_y,
+                    int64_t ldy, int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                    int transpose, int flags, void* d_workspace, size_t workspace_bytes,
+                    void* stream) {
+    (void)d_workspace; (void)workspace_bytes;
+    LQ_REQUIRE(M >= 0 && N >= 0 && K > 0 && M < WO_MAX_DIM && N < WO_MAX_DIM && K < WO_MAX_DIM,
+               "lq_group_matmul: bad shape");
+    LQ_REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
+               "lq_group_matmul: group_size must be 32, 64 or 128");
+    LQ_REQUIRE(bits == 4 || bits == 8, "lq_group_matmul: bits must be 4 or 8");
+    LQ_REQUIRE(K % group_size == 0, "lq_group_matmul: K must be a multiple of group_size");
+    LQ_REQUIRE(x_dtype == LQ_F32 || x_dtype == LQ_F16, "lq_group_matmul: x_dtype must be LQ_F32 or LQ_F16");
+    LQ_REQUIRE((flags & ~LQ_EPI_RELU) == 0, "lq_group_matmul: unknown flags");
+    if (!transpose)
+        return set_error(LQ_ERR_UNSUPPORTED, "lq_group_matmul: only transpose=true (x @ w_hat^T) is implemented");
+    if (M == 0 || N == 0) return LQ_OK;
+    LQ_REQUIRE(d_x && d_packed && d_scales && d_y, "lq_group_matmul: NULL pointer");
+    LQ_REQUIRE(ldx >= K && ldy >= N, "lq_group_matmul: leading dimension too small");
+    LQ_REQUIRE(aligned16(d_packed), "lq_group_matmul: packed weights must be 16-byte aligned");
+    const int S = group_size / 32;
+    const bool xf32 = x_dtype == LQ_F32;
+    const WoPlan p = wo_plan(K, S, true, wo_max_waves(S, xf32, true));
+    if (p.lds > WO_MAX_LDS)
+        return set_error(LQ_ERR_UNSUPPORTED, "lq_group_matmul: K too large for one workgroup's group scales");
+    WoArgs a{};
+    a.x = d_x;
+    a.ldx = ldx;
+    a.w = reinterpret_cast<const uint8_t*>(d_packed);
+    a.ldw_bytes = K * bits / 8;
+    a.w_scale = d_scales;
+    a.g_bias = d_biases;
+    a.bias = d_bias;
+    a.y = d_y;
+    a.ldy = ldy;
+    a.relu = (flags & LQ_EPI_RELU) ? 1 : 0;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.G = (int)(K / group_size);
+    a.bpw = p.bpw;
+    hipStream_t st = as_stream(stream);
+    if (M <= 2) {
+        WvArgs v{};
+        v.x = d_x; v.ldx = ldx; v.w = a.w; v.ldw_bytes = a.ldw_bytes; v.w_scale = d_scales;
+        v.g_bias = d_biases; v.bias = d_bias; v.y = d_y; v.ldy = ldy; v.relu = a.relu;
+        v.M = (int)M; v.N = (int)N; v.K = (int)K; v.G = a.G; v.gs = group_size;
+        const bool ok = bits == 8 ? launch_wv<8, false, true>(v, xf32, st) : launch_wv<4, false, true>(v, xf32, st);
+        if (ok) return launch_status("lq_group_matmul");
+    }
+    const bool vec = aligned16(d_x) && ldx % (xf32 ? 4 : 8) == 0;
+#define LQ_GM(B, SS)                                                          \
+    do {                                                                      \
+        if (vec) launch_wo<B, false, SS, true, true>(p, a, xf32, st);         \
+        else launch_wo<B, false, SS, true, false>(p, a, xf32, st);            \
+    } while (0)
+    if (bits == 8) {
+        if (S == 1) LQ_GM(8, 1); else if (S == 2) LQ_GM(8, 2); else LQ_GM(8, 4);
+    } else {
+        if (S == 1) LQ_GM(4, 1); else if (S == 2) LQ_GM(4, 2); else LQ_GM(4, 4);
+    }
+#undef LQ_GM
+    return launch_status("lq_group_matmul");
+}
+
+int lq_group_quantize_f32(const float* d_w, int64_t N, int64_t K, int group_size, int bits,
+                          uint32_t* d_packed, float* d_scales, float* d_biases, void* stream) {
+    LQ_REQUIRE(N >= 0 && K >= 0, "lq_group_quantize_f32: bad shape");
+    LQ_REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
+               "lq_group_quantize_f32: group_size must be 32, 64 or 128");
+    LQ_REQUIRE(bits == 4 || bits == 8, "lq_group_quantize_f32: bits must be 4 or 8");
+    LQ_REQUIRE(K % group_size == 0, "lq_group_quantize_f32: K must be a multiple of group_size");
+    if (N == 0 || K == 0) return LQ_OK;
+    LQ_REQUIRE(d_w && d_packed && d_scales && d_biases, "lq_group_quantize_f32: NULL pointer");
+    LQ_REQUIRE(aligned16(d_w), "lq_group_quantize_f32: weight must be 16-byte aligned");
+    const int64_t groups = N * (K / group_size);
+    const dim3 grid((unsigned)((groups + 255) / 256));
+    if (bits == 8)
+        hipLaunchKernelGGL(group_quantize_kernel<8>, grid, dim3(256), 0, as_stream(stream), d_w, N, K, group_size,
+                           d_packed, d_scales, d_biases);
+    else
+        hipLaunchKernelGGL(group_quantize_kernel<4>, grid, dim3(256), 0, as_stream(stream), d_w, N, K, group_size,
+                           d_packed, d_scales, d_biases);
+    return launch_status("lq_group_quantize_f32");
+}
+
+int lq_group_dequantize_f32(const uint32_t* d_packed, const float* d_scales, const float* d_biases,
+                            int64_t N, int64_t K, int group_size, int bits, float* d_w, void* stream) {
+    LQ_REQUIRE(N >= 0 && K >= 0, "lq_group_dequantize_f32: bad shape");
+    LQ_REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
+               "lq_group_dequantize_f32: group_size must be 32, 64 or 128");
+    LQ_REQUIRE(bits == 4 || bits == 8, "lq_group_dequantize_f32: bits must be 4 or 8");
+    LQ_REQUIRE(K % group_size == 0, "lq_group_dequantize_f32: K must be a multiple of group_size");
+    if (N == 0 || K == 0) return LQ_OK;
+    LQ_REQUIRE(d_packed && d_scales && d_w, "lq_group_dequantize_f32: NULL pointer");
+    LQ_REQUIRE(aligned16(d_w), "lq_group_dequantize_f32: output must be 16-byte aligned");
+    const int64_t words = N * K * bits / 32;
+    const dim3 grid((unsigned)((words + 255) / 256));
+    if (bits == 8)
+        hipLaunchKernelGGL(group_dequantize_kernel<8>, grid, dim3(256), 0, as_stream(stream), d_packed, d_scales,
+                           d_biases, N, K, group_size, d_w);
+    else
+        hipLaunchKernelGGL(group_dequantize_kernel<4>, grid, dim3(256), 0, as_stream(stream), d_packed, d_scales,
+                           d_biases, N, K, group_size, d_w);
+    return launch_status("lq_group_dequantize_f32");
+}
+
+}  // extern "C"

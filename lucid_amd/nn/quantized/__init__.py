@@ -8,10 +8,11 @@ MFMA GEMM over integer codes; ``QuantStub`` / ``DeQuantStub`` / ``Quantize`` /
 
 from lucid_amd.nn.quantized.intrinsic import LinearReLU
 from lucid_amd.nn.quantized.linear import Linear
+from lucid_amd.nn.quantized.mlx_linear import QuantizedLinearMLX
 from lucid_amd.nn.quantized.modules import (DeQuantize, DeQuantStub, Quantize, QuantStub,
                                             QuantWrapper)
 
-__all__ = ["Linear", "LinearReLU", "QuantStub", "DeQuantStub", "Quantize", "DeQuantize",
+__all__ = ["Linear", "QuantizedLinearMLX", "LinearReLU", "QuantStub", "DeQuantStub", "Quantize", "DeQuantize",
            "QuantWrapper"]
 
 

@@ -26,7 +26,7 @@ from lucid_amd.nn.module import Module
 from lucid_amd.nn.quantized.linear import _WeightedQuantized
 from lucid_amd.quantization._device import on_device, require_gpu, workspace
 from lucid_amd.quantization._functional import fake_quantize, quantize
-from lucid_amd.quantization._gemm import gemm_w8a8
+from lucid_amd.quantization._gemm import gemm_w8a8, gemv_w8
 from lucid_amd.quantization._qparams import calculate_qparams
 from lucid_amd.quantization._qscheme import (QDtype, per_channel_symmetric, per_tensor_affine,
                                              qint8, quint8)
@@ -73,6 +73,8 @@ class Linear(_WeightedQuantized):
             code_type = _C.I8
         else:  # a grid wider than 8 bits: Lucid's float composition on the device
             x_q = fake_quantize(x, x_scale, x_zp, qd.quant_min, qd.quant_max)
+            if self.weight_int8.dtype == np.int8:
+                return gemv_w8(x_q, self._operands(), self.bias)
             return F.linear(x_q, self._dequantized_weight(), self.bias)
         codes = empty(x.shape, np.int8, "gpu")
         if x.numel():

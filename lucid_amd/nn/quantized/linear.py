@@ -18,7 +18,8 @@ and the result is a code-backed tensor whose float values are ``(out - Z) * S``.
 equals Lucid's float composition except where the float GEMM's rounding moves ``y``
 across a rounding boundary of the output grid (one code apart; measured in the tests).
 A plain float ``x`` (not on a grid) takes Lucid's literal composition on the GPU: the
-weight dequantized once and cached, the float GEMM kernel, ReLU, fake-quantize.
+weight-only int8 GEMM (``lq_gemv_w8``: float activations against the int8 codes and
+per-channel scales, bias and ReLU fused), then fake-quantize onto the output grid.
 """
 
 from __future__ import annotations
@@ -32,7 +33,7 @@ from lucid_amd.nn.module import Module
 from lucid_amd.nn.quantized._utils import activation_qparams, quantize_weight
 from lucid_amd.quantization._device import on_device, require_gpu
 from lucid_amd.quantization._functional import dequantize, fake_quantize_to_codes
-from lucid_amd.quantization._gemm import WeightCache, code_backed_output, gemm_w8a8
+from lucid_amd.quantization._gemm import WeightCache, code_backed_output, gemm_w8a8, gemv_w8
 from lucid_amd.quantization._qscheme import QDtype, quint8
 
 
@@ -126,7 +127,10 @@ class Linear(_WeightedQuantized):
                                       self.out_qdtype.quant_min, self.out_qdtype.quant_max)
         if x.dtype != float32:
             raise TypeError(f"{type(self).__name__}: float32 input expected, got {x.dtype}")
-        y = self._activation(F.linear(x, self._dequantized_weight(), self.bias))
+        if self.weight_int8.dtype == np.int8:
+            y = gemv_w8(x, self._operands(), self.bias, relu=self._relu)
+        else:
+            y = self._activation(F.linear(x, self._dequantized_weight(), self.bias))
         return fake_quantize_to_codes(y, self.scale, self.zero_point, self.out_qdtype.quant_min,
                                       self.out_qdtype.quant_max)
 

@@ -31,13 +31,10 @@ class WeightCache:
             raise TypeError(f"int8 [out, in] weight codes expected, got {codes.dtype} {codes.shape}")
         self.codes = on_device_codes(codes)
         self.N, self.K = self.codes.shape
-        s = on_device(scale)
-        if s.numel() != self.N:
-            raise ValueError(f"weight scale has {s.numel()} entries for {self.N} channels")
-        self.scale = s.reshape(self.N)
+        self.scale = _per_row(scale, self.N, "scale")
         self.zero_point = None
         if zero_point is not None:
-            z = on_device(zero_point).reshape(self.N)
+            z = _per_row(zero_point, self.N, "zero point")
             if np.any(z.numpy() != 0):
                 self.zero_point = z
         self.sums = empty((self.N,), np.int32, "gpu")
@@ -56,6 +53,16 @@ class WeightCache:
             _C.call("lq_pack_weights_i8", self.codes.data_ptr(), self.K, self.N, self.K,
                     self._packed.data_ptr(), None)
         return self._packed
+
+
+def _per_row(p: Tensor, N: int, what: str) -> Tensor:
+    """A weight qparam as a float32 device vector of N entries (a per-tensor value repeats)."""
+    d = on_device(p)
+    if d.numel() == 1 and N != 1:
+        d = on_device(Tensor._from_numpy(np.full(N, d.item(), np.float32), "cpu"))
+    if d.numel() != N:
+        raise ValueError(f"weight {what} has {d.numel()} entries for {N} channels")
+    return d.reshape(N)
 
 
 def on_device_codes(codes: Tensor) -> Tensor:
@@ -117,6 +124,28 @@ def gemm_w8a8(codes: Tensor, code_type: int, a_scale: Tensor, a_zero_point: Tens
     else:
         _C.call("lq_gemm_w8a8", codes.data_ptr(), K, w.codes.data_ptr(), K, y.data_ptr(), w.N, M,
                 w.N, K, *common)
+    return y
+
+
+def gemv_w8(x: Tensor, w: WeightCache, bias: Tensor | None, relu: bool = False) -> Tensor:
+    """Weight-only ``x @ dequantize(W)^T + bias`` (ReLU) for a float32 / float16 input
+    (``lq_gemv_w8``): the int8 weight is read once, never expanded to float."""
+    K = x.shape[-1]
+    if K != w.K:
+        raise ValueError(f"linear: input features {K} != weight in_features {w.K}")
+    M = x.numel() // K if K else int(np.prod(x.shape[:-1], dtype=np.int64))
+    y = empty((*x.shape[:-1], w.N), x.dtype, "gpu")
+    if M == 0 or w.N == 0:
+        return y
+    if x.dtype not in (np.float32, np.float16):
+        raise TypeError(f"linear: float32 or float16 input expected, got {x.dtype}")
+    b = on_device(bias) if bias is not None else None
+    ws_bytes = _C.lib().lq_gemv_w8_workspace_size(M, w.N, K)
+    _C.call("lq_gemv_w8", x.data_ptr(), _C.F32 if x.dtype == np.float32 else _C.F16, K,
+            w.codes.data_ptr(), K, w.scale.data_ptr(),
+            w.zero_point.data_ptr() if w.zero_point is not None else None,
+            b.data_ptr() if b is not None else None, y.data_ptr(), w.N, M, w.N, K,
+            _C.EPI_RELU if relu else 0, workspace.get(ws_bytes), ws_bytes, None)
     return y
 
 

@@ -1,0 +1,113 @@
+"""Group-wise packed weights and the fused weight-only GEMM (lucid/quantization/_qgemm.py:24-314).
+
+Same three ops and signatures as Lucid's ``_qgemm`` over ``_C_engine.quantized``
+(lucid/_C/bindings/bind_quantized.cpp:17-27), on the HIP kernels of
+lucid_amd/csrc/lq_wo.hip:
+
+* ``quantize(w, group_size, bits)`` -> ``(packed int32 [N, K*bits/32], scales [N, K/gs],
+  biases [N, K/gs])``: per group ``s = (max - min) / (2^bits - 1)``, ``b = min``,
+  ``c = clip(round((w - b) / s), 0, 2^bits - 1)``, packed 32/bits codes per word, little end
+  first (``lq_group_quantize_f32``);
+* ``dequantize(...)`` -> ``c * s + b`` as float32 (``lq_group_dequantize_f32``);
+* ``quantized_matmul(x, ...)`` -> ``x @ w_hat^T`` in x's dtype without forming ``w_hat``
+  (``lq_group_matmul``; ``transpose=False`` is not implemented).
+
+Like Lucid's (Metal-only) ops these require device tensors.  The exact scale / rounding /
+pack order of MLX 0.32.3, which Lucid calls, is not visible from the reference: these ops
+follow the formula Lucid documents (_qgemm.py:84-97, 167-170).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+
+from lucid_amd import _C
+from lucid_amd._tensor import Tensor, empty, float16, float32
+from lucid_amd.quantization._device import on_device, require_gpu, workspace
+
+_GROUP_SIZES = (32, 64, 128)
+
+
+def is_available() -> bool:
+    """True when the group-wise kernels are loadable and a GPU is visible."""
+    import lucid_amd.backends as backends
+
+    return backends.quantized.available
+
+
+def _check(group_size: int, bits: int, K: int, op: str) -> None:
+    if group_size not in _GROUP_SIZES:
+        raise ValueError(f"{op}: group_size must be one of {_GROUP_SIZES}, got {group_size}")
+    if bits not in (4, 8):
+        raise ValueError(f"{op}: bits must be 4 or 8, got {bits}")
+    if K % group_size:
+        raise ValueError(f"{op}: the quantized dimension {K} is not a multiple of group_size "
+                         f"{group_size}")
+
+
+def quantize(w: Tensor, group_size: int = 64, bits: int = 8) -> tuple[Tensor, Tensor, Tensor]:
+    """Group-wise quantize a float weight ``[N, K]`` along K."""
+    require_gpu(w, "quantized.quantize")
+    if w.dtype != float32 or w.ndim != 2:
+        raise TypeError(f"quantized.quantize: float32 [out, in] weight expected, got {w.dtype} "
+                        f"{w.shape}")
+    N, K = w.shape
+    _check(group_size, bits, K, "quantized.quantize")
+    packed = empty((N, K * bits // 32), np.int32, "gpu")
+    scales = empty((N, K // group_size), float32, "gpu")
+    biases = empty((N, K // group_size), float32, "gpu")
+    if N and K:
+        _C.call("lq_group_quantize_f32", w.data_ptr(), N, K, group_size, bits, packed.data_ptr(),
+                scales.data_ptr(), biases.data_ptr(), None)
+    return packed, scales, biases
+
+
+def _unpacked_k(wq: Tensor, bits: int) -> int:
+    return wq.shape[-1] * 32 // bits
+
+
+def dequantize(wq: Tensor, scales: Tensor, biases: Tensor | None, group_size: int = 64,
+               bits: int = 8) -> Tensor:
+    """``c * s + b`` as a float32 ``[N, K]`` weight."""
+    require_gpu(wq, "quantized.dequantize")
+    N, K = wq.shape[0], _unpacked_k(wq, bits)
+    _check(group_size, bits, K, "quantized.dequantize")
+    s = on_device(scales)
+    b = on_device(biases) if biases is not None else None
+    out = empty((N, K), float32, "gpu")
+    if N and K:
+        _C.call("lq_group_dequantize_f32", wq.data_ptr(), s.data_ptr(),
+                b.data_ptr() if b is not None else None, N, K, group_size, bits, out.data_ptr(),
+                None)
+    return out
+
+
+def quantized_matmul(x: Tensor, wq: Tensor, scales: Tensor, biases: Tensor | None,
+                     transpose: bool = True, group_size: int = 64, bits: int = 8,
+                     bias: Tensor | None = None, relu: bool = False) -> Tensor:
+    """``x @ w_hat^T`` (``[..., K] -> [..., N]``) in x's dtype (float32 or float16).
+
+    ``bias`` / ``relu`` fuse the layer epilogue of ``QuantizedLinearMLX`` into the kernel.
+    """
+    require_gpu(x, "quantized.quantized_matmul")
+    if not transpose:
+        raise NotImplementedError("quantized_matmul: transpose=False is not implemented on the "
+                                  "HIP backend")
+    if x.dtype not in (float32, float16):
+        raise TypeError(f"quantized_matmul: float32 or float16 input expected, got {x.dtype}")
+    N, K = wq.shape[0], _unpacked_k(wq, bits)
+    _check(group_size, bits, K, "quantized_matmul")
+    if x.shape[-1] != K:
+        raise ValueError(f"quantized_matmul: input features {x.shape[-1]} != weight K {K}")
+    M = x.numel() // K
+    s = on_device(scales)
+    b = on_device(biases) if biases is not None else None
+    lb = on_device(bias) if bias is not None else None
+    y = empty((*x.shape[:-1], N), x.dtype, "gpu")
+    if M and N:
+        ws_bytes = _C.lib().lq_group_matmul_workspace_size(M, N, K, group_size)
+        _C.call("lq_group_matmul", x.data_ptr(), _C.F32 if x.dtype == float32 else _C.F16, K,
+                wq.data_ptr(), s.data_ptr(), b.data_ptr() if b is not None else None,
+                lb.data_ptr() if lb is not None else None, y.data_ptr(), N, M, N, K, group_size,
+                bits, 1, _C.EPI_RELU if relu else 0, workspace.get(ws_bytes), ws_bytes, None)
+    return y

@@ -21,6 +21,17 @@ import oracle as O
 pytestmark = pytest.mark.gpu
 
 
+@pytest.fixture(autouse=True)
+def _reference_engine():
+    """These tests cover the int8 sidecar layers: pin the engine that selects them (with the
+    group-wise kernels present, "auto" routes group-divisible Linears to QuantizedLinearMLX)."""
+    import lucid_amd.backends as backends
+
+    backends.quantized.engine = "reference"
+    yield
+    backends.quantized.engine = "auto"
+
+
 def _relu(y):
     return np.where(y <= 0, np.float32(0), y).astype(np.float32)
 

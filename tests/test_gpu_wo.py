@@ -1,0 +1,247 @@
+"""GPU parity of the weight-only kernels (lucid_amd/csrc/lq_wo.hip) through the C ABI.
+
+* ``lq_gemv_w8`` (per-channel int8 weight, float activations): against the oracle's
+  float64 ``x @ dequantize(W)^T + bias``.  fp32 outputs within 1e-5 of sum |terms|
+  (the scale-aware rtol of the fp32 contract); fp16 outputs within 1e-3 relative plus the
+  same accumulation allowance.
+* group-wise ``quantize`` / ``dequantize``: bit-exact against the oracle's restatement of
+  the documented formula (lucid/quantization/_qgemm.py:84-97, 167-170);
+* ``quantized_matmul``: against float64 ``x @ w_hat^T`` at the reference bench's parity
+  gate (max error / max |y| <= 1e-4, tools/bench_quantized_dispatch.py) and the scale-aware
+  1e-5.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def _t(L, a):
+    return L.tensor(np.ascontiguousarray(a), device="gpu")
+
+
+def _close(got, ref, mag, half=False):
+    got = got.astype(np.float64)
+    tol = (1e-3 * np.abs(ref) + 1e-5 * mag) if half else 1e-5 * mag + 1e-30
+    bad = np.abs(got - ref) > tol
+    assert not bad.any(), (f"{bad.sum()} of {bad.size} outside tolerance; worst "
+                           f"{np.max(np.abs(got - ref) / np.maximum(tol, 1e-30)):.3g}x")
+
+
+def run_gemv(L, x, W, s, z=None, b=None, relu=False, half=False, ldw=None):
+    from lucid_amd import _C
+
+    M, K = x.shape
+    N = W.shape[0]
+    ldw = ldw or K
+    Wp = np.zeros((N, ldw), np.int8)
+    Wp[:, :K] = W
+    xd = _t(L, x.astype(np.float16 if half else np.float32))
+    dW, ds = _t(L, Wp), _t(L, s.astype(np.float32))
+    dz = _t(L, z.astype(np.float32)) if z is not None else None
+    db = _t(L, b.astype(np.float32)) if b is not None else None
+    y = L.empty((M, N), np.float16 if half else np.float32, "gpu")
+    ws_bytes = _C.lib().lq_gemv_w8_workspace_size(M, N, K)
+    ws = L.empty((max(ws_bytes, 1),), np.uint8, "gpu")
+    _C.call("lq_gemv_w8", xd.data_ptr(), _C.F16 if half else _C.F32, K, dW.data_ptr(), ldw,
+            ds.data_ptr(), dz.data_ptr() if dz is not None else None,
+            db.data_ptr() if db is not None else None, y.data_ptr(), N, M, N, K,
+            _C.EPI_RELU if relu else 0, ws.data_ptr(), ws_bytes, None)
+    return y.numpy()
+
+
+def _gemv_ref(x, W, s, z=None, b=None, relu=False):
+    """The oracle's dequantize -> linear (float64 accumulation) and sum |terms|."""
+    ref = O.gemv_w8(x, W, s, w_zp=z, bias=b, relu=relu)
+    wd = (W.astype(np.float64) - (0.0 if z is None else z.astype(np.float64)[:, None])) * s.astype(np.float64)[:, None]
+    mag = np.abs(x.astype(np.float64)) @ np.abs(wd).T + (0.0 if b is None else np.abs(b.astype(np.float64)))
+    return ref, mag
+
+
+GEMV_SHAPES = [(1, 4096, 4096), (16, 4096, 4096), (1, 11008, 4096), (8, 4096, 11008),
+               (2, 96, 784), (17, 256, 784), (33, 100, 1000), (64, 10, 256), (100, 300, 512),
+               (1, 1, 16), (5, 70, 48)]
+
+
+@pytest.mark.parametrize("M,N,K", GEMV_SHAPES)
+def test_gemv_w8_fp32(gpu, M, N, K):
+    rng = np.random.default_rng(M * 131 + N + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[:, ::97] *= 20.0  # outliers
+    W = rng.integers(-128, 128, (N, K)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-1, N).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    got = run_gemv(gpu, x, W, s, b=b)
+    ref, mag = _gemv_ref(x, W, s, b=b)
+    _close(got, ref, mag)
+
+
+@pytest.mark.parametrize("M,N,K", [(4, 256, 784), (16, 1024, 4096), (1, 64, 1000)])
+def test_gemv_w8_zero_point_relu_and_ldw(gpu, M, N, K):
+    rng = np.random.default_rng(7 + M)
+    x = (rng.standard_normal((M, K)) * 1e3).astype(np.float32)
+    W = rng.integers(-128, 128, (N, K)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-1, N).astype(np.float32)
+    z = rng.integers(-5, 6, N).astype(np.float32)
+    ref, mag = _gemv_ref(x, W, s, z=z, relu=True)
+    _close(run_gemv(gpu, x, W, s, z=z, relu=True), ref, mag)
+    _close(run_gemv(gpu, x, W, s, z=z, relu=True, ldw=K + 48), ref, mag)  # 16-aligned rows
+    _close(run_gemv(gpu, x, W, s, z=z, relu=True, ldw=K + 3), ref, mag)   # unaligned rows
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 4096, 4096), (16, 1024, 1024), (3, 50, 784)])
+def test_gemv_w8_fp16(gpu, M, N, K):
+    rng = np.random.default_rng(11 + M)
+    x = rng.standard_normal((M, K)).astype(np.float16)
+    W = rng.integers(-128, 128, (N, K)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-2, N).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    got = run_gemv(gpu, x.astype(np.float32), W, s, b=b, half=True)
+    ref, mag = _gemv_ref(x.astype(np.float32), W, s, b=b)
+    _close(got, ref, mag, half=True)
+
+
+def test_gemv_w8_tiny_and_huge_rows(gpu):
+    """Per-row pre-scaling: rows of very different magnitude in one call."""
+    rng = np.random.default_rng(3)
+    M, N, K = 4, 128, 512
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[0] *= 1e-30
+    x[1] *= 1e30
+    x[2] = 0.0
+    W = rng.integers(-128, 128, (N, K)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-1, N).astype(np.float32)
+    got = run_gemv(gpu, x, W, s)
+    ref, mag = _gemv_ref(x, W, s)
+    _close(got, ref, mag)
+    assert np.all(got[2] == 0.0)
+
+
+# ----------------------------------------------------------------- group-wise
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_group_quantize_dequantize_exact(gpu, bits, gs):
+    from lucid_amd.quantization import _qgemm
+
+    rng = np.random.default_rng(bits * 1000 + gs)
+    N, K = 96, 1024
+    w = rng.standard_normal((N, K)).astype(np.float32)
+    w[3, :gs] = 0.25  # a constant group
+    packed, scales, biases = _qgemm.quantize(_t(gpu, w), group_size=gs, bits=bits)
+    op, os_, ob = O.group_quantize(w, gs, bits)
+    assert packed.dtype == np.int32 and packed.shape == (N, K * bits // 32)
+    np.testing.assert_array_equal(packed.numpy().view(np.uint32), op)
+    np.testing.assert_array_equal(scales.numpy(), os_)
+    np.testing.assert_array_equal(biases.numpy(), ob)
+    dense = _qgemm.dequantize(packed, scales, biases, group_size=gs, bits=bits)
+    want = O.group_dequantize(op, os_, ob, gs, bits)
+    np.testing.assert_array_equal(dense.numpy().view(np.uint32), want.view(np.uint32))
+    nob = _qgemm.dequantize(packed, scales, None, group_size=gs, bits=bits)
+    np.testing.assert_array_equal(nob.numpy(), O.group_dequantize(op, os_, None, gs, bits))
+    # half-step reconstruction bound (lucid/quantization/_qgemm.py dequantize docstring)
+    err = np.abs(want - w).reshape(N, K // gs, gs)
+    assert np.all(err <= os_[:, :, None] * 0.5 + 1e-6)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("M", [1, 2, 8, 32, 70])
+def test_quantized_matmul_parity(gpu, bits, gs, M):
+    from lucid_amd.quantization import _qgemm
+
+    rng = np.random.default_rng(bits + gs + M)
+    N, K = 1024, 1024
+    w = rng.standard_normal((N, K)).astype(np.float32)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    packed, scales, biases = _qgemm.quantize(_t(gpu, w), group_size=gs, bits=bits)
+    y = _qgemm.quantized_matmul(_t(gpu, x), packed, scales, biases, transpose=True,
+                                group_size=gs, bits=bits).numpy()
+    wd = O.group_dequantize(packed.numpy().view(np.uint32), scales.numpy(), biases.numpy(), gs,
+                            bits).astype(np.float64)
+    ref = x.astype(np.float64) @ wd.T
+    mag = np.abs(x.astype(np.float64)) @ np.abs(wd).T
+    assert np.max(np.abs(y - ref)) / max(np.max(np.abs(ref)), 1e-12) <= 1e-4
+    _close(y, ref, mag)
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs", [(1, 4096, 4096, 4, 64), (16, 11008, 4096, 8, 64),
+                                           (8, 4096, 11008, 4, 128), (3, 100, 192, 8, 32)])
+def test_quantized_matmul_shapes_bias_relu_fp16(gpu, M, N, K, bits, gs):
+    from lucid_amd.quantization import _qgemm
+
+    rng = np.random.default_rng(M + N)
+    w = (rng.standard_normal((N, K)) * 0.05).astype(np.float32)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    packed, scales, biases = _qgemm.quantize(_t(gpu, w), group_size=gs, bits=bits)
+    wd = O.group_dequantize(packed.numpy().view(np.uint32), scales.numpy(), biases.numpy(), gs,
+                            bits).astype(np.float64)
+    for half in (False, True):
+        xin = x.astype(np.float16) if half else x
+        y = _qgemm.quantized_matmul(_t(gpu, xin), packed, scales, biases, group_size=gs,
+                                    bits=bits, bias=_t(gpu, b), relu=True)
+        assert y.dtype == (np.float16 if half else np.float32)
+        xd = xin.astype(np.float64)
+        ref = np.maximum(xd @ wd.T + b, 0.0)
+        mag = np.abs(xd) @ np.abs(wd).T + np.abs(b)
+        _close(y.numpy(), ref, mag, half=half)
+
+
+def test_quantized_linear_mlx_module(gpu):
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized as nnq
+
+    rng = np.random.default_rng(0)
+    lin = nn.Linear(256, 64)
+    lin.weight = nn.Parameter(gpu.tensor(rng.normal(0, 0.05, (64, 256)).astype(np.float32)))
+    lin.bias = nn.Parameter(gpu.tensor(rng.normal(0, 0.05, 64).astype(np.float32)))
+    q = nnq.QuantizedLinearMLX.from_float(lin, bits=4, group_size=64, relu=True)
+    sd = q.state_dict()
+    assert list(sd) == ["packed_weight", "scales", "biases", "bias"]
+    assert sd["packed_weight"].dtype == np.int32 and sd["packed_weight"].shape == (64, 32)
+    x = rng.standard_normal((5, 256)).astype(np.float32)
+    y_gpu = q(gpu.tensor(x, device="gpu"))
+    y_cpu = q(gpu.tensor(x))  # device-transparent: host in, host out
+    assert y_cpu.device == "cpu" and y_gpu.device == "gpu"
+    np.testing.assert_array_equal(y_cpu.numpy(), y_gpu.numpy())
+    p, s, bb = O.group_quantize(lin.weight.numpy(), 64, 4)
+    wd = O.group_dequantize(p, s, bb, 64, 4).astype(np.float64)
+    ref = np.maximum(x.astype(np.float64) @ wd.T + lin.bias.numpy(), 0.0)
+    mag = np.abs(x.astype(np.float64)) @ np.abs(wd).T + np.abs(lin.bias.numpy())
+    _close(y_gpu.numpy(), ref, mag)
+    fresh = nnq.QuantizedLinearMLX(256, 64, bits=4, group_size=64, relu=True)
+    fresh.load_state_dict(sd)
+    np.testing.assert_array_equal(fresh(gpu.tensor(x, device="gpu")).numpy(), y_gpu.numpy())
+
+
+def test_engine_routes_linear_family(gpu):
+    """auto / mlx_group route Linear layers whose in_features a group size divides to the
+    group-wise layer; 'reference' keeps the int8 sidecar layers (_quantize.py:134-185)."""
+    import lucid_amd.backends as backends
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized as nnq
+    import lucid_amd.nn.quantized.dynamic as nnqd
+    from lucid_amd.quantization import quantize_dynamic
+
+    assert backends.quantized.available
+    model = nn.Sequential(nn.Linear(784, 256), nn.ReLU(), nn.Linear(256, 10)).to("gpu")
+    q = backends.quantized
+    try:
+        for engine in ("auto", "mlx_group"):
+            q.engine = engine
+            m = quantize_dynamic(model)
+            assert isinstance(m[0], nnqd.Linear)            # 784 divides by no group size
+            assert isinstance(m[2], nnq.QuantizedLinearMLX) and m[2].group_size == 64
+            assert m[2].bits == 8
+        q.engine = "reference"
+        m = quantize_dynamic(model)
+        assert isinstance(m[2], nnqd.Linear)
+    finally:
+        q.engine = "auto"
