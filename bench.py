@@ -13,8 +13,11 @@ The same JSON line carries:
   * ``roofline``: the GEMM kernel's achieved TOPS against the 5.0 POPS dense int8 MFMA
     peak (algorithmic ops / average launch time from the events);
   * ``components``: the rest of BASELINE configs 2 and 3 -- the GEMM M-sweep and the
-    4096x11008 / 11008x4096 shapes, and the bandwidth kernels (min/max observer,
-    quantize, dequantize) over 2^28 fp32 elements, each with its roofline fraction;
+    4096x11008 / 11008x4096 shapes, the weight-only decode GEMVs (per-channel int8 and
+    group-wise 4/8-bit weights against fp32 activations, M = 1 and 16, rotating weights),
+    and the bandwidth kernels (min/max observer, quantize, dequantize) over 2^28 fp32
+    elements, each with its roofline fraction.  Launch-bound decode shapes are timed by
+    replaying a captured HIP graph, so host launch cost stays out;
   * ``cpu_baseline``: Lucid's CPU composition for the same GEMM (dequantize both
     operands every call, fp32 sgemm on all host BLAS threads, bias add, multi-pass
     requantize), restated by the oracle package and timed on a bounded sample.
@@ -93,6 +96,102 @@ class Timer:
         return ms.value / steps
 
 
+class GraphTimer:
+    """Per-call time of launch-bound calls: one pass over `calls` is captured into a HIP
+    graph on a created stream (lq_graph_*), replayed `reps` times between HIP events on
+    that stream, so host launch cost stays out of the measurement."""
+
+    def __init__(self, C) -> None:
+        self.C = C
+        self.stream = ctypes.c_void_p()
+        C.call("lq_stream_create", ctypes.byref(self.stream))
+        self.start = ctypes.c_void_p()
+        self.stop = ctypes.c_void_p()
+        C.call("lq_event_create", ctypes.byref(self.start))
+        C.call("lq_event_create", ctypes.byref(self.stop))
+
+    def time_ms(self, calls, reps: int, warmup: int) -> float:
+        C, st = self.C, self.stream
+        C.call("lq_graph_begin_capture", st)
+        for call in calls:
+            call(st)
+        exe = ctypes.c_void_p()
+        C.call("lq_graph_end_capture", st, ctypes.byref(exe))
+        try:
+            for _ in range(warmup):
+                C.call("lq_graph_launch", exe, st)
+            C.call("lq_stream_synchronize", st)
+            C.call("lq_event_record", self.start, st)
+            for _ in range(reps):
+                C.call("lq_graph_launch", exe, st)
+            C.call("lq_event_record", self.stop, st)
+            C.call("lq_event_synchronize", self.stop)
+            ms = ctypes.c_float()
+            C.call("lq_event_elapsed_ms", ctypes.byref(ms), self.start, self.stop)
+        finally:
+            C.call("lq_graph_destroy", exe)
+        return ms.value / (reps * len(calls))
+
+
+def _rotations(nbytes: int) -> int:
+    """Copies of a weight needed to stream >= 512 MiB per pass (past the 256 MB
+    Infinity Cache, so each call reads its weight from HBM)."""
+    return max(1, -(-(512 << 20) // max(nbytes, 1)))
+
+
+def weight_only_lines(L, C, gtimer):
+    """Weight-only decode GEMMs (float activations x int8 / packed 4-8 bit weights), rotating
+    weights, graph-replayed: algorithmic bytes = weight + scales + x + y."""
+    out = []
+    rng = np.random.default_rng(11)
+    lib = C.lib()
+    for (M, N, K) in ((1, 4096, 4096), (16, 4096, 4096), (1, 11008, 4096), (16, 11008, 4096),
+                      (1, 4096, 11008), (16, 4096, 11008)):
+        rot = _rotations(N * K)
+        W = L.empty((rot * N * K,), np.int8, "gpu")
+        C.call("lq_fill_u32", W.data_ptr(), 0x3A1F05C7, rot * N * K // 4, None)
+        x = L.tensor(rng.standard_normal((M, K)).astype(np.float32), device="gpu")
+        y = L.empty((M, N), np.float32, "gpu")
+        s = L.tensor(rng.uniform(1e-3, 1e-1, N).astype(np.float32), device="gpu")
+        b = L.tensor(rng.standard_normal(N).astype(np.float32), device="gpu")
+        calls = [lambda st, r=r: C.check(lib.lq_gemv_w8(x.data_ptr(), C.F32, K, W.data_ptr() + r * N * K, K,
+                                                        s.data_ptr(), None, b.data_ptr(), y.data_ptr(),
+                                                        N, M, N, K, 0, None, 0, st), "lq_gemv_w8")
+                 for r in range(rot)]
+        ms = gtimer.time_ms(calls, 10, 2)
+        nbytes = N * K + 8.0 * N + 4.0 * M * (K + N)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"kernel": "lq_gemv_w8 (per-channel int8, fp32 x)", "M": M, "N": N, "K": K,
+                    "rotating_copies": rot, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 3)})
+        del W
+    for bits in (4, 8):
+        for M in (1, 16):
+            N = K = 4096
+            gs = 64
+            wbytes = N * K * bits // 8
+            G = K // gs
+            rot = _rotations(wbytes)
+            P = L.empty((rot * wbytes,), np.int8, "gpu")
+            C.call("lq_fill_u32", P.data_ptr(), 0x5A3C96E1, rot * wbytes // 4, None)
+            sc = L.tensor(np.full(rot * N * G, 1e-3, np.float32), device="gpu")
+            bi = L.tensor(np.full(rot * N * G, -0.1, np.float32), device="gpu")
+            x = L.tensor(rng.standard_normal((M, K)).astype(np.float32), device="gpu")
+            y = L.empty((M, N), np.float32, "gpu")
+            calls = [lambda st, r=r: C.check(lib.lq_group_matmul(
+                x.data_ptr(), C.F32, K, P.data_ptr() + r * wbytes, sc.data_ptr() + 4 * r * N * G,
+                bi.data_ptr() + 4 * r * N * G, None, y.data_ptr(), N, M, N, K, gs, bits, 1, 0, None, 0,
+                st), "lq_group_matmul") for r in range(rot)]
+            ms = gtimer.time_ms(calls, 10, 2)
+            nbytes = wbytes + 8.0 * N * G + 4.0 * M * (K + N)
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            out.append({"kernel": f"lq_group_matmul ({bits}-bit, group 64, fp32 x)", "M": M, "N": N,
+                        "K": K, "rotating_copies": rot, "us": round(ms * 1e3, 2),
+                        "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3)})
+            del P
+    return out
+
+
 class Gemm:
     """One configured lq_gemm_w8a8 call on device-resident synthetic inputs."""
 
@@ -125,24 +224,24 @@ class Gemm:
             arglists = [(self.A.data_ptr(), K, self.P.data_ptr() + r * pbytes, self.Cm.data_ptr(), N, M, N,
                          K, self.sa.data_ptr(), 1, self.sb.data_ptr(), 1, None, None, None,
                          self.bias.data_ptr(), self.os.data_ptr(), self.oz.data_ptr(), -128, 127,
-                         out_kind, 0, self.ws.data_ptr(), self.ws_bytes, None) for r in range(self.rot)]
+                         out_kind, 0, self.ws.data_ptr(), self.ws_bytes) for r in range(self.rot)]
         else:
             self.rot = 1
             f = C.lib().lq_gemm_w8a8
             arglists = [(self.A.data_ptr(), K, self.B.data_ptr(), K, self.Cm.data_ptr(), N, M, N, K,
                          self.sa.data_ptr(), 1, self.sb.data_ptr(), 1, None, None, None,
                          self.bias.data_ptr(), self.os.data_ptr(), self.oz.data_ptr(), -128, 127,
-                         out_kind, 0, self.ws.data_ptr(), self.ws_bytes, None)]
+                         out_kind, 0, self.ws.data_ptr(), self.ws_bytes)]
         state = {"i": 0}
 
         def run() -> None:
             args = arglists[state["i"] % len(arglists)]
             state["i"] += 1
-            rc = f(*args)
-            if rc:
-                C.check(rc, "lq_gemm_w8a8")
+            C.check(f(*args, None), "lq_gemm_w8a8")
 
         self.run = run
+        # one call per weight copy, on a given stream (graph capture)
+        self.calls = [lambda st, a=a: C.check(f(*a, st), "lq_gemm_w8a8") for a in arglists]
 
     @property
     def ops(self) -> float:
@@ -154,9 +253,12 @@ class Gemm:
         return self.M * self.K + self.K * self.N + self.M * self.N * ob + 4.0 * (self.M + 2 * self.N)
 
 
-def gemm_line(L, C, timer, M, N, K, out_kind, steps, warmup):
+def gemm_line(L, C, timer, gtimer, M, N, K, out_kind, steps, warmup):
     g = Gemm(L, C, M, N, K, out_kind, seed=M + N + K)
-    ms = timer.time_ms(g.run, steps, warmup)
+    if g.packed:  # decode shapes are launch-bound from Python: graph replay
+        ms = gtimer.time_ms(g.calls, max(steps // len(g.calls), 2), 1)
+    else:
+        ms = timer.time_ms(g.run, steps, warmup)
     tops = g.ops / (ms * 1e-3) / 1e12
     gbs = g.bytes / (ms * 1e-3) / 1e9
     ai = g.ops / g.bytes
@@ -280,6 +382,7 @@ def main() -> None:
         print(json.dumps({"error": "no HIP device visible"}))
         sys.exit(1)
     timer = Timer(C)
+    gtimer = GraphTimer(C)
     if args.copy_mb > 0:
         nbytes = args.copy_mb << 20
         src = L.empty((nbytes,), np.uint8, "gpu")
@@ -317,7 +420,8 @@ def main() -> None:
                           (1, 4096, 11008), (16, 4096, 11008), (128, 4096, 4096), (1024, 4096, 4096),
                           (4096, 4096, 4096), (4096, 11008, 4096), (4096, 4096, 11008)):
             for kind in (C.OUT_Q8, C.OUT_F16):
-                comps["gemm_sweep"].append(gemm_line(L, C, timer, m, n, k, kind, 20, 5))
+                comps["gemm_sweep"].append(gemm_line(L, C, timer, gtimer, m, n, k, kind, 20, 5))
+        comps["weight_only_gemv"] = weight_only_lines(L, C, gtimer)
         comps.update(bandwidth_lines(L, C, timer, 50, 10))
         line["components"] = comps
     line["cpu_baseline"] = cpu_baseline(M, N, K, args.cpu_seconds)

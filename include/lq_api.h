@@ -96,6 +96,15 @@ int lq_event_destroy(void* event);
 int lq_event_record(void* event, void* stream);
 int lq_event_synchronize(void* event);
 int lq_event_elapsed_ms(float* ms, void* start, void* stop);
+/* HIP graphs over a stream: capture the compute calls issued on `stream` between begin and
+ * end into an executable graph, replay it without per-kernel host launch cost.  No
+ * reference counterpart (Lucid's engine has no graph capture); for launch-bound callers
+ * such as per-token decode.  Every compute entry point is capture-safe: none of them
+ * allocates, memsets or synchronizes inside a call. */
+int lq_graph_begin_capture(void* stream);
+int lq_graph_end_capture(void* stream, void** graph_exec);
+int lq_graph_launch(void* graph_exec, void* stream);
+int lq_graph_destroy(void* graph_exec);
 
 /* ---- observers ------------------------------------------------------------ */
 /* Observer update modes. */

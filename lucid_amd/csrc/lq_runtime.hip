@@ -269,4 +269,33 @@ int lq_event_elapsed_ms(float* ms, void* start, void* stop) {
     return LQ_OK;
 }
 
+int lq_graph_begin_capture(void* stream) {
+    LQ_REQUIRE(stream, "lq_graph_begin_capture: capture needs a created stream, not the null stream");
+    LQ_HIP(hipStreamBeginCapture((hipStream_t)stream, hipStreamCaptureModeThreadLocal));
+    return LQ_OK;
+}
+
+int lq_graph_end_capture(void* stream, void** graph_exec) {
+    LQ_REQUIRE(stream && graph_exec, "lq_graph_end_capture: NULL argument");
+    hipGraph_t g = nullptr;
+    LQ_HIP(hipStreamEndCapture((hipStream_t)stream, &g));
+    hipGraphExec_t e = nullptr;
+    const hipError_t err = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+    hipGraphDestroy(g);
+    if (err != hipSuccess) return check_hip(err, "hipGraphInstantiate");
+    *graph_exec = (void*)e;
+    return LQ_OK;
+}
+
+int lq_graph_launch(void* graph_exec, void* stream) {
+    LQ_REQUIRE(graph_exec, "lq_graph_launch: NULL graph");
+    LQ_HIP(hipGraphLaunch((hipGraphExec_t)graph_exec, (hipStream_t)stream));
+    return LQ_OK;
+}
+
+int lq_graph_destroy(void* graph_exec) {
+    if (graph_exec) LQ_HIP(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+    return LQ_OK;
+}
+
 }  // extern "C"

@@ -31,6 +31,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <type_traits>
 
 #include "lq_internal.h"
 
@@ -435,23 +436,50 @@ __global__ __launch_bounds__(1024) void wo_gemv_valu_kernel(WvArgs a) {
         xs[m * a.Kpad + wv_slot(k)] = v;
     }
     __syncthreads();
-    if constexpr (GROUPED) {
-        for (int i = tid; i < MX * a.G; i += blockDim.x) {
-            const int m = i / a.G, g = i - m * a.G;
-            float sum = 0.0f;
-            for (int k = g * a.gs; k < (g + 1) * a.gs; ++k) sum += xs[m * a.Kpad + wv_slot(k)];
-            gsum[i] = sum;
+    // x sums: per group (group-wise) or per row (zero points), from float4 partials reduced
+    // across the lanes of a group by shuffles, then in fixed order across waves
+    if (GROUPED || a.w_zp) {
+        const int span = GROUPED ? a.gs : a.Kpad;  // elements summed into one value
+        const int per = span / 4;                  // float4 partials per value
+        float* wsum = gsum + (GROUPED ? MX * a.G : MX);  // [waves][MX] (zero-point totals)
+        for (int i0 = 0; i0 < MX * a.Kpad / 4; i0 += blockDim.x) {
+            const int i = i0 + tid;
+            float v = 0.0f;
+            if (i < MX * a.Kpad / 4) {
+                const int m = (4 * i) / a.Kpad, k = (4 * i) % a.Kpad;
+                const vf4 q = *reinterpret_cast<const vf4*>(xs + m * a.Kpad + wv_slot(k));
+                v = (q[0] + q[1]) + (q[2] + q[3]);
+            }
+            if (GROUPED) {
+                // per <= 32 lanes of one group are consecutive threads of one wave
+#pragma unroll
+                for (int off = 1; off < 64; off <<= 1)
+                    if (off < per) v += __shfl_xor(v, off, 64);
+                if (i < MX * a.Kpad / 4 && (i % per) == 0) {
+                    const int m = (4 * i) / a.Kpad, k = (4 * i) % a.Kpad;
+                    if (k < a.K) gsum[m * a.G + k / a.gs] = v;  // Kpad is a multiple of gs
+                }
+            } else {
+#pragma unroll
+                for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
+                // a wave's 64 partials lie in one row (Kpad is a multiple of 256)
+                if (lane == 0 && i0 + wave * 64 < MX * a.Kpad / 4) {
+                    const int m = (4 * (i0 + wave * 64)) / a.Kpad;
+                    const int slot = (i0 / (int)blockDim.x) * waves + wave;
+                    wsum[slot * MX + m] = v;  // distinct slot per (pass, wave); zero for other rows below
+                }
+            }
         }
-        __syncthreads();
-    } else if (a.w_zp) {
-        if (wave == 0) {
-#pragma unroll
-            for (int m = 0; m < MX; ++m) {
-                float sum = 0.0f;
-                for (int k = lane; k < a.K; k += 64) sum += xs[m * a.Kpad + wv_slot(k)];
-#pragma unroll
-                for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
-                if (lane == 0) gsum[m] = sum;
+        if (!GROUPED) {
+            __syncthreads();
+            if (tid < MX) {
+                const int passes = (MX * a.Kpad / 4 + blockDim.x - 1) / blockDim.x;
+                float t = 0.0f;
+                for (int sidx = 0; sidx < passes * waves; ++sidx) {
+                    const int i = (sidx / waves) * blockDim.x + (sidx % waves) * 64;
+                    if (i < MX * a.Kpad / 4 && (4 * i) / a.Kpad == tid) t += wsum[sidx * MX + tid];
+                }
+                gsum[tid] = t;
             }
         }
         __syncthreads();
@@ -661,33 +689,45 @@ bool launch_wv(WvArgs a, bool xf32, hipStream_t st) {
     a.NC = (int)(row_bytes / 16);
     const int Jn = (a.NC + 63) / 64;
     const int J = Jn <= 1 ? 1 : Jn <= 2 ? 2 : Jn <= 4 ? 4 : Jn <= 8 ? 8 : Jn <= 12 ? 12 : Jn <= 16 ? 16 : 0;
-    if (J == 0 || (GROUPED && J > 8)) return false;  // (group scales of 12+ chunks spill)
+    if (J == 0) return false;
     a.Kpad = J * 64 * CK;
     const int MX = a.M;
-    const size_t lds = sizeof(float) * ((size_t)MX * a.Kpad + (GROUPED ? (size_t)MX * a.G : (size_t)MX));
-    if (lds > 64 * 1024) return false;
     const int waves = a.N >= 4096 ? 16 : std::max(1, (a.N + 255) / 256);
+    const size_t passes = ((size_t)MX * a.Kpad / 4 + 64 * waves - 1) / (64 * waves);
+    const size_t lds = sizeof(float) * ((size_t)MX * a.Kpad +
+                                        (GROUPED ? (size_t)MX * a.G : (size_t)MX + passes * waves * MX));
+    if (lds > 64 * 1024) return false;
     const dim3 grid((unsigned)((a.N + waves - 1) / waves));
     const dim3 block(64 * waves);
-#define LQ_WV(MXV, XV, JV) \
-    hipLaunchKernelGGL((wo_gemv_valu_kernel<BITS, SIGNED, GROUPED, MXV, XV, JV>), grid, block, lds, st, a)
-#define LQ_WVJ(MXV, XV)                                                                    \
-    switch (J) {                                                                           \
-        case 1: LQ_WV(MXV, XV, 1); break;                                                  \
-        case 2: LQ_WV(MXV, XV, 2); break;                                                  \
-        case 4: LQ_WV(MXV, XV, 4); break;                                                  \
-        case 8: LQ_WV(MXV, XV, 8); break;                                                  \
-        case 12: LQ_WV(MXV, XV, 12); break;                                                \
-        default: LQ_WV(MXV, XV, 16); break;                                                \
-    }
-    if (MX == 1) {
-        if (xf32) { LQ_WVJ(1, true) } else { LQ_WVJ(1, false) }
-    } else {
-        if (xf32) { LQ_WVJ(2, true) } else { LQ_WVJ(2, false) }
-    }
-#undef LQ_WVJ
-#undef LQ_WV
-    return true;
+    // (instantiated only for the chunk counts whose registers fit: group scales of 12+ chunks,
+    // or of 8 chunks at 4 bits and two rows, would spill)
+    auto go = [&](auto mx, auto xf, auto jv) {
+        constexpr int MXV = decltype(mx)::value, JV = decltype(jv)::value;
+        constexpr bool XV = decltype(xf)::value;
+        constexpr bool fits = !GROUPED || (JV <= 8 && !(BITS == 4 && MXV == 2 && JV > 4));
+        if constexpr (fits) {
+            hipLaunchKernelGGL((wo_gemv_valu_kernel<BITS, SIGNED, GROUPED, MXV, XV, JV>), grid, block, lds, st, a);
+            return true;
+        } else {
+            return false;
+        }
+    };
+    auto by_j = [&](auto mx, auto xf) {
+        switch (J) {
+            case 1: return go(mx, xf, std::integral_constant<int, 1>{});
+            case 2: return go(mx, xf, std::integral_constant<int, 2>{});
+            case 4: return go(mx, xf, std::integral_constant<int, 4>{});
+            case 8: return go(mx, xf, std::integral_constant<int, 8>{});
+            case 12: return go(mx, xf, std::integral_constant<int, 12>{});
+            default: return go(mx, xf, std::integral_constant<int, 16>{});
+        }
+    };
+    using T1 = std::integral_constant<int, 1>;
+    using T2 = std::integral_constant<int, 2>;
+    using F32 = std::integral_constant<bool, true>;
+    using F16 = std::integral_constant<bool, false>;
+    if (MX == 1) return xf32 ? by_j(T1{}, F32{}) : by_j(T1{}, F16{});
+    return xf32 ? by_j(T2{}, F32{}) : by_j(T2{}, F16{});
 }
 
 constexpr int64_t WO_MAX_DIM = (int64_t)1 << 30;

@@ -245,3 +245,18 @@ def test_engine_routes_linear_family(gpu):
         assert isinstance(m[2], nnqd.Linear)
     finally:
         q.engine = "auto"
+
+
+def test_dispatch_bench_harness(gpu):
+    """The bench_quantized_dispatch counterpart: parity gate, three paths, reference keys."""
+    from lucid_amd import bench_quantized_dispatch as bqd
+
+    rep = bqd.run(iters=2, width=256)
+    rows = rep["rows"]
+    assert len(rows) == 2 * 4 * 3
+    assert {r["path"] for r in rows} == {"packed", "cached_dense", "dequant_each_call"}
+    for r in rows:
+        assert r["parity_relative_error"] <= 1e-4
+        assert r["p5_ms"] <= r["median_ms"] <= r["p95_ms"]
+        for key in ("bits", "m", "n", "k", "first_ms", "GB/s", "hbm_roofline_frac", "TOPS"):
+            assert key in r
