@@ -293,7 +293,50 @@ int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d
                     int transpose, int flags, void* d_workspace, size_t workspace_bytes,
                     void* stream);
 
+/* ---- int8 Conv2d (implicit GEMM) ------------------------------------------------- */
+/* Padding modes of a convolution (Lucid's padding_mode, lucid/nn/functional/conv.py:24-29). */
+enum { LQ_PAD_ZEROS = 0, LQ_PAD_REFLECT = 1, LQ_PAD_REPLICATE = 2, LQ_PAD_CIRCULAR = 3 };
+
+/* Weight codes w[Cout, Cin_g, KH, KW] (Lucid's weight_int8 of a quantized Conv2d,
+ * lucid/nn/quantized/conv.py:92-100) in the layout the conv kernel reads:
+ * w_p[Cout][KH][KW][Cp], Cp = Cin_g rounded up to 16 with zero codes, and the code sums
+ * d_w_sums[Cout] (NULL to skip) for the activation zero-point term.  Built once per module.
+ * No reference counterpart (a device layout; the state_dict keeps weight_int8). */
+size_t lq_conv2d_weight_pack_size(int64_t Cout, int64_t Cin_g, int64_t KH, int64_t KW);
+int lq_conv2d_pack_weights_i8(const int8_t* d_w, int64_t Cout, int64_t Cin_g, int64_t KH, int64_t KW,
+                              int8_t* d_w_packed, int32_t* d_w_sums, void* stream);
+/* Quantized Conv2d forward on activation codes x[N, C, H, W] (LQ_I8, or LQ_U8S8 for an
+ * unsigned grid with d_a_zero_point its own zero point) and packed weights:
+ *   acc[n, co, oh, ow] = sum_{c, kh, kw} (x[n, g*Cg + c, oh*sh + kh*dh - pt, ow*sw + kw*dw - pl] - za)
+ *                        * w[co, c, kh, kw]                  (exact int32, padded taps = za)
+ * then the epilogue of lq_gemm_w8a8 with a per-tensor activation scale, per-channel weight
+ * scales d_w_scale[Cout] (symmetric weights: no weight zero point), bias, LQ_EPI_RELU and
+ * out_kind, written NCHW to d_y[N, Cout, OH, OW].  Replaces dequantize -> F.conv2d ->
+ * fake_quantize of lucid/nn/quantized/conv.py:137-172 (-> lucid/nn/functional/conv.py:53-84
+ * -> lucid/_C/backend/cpu/methods/Conv.cpp:271-360).  padding_mode LQ_PAD_*; workspace of
+ * lq_conv2d_i8_workspace_size bytes (the padded NHWC copy of x).  Two launches. */
+size_t lq_conv2d_i8_workspace_size(int64_t N, int64_t C, int64_t H, int64_t W, int64_t groups, int pad_top,
+                                   int pad_bottom, int pad_left, int pad_right);
+int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64_t H, int64_t W,
+                 const int8_t* d_w_packed, const int32_t* d_w_sums, int64_t Cout, int64_t KH, int64_t KW,
+                 int stride_h, int stride_w, int pad_top, int pad_bottom, int pad_left, int pad_right,
+                 int dilation_h, int dilation_w, int64_t groups, int padding_mode, const float* d_a_scale,
+                 const float* d_a_zero_point, const float* d_w_scale, const float* d_bias,
+                 const float* d_out_scale, const float* d_out_zero_point, int out_qmin, int out_qmax,
+                 int out_kind, int flags, void* d_y, void* d_workspace, size_t workspace_bytes, void* stream);
+
 /* ---- float helpers around the quantized path ----------------------------------- */
+/* Float Conv2d y[N, Cout, OH, OW] (direct; the float model's conv during calibration,
+ * lucid/nn/functional/conv.py:53-84 -> Conv.cpp:271-360): per output, sum over (c, kh, kw)
+ * in that order in float32 (multiply then add), bias last. */
+int lq_conv2d_f32(const float* d_x, int64_t N, int64_t C, int64_t H, int64_t W, const float* d_w,
+                  const float* d_bias, int64_t Cout, int64_t KH, int64_t KW, int stride_h, int stride_w,
+                  int pad_top, int pad_bottom, int pad_left, int pad_right, int dilation_h, int dilation_w,
+                  int64_t groups, int padding_mode, float* d_y, void* stream);
+/* Eval BatchNorm over [N, C, HW]: y = ((x - mean) * (1 / sqrt(var + eps))) * gamma + beta
+ * (gamma / beta NULL: 1 / 0).  The float model's BatchNorm2d before fusion. */
+int lq_batch_norm_f32(const float* d_x, float* d_y, int64_t N, int64_t C, int64_t HW, const float* d_mean,
+                      const float* d_var, const float* d_gamma, const float* d_beta, float eps, void* stream);
 /* y = (x <= 0) ? +0 : x, NaN passes (the CPU relu of backend/cpu/Vdsp.cpp vrelu_f32,
  * reached from nn.ReLU between quantized layers). */
 int lq_relu_f32(const float* d_x, float* d_y, int64_t n, void* stream);

@@ -23,6 +23,7 @@ I8, U8, I16, I32, F16, F32, U8S8 = 1, 2, 3, 4, 5, 6, 7
 OBS_MINMAX, OBS_EMA, OBS_REPLACE = 0, 1, 2
 OUT_I32, OUT_F32, OUT_F16, OUT_Q8, OUT_QU8, OUT_FQ32, OUT_Q16, OUT_QU8S8 = 0, 1, 2, 3, 4, 5, 6, 7
 EPI_RELU, EPI_A_U8S8 = 1, 2
+PAD_ZEROS, PAD_REFLECT, PAD_REPLICATE, PAD_CIRCULAR = 0, 1, 2, 3
 
 
 class LucidError(RuntimeError):
@@ -87,6 +88,15 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_pack_weights_i8": (_I, [_P, _I64, _I64, _I64, _P, _P]),
     "lq_gemm_w8a8_packed": (_I, [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64,
                                  _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _SZ, _P]),
+    "lq_conv2d_weight_pack_size": (_SZ, [_I64, _I64, _I64, _I64]),
+    "lq_conv2d_pack_weights_i8": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P]),
+    "lq_conv2d_i8_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I, _I, _I, _I]),
+    "lq_conv2d_i8": (_I, [_P, _I, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I, _I, _I, _I, _I,
+                          _I, _I, _I, _I64, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _SZ,
+                          _P]),
+    "lq_conv2d_f32": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I, _I, _I, _I, _I, _I,
+                           _I, _I, _I64, _I, _P, _P]),
+    "lq_batch_norm_f32": (_I, [_P, _P, _I64, _I64, _I64, _P, _P, _P, _P, _F, _P]),
     "lq_gemv_w8_workspace_size": (_SZ, [_I64, _I64, _I64]),
     "lq_gemv_w8": (_I, [_P, _I, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P,
                         _SZ, _P]),

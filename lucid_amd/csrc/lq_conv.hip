@@ -1,0 +1,524 @@
+// lq_conv.hip -- int8 Conv2d as an implicit GEMM on CDNA4 MFMA (v_mfma_i32_16x16x64_i8), with
+// the W8A8 epilogue of the GEMM, plus the float direct convolution and eval BatchNorm the
+// float model runs during calibration.
+//
+// Replaces the compute of Lucid's quantized Conv2d, which dequantizes the int8 kernel and runs
+// a float conv (im2col + sgemm per batch and group) every call, then fake-quantizes
+// (lucid/nn/quantized/conv.py:137-172 -> lucid/nn/functional/conv.py:53-84 ->
+// lucid/_C/backend/cpu/methods/Conv.cpp:271-360).  Here:
+//
+//   acc[p, co] = sum_{kh,kw,c} (x[n, c, oh*sh + kh*dh - pt, ow*sw + kw*dw - pl] - za) * w[co, c, kh, kw]
+//
+// exact in int32, then y = fl32(fl32(float(acc) * fl32(sx * sw[co])) + b[co]), ReLU, requantize.
+//
+// Data layout.  The activation codes (NCHW, as the module API holds them) are first packed
+// into a padded NHWC copy, x_p[n][hp][wp][g][cp] with cp padded to a multiple of 16: the
+// spatial border (zeros padding) and the channel padding hold the activation zero point in
+// its stored units, so they contribute exactly 0 to acc; reflect / replicate / circular
+// padding are index maps of the same pack.  The weights are packed once per module into
+// w_p[g][co][kh][kw][cp] (zero channel padding) with their code sums (the zero-point term).
+// A 16-byte K chunk of the implicit im2col row of pixel p is then one contiguous load:
+// K index k = (kh * KW + kw) * Cp + c, chunk start c a multiple of 16.
+//
+// Tiling.  A workgroup (4 waves) computes 128 pixels x 64 output channels of one group with
+// K steps of 64 bytes, register-staged double buffering through LDS (16-byte chunks XOR-
+// swizzled by row so the MFMA fragment reads are conflict-free).  Pixels are the MFMA row
+// operand, so a lane's four results are four consecutive pixels of one output channel:
+// one contiguous NCHW store.
+#include <hip/hip_runtime.h>
+
+#include "lq_epilogue.h"
+#include "lq_internal.h"
+
+namespace lq {
+namespace {
+
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+constexpr int CV_BM = 128, CV_BN = 64, CV_BK = 64, CV_THREADS = 256;
+
+// ---------------------------------------------------------------- packing
+
+__device__ __forceinline__ int pad_index(int i, int n, int mode) {
+    // source index of padded coordinate i (may be < 0 or >= n), or -1 for a zero-padded tap
+    if (i >= 0 && i < n) return i;
+    switch (mode) {
+        case LQ_PAD_REFLECT: {  // mirror without repeating the edge
+            if (n == 1) return 0;
+            const int period = 2 * (n - 1);
+            int j = i % period;
+            if (j < 0) j += period;
+            return j < n ? j : period - j;
+        }
+        case LQ_PAD_REPLICATE: return i < 0 ? 0 : n - 1;
+        case LQ_PAD_CIRCULAR: {
+            int j = i % n;
+            return j < 0 ? j + n : j;
+        }
+        default: return -1;
+    }
+}
+
+struct PackArgs {
+    const int8_t* x;
+    int8_t* xp;
+    int N, C, H, W, G, Cg, Cp, Hp, Wp, pt, pl, mode;
+    const float* a_zp;
+    int a_u8s8;
+};
+
+// One thread writes the 16 channels [16j, 16j + 16) of one group at one padded position.
+__global__ __launch_bounds__(256) void conv_pack_input_kernel(PackArgs a) {
+    const int chunks = a.Cp / 16;
+    const int64_t total = (int64_t)a.N * a.Hp * a.Wp * a.G * chunks;
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= total) return;
+    const int j = (int)(id % chunks);
+    int64_t r = id / chunks;
+    const int g = (int)(r % a.G);
+    r /= a.G;
+    const int wp = (int)(r % a.Wp);
+    r /= a.Wp;
+    const int hp = (int)(r % a.Hp);
+    const int n = (int)(r / a.Hp);
+    const int fill = (a.a_zp ? (int)a.a_zp[0] : 0) - (a.a_u8s8 ? 128 : 0);
+    const int h = pad_index(hp - a.pt, a.H, a.mode);
+    const int w = pad_index(wp - a.pl, a.W, a.mode);
+    uint32_t word[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int c = 16 * j + 4 * q + b;  // channel within the group
+            int code = fill;
+            if (c < a.Cg && h >= 0 && w >= 0)
+                code = a.x[(((int64_t)n * a.C + (int64_t)g * a.Cg + c) * a.H + h) * a.W + w];
+            v |= (uint32_t)(uint8_t)code << (8 * b);
+        }
+        word[q] = v;
+    }
+    reinterpret_cast<vu4*>(a.xp)[id] = vu4{word[0], word[1], word[2], word[3]};
+}
+
+// One thread per output channel row: w_p[co][kh][kw][cp] and the row's code sum.
+__global__ __launch_bounds__(256) void conv_pack_weights_kernel(const int8_t* __restrict__ w, int Cout, int Cg,
+                                                                int KH, int KW, int Cp, int8_t* __restrict__ wp,
+                                                                int32_t* __restrict__ sums) {
+    const int co = blockIdx.x * blockDim.x + threadIdx.x;
+    if (co >= Cout) return;
+    const int64_t K = (int64_t)KH * KW * Cp;
+    int32_t s = 0;
+    for (int kh = 0; kh < KH; ++kh)
+        for (int kw = 0; kw < KW; ++kw)
+            for (int c = 0; c < Cp; ++c) {
+                int8_t v = 0;
+                if (c < Cg) v = w[(((int64_t)co * Cg + c) * KH + kh) * KW + kw];
+                wp[co * K + ((int64_t)kh * KW + kw) * Cp + c] = v;
+                s += v;
+            }
+    if (sums) sums[co] = s;
+}
+
+// ---------------------------------------------------------------- implicit GEMM
+
+struct ConvArgs {
+    const int8_t* xp;
+    const int8_t* wp;
+    void* y;
+    int N, Hp, Wp, G, Cp, Cout_g, KH, KW, sh, sw, dh, dw, OH, OW;
+    int K, P;
+    const float* a_scale;
+    const float* a_zp;
+    int a_u8s8;
+    const float* w_scale;
+    const int32_t* w_sums;
+    const float* bias;
+    const float* out_scale;
+    const float* out_zp;
+    int qmin, qmax, relu;
+};
+
+// 16-byte LDS slot of chunk c (0..3) of tile row r: rows are 64 bytes (16 banks); the XOR by
+// (r >> 2) & 3 spreads the 16 rows an MFMA fragment read touches over all 64 banks.
+__device__ __forceinline__ int cv_slot(int r, int c) { return r * 4 + (c ^ ((r >> 2) & 3)); }
+
+// Running (kh, kw, c) of a K offset, advanced by whole K steps without divisions.
+struct KPos {
+    int kh, kw, c;
+    __device__ __forceinline__ void init(int k, int Cp, int KW) {
+        const int khw = k / Cp;
+        c = k - khw * Cp;
+        kh = khw / KW;
+        kw = khw - kh * KW;
+    }
+    __device__ __forceinline__ void advance(int step, int Cp, int KW) {
+        c += step;
+        while (c >= Cp) {
+            c -= Cp;
+            if (++kw == KW) {
+                kw = 0;
+                ++kh;
+            }
+        }
+    }
+};
+
+template <int KIND>
+__global__ __launch_bounds__(CV_THREADS) void conv_i8_kernel(ConvArgs a) {
+    __shared__ vu4 lds_a[2][CV_BM * 4];
+    __shared__ vu4 lds_b[2][CV_BN * 4];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int wm = wave & 1, wn = wave >> 1;  // wave: 64 pixels x 32 channels
+    const int p0 = blockIdx.x * CV_BM;
+    const int co0 = blockIdx.y * CV_BN;
+    const int g = blockIdx.z;
+    const int GCp = a.G * a.Cp;
+    const int T = (a.K + CV_BK - 1) / CV_BK;
+
+    // A: two 16-byte chunks per thread (rows r0, r0 + 64 of the tile, chunk ca)
+    const int ca = tid & 3;
+    int64_t abase[2];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+        const int p = min(p0 + (tid >> 2) + 64 * i, a.P - 1);
+        const int n = p / (a.OH * a.OW);
+        const int rem = p - n * a.OH * a.OW;
+        const int oh = rem / a.OW, ow = rem - oh * a.OW;
+        abase[i] = (((int64_t)n * a.Hp + (int64_t)oh * a.sh) * a.Wp + (int64_t)ow * a.sw) * GCp + (int64_t)g * a.Cp;
+    }
+    KPos ka;
+    ka.init(16 * ca, a.Cp, a.KW);
+    int ka_k = 16 * ca;
+    // B: one chunk per thread (row tid >> 2, chunk tid & 3)
+    const int brow = tid >> 2;
+    const int8_t* bptr = a.wp + ((int64_t)g * a.Cout_g + min(co0 + brow, a.Cout_g - 1)) * a.K + 16 * ca;
+
+    vu4 ra[2], rb;
+    auto gload = [&](int t) {
+        const bool kin = ka_k < a.K;
+        const int64_t off = ((int64_t)ka.kh * a.dh * a.Wp + (int64_t)ka.kw * a.dw) * GCp + ka.c;
+#pragma unroll
+        for (int i = 0; i < 2; ++i)
+            ra[i] = kin ? *reinterpret_cast<const vu4*>(a.xp + abase[i] + off) : vu4{0u, 0u, 0u, 0u};
+        rb = (t * CV_BK + 16 * ca < a.K) ? *reinterpret_cast<const vu4*>(bptr + (int64_t)t * CV_BK)
+                                        : vu4{0u, 0u, 0u, 0u};
+        ka.advance(CV_BK, a.Cp, a.KW);
+        ka_k += CV_BK;
+    };
+    auto sstore = [&](int s) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) lds_a[s][cv_slot((tid >> 2) + 64 * i, ca)] = ra[i];
+        lds_b[s][cv_slot(brow, ca)] = rb;
+    };
+
+    v4i acc[4][2];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 2; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+    gload(0);
+    sstore(0);
+    __syncthreads();
+    const int fr = lane & 15, fc = lane >> 4;  // fragment row / 16-byte chunk
+    for (int t = 0; t < T; ++t) {
+        const int s = t & 1;
+        if (t + 1 < T) gload(t + 1);
+        v4i fa[4], fb[2];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const vu4 v = lds_a[s][cv_slot(wm * 64 + i * 16 + fr, fc)];
+            fa[i] = __builtin_bit_cast(v4i, v);
+        }
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+            const vu4 v = lds_b[s][cv_slot(wn * 32 + j * 16 + fr, fc)];
+            fb[j] = __builtin_bit_cast(v4i, v);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < 2; ++j) acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(fa[i], fb[j], acc[i][j], 0, 0, 0);
+        if (t + 1 < T) sstore(s ^ 1);
+        __syncthreads();
+    }
+
+    // epilogue: lane holds pixels 4*(lane/16) + r of each m-tile, channel lane % 16 of each n-tile
+    EpiParams ep;
+    ep.za = (a.a_zp ? (int)a.a_zp[0] : 0) - (a.a_u8s8 ? 128 : 0);
+    ep.has_za = a.a_zp != nullptr || a.a_u8s8;
+    ep.out_s = a.out_scale ? a.out_scale[0] : 1.0f;
+    ep.out_inv = 1.0f / ep.out_s;
+    ep.out_z = a.out_zp ? a.out_zp[0] : 0.0f;
+    ep.g = Grid{(float)a.qmin, (float)a.qmax, a.qmin == 0, false};
+    const float sa = a.a_scale ? a.a_scale[0] : 1.0f;
+    const int OHW = a.OH * a.OW;
+    const int Cout = a.G * a.Cout_g;
+    constexpr int b = OutTraits<KIND>::bytes;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int col = co0 + wn * 32 + j * 16 + fr;  // channel within the group
+        if (col >= a.Cout_g) continue;
+        const int co = g * a.Cout_g + col;
+        const float sb = a.w_scale[co];
+        const float bias = a.bias ? a.bias[co] : 0.0f;
+        const int32_t wsum = a.w_sums ? a.w_sums[co] : 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int p = p0 + wm * 64 + i * 16 + 4 * fc;
+            if (p >= a.P) continue;
+            uint32_t out[4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                uint32_t v = (uint32_t)acc[i][j][r];
+                if (ep.has_za) v -= (uint32_t)ep.za * (uint32_t)wsum;
+                out[r] = epi_one<KIND>((int32_t)v, sa, sb, a.bias ? &bias : nullptr, a.relu != 0, ep);
+            }
+            const int n = p / OHW, pix = p - n * OHW;
+            const int64_t base = ((int64_t)n * Cout + co) * OHW + pix;
+            if ((OHW & 3) == 0 && p + 3 < a.P) {  // four pixels of one image, aligned
+                if (b == 4) {
+                    *reinterpret_cast<vu4*>(reinterpret_cast<uint32_t*>(a.y) + base) = vu4{out[0], out[1], out[2], out[3]};
+                } else if (b == 2) {
+                    *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.y) + base) =
+                        make_uint2(out[0] | (out[1] << 16), out[2] | (out[3] << 16));
+                } else {
+                    *reinterpret_cast<uint32_t*>(reinterpret_cast<uint8_t*>(a.y) + base) =
+                        out[0] | (out[1] << 8) | (out[2] << 16) | (out[3] << 24);
+                }
+            } else {
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int pr = p + r;
+                    if (pr >= a.P) break;
+                    const int nr = pr / OHW, pixr = pr - nr * OHW;
+                    store_elem<KIND>(a.y, ((int64_t)nr * Cout + co) * OHW + pixr, out[r]);
+                }
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------- float helpers
+
+struct FConvArgs {
+    const float* x;
+    const float* w;
+    const float* bias;
+    float* y;
+    int N, C, H, W, Cout, G, Cg, Cout_g, KH, KW, sh, sw, pt, pl, dh, dw, OH, OW, mode;
+};
+
+// Direct float convolution, one thread per output: sum over (c, kh, kw) in that order,
+// float32 multiply then add (no FMA), bias added last.
+__global__ __launch_bounds__(256) void conv_f32_kernel(FConvArgs a) {
+    const int64_t total = (int64_t)a.N * a.Cout * a.OH * a.OW;
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= total) return;
+    const int ow = (int)(id % a.OW);
+    int64_t r = id / a.OW;
+    const int oh = (int)(r % a.OH);
+    r /= a.OH;
+    const int co = (int)(r % a.Cout);
+    const int n = (int)(r / a.Cout);
+    const int g = co / a.Cout_g;
+    float acc = 0.0f;
+    for (int c = 0; c < a.Cg; ++c) {
+        const float* xc = a.x + ((int64_t)n * a.C + (int64_t)g * a.Cg + c) * a.H * a.W;
+        const float* wc = a.w + ((int64_t)co * a.Cg + c) * a.KH * a.KW;
+        for (int kh = 0; kh < a.KH; ++kh) {
+            const int h = pad_index(oh * a.sh + kh * a.dh - a.pt, a.H, a.mode);
+            if (h < 0) continue;
+            for (int kw = 0; kw < a.KW; ++kw) {
+                const int w = pad_index(ow * a.sw + kw * a.dw - a.pl, a.W, a.mode);
+                if (w < 0) continue;
+                const float prod = xc[(int64_t)h * a.W + w] * wc[kh * a.KW + kw];
+                acc = acc + prod;
+            }
+        }
+    }
+    if (a.bias) acc = acc + a.bias[co];
+    a.y[id] = acc;
+}
+
+// Eval BatchNorm over NCHW: y = fl32(fl32(fl32(x - mean) * fl32(1 / sqrt(var + eps))) * gamma) + beta.
+__global__ __launch_bounds__(256) void batch_norm_f32_kernel(const float* __restrict__ x, float* __restrict__ y,
+                                                             int64_t N, int C, int64_t HW, const float* __restrict__ mean,
+                                                             const float* __restrict__ var, const float* __restrict__ gamma,
+                                                             const float* __restrict__ beta, float eps) {
+    const int64_t total = N * C * HW;
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= total) return;
+    const int c = (int)((id / HW) % C);
+    const float inv = 1.0f / sqrtf(var[c] + eps);
+    float v = (x[id] - mean[c]) * inv;
+    if (gamma) v = v * gamma[c];
+    if (beta) v = v + beta[c];
+    y[id] = v;
+}
+
+bool conv_geometry(int64_t H, int64_t W, int KH, int KW, int sh, int sw, int pt, int pb, int pl, int pr,
+                   int dh, int dw, int64_t* OH, int64_t* OW) {
+    if (KH < 1 || KW < 1 || sh < 1 || sw < 1 || dh < 1 || dw < 1 || pt < 0 || pb < 0 || pl < 0 || pr < 0)
+        return false;
+    const int64_t eh = (int64_t)dh * (KH - 1) + 1, ew = (int64_t)dw * (KW - 1) + 1;
+    const int64_t hp = H + pt + pb, wp = W + pl + pr;
+    if (hp < eh || wp < ew) return false;
+    *OH = (hp - eh) / sh + 1;
+    *OW = (wp - ew) / sw + 1;
+    return true;
+}
+
+constexpr int64_t CV_MAX = (int64_t)1 << 31;
+
+}  // namespace
+}  // namespace lq
+
+using namespace lq;
+
+extern "C" {
+
+size_t lq_conv2d_weight_pack_size(int64_t Cout, int64_t Cin_g, int64_t KH, int64_t KW) {
+    if (Cout < 0 || Cin_g < 1 || KH < 1 || KW < 1) return 0;
+    const int64_t Cp = (Cin_g + 15) / 16 * 16;
+    return (size_t)(Cout * KH * KW * Cp);
+}
+
+int lq_conv2d_pack_weights_i8(const int8_t* d_w, int64_t Cout, int64_t Cin_g, int64_t KH, int64_t KW,
+                              int8_t* d_w_packed, int32_t* d_w_sums, void* stream) {
+    LQ_REQUIRE(Cout >= 0 && Cin_g >= 1 && KH >= 1 && KW >= 1 && Cout * Cin_g * KH * KW < CV_MAX,
+               "lq_conv2d_pack_weights_i8: bad shape");
+    if (Cout == 0) return LQ_OK;
+    LQ_REQUIRE(d_w && d_w_packed, "lq_conv2d_pack_weights_i8: NULL pointer");
+    const int Cp = (int)((Cin_g + 15) / 16 * 16);
+    hipLaunchKernelGGL(conv_pack_weights_kernel, dim3((unsigned)((Cout + 255) / 256)), dim3(256), 0, as_stream(stream),
+                       d_w, (int)Cout, (int)Cin_g, (int)KH, (int)KW, Cp, d_w_packed, d_w_sums);
+    return launch_status("lq_conv2d_pack_weights_i8");
+}
+
+size_t lq_conv2d_i8_workspace_size(int64_t N, int64_t C, int64_t H, int64_t W, int64_t groups, int pad_top,
+                                   int pad_bottom, int pad_left, int pad_right) {
+    if (N < 0 || C < 1 || H < 1 || W < 1 || groups < 1 || C % groups) return 0;
+    const int64_t Cp = (C / groups + 15) / 16 * 16;
+    return (size_t)(N * (H + pad_top + pad_bottom) * (W + pad_left + pad_right) * groups * Cp);
+}
+
+int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64_t H, int64_t W,
+                 const int8_t* d_w_packed, const int32_t* d_w_sums, int64_t Cout, int64_t KH, int64_t KW,
+                 int stride_h, int stride_w, int pad_top, int pad_bottom, int pad_left, int pad_right,
+                 int dilation_h, int dilation_w, int64_t groups, int padding_mode, const float* d_a_scale,
+                 const float* d_a_zero_point, const float* d_w_scale, const float* d_bias,
+                 const float* d_out_scale, const float* d_out_zero_point, int out_qmin, int out_qmax,
+                 int out_kind, int flags, void* d_y, void* d_workspace, size_t workspace_bytes, void* stream) {
+    LQ_REQUIRE(N >= 0 && C >= 1 && H >= 1 && W >= 1 && Cout >= 1 && groups >= 1,
+               "lq_conv2d_i8: bad shape");
+    LQ_REQUIRE(C % groups == 0 && Cout % groups == 0, "lq_conv2d_i8: channels must divide by groups");
+    LQ_REQUIRE(x_code_type == LQ_I8 || x_code_type == LQ_U8S8, "lq_conv2d_i8: activation codes must be LQ_I8 or LQ_U8S8");
+    LQ_REQUIRE(padding_mode >= LQ_PAD_ZEROS && padding_mode <= LQ_PAD_CIRCULAR, "lq_conv2d_i8: unknown padding mode");
+    LQ_REQUIRE((flags & ~LQ_EPI_RELU) == 0, "lq_conv2d_i8: unknown flags");
+    LQ_REQUIRE(out_kind >= LQ_OUT_I32 && out_kind <= LQ_OUT_QU8S8, "lq_conv2d_i8: unknown out_kind");
+    int64_t OH = 0, OW = 0;
+    LQ_REQUIRE(conv_geometry(H, W, (int)KH, (int)KW, stride_h, stride_w, pad_top, pad_bottom, pad_left, pad_right,
+                             dilation_h, dilation_w, &OH, &OW),
+               "lq_conv2d_i8: kernel, stride, padding or dilation do not fit the input");
+    if (padding_mode != LQ_PAD_ZEROS)
+        LQ_REQUIRE(pad_top < H && pad_bottom < H && pad_left < W && pad_right < W,
+                   "lq_conv2d_i8: reflect / replicate / circular padding must be smaller than the input");
+    if (N == 0) return LQ_OK;
+    const int64_t Cg = C / groups, Cout_g = Cout / groups;
+    const int64_t Cp = (Cg + 15) / 16 * 16;
+    const int64_t Hp = H + pad_top + pad_bottom, Wp = W + pad_left + pad_right;
+    const int64_t P = N * OH * OW;
+    const int64_t K = KH * KW * Cp;
+    LQ_REQUIRE(N * C * H * W < CV_MAX && N * Hp * Wp * groups * Cp < CV_MAX && P < CV_MAX && N * Cout * OH * OW < CV_MAX,
+               "lq_conv2d_i8: tensors above 2^31 elements are not supported");
+    LQ_REQUIRE(d_x && d_w_packed && d_w_scale && d_y, "lq_conv2d_i8: NULL pointer");
+    const bool has_za = d_a_zero_point != nullptr || x_code_type == LQ_U8S8;
+    LQ_REQUIRE(!has_za || d_w_sums, "lq_conv2d_i8: an activation zero point needs the weight sums d_w_sums");
+    LQ_REQUIRE(aligned16(d_w_packed) && aligned16(d_workspace), "lq_conv2d_i8: packed weights and workspace must be 16-byte aligned");
+    const size_t need = lq_conv2d_i8_workspace_size(N, C, H, W, groups, pad_top, pad_bottom, pad_left, pad_right);
+    LQ_REQUIRE(d_workspace && workspace_bytes >= need, "lq_conv2d_i8: workspace smaller than lq_conv2d_i8_workspace_size");
+    hipStream_t st = as_stream(stream);
+
+    PackArgs pa{};
+    pa.x = d_x;
+    pa.xp = static_cast<int8_t*>(d_workspace);
+    pa.N = (int)N; pa.C = (int)C; pa.H = (int)H; pa.W = (int)W; pa.G = (int)groups; pa.Cg = (int)Cg;
+    pa.Cp = (int)Cp; pa.Hp = (int)Hp; pa.Wp = (int)Wp; pa.pt = pad_top; pa.pl = pad_left;
+    pa.mode = padding_mode;
+    pa.a_zp = d_a_zero_point;
+    pa.a_u8s8 = x_code_type == LQ_U8S8;
+    const int64_t pchunks = N * Hp * Wp * groups * (Cp / 16);
+    hipLaunchKernelGGL(conv_pack_input_kernel, dim3((unsigned)((pchunks + 255) / 256)), dim3(256), 0, st, pa);
+
+    ConvArgs a{};
+    a.xp = pa.xp;
+    a.wp = d_w_packed;
+    a.y = d_y;
+    a.N = (int)N; a.Hp = (int)Hp; a.Wp = (int)Wp; a.G = (int)groups; a.Cp = (int)Cp; a.Cout_g = (int)Cout_g;
+    a.KH = (int)KH; a.KW = (int)KW; a.sh = stride_h; a.sw = stride_w; a.dh = dilation_h; a.dw = dilation_w;
+    a.OH = (int)OH; a.OW = (int)OW; a.K = (int)K; a.P = (int)P;
+    a.a_scale = d_a_scale;
+    a.a_zp = d_a_zero_point;
+    a.a_u8s8 = pa.a_u8s8;
+    a.w_scale = d_w_scale;
+    a.w_sums = d_w_sums;
+    a.bias = d_bias;
+    a.out_scale = d_out_scale;
+    a.out_zp = d_out_zero_point;
+    a.qmin = out_qmin;
+    a.qmax = out_qmax;
+    a.relu = (flags & LQ_EPI_RELU) ? 1 : 0;
+    const dim3 grid((unsigned)((P + CV_BM - 1) / CV_BM), (unsigned)((Cout_g + CV_BN - 1) / CV_BN), (unsigned)groups);
+    switch (out_kind) {
+        case LQ_OUT_I32: hipLaunchKernelGGL(conv_i8_kernel<LQ_OUT_I32>, grid, dim3(CV_THREADS), 0, st, a); break;
+        case LQ_OUT_F32: hipLaunchKernelGGL(conv_i8_kernel<LQ_OUT_F32>, grid, dim3(CV_THREADS), 0, st, a); break;
+        case LQ_OUT_F16: hipLaunchKernelGGL(conv_i8_kernel<LQ_OUT_F16>, grid, dim3(CV_THREADS), 0, st, a); break;
+        case LQ_OUT_Q8: hipLaunchKernelGGL(conv_i8_kernel<LQ_OUT_Q8>, grid, dim3(CV_THREADS), 0, st, a); break;
+        case LQ_OUT_QU8: hipLaunchKernelGGL(conv_i8_kernel<LQ_OUT_QU8>, grid, dim3(CV_THREADS), 0, st, a); break;
+        case LQ_OUT_FQ32: hipLaunchKernelGGL(conv_i8_kernel<LQ_OUT_FQ32>, grid, dim3(CV_THREADS), 0, st, a); break;
+        case LQ_OUT_Q16: hipLaunchKernelGGL(conv_i8_kernel<LQ_OUT_Q16>, grid, dim3(CV_THREADS), 0, st, a); break;
+        default: hipLaunchKernelGGL(conv_i8_kernel<LQ_OUT_QU8S8>, grid, dim3(CV_THREADS), 0, st, a); break;
+    }
+    return launch_status("lq_conv2d_i8");
+}
+
+int lq_conv2d_f32(const float* d_x, int64_t N, int64_t C, int64_t H, int64_t W, const float* d_w,
+                  const float* d_bias, int64_t Cout, int64_t KH, int64_t KW, int stride_h, int stride_w,
+                  int pad_top, int pad_bottom, int pad_left, int pad_right, int dilation_h, int dilation_w,
+                  int64_t groups, int padding_mode, float* d_y, void* stream) {
+    LQ_REQUIRE(N >= 0 && C >= 1 && H >= 1 && W >= 1 && Cout >= 1 && groups >= 1, "lq_conv2d_f32: bad shape");
+    LQ_REQUIRE(C % groups == 0 && Cout % groups == 0, "lq_conv2d_f32: channels must divide by groups");
+    LQ_REQUIRE(padding_mode >= LQ_PAD_ZEROS && padding_mode <= LQ_PAD_CIRCULAR, "lq_conv2d_f32: unknown padding mode");
+    int64_t OH = 0, OW = 0;
+    LQ_REQUIRE(conv_geometry(H, W, (int)KH, (int)KW, stride_h, stride_w, pad_top, pad_bottom, pad_left, pad_right,
+                             dilation_h, dilation_w, &OH, &OW),
+               "lq_conv2d_f32: kernel, stride, padding or dilation do not fit the input");
+    if (padding_mode != LQ_PAD_ZEROS)
+        LQ_REQUIRE(pad_top < H && pad_bottom < H && pad_left < W && pad_right < W,
+                   "lq_conv2d_f32: reflect / replicate / circular padding must be smaller than the input");
+    if (N == 0) return LQ_OK;
+    LQ_REQUIRE(d_x && d_w && d_y, "lq_conv2d_f32: NULL pointer");
+    LQ_REQUIRE(N * C * H * W < CV_MAX && N * Cout * OH * OW < CV_MAX, "lq_conv2d_f32: tensor too large");
+    FConvArgs a{d_x, d_w, d_bias, d_y, (int)N, (int)C, (int)H, (int)W, (int)Cout, (int)groups, (int)(C / groups),
+                (int)(Cout / groups), (int)KH, (int)KW, stride_h, stride_w, pad_top, pad_left, dilation_h, dilation_w,
+                (int)OH, (int)OW, padding_mode};
+    const int64_t total = N * Cout * OH * OW;
+    hipLaunchKernelGGL(conv_f32_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, as_stream(stream), a);
+    return launch_status("lq_conv2d_f32");
+}
+
+int lq_batch_norm_f32(const float* d_x, float* d_y, int64_t N, int64_t C, int64_t HW, const float* d_mean,
+                      const float* d_var, const float* d_gamma, const float* d_beta, float eps, void* stream) {
+    LQ_REQUIRE(N >= 0 && C >= 1 && HW >= 0 && N * C * HW < CV_MAX, "lq_batch_norm_f32: bad shape");
+    if (N * HW == 0) return LQ_OK;
+    LQ_REQUIRE(d_x && d_y && d_mean && d_var, "lq_batch_norm_f32: NULL pointer");
+    const int64_t total = N * C * HW;
+    hipLaunchKernelGGL(batch_norm_f32_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, as_stream(stream),
+                       d_x, d_y, N, (int)C, HW, d_mean, d_var, d_gamma, d_beta, eps);
+    return launch_status("lq_batch_norm_f32");
+}
+
+}  // extern "C"

@@ -1,0 +1,67 @@
+// lq_epilogue.h -- the fused W8A8 epilogue shared by the GEMM and the implicit-GEMM conv.
+//
+// From an exact int32 accumulator (zero points already corrected):
+//   y = fl32(fl32(float(acc) * fl32(sa * sb)) + bias), ReLU (y <= 0 -> +0), then the output
+//   kind: int32 / f32 / f16 / requantized codes c = clip(rne(y * fl32(1/S)) + Z) of an int8,
+//   uint8, int16 or uint8-as-int8 grid / fake-quantized f32 fl32((c - Z) * S).
+// Every float op is one IEEE binary32 operation (the translation units build with
+// -ffp-contract=off).
+#pragma once
+
+#include <hip/hip_fp16.h>
+
+#include "lq_internal.h"
+
+namespace lq {
+
+struct EpiParams {
+    int za;       // effective activation zero point in A's stored units
+    bool has_za;
+    float out_inv, out_s, out_z;
+    Grid g;
+};
+
+__device__ __forceinline__ float requant_code(float y, const EpiParams& p) {
+    float t = y * p.out_inv;
+    float r = rne(t);
+    float u = r + p.out_z;
+    return clip_grid(u, p.g);
+}
+
+// Epilogue value of one element, as the bits of the output element type.
+template <int KIND>
+__device__ __forceinline__ uint32_t epi_one(int32_t acc, float sa, float sb, const float* bias_p,
+                                            bool relu, const EpiParams& p) {
+    if (KIND == LQ_OUT_I32) return (uint32_t)acc;
+    float s = sa * sb;
+    float y = (float)acc * s;
+    if (bias_p) y = y + *bias_p;  // no add without a bias: -0 stays -0
+    if (relu) y = (y <= 0.0f) ? 0.0f : y;
+    if (KIND == LQ_OUT_F32) return __float_as_uint(y);
+    if (KIND == LQ_OUT_F16) return (uint32_t)__half_as_ushort(__float2half_rn(y));
+    float c = requant_code(y, p);
+    if (KIND == LQ_OUT_Q8) return (uint32_t)(uint8_t)CodeI8::store(c);
+    if (KIND == LQ_OUT_QU8) return (uint32_t)CodeU8::store(c);
+    if (KIND == LQ_OUT_Q16) return (uint32_t)(uint16_t)CodeI16::store(c);
+    if (KIND == LQ_OUT_QU8S8) return (uint32_t)(uint8_t)CodeU8S8::store(c);
+    // LQ_OUT_FQ32
+    float d = c - p.out_z;
+    return __float_as_uint(d * p.out_s);
+}
+
+template <int KIND>
+struct OutTraits {
+    static constexpr int bytes = (KIND == LQ_OUT_I32 || KIND == LQ_OUT_F32 || KIND == LQ_OUT_FQ32) ? 4
+                                 : (KIND == LQ_OUT_F16 || KIND == LQ_OUT_Q16)                        ? 2
+                                                                                                     : 1;
+};
+
+template <int KIND>
+__device__ __forceinline__ void store_elem(void* C, int64_t idx, uint32_t v) {
+    constexpr int b = OutTraits<KIND>::bytes;
+    if (b == 4) reinterpret_cast<uint32_t*>(C)[idx] = v;
+    else if (b == 2) reinterpret_cast<uint16_t*>(C)[idx] = (uint16_t)v;
+    else reinterpret_cast<uint8_t*>(C)[idx] = (uint8_t)v;
+}
+
+}  // namespace lq

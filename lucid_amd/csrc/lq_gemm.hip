@@ -23,6 +23,7 @@
 
 #include <type_traits>
 
+#include "lq_epilogue.h"
 #include "lq_internal.h"
 
 namespace lq {
@@ -56,13 +57,6 @@ struct GemmArgs {
 
 // ------------------------------------------------------------------ epilogue
 
-struct EpiParams {
-    int za;       // effective activation zero point in A's stored units
-    bool has_za;
-    float out_inv, out_s, out_z;
-    Grid g;
-};
-
 __device__ __forceinline__ EpiParams epi_params(const GemmArgs& a) {
     EpiParams p;
     p.za = (a.a_zp ? (int)a.a_zp[0] : 0) - (a.a_u8s8 ? 128 : 0);
@@ -88,49 +82,6 @@ __device__ __forceinline__ int32_t corrected(int32_t raw, int m, int n, const Ge
         acc += (uint32_t)a.K * (uint32_t)p.za * zb;
     }
     return (int32_t)acc;
-}
-
-__device__ __forceinline__ float requant_code(float y, const EpiParams& p) {
-    float t = y * p.out_inv;
-    float r = rne(t);
-    float u = r + p.out_z;
-    return clip_grid(u, p.g);
-}
-
-// Epilogue value of one element, as the bits of the output element type.
-template <int KIND>
-__device__ __forceinline__ uint32_t epi_one(int32_t acc, float sa, float sb, const float* bias_p,
-                                            bool relu, const EpiParams& p) {
-    if (KIND == LQ_OUT_I32) return (uint32_t)acc;
-    float s = sa * sb;
-    float y = (float)acc * s;
-    if (bias_p) y = y + *bias_p;  // no add without a bias: -0 stays -0
-    if (relu) y = (y <= 0.0f) ? 0.0f : y;
-    if (KIND == LQ_OUT_F32) return __float_as_uint(y);
-    if (KIND == LQ_OUT_F16) return (uint32_t)__half_as_ushort(__float2half_rn(y));
-    float c = requant_code(y, p);
-    if (KIND == LQ_OUT_Q8) return (uint32_t)(uint8_t)CodeI8::store(c);
-    if (KIND == LQ_OUT_QU8) return (uint32_t)CodeU8::store(c);
-    if (KIND == LQ_OUT_Q16) return (uint32_t)(uint16_t)CodeI16::store(c);
-    if (KIND == LQ_OUT_QU8S8) return (uint32_t)(uint8_t)CodeU8S8::store(c);
-    // LQ_OUT_FQ32
-    float d = c - p.out_z;
-    return __float_as_uint(d * p.out_s);
-}
-
-template <int KIND>
-struct OutTraits {
-    static constexpr int bytes = (KIND == LQ_OUT_I32 || KIND == LQ_OUT_F32 || KIND == LQ_OUT_FQ32) ? 4
-                                 : (KIND == LQ_OUT_F16 || KIND == LQ_OUT_Q16)                        ? 2
-                                                                                                     : 1;
-};
-
-template <int KIND>
-__device__ __forceinline__ void store_elem(void* C, int64_t idx, uint32_t v) {
-    constexpr int b = OutTraits<KIND>::bytes;
-    if (b == 4) reinterpret_cast<uint32_t*>(C)[idx] = v;
-    else if (b == 2) reinterpret_cast<uint16_t*>(C)[idx] = (uint16_t)v;
-    else reinterpret_cast<uint8_t*>(C)[idx] = (uint8_t)v;
 }
 
 // Epilogue inputs of the four consecutive columns n..n+3 a lane owns, loaded once.

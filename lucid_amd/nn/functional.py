@@ -52,9 +52,70 @@ def linear(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
     return y
 
 
-def conv2d(x, weight, bias=None, stride=(1, 1), padding=(0, 0), dilation=(1, 1), groups=1):
-    raise NotImplementedError("float conv2d forward is not implemented on the HIP backend yet")
+PADDING_MODES = {"zeros": 0, "reflect": 1, "replicate": 2, "circular": 3}
 
 
-def batch_norm_eval(x, running_mean, running_var, weight, bias, eps):
-    raise NotImplementedError("float batch_norm forward is not implemented on the HIP backend yet")
+def _pair(v) -> tuple[int, int]:
+    if isinstance(v, (tuple, list)):
+        return (int(v[0]), int(v[1])) if len(v) > 1 else (int(v[0]), int(v[0]))
+    return int(v), int(v)
+
+
+def conv_padding(padding, kernel: tuple[int, int], dilation: tuple[int, int]) -> tuple[int, int, int, int]:
+    """(top, bottom, left, right) of a conv padding: ints, or "valid" / "same" as Lucid resolves
+    them (total d * (k - 1), the smaller half before; lucid/nn/functional/_spatial_args.py:141-164)."""
+    if isinstance(padding, str):
+        if padding == "valid":
+            return 0, 0, 0, 0
+        if padding != "same":
+            raise ValueError(f"unknown padding {padding!r}")
+        th, tw = dilation[0] * (kernel[0] - 1), dilation[1] * (kernel[1] - 1)
+        return th // 2, th - th // 2, tw // 2, tw - tw // 2
+    ph, pw = _pair(padding)
+    if ph < 0 or pw < 0:
+        raise ValueError("conv2d: padding must be non-negative")
+    return ph, ph, pw, pw
+
+
+def conv2d(x: Tensor, weight: Tensor, bias: Tensor | None = None, stride=1, padding=0, dilation=1,
+           groups: int = 1, padding_mode: str = "zeros") -> Tensor:
+    """Float 2-D convolution of NCHW ``x`` (direct kernel, ``lq_conv2d_f32``)."""
+    import numpy as np
+
+    require_gpu(x, "conv2d")
+    if x.dtype != float32 or x.ndim != 4:
+        raise TypeError(f"conv2d: float32 NCHW input expected, got {x.dtype} {x.shape}")
+    w = on_device(weight)
+    b = on_device(bias) if bias is not None else None
+    N, C, H, W = x.shape
+    Cout, Cg, KH, KW = w.shape
+    if Cg * groups != C:
+        raise ValueError(f"conv2d: input has {C} channels, weight expects {Cg} x {groups} groups")
+    sh, sw = _pair(stride)
+    dh, dw = _pair(dilation)
+    pt, pb, pl, pr = conv_padding(padding, (KH, KW), (dh, dw))
+    OH = (H + pt + pb - dh * (KH - 1) - 1) // sh + 1
+    OW = (W + pl + pr - dw * (KW - 1) - 1) // sw + 1
+    if OH < 1 or OW < 1:
+        raise ValueError("conv2d: kernel larger than the padded input")
+    y = empty((N, Cout, OH, OW), np.float32, "gpu")
+    _C.call("lq_conv2d_f32", x.data_ptr(), N, C, H, W, w.data_ptr(),
+            b.data_ptr() if b is not None else None, Cout, KH, KW, sh, sw, pt, pb, pl, pr, dh, dw,
+            groups, PADDING_MODES[padding_mode], y.data_ptr(), None)
+    return y
+
+
+def batch_norm_eval(x: Tensor, running_mean: Tensor, running_var: Tensor, weight: Tensor | None,
+                    bias: Tensor | None, eps: float) -> Tensor:
+    """Eval BatchNorm over the channel axis 1: ``((x - mean) * (1 / sqrt(var + eps))) * w + b``."""
+    import numpy as np
+
+    require_gpu(x, "batch_norm")
+    N, C = x.shape[0], x.shape[1]
+    HW = x.numel() // max(N * C, 1)
+    y = empty(x.shape, np.float32, "gpu")
+    args = [on_device(t) if t is not None else None for t in (running_mean, running_var, weight, bias)]
+    _C.call("lq_batch_norm_f32", x.data_ptr(), y.data_ptr(), N, C, HW, args[0].data_ptr(),
+            args[1].data_ptr(), args[2].data_ptr() if args[2] is not None else None,
+            args[3].data_ptr() if args[3] is not None else None, float(np.float32(eps)), None)
+    return y

@@ -73,10 +73,10 @@ class Conv2d(Module):
         self.kernel_size = _pair(kernel_size)
         self.stride = _pair(stride)
         if isinstance(padding, str):
-            self.padding_str = padding
+            self._padding_str = padding
             self.padding = (0, 0)
         else:
-            self.padding_str = None
+            self._padding_str = None
             self.padding = _pair(padding)
         self.dilation = _pair(dilation)
         self.groups = groups
@@ -91,21 +91,12 @@ class Conv2d(Module):
             self.register_parameter("bias", None)
 
     def forward(self, x: Tensor) -> Tensor:
-        return F.conv2d(x, self.weight, self.bias, self.stride, self._resolved_padding(),
-                        self.dilation, self.groups)
-
-    def _resolved_padding(self) -> tuple[int, int]:
-        if self.padding_str is None or self.padding_str == "valid":
-            return self.padding
-        if self.padding_str == "same":
-            kh, kw = self.kernel_size
-            dh, dw = self.dilation
-            return ((dh * (kh - 1)) // 2, (dw * (kw - 1)) // 2)
-        raise ValueError(f"unknown padding {self.padding_str!r}")
+        return F.conv2d(x, self.weight, self.bias, self.stride, self._padding_str or self.padding,
+                        self.dilation, self.groups, self.padding_mode)
 
     def extra_repr(self) -> str:
         return (f"{self.in_channels}, {self.out_channels}, kernel_size={self.kernel_size}, "
-                f"stride={self.stride}, padding={self.padding_str or self.padding}")
+                f"stride={self.stride}, padding={self._padding_str or self.padding}")
 
 
 class ReLU(Module):

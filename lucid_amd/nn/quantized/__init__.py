@@ -6,13 +6,14 @@ MFMA GEMM over integer codes; ``QuantStub`` / ``DeQuantStub`` / ``Quantize`` /
 ``DeQuantize`` / ``QuantWrapper`` mark the quantized region.
 """
 
-from lucid_amd.nn.quantized.intrinsic import LinearReLU
+from lucid_amd.nn.quantized.conv import Conv2d
+from lucid_amd.nn.quantized.intrinsic import ConvReLU2d, LinearReLU
 from lucid_amd.nn.quantized.linear import Linear
 from lucid_amd.nn.quantized.mlx_linear import QuantizedLinearMLX
 from lucid_amd.nn.quantized.modules import (DeQuantize, DeQuantStub, Quantize, QuantStub,
                                             QuantWrapper)
 
-__all__ = ["Linear", "QuantizedLinearMLX", "LinearReLU", "QuantStub", "DeQuantStub", "Quantize", "DeQuantize",
+__all__ = ["Linear", "QuantizedLinearMLX", "Conv2d", "ConvReLU2d", "LinearReLU", "QuantStub", "DeQuantStub", "Quantize", "DeQuantize",
            "QuantWrapper"]
 
 

@@ -1,16 +1,17 @@
-"""Quantized fused blocks (lucid/nn/quantized/intrinsic.py:23-138): ``LinearReLU``.
+"""Quantized fused blocks (lucid/nn/quantized/intrinsic.py:23-341): ``LinearReLU``,
+``ConvReLU2d``.
 
-``LinearReLU`` is ``Linear`` with ReLU applied before the output grid; on the int8 path
-the ReLU runs in the GEMM epilogue (``y <= 0 -> +0`` before requantizing).  ``from_float``
-accepts the float fused block (an ``nn.Sequential`` of ``[linear, relu]``), whose
-``qconfig`` and observer move onto the inner Linear first (``_wire_inner``,
-intrinsic.py:23-37).
+Each is its base layer with ReLU applied before the output grid; on the int8 path the ReLU
+runs in the GEMM / conv epilogue (``y <= 0 -> +0`` before requantizing).  ``from_float``
+accepts the float fused block (an ``nn.Sequential`` of ``[layer, relu]``), whose ``qconfig``
+and observer move onto the inner layer first (``_wire_inner``, intrinsic.py:23-37).
 """
 
 from __future__ import annotations
 
 from lucid_amd.nn.layers import Sequential
 from lucid_amd.nn.module import Module
+from lucid_amd.nn.quantized.conv import Conv2d
 from lucid_amd.nn.quantized.linear import Linear
 
 
@@ -31,4 +32,14 @@ class LinearReLU(Linear):
 
     @classmethod
     def from_float(cls, mod: Module) -> "LinearReLU":
+        return super().from_float(_wire_inner(mod))
+
+
+class ConvReLU2d(Conv2d):
+    """Quantized Conv2d with a fused ReLU."""
+
+    _relu = True
+
+    @classmethod
+    def from_float(cls, mod: Module) -> "ConvReLU2d":
         return super().from_float(_wire_inner(mod))

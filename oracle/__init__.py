@@ -21,6 +21,11 @@ function                      follows (lucid-official/lucid)
 ``gemm_w8a8``                 build-defined integer contract (no reference counterpart):
                               exact int32 sum, then the epilogue documented in
                               include/lq_api.h; int32 core checked by brute force
+``conv2d_acc``                exact int64 brute force of the int8 conv sum (no reference
+                              counterpart); padding modes as nn/functional/conv.py:24-29,76-81
+``conv2d_f32``                float conv, per output sum over (c, kh, kw) in float32
+                              (backend/cpu/methods/Conv.cpp:271-360 computes it by im2col +
+                              sgemm: tolerance parity; bit-exact against the GPU's op order)
 ``gemv_w8``                   nn/quantized/linear.py:206-210 (dequantize -> F.linear) with
                               float64 accumulation (tolerance reference)
 ``group_*``                   quantization/_qgemm.py:84-97, 167-170 (MLX 0.32.3 internals:
@@ -96,6 +101,11 @@ def _declare(L: ctypes.CDLL) -> None:
     L.lqo_gemm_epilogue.argtypes = [_P, _I64, _I64, _P, _I64, _P, _I64, _P, _F, _F, _I, _I, _I, _I,
                                     _P, _I64]
     L.lqo_gemv_w8.argtypes = [_P, _I64, _I64, _P, _I64, _P, _P, _P, _I, _P]
+    L.lqo_conv2d_acc.argtypes = [_P, _I, _I, _I64, _I64, _I64, _I64, _P, _I64, _I64, _I64, _I, _I,
+                                 _I, _I, _I, _I, _I, _I, _I64, _I, _P]
+    L.lqo_conv2d_acc.restype = _I
+    L.lqo_conv2d_f32.argtypes = [_P, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I, _I, _I,
+                                 _I, _I, _I, _I, _I, _I64, _I, _P]
     L.lqo_group_quantize.argtypes = [_P, _I64, _I64, _I, _I, _P, _P, _P]
     L.lqo_group_dequantize.argtypes = [_P, _P, _P, _I64, _I64, _I, _I, _P]
     L.lqo_lucid_minmax.argtypes = [_P, _I64, _P, _P]
@@ -302,6 +312,45 @@ def gemv_w8(x, W, w_scale, w_zp=None, bias=None, relu=False) -> np.ndarray:
     y = np.empty((M, N), np.float64)
     lib().lqo_gemv_w8(_ptr(x), M, K, _ptr(W), N, _ptr(_f32(w_scale)), _ptr(zb),
                       _ptr(None if bias is None else _f32(bias)), int(relu), _ptr(y))
+    return y
+
+
+def conv_out_hw(H, W, KH, KW, stride, pad, dilation):
+    sh, sw = stride
+    pt, pb, pl, pr = pad
+    dh, dw = dilation
+    return ((H + pt + pb - dh * (KH - 1) - 1) // sh + 1, (W + pl + pr - dw * (KW - 1) - 1) // sw + 1)
+
+
+def conv2d_acc(x, w, za=0, x_u8s8=False, stride=(1, 1), pad=(0, 0, 0, 0), dilation=(1, 1),
+               groups=1, mode=0) -> np.ndarray:
+    """Exact int32 conv accumulators [N, Cout, OH, OW] of codes x [N, C, H, W] (stored int8)
+    and weight codes w [Cout, C/groups, KH, KW]; pad = (top, bottom, left, right)."""
+    x = np.ascontiguousarray(x, np.int8)
+    w = np.ascontiguousarray(w, np.int8)
+    N, C, H, W = x.shape
+    Cout, _, KH, KW = w.shape
+    OH, OW = conv_out_hw(H, W, KH, KW, stride, pad, dilation)
+    acc = np.empty((N, Cout, OH, OW), np.int32)
+    ovf = lib().lqo_conv2d_acc(_ptr(x), int(x_u8s8), int(za), N, C, H, W, _ptr(w), Cout, KH, KW,
+                               stride[0], stride[1], pad[0], pad[1], pad[2], pad[3], dilation[0],
+                               dilation[1], groups, mode, _ptr(acc))
+    if ovf:
+        raise OverflowError("int32 accumulator overflow")
+    return acc
+
+
+def conv2d_f32(x, w, bias=None, stride=(1, 1), pad=(0, 0, 0, 0), dilation=(1, 1), groups=1,
+               mode=0) -> np.ndarray:
+    x = _f32(x)
+    w = _f32(w)
+    N, C, H, W = x.shape
+    Cout, _, KH, KW = w.shape
+    OH, OW = conv_out_hw(H, W, KH, KW, stride, pad, dilation)
+    y = np.empty((N, Cout, OH, OW), np.float32)
+    lib().lqo_conv2d_f32(_ptr(x), N, C, H, W, _ptr(w), _ptr(None if bias is None else _f32(bias)),
+                         Cout, KH, KW, stride[0], stride[1], pad[0], pad[1], pad[2], pad[3],
+                         dilation[0], dilation[1], groups, mode, _ptr(y))
     return y
 
 

@@ -391,6 +391,94 @@ void lqo_gemv_w8(const float* x, int64_t M, int64_t K, const int8_t* W, int64_t 
     }
 }
 
+/* ------------------------------------------------------------ convolution */
+
+/* Source index of padded coordinate i for a padding mode (0 zeros, 1 reflect, 2 replicate,
+ * 3 circular; torch / Lucid pad semantics, lucid/nn/functional/conv.py:24-29,76-81), or -1
+ * for a zero-padded tap. */
+static int64_t lqo_pad_index(int64_t i, int64_t n, int mode) {
+    if (i >= 0 && i < n) return i;
+    if (mode == 1) {
+        if (n == 1) return 0;
+        int64_t j = i < 0 ? -i : i;
+        int64_t period = 2 * (n - 1);
+        j %= period;
+        return j < n ? j : period - j;
+    }
+    if (mode == 2) return i < 0 ? 0 : n - 1;
+    if (mode == 3) return ((i % n) + n) % n;
+    return -1;
+}
+
+/* Exact integer convolution of activation codes (stored int8; unsigned-grid codes held as
+ * c - 128 when x_u8s8) against weight codes, brute force in int64:
+ *   acc[n][co][oh][ow] = sum_{c, kh, kw} (code(x[n][g*Cg+c][h][w]) - za) * w[co][c][kh][kw]
+ * with (h, w) the padding-mode image of (oh*sh + kh*dh - pt, ow*sw + kw*dw - pl); a zero-padded
+ * tap contributes 0 (its value is the zero point).  Returns 1 if a sum leaves int32. */
+int lqo_conv2d_acc(const int8_t* x, int x_u8s8, int za, int64_t N, int64_t C, int64_t H, int64_t W,
+                   const int8_t* w, int64_t Cout, int64_t KH, int64_t KW, int sh, int sw, int pt, int pb,
+                   int pl, int pr, int dh, int dw, int64_t groups, int mode, int32_t* acc) {
+    int64_t OH = (H + pt + pb - (int64_t)dh * (KH - 1) - 1) / sh + 1;
+    int64_t OW = (W + pl + pr - (int64_t)dw * (KW - 1) - 1) / sw + 1;
+    int64_t Cg = C / groups, Cog = Cout / groups;
+    int ovf = 0;
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t co = 0; co < Cout; ++co) {
+            int64_t g = co / Cog;
+            for (int64_t oh = 0; oh < OH; ++oh)
+                for (int64_t ow = 0; ow < OW; ++ow) {
+                    int64_t s = 0;
+                    for (int64_t c = 0; c < Cg; ++c)
+                        for (int64_t kh = 0; kh < KH; ++kh) {
+                            int64_t h = lqo_pad_index(oh * sh + kh * dh - pt, H, mode);
+                            if (h < 0) continue;
+                            for (int64_t kw = 0; kw < KW; ++kw) {
+                                int64_t ww = lqo_pad_index(ow * sw + kw * dw - pl, W, mode);
+                                if (ww < 0) continue;
+                                int64_t code = x[((n * C + g * Cg + c) * H + h) * W + ww];
+                                if (x_u8s8) code += 128;
+                                s += (code - za) * (int64_t)w[((co * Cg + c) * KH + kh) * KW + kw];
+                            }
+                        }
+                    if (s > INT32_MAX || s < INT32_MIN) ovf = 1;
+                    acc[((n * Cout + co) * OH + oh) * OW + ow] = (int32_t)s;
+                }
+        }
+    return ovf;
+}
+
+/* Float convolution in the GPU kernel's op order: per output, sum over (c, kh, kw) in that
+ * order of fl32(x * w) added in float32 (no FMA), then + bias. */
+void lqo_conv2d_f32(const float* x, int64_t N, int64_t C, int64_t H, int64_t W, const float* w,
+                    const float* bias, int64_t Cout, int64_t KH, int64_t KW, int sh, int sw, int pt,
+                    int pb, int pl, int pr, int dh, int dw, int64_t groups, int mode, float* y) {
+    int64_t OH = (H + pt + pb - (int64_t)dh * (KH - 1) - 1) / sh + 1;
+    int64_t OW = (W + pl + pr - (int64_t)dw * (KW - 1) - 1) / sw + 1;
+    int64_t Cg = C / groups, Cog = Cout / groups;
+    for (int64_t n = 0; n < N; ++n)
+        for (int64_t co = 0; co < Cout; ++co) {
+            int64_t g = co / Cog;
+            for (int64_t oh = 0; oh < OH; ++oh)
+                for (int64_t ow = 0; ow < OW; ++ow) {
+                    float a = 0.0f;
+                    for (int64_t c = 0; c < Cg; ++c)
+                        for (int64_t kh = 0; kh < KH; ++kh) {
+                            int64_t h = lqo_pad_index(oh * sh + kh * dh - pt, H, mode);
+                            if (h < 0) continue;
+                            for (int64_t kw = 0; kw < KW; ++kw) {
+                                int64_t ww = lqo_pad_index(ow * sw + kw * dw - pl, W, mode);
+                                if (ww < 0) continue;
+                                float prod = x[((n * C + g * Cg + c) * H + h) * W + ww] *
+                                             w[((co * Cg + c) * KH + kh) * KW + kw];
+                                a = a + prod;
+                            }
+                        }
+                    if (bias) a = a + bias[co];
+                    y[((n * Cout + co) * OH + oh) * OW + ow] = a;
+                }
+        }
+}
+
 /* ------------------------------------------- group-wise (MLX-layout) weights */
 
 /* Group-wise affine quantize (formula _qgemm.py:84-97).  A group with max == min gets

@@ -275,3 +275,118 @@ def test_qint8_output_grid(gpu):
                         qmin=-128, qmax=127, out_kind=O.OUT_Q8)
     np.testing.assert_array_equal(y.quant_source.codes.numpy(), codes)
     np.testing.assert_array_equal(y.numpy(), O.dequantize(codes, O.I8, S, Z))
+
+
+# ------------------------------------------------------------------ convolution
+
+
+def _conv_stack(L, rng):
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized as nnq
+
+    conv1 = nn.Conv2d(3, 16, 3, padding=1)
+    bn = nn.BatchNorm2d(16)
+    bn.running_mean = L.tensor(rng.normal(0, 0.1, 16).astype(np.float32))
+    bn.running_var = L.tensor(rng.uniform(0.5, 1.5, 16).astype(np.float32))
+    bn.weight = nn.Parameter(L.tensor(rng.normal(1, 0.1, 16).astype(np.float32)))
+    bn.bias = nn.Parameter(L.tensor(rng.normal(0, 0.1, 16).astype(np.float32)))
+    conv2 = nn.Conv2d(16, 32, 3, stride=2, padding=1)
+    conv3 = nn.Conv2d(32, 24, 1, padding="same")
+    conv4 = nn.Conv2d(24, 24, 3, padding=1, padding_mode="reflect", groups=4)
+    return nn.Sequential(nnq.QuantStub(), conv1, bn, nn.ReLU(), conv2, nn.ReLU(), conv3, conv4,
+                         nnq.DeQuantStub()).eval()
+
+
+def _conv_pipeline(L, seed=3):
+    import lucid_amd.quantization as Q
+
+    rng = np.random.default_rng(seed)
+    model = _conv_stack(L, rng)
+    fused = Q.fuse_modules(model, [["1", "2", "3"], ["4", "5"]])
+    prepared = Q.prepare(fused.to("gpu"), Q.get_minmax_qconfig())
+    for _ in range(3):
+        prepared(L.tensor(rng.standard_normal((4, 3, 16, 16)).astype(np.float32), device="gpu"))
+    return rng, fused, Q.convert(prepared)
+
+
+def test_static_conv_stack_exact(gpu):
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized as nnq
+    from tests.test_gpu_conv import oracle_conv
+
+    rng, fused, q = _conv_pipeline(gpu)
+    assert [type(m) for m in q] == [nnq.Quantize, nnq.ConvReLU2d, nn.Identity, nn.Identity,
+                                    nnq.ConvReLU2d, nn.Identity, nnq.Conv2d, nnq.Conv2d,
+                                    nnq.DeQuantize]
+    assert q[7].padding_mode == "reflect" and q[6].padding_str == "same"
+    x = rng.standard_normal((2, 3, 16, 16)).astype(np.float32)
+    y = q(gpu.tensor(x, device="gpu"))
+    assert y.is_code_backed
+
+    s0, z0 = q[0].scale.numpy(), q[0].zero_point.numpy()
+    codes = O.quantize(x, O.recip_tensor(s0), z0, 0, 255, O.U8S8)
+    s_in, z_in = s0, z0
+    float_layers = (fused[1][0], fused[4][0], fused[6], fused[7])
+    for mod, fl, relu, pad, mode in ((q[1], float_layers[0], True, (1, 1, 1, 1), 0),
+                                     (q[4], float_layers[1], True, (1, 1, 1, 1), 0),
+                                     (q[6], float_layers[2], False, (0, 0, 0, 0), 0),
+                                     (q[7], float_layers[3], False, (1, 1, 1, 1), 1)):
+        W = fl.weight.numpy()
+        mn, mx = O.minmax_per_channel(W, 0)
+        sw, zw = O.calc_qparams(mn, mx, True, True, -128, 127)
+        qw = O.quantize(W, O.recip_tensor(sw), zw, -128, 127, O.I8, ch_axis=0)
+        np.testing.assert_array_equal(mod.weight_int8.numpy(), qw)
+        S, Z = mod.scale.numpy(), mod.zero_point.numpy()
+        codes = oracle_conv(codes, qw, u8s8=True, za=float(z_in), stride=mod.stride, pad=pad,
+                            dilation=mod.dilation, groups=mod.groups, mode=mode, a_scale=s_in,
+                            w_scale=sw, bias=fl.bias.numpy(), out_kind=O.OUT_QU8S8,
+                            out_scale=float(S), out_zp=float(Z), qmin=0, qmax=255, relu=relu)
+        s_in, z_in = S, Z
+    np.testing.assert_array_equal(y.quant_source.codes.numpy(), codes)
+    want = O.dequantize(codes, O.U8S8, s_in, z_in)
+    np.testing.assert_array_equal(y.numpy().view(np.uint32), want.view(np.uint32))
+
+
+def test_static_conv_vs_float_composition(gpu):
+    """First conv against Lucid's float composition (dequantized kernel, float conv, ReLU,
+    fake-quantize) from the same input codes: at most one code apart, rarely."""
+    rng, fused, q = _conv_pipeline(gpu)
+    x = rng.standard_normal((4, 3, 16, 16)).astype(np.float32)
+    h = q[1](q[0](gpu.tensor(x, device="gpu")))
+    got = h.quant_source.codes.numpy().astype(np.int32)
+    s0, z0 = q[0].scale.numpy(), q[0].zero_point.numpy()
+    c0 = O.quantize(x, O.recip_tensor(s0), z0, 0, 255, O.U8S8)
+    xd = O.dequantize(c0, O.U8S8, s0, z0)
+    W = q[1].weight_int8.numpy()
+    wd = O.dequantize(W, O.I8, q[1].weight_scale.numpy(), q[1].weight_zero_point.numpy(), ch_axis=0)
+    yf = O.conv2d_f32(xd, wd, q[1].bias.numpy(), pad=(1, 1, 1, 1))
+    yf = np.where(yf <= 0, np.float32(0), yf).astype(np.float32)
+    S, Z = q[1].scale.numpy(), q[1].zero_point.numpy()
+    lit = O.quantize(yf, O.recip_tensor(S), Z, 0, 255, O.U8S8).astype(np.int32)
+    diff = np.abs(got - lit)
+    assert diff.max() <= 1 and diff.mean() < 5e-3
+
+
+def test_conv_float_input_literal_path_and_state_dict(gpu):
+    import lucid_amd.nn.quantized as nnq
+
+    rng, fused, q = _conv_pipeline(gpu)
+    x = rng.standard_normal((2, 16, 8, 8)).astype(np.float32)
+    mod = q[4]
+    y = mod(gpu.tensor(x, device="gpu"))  # plain float input: literal path
+    W = mod.weight_int8.numpy()
+    wd = O.dequantize(W, O.I8, mod.weight_scale.numpy(), mod.weight_zero_point.numpy(), ch_axis=0)
+    yf = O.conv2d_f32(x, wd, mod.bias.numpy(), stride=(2, 2), pad=(1, 1, 1, 1))
+    yf = np.where(yf <= 0, np.float32(0), yf).astype(np.float32)
+    S, Z = mod.scale.numpy(), mod.zero_point.numpy()
+    want = O.quantize(yf, O.recip_tensor(S), Z, 0, 255, O.U8S8)
+    np.testing.assert_array_equal(y.quant_source.codes.numpy(), want)
+
+    sd = mod.state_dict()
+    assert list(sd) == ["weight_int8", "weight_scale", "weight_zero_point", "bias", "scale",
+                        "zero_point"]
+    fresh = nnq.ConvReLU2d(16, 32, 3, stride=2, padding=1)
+    fresh.load_state_dict(sd)
+    inp = q[0](gpu.tensor(rng.standard_normal((1, 3, 16, 16)).astype(np.float32), device="gpu"))
+    h = q[1](inp)
+    np.testing.assert_array_equal(fresh(h).numpy(), mod(h).numpy())

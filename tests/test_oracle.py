@@ -317,3 +317,88 @@ def test_group_constant_group_exact():
     w = np.full((2, 64), 0.375, np.float32)
     p, s, b = O.group_quantize(w, 64, 4)
     np.testing.assert_array_equal(O.group_dequantize(p, s, b, 64, 4), w)
+
+
+# ------------------------------------------------------------------ convolution
+
+
+def _im2col_conv_i64(xc, w, stride, dilation, groups):
+    """Independent formulation: sliding windows (numpy) + int64 matmul per group."""
+    from numpy.lib.stride_tricks import sliding_window_view
+
+    N, C, H, W = xc.shape
+    Cout, Cg, KH, KW = w.shape
+    eh, ew = dilation[0] * (KH - 1) + 1, dilation[1] * (KW - 1) + 1
+    win = sliding_window_view(xc, (eh, ew), axis=(2, 3))[:, :, ::stride[0], ::stride[1]]
+    win = win[..., ::dilation[0], ::dilation[1]]  # [N, C, OH, OW, KH, KW]
+    OH, OW = win.shape[2], win.shape[3]
+    out = np.zeros((N, Cout, OH, OW), np.int64)
+    Cog = Cout // groups
+    for g in range(groups):
+        cols = win[:, g * Cg:(g + 1) * Cg].transpose(0, 2, 3, 1, 4, 5).reshape(N * OH * OW, -1)
+        wg = w[g * Cog:(g + 1) * Cog].reshape(Cog, -1).astype(np.int64)
+        out[:, g * Cog:(g + 1) * Cog] = (cols.astype(np.int64) @ wg.T).reshape(N, OH, OW, Cog).transpose(0, 3, 1, 2)
+    return out
+
+
+def test_conv_acc_1x1_is_gemm(O):
+    rng = np.random.default_rng(1)
+    x = rng.integers(-128, 128, (2, 24, 5, 7)).astype(np.int8)
+    w = rng.integers(-128, 128, (10, 24, 1, 1)).astype(np.int8)
+    acc = O.conv2d_acc(x, w, za=-7)
+    A = x.transpose(0, 2, 3, 1).reshape(-1, 24)
+    want = O.gemm_acc(A, w.reshape(10, 24), za=-7)
+    np.testing.assert_array_equal(acc.transpose(0, 2, 3, 1).reshape(-1, 10), want)
+
+
+def test_conv_acc_delta_kernel_reproduces_input(O):
+    rng = np.random.default_rng(2)
+    x = rng.integers(-128, 128, (1, 3, 6, 5)).astype(np.int8)
+    w = np.zeros((3, 3, 3, 3), np.int8)
+    for c in range(3):
+        w[c, c, 1, 1] = 1
+    for u8s8, za in ((False, 5), (True, 131)):
+        acc = O.conv2d_acc(x, w, za=za, x_u8s8=u8s8, pad=(1, 1, 1, 1))
+        codes = x.astype(np.int64) + (128 if u8s8 else 0)
+        np.testing.assert_array_equal(acc, codes - za)
+
+
+@pytest.mark.parametrize("stride,dilation,groups", [((1, 1), (1, 1), 1), ((2, 1), (1, 2), 1),
+                                                    ((2, 2), (2, 2), 2), ((1, 3), (1, 1), 4)])
+def test_conv_acc_matches_windowed_matmul(O, stride, dilation, groups):
+    rng = np.random.default_rng(sum(stride) + groups)
+    x = rng.integers(-128, 128, (2, 8, 11, 13)).astype(np.int8)
+    w = rng.integers(-128, 128, (8, 8 // groups, 3, 2)).astype(np.int8)
+    acc = O.conv2d_acc(x, w, za=0, stride=stride, dilation=dilation, groups=groups)
+    np.testing.assert_array_equal(acc, _im2col_conv_i64(x, w, stride, dilation, groups))
+
+
+@pytest.mark.parametrize("mode,np_mode", [(1, "reflect"), (2, "edge"), (3, "wrap")])
+def test_conv_padding_modes_match_numpy_pad(O, mode, np_mode):
+    rng = np.random.default_rng(mode)
+    x = rng.integers(-128, 128, (1, 4, 6, 7)).astype(np.int8)
+    w = rng.integers(-128, 128, (5, 4, 3, 3)).astype(np.int8)
+    pad = (2, 1, 1, 2)
+    xp = np.pad(x, ((0, 0), (0, 0), (pad[0], pad[1]), (pad[2], pad[3])), mode=np_mode)
+    want = O.conv2d_acc(xp, w, za=0)
+    np.testing.assert_array_equal(O.conv2d_acc(x, w, za=0, pad=pad, mode=mode), want)
+    xf = x.astype(np.float32) * 0.5
+    np.testing.assert_array_equal(O.conv2d_f32(xf, w.astype(np.float32), pad=pad, mode=mode),
+                                  O.conv2d_f32(xp.astype(np.float32) * 0.5, w.astype(np.float32)))
+
+
+def test_conv_f32_against_float64(O):
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((2, 6, 9, 8)).astype(np.float32)
+    w = rng.standard_normal((4, 3, 3, 3)).astype(np.float32)
+    b = rng.standard_normal(4).astype(np.float32)
+    y = O.conv2d_f32(x, w, b, stride=(2, 1), pad=(1, 1, 0, 2), groups=2)
+    xp = np.pad(x.astype(np.float64), ((0, 0), (0, 0), (1, 1), (0, 2)))
+    ref = np.zeros(y.shape)
+    for g in range(2):
+        for co in range(2 * g, 2 * g + 2):
+            for oh in range(y.shape[2]):
+                for ow in range(y.shape[3]):
+                    patch = xp[:, 3 * g:3 * g + 3, 2 * oh:2 * oh + 3, ow:ow + 3]
+                    ref[:, co, oh, ow] = (patch * w[co].astype(np.float64)).sum(axis=(1, 2, 3)) + b[co]
+    np.testing.assert_allclose(y, ref, rtol=1e-5, atol=1e-5)
