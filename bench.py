@@ -270,6 +270,52 @@ def gemm_line(L, C, timer, gtimer, M, N, K, out_kind, steps, warmup):
             "frac": round(tops / bound_tops, 3)}
 
 
+RESNET18_CONVS = (  # (name, Cin, Cout, H, K, stride, pad) at batch 32
+    ("conv1 7x7/2", 3, 64, 224, 7, 2, 3),
+    ("layer1 3x3", 64, 64, 56, 3, 1, 1),
+    ("layer2 3x3/2", 64, 128, 56, 3, 2, 1),
+    ("layer2 3x3", 128, 128, 28, 3, 1, 1),
+    ("layer2 down 1x1/2", 64, 128, 56, 1, 2, 0),
+    ("layer3 3x3", 256, 256, 14, 3, 1, 1),
+    ("layer4 3x3", 512, 512, 7, 3, 1, 1),
+)
+
+
+def conv_lines(L, C, timer, steps, warmup, batch=32):
+    """The int8 implicit-GEMM conv on ResNet-18 layer shapes (uint8 activations, per-channel
+    int8 weights, requantize to uint8 after bias + ReLU); TOPS of the true (unpadded) MACs."""
+    out = []
+    rng = np.random.default_rng(5)
+    lib = C.lib()
+    for name, cin, cout, H, k, st, pd in RESNET18_CONVS:
+        x = L.tensor(rng.integers(-128, 128, (batch, cin, H, H)).astype(np.int8), device="gpu")
+        w = L.tensor(rng.integers(-127, 128, (cout, cin, k, k)).astype(np.int8), device="gpu")
+        wp = L.empty((lib.lq_conv2d_weight_pack_size(cout, cin, k, k),), np.int8, "gpu")
+        sums = L.empty((cout,), np.int32, "gpu")
+        C.call("lq_conv2d_pack_weights_i8", w.data_ptr(), cout, cin, k, k, wp.data_ptr(), sums.data_ptr(), None)
+        OH = (H + 2 * pd - k) // st + 1
+        y = L.empty((batch, cout, OH, OH), np.int8, "gpu")
+        sa = L.tensor(np.float32(0.02), device="gpu")
+        za = L.tensor(np.float32(128.0), device="gpu")
+        sw = L.tensor(rng.uniform(1e-3, 1e-2, cout).astype(np.float32), device="gpu")
+        b = L.tensor(rng.standard_normal(cout).astype(np.float32), device="gpu")
+        so = L.tensor(np.float32(0.05), device="gpu")
+        zo = L.tensor(np.float32(0.0), device="gpu")
+        ws_bytes = lib.lq_conv2d_i8_workspace_size(batch, cin, H, H, 1, pd, pd, pd, pd)
+        ws = L.empty((ws_bytes,), np.int8, "gpu")
+        args = (x.data_ptr(), C.U8S8, batch, cin, H, H, wp.data_ptr(), sums.data_ptr(), cout, k, k, st, st,
+                pd, pd, pd, pd, 1, 1, 1, 0, sa.data_ptr(), za.data_ptr(), sw.data_ptr(), b.data_ptr(),
+                so.data_ptr(), zo.data_ptr(), 0, 255, C.OUT_QU8S8, C.EPI_RELU, y.data_ptr(), ws.data_ptr(),
+                ws_bytes, None)
+        ms = timer.time_ms(lambda: C.check(lib.lq_conv2d_i8(*args), "lq_conv2d_i8"), steps, warmup)
+        ops = 2.0 * batch * OH * OH * cout * cin * k * k
+        tops = ops / (ms * 1e-3) / 1e12
+        out.append({"layer": name, "N": batch, "Cin": cin, "Cout": cout, "H": H, "k": k, "stride": st,
+                    "us": round(ms * 1e3, 1), "TOPS": round(tops, 1),
+                    "frac": round(tops / INT8_PEAK_TOPS, 3)})
+    return out
+
+
 def bandwidth_lines(L, C, timer, steps, warmup):
     """Observer / quantize / dequantize over 2^28 fp32 (1 GiB: larger than the 256 MB
     Infinity Cache, so every pass streams HBM)."""
@@ -422,6 +468,7 @@ def main() -> None:
             for kind in (C.OUT_Q8, C.OUT_F16):
                 comps["gemm_sweep"].append(gemm_line(L, C, timer, gtimer, m, n, k, kind, 20, 5))
         comps["weight_only_gemv"] = weight_only_lines(L, C, gtimer)
+        comps["conv_resnet18_b32"] = conv_lines(L, C, timer, 10, 3)
         comps.update(bandwidth_lines(L, C, timer, 50, 10))
         line["components"] = comps
     line["cpu_baseline"] = cpu_baseline(M, N, K, args.cpu_seconds)
