@@ -355,6 +355,69 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_tiled_kernel(G
         }
 }
 
+template <int BM, int BN, int WAVES_M, int WAVES_N>
+struct DmaTile {
+    static constexpr int BK = 128, CPR = 8, KS = 2, NBUF = 2;
+    static constexpr int NW = WAVES_M * WAVES_N;
+    static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+    static constexpr int FM = WM / 16, FN = WN / 16;
+    static constexpr int ROWS_PER_INSTR = 64 / CPR;
+    static constexpr int A_I = BM / ROWS_PER_INSTR / NW;
+    static constexpr int B_I = BN / ROWS_PER_INSTR / NW;
+    static constexpr int LPS = A_I + B_I;  // copy instructions per wave per stage
+    static constexpr int SB = (BM + BN) * BK;
+    static constexpr int LDS_BYTES = NBUF * SB;
+    static_assert(A_I * ROWS_PER_INSTR * NW == BM && B_I * ROWS_PER_INSTR * NW == BN, "copy split");
+    static_assert(WN == 64 && FN == 4, "each lane owns 16 consecutive output columns of a 64-column wave tile");
+    static_assert(WM % 32 == 0, "fragment swizzle parity");
+    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
+};
+
+// LDS slot of logical 16-byte K chunk c in stage row r (tile-local) is c ^ dma_swz(r).  Bits
+// 0-2 of the row spread the 16 lanes of an A fragment (rows r..r+15) over distinct 16-byte
+// bank groups; bit 4 of the row separates the rows 16 apart that one B fragment reads (its
+// rows are permuted, see below).
+__device__ __forceinline__ int dma_swz(int r) { return (r & 7) ^ ((r >> 2) & 4); }
+
+// Saturating float -> int32 conversion (v_cvt_i32_f32: out-of-range values clamp to the
+// int32 range, NaN converts to 0).
+__device__ __forceinline__ int32_t cvt_i32_sat(float v) {
+    int32_t r;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
+// Requantized codes of the integer output kinds, clamped first to the grid [qmin, qmax] and
+// then to the storage range; lo / hi fold the two clamps into one.  NaN becomes code 0 (the
+// saturating cast of Lucid's Factory.cpp:127-146) whatever the grid: cvt_i32_sat gives 0,
+// and nan_fix restores 0 when the clamp would move it.
+struct CodeClamp {
+    int lo, hi;
+    bool nan_fix;
+};
+
+template <int KIND>
+__device__ __forceinline__ CodeClamp code_clamp(const GemmArgs& a) {
+    int slo = -128, shi = 127;
+    if (KIND == LQ_OUT_QU8 || KIND == LQ_OUT_QU8S8) slo = 0, shi = 255;
+    if (KIND == LQ_OUT_Q16) slo = -32768, shi = 32767;
+    CodeClamp c;
+    c.lo = min(max(a.qmin, slo), shi);
+    c.hi = max(min(a.qmax, shi), slo);
+    c.nan_fix = !(c.lo <= 0 && 0 <= c.hi);
+    return c;
+}
+
+template <int KIND>
+__device__ __forceinline__ int32_t requant_int(float y, const EpiParams& p, const CodeClamp& cc) {
+    const float t = y * p.out_inv;
+    const float r = rne(t);
+    const float u = r + p.out_z;
+    int32_t c = min(max(cvt_i32_sat(u), cc.lo), cc.hi);
+    if (cc.nan_fix && u != u) c = 0;
+    return c;
+}
+
 // --------------------------------------------- LDS-DMA MFMA main loop (large M)
 //
 // The production path for M > 64 when K % 128 == 0.  Global -> LDS copies use the LDS-DMA
@@ -371,6 +434,13 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_tiled_kernel(G
 // the explicit vmcnt waits below are the synchronization.  Copies of stages past the end
 // are clamped to the last stage (a valid address, landing in a buffer never read again),
 // which keeps the steady-state loop free of branches.
+//
+// Output layout: B fragment i reads, in its lane row rho, the wave-tile row
+// (rho / 4) * 16 + 4 i + rho % 4.  The MFMA's output lane l, register r then holds column
+// 16 (l / 16) + 4 i + r, so over its four B fragments a lane owns 16 consecutive columns of
+// each of its rows: the epilogue works from registers and stores 16-byte row segments
+// (int8) directly, with no LDS round trip.  The per-column epilogue inputs are loaded
+// before the main loop (they are the oldest loads, so the stage waits cover them).
 
 // s_waitcnt vmcnt(N) only (lgkmcnt and expcnt fields at their no-wait maximum).
 template <int N>
@@ -409,31 +479,12 @@ __device__ __forceinline__ void lds_dma16(v4i rsrc, uint32_t voff, uint32_t soff
         : "memory", "m0");
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N>
-struct DmaTile {
-    static constexpr int BK = 128, CPR = 8, KS = 2, NBUF = 2;
-    static constexpr int NW = WAVES_M * WAVES_N;
-    static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
-    static constexpr int FM = WM / 16, FN = WN / 16;
-    static constexpr int ROWS_PER_INSTR = 64 / CPR;
-    static constexpr int A_I = BM / ROWS_PER_INSTR / NW;
-    static constexpr int B_I = BN / ROWS_PER_INSTR / NW;
-    static constexpr int LPS = A_I + B_I;  // copy instructions per wave per stage
-    static constexpr int SB = (BM + BN) * BK;
-    // epilogue staging: each wave's WM x WN int32 tile, rows padded by 16 bytes
-    static constexpr int EPI_STRIDE = WN * 4 + 16;
-    static constexpr int EPI_BYTES = NW * WM * EPI_STRIDE;
-    static constexpr int LDS_BYTES = (NBUF * SB > EPI_BYTES) ? NBUF * SB : EPI_BYTES;
-    static_assert(A_I * ROWS_PER_INSTR * NW == BM && B_I * ROWS_PER_INSTR * NW == BN, "copy split");
-    static_assert(WN % 64 == 0, "epilogue writes 64-column row segments");
-    static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
-};
-
 template <int BM, int BN, int WAVES_M, int WAVES_N, int KIND>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_dma_kernel(GemmArgs a) {
     typedef DmaTile<BM, BN, WAVES_M, WAVES_N> P;
-    constexpr int BK = P::BK, NW = P::NW, WM = P::WM, WN = P::WN, FM = P::FM, FN = P::FN;
+    constexpr int BK = P::BK, NW = P::NW, WM = P::WM, FM = P::FM, FN = P::FN;
     constexpr int RPI = P::ROWS_PER_INSTR, A_I = P::A_I, B_I = P::B_I, SB = P::SB;
+    constexpr bool INT_CODES = KIND == LQ_OUT_Q8 || KIND == LQ_OUT_QU8 || KIND == LQ_OUT_Q16 || KIND == LQ_OUT_QU8S8;
     __shared__ __attribute__((aligned(1024))) int8_t lds[P::LDS_BYTES];
 
     const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
@@ -445,18 +496,43 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_dma_kernel(Gem
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int nk = a.K / BK;
 
+    // Epilogue inputs first: this lane's 16 columns and FM rows.
+    const EpiParams p = epi_params(a);
+    const int nc0 = n0 + wn * 64 + (lane >> 4) * 16;
+    const int mr0 = m0 + wm * WM + (lane & 15);
+    float csb[16], cbias[16];
+    int32_t czab[16];  // za * bsum[n]
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const int nn = min(nc0 + q, a.N - 1);  // clamped: out-of-range columns are never stored
+        csb[q] = a.b_scale ? a.b_scale[(int64_t)nn * a.b_stride] : 1.0f;
+        cbias[q] = a.bias ? a.bias[nn] : 0.0f;
+        czab[q] = p.has_za ? (int32_t)((uint32_t)p.za * (uint32_t)a.b_sums[nn]) : 0;
+    }
+    float rsa[FM];
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+        const int mm = min(mr0 + j * 16, a.M - 1);
+        rsa[j] = a.a_scale ? a.a_scale[(int64_t)mm * a.a_stride] : 1.0f;
+    }
+
     const v4i ra = buffer_rsrc(a.A, (uint32_t)((int64_t)a.M * a.lda));
     const v4i rb = buffer_rsrc(a.B, (uint32_t)((int64_t)a.N * a.ldb));
-    // Lane l of a copy moves chunk p = l % 8 of row l / 8 of its 8-row block: the global
-    // chunk p ^ (row & 7), so LDS holds logical chunk c at slot c ^ (row & 7).
+    // Lane l of a copy moves chunk slot l % 8 of row l / 8 of its 8-row block: the global
+    // chunk (l % 8) ^ dma_swz(row).
     uint32_t a_off[A_I], b_off[B_I];
     {
-        const int rl = lane >> 3;
-        const int cb = ((lane & 7) ^ rl) * 16;
+        const int rl = lane >> 3, slot = lane & 7;
 #pragma unroll
-        for (int j = 0; j < A_I; ++j) a_off[j] = (uint32_t)(m0 + (j * NW + wave) * RPI + rl) * (uint32_t)a.lda + cb;
+        for (int j = 0; j < A_I; ++j) {
+            const int r = (j * NW + wave) * RPI + rl;
+            a_off[j] = (uint32_t)(m0 + r) * (uint32_t)a.lda + (uint32_t)((slot ^ dma_swz(r)) * 16);
+        }
 #pragma unroll
-        for (int j = 0; j < B_I; ++j) b_off[j] = (uint32_t)(n0 + (j * NW + wave) * RPI + rl) * (uint32_t)a.ldb + cb;
+        for (int j = 0; j < B_I; ++j) {
+            const int r = (j * NW + wave) * RPI + rl;
+            b_off[j] = (uint32_t)(n0 + r) * (uint32_t)a.ldb + (uint32_t)((slot ^ dma_swz(r)) * 16);
+        }
     }
     const uint32_t lds_base = (uint32_t)reinterpret_cast<uintptr_t>(lds);
     auto issue = [&](int buf, int kt) __attribute__((always_inline)) {
@@ -467,17 +543,24 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_dma_kernel(Gem
 #pragma unroll
         for (int j = 0; j < B_I; ++j) lds_dma16(rb, b_off[j], k0, sb + BM * BK + (j * NW + wave) * RPI * BK);
     };
-    const int a_frag0 = (wm * WM + (lane & 15)) * BK;
-    const int b_frag0 = BM * BK + (wn * WN + (lane & 15)) * BK;
-    const int fsw = lane & 7;
+    // Fragment addresses.  A fragment j: rows wm*WM + 16 j + rho, rho = lane % 16; B fragment i:
+    // rows wn*64 + (rho / 4) * 16 + 4 i + rho % 4.  Logical chunk of K step s: 4 s + lane / 16.
+    // The swizzle of an A row depends on rho and the parity of j, that of a B row on rho and
+    // the parity of i; the K step flips chunk bit 2.  So two base offsets per operand, with
+    // bit 6 (chunk bit 2) toggled by s ^ parity.
+    const int rho = lane & 15, c0 = lane >> 4;
+    const int a_base = (wm * WM + rho) * BK + ((c0 ^ (rho & 7)) << 4);
+    const int b_row = wn * 64 + (rho >> 2) * 16 + (rho & 3);
+    const int b_base = BM * BK + b_row * BK + ((c0 ^ dma_swz(b_row)) << 4);
     v4i F0[FM + FN], F1[FM + FN];
     auto read_frags = [&](v4i* f, int buf, int s) __attribute__((always_inline)) {
         const int8_t* sbuf = lds + buf * SB;
-        const int off = ((s * 4 + (lane >> 4)) ^ fsw) << 4;
 #pragma unroll
-        for (int j = 0; j < FM; ++j) f[j] = *reinterpret_cast<const v4i*>(sbuf + a_frag0 + j * 16 * BK + off);
+        for (int j = 0; j < FM; ++j)
+            f[j] = *reinterpret_cast<const v4i*>(sbuf + (a_base ^ (((s ^ j) & 1) << 6)) + j * 16 * BK);
 #pragma unroll
-        for (int i = 0; i < FN; ++i) f[FM + i] = *reinterpret_cast<const v4i*>(sbuf + b_frag0 + i * 16 * BK + off);
+        for (int i = 0; i < FN; ++i)
+            f[FM + i] = *reinterpret_cast<const v4i*>(sbuf + (b_base ^ (((s ^ i) & 1) << 6)) + i * 4 * BK);
     };
     v4i acc[FN][FM];
 #pragma unroll
@@ -519,32 +602,97 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_dma_kernel(Gem
         stage(std::integral_constant<int, 0>(), kt, kt + 1 == nk);
         if (kt + 1 < nk) stage(std::integral_constant<int, 1>(), kt + 1, true);
     }
-    // Epilogue through LDS: every copy has landed and every wave is done with the stage
-    // buffers before they are reused.  Each wave stages its own WM x WN tile and reads it
-    // back as 64-column row segments, so stores are contiguous along n.
-    wait_vmcnt<0>();
-    block_barrier();
-    constexpr int ES = P::EPI_STRIDE;
-    int8_t* stile = lds + wave * WM * ES;
+    wait_vmcnt<0>();  // no copy may still target LDS when the workgroup ends
+
+    // Epilogue from registers: acc[i][j][r] is C[mr0 + 16 j][nc0 + 4 i + r].  Every lane
+    // computes (rows past M hold zeros), so the cross-lane exchange below sees whole rows;
+    // only the stores are guarded.
+    constexpr int OB = OutTraits<KIND>::bytes;
+    const bool vec = (reinterpret_cast<uintptr_t>(a.C) % 16 == 0) && ((a.ldc * OB) % 16 == 0) &&
+                     (n0 + wn * 64 + 64 <= a.N);
+    CodeClamp cc{};
+    if (INT_CODES) cc = code_clamp<KIND>(a);
+    const bool has_bias = a.bias != nullptr, relu = a.relu != 0;
 #pragma unroll
-    for (int i = 0; i < FN; ++i)
+    for (int j = 0; j < FM; ++j) {
+        const int m = mr0 + j * 16;
+        int32_t asum = 0;
+        if (a.b_zp) asum = a.a_sums[min(m, a.M - 1)];
+        uint32_t out[16];
 #pragma unroll
-        for (int j = 0; j < FM; ++j)
-            *reinterpret_cast<v4i*>(stile + (j * 16 + (lane & 15)) * ES + (i * 16 + (lane >> 4) * 4) * 4) = acc[i][j];
-    const EpiParams p = epi_params(a);
-    // Lane l owns columns (l % 16) * 4 .. +3 of each 64-column segment and rows l / 16 + 4 i:
-    // its column parameters are loaded once per segment, its WM / 4 row parameters up front.
-    RowCtx rows[WM / 4];
+        for (int q = 0; q < 16; ++q) {
+            uint32_t accu = (uint32_t)acc[q >> 2][j][q & 3] - (uint32_t)czab[q];
+            if (a.b_zp) {  // weight zero points (rare): per-column terms read here
+                const int nn = min(nc0 + q, a.N - 1);
+                const uint32_t zb = (uint32_t)(int)a.b_zp[nn];
+                accu -= zb * (uint32_t)asum;
+                accu += (uint32_t)a.K * (uint32_t)p.za * zb;
+            }
+            if (INT_CODES) {
+                const float s = rsa[j] * csb[q];
+                float y = (float)(int32_t)accu * s;
+                if (has_bias) y = y + cbias[q];
+                if (relu) y = (y <= 0.0f) ? 0.0f : y;
+                out[q] = (uint32_t)requant_int<KIND>(y, p, cc);
+            } else {
+                out[q] = epi_one<KIND>((int32_t)accu, rsa[j], csb[q], has_bias ? &cbias[q] : nullptr, relu, p);
+            }
+        }
+        const bool row_ok = m < a.M;
+        if (vec) {
+            if (OB == 1) {
+                v4i w;
 #pragma unroll
-    for (int i = 0; i < WM / 4; ++i) rows[i] = load_row(a, m0 + wm * WM + i * 4 + (lane >> 4));
-    for (int seg = 0; seg < WN / 64; ++seg) {
-        const int cc = seg * 64 + (lane & 15) * 4;
-        const ColCtx cols = load_cols<KIND>(a, n0 + wn * WN + cc);
+                for (int d = 0; d < 4; ++d)
+                    w[d] = (int)((out[4 * d] & 0xffu) | ((out[4 * d + 1] & 0xffu) << 8) |
+                                 ((out[4 * d + 2] & 0xffu) << 16) | (out[4 * d + 3] << 24));
+                if (KIND == LQ_OUT_QU8S8) w ^= v4i{(int)0x80808080, (int)0x80808080, (int)0x80808080, (int)0x80808080};
+                if (row_ok) *reinterpret_cast<v4i*>(reinterpret_cast<uint8_t*>(a.C) + (int64_t)m * a.ldc + nc0) = w;
+            } else if (OB == 2) {
 #pragma unroll
-        for (int i = 0; i < WM / 4; ++i) {
-            const int rr = i * 4 + (lane >> 4);
-            const v4i raw = *reinterpret_cast<const v4i*>(stile + rr * ES + cc * 4);
-            epilogue4c<KIND>(a, p, rows[i], cols, m0 + wm * WM + rr, raw);
+                for (int h = 0; h < 2; ++h) {
+                    v4i w;
+#pragma unroll
+                    for (int d = 0; d < 4; ++d)
+                        w[d] = (int)((out[8 * h + 2 * d] & 0xffffu) | (out[8 * h + 2 * d + 1] << 16));
+                    if (row_ok)
+                        *reinterpret_cast<v4i*>(reinterpret_cast<uint16_t*>(a.C) + (int64_t)m * a.ldc + nc0 + 8 * h) = w;
+                }
+            } else {
+                // 4-byte outputs: lane group g = lane / 16 holds 16-byte pieces h = 0..3 of
+                // columns 16 g + 4 h.  A 4x4 transpose across (g, h) -- permlane32 swaps of
+                // pieces (0,2), (1,3), then permlane16 swaps of (0,1), (2,3), all among lanes
+                // of the same row -- leaves piece (h, g) in lane group g, register h, so
+                // store h covers 64 contiguous bytes of the row.
+                uint32_t v[4][4];
+#pragma unroll
+                for (int h = 0; h < 4; ++h)
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) v[h][d] = out[4 * h + d];
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    auto s02 = __builtin_amdgcn_permlane32_swap(v[0][d], v[2][d], false, false);
+                    auto s13 = __builtin_amdgcn_permlane32_swap(v[1][d], v[3][d], false, false);
+                    v[0][d] = s02[0], v[2][d] = s02[1], v[1][d] = s13[0], v[3][d] = s13[1];
+                    auto s01 = __builtin_amdgcn_permlane16_swap(v[0][d], v[1][d], false, false);
+                    auto s23 = __builtin_amdgcn_permlane16_swap(v[2][d], v[3][d], false, false);
+                    v[0][d] = s01[0], v[1][d] = s01[1], v[2][d] = s23[0], v[3][d] = s23[1];
+                }
+                const int64_t rb0 = (int64_t)m * a.ldc + n0 + wn * 64 + (lane >> 4) * 4;
+#pragma unroll
+                for (int h = 0; h < 4; ++h)
+                    if (row_ok)
+                        *reinterpret_cast<v4i*>(reinterpret_cast<uint32_t*>(a.C) + rb0 + 16 * h) =
+                            v4i{(int)v[h][0], (int)v[h][1], (int)v[h][2], (int)v[h][3]};
+            }
+        } else if (row_ok) {
+            const int64_t base = (int64_t)m * a.ldc + nc0;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                uint32_t v = out[q];
+                if (KIND == LQ_OUT_QU8S8) v ^= 0x80u;
+                if (nc0 + q < a.N) store_elem<KIND>(a.C, base + q, v);
+            }
         }
     }
 }

@@ -281,7 +281,7 @@ int lq_graph_end_capture(void* stream, void** graph_exec) {
     LQ_HIP(hipStreamEndCapture((hipStream_t)stream, &g));
     hipGraphExec_t e = nullptr;
     const hipError_t err = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
-    hipGraphDestroy(g);
+    (void)hipGraphDestroy(g);  // the executable graph keeps what it needs
     if (err != hipSuccess) return check_hip(err, "hipGraphInstantiate");
     *graph_exec = (void*)e;
     return LQ_OK;
