@@ -252,7 +252,7 @@ __global__ __launch_bounds__(CV_THREADS) void conv_i8_kernel(ConvArgs a) {
     ep.out_s = a.out_scale ? a.out_scale[0] : 1.0f;
     ep.out_inv = 1.0f / ep.out_s;
     ep.out_z = a.out_zp ? a.out_zp[0] : 0.0f;
-    ep.g = Grid{(float)a.qmin, (float)a.qmax, a.qmin == 0, false};
+    ep.g = make_grid(a.qmin, a.qmax);
     const float sa = a.a_scale ? a.a_scale[0] : 1.0f;
     const int OHW = a.OH * a.OW;
     const int Cout = a.G * a.Cout_g;

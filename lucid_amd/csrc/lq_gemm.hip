@@ -379,14 +379,6 @@ struct DmaTile {
 // rows are permuted, see below).
 __device__ __forceinline__ int dma_swz(int r) { return (r & 7) ^ ((r >> 2) & 4); }
 
-// Saturating float -> int32 conversion (v_cvt_i32_f32: out-of-range values clamp to the
-// int32 range, NaN converts to 0).
-__device__ __forceinline__ int32_t cvt_i32_sat(float v) {
-    int32_t r;
-    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(v));
-    return r;
-}
-
 // Requantized codes of the integer output kinds, clamped first to the grid [qmin, qmax] and
 // then to the storage range; lo / hi fold the two clamps into one.  NaN becomes code 0 (the
 // saturating cast of Lucid's Factory.cpp:127-146) whatever the grid: cvt_i32_sat gives 0,

@@ -59,14 +59,17 @@ __device__ __forceinline__ float clip_tie(float v, float lo, float hi, bool lo_t
 struct Grid {
     float lo, hi;
     bool lo_ties, hi_ties;
+    int qlo, qhi;  // the same bounds as integers
 };
 
-inline Grid make_grid(int qmin, int qmax) {
+__host__ __device__ inline Grid make_grid(int qmin, int qmax) {
     Grid g;
     g.lo = (float)qmin;
     g.hi = (float)qmax;
     g.lo_ties = (qmin == 0);  // a +0 floor
     g.hi_ties = false;        // an integer cap is never -0
+    g.qlo = qmin;
+    g.qhi = qmax;
     return g;
 }
 
@@ -86,16 +89,22 @@ __device__ __forceinline__ T satcast(float v, float lo, float hi, int lo_i, int 
 // Code storage types.  store(c) writes the clipped float code c.
 struct CodeI8 {
     typedef int8_t T;
+    static constexpr int kLo = -128, kHi = 127;
+    static __device__ __forceinline__ T from_int(int c) { return (T)c; }
     static __device__ __forceinline__ T store(float c) { return satcast<int8_t>(c, -128.f, 127.f, -128, 127); }
     static __device__ __forceinline__ float load(T v) { return (float)v; }
 };
 struct CodeU8 {
     typedef uint8_t T;
+    static constexpr int kLo = 0, kHi = 255;
+    static __device__ __forceinline__ T from_int(int c) { return (T)c; }
     static __device__ __forceinline__ T store(float c) { return satcast<uint8_t>(c, 0.f, 255.f, 0, 255); }
     static __device__ __forceinline__ float load(T v) { return (float)v; }
 };
 struct CodeI16 {
     typedef int16_t T;
+    static constexpr int kLo = -32768, kHi = 32767;
+    static __device__ __forceinline__ T from_int(int c) { return (T)c; }
     static __device__ __forceinline__ T store(float c) {
         return satcast<int16_t>(c, -32768.f, 32767.f, -32768, 32767);
     }
@@ -103,6 +112,8 @@ struct CodeI16 {
 };
 struct CodeI32 {
     typedef int32_t T;
+    static constexpr int kLo = INT32_MIN, kHi = INT32_MAX;
+    static __device__ __forceinline__ T from_int(int c) { return (T)c; }
     static __device__ __forceinline__ T store(float c) {
         if (c != c) return 0;
         if (c <= -2147483648.f) return INT32_MIN;
@@ -114,11 +125,36 @@ struct CodeI32 {
 // Unsigned-grid code c kept as int8 (c - 128): the signed MFMA operand form.
 struct CodeU8S8 {
     typedef int8_t T;
+    static constexpr int kLo = 0, kHi = 255;
+    static __device__ __forceinline__ T from_int(int c) { return (T)(c - 128); }
     static __device__ __forceinline__ T store(float c) {
         return (int8_t)((int)satcast<uint8_t>(c, 0.f, 255.f, 0, 255) - 128);
     }
     static __device__ __forceinline__ float load(T v) { return (float)((int)v + 128); }
 };
+
+// Saturating float -> int32 conversion (v_cvt_i32_f32: truncates toward zero, out-of-range
+// values clamp to the int32 range, NaN converts to 0).
+__device__ __forceinline__ int32_t cvt_i32_sat(float v) {
+    int32_t r;
+    asm("v_cvt_i32_f32 %0, %1" : "=v"(r) : "v"(v));
+    return r;
+}
+
+// Stored code of x quantized onto grid g: Code::store(clip_grid(rne(x * inv) + z, g)),
+// computed in the integer domain.  The two agree for every input: the signed-zero tie rule
+// of clip_grid cannot change an integer code, truncating then clamping to integer bounds
+// equals clamping then truncating, infinities and out-of-range values saturate in both, and
+// NaN stores 0 in both (the nan_fix select restores 0 when the grid excludes it).
+template <class Code>
+__device__ __forceinline__ typename Code::T quant_store(float x, float inv, float z, const Grid& g) {
+    const float u = rne(x * inv) + z;
+    const int lo = min(max(g.qlo, Code::kLo), Code::kHi);
+    const int hi = max(min(g.qhi, Code::kHi), Code::kLo);
+    int c = min(max(cvt_i32_sat(u), lo), hi);
+    if (!(lo <= 0 && 0 <= hi) && u != u) c = 0;
+    return Code::from_int(c);
+}
 
 // Order-preserving int32 key of a float: integer order of keys is the float order with
 // -0 below +0; a NaN with the sign bit clear keys above +inf, one with it set below -inf.

@@ -678,19 +678,22 @@ __global__ __launch_bounds__(kBlock) void quantize_g4_kernel(const float* __rest
         for (int j = 0; j < 4; ++j) {
             float inv, s, z;
             group_params<MODE>(qa, gi * 4, j, t_inv, t_s, t_z, inv, s, z);
-            o.v[j] = Code::store(quant_one<Code>(v[j], inv, z, g));
+            o.v[j] = quant_store<Code>(v[j], inv, z, g);
         }
         q4[gi] = o.raw;
     };
     // Streaming reads bypass the caches (nontemporal); the 4x smaller code stores do not.
+    // Eight groups in flight per lane: the per-element rounding and clipping would otherwise
+    // leave too few loads outstanding to cover HBM latency.
+    constexpr int U = 2 * kGrpUnroll;
     const BlockRun r = block_run(ng);
     uint32_t i = r.i;
-    for (; i + (kGrpUnroll - 1) * kBlock < r.end; i += kGrpUnroll * kBlock) {
-        vf4 v[kGrpUnroll];
+    for (; i + (U - 1) * kBlock < r.end; i += U * kBlock) {
+        vf4 v[U];
 #pragma unroll
-        for (int u = 0; u < kGrpUnroll; ++u) v[u] = __builtin_nontemporal_load(&x4[i + u * kBlock]);
+        for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(&x4[i + u * kBlock]);
 #pragma unroll
-        for (int u = 0; u < kGrpUnroll; ++u) one(i + u * kBlock, v[u]);
+        for (int u = 0; u < U; ++u) one(i + u * kBlock, v[u]);
     }
     for (; i < r.end; i += kBlock) one(i, __builtin_nontemporal_load(&x4[i]));
     if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {

@@ -89,6 +89,31 @@ def test_quantize_edge_values(gpu):
                                                     qd.quant_max, code))
 
 
+@pytest.mark.parametrize("code,qmin,qmax,z", [(O.I8, -128, 127, 5.0), (O.U8, 10, 200, 0.5),
+                                               (O.U8, 0, 255, 128.0), (O.I16, -128, 127, -3.0),
+                                               (O.I32, -1000, 1000, 0.0), (O.U8S8, 0, 255, 128.0),
+                                               (O.I8, -300, 300, 0.0)])
+def test_quantize_streaming_edges(gpu, code, qmin, qmax, z):
+    # The streaming kernel's integer-domain store against the oracle's clip-then-cast, over
+    # a tensor large enough to run every block: NaN, infinities, huge values, signed zeros,
+    # ties, a grid without 0 (NaN must still store 0), a non-integer zero point and a grid
+    # wider than the storage type.
+    rng = np.random.default_rng(qmin + qmax + code)
+    n = (1 << 20) + 3
+    x = (rng.standard_normal(n) * 200).astype(np.float32)
+    idx = rng.choice(n, 4000, replace=False)
+    x[idx] = rng.choice(np.array([np.nan, np.inf, -np.inf, 1e30, -1e30, 0.0, -0.0, 0.5, -0.5,
+                                  2.5, -2.5, 1e9, -1e9], np.float32), 4000)
+    from lucid_amd import _C
+    npdt = {O.I8: np.int8, O.U8: np.uint8, O.I16: np.int16, O.I32: np.int32, O.U8S8: np.int8}[code]
+    xt = gpu.tensor(x, device="gpu")
+    out = gpu.tensor(np.zeros(n, npdt), device="gpu")
+    inv = float(O.recip_scalar(0.37))
+    _C.call("lq_quantize_per_tensor_f32", xt.data_ptr(), out.data_ptr(), n, code, None, None,
+            inv, z, qmin, qmax, None)
+    np.testing.assert_array_equal(out.numpy(), O.quantize(x, O.recip_scalar(0.37), z, qmin, qmax, code))
+
+
 @pytest.mark.parametrize("shape,axis", [((48, 64), 0), ((48, 64), 1), ((4096, 256), 0),
                                         ((3, 40, 33), 1), ((64, 256), 1), ((2, 5, 32), 2),
                                         ((256, 784), 0)])
