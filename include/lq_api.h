@@ -133,6 +133,24 @@ int lq_minmax_per_channel_f32(const float* d_x, int64_t outer, int64_t C, int64_
                               float ema_c, void* d_workspace, size_t workspace_bytes,
                               void* stream);
 
+/* Histogram of x[n] over [lo, hi] in `bins` equal bins, Lucid's histc as HistogramObserver
+ * calls it (lucid/quantization/observer.py:858-861 -> lucid/_ops/_adapters.py:1256-1279 ->
+ * lucid/_C/backend/cpu/methods/Reduction.cpp:839-884): in double precision,
+ * step = (hi - lo) / bins and v counts in bin trunc((v - lo) / step) (the top edge in the last
+ * bin); values outside [lo, hi] and NaN are skipped.  d_hist[b] = float(count) (accumulate = 0)
+ * or fl32(float(count) + d_hist[b]) (accumulate = 1: observer.py:863-865).  Needs hi > lo and
+ * lq_histc_workspace_size(bins) bytes of workspace. */
+size_t lq_histc_workspace_size(int64_t bins);
+int lq_histc_f32(const float* d_x, int64_t n, int64_t bins, double lo, double hi, int accumulate,
+                 float* d_hist, void* d_workspace, size_t workspace_bytes, void* stream);
+/* HistogramObserver._rebin (lucid/quantization/observer.py:826-848): d_out[j] is the float32
+ * sum, in source order, of d_hist[i] over the source bins i whose float32 center
+ * old_min + (i + 0.5) * old_width lands, after (c - new_min) / new_width clipped to
+ * [0, bins - 1] and truncated, on j.  old_width / new_width are the float32-rounded
+ * (max - min) / bins.  bins <= 16384; d_out must not alias d_hist. */
+int lq_hist_rebin_f32(const float* d_hist, int64_t bins, float old_min, float old_width,
+                      float new_min, float new_width, float* d_out, void* stream);
+
 /* calculate_qparams (lucid/quantization/_qparams.py:186-205) over n ranges:
  * scale[i], zero_point[i] from min[i], max[i].  symmetric != 0 selects the
  * symmetric branch; is_signed picks its zero point (0 or (qmax+qmin+1)//2). */

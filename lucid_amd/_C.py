@@ -65,6 +65,9 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_event_record": (_I, [_P, _P]),
     "lq_event_synchronize": (_I, [_P]),
     "lq_event_elapsed_ms": (_I, [ctypes.POINTER(_F), _P, _P]),
+    "lq_histc_workspace_size": (_SZ, [_I64]),
+    "lq_histc_f32": (_I, [_P, _I64, _I64, ctypes.c_double, ctypes.c_double, _I, _P, _P, _SZ, _P]),
+    "lq_hist_rebin_f32": (_I, [_P, _I64, _F, _F, _F, _F, _P, _P]),
     "lq_graph_begin_capture": (_I, [_P]),
     "lq_graph_end_capture": (_I, [_P, ctypes.POINTER(_P)]),
     "lq_graph_launch": (_I, [_P, _P]),

@@ -19,12 +19,13 @@ updated in place; the input is returned unchanged.
 from __future__ import annotations
 
 import functools
+import math
 from typing import Any
 
 import numpy as np
 
 from lucid_amd import _C
-from lucid_amd._tensor import Tensor, tensor
+from lucid_amd._tensor import Tensor, empty, tensor
 from lucid_amd.nn.module import Module
 from lucid_amd.quantization._device import ocl, require_gpu, workspace
 from lucid_amd.quantization._qparams import calculate_qparams
@@ -189,12 +190,21 @@ class MovingAveragePerChannelMinMaxObserver(PerChannelMinMaxObserver):
 
 
 class HistogramObserver(ObserverBase):
-    """Lucid's default static activation observer (observer.py:692-926).
+    """Per-tensor observer that keeps a value histogram and picks the clip range with the
+    least expected L2 quantization error (observer.py:692-926); Lucid's default static
+    activation observer.
 
-    Not part of this backend yet: its L2 clip-range search over a 2048-bin histogram
-    is a later addition.  Pin ``MinMaxObserver`` (or a moving-average observer) as the
-    activation observer of a ``QConfig`` instead.
+    Buffers ``min_val`` / ``max_val`` (running support, seeded ``+inf`` / ``-inf``) and
+    ``histogram`` (``bins`` float32 counts).  ``forward`` reads the batch range back (as
+    Lucid's ``.item()`` calls do), widens the running range, moves the stored counts onto
+    the wider bins when it grows (``lq_hist_rebin_f32``) and adds the batch's counts
+    (``lq_histc_f32``) -- the counting runs on the GPU in one pass over ``x``.
+    ``calculate_qparams`` runs the reference's coarse clip search on the host over the
+    ``bins`` counts (a data-dependent scan of a few thousand numbers, observer.py:872-926,
+    where Lucid runs it too) and reduces the winning range with ``calculate_qparams``.
     """
+
+    _QUANTILES = (0.0, 1e-5, 1e-4, 1e-3, 5e-3, 1e-2)
 
     def __init__(self, bins: int = 2048, qscheme: QScheme = per_tensor_affine,
                  qdtype: QDtype = quint8, eps: float = 1e-8) -> None:
@@ -204,14 +214,112 @@ class HistogramObserver(ObserverBase):
         self.register_buffer("max_val", tensor(np.float32(-np.inf)))
         self.register_buffer("histogram", tensor(np.zeros(bins, np.float32)))
 
+    def _batch_range(self, x: Tensor) -> tuple[float, float]:
+        """``x.min()``, ``x.max()`` (NaN-propagating) read back to the host."""
+        n = x.numel()
+        ext = tensor(np.array([np.inf, -np.inf], np.float32), device="gpu")
+        L = _C.lib()
+        ws_bytes = L.lq_minmax_workspace_size(n)
+        _C.call("lq_minmax_f32", x.data_ptr(), n, ext.data_ptr(), ext.data_ptr() + 4, _C.OBS_REPLACE,
+                0.0, workspace.get(ws_bytes), ws_bytes, None)
+        lo, hi = ext.numpy().tolist()
+        return float(lo), float(hi)
+
+    def _histc_range(self, x_lo: float, x_hi: float, lo: float, hi: float) -> tuple[float, float]:
+        """The range histc counts over (lucid/_ops/_adapters.py:1266-1276)."""
+        if lo > hi:
+            raise ValueError(f"histc: max must be at least min, got [{lo}, {hi}]")
+        if lo == hi:
+            lo, hi = x_lo, x_hi
+        if not (math.isfinite(lo) and math.isfinite(hi)):
+            raise ValueError(f"histc: range of [{lo}, {hi}] is not finite")
+        if lo == hi:
+            lo, hi = lo - 1.0, hi + 1.0
+        return lo, hi
+
     def forward(self, x: Tensor) -> Tensor:
-        raise NotImplementedError(
-            "HistogramObserver is not implemented on the HIP backend; use "
-            "MinMaxObserver / MovingAverageMinMaxObserver as the activation observer"
-        )
+        require_gpu(x, type(self).__name__)
+        if x.dtype != np.float32:
+            raise TypeError(f"{type(self).__name__}: expected float32 input, got {x.dtype}")
+        n = x.numel()
+        if n == 0:
+            raise ValueError("HistogramObserver: an empty batch has no range")
+        self._align_running_buffers(x)
+        if self.histogram.numel() != self.bins:
+            raise ValueError(f"HistogramObserver: histogram buffer has {self.histogram.numel()} "
+                             f"bins, expected {self.bins}")
+        cur_min, cur_max = self._batch_range(x)
+        old_min, old_max = float(self.min_val.item()), float(self.max_val.item())
+        first = old_min == math.inf
+        if first:
+            new_min, new_max = cur_min, cur_max
+        else:
+            new_min, new_max = min(old_min, cur_min), max(old_max, cur_max)
+        lo, hi = self._histc_range(cur_min, cur_max, new_min, new_max)
+        L = _C.lib()
+        ws_bytes = L.lq_histc_workspace_size(self.bins)
+        hist = self.histogram
+        if not first and not (new_min == old_min and new_max == old_max):
+            # the stored counts move onto the wider bins first (observer.py:865)
+            hist = empty((self.bins,), np.float32, "gpu")
+            _C.call("lq_hist_rebin_f32", self.histogram.data_ptr(), self.bins, float(np.float32(old_min)),
+                    float(np.float32((old_max - old_min) / self.bins)), float(np.float32(new_min)),
+                    float(np.float32((new_max - new_min) / self.bins)), hist.data_ptr(), None)
+        _C.call("lq_histc_f32", x.data_ptr(), n, self.bins, lo, hi, 0 if first else 1, hist.data_ptr(),
+                workspace.get(ws_bytes), ws_bytes, None)
+        if hist is not self.histogram:
+            self.histogram.copy_(hist)
+        self.min_val.copy_(tensor(np.float32(new_min), device="gpu"))
+        self.max_val.copy_(tensor(np.float32(new_max), device="gpu"))
+        return x
+
+    def _search_clip_range(self) -> tuple[float, float]:
+        """The candidate clip range with the least clip-plus-rounding error
+        (observer.py:872-901), scanned in double precision in source order."""
+        lo, hi = float(self.min_val.item()), float(self.max_val.item())
+        counts = [float(c) for c in self.histogram.numpy().tolist()]
+        total = sum(counts)
+        if total <= 0.0 or hi <= lo:
+            return lo, hi
+        bins = self.bins
+        width = (hi - lo) / bins
+        centers = [lo + (i + 0.5) * width for i in range(bins)]
+        levels = self.qdtype.quant_max - self.qdtype.quant_min
+        best_err, best = math.inf, (lo, hi)
+        for frac in self._QUANTILES:
+            cmin = _quantile_from_hist(counts, centers, frac)
+            cmax = _quantile_from_hist(counts, centers, 1.0 - frac)
+            if cmax <= cmin:
+                continue
+            step = (cmax - cmin) / max(levels, 1)
+            err = 0.0
+            for c, k in zip(centers, counts):
+                if k == 0.0:
+                    continue
+                cc = cmin if c < cmin else (cmax if c > cmax else c)
+                err += k * ((c - cc) ** 2 + (step * step) / 12.0)
+            if err < best_err:
+                best_err, best = err, (cmin, cmax)
+        return best
 
     def calculate_qparams(self) -> tuple[Tensor, Tensor]:
-        raise NotImplementedError("HistogramObserver is not implemented on the HIP backend")
+        new_min, new_max = self._search_clip_range()
+        return calculate_qparams(float(new_min), float(new_max), self.qscheme, self.qdtype, self.eps)
+
+
+def _quantile_from_hist(counts: list[float], centers: list[float], q: float) -> float:
+    """The bin center where the cumulative count first reaches ``q`` of the total
+    (observer.py:915-926)."""
+    total = sum(counts)
+    if total <= 0:
+        return centers[0]
+    target = q * total
+    acc = 0.0
+    for c, k in zip(centers, counts):
+        acc += k
+        if acc >= target:
+            return c
+    return centers[-1]
 
 
 class FixedQParamsObserver(ObserverBase):

@@ -30,6 +30,13 @@ function                      follows (lucid-official/lucid)
                               float64 accumulation (tolerance reference)
 ``group_*``                   quantization/_qgemm.py:84-97, 167-170 (MLX 0.32.3 internals:
                               parity unpinned beyond this documented formula)
+``histc``                     _ops/_adapters.py:1256-1279 -> backend/cpu/methods/
+                              Reduction.cpp:839-884 (double-precision bins, numpy)
+``hist_rebin``                quantization/observer.py:826-848 (float32 centers / index,
+                              sequential scatter_add, numpy)
+``histogram_observer``        observer.py:850-870 (forward over batches)
+``hist_clip_search``          observer.py:872-926, vectorised (cumulative sums and array
+                              errors instead of the reference's Python loops)
 ``lucid_*``                   the multi-pass CPU composition timed as the CPU baseline
 ============================  ==========================================================
 
@@ -397,3 +404,94 @@ def lucid_quantize(x, inv, z, qmin, qmax, q, t0, t1) -> None:
 
 def lucid_dequantize(q, s, z, y, t0) -> None:
     lib().lqo_lucid_dequantize(_ptr(q), q.size, np.float32(s), np.float32(z), _ptr(y), _ptr(t0))
+
+
+# ------------------------------------------------------------- histogram observer
+
+
+def histc(x: np.ndarray, bins: int, lo: float, hi: float) -> np.ndarray:
+    """float32 counts of ``x`` over ``[lo, hi]``: bin trunc((v - lo) / step) in double, the
+    top edge in the last bin, values outside the range and NaN skipped."""
+    v = np.asarray(x, np.float32).astype(np.float64).ravel()
+    step = (hi - lo) / float(bins)
+    keep = (v >= lo) & (v <= hi)
+    b = ((v[keep] - lo) / step).astype(np.int64)
+    b = np.minimum(b, bins - 1)
+    return np.bincount(b, minlength=bins).astype(np.float64).astype(np.float32)
+
+
+def hist_rebin(hist: np.ndarray, old_min: float, old_max: float, new_min: float,
+               new_max: float) -> np.ndarray:
+    """The stored histogram moved onto ``[new_min, new_max]``: float32 centers and target
+    index (each operation rounded to float32), truncation, then an in-order float32
+    scatter_add."""
+    bins = hist.size
+    f = np.float32
+    old_w = f((old_max - old_min) / bins)
+    new_w = f((new_max - new_min) / bins)
+    centers = f(old_min) + (np.arange(bins, dtype=np.float32) + f(0.5)) * old_w
+    raw = np.clip((centers - f(new_min)) / new_w, f(0.0), f(bins - 1))
+    dst = raw.astype(np.int64)
+    out = np.zeros(bins, np.float32)
+    for i in range(bins):  # float32 additions in source order
+        out[dst[i]] = np.float32(out[dst[i]] + hist[i])
+    return out
+
+
+def histogram_observer(batches, bins: int):
+    """(min_val, max_val, histogram) after ``forward`` over ``batches`` (float32 arrays)."""
+    mn, mx, hist = np.inf, -np.inf, np.zeros(bins, np.float32)
+    for x in batches:
+        x = np.asarray(x, np.float32)
+        cur_min, cur_max = float(x.min()), float(x.max())
+        if mn == np.inf:
+            new_min, new_max = cur_min, cur_max
+        else:
+            new_min, new_max = min(mn, cur_min), max(mx, cur_max)
+        lo, hi = new_min, new_max
+        if lo == hi:
+            lo, hi = cur_min, cur_max
+        if not (np.isfinite(lo) and np.isfinite(hi)):
+            raise ValueError("histc range is not finite")
+        if lo == hi:
+            lo, hi = lo - 1.0, hi + 1.0
+        h = histc(x, bins, lo, hi)
+        if mn == np.inf:
+            hist = h
+        elif new_min == mn and new_max == mx:
+            hist = (h + hist).astype(np.float32)
+        else:
+            hist = (h + hist_rebin(hist, mn, mx, new_min, new_max)).astype(np.float32)
+        mn, mx = float(np.float32(new_min)), float(np.float32(new_max))
+    return mn, mx, hist
+
+
+def hist_clip_search(hist: np.ndarray, lo: float, hi: float, levels: int,
+                     quantiles=(0.0, 1e-5, 1e-4, 1e-3, 5e-3, 1e-2)) -> tuple[float, float]:
+    """The candidate clip range [quantile(q), quantile(1 - q)] with the least
+    sum n_i ((c_i - clip(c_i))^2 + step^2 / 12)."""
+    counts = np.asarray(hist, np.float64)
+    total = counts.sum()
+    if total <= 0.0 or hi <= lo:
+        return lo, hi
+    bins = counts.size
+    width = (hi - lo) / bins
+    centers = lo + (np.arange(bins) + 0.5) * width
+    cum = np.cumsum(counts)
+
+    def quantile(q: float) -> float:
+        idx = np.nonzero(cum >= q * total)[0]
+        return float(centers[idx[0]]) if idx.size else float(centers[-1])
+
+    best_err, best = np.inf, (lo, hi)
+    nz = counts != 0.0
+    for q in quantiles:
+        cmin, cmax = quantile(q), quantile(1.0 - q)
+        if cmax <= cmin:
+            continue
+        step = (cmax - cmin) / max(levels, 1)
+        cc = np.clip(centers[nz], cmin, cmax)
+        err = float(np.sum(counts[nz] * ((centers[nz] - cc) ** 2 + step * step / 12.0)))
+        if err < best_err:
+            best_err, best = err, (cmin, cmax)
+    return best

@@ -402,3 +402,55 @@ def test_conv_f32_against_float64(O):
                     patch = xp[:, 3 * g:3 * g + 3, 2 * oh:2 * oh + 3, ow:ow + 3]
                     ref[:, co, oh, ow] = (patch * w[co].astype(np.float64)).sum(axis=(1, 2, 3)) + b[co]
     np.testing.assert_allclose(y, ref, rtol=1e-5, atol=1e-5)
+
+
+# ------------------------------------------------------------- histogram observer pins
+
+
+def test_histc_closed_form():
+    # bins of width 1 over [0, 8]: an interior value, a value on an inner edge (belongs to
+    # the upper bin), the top edge (last bin), and values the reference skips.
+    x = np.array([0.0, 0.5, 1.0, 3.25, 7.999, 8.0, -0.1, 8.1, np.nan, np.inf, -np.inf], np.float32)
+    want = np.array([2, 1, 0, 1, 0, 0, 0, 2], np.float32)
+    np.testing.assert_array_equal(O.histc(x, 8, 0.0, 8.0), want)
+
+
+def test_hist_rebin_closed_forms():
+    rng = np.random.default_rng(3)
+    h = rng.integers(0, 50, 8).astype(np.float32)
+    # twice as wide, same origin: target j collects sources 2j and 2j + 1
+    np.testing.assert_array_equal(O.hist_rebin(h, 0.0, 8.0, 0.0, 16.0),
+                                  np.concatenate([h[0::2] + h[1::2], np.zeros(4, np.float32)]))
+    # twice as wide, centred: the old support lands on targets 4..7
+    np.testing.assert_array_equal(O.hist_rebin(h, 0.0, 8.0, -8.0, 8.0),
+                                  np.concatenate([np.zeros(4, np.float32), h[0::2] + h[1::2]]))
+    # a point support (old_min == old_max) moves its whole mass to one bin
+    r = O.hist_rebin(h, 2.0, 2.0, 0.0, 8.0)
+    assert r[2] == h.sum() and np.count_nonzero(r) == 1
+    # mass is conserved for any widening
+    big = rng.integers(0, 1000, 2048).astype(np.float32)
+    assert O.hist_rebin(big, -1.3, 2.7, -5.1, 9.4).sum() == big.sum()
+
+
+def test_hist_clip_search_pins():
+    # A flat histogram gains nothing from clipping: the full support (first to last centre).
+    h = np.full(64, 10.0, np.float32)
+    lo, hi = 0.0, 64.0
+    assert O.hist_clip_search(h, lo, hi, 255) == (0.5, 63.5)
+    # The reference's documented example (observer.py:785-798): one far outlier next to a
+    # normal bulk is kept at 1e5 values and clipped at 1e6.
+    rng = np.random.default_rng(0)
+    for n, clipped in ((100_000, False), (1_000_000, True)):
+        x = rng.standard_normal(n).astype(np.float32)
+        x[0] = 50.0
+        _, _, hist = O.histogram_observer([x], 2048)
+        cmin, cmax = O.hist_clip_search(hist, float(x.min()), 50.0, 255)
+        assert (cmax < 25.0) == clipped, (n, cmax)
+    # The reference unit test (test_observer.py:64-76): a heavy tail makes the histogram
+    # range no wider than min/max.
+    data = np.concatenate([rng.standard_normal(3000), rng.uniform(5.0, 12.0, 150)]).astype(np.float32)
+    mn, mx, hist = O.histogram_observer([data], 512)
+    cmin, cmax = O.hist_clip_search(hist, mn, mx, 255)
+    s_hist, _ = O.calc_qparams(np.float32(cmin), np.float32(cmax), False, False, 0, 255)
+    s_mm, _ = O.calc_qparams(np.float32(mn), np.float32(mx), False, False, 0, 255)
+    assert s_hist <= s_mm
