@@ -311,6 +311,26 @@ int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d
                     int transpose, int flags, void* d_workspace, size_t workspace_bytes,
                     void* stream);
 
+/* ---- quantizable merges (FloatFunctional / QFunctional) ------------------------- */
+/* Operations of lq_qmerge. */
+enum { LQ_MERGE_ADD = 0, LQ_MERGE_MUL = 1, LQ_MERGE_ADD_SCALAR = 2, LQ_MERGE_MUL_SCALAR = 3, LQ_MERGE_COPY = 4 };
+/* Element-wise merge over a rows x cols block, the ops of FloatFunctional and QFunctional
+ * (lucid/nn/quantized/functional_module.py:95-120 and 195-229: add, mul, add_scalar,
+ * mul_scalar, add_relu = add with LQ_EPI_RELU, cat = LQ_MERGE_COPY into a slice).
+ * Operand a (and b for ADD / MUL) is read contiguously as float32 (type LQ_F32) or as codes
+ * (LQ_I8 / LQ_U8 / LQ_I16 / LQ_U8S8) with a per-tensor grid: value fl32(fl32(float(c) - z) * s)
+ * (d_*_scale required, d_*_zero_point NULL = 0).  t = a + b, a * b, a + scalar, a * scalar or
+ * a, one float32 operation, then ReLU (y <= 0 -> +0) with LQ_EPI_RELU.  out_type LQ_F32 stores
+ * t; a code type stores the codes of t on [qmin, qmax] with d_out_scale / d_out_zero_point
+ * (QFunctional's fake-quantize grid: clip(rne(t * fl32(1 / S)) + Z), NaN -> 0).  Element
+ * (r, c) goes to d_out[r * ld_out + c].  No reference counterpart for the fused form: Lucid
+ * runs the float op, then fake_quantize (functional_module.py:188-229). */
+int lq_qmerge(int op, const void* d_a, int a_type, const float* d_a_scale, const float* d_a_zero_point,
+              const void* d_b, int b_type, const float* d_b_scale, const float* d_b_zero_point, float scalar,
+              int64_t rows, int64_t cols, int64_t ld_out, const float* d_out_scale,
+              const float* d_out_zero_point, int qmin, int qmax, int flags, int out_type, void* d_out,
+              void* stream);
+
 /* ---- int8 Conv2d (implicit GEMM) ------------------------------------------------- */
 /* Padding modes of a convolution (Lucid's padding_mode, lucid/nn/functional/conv.py:24-29). */
 enum { LQ_PAD_ZEROS = 0, LQ_PAD_REFLECT = 1, LQ_PAD_REPLICATE = 2, LQ_PAD_CIRCULAR = 3 };

@@ -3,10 +3,12 @@
 
 The int8 layers keep Lucid's buffers and ``state_dict`` layout and run the gfx950 W8A8
 MFMA GEMM over integer codes; ``QuantStub`` / ``DeQuantStub`` / ``Quantize`` /
-``DeQuantize`` / ``QuantWrapper`` mark the quantized region.
+``DeQuantize`` / ``QuantWrapper`` mark the quantized region; ``FloatFunctional`` /
+``QFunctional`` carry residual adds and concatenations onto one grid.
 """
 
 from lucid_amd.nn.quantized.conv import Conv2d
+from lucid_amd.nn.quantized.functional_module import FloatFunctional, QFunctional
 from lucid_amd.nn.quantized.intrinsic import ConvReLU2d, LinearReLU
 from lucid_amd.nn.quantized.linear import Linear
 from lucid_amd.nn.quantized.mlx_linear import QuantizedLinearMLX
@@ -14,7 +16,7 @@ from lucid_amd.nn.quantized.modules import (DeQuantize, DeQuantStub, Quantize, Q
                                             QuantWrapper)
 
 __all__ = ["Linear", "QuantizedLinearMLX", "Conv2d", "ConvReLU2d", "LinearReLU", "QuantStub", "DeQuantStub", "Quantize", "DeQuantize",
-           "QuantWrapper"]
+           "QuantWrapper", "FloatFunctional", "QFunctional"]
 
 
 def __getattr__(name: str):

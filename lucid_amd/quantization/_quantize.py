@@ -35,7 +35,7 @@ def _observed_types() -> tuple[type, ...]:
     import lucid_amd.nn.intrinsic as nni
     import lucid_amd.nn.quantized as nnq
 
-    return (nn.Linear, nn.Conv2d, nni.ConvReLU2d, nni.LinearReLU, nnq.QuantStub)
+    return (nn.Linear, nn.Conv2d, nni.ConvReLU2d, nni.LinearReLU, nnq.QuantStub, nnq.FloatFunctional)
 
 
 def _quant_mapping() -> dict[type, _FromFloat]:
@@ -48,6 +48,7 @@ def _quant_mapping() -> dict[type, _FromFloat]:
         nni.LinearReLU: nnq.LinearReLU.from_float,
         nnq.QuantStub: nnq.Quantize.from_float,
         nnq.DeQuantStub: nnq.DeQuantize.from_float,
+        nnq.FloatFunctional: nnq.QFunctional.from_float,
     }
     if hasattr(nnq, "Conv2d"):
         mapping[nn.Conv2d] = nnq.Conv2d.from_float
