@@ -336,8 +336,9 @@ int lq_qmerge(int op, const void* d_a, int a_type, const float* d_a_scale, const
 enum { LQ_PAD_ZEROS = 0, LQ_PAD_REFLECT = 1, LQ_PAD_REPLICATE = 2, LQ_PAD_CIRCULAR = 3 };
 
 /* Weight codes w[Cout, Cin_g, KH, KW] (Lucid's weight_int8 of a quantized Conv2d,
- * lucid/nn/quantized/conv.py:92-100) in the layout the conv kernel reads:
- * w_p[Cout][KH][KW][Cp], Cp = Cin_g rounded up to 16 with zero codes, and the code sums
+ * lucid/nn/quantized/conv.py:92-100) in the layout the conv kernel reads: one row per output
+ * channel, w_p[co][(kh * KW + kw) * Cp + c] with Cp = Cin_g rounded up to 16 (zero codes),
+ * each row KH * KW * Cp bytes rounded up to a multiple of 128 (zero tail), and the code sums
  * d_w_sums[Cout] (NULL to skip) for the activation zero-point term.  Built once per module.
  * No reference counterpart (a device layout; the state_dict keeps weight_int8). */
 size_t lq_conv2d_weight_pack_size(int64_t Cout, int64_t Cin_g, int64_t KH, int64_t KW);

@@ -27,13 +27,12 @@
 // one contiguous NCHW store.
 #include <hip/hip_runtime.h>
 
+#include "lq_dma.h"
 #include "lq_epilogue.h"
 #include "lq_internal.h"
 
 namespace lq {
 namespace {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
 
 constexpr int CV_BM = 128, CV_BN = 64, CV_BK = 64, CV_THREADS = 256;
 
@@ -101,23 +100,45 @@ __global__ __launch_bounds__(256) void conv_pack_input_kernel(PackArgs a) {
     reinterpret_cast<vu4*>(a.xp)[id] = vu4{word[0], word[1], word[2], word[3]};
 }
 
-// One thread per output channel row: w_p[co][kh][kw][cp] and the row's code sum.
+// One thread per 16-byte chunk of a packed weight row w_p[co][k], k = (kh * KW + kw) * Cp + c,
+// rows ldw bytes long (K rounded up to whole 128-byte stages, the tail zero).
 __global__ __launch_bounds__(256) void conv_pack_weights_kernel(const int8_t* __restrict__ w, int Cout, int Cg,
-                                                                int KH, int KW, int Cp, int8_t* __restrict__ wp,
-                                                                int32_t* __restrict__ sums) {
-    const int co = blockIdx.x * blockDim.x + threadIdx.x;
+                                                                int KH, int KW, int Cp, int ldw,
+                                                                int8_t* __restrict__ wp) {
+    const int chunks = ldw / 16;
+    const int64_t total = (int64_t)Cout * chunks;
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= total) return;
+    const int64_t co = id / chunks;
+    const int k0 = (int)(id - co * chunks) * 16;
+    const int tap = k0 / Cp, c0 = k0 - tap * Cp;  // a chunk never crosses a tap (Cp % 16 == 0)
+    const int kh = tap / KW, kw = tap - kh * KW;
+    uint32_t word[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int c = c0 + q * 4 + b;
+            const int8_t x = (tap < KH * KW && c < Cg) ? w[((co * Cg + c) * KH + kh) * KW + kw] : (int8_t)0;
+            v |= (uint32_t)(uint8_t)x << (8 * b);
+        }
+        word[q] = v;
+    }
+    reinterpret_cast<vu4*>(wp)[id] = vu4{word[0], word[1], word[2], word[3]};
+}
+
+// sums[co] = sum of output channel co's codes (one wave per channel).
+__global__ __launch_bounds__(256) void conv_weight_sums_kernel(const int8_t* __restrict__ w, int Cout, int64_t per,
+                                                               int32_t* __restrict__ sums) {
+    const int co = blockIdx.x * 4 + (threadIdx.x >> 6);
     if (co >= Cout) return;
-    const int64_t K = (int64_t)KH * KW * Cp;
+    const int lane = threadIdx.x & 63;
     int32_t s = 0;
-    for (int kh = 0; kh < KH; ++kh)
-        for (int kw = 0; kw < KW; ++kw)
-            for (int c = 0; c < Cp; ++c) {
-                int8_t v = 0;
-                if (c < Cg) v = w[(((int64_t)co * Cg + c) * KH + kh) * KW + kw];
-                wp[co * K + ((int64_t)kh * KW + kw) * Cp + c] = v;
-                s += v;
-            }
-    if (sums) sums[co] = s;
+    for (int64_t i = lane; i < per; i += 64) s += w[(int64_t)co * per + i];
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+    if (lane == 0) sums[co] = s;
 }
 
 // ---------------------------------------------------------------- implicit GEMM
@@ -127,7 +148,7 @@ struct ConvArgs {
     const int8_t* wp;
     void* y;
     int N, Hp, Wp, G, Cp, Cout_g, KH, KW, sh, sw, dh, dw, OH, OW;
-    int K, P;
+    int K, P, ldw;  // real K; packed weight row stride (K padded to whole 128-byte stages)
     const float* a_scale;
     const float* a_zp;
     int a_u8s8;
@@ -193,7 +214,7 @@ __global__ __launch_bounds__(CV_THREADS) void conv_i8_kernel(ConvArgs a) {
     int ka_k = 16 * ca;
     // B: one chunk per thread (row tid >> 2, chunk tid & 3)
     const int brow = tid >> 2;
-    const int8_t* bptr = a.wp + ((int64_t)g * a.Cout_g + min(co0 + brow, a.Cout_g - 1)) * a.K + 16 * ca;
+    const int8_t* bptr = a.wp + ((int64_t)g * a.Cout_g + min(co0 + brow, a.Cout_g - 1)) * a.ldw + 16 * ca;
 
     vu4 ra[2], rb;
     auto gload = [&](int t) {
@@ -301,6 +322,228 @@ __global__ __launch_bounds__(CV_THREADS) void conv_i8_kernel(ConvArgs a) {
     }
 }
 
+// ------------------------------------------------- LDS-DMA implicit GEMM (production)
+//
+// The main loop of the int8 GEMM (lq_gemm.hip) with the im2col rows fetched by LDS-DMA:
+// GEMM rows are output pixels, columns output channels of a group, K = (kh, kw, c) over the
+// padded NHWC input in whole 128-byte stages (the packed weight rows carry zero columns past
+// KH * KW * Cp).  A lane's 16-byte copy of pixel row p, logical chunk k0 + 16 q, comes from
+// x_p + base(p) + tap_off(k / Cp) + k % Cp: one contiguous load per lane, any tap, any stride
+// or dilation.  Taps past KH * KW (the K padding) read the first tap again; their weights are
+// zero.  Pixel fragments are permuted (lane row rho reads tile row (rho / 4) * 16 + 4 j +
+// rho % 4), so a lane's results are 16 consecutive pixels of one output channel: one 16-byte
+// NCHW store per channel for int8 outputs.
+constexpr int CV_MAX_TAPS = 128;
+
+struct ConvDmaArgs {
+    const int8_t* xp;
+    const int8_t* wp;
+    void* y;
+    uint32_t xp_bytes;
+    int Hp, Wp, G, Cp, cp_shift, Cout_g, KH, KW, sh, sw, dh, dw, OH, OW, P, nk, ldw;
+    int kw_magic;                  // ceil(2^16 / KW): tap / KW = (tap * kw_magic) >> 16 for tap < 128
+    int kh_stride, kw_stride;      // input bytes between vertical / horizontal taps
+    const float* a_scale;
+    const float* a_zp;
+    int a_u8s8;
+    const float* w_scale;
+    const int32_t* w_sums;
+    const float* bias;
+    const float* out_scale;
+    const float* out_zp;
+    int qmin, qmax, relu;
+};
+
+template <int BM, int BN, int WAVES_M, int WAVES_N, int KIND>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void conv_i8_dma_kernel(ConvDmaArgs a) {
+    constexpr int BK = 128, NW = WAVES_M * WAVES_N, WM = BM / WAVES_M, WN = BN / WAVES_N;
+    constexpr int FM = WM / 16, FN = WN / 16;
+    constexpr int A_I = BM / 8 / NW, B_I = BN / 8 / NW, LPS = A_I + B_I, SB = (BM + BN) * BK;
+    constexpr bool INT_CODES = KIND == LQ_OUT_Q8 || KIND == LQ_OUT_QU8 || KIND == LQ_OUT_Q16 || KIND == LQ_OUT_QU8S8;
+    static_assert(WM == 64, "a lane owns 16 consecutive pixels of a 64-pixel wave tile");
+    static_assert(A_I * 8 * NW == BM && B_I * 8 * NW == BN && WN % 16 == 0, "copy split");
+    __shared__ __attribute__((aligned(1024))) int8_t lds[2 * SB];
+
+    const int p0 = blockIdx.x * BM, co0 = blockIdx.y * BN, g = blockIdx.z;
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    const int GCp = a.G * a.Cp;
+    const int taps = a.KH * a.KW;
+    // input offset of tap t (the K padding past KH * KW reads tap 0; its weights are zero)
+    auto tap_off = [&](int t) __attribute__((always_inline)) {
+        const int kh = (t * a.kw_magic) >> 16, kw = t - kh * a.KW;
+        return t < taps ? kh * a.kh_stride + kw * a.kw_stride : 0;
+    };
+
+    const v4i rx = buffer_rsrc(a.xp, a.xp_bytes);
+    const v4i rw = buffer_rsrc(a.wp + (int64_t)g * a.Cout_g * a.ldw, (uint32_t)((int64_t)a.Cout_g * a.ldw));
+    const int rl = lane >> 3, slot = lane & 7;
+    const int OHW = a.OH * a.OW;
+    uint32_t abase[A_I];
+    int aq[A_I];  // logical 16-byte chunk of the lane's copy (the swizzle is per row)
+#pragma unroll
+    for (int j = 0; j < A_I; ++j) {
+        const int r = (j * NW + wave) * 8 + rl;
+        const int p = min(p0 + r, a.P - 1);
+        const int n = p / OHW, rem = p - n * OHW;
+        const int oh = rem / a.OW, ow = rem - oh * a.OW;
+        abase[j] = (uint32_t)((((int64_t)n * a.Hp + (int64_t)oh * a.sh) * a.Wp + (int64_t)ow * a.sw) * GCp +
+                              (int64_t)g * a.Cp);
+        aq[j] = slot ^ dma_swz(r);
+    }
+    uint32_t boff[B_I];
+#pragma unroll
+    for (int j = 0; j < B_I; ++j) {
+        const int r = (j * NW + wave) * 8 + rl;
+        boff[j] = (uint32_t)((co0 + r) * a.ldw + (slot ^ dma_swz(r)) * 16);
+    }
+    const uint32_t lds_base = (uint32_t)reinterpret_cast<uintptr_t>(lds);
+    auto issue = [&](int buf, int kt) __attribute__((always_inline)) {
+        const int k0 = min(kt, a.nk - 1) * BK;
+        const uint32_t sb = lds_base + buf * SB;
+        const int tap_u = a.cp_shift < 0 ? k0 / a.Cp : 0;  // Cp a multiple of 128: one tap per stage
+#pragma unroll
+        for (int j = 0; j < A_I; ++j) {
+            const int k = k0 + 16 * aq[j];
+            const int tap = a.cp_shift < 0 ? tap_u : (k >> a.cp_shift);
+            const uint32_t off = abase[j] + (uint32_t)(tap_off(tap) + (k - tap * a.Cp));
+            lds_dma16(rx, off, 0, sb + (j * NW + wave) * 8 * BK);
+        }
+#pragma unroll
+        for (int j = 0; j < B_I; ++j) lds_dma16(rw, boff[j], (uint32_t)k0, sb + BM * BK + (j * NW + wave) * 8 * BK);
+    };
+    // Fragments: pixel fragment j (permuted rows wm*64 + (rho/4)*16 + 4j + rho%4), channel
+    // fragment i (rows wn*WN + 16 i + rho); logical chunk of K step s: 4 s + lane / 16.
+    const int rho = lane & 15, c0 = lane >> 4;
+    const int a_row = wm * 64 + (rho >> 2) * 16 + (rho & 3);
+    const int a_base = a_row * BK + ((c0 ^ dma_swz(a_row)) << 4);
+    const int b_base = BM * BK + (wn * WN + rho) * BK + ((c0 ^ (rho & 7)) << 4);
+    v4i F0[FM + FN], F1[FM + FN];
+    auto read_frags = [&](v4i* f, int buf, int s) __attribute__((always_inline)) {
+        const int8_t* sbuf = lds + buf * SB;
+#pragma unroll
+        for (int j = 0; j < FM; ++j)
+            f[j] = *reinterpret_cast<const v4i*>(sbuf + (a_base ^ (((s ^ j) & 1) << 6)) + j * 4 * BK);
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+            f[FM + i] = *reinterpret_cast<const v4i*>(sbuf + (b_base ^ (((s ^ i) & 1) << 6)) + i * 16 * BK);
+    };
+    v4i acc[FN][FM];
+#pragma unroll
+    for (int i = 0; i < FN; ++i)
+#pragma unroll
+        for (int j = 0; j < FM; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+    auto mfmas = [&](const v4i* f) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < FN; ++i)
+#pragma unroll
+            for (int j = 0; j < FM; ++j)
+                acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f[j], f[FM + i], acc[i][j], 0, 0, 0);
+    };
+    auto stage = [&](auto bc, int kt, bool last) __attribute__((always_inline)) {
+        constexpr int B = decltype(bc)::value;
+        read_frags(F1, B, 1);
+        mfmas(F0);
+        if (!last) {
+            wait_vmcnt<0>();
+            block_barrier();
+            issue(B, kt + 2);
+            read_frags(F0, B ^ 1, 0);
+        }
+        mfmas(F1);
+    };
+    issue(0, 0);
+    issue(1, 1);
+    wait_vmcnt<LPS>();
+    block_barrier();
+    read_frags(F0, 0, 0);
+    int kt = 0;
+    for (; kt + 2 < a.nk; kt += 2) {
+        stage(std::integral_constant<int, 0>(), kt, false);
+        stage(std::integral_constant<int, 1>(), kt + 1, false);
+    }
+    stage(std::integral_constant<int, 0>(), kt, kt + 1 == a.nk);
+    if (kt + 1 < a.nk) stage(std::integral_constant<int, 1>(), kt + 1, true);
+    wait_vmcnt<0>();  // no copy may still target LDS when the workgroup ends
+
+    // Epilogue: acc[i][j][r] is pixel p0 + wm*64 + 16 (lane/16) + 4 j + r, channel
+    // co0 + wn*WN + 16 i + lane % 16 (within the group).
+    EpiParams ep;
+    ep.za = (a.a_zp ? (int)a.a_zp[0] : 0) - (a.a_u8s8 ? 128 : 0);
+    ep.has_za = a.a_zp != nullptr || a.a_u8s8;
+    ep.out_s = a.out_scale ? a.out_scale[0] : 1.0f;
+    ep.out_inv = 1.0f / ep.out_s;
+    ep.out_z = a.out_zp ? a.out_zp[0] : 0.0f;
+    ep.g = make_grid(a.qmin, a.qmax);
+    CodeClamp cc{};
+    if (INT_CODES) cc = code_clamp<KIND>(a.qmin, a.qmax);
+    const float sa = a.a_scale ? a.a_scale[0] : 1.0f;
+    const int Cout = a.G * a.Cout_g;
+    const int pb = p0 + wm * 64 + c0 * 16;
+    const int nimg = min(pb, a.P - 1) / OHW;
+    const int pix0 = pb - nimg * OHW;
+    constexpr int OB = OutTraits<KIND>::bytes;
+    const bool vec = (OHW % 16 == 0) && (reinterpret_cast<uintptr_t>(a.y) % 16 == 0) && (pb + 15 < a.P);
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+        const int col = co0 + wn * WN + 16 * i + rho;
+        if (col >= a.Cout_g) continue;
+        const int co = g * a.Cout_g + col;
+        const float sb = a.w_scale[co];
+        const float bias = a.bias ? a.bias[co] : 0.0f;
+        const int32_t zsum = ep.has_za ? (int32_t)((uint32_t)ep.za * (uint32_t)a.w_sums[co]) : 0;
+        uint32_t out[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int32_t acc_c = (int32_t)((uint32_t)acc[i][q >> 2][q & 3] - (uint32_t)zsum);
+            if (INT_CODES) {
+                const float s = sa * sb;
+                float y = (float)acc_c * s;
+                if (a.bias) y = y + bias;
+                if (a.relu) y = (y <= 0.0f) ? 0.0f : y;
+                out[q] = (uint32_t)requant_int<KIND>(y, ep, cc);
+                if (KIND == LQ_OUT_QU8S8) out[q] ^= 0x80u;
+            } else {
+                out[q] = epi_one<KIND>(acc_c, sa, sb, a.bias ? &bias : nullptr, a.relu != 0, ep);
+            }
+        }
+        if (vec) {
+            const int64_t base = ((int64_t)nimg * Cout + co) * OHW + pix0;
+            if (OB == 1) {
+                v4i w;
+#pragma unroll
+                for (int d = 0; d < 4; ++d)
+                    w[d] = (int)((out[4 * d] & 0xffu) | ((out[4 * d + 1] & 0xffu) << 8) |
+                                 ((out[4 * d + 2] & 0xffu) << 16) | (out[4 * d + 3] << 24));
+                *reinterpret_cast<v4i*>(reinterpret_cast<uint8_t*>(a.y) + base) = w;
+            } else if (OB == 2) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    v4i w;
+#pragma unroll
+                    for (int d = 0; d < 4; ++d)
+                        w[d] = (int)((out[8 * h + 2 * d] & 0xffffu) | (out[8 * h + 2 * d + 1] << 16));
+                    *reinterpret_cast<v4i*>(reinterpret_cast<uint16_t*>(a.y) + base + 8 * h) = w;
+                }
+            } else {
+#pragma unroll
+                for (int h = 0; h < 4; ++h)
+                    *reinterpret_cast<v4i*>(reinterpret_cast<uint32_t*>(a.y) + base + 4 * h) =
+                        v4i{(int)out[4 * h], (int)out[4 * h + 1], (int)out[4 * h + 2], (int)out[4 * h + 3]};
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int p = pb + q;
+                if (p >= a.P) break;
+                const int nq = p / OHW, pq = p - nq * OHW;
+                store_elem<KIND>(a.y, ((int64_t)nq * Cout + co) * OHW + pq, out[q]);
+            }
+        }
+    }
+}
+
 // ---------------------------------------------------------------- float helpers
 
 struct FConvArgs {
@@ -373,6 +616,9 @@ bool conv_geometry(int64_t H, int64_t W, int KH, int KW, int sh, int sw, int pt,
 
 constexpr int64_t CV_MAX = (int64_t)1 << 31;
 
+// Packed weight row stride: K rounded up to whole 128-byte stages.
+int64_t conv_ldw(int64_t K) { return (K + 127) / 128 * 128; }
+
 }  // namespace
 }  // namespace lq
 
@@ -383,7 +629,7 @@ extern "C" {
 size_t lq_conv2d_weight_pack_size(int64_t Cout, int64_t Cin_g, int64_t KH, int64_t KW) {
     if (Cout < 0 || Cin_g < 1 || KH < 1 || KW < 1) return 0;
     const int64_t Cp = (Cin_g + 15) / 16 * 16;
-    return (size_t)(Cout * KH * KW * Cp);
+    return (size_t)(Cout * conv_ldw(KH * KW * Cp));
 }
 
 int lq_conv2d_pack_weights_i8(const int8_t* d_w, int64_t Cout, int64_t Cin_g, int64_t KH, int64_t KW,
@@ -393,8 +639,14 @@ int lq_conv2d_pack_weights_i8(const int8_t* d_w, int64_t Cout, int64_t Cin_g, in
     if (Cout == 0) return LQ_OK;
     LQ_REQUIRE(d_w && d_w_packed, "lq_conv2d_pack_weights_i8: NULL pointer");
     const int Cp = (int)((Cin_g + 15) / 16 * 16);
-    hipLaunchKernelGGL(conv_pack_weights_kernel, dim3((unsigned)((Cout + 255) / 256)), dim3(256), 0, as_stream(stream),
-                       d_w, (int)Cout, (int)Cin_g, (int)KH, (int)KW, Cp, d_w_packed, d_w_sums);
+    hipStream_t st = as_stream(stream);
+    const int64_t ldw = conv_ldw(KH * KW * Cp);
+    const int64_t chunks = Cout * (ldw / 16);
+    hipLaunchKernelGGL(conv_pack_weights_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, st, d_w,
+                       (int)Cout, (int)Cin_g, (int)KH, (int)KW, Cp, (int)ldw, d_w_packed);
+    if (d_w_sums)
+        hipLaunchKernelGGL(conv_weight_sums_kernel, dim3((unsigned)((Cout + 3) / 4)), dim3(256), 0, st, d_w, (int)Cout,
+                           Cin_g * KH * KW, d_w_sums);
     return launch_status("lq_conv2d_pack_weights_i8");
 }
 
@@ -459,7 +711,7 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
     a.y = d_y;
     a.N = (int)N; a.Hp = (int)Hp; a.Wp = (int)Wp; a.G = (int)groups; a.Cp = (int)Cp; a.Cout_g = (int)Cout_g;
     a.KH = (int)KH; a.KW = (int)KW; a.sh = stride_h; a.sw = stride_w; a.dh = dilation_h; a.dw = dilation_w;
-    a.OH = (int)OH; a.OW = (int)OW; a.K = (int)K; a.P = (int)P;
+    a.OH = (int)OH; a.OW = (int)OW; a.K = (int)K; a.P = (int)P; a.ldw = (int)conv_ldw(K);
     a.a_scale = d_a_scale;
     a.a_zp = d_a_zero_point;
     a.a_u8s8 = pa.a_u8s8;
@@ -471,6 +723,49 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
     a.qmin = out_qmin;
     a.qmax = out_qmax;
     a.relu = (flags & LQ_EPI_RELU) ? 1 : 0;
+    // LDS-DMA kernel: whole 16-byte chunks of one tap per copy (Cp a power of two up to 128,
+    // or a multiple of 128) and a tap table that fits.
+    const int64_t ldw = conv_ldw(K);
+    const int64_t ntaps = (ldw + Cp - 1) / Cp;
+    const bool pow2 = Cp <= 128 && (Cp & (Cp - 1)) == 0;
+    if ((pow2 || Cp % 128 == 0) && ntaps <= CV_MAX_TAPS && Cout_g * ldw < CV_MAX) {
+        ConvDmaArgs d{};
+        d.xp = pa.xp;
+        d.wp = d_w_packed;
+        d.y = d_y;
+        d.xp_bytes = (uint32_t)(N * Hp * Wp * groups * Cp);
+        d.Hp = (int)Hp; d.Wp = (int)Wp; d.G = (int)groups; d.Cp = (int)Cp;
+        d.cp_shift = pow2 ? __builtin_ctz((unsigned)Cp) : -1;
+        d.Cout_g = (int)Cout_g; d.KH = (int)KH; d.KW = (int)KW; d.sh = stride_h; d.sw = stride_w;
+        d.dh = dilation_h; d.dw = dilation_w; d.OH = (int)OH; d.OW = (int)OW; d.P = (int)P;
+        d.nk = (int)(ldw / 128); d.ldw = (int)ldw;
+        d.kw_magic = (int)((65536 + KW - 1) / KW);
+        d.kh_stride = (int)(dilation_h * Wp * groups * Cp);
+        d.kw_stride = (int)(dilation_w * groups * Cp);
+        d.a_scale = d_a_scale; d.a_zp = d_a_zero_point; d.a_u8s8 = pa.a_u8s8;
+        d.w_scale = d_w_scale; d.w_sums = d_w_sums; d.bias = d_bias;
+        d.out_scale = d_out_scale; d.out_zp = d_out_zero_point;
+        d.qmin = out_qmin; d.qmax = out_qmax; d.relu = a.relu;
+        const int64_t ctiles = (Cout_g + 63) / 64;
+        const bool big = ((P + 255) / 256) * ctiles * groups >= 256;
+        const dim3 grid((unsigned)((P + (big ? 255 : 127)) / (big ? 256 : 128)), (unsigned)ctiles, (unsigned)groups);
+#define LQ_CONV_DMA(K_)                                                                                        \
+    if (big) hipLaunchKernelGGL((conv_i8_dma_kernel<256, 64, 4, 1, K_>), grid, dim3(256), 0, st, d);        \
+    else hipLaunchKernelGGL((conv_i8_dma_kernel<128, 64, 2, 2, K_>), grid, dim3(256), 0, st, d);            \
+    break;
+        switch (out_kind) {
+            case LQ_OUT_I32: LQ_CONV_DMA(LQ_OUT_I32)
+            case LQ_OUT_F32: LQ_CONV_DMA(LQ_OUT_F32)
+            case LQ_OUT_F16: LQ_CONV_DMA(LQ_OUT_F16)
+            case LQ_OUT_Q8: LQ_CONV_DMA(LQ_OUT_Q8)
+            case LQ_OUT_QU8: LQ_CONV_DMA(LQ_OUT_QU8)
+            case LQ_OUT_FQ32: LQ_CONV_DMA(LQ_OUT_FQ32)
+            case LQ_OUT_Q16: LQ_CONV_DMA(LQ_OUT_Q16)
+            default: LQ_CONV_DMA(LQ_OUT_QU8S8)
+        }
+#undef LQ_CONV_DMA
+        return launch_status("lq_conv2d_i8");
+    }
     const dim3 grid((unsigned)((P + CV_BM - 1) / CV_BM), (unsigned)((Cout_g + CV_BN - 1) / CV_BN), (unsigned)groups);
     switch (out_kind) {
         case LQ_OUT_I32: hipLaunchKernelGGL(conv_i8_kernel<LQ_OUT_I32>, grid, dim3(CV_THREADS), 0, st, a); break;

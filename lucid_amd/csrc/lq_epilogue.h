@@ -49,6 +49,37 @@ __device__ __forceinline__ uint32_t epi_one(int32_t acc, float sa, float sb, con
     return __float_as_uint(d * p.out_s);
 }
 
+// Requantized codes of the integer output kinds, clamped first to the grid [qmin, qmax] and
+// then to the storage range; lo / hi fold the two clamps into one.  NaN becomes code 0 (the
+// saturating cast of Lucid's Factory.cpp:127-146) whatever the grid: cvt_i32_sat gives 0,
+// and nan_fix restores 0 when the clamp would move it.
+struct CodeClamp {
+    int lo, hi;
+    bool nan_fix;
+};
+
+template <int KIND>
+__device__ __forceinline__ CodeClamp code_clamp(int qmin, int qmax) {
+    int slo = -128, shi = 127;
+    if (KIND == LQ_OUT_QU8 || KIND == LQ_OUT_QU8S8) slo = 0, shi = 255;
+    if (KIND == LQ_OUT_Q16) slo = -32768, shi = 32767;
+    CodeClamp c;
+    c.lo = min(max(qmin, slo), shi);
+    c.hi = max(min(qmax, shi), slo);
+    c.nan_fix = !(c.lo <= 0 && 0 <= c.hi);
+    return c;
+}
+
+template <int KIND>
+__device__ __forceinline__ int32_t requant_int(float y, const EpiParams& p, const CodeClamp& cc) {
+    const float t = y * p.out_inv;
+    const float r = rne(t);
+    const float u = r + p.out_z;
+    int32_t c = min(max(cvt_i32_sat(u), cc.lo), cc.hi);
+    if (cc.nan_fix && u != u) c = 0;
+    return c;
+}
+
 template <int KIND>
 struct OutTraits {
     static constexpr int bytes = (KIND == LQ_OUT_I32 || KIND == LQ_OUT_F32 || KIND == LQ_OUT_FQ32) ? 4

@@ -23,12 +23,11 @@
 
 #include <type_traits>
 
+#include "lq_dma.h"
 #include "lq_epilogue.h"
 #include "lq_internal.h"
 
 namespace lq {
-
-typedef int v4i __attribute__((ext_vector_type(4)));
 
 struct GemmArgs {
     const int8_t* A;
@@ -373,43 +372,6 @@ struct DmaTile {
     static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 };
 
-// LDS slot of logical 16-byte K chunk c in stage row r (tile-local) is c ^ dma_swz(r).  Bits
-// 0-2 of the row spread the 16 lanes of an A fragment (rows r..r+15) over distinct 16-byte
-// bank groups; bit 4 of the row separates the rows 16 apart that one B fragment reads (its
-// rows are permuted, see below).
-__device__ __forceinline__ int dma_swz(int r) { return (r & 7) ^ ((r >> 2) & 4); }
-
-// Requantized codes of the integer output kinds, clamped first to the grid [qmin, qmax] and
-// then to the storage range; lo / hi fold the two clamps into one.  NaN becomes code 0 (the
-// saturating cast of Lucid's Factory.cpp:127-146) whatever the grid: cvt_i32_sat gives 0,
-// and nan_fix restores 0 when the clamp would move it.
-struct CodeClamp {
-    int lo, hi;
-    bool nan_fix;
-};
-
-template <int KIND>
-__device__ __forceinline__ CodeClamp code_clamp(const GemmArgs& a) {
-    int slo = -128, shi = 127;
-    if (KIND == LQ_OUT_QU8 || KIND == LQ_OUT_QU8S8) slo = 0, shi = 255;
-    if (KIND == LQ_OUT_Q16) slo = -32768, shi = 32767;
-    CodeClamp c;
-    c.lo = min(max(a.qmin, slo), shi);
-    c.hi = max(min(a.qmax, shi), slo);
-    c.nan_fix = !(c.lo <= 0 && 0 <= c.hi);
-    return c;
-}
-
-template <int KIND>
-__device__ __forceinline__ int32_t requant_int(float y, const EpiParams& p, const CodeClamp& cc) {
-    const float t = y * p.out_inv;
-    const float r = rne(t);
-    const float u = r + p.out_z;
-    int32_t c = min(max(cvt_i32_sat(u), cc.lo), cc.hi);
-    if (cc.nan_fix && u != u) c = 0;
-    return c;
-}
-
 // --------------------------------------------- LDS-DMA MFMA main loop (large M)
 //
 // The production path for M > 64 when K % 128 == 0.  Global -> LDS copies use the LDS-DMA
@@ -433,43 +395,6 @@ __device__ __forceinline__ int32_t requant_int(float y, const EpiParams& p, cons
 // each of its rows: the epilogue works from registers and stores 16-byte row segments
 // (int8) directly, with no LDS round trip.  The per-column epilogue inputs are loaded
 // before the main loop (they are the oldest loads, so the stage waits cover them).
-
-// s_waitcnt vmcnt(N) only (lgkmcnt and expcnt fields at their no-wait maximum).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// Workgroup barrier without the memory-model fence __syncthreads() adds (that fence waits
-// for every outstanding copy).  It first waits for this wave's own LDS reads (lgkmcnt(0)):
-// after the barrier another wave may copy into the buffer those reads came from.  The
-// copies themselves are covered by wait_vmcnt.  The empty asm keeps the compiler from
-// moving memory accesses across the barrier.
-__device__ __forceinline__ void block_barrier() {
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt fields at maximum
-    __builtin_amdgcn_s_barrier();
-    asm volatile("" ::: "memory");
-}
-
-// Raw buffer descriptor (base, num_records = bytes, stride 0).
-__device__ __forceinline__ v4i buffer_rsrc(const void* base, uint32_t bytes) {
-    const uint64_t b = reinterpret_cast<uint64_t>(base);
-    return v4i{__builtin_amdgcn_readfirstlane((int)(uint32_t)b),
-               __builtin_amdgcn_readfirstlane((int)(uint32_t)(b >> 32)),
-               __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
-}
-
-// 16 bytes per lane from rsrc + voff + soff into LDS at lds_addr + 16 * lane.
-__device__ __forceinline__ void lds_dma16(v4i rsrc, uint32_t voff, uint32_t soff, uint32_t lds_addr) {
-    asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "buffer_load_dwordx4 %1, %2, %3 offen lds"
-        :
-        : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
-        : "memory", "m0");
-}
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, int KIND>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_dma_kernel(GemmArgs a) {
@@ -603,7 +528,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_dma_kernel(Gem
     const bool vec = (reinterpret_cast<uintptr_t>(a.C) % 16 == 0) && ((a.ldc * OB) % 16 == 0) &&
                      (n0 + wn * 64 + 64 <= a.N);
     CodeClamp cc{};
-    if (INT_CODES) cc = code_clamp<KIND>(a);
+    if (INT_CODES) cc = code_clamp<KIND>(a.qmin, a.qmax);
     const bool has_bias = a.bias != nullptr, relu = a.relu != 0;
 #pragma unroll
     for (int j = 0; j < FM; ++j) {

@@ -149,7 +149,9 @@ def test_conv_weight_pack_layout(gpu):
     Cp = 32
     want = np.zeros((10, 3, 2, Cp), np.int8)
     want[..., :20] = w.transpose(0, 2, 3, 1)
-    np.testing.assert_array_equal(wp.numpy().reshape(10, 3, 2, Cp), want)
+    rows = wp.numpy().reshape(10, 256)  # K = 3 * 2 * 32 = 192, rows padded to 256 bytes
+    np.testing.assert_array_equal(rows[:, :192].reshape(10, 3, 2, Cp), want)
+    assert not rows[:, 192:].any()
     np.testing.assert_array_equal(sums.numpy(), w.astype(np.int64).reshape(10, -1).sum(1))
 
 
