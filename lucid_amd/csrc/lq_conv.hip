@@ -66,38 +66,132 @@ struct PackArgs {
     int a_u8s8;
 };
 
-// One thread writes the 16 channels [16j, 16j + 16) of one group at one padded position.
-__global__ __launch_bounds__(256) void conv_pack_input_kernel(PackArgs a) {
-    const int chunks = a.Cp / 16;
-    const int64_t total = (int64_t)a.N * a.Hp * a.Wp * a.G * chunks;
-    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (id >= total) return;
-    const int j = (int)(id % chunks);
-    int64_t r = id / chunks;
-    const int g = (int)(r % a.G);
-    r /= a.G;
-    const int wp = (int)(r % a.Wp);
-    r /= a.Wp;
-    const int hp = (int)(r % a.Hp);
-    const int n = (int)(r / a.Hp);
+// The padded NHWC copy in one launch.  Workgroups [0, tiles) fill the interior as a
+// transpose through LDS: a workgroup takes 256 consecutive positions p of one image plane
+// (the flattened h * W + w, so rows of any width fill the tile) and CV_PCB channels; a lane
+// loads the same dword (4 positions) of 4 consecutive channels, transposes the 4 x 4 bytes in
+// registers (v_perm) and stores 4 channel dwords to LDS; the workgroup then writes 16-byte
+// channel chunks at the padded position of each p.  Channels past Cg take the fill code (the
+// zero point).  The remaining workgroups gather the border positions (rows above / below the
+// image, columns left / right of it) -- or, for planes under half a tile, every padded
+// position: the fill code for zeros padding, else the (reflect / replicate / circular)
+// source, one thread per 16 channels of a position.
+constexpr int CV_PCB = 64;             // channels per interior workgroup
+constexpr int CV_PROW = CV_PCB + 4;    // LDS bytes per position (odd word stride)
+
+struct PackGeom {
+    int tiles;          // interior workgroups per (n, g): positions x channel tiles
+    int ptiles;         // position tiles per plane
+    int pb, pr;         // bottom / right padding
+    int border_cells;   // gathered positions per (n, g) image
+    int all_cells;      // gather every padded position (small planes), no interior tiles
+};
+
+template <bool DWORD>
+__global__ __launch_bounds__(256) void conv_pack_input_kernel(PackArgs a, PackGeom pg) {
+    const int nb = blockIdx.y;
+    const int n = nb / a.G, g = nb - n * a.G;
     const int fill = (a.a_zp ? (int)a.a_zp[0] : 0) - (a.a_u8s8 ? 128 : 0);
-    const int h = pad_index(hp - a.pt, a.H, a.mode);
-    const int w = pad_index(wp - a.pl, a.W, a.mode);
-    uint32_t word[4];
-#pragma unroll
-    for (int q = 0; q < 4; ++q) {
-        uint32_t v = 0;
-#pragma unroll
-        for (int b = 0; b < 4; ++b) {
-            const int c = 16 * j + 4 * q + b;  // channel within the group
-            int code = fill;
-            if (c < a.Cg && h >= 0 && w >= 0)
-                code = a.x[(((int64_t)n * a.C + (int64_t)g * a.Cg + c) * a.H + h) * a.W + w];
-            v |= (uint32_t)(uint8_t)code << (8 * b);
+    const int8_t* plane0 = a.x + ((int64_t)n * a.C + (int64_t)g * a.Cg) * a.H * a.W;
+    if ((int)blockIdx.x >= pg.tiles) {
+        // border positions of image (n, g)
+        const int chunks = a.Cp / 16;
+        const int id = ((int)blockIdx.x - pg.tiles) * 256 + threadIdx.x;
+        if (id >= pg.border_cells * chunks) return;
+        const int j = id % chunks, cell = id / chunks;
+        const int rowcells = (a.pt + pg.pb) * a.Wp;
+        int hp, wp;
+        if (pg.all_cells) {
+            hp = cell / a.Wp;
+            wp = cell - hp * a.Wp;
+        } else if (cell < rowcells) {
+            const int br = cell / a.Wp;
+            hp = br < a.pt ? br : a.pt + a.H + (br - a.pt);
+            wp = cell - br * a.Wp;
+        } else {
+            const int c2 = cell - rowcells, side = a.pl + pg.pr;
+            const int row = c2 / side, k = c2 - row * side;
+            hp = a.pt + row;
+            wp = k < a.pl ? k : a.pl + a.W + (k - a.pl);
         }
-        word[q] = v;
+        const int h = pad_index(hp - a.pt, a.H, a.mode);
+        const int w = pad_index(wp - a.pl, a.W, a.mode);
+        uint32_t word[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            uint32_t v = 0;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const int c = 16 * j + 4 * q + b;
+                int code = fill;
+                if (c < a.Cg && h >= 0 && w >= 0) code = plane0[((int64_t)c * a.H + h) * a.W + w];
+                v |= (uint32_t)(uint8_t)code << (8 * b);
+            }
+            word[q] = v;
+        }
+        const int64_t dst = ((((int64_t)n * a.Hp + hp) * a.Wp + wp) * a.G + g) * a.Cp + 16 * j;
+        *reinterpret_cast<vu4*>(a.xp + dst) = vu4{word[0], word[1], word[2], word[3]};
+        return;
     }
-    reinterpret_cast<vu4*>(a.xp)[id] = vu4{word[0], word[1], word[2], word[3]};
+    __shared__ uint32_t sm[256 * CV_PROW / 4];
+    const int HW = a.H * a.W;
+    const int ct = (int)blockIdx.x / pg.ptiles;
+    const int p0 = ((int)blockIdx.x - ct * pg.ptiles) * 256;
+    const int c0 = ct * CV_PCB;
+    const int cb = min(CV_PCB, a.Cp - c0);  // a multiple of 16
+    const uint32_t fill4 = (uint32_t)(uint8_t)fill * 0x01010101u;
+    const int d = threadIdx.x & 63;  // dword of the tile row: positions p .. p + 3
+    const int p = p0 + 4 * d;
+    constexpr int GROUPS = CV_PCB / 16;  // 4-channel groups per lane, all loads issued first
+    uint32_t v[GROUPS][4];
+#pragma unroll
+    for (int k = 0; k < GROUPS; ++k) {
+        const int rg = (threadIdx.x >> 6) + 4 * k;  // channels 4 rg .. 4 rg + 3 of the tile
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int c = c0 + 4 * rg + e;
+            uint32_t t = fill4;
+            if (4 * rg < cb && c < a.Cg) {
+                const int8_t* src = plane0 + (int64_t)c * HW + p;
+                if (DWORD) {
+                    if (p < HW) t = *reinterpret_cast<const uint32_t*>(src);
+                } else {
+                    t = 0;
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) t |= (uint32_t)(uint8_t)(p + i < HW ? src[i] : (int8_t)0) << (8 * i);
+                }
+            }
+            v[k][e] = t;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < GROUPS; ++k) {
+        const int rg = (threadIdx.x >> 6) + 4 * k;
+        if (4 * rg >= cb) continue;
+        // 4 x 4 byte transpose: row e = channel, byte i = position -> dword i = position
+        const uint32_t ab_lo = __builtin_amdgcn_perm(v[k][1], v[k][0], 0x05010400u);
+        const uint32_t ab_hi = __builtin_amdgcn_perm(v[k][1], v[k][0], 0x07030602u);
+        const uint32_t cd_lo = __builtin_amdgcn_perm(v[k][3], v[k][2], 0x05010400u);
+        const uint32_t cd_hi = __builtin_amdgcn_perm(v[k][3], v[k][2], 0x07030602u);
+        const uint32_t o[4] = {__builtin_amdgcn_perm(cd_lo, ab_lo, 0x05040100u),
+                               __builtin_amdgcn_perm(cd_lo, ab_lo, 0x07060302u),
+                               __builtin_amdgcn_perm(cd_hi, ab_hi, 0x05040100u),
+                               __builtin_amdgcn_perm(cd_hi, ab_hi, 0x07060302u)};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sm[((4 * d + i) * CV_PROW) / 4 + rg] = o[i];
+    }
+    __syncthreads();
+    const int chunks = cb / 16;
+    const int64_t GCp = (int64_t)a.G * a.Cp;
+    for (int j = threadIdx.x; j < 256 * chunks; j += 256) {
+        const int pl = j / chunks, cc = j - pl * chunks;
+        const int pp = p0 + pl;
+        if (pp >= HW) continue;
+        const int h = pp / a.W, w = pp - h * a.W;
+        const uint32_t* q = sm + (pl * CV_PROW) / 4 + 4 * cc;
+        const int64_t dst = (((int64_t)n * a.Hp + h + a.pt) * a.Wp + w + a.pl) * GCp + (int64_t)g * a.Cp + c0 + cc * 16;
+        *reinterpret_cast<vu4*>(a.xp + dst) = vu4{q[0], q[1], q[2], q[3]};
+    }
 }
 
 // One thread per 16-byte chunk of a packed weight row w_p[co][k], k = (kh * KW + kw) * Cp + c,
@@ -702,8 +796,20 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
     pa.mode = padding_mode;
     pa.a_zp = d_a_zero_point;
     pa.a_u8s8 = x_code_type == LQ_U8S8;
-    const int64_t pchunks = N * Hp * Wp * groups * (Cp / 16);
-    hipLaunchKernelGGL(conv_pack_input_kernel, dim3((unsigned)((pchunks + 255) / 256)), dim3(256), 0, st, pa);
+    LQ_REQUIRE(N * groups <= 65535, "lq_conv2d_i8: N * groups must be <= 65535");
+    PackGeom pg{};
+    pg.pb = pad_bottom;
+    pg.pr = pad_right;
+    pg.all_cells = H * W < 128;  // a plane under half a tile: gather every position
+    pg.ptiles = pg.all_cells ? 0 : (int)((H * W + 255) / 256);
+    pg.tiles = pg.ptiles * (int)((Cp + CV_PCB - 1) / CV_PCB);
+    pg.border_cells = pg.all_cells ? (int)(Hp * Wp) : (int)((pad_top + pad_bottom) * Wp + H * (pad_left + pad_right));
+    const int bblocks = (int)((pg.border_cells * (Cp / 16) + 255) / 256);
+    const dim3 pgrid((unsigned)(pg.tiles + bblocks), (unsigned)(N * groups));
+    if ((H * W) % 4 == 0 && (reinterpret_cast<uintptr_t>(d_x) & 3) == 0)
+        hipLaunchKernelGGL(conv_pack_input_kernel<true>, pgrid, dim3(256), 0, st, pa, pg);
+    else
+        hipLaunchKernelGGL(conv_pack_input_kernel<false>, pgrid, dim3(256), 0, st, pa, pg);
 
     ConvArgs a{};
     a.xp = pa.xp;
