@@ -155,9 +155,11 @@ def weight_only_lines(L, C, gtimer):
         y = L.empty((M, N), np.float32, "gpu")
         s = L.tensor(rng.uniform(1e-3, 1e-1, N).astype(np.float32), device="gpu")
         b = L.tensor(rng.standard_normal(N).astype(np.float32), device="gpu")
+        ws_bytes = lib.lq_gemv_w8_workspace_size(M, N, K)
+        ws = L.empty((max(ws_bytes, 1),), np.uint8, "gpu")
         calls = [lambda st, r=r: C.check(lib.lq_gemv_w8(x.data_ptr(), C.F32, K, W.data_ptr() + r * N * K, K,
                                                         s.data_ptr(), None, b.data_ptr(), y.data_ptr(),
-                                                        N, M, N, K, 0, None, 0, st), "lq_gemv_w8")
+                                                        N, M, N, K, 0, ws.data_ptr(), ws_bytes, st), "lq_gemv_w8")
                  for r in range(rot)]
         ms = gtimer.time_ms(calls, 10, 2)
         nbytes = N * K + 8.0 * N + 4.0 * M * (K + N)
@@ -179,10 +181,12 @@ def weight_only_lines(L, C, gtimer):
             bi = L.tensor(np.full(rot * N * G, -0.1, np.float32), device="gpu")
             x = L.tensor(rng.standard_normal((M, K)).astype(np.float32), device="gpu")
             y = L.empty((M, N), np.float32, "gpu")
+            ws_bytes = lib.lq_group_matmul_workspace_size(M, N, K, gs)
+            ws = L.empty((max(ws_bytes, 1),), np.uint8, "gpu")
             calls = [lambda st, r=r: C.check(lib.lq_group_matmul(
                 x.data_ptr(), C.F32, K, P.data_ptr() + r * wbytes, sc.data_ptr() + 4 * r * N * G,
-                bi.data_ptr() + 4 * r * N * G, None, y.data_ptr(), N, M, N, K, gs, bits, 1, 0, None, 0,
-                st), "lq_group_matmul") for r in range(rot)]
+                bi.data_ptr() + 4 * r * N * G, None, y.data_ptr(), N, M, N, K, gs, bits, 1, 0,
+                ws.data_ptr(), ws_bytes, st), "lq_group_matmul") for r in range(rot)]
             ms = gtimer.time_ms(calls, 10, 2)
             nbytes = wbytes + 8.0 * N * G + 4.0 * M * (K + N)
             gbs = nbytes / (ms * 1e-3) / 1e9

@@ -277,8 +277,10 @@ int lq_row_sums_i8(const int8_t* d_X, int64_t ld, int64_t rows, int64_t K, int32
  * (lucid/nn/quantized/linear.py:206-210 -> lucid/_C/nn/Linear.cpp:199), without forming
  * the float weight.  x / y of x_dtype (LQ_F32 or LQ_F16), W int8 [N, ldw] row-major,
  * d_w_zero_point / d_bias may be NULL.  Float32 accumulation (tolerance parity: the float
- * GEMM's summation order is the reference's own).  Any M; tuned for M <= 16.  Needs
- * lq_gemv_w8_workspace_size(M, N, K) bytes of device workspace. */
+ * GEMM's summation order is the reference's own).  Any M; tuned for M <= 16.  With
+ * lq_gemv_w8_workspace_size(M, N, K) bytes of device workspace (16-byte aligned; 0 for M <= 2)
+ * float32 activations are split into fp16 halves once per call instead of once per
+ * workgroup; without it (NULL) the call still runs, with identical results. */
 size_t lq_gemv_w8_workspace_size(int64_t M, int64_t N, int64_t K);
 int lq_gemv_w8(const void* d_x, int x_dtype, int64_t ldx, const int8_t* d_W, int64_t ldw,
                const float* d_w_scale, const float* d_w_zero_point, const float* d_bias,
@@ -303,7 +305,8 @@ int lq_group_dequantize_f32(const uint32_t* d_packed, const float* d_scales,
  * (LQ_F32 or LQ_F16), float32 accumulation, without forming w_hat.  Replaces
  * _C_engine.quantized.quantized_matmul (QuantizedMatmul.cpp:143-163) for transpose = 1;
  * transpose = 0 returns LQ_ERR_UNSUPPORTED.  d_biases (group offsets) and d_bias (layer
- * bias) may be NULL.  Needs lq_group_matmul_workspace_size(M, N, K, group_size) bytes. */
+ * bias) may be NULL.  lq_group_matmul_workspace_size(M, N, K, group_size) bytes of workspace
+ * let float32 activations be split once per call (as for lq_gemv_w8; NULL still runs). */
 size_t lq_group_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int group_size);
 int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d_packed,
                     const float* d_scales, const float* d_biases, const float* d_bias, void* d_y,

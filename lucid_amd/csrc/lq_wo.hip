@@ -21,8 +21,10 @@
 // Work split.  A workgroup of W waves owns 16 weight rows and one 16-row block of the
 // activations; its waves split K into equal runs of k-blocks (32*S k each, S = MFMA steps
 // per block) and stream their weight bytes with two blocks in flight.  The W partial sums
-// meet in LDS and are added in wave order (deterministic), then the epilogue runs.  One
-// launch per call, no workspace, no cross-workgroup synchronisation.
+// meet in LDS and are added in wave order (deterministic), then the epilogue runs.  No
+// cross-workgroup synchronisation.  With a workspace, float32 activations are split into
+// their hi / lo halves once per call (wo_xprep_kernel) instead of once per workgroup; the
+// products and sums are the same either way.
 //
 // K order inside a k-block: lane q (= l/16) of every step covers 8 consecutive k of its own
 // 8*S-wide quarter, so a block stays inside one weight group (group size 32*S) and a lane's
@@ -111,6 +113,8 @@ struct WoArgs {
     int M, N, K;
     int G;                   // groups per row (group-wise)
     int bpw;                 // k-blocks per wave (even; blocks past the last are zero work)
+    const vu4* xp;           // pre-split activations (wo_xprep_kernel) or null
+    const float2* xm;        // per (row, k-block) {2^-e, block sum} of the pre-split activations
 };
 
 // A lane's weight bytes for one k-block: 8*S codes from k = kc.
@@ -213,7 +217,62 @@ __device__ __forceinline__ float x_at(const XChunk<S, XF32>& xc, int i) {
     }
 }
 
-template <int BITS, bool SIGNED, int S, bool XF32, bool GROUPED, bool VEC>
+// A lane's pre-split activations for one k-block: S steps of (hi, lo) halves, and the
+// row's {2^-e, block sum}.
+template <int S>
+struct PChunk {
+    vu4 v[2 * S];
+    float2 meta;
+};
+
+// The float32 activation split of wo_gemv_kernel done once per call instead of once per
+// workgroup: one wave per (16-row tile, k-block), lanes laid out as the GEMV's (q = l / 16
+// owns 8 S consecutive k of the block, l % 16 the row).  Same zero fill (rows past M, k past
+// K), same max / sum shuffles, same power-of-two pre-scale and hi / lo split in the same
+// element order, so the GEMV's products and sums are unchanged.  Layout: block (mt, t) holds
+// 64 lanes x 2 S vu4 (hi, lo per step); meta (mt, t, row).
+template <int BITS, int S>
+__global__ __launch_bounds__(64) void wo_xprep_kernel(const float* __restrict__ x, int64_t ldx, int M, int K, int TW,
+                                                      vu4* __restrict__ xp, float2* __restrict__ xm) {
+    constexpr int NX = 8 * S;
+    const int t = blockIdx.x, mt = blockIdx.y;
+    const int lane = threadIdx.x, q = lane >> 4, l16 = lane & 15;
+    const int m = mt * 16 + l16;
+    const int kc = t * 32 * S + q * 8 * S;
+    float xs[NX];
+    float amax = 0.0f, bsum = 0.0f;
+#pragma unroll
+    for (int i = 0; i < NX; ++i) {
+        const int k = kc + i;
+        xs[i] = (m < M && k < K) ? x[(int64_t)m * ldx + k] : 0.0f;
+        amax = fmaxf(amax, fabsf(xs[i]));
+        bsum += xs[i];
+    }
+    amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+    amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+    bsum += __shfl_xor(bsum, 16, 64);
+    bsum += __shfl_xor(bsum, 32, 64);
+    int e = 0;
+    if (amax > 0.0f && amax <= 3.0e38f) e = min(max(14 - ilogbf(amax), -120), 120);
+    const float up = ldexpf(1.0f, e);
+    vu4* dst = xp + ((int64_t)(mt * TW + t) * 64 + lane) * 2 * S;
+#pragma unroll
+    for (int j = 0; j < S; ++j) {
+        h8 hi, lo;
+#pragma unroll
+        for (int h = 0; h < 8; ++h) {
+            const float v = xs[8 * j + korder<BITS>(h)] * up;
+            const _Float16 vh = (_Float16)v;
+            hi[h] = vh;
+            lo[h] = (_Float16)(v - (float)vh);
+        }
+        dst[2 * j] = __builtin_bit_cast(vu4, hi);
+        dst[2 * j + 1] = __builtin_bit_cast(vu4, lo);
+    }
+    if (q == 0) xm[(int64_t)(mt * TW + t) * 16 + l16] = make_float2(ldexpf(1.0f, -e), bsum);
+}
+
+template <int BITS, bool SIGNED, int S, bool XF32, bool GROUPED, bool VEC, bool PREP = false>
 __global__ __launch_bounds__((64 * wo_max_waves(S, XF32, GROUPED))) void wo_gemv_kernel(WoArgs a) {
     constexpr int NW = WChunk<BITS, S>::NW;
     constexpr int NX = 8 * S;
@@ -248,15 +307,45 @@ __global__ __launch_bounds__((64 * wo_max_waves(S, XF32, GROUPED))) void wo_gemv
     f4 acc = f4{0.f, 0.f, 0.f, 0.f};
     float xtot = 0.0f;
 
-    auto load_block = [&](WChunk<BITS, S>& wc, XChunk<S, XF32>& xc, int t) {
+    using XC = std::conditional_t<PREP, PChunk<S>, XChunk<S, XF32>>;
+    auto load_block = [&](WChunk<BITS, S>& wc, XC& xc, int t) {
         const int kc = t * 32 * S + q * 8 * S;
         load_w<BITS, S, VEC>(wc, wrow, kc, a.K);
-        load_x<S, XF32, VEC>(xc, xrow, row_ok, kc, a.K);
+        if constexpr (PREP) {
+            const int64_t blk = (int64_t)blockIdx.y * TW + t;
+            const vu4* src = a.xp + (blk * 64 + lane) * 2 * S;
+#pragma unroll
+            for (int i = 0; i < 2 * S; ++i) xc.v[i] = src[i];
+            xc.meta = a.xm[blk * 16 + l16];
+        } else {
+            load_x<S, XF32, VEC>(xc, xrow, row_ok, kc, a.K);
+        }
         // keep the prefetch where it is: the scheduler would otherwise sink these loads to
         // their first use and wait on them at once
         __builtin_amdgcn_sched_barrier(0);
     };
-    auto compute_block = [&](const WChunk<BITS, S>& wc, const XChunk<S, XF32>& xc, int t) {
+    auto compute_prep = [&](const WChunk<BITS, S>& wc, const PChunk<S>& xc, int t) {
+        f4 blk = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < S; ++j) {
+            const h8 wa = unpack_step<BITS, SIGNED>(&wc.w[j * NW / S]);
+            blk = mfma16(wa, __builtin_bit_cast(h8, xc.v[2 * j]), blk);
+            blk = mfma16(wa, __builtin_bit_cast(h8, xc.v[2 * j + 1]), blk);
+        }
+        const float down = xc.meta.x, bsum = xc.meta.y;
+        if constexpr (GROUPED) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int rl = 4 * q + i;
+                acc[i] += sc_lds[rl * TW + t] * (blk[i] * down) + bi_lds[rl * TW + t] * bsum;
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[i] += blk[i] * down;
+            xtot += bsum;
+        }
+    };
+    auto compute_raw = [&](const WChunk<BITS, S>& wc, const XChunk<S, XF32>& xc, int t) {
         // the block's pre-scale for this lane's row, shared by the 4 lanes of the row
         float xs[NX];
         float amax = 0.0f, bsum = 0.0f;
@@ -309,10 +398,14 @@ __global__ __launch_bounds__((64 * wo_max_waves(S, XF32, GROUPED))) void wo_gemv
     // WO_RING - 1 younger blocks in flight
     // (the predicated scalar loads of !VEC keep one block at a time: their registers would
     // not fit a ring)
+    auto compute_block = [&](const WChunk<BITS, S>& wc, const XC& xc, int t) {
+        if constexpr (PREP) compute_prep(wc, xc, t);
+        else compute_raw(wc, xc, t);
+    };
     constexpr int RING = VEC ? WO_RING : 1;
     const int t0 = wave * a.bpw;
     WChunk<BITS, S> wr[RING];
-    XChunk<S, XF32> xr[RING];
+    XC xr[RING];
 #pragma unroll
     for (int j = 0; j < RING; ++j) load_block(wr[j], xr[j], t0 + j);
     int g = 0;
@@ -667,11 +760,28 @@ WoPlan wo_plan(int64_t K, int S, bool grouped, int maxw) {
     return p;
 }
 
+// Workspace bytes of the pre-split activations: per 16-row tile and k-block, 64 lanes x 2 S
+// vu4 plus 16 {2^-e, block sum} pairs.
+size_t wo_prep_bytes(int64_t M, const WoPlan& p, int S) {
+    const int64_t blocks = (M + 15) / 16 * (int64_t)p.W * p.bpw;
+    return (size_t)blocks * (64 * 2 * S * sizeof(vu4) + 16 * sizeof(float2));
+}
+
 template <int BITS, bool SIGNED, int S, bool GROUPED, bool VEC>
-int launch_wo(const WoPlan& p, const WoArgs& a, bool xf32, hipStream_t st) {
+int launch_wo(const WoPlan& p, WoArgs a, bool xf32, hipStream_t st, void* ws, size_t ws_bytes) {
     const dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)((a.M + 15) / 16));
     const dim3 block(64 * p.W);
-    if (xf32)
+    const int TW = p.W * p.bpw;
+    if (xf32 && ws && ws_bytes >= wo_prep_bytes(a.M, p, S) && aligned16(ws)) {
+        // split the activations once, then every workgroup reads the halves
+        vu4* xp = static_cast<vu4*>(ws);
+        float2* xm = reinterpret_cast<float2*>(xp + (int64_t)(a.M + 15) / 16 * TW * 64 * 2 * S);
+        hipLaunchKernelGGL((wo_xprep_kernel<BITS, S>), dim3((unsigned)TW, (unsigned)((a.M + 15) / 16)), dim3(64), 0,
+                           st, static_cast<const float*>(a.x), a.ldx, a.M, a.K, TW, xp, xm);
+        a.xp = xp;
+        a.xm = xm;
+        hipLaunchKernelGGL((wo_gemv_kernel<BITS, SIGNED, S, true, GROUPED, VEC, true>), grid, block, p.lds, st, a);
+    } else if (xf32)
         hipLaunchKernelGGL((wo_gemv_kernel<BITS, SIGNED, S, true, GROUPED, VEC>), grid, block, p.lds, st, a);
     else
         hipLaunchKernelGGL((wo_gemv_kernel<BITS, SIGNED, S, false, GROUPED, VEC>), grid, block, p.lds, st, a);
@@ -741,15 +851,15 @@ using namespace lq;
 extern "C" {
 
 size_t lq_gemv_w8_workspace_size(int64_t M, int64_t N, int64_t K) {
-    (void)M; (void)N; (void)K;
-    return 0;
+    (void)N;
+    if (M <= 2 || K <= 0 || M >= WO_MAX_DIM || K >= WO_MAX_DIM) return 0;  // VALU path: no split
+    return wo_prep_bytes(M, wo_plan(K, 2, false, wo_max_waves(2, true, false)), 2);
 }
 
 int lq_gemv_w8(const void* d_x, int x_dtype, int64_t ldx, const int8_t* d_W, int64_t ldw,
                const float* d_w_scale, const float* d_w_zero_point, const float* d_bias,
                void* d_y, int64_t ldy, int64_t M, int64_t N, int64_t K, int flags,
                void* d_workspace, size_t workspace_bytes, void* stream) {
-    (void)d_workspace; (void)workspace_bytes;
     LQ_REQUIRE(M >= 0 && N >= 0 && K >= 0 && M < WO_MAX_DIM && N < WO_MAX_DIM && K < WO_MAX_DIM,
                "lq_gemv_w8: bad shape");
     LQ_REQUIRE(x_dtype == LQ_F32 || x_dtype == LQ_F16, "lq_gemv_w8: x_dtype must be LQ_F32 or LQ_F16");
@@ -784,14 +894,17 @@ int lq_gemv_w8(const void* d_x, int x_dtype, int64_t ldx, const int8_t* d_W, int
     }
     const bool vec = aligned16(d_W) && ldw % 16 == 0 && K % 16 == 0 && K >= 16 && aligned16(d_x) &&
                      ldx % (xf32 ? 4 : 8) == 0;
-    if (vec) launch_wo<8, true, 2, false, true>(p, a, xf32, st);
-    else launch_wo<8, true, 2, false, false>(p, a, xf32, st);
+    if (vec) launch_wo<8, true, 2, false, true>(p, a, xf32, st, d_workspace, workspace_bytes);
+    else launch_wo<8, true, 2, false, false>(p, a, xf32, st, d_workspace, workspace_bytes);
     return launch_status("lq_gemv_w8");
 }
 
 size_t lq_group_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int group_size) {
-    (void)M; (void)N; (void)K; (void)group_size;
-    return 0;
+    (void)N;
+    if (M <= 2 || K <= 0 || M >= WO_MAX_DIM || K >= WO_MAX_DIM) return 0;
+    if (group_size != 32 && group_size != 64 && group_size != 128) return 0;
+    const int S = group_size / 32;
+    return wo_prep_bytes(M, wo_plan(K, S, true, wo_max_waves(S, true, true)), S);
 }
 
 int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d_packed,
@@ -799,7 +912,6 @@ int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d
                     int64_t ldy, int64_t M, int64_t N, int64_t K, int group_size, int bits,
                     int transpose, int flags, void* d_workspace, size_t workspace_bytes,
                     void* stream) {
-    (void)d_workspace; (void)workspace_bytes;
     LQ_REQUIRE(M >= 0 && N >= 0 && K > 0 && M < WO_MAX_DIM && N < WO_MAX_DIM && K < WO_MAX_DIM,
                "lq_group_matmul: bad shape");
     LQ_REQUIRE(group_size == 32 || group_size == 64 || group_size == 128,
@@ -847,8 +959,8 @@ int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d
     const bool vec = aligned16(d_x) && ldx % (xf32 ? 4 : 8) == 0;
 #define LQ_GM(B, SS)                                                          \
     do {                                                                      \
-        if (vec) launch_wo<B, false, SS, true, true>(p, a, xf32, st);         \
-        else launch_wo<B, false, SS, true, false>(p, a, xf32, st);            \
+        if (vec) launch_wo<B, false, SS, true, true>(p, a, xf32, st, d_workspace, workspace_bytes);  \
+        else launch_wo<B, false, SS, true, false>(p, a, xf32, st, d_workspace, workspace_bytes);     \
     } while (0)
     if (bits == 8) {
         if (S == 1) LQ_GM(8, 1); else if (S == 2) LQ_GM(8, 2); else LQ_GM(8, 4);

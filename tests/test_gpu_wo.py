@@ -106,6 +106,36 @@ def test_gemv_w8_fp16(gpu, M, N, K):
     _close(got, ref, mag, half=True)
 
 
+@pytest.mark.parametrize("M,N,K", [(3, 64, 256), (16, 4096, 4096), (37, 300, 784), (9, 50, 1000)])
+def test_gemv_w8_presplit_matches_inline(gpu, M, N, K):
+    """With a workspace the fp32 activations are split into fp16 halves once per call; the
+    products and their order are those of the split done inside every workgroup, so both
+    calls agree bit for bit (with rows of very different magnitude to exercise the
+    per-block pre-scale)."""
+    from lucid_amd import _C
+
+    rng = np.random.default_rng(M * 7 + K)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[0] *= 1e-20
+    x[-1] *= 1e20
+    W = rng.integers(-128, 128, (N, K)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-1, N).astype(np.float32)
+    z = rng.integers(-3, 4, N).astype(np.float32)
+    ws_bytes = _C.lib().lq_gemv_w8_workspace_size(M, N, K)
+    assert ws_bytes > 0
+    xd, dW, ds, dz = _t(gpu, x), _t(gpu, W), _t(gpu, s), _t(gpu, z)
+    outs = []
+    for wsb in (ws_bytes, 0):
+        ws = gpu.empty((max(wsb, 1),), np.uint8, "gpu")
+        y = gpu.empty((M, N), np.float32, "gpu")
+        _C.call("lq_gemv_w8", xd.data_ptr(), _C.F32, K, dW.data_ptr(), K, ds.data_ptr(), dz.data_ptr(), None,
+                y.data_ptr(), N, M, N, K, 0, ws.data_ptr() if wsb else None, wsb, None)
+        outs.append(y.numpy())
+    np.testing.assert_array_equal(outs[0], outs[1])
+    ref, mag = _gemv_ref(x, W, s, z=z)
+    _close(outs[0], ref, mag)
+
+
 def test_gemv_w8_tiny_and_huge_rows(gpu):
     """Per-row pre-scaling: rows of very different magnitude in one call."""
     rng = np.random.default_rng(3)
@@ -169,6 +199,34 @@ def test_quantized_matmul_parity(gpu, bits, gs, M):
     mag = np.abs(x.astype(np.float64)) @ np.abs(wd).T
     assert np.max(np.abs(y - ref)) / max(np.max(np.abs(ref)), 1e-12) <= 1e-4
     _close(y, ref, mag)
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+def test_group_matmul_presplit_matches_inline(gpu, bits, gs):
+    """The once-per-call activation split (workspace given) against the in-workgroup split
+    (no workspace): bit for bit."""
+    from lucid_amd import _C
+    from lucid_amd.quantization import _qgemm
+
+    rng = np.random.default_rng(bits * 3 + gs)
+    M, N, K = 19, 200, 1024
+    w = rng.standard_normal((N, K)).astype(np.float32)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[1] *= 1e-15
+    packed, scales, biases = _qgemm.quantize(_t(gpu, w), group_size=gs, bits=bits)
+    ws_bytes = _C.lib().lq_group_matmul_workspace_size(M, N, K, gs)
+    assert ws_bytes > 0
+    xd = _t(gpu, x)
+    outs = []
+    for wsb in (ws_bytes, 0):
+        ws = gpu.empty((max(wsb, 1),), np.uint8, "gpu")
+        y = gpu.empty((M, N), np.float32, "gpu")
+        _C.call("lq_group_matmul", xd.data_ptr(), _C.F32, K, packed.data_ptr(), scales.data_ptr(),
+                biases.data_ptr(), None, y.data_ptr(), N, M, N, K, gs, bits, 1, 0,
+                ws.data_ptr() if wsb else None, wsb, None)
+        outs.append(y.numpy())
+    np.testing.assert_array_equal(outs[0], outs[1])
 
 
 @pytest.mark.parametrize("M,N,K,bits,gs", [(1, 4096, 4096, 4, 64), (16, 11008, 4096, 8, 64),
