@@ -355,8 +355,17 @@ def bandwidth_lines(L, C, timer, steps, warmup):
         lib.lq_dequantize_per_tensor(qp, C.I8, yp, C.F32, n, scale.data_ptr(), zp.data_ptr(), 0.0,
                                      0.0, None)
 
+    def qhardswish():  # nnq.Hardswish over float input: activation + grid codes in one pass
+        lib.lq_qact(C.ACT_HARDSWISH, xp, C.F32, None, None, n, 0.0, scale.data_ptr(), zp.data_ptr(), -128,
+                    127, C.I8, qp, None)
+
+    def qsigmoid_codes():  # nnq.Sigmoid over the int8 codes of a quantized layer's output
+        lib.lq_qact(C.ACT_SIGMOID, qp, C.I8, scale.data_ptr(), zp.data_ptr(), n, 0.0, scale.data_ptr(),
+                    zp.data_ptr(), -128, 127, C.I8, yp, None)
+
     for name, fn, bpe in (("minmax_observer", obs, 4), ("quantize_f32_to_i8", quant, 5),
-                          ("dequantize_i8_to_f32", dequant, 5)):
+                          ("dequantize_i8_to_f32", dequant, 5), ("qhardswish_f32_to_i8", qhardswish, 5),
+                          ("qsigmoid_i8_to_i8", qsigmoid_codes, 2)):
         ms = timer.time_ms(fn, max(steps // 5, 5), max(warmup // 5, 2))
         gbs = n * bpe / (ms * 1e-3) / 1e9
         out[name] = {"n": n, "bytes_per_elem": bpe, "us": round(ms * 1e3, 1),

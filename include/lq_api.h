@@ -334,6 +334,26 @@ int lq_qmerge(int op, const void* d_a, int a_type, const float* d_a_scale, const
               const float* d_out_zero_point, int qmin, int qmax, int flags, int out_type, void* d_out,
               void* stream);
 
+/* ---- activations (float and quantized) ------------------------------------------ */
+/* Activations of lq_qact. */
+enum { LQ_ACT_SIGMOID = 0, LQ_ACT_TANH = 1, LQ_ACT_HARDSWISH = 2, LQ_ACT_HARDSIGMOID = 3, LQ_ACT_ELU = 4,
+       LQ_ACT_LEAKY_RELU = 5 };
+/* y[i] = act(x[i]) over n contiguous elements: the float activations F.sigmoid / tanh /
+ * hardswish / hardsigmoid / elu / leaky_relu (lucid/_C/backend/cpu/methods/Activation.cpp:8-50,
+ * 375-460, 661-751; Unary.cpp:165-170) with out_type LQ_F32, and the quantized activations
+ * nnq.Sigmoid / Tanh / Hardswish / Hardsigmoid / ELU / LeakyReLU
+ * (lucid/nn/quantized/activation.py:20-475: the activation, then fake-quantize) with a code
+ * out_type (LQ_I8 / LQ_U8 / LQ_I16 / LQ_U8S8) on [qmin, qmax] with d_out_scale /
+ * d_out_zero_point (clip(rne(t * fl32(1 / S)) + Z), NaN -> 0).  param is ELU's alpha or
+ * LeakyReLU's negative_slope (as float32), ignored otherwise.  x is float32 (LQ_F32) or codes
+ * with a per-tensor grid, read as fl32(fl32(float(c) - z) * s) (d_x_scale required,
+ * d_x_zero_point NULL = 0).  Replaces _C_engine.sigmoid / tanh / hard_swish / hard_sigmoid /
+ * elu / leaky_relu (lucid/nn/functional/activations.py:99-579) followed, for the quantized
+ * modules, by the fake-quantize of _QuantizedGridModule (lucid/nn/quantized/_utils.py:29-45). */
+int lq_qact(int op, const void* d_x, int x_type, const float* d_x_scale, const float* d_x_zero_point,
+            int64_t n, float param, const float* d_out_scale, const float* d_out_zero_point, int qmin,
+            int qmax, int out_type, void* d_y, void* stream);
+
 /* ---- int8 Conv2d (implicit GEMM) ------------------------------------------------- */
 /* Padding modes of a convolution (Lucid's padding_mode, lucid/nn/functional/conv.py:24-29). */
 enum { LQ_PAD_ZEROS = 0, LQ_PAD_REFLECT = 1, LQ_PAD_REPLICATE = 2, LQ_PAD_CIRCULAR = 3 };

@@ -2,17 +2,23 @@
 
 from lucid_amd.nn.module import Module, Parameter
 from lucid_amd.nn.layers import (
+    ELU,
     BatchNorm2d,
     Conv2d,
     Flatten,
+    Hardsigmoid,
+    Hardswish,
     Identity,
+    LeakyReLU,
     Linear,
     ReLU,
     Sequential,
+    Sigmoid,
+    Tanh,
 )
 
 __all__ = ["Module", "Parameter", "Linear", "Conv2d", "ReLU", "Sequential", "Identity",
-           "BatchNorm2d", "Flatten"]
+           "BatchNorm2d", "Flatten", "Sigmoid", "Tanh", "Hardswish", "Hardsigmoid", "ELU", "LeakyReLU"]
 
 
 def __getattr__(name: str):

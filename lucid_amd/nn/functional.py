@@ -119,3 +119,50 @@ def batch_norm_eval(x: Tensor, running_mean: Tensor, running_var: Tensor, weight
             args[1].data_ptr(), args[2].data_ptr() if args[2] is not None else None,
             args[3].data_ptr() if args[3] is not None else None, float(np.float32(eps)), None)
     return y
+
+
+def _activation(x: Tensor, op: int, param: float, name: str) -> Tensor:
+    """One float activation over ``x`` (lq_qact, float32 out); a code-backed input is read
+    through its codes."""
+    from lucid_amd.nn.quantized.functional_module import _operand
+
+    ptr, xtype, xs, xz = _operand(x, name)
+    y = empty(x.shape, float32, "gpu")
+    if x.numel():
+        _C.call("lq_qact", op, ptr, xtype, xs, xz, x.numel(), param, None, None, 0, 0, _C.F32,
+                y.data_ptr(), None)
+    return y
+
+
+def sigmoid(x: Tensor) -> Tensor:
+    """``1 / (1 + exp(-x))`` (lucid/nn/functional/activations.py:498-534)."""
+    return _activation(x, _C.ACT_SIGMOID, 0.0, "sigmoid")
+
+
+def tanh(x: Tensor) -> Tensor:
+    """``tanh(x)`` (activations.py:537-579)."""
+    return _activation(x, _C.ACT_TANH, 0.0, "tanh")
+
+
+def hardswish(x: Tensor) -> Tensor:
+    """``x * min(max((x + 3) / 6, 0), 1)`` (activations.py:399-446)."""
+    return _activation(x, _C.ACT_HARDSWISH, 0.0, "hardswish")
+
+
+def hardsigmoid(x: Tensor) -> Tensor:
+    """``min(max((x + 3) / 6, 0), 1)`` (activations.py:449-495)."""
+    return _activation(x, _C.ACT_HARDSIGMOID, 0.0, "hardsigmoid")
+
+
+def elu(x: Tensor, alpha: float = 1.0) -> Tensor:
+    """``x >= 0 ? x : alpha * (exp(x) - 1)``, alpha rounded to float32 (activations.py:148-195)."""
+    import numpy as np
+
+    return _activation(x, _C.ACT_ELU, float(np.float32(alpha)), "elu")
+
+
+def leaky_relu(x: Tensor, negative_slope: float = 0.01) -> Tensor:
+    """``x >= 0 ? x : negative_slope * x``, the slope rounded to float32 (activations.py:99-145)."""
+    import numpy as np
+
+    return _activation(x, _C.ACT_LEAKY_RELU, float(np.float32(negative_slope)), "leaky_relu")

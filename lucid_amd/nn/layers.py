@@ -1,6 +1,7 @@
 """Float layers a quantized model starts from (the ``nn.Linear`` / ``nn.Conv2d`` /
 ``nn.ReLU`` / ``nn.BatchNorm2d`` / ``nn.Sequential`` inputs of ``prepare``, ``convert``
-and ``quantize_dynamic``).
+and ``quantize_dynamic``, and the activations ``convert`` swaps for quantized ones:
+``nn.Sigmoid`` / ``Tanh`` / ``Hardswish`` / ``Hardsigmoid`` / ``ELU`` / ``LeakyReLU``).
 
 Attribute names and parameter shapes follow Lucid's float modules (``weight``
 ``[out, in]`` / ``[Cout, Cin/groups, kh, kw]``, ``bias``, BatchNorm's ``running_mean`` /
@@ -102,6 +103,50 @@ class Conv2d(Module):
 class ReLU(Module):
     def forward(self, x: Tensor) -> Tensor:
         return F.relu(x)
+
+
+class Sigmoid(Module):
+    def forward(self, x: Tensor) -> Tensor:
+        return F.sigmoid(x)
+
+
+class Tanh(Module):
+    def forward(self, x: Tensor) -> Tensor:
+        return F.tanh(x)
+
+
+class Hardswish(Module):
+    def forward(self, x: Tensor) -> Tensor:
+        return F.hardswish(x)
+
+
+class Hardsigmoid(Module):
+    def forward(self, x: Tensor) -> Tensor:
+        return F.hardsigmoid(x)
+
+
+class ELU(Module):
+    def __init__(self, alpha: float = 1.0) -> None:
+        super().__init__()
+        self.alpha = alpha
+
+    def forward(self, x: Tensor) -> Tensor:
+        return F.elu(x, self.alpha)
+
+    def extra_repr(self) -> str:
+        return f"alpha={self.alpha}"
+
+
+class LeakyReLU(Module):
+    def __init__(self, negative_slope: float = 0.01) -> None:
+        super().__init__()
+        self.negative_slope = negative_slope
+
+    def forward(self, x: Tensor) -> Tensor:
+        return F.leaky_relu(x, self.negative_slope)
+
+    def extra_repr(self) -> str:
+        return f"negative_slope={self.negative_slope}"
 
 
 class Identity(Module):

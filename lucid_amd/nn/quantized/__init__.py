@@ -4,9 +4,11 @@
 The int8 layers keep Lucid's buffers and ``state_dict`` layout and run the gfx950 W8A8
 MFMA GEMM over integer codes; ``QuantStub`` / ``DeQuantStub`` / ``Quantize`` /
 ``DeQuantize`` / ``QuantWrapper`` mark the quantized region; ``FloatFunctional`` /
-``QFunctional`` carry residual adds and concatenations onto one grid.
+``QFunctional`` carry residual adds and concatenations onto one grid; ``Sigmoid`` /
+``Hardswish`` / ``Hardsigmoid`` / ``Tanh`` / ``ELU`` / ``LeakyReLU`` requantize activations.
 """
 
+from lucid_amd.nn.quantized.activation import ELU, Hardsigmoid, Hardswish, LeakyReLU, Sigmoid, Tanh
 from lucid_amd.nn.quantized.conv import Conv2d
 from lucid_amd.nn.quantized.functional_module import FloatFunctional, QFunctional
 from lucid_amd.nn.quantized.intrinsic import ConvReLU2d, LinearReLU
@@ -16,7 +18,8 @@ from lucid_amd.nn.quantized.modules import (DeQuantize, DeQuantStub, Quantize, Q
                                             QuantWrapper)
 
 __all__ = ["Linear", "QuantizedLinearMLX", "Conv2d", "ConvReLU2d", "LinearReLU", "QuantStub", "DeQuantStub", "Quantize", "DeQuantize",
-           "QuantWrapper", "FloatFunctional", "QFunctional"]
+           "QuantWrapper", "FloatFunctional", "QFunctional", "Sigmoid", "Hardswish", "Hardsigmoid",
+           "Tanh", "ELU", "LeakyReLU"]
 
 
 def __getattr__(name: str):

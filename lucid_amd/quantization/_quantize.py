@@ -35,7 +35,8 @@ def _observed_types() -> tuple[type, ...]:
     import lucid_amd.nn.intrinsic as nni
     import lucid_amd.nn.quantized as nnq
 
-    return (nn.Linear, nn.Conv2d, nni.ConvReLU2d, nni.LinearReLU, nnq.QuantStub, nnq.FloatFunctional)
+    return (nn.Linear, nn.Conv2d, nni.ConvReLU2d, nni.LinearReLU, nn.Sigmoid, nn.Hardswish,
+            nn.Hardsigmoid, nn.Tanh, nn.ELU, nn.LeakyReLU, nnq.QuantStub, nnq.FloatFunctional)
 
 
 def _quant_mapping() -> dict[type, _FromFloat]:
@@ -49,6 +50,12 @@ def _quant_mapping() -> dict[type, _FromFloat]:
         nnq.QuantStub: nnq.Quantize.from_float,
         nnq.DeQuantStub: nnq.DeQuantize.from_float,
         nnq.FloatFunctional: nnq.QFunctional.from_float,
+        nn.Sigmoid: nnq.Sigmoid.from_float,
+        nn.Hardswish: nnq.Hardswish.from_float,
+        nn.Hardsigmoid: nnq.Hardsigmoid.from_float,
+        nn.Tanh: nnq.Tanh.from_float,
+        nn.ELU: nnq.ELU.from_float,
+        nn.LeakyReLU: nnq.LeakyReLU.from_float,
     }
     if hasattr(nnq, "Conv2d"):
         mapping[nn.Conv2d] = nnq.Conv2d.from_float

@@ -37,6 +37,8 @@ function                      follows (lucid-official/lucid)
 ``histogram_observer``        observer.py:850-870 (forward over batches)
 ``hist_clip_search``          observer.py:872-926, vectorised (cumulative sums and array
                               errors instead of the reference's Python loops)
+``activation``                backend/cpu/methods/Activation.cpp:8-50, 375-460, 661-751;
+                              Unary.cpp:165-170 (numpy float32; exp / tanh within rounding)
 ``lucid_*``                   the multi-pass CPU composition timed as the CPU baseline
 ============================  ==========================================================
 
@@ -495,3 +497,35 @@ def hist_clip_search(hist: np.ndarray, lo: float, hi: float, levels: int,
         if err < best_err:
             best_err, best = err, (cmin, cmax)
     return best
+
+
+# ------------------------------------------------------------------- activations
+
+ACT_SIGMOID, ACT_TANH, ACT_HARDSWISH, ACT_HARDSIGMOID, ACT_ELU, ACT_LEAKY_RELU = 0, 1, 2, 3, 4, 5
+
+
+def activation(x: np.ndarray, op: int, param: float = 0.0) -> np.ndarray:
+    """float32 activation with the operation order of Lucid's CPU kernels
+    (backend/cpu/methods/Activation.cpp:8-50 sigmoid, 375-400 leaky_relu, 435-460 elu,
+    661-686 hard_sigmoid, 726-751 hard_swish; Unary.cpp:165-170 tanh).  Each step rounds to
+    float32; ``std::max(t, 0)`` / ``std::min(t, 1)`` are ``t < 0 ? 0 : t`` / ``1 < t ? 1 : t``
+    (NaN and -0 pass).  exp / tanh are numpy's float32 functions (the reference's are
+    vForce's: these two agree with it to within rounding, not to the bit)."""
+    f = np.float32
+    x = np.asarray(x, np.float32)
+    p = f(param)
+    with np.errstate(over="ignore", invalid="ignore"):
+        if op == ACT_SIGMOID:
+            return (f(1) / (f(1) + np.exp(-x))).astype(np.float32)
+        if op == ACT_TANH:
+            return np.tanh(x).astype(np.float32)
+        if op in (ACT_HARDSWISH, ACT_HARDSIGMOID):
+            t = ((x + f(3)) / f(6)).astype(np.float32)
+            t = np.where(t < f(0), f(0), t).astype(np.float32)
+            t = np.where(f(1) < t, f(1), t).astype(np.float32)
+            return (x * t).astype(np.float32) if op == ACT_HARDSWISH else t
+        if op == ACT_ELU:
+            return np.where(x >= f(0), x, p * (np.exp(x) - f(1))).astype(np.float32)
+        if op == ACT_LEAKY_RELU:
+            return np.where(x >= f(0), x, p * x).astype(np.float32)
+    raise ValueError(f"unknown activation {op}")

@@ -454,3 +454,71 @@ def test_hist_clip_search_pins():
     s_hist, _ = O.calc_qparams(np.float32(cmin), np.float32(cmax), False, False, 0, 255)
     s_mm, _ = O.calc_qparams(np.float32(mn), np.float32(mx), False, False, 0, 255)
     assert s_hist <= s_mm
+
+
+# ------------------------------------------------------------------- activations
+
+
+def _ulps(a, b):
+    """Distance in float32 ulps (of the larger magnitude) between two arrays; differences
+    below the smallest normal float32 count as 0 (a float32 exp overflows to inf where the
+    exact result is subnormal, and the float32 composition then returns 0)."""
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    u = np.spacing(np.maximum(np.abs(a), np.abs(b)).astype(np.float32)).astype(np.float64)
+    d = np.abs(a - b)
+    return np.where(d < np.finfo(np.float32).tiny, 0.0, d / u)
+
+
+def test_activation_docstring_kats():
+    # the examples of lucid/nn/functional/activations.py (printed to 4 decimals), and
+    # hardswish's -0 at x = -4 (x * 0 keeps x's sign)
+    f = np.float32
+    x4 = np.array([-2.0, -1.0, 0.0, 1.0], f)
+    np.testing.assert_array_equal(O.activation(x4, O.ACT_LEAKY_RELU, 0.1), f([-0.2, -0.1, 0.0, 1.0]))
+    np.testing.assert_allclose(O.activation(x4, O.ACT_ELU, 1.0), [-0.8647, -0.6321, 0.0, 1.0], atol=5e-5)
+    x5 = np.array([-4.0, -1.0, 0.0, 1.0, 4.0], f)
+    hs = O.activation(x5, O.ACT_HARDSWISH)
+    np.testing.assert_allclose(hs, [0.0, -0.3333, 0.0, 0.6667, 4.0], atol=5e-5)
+    assert np.signbit(hs[0]) and not np.signbit(hs[2])
+    np.testing.assert_allclose(O.activation(x5, O.ACT_HARDSIGMOID), [0.0, 0.3333, 0.5, 0.6667, 1.0], atol=5e-5)
+    x3 = np.array([-2.0, 0.0, 2.0], f)
+    np.testing.assert_allclose(O.activation(x3, O.ACT_SIGMOID), [0.1192, 0.5, 0.8808], atol=5e-5)
+    np.testing.assert_allclose(O.activation(x3, O.ACT_TANH), [-0.964, 0.0, 0.964], atol=5e-4)
+
+
+def test_activation_against_float64():
+    rng = np.random.default_rng(11)
+    x = np.concatenate([rng.standard_normal(20000) * 4, rng.uniform(-1e-3, 1e-3, 2000),
+                        [-3.0, 3.0, -2.9999998, 2.9999998, 80.0, -80.0, -100.0, 100.0]]).astype(np.float32)
+    xd = x.astype(np.float64)
+    # sigmoid: three roundings around exp
+    assert _ulps(O.activation(x, O.ACT_SIGMOID), 1.0 / (1.0 + np.exp(-xd))).max() <= 4
+    assert _ulps(O.activation(x, O.ACT_TANH), np.tanh(xd)).max() <= 2
+    # hardsigmoid: (x + 3) and / 6 each rounded once; the clamps are exact
+    hsd = np.clip((xd + 3.0) / 6.0, 0.0, 1.0)
+    assert _ulps(O.activation(x, O.ACT_HARDSIGMOID), hsd).max() <= 2
+    assert _ulps(O.activation(x, O.ACT_HARDSWISH), xd * hsd).max() <= 3
+    # elu: exp(x) - 1 cancels near 0, so the error there is absolute (about an ulp of 1)
+    el = O.activation(x, O.ACT_ELU, 1.5)
+    want = np.where(xd >= 0, xd, np.float64(np.float32(1.5)) * np.expm1(xd))
+    assert np.all(np.abs(el - want) <= 4 * np.spacing(np.float32(1.5)) + 1e-7 * np.abs(want))
+    # leaky_relu: one IEEE float32 multiply = the exact product rounded once
+    lr = O.activation(x, O.ACT_LEAKY_RELU, 0.2)
+    exact = np.where(xd >= 0, xd, np.float64(np.float32(0.2)) * xd).astype(np.float32)
+    np.testing.assert_array_equal(lr, exact)
+
+
+def test_activation_special_values():
+    f = np.float32
+    x = np.array([np.nan, np.inf, -np.inf, -0.0, 0.0], f)
+    for op in range(6):
+        y = O.activation(x, op, 0.5)
+        assert np.isnan(y[0]), op   # NaN passes every activation
+    np.testing.assert_array_equal(O.activation(x[1:3], O.ACT_SIGMOID), f([1.0, 0.0]))
+    np.testing.assert_array_equal(O.activation(x[1:3], O.ACT_TANH), f([1.0, -1.0]))
+    np.testing.assert_array_equal(O.activation(x[1:3], O.ACT_HARDSIGMOID), f([1.0, 0.0]))
+    np.testing.assert_array_equal(O.activation(x[1:3], O.ACT_ELU, 2.0), f([np.inf, -2.0]))
+    # -0 >= 0 holds: leaky_relu and elu keep -0
+    assert np.signbit(O.activation(x[3:4], O.ACT_LEAKY_RELU, 0.1)[0])
+    assert np.signbit(O.activation(x[3:4], O.ACT_ELU, 1.0)[0])
