@@ -374,6 +374,32 @@ def bandwidth_lines(L, C, timer, steps, warmup):
     return out
 
 
+def lookup_lines(L, C, timer, steps, warmup):
+    """nn.quantized.EmbeddingBag (mean) over a 4M x 128 int8 table (512 MB: past the Infinity
+    Cache), 65536 bags of 32 uniform random indices: random 128-byte row gathers."""
+    rows, D, bags, per = 1 << 22, 128, 1 << 16, 32
+    rng = np.random.default_rng(11)
+    codes = L.tensor(rng.integers(-127, 128, (rows, D), dtype=np.int8), device="gpu")
+    s = L.tensor(rng.uniform(1e-3, 1e-1, rows).astype(np.float32), device="gpu")
+    z = L.tensor(np.zeros(rows, np.float32), device="gpu")
+    idx = L.tensor(rng.integers(0, rows, bags * per, dtype=np.int64), device="gpu")
+    off = L.tensor(np.arange(0, bags * per, per, dtype=np.int64), device="gpu")
+    y = L.empty((bags, D), np.float32, "gpu")
+    lib = C.lib()
+
+    def bag():
+        lib.lq_embedding_bag(codes.data_ptr(), C.I8, s.data_ptr(), z.data_ptr(), rows, D, idx.data_ptr(), C.I64,
+                             bags * per, off.data_ptr(), C.I64, bags, 0, 0, C.BAG_MEAN, -1, None, y.data_ptr(), None)
+
+    ms = timer.time_ms(bag, steps, warmup)
+    nbytes = bags * per * (D + 8 + 8) + bags * (8 + 4 * D)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    C.call("lq_device_synchronize")
+    return {"embedding_bag_int8": {"rows": rows, "D": D, "bags": bags, "indices_per_bag": per, "mode": "mean",
+                                   "us": round(ms * 1e3, 1), "GB/s": round(gbs, 1),
+                                   "frac": round(gbs / HBM_PEAK_GBS, 3)}}
+
+
 def cpu_baseline(M, N, K, seconds):
     """Lucid's CPU composition of the W8A8 Linear (lucid/nn/quantized/linear.py:206-215):
     dequantize activations and weights (separate passes), fp32 sgemm (numpy's OpenBLAS on
@@ -493,6 +519,7 @@ def main() -> None:
         comps["weight_only_gemv"] = weight_only_lines(L, C, gtimer)
         comps["conv_resnet18_b32"] = conv_lines(L, C, timer, 10, 3)
         comps.update(bandwidth_lines(L, C, timer, 50, 10))
+        comps.update(lookup_lines(L, C, timer, 20, 5))
         line["components"] = comps
     line["cpu_baseline"] = cpu_baseline(M, N, K, args.cpu_seconds)
     print(json.dumps(line), flush=True)

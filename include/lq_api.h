@@ -58,7 +58,8 @@ enum {
     LQ_I32 = 4,   /* int32 (accumulators) */
     LQ_F16 = 5,   /* IEEE half */
     LQ_F32 = 6,   /* IEEE single */
-    LQ_U8S8 = 7   /* an unsigned-grid code c stored as int8 (c - 128): MFMA operand form */
+    LQ_U8S8 = 7,  /* an unsigned-grid code c stored as int8 (c - 128): MFMA operand form */
+    LQ_I64 = 8    /* int64 (indices and offsets) */
 };
 
 /* ---- runtime -------------------------------------------------------------- */
@@ -353,6 +354,35 @@ enum { LQ_ACT_SIGMOID = 0, LQ_ACT_TANH = 1, LQ_ACT_HARDSWISH = 2, LQ_ACT_HARDSIG
 int lq_qact(int op, const void* d_x, int x_type, const float* d_x_scale, const float* d_x_zero_point,
             int64_t n, float param, const float* d_out_scale, const float* d_out_zero_point, int qmin,
             int qmax, int out_type, void* d_y, void* stream);
+
+/* ---- table lookups (Embedding / EmbeddingBag) ----------------------------------- */
+/* Pooling modes of lq_embedding_bag (the engine's encoding, lucid/nn/functional/sparse.py:214). */
+enum { LQ_BAG_SUM = 0, LQ_BAG_MEAN = 1, LQ_BAG_MAX = 2 };
+/* out[i, :] = row idx[i] of a [rows, D] table: int8 codes (table_type LQ_I8) dequantized per row
+ * as fl32(fl32(float(c) - z[r]) * s[r]) (d_zero_point NULL = 0), or float32 entries (LQ_F32,
+ * d_scale unused).  Indices LQ_I32 or LQ_I64; one outside [0, rows) gives a NaN row (no read).
+ * Replaces dequantize(table, ch_axis=0) + F.embedding of nnq.Embedding.forward
+ * (lucid/nn/quantized/sparse.py:140-143 -> lucid/_C/backend/cpu/methods/Sequence.cpp:520-552),
+ * and the float lookup of nn.Embedding, without forming the float table. */
+int lq_embedding(const void* d_table, int table_type, const float* d_scale, const float* d_zero_point,
+                 int64_t rows, int64_t D, const void* d_idx, int idx_type, int64_t n_idx, float* d_out,
+                 void* stream);
+/* Pooled lookup into out[n_bags, D] (float32).  Bags: with d_offsets (LQ_I32 / LQ_I64,
+ * n_offsets entries) bag b = [off[b], off[b + 1]) and the last runs to n_idx, or to
+ * off[n_offsets - 1] with include_last_offset (then n_bags = n_offsets - 1); without, fixed
+ * bags of bag_len (a 2-D input, one bag per row).  Each bag walks its indices in order:
+ * LQ_BAG_SUM acc = acc + v, LQ_BAG_MEAN the sum / count, LQ_BAG_MAX acc = v > acc ? v : acc
+ * from the lowest float (an empty bag is 0).  Indices equal to padding_idx (-1 = none) are
+ * skipped and not counted.  d_per_sample_weights (LQ_BAG_SUM only) adds fl32(v * w[k]) instead,
+ * a padding index adding fl32(v * 0).  An index outside [0, rows) makes its bag NaN.  Offsets
+ * are clamped to [0, n_idx] (the caller validates them).  Replaces nnq.EmbeddingBag.forward
+ * (lucid/nn/quantized/sparse.py:284-304 -> lucid/_C/backend/cpu/methods/Sequence.cpp:8-93, and
+ * the per_sample_weights composite lucid/nn/functional/sparse.py:228-310). */
+int lq_embedding_bag(const void* d_table, int table_type, const float* d_scale, const float* d_zero_point,
+                     int64_t rows, int64_t D, const void* d_idx, int idx_type, int64_t n_idx,
+                     const void* d_offsets, int offsets_type, int64_t n_offsets, int include_last_offset,
+                     int64_t bag_len, int mode, int64_t padding_idx, const float* d_per_sample_weights,
+                     float* d_out, void* stream);
 
 /* ---- int8 Conv2d (implicit GEMM) ------------------------------------------------- */
 /* Padding modes of a convolution (Lucid's padding_mode, lucid/nn/functional/conv.py:24-29). */

@@ -19,13 +19,14 @@ LIB_PATH = os.path.join(_HERE, "_lib", "liblucid_amd.so")
 
 # Status and type codes of include/lq_api.h.
 OK = 0
-I8, U8, I16, I32, F16, F32, U8S8 = 1, 2, 3, 4, 5, 6, 7
+I8, U8, I16, I32, F16, F32, U8S8, I64 = 1, 2, 3, 4, 5, 6, 7, 8
 OBS_MINMAX, OBS_EMA, OBS_REPLACE = 0, 1, 2
 OUT_I32, OUT_F32, OUT_F16, OUT_Q8, OUT_QU8, OUT_FQ32, OUT_Q16, OUT_QU8S8 = 0, 1, 2, 3, 4, 5, 6, 7
 EPI_RELU, EPI_A_U8S8 = 1, 2
 PAD_ZEROS, PAD_REFLECT, PAD_REPLICATE, PAD_CIRCULAR = 0, 1, 2, 3
 MERGE_ADD, MERGE_MUL, MERGE_ADD_SCALAR, MERGE_MUL_SCALAR, MERGE_COPY = 0, 1, 2, 3, 4
 ACT_SIGMOID, ACT_TANH, ACT_HARDSWISH, ACT_HARDSIGMOID, ACT_ELU, ACT_LEAKY_RELU = 0, 1, 2, 3, 4, 5
+BAG_SUM, BAG_MEAN, BAG_MAX = 0, 1, 2
 
 
 class LucidError(RuntimeError):
@@ -70,6 +71,9 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_histc_workspace_size": (_SZ, [_I64]),
     "lq_histc_f32": (_I, [_P, _I64, _I64, ctypes.c_double, ctypes.c_double, _I, _P, _P, _SZ, _P]),
     "lq_hist_rebin_f32": (_I, [_P, _I64, _F, _F, _F, _F, _P, _P]),
+    "lq_embedding": (_I, [_P, _I, _P, _P, _I64, _I64, _P, _I, _I64, _P, _P]),
+    "lq_embedding_bag": (_I, [_P, _I, _P, _P, _I64, _I64, _P, _I, _I64, _P, _I, _I64, _I, _I64, _I, _I64, _P, _P,
+                              _P]),
     "lq_qact": (_I, [_I, _P, _I, _P, _P, _I64, _F, _P, _P, _I, _I, _I, _P, _P]),
     "lq_qmerge": (_I, [_I, _P, _I, _P, _P, _P, _I, _P, _P, _F, _I64, _I64, _I64, _P, _P, _I, _I, _I, _I,
                        _P, _P]),

@@ -21,10 +21,13 @@
 // the reference's vForce results, which are not specified to the bit).
 //
 // Work split: each thread owns groups of E consecutive elements, E = 16 bytes over the wider
-// of the input and output element sizes, so every load and store is one 4-16 byte access;
-// workgroups take contiguous runs of groups.  Misaligned pointers fall back to one element
-// per step.
+// of the input and output element sizes, so every load and store is one 4-16 byte access,
+// with four groups in flight; workgroups take contiguous runs of groups.  Misaligned pointers
+// fall back to one element per step.  One-byte code inputs read a 256-entry table of outputs
+// built per workgroup in LDS instead of evaluating the activation per element.
 #include <hip/hip_runtime.h>
+
+#include <float.h>
 
 #include <type_traits>
 
@@ -75,9 +78,23 @@ __device__ __forceinline__ float act_in(typename ElemOf<IN>::type v, float s, fl
     }
 }
 
+// fl32(t / 6): a multiply by fl32(1/6) and one fma residual step, which gives the IEEE
+// quotient for every float32 with 2^-125 <= |t| <= FLT_MAX (checked exhaustively over all 2^32
+// inputs by the oracle's lqo_div6_mismatches); the IEEE division elsewhere.
+__device__ __forceinline__ float div6(float t) {
+    constexpr float r = 1.0f / 6.0f;
+    const float a = fabsf(t);
+    if (a >= 0x1p-125f && a <= FLT_MAX) {
+        const float q0 = t * r;
+        const float e = __builtin_fmaf(-q0, 6.0f, t);
+        return __builtin_fmaf(e, r, q0);
+    }
+    return t / 6.0f;
+}
+
 // std::max(t, 0) then std::min(t, 1): a NaN or a -0 passes both.
 __device__ __forceinline__ float hard_sigmoid(float x) {
-    float t = (x + 3.0f) / 6.0f;
+    float t = div6(x + 3.0f);
     t = (t < 0.0f) ? 0.0f : t;
     t = (1.0f < t) ? 1.0f : t;
     return t;
@@ -114,14 +131,21 @@ __device__ __forceinline__ typename ElemOf<OUT>::type act_out(float t, float inv
     else return quant_store<CodeU8S8>(t, inv, z, g);
 }
 
+// One-byte codes take 256 values: their outputs are tabulated once per workgroup in LDS (by
+// the same function, so bit-identical) and each element becomes one table read.
+template <int IN>
+constexpr bool kActLut = IN == LQ_I8 || IN == LQ_U8 || IN == LQ_U8S8;
+
 template <int IN, int OUT>
 __global__ __launch_bounds__(kActBlock) void act_kernel(ActArgs a) {
     using TI = typename ElemOf<IN>::type;
     using TO = typename ElemOf<OUT>::type;
     constexpr int WIDE = sizeof(TI) > sizeof(TO) ? sizeof(TI) : sizeof(TO);
     constexpr int E = 16 / WIDE;
+    constexpr int U = 4;  // groups in flight per thread
     using VI = typename RawVec<E * sizeof(TI)>::type;
     using VO = typename RawVec<E * sizeof(TO)>::type;
+    __shared__ TO lut[kActLut<IN> ? 256 : 1];
 
     const float sx = a.x_scale ? a.x_scale[0] : 1.0f, zx = a.x_zp ? a.x_zp[0] : 0.0f;
     float inv = 1.0f, z = 0.0f;
@@ -129,27 +153,48 @@ __global__ __launch_bounds__(kActBlock) void act_kernel(ActArgs a) {
         inv = 1.0f / a.out_scale[0];
         z = a.out_zp ? a.out_zp[0] : 0.0f;
     }
+    auto f = [&](TI v) __attribute__((always_inline)) {
+        return act_out<OUT>(act_apply(a.op, act_in<IN>(v, sx, zx), a.param), inv, z, a.g);
+    };
+    if constexpr (kActLut<IN>) {
+        static_assert(kActBlock == 256, "one table entry per thread");
+        lut[threadIdx.x] = f((TI)(uint8_t)threadIdx.x);
+        __syncthreads();
+    }
+    auto g = [&](TI v) __attribute__((always_inline)) {
+        if constexpr (kActLut<IN>) return lut[(uint8_t)v];
+        else return f(v);
+    };
     const TI* x = static_cast<const TI*>(a.x);
     TO* y = static_cast<TO*>(a.y);
     const int64_t groups = a.vec ? a.n / E : 0;
     // contiguous run of groups per workgroup
     const int64_t per = (groups + gridDim.x - 1) / gridDim.x;
     const int64_t g0 = (int64_t)blockIdx.x * per, g1 = min(groups, g0 + per);
-    for (int64_t gi = g0 + threadIdx.x; gi < g1; gi += kActBlock) {
-        const VI raw = *reinterpret_cast<const VI*>(x + gi * E);
+    auto one = [&](int64_t gi, const VI& raw) __attribute__((always_inline)) {
         TI xin[E];
         __builtin_memcpy(xin, &raw, sizeof(raw));
         TO out[E];
 #pragma unroll
-        for (int e = 0; e < E; ++e) out[e] = act_out<OUT>(act_apply(a.op, act_in<IN>(xin[e], sx, zx), a.param), inv, z, a.g);
+        for (int e = 0; e < E; ++e) out[e] = g(xin[e]);
         VO ro;
         __builtin_memcpy(&ro, out, sizeof(ro));
         *reinterpret_cast<VO*>(y + gi * E) = ro;
+    };
+    const VI* xv = reinterpret_cast<const VI*>(x);
+    int64_t gi = g0 + threadIdx.x;
+    for (; gi + (U - 1) * kActBlock < g1; gi += U * kActBlock) {
+        VI raw[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) raw[u] = __builtin_nontemporal_load(&xv[gi + u * kActBlock]);
+#pragma unroll
+        for (int u = 0; u < U; ++u) one(gi + u * kActBlock, raw[u]);
     }
+    for (; gi < g1; gi += kActBlock) one(gi, __builtin_nontemporal_load(&xv[gi]));
     // elements past the last full group (all of them when misaligned), one per thread
     const int64_t rest0 = groups * E;
     for (int64_t i = rest0 + (int64_t)blockIdx.x * kActBlock + threadIdx.x; i < a.n; i += (int64_t)gridDim.x * kActBlock)
-        y[i] = act_out<OUT>(act_apply(a.op, act_in<IN>(x[i], sx, zx), a.param), inv, z, a.g);
+        y[i] = g(x[i]);
 }
 
 static bool act_type_ok(int t) { return t == LQ_F32 || t == LQ_I8 || t == LQ_U8 || t == LQ_I16 || t == LQ_U8S8; }

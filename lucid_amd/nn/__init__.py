@@ -5,6 +5,8 @@ from lucid_amd.nn.layers import (
     ELU,
     BatchNorm2d,
     Conv2d,
+    Embedding,
+    EmbeddingBag,
     Flatten,
     Hardsigmoid,
     Hardswish,
@@ -18,7 +20,8 @@ from lucid_amd.nn.layers import (
 )
 
 __all__ = ["Module", "Parameter", "Linear", "Conv2d", "ReLU", "Sequential", "Identity",
-           "BatchNorm2d", "Flatten", "Sigmoid", "Tanh", "Hardswish", "Hardsigmoid", "ELU", "LeakyReLU"]
+           "BatchNorm2d", "Flatten", "Sigmoid", "Tanh", "Hardswish", "Hardsigmoid", "ELU", "LeakyReLU",
+           "Embedding", "EmbeddingBag"]
 
 
 def __getattr__(name: str):

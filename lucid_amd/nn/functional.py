@@ -166,3 +166,145 @@ def leaky_relu(x: Tensor, negative_slope: float = 0.01) -> Tensor:
     import numpy as np
 
     return _activation(x, _C.ACT_LEAKY_RELU, float(np.float32(negative_slope)), "leaky_relu")
+
+
+# ------------------------------------------------------------------- table lookups
+
+_BAG_MODES = {"sum": 0, "mean": 1, "max": 2}
+
+
+def _strict_index() -> bool:
+    """``LUCID_STRICT_INDEX=1``: read GPU indices back and refuse bad ones
+    (lucid/nn/functional/_index_checks.py: ``_strict_index``)."""
+    import os
+
+    return os.environ.get("LUCID_STRICT_INDEX", "")[:1] not in ("", "0")
+
+
+def _indices(x: Tensor, rows: int, op: str) -> tuple[Tensor, int]:
+    """``x`` as a GPU int32 / int64 index tensor and its type code.  A float ``x`` raises
+    ``TypeError``; in strict mode an index outside ``[0, rows)`` raises ``IndexError``
+    (_index_checks.py:296-340; otherwise a bad index yields NaN, the reference's GPU policy)."""
+    import numpy as np
+
+    if not isinstance(x, Tensor):
+        raise TypeError(f"{op}: expected a Tensor of indices, got {type(x).__name__}")
+    dt = np.dtype(x.dtype)
+    if dt not in (np.int8, np.int16, np.int32, np.int64, np.bool_):
+        raise TypeError(f"{op}: indices must be an integer tensor, got {dt}; cast with .to(int64) first")
+    if dt not in (np.int32, np.int64):
+        x = Tensor._from_numpy(x.numpy().astype(np.int64), "gpu")
+    elif x.device != "gpu":
+        x = x.to("gpu")
+    if _strict_index() and x.numel():
+        host = x.numpy().ravel()
+        bad = (host < 0) | (host >= rows)
+        if bad.any():
+            v = int(host[np.argmax(bad)])
+            raise IndexError(f"{op}: index {v} is out of range for a table with {rows} entries "
+                             f"(valid range [0, {rows - 1}])")
+    return x, (_C.I64 if np.dtype(x.dtype) == np.int64 else _C.I32)
+
+
+def _padding_row(padding_idx, rows: int, op: str):
+    """``padding_idx`` as a row of a ``rows``-row table or None (_index_checks.py:390-402)."""
+    if padding_idx is None:
+        return None
+    if not -rows <= padding_idx < rows:
+        raise ValueError(f"{op}: padding_idx must be within [-{rows}, {rows}); got {padding_idx}")
+    return padding_idx + rows if padding_idx < 0 else padding_idx
+
+
+def _check_offsets(offsets: Tensor, length: int, op: str):
+    """The bag boundaries, read on the host as the reference does on both devices
+    (_index_checks.py:410-440): 1-D, within ``[0, length]``, starting at 0, never decreasing."""
+    import numpy as np
+
+    if offsets.ndim != 1:
+        raise ValueError(f"{op}: offsets must be 1-D, got shape {tuple(offsets.shape)}")
+    bounds = [int(v) for v in np.asarray(offsets.numpy()).ravel()]
+    for v in bounds:
+        if not 0 <= v <= length:
+            raise IndexError(f"{op}: offset {v} is out of range for {length} indices "
+                             f"(valid range [0, {length}])")
+    if bounds and bounds[0] != 0:
+        raise ValueError(f"{op}: offsets[0] must be 0, got {bounds[0]}")
+    for before, after in zip(bounds, bounds[1:]):
+        if after < before:
+            raise ValueError(f"{op}: offsets must not decrease, got {after} after {before}")
+    arr = np.asarray(bounds, np.int64)
+    return Tensor._from_numpy(arr, "gpu"), len(bounds)
+
+
+def table_lookup(table: int, table_type: int, scale: int | None, zero_point: int | None, rows: int, D: int,
+                 input: Tensor, op: str = "embedding") -> Tensor:
+    """``lq_embedding`` over a table given by pointers (float32, or int8 codes with row qparams)."""
+    import numpy as np
+
+    idx, itype = _indices(input, rows, op)
+    y = empty((*input.shape, D), np.float32, "gpu")
+    if idx.numel() and D:
+        _C.call("lq_embedding", table, table_type, scale, zero_point, rows, D, idx.data_ptr(), itype, idx.numel(),
+                y.data_ptr(), None)
+    return y
+
+
+def bag_lookup(table: int, table_type: int, scale: int | None, zero_point: int | None, rows: int, D: int,
+               input: Tensor, offsets: Tensor | None, mode: str, per_sample_weights: Tensor | None,
+               include_last_offset: bool, padding_idx: int | None, op: str = "embedding_bag") -> Tensor:
+    """``lq_embedding_bag`` over a table given by pointers, with the reference's argument rules
+    (lucid/nn/functional/sampling.py:489-640, sparse.py:201-334)."""
+    import numpy as np
+
+    if mode not in _BAG_MODES:
+        raise ValueError(f"embedding_bag: mode must be one of {sorted(_BAG_MODES)}, got {mode!r}")
+    pad = _padding_row(padding_idx, rows, op)
+    idx, itype = _indices(input, rows, op)
+    if per_sample_weights is not None:
+        if mode != "sum":
+            raise NotImplementedError("embedding_bag: per_sample_weights is only supported for "
+                                      f"mode='sum' (got mode={mode!r})")
+        if tuple(per_sample_weights.shape) != tuple(input.shape):
+            raise ValueError("embedding_bag: per_sample_weights must have the shape of the indices "
+                             f"{tuple(input.shape)}, got {tuple(per_sample_weights.shape)}")
+        psw = on_device(per_sample_weights)
+    else:
+        psw = None
+    off_ptr, n_off, bag_len = None, 0, 0
+    if input.ndim == 2:
+        n_bags, bag_len = int(input.shape[0]), int(input.shape[1])
+        if bag_len == 0:  # every bag empty
+            return Tensor._from_numpy(np.zeros((n_bags, D), np.float32), "gpu")
+        include_last_offset = False
+    elif input.ndim == 1:
+        if offsets is None:
+            raise ValueError("embedding_bag: offsets required for 1-D input")
+        off_t, n_off = _check_offsets(offsets, int(input.shape[0]), op)
+        off_ptr = off_t.data_ptr()
+        n_bags = n_off - 1 if include_last_offset and n_off > 0 else n_off
+    else:
+        raise ValueError(f"embedding_bag: input must be 1-D or 2-D, got {input.ndim}-D")
+    y = empty((n_bags, D), np.float32, "gpu")
+    if n_bags and D:
+        _C.call("lq_embedding_bag", table, table_type, scale, zero_point, rows, D, idx.data_ptr(), itype,
+                idx.numel(), off_ptr, _C.I64, n_off, 1 if include_last_offset else 0, bag_len, _BAG_MODES[mode],
+                -1 if pad is None else pad, psw.data_ptr() if psw is not None else None, y.data_ptr(), None)
+    return y
+
+
+def embedding(input: Tensor, weight: Tensor, padding_idx: int | None = None) -> Tensor:
+    """Rows of the float table ``weight`` (lucid/nn/functional/sparse.py:70-174); padding_idx
+    does not mask the forward lookup (Sequence.cpp:538-546)."""
+    w = on_device(weight)
+    rows, D = int(w.shape[0]), int(w.shape[1])
+    _padding_row(padding_idx, rows, "embedding")
+    return table_lookup(w.data_ptr(), _C.F32, None, None, rows, D, input)
+
+
+def embedding_bag(input: Tensor, weight: Tensor, offsets: Tensor | None = None, mode: str = "mean",
+                  per_sample_weights: Tensor | None = None, include_last_offset: bool = False,
+                  padding_idx: int | None = None) -> Tensor:
+    """Pooled rows of the float table ``weight`` (lucid/nn/functional/sampling.py:489-640)."""
+    w = on_device(weight)
+    return bag_lookup(w.data_ptr(), _C.F32, None, None, int(w.shape[0]), int(w.shape[1]), input, offsets, mode,
+                      per_sample_weights, include_last_offset, padding_idx)

@@ -105,6 +105,65 @@ class ReLU(Module):
         return F.relu(x)
 
 
+class _PaddedTable(Module):
+    """A ``[num_embeddings, embedding_dim]`` table, N(0, 1) with the padding row zeroed
+    (lucid/nn/modules/sparse.py:_PaddedTable)."""
+
+    def _init_table(self, num_embeddings: int, embedding_dim: int, weight: Tensor | None) -> None:
+        if weight is None:
+            w = _init_rng.standard_normal((num_embeddings, embedding_dim)).astype(np.float32)
+            if self.padding_idx is not None:
+                w[self.padding_idx] = 0.0
+            weight = tensor(w)
+        elif tuple(weight.shape) != (num_embeddings, embedding_dim):
+            raise ValueError(f"Shape of weight {tuple(weight.shape)} does not match "
+                             f"num_embeddings={num_embeddings} and embedding_dim={embedding_dim}")
+        self.weight = Parameter(weight)
+
+
+class Embedding(_PaddedTable):
+    """Float lookup table (lucid/nn/modules/sparse.py:93-346); ``convert`` swaps it for the
+    int8 ``nn.quantized.Embedding`` without calibration."""
+
+    def __init__(self, num_embeddings: int, embedding_dim: int, padding_idx: int | None = None,
+                 _weight: Tensor | None = None) -> None:
+        super().__init__()
+        self.num_embeddings = num_embeddings
+        self.embedding_dim = embedding_dim
+        self.padding_idx = F._padding_row(padding_idx, num_embeddings, "Embedding")
+        self._init_table(num_embeddings, embedding_dim, _weight)
+
+    def forward(self, input: Tensor) -> Tensor:
+        return F.embedding(input, self.weight, self.padding_idx)
+
+    def extra_repr(self) -> str:
+        s = f"{self.num_embeddings}, {self.embedding_dim}"
+        return s + (f", padding_idx={self.padding_idx}" if self.padding_idx is not None else "")
+
+
+class EmbeddingBag(_PaddedTable):
+    """Float pooled lookup (lucid/nn/modules/sparse.py:349-420): ``mode`` sum / mean / max."""
+
+    def __init__(self, num_embeddings: int, embedding_dim: int, mode: str = "mean",
+                 include_last_offset: bool = False, padding_idx: int | None = None,
+                 _weight: Tensor | None = None) -> None:
+        super().__init__()
+        self.num_embeddings = num_embeddings
+        self.embedding_dim = embedding_dim
+        self.mode = mode
+        self.include_last_offset = include_last_offset
+        self.padding_idx = F._padding_row(padding_idx, num_embeddings, "EmbeddingBag")
+        self._init_table(num_embeddings, embedding_dim, _weight)
+
+    def forward(self, input: Tensor, offsets: Tensor | None = None,
+                per_sample_weights: Tensor | None = None) -> Tensor:
+        return F.embedding_bag(input, self.weight, offsets, self.mode, per_sample_weights,
+                               self.include_last_offset, self.padding_idx)
+
+    def extra_repr(self) -> str:
+        return f"{self.num_embeddings}, {self.embedding_dim}, mode={self.mode}"
+
+
 class Sigmoid(Module):
     def forward(self, x: Tensor) -> Tensor:
         return F.sigmoid(x)

@@ -5,7 +5,8 @@ The int8 layers keep Lucid's buffers and ``state_dict`` layout and run the gfx95
 MFMA GEMM over integer codes; ``QuantStub`` / ``DeQuantStub`` / ``Quantize`` /
 ``DeQuantize`` / ``QuantWrapper`` mark the quantized region; ``FloatFunctional`` /
 ``QFunctional`` carry residual adds and concatenations onto one grid; ``Sigmoid`` /
-``Hardswish`` / ``Hardsigmoid`` / ``Tanh`` / ``ELU`` / ``LeakyReLU`` requantize activations.
+``Hardswish`` / ``Hardsigmoid`` / ``Tanh`` / ``ELU`` / ``LeakyReLU`` requantize activations;
+``Embedding`` / ``EmbeddingBag`` hold per-row int8 tables.
 """
 
 from lucid_amd.nn.quantized.activation import ELU, Hardsigmoid, Hardswish, LeakyReLU, Sigmoid, Tanh
@@ -16,10 +17,11 @@ from lucid_amd.nn.quantized.linear import Linear
 from lucid_amd.nn.quantized.mlx_linear import QuantizedLinearMLX
 from lucid_amd.nn.quantized.modules import (DeQuantize, DeQuantStub, Quantize, QuantStub,
                                             QuantWrapper)
+from lucid_amd.nn.quantized.sparse import Embedding, EmbeddingBag
 
 __all__ = ["Linear", "QuantizedLinearMLX", "Conv2d", "ConvReLU2d", "LinearReLU", "QuantStub", "DeQuantStub", "Quantize", "DeQuantize",
            "QuantWrapper", "FloatFunctional", "QFunctional", "Sigmoid", "Hardswish", "Hardsigmoid",
-           "Tanh", "ELU", "LeakyReLU"]
+           "Tanh", "ELU", "LeakyReLU", "Embedding", "EmbeddingBag"]
 
 
 def __getattr__(name: str):

@@ -56,6 +56,8 @@ def _quant_mapping() -> dict[type, _FromFloat]:
         nn.Tanh: nnq.Tanh.from_float,
         nn.ELU: nnq.ELU.from_float,
         nn.LeakyReLU: nnq.LeakyReLU.from_float,
+        nn.Embedding: nnq.Embedding.from_float,
+        nn.EmbeddingBag: nnq.EmbeddingBag.from_float,
     }
     if hasattr(nnq, "Conv2d"):
         mapping[nn.Conv2d] = nnq.Conv2d.from_float
@@ -174,7 +176,7 @@ def convert(model: Module, inplace: bool = False) -> Module:
         mapping = dict(mapping)
         mapping[nn.Linear] = _mlx_linear_builder(relu=False)
         mapping[nni.LinearReLU] = _mlx_linear_builder(relu=True)
-    _convert_recursive(model, mapping, always=(nnq.DeQuantStub,))
+    _convert_recursive(model, mapping, always=(nnq.DeQuantStub, nn.Embedding, nn.EmbeddingBag))
     QConfigResolver.strip(model)
     model.eval()
     return model

@@ -39,6 +39,8 @@ function                      follows (lucid-official/lucid)
                               errors instead of the reference's Python loops)
 ``activation``                backend/cpu/methods/Activation.cpp:8-50, 375-460, 661-751;
                               Unary.cpp:165-170 (numpy float32; exp / tanh within rounding)
+``embedding_bag``             backend/cpu/methods/Sequence.cpp:8-93 (bags: IndexBounds.h:107-150;
+                              per_sample_weights: nn/functional/sparse.py:228-310)
 ``lucid_*``                   the multi-pass CPU composition timed as the CPU baseline
 ============================  ==========================================================
 
@@ -121,6 +123,7 @@ def _declare(L: ctypes.CDLL) -> None:
     L.lqo_lucid_quantize.argtypes = [_P, _I64, _F, _F, _I, _I, _P, _P, _P]
     L.lqo_lucid_dequantize.argtypes = [_P, _I64, _F, _F, _P, _P]
     L.lqo_set_threads.argtypes, L.lqo_set_threads.restype = [_I], _I
+    L.lqo_div6_mismatches.argtypes, L.lqo_div6_mismatches.restype = [], _I64
 
 
 def _ptr(a: np.ndarray | None) -> int | None:
@@ -392,6 +395,12 @@ def set_threads(n: int) -> int:
     return lib().lqo_set_threads(int(n))
 
 
+def div6_mismatches() -> int:
+    """Inputs (of all 2^32 float32) where the GPU activations' fma-corrected division by 6
+    differs from the IEEE quotient (0 = the rewrite is exact)."""
+    return int(lib().lqo_div6_mismatches())
+
+
 def lucid_minmax(x: np.ndarray):
     mn = ctypes.c_float()
     mx = ctypes.c_float()
@@ -529,3 +538,58 @@ def activation(x: np.ndarray, op: int, param: float = 0.0) -> np.ndarray:
         if op == ACT_LEAKY_RELU:
             return np.where(x >= f(0), x, p * x).astype(np.float32)
     raise ValueError(f"unknown activation {op}")
+
+
+# ---------------------------------------------------------------- table lookups
+
+BAG_SUM, BAG_MEAN, BAG_MAX = 0, 1, 2
+
+
+def embedding_bag(table: np.ndarray, idx: np.ndarray, offsets=None, mode: int = BAG_MEAN,
+                  padding_idx: int = -1, include_last_offset: bool = False, bag_len: int = 0,
+                  per_sample_weights=None) -> np.ndarray:
+    """Pooled lookup over a float32 table (Lucid's CPU kernel, backend/cpu/methods/
+    Sequence.cpp:8-93, bags from IndexBounds.h:107-150; per_sample_weights as the composite of
+    nn/functional/sparse.py:228-310): each bag walks its indices in order with float32
+    additions (sum / mean) or ``v > acc`` replacements from the lowest float (max); padding
+    indices skipped and not counted (with weights they add ``v * 0``); mean divides by the
+    count when it is positive; an empty max bag is 0.  A bad index raises, as the CPU does."""
+    f = np.float32
+    table = np.asarray(table, np.float32)
+    idx = np.asarray(idx).ravel().astype(np.int64)
+    rows, D = table.shape
+    n = idx.size
+    if offsets is None:
+        nb = n // bag_len
+        bounds = [(b * bag_len, (b + 1) * bag_len) for b in range(nb)]
+    else:
+        off = [int(v) for v in np.asarray(offsets).ravel()]
+        nb = len(off) - 1 if include_last_offset and off else len(off)
+        bounds = [(off[b], off[b + 1] if b + 1 < len(off) else n) for b in range(nb)]
+    w = None if per_sample_weights is None else np.asarray(per_sample_weights, np.float32).ravel()
+    out = np.zeros((nb, D), np.float32)
+    for b, (s, e) in enumerate(bounds):
+        acc = np.full(D, np.finfo(np.float32).min if mode == BAG_MAX else 0.0, np.float32)
+        count = 0
+        for k in range(s, e):
+            r = int(idx[k])
+            pad = padding_idx >= 0 and r == padding_idx
+            if pad and w is None:
+                continue
+            if not 0 <= r < rows:
+                raise IndexError(f"embedding_bag: index {r} out of range")
+            v = table[r]
+            if w is not None:
+                acc = (acc + (v * (f(0) if pad else w[k])).astype(np.float32)).astype(np.float32)
+            elif mode == BAG_MAX:
+                acc = np.where(v > acc, v, acc).astype(np.float32)
+            else:
+                acc = (acc + v).astype(np.float32)
+            if not pad:
+                count += 1
+        if mode == BAG_MAX and count == 0:
+            acc = np.zeros(D, np.float32)
+        if mode == BAG_MEAN and count > 0:
+            acc = (acc / f(count)).astype(np.float32)
+        out[b] = acc
+    return out

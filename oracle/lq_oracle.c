@@ -13,6 +13,7 @@
  *   OB = lucid/quantization/observer.py
  *   BK = lucid/_C/backend/cpu/
  */
+#include <float.h>
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -590,4 +591,36 @@ int lqo_set_threads(int n) {
     (void)n;
     return 1;
 #endif
+}
+
+/* The division by 6 of the GPU hardsigmoid / hardswish (lucid_amd/csrc/lq_act.hip): a
+ * multiply by fl32(1/6) corrected by one fma residual step where 2^-125 <= |t| <= FLT_MAX, the
+ * IEEE division elsewhere.  Returns how many of the 2^32 float32 inputs t (NaNs skipped) give
+ * a result other than the IEEE quotient fl32(t / 6) that Lucid computes
+ * (backend/cpu/methods/Activation.cpp:680, 743); the rewrite is valid iff this is 0. */
+int64_t lqo_div6_mismatches(void) {
+    const float r = 1.0f / 6.0f;
+    int64_t bad = 0;
+#pragma omp parallel for reduction(+ : bad) schedule(static)
+    for (int64_t i = 0; i < (int64_t)1 << 32; ++i) {
+        const uint32_t u = (uint32_t)i;
+        float t;
+        memcpy(&t, &u, 4);
+        if (t != t) continue;
+        const float want = t / 6.0f;
+        float q;
+        const float a = fabsf(t);
+        if (a >= 0x1p-125f && a <= FLT_MAX) {
+            const float q0 = t * r;
+            const float e = fmaf(-q0, 6.0f, t);
+            q = fmaf(e, r, q0);
+        } else {
+            q = t / 6.0f;
+        }
+        uint32_t uq, uw;
+        memcpy(&uq, &q, 4);
+        memcpy(&uw, &want, 4);
+        bad += uq != uw;
+    }
+    return bad;
 }

@@ -522,3 +522,56 @@ def test_activation_special_values():
     # -0 >= 0 holds: leaky_relu and elu keep -0
     assert np.signbit(O.activation(x[3:4], O.ACT_LEAKY_RELU, 0.1)[0])
     assert np.signbit(O.activation(x[3:4], O.ACT_ELU, 1.0)[0])
+
+
+# ---------------------------------------------------------------- table lookups
+
+
+def test_embedding_bag_closed_forms():
+    # integer-valued tables: every float32 sum below is exact, so sum / mean / max are the
+    # textbook reductions over each bag's non-padding rows
+    rng = np.random.default_rng(5)
+    table = rng.integers(-50, 50, (30, 7)).astype(np.float32)
+    idx = rng.integers(0, 30, 40)
+    offsets = np.array([0, 0, 3, 10, 10, 25, 39])
+    pad = int(idx[4])
+    for mode in (O.BAG_SUM, O.BAG_MEAN, O.BAG_MAX):
+        got = O.embedding_bag(table, idx, offsets, mode, padding_idx=pad)
+        ends = list(offsets[1:]) + [idx.size]
+        for b, (s, e) in enumerate(zip(offsets, ends)):
+            keep = [int(r) for r in idx[s:e] if r != pad]
+            if not keep:
+                np.testing.assert_array_equal(got[b], 0.0)
+                continue
+            rows = table[keep].astype(np.float64)
+            want = {O.BAG_SUM: rows.sum(0), O.BAG_MEAN: rows.sum(0) / len(keep), O.BAG_MAX: rows.max(0)}[mode]
+            np.testing.assert_array_equal(got[b], want.astype(np.float32))
+
+
+def test_embedding_bag_in_order_float32_sum():
+    # non-exact sums: the bag is the sequential float32 accumulation (np.cumsum in float32 adds
+    # in order), not a pairwise or float64 one; include_last_offset drops the tail
+    rng = np.random.default_rng(6)
+    table = (rng.standard_normal((50, 9)) * 1e3).astype(np.float32)
+    table[::7] *= 1e-4
+    idx = rng.integers(0, 50, 60)
+    offsets = np.array([0, 17, 17, 44, 55])
+    got = O.embedding_bag(table, idx, offsets, O.BAG_SUM, include_last_offset=True)
+    assert got.shape == (4, 9)
+    for b in range(4):
+        rows = table[idx[offsets[b]:offsets[b + 1]]]
+        want = np.cumsum(rows, axis=0, dtype=np.float32)[-1] if len(rows) else np.zeros(9, np.float32)
+        np.testing.assert_array_equal(got[b], want)
+    # 2-D input: one bag per row; per_sample_weights: the float32 products summed in order
+    w = rng.standard_normal(60).astype(np.float32)
+    got2 = O.embedding_bag(table, idx.reshape(6, 10), None, O.BAG_SUM, bag_len=10, per_sample_weights=w)
+    for b in range(6):
+        prod = (table[idx[10 * b:10 * b + 10]] * w[10 * b:10 * b + 10, None]).astype(np.float32)
+        np.testing.assert_array_equal(got2[b], np.cumsum(prod, axis=0, dtype=np.float32)[-1])
+
+
+def test_div6_rewrite_is_exact_for_every_float():
+    # the GPU hardsigmoid / hardswish divide by 6 as a reciprocal multiply plus one fma
+    # residual correction (IEEE division where |t| < 2^-125 or not finite); exhaustive over
+    # all 2^32 inputs against the IEEE quotient Lucid computes
+    assert O.div6_mismatches() == 0
