@@ -22,7 +22,7 @@
 //
 // Work split: each thread owns groups of E consecutive elements, E = 16 bytes over the wider
 // of the input and output element sizes, so every load and store is one 4-16 byte access,
-// with four groups in flight; workgroups take contiguous runs of groups.  Misaligned pointers
+// with eight groups in flight; workgroups take contiguous runs of groups.  Misaligned pointers
 // fall back to one element per step.  One-byte code inputs read a 256-entry table of outputs
 // built per workgroup in LDS instead of evaluating the activation per element.
 #include <hip/hip_runtime.h>
@@ -142,7 +142,7 @@ __global__ __launch_bounds__(kActBlock) void act_kernel(ActArgs a) {
     using TO = typename ElemOf<OUT>::type;
     constexpr int WIDE = sizeof(TI) > sizeof(TO) ? sizeof(TI) : sizeof(TO);
     constexpr int E = 16 / WIDE;
-    constexpr int U = 4;  // groups in flight per thread
+    constexpr int U = 8;  // groups in flight per thread
     using VI = typename RawVec<E * sizeof(TI)>::type;
     using VO = typename RawVec<E * sizeof(TO)>::type;
     __shared__ TO lut[kActLut<IN> ? 256 : 1];
@@ -236,10 +236,10 @@ int lq_qact(int op, const void* d_x, int x_type, const float* d_x_scale, const f
     const bool vec = ((uintptr_t)d_x & mx) == 0 && ((uintptr_t)d_y & my) == 0;
     ActArgs a{op, d_x, x_type == LQ_F32 ? nullptr : d_x_scale, x_type == LQ_F32 ? nullptr : d_x_zero_point,
               n, param, d_out_scale, d_out_zero_point, make_grid(qmin, qmax), d_y, vec ? 1 : 0};
-    // enough groups per thread to amortize the scale loads; at most 8 workgroups per CU
+    // a few groups per thread; up to 32 workgroups per CU to keep enough loads in flight
     const int64_t units = vec ? n / E : n;
     int64_t blocks = (units + 4 * kActBlock - 1) / (4 * kActBlock);
-    if (blocks > 2048) blocks = 2048;
+    if (blocks > 8192) blocks = 8192;
     if (blocks < 1) blocks = 1;
     const dim3 grid((unsigned)blocks);
     hipStream_t st = as_stream(stream);
