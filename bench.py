@@ -306,7 +306,7 @@ def conv_lines(L, C, timer, steps, warmup, batch=32):
         b = L.tensor(rng.standard_normal(cout).astype(np.float32), device="gpu")
         so = L.tensor(np.float32(0.05), device="gpu")
         zo = L.tensor(np.float32(0.0), device="gpu")
-        ws_bytes = lib.lq_conv2d_i8_workspace_size(batch, cin, H, H, 1, pd, pd, pd, pd)
+        ws_bytes = lib.lq_conv2d_i8_workspace_size(batch, cin, H, H, cout, k, k, st, st, pd, pd, pd, pd, 1, 1, 1)
         ws = L.empty((ws_bytes,), np.int8, "gpu")
         args = (x.data_ptr(), C.U8S8, batch, cin, H, H, wp.data_ptr(), sums.data_ptr(), cout, k, k, st, st,
                 pd, pd, pd, pd, 1, 1, 1, 0, sa.data_ptr(), za.data_ptr(), sw.data_ptr(), b.data_ptr(),

@@ -406,9 +406,12 @@ int lq_conv2d_pack_weights_i8(const int8_t* d_w, int64_t Cout, int64_t Cin_g, in
  * out_kind, written NCHW to d_y[N, Cout, OH, OW].  Replaces dequantize -> F.conv2d ->
  * fake_quantize of lucid/nn/quantized/conv.py:137-172 (-> lucid/nn/functional/conv.py:53-84
  * -> lucid/_C/backend/cpu/methods/Conv.cpp:271-360).  padding_mode LQ_PAD_*; workspace of
- * lq_conv2d_i8_workspace_size bytes (the padded NHWC copy of x).  Two launches. */
-size_t lq_conv2d_i8_workspace_size(int64_t N, int64_t C, int64_t H, int64_t W, int64_t groups, int pad_top,
-                                   int pad_bottom, int pad_left, int pad_right);
+ * lq_conv2d_i8_workspace_size bytes (same arguments as the call: the padded NHWC copy of x,
+ * plus the int32 tile sums of a split K when the output has fewer tiles than the GPU has
+ * CUs).  Two launches (three with a split K). */
+size_t lq_conv2d_i8_workspace_size(int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout, int64_t KH, int64_t KW,
+                                   int stride_h, int stride_w, int pad_top, int pad_bottom, int pad_left,
+                                   int pad_right, int dilation_h, int dilation_w, int64_t groups);
 int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64_t H, int64_t W,
                  const int8_t* d_w_packed, const int32_t* d_w_sums, int64_t Cout, int64_t KH, int64_t KW,
                  int stride_h, int stride_w, int pad_top, int pad_bottom, int pad_left, int pad_right,

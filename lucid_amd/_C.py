@@ -102,7 +102,8 @@ _SIGNATURES: dict[str, tuple] = {
                                  _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _SZ, _P]),
     "lq_conv2d_weight_pack_size": (_SZ, [_I64, _I64, _I64, _I64]),
     "lq_conv2d_pack_weights_i8": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P]),
-    "lq_conv2d_i8_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I, _I, _I, _I]),
+    "lq_conv2d_i8_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I,
+                                          _I64]),
     "lq_conv2d_i8": (_I, [_P, _I, _I64, _I64, _I64, _I64, _P, _P, _I64, _I64, _I64, _I, _I, _I, _I, _I,
                           _I, _I, _I, _I64, _I, _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _P, _SZ,
                           _P]),

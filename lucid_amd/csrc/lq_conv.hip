@@ -27,6 +27,9 @@
 // one contiguous NCHW store.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+#include <utility>
+
 #include "lq_dma.h"
 #include "lq_epilogue.h"
 #include "lq_internal.h"
@@ -428,6 +431,10 @@ __global__ __launch_bounds__(CV_THREADS) void conv_i8_kernel(ConvArgs a) {
 // rho % 4), so a lane's results are 16 consecutive pixels of one output channel: one 16-byte
 // NCHW store per channel for int8 outputs.
 constexpr int CV_MAX_TAPS = 128;
+// Stage buffers of the 128 x 64 tile.  Two, like the 256 x 64 tile: a four-stage ring
+// (96 KB of LDS, one workgroup per CU) measured 15-30% slower on the ResNet-18 layers than
+// two stages with several workgroups per CU.
+constexpr int CV_SMALL_NBUF = 2;
 
 struct ConvDmaArgs {
     const int8_t* xp;
@@ -446,9 +453,14 @@ struct ConvDmaArgs {
     const float* out_scale;
     const float* out_zp;
     int qmin, qmax, relu;
+    // split-K: with splits > 1 a first launch (phase 0, gridDim.z = G * splits) leaves each
+    // split's exact int32 tile sums in part; a second launch (phase 1, gridDim.z = G) adds
+    // them in split order and runs the epilogue
+    int splits, phase;
+    int32_t* part;
 };
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int KIND>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int NBUF, int KIND>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void conv_i8_dma_kernel(ConvDmaArgs a) {
     constexpr int BK = 128, NW = WAVES_M * WAVES_N, WM = BM / WAVES_M, WN = BN / WAVES_N;
     constexpr int FM = WM / 16, FN = WN / 16;
@@ -456,13 +468,24 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void conv_i8_dma_kernel(Con
     constexpr bool INT_CODES = KIND == LQ_OUT_Q8 || KIND == LQ_OUT_QU8 || KIND == LQ_OUT_Q16 || KIND == LQ_OUT_QU8S8;
     static_assert(WM == 64, "a lane owns 16 consecutive pixels of a 64-pixel wave tile");
     static_assert(A_I * 8 * NW == BM && B_I * 8 * NW == BN && WN % 16 == 0, "copy split");
-    __shared__ __attribute__((aligned(1024))) int8_t lds[2 * SB];
+    static_assert(NBUF >= 2 && (NBUF - 1) * LPS < 64, "stage ring");
+    __shared__ __attribute__((aligned(1024))) int8_t lds[NBUF * SB];
 
-    const int p0 = blockIdx.x * BM, co0 = blockIdx.y * BN, g = blockIdx.z;
+    const int p0 = blockIdx.x * BM, co0 = blockIdx.y * BN;
+    const int split = a.phase == 0 ? (int)blockIdx.z % a.splits : 0;
+    const int g = a.phase == 0 ? (int)blockIdx.z / a.splits : (int)blockIdx.z;
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int GCp = a.G * a.Cp;
+    // K stages of this split: [kb, kb + nks)
+    const int per_split = (a.nk + a.splits - 1) / a.splits;
+    const int kb = split * per_split;
+    const int nks = min(a.nk - kb, per_split);
+    // this tile's partial sums: splits x (FN x FM fragments) x (threads) int32x4, thread-minor
+    constexpr int NFRAG = FN * FM;
+    const int64_t tile_lin = ((int64_t)g * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
+    v4i* part = reinterpret_cast<v4i*>(a.part) + tile_lin * a.splits * NFRAG * (64 * NW) + threadIdx.x;
     const int taps = a.KH * a.KW;
     // input offset of tap t (the K padding past KH * KW reads tap 0; its weights are zero)
     auto tap_off = [&](int t) __attribute__((always_inline)) {
@@ -494,7 +517,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void conv_i8_dma_kernel(Con
     }
     const uint32_t lds_base = (uint32_t)reinterpret_cast<uintptr_t>(lds);
     auto issue = [&](int buf, int kt) __attribute__((always_inline)) {
-        const int k0 = min(kt, a.nk - 1) * BK;
+        const int k0 = (kb + min(kt, nks - 1)) * BK;
         const uint32_t sb = lds_base + buf * SB;
         const int tap_u = a.cp_shift < 0 ? k0 / a.Cp : 0;  // Cp a multiple of 128: one tap per stage
 #pragma unroll
@@ -535,31 +558,75 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void conv_i8_dma_kernel(Con
             for (int j = 0; j < FM; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f[j], f[FM + i], acc[i][j], 0, 0, 0);
     };
+    // A ring of NBUF stage buffers: NBUF stages are issued up front; at stage kt the wait
+    // leaves stages kt+2 .. kt+NBUF-1 in flight, and after the barrier (every wave's reads of
+    // buffer kt done) stage kt+NBUF is issued into it.  Stages past the end are clamped to the
+    // last (a valid address, landing in a buffer never read again), so the counts are static.
     auto stage = [&](auto bc, int kt, bool last) __attribute__((always_inline)) {
         constexpr int B = decltype(bc)::value;
         read_frags(F1, B, 1);
         mfmas(F0);
         if (!last) {
-            wait_vmcnt<0>();
+            wait_vmcnt<(NBUF - 2) * LPS>();
             block_barrier();
-            issue(B, kt + 2);
-            read_frags(F0, B ^ 1, 0);
+            issue(B, kt + NBUF);
+            read_frags(F0, (B + 1) % NBUF, 0);
         }
         mfmas(F1);
     };
-    issue(0, 0);
-    issue(1, 1);
-    wait_vmcnt<LPS>();
-    block_barrier();
-    read_frags(F0, 0, 0);
-    int kt = 0;
-    for (; kt + 2 < a.nk; kt += 2) {
-        stage(std::integral_constant<int, 0>(), kt, false);
-        stage(std::integral_constant<int, 1>(), kt + 1, false);
+    // Epilogue inputs of this lane's FN channels, loaded before the main loop so their latency
+    // hides under it (they are the oldest loads: the stage waits cover them).
+    const int rho_e = lane & 15;
+    float csb[FN], cbias[FN];
+    int32_t cws[FN];
+    const bool epilogue_here = a.phase == 1 || a.splits == 1;
+    if (epilogue_here) {
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+            const int col = min(co0 + wn * WN + 16 * i + rho_e, a.Cout_g - 1);
+            const int co = g * a.Cout_g + col;
+            csb[i] = a.w_scale[co];
+            cbias[i] = a.bias ? a.bias[co] : 0.0f;
+            cws[i] = (a.a_zp != nullptr || a.a_u8s8) ? a.w_sums[co] : 0;
+        }
     }
-    stage(std::integral_constant<int, 0>(), kt, kt + 1 == a.nk);
-    if (kt + 1 < a.nk) stage(std::integral_constant<int, 1>(), kt + 1, true);
-    wait_vmcnt<0>();  // no copy may still target LDS when the workgroup ends
+    if (a.phase == 1) {
+        // the splits' exact sums, added in split order (int32 wrap-around: any order gives the
+        // same bits)
+#pragma unroll
+        for (int sp = 0; sp < a.splits; ++sp)
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+#pragma unroll
+                for (int j = 0; j < FM; ++j) {
+                    const v4i v = part[((int64_t)sp * NFRAG + i * FM + j) * (64 * NW)];
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) acc[i][j][r] = (int)((uint32_t)acc[i][j][r] + (uint32_t)v[r]);
+                }
+    } else {
+#pragma unroll
+        for (int j = 0; j < NBUF; ++j) issue(j, j);
+        wait_vmcnt<(NBUF - 1) * LPS>();
+        block_barrier();
+        read_frags(F0, 0, 0);
+        int kt = 0;
+        for (; kt + NBUF < nks; kt += NBUF) {
+            [&]<int... B>(std::integer_sequence<int, B...>) {
+                (stage(std::integral_constant<int, B>(), kt + B, false), ...);
+            }(std::make_integer_sequence<int, NBUF>());
+        }
+        [&]<int... B>(std::integer_sequence<int, B...>) {
+            ((kt + B < nks ? stage(std::integral_constant<int, B>(), kt + B, kt + B + 1 == nks) : void()), ...);
+        }(std::make_integer_sequence<int, NBUF>());
+        wait_vmcnt<0>();  // no copy may still target LDS when the workgroup ends
+        if (a.splits > 1) {
+#pragma unroll
+            for (int i = 0; i < FN; ++i)
+#pragma unroll
+                for (int j = 0; j < FM; ++j) part[((int64_t)split * NFRAG + i * FM + j) * (64 * NW)] = acc[i][j];
+            return;
+        }
+    }
 
     // Epilogue: acc[i][j][r] is pixel p0 + wm*64 + 16 (lane/16) + 4 j + r, channel
     // co0 + wn*WN + 16 i + lane % 16 (within the group).
@@ -584,9 +651,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void conv_i8_dma_kernel(Con
         const int col = co0 + wn * WN + 16 * i + rho;
         if (col >= a.Cout_g) continue;
         const int co = g * a.Cout_g + col;
-        const float sb = a.w_scale[co];
-        const float bias = a.bias ? a.bias[co] : 0.0f;
-        const int32_t zsum = ep.has_za ? (int32_t)((uint32_t)ep.za * (uint32_t)a.w_sums[co]) : 0;
+        const float sb = csb[i];
+        const float bias = cbias[i];
+        const int32_t zsum = ep.has_za ? (int32_t)((uint32_t)ep.za * (uint32_t)cws[i]) : 0;
         uint32_t out[16];
 #pragma unroll
         for (int q = 0; q < 16; ++q) {
@@ -713,6 +780,48 @@ constexpr int64_t CV_MAX = (int64_t)1 << 31;
 // Packed weight row stride: K rounded up to whole 128-byte stages.
 int64_t conv_ldw(int64_t K) { return (K + 127) / 128 * 128; }
 
+// Launch plan of lq_conv2d_i8, shared by the call and its workspace query.
+struct ConvPlan {
+    bool dma, big;
+    int64_t Cp, ldw, gx, gy;
+    int splits;
+    size_t pack_bytes;  // padded NHWC input (rounded up to 256 bytes)
+    size_t part_bytes;  // split-K tile sums
+};
+
+ConvPlan conv_plan(int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout, int64_t KH, int64_t KW, int pt, int pb,
+                   int pl, int pr, int64_t OH, int64_t OW, int64_t groups) {
+    ConvPlan p{};
+    const int64_t Cg = C / groups, Cout_g = Cout / groups;
+    p.Cp = (Cg + 15) / 16 * 16;
+    p.pack_bytes = (size_t)((N * (H + pt + pb) * (W + pl + pr) * groups * p.Cp + 255) / 256 * 256);
+    const int64_t K = KH * KW * p.Cp;
+    p.ldw = conv_ldw(K);
+    const int64_t ntaps = (p.ldw + p.Cp - 1) / p.Cp;
+    const bool pow2 = p.Cp <= 128 && (p.Cp & (p.Cp - 1)) == 0;
+    const int64_t P = N * OH * OW;
+    p.dma = (pow2 || p.Cp % 128 == 0) && ntaps <= CV_MAX_TAPS && Cout_g * p.ldw < CV_MAX;
+    p.splits = 1;
+    if (!p.dma) return p;
+    p.gy = (Cout_g + 63) / 64;
+    p.big = ((P + 255) / 256) * p.gy * groups >= 256;
+    p.gx = (P + (p.big ? 255 : 127)) / (p.big ? 256 : 128);
+    // fewer tiles than CUs and a long K: split K so every CU has a tile (at least four
+    // 128-byte stages per split)
+    const int64_t tiles = p.gx * p.gy * groups;
+    const int64_t nk = p.ldw / 128;
+    // (below 128 tiles: at 196 tiles a 2-way split measured slower than none)
+    if (!p.big && tiles < 128 && nk >= 8) {
+        int64_t sp = std::min<int64_t>((256 + tiles - 1) / tiles, nk / 4);
+        while (sp > 1 && (sp - 1) * ((nk + sp - 1) / sp) >= nk) --sp;
+        if (sp > 1 && tiles * sp <= 65535) {
+            p.splits = (int)sp;
+            p.part_bytes = (size_t)(tiles * sp * 128 * 64 * 4);
+        }
+    }
+    return p;
+}
+
 }  // namespace
 }  // namespace lq
 
@@ -744,11 +853,16 @@ int lq_conv2d_pack_weights_i8(const int8_t* d_w, int64_t Cout, int64_t Cin_g, in
     return launch_status("lq_conv2d_pack_weights_i8");
 }
 
-size_t lq_conv2d_i8_workspace_size(int64_t N, int64_t C, int64_t H, int64_t W, int64_t groups, int pad_top,
-                                   int pad_bottom, int pad_left, int pad_right) {
-    if (N < 0 || C < 1 || H < 1 || W < 1 || groups < 1 || C % groups) return 0;
-    const int64_t Cp = (C / groups + 15) / 16 * 16;
-    return (size_t)(N * (H + pad_top + pad_bottom) * (W + pad_left + pad_right) * groups * Cp);
+size_t lq_conv2d_i8_workspace_size(int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout, int64_t KH, int64_t KW,
+                                   int stride_h, int stride_w, int pad_top, int pad_bottom, int pad_left,
+                                   int pad_right, int dilation_h, int dilation_w, int64_t groups) {
+    if (N < 0 || C < 1 || H < 1 || W < 1 || Cout < 1 || groups < 1 || C % groups || Cout % groups) return 0;
+    int64_t OH = 0, OW = 0;
+    if (!conv_geometry(H, W, (int)KH, (int)KW, stride_h, stride_w, pad_top, pad_bottom, pad_left, pad_right,
+                       dilation_h, dilation_w, &OH, &OW))
+        return 0;
+    const ConvPlan pl = conv_plan(N, C, H, W, Cout, KH, KW, pad_top, pad_bottom, pad_left, pad_right, OH, OW, groups);
+    return pl.pack_bytes + pl.part_bytes;
 }
 
 int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64_t H, int64_t W,
@@ -784,8 +898,9 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
     const bool has_za = d_a_zero_point != nullptr || x_code_type == LQ_U8S8;
     LQ_REQUIRE(!has_za || d_w_sums, "lq_conv2d_i8: an activation zero point needs the weight sums d_w_sums");
     LQ_REQUIRE(aligned16(d_w_packed) && aligned16(d_workspace), "lq_conv2d_i8: packed weights and workspace must be 16-byte aligned");
-    const size_t need = lq_conv2d_i8_workspace_size(N, C, H, W, groups, pad_top, pad_bottom, pad_left, pad_right);
-    LQ_REQUIRE(d_workspace && workspace_bytes >= need, "lq_conv2d_i8: workspace smaller than lq_conv2d_i8_workspace_size");
+    const ConvPlan plan = conv_plan(N, C, H, W, Cout, KH, KW, pad_top, pad_bottom, pad_left, pad_right, OH, OW, groups);
+    LQ_REQUIRE(d_workspace && workspace_bytes >= plan.pack_bytes + plan.part_bytes,
+               "lq_conv2d_i8: workspace smaller than lq_conv2d_i8_workspace_size");
     hipStream_t st = as_stream(stream);
 
     PackArgs pa{};
@@ -831,10 +946,9 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
     a.relu = (flags & LQ_EPI_RELU) ? 1 : 0;
     // LDS-DMA kernel: whole 16-byte chunks of one tap per copy (Cp a power of two up to 128,
     // or a multiple of 128) and a tap table that fits.
-    const int64_t ldw = conv_ldw(K);
-    const int64_t ntaps = (ldw + Cp - 1) / Cp;
+    const int64_t ldw = plan.ldw;
     const bool pow2 = Cp <= 128 && (Cp & (Cp - 1)) == 0;
-    if ((pow2 || Cp % 128 == 0) && ntaps <= CV_MAX_TAPS && Cout_g * ldw < CV_MAX) {
+    if (plan.dma) {
         ConvDmaArgs d{};
         d.xp = pa.xp;
         d.wp = d_w_packed;
@@ -852,12 +966,22 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
         d.w_scale = d_w_scale; d.w_sums = d_w_sums; d.bias = d_bias;
         d.out_scale = d_out_scale; d.out_zp = d_out_zero_point;
         d.qmin = out_qmin; d.qmax = out_qmax; d.relu = a.relu;
-        const int64_t ctiles = (Cout_g + 63) / 64;
-        const bool big = ((P + 255) / 256) * ctiles * groups >= 256;
-        const dim3 grid((unsigned)((P + (big ? 255 : 127)) / (big ? 256 : 128)), (unsigned)ctiles, (unsigned)groups);
+        d.splits = plan.splits;
+        d.part = reinterpret_cast<int32_t*>(static_cast<int8_t*>(d_workspace) + plan.pack_bytes);
+        const bool big = plan.big;
+        const dim3 grid((unsigned)plan.gx, (unsigned)plan.gy, (unsigned)groups);
+        const dim3 grid0((unsigned)plan.gx, (unsigned)plan.gy, (unsigned)(groups * plan.splits));
+        ConvDmaArgs d1 = d;
+        d.phase = 0;
+        d1.phase = 1;
 #define LQ_CONV_DMA(K_)                                                                                        \
-    if (big) hipLaunchKernelGGL((conv_i8_dma_kernel<256, 64, 4, 1, K_>), grid, dim3(256), 0, st, d);        \
-    else hipLaunchKernelGGL((conv_i8_dma_kernel<128, 64, 2, 2, K_>), grid, dim3(256), 0, st, d);            \
+    if (big) {                                                                                                 \
+        hipLaunchKernelGGL((conv_i8_dma_kernel<256, 64, 4, 1, 2, K_>), grid, dim3(256), 0, st, d);            \
+    } else {                                                                                                   \
+        hipLaunchKernelGGL((conv_i8_dma_kernel<128, 64, 2, 2, CV_SMALL_NBUF, K_>), grid0, dim3(256), 0, st, d); \
+        if (plan.splits > 1)                                                                                   \
+            hipLaunchKernelGGL((conv_i8_dma_kernel<128, 64, 2, 2, CV_SMALL_NBUF, K_>), grid, dim3(256), 0, st, d1); \
+    }                                                                                                          \
     break;
         switch (out_kind) {
             case LQ_OUT_I32: LQ_CONV_DMA(LQ_OUT_I32)

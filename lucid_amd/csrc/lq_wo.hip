@@ -230,7 +230,9 @@ struct PChunk {
 // owns 8 S consecutive k of the block, l % 16 the row).  Same zero fill (rows past M, k past
 // K), same max / sum shuffles, same power-of-two pre-scale and hi / lo split in the same
 // element order, so the GEMV's products and sums are unchanged.  Layout: block (mt, t) holds
-// 64 lanes x 2 S vu4 (hi, lo per step); meta (mt, t, row).
+// 2 S slots (hi, lo per step) of 64 lanes' vu4 each, lane-contiguous within a slot (coalesced
+// 1 KB loads; a lane-major layout made every load touch 64 separate cache lines); meta
+// (mt, t, row).
 template <int BITS, int S>
 __global__ __launch_bounds__(64) void wo_xprep_kernel(const float* __restrict__ x, int64_t ldx, int M, int K, int TW,
                                                       vu4* __restrict__ xp, float2* __restrict__ xm) {
@@ -255,7 +257,9 @@ __global__ __launch_bounds__(64) void wo_xprep_kernel(const float* __restrict__ 
     int e = 0;
     if (amax > 0.0f && amax <= 3.0e38f) e = min(max(14 - ilogbf(amax), -120), 120);
     const float up = ldexpf(1.0f, e);
-    vu4* dst = xp + ((int64_t)(mt * TW + t) * 64 + lane) * 2 * S;
+    // slot i of the block's 2 S slots holds the 64 lanes' 16-byte pieces contiguously, so each
+    // GEMV load instruction reads 1 KB of consecutive bytes
+    vu4* dst = xp + (int64_t)(mt * TW + t) * 2 * S * 64 + lane;
 #pragma unroll
     for (int j = 0; j < S; ++j) {
         h8 hi, lo;
@@ -266,8 +270,8 @@ __global__ __launch_bounds__(64) void wo_xprep_kernel(const float* __restrict__ 
             hi[h] = vh;
             lo[h] = (_Float16)(v - (float)vh);
         }
-        dst[2 * j] = __builtin_bit_cast(vu4, hi);
-        dst[2 * j + 1] = __builtin_bit_cast(vu4, lo);
+        dst[(2 * j) * 64] = __builtin_bit_cast(vu4, hi);
+        dst[(2 * j + 1) * 64] = __builtin_bit_cast(vu4, lo);
     }
     if (q == 0) xm[(int64_t)(mt * TW + t) * 16 + l16] = make_float2(ldexpf(1.0f, -e), bsum);
 }
@@ -313,9 +317,9 @@ __global__ __launch_bounds__((64 * wo_max_waves(S, XF32, GROUPED))) void wo_gemv
         load_w<BITS, S, VEC>(wc, wrow, kc, a.K);
         if constexpr (PREP) {
             const int64_t blk = (int64_t)blockIdx.y * TW + t;
-            const vu4* src = a.xp + (blk * 64 + lane) * 2 * S;
+            const vu4* src = a.xp + blk * 2 * S * 64 + lane;
 #pragma unroll
-            for (int i = 0; i < 2 * S; ++i) xc.v[i] = src[i];
+            for (int i = 0; i < 2 * S; ++i) xc.v[i] = src[i * 64];
             xc.meta = a.xm[blk * 16 + l16];
         } else {
             load_x<S, XF32, VEC>(xc, xrow, row_ok, kc, a.K);

@@ -150,7 +150,8 @@ class Conv2d(Module):
         out_kind, code_type = kind
         codes = empty((N, Cout, OH, OW), np.int8, "gpu")
         if N:
-            ws_bytes = _C.lib().lq_conv2d_i8_workspace_size(N, C, H, W, self.groups, pt, pb, pl, pr)
+            ws_bytes = _C.lib().lq_conv2d_i8_workspace_size(N, C, H, W, Cout, KH, KW, sh, sw, pt, pb, pl, pr, dh, dw,
+                                                            self.groups)
             b = on_device(self.bias) if self.bias is not None else None
             _C.call("lq_conv2d_i8", q.codes.data_ptr(), q.code_type, N, C, H, W, ops.packed.data_ptr(),
                     ops.sums.data_ptr(), Cout, KH, KW, sh, sw, pt, pb, pl, pr, dh, dw, self.groups,

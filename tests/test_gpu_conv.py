@@ -52,7 +52,7 @@ def run_conv(L, x, w, *, u8s8=False, za=None, stride=(1, 1), pad=(0, 0, 0, 0), d
     wp, sums = pack_conv_weights(L, w)
     OH, OW = O.conv_out_hw(H, W, KH, KW, stride, pad, dilation)
     y = L.empty((N, Cout, OH, OW), _OUT_DT[out_kind], "gpu")
-    ws_bytes = _C.lib().lq_conv2d_i8_workspace_size(N, C, H, W, groups, *pad)
+    ws_bytes = _C.lib().lq_conv2d_i8_workspace_size(N, C, H, W, Cout, KH, KW, *stride, *pad, *dilation, groups)
     ws = L.empty((max(ws_bytes, 16),), np.int8, "gpu")
     keep = []
 
@@ -111,6 +111,9 @@ CASES = [
     (1, 20, 7, 9, 100, 5, 3, (1, 1), (2, 2, 1, 1), (1, 1), 1, 2),       # replicate
     (1, 17, 6, 6, 70, 3, 3, (2, 2), (1, 1, 1, 1), (1, 1), 1, 3),        # circular, ragged C
     (4, 64, 28, 28, 64, 3, 3, (1, 1), (1, 1, 1, 1), (1, 1), 1, 0),      # many pixel tiles
+    (2, 256, 7, 7, 256, 3, 3, (1, 1), (1, 1, 1, 1), (1, 1), 1, 0),      # split K over 4
+    (1, 512, 7, 7, 512, 3, 3, (1, 1), (1, 1, 1, 1), (1, 1), 1, 0),      # ResNet layer4: split K over 9
+    (2, 256, 6, 6, 128, 3, 3, (1, 1), (1, 1, 1, 1), (1, 1), 2, 0),      # split K with groups
 ]
 
 
