@@ -384,6 +384,24 @@ int lq_embedding_bag(const void* d_table, int table_type, const float* d_scale, 
                      int64_t bag_len, int mode, int64_t padding_idx, const float* d_per_sample_weights,
                      float* d_out, void* stream);
 
+/* ---- pooling ---------------------------------------------------------------------- */
+enum { LQ_POOL_MAX = 0, LQ_POOL_AVG = 1 };
+enum { LQ_POOL_ADAPTIVE = 1, LQ_POOL_COUNT_INCLUDE_PAD = 2 };
+/* 2-D pooling of x[N, C, H, W] into y[N, C, OH, OW] (NCHW, contiguous).  Windows: KH x KW at
+ * stride (stride_h, stride_w) with implicit padding (pad at most half the window; OH / OW as
+ * floor((H + 2 pad - K) / stride) + 1), or with LQ_POOL_ADAPTIVE the cells
+ * [floor(o S / O), ceil((o + 1) S / O)) of an adaptive pool.  LQ_POOL_MAX: the first
+ * in-window element replaced by any greater one or by a NaN (padding skipped); y has x's
+ * element type, and a code input stays on its grid (codes compare as their values).
+ * LQ_POOL_AVG: float32 sum in row-major window order divided by the window size (with
+ * LQ_POOL_COUNT_INCLUDE_PAD the padded size), y float32; a code input (LQ_I8 / LQ_U8 / LQ_I16 /
+ * LQ_U8S8) is read as fl32(fl32(float(c) - z) * s).  Replaces max_pool2d / avg_pool2d /
+ * adaptive_avg_pool2d (lucid/_C/backend/cpu/Pool.cpp:27-168,
+ * lucid/nn/functional/_pool_core.py:228-250, 407-434). */
+int lq_pool2d(int op, const void* d_x, int x_type, const float* d_x_scale, const float* d_x_zero_point, int64_t N,
+              int64_t C, int64_t H, int64_t W, int64_t OH, int64_t OW, int KH, int KW, int stride_h, int stride_w,
+              int pad_h, int pad_w, int flags, void* d_y, void* stream);
+
 /* ---- int8 Conv2d (implicit GEMM) ------------------------------------------------- */
 /* Padding modes of a convolution (Lucid's padding_mode, lucid/nn/functional/conv.py:24-29). */
 enum { LQ_PAD_ZEROS = 0, LQ_PAD_REFLECT = 1, LQ_PAD_REPLICATE = 2, LQ_PAD_CIRCULAR = 3 };

@@ -3,6 +3,8 @@
 from lucid_amd.nn.module import Module, Parameter
 from lucid_amd.nn.layers import (
     ELU,
+    AdaptiveAvgPool2d,
+    AvgPool2d,
     BatchNorm2d,
     Conv2d,
     Embedding,
@@ -13,6 +15,7 @@ from lucid_amd.nn.layers import (
     Identity,
     LeakyReLU,
     Linear,
+    MaxPool2d,
     ReLU,
     Sequential,
     Sigmoid,
@@ -21,7 +24,7 @@ from lucid_amd.nn.layers import (
 
 __all__ = ["Module", "Parameter", "Linear", "Conv2d", "ReLU", "Sequential", "Identity",
            "BatchNorm2d", "Flatten", "Sigmoid", "Tanh", "Hardswish", "Hardsigmoid", "ELU", "LeakyReLU",
-           "Embedding", "EmbeddingBag"]
+           "Embedding", "EmbeddingBag", "MaxPool2d", "AvgPool2d", "AdaptiveAvgPool2d"]
 
 
 def __getattr__(name: str):

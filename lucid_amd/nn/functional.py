@@ -308,3 +308,81 @@ def embedding_bag(input: Tensor, weight: Tensor, offsets: Tensor | None = None, 
     w = on_device(weight)
     return bag_lookup(w.data_ptr(), _C.F32, None, None, int(w.shape[0]), int(w.shape[1]), input, offsets, mode,
                       per_sample_weights, include_last_offset, padding_idx)
+
+
+# ------------------------------------------------------------------------- pooling
+
+
+def _pool_input(x: Tensor, op: str):
+    """(tensor, pointer, element type, scale ptr, zero-point ptr, QuantSource or None) of a
+    4-D pooling input: the codes of a code-backed activation, else float32 storage."""
+    from lucid_amd.nn.quantized.functional_module import _operand
+
+    if x.ndim != 4:
+        raise ValueError(f"{op}: expected a 4-D (N, C, H, W) input, got {x.ndim}-D")
+    ptr, xtype, xs, xz = _operand(x, op)
+    return ptr, xtype, xs, xz, x.quant_source if xtype != _C.F32 else None
+
+
+def max_pool2d(x: Tensor, kernel_size, stride=None, padding=0) -> Tensor:
+    """Max over KH x KW windows (lucid/_C/backend/cpu/Pool.cpp:27-100): NaN propagates; a
+    code-backed input keeps its grid (the max of the codes is the code of the max)."""
+    import numpy as np
+
+    from lucid_amd._tensor import QuantSource
+
+    KH, KW = _pair(kernel_size)
+    sh, sw = _pair(stride if stride is not None else kernel_size)
+    ph, pw = _pair(padding)
+    N, C, H, W = x.shape
+    if 2 * ph > KH or 2 * pw > KW:
+        raise ValueError("max_pool2d: padding should be at most half of the kernel size")
+    OH, OW = (H + 2 * ph - KH) // sh + 1, (W + 2 * pw - KW) // sw + 1
+    if OH < 1 or OW < 1:
+        raise ValueError("max_pool2d: kernel larger than the padded input")
+    ptr, xtype, _, _, q = _pool_input(x, "max_pool2d")
+    dt = np.float32 if q is None else q.codes.dtype
+    y = empty((N, C, OH, OW), dt, "gpu")
+    if y.numel():
+        _C.call("lq_pool2d", _C.POOL_MAX, ptr, xtype, None, None, N, C, H, W, OH, OW, KH, KW, sh, sw, ph, pw, 0,
+                y.data_ptr(), None)
+    if q is None:
+        return y
+    return Tensor._code_backed(QuantSource(y, q.code_type, q.scale, q.zero_point, q.quant_min, q.quant_max), y.shape)
+
+
+def avg_pool2d(x: Tensor, kernel_size, stride=None, padding=0, count_include_pad: bool = True) -> Tensor:
+    """Mean over KH x KW windows (Pool.cpp:117-168), float32 out."""
+    KH, KW = _pair(kernel_size)
+    sh, sw = _pair(stride if stride is not None else kernel_size)
+    ph, pw = _pair(padding)
+    N, C, H, W = x.shape
+    if 2 * ph > KH or 2 * pw > KW:
+        raise ValueError("avg_pool2d: padding should be at most half of the kernel size")
+    OH, OW = (H + 2 * ph - KH) // sh + 1, (W + 2 * pw - KW) // sw + 1
+    if OH < 1 or OW < 1:
+        raise ValueError("avg_pool2d: kernel larger than the padded input")
+    ptr, xtype, xs, xz, _ = _pool_input(x, "avg_pool2d")
+    y = empty((N, C, OH, OW), float32, "gpu")
+    if y.numel():
+        _C.call("lq_pool2d", _C.POOL_AVG, ptr, xtype, xs, xz, N, C, H, W, OH, OW, KH, KW, sh, sw, ph, pw,
+                _C.POOL_COUNT_INCLUDE_PAD if count_include_pad else 0, y.data_ptr(), None)
+    return y
+
+
+def adaptive_avg_pool2d(x: Tensor, output_size) -> Tensor:
+    """Mean over the adaptive cells [floor(o S / O), ceil((o + 1) S / O)) of each spatial axis
+    (lucid/nn/functional/_pool_core.py:228-250, 407-434), float32 out."""
+    N, C, H, W = x.shape
+    if isinstance(output_size, (tuple, list)):
+        OH, OW = output_size if len(output_size) > 1 else (output_size[0], output_size[0])
+    else:
+        OH = OW = output_size
+    OH = H if OH is None else int(OH)
+    OW = W if OW is None else int(OW)
+    ptr, xtype, xs, xz, _ = _pool_input(x, "adaptive_avg_pool2d")
+    y = empty((N, C, OH, OW), float32, "gpu")
+    if y.numel():
+        _C.call("lq_pool2d", _C.POOL_AVG, ptr, xtype, xs, xz, N, C, H, W, OH, OW, 1, 1, 1, 1, 0, 0,
+                _C.POOL_ADAPTIVE, y.data_ptr(), None)
+    return y

@@ -164,6 +164,44 @@ class EmbeddingBag(_PaddedTable):
         return f"{self.num_embeddings}, {self.embedding_dim}, mode={self.mode}"
 
 
+class MaxPool2d(Module):
+    def __init__(self, kernel_size: Any, stride: Any = None, padding: Any = 0) -> None:
+        super().__init__()
+        self.kernel_size = kernel_size
+        self.stride = stride if stride is not None else kernel_size
+        self.padding = padding
+
+    def forward(self, x: Tensor) -> Tensor:
+        return F.max_pool2d(x, self.kernel_size, self.stride, self.padding)
+
+    def extra_repr(self) -> str:
+        return f"kernel_size={self.kernel_size}, stride={self.stride}, padding={self.padding}"
+
+
+class AvgPool2d(Module):
+    def __init__(self, kernel_size: Any, stride: Any = None, padding: Any = 0, count_include_pad: bool = True) -> None:
+        super().__init__()
+        self.kernel_size = kernel_size
+        self.stride = stride if stride is not None else kernel_size
+        self.padding = padding
+        self.count_include_pad = count_include_pad
+
+    def forward(self, x: Tensor) -> Tensor:
+        return F.avg_pool2d(x, self.kernel_size, self.stride, self.padding, self.count_include_pad)
+
+
+class AdaptiveAvgPool2d(Module):
+    def __init__(self, output_size: Any) -> None:
+        super().__init__()
+        self.output_size = output_size
+
+    def forward(self, x: Tensor) -> Tensor:
+        return F.adaptive_avg_pool2d(x, self.output_size)
+
+    def extra_repr(self) -> str:
+        return f"output_size={self.output_size}"
+
+
 class Sigmoid(Module):
     def forward(self, x: Tensor) -> Tensor:
         return F.sigmoid(x)

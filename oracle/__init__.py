@@ -41,6 +41,8 @@ function                      follows (lucid-official/lucid)
                               Unary.cpp:165-170 (numpy float32; exp / tanh within rounding)
 ``embedding_bag``             backend/cpu/methods/Sequence.cpp:8-93 (bags: IndexBounds.h:107-150;
                               per_sample_weights: nn/functional/sparse.py:228-310)
+``pool2d``                    backend/cpu/Pool.cpp:27-168; adaptive cells nn/functional/
+                              _pool_core.py:228-250 (numpy)
 ``lucid_*``                   the multi-pass CPU composition timed as the CPU baseline
 ============================  ==========================================================
 
@@ -593,3 +595,59 @@ def embedding_bag(table: np.ndarray, idx: np.ndarray, offsets=None, mode: int = 
             acc = (acc / f(count)).astype(np.float32)
         out[b] = acc
     return out
+
+
+# ----------------------------------------------------------------------------- pooling
+
+
+def pool2d(x: np.ndarray, op: str, kernel=(1, 1), stride=(1, 1), pad=(0, 0), adaptive=None,
+           count_include_pad: bool = True) -> np.ndarray:
+    """2-D max / average pooling of float32 NCHW ``x`` (backend/cpu/Pool.cpp:27-32, 57-100,
+    117-168; adaptive cells nn/functional/_pool_core.py:228-250): max takes the first
+    in-window element then any greater one or a NaN; avg sums the in-window elements in
+    row-major order in float32 and divides by the window size (padded or not)."""
+    x = np.asarray(x, np.float32)
+    N, C, H, W = x.shape
+
+    def windows(S, K, st, p, O):
+        out = []
+        for o in range(O):
+            if adaptive is not None:
+                lo, hi = (o * S) // O, -((-(o + 1) * S) // O)
+                out.append((lo, hi, hi - lo))
+            else:
+                start = o * st - p
+                end = min(start + K, S + p)
+                lo, hi = max(start, 0), min(end, S)
+                out.append((lo, hi, end - start if count_include_pad else max(hi - lo, 0)))
+        return out
+
+    if adaptive is not None:
+        OH, OW = adaptive
+    else:
+        OH = (H + 2 * pad[0] - kernel[0]) // stride[0] + 1
+        OW = (W + 2 * pad[1] - kernel[1]) // stride[1] + 1
+    wh = windows(H, kernel[0], stride[0], pad[0], OH)
+    ww = windows(W, kernel[1], stride[1], pad[1], OW)
+    y = np.zeros((N, C, OH, OW), np.float32)
+    for oh, (h0, h1, sh) in enumerate(wh):
+        for ow, (w0, w1, sw) in enumerate(ww):
+            if op == "max":
+                best = None
+                for h in range(h0, h1):
+                    for w in range(w0, w1):
+                        v = x[:, :, h, w]
+                        if best is None:
+                            best = v.copy()
+                        else:
+                            take = (v > best) | (np.isnan(v) & ~np.isnan(best))
+                            best = np.where(take, v, best)
+                y[:, :, oh, ow] = best
+            else:
+                acc = np.zeros((N, C), np.float32)
+                for h in range(h0, h1):
+                    for w in range(w0, w1):
+                        acc = (acc + x[:, :, h, w]).astype(np.float32)
+                d = sh * sw
+                y[:, :, oh, ow] = (acc / np.float32(d)).astype(np.float32) if d > 0 else 0.0
+    return y

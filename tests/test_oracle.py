@@ -575,3 +575,32 @@ def test_div6_rewrite_is_exact_for_every_float():
     # residual correction (IEEE division where |t| < 2^-125 or not finite); exhaustive over
     # all 2^32 inputs against the IEEE quotient Lucid computes
     assert O.div6_mismatches() == 0
+
+
+# ----------------------------------------------------------------------------- pooling
+
+
+def test_pool2d_closed_forms():
+    rng = np.random.default_rng(12)
+    x = rng.integers(-50, 50, (2, 3, 8, 12)).astype(np.float32)
+    # non-overlapping windows: numpy block reductions (integer values: exact sums)
+    blocks = x.reshape(2, 3, 4, 2, 4, 3)
+    np.testing.assert_array_equal(O.pool2d(x, "max", (2, 3), (2, 3)), blocks.max(axis=(3, 5)))
+    np.testing.assert_array_equal(O.pool2d(x, "avg", (2, 3), (2, 3)),
+                                  (blocks.astype(np.float64).sum(axis=(3, 5)) / 6).astype(np.float32))
+    # adaptive to 1 x 1 is the plane mean; to the input size it is the identity
+    np.testing.assert_array_equal(O.pool2d(x, "avg", adaptive=(1, 1))[..., 0, 0],
+                                  (x.astype(np.float64).sum(axis=(2, 3)) / 96).astype(np.float32))
+    np.testing.assert_array_equal(O.pool2d(x, "avg", adaptive=(8, 12)), x)
+    # padding: max skips it, avg counts it (or not)
+    ones = np.ones((1, 1, 3, 3), np.float32)
+    np.testing.assert_array_equal(O.pool2d(-ones, "max", (3, 3), (1, 1), (1, 1)), -ones)
+    corner = O.pool2d(ones, "avg", (3, 3), (1, 1), (1, 1))[0, 0, 0, 0]
+    assert corner == np.float32(4 / 9)
+    assert O.pool2d(ones, "avg", (3, 3), (1, 1), (1, 1), count_include_pad=False)[0, 0, 0, 0] == 1.0
+    # adaptive cells of 5 -> 3: [0, 2), [1, 4), [3, 5)
+    v = np.arange(5, dtype=np.float32).reshape(1, 1, 1, 5)
+    np.testing.assert_array_equal(O.pool2d(v, "max", adaptive=(1, 3))[0, 0, 0], [1, 3, 4])
+    # NaN propagates through max
+    x[0, 0, 0, 1] = np.nan
+    assert np.isnan(O.pool2d(x, "max", (2, 3), (2, 3))[0, 0, 0, 0])
