@@ -40,6 +40,6 @@ def __getattr__(name: str):
     # Sub-packages load lazily so `import lucid_amd` stays cheap and import cycles stay out.
     import importlib
 
-    if name in ("nn", "quantization", "backends"):
+    if name in ("nn", "quantization", "backends", "serialization"):
         return importlib.import_module(f"lucid_amd.{name}")
     raise AttributeError(f"module 'lucid_amd' has no attribute {name!r}")
