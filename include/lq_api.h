@@ -384,6 +384,21 @@ int lq_embedding_bag(const void* d_table, int table_type, const float* d_scale, 
                      int64_t bag_len, int mode, int64_t padding_idx, const float* d_per_sample_weights,
                      float* d_out, void* stream);
 
+/* ---- recurrent cells --------------------------------------------------------------- */
+enum { LQ_RNN_TANH = 0, LQ_RNN_RELU = 1, LQ_RNN_LSTM = 2, LQ_RNN_GRU = 3 };
+/* One time step of B rows of a recurrent cell from its two gate products gx[b, :] = x W_ih^T +
+ * b_ih (row stride ld_gx) and gh[b, :] = h W_hh^T + b_hh (row stride ld_gh), G x H wide (G = 1,
+ * 4 for LSTM gates i, f, g, o, 3 for GRU gates r, z, n):
+ *   RNN  h' = tanh / relu(gx + gh);  LSTM  c' = s(f) c + s(i) tanh(g), h' = s(o) tanh(c');
+ *   GRU  r = s(gx_r + gh_r), z = s(gx_z + gh_z), n = tanh(gx_n + r gh_n), h' = (1 - z) n + z h
+ * with s(x) = 1 / (1 + exp(-x)) (lucid/nn/modules/rnn.py _rnn_step / _gru_step, the LSTM of
+ * lstm_forward).  h / c / h_next / c_next are [B, H] contiguous (h_next may be h, c_next may be
+ * c); h' is also written to d_y[b * ld_y + j] when d_y is not NULL.  The step the float and
+ * the dynamic int8 LSTM / GRU / cells (lucid/nn/quantized/dynamic/rnn.py) share. */
+int lq_rnn_cell(int kind, const float* d_gx, int64_t ld_gx, const float* d_gh, int64_t ld_gh, const float* d_h,
+                const float* d_c, int64_t B, int64_t H, float* d_h_next, float* d_c_next, float* d_y, int64_t ld_y,
+                void* stream);
+
 /* ---- pooling ---------------------------------------------------------------------- */
 enum { LQ_POOL_MAX = 0, LQ_POOL_AVG = 1 };
 enum { LQ_POOL_ADAPTIVE = 1, LQ_POOL_COUNT_INCLUDE_PAD = 2 };

@@ -28,6 +28,7 @@ MERGE_ADD, MERGE_MUL, MERGE_ADD_SCALAR, MERGE_MUL_SCALAR, MERGE_COPY = 0, 1, 2, 
 ACT_SIGMOID, ACT_TANH, ACT_HARDSWISH, ACT_HARDSIGMOID, ACT_ELU, ACT_LEAKY_RELU = 0, 1, 2, 3, 4, 5
 BAG_SUM, BAG_MEAN, BAG_MAX = 0, 1, 2
 POOL_MAX, POOL_AVG = 0, 1
+RNN_TANH, RNN_RELU, RNN_LSTM, RNN_GRU = 0, 1, 2, 3
 POOL_ADAPTIVE, POOL_COUNT_INCLUDE_PAD = 1, 2
 
 
@@ -77,6 +78,7 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_embedding_bag": (_I, [_P, _I, _P, _P, _I64, _I64, _P, _I, _I64, _P, _I, _I64, _I, _I64, _I, _I64, _P, _P,
                               _P]),
     "lq_pool2d": (_I, [_I, _P, _I, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _P, _P]),
+    "lq_rnn_cell": (_I, [_I, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _P, _P, _P, _I64, _P]),
     "lq_qact": (_I, [_I, _P, _I, _P, _P, _I64, _F, _P, _P, _I, _I, _I, _P, _P]),
     "lq_qmerge": (_I, [_I, _P, _I, _P, _P, _P, _I, _P, _P, _F, _I64, _I64, _I64, _P, _P, _I, _I, _I, _I,
                        _P, _P]),

@@ -22,9 +22,12 @@ from lucid_amd.nn.layers import (
     Tanh,
 )
 
+from lucid_amd.nn.rnn import GRU, LSTM, GRUCell, LSTMCell, RNNCell
+
 __all__ = ["Module", "Parameter", "Linear", "Conv2d", "ReLU", "Sequential", "Identity",
            "BatchNorm2d", "Flatten", "Sigmoid", "Tanh", "Hardswish", "Hardsigmoid", "ELU", "LeakyReLU",
-           "Embedding", "EmbeddingBag", "MaxPool2d", "AvgPool2d", "AdaptiveAvgPool2d"]
+           "Embedding", "EmbeddingBag", "MaxPool2d", "AvgPool2d", "AdaptiveAvgPool2d",
+           "LSTM", "GRU", "LSTMCell", "GRUCell", "RNNCell"]
 
 
 def __getattr__(name: str):

@@ -1,0 +1,263 @@
+"""Recurrent layers -- ``RNNCell`` / ``LSTMCell`` / ``GRUCell`` and the multi-layer,
+optionally bidirectional ``LSTM`` / ``GRU`` (lucid/nn/modules/rnn.py), on the GPU.
+
+Each layer and direction computes its input gates for every time step at once
+(``x W_ih^T + b_ih``, one matrix product over T x B rows), then walks the time steps: one
+product ``h W_hh^T + b_hh`` and one ``lq_rnn_cell`` launch per step, the new hidden state
+written straight into the layer's output sequence.  ``batch_first`` is handled by strides
+(no transposes).  Parameter names and shapes are Lucid's (``weight_ih_l{k}[_reverse]``
+``[G * hidden, in]``, ``weight_hh_l{k}``, ``bias_ih_l{k}``, ``bias_hh_l{k}``; a cell's
+``weight_ih`` ...), so ``quantize_dynamic`` finds them.  The matrix products are the float
+``lq_linear_f32`` here and the weight-only int8 GEMV in ``nn.quantized.dynamic``.
+
+Not covered: ``PackedSequence`` inputs, ``proj_size`` and inter-layer dropout (these are
+inference modules: dropout is the identity in eval).
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any
+
+import numpy as np
+
+from lucid_amd import _C
+from lucid_amd._tensor import Tensor, empty, float32, tensor
+from lucid_amd.nn.module import Module, Parameter
+from lucid_amd.quantization._device import require_gpu
+
+_GATES = {"RNN_TANH": 1, "RNN_RELU": 1, "LSTM": 4, "GRU": 3}
+_KIND = {"RNN_TANH": _C.RNN_TANH, "RNN_RELU": _C.RNN_RELU, "LSTM": _C.RNN_LSTM, "GRU": _C.RNN_GRU}
+
+
+def _init_uniform(shape, hidden: int) -> Tensor:
+    from lucid_amd.nn import layers
+
+    k = 1.0 / math.sqrt(hidden) if hidden > 0 else 0.0
+    return tensor(layers._init_rng.uniform(-k, k, size=shape).astype(np.float32))
+
+
+class _Recurrent(Module):
+    """Shared recurrence; subclasses provide ``_gates(name, x_ptr, ldx, M, K, y_ptr)``, the
+    product ``x W_{name}^T + b_{name}`` for ``name`` = ``ih{suffix}`` / ``hh{suffix}``."""
+
+    mode: str = "LSTM"
+
+    def _gates(self, name: str, x_ptr: int, ldx: int, M: int, K: int, y_ptr: int) -> None:
+        raise NotImplementedError
+
+    # -- one recurrent layer over a whole sequence -------------------------------------
+    def _layer(self, x: Tensor, T: int, B: int, batch_first: bool, sfx: str, d: int, D: int,
+               h: Tensor, c: Tensor | None, out: Tensor) -> None:
+        H, G = self.hidden_size, _GATES[self.mode]
+        K = int(x.shape[-1])
+        gx = empty((T * B, G * H), float32, "gpu")
+        self._gates("ih" + sfx, x.data_ptr(), K, T * B, K, gx.data_ptr())
+        gh = empty((B, G * H), float32, "gpu")
+        steps = range(T - 1, -1, -1) if d else range(T)
+        for t in steps:
+            self._gates("hh" + sfx, h.data_ptr(), H, B, H, gh.data_ptr())
+            if batch_first:   # rows (b, t) of [B, T, .]
+                gx_ptr, ld_gx = gx.data_ptr() + 4 * t * G * H, T * G * H
+                y_ptr, ld_y = out.data_ptr() + 4 * (t * D * H + d * H), T * D * H
+            else:             # rows (t, b) of [T, B, .]
+                gx_ptr, ld_gx = gx.data_ptr() + 4 * t * B * G * H, G * H
+                y_ptr, ld_y = out.data_ptr() + 4 * (t * B * D * H + d * H), D * H
+            _C.call("lq_rnn_cell", _KIND[self.mode], gx_ptr, ld_gx, gh.data_ptr(), G * H, h.data_ptr(),
+                    c.data_ptr() if c is not None else None, B, H, h.data_ptr(),
+                    c.data_ptr() if c is not None else None, y_ptr, ld_y, None)
+
+    def _state(self, hx: Tensor | None, idx: int, B: int) -> Tensor:
+        """A private contiguous [B, H] copy of layer-direction ``idx`` of ``hx`` (zeros if None)."""
+        H = self.hidden_size
+        s = empty((B, H), float32, "gpu")
+        if hx is None:
+            _C.call("lq_fill_u32", s.data_ptr(), 0, B * H, None)
+        else:
+            _C.call("lq_memcpy_d2d", s.data_ptr(), hx.data_ptr() + 4 * idx * B * H, 4 * B * H, None)
+        return s
+
+
+class _RNNBase(_Recurrent):
+    def __init__(self, mode: str, input_size: int, hidden_size: int, num_layers: int = 1, bias: bool = True,
+                 batch_first: bool = False, dropout: float = 0.0, bidirectional: bool = False,
+                 proj_size: int = 0) -> None:
+        super().__init__()
+        if proj_size:
+            raise NotImplementedError(f"{type(self).__name__}: proj_size is not supported on the HIP backend")
+        self.mode = mode
+        self.input_size, self.hidden_size, self.num_layers = input_size, hidden_size, num_layers
+        self.bias, self.batch_first, self.dropout, self.bidirectional = bias, batch_first, dropout, bidirectional
+        self.proj_size = 0
+        G, D = _GATES[mode], 2 if bidirectional else 1
+        for layer in range(num_layers):
+            for d in range(D):
+                sfx = f"_l{layer}" + ("_reverse" if d else "")
+                in_size = input_size if layer == 0 else D * hidden_size
+                setattr(self, f"weight_ih{sfx}", Parameter(_init_uniform((G * hidden_size, in_size), hidden_size)))
+                setattr(self, f"weight_hh{sfx}", Parameter(_init_uniform((G * hidden_size, hidden_size), hidden_size)))
+                if bias:
+                    setattr(self, f"bias_ih{sfx}", Parameter(_init_uniform((G * hidden_size,), hidden_size)))
+                    setattr(self, f"bias_hh{sfx}", Parameter(_init_uniform((G * hidden_size,), hidden_size)))
+
+    def _run(self, input: Tensor, hx: Tensor | None, cx: Tensor | None):
+        require_gpu(input, type(self).__name__)
+        if input.dtype != float32:
+            raise TypeError(f"{type(self).__name__}: float32 input expected, got {input.dtype}")
+        if input.ndim not in (2, 3):
+            raise ValueError(f"{type(self).__name__}: expected a 2-D or 3-D input, got {input.ndim}-D")
+        unbatched = input.ndim == 2   # (T, input_size) whatever batch_first says
+        x = input.reshape(int(input.shape[0]), 1, int(input.shape[1])) if unbatched else input
+        bf = self.batch_first and not unbatched
+        T, B = (int(x.shape[1]), int(x.shape[0])) if bf else (int(x.shape[0]), int(x.shape[1]))
+        D, H, L = (2 if self.bidirectional else 1), self.hidden_size, self.num_layers
+        if int(x.shape[-1]) != self.input_size:
+            raise ValueError(f"{type(self).__name__}: input size {int(x.shape[-1])} != {self.input_size}")
+        for name, st in (("hx", hx), ("cx", cx)):
+            if st is not None and int(np.prod(st.shape)) != L * D * B * H:
+                raise ValueError(f"{type(self).__name__}: {name} must hold {L * D} x {B} x {H} values, got "
+                                 f"shape {tuple(st.shape)}")
+        h_n = empty((L * D, B, H), float32, "gpu")
+        c_n = empty((L * D, B, H), float32, "gpu") if self.mode == "LSTM" else None
+        layer_in = x
+        for layer in range(L):
+            out = empty(((B, T, D * H) if bf else (T, B, D * H)), float32, "gpu")
+            for d in range(D):
+                idx = layer * D + d
+                h = self._state(hx, idx, B)
+                c = self._state(cx, idx, B) if self.mode == "LSTM" else None
+                self._layer(layer_in, T, B, bf, f"_l{layer}" + ("_reverse" if d else ""), d, D, h, c, out)
+                _C.call("lq_memcpy_d2d", h_n.data_ptr() + 4 * idx * B * H, h.data_ptr(), 4 * B * H, None)
+                if c is not None:
+                    _C.call("lq_memcpy_d2d", c_n.data_ptr() + 4 * idx * B * H, c.data_ptr(), 4 * B * H, None)
+            layer_in = out
+        out = layer_in
+        if unbatched:
+            out = out.reshape(T, D * H)
+            h_n = h_n.reshape(L * D, H)
+            c_n = c_n.reshape(L * D, H) if c_n is not None else None
+        return out, h_n, c_n
+
+    def extra_repr(self) -> str:
+        s = f"{self.input_size}, {self.hidden_size}"
+        if self.num_layers != 1:
+            s += f", num_layers={self.num_layers}"
+        if self.batch_first:
+            s += ", batch_first=True"
+        if self.bidirectional:
+            s += ", bidirectional=True"
+        return s
+
+
+class _FloatGates:
+    """``x W^T + b`` with the float32 weights (``lq_linear_f32``)."""
+
+    def _gates(self, name: str, x_ptr: int, ldx: int, M: int, K: int, y_ptr: int) -> None:
+        from lucid_amd.quantization._device import on_device
+
+        w = on_device(getattr(self, "weight_" + name))
+        b = getattr(self, "bias_" + name, None)
+        b = on_device(b) if b is not None else None
+        N = int(w.shape[0])
+        self._alive = (w, b)
+        _C.call("lq_linear_f32", x_ptr, ldx, w.data_ptr(), K, b.data_ptr() if b is not None else None, y_ptr, N,
+                M, N, K, None)
+
+
+class LSTM(_FloatGates, _RNNBase):
+    """Multi-layer LSTM (gates i, f, g, o)."""
+
+    def __init__(self, input_size: int, hidden_size: int, num_layers: int = 1, bias: bool = True,
+                 batch_first: bool = False, dropout: float = 0.0, bidirectional: bool = False,
+                 proj_size: int = 0) -> None:
+        super().__init__("LSTM", input_size, hidden_size, num_layers, bias, batch_first, dropout, bidirectional,
+                         proj_size)
+
+    def forward(self, input: Tensor, hx: tuple[Tensor, Tensor] | None = None):
+        h0, c0 = (None, None) if hx is None else hx
+        out, h_n, c_n = self._run(input, h0, c0)
+        return out, (h_n, c_n)
+
+
+class GRU(_FloatGates, _RNNBase):
+    """Multi-layer GRU (gates r, z, n)."""
+
+    def __init__(self, input_size: int, hidden_size: int, num_layers: int = 1, bias: bool = True,
+                 batch_first: bool = False, dropout: float = 0.0, bidirectional: bool = False) -> None:
+        super().__init__("GRU", input_size, hidden_size, num_layers, bias, batch_first, dropout, bidirectional)
+
+    def forward(self, input: Tensor, hx: Tensor | None = None):
+        out, h_n, _ = self._run(input, hx, None)
+        return out, h_n
+
+
+class _CellBase(_Recurrent):
+    def __init__(self, mode: str, input_size: int, hidden_size: int, bias: bool = True) -> None:
+        super().__init__()
+        self.mode = mode
+        self.input_size, self.hidden_size, self.bias = input_size, hidden_size, bias
+        G = _GATES[mode]
+        self.weight_ih = Parameter(_init_uniform((G * hidden_size, input_size), hidden_size))
+        self.weight_hh = Parameter(_init_uniform((G * hidden_size, hidden_size), hidden_size))
+        if bias:
+            self.bias_ih = Parameter(_init_uniform((G * hidden_size,), hidden_size))
+            self.bias_hh = Parameter(_init_uniform((G * hidden_size,), hidden_size))
+        else:
+            self.register_parameter("bias_ih", None)
+            self.register_parameter("bias_hh", None)
+
+    def _step(self, input: Tensor, hx: Tensor | None, cx: Tensor | None):
+        require_gpu(input, type(self).__name__)
+        if input.dtype != float32:
+            raise TypeError(f"{type(self).__name__}: float32 input expected, got {input.dtype}")
+        unbatched = input.ndim == 1
+        x = input.reshape(1, input.shape[0]) if unbatched else input
+        B, H, G = int(x.shape[0]), self.hidden_size, _GATES[self.mode]
+        if int(x.shape[1]) != self.input_size:
+            raise ValueError(f"{type(self).__name__}: input size {int(x.shape[1])} != {self.input_size}")
+        h = self._state(hx, 0, B)
+        c = self._state(cx, 0, B) if self.mode == "LSTM" else None
+        gx = empty((B, G * H), float32, "gpu")
+        gh = empty((B, G * H), float32, "gpu")
+        self._gates("ih", x.data_ptr(), self.input_size, B, self.input_size, gx.data_ptr())
+        self._gates("hh", h.data_ptr(), H, B, H, gh.data_ptr())
+        _C.call("lq_rnn_cell", _KIND[self.mode], gx.data_ptr(), G * H, gh.data_ptr(), G * H, h.data_ptr(),
+                c.data_ptr() if c is not None else None, B, H, h.data_ptr(),
+                c.data_ptr() if c is not None else None, None, 0, None)
+        if unbatched:
+            h = h.reshape(H)
+            c = c.reshape(H) if c is not None else None
+        return h, c
+
+    def extra_repr(self) -> str:
+        return f"{self.input_size}, {self.hidden_size}"
+
+
+class RNNCell(_FloatGates, _CellBase):
+    """Elman cell, ``tanh`` or ``relu`` nonlinearity."""
+
+    def __init__(self, input_size: int, hidden_size: int, bias: bool = True, nonlinearity: str = "tanh") -> None:
+        if nonlinearity not in ("tanh", "relu"):
+            raise ValueError(f"Unknown nonlinearity {nonlinearity!r}. Select from 'tanh' or 'relu'.")
+        super().__init__("RNN_TANH" if nonlinearity == "tanh" else "RNN_RELU", input_size, hidden_size, bias)
+        self.nonlinearity = nonlinearity
+
+    def forward(self, input: Tensor, hx: Tensor | None = None) -> Tensor:
+        return self._step(input, hx, None)[0]
+
+
+class LSTMCell(_FloatGates, _CellBase):
+    def __init__(self, input_size: int, hidden_size: int, bias: bool = True) -> None:
+        super().__init__("LSTM", input_size, hidden_size, bias)
+
+    def forward(self, input: Tensor, hx: tuple[Tensor, Tensor] | None = None):
+        h0, c0 = (None, None) if hx is None else hx
+        return self._step(input, h0, c0)
+
+
+class GRUCell(_FloatGates, _CellBase):
+    def __init__(self, input_size: int, hidden_size: int, bias: bool = True) -> None:
+        super().__init__("GRU", input_size, hidden_size, bias)
+
+    def forward(self, input: Tensor, hx: Tensor | None = None) -> Tensor:
+        return self._step(input, hx, None)[0]

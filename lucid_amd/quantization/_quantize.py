@@ -187,7 +187,9 @@ def _dynamic_builders() -> dict:
     import lucid_amd.nn as nn
     import lucid_amd.nn.quantized.dynamic as nnqd
 
-    builders = {nn.Linear: nnqd.Linear.from_float}
+    builders = {nn.Linear: nnqd.Linear.from_float, nn.LSTM: nnqd.LSTM.from_float, nn.GRU: nnqd.GRU.from_float,
+                nn.LSTMCell: nnqd.LSTMCell.from_float, nn.GRUCell: nnqd.GRUCell.from_float,
+                nn.RNNCell: nnqd.RNNCell.from_float}
     if backends.quantized.use_mlx():
         builders[nn.Linear] = _mlx_dynamic_builder()
     return builders
@@ -244,7 +246,7 @@ class _DynamicSwapper:
 
 def quantize_dynamic(model: Module, qconfig_spec=None, dtype: QDtype = qint8,
                      inplace: bool = False) -> Module:
-    """Replace ``Linear`` layers with dynamically quantized int8 layers."""
+    """Replace ``Linear`` and recurrent layers with dynamically quantized int8 layers."""
     model = model if inplace else copy.deepcopy(model)
     model.eval()
     builders = _dynamic_builders()

@@ -43,6 +43,8 @@ function                      follows (lucid-official/lucid)
                               per_sample_weights: nn/functional/sparse.py:228-310)
 ``pool2d``                    backend/cpu/Pool.cpp:27-168; adaptive cells nn/functional/
                               _pool_core.py:228-250 (numpy)
+``rnn_cell`` / ``rnn_forward``  nn/modules/rnn.py (_rnn_step, _gru_step, LSTM gates i, f, g, o),
+                              float64 numpy
 ``lucid_*``                   the multi-pass CPU composition timed as the CPU baseline
 ============================  ==========================================================
 
@@ -651,3 +653,59 @@ def pool2d(x: np.ndarray, op: str, kernel=(1, 1), stride=(1, 1), pad=(0, 0), ada
                 d = sh * sw
                 y[:, :, oh, ow] = (acc / np.float32(d)).astype(np.float32) if d > 0 else 0.0
     return y
+
+
+# -------------------------------------------------------------------- recurrent layers
+
+
+def _sig64(x):
+    return 1.0 / (1.0 + np.exp(-x))
+
+
+def rnn_cell(mode: str, gx: np.ndarray, gh: np.ndarray, h: np.ndarray, c=None):
+    """One step from the two gate products (float64): ``mode`` RNN_TANH / RNN_RELU / LSTM
+    (gates i, f, g, o) / GRU (gates r, z, n) as lucid/nn/modules/rnn.py writes them."""
+    H = h.shape[-1]
+    if mode in ("RNN_TANH", "RNN_RELU"):
+        pre = gx + gh
+        return (np.tanh(pre) if mode == "RNN_TANH" else np.maximum(pre, 0.0)), None
+    if mode == "LSTM":
+        g = gx + gh
+        i, f, gg, o = _sig64(g[:, :H]), _sig64(g[:, H:2 * H]), np.tanh(g[:, 2 * H:3 * H]), _sig64(g[:, 3 * H:])
+        cn = f * c + i * gg
+        return o * np.tanh(cn), cn
+    r = _sig64(gx[:, :H] + gh[:, :H])
+    z = _sig64(gx[:, H:2 * H] + gh[:, H:2 * H])
+    n = np.tanh(gx[:, 2 * H:] + r * gh[:, 2 * H:])
+    return (1.0 - z) * n + z * h, None
+
+
+def rnn_forward(mode: str, x: np.ndarray, weights: dict, num_layers: int = 1, bidirectional: bool = False,
+                h0=None, c0=None):
+    """A multi-layer (bi)directional recurrence over time-major ``x`` [T, B, I] in float64
+    with ``weights[name]`` (``weight_ih_l{k}[_reverse]`` ..., biases optional): (output
+    [T, B, D H], h_n [L D, B, H], c_n or None)."""
+    x = np.asarray(x, np.float64)
+    T, B, _ = x.shape
+    D = 2 if bidirectional else 1
+    H = weights["weight_hh_l0"].shape[1]
+    h_n, c_n = [], []
+    inp = x
+    for layer in range(num_layers):
+        outs = np.zeros((T, B, D * H))
+        for d in range(D):
+            sfx = f"_l{layer}" + ("_reverse" if d else "")
+            w_ih, w_hh = (np.asarray(weights[f"weight_{k}{sfx}"], np.float64) for k in ("ih", "hh"))
+            b_ih = np.asarray(weights.get(f"bias_ih{sfx}", np.zeros(w_ih.shape[0])), np.float64)
+            b_hh = np.asarray(weights.get(f"bias_hh{sfx}", np.zeros(w_hh.shape[0])), np.float64)
+            idx = layer * D + d
+            h = np.zeros((B, H)) if h0 is None else np.asarray(h0[idx], np.float64)
+            c = np.zeros((B, H)) if c0 is None else np.asarray(c0[idx], np.float64)
+            for t in (range(T - 1, -1, -1) if d else range(T)):
+                h, cn = rnn_cell(mode, inp[t] @ w_ih.T + b_ih, h @ w_hh.T + b_hh, h, c)
+                c = cn if cn is not None else c
+                outs[t, :, d * H:(d + 1) * H] = h
+            h_n.append(h)
+            c_n.append(c)
+        inp = outs
+    return inp, np.stack(h_n), (np.stack(c_n) if mode == "LSTM" else None)

@@ -1,0 +1,203 @@
+"""GPU parity of the recurrent layers (lq_rnn_cell inside nn.LSTM / GRU / LSTMCell / GRUCell /
+RNNCell and their dynamic int8 forms in nn.quantized.dynamic) against the oracle's float64
+recurrence.
+
+* float modules: the oracle over the same float32 weights; float32 products and gate math
+  against float64, absolute tolerance 2e-5 (states are bounded by tanh / sigmoid);
+* dynamic modules: the oracle over the dequantized weights (Lucid's forward: dequantize, then
+  the float module, lucid/nn/quantized/dynamic/rnn.py:35-56), same tolerance, the weight codes
+  and scales bit-exact against the oracle's per-channel symmetric quantization;
+* the reference's own tests (lucid/test/unit/quantization/test_dynamic_recurrent.py:44-150):
+  every type converts, holds int8 codes and no float weight, stays within 3% of the float
+  module, and leaves the float module alone.
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+ATOL = 2e-5
+
+
+def _dev(gpu, a):
+    return gpu.tensor(np.ascontiguousarray(a, dtype=np.float32), device="gpu")
+
+
+def _float_weights(mod):
+    return {n: p.numpy().astype(np.float64) for n, p in mod.named_parameters()}
+
+
+def _deq_weights(q):
+    out = {}
+    for n, b in q.named_buffers():
+        if n.endswith("_int8"):
+            out[n[:-5]] = b.numpy().astype(np.float64) * q._buffers[n[:-5] + "_scale"].numpy().astype(np.float64)[:, None]
+        elif not n.endswith("_scale"):
+            out[n] = b.numpy().astype(np.float64)
+    return out
+
+
+MODES = [("LSTM", 1, False, False), ("LSTM", 2, True, False), ("GRU", 1, False, True), ("GRU", 2, True, True)]
+
+
+@pytest.mark.parametrize("mode,layers,bidir,batch_first", MODES)
+def test_sequence_modules_match_oracle(gpu, mode, layers, bidir, batch_first):
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized.dynamic as nnqd
+    from lucid_amd.nn.layers import manual_seed
+
+    manual_seed(layers + 3 * bidir)
+    rng = np.random.default_rng(layers)
+    T, B, I, H = 7, 3, 10, 16
+    m = getattr(nn, mode)(I, H, num_layers=layers, bidirectional=bidir, batch_first=batch_first).to("gpu")
+    x = rng.standard_normal((T, B, I)).astype(np.float32)
+    D = 2 if bidir else 1
+    h0 = (rng.standard_normal((layers * D, B, H)) * 0.5).astype(np.float32)
+    c0 = (rng.standard_normal((layers * D, B, H)) * 0.5).astype(np.float32)
+    xin = x.transpose(1, 0, 2) if batch_first else x
+    hx = (_dev(gpu, h0), _dev(gpu, c0)) if mode == "LSTM" else _dev(gpu, h0)
+    for mod, weights in ((m, _float_weights(m)), (None, None)):
+        if mod is None:
+            mod = nnqd.__dict__[mode].from_float(m)
+            weights = _deq_weights(mod)
+        out, state = mod(_dev(gpu, xin), hx)
+        want, h_n, c_n = O.rnn_forward(mode, x, weights, layers, bidir, h0, c0 if mode == "LSTM" else None)
+        got = out.numpy().transpose(1, 0, 2) if batch_first else out.numpy()
+        np.testing.assert_allclose(got, want, atol=ATOL, rtol=0)
+        if mode == "LSTM":
+            np.testing.assert_allclose(state[0].numpy(), h_n, atol=ATOL, rtol=0)
+            np.testing.assert_allclose(state[1].numpy(), c_n, atol=ATOL, rtol=0)
+        else:
+            np.testing.assert_allclose(state.numpy(), h_n, atol=ATOL, rtol=0)
+
+
+@pytest.mark.parametrize("cell,mode", [("LSTMCell", "LSTM"), ("GRUCell", "GRU"), ("RNNCell", "RNN_TANH"),
+                                       ("RNNCell-relu", "RNN_RELU")])
+def test_cells_match_oracle(gpu, cell, mode):
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized.dynamic as nnqd
+
+    rng = np.random.default_rng(len(cell))
+    B, I, H = 5, 12, 9
+    name = cell.split("-")[0]
+    m = (nn.RNNCell(I, H, nonlinearity="relu") if cell.endswith("relu") else getattr(nn, name)(I, H)).to("gpu")
+    x = rng.standard_normal((B, I)).astype(np.float32)
+    h = (rng.standard_normal((B, H)) * 0.5).astype(np.float32)
+    c = (rng.standard_normal((B, H)) * 0.5).astype(np.float32)
+    for mod in (m, nnqd.__dict__[name].from_float(m)):
+        w = _float_weights(mod) if mod is m else _deq_weights(mod)
+        hx = (_dev(gpu, h), _dev(gpu, c)) if mode == "LSTM" else _dev(gpu, h)
+        res = mod(_dev(gpu, x), hx)
+        gx = x.astype(np.float64) @ w["weight_ih"].T + w["bias_ih"]
+        gh = h.astype(np.float64) @ w["weight_hh"].T + w["bias_hh"]
+        want_h, want_c = O.rnn_cell(mode, gx, gh, h.astype(np.float64), c.astype(np.float64))
+        got_h = res[0] if mode == "LSTM" else res
+        np.testing.assert_allclose(got_h.numpy(), want_h, atol=ATOL, rtol=0)
+        if mode == "LSTM":
+            np.testing.assert_allclose(res[1].numpy(), want_c, atol=ATOL, rtol=0)
+
+
+def test_dynamic_weights_are_the_oracle_codes(gpu):
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized.dynamic as nnqd
+
+    m = nn.GRU(6, 8, num_layers=2, bidirectional=True).to("gpu")
+    q = nnqd.GRU.from_float(m)
+    for name, p in m.named_parameters():
+        if not name.startswith("weight"):
+            np.testing.assert_array_equal(q._buffers[name].numpy(), p.numpy())
+            continue
+        W = p.numpy()
+        mn, mx = O.minmax_per_channel(W, 0)
+        s, z = O.calc_qparams(mn, mx, True, True, -128, 127)
+        np.testing.assert_array_equal(q._buffers[name + "_scale"].numpy(), s)
+        np.testing.assert_array_equal(q._buffers[name + "_int8"].numpy(),
+                                      O.quantize(W, O.recip_tensor(s), z, -128, 127, O.I8, ch_axis=0))
+
+
+_CASES = {
+    "Linear": (lambda nn: nn.Linear(4, 6), (3, 4)),
+    "LSTM": (lambda nn: nn.LSTM(4, 6, num_layers=2), (5, 2, 4)),
+    "GRU": (lambda nn: nn.GRU(4, 6), (5, 2, 4)),
+    "GRU-2layer-bidir": (lambda nn: nn.GRU(4, 6, num_layers=2, bidirectional=True), (5, 2, 4)),
+    "LSTMCell": (lambda nn: nn.LSTMCell(4, 6), (3, 4)),
+    "GRUCell": (lambda nn: nn.GRUCell(4, 6), (3, 4)),
+    "RNNCell-tanh": (lambda nn: nn.RNNCell(4, 6), (3, 4)),
+    "RNNCell-relu": (lambda nn: nn.RNNCell(4, 6, nonlinearity="relu"), (3, 4)),
+}
+
+
+@pytest.fixture()
+def reference_engine():
+    import lucid_amd.backends as backends
+
+    backends.quantized.engine = "reference"
+    yield
+    backends.quantized.engine = "auto"
+
+
+@pytest.mark.parametrize("case", list(_CASES))
+def test_each_type_is_quantized_and_stays_close(gpu, reference_engine, case):
+    # lucid/test/unit/quantization/test_dynamic_recurrent.py:78-100
+    import warnings
+
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized.dynamic as nnqd
+    from lucid_amd.nn.layers import manual_seed
+    from lucid_amd.quantization import quantize_dynamic
+
+    make, shape = _CASES[case]
+    manual_seed(0)
+    model = nn.Sequential(make(nn)).to("gpu")
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")
+        qmodel = quantize_dynamic(model)
+    qtype = getattr(nnqd, case.split("-")[0])
+    assert type(qmodel[0]) is qtype
+    state = qmodel.state_dict()
+    codes = [k for k in state if k.endswith("_int8")]
+    assert codes and all(state[k].dtype == np.int8 for k in codes)
+    assert not [k for k in state if ".weight" in k and not k.endswith(("_int8", "_scale", "_zero_point"))]
+    assert type(model[0]) is not qtype   # the float module is left alone
+    x = _dev(gpu, np.random.default_rng(0).standard_normal(shape))
+
+    def first(o):
+        return o[0] if isinstance(o, tuple) else o
+
+    want = first(model(x)).numpy().astype(np.float64)
+    got = first(qmodel(x)).numpy().astype(np.float64)
+    assert np.abs(got - want).mean() / (np.abs(want).mean() + 1e-9) < 0.03
+
+
+def test_default_spec_quantizes_every_recurrent_type(gpu):
+    # test_dynamic_recurrent.py:116-121
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized.dynamic as nnqd
+    from lucid_amd.quantization import quantize_dynamic
+
+    model = nn.Sequential(nn.GRU(4, 4), nn.LSTMCell(4, 4), nn.GRUCell(4, 4), nn.RNNCell(4, 4)).to("gpu")
+    q = quantize_dynamic(model)
+    assert [type(m) for m in q] == [nnqd.GRU, nnqd.LSTMCell, nnqd.GRUCell, nnqd.RNNCell]
+
+
+def test_spec_filters_recurrent_types(gpu):
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized.dynamic as nnqd
+    from lucid_amd.quantization import quantize_dynamic
+
+    model = nn.Sequential(nn.GRU(4, 4), nn.GRUCell(4, 4)).to("gpu")
+    q = quantize_dynamic(model, qconfig_spec={nn.GRUCell})
+    assert type(q[0]) is nn.GRU and type(q[1]) is nnqd.GRUCell
+
+
+def test_from_float_rejects_another_type(gpu):
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized.dynamic as nnqd
+
+    with pytest.raises(TypeError):
+        nnqd.LSTM.from_float(nn.GRU(4, 4))

@@ -604,3 +604,64 @@ def test_pool2d_closed_forms():
     # NaN propagates through max
     x[0, 0, 0, 1] = np.nan
     assert np.isnan(O.pool2d(x, "max", (2, 3), (2, 3))[0, 0, 0, 0])
+
+
+# -------------------------------------------------------------------- recurrent layers
+
+
+def _rnn_weights(rng, mode, I, H, L=1, D=1):
+    G = {"LSTM": 4, "GRU": 3}.get(mode, 1)
+    w = {}
+    for layer in range(L):
+        for d in range(D):
+            sfx = f"_l{layer}" + ("_reverse" if d else "")
+            fan = I if layer == 0 else D * H
+            w[f"weight_ih{sfx}"] = rng.uniform(-0.5, 0.5, (G * H, fan))
+            w[f"weight_hh{sfx}"] = rng.uniform(-0.5, 0.5, (G * H, H))
+            w[f"bias_ih{sfx}"] = rng.uniform(-0.5, 0.5, G * H)
+            w[f"bias_hh{sfx}"] = rng.uniform(-0.5, 0.5, G * H)
+    return w
+
+
+def test_rnn_cell_closed_forms():
+    B, H = 3, 5
+    h = np.linspace(-1, 1, B * H).reshape(B, H)
+    c = np.linspace(2, -2, B * H).reshape(B, H)
+    # zero gate products: LSTM gates i = f = o = 1/2, g = 0; GRU r = z = 1/2, n = 0
+    hl, cl = O.rnn_cell("LSTM", np.zeros((B, 4 * H)), np.zeros((B, 4 * H)), h, c)
+    np.testing.assert_allclose(cl, 0.5 * c)
+    np.testing.assert_allclose(hl, 0.5 * np.tanh(0.5 * c))
+    hg, _ = O.rnn_cell("GRU", np.zeros((B, 3 * H)), np.zeros((B, 3 * H)), h)
+    np.testing.assert_allclose(hg, 0.5 * h)
+    # saturated LSTM gates: i = f = o = 1, g = tanh(big) = 1 -> c' = c + 1, h' = tanh(c + 1)
+    big = np.full((B, 4 * H), 40.0)
+    hl, cl = O.rnn_cell("LSTM", big, np.zeros((B, 4 * H)), h, c)
+    np.testing.assert_allclose(cl, c + 1.0)
+    np.testing.assert_allclose(hl, np.tanh(c + 1.0))
+    # GRU with z -> 1 keeps h; relu RNN clips
+    gx = np.zeros((B, 3 * H))
+    gx[:, H:2 * H] = 40.0
+    np.testing.assert_allclose(O.rnn_cell("GRU", gx, np.zeros((B, 3 * H)), h)[0], h)
+    np.testing.assert_array_equal(O.rnn_cell("RNN_RELU", -np.ones((B, H)), np.zeros((B, H)), h)[0], 0.0)
+
+
+def test_rnn_forward_structure():
+    rng = np.random.default_rng(8)
+    T, B, I, H = 6, 3, 4, 5
+    x = rng.standard_normal((T, B, I))
+    for mode in ("LSTM", "GRU", "RNN_TANH"):
+        w = _rnn_weights(rng, mode, I, H, L=2, D=2)
+        out, h_n, c_n = O.rnn_forward(mode, x, w, num_layers=2, bidirectional=True)
+        assert out.shape == (T, B, 2 * H) and h_n.shape == (4, B, H)
+        # the reverse direction of layer 0 is a forward pass over the time-reversed input
+        w_rev = {k.replace("_reverse", ""): v for k, v in w.items() if k.endswith("_l0_reverse")}
+        o1, _, _ = O.rnn_forward(mode, x[::-1], w_rev)
+        l0, _, _ = O.rnn_forward(mode, x, {k: v for k, v in w.items() if "_l0" in k}, bidirectional=True)
+        np.testing.assert_allclose(l0[:, :, H:], o1[::-1])
+        # the last forward step's output is h_n of that direction; the reverse ends at t = 0
+        np.testing.assert_allclose(out[-1, :, :H], h_n[2])
+        np.testing.assert_allclose(out[0, :, H:], h_n[3])
+        # layer 2 consumes layer 1's output
+        w2 = {k.replace("_l1", "_l0"): v for k, v in w.items() if "_l1" in k}
+        o2, _, _ = O.rnn_forward(mode, l0, w2, bidirectional=True)
+        np.testing.assert_allclose(o2, out)
