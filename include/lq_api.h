@@ -399,6 +399,17 @@ int lq_rnn_cell(int kind, const float* d_gx, int64_t ld_gx, const float* d_gh, i
                 const float* d_c, int64_t B, int64_t H, float* d_h_next, float* d_c_next, float* d_y, int64_t ld_y,
                 void* stream);
 
+/* ---- transposed convolution ------------------------------------------------------- */
+/* y[p, h, w] = x[p, h / stride_h, w / stride_w] where both divide, else the zero value, over
+ * `planes` planes of H x W -> ((H - 1) stride_h + 1) x ((W - 1) stride_w + 1): the expanded
+ * input that turns conv_transpose2d into a stride-1 convolution (padding d (k - 1) - p, the
+ * kernel flipped with its channel axes swapped).  elem_type LQ_F32 (zero value 0.0) or
+ * LQ_I8 / LQ_U8S8 codes (zero value: the code of d_zero_point[0], NULL = 0).  Replaces the
+ * stride handling of F.conv_transpose2d under nnq.ConvTranspose2d
+ * (lucid/nn/quantized/conv_transpose.py:146-175); no reference counterpart as an op. */
+int lq_stride_expand(const void* d_x, int elem_type, int64_t planes, int64_t H, int64_t W, int stride_h,
+                     int stride_w, const float* d_zero_point, void* d_y, void* stream);
+
 /* ---- pooling ---------------------------------------------------------------------- */
 enum { LQ_POOL_MAX = 0, LQ_POOL_AVG = 1 };
 enum { LQ_POOL_ADAPTIVE = 1, LQ_POOL_COUNT_INCLUDE_PAD = 2 };

@@ -7,6 +7,7 @@ from lucid_amd.nn.layers import (
     AvgPool2d,
     BatchNorm2d,
     Conv2d,
+    ConvTranspose2d,
     Embedding,
     EmbeddingBag,
     Flatten,
@@ -27,7 +28,7 @@ from lucid_amd.nn.rnn import GRU, LSTM, GRUCell, LSTMCell, RNNCell
 __all__ = ["Module", "Parameter", "Linear", "Conv2d", "ReLU", "Sequential", "Identity",
            "BatchNorm2d", "Flatten", "Sigmoid", "Tanh", "Hardswish", "Hardsigmoid", "ELU", "LeakyReLU",
            "Embedding", "EmbeddingBag", "MaxPool2d", "AvgPool2d", "AdaptiveAvgPool2d",
-           "LSTM", "GRU", "LSTMCell", "GRUCell", "RNNCell"]
+           "LSTM", "GRU", "LSTMCell", "GRUCell", "RNNCell", "ConvTranspose2d"]
 
 
 def __getattr__(name: str):

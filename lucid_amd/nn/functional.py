@@ -71,6 +71,11 @@ def conv_padding(padding, kernel: tuple[int, int], dilation: tuple[int, int]) ->
             raise ValueError(f"unknown padding {padding!r}")
         th, tw = dilation[0] * (kernel[0] - 1), dilation[1] * (kernel[1] - 1)
         return th // 2, th - th // 2, tw // 2, tw - tw // 2
+    if isinstance(padding, (tuple, list)) and len(padding) == 4:   # explicit (top, bottom, left, right)
+        pads = tuple(int(v) for v in padding)
+        if min(pads) < 0:
+            raise ValueError("conv2d: padding must be non-negative")
+        return pads
     ph, pw = _pair(padding)
     if ph < 0 or pw < 0:
         raise ValueError("conv2d: padding must be non-negative")
@@ -386,3 +391,83 @@ def adaptive_avg_pool2d(x: Tensor, output_size) -> Tensor:
         _C.call("lq_pool2d", _C.POOL_AVG, ptr, xtype, xs, xz, N, C, H, W, OH, OW, 1, 1, 1, 1, 0, 0,
                 _C.POOL_ADAPTIVE, y.data_ptr(), None)
     return y
+
+
+# ------------------------------------------------------------ transposed convolution
+
+
+def convt_geometry(H: int, W: int, kernel, stride, padding, output_padding, dilation):
+    """((top, bottom, left, right) padding of the equivalent stride-1 convolution over the
+    stride-expanded input, OH, OW) of conv_transpose2d: pad d (k - 1) - p, plus the output
+    padding at the bottom / right; OH = (H - 1) s - 2 p + d (k - 1) + op + 1."""
+    (KH, KW), (sh, sw), (ph, pw) = _pair(kernel), _pair(stride), _pair(padding)
+    (oph, opw), (dh, dw) = _pair(output_padding), _pair(dilation)
+    if oph >= max(sh, dh) or opw >= max(sw, dw):
+        raise ValueError("conv_transpose2d: output_padding must be smaller than stride or dilation")
+    pt, pl = dh * (KH - 1) - ph, dw * (KW - 1) - pw
+    if pt < 0 or pl < 0:
+        raise NotImplementedError("conv_transpose2d: padding larger than dilation * (kernel - 1) is not supported "
+                                  "on the HIP backend")
+    OH = (H - 1) * sh - 2 * ph + dh * (KH - 1) + oph + 1
+    OW = (W - 1) * sw - 2 * pw + dw * (KW - 1) + opw + 1
+    return (pt, pt + oph, pl, pl + opw), OH, OW
+
+
+def convt_kernel(w, groups: int):
+    """A transposed-convolution kernel [Cin, Cout / groups, kh, kw] as the equivalent
+    convolution's [Cout, Cin / groups, kh, kw]: channel axes swapped within each group, taps
+    flipped (host numpy; codes or floats)."""
+    import numpy as np
+
+    Cin, Cout_g, KH, KW = w.shape
+    v = w.reshape(groups, Cin // groups, Cout_g, KH, KW).transpose(0, 2, 1, 3, 4)[..., ::-1, ::-1]
+    return np.ascontiguousarray(v.reshape(groups * Cout_g, Cin // groups, KH, KW))
+
+
+def stride_expand(x: Tensor, stride) -> Tensor:
+    """``x`` [N, C, H, W] spread by ``stride`` with the zero value in the gaps (the activation
+    zero point for a code-backed input, which stays code-backed on its grid)."""
+    import numpy as np
+
+    from lucid_amd._tensor import QuantSource
+
+    sh, sw = _pair(stride)
+    if (sh, sw) == (1, 1):
+        return x
+    N, C, H, W = x.shape
+    Hu, Wu = (H - 1) * sh + 1, (W - 1) * sw + 1
+    q = x.quant_source
+    if q is not None and q.code_type in (_C.I8, _C.U8S8):
+        y = empty((N, C, Hu, Wu), np.int8, "gpu")
+        _C.call("lq_stride_expand", q.codes.data_ptr(), q.code_type, N * C, H, W, sh, sw, q.zero_point.data_ptr(),
+                y.data_ptr(), None)
+        return Tensor._code_backed(QuantSource(y, q.code_type, q.scale, q.zero_point, q.quant_min, q.quant_max),
+                                   y.shape)
+    require_gpu(x, "conv_transpose2d")
+    y = empty((N, C, Hu, Wu), float32, "gpu")
+    _C.call("lq_stride_expand", x.data_ptr(), _C.F32, N * C, H, W, sh, sw, None, y.data_ptr(), None)
+    return y
+
+
+def conv_transpose2d(x: Tensor, weight: Tensor, bias: Tensor | None = None, stride=1, padding=0,
+                     output_padding=0, groups: int = 1, dilation=1) -> Tensor:
+    """Float transposed convolution (``weight`` [Cin, Cout / groups, kh, kw]): the stride-1
+    convolution of the stride-expanded input with the flipped, channel-swapped kernel
+    (the same sums as lucid/nn/functional/conv.py's conv_transpose2d, in another order)."""
+    require_gpu(x, "conv_transpose2d")
+    if x.ndim != 4 or x.dtype != float32:
+        raise TypeError(f"conv_transpose2d: float32 NCHW input expected, got {x.dtype} {x.shape}")
+    Cin, _, KH, KW = weight.shape
+    if int(x.shape[1]) != Cin:
+        raise ValueError(f"conv_transpose2d: input has {int(x.shape[1])} channels, weight expects {Cin}")
+    pads, _, _ = convt_geometry(int(x.shape[2]), int(x.shape[3]), (KH, KW), stride, padding, output_padding,
+                                dilation)
+    w = tensor_of(convt_kernel(weight.numpy(), groups))
+    return conv2d(stride_expand(x, stride), w, bias, 1, pads, dilation, groups)
+
+
+def tensor_of(a):
+    """A host array as a GPU tensor."""
+    from lucid_amd._tensor import tensor
+
+    return tensor(a, device="gpu")

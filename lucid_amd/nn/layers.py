@@ -105,6 +105,36 @@ class ReLU(Module):
         return F.relu(x)
 
 
+class ConvTranspose2d(Module):
+    """Float transposed convolution (lucid/nn/modules/conv.py ConvTranspose2d): weight
+    [in, out / groups, kh, kw]; ``convert`` swaps it for ``nn.quantized.ConvTranspose2d``."""
+
+    def __init__(self, in_channels: int, out_channels: int, kernel_size: Any, stride: Any = 1, padding: Any = 0,
+                 output_padding: Any = 0, groups: int = 1, bias: bool = True, dilation: Any = 1) -> None:
+        super().__init__()
+        if in_channels % groups or out_channels % groups:
+            raise ValueError("in_channels and out_channels must be divisible by groups")
+        self.in_channels, self.out_channels = in_channels, out_channels
+        self.kernel_size, self.stride = _pair(kernel_size), _pair(stride)
+        self.padding, self.output_padding = _pair(padding), _pair(output_padding)
+        self.dilation, self.groups = _pair(dilation), groups
+        fan_in = (out_channels // groups) * self.kernel_size[0] * self.kernel_size[1]
+        bound = 1.0 / math.sqrt(fan_in) if fan_in > 0 else 0.0
+        self.weight = Parameter(_uniform((in_channels, out_channels // groups, *self.kernel_size), bound))
+        if bias:
+            self.bias = Parameter(_uniform((out_channels,), bound))
+        else:
+            self.register_parameter("bias", None)
+
+    def forward(self, x: Tensor) -> Tensor:
+        return F.conv_transpose2d(x, self.weight, self.bias, self.stride, self.padding, self.output_padding,
+                                  self.groups, self.dilation)
+
+    def extra_repr(self) -> str:
+        return (f"{self.in_channels}, {self.out_channels}, kernel_size={self.kernel_size}, "
+                f"stride={self.stride}")
+
+
 class _PaddedTable(Module):
     """A ``[num_embeddings, embedding_dim]`` table, N(0, 1) with the padding row zeroed
     (lucid/nn/modules/sparse.py:_PaddedTable)."""

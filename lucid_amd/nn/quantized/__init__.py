@@ -11,6 +11,7 @@ MFMA GEMM over integer codes; ``QuantStub`` / ``DeQuantStub`` / ``Quantize`` /
 
 from lucid_amd.nn.quantized.activation import ELU, Hardsigmoid, Hardswish, LeakyReLU, Sigmoid, Tanh
 from lucid_amd.nn.quantized.conv import Conv2d
+from lucid_amd.nn.quantized.conv_transpose import ConvTranspose2d
 from lucid_amd.nn.quantized.functional_module import FloatFunctional, QFunctional
 from lucid_amd.nn.quantized.intrinsic import ConvReLU2d, LinearReLU
 from lucid_amd.nn.quantized.linear import Linear
@@ -21,7 +22,7 @@ from lucid_amd.nn.quantized.sparse import Embedding, EmbeddingBag
 
 __all__ = ["Linear", "QuantizedLinearMLX", "Conv2d", "ConvReLU2d", "LinearReLU", "QuantStub", "DeQuantStub", "Quantize", "DeQuantize",
            "QuantWrapper", "FloatFunctional", "QFunctional", "Sigmoid", "Hardswish", "Hardsigmoid",
-           "Tanh", "ELU", "LeakyReLU", "Embedding", "EmbeddingBag"]
+           "Tanh", "ELU", "LeakyReLU", "Embedding", "EmbeddingBag", "ConvTranspose2d"]
 
 
 def __getattr__(name: str):

@@ -45,6 +45,7 @@ function                      follows (lucid-official/lucid)
                               _pool_core.py:228-250 (numpy)
 ``rnn_cell`` / ``rnn_forward``  nn/modules/rnn.py (_rnn_step, _gru_step, LSTM gates i, f, g, o),
                               float64 numpy
+``conv_transpose2d_acc``      the direct scatter definition of conv_transpose2d, int64
 ``lucid_*``                   the multi-pass CPU composition timed as the CPU baseline
 ============================  ==========================================================
 
@@ -709,3 +710,32 @@ def rnn_forward(mode: str, x: np.ndarray, weights: dict, num_layers: int = 1, bi
             c_n.append(c)
         inp = outs
     return inp, np.stack(h_n), (np.stack(c_n) if mode == "LSTM" else None)
+
+
+# ------------------------------------------------------------ transposed convolution
+
+
+def conv_transpose2d_acc(x, w, za=0, x_u8s8=False, stride=(1, 1), pad=(0, 0), output_padding=(0, 0),
+                         dilation=(1, 1), groups=1) -> np.ndarray:
+    """Exact int64 accumulators of a transposed convolution, by its direct scatter definition
+    (lucid/nn/functional/conv.py conv_transpose2d): y[n, g Cout_g + co, ih s - p + kh d,
+    iw s - p + kw d] += (x[n, g Cin_g + ci, ih, iw] - za) w[g Cin_g + ci, co, kh, kw], for codes
+    x [N, Cin, H, W] (int8, or the c - 128 form with ``x_u8s8``) and w [Cin, Cout_g, KH, KW]."""
+    xv = np.asarray(x, np.int64) + (128 if x_u8s8 else 0) - int(za)
+    w = np.asarray(w, np.int64)
+    N, Cin, H, W = xv.shape
+    _, Cout_g, KH, KW = w.shape
+    (sh, sw), (ph, pw), (oph, opw), (dh, dw) = stride, pad, output_padding, dilation
+    OH = (H - 1) * sh - 2 * ph + dh * (KH - 1) + oph + 1
+    OW = (W - 1) * sw - 2 * pw + dw * (KW - 1) + opw + 1
+    cg = Cin // groups
+    full = np.zeros((N, groups * Cout_g, (H - 1) * sh + dh * (KH - 1) + 1 + oph,
+                     (W - 1) * sw + dw * (KW - 1) + 1 + opw), np.int64)
+    for g in range(groups):
+        xs = xv[:, g * cg:(g + 1) * cg]
+        for kh in range(KH):
+            for kw in range(KW):
+                contrib = np.einsum("nchw,co->nohw", xs, w[g * cg:(g + 1) * cg, :, kh, kw])
+                full[:, g * Cout_g:(g + 1) * Cout_g, kh * dh:kh * dh + (H - 1) * sh + 1:sh,
+                     kw * dw:kw * dw + (W - 1) * sw + 1:sw] += contrib
+    return full[:, :, ph:ph + OH, pw:pw + OW]

@@ -665,3 +665,50 @@ def test_rnn_forward_structure():
         w2 = {k.replace("_l1", "_l0"): v for k, v in w.items() if "_l1" in k}
         o2, _, _ = O.rnn_forward(mode, l0, w2, bidirectional=True)
         np.testing.assert_allclose(o2, out)
+
+
+# ------------------------------------------------------------ transposed convolution
+
+
+@pytest.mark.parametrize("stride,pad,opad,dil,groups", [((2, 2), (1, 1), (1, 1), (1, 1), 1),
+                                                        ((1, 2), (0, 1), (0, 1), (2, 1), 2),
+                                                        ((3, 3), (2, 0), (2, 1), (1, 1), 1)])
+def test_conv_transpose_is_the_adjoint_of_conv(stride, pad, opad, dil, groups):
+    # <conv(a, W), b> = <a, conv_transpose(b, W)> over integers: the transposed convolution is
+    # the adjoint of the convolution with the same stride / padding / dilation
+    rng = np.random.default_rng(sum(stride) + groups)
+    Cin, Cout, K = 4, 6, 3
+    a = rng.integers(-20, 20, (2, Cin, 11, 9)).astype(np.int8)
+    W = rng.integers(-20, 20, (Cout, Cin // groups, K, K)).astype(np.int8)
+    y = O.conv2d_acc(a, W, stride=stride, pad=(pad[0], pad[0], pad[1], pad[1]), dilation=dil, groups=groups)
+    b = rng.integers(-20, 20, y.shape).astype(np.int8)
+    # conv weight [Cout, Cin_g, K, K] is the transposed-conv weight [Cout, Cin_g] with roles swapped:
+    # as a transposed conv from Cout channels back to Cin, grouped the same way
+    wt = W.reshape(groups, Cout // groups, Cin // groups, K, K).reshape(Cout, Cin // groups, K, K)
+    back = O.conv_transpose2d_acc(b, wt, stride=stride, pad=pad, dilation=dil, groups=groups,
+                                  output_padding=(a.shape[2] - ((y.shape[2] - 1) * stride[0] - 2 * pad[0]
+                                                                + dil[0] * (K - 1) + 1),
+                                                  a.shape[3] - ((y.shape[3] - 1) * stride[1] - 2 * pad[1]
+                                                                + dil[1] * (K - 1) + 1)))
+    assert back.shape == a.shape
+    lhs = int((y.astype(np.int64) * b).sum())
+    rhs = int((a.astype(np.int64) * back).sum())
+    assert lhs == rhs
+
+
+def test_conv_transpose_equals_conv_of_expanded_input():
+    # the scatter definition against the stride-1 convolution of the stride-expanded input with
+    # the flipped, channel-swapped kernel (the route the GPU layer takes), with a zero point
+    rng = np.random.default_rng(3)
+    N, Cin, Cout, H, W, K, s, p, op, d, g = 2, 6, 4, 5, 7, 3, 2, 1, 1, 1, 2
+    x = rng.integers(-128, 128, (N, Cin, H, W)).astype(np.int8)
+    w = rng.integers(-127, 128, (Cin, Cout // g, K, K)).astype(np.int8)
+    za = 17
+    want = O.conv_transpose2d_acc(x, w, za=za, stride=(s, s), pad=(p, p), output_padding=(op, op),
+                                  dilation=(d, d), groups=g)
+    xu = np.full((N, Cin, (H - 1) * s + 1, (W - 1) * s + 1), za, np.int8)
+    xu[:, :, ::s, ::s] = x
+    wc = w.reshape(g, Cin // g, Cout // g, K, K).transpose(0, 2, 1, 3, 4)[..., ::-1, ::-1].reshape(Cout, Cin // g, K, K)
+    pt = d * (K - 1) - p
+    got = O.conv2d_acc(xu, np.ascontiguousarray(wc), za=za, pad=(pt, pt + op, pt, pt + op), dilation=(d, d), groups=g)
+    np.testing.assert_array_equal(got, want)
