@@ -194,6 +194,24 @@ def weight_only_lines(L, C, gtimer):
                         "K": K, "rotating_copies": rot, "us": round(ms * 1e3, 2),
                         "GB/s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 3)})
             del P
+    # transpose=false: dX[M, K] = dY[M, N] w_hat[N, K] (the QLoRA input gradient), a float32
+    # GEMM over tiles dequantized in LDS -- priced in flops against the fp32 peak
+    M = N = K = 4096
+    gs, bits = 64, 4
+    G = K // gs
+    P = L.empty((N * K * bits // 8,), np.int8, "gpu")
+    C.call("lq_fill_u32", P.data_ptr(), 0x5A3C96E1, N * K * bits // 32, None)
+    sc = L.tensor(np.full(N * G, 1e-3, np.float32), device="gpu")
+    bi = L.tensor(np.full(N * G, -0.1, np.float32), device="gpu")
+    dy = L.tensor(rng.standard_normal((M, N)).astype(np.float32), device="gpu")
+    dx = L.empty((M, K), np.float32, "gpu")
+    calls = [lambda st: C.check(lib.lq_group_matmul(
+        dy.data_ptr(), C.F32, N, P.data_ptr(), sc.data_ptr(), bi.data_ptr(), None, dx.data_ptr(), K, M, N, K,
+        gs, bits, 0, 0, None, 0, st), "lq_group_matmul")]
+    ms = gtimer.time_ms(calls, 5, 1)
+    tf = 2.0 * M * N * K / (ms * 1e-3) / 1e12
+    out.append({"kernel": "lq_group_matmul transpose=0 (4-bit, group 64; QLoRA dX)", "M": M, "N": N, "K": K,
+                "us": round(ms * 1e3, 2), "TFLOP/s": round(tf, 2), "frac_fp32": round(tf / 157.3, 3)})
     return out
 
 

@@ -304,10 +304,14 @@ int lq_group_dequantize_f32(const uint32_t* d_packed, const float* d_scales,
                             int bits, float* d_w, void* stream);
 /* y[m,n] = sum_k x[m,k] w_hat[n,k] (+ bias[n]) (ReLU with LQ_EPI_RELU), x / y of x_dtype
  * (LQ_F32 or LQ_F16), float32 accumulation, without forming w_hat.  Replaces
- * _C_engine.quantized.quantized_matmul (QuantizedMatmul.cpp:143-163) for transpose = 1;
- * transpose = 0 returns LQ_ERR_UNSUPPORTED.  d_biases (group offsets) and d_bias (layer
- * bias) may be NULL.  lq_group_matmul_workspace_size(M, N, K, group_size) bytes of workspace
- * let float32 activations be split once per call (as for lq_gemv_w8; NULL still runs). */
+ * _C_engine.quantized.quantized_matmul (QuantizedMatmul.cpp:143-163) for transpose = 1.
+ * transpose = 0: y[m,k] = sum_n x[m,n] w_hat[n,k] (+ bias[k]) with x [M, N] (ldx >= N) and
+ * y [M, K] (ldy >= K), w_hat tiles dequantized as lq_group_dequantize_f32 writes them -- the
+ * transpose=false product and the QLoRA input gradient dX = dY dequant(W) of the transpose=1
+ * product (QuantizedMatmulBackward::apply, QuantizedMatmul.cpp:73-90); no workspace.
+ * d_biases (group offsets) and d_bias (layer bias) may be NULL.
+ * lq_group_matmul_workspace_size(M, N, K, group_size) bytes of workspace let float32
+ * activations be split once per call for transpose = 1 (as for lq_gemv_w8; NULL still runs). */
 size_t lq_group_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int group_size);
 int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d_packed,
                     const float* d_scales, const float* d_biases, const float* d_bias, void* d_y,

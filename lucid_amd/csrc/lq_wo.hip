@@ -9,6 +9,8 @@
 //    y = sum_g (s[n,g] sum_{k in g} c[n,k] x[m,k] + b[n,g] sum_{k in g} x[m,k]) + bias[n]
 //    -- quantized_matmul with transpose=true (lucid/_C/ops/quantized/QuantizedMatmul.cpp:143-163,
 //    formula lucid/quantization/_qgemm.py:167-170).
+// The transpose=false product x . w_hat (also the QLoRA input gradient) is a separate float32
+// tiled kernel, group_matmul_nt_kernel, below.
 //
 // Operands.  The codes enter the MFMA as exact fp16 values: a code c of 8 or fewer bits is
 // placed under the exponent of 1024 (fp16 1024 + c, by v_perm byte placement or nibble
@@ -733,6 +735,102 @@ __global__ __launch_bounds__(256) void group_dequantize_kernel(const uint32_t* _
         *reinterpret_cast<vf4*>(w + id * PER + e) = vf4{out[e], out[e + 1], out[e + 2], out[e + 3]};
 }
 
+// ------------------------------------------- x . w_hat (quantized_matmul, transpose = false)
+//
+// y[m, k] = sum_n x[m, n] w_hat[n, k] for the packed w_hat[N, K] (groups along k): the product
+// of quantized_matmul with transpose=false, and the input gradient of the transpose=true
+// product, dX = dY dequant(W) (QuantizedMatmulBackward::apply, QuantizedMatmul.cpp:73-90).
+// The group scale / bias change along the summed axis n, so there is no factoring of the
+// sums as in the transpose=true kernel: each weight tile is dequantized into LDS exactly as
+// group_dequantize_kernel writes it, fl32(fl32(c s) + b), and the kernel is a float32 tiled
+// GEMM over it (64 x 64 outputs per 256-thread workgroup, 4 x 4 per thread, n in steps of 16,
+// fused multiply-adds in n order).
+constexpr int NT_T = 64, NT_K = 16;
+
+template <int BITS, bool XF32>
+__global__ __launch_bounds__(256) void group_matmul_nt_kernel(const void* __restrict__ xv, int64_t ldx,
+                                                              const uint32_t* __restrict__ packed,
+                                                              const float* __restrict__ scales,
+                                                              const float* __restrict__ biases,
+                                                              const float* __restrict__ bias, void* __restrict__ yv,
+                                                              int64_t ldy, int64_t M, int64_t N, int64_t K, int gs,
+                                                              int relu) {
+    constexpr int PER = 32 / BITS;
+    constexpr uint32_t L = (1u << BITS) - 1u;
+    constexpr int WPR = NT_T / PER;  // packed words per tile row
+    __shared__ float xs[NT_K][NT_T + 1];
+    __shared__ float ws[NT_K][NT_T];
+    const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
+    const int64_t G = K / gs, words_per_row = K / PER;
+    const int64_t KT = (K + NT_T - 1) / NT_T, MT = (M + NT_T - 1) / NT_T;
+    for (int64_t tile = blockIdx.x; tile < KT * MT; tile += gridDim.x) {
+        const int64_t k0 = (tile % KT) * NT_T, m0 = (tile / KT) * NT_T;
+        float acc[4][4] = {};
+        for (int64_t n0 = 0; n0 < N; n0 += NT_K) {
+            for (int e = threadIdx.x; e < NT_T * NT_K; e += 256) {
+                const int r = e / NT_K, kk = e % NT_K;
+                const int64_t gm = m0 + r, gn = n0 + kk;
+                float v = 0.0f;
+                if (gm < M && gn < N) {
+                    if constexpr (XF32) v = static_cast<const float*>(xv)[gm * ldx + gn];
+                    else v = (float)static_cast<const _Float16*>(xv)[gm * ldx + gn];
+                }
+                xs[kk][r] = v;
+            }
+            for (int e = threadIdx.x; e < NT_K * WPR; e += 256) {
+                const int r = e / WPR, wc = e % WPR;
+                const int64_t gn = n0 + r, gk = k0 + (int64_t)wc * PER;
+                float out[PER];
+                if (gn < N && gk < K) {  // K is a multiple of the group size, so whole words
+                    const uint32_t word = packed[gn * words_per_row + gk / PER];
+                    const int64_t gi = gn * G + gk / gs;
+                    const float s = scales[gi];
+                    const float b = biases ? biases[gi] : 0.0f;
+#pragma unroll
+                    for (int q = 0; q < PER; ++q) {
+                        const float t = (float)((word >> (q * BITS)) & L) * s;
+                        out[q] = biases ? t + b : t;
+                    }
+                } else {
+#pragma unroll
+                    for (int q = 0; q < PER; ++q) out[q] = 0.0f;
+                }
+#pragma unroll
+                for (int q = 0; q < PER; ++q) ws[r][wc * PER + q] = out[q];
+            }
+            __syncthreads();
+#pragma unroll
+            for (int kk = 0; kk < NT_K; ++kk) {
+                float xr[4], wr[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) xr[i] = xs[kk][ty + 16 * i];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) wr[j] = ws[kk][tx + 16 * j];
+#pragma unroll
+                for (int i = 0; i < 4; ++i)
+#pragma unroll
+                    for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xr[i], wr[j], acc[i][j]);
+            }
+            __syncthreads();
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int64_t gm = m0 + ty + 16 * i;
+            if (gm >= M) continue;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int64_t gk = k0 + tx + 16 * j;
+                if (gk >= K) continue;
+                float v = acc[i][j];
+                if (bias) v = v + bias[gk];
+                if (relu) v = (v <= 0.0f) ? 0.0f : v;
+                if constexpr (XF32) static_cast<float*>(yv)[gm * ldy + gk] = v;
+                else static_cast<_Float16*>(yv)[gm * ldy + gk] = (_Float16)v;
+            }
+        }
+    }
+}
+
 // ------------------------------------------------------------------ host side
 
 struct WoPlan {
@@ -924,8 +1022,27 @@ int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d
     LQ_REQUIRE(K % group_size == 0, "lq_group_matmul: K must be a multiple of group_size");
     LQ_REQUIRE(x_dtype == LQ_F32 || x_dtype == LQ_F16, "lq_group_matmul: x_dtype must be LQ_F32 or LQ_F16");
     LQ_REQUIRE((flags & ~LQ_EPI_RELU) == 0, "lq_group_matmul: unknown flags");
-    if (!transpose)
-        return set_error(LQ_ERR_UNSUPPORTED, "lq_group_matmul: only transpose=true (x @ w_hat^T) is implemented");
+    if (!transpose) {  // y[M, K] = x[M, N] w_hat[N, K]
+        if (M == 0) return LQ_OK;
+        LQ_REQUIRE(d_x && d_y && (N == 0 || (d_packed && d_scales)), "lq_group_matmul: NULL pointer");
+        LQ_REQUIRE(ldx >= N && ldy >= K, "lq_group_matmul: leading dimension too small");
+        const int64_t tiles = ((M + NT_T - 1) / NT_T) * ((K + NT_T - 1) / NT_T);
+        const dim3 grid((unsigned)std::min<int64_t>(tiles, 1 << 20));
+        const uint32_t* pk = N ? d_packed : nullptr;
+        const float* gb = N ? d_biases : nullptr;
+        const int relu = (flags & LQ_EPI_RELU) ? 1 : 0;
+        hipStream_t st = as_stream(stream);
+#define LQ_NT(B, XF)                                                                                           \
+    hipLaunchKernelGGL((group_matmul_nt_kernel<B, XF>), grid, dim3(256), 0, st, d_x, ldx, pk, d_scales, gb, d_bias, \
+                       d_y, ldy, M, N, K, group_size, relu)
+        if (bits == 8) {
+            if (x_dtype == LQ_F32) LQ_NT(8, true); else LQ_NT(8, false);
+        } else {
+            if (x_dtype == LQ_F32) LQ_NT(4, true); else LQ_NT(4, false);
+        }
+#undef LQ_NT
+        return launch_status("lq_group_matmul");
+    }
     if (M == 0 || N == 0) return LQ_OK;
     LQ_REQUIRE(d_x && d_packed && d_scales && d_y, "lq_group_matmul: NULL pointer");
     LQ_REQUIRE(ldx >= K && ldy >= N, "lq_group_matmul: leading dimension too small");

@@ -9,8 +9,11 @@ lucid_amd/csrc/lq_wo.hip:
   ``c = clip(round((w - b) / s), 0, 2^bits - 1)``, packed 32/bits codes per word, little end
   first (``lq_group_quantize_f32``);
 * ``dequantize(...)`` -> ``c * s + b`` as float32 (``lq_group_dequantize_f32``);
-* ``quantized_matmul(x, ...)`` -> ``x @ w_hat^T`` in x's dtype without forming ``w_hat``
-  (``lq_group_matmul``; ``transpose=False`` is not implemented).
+* ``quantized_matmul(x, ...)`` -> ``x @ w_hat^T`` (``transpose=True``) or ``x @ w_hat``
+  (``transpose=False``) in x's dtype (``lq_group_matmul``);
+* ``quantized_matmul_backward(dy, ...)`` -> the input gradient of ``quantized_matmul``, the
+  product against the dequantized weight in the other orientation (QLoRA's dX,
+  ``QuantizedMatmulBackward::apply``, lucid/_C/ops/quantized/QuantizedMatmul.cpp:73-90).
 
 Like Lucid's (Metal-only) ops these require device tensors.  The exact scale / rounding /
 pack order of MLX 0.32.3, which Lucid calls, is not visible from the reference: these ops
@@ -85,29 +88,46 @@ def dequantize(wq: Tensor, scales: Tensor, biases: Tensor | None, group_size: in
 def quantized_matmul(x: Tensor, wq: Tensor, scales: Tensor, biases: Tensor | None,
                      transpose: bool = True, group_size: int = 64, bits: int = 8,
                      bias: Tensor | None = None, relu: bool = False) -> Tensor:
-    """``x @ w_hat^T`` (``[..., K] -> [..., N]``) in x's dtype (float32 or float16).
+    """``x @ w_hat^T`` (``[..., K] -> [..., N]``) or, with ``transpose=False``, ``x @ w_hat``
+    (``[..., N] -> [..., K]``), in x's dtype (float32 or float16), for the packed
+    ``w_hat [N, K]``.
 
-    ``bias`` / ``relu`` fuse the layer epilogue of ``QuantizedLinearMLX`` into the kernel.
+    ``bias`` (length of the output features) / ``relu`` fuse the layer epilogue of
+    ``QuantizedLinearMLX`` into the kernel.
     """
     require_gpu(x, "quantized.quantized_matmul")
-    if not transpose:
-        raise NotImplementedError("quantized_matmul: transpose=False is not implemented on the "
-                                  "HIP backend")
     if x.dtype not in (float32, float16):
         raise TypeError(f"quantized_matmul: float32 or float16 input expected, got {x.dtype}")
     N, K = wq.shape[0], _unpacked_k(wq, bits)
     _check(group_size, bits, K, "quantized_matmul")
-    if x.shape[-1] != K:
-        raise ValueError(f"quantized_matmul: input features {x.shape[-1]} != weight K {K}")
-    M = x.numel() // K
+    d_in, d_out = (K, N) if transpose else (N, K)
+    if x.shape[-1] != d_in:
+        raise ValueError(f"quantized_matmul: input features {x.shape[-1]} != the weight's "
+                         f"{'K' if transpose else 'N'} {d_in}")
+    if bias is not None and bias.numel() != d_out:
+        raise ValueError(f"quantized_matmul: bias of {bias.numel()} for {d_out} output features")
+    M = int(np.prod(x.shape[:-1], dtype=np.int64))
     s = on_device(scales)
     b = on_device(biases) if biases is not None else None
     lb = on_device(bias) if bias is not None else None
-    y = empty((*x.shape[:-1], N), x.dtype, "gpu")
-    if M and N:
-        ws_bytes = _C.lib().lq_group_matmul_workspace_size(M, N, K, group_size)
-        _C.call("lq_group_matmul", x.data_ptr(), _C.F32 if x.dtype == float32 else _C.F16, K,
+    y = empty((*x.shape[:-1], d_out), x.dtype, "gpu")
+    if M and d_out:
+        ws_bytes = _C.lib().lq_group_matmul_workspace_size(M, N, K, group_size) if transpose else 0
+        _C.call("lq_group_matmul", x.data_ptr(), _C.F32 if x.dtype == float32 else _C.F16, d_in,
                 wq.data_ptr(), s.data_ptr(), b.data_ptr() if b is not None else None,
-                lb.data_ptr() if lb is not None else None, y.data_ptr(), N, M, N, K, group_size,
-                bits, 1, _C.EPI_RELU if relu else 0, workspace.get(ws_bytes), ws_bytes, None)
+                lb.data_ptr() if lb is not None else None, y.data_ptr(), d_out, M, N, K, group_size,
+                bits, 1 if transpose else 0, _C.EPI_RELU if relu else 0, workspace.get(ws_bytes),
+                ws_bytes, None)
     return y
+
+
+def quantized_matmul_backward(dy: Tensor, wq: Tensor, scales: Tensor, biases: Tensor | None,
+                              transpose: bool = True, group_size: int = 64, bits: int = 8) -> Tensor:
+    """The input gradient of ``quantized_matmul(x, wq, scales, biases, transpose, ...)``:
+    ``dX = dY @ dequant(W)`` for ``transpose=True``, ``dY @ dequant(W)^T`` otherwise, in dY's
+    dtype (QuantizedMatmulBackward::apply, lucid/_C/ops/quantized/QuantizedMatmul.cpp:73-90;
+    the weight, scales and biases are frozen, so dX is the only gradient).  Computed by the
+    fused product in the other orientation, without forming the dequantized weight.
+    """
+    return quantized_matmul(dy, wq, scales, biases, transpose=not transpose, group_size=group_size,
+                            bits=bits)

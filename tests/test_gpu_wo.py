@@ -318,3 +318,97 @@ def test_dispatch_bench_harness(gpu):
         assert r["p5_ms"] <= r["median_ms"] <= r["p95_ms"]
         for key in ("bits", "m", "n", "k", "first_ms", "GB/s", "hbm_roofline_frac", "TOPS"):
             assert key in r
+
+
+# ------------------------------------------- transpose=False and the QLoRA input gradient
+
+
+def _packed_case(gpu, rng, N, K, gs, bits, scale=0.05):
+    from lucid_amd.quantization import _qgemm
+
+    w = (rng.standard_normal((N, K)) * scale).astype(np.float32)
+    packed, scales, biases = _qgemm.quantize(_t(gpu, w), group_size=gs, bits=bits)
+    wd = O.group_dequantize(packed.numpy().view(np.uint32), scales.numpy(), biases.numpy(), gs,
+                            bits).astype(np.float64)
+    return packed, scales, biases, wd
+
+
+@pytest.mark.parametrize("M,N,K,bits,gs", [(1, 64, 64, 8, 64), (70, 200, 96, 4, 32),
+                                           (33, 1000, 384, 8, 128), (128, 512, 1024, 4, 64),
+                                           (5, 7, 4096, 8, 64)])
+def test_quantized_matmul_no_transpose(gpu, M, N, K, bits, gs):
+    """``x @ w_hat`` (x [M, N] -> [M, K]) with bias / ReLU and fp16 inputs, against float64."""
+    from lucid_amd.quantization import _qgemm
+
+    rng = np.random.default_rng(M * 7 + N)
+    packed, scales, biases, wd = _packed_case(gpu, rng, N, K, gs, bits)
+    x = rng.standard_normal((M, N)).astype(np.float32)
+    b = rng.standard_normal(K).astype(np.float32)
+    y = _qgemm.quantized_matmul(_t(gpu, x), packed, scales, biases, transpose=False, group_size=gs,
+                                bits=bits)
+    assert y.shape == (M, K) and y.dtype == np.float32
+    ref = x.astype(np.float64) @ wd
+    _close(y.numpy(), ref, np.abs(x.astype(np.float64)) @ np.abs(wd))
+    for half in (False, True):
+        xin = x.astype(np.float16) if half else x
+        y = _qgemm.quantized_matmul(_t(gpu, xin), packed, scales, biases, transpose=False,
+                                    group_size=gs, bits=bits, bias=_t(gpu, b), relu=True)
+        assert y.dtype == (np.float16 if half else np.float32)
+        xd = xin.astype(np.float64)
+        _close(y.numpy(), np.maximum(xd @ wd + b, 0.0), np.abs(xd) @ np.abs(wd) + np.abs(b), half=half)
+
+
+def test_quantized_matmul_no_transpose_without_group_biases_and_batched(gpu):
+    from lucid_amd.quantization import _qgemm
+
+    rng = np.random.default_rng(5)
+    packed, scales, _, _ = _packed_case(gpu, rng, 48, 256, 64, 4)
+    wd = O.group_dequantize(packed.numpy().view(np.uint32), scales.numpy(), None, 64, 4).astype(np.float64)
+    x = rng.standard_normal((2, 3, 48)).astype(np.float32)
+    y = _qgemm.quantized_matmul(_t(gpu, x), packed, scales, None, transpose=False, group_size=64, bits=4)
+    assert y.shape == (2, 3, 256)
+    xd = x.astype(np.float64)
+    _close(y.numpy(), xd @ wd, np.abs(xd) @ np.abs(wd))
+
+
+@pytest.mark.parametrize("transpose", [True, False])
+@pytest.mark.parametrize("bits", [4, 8])
+def test_quantized_matmul_backward_is_the_adjoint(gpu, transpose, bits):
+    """QLoRA's dX (QuantizedMatmulBackward::apply, QuantizedMatmul.cpp:73-90): against float64
+    ``dY dequant(W)`` (or its transpose), and the adjoint identity
+    ``<dY, f(x)> = <dX(dY), x>`` of the linear map f -- a transposed or mis-grouped product
+    fails it."""
+    from lucid_amd.quantization import _qgemm
+
+    rng = np.random.default_rng(bits + 10 * transpose)
+    M, N, K, gs = 37, 160, 512, 64
+    packed, scales, biases, wd = _packed_case(gpu, rng, N, K, gs, bits)
+    d_in, d_out = (K, N) if transpose else (N, K)
+    x = rng.standard_normal((M, d_in)).astype(np.float32)
+    dy = rng.standard_normal((M, d_out)).astype(np.float32)
+    y = _qgemm.quantized_matmul(_t(gpu, x), packed, scales, biases, transpose=transpose, group_size=gs,
+                                bits=bits).numpy().astype(np.float64)
+    dx = _qgemm.quantized_matmul_backward(_t(gpu, dy), packed, scales, biases, transpose=transpose,
+                                          group_size=gs, bits=bits)
+    assert dx.shape == x.shape and dx.dtype == np.float32
+    dyd = dy.astype(np.float64)
+    wmat = wd if transpose else wd.T   # dX = dY @ w_deq (swapaxes when transpose=False)
+    _close(dx.numpy(), dyd @ wmat, np.abs(dyd) @ np.abs(wmat))
+    lhs = float(np.sum(dyd * y))
+    rhs = float(np.sum(dx.numpy().astype(np.float64) * x))
+    mag = float(np.abs(dyd).ravel() @ (np.abs(x.astype(np.float64)) @ np.abs(wd.T if transpose else wd)).ravel())
+    assert abs(lhs - rhs) <= 1e-5 * mag
+
+
+def test_group_matmul_no_transpose_empty_reduction(gpu):
+    """N = 0: x [M, 0] @ w_hat[0, K] is the bias alone."""
+    from lucid_amd import _C
+
+    M, K = 3, 64
+    b = np.arange(K, dtype=np.float32) - 30
+    bd = _t(gpu, b)
+    x = gpu.empty((M, 1), np.float32, "gpu")
+    y = gpu.empty((M, K), np.float32, "gpu")
+    _C.call("lq_group_matmul", x.data_ptr(), _C.F32, 0, None, None, None, bd.data_ptr(), y.data_ptr(), K,
+            M, 0, K, 64, 8, 0, _C.EPI_RELU, None, 0, None)
+    np.testing.assert_array_equal(y.numpy(), np.broadcast_to(np.maximum(b, 0), (M, K)))
