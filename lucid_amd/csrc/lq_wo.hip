@@ -481,6 +481,7 @@ struct WvArgs {
     int G, gs;
     int NC;                  // 16-byte chunks per weight row
     int Kpad;                // staged activation length (J * 64 chunks of codes)
+    int xvec;                // activation rows allow 4-element vector loads
 };
 
 __device__ __forceinline__ int wv_slot(int k) {
@@ -525,14 +526,49 @@ __global__ __launch_bounds__(1024) void wo_gemv_valu_kernel(WvArgs a) {
     }
     __builtin_amdgcn_sched_barrier(0);
 
-    for (int i = tid; i < MX * a.Kpad; i += blockDim.x) {
-        const int m = i / a.Kpad, k = i - m * a.Kpad;
-        float v = 0.0f;
-        if (m < a.M && k < a.K) {
-            if constexpr (XF32) v = static_cast<const float*>(a.x)[(int64_t)m * a.ldx + k];
-            else v = (float)static_cast<const _Float16*>(a.x)[(int64_t)m * a.ldx + k];
+    // Activation staging in groups of four consecutive k (one 16-byte LDS slot; Kpad is a
+    // multiple of 4), up to XU groups per thread with every load issued before any LDS store,
+    // so the staging costs one L2 round trip per XU * blockDim.x groups instead of one per
+    // element.  Vector loads when the rows allow them (a.xvec), element loads otherwise.
+    constexpr int XU = 4;
+    const int nq = MX * a.Kpad / 4;
+    for (int base = 0; base < nq; base += XU * (int)blockDim.x) {
+        vf4 xv4[XU];
+#pragma unroll
+        for (int u = 0; u < XU; ++u) {
+            const int i = base + u * (int)blockDim.x + tid;
+            const int m = (4 * i) / a.Kpad, k = (4 * i) - m * a.Kpad;
+            vf4 v = vf4{0.0f, 0.0f, 0.0f, 0.0f};
+            if (i < nq && m < a.M && k < a.K) {
+                const int64_t o = (int64_t)m * a.ldx + k;
+                if (a.xvec && k + 4 <= a.K) {
+                    if constexpr (XF32) {
+                        v = *reinterpret_cast<const vf4*>(static_cast<const float*>(a.x) + o);
+                    } else {
+                        typedef _Float16 h4 __attribute__((ext_vector_type(4)));
+                        const h4 h = *reinterpret_cast<const h4*>(static_cast<const _Float16*>(a.x) + o);
+                        v = vf4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+                    }
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        if (k + e < a.K) {
+                            if constexpr (XF32) v[e] = static_cast<const float*>(a.x)[o + e];
+                            else v[e] = (float)static_cast<const _Float16*>(a.x)[o + e];
+                        }
+                    }
+                }
+            }
+            xv4[u] = v;
         }
-        xs[m * a.Kpad + wv_slot(k)] = v;
+#pragma unroll
+        for (int u = 0; u < XU; ++u) {
+            const int i = base + u * (int)blockDim.x + tid;
+            if (i < nq) {
+                const int m = (4 * i) / a.Kpad, k = (4 * i) - m * a.Kpad;
+                *reinterpret_cast<vf4*>(xs + m * a.Kpad + wv_slot(k)) = xv4[u];
+            }
+        }
     }
     __syncthreads();
     // x sums: per group (group-wise) or per row (zero points), from float4 partials reduced
@@ -903,6 +939,10 @@ bool launch_wv(WvArgs a, bool xf32, hipStream_t st) {
     const int J = Jn <= 1 ? 1 : Jn <= 2 ? 2 : Jn <= 4 ? 4 : Jn <= 8 ? 8 : Jn <= 12 ? 12 : Jn <= 16 ? 16 : 0;
     if (J == 0) return false;
     a.Kpad = J * 64 * CK;
+    {
+        const int eb = xf32 ? 4 : 2;  // element bytes; a 4-element load needs 4 * eb alignment
+        a.xvec = (reinterpret_cast<uintptr_t>(a.x) % (4 * eb) == 0) && ((a.ldx * eb) % (4 * eb) == 0);
+    }
     const int MX = a.M;
     const int waves = a.N >= 4096 ? 16 : std::max(1, (a.N + 255) / 256);
     const size_t passes = ((size_t)MX * a.Kpad / 4 + 64 * waves - 1) / (64 * waves);
