@@ -354,9 +354,9 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_tiled_kernel(G
         }
 }
 
-template <int BM, int BN, int WAVES_M, int WAVES_N>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int NBUF_ = 2>
 struct DmaTile {
-    static constexpr int BK = 128, CPR = 8, KS = 2, NBUF = 2;
+    static constexpr int BK = 128, CPR = 8, KS = 2, NBUF = NBUF_;
     static constexpr int NW = WAVES_M * WAVES_N;
     static constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
     static constexpr int FM = WM / 16, FN = WN / 16;
@@ -372,6 +372,22 @@ struct DmaTile {
     static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 };
 
+// LDS stage buffers of the DMA main loop (a third buffer measured the same at 4096^3: the
+// copies land within one stage).
+constexpr int GEMM_NBUF = 2;
+
+// Scheduling pattern for one K step: R fragment reads (DS) spread over Q MFMAs, each read
+// followed by its share of the MFMAs.
+template <int R, int Q, int T = 0>
+__device__ __forceinline__ void pin_reads_mfmas() {
+    if constexpr (T < R) {
+        constexpr int n = (T + 1) * Q / R - T * Q / R;
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // one DS read
+        if constexpr (n > 0) __builtin_amdgcn_sched_group_barrier(0x008, n, 0);  // n MFMAs
+        pin_reads_mfmas<R, Q, T + 1>();
+    }
+}
+
 // --------------------------------------------- LDS-DMA MFMA main loop (large M)
 //
 // The production path for M > 64 when K % 128 == 0.  Global -> LDS copies use the LDS-DMA
@@ -380,8 +396,8 @@ struct DmaTile {
 // Buffer descriptors bound A and B to M*lda and N*ldb bytes, so rows past M or N read as
 // zero (their outputs are never stored) and no per-row predicates are needed.
 //
-// Two LDS stages of BK = 128: stage kt+2 is issued right after the barrier that retires
-// stage kt, and waited for (vmcnt) one stage later.  Inside a stage the two 64-byte K steps
+// A ring of NBUF LDS stages of BK = 128: stage kt+NBUF is issued right after the barrier
+// that retires stage kt, and waited for (vmcnt) NBUF - 1 stages later.  Inside a stage the two 64-byte K steps
 // ping-pong fragment registers: step s+1's fragments are read while step s's MFMAs run.
 // The copy is issued from inline asm so the compiler neither tracks it nor inserts its own
 // conservative vmcnt(0) in front of every LDS read (it cannot tell the stage buffers apart);
@@ -394,11 +410,12 @@ struct DmaTile {
 // 16 (l / 16) + 4 i + r, so over its four B fragments a lane owns 16 consecutive columns of
 // each of its rows: the epilogue works from registers and stores 16-byte row segments
 // (int8) directly, with no LDS round trip.  The per-column epilogue inputs are loaded
-// before the main loop (they are the oldest loads, so the stage waits cover them).
+// after the main loop, so their registers do not compete with the fragment double buffer.
 
-template <int BM, int BN, int WAVES_M, int WAVES_N, int KIND>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_dma_kernel(GemmArgs a) {
-    typedef DmaTile<BM, BN, WAVES_M, WAVES_N> P;
+template <int BM, int BN, int WAVES_M, int WAVES_N, int NBUF, int KIND>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_dma_kernel(GemmArgs a) {
+    typedef DmaTile<BM, BN, WAVES_M, WAVES_N, NBUF> P;
+    static_assert(NBUF >= 2 && (NBUF - 1) * P::LPS < 64, "stage ring");
     constexpr int BK = P::BK, NW = P::NW, WM = P::WM, FM = P::FM, FN = P::FN;
     constexpr int RPI = P::ROWS_PER_INSTR, A_I = P::A_I, B_I = P::B_I, SB = P::SB;
     constexpr bool INT_CODES = KIND == LQ_OUT_Q8 || KIND == LQ_OUT_QU8 || KIND == LQ_OUT_Q16 || KIND == LQ_OUT_QU8S8;
@@ -412,26 +429,6 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_dma_kernel(Gem
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int nk = a.K / BK;
-
-    // Epilogue inputs first: this lane's 16 columns and FM rows.
-    const EpiParams p = epi_params(a);
-    const int nc0 = n0 + wn * 64 + (lane >> 4) * 16;
-    const int mr0 = m0 + wm * WM + (lane & 15);
-    float csb[16], cbias[16];
-    int32_t czab[16];  // za * bsum[n]
-#pragma unroll
-    for (int q = 0; q < 16; ++q) {
-        const int nn = min(nc0 + q, a.N - 1);  // clamped: out-of-range columns are never stored
-        csb[q] = a.b_scale ? a.b_scale[(int64_t)nn * a.b_stride] : 1.0f;
-        cbias[q] = a.bias ? a.bias[nn] : 0.0f;
-        czab[q] = p.has_za ? (int32_t)((uint32_t)p.za * (uint32_t)a.b_sums[nn]) : 0;
-    }
-    float rsa[FM];
-#pragma unroll
-    for (int j = 0; j < FM; ++j) {
-        const int mm = min(mr0 + j * 16, a.M - 1);
-        rsa[j] = a.a_scale ? a.a_scale[(int64_t)mm * a.a_stride] : 1.0f;
-    }
 
     const v4i ra = buffer_rsrc(a.A, (uint32_t)((int64_t)a.M * a.lda));
     const v4i rb = buffer_rsrc(a.B, (uint32_t)((int64_t)a.N * a.ldb));
@@ -491,34 +488,63 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_i8_dma_kernel(Gem
             for (int j = 0; j < FM; ++j)
                 acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f[FM + i], f[j], acc[i][j], 0, 0, 0);
     };
+    // The scheduler would otherwise place each fragment read right before its first MFMA
+    // (and wait for it there); pin the order instead: the next step's FM + FN reads spread
+    // over this step's FM * FN MFMAs, one read ahead of each run of MFMAs.
+    auto pin_order = [&]() __attribute__((always_inline)) { pin_reads_mfmas<FM + FN, FM * FN>(); };
     // One stage in buffer B (compile time), ending with the switch to the other buffer.
     auto stage = [&](auto bc, int kt, bool last) __attribute__((always_inline)) {
         constexpr int B = decltype(bc)::value;
         read_frags(F1, B, 1);
         mfmas(F0);
+        pin_order();
         if (!last) {
-            wait_vmcnt<0>();  // stage kt+1 (the only copy in flight) has landed
+            wait_vmcnt<(NBUF - 2) * P::LPS>();  // stage kt+1 has landed (kt+2.. may be in flight)
             block_barrier();  // ... in every wave, and every wave is done reading stage kt
-            issue(B, kt + 2);
-            read_frags(F0, B ^ 1, 0);
+            issue(B, kt + NBUF);
+            read_frags(F0, (B + 1) % NBUF, 0);
         }
         mfmas(F1);
+        if (!last) pin_order();
     };
 
     if (nk > 0) {
-        issue(0, 0);
-        issue(1, 1);
-        wait_vmcnt<P::LPS>();
+#pragma unroll
+        for (int j = 0; j < NBUF; ++j) issue(j, j);
+        wait_vmcnt<(NBUF - 1) * P::LPS>();
         block_barrier();
         read_frags(F0, 0, 0);
         int kt = 0;
-        for (; kt + 2 < nk; kt += 2) {
-            stage(std::integral_constant<int, 0>(), kt, false);
-            stage(std::integral_constant<int, 1>(), kt + 1, false);
+        for (; kt + NBUF < nk; kt += NBUF) {
+            [&]<int... Bs>(std::integer_sequence<int, Bs...>) {
+                (stage(std::integral_constant<int, Bs>(), kt + Bs, false), ...);
+            }(std::make_integer_sequence<int, NBUF>());
         }
-        stage(std::integral_constant<int, 0>(), kt, kt + 1 == nk);
-        if (kt + 1 < nk) stage(std::integral_constant<int, 1>(), kt + 1, true);
+        [&]<int... Bs>(std::integer_sequence<int, Bs...>) {
+            ((kt + Bs < nk ? stage(std::integral_constant<int, Bs>(), kt + Bs, kt + Bs + 1 == nk) : void()), ...);
+        }(std::make_integer_sequence<int, NBUF>());
     }
+    // Epilogue inputs, loaded after the main loop so their registers (52 per lane) do not
+    // compete with the fragment double buffer: this lane's 16 columns and FM rows.
+    const EpiParams p = epi_params(a);
+    const int nc0 = n0 + wn * 64 + (lane >> 4) * 16;
+    const int mr0 = m0 + wm * WM + (lane & 15);
+    float csb[16], cbias[16];
+    int32_t czab[16];  // za * bsum[n]
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+        const int nn = min(nc0 + q, a.N - 1);  // clamped: out-of-range columns are never stored
+        csb[q] = a.b_scale ? a.b_scale[(int64_t)nn * a.b_stride] : 1.0f;
+        cbias[q] = a.bias ? a.bias[nn] : 0.0f;
+        czab[q] = p.has_za ? (int32_t)((uint32_t)p.za * (uint32_t)a.b_sums[nn]) : 0;
+    }
+    float rsa[FM];
+#pragma unroll
+    for (int j = 0; j < FM; ++j) {
+        const int mm = min(mr0 + j * 16, a.M - 1);
+        rsa[j] = a.a_scale ? a.a_scale[(int64_t)mm * a.a_stride] : 1.0f;
+    }
+
     wait_vmcnt<0>();  // no copy may still target LDS when the workgroup ends
 
     // Epilogue from registers: acc[i][j][r] is C[mr0 + 16 j][nc0 + 4 i + r].  Every lane
@@ -852,13 +878,13 @@ struct GemmLaunch {
                             ((int64_t)(a.N + 256) * a.ldb < (int64_t)1 << 31);
         const int64_t dma_tiles = ((int64_t)(a.M + 255) / 256) * ((a.N + 127) / 128);
         if (dma_ok && dma_tiles >= 256) {
-            hipLaunchKernelGGL((gemm_i8_dma_kernel<256, 128, 4, 2, KIND>), dim3((unsigned)dma_tiles),
+            hipLaunchKernelGGL((gemm_i8_dma_kernel<256, 128, 4, 2, GEMM_NBUF, KIND>), dim3((unsigned)dma_tiles),
                                dim3(512), 0, st, a);
             return launch_status("lq_gemm_w8a8 (dma 256x128)");
         }
         const int64_t dma_tiles_128 = ((int64_t)(a.M + 127) / 128) * ((a.N + 127) / 128);
         if (dma_ok && dma_tiles_128 >= 128) {
-            hipLaunchKernelGGL((gemm_i8_dma_kernel<128, 128, 4, 2, KIND>), dim3((unsigned)dma_tiles_128),
+            hipLaunchKernelGGL((gemm_i8_dma_kernel<128, 128, 4, 2, GEMM_NBUF, KIND>), dim3((unsigned)dma_tiles_128),
                                dim3(512), 0, st, a);
             return launch_status("lq_gemm_w8a8 (dma 128x128)");
         }
