@@ -42,4 +42,6 @@ def __getattr__(name: str):
 
     if name in ("nn", "quantization", "backends", "serialization"):
         return importlib.import_module(f"lucid_amd.{name}")
+    if name in ("save", "load"):  # lucid.save / lucid.load
+        return getattr(importlib.import_module("lucid_amd.serialization"), name)
     raise AttributeError(f"module 'lucid_amd' has no attribute {name!r}")

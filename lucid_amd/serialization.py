@@ -14,15 +14,30 @@ for their shape and dtype, covering it without overlaps or gaps) and raises ``Va
 naming the file and tensor.  Unsigned integers widen as Lucid widens them (``U8`` to int16,
 ``U16`` to int32, ``U32`` / ``U64`` to int64, refusing uint64 values past int64); ``BF16``,
 which numpy lacks, widens exactly to float32.
+
+``save`` / ``load`` write and read Lucid's own checkpoint format
+(lucid/serialization/__init__.py:105-456): a pickle stream of the container
+``{"_lucid_format": 2, "obj": obj[, "_state_dict_metadata": ...]}`` in which every tensor is a
+persistent id, ``("tensor_v3", tid, shape, stride, offset, dtype name, device, is_param,
+requires_grad, storage id, bytes)`` -- shape / stride / offset in elements, the storage's raw
+bytes on its first record only -- or ``("tensor_ref", tid)`` for a tensor written before.
+Loading accepts the older records (``("tensor_v3", shape, dtype, device, bytes)`` and
+``("tensor", shape, dtype, device, bytes, numpy dtype)``) and rebuilds views of shared
+storages.  By default (``weights_only=True``) only the globals Lucid's restricted unpickler
+allows are resolved (builtins containers and scalars, ``collections`` dicts, numpy arrays /
+dtypes / scalars, Lucid's dtype constants); anything else raises ``pickle.UnpicklingError``.
 """
 
 from __future__ import annotations
 
+import io
 import json
 import math
 import mmap
 import os
+import pickle
 import struct
+import warnings
 from typing import Mapping
 
 import numpy as np
@@ -233,3 +248,241 @@ class safe_open:
             fh.seek(self._f.base + start)
             raw = fh.read(end - start)
         return tensor(self._f.decode(name, raw), device=self._device)
+
+
+# ------------------------------------------------------------ Lucid's pickle checkpoints
+
+# Lucid's dtype names (lucid/_dtype.py:85-100) and their numpy storage; bfloat16, which numpy
+# lacks, is read as the upper halves of float32 words.
+_LUCID_DTYPES = {"float16": np.float16, "float32": np.float32, "float64": np.float64, "int8": np.int8,
+                 "int16": np.int16, "int32": np.int32, "int64": np.int64, "bool": np.bool_,
+                 "bool_": np.bool_, "complex64": np.complex64, "complex128": np.complex128}
+_NUMPY_TO_LUCID = {np.dtype(v): k for k, v in _LUCID_DTYPES.items() if k != "bool_"}
+
+# Globals the restricted loader resolves (lucid/serialization/__init__.py:33-80).
+_SAFE_GLOBALS = {
+    ("builtins", n) for n in ("dict", "list", "tuple", "int", "float", "complex", "str", "bool", "bytes",
+                              "bytearray", "set", "slice", "NoneType")
+} | {("collections", n) for n in ("OrderedDict", "Counter", "defaultdict")} | {
+    ("numpy", "ndarray"), ("numpy", "dtype"), ("numpy.core.multiarray", "_reconstruct"),
+    ("numpy.core.multiarray", "scalar"), ("numpy._core.multiarray", "_reconstruct"),
+    ("numpy._core.multiarray", "scalar")}
+
+
+def _lucid_device(t: Tensor) -> str:
+    # Lucid's accelerator is named "metal"; a device tensor saved here loads onto Lucid's GPU
+    return "metal" if t.device == "gpu" else "cpu"
+
+
+class _Pickler(pickle.Pickler):
+    """Each tensor becomes a dense storage of its own (no sharing is claimed)."""
+
+    def __init__(self, file, protocol: int) -> None:
+        super().__init__(file, protocol=protocol)
+        self._emitted: dict[int, int] = {}
+        self._alive: list[Tensor] = []
+
+    def persistent_id(self, obj: object):
+        if not isinstance(obj, Tensor):
+            return None
+        tid = self._emitted.get(id(obj))
+        if tid is not None:
+            return ("tensor_ref", tid)
+        tid = len(self._emitted)
+        self._emitted[id(obj)] = tid
+        self._alive.append(obj)  # ids stay unique while the dump runs
+        arr = _host_array(obj)
+        name = _NUMPY_TO_LUCID.get(arr.dtype)
+        if name is None:
+            raise TypeError(f"save: no Lucid dtype for {arr.dtype}")
+        shape = [int(d) for d in arr.shape]
+        stride, acc = [], 1
+        for d in reversed(shape):
+            stride.append(acc)
+            acc *= max(d, 1)
+        stride.reverse()
+        from lucid_amd.nn.module import Parameter
+
+        return ("tensor_v3", tid, shape, stride, 0, name, _lucid_device(obj), isinstance(obj, Parameter),
+                bool(obj.requires_grad), tid, arr.tobytes())
+
+
+def save(obj: object, f, pickle_module: object = pickle, pickle_protocol: int = 4) -> None:
+    """Write ``obj`` (a state_dict, or any picklable structure holding tensors) as a Lucid
+    checkpoint (lucid/serialization/__init__.py:287-360)."""
+    if pickle_module not in (None, pickle):
+        raise NotImplementedError("save supports only the standard pickle module")
+    container: dict[str, object] = {"_lucid_format": 2, "obj": obj}
+    meta = getattr(obj, "_metadata", None)
+    if meta is not None:
+        container["_state_dict_metadata"] = meta
+    buf = io.BytesIO()
+    _Pickler(buf, pickle_protocol).dump(container)
+    if isinstance(f, (str, bytes, os.PathLike)):
+        with open(os.fspath(f), "wb") as fp:
+            fp.write(buf.getvalue())
+    else:
+        f.write(buf.getvalue())
+
+
+def _target(device_str: str, map_location: object) -> str:
+    from lucid_amd._tensor import normalize_device
+
+    if isinstance(map_location, dict):
+        return normalize_device(map_location.get(device_str, device_str))
+    if isinstance(map_location, str):
+        return normalize_device(map_location)
+    return normalize_device(device_str)
+
+
+def _storage_array(raw: object, name: str, where: str) -> np.ndarray:
+    if name == "bfloat16":
+        if not isinstance(raw, (bytes, bytearray)) or len(raw) % 2:
+            raise pickle.UnpicklingError(f"{where}: bfloat16 storage with an odd byte count")
+        return (np.frombuffer(bytes(raw), np.uint16).astype(np.uint32) << 16).view(np.float32)
+    if name not in _LUCID_DTYPES:
+        raise pickle.UnpicklingError(f"{where}: unknown dtype {name!r}")
+    dt = np.dtype(_LUCID_DTYPES[name])
+    if not isinstance(raw, (bytes, bytearray)) or len(raw) % dt.itemsize:
+        raise pickle.UnpicklingError(f"{where}: storage has no bytes, or a byte count that is not a multiple of "
+                                     f"{name}'s {dt.itemsize}")
+    return np.frombuffer(bytes(raw), dt)
+
+
+def _view(storage: np.ndarray, shape, stride, offset, where: str) -> np.ndarray:
+    shape = [int(d) for d in shape]
+    stride = [int(s) for s in stride]
+    offset = int(offset)
+    if len(shape) != len(stride) or any(d < 0 for d in shape) or any(s < 0 for s in stride) or offset < 0:
+        raise pickle.UnpicklingError(f"{where}: bad view geometry")
+    if math.prod(shape) == 0:
+        return np.zeros(shape, storage.dtype)
+    last = offset + sum((d - 1) * s for d, s in zip(shape, stride))
+    if last >= storage.size:
+        raise pickle.UnpicklingError(f"{where}: view reaches element {last} of a storage of {storage.size}")
+    it = storage.itemsize
+    return np.lib.stride_tricks.as_strided(storage[offset:], shape=shape, strides=[s * it for s in stride]).copy()
+
+
+class _Unpickler(pickle.Unpickler):
+    def __init__(self, file, map_location: object, safe: bool, **kw) -> None:
+        super().__init__(file, **kw)
+        self._map = map_location
+        self._safe = safe
+        self._storages: dict[int, np.ndarray] = {}
+        self._tensors: dict[int, Tensor] = {}
+
+    def find_class(self, module: str, name: str):
+        if module == "lucid._dtype" and name in _LUCID_DTYPES:
+            return np.dtype(_LUCID_DTYPES[name])
+        if self._safe and (module, name) not in _SAFE_GLOBALS:
+            raise pickle.UnpicklingError(f"weights_only=True: refusing to deserialize '{module}.{name}'. "
+                                         "Pass weights_only=False to allow arbitrary objects "
+                                         "(potential security risk).")
+        return super().find_class(module, name)
+
+    def _make(self, arr: np.ndarray, device_str: str, is_param: bool = False, requires_grad: bool = False) -> Tensor:
+        t = Tensor._from_numpy(arr, _target(device_str, self._map))
+        if is_param:
+            from lucid_amd.nn.module import Parameter
+
+            t = Parameter(t, bool(requires_grad))
+        t.requires_grad = bool(requires_grad)
+        if callable(self._map) and not isinstance(self._map, (str, dict)):
+            t = self._map(t, device_str)
+        return t
+
+    def persistent_load(self, pid: object):
+        if isinstance(pid, tuple) and pid:
+            tag = pid[0]
+            if tag == "tensor_ref" and len(pid) == 2:
+                tid = int(pid[1])
+                if tid not in self._tensors:
+                    raise pickle.UnpicklingError(f"reference to tensor record {tid} before it")
+                return self._tensors[tid]
+            if tag == "tensor_v3" and len(pid) == 11:
+                _, tid, shape, stride, offset, name, dev, is_param, rg, sid, raw = pid
+                where = f"tensor record {tid}"
+                base = self._storages.get(int(sid))
+                if base is None:
+                    base = _storage_array(raw, name, where)
+                    self._storages[int(sid)] = base
+                t = self._make(_view(base, shape, stride, offset, where), dev, is_param, rg)
+                self._tensors[int(tid)] = t
+                return t
+            if tag == "tensor_v3" and len(pid) == 5:
+                _, shape, name, dev, raw = pid
+                arr = _storage_array(raw, name, "tensor record")
+                return self._make(arr.reshape([int(d) for d in shape]), dev)
+            if tag == "tensor" and len(pid) == 6:
+                _, shape, name, dev, raw, _np = pid
+                arr = _storage_array(raw, name, "tensor record")
+                return self._make(arr.reshape([int(d) for d in shape]), dev)
+        raise pickle.UnpicklingError(f"Unknown persistent id: {pid}")
+
+
+def _no_frozenset(obj: object, seen: set[int]) -> None:
+    if id(obj) in seen:
+        return
+    if isinstance(obj, frozenset):
+        raise pickle.UnpicklingError("weights_only=True: refusing to deserialize 'builtins.frozenset'.")
+    if isinstance(obj, dict):
+        seen.add(id(obj))
+        for k, v in obj.items():
+            _no_frozenset(k, seen)
+            _no_frozenset(v, seen)
+    elif isinstance(obj, (list, tuple, set)):
+        seen.add(id(obj))
+        for v in obj:
+            _no_frozenset(v, seen)
+
+
+def load(f, map_location: object = None, pickle_module: object = None, *, weights_only: bool | None = True,
+         mmap: bool | None = None, **pickle_load_args):
+    """Read a checkpoint written by ``save`` (or by Lucid's ``lucid.save``), or a
+    ``.safetensors`` file (lucid/serialization/__init__.py:361-456).
+
+    ``map_location``: None (each tensor where it was saved: "metal" / "gpu" on the GPU), a
+    device name for every tensor, a dict from saved device name to target, or a callable
+    ``fn(tensor, saved_device) -> tensor``."""
+    if pickle_module not in (None, pickle):
+        raise NotImplementedError("load supports only the standard pickle module")
+    if mmap is True:
+        raise NotImplementedError("load does not support mmap=True")
+    safe = True if weights_only is None else bool(weights_only)
+    if safe and pickle_load_args:
+        raise RuntimeError("Cannot use ``pickle_load_args`` with ``weights_only=True``")
+    if map_location is not None and not (isinstance(map_location, (str, dict)) or callable(map_location)):
+        raise TypeError("map_location must be a device name, a dict of them or a callable, got "
+                        f"{type(map_location).__name__}")
+    if isinstance(f, (str, bytes, os.PathLike)):
+        path = os.fspath(f)
+        path = path.decode() if isinstance(path, bytes) else path
+        if path.endswith(".safetensors"):
+            out = load_safetensors(path)
+            if map_location is None:
+                return out
+            return {k: Tensor._from_numpy(v.numpy(), _target(v.device, map_location)) for k, v in out.items()}
+        with open(path, "rb") as fp:
+            data = fp.read()
+    else:
+        data = f.read()
+    if not safe:
+        warnings.warn("load() with weights_only=False allows arbitrary object deserialization which may "
+                      "execute untrusted code.", UserWarning, stacklevel=2)
+    container = _Unpickler(io.BytesIO(data), map_location, safe, **pickle_load_args).load()
+    if safe:
+        _no_frozenset(container, set())
+    if not isinstance(container, dict) or container.get("_lucid_format") not in (1, 2):
+        raise RuntimeError("File is not a valid Lucid checkpoint")
+    obj = container["obj"]
+    meta = container.get("_state_dict_metadata")
+    if meta is not None and isinstance(obj, dict):
+        try:
+            obj._metadata = meta
+        except AttributeError:
+            from collections import OrderedDict
+
+            obj = OrderedDict(obj)
+            obj._metadata = meta
+    return obj

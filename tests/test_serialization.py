@@ -117,3 +117,188 @@ def test_quantized_model_checkpoint_round_trip(gpu, tmp_path):
     fresh.load_state_dict(S.load_safetensors(str(path), device="gpu"))
     x = gpu.tensor(rng.standard_normal((2, 3, 16, 16)).astype(np.float32), device="gpu")
     np.testing.assert_array_equal(fresh(x).quant_source.codes.numpy(), q(x).quant_source.codes.numpy())
+
+
+# ------------------------------------------------ Lucid's pickle checkpoints (save / load)
+#
+# Pinned against the record layout of lucid/serialization/__init__.py:113-152 (what Lucid's
+# pickler writes) and :186-227 (what its loader accepts): the files are read back here by a
+# bare pickle.Unpickler that only records the persistent ids, and files in Lucid's layout
+# with shared storages and strided views -- which this module's writer never emits -- are
+# built by hand and loaded.
+
+
+class _Recorder(__import__("pickle").Unpickler):
+    def __init__(self, f):
+        super().__init__(f)
+        self.pids = []
+
+    def persistent_load(self, pid):
+        self.pids.append(pid)
+        return ("PID", len(self.pids) - 1)
+
+
+def test_lucid_save_records_and_round_trip(tmp_path):
+    import io
+    import pickle
+    from collections import OrderedDict
+
+    import lucid_amd
+
+    sd = OrderedDict(_sd())
+    sd["again"] = sd["bias"]                      # the same tensor twice -> tensor_ref
+    sd["extra"] = {"step": 3, "names": ["a", "b"], "lr": 0.5}
+    path = tmp_path / "m.lucid"
+    lucid_amd.save(sd, str(path))
+    rec = _Recorder(io.BytesIO(path.read_bytes()))
+    container = rec.load()
+    assert container["_lucid_format"] == 2 and list(container["obj"]) == list(sd)
+    v3 = [p for p in rec.pids if p[0] == "tensor_v3"]
+    refs = [p for p in rec.pids if p[0] == "tensor_ref"]
+    assert len(v3) == len(_sd()) and refs == [("tensor_ref", 2)]
+    for tid, (name, t) in enumerate(list(_sd().items())):
+        p = v3[tid]
+        arr = t.numpy()
+        assert len(p) == 11 and p[1] == tid and p[9] == tid
+        assert p[2] == list(arr.shape) and p[4] == 0 and p[6] == "cpu" and p[7] is False and p[8] is False
+        assert p[3] == [int(s) // arr.itemsize for s in arr.strides] or arr.ndim == 0
+        assert p[5] == {"bool": "bool"}.get(arr.dtype.name, arr.dtype.name)
+        assert p[10] == arr.tobytes()
+    back = lucid_amd.load(str(path))
+    assert list(back) == list(sd) and back["extra"] == sd["extra"]
+    assert back["again"] is back["bias"]
+    for k, t in _sd().items():
+        got = back[k].numpy()
+        assert got.dtype == t.numpy().dtype and got.shape == t.numpy().shape
+        np.testing.assert_array_equal(got, t.numpy())
+    # state_dict metadata round-trips (format v2)
+    sd2 = OrderedDict(w=tensor(np.ones(2, np.float32)))
+    sd2._metadata = {"": {"version": 1}}
+    buf = io.BytesIO()
+    S.save(sd2, buf)
+    assert S.load(io.BytesIO(buf.getvalue()))._metadata == {"": {"version": 1}}
+    assert pickle.loads  # the module is the standard one
+
+
+def _lucid_file(obj, records):
+    """A checkpoint in Lucid's layout: ``records`` maps a placeholder string inside ``obj`` to the
+    persistent id Lucid's pickler would emit for it."""
+    import io
+    import pickle
+
+    class P(pickle.Pickler):
+        def persistent_id(self, o):
+            return records.get(o) if isinstance(o, str) else None
+
+    buf = io.BytesIO()
+    P(buf, protocol=4).dump({"_lucid_format": 2, "obj": obj})
+    return buf.getvalue()
+
+
+def _ph(rec):
+    """Placeholders "@K" for the records (dict keys stay plain names)."""
+    return {k.lower(): "@" + k for k in rec}, {"@" + k: v for k, v in rec.items()}
+
+
+def test_lucid_load_shared_storage_views_and_old_records():
+    import io
+
+    base = np.arange(24, dtype=np.float32)
+    raw = base.tobytes()
+    rec = {
+        "A": ("tensor_v3", 0, [4, 6], [6, 1], 0, "float32", "cpu", True, True, 7, raw),
+        "AT": ("tensor_v3", 1, [6, 4], [1, 6], 0, "float32", "cpu", False, False, 7, None),   # transpose view
+        "ROW": ("tensor_v3", 2, [3], [2], 13, "float32", "cpu", False, False, 7, None),      # strided slice
+        "REF": ("tensor_ref", 1),
+        "OLD5": ("tensor_v3", [2, 2], "int16", "cpu", np.array([1, -2, 3, -4], np.int16).tobytes()),
+        "OLD6": ("tensor", [3], "int8", "cpu", np.array([5, -6, 7], np.int8).tobytes(), "int8"),
+        "BF": ("tensor_v3", 3, [2], [1], 0, "bfloat16", "cpu", False, False, 8,
+               np.array([0x3FC0, 0xC040], np.uint16).tobytes()),
+    }
+    out = S.load(io.BytesIO(_lucid_file(*_ph(rec))))
+    out = {k.upper(): v for k, v in out.items()}
+    from lucid_amd.nn.module import Parameter
+
+    A = base.reshape(4, 6)
+    assert isinstance(out["A"], Parameter) and out["A"].requires_grad
+    np.testing.assert_array_equal(out["A"].numpy(), A)
+    np.testing.assert_array_equal(out["AT"].numpy(), A.T)
+    np.testing.assert_array_equal(out["ROW"].numpy(), base[13:18:2])
+    assert out["REF"] is out["AT"]
+    np.testing.assert_array_equal(out["OLD5"].numpy(), [[1, -2], [3, -4]])
+    np.testing.assert_array_equal(out["OLD6"].numpy(), [5, -6, 7])
+    np.testing.assert_array_equal(out["BF"].numpy(), np.array([1.5, -3.0], np.float32))
+
+
+def test_lucid_load_refuses_unsafe_and_damaged_files():
+    import io
+    import os
+    import pickle
+
+    class Evil:
+        def __reduce__(self):
+            return (os.getcwd, ())
+
+    buf = io.BytesIO()
+    pickle.dump({"_lucid_format": 2, "obj": Evil()}, buf, protocol=4)
+    with pytest.raises(pickle.UnpicklingError, match="refusing"):
+        S.load(io.BytesIO(buf.getvalue()))
+    with pytest.warns(UserWarning):
+        assert S.load(io.BytesIO(buf.getvalue()), weights_only=False) == os.getcwd()
+    buf = io.BytesIO()
+    pickle.dump({"_lucid_format": 2, "obj": frozenset({1})}, buf, protocol=4)
+    with pytest.raises(pickle.UnpicklingError, match="frozenset"):
+        S.load(io.BytesIO(buf.getvalue()))
+    bad = {"X": ("tensor_v3", 0, [2], [1], 0, "float32", "cpu", False, False, 0, b"\0" * 7)}
+    with pytest.raises(pickle.UnpicklingError, match="multiple"):
+        S.load(io.BytesIO(_lucid_file(*_ph(bad))))
+    far = {"X": ("tensor_v3", 0, [3], [4], 0, "float32", "cpu", False, False, 0, b"\0" * 16)}
+    with pytest.raises(pickle.UnpicklingError, match="reaches"):
+        S.load(io.BytesIO(_lucid_file(*_ph(far))))
+    buf = io.BytesIO()
+    pickle.dump({"not": "lucid"}, buf, protocol=4)
+    with pytest.raises(RuntimeError, match="not a valid Lucid checkpoint"):
+        S.load(io.BytesIO(buf.getvalue()))
+    with pytest.raises(RuntimeError, match="pickle_load_args"):
+        S.load(io.BytesIO(buf.getvalue()), encoding="latin1")
+
+
+def test_lucid_load_dispatches_safetensors_and_maps_devices(tmp_path):
+    path = tmp_path / "m.safetensors"
+    S.save_safetensors(_sd(), str(path))
+    out = S.load(str(path))
+    np.testing.assert_array_equal(out["weight_int8"].numpy(), _sd()["weight_int8"].numpy())
+    import io
+
+    rec = {"G": ("tensor_v3", 0, [2], [1], 0, "int32", "metal", False, False, 0, np.array([1, 2], np.int32).tobytes())}
+    out = S.load(io.BytesIO(_lucid_file(*_ph(rec))), map_location={"metal": "cpu"})
+    assert out["g"].device == "cpu"
+    np.testing.assert_array_equal(out["g"].numpy(), [1, 2])
+    out = S.load(io.BytesIO(_lucid_file(*_ph(rec))), map_location="cpu")
+    assert out["g"].device == "cpu"
+    seen = []
+    rec_c = {"G": rec["G"][:6] + ("cpu",) + rec["G"][7:]}
+    out = S.load(io.BytesIO(_lucid_file(*_ph(rec_c))), map_location=lambda t, d: seen.append(d) or t)
+    assert seen == ["cpu"] and out["g"].device == "cpu"
+
+
+@pytest.mark.gpu
+def test_lucid_checkpoint_of_device_tensors(gpu, tmp_path):
+    """Device tensors are recorded as Lucid's accelerator ("metal") and load back onto the GPU."""
+    import io
+
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized.dynamic as nnqd
+
+    m = nnqd.Linear.from_float(nn.Linear(16, 8).to("gpu")) if hasattr(nnqd, "Linear") else None
+    sd = m.state_dict() if m is not None else {"w": gpu.tensor(np.ones(3, np.float32), device="gpu")}
+    buf = io.BytesIO()
+    S.save(sd, buf)
+    rec = _Recorder(io.BytesIO(buf.getvalue()))
+    rec.load()
+    assert {p[6] for p in rec.pids if p[0] == "tensor_v3"} <= {"metal", "cpu"}
+    back = S.load(io.BytesIO(buf.getvalue()))
+    for k, v in sd.items():
+        if hasattr(v, "numpy"):
+            assert back[k].device == v.device
+            np.testing.assert_array_equal(back[k].numpy(), v.numpy())
