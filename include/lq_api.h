@@ -280,8 +280,9 @@ int lq_row_sums_i8(const int8_t* d_X, int64_t ld, int64_t rows, int64_t K, int32
  * d_w_zero_point / d_bias may be NULL.  Float32 accumulation (tolerance parity: the float
  * GEMM's summation order is the reference's own).  Any M; tuned for M <= 16.  With
  * lq_gemv_w8_workspace_size(M, N, K) bytes of device workspace (16-byte aligned; 0 for M <= 2)
- * float32 activations are split into fp16 halves once per call instead of once per
- * workgroup; without it (NULL) the call still runs, with identical results. */
+ * float32 activations of M > 8 rows are split into fp16 halves once per call instead of once
+ * per workgroup (for fewer rows the in-workgroup split is faster and the workspace is not
+ * touched); without it (NULL) the call still runs, with identical results. */
 size_t lq_gemv_w8_workspace_size(int64_t M, int64_t N, int64_t K);
 int lq_gemv_w8(const void* d_x, int x_dtype, int64_t ldx, const int8_t* d_W, int64_t ldw,
                const float* d_w_scale, const float* d_w_zero_point, const float* d_bias,
