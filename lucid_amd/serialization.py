@@ -486,3 +486,142 @@ def load(f, map_location: object = None, pickle_module: object = None, *, weight
             obj = OrderedDict(obj)
             obj._metadata = meta
     return obj
+
+
+# ------------------------------------------------------------------ sharded checkpoints
+
+
+def _as_directory(path: object, name: str) -> str:
+    if isinstance(path, bytes):
+        return path.decode()
+    if isinstance(path, str):
+        return path
+    if isinstance(path, os.PathLike):
+        return str(os.fspath(path))
+    raise TypeError(f"{name}() expects a directory path as str, bytes or os.PathLike, got {type(path).__name__}")
+
+
+def _tensors_in(v: object, out: dict[int, Tensor], seen: set[int]) -> None:
+    if id(v) in seen:
+        return
+    seen.add(id(v))
+    if isinstance(v, Tensor):
+        out[id(v)] = v
+    elif isinstance(v, dict):
+        for k, x in v.items():
+            _tensors_in(k, out, seen)
+            _tensors_in(x, out, seen)
+    elif isinstance(v, (list, tuple, set, frozenset)):
+        for x in v:
+            _tensors_in(x, out, seen)
+
+
+def _shard_groups(obj: dict) -> list[tuple[list[str], int]]:
+    """Keys grouped by the tensors they reach (a tensor reached from two keys -- a tied weight --
+    joins them), each group with the bytes of its distinct tensors, in first-key order
+    (lucid/serialization/_storage_plan.py:455-482; tensors here share memory only by identity)."""
+    parent: dict[str, str] = {}
+
+    def find(k: str) -> str:
+        while parent[k] != k:
+            parent[k] = parent[parent[k]]
+            k = parent[k]
+        return k
+
+    owner: dict[int, str] = {}
+    reach: dict[str, dict[int, Tensor]] = {}
+    for k, v in obj.items():
+        parent[k] = k
+        reach[k] = {}
+        _tensors_in(v, reach[k], set())
+        for tid in reach[k]:
+            if tid in owner:
+                parent[find(k)] = find(owner[tid])
+            else:
+                owner[tid] = k
+    groups: dict[str, list[str]] = {}
+    for k in obj:
+        groups.setdefault(find(k), []).append(k)
+    out = []
+    for keys in groups.values():
+        distinct: dict[int, Tensor] = {}
+        for k in keys:
+            distinct.update(reach[k])
+        out.append((keys, sum(t.numel() * np.dtype(t.dtype).itemsize for t in distinct.values())))
+    return out
+
+
+def save_sharded(obj: object, path, *, shard_size_mb: float = 1024.0, pickle_protocol: int = 4) -> None:
+    """A checkpoint directory of ``shard-XXXXX-of-YYYYY.lucid`` files (each a ``save`` of part of
+    the state dict, keys first-fit up to ``shard_size_mb``, tied keys kept together) and an
+    ``index.json`` naming each shard's keys (lucid/serialization/__init__.py:646-744)."""
+    d = _as_directory(path, "save_sharded")
+    os.makedirs(d, exist_ok=True)
+    if not isinstance(obj, dict):
+        fname = "shard-00000-of-00001.lucid"
+        save(obj, os.path.join(d, fname), pickle_protocol=pickle_protocol)
+        with open(os.path.join(d, "index.json"), "w", encoding="utf-8") as fp:
+            json.dump({"_lucid_sharded": 1, "shards": [{"file": fname, "keys": None}]}, fp, indent=2)
+        return
+    limit = int(shard_size_mb * 1024 * 1024)
+    shards: list[dict] = []
+    cur: dict = {}
+    cur_bytes = 0
+    for keys, size in _shard_groups(obj):
+        if cur and cur_bytes + size > limit:
+            shards.append(cur)
+            cur, cur_bytes = {}, 0
+        for k in keys:
+            cur[k] = obj[k]
+        cur_bytes += size
+    if cur or not shards:
+        shards.append(cur)
+    entries = []
+    for i, part in enumerate(shards):
+        fname = f"shard-{i:05d}-of-{len(shards):05d}.lucid"
+        save(part, os.path.join(d, fname), pickle_protocol=pickle_protocol)
+        entries.append({"file": fname, "keys": list(part)})
+    index: dict[str, object] = {"_lucid_sharded": 1, "shards": entries}
+    if [k for part in shards for k in part] != list(obj):
+        index["key_order"] = list(obj)
+    meta = getattr(obj, "_metadata", None)
+    if meta is not None:
+        try:
+            json.dumps(meta)
+            index["_state_dict_metadata"] = meta
+        except (TypeError, ValueError):
+            pass
+    with open(os.path.join(d, "index.json"), "w", encoding="utf-8") as fp:
+        json.dump(index, fp, indent=2)
+
+
+def load_sharded(path, *, map_location: object = None, weights_only: bool = True) -> object:
+    """Read a directory written by ``save_sharded`` (or Lucid's) into one ordered state dict
+    (lucid/serialization/__init__.py:746-830)."""
+    from collections import OrderedDict
+
+    d = _as_directory(path, "load_sharded")
+    index_path = os.path.join(d, "index.json")
+    with open(index_path, encoding="utf-8") as fp:
+        index = json.load(fp)
+    if not isinstance(index, dict) or index.get("_lucid_sharded") != 1:
+        raise RuntimeError(f"{index_path!r} is not a valid Lucid sharded checkpoint index")
+    entries = index["shards"]
+    for e in entries:  # shard files stay inside the directory
+        f = str(e["file"])
+        if os.path.basename(f) != f or f in ("", ".", ".."):
+            raise RuntimeError(f"{index_path!r}: shard file {f!r} is not a plain file name")
+    if len(entries) == 1 and entries[0].get("keys") is None:
+        return load(os.path.join(d, str(entries[0]["file"])), map_location=map_location, weights_only=weights_only)
+    result: OrderedDict = OrderedDict()
+    for e in entries:
+        part = load(os.path.join(d, str(e["file"])), map_location=map_location, weights_only=weights_only)
+        if isinstance(part, dict):
+            result.update(part)
+    order = index.get("key_order")
+    if isinstance(order, list) and set(order) == set(result):
+        result = OrderedDict((k, result[k]) for k in order)
+    meta = index.get("_state_dict_metadata")
+    if isinstance(meta, dict):
+        result._metadata = meta
+    return result

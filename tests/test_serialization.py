@@ -302,3 +302,42 @@ def test_lucid_checkpoint_of_device_tensors(gpu, tmp_path):
         if hasattr(v, "numpy"):
             assert back[k].device == v.device
             np.testing.assert_array_equal(back[k].numpy(), v.numpy())
+
+
+def test_sharded_checkpoints(tmp_path):
+    """save_sharded / load_sharded (lucid/serialization/__init__.py:646-830): first-fit shards
+    under the cap, a tensor over the cap alone, tied keys kept in one shard with the key order
+    restored, the index layout, and the single-shard form of a non-dict object."""
+    import json
+    from collections import OrderedDict
+
+    big = tensor(np.arange(300_000, dtype=np.float32))           # 1.14 MiB, over a 1 MiB cap
+    w = tensor(np.ones((100, 100), np.float32))                   # 40 KB
+    sd = OrderedDict([("a", tensor(np.arange(10, dtype=np.int8))), ("big", big), ("w", w),
+                      ("c", tensor(np.float32(2.5))), ("tied", w)])
+    sd._metadata = {"": {"version": 2}}
+    d = tmp_path / "ckpt"
+    S.save_sharded(sd, d, shard_size_mb=0.5)
+    index = json.loads((d / "index.json").read_text())
+    assert index["_lucid_sharded"] == 1 and index["_state_dict_metadata"] == {"": {"version": 2}}
+    files = [e["file"] for e in index["shards"]]
+    assert files == [f"shard-{i:05d}-of-{len(files):05d}.lucid" for i in range(len(files))]
+    keysets = [e["keys"] for e in index["shards"]]
+    assert ["big"] in keysets                                    # over the cap: a shard of its own
+    assert any("w" in ks and "tied" in ks for ks in keysets)     # tied keys together
+    assert index["key_order"] == list(sd)
+    back = S.load_sharded(d)
+    assert list(back) == list(sd) and back._metadata == {"": {"version": 2}}
+    assert back["w"] is back["tied"]
+    for k, v in sd.items():
+        np.testing.assert_array_equal(back[k].numpy(), v.numpy())
+    S.save_sharded([1, 2, big], tmp_path / "list")
+    out = S.load_sharded(tmp_path / "list")
+    assert out[:2] == [1, 2] and np.array_equal(out[2].numpy(), big.numpy())
+    (tmp_path / "bad").mkdir()
+    (tmp_path / "bad" / "index.json").write_text(json.dumps({"_lucid_sharded": 1, "shards": [
+        {"file": "../x.lucid", "keys": ["a"]}]}))
+    with pytest.raises(RuntimeError, match="plain file name"):
+        S.load_sharded(tmp_path / "bad")
+    with pytest.raises(TypeError):
+        S.save_sharded(sd, big)
