@@ -779,9 +779,9 @@ __global__ __launch_bounds__(256) void group_dequantize_kernel(const uint32_t* _
 // The group scale / bias change along the summed axis n, so there is no factoring of the
 // sums as in the transpose=true kernel: each weight tile is dequantized into LDS exactly as
 // group_dequantize_kernel writes it, fl32(fl32(c s) + b), and the kernel is a float32 tiled
-// GEMM over it (64 x 64 outputs per 256-thread workgroup, 4 x 4 per thread, n in steps of 16,
-// fused multiply-adds in n order).
-constexpr int NT_T = 64, NT_K = 16;
+// GEMM over it (128 x 128 outputs per 256-thread workgroup, 8 x 8 per thread, n in steps of
+// 16, fused multiply-adds in n order).
+constexpr int NT_T = 128, NT_K = 16, NT_R = NT_T / 16;
 
 template <int BITS, bool XF32>
 __global__ __launch_bounds__(256) void group_matmul_nt_kernel(const void* __restrict__ xv, int64_t ldx,
@@ -801,7 +801,7 @@ __global__ __launch_bounds__(256) void group_matmul_nt_kernel(const void* __rest
     const int64_t KT = (K + NT_T - 1) / NT_T, MT = (M + NT_T - 1) / NT_T;
     for (int64_t tile = blockIdx.x; tile < KT * MT; tile += gridDim.x) {
         const int64_t k0 = (tile % KT) * NT_T, m0 = (tile / KT) * NT_T;
-        float acc[4][4] = {};
+        float acc[NT_R][NT_R] = {};
         for (int64_t n0 = 0; n0 < N; n0 += NT_K) {
             for (int e = threadIdx.x; e < NT_T * NT_K; e += 256) {
                 const int r = e / NT_K, kk = e % NT_K;
@@ -837,24 +837,24 @@ __global__ __launch_bounds__(256) void group_matmul_nt_kernel(const void* __rest
             __syncthreads();
 #pragma unroll
             for (int kk = 0; kk < NT_K; ++kk) {
-                float xr[4], wr[4];
+                float xr[NT_R], wr[NT_R];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) xr[i] = xs[kk][ty + 16 * i];
+                for (int i = 0; i < NT_R; ++i) xr[i] = xs[kk][ty + 16 * i];
 #pragma unroll
-                for (int j = 0; j < 4; ++j) wr[j] = ws[kk][tx + 16 * j];
+                for (int j = 0; j < NT_R; ++j) wr[j] = ws[kk][tx + 16 * j];
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
+                for (int i = 0; i < NT_R; ++i)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) acc[i][j] = fmaf(xr[i], wr[j], acc[i][j]);
+                    for (int j = 0; j < NT_R; ++j) acc[i][j] = fmaf(xr[i], wr[j], acc[i][j]);
             }
             __syncthreads();
         }
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NT_R; ++i) {
             const int64_t gm = m0 + ty + 16 * i;
             if (gm >= M) continue;
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
+            for (int j = 0; j < NT_R; ++j) {
                 const int64_t gk = k0 + tx + 16 * j;
                 if (gk >= K) continue;
                 float v = acc[i][j];
