@@ -794,16 +794,24 @@ __global__ __launch_bounds__(256) void group_matmul_nt_kernel(const void* __rest
     constexpr int PER = 32 / BITS;
     constexpr uint32_t L = (1u << BITS) - 1u;
     constexpr int WPR = NT_T / PER;  // packed words per tile row
-    __shared__ float xs[NT_K][NT_T + 1];
-    __shared__ float ws[NT_K][NT_T];
+    __shared__ __attribute__((aligned(16))) float xs[NT_K][NT_T + 4];  // row stride 16-byte aligned
+    __shared__ __attribute__((aligned(16))) float ws[NT_K][NT_T];
     const int tx = threadIdx.x % 16, ty = threadIdx.x / 16;
     const int64_t G = K / gs, words_per_row = K / PER;
     const int64_t KT = (K + NT_T - 1) / NT_T, MT = (M + NT_T - 1) / NT_T;
     for (int64_t tile = blockIdx.x; tile < KT * MT; tile += gridDim.x) {
         const int64_t k0 = (tile % KT) * NT_T, m0 = (tile / KT) * NT_T;
         float acc[NT_R][NT_R] = {};
-        for (int64_t n0 = 0; n0 < N; n0 += NT_K) {
-            for (int e = threadIdx.x; e < NT_T * NT_K; e += 256) {
+        // The next n-tile's activations and packed words (with their group scale / bias) are
+        // loaded into registers while this tile's FMAs run, then dequantized into LDS.
+        constexpr int XPT = NT_T * NT_K / 256, WPT = (NT_K * WPR + 255) / 256;
+        float xq[XPT];
+        uint32_t wq[WPT];
+        float sq[WPT], bq[WPT];
+        auto fetch = [&](int64_t n0) __attribute__((always_inline)) {
+#pragma unroll
+            for (int u = 0; u < XPT; ++u) {
+                const int e = threadIdx.x + 256 * u;
                 const int r = e / NT_K, kk = e % NT_K;
                 const int64_t gm = m0 + r, gn = n0 + kk;
                 float v = 0.0f;
@@ -811,37 +819,59 @@ __global__ __launch_bounds__(256) void group_matmul_nt_kernel(const void* __rest
                     if constexpr (XF32) v = static_cast<const float*>(xv)[gm * ldx + gn];
                     else v = (float)static_cast<const _Float16*>(xv)[gm * ldx + gn];
                 }
-                xs[kk][r] = v;
+                xq[u] = v;
             }
-            for (int e = threadIdx.x; e < NT_K * WPR; e += 256) {
+#pragma unroll
+            for (int u = 0; u < WPT; ++u) {
+                const int e = threadIdx.x + 256 * u;
                 const int r = e / WPR, wc = e % WPR;
                 const int64_t gn = n0 + r, gk = k0 + (int64_t)wc * PER;
-                float out[PER];
-                if (gn < N && gk < K) {  // K is a multiple of the group size, so whole words
-                    const uint32_t word = packed[gn * words_per_row + gk / PER];
+                wq[u] = 0u;
+                sq[u] = 0.0f;
+                bq[u] = 0.0f;
+                if (e < NT_K * WPR && gn < N && gk < K) {  // K is a multiple of the group size: whole words
+                    wq[u] = packed[gn * words_per_row + gk / PER];
                     const int64_t gi = gn * G + gk / gs;
-                    const float s = scales[gi];
-                    const float b = biases ? biases[gi] : 0.0f;
-#pragma unroll
-                    for (int q = 0; q < PER; ++q) {
-                        const float t = (float)((word >> (q * BITS)) & L) * s;
-                        out[q] = biases ? t + b : t;
-                    }
-                } else {
-#pragma unroll
-                    for (int q = 0; q < PER; ++q) out[q] = 0.0f;
+                    sq[u] = scales[gi];
+                    bq[u] = biases ? biases[gi] : 0.0f;
                 }
+            }
+        };
+        fetch(0);
+        for (int64_t n0 = 0; n0 < N; n0 += NT_K) {
 #pragma unroll
-                for (int q = 0; q < PER; ++q) ws[r][wc * PER + q] = out[q];
+            for (int u = 0; u < XPT; ++u) {
+                const int e = threadIdx.x + 256 * u;
+                xs[e % NT_K][e / NT_K] = xq[u];
+            }
+#pragma unroll
+            for (int u = 0; u < WPT; ++u) {
+                const int e = threadIdx.x + 256 * u;
+                if (e < NT_K * WPR) {
+                    const int r = e / WPR, wc = e % WPR;
+#pragma unroll
+                    for (int q = 0; q < PER; ++q) {  // w_hat = fl32(fl32(c s) + b); 0 past N / K (s = 0)
+                        const float t = (float)((wq[u] >> (q * BITS)) & L) * sq[u];
+                        ws[r][wc * PER + q] = biases ? t + bq[u] : t;
+                    }
+                }
             }
             __syncthreads();
+            if (n0 + NT_K < N) fetch(n0 + NT_K);
 #pragma unroll
             for (int kk = 0; kk < NT_K; ++kk) {
+                // this thread's NT_R consecutive rows and columns: 16-byte LDS reads
                 float xr[NT_R], wr[NT_R];
 #pragma unroll
-                for (int i = 0; i < NT_R; ++i) xr[i] = xs[kk][ty + 16 * i];
+                for (int i = 0; i < NT_R; i += 4) {
+                    const vf4 v = *reinterpret_cast<const vf4*>(&xs[kk][ty * NT_R + i]);
+                    xr[i] = v[0]; xr[i + 1] = v[1]; xr[i + 2] = v[2]; xr[i + 3] = v[3];
+                }
 #pragma unroll
-                for (int j = 0; j < NT_R; ++j) wr[j] = ws[kk][tx + 16 * j];
+                for (int j = 0; j < NT_R; j += 4) {
+                    const vf4 v = *reinterpret_cast<const vf4*>(&ws[kk][tx * NT_R + j]);
+                    wr[j] = v[0]; wr[j + 1] = v[1]; wr[j + 2] = v[2]; wr[j + 3] = v[3];
+                }
 #pragma unroll
                 for (int i = 0; i < NT_R; ++i)
 #pragma unroll
@@ -851,11 +881,11 @@ __global__ __launch_bounds__(256) void group_matmul_nt_kernel(const void* __rest
         }
 #pragma unroll
         for (int i = 0; i < NT_R; ++i) {
-            const int64_t gm = m0 + ty + 16 * i;
+            const int64_t gm = m0 + ty * NT_R + i;
             if (gm >= M) continue;
 #pragma unroll
             for (int j = 0; j < NT_R; ++j) {
-                const int64_t gk = k0 + tx + 16 * j;
+                const int64_t gk = k0 + tx * NT_R + j;
                 if (gk >= K) continue;
                 float v = acc[i][j];
                 if (bias) v = v + bias[gk];
