@@ -279,7 +279,9 @@ class Gemm:
 def gemm_line(L, C, timer, gtimer, M, N, K, out_kind, steps, warmup):
     g = Gemm(L, C, M, N, K, out_kind, seed=M + N + K)
     if g.packed:  # decode shapes are launch-bound from Python: graph replay
-        ms = gtimer.time_ms(g.calls, max(steps // len(g.calls), 2), 1)
+        # at least 10 replays after 2 warm-up passes: the first replays of a fresh graph run
+        # up to 2x slow, which 2 replays over a dozen weight copies did not average out
+        ms = gtimer.time_ms(g.calls, max(steps // len(g.calls), 10), 2)
     else:
         ms = timer.time_ms(g.run, steps, warmup)
     tops = g.ops / (ms * 1e-3) / 1e12
