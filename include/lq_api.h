@@ -59,7 +59,9 @@ enum {
     LQ_F16 = 5,   /* IEEE half */
     LQ_F32 = 6,   /* IEEE single */
     LQ_U8S8 = 7,  /* an unsigned-grid code c stored as int8 (c - 128): MFMA operand form */
-    LQ_I64 = 8    /* int64 (indices and offsets) */
+    LQ_I64 = 8,   /* int64 (indices and offsets) */
+    LQ_I8_QPAIR = 9  /* table lookups only: int8 rows whose d_scale holds interleaved float32
+                      * {scale, zero point} pairs per row (d_zero_point unused) */
 };
 
 /* ---- runtime -------------------------------------------------------------- */
@@ -364,8 +366,9 @@ int lq_qact(int op, const void* d_x, int x_type, const float* d_x_scale, const f
 /* Pooling modes of lq_embedding_bag (the engine's encoding, lucid/nn/functional/sparse.py:214). */
 enum { LQ_BAG_SUM = 0, LQ_BAG_MEAN = 1, LQ_BAG_MAX = 2 };
 /* out[i, :] = row idx[i] of a [rows, D] table: int8 codes (table_type LQ_I8) dequantized per row
- * as fl32(fl32(float(c) - z[r]) * s[r]) (d_zero_point NULL = 0), or float32 entries (LQ_F32,
- * d_scale unused).  Indices LQ_I32 or LQ_I64; one outside [0, rows) gives a NaN row (no read).
+ * as fl32(fl32(float(c) - z[r]) * s[r]) (d_zero_point NULL = 0), the same with the row's
+ * {s, z} read as one pair from d_scale (LQ_I8_QPAIR: one random cache line per lookup fewer),
+ * or float32 entries (LQ_F32, d_scale unused).  Indices LQ_I32 or LQ_I64; one outside [0, rows) gives a NaN row (no read).
  * Replaces dequantize(table, ch_axis=0) + F.embedding of nnq.Embedding.forward
  * (lucid/nn/quantized/sparse.py:140-143 -> lucid/_C/backend/cpu/methods/Sequence.cpp:520-552),
  * and the float lookup of nn.Embedding, without forming the float table. */

@@ -20,6 +20,7 @@ LIB_PATH = os.path.join(_HERE, "_lib", "liblucid_amd.so")
 # Status and type codes of include/lq_api.h.
 OK = 0
 I8, U8, I16, I32, F16, F32, U8S8, I64 = 1, 2, 3, 4, 5, 6, 7, 8
+I8_QPAIR = 9  # table lookups: int8 rows + interleaved {scale, zero point} pairs
 OBS_MINMAX, OBS_EMA, OBS_REPLACE = 0, 1, 2
 OUT_I32, OUT_F32, OUT_F16, OUT_Q8, OUT_QU8, OUT_FQ32, OUT_Q16, OUT_QU8S8 = 0, 1, 2, 3, 4, 5, 6, 7
 EPI_RELU, EPI_A_U8S8 = 1, 2

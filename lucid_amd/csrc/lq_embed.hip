@@ -69,7 +69,15 @@ __device__ __forceinline__ void load_row(const EmbArgs& a, int64_t r, int64_t d,
         }
     } else {
         const int8_t* p = static_cast<const int8_t*>(a.table) + r * a.D + d;
-        const float s = a.scale[r], z = a.zp ? a.zp[r] : 0.0f;
+        float s, z;
+        if (a.table_type == LQ_I8_QPAIR) {  // one 8-byte read of the row's {scale, zero point}
+            const float2 q = reinterpret_cast<const float2*>(a.scale)[r];
+            s = q.x;
+            z = q.y;
+        } else {
+            s = a.scale[r];
+            z = a.zp ? a.zp[r] : 0.0f;
+        }
         int8_t c[W];
         if constexpr (W == 4) {
             const uint32_t w = *reinterpret_cast<const uint32_t*>(p);
@@ -211,8 +219,11 @@ static int table_checks(const void* d_table, int table_type, const float* d_scal
                         int idx_type, const char* who) {
     (void)who;
     LQ_REQUIRE(rows >= 0 && D >= 0, "table lookup: negative table shape");
-    LQ_REQUIRE(table_type == LQ_I8 || table_type == LQ_F32, "table lookup: table_type must be LQ_I8 or LQ_F32");
+    LQ_REQUIRE(table_type == LQ_I8 || table_type == LQ_I8_QPAIR || table_type == LQ_F32,
+               "table lookup: table_type must be LQ_I8, LQ_I8_QPAIR or LQ_F32");
     LQ_REQUIRE(table_type == LQ_F32 || d_scale, "table lookup: an int8 table needs its row scales");
+    LQ_REQUIRE(table_type != LQ_I8_QPAIR || reinterpret_cast<uintptr_t>(d_scale) % 8 == 0,
+               "table lookup: LQ_I8_QPAIR {scale, zero point} pairs must be 8-byte aligned");
     LQ_REQUIRE(idx_type == LQ_I32 || idx_type == LQ_I64, "table lookup: indices must be LQ_I32 or LQ_I64");
     LQ_REQUIRE(rows == 0 || D == 0 || d_table, "table lookup: NULL table");
     return LQ_OK;

@@ -174,3 +174,32 @@ def test_quantized_embedding_module_and_index_rules(gpu, monkeypatch):
         bag(_dev(gpu, np.array([1, 2, 3])), _dev(gpu, np.array([0, 2, 1])))  # decreasing
     with pytest.raises(NotImplementedError):
         bag(_dev(gpu, np.array([1, 2, 3])), _dev(gpu, np.array([0])), _dev(gpu, np.ones(3, np.float32)))
+
+
+@pytest.mark.parametrize("bag", [False, True])
+def test_qpair_table_matches_separate_qparams(gpu, bag):
+    """LQ_I8_QPAIR (one interleaved {scale, zero point} pair per row) against LQ_I8 with separate
+    scale / zero-point arrays: the same dequantization, bit for bit."""
+    from lucid_amd import _C
+
+    rng = np.random.default_rng(7 + bag)
+    rows, D = 300, 40
+    codes = rng.integers(-128, 128, (rows, D)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-1, rows).astype(np.float32)
+    z = rng.integers(-20, 21, rows).astype(np.float32)
+    idx = rng.integers(0, rows, 64).astype(np.int64)
+    idx[5] = rows + 3  # out of range: NaN either way
+    t, sd, zd, pd = (gpu.tensor(a, device="gpu") for a in (codes, s, z, np.stack([s, z], 1)))
+    ii = gpu.tensor(idx, device="gpu")
+    outs = []
+    for tt, sp, zp in ((_C.I8, sd.data_ptr(), zd.data_ptr()), (_C.I8_QPAIR, pd.data_ptr(), None)):
+        if bag:
+            y = gpu.empty((16, D), np.float32, "gpu")
+            _C.call("lq_embedding_bag", t.data_ptr(), tt, sp, zp, rows, D, ii.data_ptr(), _C.I64, 64, None,
+                    _C.I64, 0, 0, 4, _C.BAG_MEAN, -1, None, y.data_ptr(), None)
+        else:
+            y = gpu.empty((64, D), np.float32, "gpu")
+            _C.call("lq_embedding", t.data_ptr(), tt, sp, zp, rows, D, ii.data_ptr(), _C.I64, 64, y.data_ptr(), None)
+        outs.append(y.numpy())
+    np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    assert np.isnan(outs[1]).any()
