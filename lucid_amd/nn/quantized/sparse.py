@@ -14,7 +14,7 @@ from __future__ import annotations
 import numpy as np
 
 from lucid_amd import _C
-from lucid_amd._tensor import Tensor, ones, tensor, zeros
+from lucid_amd._tensor import Tensor, ones, zeros
 from lucid_amd.nn import functional as F
 from lucid_amd.nn.module import Module
 from lucid_amd.nn.quantized._utils import quantize_weight
@@ -56,16 +56,11 @@ class _QuantizedTable(Module):
         if codes.device != "gpu":
             codes = codes.to("gpu")
             self.weight_int8 = codes
-        # The row's {scale, zero point} as one interleaved pair (one random cache line per
-        # lookup instead of two), built once per pair of registered buffers.
-        key = (id(self.weight_scale), id(self.weight_zero_point))
-        cached = getattr(self, "_qpair", None)
-        if cached is None or cached[0] != key:
-            pairs = np.stack([self.weight_scale.numpy().astype(np.float32).reshape(-1),
-                              self.weight_zero_point.numpy().astype(np.float32).reshape(-1)], axis=1)
-            cached = (key, tensor(np.ascontiguousarray(pairs), device="gpu"))
-            self._qpair = cached
-        return (codes.data_ptr(), _C.I8_QPAIR, cached[1].data_ptr(), None, int(codes.shape[0]),
+        # Lucid's separate per-row arrays, read as the module holds them (load_state_dict copies
+        # into these buffers in place, so a derived copy such as interleaved pairs would go stale)
+        s, z = on_device(self.weight_scale), on_device(self.weight_zero_point)
+        self._qparams_alive = (s, z)  # keep the device copies alive over the async launch
+        return (codes.data_ptr(), _C.I8, s.data_ptr(), z.data_ptr(), int(codes.shape[0]),
                 int(codes.shape[1]))
 
     def _load(self, codes: Tensor, scale: Tensor, zero_point: Tensor) -> None:

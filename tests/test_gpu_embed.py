@@ -203,3 +203,21 @@ def test_qpair_table_matches_separate_qparams(gpu, bag):
         outs.append(y.numpy())
     np.testing.assert_array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
     assert np.isnan(outs[1]).any()
+
+
+def test_quantized_table_follows_in_place_state_dict_loads(gpu):
+    """load_state_dict copies into the module's buffers in place: the next lookup must use the
+    new scales / zero points (a module that cached anything derived from them would not)."""
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized as nnq
+
+    rng = np.random.default_rng(3)
+    src = nn.EmbeddingBag(50, 16, mode="sum")
+    src.weight = nn.Parameter(gpu.tensor(rng.standard_normal((50, 16)).astype(np.float32)))
+    q = nnq.EmbeddingBag.from_float(src)
+    idx = gpu.tensor(rng.integers(0, 50, (4, 3)).astype(np.int64), device="gpu")
+    first = q(idx).numpy()
+    sd = q.state_dict()
+    sd2 = {k: (gpu.tensor(v.numpy() * 2) if k.endswith("weight_scale") else v) for k, v in sd.items()}
+    q.load_state_dict(sd2)
+    np.testing.assert_allclose(q(idx).numpy(), 2 * first, rtol=1e-6, atol=1e-6)
