@@ -69,6 +69,10 @@ enum {
 int lq_abi_version(void);
 /* Message of the last failed call on this thread ("" if none). */
 const char* lq_last_error(void);
+/* Kernel variant the last GEMM / convolution call on this thread launched, e.g.
+ * "gemm dma 256x128" ("" before any).  Diagnostics for tests and profiles; no reference
+ * counterpart. */
+const char* lq_last_path(void);
 /* Name of the backend ("hip-gfx950"); replaces the backend registration of
  * lucid/_C/backend/BackendInit.cpp:25-38. */
 const char* lq_backend_name(void);
@@ -76,12 +80,19 @@ const char* lq_backend_name(void);
 int lq_device_count(int* count);
 int lq_set_device(int device);
 int lq_get_device(int* device);
-/* Device allocations come from a per-device caching allocator: lq_free returns
- * the block to the cache (no implicit device synchronisation).  lq_empty_cache
- * releases cached blocks back to HIP.  Stands in for the engine allocator
- * (lucid/_C/core/Allocator.h) for device storage. */
+/* Device allocations come from a per-device caching allocator (stands in for the engine
+ * allocator, lucid/_C/core/Allocator.h, for device storage).  Stream contract:
+ *   lq_free_async(p, s) returns p to the cache as last used on stream s (work already
+ *   queued on s may still read or write it; no synchronisation).  lq_malloc_async(&p, n, s)
+ *   hands out a cached block freed on s at once (s runs in order), and a block freed on
+ *   another stream only after the work queued there before its free has completed (an
+ *   event recorded at the free); otherwise it allocates.  A block freed on a stream under
+ *   graph capture is reused on that stream only.  lq_malloc / lq_free are the same calls
+ *   on the null stream.  lq_empty_cache releases every cached block back to HIP. */
 int lq_malloc(void** d_ptr, size_t bytes);
 int lq_free(void* d_ptr);
+int lq_malloc_async(void** d_ptr, size_t bytes, void* stream);
+int lq_free_async(void* d_ptr, void* stream);
 int lq_empty_cache(void);
 /* Bytes currently handed out / held in the cache by the allocator. */
 int lq_memory_stats(size_t* allocated, size_t* cached);

@@ -51,12 +51,15 @@ _SZ = ctypes.c_size_t
 _SIGNATURES: dict[str, tuple] = {
     "lq_abi_version": (_I, []),
     "lq_last_error": (ctypes.c_char_p, []),
+    "lq_last_path": (ctypes.c_char_p, []),
     "lq_backend_name": (ctypes.c_char_p, []),
     "lq_device_count": (_I, [ctypes.POINTER(_I)]),
     "lq_set_device": (_I, [_I]),
     "lq_get_device": (_I, [ctypes.POINTER(_I)]),
     "lq_malloc": (_I, [ctypes.POINTER(_P), _SZ]),
     "lq_free": (_I, [_P]),
+    "lq_malloc_async": (_I, [ctypes.POINTER(_P), _SZ, _P]),
+    "lq_free_async": (_I, [_P, _P]),
     "lq_empty_cache": (_I, []),
     "lq_memory_stats": (_I, [ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
     "lq_memcpy_h2d": (_I, [_P, _P, _SZ, _P]),
@@ -178,6 +181,11 @@ def check(rc: int, what: str = "") -> None:
 def call(name: str, *args) -> None:
     """Call an int-status entry point and raise on failure."""
     check(getattr(lib(), name)(*args), name)
+
+
+def last_path() -> str:
+    """Kernel variant the last GEMM / convolution call on this thread launched."""
+    return lib().lq_last_path().decode()
 
 
 def device_count() -> int:

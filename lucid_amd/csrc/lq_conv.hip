@@ -994,6 +994,7 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
             default: LQ_CONV_DMA(LQ_OUT_QU8S8)
         }
 #undef LQ_CONV_DMA
+        note_path(big ? "conv dma 256x64" : plan.splits > 1 ? "conv dma 128x64 split-k" : "conv dma 128x64");
         return launch_status("lq_conv2d_i8");
     }
     const dim3 grid((unsigned)((P + CV_BM - 1) / CV_BM), (unsigned)((Cout_g + CV_BN - 1) / CV_BN), (unsigned)groups);
@@ -1007,6 +1008,7 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
         case LQ_OUT_Q16: hipLaunchKernelGGL(conv_i8_kernel<LQ_OUT_Q16>, grid, dim3(CV_THREADS), 0, st, a); break;
         default: hipLaunchKernelGGL(conv_i8_kernel<LQ_OUT_QU8S8>, grid, dim3(CV_THREADS), 0, st, a); break;
     }
+    note_path("conv staged 128x64");
     return launch_status("lq_conv2d_i8");
 }
 

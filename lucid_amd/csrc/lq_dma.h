@@ -44,14 +44,14 @@ __device__ __forceinline__ v4i buffer_rsrc(const void* base, uint32_t bytes) {
                __builtin_amdgcn_readfirstlane((int)bytes), 0x00020000};
 }
 
-// 16 bytes per lane from rsrc + voff + soff into LDS at lds_addr + 16 * lane.
+// 16 bytes per lane from rsrc + voff + soff into LDS at lds_addr + 16 * lane.  The LDS
+// destination travels in M0 as an input operand ("{m0}"): the compiler writes M0 itself and
+// knows the instruction reads it, so M0 is never changed behind its back.
 __device__ __forceinline__ void lds_dma16(v4i rsrc, uint32_t voff, uint32_t soff, uint32_t lds_addr) {
-    asm volatile(
-        "s_mov_b32 m0, %0\n\t"
-        "buffer_load_dwordx4 %1, %2, %3 offen lds"
-        :
-        : "s"(lds_addr), "v"(voff), "s"(rsrc), "s"(soff)
-        : "memory", "m0");
+    asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds"
+                 :
+                 : "v"(voff), "s"(rsrc), "s"(soff), "{m0}"(lds_addr)
+                 : "memory");
 }
 
 }  // namespace lq

@@ -799,6 +799,8 @@ static int launch_packed_skinny(const GemmArgs& a, hipStream_t st) {
         hipLaunchKernelGGL((gemm_i8_packed_skinny_kernel<4, 4, 4, KIND>), dim3(tiles), dim3(256), 0, st, a);
     else
         hipLaunchKernelGGL((gemm_i8_packed_skinny_kernel<8, 4, 2, KIND>), dim3(tiles), dim3(256), 0, st, a);
+    note_path(a.M <= 16 ? "gemm packed skinny m16" : a.M <= 32 ? "gemm packed skinny m32"
+              : a.M <= 64 ? "gemm packed skinny m64" : "gemm packed skinny m128");
     return launch_status("lq_gemm_w8a8_packed");
 }
 
@@ -850,27 +852,32 @@ struct GemmLaunch {
             const int64_t total = (int64_t)a.M * a.N;
             hipLaunchKernelGGL(gemm_i8_generic_kernel<KIND>, dim3((unsigned)((total + 255) / 256)),
                                dim3(256), 0, st, a);
+            note_path("gemm generic");
             return launch_status("lq_gemm_w8a8 (generic)");
         }
         if (a.M <= 16) {
             hipLaunchKernelGGL((gemm_i8_skinny_kernel<1, 8, KIND>), dim3((unsigned)((a.N + 15) / 16)),
                                dim3(512), 0, st, a);
+            note_path("gemm skinny");
             return launch_status("lq_gemm_w8a8 (skinny)");
         }
         if (a.M <= 32) {
             hipLaunchKernelGGL((gemm_i8_skinny_kernel<2, 8, KIND>), dim3((unsigned)((a.N + 15) / 16)),
                                dim3(512), 0, st, a);
+            note_path("gemm skinny");
             return launch_status("lq_gemm_w8a8 (skinny)");
         }
         if (a.M <= 64) {
             hipLaunchKernelGGL((gemm_i8_skinny_kernel<4, 8, KIND>), dim3((unsigned)((a.N + 15) / 16)),
                                dim3(512), 0, st, a);
+            note_path("gemm skinny");
             return launch_status("lq_gemm_w8a8 (skinny)");
         }
         const int64_t tiles128 = ((int64_t)(a.M + 127) / 128) * ((a.N + 127) / 128);
         if (a.M <= 128 && tiles128 < 128) {
             hipLaunchKernelGGL((gemm_i8_skinny_kernel<8, 8, KIND, 2>), dim3((unsigned)((a.N + 15) / 16)),
                                dim3(512), 0, st, a);
+            note_path("gemm skinny");
             return launch_status("lq_gemm_w8a8 (skinny)");
         }
         // LDS-DMA path: whole 128-byte K stages, 32-bit buffer offsets.
@@ -880,12 +887,14 @@ struct GemmLaunch {
         if (dma_ok && dma_tiles >= 256) {
             hipLaunchKernelGGL((gemm_i8_dma_kernel<256, 128, 4, 2, GEMM_NBUF, KIND>), dim3((unsigned)dma_tiles),
                                dim3(512), 0, st, a);
+            note_path("gemm dma 256x128");
             return launch_status("lq_gemm_w8a8 (dma 256x128)");
         }
         const int64_t dma_tiles_128 = ((int64_t)(a.M + 127) / 128) * ((a.N + 127) / 128);
         if (dma_ok && dma_tiles_128 >= 128) {
             hipLaunchKernelGGL((gemm_i8_dma_kernel<128, 128, 4, 2, GEMM_NBUF, KIND>), dim3((unsigned)dma_tiles_128),
                                dim3(512), 0, st, a);
+            note_path("gemm dma 128x128");
             return launch_status("lq_gemm_w8a8 (dma 128x128)");
         }
         const int64_t mid_tiles = ((int64_t)(a.M + 127) / 128) * ((a.N + 127) / 128);
@@ -905,6 +914,7 @@ struct GemmLaunch {
         }
         hipLaunchKernelGGL((gemm_i8_tiled_kernel<128, 128, 2, 2, KIND>),
                            dim3((unsigned)(mid_tiles * splits)), dim3(256), 0, st, a);
+        note_path(splits > 1 ? "gemm 128x128 split-k" : "gemm 128x128");
         return launch_status("lq_gemm_w8a8 (128x128)");
     }
 };

@@ -29,6 +29,10 @@ int check_hip(hipError_t e, const char* what);
         if (!(cond)) return ::lq::set_error(LQ_ERR_INVALID, msg); \
     } while (0)
 
+// Records which kernel variant a compute call launched (a static string), readable through
+// lq_last_path() on the same thread: tests assert which instantiation a shape reaches.
+void note_path(const char* path);
+
 inline int launch_status(const char* what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return check_hip(e, what);

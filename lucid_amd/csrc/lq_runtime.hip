@@ -11,11 +11,15 @@
 #include <unordered_map>
 #include <vector>
 
+#include "lq_block_cache.h"
 #include "lq_internal.h"
 
 namespace lq {
 
 static thread_local std::string g_last_error;
+static thread_local const char* g_last_path = "";
+
+void note_path(const char* path) { g_last_path = path; }
 
 int set_error(int code, const std::string& msg) {
     g_last_error = msg;
@@ -28,30 +32,57 @@ int check_hip(hipError_t e, const char* what) {
 }
 
 // ---------------------------------------------------------------------- allocator
-// Per-device caching allocator.  Freed blocks go back to a size-ordered free list and
-// are reused by later requests of up to twice their size; nothing is returned to HIP
-// until lq_empty_cache.  Blocks are reused in host call order, so work that shares a
-// block must run on one stream (the library's usage model: one stream per thread).
+// Per-device caching allocator over lq_block_cache.h: freed blocks are reused by later
+// requests of up to twice their size, on the stream they were freed on at once and on any
+// other stream once a HIP event recorded at the free has completed.  Nothing is returned to
+// HIP until lq_empty_cache.
 namespace {
-struct Block {
-    size_t size;
-    int device;
-};
-struct Allocator {
-    std::mutex mu;
-    std::unordered_map<void*, Block> live;
-    std::map<int, std::multimap<size_t, void*>> free_lists;
-    size_t allocated = 0;
-    size_t cached = 0;
-};
-Allocator& alloc() {
-    static Allocator* a = new Allocator();  // never destroyed: outlives static teardown
-    return *a;
+// Events are pooled: a free records one, the reuse (or lq_empty_cache) hands it back.
+std::mutex g_event_mu;
+std::vector<hipEvent_t> g_event_pool;
+
+void* record_marker(void* stream) {
+    hipStream_t st = as_stream(stream);
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(st, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) {
+        (void)hipGetLastError();
+        return nullptr;  // under capture: keep the block bound to this stream
+    }
+    hipEvent_t e = nullptr;
+    {
+        std::lock_guard<std::mutex> g(g_event_mu);
+        if (!g_event_pool.empty()) {
+            e = g_event_pool.back();
+            g_event_pool.pop_back();
+        }
+    }
+    if (!e && hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) {
+        (void)hipGetLastError();
+        return nullptr;
+    }
+    if (hipEventRecord(e, st) != hipSuccess) {
+        (void)hipGetLastError();
+        (void)hipEventDestroy(e);
+        return nullptr;
+    }
+    return e;
 }
-size_t round_size(size_t bytes) {
-    if (bytes == 0) bytes = 1;
-    if (bytes <= (1u << 20)) return (bytes + 511) & ~size_t(511);
-    return (bytes + (2u << 20) - 1) & ~size_t((2u << 20) - 1);
+
+bool marker_done(void* marker) {
+    const hipError_t r = hipEventQuery(reinterpret_cast<hipEvent_t>(marker));
+    if (r == hipSuccess) return true;
+    (void)hipGetLastError();  // hipErrorNotReady is not a sticky error
+    return false;
+}
+
+void release_marker(void* marker) {
+    std::lock_guard<std::mutex> g(g_event_mu);
+    g_event_pool.push_back(reinterpret_cast<hipEvent_t>(marker));
+}
+
+BlockCache& cache() {
+    static BlockCache* c = new BlockCache(MarkerOps{record_marker, marker_done, release_marker});  // never destroyed
+    return *c;
 }
 }  // namespace
 
@@ -64,6 +95,8 @@ extern "C" {
 int lq_abi_version(void) { return LQ_ABI_VERSION; }
 
 const char* lq_last_error(void) { return g_last_error.c_str(); }
+
+const char* lq_last_path(void) { return g_last_path; }
 
 const char* lq_backend_name(void) { return "hip-gfx950"; }
 
@@ -90,26 +123,14 @@ int lq_get_device(int* device) {
     return LQ_OK;
 }
 
-int lq_malloc(void** d_ptr, size_t bytes) {
+int lq_malloc_async(void** d_ptr, size_t bytes, void* stream) {
     LQ_REQUIRE(d_ptr, "lq_malloc: NULL out pointer");
     int dev = 0;
     LQ_HIP(hipGetDevice(&dev));
-    size_t sz = round_size(bytes);
-    Allocator& a = alloc();
-    {
-        std::lock_guard<std::mutex> g(a.mu);
-        auto& fl = a.free_lists[dev];
-        auto it = fl.lower_bound(sz);
-        if (it != fl.end() && it->first <= 2 * sz) {
-            void* p = it->second;
-            size_t got = it->first;
-            fl.erase(it);
-            a.live[p] = Block{got, dev};
-            a.cached -= got;
-            a.allocated += got;
-            *d_ptr = p;
-            return LQ_OK;
-        }
+    const size_t sz = BlockCache::round_size(bytes);
+    if (void* p = cache().take(dev, sz, stream)) {
+        *d_ptr = p;
+        return LQ_OK;
     }
     void* p = nullptr;
     hipError_t e = hipMalloc(&p, sz);
@@ -120,53 +141,43 @@ int lq_malloc(void** d_ptr, size_t bytes) {
         e = hipMalloc(&p, sz);
         if (e != hipSuccess) return check_hip(e, "lq_malloc: hipMalloc");
     }
-    std::lock_guard<std::mutex> g(a.mu);
-    a.live[p] = Block{sz, dev};
-    a.allocated += sz;
+    cache().add_live(p, dev, sz);
     *d_ptr = p;
     return LQ_OK;
 }
 
-int lq_free(void* d_ptr) {
+int lq_malloc(void** d_ptr, size_t bytes) { return lq_malloc_async(d_ptr, bytes, nullptr); }
+
+int lq_free_async(void* d_ptr, void* stream) {
     if (!d_ptr) return LQ_OK;
-    Allocator& a = alloc();
-    std::lock_guard<std::mutex> g(a.mu);
-    auto it = a.live.find(d_ptr);
-    if (it == a.live.end()) return set_error(LQ_ERR_INVALID, "lq_free: pointer not from lq_malloc");
-    Block b = it->second;
-    a.live.erase(it);
-    a.allocated -= b.size;
-    a.cached += b.size;
-    a.free_lists[b.device].emplace(b.size, d_ptr);
+    if (!cache().put(d_ptr, stream)) return set_error(LQ_ERR_INVALID, "lq_free: pointer not from lq_malloc");
     return LQ_OK;
 }
 
+int lq_free(void* d_ptr) { return lq_free_async(d_ptr, nullptr); }
+
 int lq_empty_cache(void) {
-    Allocator& a = alloc();
-    std::vector<std::pair<int, void*>> victims;
+    const auto victims = cache().drain();
+    if (!victims.empty()) {
+        int cur = 0;
+        LQ_HIP(hipGetDevice(&cur));
+        for (auto& v : victims) {
+            LQ_HIP(hipSetDevice(v.first));
+            LQ_HIP(hipFree(v.second));  // hipFree waits for the device's pending work
+        }
+        LQ_HIP(hipSetDevice(cur));
+    }
+    std::vector<hipEvent_t> events;
     {
-        std::lock_guard<std::mutex> g(a.mu);
-        for (auto& kv : a.free_lists)
-            for (auto& e : kv.second) victims.emplace_back(kv.first, e.second);
-        a.free_lists.clear();
-        a.cached = 0;
+        std::lock_guard<std::mutex> g(g_event_mu);
+        events.swap(g_event_pool);
     }
-    if (victims.empty()) return LQ_OK;
-    int cur = 0;
-    LQ_HIP(hipGetDevice(&cur));
-    for (auto& v : victims) {
-        LQ_HIP(hipSetDevice(v.first));
-        LQ_HIP(hipFree(v.second));
-    }
-    LQ_HIP(hipSetDevice(cur));
+    for (hipEvent_t ev : events) (void)hipEventDestroy(ev);
     return LQ_OK;
 }
 
 int lq_memory_stats(size_t* allocated, size_t* cached) {
-    Allocator& a = alloc();
-    std::lock_guard<std::mutex> g(a.mu);
-    if (allocated) *allocated = a.allocated;
-    if (cached) *cached = a.cached;
+    cache().stats(allocated, cached);
     return LQ_OK;
 }
 

@@ -7,6 +7,8 @@ a fake-quantize) is read through its codes where that is exact.
 
 from __future__ import annotations
 
+import numpy as np
+
 from lucid_amd import _C
 from lucid_amd._tensor import Tensor, empty, float32
 from lucid_amd.quantization._device import on_device, require_gpu
@@ -44,7 +46,7 @@ def linear(x: Tensor, weight: Tensor, bias: Tensor | None = None) -> Tensor:
     N = w.shape[0]
     if w.shape[1] != K:
         raise ValueError(f"linear: input features {K} != weight in_features {w.shape[1]}")
-    M = x.numel() // K if K else 0
+    M = int(np.prod(x.shape[:-1], dtype=np.int64))
     y = empty((*x.shape[:-1], N), float32, "gpu")
     if M and N:
         _C.call("lq_linear_f32", x.data_ptr(), K, w.data_ptr(), K,

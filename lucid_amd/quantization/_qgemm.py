@@ -69,12 +69,32 @@ def _unpacked_k(wq: Tensor, bits: int) -> int:
     return wq.shape[-1] * 32 // bits
 
 
+def _check_packed(wq: Tensor, scales: Tensor, biases: Tensor | None, group_size: int, bits: int,
+                  op: str) -> tuple[int, int]:
+    """Validate the packed operands on the host, before any launch: the kernels index
+    ``scales[n * (K / group_size) + k / group_size]``, so a scale table of another shape (a
+    group size other than the one it was built with) would be read past its end.  MLX, which
+    Lucid calls, rejects such operands too.  Returns (N, K)."""
+    if wq.ndim != 2 or wq.dtype not in (np.int32, np.uint32):
+        raise TypeError(f"{op}: packed weight must be a 2-D int32 / uint32 tensor, got {wq.dtype} "
+                        f"{wq.shape}")
+    N, K = wq.shape[0], _unpacked_k(wq, bits)
+    _check(group_size, bits, K, op)
+    want = (N, K // group_size)
+    for name, t in (("scales", scales), ("biases", biases)):
+        if t is None:
+            continue
+        if tuple(t.shape) != want:
+            raise ValueError(f"{op}: {name} must be {want} for a {N} x {K} weight with "
+                             f"group_size {group_size}, got {tuple(t.shape)}")
+    return N, K
+
+
 def dequantize(wq: Tensor, scales: Tensor, biases: Tensor | None, group_size: int = 64,
                bits: int = 8) -> Tensor:
     """``c * s + b`` as a float32 ``[N, K]`` weight."""
+    N, K = _check_packed(wq, scales, biases, group_size, bits, "quantized.dequantize")
     require_gpu(wq, "quantized.dequantize")
-    N, K = wq.shape[0], _unpacked_k(wq, bits)
-    _check(group_size, bits, K, "quantized.dequantize")
     s = on_device(scales)
     b = on_device(biases) if biases is not None else None
     out = empty((N, K), float32, "gpu")
@@ -95,17 +115,18 @@ def quantized_matmul(x: Tensor, wq: Tensor, scales: Tensor, biases: Tensor | Non
     ``bias`` (length of the output features) / ``relu`` fuse the layer epilogue of
     ``QuantizedLinearMLX`` into the kernel.
     """
-    require_gpu(x, "quantized.quantized_matmul")
     if x.dtype not in (float32, float16):
         raise TypeError(f"quantized_matmul: float32 or float16 input expected, got {x.dtype}")
-    N, K = wq.shape[0], _unpacked_k(wq, bits)
-    _check(group_size, bits, K, "quantized_matmul")
+    N, K = _check_packed(wq, scales, biases, group_size, bits, "quantized_matmul")
     d_in, d_out = (K, N) if transpose else (N, K)
     if x.shape[-1] != d_in:
         raise ValueError(f"quantized_matmul: input features {x.shape[-1]} != the weight's "
                          f"{'K' if transpose else 'N'} {d_in}")
-    if bias is not None and bias.numel() != d_out:
-        raise ValueError(f"quantized_matmul: bias of {bias.numel()} for {d_out} output features")
+    if bias is not None and (bias.numel() != d_out or bias.dtype != float32):
+        raise ValueError(f"quantized_matmul: bias must be float32 of {d_out} output features, got "
+                         f"{bias.dtype} of {bias.numel()}")
+    require_gpu(x, "quantized.quantized_matmul")
+    require_gpu(wq, "quantized.quantized_matmul")
     M = int(np.prod(x.shape[:-1], dtype=np.int64))
     s = on_device(scales)
     b = on_device(biases) if biases is not None else None

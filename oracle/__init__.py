@@ -26,6 +26,11 @@ function                      follows (lucid-official/lucid)
 ``conv2d_f32``                float conv, per output sum over (c, kh, kw) in float32
                               (backend/cpu/methods/Conv.cpp:271-360 computes it by im2col +
                               sgemm: tolerance parity; bit-exact against the GPU's op order)
+``linear``                    F.linear (nn/functional/linear.py:23-93 -> backend/cpu/methods/
+                              Matmul.cpp:80-122: sgemm with W transposed, then the bias
+                              add) in float64 (tolerance reference: sgemm's summation order
+                              is not knowable); pinned by the reference's own goldens
+                              lucid/test/numerical/golden/{linear_2x4_4to3,matmul_4x4}.npz
 ``gemv_w8``                   nn/quantized/linear.py:206-210 (dequantize -> F.linear) with
                               float64 accumulation (tolerance reference)
 ``group_*``                   quantization/_qgemm.py:84-97, 167-170 (MLX 0.32.3 internals:
@@ -318,6 +323,19 @@ def gemm_epilogue(acc, a_scale, b_scale, bias=None, out_scale=1.0, out_zp=0.0, q
                             _ptr(None if bias is None else _f32(bias)), np.float32(out_scale),
                             np.float32(out_zp), qmin, qmax, out_kind, int(relu), _ptr(C), N)
     return C.view(np.float16) if out_kind == OUT_F16 else C
+
+
+def linear(x, W, bias=None) -> np.ndarray:
+    """y = x W^T + bias in float64 over float32 operands (F.linear's y = sgemm(x, W^T) then
+    the bias add, Matmul.cpp:110-120).  Each product of two float32 values is exact in
+    float64; the float64 sum carries far less error than a float32 sgemm, so the result is
+    a tolerance reference for any float32 order."""
+    xd = _f32(x).astype(np.float64)
+    wd = _f32(W).astype(np.float64)
+    y = xd @ wd.T
+    if bias is not None:
+        y = y + _f32(bias).astype(np.float64)
+    return y
 
 
 def gemv_w8(x, W, w_scale, w_zp=None, bias=None, relu=False) -> np.ndarray:

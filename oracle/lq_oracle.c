@@ -423,6 +423,8 @@ int lqo_conv2d_acc(const int8_t* x, int x_u8s8, int za, int64_t N, int64_t C, in
     int64_t OW = (W + pl + pr - (int64_t)dw * (KW - 1) - 1) / sw + 1;
     int64_t Cg = C / groups, Cog = Cout / groups;
     int ovf = 0;
+    /* independent outputs; each sum is an exact int64, so the thread split changes nothing */
+#pragma omp parallel for collapse(2) reduction(| : ovf) schedule(static)
     for (int64_t n = 0; n < N; ++n)
         for (int64_t co = 0; co < Cout; ++co) {
             int64_t g = co / Cog;

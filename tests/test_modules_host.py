@@ -189,3 +189,38 @@ def test_stubs_are_identity_before_prepare():
     with warnings.catch_warnings():
         warnings.simplefilter("error")
         assert nnq.Quantize(0.1, 0)(L.tensor(np.arange(3, dtype=np.int32))).dtype == np.int32
+
+
+def test_group_ops_reject_mismatched_operands_before_launch():
+    """quantized_matmul / dequantize validate the packed weight, scales and biases on the host
+    (a scale table built for another group size would be read past its end on the device)."""
+    import lucid_amd as L
+    from lucid_amd.quantization import _qgemm
+
+    N, K = 8, 256
+    wq = L.tensor(np.zeros((N, K * 4 // 32), np.int32))  # 4-bit codes of an 8 x 256 weight
+    s64 = L.tensor(np.ones((N, K // 64), np.float32))
+    b64 = L.tensor(np.zeros((N, K // 64), np.float32))
+    x = L.tensor(np.zeros((2, K), np.float32))
+    # scales of group size 64 used with group size 32: refused, not read out of bounds
+    with pytest.raises(ValueError, match="scales must be"):
+        _qgemm.quantized_matmul(x, wq, s64, b64, group_size=32, bits=4)
+    with pytest.raises(ValueError, match="scales must be"):
+        _qgemm.dequantize(wq, s64, b64, group_size=32, bits=4)
+    with pytest.raises(ValueError, match="biases must be"):
+        _qgemm.quantized_matmul(x, wq, s64, L.tensor(np.zeros((N, 2), np.float32)), group_size=64, bits=4)
+    with pytest.raises(ValueError, match="scales must be"):
+        _qgemm.quantized_matmul(x, wq, L.tensor(np.ones((N + 1, K // 64), np.float32)), b64,
+                                group_size=64, bits=4)
+    with pytest.raises(TypeError, match="2-D int32"):
+        _qgemm.quantized_matmul(x, L.tensor(np.zeros((N, 2, 16), np.int32)), s64, b64, bits=4)
+    with pytest.raises(TypeError, match="2-D int32"):
+        _qgemm.dequantize(L.tensor(np.zeros((N, 32), np.float32)), s64, b64, bits=4)
+    with pytest.raises(ValueError, match="bias must be"):
+        _qgemm.quantized_matmul(x, wq, s64, b64, group_size=64, bits=4,
+                                bias=L.tensor(np.zeros(N + 1, np.float32)))
+    with pytest.raises(ValueError, match="group_size must be"):
+        _qgemm.quantized_matmul(x, wq, s64, b64, group_size=48, bits=4)
+    # well-formed operands get as far as the device requirement
+    with pytest.raises(L.LucidError, match="GPU"):
+        _qgemm.quantized_matmul(x, wq, s64, b64, group_size=64, bits=4)

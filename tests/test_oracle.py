@@ -247,6 +247,41 @@ def test_gemm_acc_brute_force():
         np.testing.assert_array_equal(O.gemm_acc(A, B, za, zb), want)
 
 
+def test_linear_reference_goldens():
+    """F.linear against the reference's own checked-in goldens (the inputs regenerated by the
+    recipe of lucid/test/numerical/golden/test_golden.py:55-70 and :31-40, the expected
+    outputs read from the .npz files copied under tests/golden/), at that test's atol 1e-5.
+    The square matmul golden catches a transposed operand (linear(a, b^T) == a @ b)."""
+    here = os.path.dirname(__file__)
+    rng = np.random.default_rng(0)
+    x = rng.uniform(-1.0, 1.0, size=(2, 4)).astype(np.float32)
+    w = rng.uniform(-0.5, 0.5, size=(3, 4)).astype(np.float32)
+    b = rng.uniform(-0.1, 0.1, size=(3,)).astype(np.float32)
+    want = np.load(os.path.join(here, "golden", "lucid_linear_2x4_4to3.npz"))["out"]
+    np.testing.assert_allclose(O.linear(x, w, b), want, atol=1e-5, rtol=0)
+    rng = np.random.default_rng(0)
+    a = rng.uniform(-1.0, 1.0, size=(4, 4)).astype(np.float32)
+    bm = rng.uniform(-1.0, 1.0, size=(4, 4)).astype(np.float32)
+    want = np.load(os.path.join(here, "golden", "lucid_matmul_4x4.npz"))["out"]
+    np.testing.assert_allclose(O.linear(a, bm.T), want, atol=1e-5, rtol=0)
+    assert np.max(np.abs(O.linear(a, bm) - want)) > 1e-2  # the other orientation is far off
+
+
+def test_linear_closed_forms():
+    """Identity and permutation weights select input columns exactly; zero weights leave the
+    bias; an empty K leaves the bias."""
+    rng = np.random.default_rng(6)
+    x = rng.standard_normal((5, 7)).astype(np.float32)
+    b = rng.standard_normal(7).astype(np.float32)
+    np.testing.assert_array_equal(O.linear(x, np.eye(7, dtype=np.float32), b), x.astype(np.float64) + b)
+    perm = rng.permutation(7)
+    np.testing.assert_array_equal(O.linear(x, np.eye(7, dtype=np.float32)[perm]), x[:, perm])
+    np.testing.assert_array_equal(O.linear(x, np.zeros((3, 7), np.float32), b[:3]),
+                                  np.broadcast_to(b[:3].astype(np.float64), (5, 3)))
+    np.testing.assert_array_equal(O.linear(np.zeros((2, 0), np.float32), np.zeros((4, 0), np.float32),
+                                           b[:4]), np.broadcast_to(b[:4].astype(np.float64), (2, 4)))
+
+
 def test_gemm_epilogue_structure():
     rng = np.random.default_rng(5)
     A = rng.integers(-127, 128, (8, 64), dtype=np.int8)
