@@ -259,6 +259,22 @@ int lq_gemm_w8a8(const int8_t* d_A, int64_t lda, const int8_t* d_B, int64_t ldb,
                  const int32_t* d_b_sums, const float* d_bias, const float* d_out_scale,
                  const float* d_out_zero_point, int out_qmin, int out_qmax, int out_kind,
                  int flags, void* d_workspace, size_t workspace_bytes, void* stream);
+/* lq_gemm_w8a8 without a workspace argument, allocating nothing: the code sums, split-K
+ * partials and tile counters live in a static 16 MiB device array the library holds on each
+ * GPU it runs on (lq_gemm_w8a8_noalloc_scratch_bytes()).  Shapes whose workspace
+ * (lq_gemm_w8a8_workspace_size) exceeds it fail with LQ_ERR_UNSUPPORTED.  Calls on one GPU
+ * share the array, so calls that overlap on one GPU (concurrent streams or threads) race;
+ * serialize them.  Same results as lq_gemm_w8a8.  No counterpart in the reference: for
+ * callers that cannot allocate (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc). */
+size_t lq_gemm_w8a8_noalloc_scratch_bytes(void);
+int lq_gemm_w8a8_noalloc(const int8_t* d_A, int64_t lda, const int8_t* d_B, int64_t ldb, void* d_C,
+                         int64_t ldc, int64_t M, int64_t N, int64_t K, const float* d_a_scale,
+                         int64_t a_scale_stride, const float* d_b_scale, int64_t b_scale_stride,
+                         const float* d_a_zero_point, const float* d_b_zero_point,
+                         const int32_t* d_b_sums, const float* d_bias, const float* d_out_scale,
+                         const float* d_out_zero_point, int out_qmin, int out_qmax, int out_kind,
+                         int flags, void* stream);
 /* ---- MFMA-packed weights for decode (M <= 128) ------------------------------ */
 /* Bytes of the packed form of an int8 weight B [N, K]: ceil(N/16) x ceil(K/64) tiles of
  * 1 KB.  Tile (t, s) sits at byte (t * ceil(K/64) + s) * 1024; its 16-byte chunk l holds

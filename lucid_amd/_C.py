@@ -106,6 +106,9 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_gemm_w8a8_workspace_size": (_SZ, [_I64, _I64, _I64]),
     "lq_gemm_w8a8": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64,
                           _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _SZ, _P]),
+    "lq_gemm_w8a8_noalloc_scratch_bytes": (_SZ, []),
+    "lq_gemm_w8a8_noalloc": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64,
+                                  _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "lq_packed_weights_size": (_SZ, [_I64, _I64]),
     "lq_pack_weights_i8": (_I, [_P, _I64, _I64, _I64, _P, _P]),
     "lq_gemm_w8a8_packed": (_I, [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64,

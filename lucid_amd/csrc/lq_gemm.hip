@@ -21,6 +21,8 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
+#include <mutex>
+#include <string>
 #include <type_traits>
 
 #include "lq_dma.h"
@@ -1121,6 +1123,69 @@ int lq_gemm_w8a8_packed(const int8_t* d_A, int64_t lda, const int8_t* d_B_packed
                       d_b_scale, b_scale_stride, d_a_zero_point, d_b_zero_point, d_b_sums, d_bias,
                       d_out_scale, d_out_zero_point, out_qmin, out_qmax, out_kind, flags, d_workspace,
                       workspace_bytes, stream);
+}
+
+}  // extern "C"
+
+// ------------------------------------------------------ allocation-free variant
+//
+// lq_gemm_w8a8_noalloc keeps the workspace of lq_gemm_w8a8 (the activation / weight code
+// sums, split-K partial sums and tile arrival counters) in this file-scope device array
+// instead of a caller buffer, for callers that cannot allocate (graph capture, serving
+// loops).  Each GPU the library runs on holds its own copy until the process ends; every
+// call on one GPU shares it, so calls that overlap on one GPU race.  Nothing in it is
+// assumed to persist: the code sums are recomputed and the split-K partials and counters are
+// cleared by a fill kernel inside each call that uses them.
+constexpr size_t LQ_NOALLOC_SCRATCH_BYTES = (size_t)16 << 20;
+static __device__ __align__(256) uint8_t scratch[LQ_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int NOALLOC_MAX_DEVICES = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[NOALLOC_MAX_DEVICES];  // device address of `scratch` on each device
+
+// The device address of this GPU's `scratch`, looked up once per device with that device
+// current (the array's host-side name is not a device address).
+int current_device_scratch(void** out) {
+    int dev = 0;
+    LQ_HIP(hipGetDevice(&dev));
+    LQ_REQUIRE(dev >= 0 && dev < NOALLOC_MAX_DEVICES, "lq_gemm_w8a8_noalloc: device index out of range");
+    std::lock_guard<std::mutex> g(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        if (e != hipSuccess) return check_hip(e, "lq_gemm_w8a8_noalloc: hipGetSymbolAddress(scratch)");
+        if (!p) return set_error(LQ_ERR_HIP, "lq_gemm_w8a8_noalloc: no device address for scratch");
+        g_scratch_ptr[dev] = p;
+    }
+    *out = g_scratch_ptr[dev];
+    return LQ_OK;
+}
+}  // namespace
+
+extern "C" {
+
+size_t lq_gemm_w8a8_noalloc_scratch_bytes(void) { return LQ_NOALLOC_SCRATCH_BYTES; }
+
+int lq_gemm_w8a8_noalloc(const int8_t* d_A, int64_t lda, const int8_t* d_B, int64_t ldb, void* d_C,
+                         int64_t ldc, int64_t M, int64_t N, int64_t K, const float* d_a_scale,
+                         int64_t a_scale_stride, const float* d_b_scale, int64_t b_scale_stride,
+                         const float* d_a_zero_point, const float* d_b_zero_point,
+                         const int32_t* d_b_sums, const float* d_bias, const float* d_out_scale,
+                         const float* d_out_zero_point, int out_qmin, int out_qmax, int out_kind,
+                         int flags, void* stream) {
+    const size_t need = lq_gemm_w8a8_workspace_size(M, N, K);
+    if (need > LQ_NOALLOC_SCRATCH_BYTES)
+        return set_error(LQ_ERR_UNSUPPORTED,
+                         "lq_gemm_w8a8_noalloc: this shape needs " + std::to_string(need) +
+                             " bytes of scratch, more than the " + std::to_string(LQ_NOALLOC_SCRATCH_BYTES) +
+                             " the library holds per GPU (use lq_gemm_w8a8 with a workspace)");
+    void* ws = nullptr;
+    if (const int rc = current_device_scratch(&ws)) return rc;
+    return gemm_entry(false, d_A, lda, d_B, ldb, d_C, ldc, M, N, K, d_a_scale, a_scale_stride, d_b_scale,
+                      b_scale_stride, d_a_zero_point, d_b_zero_point, d_b_sums, d_bias, d_out_scale,
+                      d_out_zero_point, out_qmin, out_qmax, out_kind, flags, ws, LQ_NOALLOC_SCRATCH_BYTES,
+                      stream);
 }
 
 }  // extern "C"
