@@ -38,7 +38,7 @@ __device__ __forceinline__ uint32_t epi_one(int32_t acc, float sa, float sb, con
     if (bias_p) y = y + *bias_p;  // no add without a bias: -0 stays -0
     if (relu) y = (y <= 0.0f) ? 0.0f : y;
     if (KIND == LQ_OUT_F32) return __float_as_uint(y);
-    if (KIND == LQ_OUT_F16) return (uint32_t)__half_as_ushort(__float2half_rn(y));
+    if (KIND == LQ_OUT_F16) return (uint32_t)__half_as_ushort(f32_to_f16_rn(y));
     float c = requant_code(y, p);
     if (KIND == LQ_OUT_Q8) return (uint32_t)(uint8_t)CodeI8::store(c);
     if (KIND == LQ_OUT_QU8) return (uint32_t)CodeU8::store(c);

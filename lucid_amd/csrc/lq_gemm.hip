@@ -31,6 +31,8 @@
 
 namespace lq {
 
+typedef float v4f __attribute__((ext_vector_type(4)));
+
 struct GemmArgs {
     const int8_t* A;
     const int8_t* B;
@@ -527,18 +529,49 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves
         }(std::make_integer_sequence<int, NBUF>());
     }
     // Epilogue inputs, loaded after the main loop so their registers (52 per lane) do not
-    // compete with the fragment double buffer: this lane's 16 columns and FM rows.
+    // compete with the fragment double buffer: this lane's 16 columns and FM rows, as 16-byte
+    // loads when the 16 columns are in range and the arrays aligned.
     const EpiParams p = epi_params(a);
     const int nc0 = n0 + wn * 64 + (lane >> 4) * 16;
     const int mr0 = m0 + wm * WM + (lane & 15);
     float csb[16], cbias[16];
     int32_t czab[16];  // za * bsum[n]
+    {
+        const bool cols_vec = nc0 + 16 <= a.N;
+        auto vec_ok = [&](const void* ptr) { return cols_vec && (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+        if (a.b_scale && a.b_stride == 1 && vec_ok(a.b_scale)) {
 #pragma unroll
-    for (int q = 0; q < 16; ++q) {
-        const int nn = min(nc0 + q, a.N - 1);  // clamped: out-of-range columns are never stored
-        csb[q] = a.b_scale ? a.b_scale[(int64_t)nn * a.b_stride] : 1.0f;
-        cbias[q] = a.bias ? a.bias[nn] : 0.0f;
-        czab[q] = p.has_za ? (int32_t)((uint32_t)p.za * (uint32_t)a.b_sums[nn]) : 0;
+            for (int h = 0; h < 4; ++h) {
+                const v4f v = *reinterpret_cast<const v4f*>(a.b_scale + nc0 + 4 * h);
+                csb[4 * h] = v[0], csb[4 * h + 1] = v[1], csb[4 * h + 2] = v[2], csb[4 * h + 3] = v[3];
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 16; ++q)
+                csb[q] = a.b_scale ? a.b_scale[(int64_t)min(nc0 + q, a.N - 1) * a.b_stride] : 1.0f;
+        }
+        if (a.bias && vec_ok(a.bias)) {
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const v4f v = *reinterpret_cast<const v4f*>(a.bias + nc0 + 4 * h);
+                cbias[4 * h] = v[0], cbias[4 * h + 1] = v[1], cbias[4 * h + 2] = v[2], cbias[4 * h + 3] = v[3];
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 16; ++q) cbias[q] = a.bias ? a.bias[min(nc0 + q, a.N - 1)] : 0.0f;
+        }
+        if (p.has_za && vec_ok(a.b_sums)) {
+#pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const v4i v = *reinterpret_cast<const v4i*>(a.b_sums + nc0 + 4 * h);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) czab[4 * h + e] = (int32_t)((uint32_t)p.za * (uint32_t)v[e]);
+            }
+        } else {
+#pragma unroll
+            for (int q = 0; q < 16; ++q)
+                czab[q] = p.has_za ? (int32_t)((uint32_t)p.za * (uint32_t)a.b_sums[min(nc0 + q, a.N - 1)]) : 0;
+        }
     }
     float rsa[FM];
 #pragma unroll
@@ -558,31 +591,10 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves
     CodeClamp cc{};
     if (INT_CODES) cc = code_clamp<KIND>(a.qmin, a.qmax);
     const bool has_bias = a.bias != nullptr, relu = a.relu != 0;
-#pragma unroll
-    for (int j = 0; j < FM; ++j) {
+
+    // Stores of one row's 16 outputs (bits of the output type in out[]).
+    auto store_row = [&](int j, const uint32_t* out) __attribute__((always_inline)) {
         const int m = mr0 + j * 16;
-        int32_t asum = 0;
-        if (a.b_zp) asum = a.a_sums[min(m, a.M - 1)];
-        uint32_t out[16];
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            uint32_t accu = (uint32_t)acc[q >> 2][j][q & 3] - (uint32_t)czab[q];
-            if (a.b_zp) {  // weight zero points (rare): per-column terms read here
-                const int nn = min(nc0 + q, a.N - 1);
-                const uint32_t zb = (uint32_t)(int)a.b_zp[nn];
-                accu -= zb * (uint32_t)asum;
-                accu += (uint32_t)a.K * (uint32_t)p.za * zb;
-            }
-            if (INT_CODES) {
-                const float s = rsa[j] * csb[q];
-                float y = (float)(int32_t)accu * s;
-                if (has_bias) y = y + cbias[q];
-                if (relu) y = (y <= 0.0f) ? 0.0f : y;
-                out[q] = (uint32_t)requant_int<KIND>(y, p, cc);
-            } else {
-                out[q] = epi_one<KIND>((int32_t)accu, rsa[j], csb[q], has_bias ? &cbias[q] : nullptr, relu, p);
-            }
-        }
         const bool row_ok = m < a.M;
         if (vec) {
             if (OB == 1) {
@@ -591,7 +603,6 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves
                 for (int d = 0; d < 4; ++d)
                     w[d] = (int)((out[4 * d] & 0xffu) | ((out[4 * d + 1] & 0xffu) << 8) |
                                  ((out[4 * d + 2] & 0xffu) << 16) | (out[4 * d + 3] << 24));
-                if (KIND == LQ_OUT_QU8S8) w ^= v4i{(int)0x80808080, (int)0x80808080, (int)0x80808080, (int)0x80808080};
                 if (row_ok) *reinterpret_cast<v4i*>(reinterpret_cast<uint8_t*>(a.C) + (int64_t)m * a.ldc + nc0) = w;
             } else if (OB == 2) {
 #pragma unroll
@@ -633,12 +644,106 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves
         } else if (row_ok) {
             const int64_t base = (int64_t)m * a.ldc + nc0;
 #pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                uint32_t v = out[q];
-                if (KIND == LQ_OUT_QU8S8) v ^= 0x80u;
-                if (nc0 + q < a.N) store_elem<KIND>(a.C, base + q, v);
-            }
+            for (int q = 0; q < 16; ++q)
+                if (nc0 + q < a.N) store_elem<KIND>(a.C, base + q, out[q]);
         }
+    };
+
+    // Integer codes, fast form.  When the output scale's reciprocal is finite and positive,
+    // the zero point integral and small, every scale and bias of this wave finite and
+    // max|sa| * max|sb| small enough that float(acc) * s cannot overflow, y is always finite,
+    // and the code clamp(rne(y * inv) + z, lo, hi) equals zi + med3(cvt(rne(y * inv)), lo - zi,
+    // hi - zi): the saturating convert keeps out-of-range values ordered and |zi| < 2^22 keeps
+    // the sum exact.  ReLU (y <= 0 -> 0, so the code of z) folds into the lower bound:
+    // rne(y * inv) <= 0 exactly when y <= 0.  The stored byte of QU8S8 is c - 128.
+    bool fast_int = false;
+    if constexpr (INT_CODES) {
+        const float zf = p.out_z;
+        bool ok = a.b_zp == nullptr && p.out_inv > 0.0f && p.out_inv < 3.0e38f && zf == __builtin_rintf(zf) &&
+                  __builtin_fabsf(zf) < 4194304.0f;
+        float amax = 0.0f, bmax = 0.0f;
+#pragma unroll
+        for (int j = 0; j < FM; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(rsa[j]));
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            bmax = __builtin_fmaxf(bmax, __builtin_fabsf(csb[q]));
+            ok = ok && __builtin_isfinite(cbias[q]);
+        }
+        // fmaxf ignores NaN: test the maxima and every scale for finiteness
+#pragma unroll
+        for (int j = 0; j < FM; ++j) ok = ok && __builtin_isfinite(rsa[j]);
+#pragma unroll
+        for (int q = 0; q < 16; ++q) ok = ok && __builtin_isfinite(csb[q]);
+        ok = ok && amax < 1.0e14f && bmax < 1.0e14f && amax * bmax < 1.0e28f;
+        fast_int = __all(ok);
+    }
+    if constexpr (INT_CODES) {
+        if (fast_int) {
+            const int zi = (int)p.out_z;
+            int L = cc.lo - zi, H = cc.hi - zi;
+            if (relu) L = min(max(L, 0), H);
+            const int shift = zi - (KIND == LQ_OUT_QU8S8 ? 128 : 0);
+            auto rows = [&](auto bias_c) __attribute__((always_inline)) {
+                constexpr bool BIAS = decltype(bias_c)::value;
+#pragma unroll
+                for (int j = 0; j < FM; ++j) {
+                    uint32_t out[16];
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) {
+                        const int32_t accq = (int32_t)((uint32_t)acc[q >> 2][j][q & 3] - (uint32_t)czab[q]);
+                        const float sc = rsa[j] * csb[q];
+                        float y = (float)accq * sc;
+                        if (BIAS) y = y + cbias[q];
+                        const float r = __builtin_rintf(y * p.out_inv);
+                        out[q] = (uint32_t)(min(max(cvt_i32_sat(r), L), H) + shift);
+                    }
+                    store_row(j, out);
+                }
+            };
+            if (has_bias) rows(std::true_type{});
+            else rows(std::false_type{});
+            return;
+        }
+    }
+    // General form (any zero points, non-finite inputs, non-integral output zero point, and
+    // the float kinds): bias and ReLU resolved outside the element loop.
+    auto rows_general = [&](auto bias_c, auto relu_c) __attribute__((always_inline)) {
+        constexpr bool BIAS = decltype(bias_c)::value, RELU = decltype(relu_c)::value;
+#pragma unroll
+        for (int j = 0; j < FM; ++j) {
+            const int m = mr0 + j * 16;
+            int32_t asum = 0;
+            if (a.b_zp) asum = a.a_sums[min(m, a.M - 1)];
+            uint32_t out[16];
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                uint32_t accu = (uint32_t)acc[q >> 2][j][q & 3] - (uint32_t)czab[q];
+                if (a.b_zp) {  // weight zero points (rare): per-column terms read here
+                    const int nn = min(nc0 + q, a.N - 1);
+                    const uint32_t zb = (uint32_t)(int)a.b_zp[nn];
+                    accu -= zb * (uint32_t)asum;
+                    accu += (uint32_t)a.K * (uint32_t)p.za * zb;
+                }
+                if (INT_CODES) {
+                    const float sc = rsa[j] * csb[q];
+                    float y = (float)(int32_t)accu * sc;
+                    if (BIAS) y = y + cbias[q];
+                    if (RELU) y = (y <= 0.0f) ? 0.0f : y;
+                    out[q] = (uint32_t)requant_int<KIND>(y, p, cc);
+                    if (KIND == LQ_OUT_QU8S8) out[q] ^= 0x80u;
+                } else {
+                    out[q] = epi_one<KIND>((int32_t)accu, rsa[j], csb[q], BIAS ? &cbias[q] : nullptr, RELU, p);
+                }
+            }
+            store_row(j, out);
+        }
+    };
+    if (has_bias) {
+        if (relu) rows_general(std::true_type{}, std::true_type{});
+        else rows_general(std::true_type{}, std::false_type{});
+    } else {
+        if (relu) rows_general(std::false_type{}, std::true_type{});
+        else rows_general(std::false_type{}, std::false_type{});
     }
 }
 

@@ -6,6 +6,7 @@
 #pragma once
 
 #include <hip/hip_runtime.h>
+#include <hip/hip_fp16.h>
 #include <stdint.h>
 
 #include <string>
@@ -52,6 +53,15 @@ typedef uint32_t vu4 __attribute__((ext_vector_type(4)));
 
 // round half to even (v_rndne_f32): Lucid's lucid.round = vvnintf.
 __device__ __forceinline__ float rne(float x) { return __builtin_rintf(x); }
+
+// float -> half, round to nearest even, of an already rounded float32 value.  The empty asm
+// hides where the value came from: otherwise the backend may fold fptrunc(fmul(a, b)) into
+// v_fma_mix (a * b rounded once, to half), which is not the two roundings the contract
+// specifies.
+__device__ __forceinline__ __half f32_to_f16_rn(float v) {
+    asm volatile("" : "+v"(v));
+    return __float2half_rn(v);
+}
 
 // clip with NaN pass-through and Lucid's signed-zero tie rule (backend/cpu/Vdsp.cpp:33-62).
 __device__ __forceinline__ float clip_tie(float v, float lo, float hi, bool lo_ties, bool hi_ties) {

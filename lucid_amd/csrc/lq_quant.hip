@@ -435,7 +435,7 @@ __device__ __forceinline__ Y to_out(float v);
 template <>
 __device__ __forceinline__ float to_out<float>(float v) { return v; }
 template <>
-__device__ __forceinline__ __half to_out<__half>(float v) { return __float2half_rn(v); }
+__device__ __forceinline__ __half to_out<__half>(float v) { return f32_to_f16_rn(v); }
 
 template <class Code, typename Y>
 __device__ __forceinline__ void dequant16(const typename Code::T* src, Y* dst, float s, float z) {
