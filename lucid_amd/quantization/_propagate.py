@@ -1,98 +1,130 @@
-"""Config resolution over a module tree (lucid/quantization/_propagate.py:50-278).
+"""Which ``QConfig`` applies to each module of a model.
 
-``QConfigResolver`` walks a model depth-first, giving each module its own ``.qconfig``
-when it has one, else a rule of the mapping (name or type), else its parent's config.
-``prepare`` stamps the result on every module; ``convert`` and ``quantize_dynamic`` strip
-it afterwards.  ``normalize_dynamic_spec`` turns ``quantize_dynamic``'s ``qconfig_spec``
-(a set of types / names, or a dict to QConfig / QDtype / None) into a mapping.
+Lucid resolves a module's recipe in three tiers (lucid/quantization/_propagate.py:50-278,
+the behaviour this file keeps): the module's own ``.qconfig`` attribute if it has one (a
+``QConfig``, or ``None`` to exclude it), else a per-name or per-type rule of the
+``QConfigMapping`` (name before type), else whatever its parent resolved to.  The root
+inherits the mapping's global recipe -- except when the caller passed no config at all
+(the entry point's stock default) and the model already carries ``.qconfig`` attributes:
+then the user has configured modules, and the stock recipe does not cover the rest.
+
+Here that is one pure function, :func:`plan_sites`, which returns every module once in
+parent-before-child order as a :class:`Site` (where it hangs in its parent, its dotted
+path and its recipe).  ``prepare`` marks and observes modules from the plan;
+``quantize_dynamic`` replaces modules from it.  Nothing is written during planning.
 """
 
 from __future__ import annotations
 
-from collections.abc import Callable, Collection, Iterator, Mapping
-from typing import NamedTuple
+from collections.abc import Callable, Collection, Mapping
+from dataclasses import dataclass
 
 from lucid_amd.nn.module import Module
 from lucid_amd.quantization._qscheme import QDtype, per_channel_symmetric, quint8
 from lucid_amd.quantization.observer import PerChannelMinMaxObserver, PlaceholderObserver
 from lucid_amd.quantization.qconfig import QConfig, QConfigMapping
 
-_MISSING = object()
+MARK = "qconfig"  # the per-module attribute the tiers read and prepare writes
 
 
-class Resolved(NamedTuple):
-    name: str
+@dataclass(frozen=True)
+class Site:
+    """One module of a model and the recipe it resolved to (``None``: stays float)."""
+
+    parent: Module | None  # None for the root
+    attr: str              # attribute name in the parent ("" for the root)
     module: Module
-    path: str
+    path: str              # dotted path from the root ("" for the root)
     qconfig: QConfig | None
 
 
-class QConfigResolver:
-    def __init__(self, mapping: QConfigMapping, *, implicit: bool = False) -> None:
-        self._mapping = mapping
-        self._implicit = implicit
+def as_mapping(qconfig: object, default: Callable[[], QConfigMapping]) -> tuple[QConfigMapping, bool]:
+    """The mapping an entry point's ``qconfig`` argument denotes, and whether it is the stock
+    default (``qconfig is None``).  A bare ``QConfig`` is the global tier."""
+    if qconfig is None:
+        return default(), True
+    if isinstance(qconfig, QConfigMapping):
+        return qconfig, False
+    if isinstance(qconfig, QConfig):
+        return QConfigMapping().set_global(qconfig), False
+    raise TypeError("qconfig must be a QConfig, a QConfigMapping or None; got "
+                    f"{type(qconfig).__name__}")
 
-    @classmethod
-    def from_argument(cls, qconfig, default: Callable[[], QConfigMapping]) -> "QConfigResolver":
-        if qconfig is None:
-            return cls(default(), implicit=True)
-        if isinstance(qconfig, QConfig):
-            return cls(QConfigMapping().set_global(qconfig))
-        if isinstance(qconfig, QConfigMapping):
-            return cls(qconfig)
-        raise TypeError("qconfig must be a QConfig, a QConfigMapping or None; got "
-                        f"{type(qconfig).__name__}")
 
-    def is_targeted(self, module: Module, path: str) -> bool:
-        return (self._mapping._has_rule(type(module), path)
-                and self._mapping.get_qconfig(type(module), path) is not None)
+_ABSENT = object()
 
-    def resolve(self, module: Module, path: str, inherited: QConfig | None) -> QConfig | None:
-        own = getattr(module, "qconfig", _MISSING)
-        if own is not _MISSING:
-            if own is not None and not isinstance(own, QConfig):
-                raise TypeError(f"{path or type(module).__name__}.qconfig must be a QConfig or "
-                                f"None; got {type(own).__name__}")
-            return own
-        if self._mapping._has_rule(type(module), path):
-            return self._mapping.get_qconfig(type(module), path)
-        return inherited
 
-    @staticmethod
-    def stamp(entry: Resolved) -> Resolved:
-        entry.module.qconfig = entry.qconfig
-        return entry
+def _own(module: Module, path: str) -> tuple[bool, QConfig | None]:
+    """(has its own recipe, that recipe) from the module's ``.qconfig`` attribute."""
+    own = getattr(module, MARK, _ABSENT)
+    if own is _ABSENT:
+        return False, None
+    if own is not None and not isinstance(own, QConfig):
+        raise TypeError(f"{path or type(module).__name__}.qconfig must be a QConfig or None; got "
+                        f"{type(own).__name__}")
+    return True, own
 
-    @staticmethod
-    def strip(model: Module) -> None:
-        for module in model.modules():
-            if "qconfig" in module.__dict__:
-                del module.__dict__["qconfig"]
 
-    def root(self, model: Module) -> Resolved:
-        seed = self._mapping._fallback()
-        if self._implicit and any("qconfig" in m.__dict__ for m in model.modules()):
-            seed = None  # explicit per-module configs opt out of the implicit default
-        return Resolved("", model, "", self.resolve(model, "", seed))
+def recipe_for(mapping: QConfigMapping, module: Module, path: str,
+               inherited: QConfig | None) -> QConfig | None:
+    """The effective recipe of one module given its parent's."""
+    has_own, own = _own(module, path)
+    if has_own:
+        return own
+    ruled, qconfig = mapping.rule_for(type(module), path)
+    return qconfig if ruled else inherited
 
-    def children(self, module: Module, path: str, qconfig: QConfig | None) -> Iterator[Resolved]:
+
+def names_a_recipe(mapping: QConfigMapping, module: Module, path: str) -> bool:
+    """Whether a per-name / per-type rule names this module with a (non-None) recipe."""
+    ruled, qconfig = mapping.rule_for(type(module), path)
+    return ruled and qconfig is not None
+
+
+def plan_sites(model: Module, mapping: QConfigMapping, *, stock_default: bool = False) -> list[Site]:
+    """Every module of ``model`` once (a module reachable along two paths is taken at its
+    first), parents before children and children in registration order, each with its
+    resolved recipe."""
+    seed = mapping.global_qconfig()
+    if stock_default and any(hasattr(m, MARK) for m in model.modules()):
+        seed = None  # the user configured modules: the stock default does not fill in
+    sites: list[Site] = []
+    visited: set[int] = set()
+
+    def visit(parent: Module | None, attr: str, module: Module, path: str,
+              inherited: QConfig | None) -> None:
+        if id(module) in visited:
+            return
+        visited.add(id(module))
+        qconfig = recipe_for(mapping, module, path, inherited)
+        sites.append(Site(parent, attr, module, path, qconfig))
         for name, child in list(module.named_children()):
-            child_path = f"{path}.{name}" if path else name
-            yield Resolved(name, child, child_path, self.resolve(child, child_path, qconfig))
+            visit(module, name, child, f"{path}.{name}" if path else name, qconfig)
 
-    def walk(self, model: Module) -> Iterator[Resolved]:
-        seen: set[int] = set()
-        stack = [self.root(model)]
-        while stack:
-            entry = stack.pop()
-            if id(entry.module) in seen:
-                continue
-            seen.add(id(entry.module))
-            yield entry
-            stack.extend(reversed(list(self.children(entry.module, entry.path, entry.qconfig))))
+    visit(None, "", model, "", seed)
+    return sites
+
+
+def mark(sites: list[Site]) -> None:
+    """Write each site's recipe onto its module (``None`` marks an exclusion)."""
+    for site in sites:
+        setattr(site.module, MARK, site.qconfig)
+
+
+def clear_marks(model: Module) -> None:
+    """Remove every module's ``.qconfig`` attribute: after conversion the marks mean nothing,
+    and a later ``prepare`` would read leftovers as the user's own per-module choices."""
+    for module in model.modules():
+        module.__dict__.pop(MARK, None)
+
+
+# ------------------------------------------------------------------ quantize_dynamic specs
 
 
 def dynamic_qconfig(dtype: QDtype) -> QConfig:
+    """quantize_dynamic's recipe for weight dtype ``dtype``: a placeholder activation observer
+    (activations are quantized at run time) and a per-output-channel symmetric weight
+    observer on ``dtype``'s grid."""
     return QConfig(
         activation=PlaceholderObserver.with_args(qdtype=quint8),
         weight=PerChannelMinMaxObserver.with_args(ch_axis=0, qscheme=per_channel_symmetric,
@@ -101,48 +133,48 @@ def dynamic_qconfig(dtype: QDtype) -> QConfig:
 
 
 def weight_dtype(qconfig: QConfig, fallback: QDtype) -> QDtype:
-    found = getattr(qconfig.weight(), "qdtype", None)
-    return found if isinstance(found, QDtype) else fallback
+    """The weight grid a recipe asks for (its weight observer's ``qdtype``), else ``fallback``."""
+    qdtype = getattr(qconfig.weight(), "qdtype", None)
+    return qdtype if isinstance(qdtype, QDtype) else fallback
 
 
-class DynamicSpec(NamedTuple):
-    mapping: QConfigMapping
-    targets: tuple[str, ...]
-
-
-def _spec_value(key: object, value: object) -> QConfig | None:
-    if value is None or isinstance(value, QConfig):
-        return value
+def _recipe_of_value(key: object, value: object) -> QConfig | None:
     if isinstance(value, QDtype):
         return dynamic_qconfig(value)
+    if value is None or isinstance(value, QConfig):
+        return value
     raise TypeError(f"qconfig_spec[{key!r}] must be a QConfig, a QDtype or None; got "
                     f"{type(value).__name__}")
 
 
-def normalize_dynamic_spec(spec: object, dtype: QDtype,
-                           default_types: Collection[type]) -> DynamicSpec:
-    default = dynamic_qconfig(dtype)
+def dynamic_rules(spec: object, dtype: QDtype,
+                  default_types: Collection[type]) -> tuple[QConfigMapping, tuple[str, ...]]:
+    """``quantize_dynamic``'s ``qconfig_spec`` as a mapping, plus the sorted labels of what it
+    asks to quantize (for messages).  ``None`` targets ``default_types``; a collection of
+    module types and / or dotted names targets each with ``dtype``'s recipe; a dict pairs
+    each with a ``QConfig``, a ``QDtype`` or ``None`` (leave float)."""
     if spec is None:
-        entries = dict.fromkeys(default_types, default)
+        pairs = [(t, dynamic_qconfig(dtype)) for t in default_types]
     elif isinstance(spec, Mapping):
-        entries = {key: _spec_value(key, value) for key, value in spec.items()}
+        pairs = [(key, _recipe_of_value(key, value)) for key, value in spec.items()]
     elif isinstance(spec, Collection) and not isinstance(spec, (str, type)):
-        entries = dict.fromkeys(spec, default)
+        recipe = dynamic_qconfig(dtype)
+        pairs = [(key, recipe) for key in spec]
     else:
         raise TypeError("qconfig_spec must be a set of module types / names or a dict mapping "
                         f"them to a QConfig, a QDtype or None; got {type(spec).__name__}")
     mapping = QConfigMapping()
-    targets: list[str] = []
-    for key, qconfig in entries.items():
-        if isinstance(key, str):
-            mapping.set_module_name(key, qconfig)
-            label = key
-        elif isinstance(key, type) and issubclass(key, Module):
-            mapping.set_object_type(key, qconfig)
+    labels: list[str] = []
+    for key, recipe in pairs:
+        if isinstance(key, type) and issubclass(key, Module):
+            mapping.set_object_type(key, recipe)
             label = key.__name__
+        elif isinstance(key, str):
+            mapping.set_module_name(key, recipe)
+            label = key
         else:
             raise TypeError(f"qconfig_spec keys must be nn.Module subclasses or module names; "
                             f"got {key!r}")
-        if qconfig is not None:
-            targets.append(label)
-    return DynamicSpec(mapping, tuple(sorted(targets)))
+        if recipe is not None:
+            labels.append(label)
+    return mapping, tuple(sorted(labels))

@@ -22,8 +22,8 @@ import warnings
 from typing import Callable
 
 from lucid_amd.nn.module import Module
-from lucid_amd.quantization._propagate import (QConfigResolver, normalize_dynamic_spec,
-                                               weight_dtype)
+from lucid_amd.quantization._propagate import (Site, as_mapping, clear_marks, dynamic_rules,
+                                               mark, names_a_recipe, plan_sites, weight_dtype)
 from lucid_amd.quantization._qscheme import QDtype, qint8
 from lucid_amd.quantization.qconfig import QConfig, QConfigMapping, get_default_qconfig_mapping
 
@@ -122,29 +122,30 @@ def _mlx_dynamic_builder():
     return build
 
 
-def _make_observer_hook(obs: Module):
-    def hook(_module, _args, output):
-        obs(output)
-
-    return hook
+def _observe_outputs(module: Module, observer: Module) -> None:
+    """Give ``module`` its activation observer: kept as ``activation_post_process`` (so
+    ``convert`` finds the calibrated range) and fed every forward output by a hook."""
+    module.activation_post_process = observer
+    module.register_forward_hook(lambda _m, _args, output: observer(output))
 
 
 def prepare(model: Module, qconfig: QConfig | QConfigMapping | None = None,
             inplace: bool = False) -> Module:
-    """Attach activation observers to every quantizable module (static PTQ)."""
-    resolver = QConfigResolver.from_argument(qconfig, get_default_qconfig_mapping)
+    """Attach activation observers to every quantizable module (static PTQ).
+
+    Each module's recipe is resolved (own ``.qconfig`` > name rule > type rule > parent;
+    the stock default only for models the user has not configured) and written onto it as
+    ``.qconfig``; each observed type with a recipe gets its activation observer."""
+    mapping, stock = as_mapping(qconfig, get_default_qconfig_mapping)
     model = model if inplace else copy.deepcopy(model)
     model.eval()
+    sites = plan_sites(model, mapping, stock_default=stock)
+    mark(sites)
     observed = _observed_types()
-    n_matched = 0
-    for _name, mod, _path, qcfg in map(resolver.stamp, resolver.walk(model)):
-        if qcfg is None or not isinstance(mod, observed):
-            continue
-        obs = qcfg.activation()
-        mod.activation_post_process = obs
-        mod.register_forward_hook(_make_observer_hook(obs))
-        n_matched += 1
-    if n_matched == 0:
+    targets = [site for site in sites if site.qconfig is not None and isinstance(site.module, observed)]
+    for site in targets:
+        _observe_outputs(site.module, site.qconfig.activation())
+    if not targets:
         warnings.warn("prepare(): the QConfigMapping matched no quantizable modules -- "
                       "convert() will leave this model unchanged.", stacklevel=2)
     return model
@@ -178,7 +179,7 @@ def convert(model: Module, inplace: bool = False) -> Module:
         mapping[nn.Linear] = _mlx_linear_builder(relu=False)
         mapping[nni.LinearReLU] = _mlx_linear_builder(relu=True)
     _convert_recursive(model, mapping, always=(nnq.DeQuantStub, nn.Embedding, nn.EmbeddingBag))
-    QConfigResolver.strip(model)
+    clear_marks(model)
     model.eval()
     return model
 
@@ -196,53 +197,42 @@ def _dynamic_builders() -> dict:
     return builders
 
 
-class _DynamicSwapper:
-    def __init__(self, spec, mapping: dict, dtype: QDtype) -> None:
-        self.resolver = QConfigResolver(spec.mapping)
-        self._targets = spec.targets
-        self._mapping = mapping
-        self._dtype = dtype
-        self._swapped = 0
-        self._unmapped: set[type] = set()
+def _replace_dynamic(model: Module, mapping: QConfigMapping, labels: tuple[str, ...],
+                     builders: dict, dtype: QDtype) -> Module:
+    """Swap every planned site that has a recipe and a dynamic builder for its quantized form,
+    parents first (a replaced module's subtree is not visited); returns the (possibly new)
+    root.  Warns when a rule names a leaf module that has no dynamic form, or when nothing
+    at all was replaced."""
+    sites = plan_sites(model, mapping)
+    root = sites[0]
+    if root.qconfig is not None and type(model) in builders:
+        return builders[type(model)](model, weight_dtype(root.qconfig, dtype))
+    replaced: list[str] = []   # paths of replaced modules; their subtrees are skipped
+    stays_float: set[type] = set()
 
-    def apply(self, model: Module) -> Module:
-        swapped = self._swap(model)
-        QConfigResolver.strip(swapped)
-        return swapped
+    def under_replaced(site: Site) -> bool:
+        return any(site.path.startswith(p + ".") for p in replaced)
 
-    def _swap(self, model: Module) -> Module:
-        root = self.resolver.root(model)
-        if root.qconfig is not None and type(model) in self._mapping:
-            return self.build(model, root.qconfig)
-        self.swap_children(root)
-        self._warn_if_left_float()
-        return model
-
-    def build(self, module: Module, qconfig: QConfig) -> Module:
-        self._swapped += 1
-        return self._mapping[type(module)](module, weight_dtype(qconfig, self._dtype))
-
-    def swap_children(self, parent) -> None:
-        for entry in self.resolver.children(parent.module, parent.path, parent.qconfig):
-            if entry.qconfig is not None and type(entry.module) in self._mapping:
-                setattr(parent.module, entry.name, self.build(entry.module, entry.qconfig))
-                continue
-            if (entry.qconfig is not None and self.resolver.is_targeted(entry.module, entry.path)
-                    and next(entry.module.children(), None) is None):
-                self._unmapped.add(type(entry.module))
-            self.swap_children(entry)
-
-    def _warn_if_left_float(self) -> None:
-        if self._unmapped:
-            mapped = sorted(t.__name__ for t in self._mapping)
-            warnings.warn(
-                f"quantize_dynamic(): {', '.join(sorted(t.__name__ for t in self._unmapped))} "
-                "has no dynamically quantized form and stays float; dynamic quantization "
-                f"covers {', '.join(mapped)}.", stacklevel=5)
-        elif self._swapped == 0:
-            warnings.warn("quantize_dynamic(): no module of a targeted type "
-                          f"({', '.join(self._targets) or 'none'}) found -- the model is "
-                          "returned unchanged.", stacklevel=5)
+    for site in sites[1:]:
+        if under_replaced(site):
+            continue
+        build = builders.get(type(site.module))
+        if site.qconfig is not None and build is not None:
+            setattr(site.parent, site.attr, build(site.module, weight_dtype(site.qconfig, dtype)))
+            replaced.append(site.path)
+        elif (site.qconfig is not None and next(site.module.children(), None) is None
+              and names_a_recipe(mapping, site.module, site.path)):
+            stays_float.add(type(site.module))
+    if stays_float:
+        covered = ", ".join(sorted(t.__name__ for t in builders))
+        warnings.warn(f"quantize_dynamic(): {', '.join(sorted(t.__name__ for t in stays_float))} "
+                      "has no dynamically quantized form and stays float; dynamic quantization "
+                      f"covers {covered}.", stacklevel=3)
+    elif not replaced:
+        warnings.warn("quantize_dynamic(): no module of a targeted type "
+                      f"({', '.join(labels) or 'none'}) found -- the model is returned "
+                      "unchanged.", stacklevel=3)
+    return model
 
 
 def quantize_dynamic(model: Module, qconfig_spec=None, dtype: QDtype = qint8,
@@ -251,5 +241,7 @@ def quantize_dynamic(model: Module, qconfig_spec=None, dtype: QDtype = qint8,
     model = model if inplace else copy.deepcopy(model)
     model.eval()
     builders = _dynamic_builders()
-    spec = normalize_dynamic_spec(qconfig_spec, dtype, tuple(builders))
-    return _DynamicSwapper(spec, builders, dtype).apply(model)
+    mapping, labels = dynamic_rules(qconfig_spec, dtype, tuple(builders))
+    model = _replace_dynamic(model, mapping, labels, builders, dtype)
+    clear_marks(model)
+    return model

@@ -62,16 +62,17 @@ class QConfigMapping:
         return self
 
     def get_qconfig(self, module_type: type, module_name: str) -> QConfig | None:
-        if module_name in self._module_name:
-            return self._module_name[module_name]
-        if module_type in self._object_type:
-            return self._object_type[module_type]
-        return self._global
+        ruled, qconfig = self.rule_for(module_type, module_name)
+        return qconfig if ruled else self._global
 
-    def _has_rule(self, module_type: type, module_name: str) -> bool:
-        return module_name in self._module_name or module_type in self._object_type
+    def rule_for(self, module_type: type, module_name: str) -> tuple[bool, QConfig | None]:
+        """(whether a name or type rule covers the module, its recipe): name before type."""
+        for table, key in ((self._module_name, module_name), (self._object_type, module_type)):
+            if key in table:
+                return True, table[key]
+        return False, None
 
-    def _fallback(self) -> QConfig | None:
+    def global_qconfig(self) -> QConfig | None:
         return self._global
 
 

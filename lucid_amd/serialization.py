@@ -491,14 +491,14 @@ def load(f, map_location: object = None, pickle_module: object = None, *, weight
 # ------------------------------------------------------------------ sharded checkpoints
 
 
-def _as_directory(path: object, name: str) -> str:
-    if isinstance(path, bytes):
-        return path.decode()
-    if isinstance(path, str):
-        return path
-    if isinstance(path, os.PathLike):
-        return str(os.fspath(path))
-    raise TypeError(f"{name}() expects a directory path as str, bytes or os.PathLike, got {type(path).__name__}")
+def _directory_of(path: object, caller: str) -> str:
+    """The directory a sharded checkpoint lives in: a str, bytes or os.PathLike path, and
+    nothing else (anything at all can be str()-ed into a path name by mistake)."""
+    try:
+        return os.fsdecode(os.fspath(path))
+    except TypeError:
+        raise TypeError(f"{caller}() expects a directory path as str, bytes or os.PathLike, got "
+                        f"{type(path).__name__}") from None
 
 
 def _tensors_in(v: object, out: dict[int, Tensor], seen: set[int]) -> None:
@@ -551,77 +551,105 @@ def _shard_groups(obj: dict) -> list[tuple[list[str], int]]:
     return out
 
 
+_INDEX = "index.json"
+_SHARDED_TAG = "_lucid_sharded"
+
+
+def _shard_file(i: int, n: int) -> str:
+    return f"shard-{i:05d}-of-{n:05d}.lucid"
+
+
+def _plan_shards(obj: dict, cap_bytes: int) -> list[list[str]]:
+    """Keys per shard: key groups (keys reaching a shared tensor stay together) in first-key
+    order, a new shard opened whenever the next group would push a non-empty shard past the
+    cap (a group over the cap alone gets its own shard); at least one shard."""
+    plan: list[list[str]] = [[]]
+    used = 0
+    for keys, nbytes in _shard_groups(obj):
+        if plan[-1] and used + nbytes > cap_bytes:
+            plan.append([])
+            used = 0
+        plan[-1].extend(keys)
+        used += nbytes
+    return plan
+
+
+def _write_index(directory: str, doc: dict) -> None:
+    with open(os.path.join(directory, _INDEX), "w", encoding="utf-8") as fp:
+        json.dump(doc, fp, indent=2)
+
+
 def save_sharded(obj: object, path, *, shard_size_mb: float = 1024.0, pickle_protocol: int = 4) -> None:
-    """A checkpoint directory of ``shard-XXXXX-of-YYYYY.lucid`` files (each a ``save`` of part of
-    the state dict, keys first-fit up to ``shard_size_mb``, tied keys kept together) and an
-    ``index.json`` naming each shard's keys (lucid/serialization/__init__.py:646-744)."""
-    d = _as_directory(path, "save_sharded")
-    os.makedirs(d, exist_ok=True)
+    """A checkpoint directory of ``shard-XXXXX-of-YYYYY.lucid`` files, each a ``save`` of part of
+    a state dict, plus an ``index.json`` naming each shard's keys -- Lucid's sharded layout
+    (lucid/serialization/__init__.py:646-744).  Keys are packed first-fit up to
+    ``shard_size_mb``; keys that share a tensor stay in one shard.  A non-dict object is one
+    shard whose index entry lists no keys.  The index also carries the dict's key order when
+    packing moved a key, and its ``_metadata`` when that is JSON-serialisable."""
+    directory = _directory_of(path, "save_sharded")
+    os.makedirs(directory, exist_ok=True)
     if not isinstance(obj, dict):
-        fname = "shard-00000-of-00001.lucid"
-        save(obj, os.path.join(d, fname), pickle_protocol=pickle_protocol)
-        with open(os.path.join(d, "index.json"), "w", encoding="utf-8") as fp:
-            json.dump({"_lucid_sharded": 1, "shards": [{"file": fname, "keys": None}]}, fp, indent=2)
+        name = _shard_file(0, 1)
+        save(obj, os.path.join(directory, name), pickle_protocol=pickle_protocol)
+        _write_index(directory, {_SHARDED_TAG: 1, "shards": [{"file": name, "keys": None}]})
         return
-    limit = int(shard_size_mb * 1024 * 1024)
-    shards: list[dict] = []
-    cur: dict = {}
-    cur_bytes = 0
-    for keys, size in _shard_groups(obj):
-        if cur and cur_bytes + size > limit:
-            shards.append(cur)
-            cur, cur_bytes = {}, 0
-        for k in keys:
-            cur[k] = obj[k]
-        cur_bytes += size
-    if cur or not shards:
-        shards.append(cur)
-    entries = []
-    for i, part in enumerate(shards):
-        fname = f"shard-{i:05d}-of-{len(shards):05d}.lucid"
-        save(part, os.path.join(d, fname), pickle_protocol=pickle_protocol)
-        entries.append({"file": fname, "keys": list(part)})
-    index: dict[str, object] = {"_lucid_sharded": 1, "shards": entries}
-    if [k for part in shards for k in part] != list(obj):
-        index["key_order"] = list(obj)
+    plan = _plan_shards(obj, int(shard_size_mb * 1024 * 1024))
+    doc: dict[str, object] = {_SHARDED_TAG: 1, "shards": []}
+    for i, keys in enumerate(plan):
+        name = _shard_file(i, len(plan))
+        save({k: obj[k] for k in keys}, os.path.join(directory, name), pickle_protocol=pickle_protocol)
+        doc["shards"].append({"file": name, "keys": list(keys)})
+    order = list(obj)
+    if sum(plan, []) != order:
+        doc["key_order"] = order
     meta = getattr(obj, "_metadata", None)
     if meta is not None:
         try:
-            json.dumps(meta)
-            index["_state_dict_metadata"] = meta
+            doc["_state_dict_metadata"] = json.loads(json.dumps(meta))
         except (TypeError, ValueError):
-            pass
-    with open(os.path.join(d, "index.json"), "w", encoding="utf-8") as fp:
-        json.dump(index, fp, indent=2)
+            pass  # metadata that JSON cannot carry is left out
+    _write_index(directory, doc)
+
+
+def _read_index(directory: str) -> dict:
+    """A sharded checkpoint's index document, validated (tag, plain shard file names)."""
+    index_path = os.path.join(directory, _INDEX)
+    with open(index_path, encoding="utf-8") as fp:
+        doc = json.load(fp)
+    if not isinstance(doc, dict) or doc.get(_SHARDED_TAG) != 1:
+        raise RuntimeError(f"{index_path!r} is not a valid Lucid sharded checkpoint index")
+    entries = doc["shards"]
+    for entry in entries:  # shard files stay inside the directory
+        name = str(entry["file"])
+        if name in ("", ".", "..") or os.path.basename(name) != name:
+            raise RuntimeError(f"{index_path!r}: shard file {name!r} is not a plain file name")
+    return doc
 
 
 def load_sharded(path, *, map_location: object = None, weights_only: bool = True) -> object:
-    """Read a directory written by ``save_sharded`` (or Lucid's) into one ordered state dict
-    (lucid/serialization/__init__.py:746-830)."""
+    """Read a directory written by ``save_sharded`` (or by Lucid) back into one ordered state
+    dict -- shards in index order, the recorded key order and metadata restored -- or the
+    single object of a key-less one-shard index (lucid/serialization/__init__.py:746-830)."""
     from collections import OrderedDict
 
-    d = _as_directory(path, "load_sharded")
-    index_path = os.path.join(d, "index.json")
-    with open(index_path, encoding="utf-8") as fp:
-        index = json.load(fp)
-    if not isinstance(index, dict) or index.get("_lucid_sharded") != 1:
-        raise RuntimeError(f"{index_path!r} is not a valid Lucid sharded checkpoint index")
-    entries = index["shards"]
-    for e in entries:  # shard files stay inside the directory
-        f = str(e["file"])
-        if os.path.basename(f) != f or f in ("", ".", ".."):
-            raise RuntimeError(f"{index_path!r}: shard file {f!r} is not a plain file name")
+    directory = _directory_of(path, "load_sharded")
+    doc = _read_index(directory)
+    entries = doc["shards"]
+
+    def read(entry: dict) -> object:
+        return load(os.path.join(directory, str(entry["file"])), map_location=map_location,
+                    weights_only=weights_only)
+
     if len(entries) == 1 and entries[0].get("keys") is None:
-        return load(os.path.join(d, str(entries[0]["file"])), map_location=map_location, weights_only=weights_only)
-    result: OrderedDict = OrderedDict()
-    for e in entries:
-        part = load(os.path.join(d, str(e["file"])), map_location=map_location, weights_only=weights_only)
+        return read(entries[0])
+    merged: OrderedDict = OrderedDict()
+    for part in map(read, entries):
         if isinstance(part, dict):
-            result.update(part)
-    order = index.get("key_order")
-    if isinstance(order, list) and set(order) == set(result):
-        result = OrderedDict((k, result[k]) for k in order)
-    meta = index.get("_state_dict_metadata")
+            merged.update(part)
+    order = doc.get("key_order")
+    if isinstance(order, list) and set(order) == set(merged):
+        merged = OrderedDict((k, merged[k]) for k in order)
+    meta = doc.get("_state_dict_metadata")
     if isinstance(meta, dict):
-        result._metadata = meta
-    return result
+        merged._metadata = meta
+    return merged

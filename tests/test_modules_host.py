@@ -134,17 +134,97 @@ def test_engine_selector():
 def test_dynamic_spec_normalisation():
     import lucid_amd.nn as nn
     from lucid_amd.quantization import qint8
-    from lucid_amd.quantization._propagate import normalize_dynamic_spec, weight_dtype
+    from lucid_amd.quantization._propagate import dynamic_rules, weight_dtype
 
-    spec = normalize_dynamic_spec({nn.Linear: qint8, "head": None}, qint8, (nn.Linear,))
-    assert spec.targets == ("Linear",)
-    assert spec.mapping.get_qconfig(nn.Linear, "x") is not None
-    assert spec.mapping.get_qconfig(nn.Linear, "head") is None
-    assert weight_dtype(spec.mapping.get_qconfig(nn.Linear, "x"), None) is qint8
-    with pytest.raises(TypeError):
-        normalize_dynamic_spec("Linear", qint8, (nn.Linear,))
-    with pytest.raises(TypeError):
-        normalize_dynamic_spec({3: qint8}, qint8, (nn.Linear,))
+    mapping, labels = dynamic_rules({nn.Linear: qint8, "head": None}, qint8, (nn.Linear,))
+    assert labels == ("Linear",)
+    assert mapping.get_qconfig(nn.Linear, "x") is not None
+    assert mapping.get_qconfig(nn.Linear, "head") is None
+    assert weight_dtype(mapping.get_qconfig(nn.Linear, "x"), None) is qint8
+    with pytest.raises(TypeError, match="qconfig_spec must be"):
+        dynamic_rules("Linear", qint8, (nn.Linear,))
+    with pytest.raises(TypeError, match="keys must be"):
+        dynamic_rules({3: qint8}, qint8, (nn.Linear,))
+    with pytest.raises(TypeError, match=r"qconfig_spec\['head'\] must be"):
+        dynamic_rules({"head": 3.0}, qint8, (nn.Linear,))
+
+
+def test_resolution_tiers_and_inheritance():
+    """Own .qconfig > name rule > type rule > parent; the root takes the global recipe, except
+    under the stock default when the user has configured modules."""
+    import lucid_amd.nn as nn
+    import lucid_amd.quantization as Q
+    from lucid_amd.quantization._propagate import plan_sites
+
+    a, b = Q.get_minmax_qconfig(), Q.get_default_qconfig()
+    inner = nn.Sequential(nn.Linear(4, 4), nn.ReLU())
+    model = nn.Sequential(nn.Linear(4, 4), inner, nn.Linear(4, 2))
+    mapping = Q.QConfigMapping().set_global(a).set_object_type(nn.ReLU, None).set_module_name("2", b)
+    got = {s.path: s.qconfig for s in plan_sites(model, mapping)}
+    assert got[""] is a and got["0"] is a and got["1"] is a and got["1.0"] is a
+    assert got["1.1"] is None and got["2"] is b
+    # a name rule beats a type rule for the same module
+    mapping.set_object_type(nn.Linear, None)
+    got = {s.path: s.qconfig for s in plan_sites(model, mapping)}
+    assert got["0"] is None and got["1.0"] is None and got["2"] is b
+    # a module's own attribute beats both; its children inherit it
+    inner.qconfig = b
+    got = {s.path: s.qconfig for s in plan_sites(model, Q.QConfigMapping().set_global(a))}
+    assert got["1"] is b and got["1.0"] is b and got["0"] is a
+    # the stock default does not fill in around user-configured modules
+    got = {s.path: s.qconfig for s in plan_sites(model, Q.QConfigMapping().set_global(a), stock_default=True)}
+    assert got[""] is None and got["0"] is None and got["1"] is b
+    del inner.qconfig
+    # a module shared along two paths is planned once, at its first occurrence
+    shared = nn.Linear(4, 4)
+    twice = nn.Sequential(shared, nn.Sequential(shared))
+    paths = [s.path for s in plan_sites(twice, Q.QConfigMapping())]
+    assert paths == ["", "0", "1"]
+    with pytest.raises(TypeError, match="qconfig must be a QConfig or None"):
+        inner.qconfig = "x"
+        plan_sites(model, Q.QConfigMapping())
+
+
+def test_quantize_dynamic_replacement_and_warnings():
+    """The dynamic swap's walk with stand-in builders (no GPU): the root itself may be
+    replaced; nested targets are; a replaced module's subtree is left alone; a named leaf
+    without a dynamic form warns that it stays float; nothing targeted warns the model is
+    unchanged."""
+    import lucid_amd.nn as nn
+    from lucid_amd.nn.module import Module
+    from lucid_amd.quantization import qint8
+    from lucid_amd.quantization._propagate import dynamic_rules
+    from lucid_amd.quantization._quantize import _replace_dynamic
+
+    class Swapped(Module):
+        def __init__(self, src, dtype):
+            super().__init__()
+            self.src, self.dtype = src, dtype
+
+    class Block(Module):  # a container type with a builder: replaced whole
+        def __init__(self):
+            super().__init__()
+            self.lin = nn.Linear(8, 8)
+
+    builders = {nn.Linear: Swapped, Block: Swapped}
+
+    def run(model, spec):
+        mapping, labels = dynamic_rules(spec, qint8, tuple(builders))
+        return _replace_dynamic(model, mapping, labels, builders, qint8)
+
+    root = nn.Linear(8, 4)
+    assert isinstance(run(root, None), Swapped)
+    model = nn.Sequential(nn.Linear(8, 8), nn.Sequential(nn.ReLU(), nn.Linear(8, 4)), Block())
+    out = run(model, {nn.Linear, Block})
+    assert out is model and isinstance(model[0], Swapped) and isinstance(model[1][1], Swapped)
+    assert isinstance(model[2], Swapped) and isinstance(model[2].src.lin, nn.Linear)  # subtree kept
+    model = nn.Sequential(nn.Linear(8, 8), nn.Sequential(nn.ReLU(), nn.Linear(8, 4)))
+    run(model, {"1.1": None, nn.Linear: qint8})  # a name rule beats the type rule
+    assert isinstance(model[0], Swapped) and isinstance(model[1][1], nn.Linear)
+    with pytest.warns(UserWarning, match="ReLU has no dynamically quantized form"):
+        run(nn.Sequential(nn.ReLU(), nn.Linear(2, 2)), {nn.ReLU})
+    with pytest.warns(UserWarning, match=r"no module of a targeted type \(Conv2d\) found"):
+        run(nn.Sequential(nn.ReLU()), {nn.Conv2d})
 
 
 def test_quantized_module_state_dict_layouts():
