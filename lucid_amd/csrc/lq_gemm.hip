@@ -21,6 +21,7 @@
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
+#include <algorithm>
 #include <mutex>
 #include <string>
 #include <type_traits>
@@ -895,12 +896,156 @@ __global__ __launch_bounds__(64 * W) void gemm_i8_packed_skinny_kernel(GemmArgs 
     for (int mt = 0; mt < MT; ++mt) epilogue4<KIND>(a, p, mt * 16 + (lane & 15), n, acc[mt]);
 }
 
+// ----------------------------------------- packed weights, 64 < M <= 128 (decode)
+//
+// The skinny kernel above keeps A's fragments in registers next to the weight stream; at
+// M = 128 that leaves room for two 1 KB weight loads in flight per wave and re-reads all of
+// A per 16 columns, so it waits on latency.  Here a workgroup owns 64 columns (one 16-column
+// n-tile per wave) and one K-split (gridDim.y): the split's A slice (M rows x up to 1 KB) is
+// staged once in LDS and shared by the four waves, and each wave issues every weight k-step
+// of its split at once (up to 16 KB in flight).  Chunk c of A row r sits at chunk slot
+// c ^ (r % 16) of the row, so the 16 rows a fragment read touches fall in 16 different bank
+// groups.  Each split stores its exact int32 partial sums to the workspace
+// ([split][m][n], rows padded to whole n-tiles); gemm_i8_decode_reduce_kernel adds the splits
+// in order and runs the epilogue.
+
+constexpr int DEC_MAX_KS = 8;  // k-steps (64 B) per split at most: a 512 B A row slice
+
+struct DecodePlan {
+    int ks_per_split, splits;
+    int64_t npad;  // partial row pitch (whole 16-column n-tiles)
+};
+
+static DecodePlan decode_plan(int64_t M, int64_t N, int64_t K) {
+    (void)M;
+    DecodePlan p;
+    const int64_t KS = (K + 63) / 64, tiles64 = (N + 63) / 64;
+    p.ks_per_split = DEC_MAX_KS;
+    p.splits = (int)((KS + p.ks_per_split - 1) / p.ks_per_split);
+    // at least 256 workgroups when K allows (whole groups of 4 k-steps per split)
+    while (tiles64 * p.splits < 256 && p.ks_per_split > 4) {
+        p.ks_per_split -= 4;
+        p.splits = (int)((KS + p.ks_per_split - 1) / p.ks_per_split);
+    }
+    if (p.splits < 1) p.splits = 1;
+    p.npad = (N + 15) / 16 * 16;
+    return p;
+}
+
+// M from which the packed path takes the split-K decode kernel (below it the skinny kernel,
+// whose per-16-column re-read of A is small).
+constexpr int DEC_MIN_M = 33;
+
+static size_t decode_partial_bytes(int64_t M, int64_t N, int64_t K) {
+    if (M < DEC_MIN_M || M > 128) return 0;
+    const DecodePlan p = decode_plan(M, N, K);
+    return sizeof(int32_t) * (size_t)p.splits * (size_t)M * (size_t)p.npad;
+}
+
+template <int MT>
+__global__ __launch_bounds__(256) void gemm_i8_decode_partial_kernel(GemmArgs a, int ks_per_split, int64_t npad,
+                                                                      int32_t* __restrict__ part) {
+    __shared__ __attribute__((aligned(1024))) int8_t As[MT * 16 * DEC_MAX_KS * 64];
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int KS = (a.K + 63) / 64;
+    const int split = blockIdx.y;
+    const int ks0 = split * ks_per_split, nks = min(KS - ks0, ks_per_split);  // >= 1 by the plan
+    const int slots = ks_per_split * 4;  // 16-byte chunk slots per A row in LDS (a multiple of 16)
+    // This wave's share of the A slice goes straight into LDS first, then its weight k-steps
+    // (exactly DEC_MAX_KS loads, steps past the split clamped to its last): vmcnt counts both
+    // in issue order, so vmcnt(DEC_MAX_KS) means this wave's A copies have landed while the
+    // weights are still streaming, and each k-step below starts as soon as its weight is in.
+    // A slice: MT*16 rows x `slots` chunks, copied 64 chunks (1 KB) per wave instruction.
+    // LDS slot g = row * slots + s holds global chunk c = s ^ (row % 16) of the row (rows
+    // past M read as zeros through the buffer bound; chunks past the split's K are never read).
+    const v4i ra = buffer_rsrc(a.A, (uint32_t)((int64_t)a.M * a.lda));
+    const uint32_t lds_base = (uint32_t)reinterpret_cast<uintptr_t>(As);
+    const int copies = MT * 16 * slots / 64;
+    for (int q = wave; q < copies; q += 4) {
+        const int g = q * 64 + lane, r = g / slots, sl = g - r * slots;
+        const uint32_t voff = (uint32_t)r * (uint32_t)a.lda + (uint32_t)((ks0 * 4 + (sl ^ (r & 15))) * 16);
+        lds_dma16(ra, voff, 0u, lds_base + (uint32_t)q * 1024u);
+    }
+    const int t = blockIdx.x * 4 + wave;  // this wave's 16-column n-tile
+    const bool has_tile = t * 16 < a.N;
+    const int tc = has_tile ? t : 0;      // a valid tile to read when this wave has none
+    const int8_t* bt = a.B + ((int64_t)tc * KS + ks0) * PACK_TILE + lane * 16;
+    v4i bf[DEC_MAX_KS];
+#pragma unroll
+    for (int j = 0; j < DEC_MAX_KS; ++j)
+        bf[j] = __builtin_nontemporal_load(reinterpret_cast<const v4i*>(bt + (int64_t)min(j, nks - 1) * PACK_TILE));
+    wait_vmcnt<DEC_MAX_KS>();
+    block_barrier();  // every wave's A copies have landed (no fence: the weights keep streaming)
+    if (!has_tile) {
+        wait_vmcnt<0>();  // no load may be in flight when the wave ends
+        return;
+    }
+    v4i acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
+    const int rl = lane & 15, cq = lane >> 4;
+#pragma unroll
+    for (int j = 0; j < DEC_MAX_KS; ++j) {
+        if (j < nks) {  // wave-uniform; a predicate, not a break, keeps bf[] in registers
+            const int c = j * 4 + cq;
+            v4i af[MT];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int r = mt * 16 + rl;
+                af[mt] = *reinterpret_cast<const v4i*>(As + (r * slots + (c ^ (r & 15))) * 16);
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+                acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[j], af[mt], acc[mt], 0, 0, 0);
+        }
+    }
+    // lane l holds C[m = 16 mt + l % 16][n = 16 t + 4 (l / 16) .. +3]
+    const int n = t * 16 + cq * 4;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+        const int m = mt * 16 + rl;
+        if (m < a.M) *reinterpret_cast<v4i*>(part + ((int64_t)split * a.M + m) * npad + n) = acc[mt];
+    }
+}
+
+template <int KIND>
+__global__ __launch_bounds__(256) void gemm_i8_decode_reduce_kernel(GemmArgs a, int splits, int64_t npad,
+                                                                     const int32_t* __restrict__ part) {
+    const int64_t q = (int64_t)blockIdx.x * 256 + threadIdx.x;  // one quad of 4 columns
+    const int64_t quads = npad / 4;
+    if (q >= (int64_t)a.M * quads) return;
+    const int m = (int)(q / quads), n = (int)(q - (int64_t)m * quads) * 4;
+    if (n >= a.N) return;
+    v4i acc = v4i{0, 0, 0, 0};
+    for (int s = 0; s < splits; ++s) acc += *reinterpret_cast<const v4i*>(part + ((int64_t)s * a.M + m) * npad + n);
+    epilogue4<KIND>(a, epi_params(a), m, n, acc);
+}
+
 template <int KIND>
 static int launch_packed_skinny(const GemmArgs& a, hipStream_t st) {
     const unsigned tiles = (unsigned)((a.N + 15) / 16);
     if (a.M <= 16)
         hipLaunchKernelGGL((gemm_i8_packed_skinny_kernel<1, 4, 16, KIND>), dim3(tiles), dim3(256), 0, st, a);
-    else if (a.M <= 32)
+    else if (a.partial != nullptr) {
+        const DecodePlan p = decode_plan(a.M, a.N, a.K);
+        const dim3 grid((unsigned)((a.N + 63) / 64), (unsigned)p.splits);
+        if (a.M <= 32)
+            hipLaunchKernelGGL((gemm_i8_decode_partial_kernel<2>), grid, dim3(256), 0, st, a, p.ks_per_split, p.npad,
+                               a.partial);
+        else if (a.M <= 64)
+            hipLaunchKernelGGL((gemm_i8_decode_partial_kernel<4>), grid, dim3(256), 0, st, a, p.ks_per_split, p.npad,
+                               a.partial);
+        else
+            hipLaunchKernelGGL((gemm_i8_decode_partial_kernel<8>), grid, dim3(256), 0, st, a, p.ks_per_split, p.npad,
+                               a.partial);
+        const int64_t quads = (int64_t)a.M * (p.npad / 4);
+        hipLaunchKernelGGL((gemm_i8_decode_reduce_kernel<KIND>), dim3((unsigned)((quads + 255) / 256)), dim3(256), 0,
+                           st, a, p.splits, p.npad, a.partial);
+        note_path(a.M <= 32 ? "gemm packed decode m32 split-k" : a.M <= 64 ? "gemm packed decode m64 split-k"
+                            : "gemm packed decode m128 split-k");
+        return launch_status("lq_gemm_w8a8_packed (decode)");
+    } else if (a.M <= 32)
         hipLaunchKernelGGL((gemm_i8_packed_skinny_kernel<2, 4, 8, KIND>), dim3(tiles), dim3(256), 0, st, a);
     else if (a.M <= 64)
         hipLaunchKernelGGL((gemm_i8_packed_skinny_kernel<4, 4, 4, KIND>), dim3(tiles), dim3(256), 0, st, a);
@@ -1033,13 +1178,17 @@ struct GemmWs {
     size_t a_sums, b_sums, partial, counters, total;
 };
 static size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
-static GemmWs gemm_ws(int64_t M, int64_t N) {
+static GemmWs gemm_ws(int64_t M, int64_t N, int64_t K) {
     GemmWs w;
     w.a_sums = 0;
     w.b_sums = w.a_sums + align256(sizeof(int32_t) * (size_t)M);
     w.partial = w.b_sums + align256(sizeof(int32_t) * (size_t)N);
+    // split-K partials: the row-major path's [M, N] sums, or the packed decode path's
+    // per-split sums (64 < M <= 128); the region serves whichever the call takes
     const bool may_split = M > 64 && ((M + 127) / 128) * ((N + 127) / 128) < 256;
-    w.counters = w.partial + (may_split ? align256(sizeof(int32_t) * (size_t)(M * N)) : 0);
+    size_t part = may_split ? sizeof(int32_t) * (size_t)(M * N) : 0;
+    part = std::max(part, decode_partial_bytes(M, N, K));
+    w.counters = w.partial + align256(part);
     const size_t tiles = (size_t)(((M + 127) / 128) * ((N + 127) / 128));
     w.total = w.counters + (may_split ? align256(sizeof(uint32_t) * tiles) : 0);
     return w;
@@ -1081,9 +1230,8 @@ int lq_pack_weights_i8(const int8_t* d_B, int64_t ldb, int64_t N, int64_t K, int
 }
 
 size_t lq_gemm_w8a8_workspace_size(int64_t M, int64_t N, int64_t K) {
-    (void)K;
-    if (M < 0 || N < 0) return 0;
-    return gemm_ws(M, N).total;
+    if (M < 0 || N < 0 || K < 0) return 0;
+    return gemm_ws(M, N, K).total;
 }
 
 }  // extern "C"
@@ -1120,7 +1268,7 @@ static int gemm_entry(bool packed, const int8_t* d_A, int64_t lda, const int8_t*
         LQ_REQUIRE(!has_za || d_b_sums,
                    "lq_gemm_w8a8_packed: an activation zero point needs the cached weight sums d_b_sums");
     }
-    const GemmWs ws = gemm_ws(M, N);
+    const GemmWs ws = gemm_ws(M, N, K);
     LQ_REQUIRE(d_workspace || workspace_bytes == 0, "lq_gemm_w8a8: NULL workspace with nonzero size");
     const bool need_asums = d_b_zero_point != nullptr;
     const bool need_bsums = has_za && d_b_sums == nullptr;
@@ -1169,6 +1317,9 @@ static int gemm_entry(bool packed, const int8_t* d_A, int64_t lda, const int8_t*
         }
     }
     if (packed) {
+        if (M >= DEC_MIN_M && d_workspace && workspace_bytes >= ws.counters &&
+            ws.counters - ws.partial >= decode_partial_bytes(M, N, K) && (int64_t)M * lda < ((int64_t)1 << 31))
+            a.partial = (int32_t*)(wsb + ws.partial);
         switch (out_kind) {
         case LQ_OUT_I32: return launch_packed_skinny<LQ_OUT_I32>(a, st);
         case LQ_OUT_F32: return launch_packed_skinny<LQ_OUT_F32>(a, st);

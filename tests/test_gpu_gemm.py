@@ -333,3 +333,38 @@ def test_baseline_sizes_checksums(gpu, M, N, K):
     np.testing.assert_array_equal(C.sum(axis=0), B64 @ A64.sum(axis=0))
     rows = rng.choice(M, min(M, 24), replace=False)
     np.testing.assert_array_equal(C[rows], A64[rows] @ B64.T)
+
+
+@pytest.mark.parametrize("M,N,K", [(17, 70, 272), (32, 4096, 4096), (33, 4100, 4096), (64, 1000, 784),
+                                   (65, 1000, 1040), (100, 300, 256), (128, 4096, 4096), (128, 11008, 4096),
+                                   (96, 512, 11008)])
+def test_packed_decode_split_k_exact(gpu, M, N, K):
+    """33 <= M <= 128 with the packed weight and a workspace: the split-K decode kernel (A's
+    K-slice staged in LDS, per-split int32 partials, ordered reduction + epilogue) -- ragged
+    N, K not a multiple of 64, several splits -- bit-exact for the int32 sums and the
+    requantized codes, with and without an activation zero point; M <= 32 stays on the
+    skinny kernel."""
+    from lucid_amd import _C
+
+    rng = np.random.default_rng(M * 3 + N + K)
+    A = _codes(rng, (M, K), -128, 127)
+    B = _codes(rng, (N, K))
+    C = run_gemm(gpu, A, B, packed=True)
+    assert _C.last_path().startswith("gemm packed decode" if M >= 33 else "gemm packed skinny")
+    np.testing.assert_array_equal(C, O.gemm_acc(A, B))
+    a_scale = rng.uniform(1e-3, 1e-1, M).astype(np.float32)
+    b_scale = rng.uniform(1e-3, 1e-1, N).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    sums = B.astype(np.int64).sum(axis=1).astype(np.int32)
+    for za, kind in ((None, O.OUT_Q8), (-7.0, O.OUT_QU8S8), (3.0, O.OUT_F16)):
+        qmin, qmax = GRID.get(kind, (-128, 127))
+        got = run_gemm(gpu, A, B, kind, a_scale, b_scale, za=za, b_sums=sums if za is not None else None,
+                       bias=bias, out_scale=0.37, out_zp=(128.0 if qmin == 0 else 3.0), qmin=qmin,
+                       qmax=qmax, relu=True, packed=True)
+        want = O.gemm_w8a8(A, B, a_scale, b_scale, za=0.0 if za is None else za, bias=bias,
+                           out_scale=0.37, out_zp=(128.0 if qmin == 0 else 3.0), qmin=qmin, qmax=qmax,
+                           out_kind=kind, relu=True)
+        if kind == O.OUT_F16:
+            np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+        else:
+            np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8))
