@@ -429,6 +429,254 @@ def lookup_lines(L, C, timer, steps, warmup):
     return out
 
 
+def _event_ms(C, stream, fn) -> float:
+    """Milliseconds between HIP events on ``stream`` around ``fn()``'s launches."""
+    e0, e1 = ctypes.c_void_p(), ctypes.c_void_p()
+    C.call("lq_event_create", ctypes.byref(e0))
+    C.call("lq_event_create", ctypes.byref(e1))
+    C.call("lq_event_record", e0, stream)
+    fn()
+    C.call("lq_event_record", e1, stream)
+    C.call("lq_event_synchronize", e1)
+    ms = ctypes.c_float()
+    C.call("lq_event_elapsed_ms", ctypes.byref(ms), e0, e1)
+    C.call("lq_event_destroy", e0)
+    C.call("lq_event_destroy", e1)
+    return ms.value
+
+
+def model_lines(L, C, gtimer, with_cpu: bool) -> dict:
+    """BASELINE configurations 1, 4 and 5 end to end (random-init weights of the configured
+    architectures, synthetic inputs), each beside Lucid's CPU composition of the same work."""
+    import lucid_amd.backends as backends
+    import lucid_amd.nn as nn
+    from lucid_amd import bench_configs as bc
+    from lucid_amd.quantization import quantize_dynamic
+
+    out = {}
+    sync = C.synchronize
+    st = gtimer.stream
+    backends.quantized.engine = "reference"  # the per-channel int8 layers of the configs
+    try:
+        # ---- config 1: dynamic int8 MLP 784 -> 256 -> ReLU -> 10, batch 64
+        rng = np.random.default_rng(2024)
+        lins = []
+        for k, n in ((784, 256), (256, 10)):
+            m = nn.Linear(k, n)
+            m.weight = nn.Parameter(L.tensor(rng.normal(0, 0.05, (n, k)).astype(np.float32)))
+            m.bias = nn.Parameter(L.tensor(rng.normal(0, 0.05, n).astype(np.float32)))
+            lins.append(m)
+        qmlp = quantize_dynamic(nn.Sequential(lins[0], nn.ReLU(), lins[1]))
+        x = L.tensor(rng.standard_normal((64, 784)).astype(np.float32), device="gpu")
+        module = warm_stats(lambda: qmlp(x), 5, 20, sync)
+        l0, l1 = bc.DynLinear(qmlp[0], 64), bc.DynLinear(qmlp[2], 64)
+        hbuf = L.empty((64, 256), np.float32, "gpu")
+        ybuf = L.empty((64, 10), np.float32, "gpu")
+
+        def mlp_calls(s_):
+            l0(x.data_ptr(), 64, hbuf.data_ptr(), s_)
+            C.call("lq_relu_f32", hbuf.data_ptr(), hbuf.data_ptr(), 64 * 256, s_)
+            l1(hbuf.data_ptr(), 64, ybuf.data_ptr(), s_)
+
+        graph_ms = gtimer.time_ms([mlp_calls], 200, 10)
+        c1 = {"workload": "config 1: dynamic int8 MLP 784-256-10, batch 64, fp32 out",
+              "module_forward_ms": module, "graph_replay_us": round(graph_ms * 1e3, 2),
+              "ops": 2.0 * 64 * (784 * 256 + 256 * 10)}
+        if with_cpu:
+            import oracle.lucid_models as LM
+
+            w = [(m.weight_int8.numpy(), m.weight_scale.numpy(), m.weight_zero_point.numpy(), m.bias.numpy())
+                 for m in (qmlp[0], qmlp[2])]
+            xh = x.numpy()
+            c1["cpu"] = cpu_leg(lambda: LM.mlp_forward(xh, w), 5, 20, 1.0, "forwards/s",
+                                "Lucid's dynamic-MLP composition on the same weights and input")
+        out["config1_mlp"] = c1
+        del qmlp, l0, l1
+
+        # ---- config 4: int8-dynamic decoder, batch 8, prefill 512, 128 greedy steps
+        rng = np.random.default_rng(44)
+        dec, glue = bc.decoder(rng)
+        qdec = quantize_dynamic(dec)
+        del dec
+        rt = bc.Int8Decoder(qdec, glue)
+        rt.set_prompt(rng.integers(0, bc.VOCAB, (bc.BATCH, bc.PREFILL)))
+        g_pre = bc.Graph(rt.prefill, st)
+        g_dec = bc.Graph(rt.decode, st)
+        for _ in range(2):
+            g_pre.launch()
+        C.call("lq_stream_synchronize", st)
+        pre = sorted(_event_ms(C, st, g_pre.launch) for _ in range(5))
+        dec_ms = []
+        for _ in range(3):
+            g_pre.launch()
+
+            def run_decode():
+                for _ in range(bc.DECODE):
+                    g_dec.launch()
+
+            dec_ms.append(_event_ms(C, st, run_decode))
+        dec_ms.sort()
+        tok = bc.BATCH * bc.DECODE
+        c4 = {"workload": "config 4: int8-dynamic decoder (6 layers, d 512, 8 heads, FFN 2048, vocab 32000), "
+                          "batch 8, prefill 512 then 128 greedy steps; fp16 attention; graph replay per step",
+              "prefill_ms": round(pre[len(pre) // 2], 3), "prefill_tokens_per_s": round(bc.BATCH * bc.PREFILL / (pre[len(pre) // 2] * 1e-3), 1),
+              "decode_ms_per_step": round(dec_ms[1] / bc.DECODE, 4),
+              "decode_tokens_per_s": round(tok / (dec_ms[1] * 1e-3), 1)}
+        if with_cpu:
+            import oracle.lucid_models as LM
+
+            cd = LM.Decoder(np.random.default_rng(4))
+            prompt = np.random.default_rng(5).integers(0, 32000, (bc.BATCH, bc.PREFILL))
+            t0 = time.perf_counter()
+            nxt = cd.step(prompt, 0)
+            pre_s = time.perf_counter() - t0
+            steps = []
+            for i in range(3):
+                t0 = time.perf_counter()
+                nxt = cd.step(nxt[:, None], bc.PREFILL + i)
+                steps.append(time.perf_counter() - t0)
+            c4["cpu"] = {"prefill_ms": round(pre_s * 1e3, 1), "decode_tokens_per_s": round(bc.BATCH / sorted(steps)[1], 2),
+                         "cores": host_threads(), "unit": "tokens/s",
+                         "sample": "one prefill of 8 x 512 and 3 decode steps of Lucid's composition (dequantize "
+                                   "every weight per call, sgemm, fake-quant; float32 attention and glue), "
+                                   "synthetic weights of the decoder's shapes"}
+        out["config4_decoder"] = c4
+        del rt, g_pre, g_dec, qdec
+
+        # ---- config 5: static int8 ResNet-18, batch 32 at 224 x 224
+        import lucid_amd.quantization as Q
+        from lucid_amd.nn.layers import manual_seed
+
+        manual_seed(5)
+        rng = np.random.default_rng(5)
+        model = bc.resnet18(rng)
+        fused = Q.fuse_modules(model, bc.resnet18_fuse_groups()).to("gpu")
+        prepared = Q.prepare(fused, Q.get_minmax_qconfig())
+        for _ in range(16):
+            prepared(L.tensor(rng.standard_normal((32, 3, 224, 224)).astype(np.float32), device="gpu"))
+        qnet = Q.convert(prepared)
+        del model, fused, prepared
+        x = L.tensor(rng.standard_normal((32, 3, 224, 224)).astype(np.float32), device="gpu")
+        fwd = warm_stats(lambda: qnet(x), 3, 10, sync)
+        c5 = {"workload": "config 5: static int8 ResNet-18 (BN folded, per-channel int8 weights, uint8 "
+                          "activations from 16 calibration batches), batch 32 at 224 x 224",
+              "forward_ms": fwd, "images_per_s": round(32 / (fwd["median"] * 1e-3), 1)}
+        if with_cpu:
+            import oracle.lucid_models as LM
+
+            stack = LM.resnet18_conv_stack(np.random.default_rng(6), 2)
+
+            def convs():
+                for xin, w, stride, pad in stack:
+                    LM.conv_layer(xin, w, stride, pad, True, (0.05, 128))
+
+            c5["cpu"] = cpu_leg(convs, 1, 3, 2.0, "images/s",
+                                "the 20 convolutions of ResNet-18 at batch 2 in Lucid's composition (dequantized "
+                                "weight, im2col + sgemm, bias, ReLU, fake-quant), pooling and fc left out",
+                                one_thread=False)
+        out["config5_resnet18"] = c5
+    finally:
+        backends.quantized.engine = "auto"
+    return out
+
+
+def cpu_micro_legs() -> dict:
+    """Lucid's CPU composition of the bandwidth kernels (2^24 fp32 elements) and the decode
+    GEMV (1 x 4096 x 4096: dequantize the weight every call, then sgemv), on all host
+    threads and on one."""
+    import oracle as O
+    import oracle.lucid_models as LM
+
+    n = 1 << 24
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal(n, dtype=np.float32)
+    q = np.empty(n, np.int8)
+    y = np.empty(n, np.float32)
+    t0, t1 = np.empty(n, np.float32), np.empty(n, np.float32)
+    inv = float(np.float32(1.0) / np.float32(0.05))
+    O.lucid_quantize(x, inv, 0.0, -128, 127, q, t0, t1)
+    out = {"cpu_model": cpu_model(), "host_cpus": os.cpu_count()}
+    out["minmax_observer"] = cpu_leg(lambda: O.lucid_minmax(x), 5, 20, 4.0 * n, "GB/s",
+                                     "2^24 fp32: min and max as two NaN-propagating reductions")
+    out["quantize_f32_to_i8"] = cpu_leg(lambda: O.lucid_quantize(x, inv, 0.0, -128, 127, q, t0, t1), 5, 20,
+                                        5.0 * n, "GB/s", "2^24 fp32 -> int8 in Lucid's passes (mul, round, add, "
+                                                         "clip, cast)")
+    out["dequantize_i8_to_f32"] = cpu_leg(lambda: O.lucid_dequantize(q, 0.05, 0.0, y, t0), 5, 20, 5.0 * n, "GB/s",
+                                          "2^24 int8 -> fp32 in Lucid's passes (cast, sub, mul)")
+    W = rng.integers(-127, 128, (4096, 4096), dtype=np.int64).astype(np.int8)
+    sw = rng.uniform(1e-3, 1e-1, 4096).astype(np.float32)
+    zw = np.zeros(4096, np.float32)
+    xv = rng.standard_normal((1, 4096)).astype(np.float32)
+    out["gemv_w8_m1_4096"] = cpu_leg(lambda: xv @ LM.dequantize_rows(W, sw, zw).T, 5, 20,
+                                     4096 * 4096 + 8.0 * 4096 + 4.0 * 2 * 4096, "GB/s",
+                                     "1 x 4096 x 4096 weight-only Linear: dequantize the int8 weight (2 passes), "
+                                     "then fp32 sgemv")
+    return out
+
+
+def warm_stats(call, warmup: int, iters: int, sync) -> dict:
+    """Median / p5 / p95 milliseconds of ``call`` over ``iters`` samples after ``warmup``
+    untimed calls, each sample bracketed by ``sync`` (the reference harness's protocol,
+    tools/_bench_timing.py:33-52: materialized end-to-end time, host dispatch included)."""
+    for _ in range(warmup):
+        call()
+    sync()
+    samples = []
+    for _ in range(iters):
+        sync()
+        t0 = time.perf_counter()
+        call()
+        sync()
+        samples.append((time.perf_counter() - t0) * 1e3)
+    samples.sort()
+    return {"median": round(samples[len(samples) // 2] if len(samples) % 2 else
+                            0.5 * (samples[len(samples) // 2 - 1] + samples[len(samples) // 2]), 4),
+            "p5": round(samples[min(iters - 1, int(iters * 0.05))], 4),
+            "p95": round(samples[min(iters - 1, int(iters * 0.95))], 4), "n": iters}
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def host_threads() -> int:
+    """Threads the CPU legs run on: the BLAS / OpenMP pools' size (all host cores)."""
+    try:
+        from threadpoolctl import threadpool_info
+
+        return max([int(i.get("num_threads", 1)) for i in threadpool_info()] or [os.cpu_count() or 1])
+    except Exception:  # pragma: no cover
+        return os.cpu_count() or 1
+
+
+def cpu_leg(call, warmup: int, iters: int, per_call: float, unit: str, sample: str, one_thread: bool = True) -> dict:
+    """A CPU-baseline measurement on all host threads and (optionally) on one: ``per_call``
+    work units per call (bytes, ops or items) reported as a rate in ``unit`` (GB/s, TOPS,
+    items/s by the scale in the unit's name) from the median time."""
+    scale = {"GB/s": 1e9, "TOPS": 1e12, "tokens/s": 1.0, "images/s": 1.0, "forwards/s": 1.0}[unit]
+
+    def rate(st):
+        return round(per_call / (st["median"] * 1e-3) / scale, 4)
+
+    out = {"unit": unit, "sample": sample, "cores": host_threads()}
+    st = warm_stats(call, warmup, iters, lambda: None)
+    out.update({"value": rate(st), "ms": st})
+    if one_thread:
+        from threadpoolctl import threadpool_limits
+
+        with threadpool_limits(limits=1):
+            st1 = warm_stats(call, min(warmup, 2), max(3, iters // 4), lambda: None)
+        out["one_thread"] = {"value": rate(st1), "ms": st1}
+    return out
+
+
 def cpu_baseline(M, N, K, seconds):
     """Lucid's CPU composition of the W8A8 Linear (lucid/nn/quantized/linear.py:206-215):
     dequantize activations and weights (separate passes), fp32 sgemm (numpy's OpenBLAS on
@@ -467,19 +715,14 @@ def cpu_baseline(M, N, K, seconds):
         t = np.clip(t, -128, 127)
         return t.astype(np.int8)
 
-    step()  # warm
-    t0 = time.perf_counter()
-    iters = 0
-    while True:
-        step()
-        iters += 1
-        if time.perf_counter() - t0 > seconds or iters >= 20:
-            break
-    dt = (time.perf_counter() - t0) / iters
+    if seconds <= 0:
+        return None
+    st = warm_stats(step, 5, 20, lambda: None)
+    dt = st["median"] * 1e-3
     return {"value": round(2.0 * M * N * K / dt / 1e12, 4), "unit": "TOPS", "cores": threads,
-            "kind": "port",
-            "sample": f"{iters} steps of the {M}x{N}x{K} W8A8 Linear (dequantize A and B, fp32 "
-                      f"sgemm, bias, requantize to int8) in {dt * iters:.1f} s; "
+            "kind": "port", "ms": st, "cpu_model": cpu_model(),
+            "sample": f"median of {st['n']} steps (after 5 warm-ups) of the {M}x{N}x{K} W8A8 Linear "
+                      f"(dequantize A and B, fp32 sgemm, bias, requantize to int8); "
                       f"{os.cpu_count()} host CPUs visible"}
 
 
@@ -549,6 +792,9 @@ def main() -> None:
         comps["conv_resnet18_b32"] = conv_lines(L, C, timer, 10, 3)
         comps.update(bandwidth_lines(L, C, timer, 50, 10))
         comps.update(lookup_lines(L, C, timer, 20, 5))
+        comps["models"] = model_lines(L, C, gtimer, args.cpu_seconds > 0)
+        if args.cpu_seconds > 0:
+            comps["cpu_legs"] = cpu_micro_legs()
         line["components"] = comps
     line["cpu_baseline"] = cpu_baseline(M, N, K, args.cpu_seconds)
     print(json.dumps(line), flush=True)

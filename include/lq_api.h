@@ -520,6 +520,41 @@ int lq_linear_f32(const float* d_x, int64_t ldx, const float* d_w, int64_t ldw,
                   const float* d_bias, float* d_y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                   void* stream);
 
+/* ---- float glue of a dynamically quantized transformer ---- */
+/* Kernels a decoder runs between its int8 Linears, each a float32 restatement of a Lucid
+ * float module; compared with float64 within tolerance.
+ * Positions: where an entry point takes (pos0, d_pos0), the first token's position is pos0,
+ * or d_pos0[0] when d_pos0 is not NULL (a device counter, so one captured decode step replays
+ * at every position; kernels clamp it into range, the caller keeps it valid). */
+/* out[r] = tok_table[clamp(tokens[r])] + pos_table[pos + r % n] for rows = B * n token rows
+ * (nn.Embedding lookups plus the positional add); pos_table has npos rows. */
+int lq_embedding_sum_f32(const float* d_tok_table, int64_t vocab, const float* d_pos_table, int64_t npos, int64_t D,
+                         const int32_t* d_tokens, int64_t rows, int64_t n, int64_t pos0, const int32_t* d_pos0,
+                         float* d_out, void* stream);
+/* y = (x - mean) / sqrt(var + eps) (* gamma + beta when given) per row of D (nn.LayerNorm,
+ * biased variance); rows ldx / ldy elements apart. */
+int lq_layer_norm_f32(const float* d_x, int64_t ldx, float* d_y, int64_t ldy, int64_t rows, int64_t D,
+                      const float* d_gamma, const float* d_beta, float eps, void* stream);
+/* y = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) (F.gelu, approximate="tanh"). */
+int lq_gelu_tanh_f32(const float* d_x, float* d_y, int64_t n, void* stream);
+/* y = a + b elementwise (residual adds). */
+int lq_add_f32(const float* d_a, const float* d_b, float* d_y, int64_t n, void* stream);
+/* qkv [B, n, 3, H, hd] float32 -> q [B, H, n, hd] fp16, and k / v written into the fp16
+ * caches [B, H, T_max, hd] at positions pos .. pos + n - 1. */
+int lq_kv_append_f16(const float* d_qkv, int64_t B, int64_t n, int64_t H, int64_t hd, int64_t pos0,
+                     const int32_t* d_pos0, int64_t T_max, void* d_q, void* d_k_cache, void* d_v_cache, void* stream);
+/* Causal attention over the fp16 cache (F.scaled_dot_product_attention, is_causal): query i of
+ * q [B, H, n, hd] sits at position pos + i and sees keys 0 .. pos + i; softmax(scale q.k) v
+ * with fp32 scores and sums; out [B, n, H, hd] float32.  hd = 64 and pos + n <= 2048
+ * (LQ_ERR_UNSUPPORTED otherwise). */
+int lq_attention_f16(const void* d_q, const void* d_k_cache, const void* d_v_cache, int64_t B, int64_t H, int64_t n,
+                     int64_t hd, int64_t pos0, const int32_t* d_pos0, int64_t T_max, float scale, float* d_out,
+                     void* stream);
+/* x[0] += delta (advances a device position counter inside a captured step). */
+int lq_increment_i32(int32_t* d_x, int32_t delta, void* stream);
+/* idx[r] = index of the first maximum of row r (numpy argmax; a NaN counts as the maximum). */
+int lq_argmax_f32(const float* d_x, int64_t rows, int64_t cols, int32_t* d_idx, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

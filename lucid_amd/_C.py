@@ -109,6 +109,14 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_gemm_w8a8_noalloc_scratch_bytes": (_SZ, []),
     "lq_gemm_w8a8_noalloc": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64,
                                   _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
+    "lq_embedding_sum_f32": (_I, [_P, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _P]),
+    "lq_layer_norm_f32": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P, _F, _P]),
+    "lq_gelu_tanh_f32": (_I, [_P, _P, _I64, _P]),
+    "lq_add_f32": (_I, [_P, _P, _P, _I64, _P]),
+    "lq_kv_append_f16": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P]),
+    "lq_attention_f16": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _F, _P, _P]),
+    "lq_increment_i32": (_I, [_P, ctypes.c_int32, _P]),
+    "lq_argmax_f32": (_I, [_P, _I64, _I64, _P, _P]),
     "lq_packed_weights_size": (_SZ, [_I64, _I64]),
     "lq_pack_weights_i8": (_I, [_P, _I64, _I64, _I64, _P, _P]),
     "lq_gemm_w8a8_packed": (_I, [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64,

@@ -1,0 +1,289 @@
+"""The model-level BASELINE configurations as runnable workloads (bench and tests).
+
+* :func:`resnet18` / :func:`resnet18_fuse_groups` -- configuration 5's network: a ResNet-18
+  of Lucid's float modules (Conv2d / BatchNorm2d / ReLU, residual adds on
+  ``nnq.FloatFunctional``, stubs at both ends) whose static-PTQ flow (fuse -> prepare ->
+  calibrate -> convert) yields the quantized module tree the bench times.
+* :func:`decoder` -- configuration 4's float decoder (6 layers, d 512, 8 heads, FFN 2048,
+  vocab 32000): the Linears as a module tree for ``quantize_dynamic``, the embeddings as
+  float32 arrays.
+* :class:`Int8Decoder` -- that decoder, after ``quantize_dynamic``, run on the device through
+  the C ABI on preallocated buffers, so a whole prefill or decode step is one captured HIP
+  graph (positions live in a device counter; the next token comes from an on-device argmax).
+  Each Linear is the dynamic module's own forward (:class:`DynLinear`): observer -> qparams
+  -> quantize -> W8A8 GEMM on the module's weight operands, bit for bit the same launches as
+  ``nnqd.Linear.forward``; the float glue is ``lq_glue.hip``.
+
+Random initialisation only: there is no network in this environment for checkpoints.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import numpy as np
+
+from lucid_amd import _C
+from lucid_amd._tensor import empty, tensor
+
+D_MODEL, HEADS, FFN, VOCAB, LAYERS = 512, 8, 2048, 32000, 6
+BATCH, PREFILL, DECODE = 8, 512, 128
+
+
+def _host(a):
+    return tensor(np.asarray(a, np.float32))
+
+
+# --------------------------------------------------------------------- configuration 5
+
+
+def resnet18(rng: np.random.Generator, num_classes: int = 1000):
+    """ResNet-18 for 3 x 224 x 224 inputs, random BatchNorm statistics and affine terms."""
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized as nnq
+
+    def bn(c):
+        m = nn.BatchNorm2d(c)
+        m.running_mean = _host(rng.normal(0, 0.1, c))
+        m.running_var = _host(rng.uniform(0.5, 1.5, c))
+        m.weight = nn.Parameter(_host(rng.normal(1, 0.1, c)))
+        m.bias = nn.Parameter(_host(rng.normal(0, 0.1, c)))
+        return m
+
+    class BasicBlock(nn.Module):
+        def __init__(self, cin, cout, stride):
+            super().__init__()
+            self.conv1 = nn.Conv2d(cin, cout, 3, stride=stride, padding=1, bias=False)
+            self.bn1 = bn(cout)
+            self.relu = nn.ReLU()
+            self.conv2 = nn.Conv2d(cout, cout, 3, padding=1, bias=False)
+            self.bn2 = bn(cout)
+            self.downsample = (nn.Sequential(nn.Conv2d(cin, cout, 1, stride=stride, bias=False), bn(cout))
+                               if stride != 1 or cin != cout else None)
+            self.skip = nnq.FloatFunctional()
+
+        def forward(self, x):
+            out = self.relu(self.bn1(self.conv1(x)))
+            out = self.bn2(self.conv2(out))
+            identity = self.downsample(x) if self.downsample is not None else x
+            return self.skip.add_relu(out, identity)
+
+    class ResNet18(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.quant = nnq.QuantStub()
+            self.conv1 = nn.Conv2d(3, 64, 7, stride=2, padding=3, bias=False)
+            self.bn1 = bn(64)
+            self.relu = nn.ReLU()
+            self.maxpool = nn.MaxPool2d(3, 2, 1)
+            chans = [(64, 64, 1), (64, 128, 2), (128, 256, 2), (256, 512, 2)]
+            for i, (cin, cout, st) in enumerate(chans, 1):
+                setattr(self, f"layer{i}", nn.Sequential(BasicBlock(cin, cout, st), BasicBlock(cout, cout, 1)))
+            self.avgpool = nn.AdaptiveAvgPool2d(1)
+            self.flatten = nn.Flatten()
+            self.fc = nn.Linear(512, num_classes)
+            self.dequant = nnq.DeQuantStub()
+
+        def forward(self, x):
+            x = self.maxpool(self.relu(self.bn1(self.conv1(self.quant(x)))))
+            for i in range(1, 5):
+                x = getattr(self, f"layer{i}")(x)
+            return self.dequant(self.fc(self.flatten(self.avgpool(x))))
+
+    return ResNet18().eval()
+
+
+def resnet18_fuse_groups() -> list[list[str]]:
+    """conv + bn (+ relu) runs of :func:`resnet18` for ``fuse_modules``."""
+    groups = [["conv1", "bn1", "relu"]]
+    for i in range(1, 5):
+        for b in range(2):
+            p = f"layer{i}.{b}"
+            groups += [[f"{p}.conv1", f"{p}.bn1", f"{p}.relu"], [f"{p}.conv2", f"{p}.bn2"]]
+            if i > 1 and b == 0:
+                groups.append([f"{p}.downsample.0", f"{p}.downsample.1"])
+    return groups
+
+
+# --------------------------------------------------------------------- configuration 4
+
+
+def decoder(rng: np.random.Generator):
+    """The decoder's Linears (N(0, 0.02) weights and biases) as a module tree, and the float
+    embeddings {"tok": [VOCAB, D], "pos": [PREFILL + DECODE, D]} (host arrays)."""
+    import lucid_amd.nn as nn
+
+    def lin(k, n):
+        m = nn.Linear(k, n)
+        m.weight = nn.Parameter(_host(rng.normal(0, 0.02, (n, k))))
+        m.bias = nn.Parameter(_host(rng.normal(0, 0.02, n)))
+        return m
+
+    class Layer(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.qkv = lin(D_MODEL, 3 * D_MODEL)
+            self.out = lin(D_MODEL, D_MODEL)
+            self.up = lin(D_MODEL, FFN)
+            self.down = lin(FFN, D_MODEL)
+
+    class Decoder(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.layers = nn.Sequential(*[Layer() for _ in range(LAYERS)])
+            self.head = lin(D_MODEL, VOCAB)
+
+    glue = {"tok": rng.normal(0, 0.02, (VOCAB, D_MODEL)).astype(np.float32),
+            "pos": rng.normal(0, 0.02, (PREFILL + DECODE, D_MODEL)).astype(np.float32)}
+    return Decoder().to("gpu"), glue
+
+
+class DynLinear:
+    """One ``nnqd.Linear`` run through the C ABI into caller buffers, allocating nothing per
+    call: ``lq_minmax_f32`` (replace) -> ``lq_calc_qparams_f32`` (per-tensor affine, the
+    module's activation grid) -> ``lq_quantize_per_tensor_f32`` (codes as c - 128) ->
+    ``lq_gemm_w8a8`` / ``lq_gemm_w8a8_packed`` (M <= 128) with ``LQ_EPI_A_U8S8``, the module's
+    weight codes, per-channel scales, cached code sums and bias, float32 out -- the launches
+    of ``nnqd.Linear.forward``."""
+
+    def __init__(self, mod, max_rows: int) -> None:
+        w = mod._operands()
+        self.N, self.K = w.N, w.K
+        if w.zero_point is not None:
+            raise ValueError("DynLinear: symmetric (zero-point-free) weights expected")
+        self.w = w
+        self.packed = w.packed()
+        self.bias = mod.bias
+        qd = mod.act_qdtype
+        self.qmin, self.qmax, self.signed = qd.quant_min, qd.quant_max, int(qd.signed)
+        if not (0 <= self.qmin and self.qmax <= 255):
+            raise ValueError("DynLinear: an unsigned 8-bit activation grid expected")
+        self.qp = empty((4,), np.float32, "gpu")  # min, max, scale, zero point
+        self.codes = empty((max_rows * self.K,), np.int8, "gpu")
+        lib = _C.lib()
+        self.mm_bytes = max(lib.lq_minmax_workspace_size(max_rows * self.K), 16)
+        self.mm_ws = empty((self.mm_bytes,), np.uint8, "gpu")
+        self.g_bytes = max(max(lib.lq_gemm_w8a8_workspace_size(m, self.N, self.K) for m in (1, max_rows)), 16)
+        self.g_ws = empty((self.g_bytes,), np.uint8, "gpu")
+
+    def __call__(self, x: int, rows: int, y: int, stream) -> None:
+        n = rows * self.K
+        q = self.qp.data_ptr()
+        mn, mx, sx, zx = q, q + 4, q + 8, q + 12
+        _C.call("lq_minmax_f32", x, n, mn, mx, _C.OBS_REPLACE, 0.0, self.mm_ws.data_ptr(), self.mm_bytes, stream)
+        _C.call("lq_calc_qparams_f32", mn, mx, 1, 0, self.signed, self.qmin, self.qmax, float(np.float32(1e-8)),
+                sx, zx, stream)
+        _C.call("lq_quantize_per_tensor_f32", x, self.codes.data_ptr(), n, _C.U8S8, sx, zx, 0.0, 0.0, self.qmin,
+                self.qmax, stream)
+        common = (sx, 0, self.w.scale.data_ptr(), 1, zx, None, self.w.sums.data_ptr(),
+                  self.bias.data_ptr() if self.bias is not None else None, None, None, 0, 0, _C.OUT_F32,
+                  _C.EPI_A_U8S8, self.g_ws.data_ptr(), self.g_bytes, stream)
+        if rows <= 128 and self.packed is not None:
+            _C.call("lq_gemm_w8a8_packed", self.codes.data_ptr(), self.K, self.packed.data_ptr(), y, self.N, rows,
+                    self.N, self.K, *common)
+        else:
+            _C.call("lq_gemm_w8a8", self.codes.data_ptr(), self.K, self.w.codes.data_ptr(), self.K, y, self.N, rows,
+                    self.N, self.K, *common)
+
+
+class Int8Decoder:
+    """Configuration 4 on the device: ``qdec`` (the output of ``quantize_dynamic`` on
+    :func:`decoder`) plus its float embeddings, run through the C ABI on preallocated
+    buffers.  ``prefill(tokens, stream)`` feeds a [batch, T] prompt from position 0;
+    ``decode(stream)`` feeds the previous step's argmax token at the next position.  Both
+    leave the last position's logits in ``self.logits`` and its argmax in ``self.next``;
+    every launch goes to ``stream``, so either step can be captured into a HIP graph and
+    replayed (the position is the device counter ``self.pos``)."""
+
+    def __init__(self, qdec, glue: dict, batch: int = BATCH, max_prompt: int = PREFILL,
+                 max_positions: int = PREFILL + DECODE) -> None:
+        self.B, self.Tp, self.Tmax = batch, max_prompt, max_positions
+        self.D, self.H, self.hd = D_MODEL, HEADS, D_MODEL // HEADS
+        rows = batch * max_prompt
+        self.layers = [tuple(DynLinear(getattr(layer, n), rows) for n in ("qkv", "out", "up", "down"))
+                       for layer in qdec.layers]
+        self.head = DynLinear(qdec.head, batch)
+        self.V = self.head.N
+        dev = lambda a: tensor(np.ascontiguousarray(a), device="gpu")  # noqa: E731
+        self.tok = dev(glue["tok"])
+        self.posemb = dev(glue["pos"])
+        self.npos = glue["pos"].shape[0]
+        f32 = lambda *s: empty(s, np.float32, "gpu")  # noqa: E731
+        self.h, self.hn, self.att, self.proj = f32(rows, self.D), f32(rows, self.D), f32(rows, self.D), f32(rows, self.D)
+        self.qkv, self.up, self.hl = f32(rows, 3 * self.D), f32(rows, FFN), f32(batch, self.D)
+        self.logits = f32(batch, self.V)
+        self.q16 = empty((batch, self.H, max_prompt, self.hd), np.float16, "gpu")
+        self.cache = [(empty((batch, self.H, self.Tmax, self.hd), np.float16, "gpu"),
+                       empty((batch, self.H, self.Tmax, self.hd), np.float16, "gpu")) for _ in self.layers]
+        self.prompt = empty((rows,), np.int32, "gpu")
+        self.next = empty((batch,), np.int32, "gpu")
+        self.pos = empty((1,), np.int32, "gpu")
+        self.scale = float(np.float32(1.0 / np.sqrt(self.hd)))
+
+    def _step(self, tokens: int, n: int, stream) -> None:
+        B, D, H, hd = self.B, self.D, self.H, self.hd
+        M = B * n
+        p = self.pos.data_ptr()
+        h, hn = self.h.data_ptr(), self.hn.data_ptr()
+        _C.call("lq_embedding_sum_f32", self.tok.data_ptr(), self.V, self.posemb.data_ptr(), self.npos, D, tokens,
+                M, n, 0, p, h, stream)
+        for (qkv, out, up, down), (kc, vc) in zip(self.layers, self.cache):
+            _C.call("lq_layer_norm_f32", h, D, hn, D, M, D, None, None, np.float32(1e-5), stream)
+            qkv(hn, M, self.qkv.data_ptr(), stream)
+            _C.call("lq_kv_append_f16", self.qkv.data_ptr(), B, n, H, hd, 0, p, self.Tmax, self.q16.data_ptr(),
+                    kc.data_ptr(), vc.data_ptr(), stream)
+            _C.call("lq_attention_f16", self.q16.data_ptr(), kc.data_ptr(), vc.data_ptr(), B, H, n, hd, 0, p,
+                    self.Tmax, np.float32(self.scale), self.att.data_ptr(), stream)
+            out(self.att.data_ptr(), M, self.proj.data_ptr(), stream)
+            _C.call("lq_add_f32", h, self.proj.data_ptr(), h, M * D, stream)
+            _C.call("lq_layer_norm_f32", h, D, hn, D, M, D, None, None, np.float32(1e-5), stream)
+            up(hn, M, self.up.data_ptr(), stream)
+            _C.call("lq_gelu_tanh_f32", self.up.data_ptr(), self.up.data_ptr(), M * FFN, stream)
+            down(self.up.data_ptr(), M, self.proj.data_ptr(), stream)
+            _C.call("lq_add_f32", h, self.proj.data_ptr(), h, M * D, stream)
+        # the last position of each sequence: layer norm over rows n * D apart, then the head
+        _C.call("lq_layer_norm_f32", h + (n - 1) * D * 4, n * D, self.hl.data_ptr(), D, B, D, None, None,
+                np.float32(1e-5), stream)
+        self.head(self.hl.data_ptr(), B, self.logits.data_ptr(), stream)
+        _C.call("lq_argmax_f32", self.logits.data_ptr(), B, self.V, self.next.data_ptr(), stream)
+        _C.call("lq_increment_i32", p, n, stream)
+
+    def set_prompt(self, tokens: np.ndarray) -> None:
+        """Upload a [batch, T] int prompt (T <= max_prompt) for :meth:`prefill`."""
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        if tokens.shape[0] != self.B or tokens.shape[1] > self.Tp:
+            raise ValueError(f"prompt of shape {tokens.shape} for batch {self.B}, at most {self.Tp} tokens")
+        if tokens.min() < 0 or tokens.max() >= self.V:
+            raise ValueError("prompt token ids out of the vocabulary")
+        self.T = tokens.shape[1]
+        _C.call("lq_memcpy_h2d", self.prompt.data_ptr(), tokens.ctypes.data, tokens.nbytes, None)
+
+    def prefill(self, stream) -> None:
+        """The prompt from position 0 (the counter is reset first)."""
+        _C.call("lq_fill_u32", self.pos.data_ptr(), 0, 1, stream)
+        self._step(self.prompt.data_ptr(), self.T, stream)
+
+    def decode(self, stream) -> None:
+        """One greedy step: the previous argmax token at the next position."""
+        self._step(self.next.data_ptr(), 1, stream)
+
+
+class Graph:
+    """A captured sequence of launches on a created stream, replayable (``lq_graph_*``)."""
+
+    def __init__(self, fn, stream) -> None:
+        self.stream = stream
+        _C.call("lq_graph_begin_capture", stream)
+        try:
+            fn(stream)
+        finally:
+            exe = ctypes.c_void_p()
+            _C.call("lq_graph_end_capture", stream, ctypes.byref(exe))
+        self.exe = exe
+
+    def launch(self) -> None:
+        _C.call("lq_graph_launch", self.exe, self.stream)
+
+    def __del__(self) -> None:
+        if getattr(self, "exe", None) is not None and _C._lib is not None:
+            _C._lib.lq_graph_destroy(self.exe)

@@ -51,6 +51,10 @@ function                      follows (lucid-official/lucid)
 ``rnn_cell`` / ``rnn_forward``  nn/modules/rnn.py (_rnn_step, _gru_step, LSTM gates i, f, g, o),
                               float64 numpy
 ``conv_transpose2d_acc``      the direct scatter definition of conv_transpose2d, int64
+``layer_norm`` / ``gelu_tanh`` /  the float glue of the int8 decoder:
+``attention`` / ``embedding_sum``  nn.LayerNorm, F.gelu(approximate="tanh"),
+                              F.scaled_dot_product_attention(is_causal) over fp16 q / k / v,
+                              token + position embedding; float64 numpy (tolerance references)
 ``lucid_*``                   the multi-pass CPU composition timed as the CPU baseline
 ============================  ==========================================================
 
@@ -757,3 +761,50 @@ def conv_transpose2d_acc(x, w, za=0, x_u8s8=False, stride=(1, 1), pad=(0, 0), ou
                 full[:, g * Cout_g:(g + 1) * Cout_g, kh * dh:kh * dh + (H - 1) * sh + 1:sh,
                      kw * dw:kw * dw + (W - 1) * sw + 1:sw] += contrib
     return full[:, :, ph:ph + OH, pw:pw + OW]
+
+
+# ------------------------------------------------- float glue of the int8 decoder (config 4)
+
+
+def layer_norm(x, gamma=None, beta=None, eps: float = 1e-5) -> np.ndarray:
+    """(x - mean) / sqrt(var + eps) * gamma + beta over the last axis, biased variance, in
+    float64 (nn.LayerNorm's forward)."""
+    x = np.asarray(x, np.float64)
+    mu = x.mean(-1, keepdims=True)
+    var = ((x - mu) ** 2).mean(-1, keepdims=True)
+    y = (x - mu) / np.sqrt(var + eps)
+    if gamma is not None:
+        y = y * np.asarray(gamma, np.float64)
+    if beta is not None:
+        y = y + np.asarray(beta, np.float64)
+    return y
+
+
+def gelu_tanh(x) -> np.ndarray:
+    """0.5 x (1 + tanh(sqrt(2 / pi) (x + 0.044715 x^3))) in float64 (F.gelu, tanh form)."""
+    x = np.asarray(x, np.float64)
+    return 0.5 * x * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (x + 0.044715 * x ** 3)))
+
+
+def attention(q, k, v, pos0: int, scale: float) -> np.ndarray:
+    """Causal attention of q [B, H, n, hd] at positions pos0 .. pos0 + n - 1 over keys /
+    values [B, H, T, hd] (T >= pos0 + n; only the first pos0 + n are visible), float64 over
+    the given (fp16) values: softmax(scale q k^T, keys <= own position) v -> [B, n, H, hd]."""
+    q, k, v = (np.asarray(a, np.float64) for a in (q, k, v))
+    B, H, n, hd = q.shape
+    T = pos0 + n
+    s = np.einsum("bhqd,bhkd->bhqk", q, k[:, :, :T]) * float(np.float32(scale))
+    visible = np.arange(T)[None, :] <= (pos0 + np.arange(n))[:, None]
+    s = np.where(visible, s, -np.inf)
+    s = np.exp(s - s.max(-1, keepdims=True))
+    s = s / s.sum(-1, keepdims=True)
+    o = np.einsum("bhqk,bhkd->bhqd", s, v[:, :, :T])
+    return o.transpose(0, 2, 1, 3)
+
+
+def embedding_sum(tok_table, pos_table, tokens, pos0: int) -> np.ndarray:
+    """tok_table[tokens] + pos_table[pos0 + i] for tokens [B, n] -> [B, n, D] (float32 add)."""
+    tokens = np.asarray(tokens)
+    n = tokens.shape[-1]
+    return (np.asarray(tok_table, np.float32)[tokens] +
+            np.asarray(pos_table, np.float32)[pos0:pos0 + n]).astype(np.float32)

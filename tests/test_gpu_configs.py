@@ -83,55 +83,9 @@ def test_pool_over_codes(gpu):
 
 
 def _resnet18(nn, nnq, rng, num_classes=1000):
-    def bn(c):
-        m = nn.BatchNorm2d(c)
-        m.running_mean = _host(rng.normal(0, 0.1, c))
-        m.running_var = _host(rng.uniform(0.5, 1.5, c))
-        m.weight = nn.Parameter(_host(rng.normal(1, 0.1, c)))
-        m.bias = nn.Parameter(_host(rng.normal(0, 0.1, c)))
-        return m
+    from lucid_amd.bench_configs import resnet18
 
-    class BasicBlock(nn.Module):
-        def __init__(self, cin, cout, stride):
-            super().__init__()
-            self.conv1 = nn.Conv2d(cin, cout, 3, stride=stride, padding=1, bias=False)
-            self.bn1 = bn(cout)
-            self.relu = nn.ReLU()
-            self.conv2 = nn.Conv2d(cout, cout, 3, padding=1, bias=False)
-            self.bn2 = bn(cout)
-            self.downsample = (nn.Sequential(nn.Conv2d(cin, cout, 1, stride=stride, bias=False), bn(cout))
-                               if stride != 1 or cin != cout else None)
-            self.skip = nnq.FloatFunctional()
-
-        def forward(self, x):
-            out = self.relu(self.bn1(self.conv1(x)))
-            out = self.bn2(self.conv2(out))
-            identity = self.downsample(x) if self.downsample is not None else x
-            return self.skip.add_relu(out, identity)
-
-    class ResNet18(nn.Module):
-        def __init__(self):
-            super().__init__()
-            self.quant = nnq.QuantStub()
-            self.conv1 = nn.Conv2d(3, 64, 7, stride=2, padding=3, bias=False)
-            self.bn1 = bn(64)
-            self.relu = nn.ReLU()
-            self.maxpool = nn.MaxPool2d(3, 2, 1)
-            chans = [(64, 64, 1), (64, 128, 2), (128, 256, 2), (256, 512, 2)]
-            for i, (cin, cout, st) in enumerate(chans, 1):
-                setattr(self, f"layer{i}", nn.Sequential(BasicBlock(cin, cout, st), BasicBlock(cout, cout, 1)))
-            self.avgpool = nn.AdaptiveAvgPool2d(1)
-            self.flatten = nn.Flatten()
-            self.fc = nn.Linear(512, num_classes)
-            self.dequant = nnq.DeQuantStub()
-
-        def forward(self, x):
-            x = self.maxpool(self.relu(self.bn1(self.conv1(self.quant(x)))))
-            for i in range(1, 5):
-                x = getattr(self, f"layer{i}")(x)
-            return self.dequant(self.fc(self.flatten(self.avgpool(x))))
-
-    return ResNet18().eval()
+    return resnet18(rng, num_classes)
 
 
 def _host(a):
@@ -141,14 +95,9 @@ def _host(a):
 
 
 def _fuse_groups():
-    groups = [["conv1", "bn1", "relu"]]
-    for i in range(1, 5):
-        for b in range(2):
-            p = f"layer{i}.{b}"
-            groups += [[f"{p}.conv1", f"{p}.bn1", f"{p}.relu"], [f"{p}.conv2", f"{p}.bn2"]]
-            if i > 1 and b == 0:
-                groups.append([f"{p}.downsample.0", f"{p}.downsample.1"])
-    return groups
+    from lucid_amd.bench_configs import resnet18_fuse_groups
+
+    return resnet18_fuse_groups()
 
 
 @pytest.fixture(scope="module")
@@ -243,38 +192,13 @@ def test_resnet18_config5_vs_float(gpu, resnet_pipeline):
 
 # ------------------------------------------------------- config 4: int8-dynamic decoder
 
-D_MODEL, HEADS, FFN, VOCAB, LAYERS = 512, 8, 2048, 32000, 6
-BATCH, PREFILL, DECODE = 8, 512, 128
+from lucid_amd.bench_configs import BATCH, D_MODEL, DECODE, FFN, HEADS, LAYERS, PREFILL, VOCAB  # noqa: E402
 
 
 def _decoder(gpu, rng):
-    """The decoder's Linears (random init, N(0, 0.02)) as a module tree quantize_dynamic can
-    walk, plus the float glue parameters (embeddings, layer norms) kept on the host."""
-    import lucid_amd.nn as nn
+    from lucid_amd.bench_configs import decoder
 
-    def lin(k, n):
-        m = nn.Linear(k, n)
-        m.weight = nn.Parameter(_host(rng.normal(0, 0.02, (n, k))))
-        m.bias = nn.Parameter(_host(rng.normal(0, 0.02, n)))
-        return m
-
-    class Layer(nn.Module):
-        def __init__(self):
-            super().__init__()
-            self.qkv = lin(D_MODEL, 3 * D_MODEL)
-            self.out = lin(D_MODEL, D_MODEL)
-            self.up = lin(D_MODEL, FFN)
-            self.down = lin(FFN, D_MODEL)
-
-    class Decoder(nn.Module):
-        def __init__(self):
-            super().__init__()
-            self.layers = nn.Sequential(*[Layer() for _ in range(LAYERS)])
-            self.head = lin(D_MODEL, VOCAB)
-
-    glue = {"tok": rng.normal(0, 0.02, (VOCAB, D_MODEL)).astype(np.float32),
-            "pos": rng.normal(0, 0.02, (PREFILL + DECODE, D_MODEL)).astype(np.float32)}
-    return Decoder().to("gpu"), glue
+    return decoder(rng)
 
 
 def _ln(x):
@@ -296,9 +220,10 @@ class _Runner:
     """One decoding session: causal attention over a KV cache and layer norm on the host in
     float32 (the test's glue), every Linear through ``dec`` on the GPU."""
 
-    def __init__(self, gpu, dec, glue, batch):
+    def __init__(self, gpu, dec, glue, batch, fp16_qkv=False):
         self.gpu, self.dec, self.glue, self.B = gpu, dec, glue, batch
         self.caches = [([], []) for _ in range(LAYERS)]
+        self.fp16_qkv = fp16_qkv
 
     def step(self, tokens, pos0):
         """Feed ``tokens`` [B, n] at positions pos0 .. pos0 + n - 1; logits of the last one."""
@@ -308,6 +233,8 @@ class _Runner:
         for li, layer in enumerate(self.dec.layers):
             qkv = _run_linear(self.gpu, layer.qkv, _ln(h).reshape(-1, D_MODEL)).reshape(B, n, 3, HEADS, hd)
             q, k, v = (qkv[:, :, i].transpose(0, 2, 1, 3) for i in range(3))
+            if self.fp16_qkv:
+                q, k, v = (a.astype(np.float16).astype(np.float32) for a in (q, k, v))
             ks, vs = self.caches[li]
             ks.append(k)
             vs.append(v)
@@ -399,3 +326,81 @@ def test_decoder_config4_generation(gpu, decoder_pair):
     assert worst > 0.98, worst
     agree = np.mean([(qs.argmax(-1) == fs.argmax(-1)).mean() for qs, fs in zip(qlogits, flogits)])
     assert agree > 0.8, agree
+
+
+# ----------------------------------------- config 4 on the device (the bench's runtime)
+
+
+def test_dyn_linear_matches_module(gpu, decoder_pair):
+    """The bench runtime's Linear (the module's four launches on caller buffers) equals
+    nnqd.Linear.forward bit for bit, on the packed (M = 8) and row-major (M = 4096) paths."""
+    from lucid_amd.bench_configs import DynLinear
+
+    rng, _, qdec, _, _ = decoder_pair
+    for name in ("qkv", "down"):
+        mod = getattr(qdec.layers[1], name)
+        dl = DynLinear(mod, BATCH * PREFILL)
+        for M in (BATCH, BATCH * PREFILL):
+            x = (rng.standard_normal((M, dl.K)) * 0.7).astype(np.float32)
+            dx = _dev(gpu, x)
+            y = gpu.empty((M, dl.N), np.float32, "gpu")
+            dl(dx.data_ptr(), M, y.data_ptr(), None)
+            np.testing.assert_array_equal(y.numpy().view(np.uint32), mod(dx).numpy().view(np.uint32),
+                                          err_msg=f"{name} M={M}")
+
+
+def test_int8_decoder_runtime(gpu, decoder_pair):
+    """The device decoder (prefill 64 tokens, then 16 greedy steps replayed from one captured
+    graph) against the host-glue runner fed the same fp16-rounded q / k / v: prefill and
+    step logits close (cosine), the same greedy tokens almost everywhere; graph replay
+    identical to eager execution."""
+    import ctypes
+
+    from lucid_amd import _C
+    from lucid_amd.bench_configs import Graph, Int8Decoder
+
+    _, _, qdec, glue, tokens = decoder_pair
+    T, steps = 64, 16
+    prompt = tokens[:, :T]
+    rt = Int8Decoder(qdec, glue, batch=BATCH, max_prompt=T, max_positions=T + steps)
+    st = ctypes.c_void_p()
+    _C.call("lq_stream_create", ctypes.byref(st))
+    rt.set_prompt(prompt)
+    rt.prefill(st)
+    _C.call("lq_stream_synchronize", st)
+    logits0 = rt.logits.numpy().copy()
+    eager = []
+    for _ in range(4):
+        rt.decode(st)
+        _C.call("lq_stream_synchronize", st)
+        eager.append(rt.next.numpy().copy())
+    # the same from a captured decode step
+    rt.prefill(st)
+    g = Graph(rt.decode, st)
+    toks, logits = [], []
+    for _ in range(steps):
+        g.launch()
+        _C.call("lq_stream_synchronize", st)
+        toks.append(rt.next.numpy().copy())
+        logits.append(rt.logits.numpy().copy())
+    _C.call("lq_stream_destroy", st)
+    for a, b in zip(eager, toks):
+        np.testing.assert_array_equal(a, b)
+    # host reference, teacher-forced on the device's tokens
+    r = _Runner(gpu, qdec, glue, BATCH, fp16_qkv=True)
+    ref0 = r.step(prompt, 0)
+    refs = []
+    nxt = ref0.argmax(-1)
+    feed = [logits0.argmax(-1)] + toks[:-1]
+    for s in range(steps):
+        refs.append(r.step(feed[s][:, None], T + s))
+
+    def cos(a, b):
+        a, b = a.astype(np.float64), b.astype(np.float64)
+        return (a * b).sum(-1) / (np.linalg.norm(a, axis=-1) * np.linalg.norm(b, axis=-1))
+
+    assert cos(logits0, ref0).min() > 0.999, cos(logits0, ref0).min()
+    assert min(cos(a, b).min() for a, b in zip(logits, refs)) > 0.995
+    agree = np.mean([(t == rf.argmax(-1)).mean() for t, rf in zip(toks, refs)])
+    assert agree > 0.9, agree
+    assert (nxt == logits0.argmax(-1)).mean() > 0.9

@@ -1,0 +1,141 @@
+"""GPU parity of the decoder glue kernels (lucid_amd/csrc/lq_glue.hip) through the C ABI:
+embedding sums, residual adds, the KV-cache append and argmax bit-exact; layer norm and the
+tanh GELU within fp32 rtol 1e-5 of the oracle's float64; attention (fp16 q / k / v, fp32
+scores and sums) within rtol 1e-4 of float64 over the same fp16 values, at prefill and
+decode positions, with the position passed by value and through a device counter."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle as O
+from _tolerance import assert_close_f32, assert_close_to_scale
+
+pytestmark = pytest.mark.gpu
+
+
+def _d(L, a):
+    return L.tensor(np.ascontiguousarray(a), device="gpu")
+
+
+def test_embedding_sum_and_add_exact(gpu):
+    from lucid_amd import _C
+
+    rng = np.random.default_rng(1)
+    V, P, D, B, n, pos0 = 1000, 64, 48, 3, 5, 7
+    tok = rng.standard_normal((V, D)).astype(np.float32)
+    pos = rng.standard_normal((P, D)).astype(np.float32)
+    ids = rng.integers(0, V, (B, n)).astype(np.int32)
+    out = gpu.empty((B * n, D), np.float32, "gpu")
+    dt, dp, di = _d(gpu, tok), _d(gpu, pos), _d(gpu, ids)
+    _C.call("lq_embedding_sum_f32", dt.data_ptr(), V, dp.data_ptr(), P, D, di.data_ptr(), B * n, n, pos0, None,
+            out.data_ptr(), None)
+    want = O.embedding_sum(tok, pos, ids, pos0).reshape(B * n, D)
+    np.testing.assert_array_equal(out.numpy(), want)
+    dpos = _d(gpu, np.array([pos0 + 3], np.int32))  # device position
+    _C.call("lq_embedding_sum_f32", dt.data_ptr(), V, dp.data_ptr(), P, D, di.data_ptr(), B * n, n, 0,
+            dpos.data_ptr(), out.data_ptr(), None)
+    np.testing.assert_array_equal(out.numpy(), O.embedding_sum(tok, pos, ids, pos0 + 3).reshape(B * n, D))
+    a, b = rng.standard_normal(1000).astype(np.float32), rng.standard_normal(1000).astype(np.float32)
+    y = gpu.empty((1000,), np.float32, "gpu")
+    da, db = _d(gpu, a), _d(gpu, b)
+    _C.call("lq_add_f32", da.data_ptr(), db.data_ptr(), y.data_ptr(), 1000, None)
+    np.testing.assert_array_equal(y.numpy(), a + b)
+    _C.call("lq_increment_i32", dpos.data_ptr(), 5, None)
+    assert dpos.numpy()[0] == pos0 + 8
+
+
+@pytest.mark.parametrize("rows,D", [(1, 512), (4096, 512), (9, 100), (3, 2048)])
+def test_layer_norm(gpu, rows, D):
+    from lucid_amd import _C
+
+    rng = np.random.default_rng(rows + D)
+    x = (rng.standard_normal((rows, D)) * 2 + 0.5).astype(np.float32)
+    g, b = rng.standard_normal(D).astype(np.float32), rng.standard_normal(D).astype(np.float32)
+    dx, dg, dbb = _d(gpu, x), _d(gpu, g), _d(gpu, b)
+    y = gpu.empty((rows, D), np.float32, "gpu")
+    _C.call("lq_layer_norm_f32", dx.data_ptr(), D, y.data_ptr(), D, rows, D, None, None, np.float32(1e-5), None)
+    assert_close_f32(y.numpy(), O.layer_norm(x, eps=1e-5))
+    _C.call("lq_layer_norm_f32", dx.data_ptr(), D, y.data_ptr(), D, rows, D, dg.data_ptr(), dbb.data_ptr(),
+            np.float32(1e-5), None)
+    assert_close_f32(y.numpy(), O.layer_norm(x, g, b, 1e-5))
+    if rows >= 3:  # strided rows: every third row, packed output
+        k = rows // 3
+        y2 = gpu.empty((k, D), np.float32, "gpu")
+        _C.call("lq_layer_norm_f32", dx.data_ptr() + 2 * D * 4, 3 * D, y2.data_ptr(), D, k, D, None, None,
+                np.float32(1e-5), None)
+        assert_close_f32(y2.numpy(), O.layer_norm(x[2::3][:k], eps=1e-5))
+
+
+def test_gelu_tanh(gpu):
+    from lucid_amd import _C
+
+    x = np.concatenate([np.linspace(-10, 10, 4001), np.random.default_rng(2).standard_normal(10000) * 3]).astype(np.float32)
+    y = gpu.empty(x.shape, np.float32, "gpu")
+    dx = _d(gpu, x)
+    _C.call("lq_gelu_tanh_f32", dx.data_ptr(), y.data_ptr(), x.size, None)
+    assert_close_f32(y.numpy(), O.gelu_tanh(x))
+
+
+def _attention_case(gpu, B, H, n, pos0, T_max, device_pos):
+    from lucid_amd import _C
+
+    hd = 64
+    rng = np.random.default_rng(B * 100 + n + pos0)
+    qkv = rng.standard_normal((B, n, 3, H, hd)).astype(np.float32)
+    kc = np.zeros((B, H, T_max, hd), np.float16)
+    vc = np.zeros((B, H, T_max, hd), np.float16)
+    kc[:, :, :pos0] = rng.standard_normal((B, H, pos0, hd))  # earlier positions already cached
+    vc[:, :, :pos0] = rng.standard_normal((B, H, pos0, hd))
+    dqkv, dk, dv = _d(gpu, qkv), _d(gpu, kc), _d(gpu, vc)
+    dq = gpu.empty((B, H, n, hd), np.float16, "gpu")
+    dpos = _d(gpu, np.array([pos0], np.int32)) if device_pos else None
+    p0 = 0 if device_pos else pos0
+    pptr = dpos.data_ptr() if device_pos else None
+    _C.call("lq_kv_append_f16", dqkv.data_ptr(), B, n, H, hd, p0, pptr, T_max, dq.data_ptr(), dk.data_ptr(),
+            dv.data_ptr(), None)
+    q16 = qkv[:, :, 0].transpose(0, 2, 1, 3).astype(np.float16)
+    np.testing.assert_array_equal(dq.numpy().view(np.uint16), q16.view(np.uint16))
+    kc[:, :, pos0:pos0 + n] = qkv[:, :, 1].transpose(0, 2, 1, 3).astype(np.float16)
+    vc[:, :, pos0:pos0 + n] = qkv[:, :, 2].transpose(0, 2, 1, 3).astype(np.float16)
+    np.testing.assert_array_equal(dk.numpy().view(np.uint16), kc.view(np.uint16))
+    np.testing.assert_array_equal(dv.numpy().view(np.uint16), vc.view(np.uint16))
+    out = gpu.empty((B, n, H, hd), np.float32, "gpu")
+    scale = np.float32(1.0 / 8.0)
+    _C.call("lq_attention_f16", dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, H, n, hd, p0, pptr, T_max,
+            scale, out.data_ptr(), None)
+    assert_close_to_scale(out.numpy(), O.attention(q16, kc, vc, pos0, scale), 1e-4)
+
+
+@pytest.mark.parametrize("B,H,n,pos0,T_max", [(2, 3, 40, 0, 64), (8, 8, 512, 0, 640), (8, 8, 1, 511, 640),
+                                              (8, 8, 1, 639, 640), (1, 2, 9, 100, 2048), (2, 1, 1, 0, 16)])
+def test_kv_append_and_attention(gpu, B, H, n, pos0, T_max):
+    print(f"attention B={B} H={H} n={n} pos0={pos0}", flush=True)
+    _attention_case(gpu, B, H, n, pos0, T_max, device_pos=False)
+    _attention_case(gpu, B, H, n, pos0, T_max, device_pos=True)
+
+
+def test_attention_rejects_unsupported(gpu):
+    from lucid_amd import _C
+
+    with pytest.raises(_C.LucidError, match="head dim"):
+        _C.call("lq_attention_f16", 1, 1, 1, 1, 1, 1, 32, 0, None, 4, np.float32(1.0), 1, None)
+    with pytest.raises(_C.LucidError, match="2048"):
+        _C.call("lq_attention_f16", 1, 1, 1, 1, 1, 1, 64, 2048, None, 4096, np.float32(1.0), 1, None)
+
+
+def test_argmax(gpu):
+    from lucid_amd import _C
+
+    rng = np.random.default_rng(3)
+    x = rng.standard_normal((9, 32000)).astype(np.float32)
+    x[1, [5, 900, 31999]] = 50.0          # ties: first index
+    x[2, 17] = np.nan                     # NaN wins
+    x[3, [40, 41]] = np.nan               # first NaN
+    x[4] = -np.inf
+    x[5, 31999] = np.inf
+    idx = gpu.empty((9,), np.int32, "gpu")
+    dx = _d(gpu, x)
+    _C.call("lq_argmax_f32", dx.data_ptr(), 9, 32000, idx.data_ptr(), None)
+    np.testing.assert_array_equal(idx.numpy(), np.argmax(x, axis=1))

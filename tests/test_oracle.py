@@ -747,3 +747,60 @@ def test_conv_transpose_equals_conv_of_expanded_input():
     pt = d * (K - 1) - p
     got = O.conv2d_acc(xu, np.ascontiguousarray(wc), za=za, pad=(pt, pt + op, pt, pt + op), dilation=(d, d), groups=g)
     np.testing.assert_array_equal(got, want)
+
+
+# ----------------------------------------------------- float glue of the int8 decoder
+
+
+def test_glue_against_torch():
+    """The decoder glue restatements against PyTorch's CPU implementations (the independent
+    oracle of Lucid's parity suite) in float64: layer norm (with and without affine), the
+    tanh GELU, and causal scaled-dot-product attention at a decode position."""
+    import torch
+    import torch.nn.functional as TF
+
+    rng = np.random.default_rng(8)
+    x = rng.standard_normal((5, 48)) * 3 + 1
+    g, b = rng.standard_normal(48), rng.standard_normal(48)
+    t = torch.from_numpy(x)
+    np.testing.assert_allclose(O.layer_norm(x, eps=1e-5), TF.layer_norm(t, (48,), eps=1e-5).numpy(), rtol=1e-12, atol=1e-12)
+    np.testing.assert_allclose(O.layer_norm(x, g, b, 1e-5),
+                               TF.layer_norm(t, (48,), torch.from_numpy(g), torch.from_numpy(b), 1e-5).numpy(),
+                               rtol=1e-12, atol=1e-12)
+    z = np.linspace(-8, 8, 101)
+    np.testing.assert_allclose(O.gelu_tanh(z), TF.gelu(torch.from_numpy(z), approximate="tanh").numpy(),
+                               rtol=1e-12, atol=1e-14)
+    B, H, n, hd, pos0 = 2, 3, 4, 8, 5
+    q = rng.standard_normal((B, H, n, hd)).astype(np.float16)
+    k = rng.standard_normal((B, H, pos0 + n + 3, hd)).astype(np.float16)  # trailing keys unused
+    v = rng.standard_normal((B, H, pos0 + n + 3, hd)).astype(np.float16)
+    T = pos0 + n
+    mask = torch.from_numpy(np.arange(T)[None, :] <= (pos0 + np.arange(n))[:, None])
+    want = TF.scaled_dot_product_attention(torch.from_numpy(q.astype(np.float64)),
+                                           torch.from_numpy(k[:, :, :T].astype(np.float64)),
+                                           torch.from_numpy(v[:, :, :T].astype(np.float64)), attn_mask=mask,
+                                           scale=0.125).numpy().transpose(0, 2, 1, 3)
+    np.testing.assert_allclose(O.attention(q, k, v, pos0, 0.125), want, rtol=1e-12, atol=1e-12)
+
+
+def test_glue_closed_forms():
+    """A constant row normalizes to 0, two values to -1 / +1; gelu(x) - gelu(-x) = x;
+    attention over one visible key returns that key's value, over identical keys the mean
+    of the values; a later key never changes an earlier query."""
+    np.testing.assert_array_equal(O.layer_norm(np.full((1, 7), 3.5)), np.zeros((1, 7)))
+    np.testing.assert_allclose(O.layer_norm(np.array([[2.0, 6.0]]), eps=0.0), [[-1.0, 1.0]], rtol=1e-15)
+    z = np.linspace(-5, 5, 41)
+    np.testing.assert_allclose(O.gelu_tanh(z) - O.gelu_tanh(-z), z, atol=1e-12)
+    rng = np.random.default_rng(9)
+    v = rng.standard_normal((1, 1, 6, 4))
+    q = rng.standard_normal((1, 1, 1, 4))
+    k = rng.standard_normal((1, 1, 6, 4))
+    np.testing.assert_allclose(O.attention(q, k, v, 0, 1.0)[0, 0, 0], v[0, 0, 0], rtol=1e-15)
+    k_same = np.repeat(k[:, :, :1], 6, axis=2)
+    np.testing.assert_allclose(O.attention(q, k_same, v, 5, 1.0)[0, 0, 0], v[0, 0].mean(0), rtol=1e-12)
+    qq = rng.standard_normal((1, 1, 3, 4))
+    a = O.attention(qq, k, v, 0, 0.5)
+    k2, v2 = k.copy(), v.copy()
+    k2[:, :, 2:] += 10
+    v2[:, :, 2:] -= 3
+    np.testing.assert_allclose(O.attention(qq, k2, v2, 0, 0.5)[:, :2], a[:, :2], rtol=1e-15)
