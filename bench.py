@@ -394,6 +394,58 @@ def bandwidth_lines(L, C, timer, steps, warmup):
     return out
 
 
+def config2_lines(L, C, gtimer) -> list:
+    """BASELINE config 2 as Lucid's call sequences, each pass captured in a HIP graph (the small
+    sizes are launch-bound): the per-tensor observe + qparams + quantize of a static or dynamic
+    activation, the dequantize back, and the per-channel round trip of a weight [C = 4096,
+    inner] (observer, qparams, quantize, dequantize).  2^20 and 2^24 fp32 fit the 256 MB
+    Infinity Cache (labelled cache-resident); 2^28 streams HBM."""
+    lib = C.lib()
+    rng = np.random.default_rng(11)
+    out = []
+    for log2n in (20, 24, 28):
+        n = 1 << log2n
+        x = L.tensor(rng.standard_normal(n, dtype=np.float32), device="gpu")
+        q = L.empty((n,), np.int8, "gpu")
+        y = L.empty((n,), np.float32, "gpu")
+        ch = 4096
+        inner = n // ch
+        st = L.empty((4 * ch + 4,), np.float32, "gpu")  # running min / max, scale, zero point
+        mn, mx = st.data_ptr(), st.data_ptr() + 4 * ch
+        sc, zp = st.data_ptr() + 8 * ch, st.data_ptr() + 12 * ch
+        ws_t = lib.lq_minmax_workspace_size(n)
+        ws_c = lib.lq_minmax_per_channel_workspace_size(1, ch, inner)
+        ws = L.empty((max(ws_t, ws_c, 1),), np.uint8, "gpu")
+        xp, qp, yp, wp = x.data_ptr(), q.data_ptr(), y.data_ptr(), ws.data_ptr()
+        tensor_calls = [
+            lambda s: C.call("lq_minmax_f32", xp, n, mn, mx, C.OBS_REPLACE, 0.0, wp, ws_t, s),
+            lambda s: C.call("lq_calc_qparams_f32", mn, mx, 1, 0, 0, 0, 255, 1.1920929e-07, sc, zp, s),
+            lambda s: C.call("lq_quantize_per_tensor_f32", xp, qp, n, C.U8S8, sc, zp, 0.0, 0.0, 0, 255, s),
+        ]
+        deq_calls = [lambda s: C.call("lq_dequantize_per_tensor", qp, C.U8S8, yp, C.F32, n, sc, zp, 0.0, 0.0, s)]
+        chan_calls = [
+            lambda s: C.call("lq_minmax_per_channel_f32", xp, 1, ch, inner, mn, mx, C.OBS_REPLACE, 0.0, wp,
+                             ws_c, s),
+            lambda s: C.call("lq_calc_qparams_f32", mn, mx, ch, 1, 1, -128, 127, 1.1920929e-07, sc, zp, s),
+            lambda s: C.call("lq_quantize_per_channel_f32", xp, qp, 1, ch, inner, C.I8, sc, zp, 0.0, -128, 127,
+                             s),
+            lambda s: C.call("lq_dequantize_per_channel", qp, C.I8, yp, C.F32, 1, ch, inner, sc, zp, 0.0, s),
+        ]
+        where = "HBM" if n * 4 > (256 << 20) else "cache-resident"
+        reps = 20 if log2n == 28 else 200
+        for name, calls, bpe in (("observe + qparams + quantize per-tensor (fp32 -> uint8)", tensor_calls, 9),
+                                 ("dequantize per-tensor (uint8 -> fp32)", deq_calls, 5),
+                                 ("per-channel round trip C=4096 (observe, qparams, quantize, dequantize)",
+                                  chan_calls, 14)):
+            us = gtimer.time_ms(calls, reps, 3) * len(calls) * 1e3
+            gbs = n * bpe / (us * 1e-6) / 1e9
+            out.append({"op": name, "n": n, "api_calls": len(calls), "bytes_per_elem": bpe, "us": round(us, 2), "GB/s": round(gbs, 1),
+                        "frac": round(gbs / HBM_PEAK_GBS, 3), "memory": where})
+        del x, q, y, ws
+        C.call("lq_device_synchronize")
+    return out
+
+
 def lookup_lines(L, C, timer, steps, warmup):
     """nn.quantized.EmbeddingBag (mean) over a 4M x 128 int8 table (512 MB: past the Infinity
     Cache), 65536 bags of 32 uniform random indices: random 128-byte row gathers."""
@@ -791,6 +843,7 @@ def main() -> None:
         comps["weight_only_gemv"] = weight_only_lines(L, C, gtimer)
         comps["conv_resnet18_b32"] = conv_lines(L, C, timer, 10, 3)
         comps.update(bandwidth_lines(L, C, timer, 50, 10))
+        comps["config2_quant_sizes"] = config2_lines(L, C, gtimer)
         comps.update(lookup_lines(L, C, timer, 20, 5))
         comps["models"] = model_lines(L, C, gtimer, args.cpu_seconds > 0)
         if args.cpu_seconds > 0:
