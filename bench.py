@@ -167,7 +167,26 @@ def weight_only_lines(L, C, gtimer):
         out.append({"kernel": "lq_gemv_w8 (per-channel int8, fp32 x)", "M": M, "N": N, "K": K,
                     "rotating_copies": rot, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
                     "frac": round(gbs / HBM_PEAK_GBS, 3)})
-        del W
+        if M < 3:  # one or two rows stay on lq_gemv_w8 (whole weight rows on the VALU)
+            del W
+            continue
+        # the entry nnq.Linear takes for 3 <= M <= 16: the same weights MFMA-packed
+        pbytes = lib.lq_packed_weights_size(N, K)
+        P = L.empty((rot * pbytes,), np.int8, "gpu")
+        for r in range(rot):
+            C.call("lq_pack_weights_i8", W.data_ptr() + r * N * K, K, N, K, P.data_ptr() + r * pbytes, None)
+        pws = lib.lq_gemv_w8_packed_workspace_size(M, N, K)
+        pw = L.empty((max(pws, 1),), np.uint8, "gpu")
+        calls = [lambda st, r=r: C.check(lib.lq_gemv_w8_packed(x.data_ptr(), C.F32, K, P.data_ptr() + r * pbytes,
+                                                               s.data_ptr(), None, b.data_ptr(), y.data_ptr(), N, M,
+                                                               N, K, 0, pw.data_ptr(), pws, st), "lq_gemv_w8_packed")
+                 for r in range(rot)]
+        ms = gtimer.time_ms(calls, 10, 2)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"kernel": "lq_gemv_w8_packed (per-channel int8, MFMA-packed, fp32 x)", "M": M, "N": N,
+                    "K": K, "rotating_copies": rot, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 3)})
+        del W, P
     for bits in (4, 8):
         for M in (1, 16):
             N = K = 4096

@@ -317,6 +317,17 @@ int lq_gemv_w8(const void* d_x, int x_dtype, int64_t ldx, const int8_t* d_W, int
                const float* d_w_scale, const float* d_w_zero_point, const float* d_bias,
                void* d_y, int64_t ldy, int64_t M, int64_t N, int64_t K, int flags,
                void* d_workspace, size_t workspace_bytes, void* stream);
+/* lq_gemv_w8 for decode (1 <= M <= 16) over the MFMA-packed weight of lq_pack_weights_i8 (the
+ * copy lq_gemm_w8a8_packed reads), so each wave loads 1 KB of consecutive weight bytes.  Same
+ * arithmetic and arguments as lq_gemv_w8 without ldw; K a positive multiple of 16; x, its rows
+ * and the packed weight 16-byte aligned; lq_gemv_w8_packed_workspace_size(M, N, K) bytes of
+ * workspace (0 when K <= 512).  Replaces the same seam as lq_gemv_w8
+ * (lucid/nn/quantized/linear.py:206-210) for the layer's decode calls. */
+size_t lq_gemv_w8_packed_workspace_size(int64_t M, int64_t N, int64_t K);
+int lq_gemv_w8_packed(const void* d_x, int x_dtype, int64_t ldx, const int8_t* d_W_packed,
+                      const float* d_w_scale, const float* d_w_zero_point, const float* d_bias, void* d_y,
+                      int64_t ldy, int64_t M, int64_t N, int64_t K, int flags, void* d_workspace,
+                      size_t workspace_bytes, void* stream);
 
 /* ---- group-wise packed weights (QuantizedLinearMLX layout) -------------------------- */
 /* Group-wise affine quantize of W[N,K] (float32) with groups of group_size (32/64/128) along K:

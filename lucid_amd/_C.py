@@ -134,6 +134,8 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_gemv_w8_workspace_size": (_SZ, [_I64, _I64, _I64]),
     "lq_gemv_w8": (_I, [_P, _I, _I64, _P, _I64, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P,
                         _SZ, _P]),
+    "lq_gemv_w8_packed_workspace_size": (_SZ, [_I64, _I64, _I64]),
+    "lq_gemv_w8_packed": (_I, [_P, _I, _I64, _P, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I, _P, _SZ, _P]),
     "lq_group_quantize_f32": (_I, [_P, _I64, _I64, _I, _I, _P, _P, _P, _P]),
     "lq_group_dequantize_f32": (_I, [_P, _P, _P, _I64, _I64, _I, _I, _P, _P]),
     "lq_group_matmul_workspace_size": (_SZ, [_I64, _I64, _I64, _I]),

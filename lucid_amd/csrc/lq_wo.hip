@@ -454,6 +454,259 @@ __global__ __launch_bounds__((64 * wo_max_waves(S, XF32, GROUPED))) void wo_gemv
     }
 }
 
+// ------------------------------------------------- split-K skinny GEMM (M <= 16)
+//
+// wo_gemv_kernel gives each workgroup 16 weight rows and all of K, so every workgroup reads
+// the whole 16-row activation block: at M = 16, K = 4096 that is 256 KB per 64 KB of weight,
+// ~6x the weight bytes through L2.  Here a workgroup owns SK_TILES 16-row weight tiles (64
+// columns) and one K range of 512: it splits its slice of x into fp16 halves once, into LDS,
+// where all its waves read it, so x crosses L2 -> CU once per 64 columns.  Its 16 waves are
+// SK_TILES tiles x SK_SUB sub-ranges (each wave a few k-blocks, so the 32 waves of two
+// workgroups per CU hide each other's latency); the sub-ranges of a tile are added in order
+// in LDS.  With one range (K <= 512) the workgroup runs the epilogue; otherwise it stores the
+// range's tile sums and wo_sk_reduce_kernel adds the ranges in range order (a second small
+// launch: a last-arriving workgroup fixup through agent-scope memory measured slower) and
+// runs the epilogue.  The products and per-block sums are those of wo_gemv_kernel (same
+// split, same MFMA steps); only the order in which the block sums are added differs.
+constexpr int SK_TILES = 4;
+constexpr int SK_SUB = 4;
+constexpr int SK_WAVES = SK_TILES * SK_SUB;
+constexpr int SK_RANGE_K = 512;  // K per workgroup
+
+template <int S>
+constexpr int sk_blocks() { return SK_RANGE_K / (32 * S); }  // k-blocks per range: 16 / S
+
+struct WoSkArgs {
+    WoArgs w;            // shapes, operands, epilogue (bpw, xp, xm unused)
+    int splits;          // K ranges per column group
+    float* part;         // [range][group][SK_TILES][64 lanes][4] tile sums
+    float* part_x;       // [range][16] activation row sums over the range
+};
+
+template <int BITS, bool SIGNED, int S, bool XF32, bool GROUPED, bool PACKED = false>
+__global__ __launch_bounds__(64 * SK_WAVES) void wo_gemv_sk_kernel(WoSkArgs sk) {
+    const WoArgs& a = sk.w;
+    constexpr int NW = WChunk<BITS, S>::NW;
+    constexpr int NX = 8 * S;
+    constexpr int KB = sk_blocks<S>();        // k-blocks per range
+    constexpr int RB = (KB + SK_SUB - 1) / SK_SUB;  // k-blocks per wave
+    constexpr int SL = XF32 ? 2 * S : S;      // 16-byte fragments per lane and k-block
+    __shared__ vu4 xs[KB * SL * 64];
+    __shared__ float2 xmeta[KB * 16];
+    __shared__ f4 red[SK_WAVES * 64];
+    __shared__ float redx[SK_SUB * 16];
+    __shared__ float gsc[GROUPED ? SK_TILES * 16 * KB : 1], gbi[GROUPED ? SK_TILES * 16 * KB : 1];
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int tile = wave % SK_TILES, sub = wave / SK_TILES;
+    const int q = lane >> 4, l16 = lane & 15;
+    const int cg = blockIdx.x, range = blockIdx.y;
+    const int TB = (a.K + 32 * S - 1) / (32 * S);
+    const int tb0 = range * KB;
+    const int nb = min(TB - tb0, KB);          // >= 1 by the grid
+    const int n0 = (cg * SK_TILES + tile) * 16;
+    const uint8_t* wrow = a.w + (int64_t)min(n0 + l16, a.N - 1) * a.ldw_bytes;
+    const bool row_ok = l16 < a.M;
+    const void* xrow = static_cast<const uint8_t*>(a.x) + (int64_t)min(l16, a.M - 1) * a.ldx * (XF32 ? 4 : 2);
+
+    // this wave's k-blocks of the range: sub, sub + SK_SUB, ... (blocks past the range
+    // re-read its last one: a static number of loads; their products are not added)
+    // x first: vmcnt counts in issue order, so the split below waits for x alone
+    const int xt = wave;                       // the k-block of x this wave splits (if < nb)
+    XChunk<S, XF32> xc;
+    load_x<S, XF32, true>(xc, xrow, row_ok, (tb0 + min(xt, nb - 1)) * 32 * S + q * 8 * S, a.K);
+    WChunk<BITS, S> wc[RB];
+    if constexpr (PACKED) {
+        // MFMA-packed int8 weight (lq_pack_weights_i8): tile (n-tile, 64-k step) is 1 KB in
+        // this kernel's lane order, so each wave load is 1 KB of consecutive bytes
+        static_assert(BITS == 8 && S == 2, "the packed layout holds 64-k steps of int8 codes");
+        const int KS = (a.K + 63) / 64;
+        const int ntile = min(n0 / 16, (a.N - 1) / 16);
+        const uint8_t* tb = a.w + (int64_t)ntile * KS * 1024 + lane * 16;
+#pragma unroll
+        for (int j = 0; j < RB; ++j) {
+            const vu4 v = __builtin_nontemporal_load(
+                reinterpret_cast<const vu4*>(tb + (int64_t)(tb0 + min(sub + SK_SUB * j, nb - 1)) * 1024));
+            wc[j].w[0] = v.x; wc[j].w[1] = v.y; wc[j].w[2] = v.z; wc[j].w[3] = v.w;
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < RB; ++j)
+            load_w<BITS, S, true>(wc[j], wrow, (tb0 + min(sub + SK_SUB * j, nb - 1)) * 32 * S + q * 8 * S, a.K);
+    }
+    if constexpr (GROUPED) {
+        if (sub == 0)
+            for (int i = lane; i < 16 * nb; i += 64) {
+                const int r = i / nb, t = i - r * nb;
+                const int64_t gi = (int64_t)min(n0 + r, a.N - 1) * a.G + (tb0 + t);
+                gsc[(tile * 16 + r) * KB + t] = a.w_scale[gi];
+                gbi[(tile * 16 + r) * KB + t] = a.g_bias ? a.g_bias[gi] : 0.0f;
+            }
+    }
+
+    // split one k-block of x (KB <= SK_WAVES): the block's pre-scale per row, hi / lo halves
+    // in the lanes' fragment order (as wo_xprep_kernel), {2^-e, block sum} per row
+    static_assert(KB <= SK_WAVES, "one k-block of x per wave");
+    {
+        float xv[NX];
+        float amax = 0.0f, bsum = 0.0f;
+        const bool live = row_ok && xt < nb && (tb0 + xt) * 32 * S + q * 8 * S < a.K;
+#pragma unroll
+        for (int e = 0; e < NX; ++e) {
+            xv[e] = live ? x_at<S, XF32>(xc, e) : 0.0f;
+            amax = fmaxf(amax, fabsf(xv[e]));
+            bsum += xv[e];
+        }
+        amax = fmaxf(amax, __shfl_xor(amax, 16, 64));
+        amax = fmaxf(amax, __shfl_xor(amax, 32, 64));
+        bsum += __shfl_xor(bsum, 16, 64);
+        bsum += __shfl_xor(bsum, 32, 64);
+        int e2 = 0;
+        if (XF32 && amax > 0.0f && amax <= 3.0e38f) e2 = min(max(14 - ilogbf(amax), -120), 120);
+        const float up = XF32 ? ldexpf(1.0f, e2) : 1.0f;
+        if (xt < nb) {
+            vu4* dst = xs + xt * SL * 64 + lane;
+#pragma unroll
+            for (int j = 0; j < S; ++j) {
+                h8 hi, lo;
+#pragma unroll
+                for (int h = 0; h < 8; ++h) {
+                    const float v = xv[8 * j + korder<BITS>(h)] * up;
+                    const _Float16 vh = (_Float16)v;
+                    hi[h] = vh;
+                    if constexpr (XF32) lo[h] = (_Float16)(v - (float)vh);
+                }
+                if constexpr (XF32) {
+                    dst[(2 * j) * 64] = __builtin_bit_cast(vu4, hi);
+                    dst[(2 * j + 1) * 64] = __builtin_bit_cast(vu4, lo);
+                } else {
+                    dst[j * 64] = __builtin_bit_cast(vu4, hi);
+                }
+            }
+            if (q == 0) xmeta[xt * 16 + l16] = make_float2(XF32 ? ldexpf(1.0f, -e2) : 1.0f, bsum);
+        }
+    }
+    __syncthreads();
+
+    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+    float xtot = 0.0f;
+#pragma unroll
+    for (int j = 0; j < RB; ++j) {
+        const int t = sub + SK_SUB * j;
+        if (t < nb) {  // wave-uniform; a predicate keeps wc[] in registers
+            const vu4* xf = xs + t * SL * 64 + lane;
+            const float2 mt = xmeta[t * 16 + l16];
+            f4 blk = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int st = 0; st < S; ++st) {
+                const h8 wa = unpack_step<BITS, SIGNED>(&wc[j].w[st * NW / S]);
+                if constexpr (XF32) {
+                    blk = mfma16(wa, __builtin_bit_cast(h8, xf[(2 * st) * 64]), blk);
+                    blk = mfma16(wa, __builtin_bit_cast(h8, xf[(2 * st + 1) * 64]), blk);
+                } else {
+                    blk = mfma16(wa, __builtin_bit_cast(h8, xf[st * 64]), blk);
+                }
+            }
+            if constexpr (GROUPED) {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int r = (tile * 16 + 4 * q + i) * KB + t;
+                    acc[i] += gsc[r] * (blk[i] * mt.x) + gbi[r] * mt.y;
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[i] += blk[i] * mt.x;
+                xtot += mt.y;
+            }
+        }
+    }
+    // the sub-ranges of each tile meet in LDS, added in sub-range order
+    red[wave * 64 + lane] = acc;
+    if (!GROUPED && tile == 0 && q == 0) redx[sub * 16 + l16] = xtot;
+    __syncthreads();
+    if (sub != 0) return;
+    acc = red[tile * 64 + lane];
+    xtot = redx[l16];
+#pragma unroll
+    for (int u = 1; u < SK_SUB; ++u) {
+        acc += red[(u * SK_TILES + tile) * 64 + lane];
+        if (!GROUPED) xtot += redx[u * 16 + l16];
+    }
+    if (sk.splits > 1) {
+        float* dst = sk.part + (((int64_t)range * gridDim.x + cg) * SK_TILES + tile) * 256 + lane * 4;
+        *reinterpret_cast<f4*>(dst) = acc;
+        if (!GROUPED && tile == 0 && q == 0 && cg == 0) sk.part_x[range * 16 + l16] = xtot;
+        return;
+    }
+    if (n0 >= a.N || !row_ok) return;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int n = n0 + 4 * q + i;
+        if (n < a.N) {
+            float v = acc[i];
+            if constexpr (!GROUPED) {
+                if (a.w_zp) v = v - a.w_zp[n] * xtot;
+                v = a.w_scale[n] * v;
+            }
+            if (a.bias) v = v + a.bias[n];
+            if (a.relu && v <= 0.0f) v = 0.0f;
+            if constexpr (XF32)
+                reinterpret_cast<float*>(a.y)[(int64_t)l16 * a.ldy + n] = v;
+            else
+                reinterpret_cast<_Float16*>(a.y)[(int64_t)l16 * a.ldy + n] = (_Float16)v;
+        }
+    }
+}
+
+// Adds the K ranges' tile sums in range order and runs the epilogue: one thread per lane
+// slot of a tile (4 outputs of one activation row).
+template <bool XF32, bool GROUPED>
+__global__ __launch_bounds__(256) void wo_sk_reduce_kernel(WoSkArgs sk, int groups) {
+    const WoArgs& a = sk.w;
+    const int64_t g = (int64_t)blockIdx.x * 256 + threadIdx.x;  // (group, tile, lane)
+    if (g >= (int64_t)groups * SK_TILES * 64) return;
+    const int lane = (int)(g & 63), q = lane >> 4, l16 = lane & 15;
+    const int64_t gt = g >> 6;  // group * SK_TILES + tile
+    const int n0 = (int)(gt * 16);
+    if (n0 >= a.N || l16 >= a.M) return;
+    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+    float xtot = 0.0f;
+    // eight ranges' loads in flight, then their sums in range order
+    for (int r0 = 0; r0 < sk.splits; r0 += 8) {
+        f4 v[8];
+        float xv[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int r = min(r0 + u, sk.splits - 1);
+            v[u] = *reinterpret_cast<const f4*>(sk.part + ((int64_t)r * groups * SK_TILES + gt) * 256 + lane * 4);
+            xv[u] = GROUPED ? 0.0f : sk.part_x[r * 16 + l16];
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (r0 + u < sk.splits) {
+                acc += v[u];
+                if (!GROUPED) xtot += xv[u];
+            }
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int n = n0 + 4 * q + i;
+        if (n < a.N) {
+            float v = acc[i];
+            if constexpr (!GROUPED) {
+                if (a.w_zp) v = v - a.w_zp[n] * xtot;
+                v = a.w_scale[n] * v;
+            }
+            if (a.bias) v = v + a.bias[n];
+            if (a.relu && v <= 0.0f) v = 0.0f;
+            if constexpr (XF32)
+                reinterpret_cast<float*>(a.y)[(int64_t)l16 * a.ldy + n] = v;
+            else
+                reinterpret_cast<_Float16*>(a.y)[(int64_t)l16 * a.ldy + n] = (_Float16)v;
+        }
+    }
+}
+
 // ------------------------------------------------- one or two activation rows (VALU)
 //
 // For M <= 2 the MFMA's 16 activation columns are mostly empty and the per-block hi/lo split
@@ -935,6 +1188,73 @@ size_t wo_prep_bytes(int64_t M, const WoPlan& p, int S) {
     return (size_t)blocks * (64 * 2 * S * sizeof(vu4) + 16 * sizeof(float2));
 }
 
+// Split-K layout of wo_gemv_sk_kernel: 64-column groups x K ranges of SK_RANGE_K.
+struct SkPlan {
+    int splits;
+    int64_t groups;
+};
+
+SkPlan sk_plan(int64_t N, int64_t K) {
+    return SkPlan{(int)((K + SK_RANGE_K - 1) / SK_RANGE_K), (N + 16 * SK_TILES - 1) / (16 * SK_TILES)};
+}
+
+// Workspace: the ranges' tile sums and activation row sums (none for a single range).
+size_t sk_ws_bytes(const SkPlan& p) {
+    if (p.splits <= 1) return 0;
+    const size_t part = (size_t)p.splits * (size_t)p.groups * SK_TILES * 256 * sizeof(float);
+    return ((part + 255) & ~(size_t)255) + (size_t)p.splits * 16 * sizeof(float);
+}
+
+// The split-K route: 3 <= M <= 16 with vector-aligned operands (the kernel's loads are
+// unconditional 16-byte loads) and, when K is split, the workspace for the range sums.
+constexpr int SK_MIN_M = 3, SK_MAX_M = 16;
+
+// Row-major weights take the split-K kernel from 12 rows, or for weights over 16 MB (measured
+// at K = N = 4096: M = 3..8 9.2-10 us on wo_gemv_kernel's in-workgroup split against 11.1-11.8
+// here, equal from M = 12; at 11008 x 4096 this kernel is faster from M = 3: 20.5 against 24 us).
+bool sk_preferred(const WoArgs& a) { return a.M >= 12 || (int64_t)a.N * a.K > ((int64_t)1 << 24); }
+
+bool sk_fits(const WoArgs& a, bool xf32, int S, void* ws, size_t ws_bytes) {
+    if (a.M < SK_MIN_M || a.M > SK_MAX_M) return false;
+    const int eb = xf32 ? 4 : 2;
+    if (!aligned16(a.w) || a.ldw_bytes % 16 || a.K % (8 * S) || a.K < 8 * S) return false;
+    if (!aligned16(a.x) || (a.ldx * eb) % 16) return false;
+    const SkPlan p = sk_plan(a.N, a.K);
+    if (p.splits > 65535 || p.groups > ((int64_t)1 << 30)) return false;
+    const size_t need = sk_ws_bytes(p);
+    return need == 0 || (ws && aligned16(ws) && ws_bytes >= need);
+}
+
+template <int BITS, bool SIGNED, int S, bool GROUPED, bool PACKED = false>
+int launch_sk(const WoArgs& a, bool xf32, hipStream_t st, void* ws) {
+    const SkPlan p = sk_plan(a.N, a.K);
+    WoSkArgs k{};
+    k.w = a;
+    k.splits = p.splits;
+    if (p.splits > 1) {
+        const size_t part = (size_t)p.splits * (size_t)p.groups * SK_TILES * 256 * sizeof(float);
+        k.part = static_cast<float*>(ws);
+        k.part_x = reinterpret_cast<float*>(static_cast<char*>(ws) + ((part + 255) & ~(size_t)255));
+    }
+    const dim3 grid((unsigned)p.groups, (unsigned)p.splits);
+    if (xf32)
+        hipLaunchKernelGGL((wo_gemv_sk_kernel<BITS, SIGNED, S, true, GROUPED, PACKED>), grid, dim3(64 * SK_WAVES), 0,
+                           st, k);
+    else
+        hipLaunchKernelGGL((wo_gemv_sk_kernel<BITS, SIGNED, S, false, GROUPED, PACKED>), grid, dim3(64 * SK_WAVES), 0,
+                           st, k);
+    if (p.splits > 1) {
+        const unsigned blocks = (unsigned)((p.groups * SK_TILES * 64 + 255) / 256);
+        if (xf32)
+            hipLaunchKernelGGL((wo_sk_reduce_kernel<true, GROUPED>), dim3(blocks), dim3(256), 0, st, k, (int)p.groups);
+        else
+            hipLaunchKernelGGL((wo_sk_reduce_kernel<false, GROUPED>), dim3(blocks), dim3(256), 0, st, k, (int)p.groups);
+    }
+    note_path(PACKED ? (p.splits > 1 ? "wo packed split-k" : "wo packed split-k single range")
+                     : (p.splits > 1 ? "wo split-k" : "wo split-k single range"));
+    return LQ_OK;
+}
+
 template <int BITS, bool SIGNED, int S, bool GROUPED, bool VEC>
 int launch_wo(const WoPlan& p, WoArgs a, bool xf32, hipStream_t st, void* ws, size_t ws_bytes) {
     const dim3 grid((unsigned)((a.N + 15) / 16), (unsigned)((a.M + 15) / 16));
@@ -952,10 +1272,13 @@ int launch_wo(const WoPlan& p, WoArgs a, bool xf32, hipStream_t st, void* ws, si
         a.xp = xp;
         a.xm = xm;
         hipLaunchKernelGGL((wo_gemv_kernel<BITS, SIGNED, S, true, GROUPED, VEC, true>), grid, block, p.lds, st, a);
+        note_path("wo mfma presplit");
+        return LQ_OK;
     } else if (xf32)
         hipLaunchKernelGGL((wo_gemv_kernel<BITS, SIGNED, S, true, GROUPED, VEC>), grid, block, p.lds, st, a);
     else
         hipLaunchKernelGGL((wo_gemv_kernel<BITS, SIGNED, S, false, GROUPED, VEC>), grid, block, p.lds, st, a);
+    note_path("wo mfma");
     return LQ_OK;
 }
 
@@ -992,6 +1315,7 @@ bool launch_wv(WvArgs a, bool xf32, hipStream_t st) {
         constexpr bool fits = !GROUPED || (JV <= 8 && !(BITS == 4 && MXV == 2 && JV > 4));
         if constexpr (fits) {
             hipLaunchKernelGGL((wo_gemv_valu_kernel<BITS, SIGNED, GROUPED, MXV, XV, JV>), grid, block, lds, st, a);
+            note_path("wo valu");
             return true;
         } else {
             return false;
@@ -1026,9 +1350,10 @@ using namespace lq;
 extern "C" {
 
 size_t lq_gemv_w8_workspace_size(int64_t M, int64_t N, int64_t K) {
-    (void)N;
-    if (M <= 2 || K <= 0 || M >= WO_MAX_DIM || K >= WO_MAX_DIM) return 0;  // VALU path: no split
-    return wo_prep_bytes(M, wo_plan(K, 2, false, wo_max_waves(2, true, false)), 2);
+    if (M <= 2 || K <= 0 || M >= WO_MAX_DIM || K >= WO_MAX_DIM || N >= WO_MAX_DIM) return 0;  // VALU path
+    const size_t prep = wo_prep_bytes(M, wo_plan(K, 2, false, wo_max_waves(2, true, false)), 2);
+    if (M <= SK_MAX_M) return std::max(prep, sk_ws_bytes(sk_plan(std::max<int64_t>(N, 1), K)));
+    return prep;
 }
 
 int lq_gemv_w8(const void* d_x, int x_dtype, int64_t ldx, const int8_t* d_W, int64_t ldw,
@@ -1067,6 +1392,10 @@ int lq_gemv_w8(const void* d_x, int x_dtype, int64_t ldx, const int8_t* d_W, int
         v.M = (int)M; v.N = (int)N; v.K = (int)K;
         if (launch_wv<8, true, false>(v, xf32, st)) return launch_status("lq_gemv_w8");
     }
+    if (sk_preferred(a) && sk_fits(a, xf32, 2, d_workspace, workspace_bytes)) {
+        const int rc = launch_sk<8, true, 2, false>(a, xf32, st, d_workspace);
+        return rc ? rc : launch_status("lq_gemv_w8");
+    }
     const bool vec = aligned16(d_W) && ldw % 16 == 0 && K % 16 == 0 && K >= 16 && aligned16(d_x) &&
                      ldx % (xf32 ? 4 : 8) == 0;
     if (vec) launch_wo<8, true, 2, false, true>(p, a, xf32, st, d_workspace, workspace_bytes);
@@ -1074,12 +1403,55 @@ int lq_gemv_w8(const void* d_x, int x_dtype, int64_t ldx, const int8_t* d_W, int
     return launch_status("lq_gemv_w8");
 }
 
+size_t lq_gemv_w8_packed_workspace_size(int64_t M, int64_t N, int64_t K) {
+    if (M < 1 || M > SK_MAX_M || K <= 0 || K >= WO_MAX_DIM || N <= 0 || N >= WO_MAX_DIM) return 0;
+    return sk_ws_bytes(sk_plan(N, K));
+}
+
+int lq_gemv_w8_packed(const void* d_x, int x_dtype, int64_t ldx, const int8_t* d_W_packed,
+                      const float* d_w_scale, const float* d_w_zero_point, const float* d_bias, void* d_y,
+                      int64_t ldy, int64_t M, int64_t N, int64_t K, int flags, void* d_workspace,
+                      size_t workspace_bytes, void* stream) {
+    LQ_REQUIRE(M >= 0 && N >= 0 && K >= 0 && N < WO_MAX_DIM && K < WO_MAX_DIM, "lq_gemv_w8_packed: bad shape");
+    LQ_REQUIRE(M <= SK_MAX_M, "lq_gemv_w8_packed: at most 16 activation rows (use lq_gemv_w8)");
+    LQ_REQUIRE(x_dtype == LQ_F32 || x_dtype == LQ_F16, "lq_gemv_w8_packed: x_dtype must be LQ_F32 or LQ_F16");
+    LQ_REQUIRE((flags & ~LQ_EPI_RELU) == 0, "lq_gemv_w8_packed: unknown flags");
+    if (M == 0 || N == 0) return LQ_OK;
+    LQ_REQUIRE(d_x && d_W_packed && d_y && d_w_scale, "lq_gemv_w8_packed: NULL pointer");
+    LQ_REQUIRE(ldx >= K && ldy >= N, "lq_gemv_w8_packed: leading dimension too small");
+    const bool xf32 = x_dtype == LQ_F32;
+    const int eb = xf32 ? 4 : 2;
+    LQ_REQUIRE(K >= 16 && K % 16 == 0, "lq_gemv_w8_packed: K must be a positive multiple of 16");
+    LQ_REQUIRE(aligned16(d_W_packed) && aligned16(d_x) && (ldx * eb) % 16 == 0,
+               "lq_gemv_w8_packed: the weight, x and its rows must be 16-byte aligned");
+    const size_t need = sk_ws_bytes(sk_plan(N, K));
+    LQ_REQUIRE(need == 0 || (d_workspace && aligned16(d_workspace) && workspace_bytes >= need),
+               "lq_gemv_w8_packed: workspace smaller than lq_gemv_w8_packed_workspace_size");
+    WoArgs a{};
+    a.x = d_x;
+    a.ldx = ldx;
+    a.w = reinterpret_cast<const uint8_t*>(d_W_packed);
+    a.ldw_bytes = K;
+    a.w_scale = d_w_scale;
+    a.w_zp = d_w_zero_point;
+    a.bias = d_bias;
+    a.y = d_y;
+    a.ldy = ldy;
+    a.relu = (flags & LQ_EPI_RELU) ? 1 : 0;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    const int rc = launch_sk<8, true, 2, false, true>(a, xf32, as_stream(stream), d_workspace);
+    return rc ? rc : launch_status("lq_gemv_w8_packed");
+}
+
 size_t lq_group_matmul_workspace_size(int64_t M, int64_t N, int64_t K, int group_size) {
-    (void)N;
-    if (M <= 2 || K <= 0 || M >= WO_MAX_DIM || K >= WO_MAX_DIM) return 0;
+    if (M <= 2 || K <= 0 || M >= WO_MAX_DIM || K >= WO_MAX_DIM || N >= WO_MAX_DIM) return 0;
     if (group_size != 32 && group_size != 64 && group_size != 128) return 0;
     const int S = group_size / 32;
-    return wo_prep_bytes(M, wo_plan(K, S, true, wo_max_waves(S, true, true)), S);
+    const size_t prep = wo_prep_bytes(M, wo_plan(K, S, true, wo_max_waves(S, true, true)), S);
+    if (M <= SK_MAX_M) return std::max(prep, sk_ws_bytes(sk_plan(std::max<int64_t>(N, 1), K)));
+    return prep;
 }
 
 int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d_packed,
@@ -1149,6 +1521,16 @@ int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d
         v.M = (int)M; v.N = (int)N; v.K = (int)K; v.G = a.G; v.gs = group_size;
         const bool ok = bits == 8 ? launch_wv<8, false, true>(v, xf32, st) : launch_wv<4, false, true>(v, xf32, st);
         if (ok) return launch_status("lq_group_matmul");
+    }
+    if (sk_preferred(a) && sk_fits(a, xf32, S, d_workspace, workspace_bytes)) {
+        int rc;
+        if (bits == 8) rc = S == 1 ? launch_sk<8, false, 1, true>(a, xf32, st, d_workspace)
+                            : S == 2 ? launch_sk<8, false, 2, true>(a, xf32, st, d_workspace)
+                                     : launch_sk<8, false, 4, true>(a, xf32, st, d_workspace);
+        else rc = S == 1 ? launch_sk<4, false, 1, true>(a, xf32, st, d_workspace)
+                  : S == 2 ? launch_sk<4, false, 2, true>(a, xf32, st, d_workspace)
+                           : launch_sk<4, false, 4, true>(a, xf32, st, d_workspace);
+        return rc ? rc : launch_status("lq_group_matmul");
     }
     const bool vec = aligned16(d_x) && ldx % (xf32 ? 4 : 8) == 0;
 #define LQ_GM(B, SS)                                                          \

@@ -127,6 +127,9 @@ def gemm_w8a8(codes: Tensor, code_type: int, a_scale: Tensor, a_zero_point: Tens
     return y
 
 
+GEMV_PACKED_MAX_M = 16  # lq_gemv_w8_packed's row limit
+
+
 def gemv_w8(x: Tensor, w: WeightCache, bias: Tensor | None, relu: bool = False) -> Tensor:
     """Weight-only ``x @ dequantize(W)^T + bias`` (ReLU) for a float32 / float16 input
     (``lq_gemv_w8``): the int8 weight is read once, never expanded to float."""
@@ -140,6 +143,18 @@ def gemv_w8(x: Tensor, w: WeightCache, bias: Tensor | None, relu: bool = False) 
     if x.dtype not in (np.float32, np.float16):
         raise TypeError(f"linear: float32 or float16 input expected, got {x.dtype}")
     b = on_device(bias) if bias is not None else None
+    xt = _C.F32 if x.dtype == np.float32 else _C.F16
+    # 3 <= M <= 16: the MFMA-packed weight (1 KB per wave load); one or two rows read whole
+    # weight rows on the VALU kernel of lq_gemv_w8
+    use_packed = 3 <= M <= GEMV_PACKED_MAX_M and K >= 16 and x.data_ptr() % 16 == 0
+    packed = w.packed() if use_packed else None
+    if packed is not None:
+        ws_bytes = _C.lib().lq_gemv_w8_packed_workspace_size(M, w.N, K)
+        _C.call("lq_gemv_w8_packed", x.data_ptr(), xt, K, packed.data_ptr(), w.scale.data_ptr(),
+                w.zero_point.data_ptr() if w.zero_point is not None else None,
+                b.data_ptr() if b is not None else None, y.data_ptr(), w.N, M, w.N, K,
+                _C.EPI_RELU if relu else 0, workspace.get(ws_bytes), ws_bytes, None)
+        return y
     ws_bytes = _C.lib().lq_gemv_w8_workspace_size(M, w.N, K)
     _C.call("lq_gemv_w8", x.data_ptr(), _C.F32 if x.dtype == np.float32 else _C.F16, K,
             w.codes.data_ptr(), K, w.scale.data_ptr(),

@@ -101,12 +101,12 @@ def test_gemv_w8_fp16(gpu, M, N, K):
     _close(got, ref, half=True)
 
 
-@pytest.mark.parametrize("M,N,K", [(3, 64, 256), (16, 4096, 4096), (37, 300, 784), (9, 50, 1000)])
+@pytest.mark.parametrize("M,N,K", [(17, 64, 256), (24, 4096, 4096), (37, 300, 784), (19, 50, 1000)])
 def test_gemv_w8_presplit_matches_inline(gpu, M, N, K):
-    """With a workspace the fp32 activations are split into fp16 halves once per call; the
-    products and their order are those of the split done inside every workgroup, so both
-    calls agree bit for bit (with rows of very different magnitude to exercise the
-    per-block pre-scale)."""
+    """Above 16 rows, with a workspace the fp32 activations are split into fp16 halves once
+    per call; the products and their order are those of the split done inside every
+    workgroup, so both calls agree bit for bit (with rows of very different magnitude to
+    exercise the per-block pre-scale)."""
     from lucid_amd import _C
 
     rng = np.random.default_rng(M * 7 + K)
@@ -129,6 +129,125 @@ def test_gemv_w8_presplit_matches_inline(gpu, M, N, K):
     np.testing.assert_array_equal(outs[0], outs[1])
     ref = _gemv_ref(x, W, s, z=z)
     _close(outs[0], ref)
+
+
+SPLIT_K_SHAPES = [(16, 4096, 4096), (3, 4608, 4096), (7, 11008, 4096), (16, 4096, 11008), (12, 100, 784),
+                  (16, 1000, 1024), (13, 64, 2048), (14, 300, 16)]
+
+
+@pytest.mark.parametrize("half", [False, True])
+@pytest.mark.parametrize("M,N,K", SPLIT_K_SHAPES)
+def test_gemv_w8_split_k(gpu, M, N, K, half):
+    """3 <= M <= 16 with the workspace, from 12 rows or over 16 MB of weight: the split-K
+    kernel (x split once per workgroup into LDS, the K ranges' sums added in range order by a
+    second launch).  Against the oracle at
+    the same tolerance, with a zero point, bias and ReLU; three calls in a row give the same
+    bits."""
+    from lucid_amd import _C
+
+    print(f"gemv split-k M={M} N={N} K={K} half={half}", flush=True)
+    rng = np.random.default_rng(M * 1000 + K + half)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[:, ::53] *= 30.0
+    x[-1] *= 1e-6
+    W = rng.integers(-128, 128, (N, K)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-2 if half else 1e-1, N).astype(np.float32)
+    z = rng.integers(-4, 5, N).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    outs = [run_gemv(gpu, x, W, s, z=z, b=b, relu=True, half=half) for _ in range(3)]
+    assert _C.last_path() in ("wo split-k", "wo split-k single range")
+    for o in outs[1:]:
+        np.testing.assert_array_equal(o.view(np.uint16 if half else np.uint32),
+                                      outs[0].view(np.uint16 if half else np.uint32))
+    xr = x.astype(np.float16).astype(np.float32) if half else x
+    _close(outs[0], _gemv_ref(xr, W, s, z=z, b=b, relu=True), half=half)
+
+
+def test_gemv_w8_split_k_interleaved_shapes(gpu):
+    """Calls of different shapes sharing one workspace, alternating: each call's result
+    depends only on its own operands (same bits on every repetition)."""
+    from lucid_amd import _C
+
+    rng = np.random.default_rng(5)
+    cases = []
+    for (M, N, K) in ((16, 4096, 4096), (12, 256, 3072), (16, 11008, 4096)):
+        x = rng.standard_normal((M, K)).astype(np.float32)
+        W = rng.integers(-128, 128, (N, K)).astype(np.int8)
+        s = rng.uniform(1e-3, 1e-1, N).astype(np.float32)
+        cases.append((x, W, s, _gemv_ref(x, W, s)))
+    nbytes = max(_C.lib().lq_gemv_w8_workspace_size(c[0].shape[0], c[1].shape[0], c[0].shape[1]) for c in cases)
+    ws = gpu.empty((nbytes,), np.uint8, "gpu")
+    first = {}
+    for rep in range(3):
+        for i, (x, W, s, ref) in enumerate(cases):
+            M, K = x.shape
+            N = W.shape[0]
+            y = gpu.empty((M, N), np.float32, "gpu")
+            _C.call("lq_gemv_w8", _t(gpu, x).data_ptr(), _C.F32, K, _t(gpu, W).data_ptr(), K,
+                    _t(gpu, s).data_ptr(), None, None, y.data_ptr(), N, M, N, K, 0, ws.data_ptr(), nbytes, None)
+            got = y.numpy()
+            if rep == 0:
+                _close(got, ref)
+                first[i] = got
+            else:
+                np.testing.assert_array_equal(got, first[i])
+
+
+def run_gemv_packed(L, x, W, s, z=None, b=None, relu=False, half=False):
+    from lucid_amd import _C
+
+    M, K = x.shape
+    N = W.shape[0]
+    dW = _t(L, W)
+    pk = L.empty((max(_C.lib().lq_packed_weights_size(N, K), 16),), np.int8, "gpu")
+    _C.call("lq_pack_weights_i8", dW.data_ptr(), K, N, K, pk.data_ptr(), None)
+    xd = _t(L, x.astype(np.float16 if half else np.float32))
+    ds = _t(L, s.astype(np.float32))
+    dz = _t(L, z.astype(np.float32)) if z is not None else None
+    db = _t(L, b.astype(np.float32)) if b is not None else None
+    y = L.empty((M, N), np.float16 if half else np.float32, "gpu")
+    ws_bytes = _C.lib().lq_gemv_w8_packed_workspace_size(M, N, K)
+    ws = L.empty((max(ws_bytes, 1),), np.uint8, "gpu")
+    _C.call("lq_gemv_w8_packed", xd.data_ptr(), _C.F16 if half else _C.F32, K, pk.data_ptr(), ds.data_ptr(),
+            dz.data_ptr() if dz is not None else None, db.data_ptr() if db is not None else None, y.data_ptr(),
+            N, M, N, K, _C.EPI_RELU if relu else 0, ws.data_ptr(), ws_bytes, None)
+    return y.numpy()
+
+
+@pytest.mark.parametrize("half", [False, True])
+@pytest.mark.parametrize("M,N,K", [(16, 4096, 4096), (1, 11008, 4096), (2, 4096, 11008), (8, 100, 784),
+                                   (3, 1000, 1024), (16, 70, 16), (5, 33, 528)])
+def test_gemv_w8_packed(gpu, M, N, K, half):
+    """The decode entry over the MFMA-packed weight: against the oracle like lq_gemv_w8, with a
+    zero point, bias and ReLU, and bit for bit lq_gemv_w8 where that takes its split-K route
+    (same kernel, same products and order; only where the weight bytes come from differs)."""
+    from lucid_amd import _C
+
+    print(f"gemv packed M={M} N={N} K={K} half={half}", flush=True)
+    rng = np.random.default_rng(M * 31 + N + K + half)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    x[:, ::41] *= 25.0
+    W = rng.integers(-128, 128, (N, K)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-2 if half else 1e-1, N).astype(np.float32)
+    z = rng.integers(-4, 5, N).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    got = run_gemv_packed(gpu, x, W, s, z=z, b=b, relu=True, half=half)
+    assert _C.last_path() in ("wo packed split-k", "wo packed split-k single range")
+    xr = x.astype(np.float16).astype(np.float32) if half else x
+    _close(got, _gemv_ref(xr, W, s, z=z, b=b, relu=True), half=half)
+    rowmajor = run_gemv(gpu, x, W, s, z=z, b=b, relu=True, half=half)
+    if _C.last_path() == "wo split-k" or _C.last_path() == "wo split-k single range":
+        np.testing.assert_array_equal(got.view(np.uint16 if half else np.uint32),
+                                      rowmajor.view(np.uint16 if half else np.uint32))
+
+
+def test_gemv_w8_packed_rejects(gpu):
+    from lucid_amd import _C
+
+    with pytest.raises(_C.LucidError, match="16 activation rows"):
+        _C.call("lq_gemv_w8_packed", 16, _C.F32, 64, 16, 16, None, None, 16, 64, 17, 64, 64, 0, None, 0, None)
+    with pytest.raises(_C.LucidError, match="multiple of 16"):
+        _C.call("lq_gemv_w8_packed", 16, _C.F32, 72, 16, 16, None, None, 16, 64, 4, 64, 72, 0, None, 0, None)
 
 
 def test_gemv_w8_tiny_and_huge_rows(gpu):
@@ -221,6 +340,40 @@ def test_group_matmul_presplit_matches_inline(gpu, bits, gs):
                 ws.data_ptr() if wsb else None, wsb, None)
         outs.append(y.numpy())
     np.testing.assert_array_equal(outs[0], outs[1])
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("gs", [32, 64, 128])
+@pytest.mark.parametrize("M,N,K", [(16, 4096, 4096), (5, 4608, 4096), (12, 1000, 2048)])
+def test_group_matmul_split_k(gpu, M, N, K, bits, gs):
+    """Group-wise weights on the split-K kernel (3 <= M <= 16 with the workspace): the bench
+    gate and the scale-aware 1e-5 against float64, repeatable bit for bit."""
+    from lucid_amd import _C
+    from lucid_amd.quantization import _qgemm
+
+    print(f"group split-k M={M} N={N} K={K} bits={bits} gs={gs}", flush=True)
+    rng = np.random.default_rng(M + N + bits + gs)
+    w = rng.standard_normal((N, K)).astype(np.float32)
+    x = rng.standard_normal((M, K)).astype(np.float32)
+    b = rng.standard_normal(N).astype(np.float32)
+    packed, scales, biases = _qgemm.quantize(_t(gpu, w), group_size=gs, bits=bits)
+    ws_bytes = _C.lib().lq_group_matmul_workspace_size(M, N, K, gs)
+    ws = gpu.empty((max(ws_bytes, 1),), np.uint8, "gpu")
+    xd, bd = _t(gpu, x), _t(gpu, b)
+    outs = []
+    for _ in range(2):
+        y = gpu.empty((M, N), np.float32, "gpu")
+        _C.call("lq_group_matmul", xd.data_ptr(), _C.F32, K, packed.data_ptr(), scales.data_ptr(),
+                biases.data_ptr(), bd.data_ptr(), y.data_ptr(), N, M, N, K, gs, bits, 1, 0, ws.data_ptr(), ws_bytes,
+                None)
+        outs.append(y.numpy())
+        assert _C.last_path() in ("wo split-k", "wo split-k single range")
+    np.testing.assert_array_equal(outs[0], outs[1])
+    wd = O.group_dequantize(packed.numpy().view(np.uint32), scales.numpy(), biases.numpy(), gs,
+                            bits).astype(np.float64)
+    ref = x.astype(np.float64) @ wd.T + b
+    assert np.max(np.abs(outs[0] - ref)) / max(np.max(np.abs(ref)), 1e-12) <= 1e-4
+    _close(outs[0], ref)
 
 
 @pytest.mark.parametrize("M,N,K,bits,gs", [(1, 4096, 4096, 4, 64), (16, 11008, 4096, 8, 64),
