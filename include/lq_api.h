@@ -550,6 +550,12 @@ int lq_layer_norm_f32(const float* d_x, int64_t ldx, float* d_y, int64_t ldy, in
 int lq_gelu_tanh_f32(const float* d_x, float* d_y, int64_t n, void* stream);
 /* y = a + b elementwise (residual adds). */
 int lq_add_f32(const float* d_a, const float* d_b, float* d_y, int64_t n, void* stream);
+/* y = a + fl32(b * s), each operation rounded once: a LoRA layer's output plus its scaled
+ * low-rank update, and a merge's weight plus the scaled delta
+ * (lucid/peft/tuners/lora/_layer.py:796-803, 971-989). */
+int lq_add_scaled_f32(const float* d_a, const float* d_b, float s, float* d_y, int64_t n, void* stream);
+/* y [cols, rows] = x [rows, cols]^T (float32; y must not alias x). */
+int lq_transpose_f32(const float* d_x, int64_t rows, int64_t cols, float* d_y, void* stream);
 /* qkv [B, n, 3, H, hd] float32 -> q [B, H, n, hd] fp16, and k / v written into the fp16
  * caches [B, H, T_max, hd] at positions pos .. pos + n - 1. */
 int lq_kv_append_f16(const float* d_qkv, int64_t B, int64_t n, int64_t H, int64_t hd, int64_t pos0,

@@ -113,6 +113,8 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_layer_norm_f32": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P, _F, _P]),
     "lq_gelu_tanh_f32": (_I, [_P, _P, _I64, _P]),
     "lq_add_f32": (_I, [_P, _P, _P, _I64, _P]),
+    "lq_add_scaled_f32": (_I, [_P, _P, _F, _P, _I64, _P]),
+    "lq_transpose_f32": (_I, [_P, _I64, _I64, _P, _P]),
     "lq_kv_append_f16": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P]),
     "lq_attention_f16": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _F, _P, _P]),
     "lq_increment_i32": (_I, [_P, ctypes.c_int32, _P]),

@@ -1017,8 +1017,17 @@ __global__ __launch_bounds__(256) void gemm_i8_decode_reduce_kernel(GemmArgs a, 
     if (q >= (int64_t)a.M * quads) return;
     const int m = (int)(q / quads), n = (int)(q - (int64_t)m * quads) * 4;
     if (n >= a.N) return;
+    // eight splits' loads in flight at a time (integer sums: exact in any order)
     v4i acc = v4i{0, 0, 0, 0};
-    for (int s = 0; s < splits; ++s) acc += *reinterpret_cast<const v4i*>(part + ((int64_t)s * a.M + m) * npad + n);
+    for (int s0 = 0; s0 < splits; s0 += 8) {
+        v4i v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            v[u] = *reinterpret_cast<const v4i*>(part + ((int64_t)min(s0 + u, splits - 1) * a.M + m) * npad + n);
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+            if (s0 + u < splits) acc += v[u];
+    }
     epilogue4<KIND>(a, epi_params(a), m, n, acc);
 }
 

@@ -98,6 +98,32 @@ __global__ void add_kernel(const float* __restrict__ a, const float* __restrict_
         y[i] = a[i] + b[i];
 }
 
+// y = a + fl32(b * s): the scaled add of an adapter's update, each operation rounded once
+// (the kernel is built without contraction, so no fma fuses them).
+__global__ void add_scaled_kernel(const float* __restrict__ a, const float* __restrict__ b, float s, float* __restrict__ y,
+                                  int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+        const float t = b[i] * s;
+        y[i] = a[i] + t;
+    }
+}
+
+// y[c][r] = x[r][c] through a 32 x 33 LDS tile (conflict-free transposed reads).
+__global__ __launch_bounds__(256) void transpose_kernel(const float* __restrict__ x, int64_t rows, int64_t cols,
+                                                        float* __restrict__ y) {
+    __shared__ float t[32][33];
+    const int64_t r0 = (int64_t)blockIdx.y * 32, c0 = (int64_t)blockIdx.x * 32;
+    for (int i = threadIdx.y; i < 32; i += 8) {
+        const int64_t r = r0 + i, c = c0 + threadIdx.x;
+        if (r < rows && c < cols) t[i][threadIdx.x] = x[r * cols + c];
+    }
+    __syncthreads();
+    for (int i = threadIdx.y; i < 32; i += 8) {
+        const int64_t c = c0 + i, r = r0 + threadIdx.x;
+        if (r < rows && c < cols) y[c * rows + r] = t[threadIdx.x][i];
+    }
+}
+
 // qkv [B, n, 3, H, hd] float32 -> q [B, H, n, hd] fp16; k, v appended to the caches
 // [B, H, T_max, hd] fp16 at positions pos0 .. pos0 + n - 1.
 __global__ void kv_append_kernel(const float* __restrict__ qkv, int64_t B, int64_t n, int64_t H, int64_t hd, int64_t pos0,
@@ -287,6 +313,25 @@ int lq_add_f32(const float* d_a, const float* d_b, float* d_y, int64_t n, void* 
     LQ_REQUIRE(d_a && d_b && d_y, "lq_add_f32: NULL pointer");
     hipLaunchKernelGGL(add_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), d_a, d_b, d_y, n);
     return launch_status("lq_add_f32");
+}
+
+int lq_add_scaled_f32(const float* d_a, const float* d_b, float s, float* d_y, int64_t n, void* stream) {
+    LQ_REQUIRE(n >= 0, "lq_add_scaled_f32: n < 0");
+    if (n == 0) return LQ_OK;
+    LQ_REQUIRE(d_a && d_b && d_y, "lq_add_scaled_f32: NULL pointer");
+    hipLaunchKernelGGL(add_scaled_kernel, dim3(grid_for(n)), dim3(256), 0, as_stream(stream), d_a, d_b, s, d_y, n);
+    return launch_status("lq_add_scaled_f32");
+}
+
+int lq_transpose_f32(const float* d_x, int64_t rows, int64_t cols, float* d_y, void* stream) {
+    LQ_REQUIRE(rows >= 0 && cols >= 0 && rows < ((int64_t)1 << 36) && cols < ((int64_t)1 << 36),
+               "lq_transpose_f32: bad shape");
+    if (rows == 0 || cols == 0) return LQ_OK;
+    LQ_REQUIRE(d_x && d_y && d_x != d_y, "lq_transpose_f32: NULL or aliased pointer");
+    LQ_REQUIRE((rows + 31) / 32 < 65536, "lq_transpose_f32: too many rows for the grid");
+    const dim3 grid((unsigned)((cols + 31) / 32), (unsigned)((rows + 31) / 32));
+    hipLaunchKernelGGL(transpose_kernel, grid, dim3(32, 8), 0, as_stream(stream), d_x, rows, cols, d_y);
+    return launch_status("lq_transpose_f32");
 }
 
 int lq_kv_append_f16(const float* d_qkv, int64_t B, int64_t n, int64_t H, int64_t hd, int64_t pos0,
