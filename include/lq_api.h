@@ -455,6 +455,24 @@ int lq_rnn_cell(int kind, const float* d_gx, int64_t ld_gx, const float* d_gh, i
  * (lucid/nn/quantized/conv_transpose.py:146-175); no reference counterpart as an op. */
 int lq_stride_expand(const void* d_x, int elem_type, int64_t planes, int64_t H, int64_t W, int stride_h,
                      int stride_w, const float* d_zero_point, void* d_y, void* stream);
+/* The depth gather of a 3-D convolution run as a 2-D one: x [N, C, D, HW] (elements LQ_F32,
+ * or int8 codes LQ_I8 / LQ_U8S8) -> y [N OD, groups, KD, C / groups, HW], where output depth od
+ * reads input depth e = od stride - pad + kd dilation for kernel depth kd; out-of-range
+ * depths (pad_mode 0), and with expand > 1 the depths e % expand != 0 of a transposed
+ * convolution's stride-expanded axis (e / expand otherwise), hold the zero value (the zero
+ * point code read from d_zero_point for codes, minus 128 for LQ_U8S8; 0.0 for floats);
+ * pad_mode 1 / 2 / 3 map them reflect / replicate / circular (expand 1).  The 3-D layers of
+ * lucid/nn/quantized/conv.py:491 (Conv3d), intrinsic.py:344 (ConvReLU3d) and
+ * conv_transpose.py:473 (ConvTranspose3d) and their float modules run on the 2-D
+ * implicit-GEMM convolution this way; no reference counterpart as an op. */
+int lq_depth_gather(const void* d_x, int elem_type, int64_t N, int64_t C, int64_t D, int64_t HW, int64_t groups,
+                    int64_t KD, int64_t OD, int64_t stride, int64_t pad, int64_t dilation, int64_t expand,
+                    int pad_mode, const float* d_zero_point, void* d_y, void* stream);
+/* y[a][c][b][p] = x[a][b][c][p] for elements of 1, 2 or 4 bytes (y must not alias x): the
+ * 2-D convolution's [N, OD, Cout, OH OW] output back to NCDHW, and kernels into the gathered
+ * channel order. */
+int lq_permute_0213(const void* d_x, int elem_bytes, int64_t A, int64_t B, int64_t C, int64_t P, void* d_y,
+                    void* stream);
 
 /* ---- pooling ---------------------------------------------------------------------- */
 enum { LQ_POOL_MAX = 0, LQ_POOL_AVG = 1 };

@@ -84,6 +84,9 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_pool2d": (_I, [_I, _P, _I, _P, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _P, _P]),
     "lq_rnn_cell": (_I, [_I, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _P, _P, _P, _I64, _P]),
     "lq_stride_expand": (_I, [_P, _I, _I64, _I64, _I64, _I, _I, _P, _P, _P]),
+    "lq_depth_gather": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _P,
+                             _P, _P]),
+    "lq_permute_0213": (_I, [_P, _I, _I64, _I64, _I64, _I64, _P, _P]),
     "lq_qact": (_I, [_I, _P, _I, _P, _P, _I64, _F, _P, _P, _I, _I, _I, _P, _P]),
     "lq_qmerge": (_I, [_I, _P, _I, _P, _P, _P, _I, _P, _P, _F, _I64, _I64, _I64, _P, _P, _I, _I, _I, _I,
                        _P, _P]),

@@ -5,9 +5,15 @@ from lucid_amd.nn.layers import (
     ELU,
     AdaptiveAvgPool2d,
     AvgPool2d,
+    BatchNorm1d,
     BatchNorm2d,
+    BatchNorm3d,
+    Conv1d,
     Conv2d,
+    Conv3d,
+    ConvTranspose1d,
     ConvTranspose2d,
+    ConvTranspose3d,
     Embedding,
     EmbeddingBag,
     Flatten,
@@ -28,7 +34,8 @@ from lucid_amd.nn.rnn import GRU, LSTM, GRUCell, LSTMCell, RNNCell
 __all__ = ["Module", "Parameter", "Linear", "Conv2d", "ReLU", "Sequential", "Identity",
            "BatchNorm2d", "Flatten", "Sigmoid", "Tanh", "Hardswish", "Hardsigmoid", "ELU", "LeakyReLU",
            "Embedding", "EmbeddingBag", "MaxPool2d", "AvgPool2d", "AdaptiveAvgPool2d",
-           "LSTM", "GRU", "LSTMCell", "GRUCell", "RNNCell", "ConvTranspose2d"]
+           "LSTM", "GRU", "LSTMCell", "GRUCell", "RNNCell", "ConvTranspose2d", "Conv1d", "Conv3d",
+           "ConvTranspose1d", "ConvTranspose3d", "BatchNorm1d", "BatchNorm3d"]
 
 
 def __getattr__(name: str):

@@ -473,3 +473,211 @@ def tensor_of(a):
     from lucid_amd._tensor import tensor
 
     return tensor(a, device="gpu")
+
+
+# ------------------------------------------------------- 1-D and 3-D convolutions
+#
+# Both run on the 2-D kernels: a 1-D convolution is the 2-D one over a height-1 image; a 3-D
+# convolution is the 2-D one over the depth-gathered input (lq_depth_gather: the KD input
+# slices an output depth reads, stacked as channels), with the kernel rearranged to
+# [Cout, KD C/groups, KH, KW] and the output permuted back to NCDHW (lq_permute_0213).  The
+# sums are the 3-D convolution's products, exactly (codes) or in another order (floats).
+
+
+def _ntuple(v, n: int) -> tuple[int, ...]:
+    if isinstance(v, (tuple, list)):
+        vals = tuple(int(x) for x in v)
+        return vals if len(vals) == n else (vals[0],) * n
+    return (int(v),) * n
+
+
+def conv_padding_nd(padding, kernel: tuple[int, ...], dilation: tuple[int, ...]) -> list[tuple[int, int]]:
+    """(before, after) per spatial axis: ints (symmetric), or "valid" / "same" as Lucid resolves
+    them (total d (k - 1), the smaller half before)."""
+    n = len(kernel)
+    if isinstance(padding, str):
+        if padding == "valid":
+            return [(0, 0)] * n
+        if padding != "same":
+            raise ValueError(f"unknown padding {padding!r}")
+        out = []
+        for k, d in zip(kernel, dilation):
+            t = d * (k - 1)
+            out.append((t // 2, t - t // 2))
+        return out
+    pads = _ntuple(padding, n)
+    if min(pads) < 0:
+        raise ValueError("conv: padding must be non-negative")
+    return [(p, p) for p in pads]
+
+
+def _grid_of(q, codes):
+    from lucid_amd._tensor import QuantSource
+
+    return Tensor._code_backed(QuantSource(codes, q.code_type, q.scale, q.zero_point, q.quant_min, q.quant_max),
+                               codes.shape)
+
+
+def depth_gather(x: Tensor, groups: int, KD: int, OD: int, stride: int, pad: int, dilation: int,
+                 expand: int = 1, padding_mode: str = "zeros") -> Tensor:
+    """NCDHW ``x`` -> [N OD, KD C, H, W]: for each output depth the KD input slices it reads,
+    stacked as channels per group (a code-backed input stays code-backed on its grid)."""
+    import numpy as np
+
+    require_gpu(x, "conv3d")
+    N, C, D, H, W = (int(s) for s in x.shape)
+    shape = (N * OD, KD * C, H, W)
+    mode = PADDING_MODES[padding_mode]
+    q = x.quant_source
+    if q is not None and q.code_type in (_C.I8, _C.U8S8):
+        y = empty(shape, np.int8, "gpu")
+        _C.call("lq_depth_gather", q.codes.data_ptr(), q.code_type, N, C, D, H * W, groups, KD, OD, stride, pad,
+                dilation, expand, mode, q.zero_point.data_ptr(), y.data_ptr(), None)
+        return _grid_of(q, y)
+    if x.dtype != float32:
+        raise TypeError(f"conv3d: float32 input expected, got {x.dtype}")
+    y = empty(shape, float32, "gpu")
+    _C.call("lq_depth_gather", x.data_ptr(), _C.F32, N, C, D, H * W, groups, KD, OD, stride, pad, dilation, expand,
+            mode, None, y.data_ptr(), None)
+    return y
+
+
+def permute_depth(y2: Tensor, N: int, OD: int) -> Tensor:
+    """The 2-D convolution's [N OD, Cout, OH, OW] as NCDHW [N, Cout, OD, OH, OW]."""
+    import numpy as np
+
+    _, Cout, OH, OW = (int(s) for s in y2.shape)
+    shape = (N, Cout, OD, OH, OW)
+    q = y2.quant_source
+    if q is not None and y2._buf is None:
+        codes = empty(shape, np.int8, "gpu")
+        _C.call("lq_permute_0213", q.codes.data_ptr(), 1, N, OD, Cout, OH * OW, codes.data_ptr(), None)
+        return _grid_of(q, codes)
+    y = empty(shape, float32, "gpu")
+    _C.call("lq_permute_0213", y2.data_ptr(), 4, N, OD, Cout, OH * OW, y.data_ptr(), None)
+    return y
+
+
+def gathered_kernel(w: Tensor) -> Tensor:
+    """A 3-D kernel [Cout, Cg, KD, KH, KW] in the gathered channel order [Cout, KD Cg, KH, KW]
+    (float32 or int8, on the GPU)."""
+    import numpy as np
+
+    w = w if w.device == "gpu" else w.to("gpu")
+    Cout, Cg, KD, KH, KW = (int(s) for s in w.shape)
+    out = empty((Cout, KD * Cg, KH, KW), w.dtype, "gpu")
+    _C.call("lq_permute_0213", w.data_ptr(), np.dtype(w.dtype).itemsize, Cout, Cg, KD, KH * KW, out.data_ptr(), None)
+    return out
+
+
+def conv3d_geometry(x_shape, kernel, stride, padding, dilation):
+    """(depth pads, (top, bottom, left, right), OD) of a 3-D convolution."""
+    _, _, D, H, W = x_shape
+    (pdf, pdb), (pt, pb), (pl, pr) = conv_padding_nd(padding, kernel, dilation)
+    OD = (D + pdf + pdb - dilation[0] * (kernel[0] - 1) - 1) // stride[0] + 1
+    if OD < 1:
+        raise ValueError("conv3d: kernel larger than the padded input")
+    return (pdf, pdb), (pt, pb, pl, pr), OD
+
+
+def conv3d(x: Tensor, weight: Tensor, bias: Tensor | None = None, stride=1, padding=0, dilation=1,
+           groups: int = 1, padding_mode: str = "zeros") -> Tensor:
+    """Float 3-D convolution of NCDHW ``x`` (lucid/nn/functional/conv.py via _convnd, rank 3)."""
+    require_gpu(x, "conv3d")
+    if x.dtype != float32 or x.ndim != 5:
+        raise TypeError(f"conv3d: float32 NCDHW input expected, got {x.dtype} {x.shape}")
+    Cout, Cg, KD, KH, KW = (int(s) for s in weight.shape)
+    if Cg * groups != int(x.shape[1]):
+        raise ValueError(f"conv3d: input has {int(x.shape[1])} channels, weight expects {Cg} x {groups} groups")
+    s, d = _ntuple(stride, 3), _ntuple(dilation, 3)
+    (pdf, _), pads, OD = conv3d_geometry(x.shape, (KD, KH, KW), s, padding, d)
+    xg = depth_gather(x, groups, KD, OD, s[0], pdf, d[0], 1, padding_mode)
+    y2 = conv2d(xg, gathered_kernel(on_device(weight)), bias, s[1:], pads, d[1:], groups, padding_mode)
+    return permute_depth(y2, int(x.shape[0]), OD)
+
+
+def conv1d(x: Tensor, weight: Tensor, bias: Tensor | None = None, stride=1, padding=0, dilation=1,
+           groups: int = 1, padding_mode: str = "zeros") -> Tensor:
+    """Float 1-D convolution of NCL ``x``: the 2-D one over a height-1 image."""
+    require_gpu(x, "conv1d")
+    if x.dtype != float32 or x.ndim != 3:
+        raise TypeError(f"conv1d: float32 NCL input expected, got {x.dtype} {x.shape}")
+    Cout, Cg, K = (int(s) for s in weight.shape)
+    (pl, pr), = conv_padding_nd(padding, (K,), _ntuple(dilation, 1))
+    N, C, Lx = (int(s) for s in x.shape)
+    y = conv2d(x.reshape(N, C, 1, Lx), on_device(weight).reshape(Cout, Cg, 1, K), bias, (1, _ntuple(stride, 1)[0]),
+               (0, 0, pl, pr), (1, _ntuple(dilation, 1)[0]), groups, padding_mode)
+    return y.reshape(N, Cout, int(y.shape[3]))
+
+
+def convt_kernel_nd(w, groups: int):
+    """A transposed-convolution kernel [Cin, Cout / groups, *k] as the equivalent convolution's
+    [Cout, Cin / groups, *k]: channel axes swapped within each group, every tap axis flipped
+    (host numpy; codes or floats)."""
+    import numpy as np
+
+    Cin, Cout_g = w.shape[:2]
+    ks = w.shape[2:]
+    v = w.reshape(groups, Cin // groups, Cout_g, *ks).swapaxes(1, 2)
+    v = v[(slice(None),) * 3 + (slice(None, None, -1),) * len(ks)]
+    return np.ascontiguousarray(v.reshape(groups * Cout_g, Cin // groups, *ks))
+
+
+def convt3d_geometry(x_shape, kernel, stride, padding, output_padding, dilation):
+    """(depth pad of the equivalent stride-1 convolution, H/W pads, OD, OH, OW) of
+    conv_transpose3d; OD = (D - 1) s - 2 p + d (k - 1) + op + 1 per axis."""
+    _, _, D, H, W = x_shape
+    k, s, p = _ntuple(kernel, 3), _ntuple(stride, 3), _ntuple(padding, 3)
+    op, d = _ntuple(output_padding, 3), _ntuple(dilation, 3)
+    if op[0] >= max(s[0], d[0]):
+        raise ValueError("conv_transpose3d: output_padding must be smaller than stride or dilation")
+    pd = d[0] * (k[0] - 1) - p[0]
+    if pd < 0:
+        raise NotImplementedError("conv_transpose3d: padding larger than dilation * (kernel - 1) is not supported "
+                                  "on the HIP backend")
+    pads, OH, OW = convt_geometry(H, W, k[1:], s[1:], p[1:], op[1:], d[1:])
+    OD = (D - 1) * s[0] - 2 * p[0] + d[0] * (k[0] - 1) + op[0] + 1
+    return pd, pads, OD, OH, OW
+
+
+def conv_transpose3d(x: Tensor, weight: Tensor, bias: Tensor | None = None, stride=1, padding=0,
+                     output_padding=0, groups: int = 1, dilation=1) -> Tensor:
+    """Float 3-D transposed convolution (``weight`` [Cin, Cout / groups, kd, kh, kw]): H / W
+    spread by the stride, the depth expansion folded into the gather, then the stride-1 2-D
+    convolution with the flipped, channel-swapped kernel."""
+    require_gpu(x, "conv_transpose3d")
+    if x.ndim != 5 or x.dtype != float32:
+        raise TypeError(f"conv_transpose3d: float32 NCDHW input expected, got {x.dtype} {x.shape}")
+    Cin = int(weight.shape[0])
+    if int(x.shape[1]) != Cin:
+        raise ValueError(f"conv_transpose3d: input has {int(x.shape[1])} channels, weight expects {Cin}")
+    k = tuple(int(v) for v in weight.shape[2:])
+    s, d = _ntuple(stride, 3), _ntuple(dilation, 3)
+    pd, pads, OD, _, _ = convt3d_geometry(x.shape, k, s, padding, output_padding, d)
+    w = gathered_kernel(tensor_of(convt_kernel_nd(weight.numpy(), groups)))
+    return convt3d_apply(x, s, pd, d[0], k[0], OD, groups, lambda xg: conv2d(xg, w, bias, 1, pads, d[1:], groups))
+
+
+def convt3d_apply(x: Tensor, s, pd: int, dd: int, KD: int, OD: int, groups: int, conv) -> Tensor:
+    """Expand H / W by the stride, gather the expanded depth axis (channels grouped as the
+    equivalent convolution's groups), run ``conv`` (the stride-1 2-D convolution), permute to
+    NCDHW."""
+    N, C, D, H, W = (int(v) for v in x.shape)
+    xe = stride_expand(x.reshape(N, C * D, H, W), s[1:])
+    Hu, Wu = int(xe.shape[2]), int(xe.shape[3])
+    xg = depth_gather(xe.reshape(N, C, D, Hu, Wu), groups, KD, OD, 1, pd, dd, s[0])
+    return permute_depth(conv(xg), N, OD)
+
+
+def conv_transpose1d(x: Tensor, weight: Tensor, bias: Tensor | None = None, stride=1, padding=0,
+                     output_padding=0, groups: int = 1, dilation=1) -> Tensor:
+    """Float 1-D transposed convolution: the 2-D one over a height-1 image."""
+    require_gpu(x, "conv_transpose1d")
+    if x.ndim != 3:
+        raise TypeError(f"conv_transpose1d: NCL input expected, got {x.shape}")
+    Cin, Cout_g, K = (int(v) for v in weight.shape)
+    N, C, Lx = (int(v) for v in x.shape)
+    w2 = tensor_of(weight.numpy().reshape(Cin, Cout_g, 1, K))
+    y = conv_transpose2d(x.reshape(N, C, 1, Lx), w2, bias, (1, _ntuple(stride, 1)[0]), (0, _ntuple(padding, 1)[0]),
+                         (0, _ntuple(output_padding, 1)[0]), groups, (1, _ntuple(dilation, 1)[0]))
+    return y.reshape(N, int(y.shape[1]), int(y.shape[3]))

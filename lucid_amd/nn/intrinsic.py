@@ -3,7 +3,7 @@
 
 from __future__ import annotations
 
-from lucid_amd.nn.layers import Conv2d, Linear, ReLU, Sequential
+from lucid_amd.nn.layers import Conv1d, Conv2d, Conv3d, Linear, ReLU, Sequential
 
 
 class _FusedModule(Sequential):
@@ -20,4 +20,14 @@ class ConvReLU2d(_FusedModule):
         super().__init__(conv, relu)
 
 
-__all__ = ["LinearReLU", "ConvReLU2d"]
+class ConvReLU1d(_FusedModule):
+    def __init__(self, conv: Conv1d, relu: ReLU) -> None:
+        super().__init__(conv, relu)
+
+
+class ConvReLU3d(_FusedModule):
+    def __init__(self, conv: Conv3d, relu: ReLU) -> None:
+        super().__init__(conv, relu)
+
+
+__all__ = ["LinearReLU", "ConvReLU1d", "ConvReLU2d", "ConvReLU3d"]

@@ -100,6 +100,62 @@ class Conv2d(Module):
                 f"stride={self.stride}, padding={self._padding_str or self.padding}")
 
 
+def _ntuple(v: Any, n: int) -> tuple[int, ...]:
+    if isinstance(v, (tuple, list)):
+        vals = tuple(int(x) for x in v)
+        return vals if len(vals) == n else (vals[0],) * n
+    return (int(v),) * n
+
+
+class _ConvNd(Module):
+    """Float convolution of spatial rank ``_rank`` (lucid/nn/modules/conv.py Conv1d / Conv3d):
+    weight [out, in / groups, *kernel]; ``convert`` swaps it for its nn.quantized form."""
+
+    _rank = 2
+
+    def __init__(self, in_channels: int, out_channels: int, kernel_size: Any, stride: Any = 1,
+                 padding: Any = 0, dilation: Any = 1, groups: int = 1, bias: bool = True,
+                 padding_mode: str = "zeros") -> None:
+        super().__init__()
+        if in_channels % groups or out_channels % groups:
+            raise ValueError("in_channels and out_channels must be divisible by groups")
+        n = self._rank
+        self.in_channels, self.out_channels = in_channels, out_channels
+        self.kernel_size, self.stride = _ntuple(kernel_size, n), _ntuple(stride, n)
+        if isinstance(padding, str):
+            self._padding_str, self.padding = padding, (0,) * n
+        else:
+            self._padding_str, self.padding = None, _ntuple(padding, n)
+        self.dilation, self.groups, self.padding_mode = _ntuple(dilation, n), groups, padding_mode
+        fan_in = (in_channels // groups) * int(np.prod(self.kernel_size))
+        bound = 1.0 / math.sqrt(fan_in) if fan_in > 0 else 0.0
+        self.weight = Parameter(_uniform((out_channels, in_channels // groups, *self.kernel_size), bound))
+        if bias:
+            self.bias = Parameter(_uniform((out_channels,), bound))
+        else:
+            self.register_parameter("bias", None)
+
+    def extra_repr(self) -> str:
+        return (f"{self.in_channels}, {self.out_channels}, kernel_size={self.kernel_size}, "
+                f"stride={self.stride}, padding={self._padding_str or self.padding}")
+
+
+class Conv1d(_ConvNd):
+    _rank = 1
+
+    def forward(self, x: Tensor) -> Tensor:
+        return F.conv1d(x, self.weight, self.bias, self.stride, self._padding_str or self.padding,
+                        self.dilation, self.groups, self.padding_mode)
+
+
+class Conv3d(_ConvNd):
+    _rank = 3
+
+    def forward(self, x: Tensor) -> Tensor:
+        return F.conv3d(x, self.weight, self.bias, self.stride, self._padding_str or self.padding,
+                        self.dilation, self.groups, self.padding_mode)
+
+
 class ReLU(Module):
     def forward(self, x: Tensor) -> Tensor:
         return F.relu(x)
@@ -133,6 +189,50 @@ class ConvTranspose2d(Module):
     def extra_repr(self) -> str:
         return (f"{self.in_channels}, {self.out_channels}, kernel_size={self.kernel_size}, "
                 f"stride={self.stride}")
+
+
+class _ConvTransposeNd(Module):
+    """Float transposed convolution of spatial rank ``_rank``: weight [in, out / groups, *kernel]."""
+
+    _rank = 1
+
+    def __init__(self, in_channels: int, out_channels: int, kernel_size: Any, stride: Any = 1, padding: Any = 0,
+                 output_padding: Any = 0, groups: int = 1, bias: bool = True, dilation: Any = 1) -> None:
+        super().__init__()
+        if in_channels % groups or out_channels % groups:
+            raise ValueError("in_channels and out_channels must be divisible by groups")
+        n = self._rank
+        self.in_channels, self.out_channels = in_channels, out_channels
+        self.kernel_size, self.stride = _ntuple(kernel_size, n), _ntuple(stride, n)
+        self.padding, self.output_padding = _ntuple(padding, n), _ntuple(output_padding, n)
+        self.dilation, self.groups = _ntuple(dilation, n), groups
+        fan_in = (out_channels // groups) * int(np.prod(self.kernel_size))
+        bound = 1.0 / math.sqrt(fan_in) if fan_in > 0 else 0.0
+        self.weight = Parameter(_uniform((in_channels, out_channels // groups, *self.kernel_size), bound))
+        if bias:
+            self.bias = Parameter(_uniform((out_channels,), bound))
+        else:
+            self.register_parameter("bias", None)
+
+    def extra_repr(self) -> str:
+        return (f"{self.in_channels}, {self.out_channels}, kernel_size={self.kernel_size}, "
+                f"stride={self.stride}")
+
+
+class ConvTranspose1d(_ConvTransposeNd):
+    _rank = 1
+
+    def forward(self, x: Tensor) -> Tensor:
+        return F.conv_transpose1d(x, self.weight, self.bias, self.stride, self.padding, self.output_padding,
+                                  self.groups, self.dilation)
+
+
+class ConvTranspose3d(_ConvTransposeNd):
+    _rank = 3
+
+    def forward(self, x: Tensor) -> Tensor:
+        return F.conv_transpose3d(x, self.weight, self.bias, self.stride, self.padding, self.output_padding,
+                                  self.groups, self.dilation)
 
 
 class _PaddedTable(Module):
@@ -320,6 +420,14 @@ class BatchNorm2d(Module):
 
     def extra_repr(self) -> str:
         return f"{self.num_features}, eps={self.eps}"
+
+
+class BatchNorm1d(BatchNorm2d):
+    """Eval BatchNorm over [N, C] or [N, C, L] (the channel axis 1)."""
+
+
+class BatchNorm3d(BatchNorm2d):
+    """Eval BatchNorm over NCDHW."""
 
 
 class Sequential(Module):

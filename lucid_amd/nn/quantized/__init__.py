@@ -11,6 +11,8 @@ MFMA GEMM over integer codes; ``QuantStub`` / ``DeQuantStub`` / ``Quantize`` /
 
 from lucid_amd.nn.quantized.activation import ELU, Hardsigmoid, Hardswish, LeakyReLU, Sigmoid, Tanh
 from lucid_amd.nn.quantized.conv import Conv2d
+from lucid_amd.nn.quantized.conv_nd import (Conv1d, Conv3d, ConvReLU1d, ConvReLU3d, ConvTranspose1d,
+                                            ConvTranspose3d)
 from lucid_amd.nn.quantized.conv_transpose import ConvTranspose2d
 from lucid_amd.nn.quantized.functional_module import FloatFunctional, QFunctional
 from lucid_amd.nn.quantized.intrinsic import ConvReLU2d, LinearReLU
@@ -22,7 +24,8 @@ from lucid_amd.nn.quantized.sparse import Embedding, EmbeddingBag
 
 __all__ = ["Linear", "QuantizedLinearMLX", "Conv2d", "ConvReLU2d", "LinearReLU", "QuantStub", "DeQuantStub", "Quantize", "DeQuantize",
            "QuantWrapper", "FloatFunctional", "QFunctional", "Sigmoid", "Hardswish", "Hardsigmoid",
-           "Tanh", "ELU", "LeakyReLU", "Embedding", "EmbeddingBag", "ConvTranspose2d"]
+           "Tanh", "ELU", "LeakyReLU", "Embedding", "EmbeddingBag", "ConvTranspose2d", "Conv1d", "Conv3d",
+           "ConvReLU1d", "ConvReLU3d", "ConvTranspose1d", "ConvTranspose3d"]
 
 
 def __getattr__(name: str):

@@ -35,7 +35,8 @@ def _observed_types() -> tuple[type, ...]:
     import lucid_amd.nn.intrinsic as nni
     import lucid_amd.nn.quantized as nnq
 
-    return (nn.Linear, nn.Conv2d, nn.ConvTranspose2d, nni.ConvReLU2d, nni.LinearReLU, nn.Sigmoid, nn.Hardswish,
+    return (nn.Linear, nn.Conv1d, nn.Conv2d, nn.Conv3d, nn.ConvTranspose1d, nn.ConvTranspose2d, nn.ConvTranspose3d,
+            nni.ConvReLU1d, nni.ConvReLU2d, nni.ConvReLU3d, nni.LinearReLU, nn.Sigmoid, nn.Hardswish,
             nn.Hardsigmoid, nn.Tanh, nn.ELU, nn.LeakyReLU, nnq.QuantStub, nnq.FloatFunctional)
 
 
@@ -56,7 +57,13 @@ def _quant_mapping() -> dict[type, _FromFloat]:
         nn.Tanh: nnq.Tanh.from_float,
         nn.ELU: nnq.ELU.from_float,
         nn.LeakyReLU: nnq.LeakyReLU.from_float,
+        nn.ConvTranspose1d: nnq.ConvTranspose1d.from_float,
         nn.ConvTranspose2d: nnq.ConvTranspose2d.from_float,
+        nn.ConvTranspose3d: nnq.ConvTranspose3d.from_float,
+        nn.Conv1d: nnq.Conv1d.from_float,
+        nn.Conv3d: nnq.Conv3d.from_float,
+        nni.ConvReLU1d: nnq.ConvReLU1d.from_float,
+        nni.ConvReLU3d: nnq.ConvReLU3d.from_float,
         nn.Embedding: nnq.Embedding.from_float,
         nn.EmbeddingBag: nnq.EmbeddingBag.from_float,
     }

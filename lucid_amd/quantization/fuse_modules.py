@@ -73,19 +73,23 @@ def fuse_conv_bn_eval(conv: Module, bn: Module) -> Module:
 
 def _fuse_run(mods: Sequence[Module]) -> list[Module]:
     import lucid_amd.nn.intrinsic as nni
-    from lucid_amd.nn.layers import BatchNorm2d, Conv2d, Identity, Linear, ReLU
+    from lucid_amd.nn.layers import (BatchNorm1d, BatchNorm2d, BatchNorm3d, Conv1d, Conv2d, Conv3d, Identity, Linear,
+                                     ReLU)
 
     ids = [Identity() for _ in range(len(mods) - 1)]
     first = mods[0]
-    if isinstance(first, Conv2d):
-        conv: Module = first
-        rest = list(mods[1:])
-        if rest and isinstance(rest[0], BatchNorm2d):
-            conv = fuse_conv_bn_eval(first, rest.pop(0))
-        if rest and isinstance(rest[0], ReLU):
-            rest.pop(0)
-            return [nni.ConvReLU2d(conv, ReLU()), *ids]
-        return [conv, *ids]
+    runs = ((Conv1d, BatchNorm1d, nni.ConvReLU1d), (Conv2d, BatchNorm2d, nni.ConvReLU2d),
+            (Conv3d, BatchNorm3d, nni.ConvReLU3d))
+    for conv_t, bn_t, fused_t in runs:
+        if type(first) is conv_t:
+            conv: Module = first
+            rest = list(mods[1:])
+            if rest and type(rest[0]) is bn_t:
+                conv = fuse_conv_bn_eval(first, rest.pop(0))
+            if rest and isinstance(rest[0], ReLU):
+                rest.pop(0)
+                return [fused_t(conv, ReLU()), *ids]
+            return [conv, *ids]
     if isinstance(first, Linear) and len(mods) == 2 and isinstance(mods[1], ReLU):
         return [nni.LinearReLU(first, ReLU()), *ids]
     raise ValueError(f"fuse_modules: unsupported fusion pattern {[type(m).__name__ for m in mods]}")

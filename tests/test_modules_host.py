@@ -304,3 +304,49 @@ def test_group_ops_reject_mismatched_operands_before_launch():
     # well-formed operands get as far as the device requirement
     with pytest.raises(L.LucidError, match="GPU"):
         _qgemm.quantized_matmul(x, wq, s64, b64, group_size=64, bits=4)
+
+
+def test_fuse_conv1d_conv3d_bn_relu():
+    """[Conv1d, BatchNorm1d, ReLU] and [Conv3d, BatchNorm3d] fold the BN into the conv (the
+    closed form of lucid/nn/utils/fusion.py:52-106 over any kernel rank); the 1-D run becomes
+    ConvReLU1d, a BatchNorm of the wrong rank is not fused."""
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.intrinsic as nni
+    from lucid_amd._tensor import tensor
+    from lucid_amd.quantization import fuse_modules
+
+    rng = np.random.default_rng(0)
+    for conv, bn, relu in ((nn.Conv1d(3, 4, 3), nn.BatchNorm1d(4), True), (nn.Conv3d(3, 4, 3), nn.BatchNorm3d(4), False)):
+        bn.running_mean = tensor(rng.standard_normal(4).astype(np.float32))
+        bn.running_var = tensor(rng.uniform(0.5, 2, 4).astype(np.float32))
+        mods = [conv, bn] + ([nn.ReLU()] if relu else [])
+        model = nn.Sequential(*mods).eval()
+        fused = fuse_modules(model, [[str(i) for i in range(len(mods))]])
+        head = fused[0]
+        assert isinstance(head, nni.ConvReLU1d) if relu else type(head) is nn.Conv3d
+        inner = head[0] if relu else head
+        w = conv.weight.numpy()
+        scale = (1.0 / np.sqrt(bn.running_var.numpy() + np.float32(bn.eps))).astype(np.float32)
+        want = (w * scale.reshape((-1,) + (1,) * (w.ndim - 1))).astype(np.float32)
+        np.testing.assert_array_equal(inner.weight.numpy(), want)
+    with pytest.raises(ValueError, match="unsupported"):
+        fuse_modules(nn.Sequential(nn.BatchNorm1d(4), nn.Conv1d(4, 4, 1)).eval(), [["0", "1"]])
+
+
+def test_conv_nd_modules_map_and_keep_state_dict_layout():
+    """convert's table covers the 1-D / 3-D family; the quantized modules keep Lucid's buffer
+    names and shapes (weight_int8 [out, in / groups, *k], transposed [in, out / groups, *k])."""
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.intrinsic as nni
+    import lucid_amd.nn.quantized as nnq
+    from lucid_amd.quantization._quantize import _observed_types, _quant_mapping
+
+    mapping = _quant_mapping()
+    for t in (nn.Conv1d, nn.Conv3d, nn.ConvTranspose1d, nn.ConvTranspose3d, nni.ConvReLU1d, nni.ConvReLU3d):
+        assert t in mapping and t in _observed_types()
+    sd = nnq.Conv3d(4, 8, (3, 2, 1), groups=2).state_dict()
+    assert sd["weight_int8"].shape == (8, 2, 3, 2, 1) and sd["weight_scale"].shape == (8,)
+    sd = nnq.ConvTranspose3d(4, 6, 3, groups=2).state_dict()
+    assert sd["weight_int8"].shape == (4, 3, 3, 3, 3) and sd["weight_scale"].shape == (3,)
+    assert set(nnq.Conv1d(2, 3, 5).state_dict()) == {"weight_int8", "weight_scale", "weight_zero_point", "bias",
+                                                      "scale", "zero_point"}
