@@ -41,6 +41,6 @@ __all__ = ["Module", "Parameter", "Linear", "Conv2d", "ReLU", "Sequential", "Ide
 def __getattr__(name: str):
     import importlib
 
-    if name in ("quantized", "intrinsic", "functional"):
+    if name in ("quantized", "intrinsic", "functional", "utils"):
         return importlib.import_module(f"lucid_amd.nn.{name}")
     raise AttributeError(f"module 'lucid_amd.nn' has no attribute {name!r}")

@@ -10,8 +10,15 @@ written straight into the layer's output sequence.  ``batch_first`` is handled b
 ``weight_ih`` ...), so ``quantize_dynamic`` finds them.  The matrix products are the float
 ``lq_linear_f32`` here and the weight-only int8 GEMV in ``nn.quantized.dynamic``.
 
-Not covered: ``PackedSequence`` inputs, ``proj_size`` and inter-layer dropout (these are
-inference modules: dropout is the identity in eval).
+A ``PackedSequence`` input (``lucid_amd.nn.utils.rnn``) runs the same recurrence over the
+packed rows: step t advances the first ``batch_sizes[t]`` sequences (descending lengths, so
+the live ones are a prefix), the reverse direction walks the steps backwards so a sequence
+joins at its own last step with its initial state, ``h_n`` holds each sequence's state after
+its own last step, and an unsorted batch's states are permuted on the way in and out
+(lucid/nn/quantized/dynamic/rnn.py:167-197 runs packed input through the float shell).
+
+Not covered: ``proj_size`` and inter-layer dropout (these are inference modules: dropout is
+the identity in eval).
 """
 
 from __future__ import annotations
@@ -67,6 +74,24 @@ class _Recurrent(Module):
                     c.data_ptr() if c is not None else None, B, H, h.data_ptr(),
                     c.data_ptr() if c is not None else None, y_ptr, ld_y, None)
 
+    def _layer_packed(self, x: Tensor, sizes: list[int], offsets: list[int], sfx: str, d: int, D: int,
+                      h: Tensor, c: Tensor | None, out: Tensor) -> None:
+        """One layer and direction over packed rows ``x`` [total, K]; writes its column block
+        of ``out`` [total, D H]."""
+        H, G = self.hidden_size, _GATES[self.mode]
+        K, total = int(x.shape[-1]), int(x.shape[0])
+        gx = empty((total, G * H), float32, "gpu")
+        self._gates("ih" + sfx, x.data_ptr(), K, total, K, gx.data_ptr())
+        gh = empty((sizes[0], G * H), float32, "gpu")
+        steps = range(len(sizes) - 1, -1, -1) if d else range(len(sizes))
+        for t in steps:
+            bs = sizes[t]
+            self._gates("hh" + sfx, h.data_ptr(), H, bs, H, gh.data_ptr())
+            _C.call("lq_rnn_cell", _KIND[self.mode], gx.data_ptr() + 4 * offsets[t] * G * H, G * H, gh.data_ptr(),
+                    G * H, h.data_ptr(), c.data_ptr() if c is not None else None, bs, H, h.data_ptr(),
+                    c.data_ptr() if c is not None else None, out.data_ptr() + 4 * (offsets[t] * D * H + d * H), D * H,
+                    None)
+
     def _state(self, hx: Tensor | None, idx: int, B: int) -> Tensor:
         """A private contiguous [B, H] copy of layer-direction ``idx`` of ``hx`` (zeros if None)."""
         H = self.hidden_size
@@ -100,7 +125,61 @@ class _RNNBase(_Recurrent):
                     setattr(self, f"bias_ih{sfx}", Parameter(_init_uniform((G * hidden_size,), hidden_size)))
                     setattr(self, f"bias_hh{sfx}", Parameter(_init_uniform((G * hidden_size,), hidden_size)))
 
+    def _run_packed(self, packed, hx: Tensor | None, cx: Tensor | None):
+        from lucid_amd.nn.utils.rnn import PackedSequence, _gather_rows
+
+        data = packed.data
+        require_gpu(data, type(self).__name__)
+        if data.dtype != float32 or data.ndim != 2:
+            raise TypeError(f"{type(self).__name__}: packed data must be float32 [total, input_size]")
+        if int(data.shape[1]) != self.input_size:
+            raise ValueError(f"{type(self).__name__}: input size {int(data.shape[1])} != {self.input_size}")
+        sizes = packed.sizes
+        offsets = [0]
+        for bs in sizes[:-1]:
+            offsets.append(offsets[-1] + bs)
+        B, D, H, L = sizes[0], (2 if self.bidirectional else 1), self.hidden_size, self.num_layers
+        order = [int(v) for v in packed.sorted_indices.numpy()] if packed.sorted_indices is not None else None
+
+        def permute(st: Tensor | None, perm: list[int] | None) -> Tensor | None:
+            """States [L D, B, H] with their batch axis reordered (row gather)."""
+            if st is None or perm is None:
+                return st
+            if int(np.prod(st.shape)) != L * D * B * H:
+                raise ValueError(f"{type(self).__name__}: states must hold {L * D} x {B} x {H} values")
+            idx = [ld * B + p for ld in range(L * D) for p in perm]
+            return _gather_rows(st, L * D * B, H, idx).reshape(L * D, B, H)
+
+        hx, cx = permute(hx, order), permute(cx, order)
+        for name, st in (("hx", hx), ("cx", cx)):
+            if st is not None and int(np.prod(st.shape)) != L * D * B * H:
+                raise ValueError(f"{type(self).__name__}: {name} must hold {L * D} x {B} x {H} values, got "
+                                 f"shape {tuple(st.shape)}")
+        h_n = empty((L * D, B, H), float32, "gpu")
+        c_n = empty((L * D, B, H), float32, "gpu") if self.mode == "LSTM" else None
+        layer_in = data
+        total = int(data.shape[0])
+        for layer in range(L):
+            out = empty((total, D * H), float32, "gpu")
+            for d in range(D):
+                idx = layer * D + d
+                h = self._state(hx, idx, B)
+                c = self._state(cx, idx, B) if self.mode == "LSTM" else None
+                self._layer_packed(layer_in, sizes, offsets, f"_l{layer}" + ("_reverse" if d else ""), d, D, h, c,
+                                   out)
+                _C.call("lq_memcpy_d2d", h_n.data_ptr() + 4 * idx * B * H, h.data_ptr(), 4 * B * H, None)
+                if c is not None:
+                    _C.call("lq_memcpy_d2d", c_n.data_ptr() + 4 * idx * B * H, c.data_ptr(), 4 * B * H, None)
+            layer_in = out
+        unsort = [int(v) for v in packed.unsorted_indices.numpy()] if packed.unsorted_indices is not None else None
+        out_seq = PackedSequence(layer_in, sizes, packed.sorted_indices, packed.unsorted_indices)
+        return out_seq, permute(h_n, unsort), permute(c_n, unsort)
+
     def _run(self, input: Tensor, hx: Tensor | None, cx: Tensor | None):
+        from lucid_amd.nn.utils.rnn import PackedSequence
+
+        if isinstance(input, PackedSequence):
+            return self._run_packed(input, hx, cx)
         require_gpu(input, type(self).__name__)
         if input.dtype != float32:
             raise TypeError(f"{type(self).__name__}: float32 input expected, got {input.dtype}")

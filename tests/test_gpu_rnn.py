@@ -201,3 +201,85 @@ def test_from_float_rejects_another_type(gpu):
 
     with pytest.raises(TypeError):
         nnqd.LSTM.from_float(nn.GRU(4, 4))
+
+
+# ------------------------------------------------------------------ packed sequences
+
+
+def test_pack_pad_round_trip(gpu):
+    """pack_padded_sequence / pad_packed_sequence / pack_sequence / pad_sequence as row moves:
+    bit-exact round trips, sorted and unsorted, time- and batch-major (lucid/nn/utils/rnn.py:
+    394-777); batch_sizes, the permutations and the returned lengths as Lucid documents them."""
+    from lucid_amd.nn.utils.rnn import pack_padded_sequence, pack_sequence, pad_packed_sequence, pad_sequence
+
+    rng = np.random.default_rng(2)
+    T, B, F = 6, 4, 5
+    lens = [3, 6, 2, 5]
+    x = rng.standard_normal((T, B, F)).astype(np.float32)
+    for batch_first in (False, True):
+        xin = x.transpose(1, 0, 2) if batch_first else x
+        p = pack_padded_sequence(_dev(gpu, xin), lens, batch_first=batch_first, enforce_sorted=False)
+        assert p.batch_sizes.numpy().tolist() == [4, 4, 3, 2, 2, 1]
+        assert p.sorted_indices.numpy().tolist() == [1, 3, 0, 2]
+        assert p.unsorted_indices.numpy().tolist() == [2, 0, 3, 1]
+        rows = [x[t, b] for t in range(T) for b in [1, 3, 0, 2] if lens[b] > t]
+        np.testing.assert_array_equal(p.data.numpy(), np.stack(rows))
+        padded, got_lens = pad_packed_sequence(p, batch_first=batch_first, padding_value=-7.0)
+        want = xin.copy()
+        for b, n in enumerate(lens):
+            if batch_first:
+                want[b, n:] = -7.0
+            else:
+                want[n:, b] = -7.0
+        np.testing.assert_array_equal(padded.numpy(), want)
+        assert got_lens.numpy().tolist() == lens
+    with pytest.raises(ValueError, match="sorted in decreasing order"):
+        pack_padded_sequence(_dev(gpu, x), lens)
+    seqs = [_dev(gpu, rng.standard_normal((n, F)).astype(np.float32)) for n in (5, 5, 2)]
+    ps = pack_sequence(seqs)
+    assert ps.batch_sizes.numpy().tolist() == [3, 3, 2, 2, 2]
+    padded = pad_sequence(seqs, batch_first=True, padding_value=1.5).numpy()
+    np.testing.assert_array_equal(padded[2, :2], seqs[2].numpy())
+    assert np.all(padded[2, 2:] == 1.5)
+
+
+@pytest.mark.parametrize("mode,layers,bidir", [("LSTM", 2, True), ("GRU", 1, False), ("LSTM", 1, False),
+                                               ("GRU", 2, True)])
+@pytest.mark.parametrize("dynamic", [False, True])
+def test_packed_sequence_recurrence(gpu, mode, layers, bidir, dynamic):
+    """An unsorted PackedSequence through LSTM / GRU (float and dynamic int8): each sequence's
+    outputs and final states equal the oracle's float64 recurrence over that sequence alone
+    (the packed recurrence advances only the live sequences at each step), within 2e-5; the
+    output comes back packed with the input's batch sizes and permutations."""
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized.dynamic as nnqd
+    from lucid_amd.nn.layers import manual_seed
+    from lucid_amd.nn.utils.rnn import PackedSequence, pack_padded_sequence, pad_packed_sequence
+
+    manual_seed(11 + layers)
+    rng = np.random.default_rng(layers + 2 * bidir)
+    T, B, I, H = 7, 5, 6, 8
+    lens = [4, 7, 1, 7, 3]
+    D = 2 if bidir else 1
+    m = getattr(nn, mode)(I, H, num_layers=layers, bidirectional=bidir).to("gpu")
+    mod = nnqd.__dict__[mode].from_float(m) if dynamic else m
+    weights = _deq_weights(mod) if dynamic else _float_weights(m)
+    x = rng.standard_normal((T, B, I)).astype(np.float32)
+    h0 = (rng.standard_normal((layers * D, B, H)) * 0.5).astype(np.float32)
+    c0 = (rng.standard_normal((layers * D, B, H)) * 0.5).astype(np.float32)
+    packed = pack_padded_sequence(_dev(gpu, x), lens, enforce_sorted=False)
+    hx = (_dev(gpu, h0), _dev(gpu, c0)) if mode == "LSTM" else _dev(gpu, h0)
+    out, state = mod(packed, hx)
+    assert isinstance(out, PackedSequence)
+    assert out.batch_sizes.numpy().tolist() == packed.batch_sizes.numpy().tolist()
+    padded, got_lens = pad_packed_sequence(out)
+    assert got_lens.numpy().tolist() == lens
+    h_n = state[0].numpy() if mode == "LSTM" else state.numpy()
+    for b, n in enumerate(lens):
+        want, wh, wc = O.rnn_forward(mode, x[:n, b:b + 1], weights, layers, bidir, h0[:, b:b + 1],
+                                     c0[:, b:b + 1] if mode == "LSTM" else None)
+        np.testing.assert_allclose(padded.numpy()[:n, b:b + 1], want, atol=ATOL, rtol=0)
+        assert np.all(padded.numpy()[n:, b] == 0.0)
+        np.testing.assert_allclose(h_n[:, b:b + 1], wh, atol=ATOL, rtol=0)
+        if mode == "LSTM":
+            np.testing.assert_allclose(state[1].numpy()[:, b:b + 1], wc, atol=ATOL, rtol=0)

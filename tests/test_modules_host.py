@@ -350,3 +350,22 @@ def test_conv_nd_modules_map_and_keep_state_dict_layout():
     assert sd["weight_int8"].shape == (4, 3, 3, 3, 3) and sd["weight_scale"].shape == (3,)
     assert set(nnq.Conv1d(2, 3, 5).state_dict()) == {"weight_int8", "weight_scale", "weight_zero_point", "bias",
                                                       "scale", "zero_point"}
+
+
+def test_packed_sequence_validation():
+    """PackedSequence checks its batch sizes and derives the inverse permutation
+    (lucid/nn/utils/rnn.py:140-150, 184-260)."""
+    from lucid_amd._tensor import tensor
+    from lucid_amd.nn.utils.rnn import PackedSequence
+
+    data = tensor(np.zeros((3, 2), np.float32))
+    p = PackedSequence(data, [2, 1], [1, 0])
+    assert p.unsorted_indices.numpy().tolist() == [1, 0]
+    assert p.batch_sizes.numpy().dtype == np.int64
+    data, bs, si, ui = p  # a 4-tuple
+    with pytest.raises(ValueError, match="non-increasing"):
+        PackedSequence(data, [1, 2])
+    with pytest.raises(ValueError, match="sums to"):
+        PackedSequence(data, [2, 2])
+    with pytest.raises(ValueError, match="permutation"):
+        PackedSequence(data, [2, 1], [0, 0])
