@@ -580,6 +580,16 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void conv_i8_dma_kernel(Con
     float csb[FN], cbias[FN];
     int32_t cws[FN];
     const bool epilogue_here = a.phase == 1 || a.splits == 1;
+    // the per-call scalars too (their loads and the reciprocal would otherwise open the
+    // epilogue with a memory round trip)
+    EpiParams ep;
+    ep.za = (a.a_zp ? (int)a.a_zp[0] : 0) - (a.a_u8s8 ? 128 : 0);
+    ep.has_za = a.a_zp != nullptr || a.a_u8s8;
+    ep.out_s = a.out_scale ? a.out_scale[0] : 1.0f;
+    ep.out_inv = 1.0f / ep.out_s;
+    ep.out_z = a.out_zp ? a.out_zp[0] : 0.0f;
+    ep.g = make_grid(a.qmin, a.qmax);
+    const float sa = a.a_scale ? a.a_scale[0] : 1.0f;
     if (epilogue_here) {
 #pragma unroll
         for (int i = 0; i < FN; ++i) {
@@ -630,16 +640,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void conv_i8_dma_kernel(Con
 
     // Epilogue: acc[i][j][r] is pixel p0 + wm*64 + 16 (lane/16) + 4 j + r, channel
     // co0 + wn*WN + 16 i + lane % 16 (within the group).
-    EpiParams ep;
-    ep.za = (a.a_zp ? (int)a.a_zp[0] : 0) - (a.a_u8s8 ? 128 : 0);
-    ep.has_za = a.a_zp != nullptr || a.a_u8s8;
-    ep.out_s = a.out_scale ? a.out_scale[0] : 1.0f;
-    ep.out_inv = 1.0f / ep.out_s;
-    ep.out_z = a.out_zp ? a.out_zp[0] : 0.0f;
-    ep.g = make_grid(a.qmin, a.qmax);
     CodeClamp cc{};
     if (INT_CODES) cc = code_clamp<KIND>(a.qmin, a.qmax);
-    const float sa = a.a_scale ? a.a_scale[0] : 1.0f;
     const int Cout = a.G * a.Cout_g;
     const int pb = p0 + wm * 64 + c0 * 16;
     const int nimg = min(pb, a.P - 1) / OHW;
@@ -694,12 +696,22 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void conv_i8_dma_kernel(Con
                         v4i{(int)out[4 * h], (int)out[4 * h + 1], (int)out[4 * h + 2], (int)out[4 * h + 3]};
             }
         } else {
+            // 16 consecutive pixels from (image nimg, pixel pix0): at most one image boundary
+            // when OHW >= 16 (else the division per pixel)
+            const int64_t base = ((int64_t)nimg * Cout + co) * OHW + pix0;
+            const int64_t next = ((int64_t)(nimg + 1) * Cout + co) * OHW + pix0 - OHW;
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
                 const int p = pb + q;
                 if (p >= a.P) break;
-                const int nq = p / OHW, pq = p - nq * OHW;
-                store_elem<KIND>(a.y, ((int64_t)nq * Cout + co) * OHW + pq, out[q]);
+                int64_t idx;
+                if (OHW >= 16) {
+                    idx = pix0 + q < OHW ? base + q : next + q;
+                } else {
+                    const int nq = p / OHW, pq = p - nq * OHW;
+                    idx = ((int64_t)nq * Cout + co) * OHW + pq;
+                }
+                store_elem<KIND>(a.y, idx, out[q]);
             }
         }
     }
