@@ -372,7 +372,8 @@ struct DmaTile {
     static constexpr int SB = (BM + BN) * BK;
     static constexpr int LDS_BYTES = NBUF * SB;
     static_assert(A_I * ROWS_PER_INSTR * NW == BM && B_I * ROWS_PER_INSTR * NW == BN, "copy split");
-    static_assert(WN == 64 && FN == 4, "each lane owns 16 consecutive output columns of a 64-column wave tile");
+    static constexpr int NH = WN / 64;  // 64-column halves of the wave tile
+    static_assert(WN % 64 == 0 && NH <= 2, "each lane owns 16 consecutive output columns of each 64-column half");
     static_assert(WM % 32 == 0, "fragment swizzle parity");
     static_assert(LDS_BYTES <= 160 * 1024, "LDS budget");
 };
@@ -380,6 +381,32 @@ struct DmaTile {
 // LDS stage buffers of the DMA main loop (a third buffer measured the same at 4096^3: the
 // copies land within one stage).
 constexpr int GEMM_NBUF = 2;
+
+// v_med3_i32: the median of x, lo, hi, which is min(max(x, lo), hi) whenever lo <= hi (one
+// instruction where the compiler, not knowing lo <= hi, emits two).
+__device__ __forceinline__ int32_t med3_i32(int32_t x, int32_t lo, int32_t hi) {
+    int32_t r;
+    asm("v_med3_i32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(lo), "v"(hi));
+    return r;
+}
+
+// The low bytes of v[0..3] as one dword (byte d = v[d] & 0xff): three v_perm_b32.
+__device__ __forceinline__ uint32_t pack_low_bytes(const uint32_t* v) {
+    // v_perm_b32 selects bytes of {src0, src1} (src1 = bytes 0-3, src0 = 4-7; 0x0c gives 0)
+    const uint32_t lo = __builtin_amdgcn_perm(v[1], v[0], 0x0c0c0400u);  // v0.b0, v1.b0, 0, 0
+    const uint32_t hi = __builtin_amdgcn_perm(v[3], v[2], 0x0c0c0400u);  // v2.b0, v3.b0, 0, 0
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);                    // lo.b0, lo.b1, hi.b0, hi.b1
+}
+
+// Calls f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>): a loop whose body
+// indexes register arrays, unrolled whatever the body's size (a loop the unroller leaves
+// rolled turns such an array into scratch memory).
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    [&]<int... Is>(std::integer_sequence<int, Is...>) {
+        (f(std::integral_constant<int, Is>()), ...);
+    }(std::make_integer_sequence<int, N>());
+}
 
 // Scheduling pattern for one K step: R fragment reads (DS) spread over Q MFMAs, each read
 // followed by its share of the MFMAs.
@@ -408,7 +435,8 @@ __device__ __forceinline__ void pin_reads_mfmas() {
 // conservative vmcnt(0) in front of every LDS read (it cannot tell the stage buffers apart);
 // the explicit vmcnt waits below are the synchronization.  Copies of stages past the end
 // are clamped to the last stage (a valid address, landing in a buffer never read again),
-// which keeps the steady-state loop free of branches.
+// which keeps the steady-state loop free of branches; with a two-stage ring (wait =
+// vmcnt(0)) the tail stages after the loop issue no copies at all.
 //
 // Output layout: B fragment i reads, in its lane row rho, the wave-tile row
 // (rho / 4) * 16 + 4 i + rho % 4.  The MFMA's output lane l, register r then holds column
@@ -418,10 +446,11 @@ __device__ __forceinline__ void pin_reads_mfmas() {
 // after the main loop, so their registers do not compete with the fragment double buffer.
 
 template <int BM, int BN, int WAVES_M, int WAVES_N, int NBUF, int KIND>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves_per_eu(2))) void gemm_i8_dma_kernel(GemmArgs a) {
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N)
+__attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N >= 8 ? 2 : 1))) void gemm_i8_dma_kernel(GemmArgs a) {
     typedef DmaTile<BM, BN, WAVES_M, WAVES_N, NBUF> P;
     static_assert(NBUF >= 2 && (NBUF - 1) * P::LPS < 64, "stage ring");
-    constexpr int BK = P::BK, NW = P::NW, WM = P::WM, FM = P::FM, FN = P::FN;
+    constexpr int BK = P::BK, NW = P::NW, WM = P::WM, WN = P::WN, FM = P::FM, FN = P::FN, NH = P::NH;
     constexpr int RPI = P::ROWS_PER_INSTR, A_I = P::A_I, B_I = P::B_I, SB = P::SB;
     constexpr bool INT_CODES = KIND == LQ_OUT_Q8 || KIND == LQ_OUT_QU8 || KIND == LQ_OUT_Q16 || KIND == LQ_OUT_QU8S8;
     __shared__ __attribute__((aligned(1024))) int8_t lds[P::LDS_BYTES];
@@ -463,13 +492,14 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves
         for (int j = 0; j < B_I; ++j) lds_dma16(rb, b_off[j], k0, sb + BM * BK + (j * NW + wave) * RPI * BK);
     };
     // Fragment addresses.  A fragment j: rows wm*WM + 16 j + rho, rho = lane % 16; B fragment i:
-    // rows wn*64 + (rho / 4) * 16 + 4 i + rho % 4.  Logical chunk of K step s: 4 s + lane / 16.
+    // rows wn*WN + 64 (i / 4) + (rho / 4) * 16 + 4 (i % 4) + rho % 4.  Logical chunk of K step s:
+    // 4 s + lane / 16.
     // The swizzle of an A row depends on rho and the parity of j, that of a B row on rho and
     // the parity of i; the K step flips chunk bit 2.  So two base offsets per operand, with
     // bit 6 (chunk bit 2) toggled by s ^ parity.
     const int rho = lane & 15, c0 = lane >> 4;
     const int a_base = (wm * WM + rho) * BK + ((c0 ^ (rho & 7)) << 4);
-    const int b_row = wn * 64 + (rho >> 2) * 16 + (rho & 3);
+    const int b_row = wn * WN + (rho >> 2) * 16 + (rho & 3);
     const int b_base = BM * BK + b_row * BK + ((c0 ^ dma_swz(b_row)) << 4);
     v4i F0[FM + FN], F1[FM + FN];
     auto read_frags = [&](v4i* f, int buf, int s) __attribute__((always_inline)) {
@@ -479,7 +509,8 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves
             f[j] = *reinterpret_cast<const v4i*>(sbuf + (a_base ^ (((s ^ j) & 1) << 6)) + j * 16 * BK);
 #pragma unroll
         for (int i = 0; i < FN; ++i)
-            f[FM + i] = *reinterpret_cast<const v4i*>(sbuf + (b_base ^ (((s ^ i) & 1) << 6)) + i * 4 * BK);
+            f[FM + i] = *reinterpret_cast<const v4i*>(sbuf + (b_base ^ (((s ^ i) & 1) << 6)) + (i & 3) * 4 * BK +
+                                                      (i >> 2) * 64 * BK);
     };
     v4i acc[FN][FM];
 #pragma unroll
@@ -498,15 +529,16 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves
     // over this step's FM * FN MFMAs, one read ahead of each run of MFMAs.
     auto pin_order = [&]() __attribute__((always_inline)) { pin_reads_mfmas<FM + FN, FM * FN>(); };
     // One stage in buffer B (compile time), ending with the switch to the other buffer.
-    auto stage = [&](auto bc, int kt, bool last) __attribute__((always_inline)) {
+    auto stage = [&](auto bc, int kt, bool last, auto tail_c) __attribute__((always_inline)) {
         constexpr int B = decltype(bc)::value;
+        constexpr bool TAIL = decltype(tail_c)::value;
         read_frags(F1, B, 1);
         mfmas(F0);
         pin_order();
         if (!last) {
             wait_vmcnt<(NBUF - 2) * P::LPS>();  // stage kt+1 has landed (kt+2.. may be in flight)
             block_barrier();  // ... in every wave, and every wave is done reading stage kt
-            issue(B, kt + NBUF);
+            if constexpr (!TAIL || NBUF > 2) issue(B, kt + NBUF);
             read_frags(F0, (B + 1) % NBUF, 0);
         }
         mfmas(F1);
@@ -522,230 +554,267 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves
         int kt = 0;
         for (; kt + NBUF < nk; kt += NBUF) {
             [&]<int... Bs>(std::integer_sequence<int, Bs...>) {
-                (stage(std::integral_constant<int, Bs>(), kt + Bs, false), ...);
+                (stage(std::integral_constant<int, Bs>(), kt + Bs, false, std::false_type()), ...);
             }(std::make_integer_sequence<int, NBUF>());
         }
         [&]<int... Bs>(std::integer_sequence<int, Bs...>) {
-            ((kt + Bs < nk ? stage(std::integral_constant<int, Bs>(), kt + Bs, kt + Bs + 1 == nk) : void()), ...);
+            ((kt + Bs < nk ? stage(std::integral_constant<int, Bs>(), kt + Bs, kt + Bs + 1 == nk, std::true_type())
+                           : void()),
+             ...);
         }(std::make_integer_sequence<int, NBUF>());
     }
     // Epilogue inputs, loaded after the main loop so their registers (52 per lane) do not
     // compete with the fragment double buffer: this lane's 16 columns and FM rows, as 16-byte
     // loads when the 16 columns are in range and the arrays aligned.
     const EpiParams p = epi_params(a);
-    const int nc0 = n0 + wn * 64 + (lane >> 4) * 16;
     const int mr0 = m0 + wm * WM + (lane & 15);
-    float csb[16], cbias[16];
-    int32_t czab[16];  // za * bsum[n]
-    {
-        const bool cols_vec = nc0 + 16 <= a.N;
-        auto vec_ok = [&](const void* ptr) { return cols_vec && (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
-        if (a.b_scale && a.b_stride == 1 && vec_ok(a.b_scale)) {
-#pragma unroll
-            for (int h = 0; h < 4; ++h) {
-                const v4f v = *reinterpret_cast<const v4f*>(a.b_scale + nc0 + 4 * h);
-                csb[4 * h] = v[0], csb[4 * h + 1] = v[1], csb[4 * h + 2] = v[2], csb[4 * h + 3] = v[3];
+    // Both halves' column inputs and the row scales are loaded (and waited for) before any
+    // output store: stores count in vmcnt too, so a wait placed after the first half's stores
+    // would also wait for those stores to drain.
+    float csbs[NH][16], cbiass[NH][16];
+    int32_t czabs[NH][16];  // za * bsum[n]
+    static_for<NH>([&](auto h_c) __attribute__((always_inline)) {
+        constexpr int HF = decltype(h_c)::value;
+        const int nc0 = n0 + wn * WN + HF * 64 + (lane >> 4) * 16;
+        float* csb = csbs[HF];
+        float* cbias = cbiass[HF];
+        int32_t* czab = czabs[HF];
+        {
+            const bool cols_vec = nc0 + 16 <= a.N;
+            auto vec_ok = [&](const void* ptr) { return cols_vec && (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
+            if (a.b_scale && a.b_stride == 1 && vec_ok(a.b_scale)) {
+    #pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    const v4f v = *reinterpret_cast<const v4f*>(a.b_scale + nc0 + 4 * h);
+                    csb[4 * h] = v[0], csb[4 * h + 1] = v[1], csb[4 * h + 2] = v[2], csb[4 * h + 3] = v[3];
+                }
+            } else {
+    #pragma unroll
+                for (int q = 0; q < 16; ++q)
+                    csb[q] = a.b_scale ? a.b_scale[(int64_t)min(nc0 + q, a.N - 1) * a.b_stride] : 1.0f;
             }
-        } else {
-#pragma unroll
-            for (int q = 0; q < 16; ++q)
-                csb[q] = a.b_scale ? a.b_scale[(int64_t)min(nc0 + q, a.N - 1) * a.b_stride] : 1.0f;
-        }
-        if (a.bias && vec_ok(a.bias)) {
-#pragma unroll
-            for (int h = 0; h < 4; ++h) {
-                const v4f v = *reinterpret_cast<const v4f*>(a.bias + nc0 + 4 * h);
-                cbias[4 * h] = v[0], cbias[4 * h + 1] = v[1], cbias[4 * h + 2] = v[2], cbias[4 * h + 3] = v[3];
+            if (a.bias && vec_ok(a.bias)) {
+    #pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    const v4f v = *reinterpret_cast<const v4f*>(a.bias + nc0 + 4 * h);
+                    cbias[4 * h] = v[0], cbias[4 * h + 1] = v[1], cbias[4 * h + 2] = v[2], cbias[4 * h + 3] = v[3];
+                }
+            } else {
+    #pragma unroll
+                for (int q = 0; q < 16; ++q) cbias[q] = a.bias ? a.bias[min(nc0 + q, a.N - 1)] : 0.0f;
             }
-        } else {
-#pragma unroll
-            for (int q = 0; q < 16; ++q) cbias[q] = a.bias ? a.bias[min(nc0 + q, a.N - 1)] : 0.0f;
-        }
-        if (p.has_za && vec_ok(a.b_sums)) {
-#pragma unroll
-            for (int h = 0; h < 4; ++h) {
-                const v4i v = *reinterpret_cast<const v4i*>(a.b_sums + nc0 + 4 * h);
-#pragma unroll
-                for (int e = 0; e < 4; ++e) czab[4 * h + e] = (int32_t)((uint32_t)p.za * (uint32_t)v[e]);
+            if (p.has_za && vec_ok(a.b_sums)) {
+    #pragma unroll
+                for (int h = 0; h < 4; ++h) {
+                    const v4i v = *reinterpret_cast<const v4i*>(a.b_sums + nc0 + 4 * h);
+    #pragma unroll
+                    for (int e = 0; e < 4; ++e) czab[4 * h + e] = (int32_t)((uint32_t)p.za * (uint32_t)v[e]);
+                }
+            } else {
+    #pragma unroll
+                for (int q = 0; q < 16; ++q)
+                    czab[q] = p.has_za ? (int32_t)((uint32_t)p.za * (uint32_t)a.b_sums[min(nc0 + q, a.N - 1)]) : 0;
             }
-        } else {
-#pragma unroll
-            for (int q = 0; q < 16; ++q)
-                czab[q] = p.has_za ? (int32_t)((uint32_t)p.za * (uint32_t)a.b_sums[min(nc0 + q, a.N - 1)]) : 0;
         }
-    }
+    });
     float rsa[FM];
-#pragma unroll
-    for (int j = 0; j < FM; ++j) {
+    static_for<FM>([&](auto j_c) __attribute__((always_inline)) {
+        constexpr int j = decltype(j_c)::value;
         const int mm = min(mr0 + j * 16, a.M - 1);
         rsa[j] = a.a_scale ? a.a_scale[(int64_t)mm * a.a_stride] : 1.0f;
-    }
+    });
 
     wait_vmcnt<0>();  // no copy may still target LDS when the workgroup ends
 
-    // Epilogue from registers: acc[i][j][r] is C[mr0 + 16 j][nc0 + 4 i + r].  Every lane
-    // computes (rows past M hold zeros), so the cross-lane exchange below sees whole rows;
-    // only the stores are guarded.
-    constexpr int OB = OutTraits<KIND>::bytes;
-    const bool vec = (reinterpret_cast<uintptr_t>(a.C) % 16 == 0) && ((a.ldc * OB) % 16 == 0) &&
-                     (n0 + wn * 64 + 64 <= a.N);
-    CodeClamp cc{};
-    if (INT_CODES) cc = code_clamp<KIND>(a.qmin, a.qmax);
-    const bool has_bias = a.bias != nullptr, relu = a.relu != 0;
+    // One 64-column half HF of the wave tile at a time: acc[4 HF + i][j][r] is
+    // C[mr0 + 16 j][nc0 + 4 i + r].
+    auto epilogue_half = [&](auto h_c) __attribute__((always_inline)) {
+        constexpr int HF = decltype(h_c)::value;
+        const int ncw = n0 + wn * WN + HF * 64;  // first column of this 64-column half
+        const int nc0 = ncw + (lane >> 4) * 16;
+        const float* csb = csbs[HF];
+        const float* cbias = cbiass[HF];
+        const int32_t* czab = czabs[HF];
 
-    // Stores of one row's 16 outputs (bits of the output type in out[]).
-    auto store_row = [&](int j, const uint32_t* out) __attribute__((always_inline)) {
-        const int m = mr0 + j * 16;
-        const bool row_ok = m < a.M;
-        if (vec) {
-            if (OB == 1) {
-                v4i w;
-#pragma unroll
-                for (int d = 0; d < 4; ++d)
-                    w[d] = (int)((out[4 * d] & 0xffu) | ((out[4 * d + 1] & 0xffu) << 8) |
-                                 ((out[4 * d + 2] & 0xffu) << 16) | (out[4 * d + 3] << 24));
-                if (row_ok) *reinterpret_cast<v4i*>(reinterpret_cast<uint8_t*>(a.C) + (int64_t)m * a.ldc + nc0) = w;
-            } else if (OB == 2) {
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    v4i w;
-#pragma unroll
-                    for (int d = 0; d < 4; ++d)
-                        w[d] = (int)((out[8 * h + 2 * d] & 0xffffu) | (out[8 * h + 2 * d + 1] << 16));
-                    if (row_ok)
-                        *reinterpret_cast<v4i*>(reinterpret_cast<uint16_t*>(a.C) + (int64_t)m * a.ldc + nc0 + 8 * h) = w;
-                }
-            } else {
-                // 4-byte outputs: lane group g = lane / 16 holds 16-byte pieces h = 0..3 of
-                // columns 16 g + 4 h.  A 4x4 transpose across (g, h) -- permlane32 swaps of
-                // pieces (0,2), (1,3), then permlane16 swaps of (0,1), (2,3), all among lanes
-                // of the same row -- leaves piece (h, g) in lane group g, register h, so
-                // store h covers 64 contiguous bytes of the row.
-                uint32_t v[4][4];
-#pragma unroll
-                for (int h = 0; h < 4; ++h)
-#pragma unroll
-                    for (int d = 0; d < 4; ++d) v[h][d] = out[4 * h + d];
-#pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    auto s02 = __builtin_amdgcn_permlane32_swap(v[0][d], v[2][d], false, false);
-                    auto s13 = __builtin_amdgcn_permlane32_swap(v[1][d], v[3][d], false, false);
-                    v[0][d] = s02[0], v[2][d] = s02[1], v[1][d] = s13[0], v[3][d] = s13[1];
-                    auto s01 = __builtin_amdgcn_permlane16_swap(v[0][d], v[1][d], false, false);
-                    auto s23 = __builtin_amdgcn_permlane16_swap(v[2][d], v[3][d], false, false);
-                    v[0][d] = s01[0], v[1][d] = s01[1], v[2][d] = s23[0], v[3][d] = s23[1];
-                }
-                const int64_t rb0 = (int64_t)m * a.ldc + n0 + wn * 64 + (lane >> 4) * 4;
-#pragma unroll
-                for (int h = 0; h < 4; ++h)
-                    if (row_ok)
-                        *reinterpret_cast<v4i*>(reinterpret_cast<uint32_t*>(a.C) + rb0 + 16 * h) =
-                            v4i{(int)v[h][0], (int)v[h][1], (int)v[h][2], (int)v[h][3]};
-            }
-        } else if (row_ok) {
-            const int64_t base = (int64_t)m * a.ldc + nc0;
-#pragma unroll
-            for (int q = 0; q < 16; ++q)
-                if (nc0 + q < a.N) store_elem<KIND>(a.C, base + q, out[q]);
-        }
-    };
+        // Epilogue from registers.  Every lane computes (rows past M hold zeros), so the
+        // cross-lane exchange below sees whole rows; only the stores are guarded.
+        constexpr int OB = OutTraits<KIND>::bytes;
+        const bool vec = (reinterpret_cast<uintptr_t>(a.C) % 16 == 0) && ((a.ldc * OB) % 16 == 0) &&
+                         (ncw + 64 <= a.N);
+        CodeClamp cc{};
+        if (INT_CODES) cc = code_clamp<KIND>(a.qmin, a.qmax);
+        const bool has_bias = a.bias != nullptr, relu = a.relu != 0;
 
-    // Integer codes, fast form.  When the output scale's reciprocal is finite and positive,
-    // the zero point integral and small, every scale and bias of this wave finite and
-    // max|sa| * max|sb| small enough that float(acc) * s cannot overflow, y is always finite,
-    // and the code clamp(rne(y * inv) + z, lo, hi) equals zi + med3(cvt(rne(y * inv)), lo - zi,
-    // hi - zi): the saturating convert keeps out-of-range values ordered and |zi| < 2^22 keeps
-    // the sum exact.  ReLU (y <= 0 -> 0, so the code of z) folds into the lower bound:
-    // rne(y * inv) <= 0 exactly when y <= 0.  The stored byte of QU8S8 is c - 128.
-    bool fast_int = false;
-    if constexpr (INT_CODES) {
-        const float zf = p.out_z;
-        bool ok = a.b_zp == nullptr && p.out_inv > 0.0f && p.out_inv < 3.0e38f && zf == __builtin_rintf(zf) &&
-                  __builtin_fabsf(zf) < 4194304.0f;
-        float amax = 0.0f, bmax = 0.0f;
-#pragma unroll
-        for (int j = 0; j < FM; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(rsa[j]));
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            bmax = __builtin_fmaxf(bmax, __builtin_fabsf(csb[q]));
-            ok = ok && __builtin_isfinite(cbias[q]);
-        }
-        // fmaxf ignores NaN: test the maxima and every scale for finiteness
-#pragma unroll
-        for (int j = 0; j < FM; ++j) ok = ok && __builtin_isfinite(rsa[j]);
-#pragma unroll
-        for (int q = 0; q < 16; ++q) ok = ok && __builtin_isfinite(csb[q]);
-        ok = ok && amax < 1.0e14f && bmax < 1.0e14f && amax * bmax < 1.0e28f;
-        fast_int = __all(ok);
-    }
-    if constexpr (INT_CODES) {
-        if (fast_int) {
-            const int zi = (int)p.out_z;
-            int L = cc.lo - zi, H = cc.hi - zi;
-            if (relu) L = min(max(L, 0), H);
-            const int shift = zi - (KIND == LQ_OUT_QU8S8 ? 128 : 0);
-            auto rows = [&](auto bias_c) __attribute__((always_inline)) {
-                constexpr bool BIAS = decltype(bias_c)::value;
-#pragma unroll
-                for (int j = 0; j < FM; ++j) {
-                    uint32_t out[16];
-#pragma unroll
-                    for (int q = 0; q < 16; ++q) {
-                        const int32_t accq = (int32_t)((uint32_t)acc[q >> 2][j][q & 3] - (uint32_t)czab[q]);
-                        const float sc = rsa[j] * csb[q];
-                        float y = (float)accq * sc;
-                        if (BIAS) y = y + cbias[q];
-                        const float r = __builtin_rintf(y * p.out_inv);
-                        out[q] = (uint32_t)(min(max(cvt_i32_sat(r), L), H) + shift);
-                    }
-                    store_row(j, out);
-                }
-            };
-            if (has_bias) rows(std::true_type{});
-            else rows(std::false_type{});
-            return;
-        }
-    }
-    // General form (any zero points, non-finite inputs, non-integral output zero point, and
-    // the float kinds): bias and ReLU resolved outside the element loop.
-    auto rows_general = [&](auto bias_c, auto relu_c) __attribute__((always_inline)) {
-        constexpr bool BIAS = decltype(bias_c)::value, RELU = decltype(relu_c)::value;
-#pragma unroll
-        for (int j = 0; j < FM; ++j) {
+        // Stores of one row's 16 outputs (bits of the output type in out[]).
+        auto store_row = [&](int j, const uint32_t* out) __attribute__((always_inline)) {
             const int m = mr0 + j * 16;
-            int32_t asum = 0;
-            if (a.b_zp) asum = a.a_sums[min(m, a.M - 1)];
-            uint32_t out[16];
-#pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                uint32_t accu = (uint32_t)acc[q >> 2][j][q & 3] - (uint32_t)czab[q];
-                if (a.b_zp) {  // weight zero points (rare): per-column terms read here
-                    const int nn = min(nc0 + q, a.N - 1);
-                    const uint32_t zb = (uint32_t)(int)a.b_zp[nn];
-                    accu -= zb * (uint32_t)asum;
-                    accu += (uint32_t)a.K * (uint32_t)p.za * zb;
-                }
-                if (INT_CODES) {
-                    const float sc = rsa[j] * csb[q];
-                    float y = (float)(int32_t)accu * sc;
-                    if (BIAS) y = y + cbias[q];
-                    if (RELU) y = (y <= 0.0f) ? 0.0f : y;
-                    out[q] = (uint32_t)requant_int<KIND>(y, p, cc);
-                    if (KIND == LQ_OUT_QU8S8) out[q] ^= 0x80u;
+            const bool row_ok = m < a.M;
+            if (vec) {
+                if (OB == 1) {
+                    v4i w;
+    #pragma unroll
+                    for (int d = 0; d < 4; ++d) w[d] = (int)pack_low_bytes(out + 4 * d);
+                    if (row_ok) *reinterpret_cast<v4i*>(reinterpret_cast<uint8_t*>(a.C) + (int64_t)m * a.ldc + nc0) = w;
+                } else if (OB == 2) {
+    #pragma unroll
+                    for (int h = 0; h < 2; ++h) {
+                        v4i w;
+    #pragma unroll
+                        for (int d = 0; d < 4; ++d)
+                            w[d] = (int)((out[8 * h + 2 * d] & 0xffffu) | (out[8 * h + 2 * d + 1] << 16));
+                        if (row_ok)
+                            *reinterpret_cast<v4i*>(reinterpret_cast<uint16_t*>(a.C) + (int64_t)m * a.ldc + nc0 + 8 * h) = w;
+                    }
                 } else {
-                    out[q] = epi_one<KIND>((int32_t)accu, rsa[j], csb[q], BIAS ? &cbias[q] : nullptr, RELU, p);
+                    // 4-byte outputs: lane group g = lane / 16 holds 16-byte pieces h = 0..3 of
+                    // columns 16 g + 4 h.  A 4x4 transpose across (g, h) -- permlane32 swaps of
+                    // pieces (0,2), (1,3), then permlane16 swaps of (0,1), (2,3), all among lanes
+                    // of the same row -- leaves piece (h, g) in lane group g, register h, so
+                    // store h covers 64 contiguous bytes of the row.
+                    uint32_t v[4][4];
+    #pragma unroll
+                    for (int h = 0; h < 4; ++h)
+    #pragma unroll
+                        for (int d = 0; d < 4; ++d) v[h][d] = out[4 * h + d];
+    #pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        auto s02 = __builtin_amdgcn_permlane32_swap(v[0][d], v[2][d], false, false);
+                        auto s13 = __builtin_amdgcn_permlane32_swap(v[1][d], v[3][d], false, false);
+                        v[0][d] = s02[0], v[2][d] = s02[1], v[1][d] = s13[0], v[3][d] = s13[1];
+                        auto s01 = __builtin_amdgcn_permlane16_swap(v[0][d], v[1][d], false, false);
+                        auto s23 = __builtin_amdgcn_permlane16_swap(v[2][d], v[3][d], false, false);
+                        v[0][d] = s01[0], v[1][d] = s01[1], v[2][d] = s23[0], v[3][d] = s23[1];
+                    }
+                    const int64_t rb0 = (int64_t)m * a.ldc + ncw + (lane >> 4) * 4;
+    #pragma unroll
+                    for (int h = 0; h < 4; ++h)
+                        if (row_ok)
+                            *reinterpret_cast<v4i*>(reinterpret_cast<uint32_t*>(a.C) + rb0 + 16 * h) =
+                                v4i{(int)v[h][0], (int)v[h][1], (int)v[h][2], (int)v[h][3]};
                 }
+            } else if (row_ok) {
+                const int64_t base = (int64_t)m * a.ldc + nc0;
+    #pragma unroll
+                for (int q = 0; q < 16; ++q)
+                    if (nc0 + q < a.N) store_elem<KIND>(a.C, base + q, out[q]);
             }
-            store_row(j, out);
+        };
+
+        // Integer codes, fast form.  When the output scale's reciprocal is finite and positive,
+        // the zero point integral and small, every scale and bias of this wave finite and
+        // max|sa| * max|sb| small enough that float(acc) * s cannot overflow, y is always finite,
+        // and the code clamp(rne(y * inv) + z, lo, hi) equals zi + med3(cvt(rne(y * inv)), lo - zi,
+        // hi - zi): the saturating convert keeps out-of-range values ordered and |zi| < 2^22 keeps
+        // the sum exact.  ReLU (y <= 0 -> 0, so the code of z) folds into the lower bound:
+        // rne(y * inv) <= 0 exactly when y <= 0.  The stored byte of QU8S8 is c - 128.
+        bool fast_int = false;
+        if constexpr (INT_CODES) {
+            const float zf = p.out_z;
+            bool ok = a.b_zp == nullptr && p.out_inv > 0.0f && p.out_inv < 3.0e38f && zf == __builtin_rintf(zf) &&
+                      __builtin_fabsf(zf) < 4194304.0f;
+            float amax = 0.0f, bmax = 0.0f;
+    #pragma unroll
+            for (int j = 0; j < FM; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(rsa[j]));
+    #pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                bmax = __builtin_fmaxf(bmax, __builtin_fabsf(csb[q]));
+                ok = ok && __builtin_isfinite(cbias[q]);
+            }
+            // fmaxf ignores NaN: test the maxima and every scale for finiteness
+    #pragma unroll
+            for (int j = 0; j < FM; ++j) ok = ok && __builtin_isfinite(rsa[j]);
+    #pragma unroll
+            for (int q = 0; q < 16; ++q) ok = ok && __builtin_isfinite(csb[q]);
+            ok = ok && amax < 1.0e14f && bmax < 1.0e14f && amax * bmax < 1.0e28f;
+            fast_int = __all(ok);
+        }
+        if constexpr (INT_CODES) {
+            if (fast_int) {
+                const int zi = (int)p.out_z;
+                int L = cc.lo - zi, H = cc.hi - zi;
+                if (relu) L = max(L, 0);
+                L = min(L, H);  // med3(x, L, H) = min(max(x, L), H) needs L <= H
+                const int shift = zi - (KIND == LQ_OUT_QU8S8 ? 128 : 0);
+                // ZA / SHIFT off when the activation zero point / the code shift are zero:
+                // two VALU ops fewer per element.
+                auto rows = [&](auto bias_c, auto za_c, auto shift_c) __attribute__((always_inline)) {
+                    constexpr bool BIAS = decltype(bias_c)::value, ZA = decltype(za_c)::value;
+                    constexpr bool SHIFT = decltype(shift_c)::value;
+                    static_for<FM>([&](auto j_c) __attribute__((always_inline)) {
+                        constexpr int j = decltype(j_c)::value;
+                        uint32_t out[16];
+    #pragma unroll
+                        for (int q = 0; q < 16; ++q) {
+                            int32_t accq = acc[4 * HF + (q >> 2)][j][q & 3];
+                            if (ZA) accq = (int32_t)((uint32_t)accq - (uint32_t)czab[q]);
+                            const float sc = rsa[j] * csb[q];
+                            float y = (float)accq * sc;
+                            if (BIAS) y = y + cbias[q];
+                            const float r = __builtin_rintf(y * p.out_inv);
+                            int32_t c = med3_i32(cvt_i32_sat(r), L, H);
+                            if (SHIFT) c += shift;
+                            out[q] = (uint32_t)c;
+                        }
+                        store_row(j, out);
+                    });
+                };
+                auto rows_za = [&](auto bias_c) __attribute__((always_inline)) {
+                    if (p.has_za) {
+                        if (shift != 0) rows(bias_c, std::true_type{}, std::true_type{});
+                        else rows(bias_c, std::true_type{}, std::false_type{});
+                    } else {
+                        if (shift != 0) rows(bias_c, std::false_type{}, std::true_type{});
+                        else rows(bias_c, std::false_type{}, std::false_type{});
+                    }
+                };
+                if (has_bias) rows_za(std::true_type{});
+                else rows_za(std::false_type{});
+                return;
+            }
+        }
+        // General form (any zero points, non-finite inputs, non-integral output zero point, and
+        // the float kinds): bias and ReLU resolved outside the element loop.
+        auto rows_general = [&](auto bias_c, auto relu_c) __attribute__((always_inline)) {
+            constexpr bool BIAS = decltype(bias_c)::value, RELU = decltype(relu_c)::value;
+            static_for<FM>([&](auto j_c) __attribute__((always_inline)) {
+                constexpr int j = decltype(j_c)::value;
+                const int m = mr0 + j * 16;
+                int32_t asum = 0;
+                if (a.b_zp) asum = a.a_sums[min(m, a.M - 1)];
+                uint32_t out[16];
+    #pragma unroll
+                for (int q = 0; q < 16; ++q) {
+                    uint32_t accu = (uint32_t)acc[4 * HF + (q >> 2)][j][q & 3] - (uint32_t)czab[q];
+                    if (a.b_zp) {  // weight zero points (rare): per-column terms read here
+                        const int nn = min(nc0 + q, a.N - 1);
+                        const uint32_t zb = (uint32_t)(int)a.b_zp[nn];
+                        accu -= zb * (uint32_t)asum;
+                        accu += (uint32_t)a.K * (uint32_t)p.za * zb;
+                    }
+                    if (INT_CODES) {
+                        const float sc = rsa[j] * csb[q];
+                        float y = (float)(int32_t)accu * sc;
+                        if (BIAS) y = y + cbias[q];
+                        if (RELU) y = (y <= 0.0f) ? 0.0f : y;
+                        out[q] = (uint32_t)requant_int<KIND>(y, p, cc);
+                        if (KIND == LQ_OUT_QU8S8) out[q] ^= 0x80u;
+                    } else {
+                        out[q] = epi_one<KIND>((int32_t)accu, rsa[j], csb[q], BIAS ? &cbias[q] : nullptr, RELU, p);
+                    }
+                }
+                store_row(j, out);
+            });
+        };
+        if (has_bias) {
+            if (relu) rows_general(std::true_type{}, std::true_type{});
+            else rows_general(std::true_type{}, std::false_type{});
+        } else {
+            if (relu) rows_general(std::false_type{}, std::true_type{});
+            else rows_general(std::false_type{}, std::false_type{});
         }
     };
-    if (has_bias) {
-        if (relu) rows_general(std::true_type{}, std::true_type{});
-        else rows_general(std::true_type{}, std::false_type{});
-    } else {
-        if (relu) rows_general(std::false_type{}, std::true_type{});
-        else rows_general(std::false_type{}, std::false_type{});
-    }
+    epilogue_half(std::integral_constant<int, 0>());
+    if constexpr (NH > 1) epilogue_half(std::integral_constant<int, 1>());
 }
 
 // ------------------------------------------------------ skinny-M (decode) kernel
@@ -1145,6 +1214,16 @@ struct GemmLaunch {
         const bool dma_ok = (a.K % 128 == 0) && ((int64_t)(a.M + 256) * a.lda < (int64_t)1 << 31) &&
                             ((int64_t)(a.N + 256) * a.ldb < (int64_t)1 << 31);
         const int64_t dma_tiles = ((int64_t)(a.M + 255) / 256) * ((a.N + 127) / 128);
+        // 256x256 tiles (8 waves of 128x64: a third fewer LDS fragment bytes per MFMA) take
+        // ~15% less time per op than 256x128 tiles (waves of 64x64) but come in half as many
+        // workgroups: compare the two in rounds of 256 workgroups (one per CU).
+        const int64_t t256 = ((int64_t)(a.M + 255) / 256) * ((a.N + 255) / 256);
+        if (dma_ok && t256 >= 256 && ((t256 + 255) / 256) * 100 <= ((dma_tiles + 255) / 256) * 57) {
+            hipLaunchKernelGGL((gemm_i8_dma_kernel<256, 256, 2, 4, GEMM_NBUF, KIND>), dim3((unsigned)t256),
+                               dim3(512), 0, st, a);
+            note_path("gemm dma 256x256");
+            return launch_status("lq_gemm_w8a8 (dma 256x256)");
+        }
         if (dma_ok && dma_tiles >= 256) {
             hipLaunchKernelGGL((gemm_i8_dma_kernel<256, 128, 4, 2, GEMM_NBUF, KIND>), dim3((unsigned)dma_tiles),
                                dim3(512), 0, st, a);

@@ -1,7 +1,7 @@
 """GPU parity of the W8A8 int8 MFMA GEMM (lq_gemm_w8a8) through the C ABI.
 
 * int32 accumulators: bit-exact against the oracle's int64 brute force on every kernel
-  path (skinny M <= 64; LDS-DMA 256x128 and 128x128 tiles; register-staged 128x128 tiles
+  path (skinny M <= 64; LDS-DMA 256x256, 256x128 and 128x128 tiles; register-staged 128x128 tiles
   with and without split-K; generic);
 * every epilogue kind (f32, f16, requantized int8 / uint8 / int16 / uint8-as-int8,
   fake-quantized f32) with activation and weight zero points, bias and ReLU: bit-exact
@@ -114,7 +114,7 @@ def _codes(rng, shape, lo=-127, hi=127):
 
 # Shapes chosen to hit every dispatch path of the kernel selector:
 #   M <= 16 / 32 / 64 -> skinny (1, 2, 4 m-tiles); K % 128 == 0 with enough tiles -> LDS-DMA
-#   256x128 / 128x128; otherwise register-staged 128x128 (split-K when tiles are few);
+#   256x256 / 256x128 / 128x128; otherwise register-staged 128x128 (split-K when tiles are few);
 #   K % 16 != 0 or unaligned -> generic.
 ACC_SHAPES = [
     (1, 64, 64), (1, 1000, 784), (3, 4096, 512), (16, 256, 4096), (17, 100, 256),
@@ -146,10 +146,11 @@ def test_int32_accumulator_staged_many_tiles(gpu):
 
 
 @pytest.mark.parametrize("M,N,K", [(1500, 2900, 256), (2000, 6400, 384), (257, 16384, 128),
-                                   (4096, 4100, 128), (1000, 2100, 256), (300, 7000, 128)])
+                                   (4096, 4100, 128), (1000, 2100, 256), (300, 7000, 128),
+                                   (3900, 8000, 128)])
 def test_int32_accumulator_dma_path(gpu, M, N, K):
-    """The LDS-DMA 256x128 path (K % 128 == 0, >= 128 tiles) with ragged M and N: rows past
-    M or N come in as zeros through the buffer bounds and are never stored."""
+    """The LDS-DMA 256x128 and 256x256 paths (K % 128 == 0, >= 128 / 256 tiles) with ragged M
+    and N: rows past M or N come in as zeros through the buffer bounds and are never stored."""
     rng = np.random.default_rng(M + N + K)
     A = _codes(rng, (M, K), -128, 127)
     B = _codes(rng, (N, K), -128, 127)

@@ -1,10 +1,10 @@
 """The kernel instantiations the bench times, each checked bit-exactly against the oracle on
 the shapes (or the path) the bench runs.
 
-* W8A8 GEMM through the 256x128 LDS-DMA tile (the headline): every output kind with the full
-  epilogue (per-row and per-column scales, bias, ReLU, activation and weight zero points) on
-  shapes with >= 256 such tiles; the benched 4096^3 launches (int8 and f16 out) in full; the
-  4096x11008 shapes on sampled rows; the 128x128 tile at M = 1024.
+* W8A8 GEMM through the 256x256 LDS-DMA tile (the headline) and the 256x128 tile: every output
+  kind with the full epilogue (per-row and per-column scales, bias, ReLU, activation and weight
+  zero points) on shapes that reach each tile; the benched 4096^3 launches (int8 and f16 out)
+  in full; the 4096x11008 shapes on sampled rows; the 128x128 tile at M = 1024.
 * int8 Conv2d through the 256x64 tile: the ResNet-18 layers at batch 32 exactly as the bench
   configures them, plus every output kind on one 256x64 shape.
 * Config 2: observer, qparams, quantize and dequantize over 2^24 and 2^28 elements with the
@@ -45,14 +45,18 @@ def _path():
     return _C.last_path()
 
 
-# ------------------------------------------------------------------ GEMM 256x128
+# ------------------------------------------------------- GEMM 256x256 and 256x128
 
 
-@pytest.mark.parametrize("M,N,K", [(2048, 4096, 256), (2100, 4100, 384)])
-def test_gemm_256x128_every_kind_exact(gpu, M, N, K):
-    """>= 256 tiles of 256x128 with K % 128 == 0: the DMA 256x128 kernel, every output kind,
-    both epilogue forms (scales + bias; zero points + ReLU).  N = 4100 leaves a 4-column
-    tail handled by the scalar stores of the same kernel."""
+@pytest.mark.parametrize("M,N,K,path", [(2048, 4096, 256, "gemm dma 256x128"),
+                                        (2100, 4100, 384, "gemm dma 256x128"),
+                                        (4096, 4096, 256, "gemm dma 256x256"),
+                                        (4000, 4050, 384, "gemm dma 256x256")])
+def test_gemm_dma_every_kind_exact(gpu, M, N, K, path):
+    """K % 128 == 0 with enough tiles for the DMA kernels: 256 tiles of 256x256 (one round)
+    take the 256x256 kernel, fewer take 256 or more tiles of 256x128.  Every output kind, both
+    epilogue forms (scales + bias; zero points + ReLU).  N = 4100 / 4050 leave 4- and 18-column
+    tails handled by the scalar stores of the same kernel."""
     rng = np.random.default_rng(M + N + K)
     A = _codes(rng, (M, K), -128, 127)
     B = _codes(rng, (N, K))
@@ -67,10 +71,10 @@ def test_gemm_256x128_every_kind_exact(gpu, M, N, K):
         qmin, qmax = GRID.get(kind, (-128, 127))
         out_scale, out_zp = 0.37, (128.0 if qmin == 0 else -3.0)
         for (za, zbv, with_bias, relu), acc in zip(forms, accs):
-            print(f"gemm 256x128 M={M} N={N} K={K} kind={kind} za={za} relu={relu}", flush=True)
+            print(f"gemm {path} M={M} N={N} K={K} kind={kind} za={za} relu={relu}", flush=True)
             got = run_gemm(gpu, A, B, kind, a_scale, b_scale, za, zbv, None,
                            bias if with_bias else None, out_scale, out_zp, qmin, qmax, relu)
-            assert _path() == "gemm dma 256x128"
+            assert _path() == path
             want = O.gemm_epilogue(acc, a_scale, b_scale, bias if with_bias else None, out_scale,
                                    out_zp, qmin, qmax, kind, relu)
             _same_bits(got, want)
@@ -97,12 +101,12 @@ def test_gemm_headline_4096_full_exact(gpu):
     for kind in (O.OUT_Q8, O.OUT_F16):
         print(f"gemm headline 4096^3 kind={kind}", flush=True)
         got = run_gemm(gpu, A, B, kind, sa, sb, bias=bias, out_scale=64.0, out_zp=0.0)
-        assert _path() == "gemm dma 256x128"
+        assert _path() == "gemm dma 256x256"
         _same_bits(got, O.gemm_epilogue(acc, sa, sb, bias, 64.0, 0.0, -128, 127, kind, False))
 
 
-@pytest.mark.parametrize("M,N,K,path", [(4096, 11008, 4096, "gemm dma 256x128"),
-                                        (4096, 4096, 11008, "gemm dma 256x128"),
+@pytest.mark.parametrize("M,N,K,path", [(4096, 11008, 4096, "gemm dma 256x256"),
+                                        (4096, 4096, 11008, "gemm dma 256x256"),
                                         (1024, 4096, 4096, "gemm dma 128x128")])
 def test_gemm_sweep_shapes_exact(gpu, M, N, K, path):
     """The sweep's large shapes: 64 sampled rows in full (4096-row shapes), every row at
