@@ -41,6 +41,7 @@ if ROOT not in sys.path:
 HBM_PEAK_GBS = 8000.0
 INT8_PEAK_TOPS = 5000.0
 CLOCK_SETTLE_S = 0.5
+SWEEP_SETTLE_S = 0.15  # per row-major GEMM sweep line
 
 
 def _parse() -> argparse.Namespace:
@@ -295,6 +296,15 @@ class Gemm:
         return self.M * self.K + self.K * self.N + self.M * self.N * ob + 4.0 * (self.M + 2 * self.N)
 
 
+def settle(C, fn, seconds: float) -> None:
+    """Run fn untimed in batches of 16 for `seconds` of wall time, then synchronize."""
+    t_end = time.perf_counter() + seconds
+    while time.perf_counter() < t_end:
+        for _ in range(16):
+            fn()
+        C.synchronize()
+
+
 def gemm_line(L, C, timer, gtimer, M, N, K, out_kind, steps, warmup):
     g = Gemm(L, C, M, N, K, out_kind, seed=M + N + K)
     if g.packed:  # decode shapes are launch-bound from Python: graph replay
@@ -302,6 +312,9 @@ def gemm_line(L, C, timer, gtimer, M, N, K, out_kind, steps, warmup):
         # up to 2x slow, which 2 replays over a dozen weight copies did not average out
         ms = gtimer.time_ms(g.calls, max(steps // len(g.calls), 10), 2)
     else:
+        # The same clock settle as the headline: a few hundred microseconds of warm-up steps
+        # leave long launches in the GPU's ramp from idle clocks (10-20% slow).
+        settle(C, g.run, SWEEP_SETTLE_S)
         ms = timer.time_ms(g.run, steps, warmup)
     tops = g.ops / (ms * 1e-3) / 1e12
     gbs = g.bytes / (ms * 1e-3) / 1e9

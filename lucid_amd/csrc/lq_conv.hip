@@ -460,8 +460,11 @@ struct ConvDmaArgs {
     int32_t* part;
 };
 
+// Two waves per SIMD (<= 256 registers): the LDS ring leaves room for two workgroups per CU,
+// and their main loops and epilogues overlap.
 template <int BM, int BN, int WAVES_M, int WAVES_N, int NBUF, int KIND>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void conv_i8_dma_kernel(ConvDmaArgs a) {
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves_per_eu(2))) void conv_i8_dma_kernel(
+    ConvDmaArgs a) {
     constexpr int BK = 128, NW = WAVES_M * WAVES_N, WM = BM / WAVES_M, WN = BN / WAVES_N;
     constexpr int FM = WM / 16, FN = WN / 16;
     constexpr int A_I = BM / 8 / NW, B_I = BN / 8 / NW, LPS = A_I + B_I, SB = (BM + BN) * BK;
@@ -648,37 +651,14 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void conv_i8_dma_kernel(Con
     const int pix0 = pb - nimg * OHW;
     constexpr int OB = OutTraits<KIND>::bytes;
     const bool vec = (OHW % 16 == 0) && (reinterpret_cast<uintptr_t>(a.y) % 16 == 0) && (pb + 15 < a.P);
-#pragma unroll
-    for (int i = 0; i < FN; ++i) {
-        const int col = co0 + wn * WN + 16 * i + rho;
-        if (col >= a.Cout_g) continue;
-        const int co = g * a.Cout_g + col;
-        const float sb = csb[i];
-        const float bias = cbias[i];
-        const int32_t zsum = ep.has_za ? (int32_t)((uint32_t)ep.za * (uint32_t)cws[i]) : 0;
-        uint32_t out[16];
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const int32_t acc_c = (int32_t)((uint32_t)acc[i][q >> 2][q & 3] - (uint32_t)zsum);
-            if (INT_CODES) {
-                const float s = sa * sb;
-                float y = (float)acc_c * s;
-                if (a.bias) y = y + bias;
-                if (a.relu) y = (y <= 0.0f) ? 0.0f : y;
-                out[q] = (uint32_t)requant_int<KIND>(y, ep, cc);
-                if (KIND == LQ_OUT_QU8S8) out[q] ^= 0x80u;
-            } else {
-                out[q] = epi_one<KIND>(acc_c, sa, sb, a.bias ? &bias : nullptr, a.relu != 0, ep);
-            }
-        }
+    // Stores of one channel's 16 consecutive pixels (out[] holds the output type's bits).
+    auto store_col = [&](const int co, const uint32_t* out) __attribute__((always_inline)) {
         if (vec) {
             const int64_t base = ((int64_t)nimg * Cout + co) * OHW + pix0;
             if (OB == 1) {
                 v4i w;
 #pragma unroll
-                for (int d = 0; d < 4; ++d)
-                    w[d] = (int)((out[4 * d] & 0xffu) | ((out[4 * d + 1] & 0xffu) << 8) |
-                                 ((out[4 * d + 2] & 0xffu) << 16) | (out[4 * d + 3] << 24));
+                for (int d = 0; d < 4; ++d) w[d] = (int)pack_low_bytes(out + 4 * d);
                 *reinterpret_cast<v4i*>(reinterpret_cast<uint8_t*>(a.y) + base) = w;
             } else if (OB == 2) {
 #pragma unroll
@@ -714,6 +694,92 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void conv_i8_dma_kernel(Con
                 store_elem<KIND>(a.y, idx, out[q]);
             }
         }
+    };
+
+    // Integer codes, fast form (as in the GEMM epilogue): with the output scale's reciprocal
+    // finite and positive, the zero point integral and small, and every scale and bias of this
+    // wave finite and small enough that y stays finite, clamp(rne(y * inv) + z, lo, hi) equals
+    // zi + med3(cvt(rne(y * inv)), lo - zi, hi - zi), and ReLU folds into the lower bound.
+    if constexpr (INT_CODES) {
+        const float zf = ep.out_z;
+        bool ok = ep.out_inv > 0.0f && ep.out_inv < 3.0e38f && zf == __builtin_rintf(zf) &&
+                  __builtin_fabsf(zf) < 4194304.0f && __builtin_isfinite(sa);
+        float bmax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+            bmax = __builtin_fmaxf(bmax, __builtin_fabsf(csb[i]));
+            ok = ok && __builtin_isfinite(csb[i]) && __builtin_isfinite(cbias[i]);
+        }
+        const float amax = __builtin_fabsf(sa);
+        ok = ok && amax < 1.0e14f && bmax < 1.0e14f && amax * bmax < 1.0e28f;
+        if (__all(ok)) {
+            const int zi = (int)zf;
+            int L = cc.lo - zi, H = cc.hi - zi;
+            if (a.relu) L = max(L, 0);
+            L = min(L, H);  // med3(x, L, H) = min(max(x, L), H) needs L <= H
+            const int shift = zi - (KIND == LQ_OUT_QU8S8 ? 128 : 0);
+            auto cols = [&](auto bias_c, auto za_c, auto shift_c) __attribute__((always_inline)) {
+                constexpr bool BIAS = decltype(bias_c)::value, ZA = decltype(za_c)::value;
+                constexpr bool SHIFT = decltype(shift_c)::value;
+                static_for<FN>([&](auto i_c) __attribute__((always_inline)) {
+                    constexpr int i = decltype(i_c)::value;
+                    const int col = co0 + wn * WN + 16 * i + rho;
+                    if (col >= a.Cout_g) return;
+                    const float sc = sa * csb[i];
+                    const uint32_t zsum = (uint32_t)ep.za * (uint32_t)cws[i];
+                    uint32_t out[16];
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) {
+                        int32_t accq = acc[i][q >> 2][q & 3];
+                        if (ZA) accq = (int32_t)((uint32_t)accq - zsum);
+                        float y = (float)accq * sc;
+                        if (BIAS) y = y + cbias[i];
+                        const float r = __builtin_rintf(y * ep.out_inv);
+                        int32_t c = med3_i32(cvt_i32_sat(r), L, H);
+                        if (SHIFT) c += shift;
+                        out[q] = (uint32_t)c;
+                    }
+                    store_col(g * a.Cout_g + col, out);
+                });
+            };
+            auto cols_za = [&](auto bias_c) __attribute__((always_inline)) {
+                if (ep.has_za) {
+                    if (shift != 0) cols(bias_c, std::true_type{}, std::true_type{});
+                    else cols(bias_c, std::true_type{}, std::false_type{});
+                } else {
+                    if (shift != 0) cols(bias_c, std::false_type{}, std::true_type{});
+                    else cols(bias_c, std::false_type{}, std::false_type{});
+                }
+            };
+            if (a.bias) cols_za(std::true_type{});
+            else cols_za(std::false_type{});
+            return;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+        const int col = co0 + wn * WN + 16 * i + rho;
+        if (col >= a.Cout_g) continue;
+        const int co = g * a.Cout_g + col;
+        const float sb = csb[i];
+        const float bias = cbias[i];
+        const int32_t zsum = ep.has_za ? (int32_t)((uint32_t)ep.za * (uint32_t)cws[i]) : 0;
+        uint32_t out[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int32_t acc_c = (int32_t)((uint32_t)acc[i][q >> 2][q & 3] - (uint32_t)zsum);
+            if (INT_CODES) {
+                const float s = sa * sb;
+                float y = (float)acc_c * s;
+                if (a.bias) y = y + bias;
+                if (a.relu) y = (y <= 0.0f) ? 0.0f : y;
+                out[q] = (uint32_t)requant_int<KIND>(y, ep, cc);
+                if (KIND == LQ_OUT_QU8S8) out[q] ^= 0x80u;
+            } else {
+                out[q] = epi_one<KIND>(acc_c, sa, sb, a.bias ? &bias : nullptr, a.relu != 0, ep);
+            }
+        }
+        store_col(co, out);
     }
 }
 

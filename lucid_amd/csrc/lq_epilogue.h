@@ -10,6 +10,8 @@
 
 #include <hip/hip_fp16.h>
 
+#include <utility>
+
 #include "lq_internal.h"
 
 namespace lq {
@@ -93,6 +95,32 @@ __device__ __forceinline__ void store_elem(void* C, int64_t idx, uint32_t v) {
     if (b == 4) reinterpret_cast<uint32_t*>(C)[idx] = v;
     else if (b == 2) reinterpret_cast<uint16_t*>(C)[idx] = (uint16_t)v;
     else reinterpret_cast<uint8_t*>(C)[idx] = (uint8_t)v;
+}
+
+// v_med3_i32: the median of x, lo, hi, which is min(max(x, lo), hi) whenever lo <= hi (one
+// instruction where the compiler, not knowing lo <= hi, emits two).
+__device__ __forceinline__ int32_t med3_i32(int32_t x, int32_t lo, int32_t hi) {
+    int32_t r;
+    asm("v_med3_i32 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(lo), "v"(hi));
+    return r;
+}
+
+// The low bytes of v[0..3] as one dword (byte d = v[d] & 0xff): three v_perm_b32.
+__device__ __forceinline__ uint32_t pack_low_bytes(const uint32_t* v) {
+    // v_perm_b32 selects bytes of {src0, src1} (src1 = bytes 0-3, src0 = 4-7; 0x0c gives 0)
+    const uint32_t lo = __builtin_amdgcn_perm(v[1], v[0], 0x0c0c0400u);  // v0.b0, v1.b0, 0, 0
+    const uint32_t hi = __builtin_amdgcn_perm(v[3], v[2], 0x0c0c0400u);  // v2.b0, v3.b0, 0, 0
+    return __builtin_amdgcn_perm(hi, lo, 0x05040100u);                    // lo.b0, lo.b1, hi.b0, hi.b1
+}
+
+// Calls f(integral_constant<int, 0>) ... f(integral_constant<int, N - 1>): a loop whose body
+// indexes register arrays, unrolled whatever the body's size (a loop the unroller leaves
+// rolled turns such an array into scratch memory).
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+    [&]<int... Is>(std::integer_sequence<int, Is...>) {
+        (f(std::integral_constant<int, Is>()), ...);
+    }(std::make_integer_sequence<int, N>());
 }
 
 }  // namespace lq
