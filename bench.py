@@ -62,14 +62,16 @@ def _parse() -> argparse.Namespace:
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_w8a8_4096_traffic.json")
 
 
-def measured_traffic():
+def measured_traffic(path: str):
     """HBM bytes per launch of the headline GEMM kernel, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE summary (scaled by the copy-kernel calibration), or None."""
+    FETCH_SIZE / WRITE_SIZE summary (scaled by the copy-kernel calibration); None when there
+    is none or it was measured on another kernel than the dispatch path `path` this run took."""
     try:
         with open(TRAFFIC_FILE) as f:
-            return json.load(f).get("hbm_bytes_per_launch")
+            rec = json.load(f)
     except (OSError, ValueError):
         return None
+    return rec.get("hbm_bytes_per_launch") if rec.get("path") == path else None
 
 
 class Timer:
@@ -843,6 +845,7 @@ def main() -> None:
             head.run()
         C.synchronize()
     ms = timer.time_ms(head.run, args.steps, args.warmup)
+    head_path = C.last_path()
     tops = head.ops / (ms * 1e-3) / 1e12
     line = {
         "metric": "int8 GEMM TOPS + quant/dequant/GEMV GB/s (% roofline), 1xMI355X",
@@ -863,7 +866,8 @@ def main() -> None:
                    "M": M, "N": N, "K": K, "out": "int8"},
         "roofline": {"bound": "mfma", "achieved": round(tops, 2), "peak": INT8_PEAK_TOPS,
                      "unit": "TFLOP/s", "frac": round(tops / INT8_PEAK_TOPS, 4),
-                     "traffic": measured_traffic()},
+                     "traffic": measured_traffic(head_path),
+                     "ops": "int8 multiply-adds, 2 ops each (the contract's unit name is TFLOP/s)"},
     }
     if args.components:
         comps = {"gemm_sweep": []}
