@@ -838,27 +838,28 @@ __global__ __launch_bounds__(64 * W) void gemm_i8_skinny_kernel(GemmArgs a) {
                 acc[t] = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[u], af[u][t], acc[t], 0, 0, 0);
     }
 
+    const EpiParams p = epi_params(a);
     if (W > 1) {
+        // the waves' partial sums meet in LDS; wave w then adds up (in wave order) and stores
+        // the m-tiles t = w, w + W, ...
         __shared__ v4i red[W][MT][64];
 #pragma unroll
         for (int t = 0; t < MT; ++t) red[wave][t][lane] = acc[t];
         __syncthreads();
-        if (wave != 0) return;
-#pragma unroll
-        for (int t = 0; t < MT; ++t) {
+        for (int t = wave; t < MT; t += W) {
             v4i s = red[0][t][lane];
             for (int w = 1; w < W; ++w) s += red[w][t][lane];
-            acc[t] = s;
+            epilogue4<KIND>(a, p, t * 16 + (lane & 15), n0 + (lane >> 4) * 4, s);
         }
+        return;
     }
 
-    const EpiParams p = epi_params(a);
-#pragma unroll
-    for (int t = 0; t < MT; ++t) {
+    static_for<MT>([&](auto t_c) __attribute__((always_inline)) {
+        constexpr int t = decltype(t_c)::value;
         const int m = t * 16 + (lane & 15);
         const int n = n0 + (lane >> 4) * 4;
         epilogue4<KIND>(a, p, m, n, acc[t]);
-    }
+    });
 }
 
 // --------------------------------------------- packed weights (decode, M <= 64)
@@ -952,7 +953,7 @@ __global__ __launch_bounds__(64 * W) void gemm_i8_packed_skinny_kernel(GemmArgs 
 // ([split][m][n], rows padded to whole n-tiles); gemm_i8_decode_reduce_kernel adds the splits
 // in order and runs the epilogue.
 
-constexpr int DEC_MAX_KS = 8;  // k-steps (64 B) per split at most: a 512 B A row slice
+constexpr int DEC_MAX_KS = 16;  // k-steps (64 B) per split at most: a 1 KB A row slice (M = 128: 128 KB of LDS)
 
 struct DecodePlan {
     int ks_per_split, splits;
