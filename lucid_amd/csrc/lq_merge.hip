@@ -107,6 +107,54 @@ __global__ __launch_bounds__(kMergeBlock) void merge_kernel(MergeArgs m) {
     }
 }
 
+// Byte codes, contiguous operands and output, 16 elements (one 16-byte load of each operand,
+// one 16-byte store) per thread per step: the residual adds of a quantized network.  Each
+// element goes through the same operations as merge_kernel (merge_load, the op, ReLU,
+// quant_store), so the two paths agree bit for bit.
+template <int T>
+__device__ __forceinline__ float byte_code(uint32_t b) {  // b: the stored byte in bits 0-7
+    if constexpr (T == LQ_I8) return (float)(int)(int8_t)(uint8_t)b;
+    else if constexpr (T == LQ_U8) return (float)(int)(uint8_t)b;
+    else return (float)((int)(int8_t)(uint8_t)b + 128);  // LQ_U8S8
+}
+
+template <int OUT>
+__device__ __forceinline__ uint32_t byte_store(float t, float inv, float z, const Grid& g) {
+    if constexpr (OUT == LQ_I8) return (uint8_t)quant_store<CodeI8>(t, inv, z, g);
+    else if constexpr (OUT == LQ_U8) return (uint8_t)quant_store<CodeU8>(t, inv, z, g);
+    else return (uint8_t)quant_store<CodeU8S8>(t, inv, z, g);
+}
+
+template <int AT, int BT, int OUT, bool MUL>
+__global__ __launch_bounds__(kMergeBlock) void merge_bytes16_kernel(MergeArgs m, int64_t n16) {
+    const float sa = m.a_scale[0], za = m.a_zp ? m.a_zp[0] : 0.0f;
+    const float sb = m.b_scale[0], zb = m.b_zp ? m.b_zp[0] : 0.0f;
+    const float s = m.out_scale[0], inv = 1.0f / s, z = m.out_zp ? m.out_zp[0] : 0.0f;
+    const vu4* A = static_cast<const vu4*>(m.a);
+    const vu4* B = static_cast<const vu4*>(m.b);
+    vu4* Y = static_cast<vu4*>(m.out);
+    for (int64_t v = (int64_t)blockIdx.x * kMergeBlock + threadIdx.x; v < n16; v += (int64_t)gridDim.x * kMergeBlock) {
+        const vu4 xa = A[v], xb = B[v];
+        vu4 y;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+            uint32_t o = 0;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const float a = (byte_code<AT>(xa[w] >> (8 * e)) - za) * sa;
+                const float b = (byte_code<BT>(xb[w] >> (8 * e)) - zb) * sb;
+                float t = MUL ? a * b : a + b;
+                if (m.relu) t = (t <= 0.0f) ? 0.0f : t;
+                o |= byte_store<OUT>(t, inv, z, m.g) << (8 * e);
+            }
+            y[w] = o;
+        }
+        Y[v] = y;
+    }
+}
+
+static bool byte_code_type(int t) { return t == LQ_I8 || t == LQ_U8 || t == LQ_U8S8; }
+
 static bool merge_type_ok(int t) { return t == LQ_F32 || t == LQ_I8 || t == LQ_U8 || t == LQ_I16 || t == LQ_U8S8; }
 
 }  // namespace lq
@@ -140,6 +188,34 @@ int lq_qmerge(int op, const void* d_a, int a_type, const float* d_a_scale, const
                 binary ? d_b : nullptr, b_type, binary && b_type != LQ_F32 ? d_b_scale : nullptr, d_b_zero_point,
                 scalar, rows, cols, ld_out, d_out_scale, d_out_zero_point, make_grid(qmin, qmax),
                 (flags & LQ_EPI_RELU) != 0, d_out};
+    hipStream_t st0 = as_stream(stream);
+    const int64_t n = rows * cols;
+    if (binary && (ld_out == cols || rows == 1) && byte_code_type(a_type) && a_type == b_type &&
+        byte_code_type(out_type) && n % 16 == 0 &&
+        ((reinterpret_cast<uintptr_t>(d_a) | reinterpret_cast<uintptr_t>(d_b) | reinterpret_cast<uintptr_t>(d_out)) &
+         15) == 0) {
+        const int64_t n16 = n / 16;
+        int64_t blocks = (n16 + kMergeBlock - 1) / kMergeBlock;
+        if (blocks > 8192) blocks = 8192;
+        const dim3 g16((unsigned)blocks);
+#define LQ_MERGE16(AT, OT)                                                                                 \
+    do {                                                                                                   \
+        if (op == LQ_MERGE_ADD) hipLaunchKernelGGL((merge_bytes16_kernel<AT, AT, OT, false>), g16, dim3(kMergeBlock), 0, st0, m, n16); \
+        else hipLaunchKernelGGL((merge_bytes16_kernel<AT, AT, OT, true>), g16, dim3(kMergeBlock), 0, st0, m, n16);  \
+    } while (0)
+#define LQ_MERGE16_OUT(AT)                                   \
+    do {                                                     \
+        if (out_type == LQ_I8) LQ_MERGE16(AT, LQ_I8);        \
+        else if (out_type == LQ_U8) LQ_MERGE16(AT, LQ_U8);   \
+        else LQ_MERGE16(AT, LQ_U8S8);                        \
+    } while (0)
+        if (a_type == LQ_I8) LQ_MERGE16_OUT(LQ_I8);
+        else if (a_type == LQ_U8) LQ_MERGE16_OUT(LQ_U8);
+        else LQ_MERGE16_OUT(LQ_U8S8);
+#undef LQ_MERGE16_OUT
+#undef LQ_MERGE16
+        return launch_status("lq_qmerge");
+    }
     int64_t bx = (cols + 4 * kMergeBlock - 1) / (4 * kMergeBlock);
     if (bx > 4096) bx = 4096;
     const int64_t by = rows < 65535 ? rows : 65535;

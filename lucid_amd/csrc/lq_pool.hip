@@ -52,15 +52,33 @@ __device__ __forceinline__ void pool_window(const PoolArgs& a, int o, int S, int
     span = a.count_include_pad ? end - start : (hi > lo ? hi - lo : 0);
 }
 
+// (nc, oh, ow) of flat output index i: 32-bit divisions when the output count fits (a 64-bit
+// division is a long instruction sequence on this GPU, and three per output dominated the
+// pooling kernels).
+__device__ __forceinline__ void pool_coords(const PoolArgs& a, int64_t i, int64_t total, int64_t& nc, int& oh,
+                                            int& ow) {
+    if (total <= 0x7fffffff) {
+        const uint32_t u = (uint32_t)i, q = u / (uint32_t)a.OW;
+        ow = (int)(u - q * (uint32_t)a.OW);
+        const uint32_t r = q / (uint32_t)a.OH;
+        oh = (int)(q - r * (uint32_t)a.OH);
+        nc = r;
+    } else {
+        ow = (int)(i % a.OW);
+        const int64_t t = i / a.OW;
+        oh = (int)(t % a.OH);
+        nc = t / a.OH;
+    }
+}
+
 template <int T>
 __global__ __launch_bounds__(256) void max_pool_kernel(PoolArgs a) {
     using E = typename PoolElem<T>::type;
     const int64_t total = a.NC * a.OH * a.OW;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-        const int ow = (int)(i % a.OW);
-        const int64_t t = i / a.OW;
-        const int oh = (int)(t % a.OH);
-        const int64_t nc = t / a.OH;
+        int64_t nc;
+        int oh, ow;
+        pool_coords(a, i, total, nc, oh, ow);
         int h0, h1, w0, w1, sp;
         pool_window(a, oh, a.H, a.OH, a.KH, a.sh, a.ph, h0, h1, sp);
         pool_window(a, ow, a.W, a.OW, a.KW, a.sw, a.pw, w0, w1, sp);
@@ -99,10 +117,9 @@ __global__ __launch_bounds__(256) void avg_pool_kernel(PoolArgs a) {
     const float s = a.x_scale ? a.x_scale[0] : 1.0f, z = a.x_zp ? a.x_zp[0] : 0.0f;
     const int64_t total = a.NC * a.OH * a.OW;
     for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < total; i += (int64_t)gridDim.x * 256) {
-        const int ow = (int)(i % a.OW);
-        const int64_t t = i / a.OW;
-        const int oh = (int)(t % a.OH);
-        const int64_t nc = t / a.OH;
+        int64_t nc;
+        int oh, ow;
+        pool_coords(a, i, total, nc, oh, ow);
         int h0, h1, w0, w1, sph, spw;
         pool_window(a, oh, a.H, a.OH, a.KH, a.sh, a.ph, h0, h1, sph);
         pool_window(a, ow, a.W, a.OW, a.KW, a.sw, a.pw, w0, w1, spw);

@@ -48,14 +48,16 @@ def _want_codes(t, s, z, qmin, qmax):
 
 
 @pytest.mark.parametrize("op", ["add", "mul", "add_relu", "add_scalar", "mul_scalar"])
-@pytest.mark.parametrize("kinds", [("f32", "f32"), ("i8", "u8s8"), ("u8s8", "u8s8"), ("i8", "f32")])
+@pytest.mark.parametrize("kinds", [("f32", "f32"), ("i8", "u8s8"), ("u8s8", "u8s8"), ("i8", "f32"), ("i8", "i8")])
 @pytest.mark.parametrize("qdtype", ["quint8", "qint8"])
-def test_qfunctional_matches_oracle(gpu, op, kinds, qdtype):
+@pytest.mark.parametrize("shape", [(3, 5, 37), (2, 48, 7, 16)])
+def test_qfunctional_matches_oracle(gpu, op, kinds, qdtype, shape):
+    """(2, 48, 7, 16) has a multiple of 16 elements: two operands of one byte code type take
+    the 16-bytes-per-thread path; (3, 5, 37) the per-element one."""
     import lucid_amd.nn.quantized as nnq
 
     Q = gpu.quantization
-    rng = np.random.default_rng(len(op) * 7 + len(kinds[0]))
-    shape = (3, 5, 37)
+    rng = np.random.default_rng(len(op) * 7 + len(kinds[0]) + len(shape))
     x = (rng.standard_normal(shape) * 2).astype(np.float32)
     y = (rng.standard_normal(shape) * 2).astype(np.float32)
     xa, xv = _operand(gpu, x, kinds[0], 1)
