@@ -197,6 +197,145 @@ __global__ __launch_bounds__(256) void conv_pack_input_kernel(PackArgs a, PackGe
     }
 }
 
+// ---------------------------------------------------------------- tap-im2col form
+//
+// Inputs with 2..4 channels per group (images) waste most of a 16-channel padded position.
+// For them the KW taps of a kernel row and the channels are packed together: position
+// (n, hp, ow) of the packed input holds, per group, the 32 bytes
+//   xt[j = kw * Cg + c] = x[n][g Cg + c][hp - pt][ow sw + kw dw - pl]   (j < KW Cg; the rest fill)
+// and the convolution runs as a KH x 1 one over 32 channels at horizontal stride 1:
+// K = KH x 32 (the ResNet stem, 7x7 over 3 channels: 224 bytes = 2 stages instead of
+// 7 x 7 x 16 = 784 = 7).  Weight rows are [co][kh * 32 + kw * Cg + c].  The form depends only on
+// what the weight pack knows (channels per group and KW), so the pack and the call agree;
+// one channel per group (depthwise) keeps the plain form.
+__host__ __device__ constexpr bool conv_taps_form(int64_t Cg, int64_t KW) {
+    return Cg >= 2 && Cg <= 4 && KW >= 2 && Cg * KW <= 32;
+}
+constexpr int CV_TAPS_CP = 32;        // bytes per position and group in the tap-im2col form
+constexpr int CV_TAPS_OWB = 128;      // output columns per pack workgroup (two chunks each)
+constexpr int CV_TAPS_SPAN = 512;     // input bytes of one channel row staged per workgroup
+
+struct TapsArgs {
+    const int8_t* x;
+    int8_t* xp;
+    int N, C, H, W, G, Cg, Hp, OW, KW, sw, dw, pt, pl, mode;
+    int owb, span;  // output columns per workgroup, staged input bytes per channel
+    const float* a_zp;
+    int a_u8s8;
+};
+
+// One workgroup per (image n, CV_TAPS_ROWS consecutive padded rows, column block): per group,
+// the Cg input rows each padded row reads are staged in LDS (padding sources resolved), then
+// each thread writes 16-byte halves of 32-byte positions.  A thread always writes the same
+// half (the item stride is even), so its 16 byte offsets into a staged row are computed once.
+constexpr int CV_TAPS_ROWS = 4;
+
+__global__ __launch_bounds__(256) void conv_pack_taps_kernel(TapsArgs a) {
+    __shared__ int8_t rows[CV_TAPS_ROWS * 4 * CV_TAPS_SPAN];  // rows x Cg (<= 4) x span
+    const int hblocks = (a.Hp + CV_TAPS_ROWS - 1) / CV_TAPS_ROWS;
+    const int n = blockIdx.x / hblocks, hp0 = (blockIdx.x - n * hblocks) * CV_TAPS_ROWS;
+    const int ow0 = blockIdx.y * a.owb;
+    const int fill = (a.a_zp ? (int)a.a_zp[0] : 0) - (a.a_u8s8 ? 128 : 0);
+    const int col0 = ow0 * a.sw - a.pl;  // input column of staged byte 0
+    const int rowbytes = a.Cg * a.span;  // one padded row's staged channels
+    // byte b of this thread's half: staged offset c * span + kw * dw, or -1 (fill)
+    const int half = threadIdx.x & 1;
+    int off[16];
+    {
+        int kw = (half * 16) / a.Cg, c = half * 16 - kw * a.Cg;
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            off[b] = kw < a.KW ? c * a.span + kw * a.dw : -1;
+            if (++c == a.Cg) {
+                c = 0;
+                ++kw;
+            }
+        }
+    }
+    const int items = CV_TAPS_ROWS * a.owb * 2;
+    // staged bytes j = threadIdx.x + 256 jj (span <= 512): their source columns, and the
+    // source rows of the block's padded rows, resolved once
+    int wsrc[2], hsrc[CV_TAPS_ROWS];
+#pragma unroll
+    for (int jj = 0; jj < 2; ++jj) {
+        const int j = threadIdx.x + 256 * jj;
+        wsrc[jj] = j < a.span ? pad_index(col0 + j, a.W, a.mode) : -1;
+    }
+#pragma unroll
+    for (int r = 0; r < CV_TAPS_ROWS; ++r) hsrc[r] = hp0 + r < a.Hp ? pad_index(hp0 + r - a.pt, a.H, a.mode) : -1;
+    for (int g = 0; g < a.G; ++g) {
+        // every load of the stage first (one memory round trip), then the LDS stores
+        int8_t v[CV_TAPS_ROWS][4][2];
+#pragma unroll
+        for (int r = 0; r < CV_TAPS_ROWS; ++r)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    v[r][c][jj] = (int8_t)fill;
+                    if (c < a.Cg && hsrc[r] >= 0 && wsrc[jj] >= 0)
+                        v[r][c][jj] = a.x[(((int64_t)n * a.C + (int64_t)g * a.Cg + c) * a.H + hsrc[r]) * a.W + wsrc[jj]];
+                }
+#pragma unroll
+        for (int r = 0; r < CV_TAPS_ROWS; ++r)
+#pragma unroll
+            for (int c = 0; c < 4; ++c)
+#pragma unroll
+                for (int jj = 0; jj < 2; ++jj) {
+                    const int j = threadIdx.x + 256 * jj;
+                    if (c < a.Cg && j < a.span) rows[r * rowbytes + c * a.span + j] = v[r][c][jj];
+                }
+        __syncthreads();
+        for (int it = threadIdx.x; it < items; it += 256) {
+            const int pos = it >> 1;
+            const int r = pos / a.owb, col = pos - r * a.owb;
+            const int hp = hp0 + r, ow = ow0 + col;
+            if (hp >= a.Hp || ow >= a.OW) continue;
+            const int8_t* row = rows + r * rowbytes + col * a.sw;
+            uint32_t word[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t v = 0;
+#pragma unroll
+                for (int b = 0; b < 4; ++b) {
+                    const int o = off[4 * q + b];
+                    v |= (uint32_t)(uint8_t)(o >= 0 ? (int)row[o] : fill) << (8 * b);
+                }
+                word[q] = v;
+            }
+            const int64_t dst = ((((int64_t)n * a.Hp + hp) * a.OW + ow) * a.G + g) * CV_TAPS_CP + half * 16;
+            *reinterpret_cast<vu4*>(a.xp + dst) = vu4{word[0], word[1], word[2], word[3]};
+        }
+        __syncthreads();
+    }
+}
+
+// Weight rows of the tap-im2col form: one thread per 16-byte chunk of w_p[co][kh * 32 + j].
+__global__ __launch_bounds__(256) void conv_pack_weights_taps_kernel(const int8_t* __restrict__ w, int Cout, int Cg,
+                                                                     int KH, int KW, int ldw, int8_t* __restrict__ wp) {
+    const int chunks = ldw / 16;
+    const int64_t total = (int64_t)Cout * chunks;
+    const int64_t id = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= total) return;
+    const int64_t co = id / chunks;
+    const int k0 = (int)(id - co * chunks) * 16;
+    uint32_t word[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        uint32_t v = 0;
+#pragma unroll
+        for (int b = 0; b < 4; ++b) {
+            const int k = k0 + q * 4 + b;
+            const int kh = k / CV_TAPS_CP, j = k - kh * CV_TAPS_CP;
+            const int kw = j / Cg, c = j - kw * Cg;
+            const int8_t x = (kh < KH && kw < KW) ? w[((co * Cg + c) * KH + kh) * KW + kw] : (int8_t)0;
+            v |= (uint32_t)(uint8_t)x << (8 * b);
+        }
+        word[q] = v;
+    }
+    reinterpret_cast<vu4*>(wp)[id] = vu4{word[0], word[1], word[2], word[3]};
+}
+
 // One thread per 16-byte chunk of a packed weight row w_p[co][k], k = (kh * KW + kw) * Cp + c,
 // rows ldw bytes long (K rounded up to whole 128-byte stages, the tail zero).
 __global__ __launch_bounds__(256) void conv_pack_weights_kernel(const int8_t* __restrict__ w, int Cout, int Cg,
@@ -861,6 +1000,7 @@ int64_t conv_ldw(int64_t K) { return (K + 127) / 128 * 128; }
 // Launch plan of lq_conv2d_i8, shared by the call and its workspace query.
 struct ConvPlan {
     bool dma, big;
+    bool taps;      // tap-im2col form: packed input [n][hp][ow][g][32], a KH x 1 convolution
     int64_t Cp, ldw, gx, gy;
     int splits;
     size_t pack_bytes;  // padded NHWC input (rounded up to 256 bytes)
@@ -871,9 +1011,11 @@ ConvPlan conv_plan(int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout, int
                    int pl, int pr, int64_t OH, int64_t OW, int64_t groups) {
     ConvPlan p{};
     const int64_t Cg = C / groups, Cout_g = Cout / groups;
-    p.Cp = (Cg + 15) / 16 * 16;
-    p.pack_bytes = (size_t)((N * (H + pt + pb) * (W + pl + pr) * groups * p.Cp + 255) / 256 * 256);
-    const int64_t K = KH * KW * p.Cp;
+    p.taps = conv_taps_form(Cg, KW);
+    p.Cp = p.taps ? CV_TAPS_CP : (Cg + 15) / 16 * 16;
+    const int64_t Wpk = p.taps ? OW : W + pl + pr;  // packed input width
+    p.pack_bytes = (size_t)((N * (H + pt + pb) * Wpk * groups * p.Cp + 255) / 256 * 256);
+    const int64_t K = KH * (p.taps ? 1 : KW) * p.Cp;
     p.ldw = conv_ldw(K);
     const int64_t ntaps = (p.ldw + p.Cp - 1) / p.Cp;
     const bool pow2 = p.Cp <= 128 && (p.Cp & (p.Cp - 1)) == 0;
@@ -909,6 +1051,7 @@ extern "C" {
 
 size_t lq_conv2d_weight_pack_size(int64_t Cout, int64_t Cin_g, int64_t KH, int64_t KW) {
     if (Cout < 0 || Cin_g < 1 || KH < 1 || KW < 1) return 0;
+    if (conv_taps_form(Cin_g, KW)) return (size_t)(Cout * conv_ldw(KH * CV_TAPS_CP));
     const int64_t Cp = (Cin_g + 15) / 16 * 16;
     return (size_t)(Cout * conv_ldw(KH * KW * Cp));
 }
@@ -921,10 +1064,17 @@ int lq_conv2d_pack_weights_i8(const int8_t* d_w, int64_t Cout, int64_t Cin_g, in
     LQ_REQUIRE(d_w && d_w_packed, "lq_conv2d_pack_weights_i8: NULL pointer");
     const int Cp = (int)((Cin_g + 15) / 16 * 16);
     hipStream_t st = as_stream(stream);
-    const int64_t ldw = conv_ldw(KH * KW * Cp);
-    const int64_t chunks = Cout * (ldw / 16);
-    hipLaunchKernelGGL(conv_pack_weights_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, st, d_w,
-                       (int)Cout, (int)Cin_g, (int)KH, (int)KW, Cp, (int)ldw, d_w_packed);
+    if (conv_taps_form(Cin_g, KW)) {
+        const int64_t ldw = conv_ldw(KH * CV_TAPS_CP);
+        const int64_t chunks = Cout * (ldw / 16);
+        hipLaunchKernelGGL(conv_pack_weights_taps_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, st,
+                           d_w, (int)Cout, (int)Cin_g, (int)KH, (int)KW, (int)ldw, d_w_packed);
+    } else {
+        const int64_t ldw = conv_ldw(KH * KW * Cp);
+        const int64_t chunks = Cout * (ldw / 16);
+        hipLaunchKernelGGL(conv_pack_weights_kernel, dim3((unsigned)((chunks + 255) / 256)), dim3(256), 0, st, d_w,
+                           (int)Cout, (int)Cin_g, (int)KH, (int)KW, Cp, (int)ldw, d_w_packed);
+    }
     if (d_w_sums)
         hipLaunchKernelGGL(conv_weight_sums_kernel, dim3((unsigned)((Cout + 3) / 4)), dim3(256), 0, st, d_w, (int)Cout,
                            Cin_g * KH * KW, d_w_sums);
@@ -966,10 +1116,15 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
                    "lq_conv2d_i8: reflect / replicate / circular padding must be smaller than the input");
     if (N == 0) return LQ_OK;
     const int64_t Cg = C / groups, Cout_g = Cout / groups;
-    const int64_t Cp = (Cg + 15) / 16 * 16;
-    const int64_t Hp = H + pad_top + pad_bottom, Wp = W + pad_left + pad_right;
+    // the packed input's geometry: padded NHWC, or the tap-im2col form (a KH x 1 convolution
+    // at horizontal stride 1 over 32 bytes per position, the packing applied the columns)
+    const bool taps = conv_taps_form(Cg, KW);
+    const int64_t Cp = taps ? CV_TAPS_CP : (Cg + 15) / 16 * 16;
+    const int64_t Hp = H + pad_top + pad_bottom, Wp = taps ? OW : W + pad_left + pad_right;
+    const int64_t KWe = taps ? 1 : KW;
+    const int swe = taps ? 1 : stride_w, dwe = taps ? 1 : dilation_w;
     const int64_t P = N * OH * OW;
-    const int64_t K = KH * KW * Cp;
+    const int64_t K = KH * KWe * Cp;
     LQ_REQUIRE(N * C * H * W < CV_MAX && N * Hp * Wp * groups * Cp < CV_MAX && P < CV_MAX && N * Cout * OH * OW < CV_MAX,
                "lq_conv2d_i8: tensors above 2^31 elements are not supported");
     LQ_REQUIRE(d_x && d_w_packed && d_w_scale && d_y, "lq_conv2d_i8: NULL pointer");
@@ -999,17 +1154,36 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
     pg.border_cells = pg.all_cells ? (int)(Hp * Wp) : (int)((pad_top + pad_bottom) * Wp + H * (pad_left + pad_right));
     const int bblocks = (int)((pg.border_cells * (Cp / 16) + 255) / 256);
     const dim3 pgrid((unsigned)(pg.tiles + bblocks), (unsigned)(N * groups));
-    if ((H * W) % 4 == 0 && (reinterpret_cast<uintptr_t>(d_x) & 3) == 0)
+    if (taps) {
+        TapsArgs ta{};
+        ta.x = d_x;
+        ta.xp = pa.xp;
+        ta.N = (int)N; ta.C = (int)C; ta.H = (int)H; ta.W = (int)W; ta.G = (int)groups; ta.Cg = (int)Cg;
+        ta.Hp = (int)Hp; ta.OW = (int)OW; ta.KW = (int)KW; ta.sw = stride_w; ta.dw = dilation_w;
+        ta.pt = pad_top; ta.pl = pad_left; ta.mode = padding_mode;
+        ta.a_zp = d_a_zero_point; ta.a_u8s8 = pa.a_u8s8;
+        // output columns per workgroup: as many of CV_TAPS_OWB as the staged rows hold
+        const int64_t reach = (KW - 1) * (int64_t)dilation_w + 1;
+        LQ_REQUIRE(reach <= CV_TAPS_SPAN, "lq_conv2d_i8: dilated kernel row wider than the tap staging buffer");
+        ta.owb = (int)std::min<int64_t>(CV_TAPS_OWB, (CV_TAPS_SPAN - reach) / stride_w + 1);
+        ta.span = (int)((ta.owb - 1) * (int64_t)stride_w + reach);
+        const int64_t hblocks = (Hp + CV_TAPS_ROWS - 1) / CV_TAPS_ROWS;
+        LQ_REQUIRE(N * hblocks <= 2147483647LL && (OW + ta.owb - 1) / ta.owb <= 65535,
+                   "lq_conv2d_i8: too many input rows or output columns for the tap packing");
+        const dim3 tgrid((unsigned)(N * hblocks), (unsigned)((OW + ta.owb - 1) / ta.owb));
+        hipLaunchKernelGGL(conv_pack_taps_kernel, tgrid, dim3(256), 0, st, ta);
+    } else if ((H * W) % 4 == 0 && (reinterpret_cast<uintptr_t>(d_x) & 3) == 0) {
         hipLaunchKernelGGL(conv_pack_input_kernel<true>, pgrid, dim3(256), 0, st, pa, pg);
-    else
+    } else {
         hipLaunchKernelGGL(conv_pack_input_kernel<false>, pgrid, dim3(256), 0, st, pa, pg);
+    }
 
     ConvArgs a{};
     a.xp = pa.xp;
     a.wp = d_w_packed;
     a.y = d_y;
     a.N = (int)N; a.Hp = (int)Hp; a.Wp = (int)Wp; a.G = (int)groups; a.Cp = (int)Cp; a.Cout_g = (int)Cout_g;
-    a.KH = (int)KH; a.KW = (int)KW; a.sh = stride_h; a.sw = stride_w; a.dh = dilation_h; a.dw = dilation_w;
+    a.KH = (int)KH; a.KW = (int)KWe; a.sh = stride_h; a.sw = swe; a.dh = dilation_h; a.dw = dwe;
     a.OH = (int)OH; a.OW = (int)OW; a.K = (int)K; a.P = (int)P; a.ldw = (int)conv_ldw(K);
     a.a_scale = d_a_scale;
     a.a_zp = d_a_zero_point;
@@ -1034,12 +1208,12 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
         d.xp_bytes = (uint32_t)(N * Hp * Wp * groups * Cp);
         d.Hp = (int)Hp; d.Wp = (int)Wp; d.G = (int)groups; d.Cp = (int)Cp;
         d.cp_shift = pow2 ? __builtin_ctz((unsigned)Cp) : -1;
-        d.Cout_g = (int)Cout_g; d.KH = (int)KH; d.KW = (int)KW; d.sh = stride_h; d.sw = stride_w;
-        d.dh = dilation_h; d.dw = dilation_w; d.OH = (int)OH; d.OW = (int)OW; d.P = (int)P;
+        d.Cout_g = (int)Cout_g; d.KH = (int)KH; d.KW = (int)KWe; d.sh = stride_h; d.sw = swe;
+        d.dh = dilation_h; d.dw = dwe; d.OH = (int)OH; d.OW = (int)OW; d.P = (int)P;
         d.nk = (int)(ldw / 128); d.ldw = (int)ldw;
-        d.kw_magic = (int)((65536 + KW - 1) / KW);
+        d.kw_magic = (int)((65536 + KWe - 1) / KWe);
         d.kh_stride = (int)(dilation_h * Wp * groups * Cp);
-        d.kw_stride = (int)(dilation_w * groups * Cp);
+        d.kw_stride = (int)(dwe * groups * Cp);
         d.a_scale = d_a_scale; d.a_zp = d_a_zero_point; d.a_u8s8 = pa.a_u8s8;
         d.w_scale = d_w_scale; d.w_sums = d_w_sums; d.bias = d_bias;
         d.out_scale = d_out_scale; d.out_zp = d_out_zero_point;
@@ -1072,7 +1246,10 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
             default: LQ_CONV_DMA(LQ_OUT_QU8S8)
         }
 #undef LQ_CONV_DMA
-        note_path(big ? "conv dma 256x64" : plan.splits > 1 ? "conv dma 128x64 split-k" : "conv dma 128x64");
+        if (taps)
+            note_path(big ? "conv taps dma 256x64" : plan.splits > 1 ? "conv taps dma 128x64 split-k" : "conv taps dma 128x64");
+        else
+            note_path(big ? "conv dma 256x64" : plan.splits > 1 ? "conv dma 128x64 split-k" : "conv dma 128x64");
         return launch_status("lq_conv2d_i8");
     }
     const dim3 grid((unsigned)((P + CV_BM - 1) / CV_BM), (unsigned)((Cout_g + CV_BN - 1) / CV_BN), (unsigned)groups);
@@ -1086,7 +1263,7 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
         case LQ_OUT_Q16: hipLaunchKernelGGL(conv_i8_kernel<LQ_OUT_Q16>, grid, dim3(CV_THREADS), 0, st, a); break;
         default: hipLaunchKernelGGL(conv_i8_kernel<LQ_OUT_QU8S8>, grid, dim3(CV_THREADS), 0, st, a); break;
     }
-    note_path("conv staged 128x64");
+    note_path(taps ? "conv taps staged 128x64" : "conv staged 128x64");
     return launch_status("lq_conv2d_i8");
 }
 

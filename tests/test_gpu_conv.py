@@ -114,6 +114,13 @@ CASES = [
     (2, 256, 7, 7, 256, 3, 3, (1, 1), (1, 1, 1, 1), (1, 1), 1, 0),      # split K over 4
     (1, 512, 7, 7, 512, 3, 3, (1, 1), (1, 1, 1, 1), (1, 1), 1, 0),      # ResNet layer4: split K over 9
     (2, 256, 6, 6, 128, 3, 3, (1, 1), (1, 1, 1, 1), (1, 1), 2, 0),      # split K with groups
+    # tap-im2col form (2..4 channels per group, KW x Cg <= 32)
+    (2, 4, 17, 19, 24, 3, 5, (1, 2), (1, 1, 2, 2), (1, 1), 1, 0),       # Cg 4, KW 5
+    (1, 2, 12, 30, 16, 5, 9, (2, 3), (2, 2, 4, 4), (1, 2), 1, 1),       # Cg 2, reflect, dilated row
+    (1, 6, 10, 10, 8, 3, 3, (1, 1), (1, 1, 1, 1), (1, 1), 2, 2),        # Cg 3, two groups, replicate
+    (1, 3, 9, 9, 5, 3, 7, (1, 1), (1, 1, 3, 3), (1, 1), 1, 3),          # circular, 21 taps x channels
+    (1, 3, 5, 300, 8, 3, 3, (1, 2), (1, 1, 1, 1), (1, 1), 1, 0),        # 150 output columns: two blocks
+    (3, 3, 1, 40, 12, 1, 5, (1, 1), (0, 0, 2, 2), (1, 1), 1, 0),        # a 1-D conv (height 1)
 ]
 
 
@@ -155,6 +162,19 @@ def test_conv_weight_pack_layout(gpu):
     rows = wp.numpy().reshape(10, 256)  # K = 3 * 2 * 32 = 192, rows padded to 256 bytes
     np.testing.assert_array_equal(rows[:, :192].reshape(10, 3, 2, Cp), want)
     assert not rows[:, 192:].any()
+    np.testing.assert_array_equal(sums.numpy(), w.astype(np.int64).reshape(10, -1).sum(1))
+
+
+def test_conv_weight_pack_taps_layout(gpu):
+    """2..4 channels per group: rows [co][kh * 32 + kw * Cg + c], 32 bytes per kernel row."""
+    rng = np.random.default_rng(5)
+    w = _codes(rng, (10, 3, 7, 7))
+    wp, sums = pack_conv_weights(gpu, w)
+    rows = wp.numpy().reshape(10, 256)  # K = 7 * 32 = 224, rows padded to 256 bytes
+    want = np.zeros((10, 7, 32), np.int8)
+    want[:, :, :21] = w.transpose(0, 2, 3, 1).reshape(10, 7, 21)
+    np.testing.assert_array_equal(rows[:, :224].reshape(10, 7, 32), want)
+    assert not rows[:, 224:].any()
     np.testing.assert_array_equal(sums.numpy(), w.astype(np.int64).reshape(10, -1).sum(1))
 
 

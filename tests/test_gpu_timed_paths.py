@@ -125,7 +125,7 @@ def test_gemm_sweep_shapes_exact(gpu, M, N, K, path):
 # ------------------------------------------------------------------- conv 256x64
 
 RESNET18_B32 = (  # the bench's layers at batch 32: (name, Cin, Cout, H, k, stride, pad, kernel path)
-    ("conv1 7x7/2", 3, 64, 224, 7, 2, 3, "conv dma 256x64"),
+    ("conv1 7x7/2", 3, 64, 224, 7, 2, 3, "conv taps dma 256x64"),
     ("layer1 3x3", 64, 64, 56, 3, 1, 1, "conv dma 256x64"),
     ("layer2 3x3/2", 64, 128, 56, 3, 2, 1, "conv dma 128x64"),
     ("layer2 3x3", 128, 128, 28, 3, 1, 1, "conv dma 128x64"),
