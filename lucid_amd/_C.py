@@ -196,9 +196,18 @@ def check(rc: int, what: str = "") -> None:
         raise LucidError(f"{what}: {msg}" if what else msg)
 
 
+_entry_points: dict = {}
+
+
 def call(name: str, *args) -> None:
-    """Call an int-status entry point and raise on failure."""
-    check(getattr(lib(), name)(*args), name)
+    """Call an int-status entry point and raise on failure (the ctypes function object is
+    looked up once per name)."""
+    f = _entry_points.get(name)
+    if f is None:
+        f = _entry_points[name] = getattr(lib(), name)
+    rc = f(*args)
+    if rc != OK:
+        check(rc, name)
 
 
 def last_path() -> str:

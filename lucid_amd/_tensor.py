@@ -19,6 +19,7 @@ modules (lucid/nn/quantized/linear.py:206-215).
 from __future__ import annotations
 
 import ctypes
+import math
 from dataclasses import dataclass
 from typing import Any, Sequence
 
@@ -154,7 +155,7 @@ class Tensor:
         return len(self._shape)
 
     def numel(self) -> int:
-        return int(np.prod(self._shape, dtype=np.int64))
+        return math.prod(self._shape)
 
     @property
     def size(self) -> int:

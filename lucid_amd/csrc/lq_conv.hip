@@ -599,6 +599,386 @@ struct ConvDmaArgs {
     int32_t* part;
 };
 
+// Epilogue of one wave's tile of 64 pixels x 16 FN channels: acc[i][j][r] is pixel
+// pb + 4 j + r of this lane's run (pb = the wave's first pixel + 16 (lane / 16)), channel
+// co_w + 16 i + lane % 16 of group g.  A lane owns 16 consecutive pixels of each of its FN
+// channels, stored as 16-byte NCHW runs when the run lies in one image and is aligned.
+template <int FN, int KIND>
+__device__ __forceinline__ void conv_epilogue(const ConvDmaArgs& a, v4i (&acc)[FN][4], const int pb, const int co_w,
+                                              const int g, const int lane, const float* csb, const float* cbias,
+                                              const int32_t* cws, const float sa, const EpiParams& ep) {
+    constexpr bool INT_CODES = KIND == LQ_OUT_Q8 || KIND == LQ_OUT_QU8 || KIND == LQ_OUT_Q16 || KIND == LQ_OUT_QU8S8;
+    const int rho = lane & 15;
+    const int OHW = a.OH * a.OW;
+    CodeClamp cc{};
+    if (INT_CODES) cc = code_clamp<KIND>(a.qmin, a.qmax);
+    const int Cout = a.G * a.Cout_g;
+    const int nimg = min(pb, a.P - 1) / OHW;
+    const int pix0 = pb - nimg * OHW;
+    constexpr int OB = OutTraits<KIND>::bytes;
+    const bool vec = (OHW % 16 == 0) && (reinterpret_cast<uintptr_t>(a.y) % 16 == 0) && (pb + 15 < a.P);
+    // Stores of one channel's 16 consecutive pixels (out[] holds the output type's bits).
+    auto store_col = [&](const int co, const uint32_t* out) __attribute__((always_inline)) {
+        if (vec) {
+            const int64_t base = ((int64_t)nimg * Cout + co) * OHW + pix0;
+            if (OB == 1) {
+                v4i w;
+#pragma unroll
+                for (int d = 0; d < 4; ++d) w[d] = (int)pack_low_bytes(out + 4 * d);
+                *reinterpret_cast<v4i*>(reinterpret_cast<uint8_t*>(a.y) + base) = w;
+            } else if (OB == 2) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h) {
+                    v4i w;
+#pragma unroll
+                    for (int d = 0; d < 4; ++d)
+                        w[d] = (int)((out[8 * h + 2 * d] & 0xffffu) | (out[8 * h + 2 * d + 1] << 16));
+                    *reinterpret_cast<v4i*>(reinterpret_cast<uint16_t*>(a.y) + base + 8 * h) = w;
+                }
+            } else {
+#pragma unroll
+                for (int h = 0; h < 4; ++h)
+                    *reinterpret_cast<v4i*>(reinterpret_cast<uint32_t*>(a.y) + base + 4 * h) =
+                        v4i{(int)out[4 * h], (int)out[4 * h + 1], (int)out[4 * h + 2], (int)out[4 * h + 3]};
+            }
+        } else {
+            // 16 consecutive pixels from (image nimg, pixel pix0): at most one image boundary
+            // when OHW >= 16 (else the division per pixel)
+            const int64_t base = ((int64_t)nimg * Cout + co) * OHW + pix0;
+            const int64_t next = ((int64_t)(nimg + 1) * Cout + co) * OHW + pix0 - OHW;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const int p = pb + q;
+                if (p >= a.P) break;
+                int64_t idx;
+                if (OHW >= 16) {
+                    idx = pix0 + q < OHW ? base + q : next + q;
+                } else {
+                    const int nq = p / OHW, pq = p - nq * OHW;
+                    idx = ((int64_t)nq * Cout + co) * OHW + pq;
+                }
+                store_elem<KIND>(a.y, idx, out[q]);
+            }
+        }
+    };
+
+    // Integer codes, fast form (as in the GEMM epilogue): with the output scale's reciprocal
+    // finite and positive, the zero point integral and small, and every scale and bias of this
+    // wave finite and small enough that y stays finite, clamp(rne(y * inv) + z, lo, hi) equals
+    // zi + med3(rne(y * inv), lo - zi, hi - zi), the rounding and clamp on rne_bits against
+    // bounds shifted by RNE_MAGIC_BITS (|zi| < 2^21), and ReLU folds into the lower bound.
+    if constexpr (INT_CODES) {
+        const float zf = ep.out_z;
+        bool ok = ep.out_inv > 0.0f && ep.out_inv < 3.0e38f && zf == __builtin_rintf(zf) &&
+                  __builtin_fabsf(zf) < 2097152.0f && __builtin_isfinite(sa);
+        float bmax = 0.0f;
+#pragma unroll
+        for (int i = 0; i < FN; ++i) {
+            bmax = __builtin_fmaxf(bmax, __builtin_fabsf(csb[i]));
+            ok = ok && __builtin_isfinite(csb[i]) && __builtin_isfinite(cbias[i]);
+        }
+        const float amax = __builtin_fabsf(sa);
+        ok = ok && amax < 1.0e14f && bmax < 1.0e14f && amax * bmax < 1.0e28f;
+        if (__all(ok)) {
+            const int zi = (int)zf;
+            int L = cc.lo - zi, H = cc.hi - zi;
+            if (a.relu) L = max(L, 0);
+            L = min(L, H);  // med3(x, L, H) = min(max(x, L), H) needs L <= H
+            const int Lm = L + RNE_MAGIC_BITS, Hm = H + RNE_MAGIC_BITS;
+            const int shift = zi - (KIND == LQ_OUT_QU8S8 ? 128 : 0);
+            auto cols = [&](auto bias_c, auto za_c, auto shift_c) __attribute__((always_inline)) {
+                constexpr bool BIAS = decltype(bias_c)::value, ZA = decltype(za_c)::value;
+                constexpr bool SHIFT = decltype(shift_c)::value;
+                static_for<FN>([&](auto i_c) __attribute__((always_inline)) {
+                    constexpr int i = decltype(i_c)::value;
+                    const int col = co_w + 16 * i + rho;
+                    if (col >= a.Cout_g) return;
+                    const float sc = sa * csb[i];
+                    const uint32_t zsum = (uint32_t)ep.za * (uint32_t)cws[i];
+                    uint32_t out[16];
+#pragma unroll
+                    for (int q = 0; q < 16; ++q) {
+                        int32_t accq = acc[i][q >> 2][q & 3];
+                        if (ZA) accq = (int32_t)((uint32_t)accq - zsum);
+                        float y = (float)accq * sc;
+                        if (BIAS) y = y + cbias[i];
+                        int32_t c = med3_i32(rne_bits(y * ep.out_inv), Lm, Hm);
+                        if (SHIFT) c += shift;
+                        out[q] = (uint32_t)c;  // low byte / halfword: the code
+                    }
+                    store_col(g * a.Cout_g + col, out);
+                });
+            };
+            auto cols_za = [&](auto bias_c) __attribute__((always_inline)) {
+                if (ep.has_za) {
+                    if (shift != 0) cols(bias_c, std::true_type{}, std::true_type{});
+                    else cols(bias_c, std::true_type{}, std::false_type{});
+                } else {
+                    if (shift != 0) cols(bias_c, std::false_type{}, std::true_type{});
+                    else cols(bias_c, std::false_type{}, std::false_type{});
+                }
+            };
+            if (a.bias) cols_za(std::true_type{});
+            else cols_za(std::false_type{});
+            return;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < FN; ++i) {
+        const int col = co_w + 16 * i + rho;
+        if (col >= a.Cout_g) continue;
+        const int co = g * a.Cout_g + col;
+        const float sb = csb[i];
+        const float bias = cbias[i];
+        const int32_t zsum = ep.has_za ? (int32_t)((uint32_t)ep.za * (uint32_t)cws[i]) : 0;
+        uint32_t out[16];
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+            const int32_t acc_c = (int32_t)((uint32_t)acc[i][q >> 2][q & 3] - (uint32_t)zsum);
+            if (INT_CODES) {
+                const float s = sa * sb;
+                float y = (float)acc_c * s;
+                if (a.bias) y = y + bias;
+                if (a.relu) y = (y <= 0.0f) ? 0.0f : y;
+                out[q] = (uint32_t)requant_int<KIND>(y, ep, cc);
+                if (KIND == LQ_OUT_QU8S8) out[q] ^= 0x80u;
+            } else {
+                out[q] = epi_one<KIND>(acc_c, sa, sb, a.bias ? &bias : nullptr, a.relu != 0, ep);
+            }
+        }
+        store_col(co, out);
+    }
+}
+
+// ---------------------------------------------------------------- halo-staged direct conv
+//
+// Stride-1, zeros-padded, undilated, ungrouped convolutions with C and Cout multiples of 64
+// (the ResNet 3x3 layers) skip the padded NHWC copy.  A workgroup of four waves owns 256
+// consecutive output pixels (flattened n, oh, ow) x 64 output channels.  For each block of 64
+// input channels it stages in LDS
+//   * the halo: every padded input row its pixels read -- padded rows of consecutive images
+//     stack, row R = n * Hp + hp, and the tile needs rows R0 .. R0 + HR - 1 -- at all Wp padded
+//     columns, 64 channels per position (64 bytes; 16-byte chunk c at slot c ^ ((pos >> 4) & 3),
+//     which spreads the four 4-pixel runs of an A fragment over distinct banks), read from the
+//     NCHW codes as dwords (4 columns of one channel) and transposed 4 x 4 in registers
+//     (v_perm); padding positions and rows past the last image hold the activation zero point;
+//   * the block's weights for the 64 output channels, [tap][co][64 bytes] (chunk slot
+//     c ^ ((co >> 2) & 3)), by LDS-DMA from the packed rows;
+// then runs every tap from LDS: tap (kh, kw) of pixel (n, oh, ow) is halo position
+// (n * Hp + oh + kh - R0) * Wp + ow + kw.  Each staged input byte serves all KH * KW taps and
+// no padded copy of the activation goes through HBM.  Pixels are the MFMA row operand in the
+// permuted order of the DMA kernel (a lane ends with 16 consecutive pixels of each of its
+// channels), so the epilogue is the same.
+struct HaloArgs {
+    ConvDmaArgs e;      // output, geometry (P, OH, OW, Cout_g, G = 1), epilogue operands
+    const int8_t* x;    // NCHW activation codes
+    int N, C, H, W, Hp, Wp, pt, pl, KH, KW, nc;  // nc = C / 64 input channel blocks
+    int halo_bytes;     // LDS bytes of the largest tile's halo (a multiple of 1024)
+};
+
+__device__ __forceinline__ int halo_slot(int pos, int chunk) { return chunk ^ ((pos >> 4) & 3); }
+
+template <int KIND>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void conv_i8_halo_kernel(HaloArgs h) {
+    const ConvDmaArgs& a = h.e;
+    extern __shared__ __attribute__((aligned(1024))) int8_t halo_lds[];
+    int8_t* hal = halo_lds;
+    const int8_t* wl = halo_lds + h.halo_bytes;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int p0 = blockIdx.x * 256, co0 = blockIdx.y * 64;
+    const int OHW = a.OH * a.OW, T = h.KH * h.KW;
+    // padded rows of this tile (stride 1: output row oh reads padded rows oh .. oh + KH - 1)
+    const int plast = min(p0 + 255, a.P - 1);
+    const int n0 = p0 / OHW, oh0 = (p0 - n0 * OHW) / a.OW;
+    const int n1 = plast / OHW, oh1 = (plast - n1 * OHW) / a.OW;
+    const int R0 = n0 * h.Hp + oh0;
+    const int HR = n1 * h.Hp + oh1 + h.KH - R0;
+
+    // epilogue operands (the oldest loads: the staging waits cover them)
+    const int rho = lane & 15, c0 = lane >> 4;
+    float csb[4], cbias[4];
+    int32_t cws[4];
+    EpiParams ep;
+    ep.za = (a.a_zp ? (int)a.a_zp[0] : 0) - (a.a_u8s8 ? 128 : 0);
+    ep.has_za = a.a_zp != nullptr || a.a_u8s8;
+    ep.out_s = a.out_scale ? a.out_scale[0] : 1.0f;
+    ep.out_inv = 1.0f / ep.out_s;
+    ep.out_z = a.out_zp ? a.out_zp[0] : 0.0f;
+    ep.g = make_grid(a.qmin, a.qmax);
+    const float sa = a.a_scale ? a.a_scale[0] : 1.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int co = min(co0 + 16 * i + rho, a.Cout_g - 1);
+        csb[i] = a.w_scale[co];
+        cbias[i] = a.bias ? a.bias[co] : 0.0f;
+        cws[i] = ep.has_za ? a.w_sums[co] : 0;
+    }
+    const uint32_t fill8 = (uint32_t)(uint8_t)(int8_t)ep.za;
+    const uint32_t fill = fill8 * 0x01010101u;
+
+    // halo position of tap (0, 0) for the four pixels of this lane's A fragments
+    int basepos[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int q = min(p0 + wave * 64 + (rho >> 2) * 16 + 4 * j + (rho & 3), a.P - 1);
+        const int n = q / OHW, r = q - n * OHW;
+        const int oh = r / a.OW, ow = r - oh * a.OW;
+        basepos[j] = (n * h.Hp + oh - R0) * h.Wp + ow;
+    }
+
+    const v4i rw = buffer_rsrc(a.wp, (uint32_t)((int64_t)a.Cout_g * a.ldw));
+    const uint32_t wl_base = (uint32_t)reinterpret_cast<uintptr_t>(wl);
+    const int side = h.Wp - h.W;                 // padding columns per row
+    // this thread's staging pair and first row (the same for every channel block)
+    const int Wq = h.W >> 2;                     // column quads per row
+    const int pairs = 16 * Wq, groups = max(1, 256 / pairs);
+    const int pair = tid % pairs, r_t = tid / pairs;
+    const int cq_t = pair / Wq, iq_t = pair - cq_t * Wq;
+    int n_t, hp_t;
+    {
+        const int R = R0 + r_t;
+        n_t = R / h.Hp;
+        hp_t = R - n_t * h.Hp;
+    }
+    v4i acc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[i][j] = v4i{0, 0, 0, 0};
+
+    for (int cb = 0; cb < h.nc; ++cb) {
+        if (cb > 0) block_barrier();  // every wave is done reading the previous block
+        // weights of this channel block: row (tap, co) of 64 bytes, 16 rows per copy
+        for (int i = wave; i < T * 4; i += 4) {
+            const int row = i * 16 + (lane >> 2);
+            const int tap = row >> 6, co = row & 63;
+            const int chunk = (lane & 3) ^ ((co >> 2) & 3);
+            const uint32_t off = (uint32_t)((co0 + co) * a.ldw + tap * h.C + cb * 64 + chunk * 16);
+            lds_dma16(rw, off, 0, wl_base + (uint32_t)i * 1024u);
+        }
+        // halo interior: thread t owns the pair (channel quad cq, column quad iq) of index
+        // t % pairs (iq fastest, so a wave's dword loads run along channel rows) and walks the
+        // rows r = t / pairs, + groups, ...; each row's image and input row advance by
+        // increments.  Rows outside an image load a clamped in-range address and take the
+        // fill code by a select (no branches).  ROWS rows are in flight per step.
+        if (tid < pairs * groups) {
+            constexpr int ROWS = 4;
+            const int8_t* xpair = h.x + ((int64_t)cb * 64 + 4 * cq_t) * h.H * h.W + 4 * iq_t;
+            int n = n_t, hp = hp_t;  // image and padded row of row r_t
+            for (int r0 = r_t; r0 < HR; r0 += ROWS * groups) {
+                uint32_t d[ROWS][4];
+                int rr[ROWS];
+#pragma unroll
+                for (int b = 0; b < ROWS; ++b) {
+                    rr[b] = r0 + b * groups;
+                    const int ih = hp - h.pt;
+                    const bool ok = rr[b] < HR && n < h.N && ih >= 0 && ih < h.H;
+                    const int nc = min(n, h.N - 1), ic = min(max(ih, 0), h.H - 1);
+                    const int8_t* src = xpair + ((int64_t)nc * h.C * h.H + ic) * h.W;
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const uint32_t v = *reinterpret_cast<const uint32_t*>(src + (int64_t)t * h.H * h.W);
+                        d[b][t] = ok ? v : fill;
+                    }
+                    hp += groups;
+                    while (hp >= h.Hp) hp -= h.Hp, ++n;
+                }
+#pragma unroll
+                for (int b = 0; b < ROWS; ++b) {
+                    if (rr[b] >= HR) continue;
+                    // 4 x 4 byte transpose: o[e] = channel bytes (4 cq + 0..3) of column 4 iq + e
+                    const uint32_t t01l = __builtin_amdgcn_perm(d[b][1], d[b][0], 0x05010400u);
+                    const uint32_t t01h = __builtin_amdgcn_perm(d[b][1], d[b][0], 0x07030602u);
+                    const uint32_t t23l = __builtin_amdgcn_perm(d[b][3], d[b][2], 0x05010400u);
+                    const uint32_t t23h = __builtin_amdgcn_perm(d[b][3], d[b][2], 0x07030602u);
+                    const uint32_t o[4] = {__builtin_amdgcn_perm(t23l, t01l, 0x05040100u),
+                                           __builtin_amdgcn_perm(t23l, t01l, 0x07060302u),
+                                           __builtin_amdgcn_perm(t23h, t01h, 0x05040100u),
+                                           __builtin_amdgcn_perm(t23h, t01h, 0x07060302u)};
+                    const int pos0 = rr[b] * h.Wp + h.pl + 4 * iq_t;
+                    // column e of step k is (k + iq) & 3: neighbouring lanes (consecutive iq)
+                    // write different positions' banks in the same instruction
+#pragma unroll
+                    for (int k = 0; k < 4; ++k) {
+                        const int e = (k + iq_t) & 3;
+                        const uint32_t v = e == 0 ? o[0] : e == 1 ? o[1] : e == 2 ? o[2] : o[3];
+                        const int pos = pos0 + e;
+                        *reinterpret_cast<uint32_t*>(hal + pos * 64 + (halo_slot(pos, cq_t >> 2) << 4) + (cq_t & 3) * 4) = v;
+                    }
+                }
+            }
+        }
+        // padding columns: the fill code in all four chunks
+        for (int v = tid; v < HR * side * 4; v += 256) {
+            const int chunk = v & 3, cell = v >> 2;
+            const int r = cell / side, k = cell - r * side;
+            const int pos = r * h.Wp + (k < h.pl ? k : h.W + k);
+            *reinterpret_cast<v4i*>(hal + pos * 64 + (halo_slot(pos, chunk) << 4)) =
+                v4i{(int)fill, (int)fill, (int)fill, (int)fill};
+        }
+        wait_vmcnt<0>();
+        block_barrier();
+
+        // every tap from LDS; fragments of tap t + 1 are read while tap t's MFMAs run
+        auto read_frags = [&](v4i* f, int t) __attribute__((always_inline)) {
+            const int kh = t / h.KW, kw = t - kh * h.KW;
+            const int toff = kh * h.Wp + kw;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const int pos = basepos[j] + toff;
+                f[j] = *reinterpret_cast<const v4i*>(hal + pos * 64 + (halo_slot(pos, c0) << 4));
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int co = 16 * i + rho;
+                f[4 + i] = *reinterpret_cast<const v4i*>(wl + (t * 64 + co) * 64 + ((c0 ^ ((co >> 2) & 3)) << 4));
+            }
+        };
+        auto mfmas = [&](const v4i* f) __attribute__((always_inline)) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j)
+                    acc[i][j] = __builtin_amdgcn_mfma_i32_16x16x64_i8(f[j], f[4 + i], acc[i][j], 0, 0, 0);
+        };
+        v4i F0[8], F1[8];
+        read_frags(F0, 0);
+        int t = 0;
+        for (; t + 2 <= T; t += 2) {
+            read_frags(F1, t + 1);
+            mfmas(F0);
+            if (t + 2 < T) read_frags(F0, t + 2);
+            mfmas(F1);
+        }
+        if (t < T) mfmas(F0);
+    }
+    conv_epilogue<4, KIND>(a, acc, p0 + wave * 64 + c0 * 16, co0, 0, lane, csb, cbias, cws, sa, ep);
+}
+
+// Halo plan: the largest halo over the tiles (exact, by walking the tile starts), or 0 when
+// the shape does not take the halo kernel.
+constexpr int CV_HALO_LDS = 80 * 1024;  // two workgroups per CU
+int64_t halo_bytes_for(int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout, int64_t KH, int64_t KW, int sh,
+                       int sw, int pt, int pb, int pl, int pr, int dh, int dw, int64_t groups, int mode, int64_t OH,
+                       int64_t OW) {
+    if (groups != 1 || sh != 1 || sw != 1 || dh != 1 || dw != 1 || mode != LQ_PAD_ZEROS) return 0;
+    // (W <= 64: the 16 channel quads x W / 4 column quads of a row fit the 256 threads)
+    if (C % 64 != 0 || Cout % 64 != 0 || W % 4 != 0 || W > 64 || KH * KW > 16 || C / 64 > 4) return 0;
+    const int64_t Hp = H + pt + pb, Wp = W + pl + pr, OHW = OH * OW, P = N * OHW;
+    if (OHW < 64 || P < 256) return 0;
+    int64_t hr = 0;
+    for (int64_t p0 = 0; p0 < P; p0 += 256) {
+        const int64_t last = std::min(p0 + 255, P - 1);
+        const int64_t n0 = p0 / OHW, oh0 = (p0 - n0 * OHW) / OW;
+        const int64_t n1 = last / OHW, oh1 = (last - n1 * OHW) / OW;
+        hr = std::max(hr, n1 * Hp + oh1 + KH - (n0 * Hp + oh0));
+    }
+    const int64_t bytes = (hr * Wp * 64 + 1023) / 1024 * 1024;
+    if (bytes + KH * KW * 4096 > CV_HALO_LDS) return 0;
+    return bytes;
+}
+
 // Two waves per SIMD (<= 256 registers): the LDS ring leaves room for two workgroups per CU,
 // and their main loops and epilogues overlap.
 template <int BM, int BN, int WAVES_M, int WAVES_N, int NBUF, int KIND>
@@ -607,7 +987,6 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves
     constexpr int BK = 128, NW = WAVES_M * WAVES_N, WM = BM / WAVES_M, WN = BN / WAVES_N;
     constexpr int FM = WM / 16, FN = WN / 16;
     constexpr int A_I = BM / 8 / NW, B_I = BN / 8 / NW, LPS = A_I + B_I, SB = (BM + BN) * BK;
-    constexpr bool INT_CODES = KIND == LQ_OUT_Q8 || KIND == LQ_OUT_QU8 || KIND == LQ_OUT_Q16 || KIND == LQ_OUT_QU8S8;
     static_assert(WM == 64, "a lane owns 16 consecutive pixels of a 64-pixel wave tile");
     static_assert(A_I * 8 * NW == BM && B_I * 8 * NW == BN && WN % 16 == 0, "copy split");
     static_assert(NBUF >= 2 && (NBUF - 1) * LPS < 64, "stage ring");
@@ -780,146 +1159,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves
         }
     }
 
-    // Epilogue: acc[i][j][r] is pixel p0 + wm*64 + 16 (lane/16) + 4 j + r, channel
-    // co0 + wn*WN + 16 i + lane % 16 (within the group).
-    CodeClamp cc{};
-    if (INT_CODES) cc = code_clamp<KIND>(a.qmin, a.qmax);
-    const int Cout = a.G * a.Cout_g;
-    const int pb = p0 + wm * 64 + c0 * 16;
-    const int nimg = min(pb, a.P - 1) / OHW;
-    const int pix0 = pb - nimg * OHW;
-    constexpr int OB = OutTraits<KIND>::bytes;
-    const bool vec = (OHW % 16 == 0) && (reinterpret_cast<uintptr_t>(a.y) % 16 == 0) && (pb + 15 < a.P);
-    // Stores of one channel's 16 consecutive pixels (out[] holds the output type's bits).
-    auto store_col = [&](const int co, const uint32_t* out) __attribute__((always_inline)) {
-        if (vec) {
-            const int64_t base = ((int64_t)nimg * Cout + co) * OHW + pix0;
-            if (OB == 1) {
-                v4i w;
-#pragma unroll
-                for (int d = 0; d < 4; ++d) w[d] = (int)pack_low_bytes(out + 4 * d);
-                *reinterpret_cast<v4i*>(reinterpret_cast<uint8_t*>(a.y) + base) = w;
-            } else if (OB == 2) {
-#pragma unroll
-                for (int h = 0; h < 2; ++h) {
-                    v4i w;
-#pragma unroll
-                    for (int d = 0; d < 4; ++d)
-                        w[d] = (int)((out[8 * h + 2 * d] & 0xffffu) | (out[8 * h + 2 * d + 1] << 16));
-                    *reinterpret_cast<v4i*>(reinterpret_cast<uint16_t*>(a.y) + base + 8 * h) = w;
-                }
-            } else {
-#pragma unroll
-                for (int h = 0; h < 4; ++h)
-                    *reinterpret_cast<v4i*>(reinterpret_cast<uint32_t*>(a.y) + base + 4 * h) =
-                        v4i{(int)out[4 * h], (int)out[4 * h + 1], (int)out[4 * h + 2], (int)out[4 * h + 3]};
-            }
-        } else {
-            // 16 consecutive pixels from (image nimg, pixel pix0): at most one image boundary
-            // when OHW >= 16 (else the division per pixel)
-            const int64_t base = ((int64_t)nimg * Cout + co) * OHW + pix0;
-            const int64_t next = ((int64_t)(nimg + 1) * Cout + co) * OHW + pix0 - OHW;
-#pragma unroll
-            for (int q = 0; q < 16; ++q) {
-                const int p = pb + q;
-                if (p >= a.P) break;
-                int64_t idx;
-                if (OHW >= 16) {
-                    idx = pix0 + q < OHW ? base + q : next + q;
-                } else {
-                    const int nq = p / OHW, pq = p - nq * OHW;
-                    idx = ((int64_t)nq * Cout + co) * OHW + pq;
-                }
-                store_elem<KIND>(a.y, idx, out[q]);
-            }
-        }
-    };
-
-    // Integer codes, fast form (as in the GEMM epilogue): with the output scale's reciprocal
-    // finite and positive, the zero point integral and small, and every scale and bias of this
-    // wave finite and small enough that y stays finite, clamp(rne(y * inv) + z, lo, hi) equals
-    // zi + med3(cvt(rne(y * inv)), lo - zi, hi - zi), and ReLU folds into the lower bound.
-    if constexpr (INT_CODES) {
-        const float zf = ep.out_z;
-        bool ok = ep.out_inv > 0.0f && ep.out_inv < 3.0e38f && zf == __builtin_rintf(zf) &&
-                  __builtin_fabsf(zf) < 4194304.0f && __builtin_isfinite(sa);
-        float bmax = 0.0f;
-#pragma unroll
-        for (int i = 0; i < FN; ++i) {
-            bmax = __builtin_fmaxf(bmax, __builtin_fabsf(csb[i]));
-            ok = ok && __builtin_isfinite(csb[i]) && __builtin_isfinite(cbias[i]);
-        }
-        const float amax = __builtin_fabsf(sa);
-        ok = ok && amax < 1.0e14f && bmax < 1.0e14f && amax * bmax < 1.0e28f;
-        if (__all(ok)) {
-            const int zi = (int)zf;
-            int L = cc.lo - zi, H = cc.hi - zi;
-            if (a.relu) L = max(L, 0);
-            L = min(L, H);  // med3(x, L, H) = min(max(x, L), H) needs L <= H
-            const int shift = zi - (KIND == LQ_OUT_QU8S8 ? 128 : 0);
-            auto cols = [&](auto bias_c, auto za_c, auto shift_c) __attribute__((always_inline)) {
-                constexpr bool BIAS = decltype(bias_c)::value, ZA = decltype(za_c)::value;
-                constexpr bool SHIFT = decltype(shift_c)::value;
-                static_for<FN>([&](auto i_c) __attribute__((always_inline)) {
-                    constexpr int i = decltype(i_c)::value;
-                    const int col = co0 + wn * WN + 16 * i + rho;
-                    if (col >= a.Cout_g) return;
-                    const float sc = sa * csb[i];
-                    const uint32_t zsum = (uint32_t)ep.za * (uint32_t)cws[i];
-                    uint32_t out[16];
-#pragma unroll
-                    for (int q = 0; q < 16; ++q) {
-                        int32_t accq = acc[i][q >> 2][q & 3];
-                        if (ZA) accq = (int32_t)((uint32_t)accq - zsum);
-                        float y = (float)accq * sc;
-                        if (BIAS) y = y + cbias[i];
-                        const float r = __builtin_rintf(y * ep.out_inv);
-                        int32_t c = med3_i32(cvt_i32_sat(r), L, H);
-                        if (SHIFT) c += shift;
-                        out[q] = (uint32_t)c;
-                    }
-                    store_col(g * a.Cout_g + col, out);
-                });
-            };
-            auto cols_za = [&](auto bias_c) __attribute__((always_inline)) {
-                if (ep.has_za) {
-                    if (shift != 0) cols(bias_c, std::true_type{}, std::true_type{});
-                    else cols(bias_c, std::true_type{}, std::false_type{});
-                } else {
-                    if (shift != 0) cols(bias_c, std::false_type{}, std::true_type{});
-                    else cols(bias_c, std::false_type{}, std::false_type{});
-                }
-            };
-            if (a.bias) cols_za(std::true_type{});
-            else cols_za(std::false_type{});
-            return;
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < FN; ++i) {
-        const int col = co0 + wn * WN + 16 * i + rho;
-        if (col >= a.Cout_g) continue;
-        const int co = g * a.Cout_g + col;
-        const float sb = csb[i];
-        const float bias = cbias[i];
-        const int32_t zsum = ep.has_za ? (int32_t)((uint32_t)ep.za * (uint32_t)cws[i]) : 0;
-        uint32_t out[16];
-#pragma unroll
-        for (int q = 0; q < 16; ++q) {
-            const int32_t acc_c = (int32_t)((uint32_t)acc[i][q >> 2][q & 3] - (uint32_t)zsum);
-            if (INT_CODES) {
-                const float s = sa * sb;
-                float y = (float)acc_c * s;
-                if (a.bias) y = y + bias;
-                if (a.relu) y = (y <= 0.0f) ? 0.0f : y;
-                out[q] = (uint32_t)requant_int<KIND>(y, ep, cc);
-                if (KIND == LQ_OUT_QU8S8) out[q] ^= 0x80u;
-            } else {
-                out[q] = epi_one<KIND>(acc_c, sa, sb, a.bias ? &bias : nullptr, a.relu != 0, ep);
-            }
-        }
-        store_col(co, out);
-    }
+    conv_epilogue<FN, KIND>(a, acc, p0 + wm * 64 + c0 * 16, co0 + wn * WN, g, lane, csb, cbias, cws, sa, ep);
 }
 
 // ---------------------------------------------------------------- float helpers
@@ -1135,6 +1375,51 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
     LQ_REQUIRE(d_workspace && workspace_bytes >= plan.pack_bytes + plan.part_bytes,
                "lq_conv2d_i8: workspace smaller than lq_conv2d_i8_workspace_size");
     hipStream_t st = as_stream(stream);
+
+    // halo-staged direct kernel: no padded copy of the input (the workspace goes unused)
+    // (integer-code outputs only: the float kinds' epilogue does not fit this kernel's
+    // register budget without spilling)
+    const bool halo_kind = out_kind == LQ_OUT_Q8 || out_kind == LQ_OUT_QU8 || out_kind == LQ_OUT_QU8S8;
+    const int64_t halo = (halo_kind && (reinterpret_cast<uintptr_t>(d_x) & 3) == 0 && !plan.taps && plan.Cp == C)
+                             ? halo_bytes_for(N, C, H, W, Cout, KH, KW, stride_h, stride_w, pad_top, pad_bottom,
+                                              pad_left, pad_right, dilation_h, dilation_w, groups, padding_mode, OH, OW)
+                             : 0;
+    if (halo > 0) {
+        HaloArgs hg{};
+        ConvDmaArgs& d = hg.e;
+        d.wp = d_w_packed;
+        d.y = d_y;
+        d.G = 1; d.Cp = (int)C; d.Cout_g = (int)Cout; d.KH = (int)KH; d.KW = (int)KW; d.sh = 1; d.sw = 1;
+        d.dh = 1; d.dw = 1; d.OH = (int)OH; d.OW = (int)OW; d.P = (int)P; d.ldw = (int)plan.ldw;
+        d.a_scale = d_a_scale; d.a_zp = d_a_zero_point; d.a_u8s8 = x_code_type == LQ_U8S8;
+        d.w_scale = d_w_scale; d.w_sums = d_w_sums; d.bias = d_bias;
+        d.out_scale = d_out_scale; d.out_zp = d_out_zero_point;
+        d.qmin = out_qmin; d.qmax = out_qmax; d.relu = (flags & LQ_EPI_RELU) ? 1 : 0;
+        d.splits = 1; d.phase = 1;
+        hg.x = d_x;
+        hg.N = (int)N; hg.C = (int)C; hg.H = (int)H; hg.W = (int)W;
+        hg.Hp = (int)(H + pad_top + pad_bottom); hg.Wp = (int)(W + pad_left + pad_right);
+        hg.pt = pad_top; hg.pl = pad_left; hg.KH = (int)KH; hg.KW = (int)KW; hg.nc = (int)(C / 64);
+        hg.halo_bytes = (int)halo;
+        const size_t lds = (size_t)halo + (size_t)(KH * KW) * 4096;
+        const dim3 grid((unsigned)((P + 255) / 256), (unsigned)(Cout / 64));
+#define LQ_CONV_HALO(K_)                                                                                    \
+    {                                                                                                       \
+        const hipError_t e_ = hipFuncSetAttribute(reinterpret_cast<const void*>(&conv_i8_halo_kernel<K_>),  \
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);     \
+        if (e_ != hipSuccess) return set_error(LQ_ERR_HIP, std::string("lq_conv2d_i8 (halo): ") + hipGetErrorString(e_)); \
+        hipLaunchKernelGGL((conv_i8_halo_kernel<K_>), grid, dim3(256), lds, st, hg);                        \
+    }                                                                                                       \
+    break;
+        switch (out_kind) {
+            case LQ_OUT_Q8: LQ_CONV_HALO(LQ_OUT_Q8)
+            case LQ_OUT_QU8: LQ_CONV_HALO(LQ_OUT_QU8)
+            default: LQ_CONV_HALO(LQ_OUT_QU8S8)
+        }
+#undef LQ_CONV_HALO
+        note_path("conv halo");
+        return launch_status("lq_conv2d_i8");
+    }
 
     PackArgs pa{};
     pa.x = d_x;

@@ -105,6 +105,18 @@ __device__ __forceinline__ int32_t med3_i32(int32_t x, int32_t lo, int32_t hi) {
     return r;
 }
 
+// Round-to-nearest-even of t to an integer, carried in the bit pattern of a float:
+// t + 1.5 * 2^23 lies in [2^23, 2^24) for |t| < 2^22, where binary32 spacing is exactly 1, so
+// the one IEEE addition rounds t to an integer with ties to even (1.5 * 2^23 is even) and the
+// bits are RNE_MAGIC_BITS + rne(t).  Outside that range the bits stay ordered for a clamp to
+// [lo, hi] + RNE_MAGIC_BITS with |lo|, |hi| < 2^22: t >= 2^22 gives bits >= 0x4B800000, t <=
+// -2^22 gives bits <= 0x4B000000 or a negative int (t + magic < 0, or -inf), +inf 0x7F800000.
+// NaN is not ordered (its bits read as the largest positive values): callers exclude it.
+// RNE_MAGIC_BITS has zero low 16 bits, so after the clamp the low byte / halfword of the bits
+// is the code itself: no conversion back to an integer is needed for 8- and 16-bit stores.
+constexpr int32_t RNE_MAGIC_BITS = 0x4B400000;
+__device__ __forceinline__ int32_t rne_bits(float t) { return __float_as_int(t + 12582912.0f); }
+
 // The low bytes of v[0..3] as one dword (byte d = v[d] & 0xff): three v_perm_b32.
 __device__ __forceinline__ uint32_t pack_low_bytes(const uint32_t* v) {
     // v_perm_b32 selects bytes of {src0, src1} (src1 = bytes 0-3, src0 = 4-7; 0x0c gives 0)

@@ -427,7 +427,11 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N >= 8 ? 2 : 1))) void gemm_i
     constexpr int BK = P::BK, NW = P::NW, WM = P::WM, WN = P::WN, FM = P::FM, FN = P::FN, NH = P::NH;
     constexpr int RPI = P::ROWS_PER_INSTR, A_I = P::A_I, B_I = P::B_I, SB = P::SB;
     constexpr bool INT_CODES = KIND == LQ_OUT_Q8 || KIND == LQ_OUT_QU8 || KIND == LQ_OUT_Q16 || KIND == LQ_OUT_QU8S8;
-    __shared__ __attribute__((aligned(1024))) int8_t lds[P::LDS_BYTES];
+    // Stage ring, then the epilogue inputs (EPI_ARR bytes each: column scales, bias, column code
+    // sums, row scales).
+    constexpr int EPI_ARR = 1024;
+    static_assert(BM <= EPI_ARR / 4 && BN <= EPI_ARR / 4 && P::LDS_BYTES + 4 * EPI_ARR <= 160 * 1024, "epilogue LDS");
+    __shared__ __attribute__((aligned(1024))) int8_t lds[P::LDS_BYTES + 4 * EPI_ARR];
 
     const int tiles_m = (a.M + BM - 1) / BM, tiles_n = (a.N + BN - 1) / BN;
     int tm, tn;
@@ -437,6 +441,29 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N >= 8 ? 2 : 1))) void gemm_i
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
     const int nk = a.K / BK;
+    const EpiParams p = epi_params(a);
+
+    // Epilogue inputs of a whole tile (both dimensions in range, unit-stride scales, 16-byte
+    // aligned arrays) are copied into LDS before the main loop, one LDS-DMA per array (waves 0-3),
+    // so the epilogue reads them from LDS instead of waiting for global loads after the loop.
+    // These copies are older than every stage copy, so the prologue's vmcnt wait covers them
+    // and its barrier publishes them.
+    auto al16 = [](const void* q) { return (reinterpret_cast<uintptr_t>(q) & 15) == 0; };
+    const bool pre = nk > 0 && n0 + BN <= a.N && m0 + BM <= a.M && a.b_scale && a.b_stride == 1 &&
+                     al16(a.b_scale) && a.a_scale && a.a_stride == 1 && al16(a.a_scale) &&
+                     (!a.bias || al16(a.bias)) && (!p.has_za || al16(a.b_sums));
+    const uint32_t lds_epi = (uint32_t)reinterpret_cast<uintptr_t>(lds) + P::LDS_BYTES;
+    if (pre && wave < 4) {
+        const void* src = wave == 0 ? (const void*)a.b_scale
+                          : wave == 1 ? (const void*)a.bias
+                          : wave == 2 ? (p.has_za ? (const void*)a.b_sums : nullptr)
+                                      : (const void*)a.a_scale;
+        const int first = wave == 3 ? m0 : n0, count = wave == 3 ? a.M : a.N;
+        if (src) {
+            const v4i r = buffer_rsrc(src, (uint32_t)count * 4u);
+            lds_dma16(r, (uint32_t)lane * 16u, (uint32_t)first * 4u, lds_epi + wave * EPI_ARR);
+        }
+    }
 
     const v4i ra = buffer_rsrc(a.A, (uint32_t)((int64_t)a.M * a.lda));
     const v4i rb = buffer_rsrc(a.B, (uint32_t)((int64_t)a.N * a.ldb));
@@ -537,10 +564,10 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N >= 8 ? 2 : 1))) void gemm_i
              ...);
         }(std::make_integer_sequence<int, NBUF>());
     }
-    // Epilogue inputs, loaded after the main loop so their registers (52 per lane) do not
-    // compete with the fragment double buffer: this lane's 16 columns and FM rows, as 16-byte
-    // loads when the 16 columns are in range and the arrays aligned.
-    const EpiParams p = epi_params(a);
+    // Epilogue inputs: from LDS when the prologue copied them there, else loaded after the main
+    // loop so their registers (52 per lane) do not compete with the fragment double buffer:
+    // this lane's 16 columns and FM rows, as 16-byte loads when the 16 columns are in range and
+    // the arrays aligned.
     const int mr0 = m0 + wm * WM + (lane & 15);
     // Both halves' column inputs and the row scales are loaded (and waited for) before any
     // output store: stores count in vmcnt too, so a wait placed after the first half's stores
@@ -553,7 +580,22 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N >= 8 ? 2 : 1))) void gemm_i
         float* csb = csbs[HF];
         float* cbias = cbiass[HF];
         int32_t* czab = czabs[HF];
-        {
+        if (pre) {
+            const float* le = reinterpret_cast<const float*>(lds + P::LDS_BYTES);
+            const int c = nc0 - n0;
+    #pragma unroll
+            for (int h = 0; h < 4; ++h) {
+                const v4f v = *reinterpret_cast<const v4f*>(le + c + 4 * h);
+                const v4f w = a.bias ? *reinterpret_cast<const v4f*>(le + EPI_ARR / 4 + c + 4 * h) : v4f{0, 0, 0, 0};
+                const v4i u = p.has_za ? *reinterpret_cast<const v4i*>(le + EPI_ARR / 2 + c + 4 * h) : v4i{0, 0, 0, 0};
+    #pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    csb[4 * h + e] = v[e];
+                    cbias[4 * h + e] = w[e];
+                    czab[4 * h + e] = (int32_t)((uint32_t)p.za * (uint32_t)u[e]);
+                }
+            }
+        } else {
             const bool cols_vec = nc0 + 16 <= a.N;
             auto vec_ok = [&](const void* ptr) { return cols_vec && (reinterpret_cast<uintptr_t>(ptr) & 15) == 0; };
             if (a.b_scale && a.b_stride == 1 && vec_ok(a.b_scale)) {
@@ -594,8 +636,12 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N >= 8 ? 2 : 1))) void gemm_i
     float rsa[FM];
     static_for<FM>([&](auto j_c) __attribute__((always_inline)) {
         constexpr int j = decltype(j_c)::value;
-        const int mm = min(mr0 + j * 16, a.M - 1);
-        rsa[j] = a.a_scale ? a.a_scale[(int64_t)mm * a.a_stride] : 1.0f;
+        if (pre) {
+            rsa[j] = reinterpret_cast<const float*>(lds + P::LDS_BYTES + 3 * EPI_ARR)[mr0 - m0 + j * 16];
+        } else {
+            const int mm = min(mr0 + j * 16, a.M - 1);
+            rsa[j] = a.a_scale ? a.a_scale[(int64_t)mm * a.a_stride] : 1.0f;
+        }
     });
 
     wait_vmcnt<0>();  // no copy may still target LDS when the workgroup ends
@@ -676,16 +722,19 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N >= 8 ? 2 : 1))) void gemm_i
 
         // Integer codes, fast form.  When the output scale's reciprocal is finite and positive,
         // the zero point integral and small, every scale and bias of this wave finite and
-        // max|sa| * max|sb| small enough that float(acc) * s cannot overflow, y is always finite,
-        // and the code clamp(rne(y * inv) + z, lo, hi) equals zi + med3(cvt(rne(y * inv)), lo - zi,
-        // hi - zi): the saturating convert keeps out-of-range values ordered and |zi| < 2^22 keeps
-        // the sum exact.  ReLU (y <= 0 -> 0, so the code of z) folds into the lower bound:
+        // max|sa| * max|sb| small enough that float(acc) * s cannot overflow, y is always finite
+        // (y * inv may be infinite, never NaN), and the code clamp(rne(y * inv) + z, lo, hi)
+        // equals zi + med3(rne(y * inv), lo - zi, hi - zi).  The rounding is rne_bits (one add
+        // whose float bits are RNE_MAGIC_BITS + rne(t), ordered outside the exact range), so the
+        // clamp runs on the bits against bounds shifted by RNE_MAGIC_BITS and the low byte or
+        // halfword of the result is the code: |zi| < 2^21 keeps the shifted bounds inside the
+        // exact window.  ReLU (y <= 0 -> 0, so the code of z) folds into the lower bound:
         // rne(y * inv) <= 0 exactly when y <= 0.  The stored byte of QU8S8 is c - 128.
         bool fast_int = false;
         if constexpr (INT_CODES) {
             const float zf = p.out_z;
             bool ok = a.b_zp == nullptr && p.out_inv > 0.0f && p.out_inv < 3.0e38f && zf == __builtin_rintf(zf) &&
-                      __builtin_fabsf(zf) < 4194304.0f;
+                      __builtin_fabsf(zf) < 2097152.0f;
             float amax = 0.0f, bmax = 0.0f;
     #pragma unroll
             for (int j = 0; j < FM; ++j) amax = __builtin_fmaxf(amax, __builtin_fabsf(rsa[j]));
@@ -708,6 +757,7 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N >= 8 ? 2 : 1))) void gemm_i
                 int L = cc.lo - zi, H = cc.hi - zi;
                 if (relu) L = max(L, 0);
                 L = min(L, H);  // med3(x, L, H) = min(max(x, L), H) needs L <= H
+                const int Lm = L + RNE_MAGIC_BITS, Hm = H + RNE_MAGIC_BITS;
                 const int shift = zi - (KIND == LQ_OUT_QU8S8 ? 128 : 0);
                 // ZA / SHIFT off when the activation zero point / the code shift are zero:
                 // two VALU ops fewer per element.
@@ -724,10 +774,9 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N >= 8 ? 2 : 1))) void gemm_i
                             const float sc = rsa[j] * csb[q];
                             float y = (float)accq * sc;
                             if (BIAS) y = y + cbias[q];
-                            const float r = __builtin_rintf(y * p.out_inv);
-                            int32_t c = med3_i32(cvt_i32_sat(r), L, H);
+                            int32_t c = med3_i32(rne_bits(y * p.out_inv), Lm, Hm);
                             if (SHIFT) c += shift;
-                            out[q] = (uint32_t)c;
+                            out[q] = (uint32_t)c;  // low byte / halfword: the code
                         }
                         store_row(j, out);
                     });

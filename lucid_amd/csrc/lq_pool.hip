@@ -14,6 +14,8 @@
 // the fake-quantized floats.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
+
 #include "lq_internal.h"
 
 namespace lq {
@@ -132,6 +134,104 @@ __global__ __launch_bounds__(256) void avg_pool_kernel(PoolArgs a) {
     }
 }
 
+// Plane-staged pooling: a workgroup owns pp consecutive (n, c) planes, which are contiguous in
+// memory.  It copies their bytes into LDS with 16-byte loads (byte loads for the partial chunks
+// at the tensor's ends, or everywhere when x is not 16-byte aligned), then computes each output
+// from LDS with the same window rules and the same element order as the per-output kernels
+// above, so the results are identical; only the global traffic changes (one coalesced read of
+// each plane instead of one narrow load per window element per output).
+constexpr int POOL_PLANE_LDS = 24576;  // bytes of planes per workgroup (two workgroups per CU or more)
+
+template <int T, bool MAX>
+__global__ __launch_bounds__(256) void pool_planes_kernel(PoolArgs a, int pp, int64_t total_bytes, int aligned) {
+    using E = typename PoolElem<T>::type;
+    extern __shared__ __attribute__((aligned(16))) uint8_t pool_lds[];
+    const int tid = threadIdx.x;
+    const int64_t HW = (int64_t)a.H * a.W;
+    const int64_t nc0 = (int64_t)blockIdx.x * pp;
+    const int np = (int)min((int64_t)pp, a.NC - nc0);
+    const int64_t b0 = nc0 * HW * (int64_t)sizeof(E), b1 = (nc0 + np) * HW * (int64_t)sizeof(E);
+    const int64_t c0 = b0 & ~(int64_t)15, c1 = (b1 + 15) & ~(int64_t)15;
+    const uint8_t* xb = static_cast<const uint8_t*>(a.x);
+    for (int64_t c = c0 + 16 * tid; c < c1; c += 16 * 256) {
+        uint8_t* dst = pool_lds + (c - c0);
+        if (aligned && c + 16 <= total_bytes) {
+            *reinterpret_cast<int4*>(dst) = *reinterpret_cast<const int4*>(xb + c);
+        } else {
+#pragma unroll
+            for (int e = 0; e < 16; ++e)
+                if (c + e < total_bytes) dst[e] = xb[c + e];
+        }
+    }
+    __syncthreads();
+    const E* P = reinterpret_cast<const E*>(pool_lds + (b0 - c0));  // b0 - c0 is a multiple of sizeof(E)
+    const int OHW = a.OH * a.OW;
+    const float s = a.x_scale ? a.x_scale[0] : 1.0f, z = a.x_zp ? a.x_zp[0] : 0.0f;
+    // work item = (plane, output column, row group): the column window is computed once, the
+    // rows og, og + G, ... follow (G row groups keep the 256 threads busy on narrow planes)
+    const int cols = np * a.OW;
+    const int G = max(1, min(a.OH, 256 / max(cols, 1)));
+    for (int item = tid; item < cols * G; item += 256) {
+        const int og = item / cols, c = item - og * cols;
+        const int pl = c / a.OW, ow = c - pl * a.OW;
+        int w0, w1, spw;
+        pool_window(a, ow, a.W, a.OW, a.KW, a.sw, a.pw, w0, w1, spw);
+        const E* xp = P + (int64_t)pl * HW;
+        const int64_t o0 = (nc0 + pl) * OHW + ow;
+        if constexpr (MAX && T != LQ_F32) {
+            // integer codes: the window maximum, order-free, so rows and columns outside the
+            // window are clamped onto its edge (a repeated element leaves the maximum alone)
+            // and fixed windows up to 3 x 3 run unrolled and branch-free
+            if (!a.adaptive && a.KH <= 3 && a.KW <= 3) {
+                int wc[3];
+#pragma unroll
+                for (int k = 0; k < 3; ++k) wc[k] = min(max(ow * a.sw - a.pw + min(k, a.KW - 1), w0), w1 - 1);
+                for (int oh = og; oh < a.OH; oh += G) {
+                    int h0, h1, sph;
+                    pool_window(a, oh, a.H, a.OH, a.KH, a.sh, a.ph, h0, h1, sph);
+                    int best = (int)xp[h0 * a.W + w0];
+#pragma unroll
+                    for (int kh = 0; kh < 3; ++kh) {
+                        const int hh = min(max(oh * a.sh - a.ph + min(kh, a.KH - 1), h0), h1 - 1);
+                        const E* row = xp + hh * a.W;
+#pragma unroll
+                        for (int k = 0; k < 3; ++k) best = max(best, (int)row[wc[k]]);
+                    }
+                    static_cast<E*>(a.y)[o0 + (int64_t)oh * a.OW] = (E)best;
+                }
+                continue;
+            }
+        }
+        for (int oh = og; oh < a.OH; oh += G) {
+            int h0, h1, sph;
+            pool_window(a, oh, a.H, a.OH, a.KH, a.sh, a.ph, h0, h1, sph);
+            const int64_t o = o0 + (int64_t)oh * a.OW;
+            if constexpr (MAX) {
+                E best = E(0);
+                bool any = false;
+                for (int h = h0; h < h1; ++h)
+                    for (int w = w0; w < w1; ++w) {
+                        const E v = xp[h * a.W + w];
+                        bool take = !any || v > best;
+                        if constexpr (T == LQ_F32) take = take || (v != v && !(best != best));
+                        if (take) best = v;
+                        any = true;
+                    }
+                if constexpr (T == LQ_F32) {
+                    if (!any) best = -__builtin_inff();
+                }
+                static_cast<E*>(a.y)[o] = best;
+            } else {
+                float sum = 0.0f;
+                for (int h = h0; h < h1; ++h)
+                    for (int w = w0; w < w1; ++w) sum = sum + pool_load<T>(a, xp + h * a.W + w, s, z);
+                const int denom = sph * spw;
+                static_cast<float*>(a.y)[o] = denom > 0 ? sum / (float)denom : 0.0f;
+            }
+        }
+    }
+}
+
 }  // namespace lq
 
 using namespace lq;
@@ -165,10 +265,39 @@ int lq_pool2d(int op, const void* d_x, int x_type, const float* d_x_scale, const
     PoolArgs a{d_x, x_type, x_type == LQ_F32 ? nullptr : d_x_scale, x_type == LQ_F32 ? nullptr : d_x_zero_point,
                N * C, (int)H, (int)W, (int)OH, (int)OW, KH, KW, stride_h, stride_w, pad_h, pad_w, adaptive ? 1 : 0,
                (flags & LQ_POOL_COUNT_INCLUDE_PAD) ? 1 : 0, d_y};
+    hipStream_t st = as_stream(stream);
+    const int esz = x_type == LQ_F32 ? 4 : x_type == LQ_I16 ? 2 : 1;
+    const int64_t plane_bytes = H * W * esz;
+    if (plane_bytes <= POOL_PLANE_LDS && N * C < ((int64_t)1 << 31)) {
+        // planes per workgroup: as many as the LDS budget holds, but no fewer than ~1024
+        // workgroups when there are that many planes (small planes: a thread per column)
+        const int64_t nc = N * C;
+        const int pp = (int)std::max<int64_t>(1, std::min<int64_t>(POOL_PLANE_LDS / plane_bytes, (nc + 1023) / 1024));
+        const int64_t blocks = (N * C + pp - 1) / pp;
+        const size_t lds = (size_t)(((int64_t)pp * plane_bytes + 15) / 16 * 16 + 16);
+        const int al = (reinterpret_cast<uintptr_t>(d_x) & 15) == 0 ? 1 : 0;
+        const int64_t tb = N * C * plane_bytes;
+        const dim3 pg((unsigned)blocks);
+#define LQ_POOL_PLANES(MX)                                                                                   \
+    switch (x_type) {                                                                                        \
+        case LQ_F32: hipLaunchKernelGGL((pool_planes_kernel<LQ_F32, MX>), pg, dim3(256), lds, st, a, pp, tb, al); break; \
+        case LQ_I8: hipLaunchKernelGGL((pool_planes_kernel<LQ_I8, MX>), pg, dim3(256), lds, st, a, pp, tb, al); break;   \
+        case LQ_U8: hipLaunchKernelGGL((pool_planes_kernel<LQ_U8, MX>), pg, dim3(256), lds, st, a, pp, tb, al); break;   \
+        case LQ_I16: hipLaunchKernelGGL((pool_planes_kernel<LQ_I16, MX>), pg, dim3(256), lds, st, a, pp, tb, al); break; \
+        default: hipLaunchKernelGGL((pool_planes_kernel<LQ_U8S8, MX>), pg, dim3(256), lds, st, a, pp, tb, al); break;    \
+    }
+        if (op == LQ_POOL_MAX) {
+            LQ_POOL_PLANES(true)
+        } else {
+            LQ_POOL_PLANES(false)
+        }
+#undef LQ_POOL_PLANES
+        note_path("pool planes");
+        return launch_status("lq_pool2d");
+    }
     int64_t blocks = (total + 255) / 256;
     if (blocks > 65536) blocks = 65536;
     const dim3 grid((unsigned)blocks);
-    hipStream_t st = as_stream(stream);
 #define LQ_POOL_LAUNCH(K)                                                                               \
     switch (x_type) {                                                                                   \
         case LQ_F32: hipLaunchKernelGGL(K<LQ_F32>, grid, dim3(256), 0, st, a); break;                   \
@@ -183,6 +312,7 @@ int lq_pool2d(int op, const void* d_x, int x_type, const float* d_x_scale, const
         LQ_POOL_LAUNCH(avg_pool_kernel)
     }
 #undef LQ_POOL_LAUNCH
+    note_path("pool per output");
     return launch_status("lq_pool2d");
 }
 

@@ -283,15 +283,17 @@ class Module:
         raise NotImplementedError(f"{type(self).__name__}.forward")
 
     def __call__(self, *args: Any, **kwargs: Any) -> Any:
-        for hook in list(self._forward_pre_hooks.values()):
-            r = hook(self, args)
-            if r is not None:
-                args = r if isinstance(r, tuple) else (r,)
+        if self._forward_pre_hooks:
+            for hook in list(self._forward_pre_hooks.values()):
+                r = hook(self, args)
+                if r is not None:
+                    args = r if isinstance(r, tuple) else (r,)
         out = self.forward(*args, **kwargs)
-        for hook in list(self._forward_hooks.values()):
-            r = hook(self, args, out)
-            if r is not None:
-                out = r
+        if self._forward_hooks:
+            for hook in list(self._forward_hooks.values()):
+                r = hook(self, args, out)
+                if r is not None:
+                    out = r
         return out
 
     # ------------------------------------------------------------------- repr

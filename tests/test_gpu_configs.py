@@ -79,6 +79,33 @@ def test_pool_over_codes(gpu):
     np.testing.assert_array_equal(F.adaptive_avg_pool2d(xq, 1).numpy(), O.pool2d(vals, "avg", adaptive=(1, 1)))
 
 
+@pytest.mark.parametrize("shape,geom,offset", [
+    ((4, 64, 112, 112), ((3, 3), (2, 2), (1, 1)), 0),   # the ResNet-18 stem pool: one plane per workgroup
+    ((3, 7, 33, 29), ((2, 3), (2, 1), (1, 1)), 0),      # odd planes: several per workgroup, unaligned starts
+    ((3, 7, 33, 29), ((3, 3), (1, 1), (1, 1)), 1),      # x not 16-byte aligned: byte loads
+    ((2, 3, 181, 181), ((3, 3), (2, 2), (1, 1)), 0),    # planes over the LDS budget: per-output kernel
+])
+def test_max_pool_codes_paths(gpu, shape, geom, offset):
+    # max pooling of int8 codes through the C ABI on both kernels (plane-staged and per
+    # output), against the oracle's pooling of the same values
+    from lucid_amd import _C
+
+    k, s, p = geom
+    rng = np.random.default_rng(sum(shape) + offset)
+    codes = rng.integers(-128, 128, shape, dtype=np.int64).astype(np.int8)
+    N, C, H, W = shape
+    OH, OW = (H + 2 * p[0] - k[0]) // s[0] + 1, (W + 2 * p[1] - k[1]) // s[1] + 1
+    buf = gpu.tensor(np.concatenate([np.zeros(offset, np.int8), codes.ravel()]), device="gpu")
+    y = gpu.empty((N, C, OH, OW), np.int8, "gpu")
+    _C.call("lq_pool2d", _C.POOL_MAX, buf.data_ptr() + offset, _C.I8, None, None, N, C, H, W, OH, OW, k[0], k[1],
+            s[0], s[1], p[0], p[1], 0, y.data_ptr(), None)
+    gpu.synchronize()
+    path = _C.last_path()
+    assert path == ("pool per output" if H * W > 24576 else "pool planes"), path
+    want = O.pool2d(codes.astype(np.float32), "max", k, s, p)
+    np.testing.assert_array_equal(y.numpy().astype(np.float32), want)
+
+
 # ------------------------------------------------------------------- config 5: ResNet-18
 
 

@@ -152,6 +152,57 @@ def test_conv_i8_every_out_kind(gpu, kind):
     _check(run_conv(gpu, x, w, **kw), oracle_conv(x, w, **kw), kind)
 
 
+HALO_CASES = [
+    # (N, C, H, W, Cout, KH, KW, pad): stride-1, zeros-padded convolutions with C and Cout
+    # multiples of 64 and W % 4 == 0, which take the halo-staged kernel
+    (8, 64, 56, 56, 64, 3, 3, (1, 1, 1, 1)),     # ResNet-18 layer1 at batch 8: tiles across images
+    (3, 128, 28, 28, 128, 3, 3, (1, 1, 1, 1)),   # two channel blocks, two output-channel blocks
+    (4, 256, 12, 12, 64, 3, 3, (1, 1, 1, 1)),    # four channel blocks, a tile spans 1.8 images
+    (2, 64, 12, 20, 128, 3, 3, (0, 2, 1, 1)),    # asymmetric padding, ragged last tile
+    (4, 64, 9, 8, 64, 2, 3, (1, 1, 0, 2)),       # non-square kernel, one-sided column padding
+]
+
+
+@pytest.mark.parametrize("case", HALO_CASES)
+@pytest.mark.parametrize("kind", [O.OUT_QU8S8, O.OUT_Q8, O.OUT_QU8])
+def test_conv_halo_exact(gpu, case, kind):
+    # the halo-staged kernel (input rows staged in LDS from the NCHW codes, no padded copy)
+    # against the oracle's int64 convolution and epilogue, for each integer output kind,
+    # with and without an activation zero point, ReLU and bias
+    from lucid_amd import _C
+
+    N, C, H, W, Cout, KH, KW, pad = case
+    rng = np.random.default_rng(N * 1000 + C + H + Cout + kind)
+    x = _codes(rng, (N, C, H, W))
+    w = _codes(rng, (Cout, C, KH, KW), -127, 127)
+    ws = rng.uniform(1e-3, 2e-2, Cout).astype(np.float32)
+    qmin, qmax = GRID.get(kind, (-128, 127))
+    zp = 128.0 if qmin == 0 else -3.0
+    for u8s8, za, relu, bias in ((True, 131.0, True, True), (False, None, False, False), (False, -3.0, True, True)):
+        kw = dict(stride=(1, 1), pad=pad, w_scale=ws, out_kind=kind, qmin=qmin, qmax=qmax, out_zp=zp,
+                  bias=rng.standard_normal(Cout).astype(np.float32) if bias else None, a_scale=0.03,
+                  out_scale=0.3)
+        got = run_conv(gpu, x, w, u8s8=u8s8, za=za, relu=relu, **kw)
+        assert _C.last_path() == "conv halo", _C.last_path()
+        want = oracle_conv(x, w, u8s8=u8s8, za=za, relu=relu, **kw)
+        _check(got, want, kind)
+
+
+def test_conv_halo_declines(gpu):
+    # shapes outside the halo kernel's reach keep the packed-input kernels
+    from lucid_amd import _C
+
+    rng = np.random.default_rng(77)
+    for (C, W, stride, kind) in ((64, 14, (1, 1), O.OUT_QU8S8), (64, 16, (2, 2), O.OUT_QU8S8),
+                                 (48, 16, (1, 1), O.OUT_QU8S8), (64, 16, (1, 1), O.OUT_F32)):
+        x = _codes(rng, (4, C, 16, W))
+        w = _codes(rng, (64, C, 3, 3), -127, 127)
+        kw = dict(stride=stride, pad=(1, 1, 1, 1), out_kind=kind)
+        got = run_conv(gpu, x, w, **kw)
+        assert _C.last_path() != "conv halo", (C, W, stride, kind)
+        _check(got, oracle_conv(x, w, **kw), kind)
+
+
 def test_conv_weight_pack_layout(gpu):
     rng = np.random.default_rng(4)
     w = _codes(rng, (10, 20, 3, 2))
