@@ -752,16 +752,17 @@ __device__ __forceinline__ void conv_epilogue(const ConvDmaArgs& a, v4i (&acc)[F
 
 // ---------------------------------------------------------------- halo-staged direct conv
 //
-// Stride-1, zeros-padded, undilated, ungrouped convolutions with C and Cout multiples of 64
-// (the ResNet 3x3 layers) skip the padded NHWC copy.  A workgroup of four waves owns 256
-// consecutive output pixels (flattened n, oh, ow) x 64 output channels.  For each block of 64
-// input channels it stages in LDS
+// Stride-1, zeros-padded, undilated, ungrouped convolutions with 64 input channels, Cout a
+// multiple of 64 and H * W a multiple of 16 (ResNet-18 layer1) skip the padded NHWC copy.  A
+// workgroup of four waves owns 256 consecutive output pixels (flattened n, oh, ow) x 64 output
+// channels.  For each block of 64 input channels it stages in LDS
 //   * the halo: every padded input row its pixels read -- padded rows of consecutive images
 //     stack, row R = n * Hp + hp, and the tile needs rows R0 .. R0 + HR - 1 -- at all Wp padded
 //     columns, 64 channels per position (64 bytes; 16-byte chunk c at slot c ^ ((pos >> 4) & 3),
 //     which spreads the four 4-pixel runs of an A fragment over distinct banks), read from the
-//     NCHW codes as dwords (4 columns of one channel) and transposed 4 x 4 in registers
-//     (v_perm); padding positions and rows past the last image hold the activation zero point;
+//     NCHW codes as 16-byte chunks of each channel's contiguous run of rows and transposed 4 x 4
+//     in registers (v_perm); padding positions and rows past the last image hold the
+//     activation zero point;
 //   * the block's weights for the 64 output channels, [tap][co][64 bytes] (chunk slot
 //     c ^ ((co >> 2) & 3)), by LDS-DMA from the packed rows;
 // then runs every tap from LDS: tap (kh, kw) of pixel (n, oh, ow) is halo position
@@ -769,14 +770,28 @@ __device__ __forceinline__ void conv_epilogue(const ConvDmaArgs& a, v4i (&acc)[F
 // no padded copy of the activation goes through HBM.  Pixels are the MFMA row operand in the
 // permuted order of the DMA kernel (a lane ends with 16 consecutive pixels of each of its
 // channels), so the epilogue is the same.
+constexpr int CV_HALO_ITEMS = 3;  // staged 4-channel x 16-byte items per thread per image
+
 struct HaloArgs {
     ConvDmaArgs e;      // output, geometry (P, OH, OW, Cout_g, G = 1), epilogue operands
     const int8_t* x;    // NCHW activation codes
     int N, C, H, W, Hp, Wp, pt, pl, KH, KW, nc;  // nc = C / 64 input channel blocks
     int halo_bytes;     // LDS bytes of the largest tile's halo (a multiple of 1024)
+    float inv_ohw, inv_ow, inv_hp, inv_w;  // 1 / (OH * OW), 1 / OW, 1 / Hp, 1 / W (div_small)
+    int dummy_pos;      // halo position past the last row: a sink for bytes outside the run
 };
 
 __device__ __forceinline__ int halo_slot(int pos, int chunk) { return chunk ^ ((pos >> 4) & 3); }
+
+// q / d for 0 <= q < 2^24 and d >= 1 by a float reciprocal estimate (within one of the quotient
+// for such q) and one correction each way: a handful of VALU ops where an integer division
+// by a runtime value is a long sequence.
+__device__ __forceinline__ int div_small(int q, int d, float inv) {
+    int n = (int)((float)q * inv);
+    n -= (n * d > q) ? 1 : 0;
+    n += ((n + 1) * d <= q) ? 1 : 0;
+    return n;
+}
 
 template <int KIND>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void conv_i8_halo_kernel(HaloArgs h) {
@@ -790,8 +805,8 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
     const int OHW = a.OH * a.OW, T = h.KH * h.KW;
     // padded rows of this tile (stride 1: output row oh reads padded rows oh .. oh + KH - 1)
     const int plast = min(p0 + 255, a.P - 1);
-    const int n0 = p0 / OHW, oh0 = (p0 - n0 * OHW) / a.OW;
-    const int n1 = plast / OHW, oh1 = (plast - n1 * OHW) / a.OW;
+    const int n0 = div_small(p0, OHW, h.inv_ohw), oh0 = div_small(p0 - n0 * OHW, a.OW, h.inv_ow);
+    const int n1 = div_small(plast, OHW, h.inv_ohw), oh1 = div_small(plast - n1 * OHW, a.OW, h.inv_ow);
     const int R0 = n0 * h.Hp + oh0;
     const int HR = n1 * h.Hp + oh1 + h.KH - R0;
 
@@ -822,25 +837,15 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
         const int q = min(p0 + wave * 64 + (rho >> 2) * 16 + 4 * j + (rho & 3), a.P - 1);
-        const int n = q / OHW, r = q - n * OHW;
-        const int oh = r / a.OW, ow = r - oh * a.OW;
+        const int n = div_small(q, OHW, h.inv_ohw), r = q - n * OHW;
+        const int oh = div_small(r, a.OW, h.inv_ow), ow = r - oh * a.OW;
         basepos[j] = (n * h.Hp + oh - R0) * h.Wp + ow;
     }
 
     const v4i rw = buffer_rsrc(a.wp, (uint32_t)((int64_t)a.Cout_g * a.ldw));
     const uint32_t wl_base = (uint32_t)reinterpret_cast<uintptr_t>(wl);
     const int side = h.Wp - h.W;                 // padding columns per row
-    // this thread's staging pair and first row (the same for every channel block)
-    const int Wq = h.W >> 2;                     // column quads per row
-    const int pairs = 16 * Wq, groups = max(1, 256 / pairs);
-    const int pair = tid % pairs, r_t = tid / pairs;
-    const int cq_t = pair / Wq, iq_t = pair - cq_t * Wq;
-    int n_t, hp_t;
-    {
-        const int R = R0 + r_t;
-        n_t = R / h.Hp;
-        hp_t = R - n_t * h.Hp;
-    }
+    const int nA = div_small(R0, h.Hp, h.inv_hp), nB = min(div_small(R0 + HR - 1, h.Hp, h.inv_hp), h.N - 1);
     v4i acc[4][4];
 #pragma unroll
     for (int i = 0; i < 4; ++i)
@@ -857,65 +862,71 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) void c
             const uint32_t off = (uint32_t)((co0 + co) * a.ldw + tap * h.C + cb * 64 + chunk * 16);
             lds_dma16(rw, off, 0, wl_base + (uint32_t)i * 1024u);
         }
-        // halo interior: thread t owns the pair (channel quad cq, column quad iq) of index
-        // t % pairs (iq fastest, so a wave's dword loads run along channel rows) and walks the
-        // rows r = t / pairs, + groups, ...; each row's image and input row advance by
-        // increments.  Rows outside an image load a clamped in-range address and take the
-        // fill code by a select (no branches).  ROWS rows are in flight per step.
-        if (tid < pairs * groups) {
-            constexpr int ROWS = 4;
-            const int8_t* xpair = h.x + ((int64_t)cb * 64 + 4 * cq_t) * h.H * h.W + 4 * iq_t;
-            int n = n_t, hp = hp_t;  // image and padded row of row r_t
-            for (int r0 = r_t; r0 < HR; r0 += ROWS * groups) {
-                uint32_t d[ROWS][4];
-                int rr[ROWS];
+        // halo interior, image by image: the tile's input rows ihA..ihB of image n are one
+        // contiguous run of bytes in each channel plane.  Work item = (channel quad cq, 16-byte
+        // chunk k of the run), k fastest so a wave's loads run along channel planes; a thread
+        // loads its items' 4 x 16 bytes (4 channels) first, then transposes each column of 4
+        // channel bytes into a dword (v_perm) and writes it at its halo position.  Bytes of a
+        // chunk outside the run (alignment) go to a dummy slot past the halo.
+        for (int n = nA; n <= nB; ++n) {
+            const int hpA = max(R0 - n * h.Hp, 0), hpB = min(R0 + HR - 1 - n * h.Hp, h.Hp - 1);
+            const int ihA = max(hpA - h.pt, 0), ihB = min(hpB - h.pt, h.H - 1);
+            if (ihA > ihB) continue;
+            const int b0 = ihA * h.W, b1 = (ihB + 1) * h.W;  // byte range of the run in a plane
+            const int kA = b0 >> 4, nk = ((b1 - 1) >> 4) - kA + 1;
+            const int items = nk * 16;
+            const int rowbase = n * h.Hp + h.pt - R0;  // halo row of input row 0 of image n
+            const int8_t* plane0 = h.x + ((int64_t)n * h.C + cb * 64) * h.H * h.W;
+            constexpr int IT = CV_HALO_ITEMS;
+            v4i d[IT][4];
+            int kk[IT], cq[IT];
 #pragma unroll
-                for (int b = 0; b < ROWS; ++b) {
-                    rr[b] = r0 + b * groups;
-                    const int ih = hp - h.pt;
-                    const bool ok = rr[b] < HR && n < h.N && ih >= 0 && ih < h.H;
-                    const int nc = min(n, h.N - 1), ic = min(max(ih, 0), h.H - 1);
-                    const int8_t* src = xpair + ((int64_t)nc * h.C * h.H + ic) * h.W;
+            for (int b = 0; b < IT; ++b) {
+                const int it = min(tid + b * 256, items - 1);
+                cq[b] = div_small(it, nk, __builtin_amdgcn_rcpf((float)nk));
+                kk[b] = kA + it - cq[b] * nk;
+                const int8_t* src = plane0 + (int64_t)(4 * cq[b]) * h.H * h.W + 16 * kk[b];
 #pragma unroll
-                    for (int t = 0; t < 4; ++t) {
-                        const uint32_t v = *reinterpret_cast<const uint32_t*>(src + (int64_t)t * h.H * h.W);
-                        d[b][t] = ok ? v : fill;
-                    }
-                    hp += groups;
-                    while (hp >= h.Hp) hp -= h.Hp, ++n;
-                }
+                for (int t = 0; t < 4; ++t) d[b][t] = *reinterpret_cast<const v4i*>(src + (int64_t)t * h.H * h.W);
+            }
 #pragma unroll
-                for (int b = 0; b < ROWS; ++b) {
-                    if (rr[b] >= HR) continue;
-                    // 4 x 4 byte transpose: o[e] = channel bytes (4 cq + 0..3) of column 4 iq + e
-                    const uint32_t t01l = __builtin_amdgcn_perm(d[b][1], d[b][0], 0x05010400u);
-                    const uint32_t t01h = __builtin_amdgcn_perm(d[b][1], d[b][0], 0x07030602u);
-                    const uint32_t t23l = __builtin_amdgcn_perm(d[b][3], d[b][2], 0x05010400u);
-                    const uint32_t t23h = __builtin_amdgcn_perm(d[b][3], d[b][2], 0x07030602u);
+            for (int b = 0; b < IT; ++b) {
+                if (tid + b * 256 >= items) continue;
+                const int j0 = 16 * kk[b];
+                int ih = div_small(j0, h.W, h.inv_w), col = j0 - ih * h.W;
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {  // dword q of each channel: columns 4 q .. 4 q + 3
+                    const uint32_t t01l = __builtin_amdgcn_perm(d[b][1][q], d[b][0][q], 0x05010400u);
+                    const uint32_t t01h = __builtin_amdgcn_perm(d[b][1][q], d[b][0][q], 0x07030602u);
+                    const uint32_t t23l = __builtin_amdgcn_perm(d[b][3][q], d[b][2][q], 0x05010400u);
+                    const uint32_t t23h = __builtin_amdgcn_perm(d[b][3][q], d[b][2][q], 0x07030602u);
                     const uint32_t o[4] = {__builtin_amdgcn_perm(t23l, t01l, 0x05040100u),
                                            __builtin_amdgcn_perm(t23l, t01l, 0x07060302u),
                                            __builtin_amdgcn_perm(t23h, t01h, 0x05040100u),
                                            __builtin_amdgcn_perm(t23h, t01h, 0x07060302u)};
-                    const int pos0 = rr[b] * h.Wp + h.pl + 4 * iq_t;
-                    // column e of step k is (k + iq) & 3: neighbouring lanes (consecutive iq)
-                    // write different positions' banks in the same instruction
 #pragma unroll
-                    for (int k = 0; k < 4; ++k) {
-                        const int e = (k + iq_t) & 3;
-                        const uint32_t v = e == 0 ? o[0] : e == 1 ? o[1] : e == 2 ? o[2] : o[3];
-                        const int pos = pos0 + e;
-                        *reinterpret_cast<uint32_t*>(hal + pos * 64 + (halo_slot(pos, cq_t >> 2) << 4) + (cq_t & 3) * 4) = v;
+                    for (int e = 0; e < 4; ++e) {
+                        const int j = j0 + 4 * q + e;
+                        const int pos = (j >= b0 && j < b1) ? (rowbase + ih) * h.Wp + h.pl + col : h.dummy_pos;
+                        *reinterpret_cast<uint32_t*>(hal + pos * 64 + (halo_slot(pos, cq[b] >> 2) << 4) + (cq[b] & 3) * 4) = o[e];
+                        if (++col == h.W) col = 0, ++ih;
                     }
                 }
             }
         }
-        // padding columns: the fill code in all four chunks
-        for (int v = tid; v < HR * side * 4; v += 256) {
-            const int chunk = v & 3, cell = v >> 2;
-            const int r = cell / side, k = cell - r * side;
-            const int pos = r * h.Wp + (k < h.pl ? k : h.W + k);
-            *reinterpret_cast<v4i*>(hal + pos * 64 + (halo_slot(pos, chunk) << 4)) =
-                v4i{(int)fill, (int)fill, (int)fill, (int)fill};
+        // fill code: every position of a halo row outside the images, the padding columns of
+        // the others (16-byte chunks)
+        for (int r = 0; r < HR; ++r) {
+            const int R = R0 + r, n = div_small(R, h.Hp, h.inv_hp), hp = R - n * h.Hp;
+            const bool inside = n < h.N && hp >= h.pt && hp < h.pt + h.H;
+            const int cells = inside ? side : h.Wp;
+            for (int v = tid; v < cells * 4; v += 256) {
+                const int chunk = v & 3, k = v >> 2;
+                const int wp = inside ? (k < h.pl ? k : h.W + k) : k;
+                const int pos = r * h.Wp + wp;
+                *reinterpret_cast<v4i*>(hal + pos * 64 + (halo_slot(pos, chunk) << 4)) =
+                    v4i{(int)fill, (int)fill, (int)fill, (int)fill};
+            }
         }
         wait_vmcnt<0>();
         block_barrier();
@@ -964,17 +975,28 @@ int64_t halo_bytes_for(int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout,
                        int64_t OW) {
     if (groups != 1 || sh != 1 || sw != 1 || dh != 1 || dw != 1 || mode != LQ_PAD_ZEROS) return 0;
     // (W <= 64: the 16 channel quads x W / 4 column quads of a row fit the 256 threads)
-    if (C % 64 != 0 || Cout % 64 != 0 || W % 4 != 0 || W > 64 || KH * KW > 16 || C / 64 > 4) return 0;
+    // One block of 64 input channels: with more, the single-buffered staging of each block is
+    // exposed (ResNet layer2, C = 128: 21.8 us against 19.0 us for the packed-input kernel).
+    if (C != 64 || Cout % 64 != 0 || (H * W) % 16 != 0 || KH * KW > 16) return 0;
     const int64_t Hp = H + pt + pb, Wp = W + pl + pr, OHW = OH * OW, P = N * OHW;
-    if (OHW < 64 || P < 256) return 0;
+    if (OHW < 64 || P < 256 || N * Hp >= (1 << 24) || P >= (1 << 24)) return 0;
     int64_t hr = 0;
     for (int64_t p0 = 0; p0 < P; p0 += 256) {
         const int64_t last = std::min(p0 + 255, P - 1);
         const int64_t n0 = p0 / OHW, oh0 = (p0 - n0 * OHW) / OW;
         const int64_t n1 = last / OHW, oh1 = (last - n1 * OHW) / OW;
-        hr = std::max(hr, n1 * Hp + oh1 + KH - (n0 * Hp + oh0));
+        const int64_t R0 = n0 * Hp + oh0, R1 = n1 * Hp + oh1 + KH - 1;
+        hr = std::max(hr, R1 - R0 + 1);
+        // per image, the run of input rows must fit CV_HALO_ITEMS items per thread
+        for (int64_t n = R0 / Hp; n <= std::min(R1 / Hp, N - 1); ++n) {
+            const int64_t ihA = std::max<int64_t>(std::max<int64_t>(R0 - n * Hp, 0) - pt, 0);
+            const int64_t ihB = std::min<int64_t>(std::min<int64_t>(R1 - n * Hp, Hp - 1) - pt, H - 1);
+            if (ihA > ihB) continue;
+            const int64_t nk = ((ihB + 1) * W - 1) / 16 - (ihA * W) / 16 + 1;
+            if (nk * 16 > CV_HALO_ITEMS * 256) return 0;
+        }
     }
-    const int64_t bytes = (hr * Wp * 64 + 1023) / 1024 * 1024;
+    const int64_t bytes = (hr * Wp * 64 + 1023) / 1024 * 1024 + 1024;  // + the dummy position
     if (bytes + KH * KW * 4096 > CV_HALO_LDS) return 0;
     return bytes;
 }
@@ -1380,7 +1402,7 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
     // (integer-code outputs only: the float kinds' epilogue does not fit this kernel's
     // register budget without spilling)
     const bool halo_kind = out_kind == LQ_OUT_Q8 || out_kind == LQ_OUT_QU8 || out_kind == LQ_OUT_QU8S8;
-    const int64_t halo = (halo_kind && (reinterpret_cast<uintptr_t>(d_x) & 3) == 0 && !plan.taps && plan.Cp == C)
+    const int64_t halo = (halo_kind && (reinterpret_cast<uintptr_t>(d_x) & 15) == 0 && !plan.taps && plan.Cp == C)
                              ? halo_bytes_for(N, C, H, W, Cout, KH, KW, stride_h, stride_w, pad_top, pad_bottom,
                                               pad_left, pad_right, dilation_h, dilation_w, groups, padding_mode, OH, OW)
                              : 0;
@@ -1401,6 +1423,11 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
         hg.Hp = (int)(H + pad_top + pad_bottom); hg.Wp = (int)(W + pad_left + pad_right);
         hg.pt = pad_top; hg.pl = pad_left; hg.KH = (int)KH; hg.KW = (int)KW; hg.nc = (int)(C / 64);
         hg.halo_bytes = (int)halo;
+        hg.inv_ohw = 1.0f / (float)(OH * OW);
+        hg.inv_ow = 1.0f / (float)OW;
+        hg.inv_hp = 1.0f / (float)hg.Hp;
+        hg.inv_w = 1.0f / (float)W;
+        hg.dummy_pos = (int)((halo - 1024) / 64);
         const size_t lds = (size_t)halo + (size_t)(KH * KW) * 4096;
         const dim3 grid((unsigned)((P + 255) / 256), (unsigned)(Cout / 64));
 #define LQ_CONV_HALO(K_)                                                                                    \

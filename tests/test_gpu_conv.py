@@ -153,13 +153,14 @@ def test_conv_i8_every_out_kind(gpu, kind):
 
 
 HALO_CASES = [
-    # (N, C, H, W, Cout, KH, KW, pad): stride-1, zeros-padded convolutions with C and Cout
-    # multiples of 64 and W % 4 == 0, which take the halo-staged kernel
+    # (N, C, H, W, Cout, KH, KW, pad): stride-1, zeros-padded convolutions with C = 64, Cout a
+    # multiple of 64 and H * W % 16 == 0, which take the halo-staged kernel
     (8, 64, 56, 56, 64, 3, 3, (1, 1, 1, 1)),     # ResNet-18 layer1 at batch 8: tiles across images
-    (3, 128, 28, 28, 128, 3, 3, (1, 1, 1, 1)),   # two channel blocks, two output-channel blocks
-    (4, 256, 12, 12, 64, 3, 3, (1, 1, 1, 1)),    # four channel blocks, a tile spans 1.8 images
+    (3, 64, 28, 28, 128, 3, 3, (1, 1, 1, 1)),    # two output-channel blocks
+    (6, 64, 12, 12, 64, 3, 3, (1, 1, 1, 1)),     # a tile spans 1.8 images
     (2, 64, 12, 20, 128, 3, 3, (0, 2, 1, 1)),    # asymmetric padding, ragged last tile
-    (4, 64, 9, 8, 64, 2, 3, (1, 1, 0, 2)),       # non-square kernel, one-sided column padding
+    (4, 64, 8, 10, 64, 2, 3, (1, 1, 0, 2)),      # non-square kernel, one-sided column padding
+    (3, 64, 16, 36, 64, 3, 3, (1, 1, 1, 1)),     # rows that do not start on 16-byte chunks
 ]
 
 
@@ -193,13 +194,14 @@ def test_conv_halo_declines(gpu):
     from lucid_amd import _C
 
     rng = np.random.default_rng(77)
-    for (C, W, stride, kind) in ((64, 14, (1, 1), O.OUT_QU8S8), (64, 16, (2, 2), O.OUT_QU8S8),
-                                 (48, 16, (1, 1), O.OUT_QU8S8), (64, 16, (1, 1), O.OUT_F32)):
-        x = _codes(rng, (4, C, 16, W))
+    for (C, H, W, stride, kind) in ((64, 15, 14, (1, 1), O.OUT_QU8S8), (64, 16, 16, (2, 2), O.OUT_QU8S8),
+                                    (48, 16, 16, (1, 1), O.OUT_QU8S8), (128, 16, 16, (1, 1), O.OUT_QU8S8),
+                                    (64, 16, 16, (1, 1), O.OUT_F32)):
+        x = _codes(rng, (4, C, H, W))
         w = _codes(rng, (64, C, 3, 3), -127, 127)
         kw = dict(stride=stride, pad=(1, 1, 1, 1), out_kind=kind)
         got = run_conv(gpu, x, w, **kw)
-        assert _C.last_path() != "conv halo", (C, W, stride, kind)
+        assert _C.last_path() != "conv halo", (C, H, W, stride, kind)
         _check(got, oracle_conv(x, w, **kw), kind)
 
 
