@@ -630,19 +630,7 @@ def model_lines(L, C, gtimer, with_cpu: bool) -> dict:
         del rt, g_pre, g_dec, qdec
 
         # ---- config 5: static int8 ResNet-18, batch 32 at 224 x 224
-        import lucid_amd.quantization as Q
-        from lucid_amd.nn.layers import manual_seed
-
-        manual_seed(5)
-        rng = np.random.default_rng(5)
-        model = bc.resnet18(rng)
-        fused = Q.fuse_modules(model, bc.resnet18_fuse_groups()).to("gpu")
-        prepared = Q.prepare(fused, Q.get_minmax_qconfig())
-        for _ in range(16):
-            prepared(L.tensor(rng.standard_normal((32, 3, 224, 224)).astype(np.float32), device="gpu"))
-        qnet = Q.convert(prepared)
-        del model, fused, prepared
-        x = L.tensor(rng.standard_normal((32, 3, 224, 224)).astype(np.float32), device="gpu")
+        qnet, x = bc.static_resnet18(batch=32, calib_batches=16)
         fwd = warm_stats(lambda: qnet(x), 3, 10, sync)
         c5 = {"workload": "config 5: static int8 ResNet-18 (BN folded, per-channel int8 weights, uint8 "
                           "activations from 16 calibration batches), batch 32 at 224 x 224",

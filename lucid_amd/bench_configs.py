@@ -287,3 +287,54 @@ class Graph:
     def __del__(self) -> None:
         if getattr(self, "exe", None) is not None and _C._lib is not None:
             _C._lib.lq_graph_destroy(self.exe)
+
+
+def static_resnet18(batch: int = 32, calib_batches: int = 16, seed: int = 5):
+    """ResNet-18 with BatchNorm folded, MinMax-calibrated on
+    ``calib_batches`` random batches, converted to the static int8 layers.  Returns the
+    quantized model and one device input batch."""
+    import lucid_amd as L
+    import lucid_amd.quantization as Q
+    from lucid_amd.nn.layers import manual_seed
+
+    manual_seed(seed)
+    rng = np.random.default_rng(seed)
+    fused = Q.fuse_modules(resnet18(rng), resnet18_fuse_groups()).to("gpu")
+    prepared = Q.prepare(fused, Q.get_minmax_qconfig())
+    for _ in range(calib_batches):
+        prepared(L.tensor(rng.standard_normal((batch, 3, 224, 224)).astype(np.float32), device="gpu"))
+    qnet = Q.convert(prepared)
+    x = L.tensor(rng.standard_normal((batch, 3, 224, 224)).astype(np.float32), device="gpu")
+    return qnet, x
+
+
+def _main(argv: list[str]) -> None:
+    """``python3 -m lucid_amd.bench_configs resnet18 [forwards]``: time the configuration-5
+    forward (module dispatch included) after three warm-up forwards; a profiler run wraps it."""
+    import time
+
+    import lucid_amd as L
+    import lucid_amd.backends as backends
+
+    if not argv or argv[0] != "resnet18":
+        raise SystemExit("usage: python3 -m lucid_amd.bench_configs resnet18 [forwards]")
+    n = int(argv[1]) if len(argv) > 1 else 10
+    backends.quantized.engine = "reference"  # the per-channel int8 layers
+    qnet, x = static_resnet18(calib_batches=4)
+    for _ in range(3):
+        qnet(x)
+    L.synchronize()
+    ts = []
+    for _ in range(n):
+        t0 = time.perf_counter()
+        qnet(x)
+        L.synchronize()
+        ts.append((time.perf_counter() - t0) * 1e3)
+    ts.sort()
+    print(f"resnet18 batch 32: forward median {ts[len(ts) // 2]:.3f} ms over {n}")
+
+
+if __name__ == "__main__":
+    import sys
+
+    _main(sys.argv[1:])
