@@ -172,6 +172,19 @@ int lq_calc_qparams_f32(const float* d_min, const float* d_max, int64_t n, int s
                         int is_signed, int qmin, int qmax, float eps, float* d_scale,
                         float* d_zero_point, void* stream);
 
+/* Dynamic per-tensor activation quantization: the live range of x[n] (MinMaxObserver in
+ * replace mode), per-tensor affine qparams from it with eps (calculate_qparams,
+ * lucid/quantization/_qparams.py:186-205) and the quantize of x onto them as codes q[n] of
+ * q_dtype -- the activation step of the dynamic Linear, lucid/nn/quantized/dynamic/linear.py:
+ * 85-92.  d_qparams[0..3] receive {min, max, scale, zero point}.  The same bits as
+ * lq_minmax_f32 (LQ_OBS_REPLACE) -> lq_calc_qparams_f32 (asymmetric) ->
+ * lq_quantize_per_tensor_f32 with the device scale; one launch for n <= 16384 (workspace
+ * unused), those three otherwise (workspace of lq_dynamic_quantize_workspace_size(n) bytes). */
+size_t lq_dynamic_quantize_workspace_size(int64_t n);
+int lq_dynamic_quantize_f32(const float* d_x, int64_t n, int q_dtype, int qmin, int qmax, float eps,
+                            float* d_qparams, void* d_q, void* d_workspace, size_t workspace_bytes,
+                            void* stream);
+
 /* ---- quantize / dequantize / fake-quantize --------------------------------- */
 /* Per-tensor quantize of x[n] to codes q[n] of type q_dtype (LQ_I8, LQ_U8,
  * LQ_I16, LQ_I32 or LQ_U8S8).  Scale: if d_scale != NULL the kernel uses

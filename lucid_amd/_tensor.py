@@ -126,6 +126,19 @@ class Tensor:
         return t
 
     @classmethod
+    def _element_view(cls, base: "Tensor", index: int) -> "Tensor":
+        """A 0-d tensor sharing element ``index`` of a flat device tensor's storage."""
+        if base._device != "gpu" or base._buf is None or not 0 <= index < base.numel():
+            raise ValueError("_element_view: a materialized device tensor and an index in range")
+        t = cls()
+        t._shape = ()
+        t._dtype = base._dtype
+        t._device = "gpu"
+        t._buf = base._buf
+        t._offset = base._offset + index * base._dtype.itemsize
+        return t
+
+    @classmethod
     def _code_backed(cls, q: QuantSource, shape: Sequence[int]) -> "Tensor":
         t = cls()
         t._shape = tuple(int(s) for s in shape)

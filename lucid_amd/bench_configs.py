@@ -140,11 +140,11 @@ def decoder(rng: np.random.Generator):
 
 class DynLinear:
     """One ``nnqd.Linear`` run through the C ABI into caller buffers, allocating nothing per
-    call: ``lq_minmax_f32`` (replace) -> ``lq_calc_qparams_f32`` (per-tensor affine, the
-    module's activation grid) -> ``lq_quantize_per_tensor_f32`` (codes as c - 128) ->
-    ``lq_gemm_w8a8`` / ``lq_gemm_w8a8_packed`` (M <= 128) with ``LQ_EPI_A_U8S8``, the module's
-    weight codes, per-channel scales, cached code sums and bias, float32 out -- the launches
-    of ``nnqd.Linear.forward``."""
+    call: ``lq_dynamic_quantize_f32`` (live range, per-tensor affine qparams on the module's
+    activation grid, codes as c - 128; one launch at decode sizes) -> ``lq_gemm_w8a8`` /
+    ``lq_gemm_w8a8_packed`` (M <= 128) with ``LQ_EPI_A_U8S8``, the module's weight codes,
+    per-channel scales, cached code sums and bias, float32 out -- the launches of
+    ``nnqd.Linear.forward``."""
 
     def __init__(self, mod, max_rows: int) -> None:
         w = mod._operands()
@@ -161,7 +161,7 @@ class DynLinear:
         self.qp = empty((4,), np.float32, "gpu")  # min, max, scale, zero point
         self.codes = empty((max_rows * self.K,), np.int8, "gpu")
         lib = _C.lib()
-        self.mm_bytes = max(lib.lq_minmax_workspace_size(max_rows * self.K), 16)
+        self.mm_bytes = max(lib.lq_dynamic_quantize_workspace_size(max_rows * self.K), 16)
         self.mm_ws = empty((self.mm_bytes,), np.uint8, "gpu")
         self.g_bytes = max(max(lib.lq_gemm_w8a8_workspace_size(m, self.N, self.K) for m in (1, max_rows)), 16)
         self.g_ws = empty((self.g_bytes,), np.uint8, "gpu")
@@ -170,11 +170,8 @@ class DynLinear:
         n = rows * self.K
         q = self.qp.data_ptr()
         mn, mx, sx, zx = q, q + 4, q + 8, q + 12
-        _C.call("lq_minmax_f32", x, n, mn, mx, _C.OBS_REPLACE, 0.0, self.mm_ws.data_ptr(), self.mm_bytes, stream)
-        _C.call("lq_calc_qparams_f32", mn, mx, 1, 0, self.signed, self.qmin, self.qmax, float(np.float32(1e-8)),
-                sx, zx, stream)
-        _C.call("lq_quantize_per_tensor_f32", x, self.codes.data_ptr(), n, _C.U8S8, sx, zx, 0.0, 0.0, self.qmin,
-                self.qmax, stream)
+        _C.call("lq_dynamic_quantize_f32", x, n, _C.U8S8, self.qmin, self.qmax, float(np.float32(1e-8)), mn,
+                self.codes.data_ptr(), self.mm_ws.data_ptr(), self.mm_bytes, stream)
         common = (sx, 0, self.w.scale.data_ptr(), 1, zx, None, self.w.sums.data_ptr(),
                   self.bias.data_ptr() if self.bias is not None else None, None, None, 0, 0, _C.OUT_F32,
                   _C.EPI_A_U8S8, self.g_ws.data_ptr(), self.g_bytes, stream)

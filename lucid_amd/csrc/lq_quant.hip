@@ -862,6 +862,79 @@ static bool g4_ok(const void* f, const void* c, int64_t n) {
     return aligned16(f) && ((reinterpret_cast<uintptr_t>(c) & ca) == 0) && n < ((int64_t)1 << 32);
 }
 
+// ------------------------------------------------- dynamic activation quantization
+//
+// The dynamic Linear's activation step (lucid/nn/quantized/dynamic/linear.py:85-92): the live
+// range of x (MinMaxObserver, replace), per-tensor affine qparams from it (_qparams.py:186-205)
+// and the quantize on that grid, in one launch of one workgroup for tensors up to
+// DYN_SMALL_MAX elements (a decode step's rows).  The same device arithmetic as the
+// separate launches: extrema as ordered integer keys (order-free), the asymmetric branch of
+// calc_qparams_kernel, the reciprocal 1.0f / s and quant_one of the per-tensor quantize, so
+// the scalars and codes are the same bits.
+constexpr int64_t DYN_SMALL_MAX = 16384;  // above it, one workgroup is slower than three launches
+constexpr int kDynBlock = 1024;
+
+template <class Code>
+__global__ __launch_bounds__(kDynBlock) void dyn_quant_small_kernel(const float* __restrict__ x, int n,
+                                                                    typename Code::T* __restrict__ q,
+                                                                    float* __restrict__ qp, int qmin, float eps,
+                                                                    float width_f, Grid g, bool vec_ok) {
+    __shared__ int32_t smin[kDynBlock / 64], smax[kDynBlock / 64];
+    __shared__ float s_sz[2];
+    const int tid = threadIdx.x;
+    int32_t kmin = KEY_POS_INF, kmax = KEY_NEG_INF;
+    const int nq = vec_ok ? (n >> 2) : 0;
+    for (int i = tid; i < nq; i += kDynBlock) {
+        const vf4 v = reinterpret_cast<const vf4*>(x)[i];
+        key_accum(kmin, kmax, v.x);
+        key_accum(kmin, kmax, v.y);
+        key_accum(kmin, kmax, v.z);
+        key_accum(kmin, kmax, v.w);
+    }
+    for (int i = 4 * nq + tid; i < n; i += kDynBlock) key_accum(kmin, kmax, x[i]);
+    kmin = wave_min(kmin);
+    kmax = wave_max(kmax);
+    if ((tid & 63) == 0) {
+        smin[tid >> 6] = kmin;
+        smax[tid >> 6] = kmax;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kDynBlock / 64; ++w) {
+            kmin = min(kmin, smin[w]);
+            kmax = max(kmax, smax[w]);
+        }
+        float cmin, cmax;
+        decode_keys(kmin, kmax, cmin, cmax);
+        qp[0] = cmin;
+        qp[1] = cmax;
+        const float mn = extreme_min(cmin, 0.0f), mx = extreme_max(cmax, 0.0f);
+        const float w = mx - mn;
+        const float qq = w / width_f;
+        const float sc = extreme_max(qq, eps);
+        const float r = rne(mn / sc);
+        const float z = clip_grid((float)qmin - r, g);
+        qp[2] = sc;
+        qp[3] = z;
+        s_sz[0] = sc;
+        s_sz[1] = z;
+    }
+    __syncthreads();
+    const float sc = s_sz[0], z = s_sz[1];
+    const float inv = 1.0f / sc;
+    for (int i = tid; i < n; i += kDynBlock) q[i] = Code::store(quant_one<Code>(x[i], inv, z, g));
+}
+
+template <class Code>
+struct DynQuantSmall {
+    static int run(const float* x, int64_t n, void* q, float* qp, int qmin, float eps, float width_f, Grid g,
+                   hipStream_t st) {
+        hipLaunchKernelGGL(dyn_quant_small_kernel<Code>, dim3(1), dim3(kDynBlock), 0, st, x, (int)n,
+                           (typename Code::T*)q, qp, qmin, eps, width_f, g, aligned16(x));
+        return launch_status("lq_dynamic_quantize_f32");
+    }
+};
+
 template <class Code>
 struct QuantPt {
     static int run(const float* x, void* q, int64_t n, PtParams pp, Grid g, hipStream_t st) {
@@ -1077,6 +1150,37 @@ int lq_quantize_per_tensor_f32(const float* d_x, void* d_q, int64_t n, int q_dty
     LQ_REQUIRE(qmax >= qmin, "lq_quantize_per_tensor_f32: qmax < qmin");
     PtParams pp{d_scale, d_zero_point, inv_scale_value, 0.0f, zero_point_value};
     return dispatch_code<QuantPt>(q_dtype, d_x, d_q, n, pp, make_grid(qmin, qmax), as_stream(stream));
+}
+
+size_t lq_dynamic_quantize_workspace_size(int64_t n) {
+    if (n < 0) return 0;
+    return (n > 0 && n <= DYN_SMALL_MAX) ? 0 : lq_minmax_workspace_size(n);
+}
+
+int lq_dynamic_quantize_f32(const float* d_x, int64_t n, int q_dtype, int qmin, int qmax, float eps, float* d_qparams,
+                            void* d_q, void* d_workspace, size_t workspace_bytes, void* stream) {
+    LQ_REQUIRE(n >= 0, "lq_dynamic_quantize_f32: n < 0");
+    LQ_REQUIRE(d_qparams, "lq_dynamic_quantize_f32: NULL qparams");
+    LQ_REQUIRE(n == 0 || (d_x && d_q), "lq_dynamic_quantize_f32: NULL pointer");
+    LQ_REQUIRE(valid_code(q_dtype), "lq_dynamic_quantize_f32: bad code dtype");
+    LQ_REQUIRE(qmax > qmin, "lq_dynamic_quantize_f32: qmax <= qmin");
+    const Grid g = make_grid(qmin, qmax);
+    const float width_f = (float)(qmax - qmin);
+    hipStream_t st = as_stream(stream);
+    if (n > 0 && n <= DYN_SMALL_MAX) {
+        note_path("dynamic quantize fused");
+        return dispatch_code<DynQuantSmall>(q_dtype, d_x, n, d_q, d_qparams, qmin, eps, width_f, g, st);
+    }
+    // the separate launches: observer (replace), qparams, quantize with the device scale
+    note_path("dynamic quantize");
+    int rc = lq_minmax_f32(d_x, n, d_qparams, d_qparams + 1, LQ_OBS_REPLACE, 0.0f, d_workspace, workspace_bytes,
+                           stream);
+    if (rc) return rc;
+    rc = lq_calc_qparams_f32(d_qparams, d_qparams + 1, 1, 0, 0, qmin, qmax, eps, d_qparams + 2, d_qparams + 3,
+                             stream);
+    if (rc) return rc;
+    return lq_quantize_per_tensor_f32(d_x, d_q, n, q_dtype, d_qparams + 2, d_qparams + 3, 0.0f, 0.0f, qmin, qmax,
+                                      stream);
 }
 
 int lq_quantize_per_channel_f32(const float* d_x, void* d_q, int64_t outer, int64_t C,

@@ -2,13 +2,15 @@
 
 Per forward, Lucid measures the input range, derives per-tensor affine ``quint8`` qparams,
 fake-quantizes ``x`` onto them, dequantizes the per-channel int8 weight and runs a float
-``F.linear`` (linear.py:85-92).  Here the same forward is four device launches on one
-stream, with no host round-trip:
+``F.linear`` (linear.py:85-92).  Here the same forward runs on one stream, with no host
+round-trip:
 
-1. ``lq_minmax_f32`` (replace mode): ``x.min()``, ``x.max()`` into device scalars;
-2. ``lq_calc_qparams_f32``: ``(sx, zx)`` with Lucid's per-tensor affine rule;
-3. ``lq_quantize_per_tensor_f32``: the unsigned codes of ``x``, stored as ``c - 128``;
-4. ``lq_gemm_w8a8`` (``LQ_EPI_A_U8S8``): ``y = fl32(fl32(acc * fl32(sx * sw[n])) + b[n])``
+1. ``lq_dynamic_quantize_f32``: ``x.min()`` / ``x.max()`` (observer, replace mode), ``(sx, zx)``
+   with Lucid's per-tensor affine rule, and the codes of ``x`` (unsigned grids stored as
+   ``c - 128``) -- one launch for up to 16384 elements (a decode step), else the three
+   launches ``lq_minmax_f32`` -> ``lq_calc_qparams_f32`` -> ``lq_quantize_per_tensor_f32``,
+   with the same bits;
+2. ``lq_gemm_w8a8`` (``LQ_EPI_A_U8S8``): ``y = fl32(fl32(acc * fl32(sx * sw[n])) + b[n])``
    over the exact int32 ``acc = sum_k (qx - zx) * qw``.
 
 The float32 output equals Lucid's float composition up to the float GEMM's summation
@@ -30,6 +32,9 @@ from lucid_amd.quantization._gemm import gemm_w8a8, gemv_w8
 from lucid_amd.quantization._qparams import calculate_qparams
 from lucid_amd.quantization._qscheme import (QDtype, per_channel_symmetric, per_tensor_affine,
                                              qint8, quint8)
+
+
+_EPS = float(np.float32(1e-8))  # calculate_qparams' default eps, as the float32 kernels read it
 
 
 def dynamic_qparams(x: Tensor, qdtype: QDtype) -> tuple[Tensor, Tensor]:
@@ -66,23 +71,25 @@ class Linear(_WeightedQuantized):
             raise TypeError(f"dynamic Linear: float32 input expected, got {x.dtype}")
         self._device_buffers()
         qd = self.act_qdtype
-        x_scale, x_zp = dynamic_qparams(x, qd)
         if self.weight_int8.dtype == np.int8 and qd.quant_min >= 0 and qd.quant_max <= 255:
             code_type = _C.U8S8
         elif self.weight_int8.dtype == np.int8 and qd.quant_min >= -128 and qd.quant_max <= 127:
             code_type = _C.I8
         else:  # a grid wider than 8 bits: Lucid's float composition on the device
+            x_scale, x_zp = dynamic_qparams(x, qd)
             x_q = fake_quantize(x, x_scale, x_zp, qd.quant_min, qd.quant_max)
             if self.weight_int8.dtype == np.int8:
                 return gemv_w8(x_q, self._operands(), self.bias)
             return F.linear(x_q, self._dequantized_weight(), self.bias)
+        n = x.numel()
+        qp = empty((4,), float32, "gpu")  # min, max, scale, zero point
         codes = empty(x.shape, np.int8, "gpu")
-        if x.numel():
-            _C.call("lq_quantize_per_tensor_f32", x.data_ptr(), codes.data_ptr(), x.numel(),
-                    code_type, x_scale.data_ptr(), x_zp.data_ptr(), 0.0, 0.0, qd.quant_min,
-                    qd.quant_max, None)
-        return gemm_w8a8(codes, code_type, x_scale, x_zp, self._operands(), self.bias,
-                         _C.OUT_F32)
+        ws = _C.lib().lq_dynamic_quantize_workspace_size(n)
+        _C.call("lq_dynamic_quantize_f32", x.data_ptr() if n else None, n, code_type, qd.quant_min,
+                qd.quant_max, _EPS, qp.data_ptr(), codes.data_ptr() if n else None,
+                workspace.get(ws) if ws else None, ws, None)
+        return gemm_w8a8(codes, code_type, Tensor._element_view(qp, 2), Tensor._element_view(qp, 3),
+                         self._operands(), self.bias, _C.OUT_F32)
 
     @classmethod
     def from_float(cls, mod: Module, dtype: QDtype = qint8) -> "Linear":

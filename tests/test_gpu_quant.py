@@ -282,3 +282,90 @@ def test_observer_state_dict_round_trip(gpu):
     fresh = Q.PerChannelMinMaxObserver(ch_axis=0)
     fresh.load_state_dict(pc.state_dict())
     np.testing.assert_array_equal(fresh.min_val.numpy(), [0, 3, 6, 9])
+
+
+# ------------------------------------------------------ dynamic activation quantization
+
+
+def _dyn_inputs(n, seed):
+    rng = np.random.default_rng(seed)
+    x = (rng.standard_normal(n) * 3).astype(np.float32)
+    if n > 8:
+        x[3] = np.float32(-0.0)
+        x[n // 2] *= np.float32(40.0)  # an outlier sets the range
+    return x
+
+
+@pytest.mark.parametrize("n", [1, 5, 4096, 4097, 16384, 16385, 300000])
+@pytest.mark.parametrize("grid", [(0, 255, "U8S8"), (-128, 127, "I8")])
+def test_dynamic_quantize_matches_separate_calls(gpu, n, grid):
+    """lq_dynamic_quantize_f32 (one launch up to 16384 elements, three above) against the
+    observer -> qparams -> quantize launches it replaces, and against the oracle: the min, max,
+    scale, zero point and every code the same bits."""
+    from lucid_amd import _C
+
+    qmin, qmax, ct = grid
+    code_type = getattr(_C, ct)
+    x = _dyn_inputs(n, n + abs(qmin))
+    xd = gpu.tensor(x, device="gpu")
+    eps = float(np.float32(1e-8))
+    qp = gpu.empty((4,), np.float32, "gpu")
+    codes = gpu.empty((n,), np.int8, "gpu")
+    ws_bytes = _C.lib().lq_dynamic_quantize_workspace_size(n)
+    ws = gpu.empty((max(ws_bytes, 16),), np.uint8, "gpu")
+    _C.call("lq_dynamic_quantize_f32", xd.data_ptr(), n, code_type, qmin, qmax, eps, qp.data_ptr(),
+            codes.data_ptr(), ws.data_ptr(), ws_bytes, None)
+    gpu.synchronize()
+    assert _C.last_path() == ("dynamic quantize fused" if n <= 16384 else "dynamic quantize")
+    # the separate launches
+    qp2 = gpu.empty((4,), np.float32, "gpu")
+    codes2 = gpu.empty((n,), np.int8, "gpu")
+    mm_bytes = _C.lib().lq_minmax_workspace_size(n)
+    mm = gpu.empty((mm_bytes,), np.uint8, "gpu")
+    p = qp2.data_ptr()
+    _C.call("lq_minmax_f32", xd.data_ptr(), n, p, p + 4, _C.OBS_REPLACE, 0.0, mm.data_ptr(), mm_bytes, None)
+    _C.call("lq_calc_qparams_f32", p, p + 4, 1, 0, int(qmin < 0), qmin, qmax, eps, p + 8, p + 12, None)
+    _C.call("lq_quantize_per_tensor_f32", xd.data_ptr(), codes2.data_ptr(), n, code_type, p + 8, p + 12, 0.0, 0.0,
+            qmin, qmax, None)
+    a, b = qp.numpy(), qp2.numpy()
+    np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
+    np.testing.assert_array_equal(codes.numpy(), codes2.numpy())
+    # the oracle
+    mn, mx = O.minmax(x, mode=O.OBS_REPLACE)
+    s, z = O.calc_qparams(mn, mx, False, qmin < 0, qmin, qmax)
+    want = O.quantize(x, O.recip_tensor(np.array([s], np.float32))[0], z, qmin, qmax,
+                      O.U8S8 if ct == "U8S8" else O.I8)
+    np.testing.assert_array_equal(a.view(np.uint32), np.array([mn, mx, s, z], np.float32).view(np.uint32))
+    np.testing.assert_array_equal(codes.numpy(), want.astype(np.int8))
+
+
+def test_dynamic_quantize_edge_ranges(gpu):
+    """Zero range (all equal), negative-only, NaN and infinities: the fused launch against the
+    separate ones."""
+    from lucid_amd import _C
+
+    eps = float(np.float32(1e-8))
+    cases = [np.full(100, 1.5, np.float32), -np.abs(_dyn_inputs(777, 1)), np.zeros(64, np.float32),
+             np.array([1.0, np.nan, -2.0, 3.0] * 50, np.float32), np.array([np.inf, -1.0, 2.0] * 30, np.float32)]
+    for x in cases:
+        n = x.size
+        xd = gpu.tensor(x, device="gpu")
+        out = []
+        for fused in (True, False):
+            qp = gpu.empty((4,), np.float32, "gpu")
+            codes = gpu.empty((n,), np.int8, "gpu")
+            if fused:
+                _C.call("lq_dynamic_quantize_f32", xd.data_ptr(), n, _C.U8S8, 0, 255, eps, qp.data_ptr(),
+                        codes.data_ptr(), None, 0, None)
+            else:
+                mm_bytes = _C.lib().lq_minmax_workspace_size(n)
+                mm = gpu.empty((mm_bytes,), np.uint8, "gpu")
+                p = qp.data_ptr()
+                _C.call("lq_minmax_f32", xd.data_ptr(), n, p, p + 4, _C.OBS_REPLACE, 0.0, mm.data_ptr(), mm_bytes,
+                        None)
+                _C.call("lq_calc_qparams_f32", p, p + 4, 1, 0, 0, 0, 255, eps, p + 8, p + 12, None)
+                _C.call("lq_quantize_per_tensor_f32", xd.data_ptr(), codes.data_ptr(), n, _C.U8S8, p + 8, p + 12,
+                        0.0, 0.0, 0, 255, None)
+            out.append((qp.numpy(), codes.numpy()))
+        np.testing.assert_array_equal(out[0][0].view(np.uint32), out[1][0].view(np.uint32))
+        np.testing.assert_array_equal(out[0][1], out[1][1])
