@@ -34,6 +34,10 @@ int check_hip(hipError_t e, const char* what);
 // lq_last_path() on the same thread: tests assert which instantiation a shape reaches.
 void note_path(const char* path);
 
+// Compute units of the current device (queried once per device, then cached): the grid
+// size of persistent kernels that walk their work items in a loop.
+int device_cu_count();
+
 inline int launch_status(const char* what) {
     hipError_t e = hipGetLastError();
     if (e != hipSuccess) return check_hip(e, what);

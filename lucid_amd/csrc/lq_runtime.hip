@@ -26,6 +26,22 @@ int set_error(int code, const std::string& msg) {
     return code;
 }
 
+int device_cu_count() {
+    constexpr int kMaxDevices = 64;
+    static int counts[kMaxDevices];  // 0 = not queried yet; racing first queries store the same value
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 256;
+    if (dev >= kMaxDevices) {
+        int n = 0;
+        return hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+    }
+    int n = __atomic_load_n(&counts[dev], __ATOMIC_RELAXED);
+    if (n > 0) return n;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    __atomic_store_n(&counts[dev], n, __ATOMIC_RELAXED);
+    return n;
+}
+
 int check_hip(hipError_t e, const char* what) {
     std::string m = std::string(what) + ": " + hipGetErrorName(e) + " (" + hipGetErrorString(e) + ")";
     return set_error(e == hipErrorOutOfMemory ? LQ_ERR_NOMEM : LQ_ERR_HIP, m);

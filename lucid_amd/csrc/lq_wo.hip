@@ -717,6 +717,12 @@ __global__ __launch_bounds__(256) void wo_sk_reduce_kernel(WoSkArgs sk, int grou
 // byte select) and accumulates in fp32 with FMA.  A 64-lane shuffle reduction finishes each
 // row.  The LDS copy of x is swizzled (16-byte slot f of a 256-byte row stored at
 // f ^ ... rotated by f >> 4) so the 64 lanes' float4 reads of their chunks are conflict-free.
+// One activation row, per-channel weights, K <= 256 * 16 codes (wv_persistent): the grid is
+// persistent (at most one workgroup per CU): wave w of workgroup b takes rows gw, gw + S, ...
+// (gw = b * waves + w, S = all waves of the grid), staging x once per workgroup, and loads the
+// next row's chunks before it reduces the current one.  Each row's arithmetic is the same as
+// with one row per wave (same bits).  The other forms keep one row per wave: a second row's
+// chunks in flight would not fit their registers.
 
 struct WvArgs {
     const void* x;
@@ -744,11 +750,21 @@ __device__ __forceinline__ int wv_slot(int k) {
     return (((f & ~15) | ((f + (f >> 4)) & 15)) << 2) | (k & 3);
 }
 
+// Staged activation index 4 * i -> (row m, element k) of the [MX][Kpad] copy, MX <= 2: a
+// compare instead of an integer division by the runtime Kpad.
+template <int MX>
+__device__ __forceinline__ int wv_row(int e4, int Kpad) {
+    static_assert(MX == 1 || MX == 2, "one or two activation rows");
+    return MX == 2 && e4 >= Kpad ? 1 : 0;
+}
+
 __device__ __forceinline__ uint32_t opaque_and(uint32_t v, uint32_t m) {
     uint32_t r;
     __asm__("v_and_b32 %0, %1, %2" : "=v"(r) : "v"(v), "v"(m));
     return r;
 }
+
+constexpr bool wv_persistent(bool grouped, int mx, int j) { return !grouped && mx == 1 && j <= 4; }
 
 template <int BITS, bool SIGNED, bool GROUPED, int MX, bool XF32, int J>
 __global__ __launch_bounds__(1024) void wo_gemv_valu_kernel(WvArgs a) {
@@ -756,27 +772,31 @@ __global__ __launch_bounds__(1024) void wo_gemv_valu_kernel(WvArgs a) {
     extern __shared__ __attribute__((aligned(16))) float wv_lds[];
     float* xs = wv_lds;                                   // [MX][Kpad], swizzled
     float* gsum = xs + MX * a.Kpad;                       // [MX][G] (group-wise) or [MX] totals
+    constexpr bool PF = wv_persistent(GROUPED, MX, J);  // rows in a loop, the next one prefetched
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int waves = blockDim.x >> 6;
-    const int n = blockIdx.x * waves + wave;
-    const bool n_ok = n < a.N;
-    const uint8_t* row = a.w + (int64_t)min(n, a.N - 1) * a.ldw_bytes;
+    const int gw = blockIdx.x * waves + wave;  // this wave's first row
+    const int wstride = gridDim.x * waves;
 
-    // every chunk load at once, before the activation staging so the two latencies overlap
-    // (clamped to the row; chunks past the row meet zero x)
+    // every chunk load of a row at once (clamped to the row; chunks past the row meet zero x)
+    auto load_row = [&](int n, vu4* w, float* sgv, float* bgv) {
+        const uint8_t* row = a.w + (int64_t)n * a.ldw_bytes;
+#pragma unroll
+        for (int j = 0; j < J; ++j) {
+            const int c = min(lane + 64 * j, a.NC - 1);
+            w[j] = __builtin_nontemporal_load(reinterpret_cast<const vu4*>(row) + c);
+            if constexpr (GROUPED) {
+                const int64_t gi = (int64_t)n * a.G + min((lane + 64 * j) * CK / a.gs, a.G - 1);
+                sgv[j] = a.w_scale[gi];
+                bgv[j] = a.g_bias ? a.g_bias[gi] : 0.0f;
+            }
+        }
+    };
+    // the first row's loads go out before the activation staging so the two latencies overlap
     vu4 wc[J];
     float sg[GROUPED ? J : 1], bg[GROUPED ? J : 1];
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const int c = min(lane + 64 * j, a.NC - 1);
-        wc[j] = __builtin_nontemporal_load(reinterpret_cast<const vu4*>(row) + c);
-        if constexpr (GROUPED) {
-            const int64_t gi = (int64_t)min(n, a.N - 1) * a.G + min((lane + 64 * j) * CK / a.gs, a.G - 1);
-            sg[j] = a.w_scale[gi];
-            bg[j] = a.g_bias ? a.g_bias[gi] : 0.0f;
-        }
-    }
+    load_row(min(gw, a.N - 1), wc, sg, bg);
     __builtin_amdgcn_sched_barrier(0);
 
     // Activation staging in groups of four consecutive k (one 16-byte LDS slot; Kpad is a
@@ -790,7 +810,7 @@ __global__ __launch_bounds__(1024) void wo_gemv_valu_kernel(WvArgs a) {
 #pragma unroll
         for (int u = 0; u < XU; ++u) {
             const int i = base + u * (int)blockDim.x + tid;
-            const int m = (4 * i) / a.Kpad, k = (4 * i) - m * a.Kpad;
+            const int m = wv_row<MX>(4 * i, a.Kpad), k = (4 * i) - m * a.Kpad;
             vf4 v = vf4{0.0f, 0.0f, 0.0f, 0.0f};
             if (i < nq && m < a.M && k < a.K) {
                 const int64_t o = (int64_t)m * a.ldx + k;
@@ -818,7 +838,7 @@ __global__ __launch_bounds__(1024) void wo_gemv_valu_kernel(WvArgs a) {
         for (int u = 0; u < XU; ++u) {
             const int i = base + u * (int)blockDim.x + tid;
             if (i < nq) {
-                const int m = (4 * i) / a.Kpad, k = (4 * i) - m * a.Kpad;
+                const int m = wv_row<MX>(4 * i, a.Kpad), k = (4 * i) - m * a.Kpad;
                 *reinterpret_cast<vf4*>(xs + m * a.Kpad + wv_slot(k)) = xv4[u];
             }
         }
@@ -834,7 +854,7 @@ __global__ __launch_bounds__(1024) void wo_gemv_valu_kernel(WvArgs a) {
             const int i = i0 + tid;
             float v = 0.0f;
             if (i < MX * a.Kpad / 4) {
-                const int m = (4 * i) / a.Kpad, k = (4 * i) % a.Kpad;
+                const int m = wv_row<MX>(4 * i, a.Kpad), k = (4 * i) - m * a.Kpad;
                 const vf4 q = *reinterpret_cast<const vf4*>(xs + m * a.Kpad + wv_slot(k));
                 v = (q[0] + q[1]) + (q[2] + q[3]);
             }
@@ -844,7 +864,7 @@ __global__ __launch_bounds__(1024) void wo_gemv_valu_kernel(WvArgs a) {
                 for (int off = 1; off < 64; off <<= 1)
                     if (off < per) v += __shfl_xor(v, off, 64);
                 if (i < MX * a.Kpad / 4 && (i % per) == 0) {
-                    const int m = (4 * i) / a.Kpad, k = (4 * i) % a.Kpad;
+                    const int m = wv_row<MX>(4 * i, a.Kpad), k = (4 * i) - m * a.Kpad;
                     if (k < a.K) gsum[m * a.G + k / a.gs] = v;  // Kpad is a multiple of gs
                 }
             } else {
@@ -852,7 +872,7 @@ __global__ __launch_bounds__(1024) void wo_gemv_valu_kernel(WvArgs a) {
                 for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
                 // a wave's 64 partials lie in one row (Kpad is a multiple of 256)
                 if (lane == 0 && i0 + wave * 64 < MX * a.Kpad / 4) {
-                    const int m = (4 * (i0 + wave * 64)) / a.Kpad;
+                    const int m = wv_row<MX>(4 * (i0 + wave * 64), a.Kpad);
                     const int slot = (i0 / (int)blockDim.x) * waves + wave;
                     wsum[slot * MX + m] = v;  // distinct slot per (pass, wave); zero for other rows below
                 }
@@ -865,88 +885,103 @@ __global__ __launch_bounds__(1024) void wo_gemv_valu_kernel(WvArgs a) {
                 float t = 0.0f;
                 for (int sidx = 0; sidx < passes * waves; ++sidx) {
                     const int i = (sidx / waves) * blockDim.x + (sidx % waves) * 64;
-                    if (i < MX * a.Kpad / 4 && (4 * i) / a.Kpad == tid) t += wsum[sidx * MX + tid];
+                    if (i < MX * a.Kpad / 4 && wv_row<MX>(4 * i, a.Kpad) == tid) t += wsum[sidx * MX + tid];
                 }
                 gsum[tid] = t;
             }
         }
         __syncthreads();
     }
-    if (!n_ok) return;
+    if (gw >= a.N) return;
 
-    float acc[MX];
+    for (int n = gw; n < a.N; n += wstride) {
+        const int nn = n + wstride;
+        const bool more = PF && nn < a.N;  // wave-uniform
+        vu4 wn[PF ? J : 1];
+        float sgn[PF && GROUPED ? J : 1], bgn[PF && GROUPED ? J : 1];
+        if (more) load_row(nn, wn, sgn, bgn);
+        float acc[MX];
 #pragma unroll
-    for (int m = 0; m < MX; ++m) acc[m] = 0.0f;
+        for (int m = 0; m < MX; ++m) acc[m] = 0.0f;
 #pragma unroll
-    for (int j = 0; j < J; ++j) {
-        const int c = lane + 64 * j;
-        const int k0 = c * CK;
-        float p[MX];
+        for (int j = 0; j < J; ++j) {
+            const int c = lane + 64 * j;
+            const int k0 = c * CK;
+            float p[MX];
 #pragma unroll
-        for (int m = 0; m < MX; ++m) p[m] = 0.0f;
+            for (int m = 0; m < MX; ++m) p[m] = 0.0f;
 #pragma unroll
-        for (int wi = 0; wi < 4; ++wi) {
-            const uint32_t wd = wc[j][wi];
-            float code[32 / BITS];
-            if constexpr (BITS == 8) {
+            for (int wi = 0; wi < 4; ++wi) {
+                const uint32_t wd = wc[j][wi];
+                float code[32 / BITS];
+                if constexpr (BITS == 8) {
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    code[e] = SIGNED ? (float)(signed char)(wd >> (8 * e)) : (float)((wd >> (8 * e)) & 0xFFu);
+                    for (int e = 0; e < 4; ++e)
+                        code[e] = SIGNED ? (float)(signed char)(wd >> (8 * e)) : (float)((wd >> (8 * e)) & 0xFFu);
+                } else {
+                    const uint32_t lo = opaque_and(wd, 0x0F0F0F0Fu);
+                    const uint32_t hi = opaque_and(wd >> 4, 0x0F0F0F0Fu);
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        code[2 * e] = (float)((lo >> (8 * e)) & 0xFFu);
+                        code[2 * e + 1] = (float)((hi >> (8 * e)) & 0xFFu);
+                    }
+                }
+                const int kw = k0 + wi * (32 / BITS);
+#pragma unroll
+                for (int m = 0; m < MX; ++m) {
+#pragma unroll
+                    for (int f = 0; f < 32 / BITS; f += 4) {
+                        const vf4 xv = *reinterpret_cast<const vf4*>(xs + m * a.Kpad + wv_slot(kw + f));
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) p[m] = fmaf(code[f + e], xv[e], p[m]);
+                    }
+                }
+            }
+            if constexpr (GROUPED) {
+                const bool first = c < a.NC && (k0 % a.gs) == 0;
+                const int g = min(k0 / a.gs, a.G - 1);
+#pragma unroll
+                for (int m = 0; m < MX; ++m) {
+                    acc[m] = fmaf(sg[j], p[m], acc[m]);
+                    if (first) acc[m] = fmaf(bg[j], gsum[m * a.G + g], acc[m]);
+                }
             } else {
-                const uint32_t lo = opaque_and(wd, 0x0F0F0F0Fu);
-                const uint32_t hi = opaque_and(wd >> 4, 0x0F0F0F0Fu);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    code[2 * e] = (float)((lo >> (8 * e)) & 0xFFu);
-                    code[2 * e + 1] = (float)((hi >> (8 * e)) & 0xFFu);
-                }
-            }
-            const int kw = k0 + wi * (32 / BITS);
-#pragma unroll
-            for (int m = 0; m < MX; ++m) {
-#pragma unroll
-                for (int f = 0; f < 32 / BITS; f += 4) {
-                    const vf4 xv = *reinterpret_cast<const vf4*>(xs + m * a.Kpad + wv_slot(kw + f));
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) p[m] = fmaf(code[f + e], xv[e], p[m]);
-                }
+                for (int m = 0; m < MX; ++m) acc[m] += p[m];
             }
         }
-        if constexpr (GROUPED) {
-            const bool first = c < a.NC && (k0 % a.gs) == 0;
-            const int g = min(k0 / a.gs, a.G - 1);
-#pragma unroll
-            for (int m = 0; m < MX; ++m) {
-                acc[m] = fmaf(sg[j], p[m], acc[m]);
-                if (first) acc[m] = fmaf(bg[j], gsum[m * a.G + g], acc[m]);
-            }
-        } else {
-#pragma unroll
-            for (int m = 0; m < MX; ++m) acc[m] += p[m];
-        }
-    }
-#pragma unroll
-    for (int m = 0; m < MX; ++m) {
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) acc[m] += __shfl_xor(acc[m], off, 64);
-    }
-    if (lane == 0) {
 #pragma unroll
         for (int m = 0; m < MX; ++m) {
-            if (m >= a.M) break;
-            float v = acc[m];
-            if constexpr (!GROUPED) {
-                if (a.w_zp) v = v - a.w_zp[n] * gsum[m];
-                v = a.w_scale[n] * v;
-            }
-            if (a.bias) v = v + a.bias[n];
-            if (a.relu && v <= 0.0f) v = 0.0f;
-            if constexpr (XF32)
-                reinterpret_cast<float*>(a.y)[(int64_t)m * a.ldy + n] = v;
-            else
-                reinterpret_cast<_Float16*>(a.y)[(int64_t)m * a.ldy + n] = (_Float16)v;
+#pragma unroll
+            for (int off = 32; off > 0; off >>= 1) acc[m] += __shfl_xor(acc[m], off, 64);
         }
-    }
+        if (lane == 0) {
+#pragma unroll
+            for (int m = 0; m < MX; ++m) {
+                if (m >= a.M) break;
+                float v = acc[m];
+                if constexpr (!GROUPED) {
+                    if (a.w_zp) v = v - a.w_zp[n] * gsum[m];
+                    v = a.w_scale[n] * v;
+                }
+                if (a.bias) v = v + a.bias[n];
+                if (a.relu && v <= 0.0f) v = 0.0f;
+                if constexpr (XF32)
+                    reinterpret_cast<float*>(a.y)[(int64_t)m * a.ldy + n] = v;
+                else
+                    reinterpret_cast<_Float16*>(a.y)[(int64_t)m * a.ldy + n] = (_Float16)v;
+            }
+        }
+        if constexpr (!PF) break;  // one row per wave (the grid covers every row)
+        if (more) {
+#pragma unroll
+            for (int j = 0; j < J; ++j) {
+                wc[j] = wn[j];
+                if constexpr (GROUPED) sg[j] = sgn[j], bg[j] = bgn[j];
+            }
+        }
+    }  // rows of this wave
 }
 
 // ------------------------------------------------- group-wise quantize / dequantize
@@ -1305,7 +1340,9 @@ bool launch_wv(WvArgs a, bool xf32, hipStream_t st) {
     const size_t lds = sizeof(float) * ((size_t)MX * a.Kpad +
                                         (GROUPED ? (size_t)MX * a.G : (size_t)MX + passes * waves * MX));
     if (lds > 64 * 1024) return false;
-    const dim3 grid((unsigned)((a.N + waves - 1) / waves));
+    const int64_t row_groups = (a.N + waves - 1) / waves;
+    const bool persist = wv_persistent(GROUPED, MX, J);  // at most one workgroup per CU
+    const dim3 grid((unsigned)(persist ? std::min<int64_t>(row_groups, device_cu_count()) : row_groups));
     const dim3 block(64 * waves);
     // (instantiated only for the chunk counts whose registers fit: group scales of 12+ chunks,
     // or of 8 chunks at 4 bits and two rows, would spill)

@@ -76,6 +76,25 @@ def test_gemv_w8_fp32(gpu, M, N, K):
     _close(got, ref)
 
 
+@pytest.mark.parametrize("K", [4096, 1008])
+def test_gemv_w8_row_loop_is_bit_identical(gpu, K):
+    """One activation row with per-channel weights runs a persistent grid: a wave takes rows
+    gw, gw + S, ... (S = every wave of the grid).  Row r's arithmetic must not depend on which
+    wave or which pass takes it: the rows of an 11008-row call equal, bit for bit, the same rows
+    computed in calls over 4096-row slices (one row per wave) and over a 1000-row slice
+    (K = 1008: one 16-byte chunk per lane)."""
+    rng = np.random.default_rng(K + 7)
+    x = rng.standard_normal((1, K)).astype(np.float32)
+    W = rng.integers(-128, 128, (11008, K)).astype(np.int8)
+    s = rng.uniform(1e-3, 1e-1, 11008).astype(np.float32)
+    b = rng.standard_normal(11008).astype(np.float32)
+    full = run_gemv(gpu, x, W, s, b=b, relu=True)
+    for lo, hi in ((0, 4096), (4096, 8192), (8192, 11008), (5000, 6000)):
+        part = run_gemv(gpu, x, W[lo:hi], s[lo:hi], b=b[lo:hi], relu=True)
+        np.testing.assert_array_equal(full[:, lo:hi].view(np.uint32), part.view(np.uint32))
+    _close(full, _gemv_ref(x, W, s, b=b, relu=True))
+
+
 @pytest.mark.parametrize("M,N,K", [(4, 256, 784), (16, 1024, 4096), (1, 64, 1000)])
 def test_gemv_w8_zero_point_relu_and_ldw(gpu, M, N, K):
     rng = np.random.default_rng(7 + M)
