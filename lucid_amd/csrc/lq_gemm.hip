@@ -1110,18 +1110,28 @@ __global__ __launch_bounds__(256) void gemm_i8_decode_reduce_kernel(GemmArgs a, 
     if (q >= (int64_t)a.M * quads) return;
     const int m = (int)(q / quads), n = (int)(q - (int64_t)m * quads) * 4;
     if (n >= a.N) return;
-    // eight splits' loads in flight at a time (integer sums: exact in any order)
+    // the epilogue's inputs are loaded with the partial sums, not after them (one round trip)
+    const EpiParams p = epi_params(a);
+    const RowCtx row = load_row(a, m);
+    const ColCtx cols = load_cols<KIND>(a, n);
+    // U splits' loads in flight at a time, none past the last split (integer sums: exact in
+    // any order)
     v4i acc = v4i{0, 0, 0, 0};
-    for (int s0 = 0; s0 < splits; s0 += 8) {
-        v4i v[8];
+    auto add_splits = [&](auto uc) {
+        constexpr int U = decltype(uc)::value;
+        for (int s0 = 0; s0 < splits; s0 += U) {
+            v4i v[U];
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            v[u] = *reinterpret_cast<const v4i*>(part + ((int64_t)min(s0 + u, splits - 1) * a.M + m) * npad + n);
+            for (int u = 0; u < U; ++u)
+                v[u] = s0 + u < splits ? *reinterpret_cast<const v4i*>(part + ((int64_t)(s0 + u) * a.M + m) * npad + n)
+                                       : v4i{0, 0, 0, 0};
 #pragma unroll
-        for (int u = 0; u < 8; ++u)
-            if (s0 + u < splits) acc += v[u];
-    }
-    epilogue4<KIND>(a, epi_params(a), m, n, acc);
+            for (int u = 0; u < U; ++u) acc += v[u];
+        }
+    };
+    if (splits <= 4) add_splits(std::integral_constant<int, 4>());
+    else add_splits(std::integral_constant<int, 8>());
+    epilogue4c<KIND>(a, p, row, cols, m, acc);
 }
 
 template <int KIND>

@@ -669,6 +669,15 @@ __global__ __launch_bounds__(256) void wo_sk_reduce_kernel(WoSkArgs sk, int grou
     const int64_t gt = g >> 6;  // group * SK_TILES + tile
     const int n0 = (int)(gt * 16);
     if (n0 >= a.N || l16 >= a.M) return;
+    // the epilogue's per-column inputs are loaded with the partial sums, not after them
+    float wsc[4], wzp[4], wbi[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const int n = min(n0 + 4 * q + i, a.N - 1);  // clamped: columns past N are never stored
+        wsc[i] = GROUPED ? 1.0f : a.w_scale[n];
+        wzp[i] = (!GROUPED && a.w_zp) ? a.w_zp[n] : 0.0f;
+        wbi[i] = a.bias ? a.bias[n] : 0.0f;
+    }
     f4 acc = f4{0.f, 0.f, 0.f, 0.f};
     float xtot = 0.0f;
     // eight ranges' loads in flight, then their sums in range order
@@ -694,10 +703,10 @@ __global__ __launch_bounds__(256) void wo_sk_reduce_kernel(WoSkArgs sk, int grou
         if (n < a.N) {
             float v = acc[i];
             if constexpr (!GROUPED) {
-                if (a.w_zp) v = v - a.w_zp[n] * xtot;
-                v = a.w_scale[n] * v;
+                if (a.w_zp) v = v - wzp[i] * xtot;
+                v = wsc[i] * v;
             }
-            if (a.bias) v = v + a.bias[n];
+            if (a.bias) v = v + wbi[i];
             if (a.relu && v <= 0.0f) v = 0.0f;
             if constexpr (XF32)
                 reinterpret_cast<float*>(a.y)[(int64_t)l16 * a.ldy + n] = v;
