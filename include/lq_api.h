@@ -577,6 +577,12 @@ int lq_embedding_sum_f32(const float* d_tok_table, int64_t vocab, const float* d
  * biased variance); rows ldx / ldy elements apart. */
 int lq_layer_norm_f32(const float* d_x, int64_t ldx, float* d_y, int64_t ldy, int64_t rows, int64_t D,
                       const float* d_gamma, const float* d_beta, float eps, void* stream);
+/* x = x + res, then y = lq_layer_norm_f32(x) per row (a pre-norm block's residual add fused with
+ * the next norm: the same bits as lq_add_f32 followed by lq_layer_norm_f32, one launch); rows
+ * ldx / ldres / ldy elements apart, y must not overlap x or res. */
+int lq_add_layer_norm_f32(float* d_x, int64_t ldx, const float* d_res, int64_t ldres, float* d_y, int64_t ldy,
+                          int64_t rows, int64_t D, const float* d_gamma, const float* d_beta, float eps,
+                          void* stream);
 /* y = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) (F.gelu, approximate="tanh"). */
 int lq_gelu_tanh_f32(const float* d_x, float* d_y, int64_t n, void* stream);
 /* y = a + b elementwise (residual adds). */

@@ -116,6 +116,7 @@ _SIGNATURES: dict[str, tuple] = {
                                   _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P]),
     "lq_embedding_sum_f32": (_I, [_P, _I64, _P, _I64, _I64, _P, _I64, _I64, _I64, _P, _P, _P]),
     "lq_layer_norm_f32": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P, _F, _P]),
+    "lq_add_layer_norm_f32": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _P, _F, _P]),
     "lq_gelu_tanh_f32": (_I, [_P, _P, _I64, _P]),
     "lq_add_f32": (_I, [_P, _P, _P, _I64, _P]),
     "lq_add_scaled_f32": (_I, [_P, _P, _F, _P, _I64, _P]),

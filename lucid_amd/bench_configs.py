@@ -224,20 +224,24 @@ class Int8Decoder:
         h, hn = self.h.data_ptr(), self.hn.data_ptr()
         _C.call("lq_embedding_sum_f32", self.tok.data_ptr(), self.V, self.posemb.data_ptr(), self.npos, D, tokens,
                 M, n, 0, p, h, stream)
-        for (qkv, out, up, down), (kc, vc) in zip(self.layers, self.cache):
-            _C.call("lq_layer_norm_f32", h, D, hn, D, M, D, None, None, np.float32(1e-5), stream)
+        proj, eps = self.proj.data_ptr(), np.float32(1e-5)
+        for li, ((qkv, out, up, down), (kc, vc)) in enumerate(zip(self.layers, self.cache)):
+            # each residual add that a norm follows runs inside that norm's launch (same bits)
+            if li == 0:
+                _C.call("lq_layer_norm_f32", h, D, hn, D, M, D, None, None, eps, stream)
+            else:
+                _C.call("lq_add_layer_norm_f32", h, D, proj, D, hn, D, M, D, None, None, eps, stream)
             qkv(hn, M, self.qkv.data_ptr(), stream)
             _C.call("lq_kv_append_f16", self.qkv.data_ptr(), B, n, H, hd, 0, p, self.Tmax, self.q16.data_ptr(),
                     kc.data_ptr(), vc.data_ptr(), stream)
             _C.call("lq_attention_f16", self.q16.data_ptr(), kc.data_ptr(), vc.data_ptr(), B, H, n, hd, 0, p,
                     self.Tmax, np.float32(self.scale), self.att.data_ptr(), stream)
-            out(self.att.data_ptr(), M, self.proj.data_ptr(), stream)
-            _C.call("lq_add_f32", h, self.proj.data_ptr(), h, M * D, stream)
-            _C.call("lq_layer_norm_f32", h, D, hn, D, M, D, None, None, np.float32(1e-5), stream)
+            out(self.att.data_ptr(), M, proj, stream)
+            _C.call("lq_add_layer_norm_f32", h, D, proj, D, hn, D, M, D, None, None, eps, stream)
             up(hn, M, self.up.data_ptr(), stream)
             _C.call("lq_gelu_tanh_f32", self.up.data_ptr(), self.up.data_ptr(), M * FFN, stream)
-            down(self.up.data_ptr(), M, self.proj.data_ptr(), stream)
-            _C.call("lq_add_f32", h, self.proj.data_ptr(), h, M * D, stream)
+            down(self.up.data_ptr(), M, proj, stream)
+        _C.call("lq_add_f32", h, proj, h, M * D, stream)
         # the last position of each sequence: layer norm over rows n * D apart, then the head
         _C.call("lq_layer_norm_f32", h + (n - 1) * D * 4, n * D, self.hl.data_ptr(), D, B, D, None, None,
                 np.float32(1e-5), stream)

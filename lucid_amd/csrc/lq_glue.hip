@@ -49,13 +49,21 @@ __global__ __launch_bounds__(256) void embedding_sum_kernel(const float* __restr
 
 // y = (x - mean) / sqrt(var + eps) [* gamma + beta]: mean and biased variance in float32
 // over the row (wave-level tree sums), one workgroup per row.
-__global__ __launch_bounds__(256) void layer_norm_kernel(const float* __restrict__ x, int64_t ldx, float* __restrict__ y,
-                                                         int64_t ldy, int64_t rows, int64_t D,
-                                                         const float* __restrict__ gamma,
+// RES: the row is first replaced by x + res (the residual add, one rounding per element, each
+// element written and read back by the same thread), and the norm runs on the sums: the same
+// bits as a separate add followed by the norm, one launch instead of two.
+template <bool RES>
+__global__ __launch_bounds__(256) void layer_norm_kernel(float* x, int64_t ldx, const float* __restrict__ res,
+                                                         int64_t ldres, float* __restrict__ y, int64_t ldy,
+                                                         int64_t rows, int64_t D, const float* __restrict__ gamma,
                                                          const float* __restrict__ beta, float eps) {
     const int64_t r = blockIdx.x;
     if (r >= rows) return;
-    const float* xr = x + r * ldx;
+    float* xr = x + r * ldx;
+    if constexpr (RES) {
+        const float* rr = res + r * ldres;
+        for (int64_t d = threadIdx.x; d < D; d += blockDim.x) xr[d] = xr[d] + rr[d];
+    }
     __shared__ float part[8];
     auto block_sum = [&](float v) {
         for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
@@ -294,9 +302,21 @@ int lq_layer_norm_f32(const float* d_x, int64_t ldx, float* d_y, int64_t ldy, in
     if (rows == 0) return LQ_OK;
     LQ_REQUIRE(d_x && d_y, "lq_layer_norm_f32: NULL pointer");
     LQ_REQUIRE(rows <= 0x7fffffff, "lq_layer_norm_f32: too many rows");
-    hipLaunchKernelGGL(layer_norm_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), d_x, ldx, d_y, ldy,
-                       rows, D, d_gamma, d_beta, eps);
+    hipLaunchKernelGGL(layer_norm_kernel<false>, dim3((unsigned)rows), dim3(256), 0, as_stream(stream),
+                       const_cast<float*>(d_x), ldx, nullptr, 0, d_y, ldy, rows, D, d_gamma, d_beta, eps);
     return launch_status("lq_layer_norm_f32");
+}
+
+int lq_add_layer_norm_f32(float* d_x, int64_t ldx, const float* d_res, int64_t ldres, float* d_y, int64_t ldy,
+                          int64_t rows, int64_t D, const float* d_gamma, const float* d_beta, float eps,
+                          void* stream) {
+    LQ_REQUIRE(rows >= 0 && D > 0 && ldx >= D && ldres >= D && ldy >= D, "lq_add_layer_norm_f32: bad shape");
+    if (rows == 0) return LQ_OK;
+    LQ_REQUIRE(d_x && d_res && d_y, "lq_add_layer_norm_f32: NULL pointer");
+    LQ_REQUIRE(rows <= 0x7fffffff, "lq_add_layer_norm_f32: too many rows");
+    hipLaunchKernelGGL(layer_norm_kernel<true>, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), d_x, ldx,
+                       d_res, ldres, d_y, ldy, rows, D, d_gamma, d_beta, eps);
+    return launch_status("lq_add_layer_norm_f32");
 }
 
 int lq_gelu_tanh_f32(const float* d_x, float* d_y, int64_t n, void* stream) {

@@ -46,6 +46,37 @@ def test_embedding_sum_and_add_exact(gpu):
     assert dpos.numpy()[0] == pos0 + 8
 
 
+@pytest.mark.parametrize("rows,D", [(8, 512), (4096, 512), (9, 100), (6, 2048)])
+def test_add_layer_norm_matches_add_then_norm(gpu, rows, D):
+    """lq_add_layer_norm_f32 (x += res, then the norm of x) gives the bits of lq_add_f32
+    followed by lq_layer_norm_f32, for the updated residual stream and for the norm, with and
+    without gamma / beta and with strided rows."""
+    from lucid_amd import _C
+
+    rng = np.random.default_rng(rows * 7 + D)
+    x = (rng.standard_normal((rows, D)) * 2 + 0.5).astype(np.float32)
+    res = rng.standard_normal((rows, 2 * D)).astype(np.float32)  # rows 2 D apart, the first D used
+    g, b = rng.standard_normal(D).astype(np.float32), rng.standard_normal(D).astype(np.float32)
+    dg, dbb = _d(gpu, g), _d(gpu, b)
+    dres = _d(gpu, res)
+    rc = _d(gpu, np.ascontiguousarray(res[:, :D]))
+    for gamma, beta in ((None, None), (dg.data_ptr(), dbb.data_ptr())):
+        xa, xb = _d(gpu, x), _d(gpu, x)
+        ya = gpu.empty((rows, D), np.float32, "gpu")
+        yb = gpu.empty((rows, 3 * D), np.float32, "gpu")
+        _C.call("lq_add_f32", xa.data_ptr(), rc.data_ptr(), xa.data_ptr(), rows * D, None)
+        _C.call("lq_layer_norm_f32", xa.data_ptr(), D, ya.data_ptr(), D, rows, D, gamma, beta, np.float32(1e-5),
+                None)
+        _C.call("lq_add_layer_norm_f32", xb.data_ptr(), D, dres.data_ptr(), 2 * D, yb.data_ptr(), 3 * D, rows, D,
+                gamma, beta, np.float32(1e-5), None)
+        np.testing.assert_array_equal(xb.numpy().view(np.uint32), xa.numpy().view(np.uint32))
+        np.testing.assert_array_equal(yb.numpy()[:, :D].view(np.uint32), ya.numpy().view(np.uint32))
+        want = x + res[:, :D]
+        np.testing.assert_array_equal(xb.numpy(), want)
+        assert_close_f32(yb.numpy()[:, :D], O.layer_norm(want, None if gamma is None else g,
+                                                          None if beta is None else b, 1e-5))
+
+
 @pytest.mark.parametrize("rows,D", [(1, 512), (4096, 512), (9, 100), (3, 2048)])
 def test_layer_norm(gpu, rows, D):
     from lucid_amd import _C
