@@ -100,12 +100,17 @@ class Decoder:
         self.k = [np.zeros((batch, heads, positions, self.hd), F32) for _ in range(layers)]
         self.v = [np.zeros((batch, heads, positions, self.hd), F32) for _ in range(layers)]
 
-    def step(self, tokens: np.ndarray, pos0: int) -> np.ndarray:
-        """Feed tokens [B, n] at positions pos0 ..; returns the next greedy token of each row."""
+    def step(self, tokens: np.ndarray, pos0: int, trace: list | None = None) -> np.ndarray:
+        """Feed tokens [B, n] at positions pos0 ..; returns the next greedy token of each row.
+
+        ``trace``, when a list, receives one dict of intermediates per layer and a last one
+        with the logits (the pins of this composition compare each stage on its own inputs)."""
         B, n = tokens.shape
         h = self.tok[tokens] + self.pos[pos0:pos0 + n]
         for li, (qkv_w, out_w, up_w, down_w) in enumerate(self.layers):
-            qkv = dynamic_linear(layer_norm(h).reshape(B * n, self.d), qkv_w).reshape(B, n, 3, self.h, self.hd)
+            rec = {"h_in": h}
+            ln1 = layer_norm(h).reshape(B * n, self.d)
+            qkv = dynamic_linear(ln1, qkv_w).reshape(B, n, 3, self.h, self.hd)
             q = qkv[:, :, 0].transpose(0, 2, 1, 3)
             self.k[li][:, :, pos0:pos0 + n] = qkv[:, :, 1].transpose(0, 2, 1, 3)
             self.v[li][:, :, pos0:pos0 + n] = qkv[:, :, 2].transpose(0, 2, 1, 3)
@@ -116,19 +121,34 @@ class Decoder:
             att = np.exp(att - att.max(-1, keepdims=True))
             att = att / att.sum(-1, keepdims=True)
             o = (att @ V).transpose(0, 2, 1, 3).reshape(B * n, self.d)
-            h = h + dynamic_linear(o, out_w).reshape(B, n, self.d)
-            f = gelu_tanh(dynamic_linear(layer_norm(h).reshape(B * n, self.d), up_w))
-            h = h + dynamic_linear(f, down_w).reshape(B, n, self.d)
-        logits = dynamic_linear(layer_norm(h[:, -1]), self.head)
+            proj = dynamic_linear(o, out_w).reshape(B, n, self.d)
+            h = h + proj
+            ln2 = layer_norm(h).reshape(B * n, self.d)
+            up = dynamic_linear(ln2, up_w)
+            f = gelu_tanh(up)
+            down = dynamic_linear(f, down_w).reshape(B, n, self.d)
+            if trace is not None:
+                rec.update(ln1=ln1, qkv=qkv, K=K.copy(), V=V.copy(), o=o, proj=proj, h_mid=h, ln2=ln2,
+                           up=up, f=f, down=down)
+            h = h + down
+            if trace is not None:
+                rec["h_out"] = h
+                trace.append(rec)
+        lnf = layer_norm(h[:, -1])
+        logits = dynamic_linear(lnf, self.head)
+        if trace is not None:
+            trace.append({"h": h, "lnf": lnf, "logits": logits})
         return logits.argmax(-1)
 
 
 # ------------------------------------------------------------------- configuration 5
 
 
-def conv_layer(x: np.ndarray, w: tuple, stride: int, pad: int, relu: bool, act: tuple) -> np.ndarray:
+def conv_layer(x: np.ndarray, w: tuple, stride: int, pad: int, relu: bool, act: tuple,
+               trace: dict | None = None) -> np.ndarray:
     """nnq.Conv2d(ReLU2d): dequantized weight, im2col + sgemm, bias, ReLU, fake-quantize onto
-    the layer's uint8 activation grid.  x [N, C, H, W] float32 -> [N, Cout, OH, OW]."""
+    the layer's uint8 activation grid.  x [N, C, H, W] float32 -> [N, Cout, OH, OW].
+    ``trace``, when a dict, receives the float result before the fake-quantize."""
     q, s, z, b = w
     Cout, C, KH, KW = q.shape
     wd = dequantize_rows(q, s, z).reshape(Cout, -1)
@@ -140,6 +160,8 @@ def conv_layer(x: np.ndarray, w: tuple, stride: int, pad: int, relu: bool, act: 
     y = y + b
     if relu:
         y = np.where(y <= 0, F32(0), y).astype(F32)
+    if trace is not None:
+        trace["pre_quant"] = np.ascontiguousarray(y.reshape(N, OH, OW, Cout).transpose(0, 3, 1, 2))
     y = fake_quantize(y, act[0], act[1], 0, 255)
     return np.ascontiguousarray(y.reshape(N, OH, OW, Cout).transpose(0, 3, 1, 2))
 
