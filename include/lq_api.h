@@ -60,8 +60,9 @@ enum {
     LQ_F32 = 6,   /* IEEE single */
     LQ_U8S8 = 7,  /* an unsigned-grid code c stored as int8 (c - 128): MFMA operand form */
     LQ_I64 = 8,   /* int64 (indices and offsets) */
-    LQ_I8_QPAIR = 9  /* table lookups only: int8 rows whose d_scale holds interleaved float32
+    LQ_I8_QPAIR = 9, /* table lookups only: int8 rows whose d_scale holds interleaved float32
                       * {scale, zero point} pairs per row (d_zero_point unused) */
+    LQ_BF16 = 10     /* bfloat16 (the upper 16 bits of a float32) */
 };
 
 /* ---- runtime -------------------------------------------------------------- */
@@ -244,7 +245,7 @@ enum {
 /* Flag bits of lq_gemm_w8a8.  LQ_EPI_A_U8S8: A holds unsigned-grid codes c stored as int8
  * (c - 128, the LQ_U8S8 form); d_a_zero_point (NULL = 0) is the grid's own zero point and
  * the kernel applies the 128 shift. */
-enum { LQ_EPI_RELU = 1, LQ_EPI_A_U8S8 = 2 };
+enum { LQ_EPI_RELU = 1, LQ_EPI_A_U8S8 = 2, LQ_EPI_ROUND_BF16 = 4 /* lq_group_matmul only */ };
 
 /* C[m,n] epilogue of acc[m,n] = sum_k (A[m,k] - za) * (B[n,k] - zb[n])  (exact int32),
  * A int8 [M,K] row-major (lda), B int8 [N,K] row-major (ldb; Lucid's weight_int8 [out,in]).
@@ -359,6 +360,13 @@ int lq_group_dequantize_f32(const uint32_t* d_packed, const float* d_scales,
 /* y[m,n] = sum_k x[m,k] w_hat[n,k] (+ bias[n]) (ReLU with LQ_EPI_RELU), x / y of x_dtype
  * (LQ_F32 or LQ_F16), float32 accumulation, without forming w_hat.  Replaces
  * _C_engine.quantized.quantized_matmul (QuantizedMatmul.cpp:143-163) for transpose = 1.
+ * Dtype rule of the reference: scales and group biases are cast to x's dtype before the
+ * product (QuantizedMatmul.cpp:153-164) and the result is x's dtype; QuantizedLinearMLX then
+ * adds its bias cast to that dtype (mlx_linear.py:215-222).  So with LQ_F16 x the scales,
+ * group biases and bias are rounded to half, the float32 sum is rounded to half, and the
+ * bias is added in half.  LQ_EPI_ROUND_BF16 (float32 x and y only) applies the same rule
+ * for bfloat16: a caller with bfloat16 activations widens x to float32 (exact, lq_cast),
+ * calls with this flag and narrows y (exact: y is bfloat16-valued).
  * transpose = 0: y[m,k] = sum_n x[m,n] w_hat[n,k] (+ bias[k]) with x [M, N] (ldx >= N) and
  * y [M, K] (ldy >= K), w_hat tiles dequantized as lq_group_dequantize_f32 writes them -- the
  * transpose=false product and the QLoRA input gradient dX = dY dequant(W) of the transpose=1
@@ -553,6 +561,10 @@ int lq_conv2d_f32(const float* d_x, int64_t N, int64_t C, int64_t H, int64_t W, 
  * (gamma / beta NULL: 1 / 0).  The float model's BatchNorm2d before fusion. */
 int lq_batch_norm_f32(const float* d_x, float* d_y, int64_t N, int64_t C, int64_t HW, const float* d_mean,
                       const float* d_var, const float* d_gamma, const float* d_beta, float eps, void* stream);
+/* y[i] = x[i] converted between LQ_F32, LQ_F16 and LQ_BF16 (round to nearest even when
+ * narrowing; exact when widening), n elements; x and y may not overlap unless equal with
+ * equal types.  Replaces astype_op (lucid/_C/ops/ufunc/Astype.cpp:42) between float types. */
+int lq_cast(const void* d_x, int x_dtype, void* d_y, int y_dtype, int64_t n, void* stream);
 /* y = (x <= 0) ? +0 : x, NaN passes (the CPU relu of backend/cpu/Vdsp.cpp vrelu_f32,
  * reached from nn.ReLU between quantized layers). */
 int lq_relu_f32(const float* d_x, float* d_y, int64_t n, void* stream);

@@ -12,6 +12,9 @@ from lucid_amd._C import BackendUnavailable, LucidError, is_available, synchroni
 from lucid_amd._tensor import (
     QuantSource,
     Tensor,
+    bf16_from_f32,
+    bf16_to_f32,
+    bfloat16,
     bool_,
     dtype,
     empty,

@@ -37,6 +37,37 @@ int32 = np.dtype(np.int32)
 int64 = np.dtype(np.int64)
 uint32 = np.dtype(np.uint32)
 bool_ = np.dtype(np.bool_)
+# bfloat16 (Lucid's BF16, lucid/_C/core/Dtype.h:63-80): numpy has no such type, so host arrays
+# hold the 16-bit patterns in a one-field structured dtype, distinct from uint16 / float16.
+# bf16_from_f32 / bf16_to_f32 convert; a device tensor converts with Tensor.to(dtype=...).
+bfloat16 = np.dtype([("bfloat16", "<u2")])
+FLOAT_TYPE_CODE = {float32: _C.F32, float16: _C.F16, bfloat16: _C.BF16}  # element-type codes
+
+
+def bf16_from_f32(a: Any) -> np.ndarray:
+    """float32 values -> bfloat16 array, round to nearest even (NaN stays a quiet NaN)."""
+    u = np.ascontiguousarray(a, np.float32).view(np.uint32).astype(np.uint64)
+    nan = (u & 0x7FFFFFFF) > 0x7F800000
+    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+    r = np.where(nan, ((u >> 16) | 0x40).astype(np.uint16), r)
+    return r.view(bfloat16)
+
+
+def bf16_to_f32(a: np.ndarray) -> np.ndarray:
+    """bfloat16 array -> float32 (exact)."""
+    bits = np.ascontiguousarray(a).view(np.uint16)
+    return (bits.astype(np.uint32) << 16).view(np.float32)
+
+
+def _host_astype(arr: np.ndarray, dt: np.dtype) -> np.ndarray:
+    dt = np.dtype(dt)
+    if arr.dtype == dt:
+        return arr
+    if dt == bfloat16:
+        return bf16_from_f32(arr if arr.dtype != bfloat16 else bf16_to_f32(arr))
+    if arr.dtype == bfloat16:
+        return bf16_to_f32(arr).astype(dt)
+    return arr.astype(dt)
 
 dtype = np.dtype
 
@@ -226,9 +257,17 @@ class Tensor:
             if dev != self._device:
                 t = Tensor._from_numpy(self.numpy(), dev)
         if dtype is not None and np.dtype(dtype) != t._dtype:
+            dt = np.dtype(dtype)
             if t._device != "cpu":
-                raise _C.LucidError("dtype conversion of a device tensor is not part of this backend")
-            t = Tensor._from_numpy(t._host.astype(dtype), "cpu")
+                if t._dtype not in FLOAT_TYPE_CODE or dt not in FLOAT_TYPE_CODE:
+                    raise _C.LucidError("device dtype conversion is between float32, float16 and "
+                                        f"bfloat16 only, not {t._dtype} -> {dt}")
+                out = Tensor._empty(t._shape, dt, "gpu")
+                _C.call("lq_cast", t.data_ptr(), FLOAT_TYPE_CODE[t._dtype], out.data_ptr(),
+                        FLOAT_TYPE_CODE[dt], t.numel(), None)
+                out.requires_grad = t.requires_grad
+                return out
+            t = Tensor._from_numpy(_host_astype(t._host, dt), "cpu")
         return t
 
     def cpu(self) -> "Tensor":
@@ -341,7 +380,7 @@ def tensor(data: Any, dtype: Any = None, device: Any = "cpu", requires_grad: boo
     else:
         arr = np.asarray(data)
     if dtype is not None:
-        arr = arr.astype(dtype)
+        arr = _host_astype(arr, dtype)
     elif arr.dtype == np.float64:
         arr = arr.astype(np.float32)
     elif arr.dtype == np.int64 and not isinstance(data, np.ndarray):

@@ -1,11 +1,14 @@
-// lq_float.hip -- float32 helper kernels around the quantized path: ReLU and the float
-// Linear used to calibrate (run) the float model before convert().
+// lq_float.hip -- float helper kernels around the quantized path: ReLU, the float Linear
+// used to calibrate (run) the float model before convert(), and conversions between float32,
+// half and bfloat16 (Lucid's astype between float dtypes).
 //
 // ReLU follows Lucid's CPU rule `x <= 0 ? 0 : x` (lucid/_C/backend/cpu/Vdsp.cpp vrelu_f32:
 // NaN passes, -0 becomes +0).  The float Linear is y = x W^T + b
 // (lucid/_C/backend/cpu/methods/Matmul.cpp:80-122); its summation order, like Accelerate's
 // sgemm order, is an implementation detail, so only tolerance parity applies to it.
 #include <hip/hip_runtime.h>
+
+#include <algorithm>
 
 #include "lq_internal.h"
 
@@ -17,6 +20,23 @@ __global__ void relu_f32_kernel(const float* __restrict__ x, float* __restrict__
     for (; i < n; i += stride) {
         float v = x[i];
         y[i] = (v <= 0.0f) ? 0.0f : v;
+    }
+}
+
+// One element per thread-iteration; every conversion is exact when widening and rounds to
+// nearest even when narrowing (half through v_cvt_f16_f32, bfloat16 on the upper 16 bits).
+template <int XT, int YT>
+__global__ void cast_kernel(const void* __restrict__ xv, void* __restrict__ yv, int64_t n) {
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) {
+        float v;
+        if constexpr (XT == LQ_F32) v = static_cast<const float*>(xv)[i];
+        else if constexpr (XT == LQ_F16) v = __half2float(static_cast<const __half*>(xv)[i]);
+        else v = bf16_bits_to_f32(static_cast<const uint16_t*>(xv)[i]);
+        if constexpr (YT == LQ_F32) static_cast<float*>(yv)[i] = v;
+        else if constexpr (YT == LQ_F16) static_cast<__half*>(yv)[i] = f32_to_f16_rn(v);
+        else static_cast<uint16_t*>(yv)[i] = f32_to_bf16_bits(v);
     }
 }
 
@@ -76,6 +96,24 @@ __global__ __launch_bounds__(256) void linear_f32_kernel(const float* __restrict
 using namespace lq;
 
 extern "C" {
+
+int lq_cast(const void* d_x, int x_dtype, void* d_y, int y_dtype, int64_t n, void* stream) {
+    auto is_float = [](int t) { return t == LQ_F32 || t == LQ_F16 || t == LQ_BF16; };
+    LQ_REQUIRE(is_float(x_dtype) && is_float(y_dtype), "lq_cast: types must be LQ_F32, LQ_F16 or LQ_BF16");
+    LQ_REQUIRE(n >= 0, "lq_cast: negative count");
+    if (n == 0) return LQ_OK;
+    LQ_REQUIRE(d_x && d_y, "lq_cast: NULL pointer");
+    const int64_t blocks = std::min<int64_t>((n + 255) / 256, 4096);
+    hipStream_t st = as_stream(stream);
+    const dim3 g((unsigned)blocks), b(256);
+#define LQ_CAST(X, Y) \
+    if (x_dtype == X && y_dtype == Y) hipLaunchKernelGGL((cast_kernel<X, Y>), g, b, 0, st, d_x, d_y, n)
+    LQ_CAST(LQ_F32, LQ_F32); LQ_CAST(LQ_F32, LQ_F16); LQ_CAST(LQ_F32, LQ_BF16);
+    LQ_CAST(LQ_F16, LQ_F32); LQ_CAST(LQ_F16, LQ_F16); LQ_CAST(LQ_F16, LQ_BF16);
+    LQ_CAST(LQ_BF16, LQ_F32); LQ_CAST(LQ_BF16, LQ_F16); LQ_CAST(LQ_BF16, LQ_BF16);
+#undef LQ_CAST
+    return launch_status("lq_cast");
+}
 
 int lq_relu_f32(const float* d_x, float* d_y, int64_t n, void* stream) {
     LQ_REQUIRE(n >= 0, "lq_relu_f32: n < 0");

@@ -67,6 +67,32 @@ __device__ __forceinline__ __half f32_to_f16_rn(float v) {
     return __float2half_rn(v);
 }
 
+// float -> bfloat16 bits, round to nearest even on the upper 16 bits (overflow rounds to
+// infinity; a NaN stays a quiet NaN of the same sign).
+__host__ __device__ inline uint16_t f32_to_bf16_bits(float v) {
+    uint32_t u;
+    __builtin_memcpy(&u, &v, 4);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+__host__ __device__ inline float bf16_bits_to_f32(uint16_t b) {
+    const uint32_t u = (uint32_t)b << 16;
+    float v;
+    __builtin_memcpy(&v, &u, 4);
+    return v;
+}
+
+// A float32 value rounded to the precision of a narrower float type and kept in float32:
+// mode 0 none, 1 IEEE half (values past the half range become infinities), 2 bfloat16.
+// This is the value of Lucid's astype(x.dtype) of a float32 operand.
+enum { LQ_ROUND_NONE = 0, LQ_ROUND_F16 = 1, LQ_ROUND_BF16 = 2 };
+__device__ __forceinline__ float round_to(float v, int mode) {
+    if (mode == LQ_ROUND_F16) return __half2float(f32_to_f16_rn(v));
+    if (mode == LQ_ROUND_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
+    return v;
+}
+
 // clip with NaN pass-through and Lucid's signed-zero tie rule (backend/cpu/Vdsp.cpp:33-62).
 __device__ __forceinline__ float clip_tie(float v, float lo, float hi, bool lo_ties, bool hi_ties) {
     if (lo_ties ? v <= lo : v < lo) return lo;

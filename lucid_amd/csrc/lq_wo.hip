@@ -98,6 +98,19 @@ __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
 }
 
+// Epilogue of one output: the float32 product rounded to the activation's type (hmode, a
+// LQ_ROUND_* value), the layer bias rounded to that type and added there, then ReLU --
+// Lucid's quantized_matmul returning x's dtype and QuantizedLinearMLX's y + bias.to(y.dtype),
+// relu (lucid/nn/quantized/mlx_linear.py:215-222).  A half or bfloat16 sum of two such values
+// is exact in float32 before its rounding (24 >= 2 p + 2 bits), so the float32 add then round
+// equals the narrow add.  hmode 0 leaves the float32 result as it is.
+__device__ __forceinline__ float wo_finish(float v, bool has_bias, float b, int relu, int hmode) {
+    v = round_to(v, hmode);
+    if (has_bias) v = round_to(v + round_to(b, hmode), hmode);
+    if (relu && v <= 0.0f) v = 0.0f;
+    return v;
+}
+
 // ------------------------------------------------------------------ kernel
 
 struct WoArgs {
@@ -112,6 +125,7 @@ struct WoArgs {
     void* y;
     int64_t ldy;
     int relu;
+    int hmode;               // LQ_ROUND_*: the activation's float type (group-wise; see wo_finish)
     int M, N, K;
     int G;                   // groups per row (group-wise)
     int bpw;                 // k-blocks per wave (even; blocks past the last are zero work)
@@ -300,8 +314,8 @@ __global__ __launch_bounds__((64 * wo_max_waves(S, XF32, GROUPED))) void wo_gemv
         for (int i = tid; i < 16 * TW; i += blockDim.x) {
             const int n = min(n0 + i / TW, a.N - 1);
             const int64_t gi = (int64_t)n * a.G + min(i % TW, a.G - 1);
-            sc_lds[i] = a.w_scale[gi];
-            bi_lds[i] = a.g_bias ? a.g_bias[gi] : 0.0f;
+            sc_lds[i] = round_to(a.w_scale[gi], a.hmode);
+            bi_lds[i] = a.g_bias ? round_to(a.g_bias[gi], a.hmode) : 0.0f;
         }
         __syncthreads();
     }
@@ -444,8 +458,7 @@ __global__ __launch_bounds__((64 * wo_max_waves(S, XF32, GROUPED))) void wo_gemv
                 }
                 v = a.w_scale[on] * v;
             }
-            if (a.bias) v = v + a.bias[on];
-            if (a.relu && v <= 0.0f) v = 0.0f;
+            v = wo_finish(v, a.bias != nullptr, a.bias ? a.bias[on] : 0.0f, a.relu, a.hmode);
             if constexpr (XF32)
                 reinterpret_cast<float*>(a.y)[(int64_t)om * a.ldy + on] = v;
             else
@@ -539,8 +552,8 @@ __global__ __launch_bounds__(64 * SK_WAVES) void wo_gemv_sk_kernel(WoSkArgs sk) 
             for (int i = lane; i < 16 * nb; i += 64) {
                 const int r = i / nb, t = i - r * nb;
                 const int64_t gi = (int64_t)min(n0 + r, a.N - 1) * a.G + (tb0 + t);
-                gsc[(tile * 16 + r) * KB + t] = a.w_scale[gi];
-                gbi[(tile * 16 + r) * KB + t] = a.g_bias ? a.g_bias[gi] : 0.0f;
+                gsc[(tile * 16 + r) * KB + t] = round_to(a.w_scale[gi], a.hmode);
+                gbi[(tile * 16 + r) * KB + t] = a.g_bias ? round_to(a.g_bias[gi], a.hmode) : 0.0f;
             }
     }
 
@@ -648,8 +661,7 @@ __global__ __launch_bounds__(64 * SK_WAVES) void wo_gemv_sk_kernel(WoSkArgs sk) 
                 if (a.w_zp) v = v - a.w_zp[n] * xtot;
                 v = a.w_scale[n] * v;
             }
-            if (a.bias) v = v + a.bias[n];
-            if (a.relu && v <= 0.0f) v = 0.0f;
+            v = wo_finish(v, a.bias != nullptr, a.bias ? a.bias[n] : 0.0f, a.relu, a.hmode);
             if constexpr (XF32)
                 reinterpret_cast<float*>(a.y)[(int64_t)l16 * a.ldy + n] = v;
             else
@@ -706,8 +718,7 @@ __global__ __launch_bounds__(256) void wo_sk_reduce_kernel(WoSkArgs sk, int grou
                 if (a.w_zp) v = v - wzp[i] * xtot;
                 v = wsc[i] * v;
             }
-            if (a.bias) v = v + wbi[i];
-            if (a.relu && v <= 0.0f) v = 0.0f;
+            v = wo_finish(v, a.bias != nullptr, wbi[i], a.relu, a.hmode);
             if constexpr (XF32)
                 reinterpret_cast<float*>(a.y)[(int64_t)l16 * a.ldy + n] = v;
             else
@@ -745,6 +756,7 @@ struct WvArgs {
     void* y;
     int64_t ldy;
     int relu;
+    int hmode;               // LQ_ROUND_* (see wo_finish)
     int M, N, K;
     int G, gs;
     int NC;                  // 16-byte chunks per weight row
@@ -797,8 +809,8 @@ __global__ __launch_bounds__(1024) void wo_gemv_valu_kernel(WvArgs a) {
             w[j] = __builtin_nontemporal_load(reinterpret_cast<const vu4*>(row) + c);
             if constexpr (GROUPED) {
                 const int64_t gi = (int64_t)n * a.G + min((lane + 64 * j) * CK / a.gs, a.G - 1);
-                sgv[j] = a.w_scale[gi];
-                bgv[j] = a.g_bias ? a.g_bias[gi] : 0.0f;
+                sgv[j] = round_to(a.w_scale[gi], a.hmode);
+                bgv[j] = a.g_bias ? round_to(a.g_bias[gi], a.hmode) : 0.0f;
             }
         }
     };
@@ -974,8 +986,7 @@ __global__ __launch_bounds__(1024) void wo_gemv_valu_kernel(WvArgs a) {
                     if (a.w_zp) v = v - a.w_zp[n] * gsum[m];
                     v = a.w_scale[n] * v;
                 }
-                if (a.bias) v = v + a.bias[n];
-                if (a.relu && v <= 0.0f) v = 0.0f;
+                v = wo_finish(v, a.bias != nullptr, a.bias ? a.bias[n] : 0.0f, a.relu, a.hmode);
                 if constexpr (XF32)
                     reinterpret_cast<float*>(a.y)[(int64_t)m * a.ldy + n] = v;
                 else
@@ -1087,7 +1098,7 @@ __global__ __launch_bounds__(256) void group_matmul_nt_kernel(const void* __rest
                                                               const float* __restrict__ biases,
                                                               const float* __restrict__ bias, void* __restrict__ yv,
                                                               int64_t ldy, int64_t M, int64_t N, int64_t K, int gs,
-                                                              int relu) {
+                                                              int relu, int hmode) {
     constexpr int PER = 32 / BITS;
     constexpr uint32_t L = (1u << BITS) - 1u;
     constexpr int WPR = NT_T / PER;  // packed words per tile row
@@ -1129,8 +1140,8 @@ __global__ __launch_bounds__(256) void group_matmul_nt_kernel(const void* __rest
                 if (e < NT_K * WPR && gn < N && gk < K) {  // K is a multiple of the group size: whole words
                     wq[u] = packed[gn * words_per_row + gk / PER];
                     const int64_t gi = gn * G + gk / gs;
-                    sq[u] = scales[gi];
-                    bq[u] = biases ? biases[gi] : 0.0f;
+                    sq[u] = round_to(scales[gi], hmode);
+                    bq[u] = biases ? round_to(biases[gi], hmode) : 0.0f;
                 }
             }
         };
@@ -1184,9 +1195,7 @@ __global__ __launch_bounds__(256) void group_matmul_nt_kernel(const void* __rest
             for (int j = 0; j < NT_R; ++j) {
                 const int64_t gk = k0 + tx * NT_R + j;
                 if (gk >= K) continue;
-                float v = acc[i][j];
-                if (bias) v = v + bias[gk];
-                if (relu) v = (v <= 0.0f) ? 0.0f : v;
+                const float v = wo_finish(acc[i][j], bias != nullptr, bias ? bias[gk] : 0.0f, relu, hmode);
                 if constexpr (XF32) static_cast<float*>(yv)[gm * ldy + gk] = v;
                 else static_cast<_Float16*>(yv)[gm * ldy + gk] = (_Float16)v;
             }
@@ -1512,7 +1521,11 @@ int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d
     LQ_REQUIRE(bits == 4 || bits == 8, "lq_group_matmul: bits must be 4 or 8");
     LQ_REQUIRE(K % group_size == 0, "lq_group_matmul: K must be a multiple of group_size");
     LQ_REQUIRE(x_dtype == LQ_F32 || x_dtype == LQ_F16, "lq_group_matmul: x_dtype must be LQ_F32 or LQ_F16");
-    LQ_REQUIRE((flags & ~LQ_EPI_RELU) == 0, "lq_group_matmul: unknown flags");
+    LQ_REQUIRE((flags & ~(LQ_EPI_RELU | LQ_EPI_ROUND_BF16)) == 0, "lq_group_matmul: unknown flags");
+    LQ_REQUIRE(!(flags & LQ_EPI_ROUND_BF16) || x_dtype == LQ_F32,
+               "lq_group_matmul: LQ_EPI_ROUND_BF16 needs float32 x and y");
+    // scales, group biases, layer bias and product in x's type (QuantizedMatmul.cpp:153-164)
+    const int hmode = x_dtype == LQ_F16 ? LQ_ROUND_F16 : (flags & LQ_EPI_ROUND_BF16) ? LQ_ROUND_BF16 : LQ_ROUND_NONE;
     if (!transpose) {  // y[M, K] = x[M, N] w_hat[N, K]
         if (M == 0) return LQ_OK;
         LQ_REQUIRE(d_x && d_y && (N == 0 || (d_packed && d_scales)), "lq_group_matmul: NULL pointer");
@@ -1525,7 +1538,7 @@ int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d
         hipStream_t st = as_stream(stream);
 #define LQ_NT(B, XF)                                                                                           \
     hipLaunchKernelGGL((group_matmul_nt_kernel<B, XF>), grid, dim3(256), 0, st, d_x, ldx, pk, d_scales, gb, d_bias, \
-                       d_y, ldy, M, N, K, group_size, relu)
+                       d_y, ldy, M, N, K, group_size, relu, hmode)
         if (bits == 8) {
             if (x_dtype == LQ_F32) LQ_NT(8, true); else LQ_NT(8, false);
         } else {
@@ -1554,6 +1567,7 @@ int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d
     a.y = d_y;
     a.ldy = ldy;
     a.relu = (flags & LQ_EPI_RELU) ? 1 : 0;
+    a.hmode = hmode;
     a.M = (int)M;
     a.N = (int)N;
     a.K = (int)K;
@@ -1563,7 +1577,7 @@ int lq_group_matmul(const void* d_x, int x_dtype, int64_t ldx, const uint32_t* d
     if (M <= 2) {
         WvArgs v{};
         v.x = d_x; v.ldx = ldx; v.w = a.w; v.ldw_bytes = a.ldw_bytes; v.w_scale = d_scales;
-        v.g_bias = d_biases; v.bias = d_bias; v.y = d_y; v.ldy = ldy; v.relu = a.relu;
+        v.g_bias = d_biases; v.bias = d_bias; v.y = d_y; v.ldy = ldy; v.relu = a.relu; v.hmode = hmode;
         v.M = (int)M; v.N = (int)N; v.K = (int)K; v.G = a.G; v.gs = group_size;
         const bool ok = bits == 8 ? launch_wv<8, false, true>(v, xf32, st) : launch_wv<4, false, true>(v, xf32, st);
         if (ok) return launch_status("lq_group_matmul");

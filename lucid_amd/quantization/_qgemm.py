@@ -25,7 +25,7 @@ from __future__ import annotations
 import numpy as np
 
 from lucid_amd import _C
-from lucid_amd._tensor import Tensor, empty, float16, float32
+from lucid_amd._tensor import Tensor, bfloat16, empty, float16, float32
 from lucid_amd.quantization._device import on_device, require_gpu, workspace
 
 _GROUP_SIZES = (32, 64, 128)
@@ -109,14 +109,20 @@ def quantized_matmul(x: Tensor, wq: Tensor, scales: Tensor, biases: Tensor | Non
                      transpose: bool = True, group_size: int = 64, bits: int = 8,
                      bias: Tensor | None = None, relu: bool = False) -> Tensor:
     """``x @ w_hat^T`` (``[..., K] -> [..., N]``) or, with ``transpose=False``, ``x @ w_hat``
-    (``[..., N] -> [..., K]``), in x's dtype (float32 or float16), for the packed
+    (``[..., N] -> [..., K]``), in x's dtype (float32, float16 or bfloat16), for the packed
     ``w_hat [N, K]``.
 
     ``bias`` (length of the output features) / ``relu`` fuse the layer epilogue of
     ``QuantizedLinearMLX`` into the kernel.
+
+    Dtypes follow Lucid (QuantizedMatmul.cpp:153-164, mlx_linear.py:215-222): the scales,
+    group biases and ``bias`` are rounded to x's dtype, the product is x's dtype and the bias
+    is added in that dtype.  A bfloat16 x is widened to float32 (exact), multiplied with the
+    bfloat16 rounding rule (``lq_group_matmul``'s ``LQ_EPI_ROUND_BF16``) and the bfloat16-valued
+    result narrowed back (exact): three launches on one stream.
     """
-    if x.dtype not in (float32, float16):
-        raise TypeError(f"quantized_matmul: float32 or float16 input expected, got {x.dtype}")
+    if x.dtype not in (float32, float16, bfloat16):
+        raise TypeError(f"quantized_matmul: float32, float16 or bfloat16 input expected, got {x.dtype}")
     N, K = _check_packed(wq, scales, biases, group_size, bits, "quantized_matmul")
     d_in, d_out = (K, N) if transpose else (N, K)
     if x.shape[-1] != d_in:
@@ -131,15 +137,17 @@ def quantized_matmul(x: Tensor, wq: Tensor, scales: Tensor, biases: Tensor | Non
     s = on_device(scales)
     b = on_device(biases) if biases is not None else None
     lb = on_device(bias) if bias is not None else None
-    y = empty((*x.shape[:-1], d_out), x.dtype, "gpu")
+    bf16 = x.dtype == bfloat16
+    xk = x.to(dtype=float32) if bf16 else x
+    y = empty((*x.shape[:-1], d_out), float32 if bf16 else x.dtype, "gpu")
     if M and d_out:
         ws_bytes = _C.lib().lq_group_matmul_workspace_size(M, N, K, group_size) if transpose else 0
-        _C.call("lq_group_matmul", x.data_ptr(), _C.F32 if x.dtype == float32 else _C.F16, d_in,
+        flags = (_C.EPI_RELU if relu else 0) | (_C.EPI_ROUND_BF16 if bf16 else 0)
+        _C.call("lq_group_matmul", xk.data_ptr(), _C.F32 if xk.dtype == float32 else _C.F16, d_in,
                 wq.data_ptr(), s.data_ptr(), b.data_ptr() if b is not None else None,
                 lb.data_ptr() if lb is not None else None, y.data_ptr(), d_out, M, N, K, group_size,
-                bits, 1 if transpose else 0, _C.EPI_RELU if relu else 0, workspace.get(ws_bytes),
-                ws_bytes, None)
-    return y
+                bits, 1 if transpose else 0, flags, workspace.get(ws_bytes), ws_bytes, None)
+    return y.to(dtype=bfloat16) if bf16 else y
 
 
 def quantized_matmul_backward(dy: Tensor, wq: Tensor, scales: Tensor, biases: Tensor | None,

@@ -34,7 +34,9 @@ function                      follows (lucid-official/lucid)
 ``gemv_w8``                   nn/quantized/linear.py:206-210 (dequantize -> F.linear) with
                               float64 accumulation (tolerance reference)
 ``group_*``                   quantization/_qgemm.py:84-97, 167-170 (MLX 0.32.3 internals:
-                              parity unpinned beyond this documented formula)
+                              parity unpinned beyond this documented formula);
+                              ``group_matmul`` adds the dtype rule of QuantizedMatmul.cpp:153-164
+                              and mlx_linear.py:215-222 (``round_to`` / ``bf16_round``)
 ``histc``                     _ops/_adapters.py:1256-1279 -> backend/cpu/methods/
                               Reduction.cpp:839-884 (double-precision bins, numpy)
 ``hist_rebin``                quantization/observer.py:826-848 (float32 centers / index,
@@ -413,6 +415,74 @@ def group_dequantize(packed, scales, biases, group_size: int, bits: int) -> np.n
                                _ptr(None if biases is None else _f32(biases)), N, K, group_size,
                                bits, _ptr(w))
     return w
+
+
+def group_codes(packed, bits: int) -> np.ndarray:
+    """The codes c [N, K] of a packed weight: 32/bits codes per uint32, little end first."""
+    packed = np.ascontiguousarray(packed, np.uint32)
+    per = 32 // bits
+    shifts = (np.arange(per, dtype=np.uint32) * bits)
+    c = (packed[:, :, None] >> shifts[None, None, :]) & np.uint32((1 << bits) - 1)
+    return c.reshape(packed.shape[0], -1).astype(np.float64)
+
+
+def bf16_round(x) -> np.ndarray:
+    """Values rounded to bfloat16 precision (8 significant bits, float32's exponent range,
+    round half to even, overflow to infinity), returned as float32.  One rounding from the
+    given value (float32 or float64), written with frexp / rint in float64 (an arithmetic
+    route, independent of bit tricks)."""
+    x = np.asarray(x, np.float64)
+    out = x.copy()
+    fin = np.isfinite(x) & (x != 0)
+    m, e = np.frexp(x[fin])                      # x = m 2^e, 0.5 <= |m| < 1
+    ulp_e = np.maximum(e - 8, -133)              # spacing 2^(e-8); subnormal floor 2^-133
+    out[fin] = np.rint(np.ldexp(x[fin], -ulp_e)) * np.ldexp(1.0, ulp_e)
+    with np.errstate(over="ignore"):
+        return out.astype(np.float32)
+
+
+def round_to(x, dtype: str) -> np.ndarray:
+    """One rounding of the given values to 'f32', 'f16' or 'bf16' (Lucid's astype), kept as
+    float64."""
+    x = np.asarray(x, np.float64)
+    with np.errstate(over="ignore"):
+        if dtype == "f16":
+            return x.astype(np.float16).astype(np.float64)
+        if dtype == "bf16":
+            return bf16_round(x).astype(np.float64)
+        return x.astype(np.float32).astype(np.float64)
+
+
+def group_matmul(x, packed, scales, biases, group_size: int, bits: int, dtype: str = "f32",
+                 bias=None, relu: bool = False, transpose: bool = True) -> np.ndarray:
+    """quantized_matmul in x's dtype, then QuantizedLinearMLX's bias and ReLU, over the rounded
+    operands (tolerance reference: MLX's summation order is not knowable): scales and group
+    biases cast to x's dtype (lucid/_C/ops/quantized/QuantizedMatmul.cpp:153-164), w_hat =
+    c s + b per group (lucid/quantization/_qgemm.py:167-170), y = x w_hat^T (transpose) or
+    x w_hat in float64, rounded once to x's dtype ('f16' / 'bf16'; 'f32' keeps the float64
+    sum), then fl(y + fl(bias)) and ReLU (lucid/nn/quantized/mlx_linear.py:215-222).  x holds
+    values of its dtype."""
+    c = group_codes(packed, bits)
+    N, K = c.shape
+    half = dtype != "f32"
+
+    def rep(a):
+        a = np.asarray(a, np.float32)
+        return np.repeat((round_to(a, dtype) if half else a.astype(np.float64)).reshape(N, K // group_size),
+                         group_size, axis=1)
+
+    w = c * rep(scales)
+    if biases is not None:
+        w = w + rep(biases)
+    y = np.asarray(x, np.float64) @ (w.T if transpose else w)
+    if half:
+        y = round_to(y, dtype)
+    if bias is not None:
+        b = np.asarray(bias, np.float32).astype(np.float64)
+        y = round_to(y + round_to(b, dtype), dtype) if half else y + b
+    if relu:
+        y = np.where(y <= 0, 0.0, y)
+    return y
 
 
 # ------------------------------------------- Lucid's multi-pass CPU composition

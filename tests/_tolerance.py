@@ -3,7 +3,9 @@ reference test suite's scale-aware convention (lucid/test/_helpers/compare.py:54
 ``assert_close_to_scale``): ``|got - want| <= atol + rtol * |want|`` elementwise with
 ``atol = rtol * max|want|`` -- the absolute floor is the largest expected magnitude times
 rtol, never looser than rtol allows the largest entry.  fp32 outputs use rtol 1e-5 and fp16
-outputs rtol 1e-3, with fp16's subnormal step as the floor."""
+outputs rtol 1e-3, with fp16's subnormal step as the floor.
+bfloat16 outputs (no north-star tolerance is stated for them) use rtol 2^-7, two of the
+type's ulps at the top of a binade."""
 
 from __future__ import annotations
 
@@ -11,6 +13,7 @@ import numpy as np
 
 F32_RTOL = 1e-5
 F16_RTOL = 1e-3
+BF16_RTOL = 2.0 ** -7
 
 
 def assert_close_to_scale(got, want, rtol: float, floor: float = 0.0) -> None:

@@ -354,6 +354,57 @@ def test_group_constant_group_exact():
     np.testing.assert_array_equal(O.group_dequantize(p, s, b, 64, 4), w)
 
 
+def test_bf16_round_ties_and_torch():
+    """bfloat16 rounding: half-even ties at 1 (spacing 2^-7), the subnormal floor 2^-133,
+    overflow past the largest finite value, signed zeros; and torch's float32 -> bfloat16
+    conversion (round to nearest even) on values over the whole exponent range."""
+    import torch
+
+    ties = np.array([1 + 2.0 ** -8, 1 + 3 * 2.0 ** -8, -(1 + 2.0 ** -8), 2.0 ** -134, 3 * 2.0 ** -134,
+                     3.3961775e38, 3.4e38, -0.0])
+    want = np.array([1.0, 1 + 2.0 ** -6, -1.0, 0.0, 2.0 ** -132, 3.3895314e38, np.inf, -0.0], np.float32)
+    got = O.bf16_round(ties)
+    np.testing.assert_array_equal(got.view(np.uint32), want.view(np.uint32))
+    rng = np.random.default_rng(3)
+    v = (rng.standard_normal(200000) * np.exp(rng.uniform(-100, 87, 200000))).astype(np.float32)
+    t = torch.from_numpy(v).to(torch.bfloat16).float().numpy()
+    np.testing.assert_array_equal(O.bf16_round(v).view(np.uint32), t.view(np.uint32))
+
+
+def test_group_matmul_dtype_rule_closed_forms():
+    """The dtype rule of quantized_matmul: one group of 64 codes equal to 1, x = e_0, scale
+    1 + 2^-12 and group bias 2^-12 (neither a half value): in float32 the product is
+    1 + 2^-12 + 2^-12; in half the scale rounds to 1 and the group bias stays 2^-12, so the
+    float64 product 1 + 2^-12 rounds (half spacing 2^-10 at 1) to 1; a layer bias of 3 2^-11
+    is cast to half (exact) and added in half: fl16(1 + 3 2^-11) = 1 + 2^-9.  bfloat16: the
+    scale rounds to 1 (spacing 2^-7), the product to 1, and 1 + 3 2^-11 rounds to 1."""
+    codes = np.ones((1, 64), np.uint32)
+    packed = (codes.reshape(1, 8, 8) << (np.arange(8, dtype=np.uint32) * 4)).sum(-1).astype(np.uint32)
+    np.testing.assert_array_equal(O.group_codes(packed, 4), np.ones((1, 64)))
+    s = np.array([[1 + 2.0 ** -12]], np.float32)
+    b = np.array([[2.0 ** -12]], np.float32)
+    x = np.zeros((1, 64))
+    x[0, 0] = 1.0
+    assert O.group_matmul(x, packed, s, b, 64, 4)[0, 0] == np.float64(np.float32(1 + 2.0 ** -12)) + 2.0 ** -12
+    assert O.group_matmul(x, packed, s, b, 64, 4, "f16")[0, 0] == 1.0
+    lb = np.array([3 * 2.0 ** -11], np.float32)
+    assert O.group_matmul(x, packed, s, b, 64, 4, "f16", bias=lb)[0, 0] == 1 + 2.0 ** -9
+    assert O.group_matmul(x, packed, s, b, 64, 4, "bf16", bias=lb)[0, 0] == 1.0
+    assert O.group_matmul(-x, packed, s, b, 64, 4, "f16", relu=True)[0, 0] == 0.0
+    # float32 mode equals the float64 product against the pinned dequantize
+    rng = np.random.default_rng(5)
+    w = rng.standard_normal((12, 128)).astype(np.float32)
+    for bits in (4, 8):
+        p, sc, bi = O.group_quantize(w, 32, bits)
+        xx = rng.standard_normal((3, 128))
+        ref = xx @ O.group_dequantize(p, sc, bi, 32, bits).astype(np.float64).T
+        np.testing.assert_allclose(O.group_matmul(xx, p, sc, bi, 32, bits), ref, rtol=1e-6, atol=1e-6)
+        xt = rng.standard_normal((3, 12))
+        np.testing.assert_allclose(O.group_matmul(xt, p, sc, bi, 32, bits, transpose=False),
+                                   xt @ O.group_dequantize(p, sc, bi, 32, bits).astype(np.float64),
+                                   rtol=1e-6, atol=1e-6)
+
+
 # ------------------------------------------------------------------ convolution
 
 
