@@ -484,11 +484,21 @@ def tensor_of(a):
 # sums are the 3-D convolution's products, exactly (codes) or in another order (floats).
 
 
-def _ntuple(v, n: int) -> tuple[int, ...]:
-    if isinstance(v, (tuple, list)):
-        vals = tuple(int(x) for x in v)
-        return vals if len(vals) == n else (vals[0],) * n
-    return (int(v),) * n
+def _ntuple(v, n: int, name: str = "") -> tuple[int, ...]:
+    """``v`` as ``n`` ints, read as Lucid reads a convolution's sizes (nn/modules/
+    _conv_common.py:16, nn/functional/_spatial_args.py:28): one int, or a sequence of one, is
+    repeated -- except a ``kernel_size``, which must name every axis -- a sequence of ``n``
+    is taken as it is, and any other length raises ValueError."""
+    if not isinstance(v, (tuple, list)):
+        return (int(v),) * n
+    vals = tuple(int(x) for x in v)
+    if len(vals) == n:
+        return vals
+    if len(vals) == 1 and name != "kernel_size":
+        return vals * n
+    what = name or "argument"
+    raise ValueError(f"{what} must be an int or a sequence of {n}"
+                     f"{'' if name == 'kernel_size' else ' (or of one)'}; got {list(vals)}")
 
 
 def conv_padding_nd(padding, kernel: tuple[int, ...], dilation: tuple[int, ...]) -> list[tuple[int, int]]:
@@ -589,7 +599,7 @@ def conv3d(x: Tensor, weight: Tensor, bias: Tensor | None = None, stride=1, padd
     Cout, Cg, KD, KH, KW = (int(s) for s in weight.shape)
     if Cg * groups != int(x.shape[1]):
         raise ValueError(f"conv3d: input has {int(x.shape[1])} channels, weight expects {Cg} x {groups} groups")
-    s, d = _ntuple(stride, 3), _ntuple(dilation, 3)
+    s, d = _ntuple(stride, 3, "stride"), _ntuple(dilation, 3, "dilation")
     (pdf, _), pads, OD = conv3d_geometry(x.shape, (KD, KH, KW), s, padding, d)
     xg = depth_gather(x, groups, KD, OD, s[0], pdf, d[0], 1, padding_mode)
     y2 = conv2d(xg, gathered_kernel(on_device(weight)), bias, s[1:], pads, d[1:], groups, padding_mode)
@@ -627,7 +637,7 @@ def convt3d_geometry(x_shape, kernel, stride, padding, output_padding, dilation)
     """(depth pad of the equivalent stride-1 convolution, H/W pads, OD, OH, OW) of
     conv_transpose3d; OD = (D - 1) s - 2 p + d (k - 1) + op + 1 per axis."""
     _, _, D, H, W = x_shape
-    k, s, p = _ntuple(kernel, 3), _ntuple(stride, 3), _ntuple(padding, 3)
+    k, s, p = _ntuple(kernel, 3, "kernel_size"), _ntuple(stride, 3, "stride"), _ntuple(padding, 3, "padding")
     op, d = _ntuple(output_padding, 3), _ntuple(dilation, 3)
     if op[0] >= max(s[0], d[0]):
         raise ValueError("conv_transpose3d: output_padding must be smaller than stride or dilation")
@@ -652,7 +662,7 @@ def conv_transpose3d(x: Tensor, weight: Tensor, bias: Tensor | None = None, stri
     if int(x.shape[1]) != Cin:
         raise ValueError(f"conv_transpose3d: input has {int(x.shape[1])} channels, weight expects {Cin}")
     k = tuple(int(v) for v in weight.shape[2:])
-    s, d = _ntuple(stride, 3), _ntuple(dilation, 3)
+    s, d = _ntuple(stride, 3, "stride"), _ntuple(dilation, 3, "dilation")
     pd, pads, OD, _, _ = convt3d_geometry(x.shape, k, s, padding, output_padding, d)
     w = gathered_kernel(tensor_of(convt_kernel_nd(weight.numpy(), groups)))
     return convt3d_apply(x, s, pd, d[0], k[0], OD, groups, lambda xg: conv2d(xg, w, bias, 1, pads, d[1:], groups))

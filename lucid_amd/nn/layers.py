@@ -100,11 +100,10 @@ class Conv2d(Module):
                 f"stride={self.stride}, padding={self._padding_str or self.padding}")
 
 
-def _ntuple(v: Any, n: int) -> tuple[int, ...]:
-    if isinstance(v, (tuple, list)):
-        vals = tuple(int(x) for x in v)
-        return vals if len(vals) == n else (vals[0],) * n
-    return (int(v),) * n
+def _ntuple(v: Any, n: int, name: str = "") -> tuple[int, ...]:
+    from lucid_amd.nn.functional import _ntuple as ntuple
+
+    return ntuple(v, n, name)
 
 
 class _ConvNd(Module):
@@ -121,12 +120,12 @@ class _ConvNd(Module):
             raise ValueError("in_channels and out_channels must be divisible by groups")
         n = self._rank
         self.in_channels, self.out_channels = in_channels, out_channels
-        self.kernel_size, self.stride = _ntuple(kernel_size, n), _ntuple(stride, n)
+        self.kernel_size, self.stride = _ntuple(kernel_size, n, "kernel_size"), _ntuple(stride, n, "stride")
         if isinstance(padding, str):
             self._padding_str, self.padding = padding, (0,) * n
         else:
-            self._padding_str, self.padding = None, _ntuple(padding, n)
-        self.dilation, self.groups, self.padding_mode = _ntuple(dilation, n), groups, padding_mode
+            self._padding_str, self.padding = None, _ntuple(padding, n, "padding")
+        self.dilation, self.groups, self.padding_mode = _ntuple(dilation, n, "dilation"), groups, padding_mode
         fan_in = (in_channels // groups) * int(np.prod(self.kernel_size))
         bound = 1.0 / math.sqrt(fan_in) if fan_in > 0 else 0.0
         self.weight = Parameter(_uniform((out_channels, in_channels // groups, *self.kernel_size), bound))
@@ -203,9 +202,9 @@ class _ConvTransposeNd(Module):
             raise ValueError("in_channels and out_channels must be divisible by groups")
         n = self._rank
         self.in_channels, self.out_channels = in_channels, out_channels
-        self.kernel_size, self.stride = _ntuple(kernel_size, n), _ntuple(stride, n)
-        self.padding, self.output_padding = _ntuple(padding, n), _ntuple(output_padding, n)
-        self.dilation, self.groups = _ntuple(dilation, n), groups
+        self.kernel_size, self.stride = _ntuple(kernel_size, n, "kernel_size"), _ntuple(stride, n, "stride")
+        self.padding, self.output_padding = _ntuple(padding, n, "padding"), _ntuple(output_padding, n, "output_padding")
+        self.dilation, self.groups = _ntuple(dilation, n, "dilation"), groups
         fan_in = (out_channels // groups) * int(np.prod(self.kernel_size))
         bound = 1.0 / math.sqrt(fan_in) if fan_in > 0 else 0.0
         self.weight = Parameter(_uniform((in_channels, out_channels // groups, *self.kernel_size), bound))

@@ -45,9 +45,9 @@ class _QuantizedConvNd(Module):
         super().__init__()
         n = self._rank
         self.in_channels, self.out_channels = in_channels, out_channels
-        self.kernel_size, self.stride = F._ntuple(kernel_size, n), F._ntuple(stride, n)
-        self.padding = padding if isinstance(padding, str) else F._ntuple(padding, n)
-        self.dilation, self.groups = F._ntuple(dilation, n), groups
+        self.kernel_size, self.stride = F._ntuple(kernel_size, n, "kernel_size"), F._ntuple(stride, n, "stride")
+        self.padding = padding if isinstance(padding, str) else F._ntuple(padding, n, "padding")
+        self.dilation, self.groups = F._ntuple(dilation, n, "dilation"), groups
         self.padding_str: str | None = None
         self.padding_mode = "zeros"
         self.weight_ch_axis = 0
@@ -197,9 +197,9 @@ class _QuantizedConvTransposeNd(_QuantizedConvNd):
         Module.__init__(self)
         n = self._rank
         self.in_channels, self.out_channels = in_channels, out_channels
-        self.kernel_size, self.stride = F._ntuple(kernel_size, n), F._ntuple(stride, n)
-        self.padding, self.output_padding = F._ntuple(padding, n), F._ntuple(output_padding, n)
-        self.dilation, self.groups = F._ntuple(dilation, n), groups
+        self.kernel_size, self.stride = F._ntuple(kernel_size, n, "kernel_size"), F._ntuple(stride, n, "stride")
+        self.padding, self.output_padding = F._ntuple(padding, n, "padding"), F._ntuple(output_padding, n, "output_padding")
+        self.dilation, self.groups = F._ntuple(dilation, n, "dilation"), groups
         self.padding_str, self.padding_mode = None, "zeros"
         self.weight_ch_axis = 1
         self.out_qdtype: QDtype = quint8

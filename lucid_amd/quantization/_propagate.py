@@ -81,10 +81,13 @@ def names_a_recipe(mapping: QConfigMapping, module: Module, path: str) -> bool:
     return ruled and qconfig is not None
 
 
-def plan_sites(model: Module, mapping: QConfigMapping, *, stock_default: bool = False) -> list[Site]:
-    """Every module of ``model`` once (a module reachable along two paths is taken at its
-    first), parents before children and children in registration order, each with its
-    resolved recipe."""
+def plan_sites(model: Module, mapping: QConfigMapping, *, stock_default: bool = False,
+               every_occurrence: bool = False) -> list[Site]:
+    """Every module of ``model``, parents before children and children in registration
+    order, each with its resolved recipe.  A module reachable along two paths is taken at its
+    first only, unless ``every_occurrence``: then each (parent, attribute) slot is a site of
+    its own (a tied layer is swapped in every place it is used; only a module that contains
+    itself is cut off)."""
     seed = mapping.global_qconfig()
     if stock_default and any(hasattr(m, MARK) for m in model.modules()):
         seed = None  # the user configured modules: the stock default does not fill in
@@ -100,6 +103,8 @@ def plan_sites(model: Module, mapping: QConfigMapping, *, stock_default: bool = 
         sites.append(Site(parent, attr, module, path, qconfig))
         for name, child in list(module.named_children()):
             visit(module, name, child, f"{path}.{name}" if path else name, qconfig)
+        if every_occurrence:
+            visited.discard(id(module))  # ancestors only: siblings may hold it again
 
     visit(None, "", model, "", seed)
     return sites

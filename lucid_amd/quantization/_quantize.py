@@ -208,9 +208,10 @@ def _replace_dynamic(model: Module, mapping: QConfigMapping, labels: tuple[str, 
                      builders: dict, dtype: QDtype) -> Module:
     """Swap every planned site that has a recipe and a dynamic builder for its quantized form,
     parents first (a replaced module's subtree is not visited); returns the (possibly new)
-    root.  Warns when a rule names a leaf module that has no dynamic form, or when nothing
-    at all was replaced."""
-    sites = plan_sites(model, mapping)
+    root.  A module used at several places (a tied layer) is swapped at each of them, by one
+    quantized module built at its first place.  Warns when a rule names a leaf module that
+    has no dynamic form, or when nothing at all was replaced."""
+    sites = plan_sites(model, mapping, every_occurrence=True)
     root = sites[0]
     if root.qconfig is not None and type(model) in builders:
         return builders[type(model)](model, weight_dtype(root.qconfig, dtype))
@@ -220,12 +221,16 @@ def _replace_dynamic(model: Module, mapping: QConfigMapping, labels: tuple[str, 
     def under_replaced(site: Site) -> bool:
         return any(site.path.startswith(p + ".") for p in replaced)
 
+    built: dict[int, Module] = {}  # id of a float module -> its quantized form
     for site in sites[1:]:
         if under_replaced(site):
             continue
         build = builders.get(type(site.module))
         if site.qconfig is not None and build is not None:
-            setattr(site.parent, site.attr, build(site.module, weight_dtype(site.qconfig, dtype)))
+            key = id(site.module)
+            if key not in built:
+                built[key] = build(site.module, weight_dtype(site.qconfig, dtype))
+            setattr(site.parent, site.attr, built[key])
             replaced.append(site.path)
         elif (site.qconfig is not None and next(site.module.children(), None) is None
               and names_a_recipe(mapping, site.module, site.path)):

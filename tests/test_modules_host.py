@@ -225,6 +225,18 @@ def test_quantize_dynamic_replacement_and_warnings():
         run(nn.Sequential(nn.ReLU(), nn.Linear(2, 2)), {nn.ReLU})
     with pytest.warns(UserWarning, match=r"no module of a targeted type \(Conv2d\) found"):
         run(nn.Sequential(nn.ReLU()), {nn.Conv2d})
+    # a Linear tied at two places (the reference's swap walks every parent slot,
+    # lucid/quantization/_quantize.py:588-602): both slots are swapped, to one quantized module
+    shared = nn.Linear(4, 4)
+    tied = nn.Sequential(shared, nn.ReLU(), shared, nn.Sequential(shared))
+    run(tied, {nn.Linear})
+    assert isinstance(tied[0], Swapped) and tied[2] is tied[0] and tied[3][0] is tied[0]
+    assert tied[0].src is shared
+    # a tied layer excluded by name at one place stays float only there
+    shared = nn.Linear(4, 4)
+    tied = nn.Sequential(shared, shared)
+    run(tied, {"1": None, nn.Linear: qint8})
+    assert isinstance(tied[0], Swapped) and tied[1] is shared
 
 
 def test_quantized_module_state_dict_layouts():
@@ -369,3 +381,25 @@ def test_packed_sequence_validation():
         PackedSequence(data, [2, 2])
     with pytest.raises(ValueError, match="permutation"):
         PackedSequence(data, [2, 1], [0, 0])
+
+
+def test_conv_size_arguments_refuse_wrong_lengths():
+    """A convolution's size arguments are read as Lucid reads them (nn/modules/_conv_common.py:16,
+    nn/functional/_spatial_args.py:28): an int or a sequence of one repeats, a sequence of the
+    rank is taken, any other length raises -- and a kernel_size must name every axis."""
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized as nnq
+    from lucid_amd.nn.functional import _ntuple
+
+    assert _ntuple(3, 3) == (3, 3, 3) and _ntuple([2], 3, "stride") == (2, 2, 2)
+    assert _ntuple((1, 2, 3), 3, "kernel_size") == (1, 2, 3)
+    for bad, name in (((3, 5), "kernel_size"), ([2, 2, 2, 2], "stride"), ((3,), "kernel_size")):
+        with pytest.raises(ValueError, match=name):
+            _ntuple(bad, 3, name)
+    with pytest.raises(ValueError, match="kernel_size"):
+        nn.Conv3d(2, 2, kernel_size=(3, 5))
+    with pytest.raises(ValueError, match="stride"):
+        nn.Conv1d(2, 2, 3, stride=(1, 2))
+    with pytest.raises(ValueError, match="padding"):
+        nnq.Conv3d(2, 2, 3, padding=(1, 1))
+    assert nn.Conv3d(2, 2, 3, stride=[2]).stride == (2, 2, 2)
