@@ -94,6 +94,13 @@ int lq_malloc(void** d_ptr, size_t bytes);
 int lq_free(void* d_ptr);
 int lq_malloc_async(void** d_ptr, size_t bytes, void* stream);
 int lq_free_async(void* d_ptr, void* stream);
+/* Marks the live allocation d_ptr (as lq_malloc returned it) as used by work queued on
+ * `stream` besides the stream it will be freed on: at its free a completion event is
+ * recorded on `stream` too, and the block is handed out again -- on any stream -- only after
+ * that work has completed.  For tensors read or written by a side stream (graph replays,
+ * copies on their own stream).  No reference counterpart (Lucid's engine runs one stream);
+ * the role of torch's Tensor.record_stream. */
+int lq_record_stream(void* d_ptr, void* stream);
 int lq_empty_cache(void);
 /* Bytes currently handed out / held in the cache by the allocator. */
 int lq_memory_stats(size_t* allocated, size_t* cached);
@@ -103,6 +110,8 @@ int lq_memcpy_d2d(void* d_dst, const void* d_src, size_t bytes, void* stream);
 /* Fill `count` 32-bit words with `value` using a kernel (graph-capture safe). */
 int lq_fill_u32(void* d_dst, uint32_t value, size_t count, void* stream);
 int lq_stream_create(void** stream);
+/* Waits for the stream's work, drops it from every allocation's lq_record_stream uses, then
+ * destroys it. */
 int lq_stream_destroy(void* stream);
 int lq_stream_synchronize(void* stream);
 int lq_device_synchronize(void);
@@ -117,6 +126,8 @@ int lq_event_elapsed_ms(float* ms, void* start, void* stop);
  * such as per-token decode.  Every compute entry point is capture-safe: none of them
  * allocates, memsets or synchronizes inside a call. */
 int lq_graph_begin_capture(void* stream);
+/* *graph_exec: an opaque handle owning the captured graph and its executable form, both
+ * kept until lq_graph_destroy. */
 int lq_graph_end_capture(void* stream, void** graph_exec);
 int lq_graph_launch(void* graph_exec, void* stream);
 int lq_graph_destroy(void* graph_exec);

@@ -61,6 +61,7 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_free": (_I, [_P]),
     "lq_malloc_async": (_I, [ctypes.POINTER(_P), _SZ, _P]),
     "lq_free_async": (_I, [_P, _P]),
+    "lq_record_stream": (_I, [_P, _P]),
     "lq_empty_cache": (_I, []),
     "lq_memory_stats": (_I, [ctypes.POINTER(_SZ), ctypes.POINTER(_SZ)]),
     "lq_memcpy_h2d": (_I, [_P, _P, _SZ, _P]),

@@ -276,6 +276,17 @@ class Tensor:
     def gpu(self) -> "Tensor":
         return self.to("gpu")
 
+    def record_stream(self, stream: Any) -> None:
+        """Mark this device tensor's storage as used by work queued on ``stream`` (an
+        ``lq_stream_create`` handle), so that when the storage is freed it is not handed out
+        again before that work completes (``lq_record_stream``).  Device memory is freed on
+        the null stream; work on a created stream is not ordered with it without this."""
+        if self._device == "cpu":
+            return
+        if self._buf is None:
+            self._materialize()
+        _C.call("lq_record_stream", self._buf.ptr, stream)
+
     def detach(self) -> "Tensor":
         return self
 

@@ -166,6 +166,12 @@ class DynLinear:
         self.g_bytes = max(max(lib.lq_gemm_w8a8_workspace_size(m, self.N, self.K) for m in (1, max_rows)), 16)
         self.g_ws = empty((self.g_bytes,), np.uint8, "gpu")
 
+    def tensors(self) -> list:
+        """Every device tensor a call reads or writes."""
+        w = self.w
+        return [t for t in (self.qp, self.codes, self.mm_ws, self.g_ws, self.packed, self.bias, w.codes, w.scale,
+                            w.sums) if t is not None]
+
     def __call__(self, x: int, rows: int, y: int, stream) -> None:
         n = rows * self.K
         q = self.qp.data_ptr()
@@ -216,8 +222,25 @@ class Int8Decoder:
         self.next = empty((batch,), np.int32, "gpu")
         self.pos = empty((1,), np.int32, "gpu")
         self.scale = float(np.float32(1.0 / np.sqrt(self.hd)))
+        self._streams: set = set()
+
+    def _use_stream(self, stream) -> None:
+        """Tie every buffer and weight the steps touch to ``stream`` (once per stream): when
+        this runtime is dropped while work queued there is still running, the allocator does
+        not hand the memory out before that work completes (``Tensor.record_stream``)."""
+        key = getattr(stream, "value", stream)
+        if key is None or key in self._streams:
+            return
+        self._streams.add(key)
+        bufs = [self.tok, self.posemb, self.h, self.hn, self.att, self.proj, self.qkv, self.up, self.hl,
+                self.logits, self.q16, self.prompt, self.next, self.pos]
+        bufs += [t for kv in self.cache for t in kv]
+        bufs += [t for lins in self.layers for lin in lins for t in lin.tensors()] + self.head.tensors()
+        for t in bufs:
+            t.record_stream(stream)
 
     def _step(self, tokens: int, n: int, stream) -> None:
+        self._use_stream(stream)
         B, D, H, hd = self.B, self.D, self.H, self.hd
         M = B * n
         p = self.pos.data_ptr()

@@ -9,7 +9,13 @@
 //   * its marker reports completion: the work queued on the freeing stream before the free
 //     has finished, so no kernel still reads or writes the block.
 // A block whose stream recorded no marker (a stream under graph capture) is reused on that
-// stream only.  Requests are served from blocks of up to twice the rounded size.
+// stream only.  A live block may also be marked as used on other streams (record_use, the
+// role of torch's record_stream): its free then records a marker on each of them too, and
+// the block is reused -- on any stream, the freeing one included -- only once every one of
+// those markers reports completion (a use stream that records no marker keeps the block out
+// of circulation until drain).  A stream about to be destroyed is first dropped from those
+// records (forget_stream, after its work has finished).  Requests are served from blocks of
+// up to twice the rounded size.
 #pragma once
 
 #include <stddef.h>
@@ -36,6 +42,7 @@ public:
         void* ptr;
         void* stream;  // stream of the last use (the free's stream)
         void* marker;  // completion marker on that stream, or nullptr (stream-bound)
+        std::vector<void*> uses;  // markers on the other streams that used it (nullptr: none recordable)
     };
 
     explicit BlockCache(MarkerOps ops) : ops_(ops) {}
@@ -56,11 +63,15 @@ public:
             FreeBlock& b = it->second;
             const bool same_stream = b.stream == stream;
             if (!same_stream && !(b.marker && ops_.done(b.marker))) continue;
+            bool uses_done = true;
+            for (void* m : b.uses) uses_done = uses_done && m && ops_.done(m);
+            if (!uses_done) continue;
             void* p = b.ptr;
             const size_t got = it->first;
             if (b.marker) ops_.release(b.marker);
+            for (void* m : b.uses) ops_.release(m);
             fl.erase(it);
-            live_[p] = Live{got, device};
+            live_[p] = Live{got, device, {}};
             cached_ -= got;
             allocated_ += got;
             return p;
@@ -71,8 +82,34 @@ public:
     // Registers a fresh allocation as live.
     void add_live(void* p, int device, size_t rounded) {
         std::lock_guard<std::mutex> g(mu_);
-        live_[p] = Live{rounded, device};
+        live_[p] = Live{rounded, device, {}};
         allocated_ += rounded;
+    }
+
+    // Marks a live block as used on `stream` besides the one it will be freed on; false if
+    // `p` is not live.
+    bool record_use(void* p, void* stream) {
+        std::lock_guard<std::mutex> g(mu_);
+        auto it = live_.find(p);
+        if (it == live_.end()) return false;
+        auto& u = it->second.uses;
+        bool seen = false;
+        for (void* s : u) seen = seen || s == stream;
+        if (!seen) u.push_back(stream);
+        return true;
+    }
+
+    // Drops `stream` from every live block's recorded uses: the caller has waited for the
+    // stream's work and is about to destroy it, and a free must not record a marker on a
+    // destroyed stream.
+    void forget_stream(void* stream) {
+        std::lock_guard<std::mutex> g(mu_);
+        for (auto& kv : live_) {
+            auto& u = kv.second.uses;
+            for (size_t i = 0; i < u.size();)
+                if (u[i] == stream) u.erase(u.begin() + (long)i);
+                else ++i;
+        }
     }
 
     // Returns a live block to the cache as last used on `stream`; false if `p` is not live.
@@ -84,7 +121,10 @@ public:
         live_.erase(it);
         allocated_ -= l.size;
         cached_ += l.size;
-        free_[l.device].emplace(l.size, FreeBlock{p, stream, ops_.record(stream)});
+        FreeBlock fb{p, stream, ops_.record(stream), {}};
+        for (void* s : l.uses)
+            if (s != stream) fb.uses.push_back(ops_.record(s));
+        free_[l.device].emplace(l.size, std::move(fb));
         return true;
     }
 
@@ -96,6 +136,8 @@ public:
         for (auto& kv : free_)
             for (auto& e : kv.second) {
                 if (e.second.marker) ops_.release(e.second.marker);
+                for (void* m : e.second.uses)
+                    if (m) ops_.release(m);
                 out.emplace_back(kv.first, e.second.ptr);
             }
         free_.clear();
@@ -113,6 +155,7 @@ private:
     struct Live {
         size_t size;
         int device;
+        std::vector<void*> uses;  // streams recorded by record_use
     };
     MarkerOps ops_;
     std::mutex mu_;

@@ -172,6 +172,12 @@ int lq_free_async(void* d_ptr, void* stream) {
 
 int lq_free(void* d_ptr) { return lq_free_async(d_ptr, nullptr); }
 
+int lq_record_stream(void* d_ptr, void* stream) {
+    LQ_REQUIRE(d_ptr, "lq_record_stream: NULL pointer");
+    if (!cache().record_use(d_ptr, stream)) return set_error(LQ_ERR_INVALID, "lq_record_stream: pointer not from lq_malloc");
+    return LQ_OK;
+}
+
 int lq_empty_cache(void) {
     const auto victims = cache().drain();
     if (!victims.empty()) {
@@ -228,6 +234,14 @@ __global__ void lq_fill_u32_kernel(uint32_t* __restrict__ dst, uint32_t value, s
     for (; i < count; i += stride) dst[i] = value;
 }
 
+namespace lq {
+// A captured graph and its executable form, owned together by an lq_graph_* handle.
+struct CapturedGraph {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+};
+}  // namespace lq
+
 extern "C" {
 
 int lq_fill_u32(void* d_dst, uint32_t value, size_t count, void* stream) {
@@ -250,6 +264,10 @@ int lq_stream_create(void** stream) {
 
 int lq_stream_destroy(void* stream) {
     if (!stream) return LQ_OK;
+    // blocks that recorded a use on this stream must not record an event on it once it is
+    // gone: wait for its work, then drop it from their records
+    LQ_HIP(hipStreamSynchronize(as_stream(stream)));
+    cache().forget_stream(stream);
     LQ_HIP(hipStreamDestroy(as_stream(stream)));
     return LQ_OK;
 }
@@ -308,20 +326,32 @@ int lq_graph_end_capture(void* stream, void** graph_exec) {
     LQ_HIP(hipStreamEndCapture((hipStream_t)stream, &g));
     hipGraphExec_t e = nullptr;
     const hipError_t err = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(g);  // the executable graph keeps what it needs
-    if (err != hipSuccess) return check_hip(err, "hipGraphInstantiate");
-    *graph_exec = (void*)e;
+    if (err != hipSuccess) {
+        (void)hipGraphDestroy(g);
+        return check_hip(err, "hipGraphInstantiate");
+    }
+    // The handle owns both graphs: the captured one stays alive for as long as its
+    // executable form (a tool that maps an executable graph's nodes back to the captured
+    // graph at launch, such as a tracing profiler, reads it), and both go in
+    // lq_graph_destroy.
+    *graph_exec = new CapturedGraph{g, e};
     return LQ_OK;
 }
 
 int lq_graph_launch(void* graph_exec, void* stream) {
     LQ_REQUIRE(graph_exec, "lq_graph_launch: NULL graph");
-    LQ_HIP(hipGraphLaunch((hipGraphExec_t)graph_exec, (hipStream_t)stream));
+    LQ_HIP(hipGraphLaunch(static_cast<CapturedGraph*>(graph_exec)->exec, (hipStream_t)stream));
     return LQ_OK;
 }
 
 int lq_graph_destroy(void* graph_exec) {
-    if (graph_exec) LQ_HIP(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+    if (!graph_exec) return LQ_OK;
+    CapturedGraph* cg = static_cast<CapturedGraph*>(graph_exec);
+    const hipError_t e1 = hipGraphExecDestroy(cg->exec);
+    const hipError_t e2 = hipGraphDestroy(cg->graph);
+    delete cg;
+    LQ_HIP(e1);
+    LQ_HIP(e2);
     return LQ_OK;
 }
 

@@ -1,6 +1,7 @@
 // CPU check of the caching allocator's bookkeeping (lucid_amd/csrc/lq_block_cache.h) with
 // fake completion markers: same-stream reuse, cross-stream reuse only after completion,
-// stream-bound blocks without a marker, the size window, per-device lists, stats and drain.
+// stream-bound blocks without a marker, side-stream uses (record_use), the size window,
+// per-device lists, stats and drain.
 // Built and run by tests/test_block_cache.py; prints "ok" and exits 0 on success.
 #include <cstdio>
 #include <cstdlib>
@@ -92,6 +93,44 @@ int main() {
     CHECK(c.take(0, 4096, reinterpret_cast<void*>(0x30)) == a);  // a completed: any stream
     CHECK(c.take(0, 4096, reinterpret_cast<void*>(0x30)) == nullptr);  // b: bound to s2
     CHECK(c.take(0, 4096, s2) == b);
+
+    // side-stream use (record_use): a block freed on the null stream after work on s2 read
+    // it is reused -- even on the null stream itself -- only after s2's work completes
+    void* s0 = nullptr;
+    CHECK(c.put(a, s1) && c.put(b, s2));
+    complete_all(s1);
+    complete_all(s2);
+    CHECK(c.take(0, 4096, s0) != nullptr && c.take(0, 4096, s0) != nullptr);  // a and b, live again
+    CHECK(!c.record_use(&pool[2], s2));  // not live
+    CHECK(c.record_use(a, s2) && c.record_use(a, s2));  // recorded once
+    CHECK(c.put(a, s0));
+    CHECK(c.take(0, 4096, s0) == nullptr);  // s2's marker pending: not even on the free stream
+    complete_all(s0);
+    CHECK(c.take(0, 4096, s1) == nullptr);
+    complete_all(s2);
+    CHECK(c.take(0, 4096, s0) == a);
+    // a use stream that cannot record a marker keeps the block out until drain
+    CHECK(c.record_use(a, s2));
+    g_no_marker_streams = true;
+    CHECK(c.put(a, s1));  // neither s1 nor s2 can record
+    g_no_marker_streams = false;
+    CHECK(c.take(0, 4096, s1) == nullptr);
+    // the use list does not survive a free: a's next life starts clean
+    CHECK(c.put(b, s0));
+    complete_all(s0);
+    CHECK(c.take(0, 4096, s2) == b);
+    CHECK(c.put(b, s2));
+    CHECK(c.take(0, 4096, s2) == b);
+    (void)c.drain();  // a (held back) goes to the caller; markers released
+    CHECK(c.take(0, 4096, s1) == nullptr);
+    c.add_live(a, 0, 4096);
+    // a use stream destroyed before the free (forget_stream): no marker is recorded on it
+    CHECK(c.record_use(a, s2));
+    c.forget_stream(s2);
+    const size_t before = g_live_markers.size();
+    CHECK(c.put(a, s1));
+    CHECK(g_live_markers.size() == before + 1);  // only s1's
+    CHECK(c.take(0, 4096, s1) == a);
 
     // stats and drain
     size_t al = 0, ca = 0;
