@@ -51,6 +51,10 @@ def _parse() -> argparse.Namespace:
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--components", dest="components", action="store_true", default=True)
     p.add_argument("--no-components", dest="components", action="store_false")
+    p.add_argument("--only", default="",
+                   help="comma-separated component groups to run (gemm_sweep, weight_only_gemv, "
+                        "conv_resnet18_b32, bandwidth, config2_quant_sizes, lookup, models, dispatch); "
+                        "default all -- for profiling one group")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="bound on the CPU-baseline sample's wall time")
     p.add_argument("--copy-mb", type=int, default=0,
@@ -398,24 +402,24 @@ def bandwidth_lines(L, C, timer, steps, warmup):
     out = {}
 
     def obs():
-        lib.lq_minmax_f32(xp, n, rmin.data_ptr(), rmax.data_ptr(), C.OBS_MINMAX, 0.0, ws.data_ptr(),
-                          ws_bytes, None)
+        C.call("lq_minmax_f32", xp, n, rmin.data_ptr(), rmax.data_ptr(), C.OBS_MINMAX, 0.0, ws.data_ptr(),
+               ws_bytes, None)
 
     def quant():
-        lib.lq_quantize_per_tensor_f32(xp, qp, n, C.I8, scale.data_ptr(), zp.data_ptr(), 0.0, 0.0,
-                                       -128, 127, None)
+        C.call("lq_quantize_per_tensor_f32", xp, qp, n, C.I8, scale.data_ptr(), zp.data_ptr(), 0.0, 0.0,
+               -128, 127, None)
 
     def dequant():
-        lib.lq_dequantize_per_tensor(qp, C.I8, yp, C.F32, n, scale.data_ptr(), zp.data_ptr(), 0.0,
-                                     0.0, None)
+        C.call("lq_dequantize_per_tensor", qp, C.I8, yp, C.F32, n, scale.data_ptr(), zp.data_ptr(), 0.0,
+               0.0, None)
 
     def qhardswish():  # nnq.Hardswish over float input: activation + grid codes in one pass
-        lib.lq_qact(C.ACT_HARDSWISH, xp, C.F32, None, None, n, 0.0, scale.data_ptr(), zp.data_ptr(), -128,
-                    127, C.I8, qp, None)
+        C.call("lq_qact", C.ACT_HARDSWISH, xp, C.F32, None, None, n, 0.0, scale.data_ptr(), zp.data_ptr(), -128,
+               127, C.I8, qp, None)
 
     def qsigmoid_codes():  # nnq.Sigmoid over the int8 codes of a quantized layer's output
-        lib.lq_qact(C.ACT_SIGMOID, qp, C.I8, scale.data_ptr(), zp.data_ptr(), n, 0.0, scale.data_ptr(),
-                    zp.data_ptr(), -128, 127, C.I8, yp, None)
+        C.call("lq_qact", C.ACT_SIGMOID, qp, C.I8, scale.data_ptr(), zp.data_ptr(), n, 0.0, scale.data_ptr(),
+               zp.data_ptr(), -128, 127, C.I8, yp, None)
 
     for name, fn, bpe in (("minmax_observer", obs, 4), ("quantize_f32_to_i8", quant, 5),
                           ("dequantize_i8_to_f32", dequant, 5), ("qhardswish_f32_to_i8", qhardswish, 5),
@@ -497,12 +501,12 @@ def lookup_lines(L, C, timer, steps, warmup):
     lib = C.lib()
 
     def bag():
-        lib.lq_embedding_bag(codes.data_ptr(), C.I8_QPAIR, sz.data_ptr(), None, rows, D, idx.data_ptr(), C.I64,
-                             bags * per, off.data_ptr(), C.I64, bags, 0, 0, C.BAG_MEAN, -1, None, y.data_ptr(), None)
+        C.call("lq_embedding_bag", codes.data_ptr(), C.I8_QPAIR, sz.data_ptr(), None, rows, D, idx.data_ptr(),
+               C.I64, bags * per, off.data_ptr(), C.I64, bags, 0, 0, C.BAG_MEAN, -1, None, y.data_ptr(), None)
 
     def bag_separate():
-        lib.lq_embedding_bag(codes.data_ptr(), C.I8, s.data_ptr(), z.data_ptr(), rows, D, idx.data_ptr(), C.I64,
-                             bags * per, off.data_ptr(), C.I64, bags, 0, 0, C.BAG_MEAN, -1, None, y.data_ptr(), None)
+        C.call("lq_embedding_bag", codes.data_ptr(), C.I8, s.data_ptr(), z.data_ptr(), rows, D, idx.data_ptr(),
+               C.I64, bags * per, off.data_ptr(), C.I64, bags, 0, 0, C.BAG_MEAN, -1, None, y.data_ptr(), None)
 
     nbytes = bags * per * (D + 8 + 8) + bags * (8 + 4 * D)
     out = {}
@@ -858,19 +862,29 @@ def main() -> None:
                      "ops": "int8 multiply-adds, 2 ops each (the contract's unit name is TFLOP/s)"},
     }
     if args.components:
-        comps = {"gemm_sweep": []}
-        for (m, n, k) in ((1, 4096, 4096), (16, 4096, 4096), (1, 11008, 4096), (16, 11008, 4096),
-                          (1, 4096, 11008), (16, 4096, 11008), (128, 4096, 4096), (1024, 4096, 4096),
-                          (4096, 4096, 4096), (4096, 11008, 4096), (4096, 4096, 11008)):
-            for kind in (C.OUT_Q8, C.OUT_F16):
-                comps["gemm_sweep"].append(gemm_line(L, C, timer, gtimer, m, n, k, kind, 20, 5))
-        comps["weight_only_gemv"] = weight_only_lines(L, C, gtimer)
-        comps["conv_resnet18_b32"] = conv_lines(L, C, timer, 10, 3)
-        comps.update(bandwidth_lines(L, C, timer, 50, 10))
-        comps["config2_quant_sizes"] = config2_lines(L, C, gtimer)
-        comps.update(lookup_lines(L, C, timer, 20, 5))
-        comps["models"] = model_lines(L, C, gtimer, args.cpu_seconds > 0)
-        if args.cpu_seconds > 0:
+        only = {g for g in args.only.split(",") if g}
+        run = lambda group: not only or group in only  # noqa: E731
+        comps = {}
+        if run("gemm_sweep"):
+            comps["gemm_sweep"] = []
+            for (m, n, k) in ((1, 4096, 4096), (16, 4096, 4096), (1, 11008, 4096), (16, 11008, 4096),
+                              (1, 4096, 11008), (16, 4096, 11008), (128, 4096, 4096), (1024, 4096, 4096),
+                              (4096, 4096, 4096), (4096, 11008, 4096), (4096, 4096, 11008)):
+                for kind in (C.OUT_Q8, C.OUT_F16):
+                    comps["gemm_sweep"].append(gemm_line(L, C, timer, gtimer, m, n, k, kind, 20, 5))
+        if run("weight_only_gemv"):
+            comps["weight_only_gemv"] = weight_only_lines(L, C, gtimer)
+        if run("conv_resnet18_b32"):
+            comps["conv_resnet18_b32"] = conv_lines(L, C, timer, 10, 3)
+        if run("bandwidth"):
+            comps.update(bandwidth_lines(L, C, timer, 50, 10))
+        if run("config2_quant_sizes"):
+            comps["config2_quant_sizes"] = config2_lines(L, C, gtimer)
+        if run("lookup"):
+            comps.update(lookup_lines(L, C, timer, 20, 5))
+        if run("models"):
+            comps["models"] = model_lines(L, C, gtimer, args.cpu_seconds > 0)
+        if args.cpu_seconds > 0 and not only:
             comps["cpu_legs"] = cpu_micro_legs()
         line["components"] = comps
     line["cpu_baseline"] = cpu_baseline(M, N, K, args.cpu_seconds)

@@ -85,12 +85,21 @@ __host__ __device__ inline float bf16_bits_to_f32(uint16_t b) {
 
 // A float32 value rounded to the precision of a narrower float type and kept in float32:
 // mode 0 none, 1 IEEE half (values past the half range become infinities), 2 bfloat16.
-// This is the value of Lucid's astype(x.dtype) of a float32 operand.
+// This is the value of Lucid's astype(x.dtype) of a float32 operand.  round_to is for values
+// loaded from memory (no arithmetic to fuse the rounding into, and no barrier that would hold
+// back the loads around it); round_result_to for values just computed, whose half rounding
+// must not fold into the arithmetic that produced them (see f32_to_f16_rn).
 enum { LQ_ROUND_NONE = 0, LQ_ROUND_F16 = 1, LQ_ROUND_BF16 = 2 };
 __device__ __forceinline__ float round_to(float v, int mode) {
+    // both roundings, then a select: no branch to split the loads around a call site into
+    // separately waited groups
+    const float h = __half2float(__float2half_rn(v));
+    const float b = bf16_bits_to_f32(f32_to_bf16_bits(v));
+    return mode == LQ_ROUND_F16 ? h : mode == LQ_ROUND_BF16 ? b : v;
+}
+__device__ __forceinline__ float round_result_to(float v, int mode) {
     if (mode == LQ_ROUND_F16) return __half2float(f32_to_f16_rn(v));
-    if (mode == LQ_ROUND_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(v));
-    return v;
+    return round_to(v, mode);
 }
 
 // clip with NaN pass-through and Lucid's signed-zero tie rule (backend/cpu/Vdsp.cpp:33-62).

@@ -105,8 +105,12 @@ __device__ __forceinline__ f4 mfma16(h8 a, h8 b, f4 c) {
 // is exact in float32 before its rounding (24 >= 2 p + 2 bits), so the float32 add then round
 // equals the narrow add.  hmode 0 leaves the float32 result as it is.
 __device__ __forceinline__ float wo_finish(float v, bool has_bias, float b, int relu, int hmode) {
-    v = round_to(v, hmode);
-    if (has_bias) v = round_to(v + round_to(b, hmode), hmode);
+    if (hmode == LQ_ROUND_NONE) {
+        if (has_bias) v = v + b;
+    } else {
+        v = round_result_to(v, hmode);
+        if (has_bias) v = round_result_to(v + round_to(b, hmode), hmode);
+    }
     if (relu && v <= 0.0f) v = 0.0f;
     return v;
 }
@@ -787,8 +791,9 @@ __device__ __forceinline__ uint32_t opaque_and(uint32_t v, uint32_t m) {
 
 constexpr bool wv_persistent(bool grouped, int mx, int j) { return !grouped && mx == 1 && j <= 4; }
 
-template <int BITS, bool SIGNED, bool GROUPED, int MX, bool XF32, int J>
+template <int BITS, bool SIGNED, bool GROUPED, int MX, bool XF32, int J, int HM = LQ_ROUND_NONE>
 __global__ __launch_bounds__(1024) void wo_gemv_valu_kernel(WvArgs a) {
+    // HM: the group scales' rounding (a.hmode as a constant, so the default costs nothing)
     constexpr int CK = 16 * 8 / BITS;  // codes per 16-byte chunk
     extern __shared__ __attribute__((aligned(16))) float wv_lds[];
     float* xs = wv_lds;                                   // [MX][Kpad], swizzled
@@ -809,8 +814,8 @@ __global__ __launch_bounds__(1024) void wo_gemv_valu_kernel(WvArgs a) {
             w[j] = __builtin_nontemporal_load(reinterpret_cast<const vu4*>(row) + c);
             if constexpr (GROUPED) {
                 const int64_t gi = (int64_t)n * a.G + min((lane + 64 * j) * CK / a.gs, a.G - 1);
-                sgv[j] = round_to(a.w_scale[gi], a.hmode);
-                bgv[j] = a.g_bias ? round_to(a.g_bias[gi], a.hmode) : 0.0f;
+                sgv[j] = a.w_scale[gi];  // rounded to x's type where used: a rounding here would
+                bgv[j] = a.g_bias ? a.g_bias[gi] : 0.0f;  // wait for the prefetched row's loads
             }
         }
     };
@@ -964,8 +969,8 @@ __global__ __launch_bounds__(1024) void wo_gemv_valu_kernel(WvArgs a) {
                 const int g = min(k0 / a.gs, a.G - 1);
 #pragma unroll
                 for (int m = 0; m < MX; ++m) {
-                    acc[m] = fmaf(sg[j], p[m], acc[m]);
-                    if (first) acc[m] = fmaf(bg[j], gsum[m * a.G + g], acc[m]);
+                    acc[m] = fmaf(round_to(sg[j], HM), p[m], acc[m]);
+                    if (first) acc[m] = fmaf(round_to(bg[j], HM), gsum[m * a.G + g], acc[m]);
                 }
             } else {
 #pragma unroll
@@ -1369,7 +1374,15 @@ bool launch_wv(WvArgs a, bool xf32, hipStream_t st) {
         constexpr bool XV = decltype(xf)::value;
         constexpr bool fits = !GROUPED || (JV <= 8 && !(BITS == 4 && MXV == 2 && JV > 4));
         if constexpr (fits) {
-            hipLaunchKernelGGL((wo_gemv_valu_kernel<BITS, SIGNED, GROUPED, MXV, XV, JV>), grid, block, lds, st, a);
+            // group scales rounded to x's type: half x always, bfloat16 on request
+            if constexpr (GROUPED && !XV)
+                hipLaunchKernelGGL((wo_gemv_valu_kernel<BITS, SIGNED, GROUPED, MXV, XV, JV, LQ_ROUND_F16>), grid,
+                                   block, lds, st, a);
+            else if (GROUPED && a.hmode == LQ_ROUND_BF16)
+                hipLaunchKernelGGL((wo_gemv_valu_kernel<BITS, SIGNED, GROUPED, MXV, XV, JV, LQ_ROUND_BF16>), grid,
+                                   block, lds, st, a);
+            else
+                hipLaunchKernelGGL((wo_gemv_valu_kernel<BITS, SIGNED, GROUPED, MXV, XV, JV>), grid, block, lds, st, a);
             note_path("wo valu");
             return true;
         } else {

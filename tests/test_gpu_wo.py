@@ -255,7 +255,7 @@ def test_gemv_w8_packed(gpu, M, N, K, half):
     xr = x.astype(np.float16).astype(np.float32) if half else x
     _close(got, _gemv_ref(xr, W, s, z=z, b=b, relu=True), half=half)
     rowmajor = run_gemv(gpu, x, W, s, z=z, b=b, relu=True, half=half)
-    if _C.last_path() == "wo split-k" or _C.last_path() == "wo split-k single range":
+    if _C.last_path() in ("wo split-k", "wo split-k single range"):
         np.testing.assert_array_equal(got.view(np.uint16 if half else np.uint32),
                                       rowmajor.view(np.uint16 if half else np.uint32))
 
@@ -666,3 +666,4 @@ def test_quantized_linear_mlx_module_bf16(gpu):
                          sd["biases"].numpy(), 64, 4, "bf16")
     mag = np.maximum(np.maximum(np.abs(got), np.abs(want)), np.abs(pre))
     assert np.max(np.abs(got - want) / _ulp(mag, "bf16")) <= 1.0
+
