@@ -57,7 +57,7 @@ def warm_ms(C, call, n_warmup: int, n_iter: int) -> tuple[float, float, float]:
             samples[min(n_iter - 1, int(n_iter * 0.95))])
 
 
-def run(iters: int = 20, width: int = 1024, seed: int = 20260920) -> dict:
+def run(iters: int = 20, width: int = 1024, seed: int = 20260920, verbose: bool = True) -> dict:
     import lucid_amd as L
     from lucid_amd import _C as C
     from lucid_amd.nn import functional as F
@@ -109,7 +109,8 @@ def run(iters: int = 20, width: int = 1024, seed: int = 20260920) -> dict:
                     "host_cores": os.cpu_count(),
                 }
                 rows.append(row)
-                print(json.dumps(row), flush=True)
+                if verbose:
+                    print(json.dumps(row), flush=True)
     return {
         "environment": {"platform": platform.platform(), "python": platform.python_version(),
                         "device": "AMD Instinct MI355X (gfx950)",

@@ -61,6 +61,32 @@ def random_weight(rng: np.random.Generator, n: int, k: int) -> tuple:
     return q, rng.uniform(1e-4, 1e-3, n).astype(F32), np.zeros(n, F32), rng.normal(0, 0.02, n).astype(F32)
 
 
+# ------------------------------------------------------------------- configuration 3
+
+
+def w8a8_linear(A: np.ndarray, B: np.ndarray, sa: np.ndarray, sb: np.ndarray, bias: np.ndarray,
+                out_scale: float) -> np.ndarray:
+    """The W8A8 Linear of the headline as Lucid's CPU path computes it (nn/quantized/
+    linear.py:206-215): dequantize the int8 activations (per-row scale sa [M, 1], zero point 0)
+    and weights (per-output-channel scale sb [N, 1]) in separate passes, fp32 sgemm with the
+    weight transposed, bias add, then the multi-pass requantize onto the int8 output grid
+    (multiply by the float32 reciprocal of out_scale, round half even, add zero point 0, clip,
+    cast)."""
+    xa = A.astype(F32)
+    xa = xa - F32(0.0)
+    xa = xa * sa
+    wb = B.astype(F32)
+    wb = wb - F32(0.0)
+    wb = wb * sb
+    y = xa @ wb.T
+    y = y + bias
+    t = y * (F32(1.0) / F32(out_scale))
+    t = np.rint(t)
+    t = t + F32(0.0)
+    t = np.clip(t, -128, 127)
+    return t.astype(np.int8)
+
+
 # ------------------------------------------------------------------- configuration 1
 
 

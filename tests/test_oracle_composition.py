@@ -244,3 +244,27 @@ def test_conv_layer_matches_pinned_composition():
         worst, rate = _code_diff(tr["pre_quant"], pin, *act)
         print(f"conv {cin}->{cout} k{k}/{st} codes: worst {worst}, rate {rate:.2e}")
         assert worst <= 1 and rate < 5e-3
+
+
+def test_w8a8_linear_matches_pinned_integer_composition():
+    """The headline's CPU step (dequantize A and B, fp32 sgemm, bias, multi-pass requantize)
+    against the pinned integer composition (exact int32 sum, then the epilogue): its float
+    result before the requantize within the scale-aware rtol 1e-5 of the float64 product, and
+    the int8 codes within one code, at a reported rate."""
+    rng = np.random.default_rng(15)
+    M, N, K = 64, 96, 512
+    A = rng.integers(-127, 128, (M, K)).astype(np.int8)
+    B = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    sa = rng.uniform(1e-3, 1e-1, (M, 1)).astype(F32)
+    sb = rng.uniform(1e-3, 1e-1, (N, 1)).astype(F32)
+    bias = rng.standard_normal(N).astype(F32)
+    got = LM.w8a8_linear(A, B, sa, sb, bias, 64.0).astype(np.int64)
+    acc = O.gemm_acc(A, B).astype(np.float64)
+    y64 = acc * (sa.astype(np.float64) * sb.astype(np.float64).T) + bias
+    want_codes = O.gemm_w8a8(A, B, sa.ravel(), sb.ravel(), bias=bias, out_scale=64.0, out_kind=O.OUT_Q8).astype(np.int64)
+    d = np.abs(got - want_codes)
+    print(f"w8a8 codes vs the integer composition: worst {d.max()}, rate {(d != 0).mean():.2e}")
+    assert d.max() <= 1 and (d != 0).mean() < 5e-3
+    # the float stage: the codes are the pinned rule applied to a float32 product close to y64
+    float_codes = O.quantize(y64.astype(F32), O.recip_tensor(F32(64.0)), 0.0, -128, 127, O.I8).astype(np.int64)
+    assert np.abs(got - float_codes).max() <= 1
