@@ -193,6 +193,18 @@ int lq_calc_qparams_f32(const float* d_min, const float* d_max, int64_t n, int s
  * lq_quantize_per_tensor_f32 with the device scale; one launch for n <= 16384 (workspace
  * unused), those three otherwise (workspace of lq_dynamic_quantize_workspace_size(n) bytes). */
 size_t lq_dynamic_quantize_workspace_size(int64_t n);
+/* lq_layer_norm_f32 (d_res NULL) or lq_add_layer_norm_f32 (x += res written back first) on
+ * rows x D, then lq_dynamic_quantize_f32 of the normalized rows into codes q [rows, D] and
+ * d_qparams {min, max, scale, zero point}: one launch, the same bits (the normalized values
+ * stay on chip).  The input step of a dynamic Linear after a LayerNorm (nn.LayerNorm ->
+ * lucid/nn/quantized/dynamic/linear.py:85-92); rows * D <= 12288 (LQ_ERR_UNSUPPORTED above). */
+int lq_layer_norm_quantize_f32(float* d_x, int64_t ldx, const float* d_res, int64_t ldres, int64_t rows, int64_t D,
+                               const float* d_gamma, const float* d_beta, float ln_eps, int q_dtype, int qmin,
+                               int qmax, float eps, float* d_qparams, void* d_q, void* stream);
+/* lq_gelu_tanh_f32 then lq_dynamic_quantize_f32 of the result, in one launch with the same
+ * bits (F.gelu(approximate="tanh") feeding a dynamic Linear); n <= 16384. */
+int lq_gelu_quantize_f32(const float* d_x, int64_t n, int q_dtype, int qmin, int qmax, float eps, float* d_qparams,
+                         void* d_q, void* stream);
 int lq_dynamic_quantize_f32(const float* d_x, int64_t n, int q_dtype, int qmin, int qmax, float eps,
                             float* d_qparams, void* d_q, void* d_workspace, size_t workspace_bytes,
                             void* stream);
@@ -622,15 +634,26 @@ int lq_kv_append_f16(const float* d_qkv, int64_t B, int64_t n, int64_t H, int64_
                      const int32_t* d_pos0, int64_t T_max, void* d_q, void* d_k_cache, void* d_v_cache, void* stream);
 /* Causal attention over the fp16 cache (F.scaled_dot_product_attention, is_causal): query i of
  * q [B, H, n, hd] sits at position pos + i and sees keys 0 .. pos + i; softmax(scale q.k) v
- * with fp32 scores and sums; out [B, n, H, hd] float32.  hd = 64 and pos + n <= 2048
- * (LQ_ERR_UNSUPPORTED otherwise). */
+ * with fp32 scores and sums (fp16 MFMA products for n > 1); out [B, n, H, hd] float32.
+ * hd = 64; a single query (n = 1) sees at most 2048 keys (LQ_ERR_UNSUPPORTED otherwise). */
 int lq_attention_f16(const void* d_q, const void* d_k_cache, const void* d_v_cache, int64_t B, int64_t H, int64_t n,
                      int64_t hd, int64_t pos0, const int32_t* d_pos0, int64_t T_max, float scale, float* d_out,
                      void* stream);
+/* One decode step's lq_kv_append_f16 + lq_attention_f16 (n = 1) in one launch: qkv [B, 1, 3,
+ * H, hd] float32; k / v rounded to fp16 into the caches at the position, q rounded to fp16,
+ * then the attention of that query over keys 0 .. pos; out [B, 1, H, hd] float32.  Same
+ * rounding of q / k / v as the two calls.  hd = 64, at most 2048 keys. */
+int lq_kv_append_attention_f16(const float* d_qkv, int64_t B, int64_t H, int64_t hd, int64_t pos0,
+                               const int32_t* d_pos0, int64_t T_max, void* d_k_cache, void* d_v_cache, float scale,
+                               float* d_out, void* stream);
 /* x[0] += delta (advances a device position counter inside a captured step). */
 int lq_increment_i32(int32_t* d_x, int32_t delta, void* stream);
 /* idx[r] = index of the first maximum of row r (numpy argmax; a NaN counts as the maximum). */
 int lq_argmax_f32(const float* d_x, int64_t rows, int64_t cols, int32_t* d_idx, void* stream);
+/* lq_argmax_f32 and lq_increment_i32(d_pos, delta) in one launch (the end of a decode step:
+ * the greedy token and the position advance; the argmax does not read *d_pos). */
+int lq_argmax_next_f32(const float* d_x, int64_t rows, int64_t cols, int32_t* d_idx, int32_t* d_pos, int32_t delta,
+                       void* stream);
 
 #ifdef __cplusplus
 }

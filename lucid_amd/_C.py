@@ -104,6 +104,8 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_quantize_per_tensor_f32": (_I, [_P, _P, _I64, _I, _P, _P, _F, _F, _I, _I, _P]),
     "lq_dynamic_quantize_workspace_size": (_SZ, [_I64]),
     "lq_dynamic_quantize_f32": (_I, [_P, _I64, _I, _I, _I, _F, _P, _P, _P, _SZ, _P]),
+    "lq_layer_norm_quantize_f32": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P, _F, _I, _I, _I, _F, _P, _P, _P]),
+    "lq_gelu_quantize_f32": (_I, [_P, _I64, _I, _I, _I, _F, _P, _P, _P]),
     "lq_quantize_per_channel_f32": (_I, [_P, _P, _I64, _I64, _I64, _I, _P, _P, _F, _I, _I, _P]),
     "lq_dequantize_per_tensor": (_I, [_P, _I, _P, _I, _I64, _P, _P, _F, _F, _P]),
     "lq_dequantize_per_channel": (_I, [_P, _I, _P, _I, _I64, _I64, _I64, _P, _P, _F, _P]),
@@ -127,6 +129,8 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_attention_f16": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _F, _P, _P]),
     "lq_increment_i32": (_I, [_P, ctypes.c_int32, _P]),
     "lq_argmax_f32": (_I, [_P, _I64, _I64, _P, _P]),
+    "lq_argmax_next_f32": (_I, [_P, _I64, _I64, _P, _P, ctypes.c_int32, _P]),
+    "lq_kv_append_attention_f16": (_I, [_P, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _F, _P, _P]),
     "lq_packed_weights_size": (_SZ, [_I64, _I64]),
     "lq_pack_weights_i8": (_I, [_P, _I64, _I64, _I64, _P, _P]),
     "lq_gemm_w8a8_packed": (_I, [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64,

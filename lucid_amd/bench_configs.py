@@ -172,12 +172,37 @@ class DynLinear:
         return [t for t in (self.qp, self.codes, self.mm_ws, self.g_ws, self.packed, self.bias, w.codes, w.scale,
                             w.sums) if t is not None]
 
+    EPS = float(np.float32(1e-8))
+    LN_FUSED_MAX, GELU_FUSED_MAX = 12288, 16384  # one-workgroup limits of the fused input steps
+
     def __call__(self, x: int, rows: int, y: int, stream) -> None:
         n = rows * self.K
-        q = self.qp.data_ptr()
-        mn, mx, sx, zx = q, q + 4, q + 8, q + 12
-        _C.call("lq_dynamic_quantize_f32", x, n, _C.U8S8, self.qmin, self.qmax, float(np.float32(1e-8)), mn,
+        _C.call("lq_dynamic_quantize_f32", x, n, _C.U8S8, self.qmin, self.qmax, self.EPS, self.qp.data_ptr(),
                 self.codes.data_ptr(), self.mm_ws.data_ptr(), self.mm_bytes, stream)
+        self.gemm(rows, y, stream)
+
+    def quantize_ln(self, x: int, ldx: int, res, ldres: int, rows: int, stream) -> bool:
+        """The input step fused with the LayerNorm before it (x += res first when res is given):
+        lq_layer_norm_quantize_f32, the bits of the norm then the input step.  False (nothing
+        launched) when the rows exceed one workgroup's limit."""
+        if rows * self.K > self.LN_FUSED_MAX:
+            return False
+        _C.call("lq_layer_norm_quantize_f32", x, ldx, res, ldres, rows, self.K, None, None, np.float32(1e-5),
+                _C.U8S8, self.qmin, self.qmax, self.EPS, self.qp.data_ptr(), self.codes.data_ptr(), stream)
+        return True
+
+    def quantize_gelu(self, x: int, rows: int, stream) -> bool:
+        """The input step fused with the GELU before it (lq_gelu_quantize_f32)."""
+        if rows * self.K > self.GELU_FUSED_MAX:
+            return False
+        _C.call("lq_gelu_quantize_f32", x, rows * self.K, _C.U8S8, self.qmin, self.qmax, self.EPS,
+                self.qp.data_ptr(), self.codes.data_ptr(), stream)
+        return True
+
+    def gemm(self, rows: int, y: int, stream) -> None:
+        """The int8 product of the codes the last input step left, float32 out."""
+        q = self.qp.data_ptr()
+        sx, zx = q + 8, q + 12
         common = (sx, 0, self.w.scale.data_ptr(), 1, zx, None, self.w.sums.data_ptr(),
                   self.bias.data_ptr() if self.bias is not None else None, None, None, 0, 0, _C.OUT_F32,
                   _C.EPI_A_U8S8, self.g_ws.data_ptr(), self.g_bytes, stream)
@@ -249,28 +274,47 @@ class Int8Decoder:
                 M, n, 0, p, h, stream)
         proj, eps = self.proj.data_ptr(), np.float32(1e-5)
         for li, ((qkv, out, up, down), (kc, vc)) in enumerate(zip(self.layers, self.cache)):
-            # each residual add that a norm follows runs inside that norm's launch (same bits)
-            if li == 0:
-                _C.call("lq_layer_norm_f32", h, D, hn, D, M, D, None, None, eps, stream)
+            # each residual add that a norm follows runs inside that norm's launch, and at decode
+            # sizes the norm runs inside the next Linear's input step (same bits either way)
+            res = None if li == 0 else proj
+            if not qkv.quantize_ln(h, D, res, D, M, stream):
+                if res is None:
+                    _C.call("lq_layer_norm_f32", h, D, hn, D, M, D, None, None, eps, stream)
+                else:
+                    _C.call("lq_add_layer_norm_f32", h, D, proj, D, hn, D, M, D, None, None, eps, stream)
+                _C.call("lq_dynamic_quantize_f32", hn, M * D, _C.U8S8, qkv.qmin, qkv.qmax, qkv.EPS,
+                        qkv.qp.data_ptr(), qkv.codes.data_ptr(), qkv.mm_ws.data_ptr(), qkv.mm_bytes, stream)
+            qkv.gemm(M, self.qkv.data_ptr(), stream)
+            if n == 1:  # the step's k / v appended and attended in one launch
+                _C.call("lq_kv_append_attention_f16", self.qkv.data_ptr(), B, H, hd, 0, p, self.Tmax, kc.data_ptr(),
+                        vc.data_ptr(), np.float32(self.scale), self.att.data_ptr(), stream)
             else:
-                _C.call("lq_add_layer_norm_f32", h, D, proj, D, hn, D, M, D, None, None, eps, stream)
-            qkv(hn, M, self.qkv.data_ptr(), stream)
-            _C.call("lq_kv_append_f16", self.qkv.data_ptr(), B, n, H, hd, 0, p, self.Tmax, self.q16.data_ptr(),
-                    kc.data_ptr(), vc.data_ptr(), stream)
-            _C.call("lq_attention_f16", self.q16.data_ptr(), kc.data_ptr(), vc.data_ptr(), B, H, n, hd, 0, p,
-                    self.Tmax, np.float32(self.scale), self.att.data_ptr(), stream)
+                _C.call("lq_kv_append_f16", self.qkv.data_ptr(), B, n, H, hd, 0, p, self.Tmax, self.q16.data_ptr(),
+                        kc.data_ptr(), vc.data_ptr(), stream)
+                _C.call("lq_attention_f16", self.q16.data_ptr(), kc.data_ptr(), vc.data_ptr(), B, H, n, hd, 0, p,
+                        self.Tmax, np.float32(self.scale), self.att.data_ptr(), stream)
             out(self.att.data_ptr(), M, proj, stream)
-            _C.call("lq_add_layer_norm_f32", h, D, proj, D, hn, D, M, D, None, None, eps, stream)
-            up(hn, M, self.up.data_ptr(), stream)
-            _C.call("lq_gelu_tanh_f32", self.up.data_ptr(), self.up.data_ptr(), M * FFN, stream)
-            down(self.up.data_ptr(), M, proj, stream)
-        _C.call("lq_add_f32", h, proj, h, M * D, stream)
-        # the last position of each sequence: layer norm over rows n * D apart, then the head
-        _C.call("lq_layer_norm_f32", h + (n - 1) * D * 4, n * D, self.hl.data_ptr(), D, B, D, None, None,
-                np.float32(1e-5), stream)
-        self.head(self.hl.data_ptr(), B, self.logits.data_ptr(), stream)
-        _C.call("lq_argmax_f32", self.logits.data_ptr(), B, self.V, self.next.data_ptr(), stream)
-        _C.call("lq_increment_i32", p, n, stream)
+            if not up.quantize_ln(h, D, proj, D, M, stream):
+                _C.call("lq_add_layer_norm_f32", h, D, proj, D, hn, D, M, D, None, None, eps, stream)
+                up(hn, M, self.up.data_ptr(), stream)
+            else:
+                up.gemm(M, self.up.data_ptr(), stream)
+            if down.quantize_gelu(self.up.data_ptr(), M, stream):
+                down.gemm(M, proj, stream)
+            else:
+                _C.call("lq_gelu_tanh_f32", self.up.data_ptr(), self.up.data_ptr(), M * FFN, stream)
+                down(self.up.data_ptr(), M, proj, stream)
+        # the last position of each sequence: the residual add and layer norm over rows n * D
+        # apart (only those rows of h are read again), then the head
+        hl, pl = h + (n - 1) * D * 4, proj + (n - 1) * D * 4
+        if self.head.quantize_ln(hl, n * D, pl, n * D, B, stream):
+            self.head.gemm(B, self.logits.data_ptr(), stream)
+        else:
+            _C.call("lq_add_layer_norm_f32", hl, n * D, pl, n * D, self.hl.data_ptr(), D, B, D, None, None, eps,
+                    stream)
+            self.head(self.hl.data_ptr(), B, self.logits.data_ptr(), stream)
+        # the greedy token and the position advance in one launch
+        _C.call("lq_argmax_next_f32", self.logits.data_ptr(), B, self.V, self.next.data_ptr(), p, n, stream)
 
     def set_prompt(self, tokens: np.ndarray) -> None:
         """Upload a [batch, T] int prompt (T <= max_prompt) for :meth:`prefill`."""
@@ -332,16 +376,56 @@ def static_resnet18(batch: int = 32, calib_batches: int = 16, seed: int = 5):
     return qnet, x
 
 
+def _decoder_eager(n_decode: int) -> None:
+    """Configuration 4 launched eagerly on a created stream (no graph): two prefills of the
+    8 x 512 prompt, then ``n_decode`` greedy steps, each timed with host clocks around a
+    stream synchronize.  For kernel traces: a profiler then sees plain kernel launches."""
+    import ctypes
+    import time
+
+    import lucid_amd.backends as backends
+    from lucid_amd.quantization import quantize_dynamic
+
+    backends.quantized.engine = "reference"
+    rng = np.random.default_rng(44)
+    dec, glue = decoder(rng)
+    rt = Int8Decoder(quantize_dynamic(dec), glue)
+    rt.set_prompt(rng.integers(0, VOCAB, (BATCH, PREFILL)))
+    st = ctypes.c_void_p()
+    _C.call("lq_stream_create", ctypes.byref(st))
+    try:
+        pre = []
+        for _ in range(2):
+            t0 = time.perf_counter()
+            rt.prefill(st)
+            _C.call("lq_stream_synchronize", st)
+            pre.append((time.perf_counter() - t0) * 1e3)
+        t0 = time.perf_counter()
+        for _ in range(n_decode):
+            rt.decode(st)
+        _C.call("lq_stream_synchronize", st)
+        dt = (time.perf_counter() - t0) * 1e3 / max(n_decode, 1)
+        print(f"decoder eager: prefill {min(pre):.3f} ms, decode {dt:.4f} ms/step over {n_decode} "
+              f"(host launch time included)")
+    finally:
+        _C.call("lq_stream_destroy", st)
+
+
 def _main(argv: list[str]) -> None:
     """``python3 -m lucid_amd.bench_configs resnet18 [forwards]``: time the configuration-5
-    forward (module dispatch included) after three warm-up forwards; a profiler run wraps it."""
+    forward (module dispatch included) after three warm-up forwards;
+    ``python3 -m lucid_amd.bench_configs decoder [steps]``: configuration 4 launched eagerly
+    (two prefills, then greedy steps).  A profiler run wraps either."""
     import time
 
     import lucid_amd as L
     import lucid_amd.backends as backends
 
+    if argv and argv[0] == "decoder":
+        _decoder_eager(int(argv[1]) if len(argv) > 1 else 16)
+        return
     if not argv or argv[0] != "resnet18":
-        raise SystemExit("usage: python3 -m lucid_amd.bench_configs resnet18 [forwards]")
+        raise SystemExit("usage: python3 -m lucid_amd.bench_configs resnet18|decoder [count]")
     n = int(argv[1]) if len(argv) > 1 else 10
     backends.quantized.engine = "reference"  # the per-channel int8 layers
     qnet, x = static_resnet18(calib_batches=4)

@@ -6,12 +6,13 @@
 // their results are compared with float64 restatements within tolerance (their summation
 // order is not knowable from the reference either).
 //
-// Attention.  One workgroup (256 threads) per (batch, head, block of QPB queries): the
-// block's queries go to LDS; every thread scores its keys against all QPB queries (fp16
-// K rows, fp32 dot products) into an LDS score table; each wave turns two rows into
-// softmax weights (max, exp, sum by wave reduction); then each thread accumulates output
-// dims from fp16 V rows read coalesced across the 64 lanes.  Query i (absolute position
-// pos0 + i) sees keys 0 .. pos0 + i.  KV cache layout [B][H][T_max][hd] fp16.
+// Attention.  Several queries (prefill): flash attention on MFMA, one workgroup per (batch,
+// head, 64 queries) streaming 32-key blocks through LDS (attention_mfma_kernel).  One query
+// (decode): one workgroup per (batch, head) over the whole key range, scores and weighted V
+// rows spread over its 256 threads (attention_decode_kernel), optionally taking the step's
+// q / k / v straight from the qkv projection and appending k / v to the caches itself.
+// Query i (absolute position pos0 + i) sees keys 0 .. pos0 + i.  KV cache layout
+// [B][H][T_max][hd] fp16.
 #include <hip/hip_runtime.h>
 #include <hip/hip_fp16.h>
 
@@ -94,11 +95,8 @@ __global__ __launch_bounds__(256) void layer_norm_kernel(float* x, int64_t ldx, 
 
 // gelu, tanh form: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
 __global__ void gelu_tanh_kernel(const float* __restrict__ x, float* __restrict__ y, int64_t n) {
-    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
-        const float v = x[i];
-        const float u = 0.7978845608f * (v + 0.044715f * v * v * v);
-        y[i] = 0.5f * v * (1.0f + tanhf(u));
-    }
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+        y[i] = gelu_tanh_f32(x[i]);
 }
 
 __global__ void add_kernel(const float* __restrict__ a, const float* __restrict__ b, float* __restrict__ y, int64_t n) {
@@ -155,115 +153,323 @@ __global__ void kv_append_kernel(const float* __restrict__ qkv, int64_t B, int64
     }
 }
 
-template <int QPB>
-__global__ __launch_bounds__(ATT_THREADS) void attention_kernel(const __half* __restrict__ q, const __half* __restrict__ kc,
-                                                                const __half* __restrict__ vc, int64_t B, int64_t H,
-                                                                int64_t n, int64_t pos0, const int32_t* __restrict__ d_pos0,
-                                                                int64_t T_max, float scale, float* __restrict__ out) {
-    __shared__ float qs[QPB][ATT_HD];
-    __shared__ float p[QPB][ATT_MAX_T];
-    __shared__ float rinv[QPB];
-    pos0 = position(pos0, d_pos0, min(T_max, (int64_t)ATT_MAX_T) - n);
-    const int b = blockIdx.z, h = blockIdx.y, q0 = blockIdx.x * QPB;
-    const int nq = (int)min((int64_t)QPB, n - q0);
+typedef _Float16 h4v __attribute__((ext_vector_type(4)));
+typedef _Float16 h8v __attribute__((ext_vector_type(8)));
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// Flash attention over blocks of FA_Q queries (4 waves x 16) on CDNA4 MFMA.  Per block of
+// FA_KB keys, staged in LDS (K rows, and V transposed), each wave computes the score tile
+// S^T = K Q^T with v_mfma_f32_16x16x32_f16 -- a lane then holds 4 keys (4g + i) of one query
+// (l16), which is exactly the A-operand layout of P in O += P V with
+// v_mfma_f32_16x16x16_f16, so the weights never leave registers -- and keeps the running
+// max / sum of each query (online softmax, float32); the weights enter the PV product as fp16
+// hi + lo halves (about 22 significant bits).  O's accumulator lane holds queries
+// 4g + i of one dim, so the per-query rescale factors move there by lane shuffles.  Scores,
+// exponentials and the products accumulate in float32 over fp16 q / k / v.  Query i sees keys
+// 0 .. pos0 + i (causal); every query sees key 0, so the running max is finite after the
+// first block.  The next key block is loaded into registers while this one is computed.
+constexpr int FA_Q = 64, FA_KB = 32;
+constexpr int FA_KS = 72;  // K row stride in LDS (halves): 144 B keeps 16-byte rows, staggers banks
+constexpr int FA_VS = 40;  // V^T row stride (halves)
+
+__device__ __forceinline__ f4v mfma_16x16x32(h8v a, h8v b, f4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+__device__ __forceinline__ f4v mfma_16x16x16(h4v a, h4v b, f4v c) {
+    return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
+}
+
+__global__ __launch_bounds__(256) void attention_mfma_kernel(const __half* __restrict__ q, const __half* __restrict__ kc,
+                                                             const __half* __restrict__ vc, int64_t B, int64_t H,
+                                                             int64_t n, int64_t pos0,
+                                                             const int32_t* __restrict__ d_pos0, int64_t T_max,
+                                                             float scale, float* __restrict__ out) {
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[FA_KB * FA_KS];  // [key][dim]
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[ATT_HD * FA_VS];  // [dim][key]
+    pos0 = position(pos0, d_pos0, T_max - n);
+    const int b = blockIdx.z, h = blockIdx.y;
+    const int64_t q0 = (int64_t)blockIdx.x * FA_Q;
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, l16 = lane & 15;
+    const int64_t bh = (int64_t)b * H + h;
+    const int64_t qw = q0 + wave * 16;  // this wave's first query
+    // B operand of S^T: query qw + l16, dims 8g .. 8g + 7 and 32 + 8g .. 32 + 8g + 7
+    const _Float16* qrow = reinterpret_cast<const _Float16*>(q) + (bh * n + min(qw + l16, n - 1)) * ATT_HD;
+    const h8v qf0 = *reinterpret_cast<const h8v*>(qrow + 8 * g);
+    const h8v qf1 = *reinterpret_cast<const h8v*>(qrow + 32 + 8 * g);
+    const int64_t qabs = pos0 + qw + l16;  // position of the query this lane scores
+    const int64_t kend = min(pos0 + q0 + FA_Q, pos0 + n);  // keys some query of the block sees
+    float m_run = -INFINITY, l_run = 0.0f;
+    f4v o[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) o[c] = f4v{0.f, 0.f, 0.f, 0.f};
+
+    // staging: thread -> key kk of the block, dims c8 .. c8 + 7
+    const int kk = tid >> 3, c8 = (tid & 7) * 8;
+    auto fetch = [&](int64_t kb, uint4& kv, uint4& vv) {
+        const int64_t key = kb + kk;
+        kv = uint4{0u, 0u, 0u, 0u};
+        vv = uint4{0u, 0u, 0u, 0u};
+        if (key < kend) {
+            kv = *reinterpret_cast<const uint4*>(kc + (bh * T_max + key) * ATT_HD + c8);
+            vv = *reinterpret_cast<const uint4*>(vc + (bh * T_max + key) * ATT_HD + c8);
+        }
+    };
+    uint4 kv, vv;
+    fetch(0, kv, vv);
+    for (int64_t kb = 0; kb < kend; kb += FA_KB) {
+        *reinterpret_cast<uint4*>(Ks + kk * FA_KS + c8) = kv;
+        const _Float16* vh = reinterpret_cast<const _Float16*>(&vv);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) Vt[(c8 + j) * FA_VS + kk] = vh[j];
+        __syncthreads();
+        if (kb + FA_KB < kend) fetch(kb + FA_KB, kv, vv);  // in flight during this block
+        // S^T tiles: keys kb + 16 t + 4 g + i against query l16
+        f4v sc[2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+            const _Float16* kr = Ks + (16 * t + l16) * FA_KS;
+            f4v acc = f4v{0.f, 0.f, 0.f, 0.f};
+            acc = mfma_16x16x32(*reinterpret_cast<const h8v*>(kr + 8 * g), qf0, acc);
+            acc = mfma_16x16x32(*reinterpret_cast<const h8v*>(kr + 32 + 8 * g), qf1, acc);
+            sc[t] = acc;
+        }
+        float mb = -INFINITY;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int64_t key = kb + 16 * t + 4 * g + i;
+                const float v = (key <= qabs && key < kend) ? sc[t][i] * scale : -INFINITY;
+                sc[t][i] = v;
+                mb = fmaxf(mb, v);
+            }
+        mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
+        mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
+        const float m_new = fmaxf(m_run, mb);
+        const float corr = expf(m_run - m_new);
+        float ps = 0.0f;
+        h4v pa[2], pl[2];  // the weights as fp16 hi + lo: ~22 significant bits into the MFMA
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const float pv = expf(sc[t][i] - m_new);
+                ps += pv;
+                pa[t][i] = (_Float16)pv;
+                pl[t][i] = (_Float16)(pv - (float)pa[t][i]);
+            }
+        ps += __shfl_xor(ps, 16, 64);
+        ps += __shfl_xor(ps, 32, 64);
+        l_run = l_run * corr + ps;
+        m_run = m_new;
+        // O rows are queries 4 g + i: their factors live in lanes 4 g + i
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const float ci = __shfl(corr, 4 * g + i, 64);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) o[c][i] *= ci;
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const h4v vb = *reinterpret_cast<const h4v*>(Vt + (16 * c + l16) * FA_VS + 16 * t + 4 * g);
+                o[c] = mfma_16x16x16(pa[t], vb, o[c]);
+                o[c] = mfma_16x16x16(pl[t], vb, o[c]);
+            }
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+        const float li = __shfl(l_run, 4 * g + i, 64);
+        const int64_t qi = qw + 4 * g + i;
+        if (qi < n) {
+            float* orow = out + (((int64_t)b * n + qi) * H + h) * ATT_HD + l16;
+#pragma unroll
+            for (int c = 0; c < 4; ++c) orow[16 * c] = o[c][i] / li;
+        }
+    }
+}
+
+// One query per (batch, head) -- the decode step -- over up to ATT_MAX_T keys: 256 threads
+// score keys t, t + 256, ... (fp32 dot products of fp16 rows, in dim order), the softmax
+// runs over an LDS table, then thread (key slot ks, dim chunk dc) accumulates
+// p[t] V[t][8 dc .. 8 dc + 7] over keys t = ks, ks + 32, ... (16-byte row loads, several in
+// flight), and the 32 key slots' partial vectors are added in slot order.  FUSED: the step's
+// q, k, v come as float32 from the qkv projection [B][3][H][hd]; k and v are rounded to fp16
+// into the caches at the position first (kv_append_kernel's rounding), q into LDS.
+template <bool FUSED>
+__global__ __launch_bounds__(ATT_THREADS) void attention_decode_kernel(const void* __restrict__ qsrc,
+                                                                       __half* __restrict__ kc,
+                                                                       __half* __restrict__ vc, int64_t B,
+                                                                       int64_t H, int64_t pos0,
+                                                                       const int32_t* __restrict__ d_pos0,
+                                                                       int64_t T_max, float scale,
+                                                                       float* __restrict__ out) {
+    __shared__ float qs[ATT_HD];
+    __shared__ float p[ATT_MAX_T];
+    __shared__ float red[ATT_THREADS / 64];
+    __shared__ float part[32][ATT_HD + 1];
+    pos0 = position(pos0, d_pos0, min(T_max, (int64_t)ATT_MAX_T) - 1);
+    const int b = blockIdx.y, h = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int64_t bh = (int64_t)b * H + h;
-    for (int e = tid; e < QPB * ATT_HD; e += ATT_THREADS) {
-        const int qi = e / ATT_HD, d = e % ATT_HD;
-        qs[qi][d] = qi < nq ? __half2float(q[(bh * n + q0 + qi) * ATT_HD + d]) : 0.0f;
+    if (tid < ATT_HD) {
+        if constexpr (FUSED) {
+            const float* qkv = static_cast<const float*>(qsrc) + (int64_t)b * 3 * H * ATT_HD + (int64_t)h * ATT_HD;
+            const __half qh = f32_to_f16_rn(qkv[tid]);
+            kc[(bh * T_max + pos0) * ATT_HD + tid] = f32_to_f16_rn(qkv[(int64_t)H * ATT_HD + tid]);
+            vc[(bh * T_max + pos0) * ATT_HD + tid] = f32_to_f16_rn(qkv[(int64_t)2 * H * ATT_HD + tid]);
+            qs[tid] = __half2float(qh);
+        } else {
+            qs[tid] = __half2float(static_cast<const __half*>(qsrc)[bh * ATT_HD + tid]);
+        }
     }
     __syncthreads();
-    const int kend = (int)(pos0 + q0 + nq);  // keys 0 .. kend - 1 reach some query of the block
+    const int T = (int)pos0 + 1;
     // scores
-    for (int t = tid; t < kend; t += ATT_THREADS) {
+    for (int t = tid; t < T; t += ATT_THREADS) {
         const __half* kr = kc + (bh * T_max + t) * ATT_HD;
-        float kv[ATT_HD];
+        uint4 w[ATT_HD / 8];
+#pragma unroll
+        for (int c = 0; c < ATT_HD / 8; ++c) w[c] = *reinterpret_cast<const uint4*>(kr + 8 * c);
+        float s = 0.0f;
 #pragma unroll
         for (int c = 0; c < ATT_HD / 8; ++c) {
-            const uint4 w = *reinterpret_cast<const uint4*>(kr + 8 * c);
-            const __half* hw = reinterpret_cast<const __half*>(&w);
+            const __half* hw = reinterpret_cast<const __half*>(&w[c]);
 #pragma unroll
-            for (int j = 0; j < 8; ++j) kv[8 * c + j] = __half2float(hw[j]);
+            for (int j = 0; j < 8; ++j) s += qs[8 * c + j] * __half2float(hw[j]);
         }
-#pragma unroll
-        for (int qi = 0; qi < QPB; ++qi) {
-            float s = 0.0f;
-#pragma unroll
-            for (int d = 0; d < ATT_HD; ++d) s += qs[qi][d] * kv[d];
-            p[qi][t] = (t <= pos0 + q0 + qi) ? s * scale : -INFINITY;
-        }
+        p[t] = s * scale;
     }
     __syncthreads();
-    // softmax weights, rows spread over the waves
-    for (int qi = wave; qi < QPB; qi += ATT_THREADS / 64) {
-        float m = -INFINITY;
-        for (int t = lane; t < kend; t += 64) m = fmaxf(m, p[qi][t]);
-        for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
-        float s = 0.0f;
-        for (int t = lane; t < kend; t += 64) {
-            const float e = expf(p[qi][t] - m);
-            p[qi][t] = e;
-            s += e;
-        }
-        for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-        if (lane == 0) rinv[qi] = 1.0f / s;
-    }
+    // softmax over the T scores
+    float m = -INFINITY;
+    for (int t = tid; t < T; t += ATT_THREADS) m = fmaxf(m, p[t]);
+    for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
+    if (lane == 0) red[wave] = m;
     __syncthreads();
-    // outputs: thread -> (query, dim); lanes run over the 64 dims so V rows load coalesced
-    for (int e = tid; e < QPB * ATT_HD; e += ATT_THREADS) {
-        const int qi = e / ATT_HD, d = e % ATT_HD;
-        if (qi >= nq) continue;
-        const int last = (int)(pos0 + q0 + qi);
-        float acc = 0.0f;
-        const __half* vcol = vc + bh * T_max * ATT_HD + d;
-#pragma unroll 8
-        for (int t = 0; t <= last; ++t) acc += p[qi][t] * __half2float(vcol[(int64_t)t * ATT_HD]);
-        out[(((int64_t)b * n + q0 + qi) * H + h) * ATT_HD + d] = acc * rinv[qi];
+    m = red[0];
+    for (int w = 1; w < ATT_THREADS / 64; ++w) m = fmaxf(m, red[w]);
+    __syncthreads();
+    float sum = 0.0f;
+    for (int t = tid; t < T; t += ATT_THREADS) {
+        const float e = expf(p[t] - m);
+        p[t] = e;
+        sum += e;
+    }
+    for (int off = 32; off > 0; off >>= 1) sum += __shfl_xor(sum, off, 64);
+    if (lane == 0) red[wave] = sum;
+    __syncthreads();
+    sum = 0.0f;
+    for (int w = 0; w < ATT_THREADS / 64; ++w) sum += red[w];
+    const float rinv = 1.0f / sum;
+    // weighted V rows: thread (ks, dc) over keys ks, ks + 32, ...
+    const int ks = tid >> 3, dc = tid & 7;
+    float acc[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
+    const __half* vbase = vc + bh * T_max * ATT_HD + 8 * dc;
+    int t = ks;
+    for (; t + 96 < T; t += 128) {  // four rows in flight
+        uint4 w[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) w[u] = *reinterpret_cast<const uint4*>(vbase + (int64_t)(t + 32 * u) * ATT_HD);
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const float pu = p[t + 32 * u];
+            const __half* hw = reinterpret_cast<const __half*>(&w[u]);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j] += pu * __half2float(hw[j]);
+        }
+    }
+    for (; t < T; t += 32) {
+        const uint4 w = *reinterpret_cast<const uint4*>(vbase + (int64_t)t * ATT_HD);
+        const float pu = p[t];
+        const __half* hw = reinterpret_cast<const __half*>(&w);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] += pu * __half2float(hw[j]);
+    }
+#pragma unroll
+    for (int j = 0; j < 8; ++j) part[ks][8 * dc + j] = acc[j];
+    __syncthreads();
+    if (tid < ATT_HD) {
+        float o = 0.0f;
+        for (int k2 = 0; k2 < 32; ++k2) o += part[k2][tid];
+        out[((int64_t)b * H + h) * ATT_HD + tid] = o * rinv;
     }
 }
 
 // Index of the first maximum of each row (numpy argmax; NaN compares as the maximum, as
-// numpy's does).  One workgroup per row.
-__global__ __launch_bounds__(256) void argmax_kernel(const float* __restrict__ x, int64_t rows, int64_t cols,
-                                                     int32_t* __restrict__ idx) {
+// numpy's does).  One workgroup of 1024 threads per row: each thread scans its float4s
+// (several loads in flight) in index order, then the (value, index) pairs meet by wave
+// shuffles and LDS under one rule -- NaN over numbers, larger value, lower index on ties --
+// so the result does not depend on the combining order.  With `d_pos`, the first workgroup
+// also adds `delta` to *d_pos (the decode step's position advance, which nothing in this
+// kernel reads).
+__device__ __forceinline__ bool argmax_takes(float ov, int oi, float mv, int mi) {
+    if (oi < 0) return false;
+    if (mi < 0) return true;
+    if (mv != mv) return (ov != ov) && oi < mi;
+    if (ov != ov) return true;
+    return ov > mv || (ov == mv && oi < mi);
+}
+
+__global__ __launch_bounds__(1024) void argmax_kernel(const float* __restrict__ x, int64_t rows, int64_t cols,
+                                                      int32_t* __restrict__ idx, int32_t* __restrict__ d_pos,
+                                                      int32_t delta, bool vec) {
     const int64_t r = blockIdx.x;
+    if (d_pos && r == 0 && threadIdx.x == 0) d_pos[0] += delta;
     if (r >= rows) return;
     const float* xr = x + r * cols;
     float bv = -INFINITY;
     int bi = -1;
-    for (int64_t c = threadIdx.x; c < cols; c += blockDim.x) {
-        const float v = xr[c];
-        const bool better = bi < 0 || (v != v && bv == bv) || v > bv;  // first NaN wins, then the max
-        if (better && !(bv != bv)) {
+    auto see = [&](float v, int c) {
+        if (argmax_takes(v, c, bv, bi)) {
             bv = v;
-            bi = (int)c;
+            bi = c;
+        }
+    };
+    const int64_t nv = vec ? cols / 4 : 0;
+    int64_t i = threadIdx.x;
+    for (; i + 3 * 1024 < nv; i += 4 * 1024) {
+        vf4 v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) v[u] = reinterpret_cast<const vf4*>(xr)[i + 1024 * u];
+#pragma unroll
+        for (int u = 0; u < 4; ++u)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) see(v[u][e], (int)(4 * (i + 1024 * u) + e));
+    }
+    for (; i < nv; i += 1024) {
+        const vf4 v = reinterpret_cast<const vf4*>(xr)[i];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) see(v[e], (int)(4 * i + e));
+    }
+    for (int64_t c = 4 * nv + threadIdx.x; c < cols; c += 1024) see(xr[c], (int)c);
+    for (int off = 32; off > 0; off >>= 1) {
+        const float ov = __shfl_xor(bv, off, 64);
+        const int oi = __shfl_xor(bi, off, 64);
+        if (argmax_takes(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
         }
     }
-    __shared__ float sv[256];
-    __shared__ int si[256];
-    sv[threadIdx.x] = bv;
-    si[threadIdx.x] = bi;
+    __shared__ float sv[16];
+    __shared__ int si[16];
+    if ((threadIdx.x & 63) == 0) {
+        sv[threadIdx.x >> 6] = bv;
+        si[threadIdx.x >> 6] = bi;
+    }
     __syncthreads();
-    for (int s = 128; s > 0; s >>= 1) {
-        if ((int)threadIdx.x < s) {
-            const float ov = sv[threadIdx.x + s];
-            const int oi = si[threadIdx.x + s];
-            const float mv = sv[threadIdx.x];
-            const int mi = si[threadIdx.x];
-            bool take;
-            if (oi < 0) take = false;
-            else if (mi < 0) take = true;
-            else if (mv != mv) take = (ov != ov) && oi < mi;
-            else if (ov != ov) take = true;
-            else take = ov > mv || (ov == mv && oi < mi);
-            if (take) {
-                sv[threadIdx.x] = ov;
-                si[threadIdx.x] = oi;
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 16; ++w)
+            if (argmax_takes(sv[w], si[w], bv, bi)) {
+                bv = sv[w];
+                bi = si[w];
             }
-        }
-        __syncthreads();
+        idx[r] = bi < 0 ? 0 : bi;
     }
-    if (threadIdx.x == 0) idx[r] = si[0] < 0 ? 0 : si[0];
 }
 
 __global__ void increment_kernel(int32_t* __restrict__ x, int32_t delta) {
@@ -372,22 +578,38 @@ int lq_attention_f16(const void* d_q, const void* d_k_cache, const void* d_v_cac
     LQ_REQUIRE(B >= 0 && H > 0 && n >= 0 && pos0 >= 0 && n <= T_max && (d_pos0 || pos0 + n <= T_max),
                "lq_attention_f16: bad shape");
     if (hd != ATT_HD) return set_error(LQ_ERR_UNSUPPORTED, "lq_attention_f16: head dim must be 64");
-    if ((d_pos0 ? n : pos0 + n) > ATT_MAX_T)
-        return set_error(LQ_ERR_UNSUPPORTED, "lq_attention_f16: more than 2048 keys");
+    if (n == 1 && (d_pos0 ? min(T_max, (int64_t)ATT_MAX_T + 1) : pos0 + 1) > ATT_MAX_T)
+        return set_error(LQ_ERR_UNSUPPORTED, "lq_attention_f16: a single query over more than 2048 keys");
     if (B == 0 || n == 0) return LQ_OK;
     LQ_REQUIRE(d_q && d_k_cache && d_v_cache && d_out, "lq_attention_f16: NULL pointer");
     LQ_REQUIRE(B <= 65535 && H <= 65535, "lq_attention_f16: grid too large");
     hipStream_t st = as_stream(stream);
     if (n == 1) {
-        hipLaunchKernelGGL((attention_kernel<1>), dim3(1, (unsigned)H, (unsigned)B), dim3(ATT_THREADS), 0, st,
-                           (const __half*)d_q, (const __half*)d_k_cache, (const __half*)d_v_cache, B, H, n, pos0,
-                           d_pos0, T_max, scale, d_out);
+        hipLaunchKernelGGL((attention_decode_kernel<false>), dim3((unsigned)H, (unsigned)B), dim3(ATT_THREADS), 0, st,
+                           d_q, (__half*)d_k_cache, (__half*)d_v_cache, B, H, pos0, d_pos0, T_max, scale, d_out);
     } else {
-        hipLaunchKernelGGL((attention_kernel<8>), dim3((unsigned)((n + 7) / 8), (unsigned)H, (unsigned)B),
-                           dim3(ATT_THREADS), 0, st, (const __half*)d_q, (const __half*)d_k_cache,
-                           (const __half*)d_v_cache, B, H, n, pos0, d_pos0, T_max, scale, d_out);
+        hipLaunchKernelGGL(attention_mfma_kernel, dim3((unsigned)((n + FA_Q - 1) / FA_Q), (unsigned)H, (unsigned)B),
+                           dim3(256), 0, st, (const __half*)d_q, (const __half*)d_k_cache, (const __half*)d_v_cache,
+                           B, H, n, pos0, d_pos0, T_max, scale, d_out);
     }
     return launch_status("lq_attention_f16");
+}
+
+int lq_kv_append_attention_f16(const float* d_qkv, int64_t B, int64_t H, int64_t hd, int64_t pos0,
+                               const int32_t* d_pos0, int64_t T_max, void* d_k_cache, void* d_v_cache, float scale,
+                               float* d_out, void* stream) {
+    LQ_REQUIRE(B >= 0 && H > 0 && pos0 >= 0 && T_max >= 1 && (d_pos0 || pos0 + 1 <= T_max),
+               "lq_kv_append_attention_f16: bad shape");
+    if (hd != ATT_HD) return set_error(LQ_ERR_UNSUPPORTED, "lq_kv_append_attention_f16: head dim must be 64");
+    if ((d_pos0 ? min(T_max, (int64_t)ATT_MAX_T + 1) : pos0 + 1) > ATT_MAX_T)
+        return set_error(LQ_ERR_UNSUPPORTED, "lq_kv_append_attention_f16: more than 2048 keys");
+    if (B == 0) return LQ_OK;
+    LQ_REQUIRE(d_qkv && d_k_cache && d_v_cache && d_out, "lq_kv_append_attention_f16: NULL pointer");
+    LQ_REQUIRE(B <= 65535 && H <= 65535, "lq_kv_append_attention_f16: grid too large");
+    hipLaunchKernelGGL((attention_decode_kernel<true>), dim3((unsigned)H, (unsigned)B), dim3(ATT_THREADS), 0,
+                       as_stream(stream), d_qkv, (__half*)d_k_cache, (__half*)d_v_cache, B, H, pos0, d_pos0, T_max,
+                       scale, d_out);
+    return launch_status("lq_kv_append_attention_f16");
 }
 
 int lq_increment_i32(int32_t* d_x, int32_t delta, void* stream) {
@@ -401,8 +623,20 @@ int lq_argmax_f32(const float* d_x, int64_t rows, int64_t cols, int32_t* d_idx, 
     if (rows == 0) return LQ_OK;
     LQ_REQUIRE(d_x && d_idx, "lq_argmax_f32: NULL pointer");
     LQ_REQUIRE(rows <= 0x7fffffff, "lq_argmax_f32: too many rows");
-    hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), d_x, rows, cols, d_idx);
+    const bool vec = aligned16(d_x) && cols % 4 == 0;
+    hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(1024), 0, as_stream(stream), d_x, rows, cols, d_idx,
+                       nullptr, 0, vec);
     return launch_status("lq_argmax_f32");
+}
+
+int lq_argmax_next_f32(const float* d_x, int64_t rows, int64_t cols, int32_t* d_idx, int32_t* d_pos, int32_t delta,
+                       void* stream) {
+    LQ_REQUIRE(rows >= 1 && cols > 0 && cols <= 0x7fffffff && rows <= 0x7fffffff, "lq_argmax_next_f32: bad shape");
+    LQ_REQUIRE(d_x && d_idx && d_pos, "lq_argmax_next_f32: NULL pointer");
+    const bool vec = aligned16(d_x) && cols % 4 == 0;
+    hipLaunchKernelGGL(argmax_kernel, dim3((unsigned)rows), dim3(1024), 0, as_stream(stream), d_x, rows, cols, d_idx,
+                       d_pos, delta, vec);
+    return launch_status("lq_argmax_next_f32");
 }
 
 }  // extern "C"

@@ -102,6 +102,14 @@ __device__ __forceinline__ float round_result_to(float v, int mode) {
     return round_to(v, mode);
 }
 
+// gelu, tanh form: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) (F.gelu(approximate="tanh")),
+// one float32 rounding per operation in this order; shared so a fused kernel gives the same
+// bits as the standalone one.
+__device__ __forceinline__ float gelu_tanh_f32(float v) {
+    const float u = 0.7978845608f * (v + 0.044715f * v * v * v);
+    return 0.5f * v * (1.0f + tanhf(u));
+}
+
 // clip with NaN pass-through and Lucid's signed-zero tie rule (backend/cpu/Vdsp.cpp:33-62).
 __device__ __forceinline__ float clip_tie(float v, float lo, float hi, bool lo_ties, bool hi_ties) {
     if (lo_ties ? v <= lo : v < lo) return lo;

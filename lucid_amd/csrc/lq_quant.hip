@@ -935,6 +935,131 @@ struct DynQuantSmall {
     }
 };
 
+// The same step with the input produced in the launch: GELU of x (the FFN's down projection
+// reads gelu(up(...))), or the layer norm of `rows` rows of D (optionally after the residual
+// add x += res, written back), as lq_gelu_tanh_f32 / lq_layer_norm_f32 /
+// lq_add_layer_norm_f32 compute them -- gelu_tanh_f32, and each row's mean and variance as
+// layer_norm_kernel sums them (256 threads per row, thread t over elements t, t + 256, ..., a
+// wave tree, the four wave sums in order) -- so the codes and qparams are the bits of that
+// call followed by lq_dynamic_quantize_f32.  The normalized rows wait in LDS.
+enum { DQ_GELU = 1, DQ_LN = 2, DQ_LN_RES = 3 };
+constexpr int64_t DQ_LN_MAX = 12288;  // normalized values held in LDS (48 KB)
+
+template <class Code, int SRC>
+__global__ __launch_bounds__(kDynBlock) void dyn_quant_fused_kernel(float* x, int64_t ldx, const float* res,
+                                                                    int64_t ldres, int rows, int D,
+                                                                    const float* __restrict__ gamma,
+                                                                    const float* __restrict__ beta, float ln_eps,
+                                                                    typename Code::T* __restrict__ q,
+                                                                    float* __restrict__ qp, int qmin, float eps,
+                                                                    float width_f, Grid g) {
+    extern __shared__ float ys[];
+    __shared__ float part[kDynBlock / 256][4];
+    __shared__ int32_t smin[kDynBlock / 64], smax[kDynBlock / 64];
+    __shared__ float s_sz[2];
+    const int tid = threadIdx.x;
+    const int n = SRC == DQ_GELU ? D : rows * D;  // GELU: x is n = D contiguous values
+    if constexpr (SRC != DQ_GELU) {
+        const int slot = tid >> 8, t = tid & 255, w = t >> 6, lane = t & 63;
+        for (int r0 = 0; r0 < rows; r0 += kDynBlock / 256) {
+            const int r = r0 + slot;
+            const bool act = r < rows;
+            float* xr = x + (int64_t)(act ? r : 0) * ldx;
+            if (SRC == DQ_LN_RES && act) {
+                const float* rr = res + (int64_t)r * ldres;
+                for (int d = t; d < D; d += 256) xr[d] = xr[d] + rr[d];
+            }
+            float sm = 0.0f;
+            if (act)
+                for (int d = t; d < D; d += 256) sm += xr[d];
+            for (int off = 32; off > 0; off >>= 1) sm += __shfl_xor(sm, off, 64);
+            if (lane == 0) part[slot][w] = sm;
+            __syncthreads();
+            float tot = 0.0f;
+            for (int ww = 0; ww < 4; ++ww) tot += part[slot][ww];
+            __syncthreads();
+            const float mean = tot / (float)D;
+            float qv = 0.0f;
+            if (act)
+                for (int d = t; d < D; d += 256) {
+                    const float c = xr[d] - mean;
+                    qv += c * c;
+                }
+            for (int off = 32; off > 0; off >>= 1) qv += __shfl_xor(qv, off, 64);
+            if (lane == 0) part[slot][w] = qv;
+            __syncthreads();
+            tot = 0.0f;
+            for (int ww = 0; ww < 4; ++ww) tot += part[slot][ww];
+            __syncthreads();
+            const float var = tot / (float)D;
+            const float inv = 1.0f / sqrtf(var + ln_eps);
+            if (act)
+                for (int d = t; d < D; d += 256) {
+                    float v = (xr[d] - mean) * inv;
+                    if (gamma) v = v * gamma[d];
+                    if (beta) v = v + beta[d];
+                    ys[r * D + d] = v;
+                }
+        }
+        __syncthreads();
+    }
+    auto val = [&](int i) -> float {
+        if constexpr (SRC == DQ_GELU) return gelu_tanh_f32(x[i]);
+        else return ys[i];
+    };
+    int32_t kmin = KEY_POS_INF, kmax = KEY_NEG_INF;
+    for (int i = tid; i < n; i += kDynBlock) key_accum(kmin, kmax, val(i));
+    kmin = wave_min(kmin);
+    kmax = wave_max(kmax);
+    if ((tid & 63) == 0) {
+        smin[tid >> 6] = kmin;
+        smax[tid >> 6] = kmax;
+    }
+    __syncthreads();
+    if (tid == 0) {
+        for (int w = 1; w < kDynBlock / 64; ++w) {
+            kmin = min(kmin, smin[w]);
+            kmax = max(kmax, smax[w]);
+        }
+        float cmin, cmax;
+        decode_keys(kmin, kmax, cmin, cmax);
+        qp[0] = cmin;
+        qp[1] = cmax;
+        const float mn = extreme_min(cmin, 0.0f), mx = extreme_max(cmax, 0.0f);
+        const float wd = mx - mn;
+        const float qq = wd / width_f;
+        const float sc = extreme_max(qq, eps);
+        const float r = rne(mn / sc);
+        const float z = clip_grid((float)qmin - r, g);
+        qp[2] = sc;
+        qp[3] = z;
+        s_sz[0] = sc;
+        s_sz[1] = z;
+    }
+    __syncthreads();
+    const float sc = s_sz[0], z = s_sz[1];
+    const float inv = 1.0f / sc;
+    for (int i = tid; i < n; i += kDynBlock) q[i] = Code::store(quant_one<Code>(val(i), inv, z, g));
+}
+
+template <class Code>
+struct DynQuantFused {
+    static int run(int src, float* x, int64_t ldx, const float* res, int64_t ldres, int rows, int D,
+                   const float* gamma, const float* beta, float ln_eps, void* q, float* qp, int qmin, float eps,
+                   float width_f, Grid g, hipStream_t st) {
+        typedef typename Code::T T;
+        const size_t lds = src == DQ_GELU ? 0 : sizeof(float) * (size_t)rows * D;
+#define LQ_DQF(S) \
+    hipLaunchKernelGGL((dyn_quant_fused_kernel<Code, S>), dim3(1), dim3(kDynBlock), lds, st, x, ldx, res, ldres, rows, D, \
+                       gamma, beta, ln_eps, (T*)q, qp, qmin, eps, width_f, g)
+        if (src == DQ_GELU) LQ_DQF(DQ_GELU);
+        else if (src == DQ_LN) LQ_DQF(DQ_LN);
+        else LQ_DQF(DQ_LN_RES);
+#undef LQ_DQF
+        return launch_status(src == DQ_GELU ? "lq_gelu_quantize_f32" : "lq_layer_norm_quantize_f32");
+    }
+};
+
 template <class Code>
 struct QuantPt {
     static int run(const float* x, void* q, int64_t n, PtParams pp, Grid g, hipStream_t st) {
@@ -1181,6 +1306,33 @@ int lq_dynamic_quantize_f32(const float* d_x, int64_t n, int q_dtype, int qmin, 
     if (rc) return rc;
     return lq_quantize_per_tensor_f32(d_x, d_q, n, q_dtype, d_qparams + 2, d_qparams + 3, 0.0f, 0.0f, qmin, qmax,
                                       stream);
+}
+
+int lq_layer_norm_quantize_f32(float* d_x, int64_t ldx, const float* d_res, int64_t ldres, int64_t rows, int64_t D,
+                               const float* d_gamma, const float* d_beta, float ln_eps, int q_dtype, int qmin,
+                               int qmax, float eps, float* d_qparams, void* d_q, void* stream) {
+    LQ_REQUIRE(rows > 0 && D > 0 && ldx >= D && (!d_res || ldres >= D), "lq_layer_norm_quantize_f32: bad shape");
+    LQ_REQUIRE(d_x && d_qparams && d_q, "lq_layer_norm_quantize_f32: NULL pointer");
+    LQ_REQUIRE(valid_code(q_dtype), "lq_layer_norm_quantize_f32: bad code dtype");
+    LQ_REQUIRE(qmax > qmin, "lq_layer_norm_quantize_f32: qmax <= qmin");
+    if (rows * D > DQ_LN_MAX)
+        return set_error(LQ_ERR_UNSUPPORTED, "lq_layer_norm_quantize_f32: more than 12288 values (one workgroup)");
+    return dispatch_code<DynQuantFused>(q_dtype, d_res ? (int)DQ_LN_RES : (int)DQ_LN, d_x, ldx, d_res, ldres,
+                                        (int)rows, (int)D, d_gamma, d_beta, ln_eps, d_q, d_qparams, qmin, eps,
+                                        (float)(qmax - qmin), make_grid(qmin, qmax), as_stream(stream));
+}
+
+int lq_gelu_quantize_f32(const float* d_x, int64_t n, int q_dtype, int qmin, int qmax, float eps, float* d_qparams,
+                         void* d_q, void* stream) {
+    LQ_REQUIRE(n > 0, "lq_gelu_quantize_f32: n <= 0");
+    LQ_REQUIRE(d_x && d_qparams && d_q, "lq_gelu_quantize_f32: NULL pointer");
+    LQ_REQUIRE(valid_code(q_dtype), "lq_gelu_quantize_f32: bad code dtype");
+    LQ_REQUIRE(qmax > qmin, "lq_gelu_quantize_f32: qmax <= qmin");
+    if (n > DYN_SMALL_MAX)
+        return set_error(LQ_ERR_UNSUPPORTED, "lq_gelu_quantize_f32: more than 16384 values (one workgroup)");
+    return dispatch_code<DynQuantFused>(q_dtype, (int)DQ_GELU, const_cast<float*>(d_x), (int64_t)n, nullptr,
+                                        (int64_t)0, 1, (int)n, nullptr, nullptr, 0.0f, d_q, d_qparams, qmin, eps,
+                                        (float)(qmax - qmin), make_grid(qmin, qmax), as_stream(stream));
 }
 
 int lq_quantize_per_channel_f32(const float* d_x, void* d_q, int64_t outer, int64_t C,

@@ -140,7 +140,9 @@ def _attention_case(gpu, B, H, n, pos0, T_max, device_pos):
 
 
 @pytest.mark.parametrize("B,H,n,pos0,T_max", [(2, 3, 40, 0, 64), (8, 8, 512, 0, 640), (8, 8, 1, 511, 640),
-                                              (8, 8, 1, 639, 640), (1, 2, 9, 100, 2048), (2, 1, 1, 0, 16)])
+                                              (8, 8, 1, 639, 640), (1, 2, 9, 100, 2048), (2, 1, 1, 0, 16),
+                                              (2, 3, 70, 5, 80), (1, 1, 130, 3000, 3200), (3, 2, 64, 0, 64),
+                                              (1, 1, 1, 2047, 2048)])
 def test_kv_append_and_attention(gpu, B, H, n, pos0, T_max):
     print(f"attention B={B} H={H} n={n} pos0={pos0}", flush=True)
     _attention_case(gpu, B, H, n, pos0, T_max, device_pos=False)
@@ -154,6 +156,8 @@ def test_attention_rejects_unsupported(gpu):
         _C.call("lq_attention_f16", 1, 1, 1, 1, 1, 1, 32, 0, None, 4, np.float32(1.0), 1, None)
     with pytest.raises(_C.LucidError, match="2048"):
         _C.call("lq_attention_f16", 1, 1, 1, 1, 1, 1, 64, 2048, None, 4096, np.float32(1.0), 1, None)
+    with pytest.raises(_C.LucidError, match="2048"):
+        _C.call("lq_kv_append_attention_f16", 1, 1, 1, 64, 2048, None, 4096, 1, 1, np.float32(1.0), 1, None)
 
 
 def test_argmax(gpu):
@@ -170,3 +174,114 @@ def test_argmax(gpu):
     dx = _d(gpu, x)
     _C.call("lq_argmax_f32", dx.data_ptr(), 9, 32000, idx.data_ptr(), None)
     np.testing.assert_array_equal(idx.numpy(), np.argmax(x, axis=1))
+    # the same with the position advance fused in; ragged widths take the scalar loads
+    pos = _d(gpu, np.array([7], np.int32))
+    _C.call("lq_argmax_next_f32", dx.data_ptr(), 9, 32000, idx.data_ptr(), pos.data_ptr(), 3, None)
+    np.testing.assert_array_equal(idx.numpy(), np.argmax(x, axis=1))
+    assert pos.numpy()[0] == 10
+    for cols in (1, 5, 1023, 4097, 33333):
+        y = rng.standard_normal((3, cols)).astype(np.float32)
+        y[0, cols // 2] = np.nan
+        y[1, -1] = y[1].max() + 1.0
+        y[2, :] = 0.5  # all tied: index 0
+        dy = _d(gpu, y)
+        _C.call("lq_argmax_f32", dy.data_ptr(), 3, cols, idx.data_ptr(), None)
+        np.testing.assert_array_equal(idx.numpy()[:3], np.argmax(y, axis=1), err_msg=f"cols={cols}")
+
+
+def test_kv_append_attention_fused_equals_two_calls(gpu):
+    """The decode step's fused append + attention: the caches and the output bit for bit those
+    of lq_kv_append_f16 followed by lq_attention_f16 (n = 1), with the position by value and
+    from the device counter."""
+    from lucid_amd import _C
+
+    B, H, hd, T_max = 8, 8, 64, 640
+    rng = np.random.default_rng(31)
+    for pos0, device_pos in ((0, False), (511, True), (639, False)):
+        qkv = rng.standard_normal((B, 1, 3, H, hd)).astype(np.float32)
+        kc = rng.standard_normal((B, H, T_max, hd)).astype(np.float16)
+        vc = rng.standard_normal((B, H, T_max, hd)).astype(np.float16)
+        dqkv = _d(gpu, qkv)
+        k1, v1, k2, v2 = _d(gpu, kc), _d(gpu, vc), _d(gpu, kc), _d(gpu, vc)
+        dpos = _d(gpu, np.array([pos0], np.int32))
+        p0, pp = (0, dpos.data_ptr()) if device_pos else (pos0, None)
+        dq = gpu.empty((B, H, 1, hd), np.float16, "gpu")
+        o1, o2 = gpu.empty((B, 1, H, hd), np.float32, "gpu"), gpu.empty((B, 1, H, hd), np.float32, "gpu")
+        scale = np.float32(0.125)
+        _C.call("lq_kv_append_f16", dqkv.data_ptr(), B, 1, H, hd, p0, pp, T_max, dq.data_ptr(), k1.data_ptr(),
+                v1.data_ptr(), None)
+        _C.call("lq_attention_f16", dq.data_ptr(), k1.data_ptr(), v1.data_ptr(), B, H, 1, hd, p0, pp, T_max, scale,
+                o1.data_ptr(), None)
+        _C.call("lq_kv_append_attention_f16", dqkv.data_ptr(), B, H, hd, p0, pp, T_max, k2.data_ptr(), v2.data_ptr(),
+                scale, o2.data_ptr(), None)
+        np.testing.assert_array_equal(k1.numpy().view(np.uint16), k2.numpy().view(np.uint16))
+        np.testing.assert_array_equal(v1.numpy().view(np.uint16), v2.numpy().view(np.uint16))
+        np.testing.assert_array_equal(o1.numpy().view(np.uint32), o2.numpy().view(np.uint32))
+
+
+@pytest.mark.parametrize("rows,D,with_res", [(8, 512, False), (8, 512, True), (3, 700, True), (24, 512, True),
+                                             (1, 12288, False)])
+def test_layer_norm_quantize_equals_two_calls(gpu, rows, D, with_res):
+    """lq_layer_norm_quantize_f32: x (after x += res), the codes and the qparams bit for bit
+    those of lq_(add_)layer_norm_f32 followed by lq_dynamic_quantize_f32 on the unsigned grid
+    stored as c - 128 (the dynamic Linear's input)."""
+    from lucid_amd import _C
+
+    rng = np.random.default_rng(rows * 7 + D)
+    x = (rng.standard_normal((rows, D)) * 3 + 1).astype(np.float32)
+    r = rng.standard_normal((rows, D)).astype(np.float32)
+    x1, x2, dr = _d(gpu, x), _d(gpu, x), _d(gpu, r)
+    y = gpu.empty((rows, D), np.float32, "gpu")
+    q1, q2 = gpu.empty((rows * D,), np.int8, "gpu"), gpu.empty((rows * D,), np.int8, "gpu")
+    qp1, qp2 = gpu.empty((4,), np.float32, "gpu"), gpu.empty((4,), np.float32, "gpu")
+    eps_ln, eps = np.float32(1e-5), np.float32(1e-8)
+    ws_n = _C.lib().lq_dynamic_quantize_workspace_size(rows * D)
+    ws = gpu.empty((max(ws_n, 16),), np.uint8, "gpu")
+    if with_res:
+        _C.call("lq_add_layer_norm_f32", x1.data_ptr(), D, dr.data_ptr(), D, y.data_ptr(), D, rows, D, None, None,
+                eps_ln, None)
+    else:
+        _C.call("lq_layer_norm_f32", x1.data_ptr(), D, y.data_ptr(), D, rows, D, None, None, eps_ln, None)
+    _C.call("lq_dynamic_quantize_f32", y.data_ptr(), rows * D, _C.U8S8, 0, 255, eps, qp1.data_ptr(), q1.data_ptr(),
+            ws.data_ptr(), ws_n, None)
+    _C.call("lq_layer_norm_quantize_f32", x2.data_ptr(), D, dr.data_ptr() if with_res else None, D, rows, D, None,
+            None, eps_ln, _C.U8S8, 0, 255, eps, qp2.data_ptr(), q2.data_ptr(), None)
+    np.testing.assert_array_equal(x1.numpy().view(np.uint32), x2.numpy().view(np.uint32))
+    np.testing.assert_array_equal(q1.numpy(), q2.numpy())
+    np.testing.assert_array_equal(qp1.numpy().view(np.uint32), qp2.numpy().view(np.uint32))
+    # and the norm itself against float64 (the codes' source)
+    xr = x + r if with_res else x
+    sc, zp = qp2.numpy()[2], qp2.numpy()[3]
+    codes = q2.numpy().astype(np.int64) + 128
+    deq = (codes - zp) * sc
+    assert np.max(np.abs(deq - O.layer_norm(xr).ravel())) <= sc * 0.5 + 1e-4
+
+
+def test_layer_norm_quantize_rejects_large(gpu):
+    from lucid_amd import _C
+
+    with pytest.raises(_C.LucidError, match="12288"):
+        _C.call("lq_layer_norm_quantize_f32", 1, 512, None, 512, 25, 512, None, None, np.float32(1e-5), _C.U8S8, 0,
+                255, np.float32(1e-8), 1, 1, None)
+    with pytest.raises(_C.LucidError, match="16384"):
+        _C.call("lq_gelu_quantize_f32", 1, 16385, _C.U8S8, 0, 255, np.float32(1e-8), 1, 1, None)
+
+
+@pytest.mark.parametrize("n", [16384, 4096, 333])
+def test_gelu_quantize_equals_two_calls(gpu, n):
+    from lucid_amd import _C
+
+    rng = np.random.default_rng(n)
+    x = (rng.standard_normal(n) * 2).astype(np.float32)
+    dx = _d(gpu, x)
+    y = gpu.empty((n,), np.float32, "gpu")
+    q1, q2 = gpu.empty((n,), np.int8, "gpu"), gpu.empty((n,), np.int8, "gpu")
+    qp1, qp2 = gpu.empty((4,), np.float32, "gpu"), gpu.empty((4,), np.float32, "gpu")
+    eps = np.float32(1e-8)
+    ws = gpu.empty((16,), np.uint8, "gpu")
+    _C.call("lq_gelu_tanh_f32", dx.data_ptr(), y.data_ptr(), n, None)
+    _C.call("lq_dynamic_quantize_f32", y.data_ptr(), n, _C.U8S8, 0, 255, eps, qp1.data_ptr(), q1.data_ptr(),
+            ws.data_ptr(), 16, None)
+    _C.call("lq_gelu_quantize_f32", dx.data_ptr(), n, _C.U8S8, 0, 255, eps, qp2.data_ptr(), q2.data_ptr(), None)
+    np.testing.assert_array_equal(q1.numpy(), q2.numpy())
+    np.testing.assert_array_equal(qp1.numpy().view(np.uint32), qp2.numpy().view(np.uint32))
