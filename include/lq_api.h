@@ -201,10 +201,6 @@ size_t lq_dynamic_quantize_workspace_size(int64_t n);
 int lq_layer_norm_quantize_f32(float* d_x, int64_t ldx, const float* d_res, int64_t ldres, int64_t rows, int64_t D,
                                const float* d_gamma, const float* d_beta, float ln_eps, int q_dtype, int qmin,
                                int qmax, float eps, float* d_qparams, void* d_q, void* stream);
-/* lq_gelu_tanh_f32 then lq_dynamic_quantize_f32 of the result, in one launch with the same
- * bits (F.gelu(approximate="tanh") feeding a dynamic Linear); n <= 16384. */
-int lq_gelu_quantize_f32(const float* d_x, int64_t n, int q_dtype, int qmin, int qmax, float eps, float* d_qparams,
-                         void* d_q, void* stream);
 int lq_dynamic_quantize_f32(const float* d_x, int64_t n, int q_dtype, int qmin, int qmax, float eps,
                             float* d_qparams, void* d_q, void* d_workspace, size_t workspace_bytes,
                             void* stream);
@@ -268,7 +264,9 @@ enum {
 /* Flag bits of lq_gemm_w8a8.  LQ_EPI_A_U8S8: A holds unsigned-grid codes c stored as int8
  * (c - 128, the LQ_U8S8 form); d_a_zero_point (NULL = 0) is the grid's own zero point and
  * the kernel applies the 128 shift. */
-enum { LQ_EPI_RELU = 1, LQ_EPI_A_U8S8 = 2, LQ_EPI_ROUND_BF16 = 4 /* lq_group_matmul only */ };
+enum { LQ_EPI_RELU = 1, LQ_EPI_A_U8S8 = 2, LQ_EPI_ROUND_BF16 = 4 /* lq_group_matmul only */,
+       LQ_EPI_GELU = 8 /* lq_gemm_w8a8(_packed), LQ_OUT_F32 only: y = gelu_tanh(y) after the bias,
+                          the bits of lq_gelu_tanh_f32 on the output (F.gelu after the Linear) */ };
 
 /* C[m,n] epilogue of acc[m,n] = sum_k (A[m,k] - za) * (B[n,k] - zb[n])  (exact int32),
  * A int8 [M,K] row-major (lda), B int8 [N,K] row-major (ldb; Lucid's weight_int8 [out,in]).

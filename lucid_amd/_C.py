@@ -24,7 +24,7 @@ I8_QPAIR = 9  # table lookups: int8 rows + interleaved {scale, zero point} pairs
 BF16 = 10
 OBS_MINMAX, OBS_EMA, OBS_REPLACE = 0, 1, 2
 OUT_I32, OUT_F32, OUT_F16, OUT_Q8, OUT_QU8, OUT_FQ32, OUT_Q16, OUT_QU8S8 = 0, 1, 2, 3, 4, 5, 6, 7
-EPI_RELU, EPI_A_U8S8, EPI_ROUND_BF16 = 1, 2, 4
+EPI_RELU, EPI_A_U8S8, EPI_ROUND_BF16, EPI_GELU = 1, 2, 4, 8
 PAD_ZEROS, PAD_REFLECT, PAD_REPLICATE, PAD_CIRCULAR = 0, 1, 2, 3
 MERGE_ADD, MERGE_MUL, MERGE_ADD_SCALAR, MERGE_MUL_SCALAR, MERGE_COPY = 0, 1, 2, 3, 4
 ACT_SIGMOID, ACT_TANH, ACT_HARDSWISH, ACT_HARDSIGMOID, ACT_ELU, ACT_LEAKY_RELU = 0, 1, 2, 3, 4, 5
@@ -105,7 +105,6 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_dynamic_quantize_workspace_size": (_SZ, [_I64]),
     "lq_dynamic_quantize_f32": (_I, [_P, _I64, _I, _I, _I, _F, _P, _P, _P, _SZ, _P]),
     "lq_layer_norm_quantize_f32": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P, _F, _I, _I, _I, _F, _P, _P, _P]),
-    "lq_gelu_quantize_f32": (_I, [_P, _I64, _I, _I, _I, _F, _P, _P, _P]),
     "lq_quantize_per_channel_f32": (_I, [_P, _P, _I64, _I64, _I64, _I, _P, _P, _F, _I, _I, _P]),
     "lq_dequantize_per_tensor": (_I, [_P, _I, _P, _I, _I64, _P, _P, _F, _F, _P]),
     "lq_dequantize_per_channel": (_I, [_P, _I, _P, _I, _I64, _I64, _I64, _P, _P, _F, _P]),

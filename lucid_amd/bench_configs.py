@@ -173,7 +173,7 @@ class DynLinear:
                             w.sums) if t is not None]
 
     EPS = float(np.float32(1e-8))
-    LN_FUSED_MAX, GELU_FUSED_MAX = 12288, 16384  # one-workgroup limits of the fused input steps
+    LN_FUSED_MAX = 12288  # one-workgroup limit of the fused layer norm + input step
 
     def __call__(self, x: int, rows: int, y: int, stream) -> None:
         n = rows * self.K
@@ -191,21 +191,15 @@ class DynLinear:
                 _C.U8S8, self.qmin, self.qmax, self.EPS, self.qp.data_ptr(), self.codes.data_ptr(), stream)
         return True
 
-    def quantize_gelu(self, x: int, rows: int, stream) -> bool:
-        """The input step fused with the GELU before it (lq_gelu_quantize_f32)."""
-        if rows * self.K > self.GELU_FUSED_MAX:
-            return False
-        _C.call("lq_gelu_quantize_f32", x, rows * self.K, _C.U8S8, self.qmin, self.qmax, self.EPS,
-                self.qp.data_ptr(), self.codes.data_ptr(), stream)
-        return True
-
-    def gemm(self, rows: int, y: int, stream) -> None:
-        """The int8 product of the codes the last input step left, float32 out."""
+    def gemm(self, rows: int, y: int, stream, gelu: bool = False) -> None:
+        """The int8 product of the codes the last input step left, float32 out (with the tanh
+        GELU of the following float module in its epilogue when ``gelu``)."""
         q = self.qp.data_ptr()
         sx, zx = q + 8, q + 12
+        flags = _C.EPI_A_U8S8 | (_C.EPI_GELU if gelu else 0)
         common = (sx, 0, self.w.scale.data_ptr(), 1, zx, None, self.w.sums.data_ptr(),
                   self.bias.data_ptr() if self.bias is not None else None, None, None, 0, 0, _C.OUT_F32,
-                  _C.EPI_A_U8S8, self.g_ws.data_ptr(), self.g_bytes, stream)
+                  flags, self.g_ws.data_ptr(), self.g_bytes, stream)
         if rows <= 128 and self.packed is not None:
             _C.call("lq_gemm_w8a8_packed", self.codes.data_ptr(), self.K, self.packed.data_ptr(), y, self.N, rows,
                     self.N, self.K, *common)
@@ -296,14 +290,10 @@ class Int8Decoder:
             out(self.att.data_ptr(), M, proj, stream)
             if not up.quantize_ln(h, D, proj, D, M, stream):
                 _C.call("lq_add_layer_norm_f32", h, D, proj, D, hn, D, M, D, None, None, eps, stream)
-                up(hn, M, self.up.data_ptr(), stream)
-            else:
-                up.gemm(M, self.up.data_ptr(), stream)
-            if down.quantize_gelu(self.up.data_ptr(), M, stream):
-                down.gemm(M, proj, stream)
-            else:
-                _C.call("lq_gelu_tanh_f32", self.up.data_ptr(), self.up.data_ptr(), M * FFN, stream)
-                down(self.up.data_ptr(), M, proj, stream)
+                _C.call("lq_dynamic_quantize_f32", hn, M * D, _C.U8S8, up.qmin, up.qmax, up.EPS, up.qp.data_ptr(),
+                        up.codes.data_ptr(), up.mm_ws.data_ptr(), up.mm_bytes, stream)
+            up.gemm(M, self.up.data_ptr(), stream, gelu=True)  # the GELU in the product's epilogue
+            down(self.up.data_ptr(), M, proj, stream)
         # the last position of each sequence: the residual add and layer norm over rows n * D
         # apart (only those rows of h are read again), then the head
         hl, pl = h + (n - 1) * D * 4, proj + (n - 1) * D * 4

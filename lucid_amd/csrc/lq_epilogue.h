@@ -31,15 +31,17 @@ __device__ __forceinline__ float requant_code(float y, const EpiParams& p) {
 }
 
 // Epilogue value of one element, as the bits of the output element type.
+// gelu (float32 output only): the tanh GELU of y after the bias, the float module that follows
+// the Linear (gelu_tanh_f32, the bits of the standalone kernel).
 template <int KIND>
 __device__ __forceinline__ uint32_t epi_one(int32_t acc, float sa, float sb, const float* bias_p,
-                                            bool relu, const EpiParams& p) {
+                                            bool relu, const EpiParams& p, bool gelu = false) {
     if (KIND == LQ_OUT_I32) return (uint32_t)acc;
     float s = sa * sb;
     float y = (float)acc * s;
     if (bias_p) y = y + *bias_p;  // no add without a bias: -0 stays -0
     if (relu) y = (y <= 0.0f) ? 0.0f : y;
-    if (KIND == LQ_OUT_F32) return __float_as_uint(y);
+    if (KIND == LQ_OUT_F32) return __float_as_uint(gelu ? gelu_tanh_f32(y) : y);
     if (KIND == LQ_OUT_F16) return (uint32_t)__half_as_ushort(f32_to_f16_rn(y));
     float c = requant_code(y, p);
     if (KIND == LQ_OUT_Q8) return (uint32_t)(uint8_t)CodeI8::store(c);

@@ -53,6 +53,7 @@ struct GemmArgs {
     int qmin, qmax;
     int out_kind;
     int relu;
+    int gelu;                // float32 out: tanh GELU after the bias (LQ_EPI_GELU)
     int a_u8s8;              // A holds unsigned codes c as int8 (c - 128): the zero point shifts by 128
     int32_t* partial;        // split-K: [M,N] int32 accumulation buffer (zeroed)
     uint32_t* counters;      // split-K: one arrival counter per output tile (zeroed)
@@ -147,7 +148,8 @@ __device__ __forceinline__ void epilogue4c(const GemmArgs& a, const EpiParams& p
             acc -= (uint32_t)c.zb[r] * (uint32_t)row.asum;
             acc += (uint32_t)a.K * (uint32_t)p.za * (uint32_t)c.zb[r];
         }
-        out[r] = epi_one<KIND>((int32_t)acc, row.sa, c.sb[r], a.bias ? &c.bias[r] : nullptr, a.relu != 0, p);
+        out[r] = epi_one<KIND>((int32_t)acc, row.sa, c.sb[r], a.bias ? &c.bias[r] : nullptr, a.relu != 0, p,
+                               a.gelu != 0);
     }
     const int64_t base = (int64_t)m * a.ldc + c.n;
     constexpr int b = OutTraits<KIND>::bytes;
@@ -822,7 +824,8 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N >= 8 ? 2 : 1))) void gemm_i
                         out[q] = (uint32_t)requant_int<KIND>(y, p, cc);
                         if (KIND == LQ_OUT_QU8S8) out[q] ^= 0x80u;
                     } else {
-                        out[q] = epi_one<KIND>((int32_t)accu, rsa[j], csb[q], BIAS ? &cbias[q] : nullptr, RELU, p);
+                        out[q] = epi_one<KIND>((int32_t)accu, rsa[j], csb[q], BIAS ? &cbias[q] : nullptr, RELU, p,
+                                               a.gelu != 0);
                     }
                 }
                 store_row(j, out);
@@ -1185,7 +1188,7 @@ __global__ __launch_bounds__(256) void gemm_i8_generic_kernel(GemmArgs a) {
     const float sa = a.a_scale ? a.a_scale[(int64_t)m * a.a_stride] : 1.0f;
     const float sb = a.b_scale ? a.b_scale[(int64_t)n * a.b_stride] : 1.0f;
     store_elem<KIND>(a.C, (int64_t)m * a.ldc + n,
-                     epi_one<KIND>(acc, sa, sb, a.bias ? a.bias + n : nullptr, a.relu != 0, p));
+                     epi_one<KIND>(acc, sa, sb, a.bias ? a.bias + n : nullptr, a.relu != 0, p, a.gelu != 0));
 }
 
 // ------------------------------------------------------------------ row sums
@@ -1381,7 +1384,9 @@ static int gemm_entry(bool packed, const int8_t* d_A, int64_t lda, const int8_t*
                          out_kind == LQ_OUT_QU8S8 || out_kind == LQ_OUT_FQ32;
     LQ_REQUIRE(!requant || d_out_scale, "lq_gemm_w8a8: requantizing output needs d_out_scale");
     LQ_REQUIRE(!requant || out_qmax >= out_qmin, "lq_gemm_w8a8: out_qmax < out_qmin");
-    LQ_REQUIRE((flags & ~(LQ_EPI_RELU | LQ_EPI_A_U8S8)) == 0, "lq_gemm_w8a8: unknown flags");
+    LQ_REQUIRE((flags & ~(LQ_EPI_RELU | LQ_EPI_A_U8S8 | LQ_EPI_GELU)) == 0, "lq_gemm_w8a8: unknown flags");
+    LQ_REQUIRE(!(flags & LQ_EPI_GELU) || (out_kind == LQ_OUT_F32 && !(flags & LQ_EPI_RELU)),
+               "lq_gemm_w8a8: LQ_EPI_GELU needs float32 output and no ReLU");
     const bool has_za = d_a_zero_point != nullptr || (flags & LQ_EPI_A_U8S8);
     if (packed) {
         if (M > 128) return set_error(LQ_ERR_UNSUPPORTED, "lq_gemm_w8a8_packed: M > 128 (use lq_gemm_w8a8)");
@@ -1422,6 +1427,7 @@ static int gemm_entry(bool packed, const int8_t* d_A, int64_t lda, const int8_t*
     a.qmax = out_qmax;
     a.out_kind = out_kind;
     a.relu = (flags & LQ_EPI_RELU) ? 1 : 0;
+    a.gelu = (flags & LQ_EPI_GELU) ? 1 : 0;
     a.a_u8s8 = (flags & LQ_EPI_A_U8S8) ? 1 : 0;
     a.splits = 1;
     char* wsb = (char*)d_workspace;

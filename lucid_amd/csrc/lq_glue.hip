@@ -21,7 +21,6 @@
 namespace lq {
 namespace {
 
-constexpr int ATT_THREADS = 256;
 constexpr int ATT_MAX_T = 2048;  // keys per query at most (LDS score table)
 constexpr int ATT_HD = 64;       // head dim of the kernels below
 
@@ -291,15 +290,17 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const __half* __res
     }
 }
 
-// One query per (batch, head) -- the decode step -- over up to ATT_MAX_T keys: 256 threads
-// score keys t, t + 256, ... (fp32 dot products of fp16 rows, in dim order), the softmax
-// runs over an LDS table, then thread (key slot ks, dim chunk dc) accumulates
-// p[t] V[t][8 dc .. 8 dc + 7] over keys t = ks, ks + 32, ... (16-byte row loads, several in
-// flight), and the 32 key slots' partial vectors are added in slot order.  FUSED: the step's
+// One query per (batch, head) -- the decode step -- over up to ATT_MAX_T keys: DEC_THREADS
+// threads score keys t, t + DEC_THREADS, ... (fp32 dot products of fp16 rows, in dim order),
+// the softmax runs over an LDS table, then thread (key slot ks, dim chunk dc) accumulates
+// p[t] V[t][8 dc .. 8 dc + 7] over keys t = ks, ks + DEC_SLOTS, ... (16-byte row loads,
+// several in flight), and the key slots' partial vectors are added in slot order.  FUSED: the step's
 // q, k, v come as float32 from the qkv projection [B][3][H][hd]; k and v are rounded to fp16
 // into the caches at the position first (kv_append_kernel's rounding), q into LDS.
+constexpr int DEC_THREADS = 1024, DEC_SLOTS = DEC_THREADS / 8;
+
 template <bool FUSED>
-__global__ __launch_bounds__(ATT_THREADS) void attention_decode_kernel(const void* __restrict__ qsrc,
+__global__ __launch_bounds__(DEC_THREADS) void attention_decode_kernel(const void* __restrict__ qsrc,
                                                                        __half* __restrict__ kc,
                                                                        __half* __restrict__ vc, int64_t B,
                                                                        int64_t H, int64_t pos0,
@@ -308,8 +309,8 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_decode_kernel(const voi
                                                                        float* __restrict__ out) {
     __shared__ float qs[ATT_HD];
     __shared__ float p[ATT_MAX_T];
-    __shared__ float red[ATT_THREADS / 64];
-    __shared__ float part[32][ATT_HD + 1];
+    __shared__ float red[DEC_THREADS / 64];
+    __shared__ float part[DEC_SLOTS][ATT_HD + 1];
     pos0 = position(pos0, d_pos0, min(T_max, (int64_t)ATT_MAX_T) - 1);
     const int b = blockIdx.y, h = blockIdx.x;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -328,7 +329,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_decode_kernel(const voi
     __syncthreads();
     const int T = (int)pos0 + 1;
     // scores
-    for (int t = tid; t < T; t += ATT_THREADS) {
+    for (int t = tid; t < T; t += DEC_THREADS) {
         const __half* kr = kc + (bh * T_max + t) * ATT_HD;
         uint4 w[ATT_HD / 8];
 #pragma unroll
@@ -345,15 +346,15 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_decode_kernel(const voi
     __syncthreads();
     // softmax over the T scores
     float m = -INFINITY;
-    for (int t = tid; t < T; t += ATT_THREADS) m = fmaxf(m, p[t]);
+    for (int t = tid; t < T; t += DEC_THREADS) m = fmaxf(m, p[t]);
     for (int off = 32; off > 0; off >>= 1) m = fmaxf(m, __shfl_xor(m, off, 64));
     if (lane == 0) red[wave] = m;
     __syncthreads();
     m = red[0];
-    for (int w = 1; w < ATT_THREADS / 64; ++w) m = fmaxf(m, red[w]);
+    for (int w = 1; w < DEC_THREADS / 64; ++w) m = fmaxf(m, red[w]);
     __syncthreads();
     float sum = 0.0f;
-    for (int t = tid; t < T; t += ATT_THREADS) {
+    for (int t = tid; t < T; t += DEC_THREADS) {
         const float e = expf(p[t] - m);
         p[t] = e;
         sum += e;
@@ -362,28 +363,29 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_decode_kernel(const voi
     if (lane == 0) red[wave] = sum;
     __syncthreads();
     sum = 0.0f;
-    for (int w = 0; w < ATT_THREADS / 64; ++w) sum += red[w];
+    for (int w = 0; w < DEC_THREADS / 64; ++w) sum += red[w];
     const float rinv = 1.0f / sum;
-    // weighted V rows: thread (ks, dc) over keys ks, ks + 32, ...
+    // weighted V rows: thread (ks, dc) over keys ks, ks + DEC_SLOTS, ...
     const int ks = tid >> 3, dc = tid & 7;
     float acc[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) acc[j] = 0.0f;
     const __half* vbase = vc + bh * T_max * ATT_HD + 8 * dc;
     int t = ks;
-    for (; t + 96 < T; t += 128) {  // four rows in flight
+    for (; t + 3 * DEC_SLOTS < T; t += 4 * DEC_SLOTS) {  // four rows in flight
         uint4 w[4];
 #pragma unroll
-        for (int u = 0; u < 4; ++u) w[u] = *reinterpret_cast<const uint4*>(vbase + (int64_t)(t + 32 * u) * ATT_HD);
+        for (int u = 0; u < 4; ++u)
+            w[u] = *reinterpret_cast<const uint4*>(vbase + (int64_t)(t + DEC_SLOTS * u) * ATT_HD);
 #pragma unroll
         for (int u = 0; u < 4; ++u) {
-            const float pu = p[t + 32 * u];
+            const float pu = p[t + DEC_SLOTS * u];
             const __half* hw = reinterpret_cast<const __half*>(&w[u]);
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[j] += pu * __half2float(hw[j]);
         }
     }
-    for (; t < T; t += 32) {
+    for (; t < T; t += DEC_SLOTS) {
         const uint4 w = *reinterpret_cast<const uint4*>(vbase + (int64_t)t * ATT_HD);
         const float pu = p[t];
         const __half* hw = reinterpret_cast<const __half*>(&w);
@@ -395,7 +397,7 @@ __global__ __launch_bounds__(ATT_THREADS) void attention_decode_kernel(const voi
     __syncthreads();
     if (tid < ATT_HD) {
         float o = 0.0f;
-        for (int k2 = 0; k2 < 32; ++k2) o += part[k2][tid];
+        for (int k2 = 0; k2 < DEC_SLOTS; ++k2) o += part[k2][tid];
         out[((int64_t)b * H + h) * ATT_HD + tid] = o * rinv;
     }
 }
@@ -585,7 +587,7 @@ int lq_attention_f16(const void* d_q, const void* d_k_cache, const void* d_v_cac
     LQ_REQUIRE(B <= 65535 && H <= 65535, "lq_attention_f16: grid too large");
     hipStream_t st = as_stream(stream);
     if (n == 1) {
-        hipLaunchKernelGGL((attention_decode_kernel<false>), dim3((unsigned)H, (unsigned)B), dim3(ATT_THREADS), 0, st,
+        hipLaunchKernelGGL((attention_decode_kernel<false>), dim3((unsigned)H, (unsigned)B), dim3(DEC_THREADS), 0, st,
                            d_q, (__half*)d_k_cache, (__half*)d_v_cache, B, H, pos0, d_pos0, T_max, scale, d_out);
     } else {
         hipLaunchKernelGGL(attention_mfma_kernel, dim3((unsigned)((n + FA_Q - 1) / FA_Q), (unsigned)H, (unsigned)B),
@@ -606,7 +608,7 @@ int lq_kv_append_attention_f16(const float* d_qkv, int64_t B, int64_t H, int64_t
     if (B == 0) return LQ_OK;
     LQ_REQUIRE(d_qkv && d_k_cache && d_v_cache && d_out, "lq_kv_append_attention_f16: NULL pointer");
     LQ_REQUIRE(B <= 65535 && H <= 65535, "lq_kv_append_attention_f16: grid too large");
-    hipLaunchKernelGGL((attention_decode_kernel<true>), dim3((unsigned)H, (unsigned)B), dim3(ATT_THREADS), 0,
+    hipLaunchKernelGGL((attention_decode_kernel<true>), dim3((unsigned)H, (unsigned)B), dim3(DEC_THREADS), 0,
                        as_stream(stream), d_qkv, (__half*)d_k_cache, (__half*)d_v_cache, B, H, pos0, d_pos0, T_max,
                        scale, d_out);
     return launch_status("lq_kv_append_attention_f16");

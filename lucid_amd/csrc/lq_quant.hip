@@ -935,14 +935,15 @@ struct DynQuantSmall {
     }
 };
 
-// The same step with the input produced in the launch: GELU of x (the FFN's down projection
-// reads gelu(up(...))), or the layer norm of `rows` rows of D (optionally after the residual
-// add x += res, written back), as lq_gelu_tanh_f32 / lq_layer_norm_f32 /
-// lq_add_layer_norm_f32 compute them -- gelu_tanh_f32, and each row's mean and variance as
-// layer_norm_kernel sums them (256 threads per row, thread t over elements t, t + 256, ..., a
-// wave tree, the four wave sums in order) -- so the codes and qparams are the bits of that
-// call followed by lq_dynamic_quantize_f32.  The normalized rows wait in LDS.
-enum { DQ_GELU = 1, DQ_LN = 2, DQ_LN_RES = 3 };
+// The same step with the input produced in the launch: the layer norm of `rows` rows of D
+// (optionally after the residual add x += res, written back), as lq_layer_norm_f32 /
+// lq_add_layer_norm_f32 compute it -- each row's mean and variance as layer_norm_kernel sums
+// them (256 threads per row, thread t over elements t, t + 256, ..., a wave tree, the four
+// wave sums in order) -- so the codes and qparams are the bits of that call followed by
+// lq_dynamic_quantize_f32.  The normalized rows wait in LDS.  (A GELU before the quantize
+// belongs in the producing GEMM's epilogue instead, LQ_EPI_GELU: one workgroup evaluating
+// tanh for a whole FFN row block was slower than the separate launches.)
+enum { DQ_LN = 2, DQ_LN_RES = 3 };
 constexpr int64_t DQ_LN_MAX = 12288;  // normalized values held in LDS (48 KB)
 
 template <class Code, int SRC>
@@ -958,8 +959,8 @@ __global__ __launch_bounds__(kDynBlock) void dyn_quant_fused_kernel(float* x, in
     __shared__ int32_t smin[kDynBlock / 64], smax[kDynBlock / 64];
     __shared__ float s_sz[2];
     const int tid = threadIdx.x;
-    const int n = SRC == DQ_GELU ? D : rows * D;  // GELU: x is n = D contiguous values
-    if constexpr (SRC != DQ_GELU) {
+    const int n = rows * D;
+    {
         const int slot = tid >> 8, t = tid & 255, w = t >> 6, lane = t & 63;
         for (int r0 = 0; r0 < rows; r0 += kDynBlock / 256) {
             const int r = r0 + slot;
@@ -1003,10 +1004,7 @@ __global__ __launch_bounds__(kDynBlock) void dyn_quant_fused_kernel(float* x, in
         }
         __syncthreads();
     }
-    auto val = [&](int i) -> float {
-        if constexpr (SRC == DQ_GELU) return gelu_tanh_f32(x[i]);
-        else return ys[i];
-    };
+    auto val = [&](int i) -> float { return ys[i]; };
     int32_t kmin = KEY_POS_INF, kmax = KEY_NEG_INF;
     for (int i = tid; i < n; i += kDynBlock) key_accum(kmin, kmax, val(i));
     kmin = wave_min(kmin);
@@ -1048,15 +1046,14 @@ struct DynQuantFused {
                    const float* gamma, const float* beta, float ln_eps, void* q, float* qp, int qmin, float eps,
                    float width_f, Grid g, hipStream_t st) {
         typedef typename Code::T T;
-        const size_t lds = src == DQ_GELU ? 0 : sizeof(float) * (size_t)rows * D;
+        const size_t lds = sizeof(float) * (size_t)rows * D;
 #define LQ_DQF(S) \
     hipLaunchKernelGGL((dyn_quant_fused_kernel<Code, S>), dim3(1), dim3(kDynBlock), lds, st, x, ldx, res, ldres, rows, D, \
                        gamma, beta, ln_eps, (T*)q, qp, qmin, eps, width_f, g)
-        if (src == DQ_GELU) LQ_DQF(DQ_GELU);
-        else if (src == DQ_LN) LQ_DQF(DQ_LN);
+        if (src == DQ_LN) LQ_DQF(DQ_LN);
         else LQ_DQF(DQ_LN_RES);
 #undef LQ_DQF
-        return launch_status(src == DQ_GELU ? "lq_gelu_quantize_f32" : "lq_layer_norm_quantize_f32");
+        return launch_status("lq_layer_norm_quantize_f32");
     }
 };
 
@@ -1319,19 +1316,6 @@ int lq_layer_norm_quantize_f32(float* d_x, int64_t ldx, const float* d_res, int6
         return set_error(LQ_ERR_UNSUPPORTED, "lq_layer_norm_quantize_f32: more than 12288 values (one workgroup)");
     return dispatch_code<DynQuantFused>(q_dtype, d_res ? (int)DQ_LN_RES : (int)DQ_LN, d_x, ldx, d_res, ldres,
                                         (int)rows, (int)D, d_gamma, d_beta, ln_eps, d_q, d_qparams, qmin, eps,
-                                        (float)(qmax - qmin), make_grid(qmin, qmax), as_stream(stream));
-}
-
-int lq_gelu_quantize_f32(const float* d_x, int64_t n, int q_dtype, int qmin, int qmax, float eps, float* d_qparams,
-                         void* d_q, void* stream) {
-    LQ_REQUIRE(n > 0, "lq_gelu_quantize_f32: n <= 0");
-    LQ_REQUIRE(d_x && d_qparams && d_q, "lq_gelu_quantize_f32: NULL pointer");
-    LQ_REQUIRE(valid_code(q_dtype), "lq_gelu_quantize_f32: bad code dtype");
-    LQ_REQUIRE(qmax > qmin, "lq_gelu_quantize_f32: qmax <= qmin");
-    if (n > DYN_SMALL_MAX)
-        return set_error(LQ_ERR_UNSUPPORTED, "lq_gelu_quantize_f32: more than 16384 values (one workgroup)");
-    return dispatch_code<DynQuantFused>(q_dtype, (int)DQ_GELU, const_cast<float*>(d_x), (int64_t)n, nullptr,
-                                        (int64_t)0, 1, (int)n, nullptr, nullptr, 0.0f, d_q, d_qparams, qmin, eps,
                                         (float)(qmax - qmin), make_grid(qmin, qmax), as_stream(stream));
 }
 

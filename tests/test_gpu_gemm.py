@@ -369,3 +369,42 @@ def test_packed_decode_split_k_exact(gpu, M, N, K):
             np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
         else:
             np.testing.assert_array_equal(got.view(np.uint8), want.view(np.uint8))
+
+
+@pytest.mark.parametrize("M,N,K,packed", [(8, 2048, 512, True), (3, 100, 784, True), (512, 2048, 512, False),
+                                          (70, 300, 256, False), (4096, 1024, 512, False)])
+def test_gemm_gelu_epilogue_equals_gelu_kernel(gpu, M, N, K, packed):
+    """LQ_EPI_GELU: the float32 output with the tanh GELU applied in the epilogue is bit for bit
+    lq_gelu_tanh_f32 on the output without it (the FFN's up projection followed by F.gelu), on
+    the decode (packed) and the tiled paths, with the activation zero point of the dynamic
+    Linear (unsigned codes as c - 128)."""
+    from lucid_amd import _C
+
+    rng = np.random.default_rng(M + N + K)
+    A = rng.integers(-128, 128, (M, K)).astype(np.int8)
+    B = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    sa = np.float32(rng.uniform(1e-3, 1e-2))
+    sb = rng.uniform(1e-4, 1e-3, N).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    sums = B.astype(np.int64).sum(1).astype(np.int32)
+    kw = dict(a_scale=sa, b_scale=sb, za=131.0, b_sums=sums, bias=bias, packed=packed, flags=_C.EPI_A_U8S8)
+    plain = run_gemm(gpu, A, B, O.OUT_F32, **kw)
+    kw["flags"] |= _C.EPI_GELU
+    fused = run_gemm(gpu, A, B, O.OUT_F32, **kw)
+    dy = _dev(gpu, plain)
+    g = gpu.empty(plain.shape, np.float32, "gpu")
+    _C.call("lq_gelu_tanh_f32", dy.data_ptr(), g.data_ptr(), plain.size, None)
+    np.testing.assert_array_equal(fused.view(np.uint32), g.numpy().view(np.uint32))
+    assert_close_f32_gelu = np.max(np.abs(fused - O.gelu_tanh(plain))) <= 1e-5 * max(np.max(np.abs(plain)), 1.0)
+    assert assert_close_f32_gelu
+
+
+def test_gemm_gelu_rejects(gpu):
+    from lucid_amd import _C
+
+    A = np.zeros((4, 64), np.int8)
+    B = np.zeros((8, 64), np.int8)
+    with pytest.raises(_C.LucidError, match="GELU"):
+        run_gemm(gpu, A, B, O.OUT_Q8, out_scale=1.0, flags=_C.EPI_GELU)
+    with pytest.raises(_C.LucidError, match="GELU"):
+        run_gemm(gpu, A, B, O.OUT_F32, relu=True, flags=_C.EPI_GELU)

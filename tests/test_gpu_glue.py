@@ -263,25 +263,3 @@ def test_layer_norm_quantize_rejects_large(gpu):
     with pytest.raises(_C.LucidError, match="12288"):
         _C.call("lq_layer_norm_quantize_f32", 1, 512, None, 512, 25, 512, None, None, np.float32(1e-5), _C.U8S8, 0,
                 255, np.float32(1e-8), 1, 1, None)
-    with pytest.raises(_C.LucidError, match="16384"):
-        _C.call("lq_gelu_quantize_f32", 1, 16385, _C.U8S8, 0, 255, np.float32(1e-8), 1, 1, None)
-
-
-@pytest.mark.parametrize("n", [16384, 4096, 333])
-def test_gelu_quantize_equals_two_calls(gpu, n):
-    from lucid_amd import _C
-
-    rng = np.random.default_rng(n)
-    x = (rng.standard_normal(n) * 2).astype(np.float32)
-    dx = _d(gpu, x)
-    y = gpu.empty((n,), np.float32, "gpu")
-    q1, q2 = gpu.empty((n,), np.int8, "gpu"), gpu.empty((n,), np.int8, "gpu")
-    qp1, qp2 = gpu.empty((4,), np.float32, "gpu"), gpu.empty((4,), np.float32, "gpu")
-    eps = np.float32(1e-8)
-    ws = gpu.empty((16,), np.uint8, "gpu")
-    _C.call("lq_gelu_tanh_f32", dx.data_ptr(), y.data_ptr(), n, None)
-    _C.call("lq_dynamic_quantize_f32", y.data_ptr(), n, _C.U8S8, 0, 255, eps, qp1.data_ptr(), q1.data_ptr(),
-            ws.data_ptr(), 16, None)
-    _C.call("lq_gelu_quantize_f32", dx.data_ptr(), n, _C.U8S8, 0, 255, eps, qp2.data_ptr(), q2.data_ptr(), None)
-    np.testing.assert_array_equal(q1.numpy(), q2.numpy())
-    np.testing.assert_array_equal(qp1.numpy().view(np.uint32), qp2.numpy().view(np.uint32))
