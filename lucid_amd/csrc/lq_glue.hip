@@ -47,49 +47,22 @@ __global__ __launch_bounds__(256) void embedding_sum_kernel(const float* __restr
     for (int64_t d = threadIdx.x; d < D; d += blockDim.x) out[r * D + d] = a[d] + p[d];
 }
 
-// y = (x - mean) / sqrt(var + eps) [* gamma + beta]: mean and biased variance in float32
-// over the row (wave-level tree sums), one workgroup per row.
-// RES: the row is first replaced by x + res (the residual add, one rounding per element, each
-// element written and read back by the same thread), and the norm runs on the sums: the same
-// bits as a separate add followed by the norm, one launch instead of two.
-template <bool RES>
-__global__ __launch_bounds__(256) void layer_norm_kernel(float* x, int64_t ldx, const float* __restrict__ res,
-                                                         int64_t ldres, float* __restrict__ y, int64_t ldy,
-                                                         int64_t rows, int64_t D, const float* __restrict__ gamma,
-                                                         const float* __restrict__ beta, float eps) {
+// y = (x - mean) / sqrt(var + eps) [* gamma + beta]: mean and biased variance in float32, one
+// workgroup of LN_T threads per row in ln_row's order (the order the fused norm + quantize
+// uses).  RES: the row is first replaced by x + res (the residual add, one rounding per
+// element), and the norm runs on the sums: the same bits as a separate add followed by the
+// norm, one launch instead of two.
+template <int MAXC, bool CACHED>
+__global__ __launch_bounds__(LN_T) void layer_norm_kernel(float* x, int64_t ldx, const float* __restrict__ res,
+                                                          int64_t ldres, float* __restrict__ y, int64_t ldy,
+                                                          int64_t rows, int64_t D, const float* __restrict__ gamma,
+                                                          const float* __restrict__ beta, float eps) {
+    __shared__ float part[2];
     const int64_t r = blockIdx.x;
     if (r >= rows) return;
-    float* xr = x + r * ldx;
-    if constexpr (RES) {
-        const float* rr = res + r * ldres;
-        for (int64_t d = threadIdx.x; d < D; d += blockDim.x) xr[d] = xr[d] + rr[d];
-    }
-    __shared__ float part[8];
-    auto block_sum = [&](float v) {
-        for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off, 64);
-        if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
-        __syncthreads();
-        float s = 0.0f;
-        for (int w = 0; w < (int)(blockDim.x >> 6); ++w) s += part[w];
-        __syncthreads();
-        return s;
-    };
-    float s = 0.0f;
-    for (int64_t d = threadIdx.x; d < D; d += blockDim.x) s += xr[d];
-    const float mean = block_sum(s) / (float)D;
-    float q = 0.0f;
-    for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
-        const float c = xr[d] - mean;
-        q += c * c;
-    }
-    const float var = block_sum(q) / (float)D;
-    const float inv = 1.0f / sqrtf(var + eps);
-    for (int64_t d = threadIdx.x; d < D; d += blockDim.x) {
-        float v = (xr[d] - mean) * inv;
-        if (gamma) v = v * gamma[d];
-        if (beta) v = v + beta[d];
-        y[r * ldy + d] = v;
-    }
+    float v[4 * MAXC];
+    ln_row<MAXC, CACHED>(x + r * ldx, res ? res + r * ldres : nullptr, true, (int)D, threadIdx.x, gamma, beta, eps, v,
+                         part, y + r * ldy);
 }
 
 // gelu, tanh form: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
@@ -504,26 +477,39 @@ int lq_embedding_sum_f32(const float* d_tok_table, int64_t vocab, const float* d
     return launch_status("lq_embedding_sum_f32");
 }
 
+static int launch_layer_norm(float* x, int64_t ldx, const float* res, int64_t ldres, float* y, int64_t ldy,
+                             int64_t rows, int64_t D, const float* gamma, const float* beta, float eps,
+                             hipStream_t st) {
+    const dim3 grid((unsigned)rows), block(LN_T);
+    if (D <= 4 * LN_T) hipLaunchKernelGGL((layer_norm_kernel<1, true>), grid, block, 0, st, x, ldx, res, ldres, y, ldy,
+                                          rows, D, gamma, beta, eps);
+    else if (D <= 16 * LN_T) hipLaunchKernelGGL((layer_norm_kernel<4, true>), grid, block, 0, st, x, ldx, res, ldres,
+                                                y, ldy, rows, D, gamma, beta, eps);
+    else hipLaunchKernelGGL((layer_norm_kernel<1, false>), grid, block, 0, st, x, ldx, res, ldres, y, ldy, rows, D,
+                            gamma, beta, eps);
+    return LQ_OK;
+}
+
 int lq_layer_norm_f32(const float* d_x, int64_t ldx, float* d_y, int64_t ldy, int64_t rows, int64_t D,
                       const float* d_gamma, const float* d_beta, float eps, void* stream) {
-    LQ_REQUIRE(rows >= 0 && D > 0 && ldx >= D && ldy >= D, "lq_layer_norm_f32: bad shape");
+    LQ_REQUIRE(rows >= 0 && D > 0 && D < ((int64_t)1 << 30) && ldx >= D && ldy >= D, "lq_layer_norm_f32: bad shape");
     if (rows == 0) return LQ_OK;
     LQ_REQUIRE(d_x && d_y, "lq_layer_norm_f32: NULL pointer");
     LQ_REQUIRE(rows <= 0x7fffffff, "lq_layer_norm_f32: too many rows");
-    hipLaunchKernelGGL(layer_norm_kernel<false>, dim3((unsigned)rows), dim3(256), 0, as_stream(stream),
-                       const_cast<float*>(d_x), ldx, nullptr, 0, d_y, ldy, rows, D, d_gamma, d_beta, eps);
+    launch_layer_norm(const_cast<float*>(d_x), ldx, nullptr, 0, d_y, ldy, rows, D, d_gamma, d_beta, eps,
+                      as_stream(stream));
     return launch_status("lq_layer_norm_f32");
 }
 
 int lq_add_layer_norm_f32(float* d_x, int64_t ldx, const float* d_res, int64_t ldres, float* d_y, int64_t ldy,
                           int64_t rows, int64_t D, const float* d_gamma, const float* d_beta, float eps,
                           void* stream) {
-    LQ_REQUIRE(rows >= 0 && D > 0 && ldx >= D && ldres >= D && ldy >= D, "lq_add_layer_norm_f32: bad shape");
+    LQ_REQUIRE(rows >= 0 && D > 0 && D < ((int64_t)1 << 30) && ldx >= D && ldres >= D && ldy >= D,
+               "lq_add_layer_norm_f32: bad shape");
     if (rows == 0) return LQ_OK;
     LQ_REQUIRE(d_x && d_res && d_y, "lq_add_layer_norm_f32: NULL pointer");
     LQ_REQUIRE(rows <= 0x7fffffff, "lq_add_layer_norm_f32: too many rows");
-    hipLaunchKernelGGL(layer_norm_kernel<true>, dim3((unsigned)rows), dim3(256), 0, as_stream(stream), d_x, ldx,
-                       d_res, ldres, d_y, ldy, rows, D, d_gamma, d_beta, eps);
+    launch_layer_norm(d_x, ldx, d_res, ldres, d_y, ldy, rows, D, d_gamma, d_beta, eps, as_stream(stream));
     return launch_status("lq_add_layer_norm_f32");
 }
 

@@ -110,6 +110,88 @@ __device__ __forceinline__ float gelu_tanh_f32(float v) {
     return 0.5f * v * (1.0f + tanhf(u));
 }
 
+// Layer norm of one row by a group of LN_T threads (two waves), in one fixed order shared by
+// the standalone norm (lq_layer_norm_f32) and the norm fused into a dynamic quantize, so the
+// two give the same bits: thread t owns the 4-element chunks c = t, t + LN_T, ... of the row
+// (elements 4c .. 4c + 3 below D); the row sum adds each thread's elements in index order,
+// then a shuffle tree over each wave, then the two wave sums in order; the variance sums the
+// squared deviations the same way.  CACHED keeps the thread's (at most 4 MAXC) values in
+// registers between the passes, otherwise they are read again from x.  Every thread of the
+// workgroup calls it (it holds barriers); `act` says whether this thread's row exists.  On
+// return v[] holds the normalized values of the thread's chunks (CACHED), and the row of x
+// holds x + res (res given).  part: 2 floats of LDS per row slot.
+constexpr int LN_T = 128;
+
+template <int MAXC, bool CACHED>
+__device__ __forceinline__ void ln_row(float* xr, const float* rr, bool act, int D, int t, const float* gamma,
+                                       const float* beta, float eps, float (&v)[4 * MAXC], float* part,
+                                       float* y) {
+    const int lane = t & 63, w = t >> 6;
+    const int nch = (D + 3) >> 2;
+    auto elem = [&](int j, int e) -> float {  // the current value of chunk j, element e
+        if constexpr (CACHED) return v[4 * j + e];
+        else return xr[4 * (t + LN_T * j) + e];
+    };
+    // the residual add, written back (each element by the thread that reads it again)
+    if constexpr (CACHED) {
+#pragma unroll
+        for (int j = 0; j < MAXC; ++j)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int idx = 4 * (t + LN_T * j) + e;
+                float a = 0.0f;
+                if (act && idx < D) {
+                    a = xr[idx];
+                    if (rr) {
+                        a = a + rr[idx];
+                        xr[idx] = a;
+                    }
+                }
+                v[4 * j + e] = a;
+            }
+    } else if (rr && act) {
+        for (int c = t; c < nch; c += LN_T)
+            for (int e = 0; e < 4; ++e) {
+                const int idx = 4 * c + e;
+                if (idx < D) xr[idx] = xr[idx] + rr[idx];
+            }
+    }
+    const int jn = CACHED ? MAXC : (nch + LN_T - 1) / LN_T;
+    auto row_sum = [&](auto term) -> float {
+        float s = 0.0f;
+        if (act)
+            for (int j = 0; j < jn; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (4 * (t + LN_T * j) + e < D) s += term(elem(j, e));
+        for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
+        if (lane == 0) part[w] = s;
+        __syncthreads();
+        const float tot = part[0] + part[1];
+        __syncthreads();
+        return tot;
+    };
+    const float mean = row_sum([](float a) { return a; }) / (float)D;
+    const float var = row_sum([&](float a) {
+                          const float c = a - mean;
+                          return c * c;
+                      }) / (float)D;
+    const float inv = 1.0f / sqrtf(var + eps);
+    if (!act) return;
+    for (int j = 0; j < jn; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int idx = 4 * (t + LN_T * j) + e;
+            if (idx < D) {
+                float a = (elem(j, e) - mean) * inv;
+                if (gamma) a = a * gamma[idx];
+                if (beta) a = a + beta[idx];
+                if constexpr (CACHED) v[4 * j + e] = a;
+                if (y) y[idx] = a;
+            }
+        }
+}
+
 // clip with NaN pass-through and Lucid's signed-zero tie rule (backend/cpu/Vdsp.cpp:33-62).
 __device__ __forceinline__ float clip_tie(float v, float lo, float hi, bool lo_ties, bool hi_ties) {
     if (lo_ties ? v <= lo : v < lo) return lo;

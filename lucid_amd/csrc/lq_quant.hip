@@ -937,14 +937,14 @@ struct DynQuantSmall {
 
 // The same step with the input produced in the launch: the layer norm of `rows` rows of D
 // (optionally after the residual add x += res, written back), as lq_layer_norm_f32 /
-// lq_add_layer_norm_f32 compute it -- each row's mean and variance as layer_norm_kernel sums
-// them (256 threads per row, thread t over elements t, t + 256, ..., a wave tree, the four
-// wave sums in order) -- so the codes and qparams are the bits of that call followed by
+// lq_add_layer_norm_f32 compute it -- ln_row, eight rows at a time on the workgroup's 1024
+// threads -- so the codes and qparams are the bits of that call followed by
 // lq_dynamic_quantize_f32.  The normalized rows wait in LDS.  (A GELU before the quantize
 // belongs in the producing GEMM's epilogue instead, LQ_EPI_GELU: one workgroup evaluating
 // tanh for a whole FFN row block was slower than the separate launches.)
 enum { DQ_LN = 2, DQ_LN_RES = 3 };
 constexpr int64_t DQ_LN_MAX = 12288;  // normalized values held in LDS (48 KB)
+constexpr int DQ_LN_MAXD = 16 * LN_T;  // widest row kept in registers by ln_row<4>
 
 template <class Code, int SRC>
 __global__ __launch_bounds__(kDynBlock) void dyn_quant_fused_kernel(float* x, int64_t ldx, const float* res,
@@ -955,52 +955,25 @@ __global__ __launch_bounds__(kDynBlock) void dyn_quant_fused_kernel(float* x, in
                                                                     float* __restrict__ qp, int qmin, float eps,
                                                                     float width_f, Grid g) {
     extern __shared__ float ys[];
-    __shared__ float part[kDynBlock / 256][4];
+    __shared__ float part[kDynBlock / LN_T][2];
     __shared__ int32_t smin[kDynBlock / 64], smax[kDynBlock / 64];
     __shared__ float s_sz[2];
     const int tid = threadIdx.x;
     const int n = rows * D;
     {
-        const int slot = tid >> 8, t = tid & 255, w = t >> 6, lane = t & 63;
-        for (int r0 = 0; r0 < rows; r0 += kDynBlock / 256) {
+        const int slot = tid / LN_T, t = tid % LN_T;
+        for (int r0 = 0; r0 < rows; r0 += kDynBlock / LN_T) {
             const int r = r0 + slot;
             const bool act = r < rows;
             float* xr = x + (int64_t)(act ? r : 0) * ldx;
-            if (SRC == DQ_LN_RES && act) {
-                const float* rr = res + (int64_t)r * ldres;
-                for (int d = t; d < D; d += 256) xr[d] = xr[d] + rr[d];
+            const float* rr = SRC == DQ_LN_RES ? res + (int64_t)(act ? r : 0) * ldres : nullptr;
+            if (D <= DQ_LN_MAXD) {
+                float v[16];
+                ln_row<4, true>(xr, rr, act, D, t, gamma, beta, ln_eps, v, part[slot], ys + (act ? r : 0) * D);
+            } else {  // wider rows are read from HBM again, as the standalone kernel does
+                float v[4];
+                ln_row<1, false>(xr, rr, act, D, t, gamma, beta, ln_eps, v, part[slot], ys + (act ? r : 0) * D);
             }
-            float sm = 0.0f;
-            if (act)
-                for (int d = t; d < D; d += 256) sm += xr[d];
-            for (int off = 32; off > 0; off >>= 1) sm += __shfl_xor(sm, off, 64);
-            if (lane == 0) part[slot][w] = sm;
-            __syncthreads();
-            float tot = 0.0f;
-            for (int ww = 0; ww < 4; ++ww) tot += part[slot][ww];
-            __syncthreads();
-            const float mean = tot / (float)D;
-            float qv = 0.0f;
-            if (act)
-                for (int d = t; d < D; d += 256) {
-                    const float c = xr[d] - mean;
-                    qv += c * c;
-                }
-            for (int off = 32; off > 0; off >>= 1) qv += __shfl_xor(qv, off, 64);
-            if (lane == 0) part[slot][w] = qv;
-            __syncthreads();
-            tot = 0.0f;
-            for (int ww = 0; ww < 4; ++ww) tot += part[slot][ww];
-            __syncthreads();
-            const float var = tot / (float)D;
-            const float inv = 1.0f / sqrtf(var + ln_eps);
-            if (act)
-                for (int d = t; d < D; d += 256) {
-                    float v = (xr[d] - mean) * inv;
-                    if (gamma) v = v * gamma[d];
-                    if (beta) v = v + beta[d];
-                    ys[r * D + d] = v;
-                }
         }
         __syncthreads();
     }
