@@ -57,6 +57,10 @@ def _parse() -> argparse.Namespace:
                         "default all -- for profiling one group")
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="bound on the CPU-baseline sample's wall time")
+    p.add_argument("--eager", action="store_true",
+                   help="component timings launch each pass eagerly on a created stream instead of "
+                        "replaying a captured HIP graph (for runs under rocprofv3, which has aborted "
+                        "inside graph replay here); launch cost then stays in the figures")
     p.add_argument("--copy-mb", type=int, default=0,
                    help="also run one device-to-device copy of this many MiB (the known-size "
                         "kernel that scales rocprofv3 FETCH_SIZE / WRITE_SIZE readings)")
@@ -141,6 +145,26 @@ class GraphTimer:
         return ms.value / (reps * len(calls))
 
 
+class EagerTimer(GraphTimer):
+    """GraphTimer's interface with the passes launched eagerly on the created stream."""
+
+    def time_ms(self, calls, reps: int, warmup: int) -> float:
+        C, st = self.C, self.stream
+        for _ in range(warmup):
+            for call in calls:
+                call(st)
+        C.call("lq_stream_synchronize", st)
+        C.call("lq_event_record", self.start, st)
+        for _ in range(reps):
+            for call in calls:
+                call(st)
+        C.call("lq_event_record", self.stop, st)
+        C.call("lq_event_synchronize", self.stop)
+        ms = ctypes.c_float()
+        C.call("lq_event_elapsed_ms", ctypes.byref(ms), self.start, self.stop)
+        return ms.value / (reps * len(calls))
+
+
 def _rotations(nbytes: int) -> int:
     """Copies of a weight needed to stream >= 512 MiB per pass (past the 256 MB
     Infinity Cache, so each call reads its weight from HBM)."""
@@ -153,6 +177,22 @@ def weight_only_lines(L, C, gtimer):
     out = []
     rng = np.random.default_rng(11)
     lib = C.lib()
+    # the one-launch streaming-read floor for the same weight sizes (lq_read_floor: each byte
+    # loaded once, nothing stored), so the GEMV lines can be read as a fraction of it
+    sink = L.empty((256,), np.uint32, "gpu")
+    for nbytes in (4096 * 4096, 11008 * 4096, 4096 * 4096 // 2):
+        rot = _rotations(nbytes)
+        W = L.empty((rot * nbytes,), np.int8, "gpu")
+        C.call("lq_fill_u32", W.data_ptr(), 0x3A1F05C7, rot * nbytes // 4, None)
+        calls = [lambda st, r=r: C.check(lib.lq_read_floor(W.data_ptr() + r * nbytes, nbytes, 0xFFFFFFFF,
+                                                           sink.data_ptr(), st), "lq_read_floor")
+                 for r in range(rot)]
+        ms = gtimer.time_ms(calls, 10, 2)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out.append({"kernel": "lq_read_floor (one-launch streaming read, the floor)", "bytes": nbytes,
+                    "rotating_copies": rot, "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 3)})
+        del W
     for (M, N, K) in ((1, 4096, 4096), (16, 4096, 4096), (1, 11008, 4096), (16, 11008, 4096),
                       (1, 4096, 11008), (16, 4096, 11008)):
         rot = _rotations(N * K)
@@ -854,7 +894,7 @@ def main() -> None:
         print(json.dumps({"error": "no HIP device visible"}))
         sys.exit(1)
     timer = Timer(C)
-    gtimer = GraphTimer(C)
+    gtimer = EagerTimer(C) if args.eager else GraphTimer(C)
     if args.copy_mb > 0:
         nbytes = args.copy_mb << 20
         src = L.empty((nbytes,), np.uint8, "gpu")

@@ -109,6 +109,12 @@ int lq_memcpy_d2h(void* h_dst, const void* d_src, size_t bytes, void* stream);
 int lq_memcpy_d2d(void* d_dst, const void* d_src, size_t bytes, void* stream);
 /* Fill `count` 32-bit words with `value` using a kernel (graph-capture safe). */
 int lq_fill_u32(void* d_dst, uint32_t value, size_t count, void* stream);
+/* The one-launch streaming-read floor the bandwidth-bound kernels are measured against: reads
+ * `bytes` (a multiple of 16, 16-byte aligned) of d_src once, in 16 KB per workgroup, and
+ * stores to d_sink[0..255] only when a thread's XOR of its words equals `never` (pick a value
+ * that cannot occur, or give a 1 KB sink).  A measurement kernel with no counterpart in the
+ * reference: Lucid's dispatch bench has no device floor to compare against. */
+int lq_read_floor(const void* d_src, size_t bytes, uint32_t never, uint32_t* d_sink, void* stream);
 int lq_stream_create(void** stream);
 /* Waits for the stream's work, drops it from every allocation's lq_record_stream uses, then
  * destroys it. */
@@ -330,6 +336,30 @@ int lq_gemm_w8a8_packed(const int8_t* d_A, int64_t lda, const int8_t* d_B_packed
                         const int32_t* d_b_sums, const float* d_bias, const float* d_out_scale,
                         const float* d_out_zero_point, int out_qmin, int out_qmax, int out_kind,
                         int flags, void* d_workspace, size_t workspace_bytes, void* stream);
+
+/* nnqd.Linear's whole forward at decode sizes in one launch, with the float module before it
+ * folded in: the input a [M, K] is
+ *   src LQ_DL_PLAIN   a = x
+ *       LQ_DL_LN      a = layer_norm(x)                      (the bits of lq_layer_norm_f32)
+ *       LQ_DL_ADD_LN  s = x + res, a = layer_norm(s)         (lq_add_layer_norm_f32; s is
+ *                     stored to d_sum when it is not NULL -- a buffer other than x, which
+ *                     stays as it was)
+ * (gamma / beta NULL: 1 / 0), then the live min / max of all M x K values, the per-tensor affine
+ * qparams on the unsigned grid [qmin, qmax] (0 <= qmin < qmax <= 255; stored to d_qparams as
+ * {min, max, scale, zero point} when not NULL), the codes of lq_dynamic_quantize_f32, and the
+ * float32 product of lq_gemm_w8a8_packed (LQ_EPI_A_U8S8) with the packed weight, its per-row
+ * scales and code sums and the bias; flags 0 or LQ_EPI_GELU.  The bits of those launches in
+ * sequence.  For M <= 16, K a multiple of 16, M K <= 16384 (with a norm: K <= 2048 and
+ * M K <= 8192), x rows 16-byte aligned without a norm; LQ_ERR_UNSUPPORTED otherwise.
+ * Replaces, as one call, the steps of Lucid's dynamic Linear forward
+ * (lucid/nn/quantized/dynamic/linear.py:85-92: calculate_qparams of x.min() / x.max(),
+ * fake_quantize, the linear) and the LayerNorm module that precedes it in a decoder. */
+enum { LQ_DL_PLAIN = 0, LQ_DL_LN = 1, LQ_DL_ADD_LN = 2 };
+int lq_dynamic_linear_packed_f32(const float* d_x, int64_t ldx, const float* d_res, int64_t ldres, float* d_sum,
+                                 int64_t ld_sum, int src, const float* d_gamma, const float* d_beta, float ln_eps,
+                                 int64_t M, int64_t K, int qmin, int qmax, float eps, float* d_qparams,
+                                 const int8_t* d_w_packed, const float* d_w_scale, const int32_t* d_w_sums,
+                                 const float* d_bias, int64_t N, float* d_y, int64_t ldy, int flags, void* stream);
 
 /* sums[r] = sum_k X[r,k] over int8 rows (the weight code sums a module caches for the
  * activation zero-point correction).  No reference counterpart (Lucid has no integer GEMM). */

@@ -25,6 +25,7 @@ BF16 = 10
 OBS_MINMAX, OBS_EMA, OBS_REPLACE = 0, 1, 2
 OUT_I32, OUT_F32, OUT_F16, OUT_Q8, OUT_QU8, OUT_FQ32, OUT_Q16, OUT_QU8S8 = 0, 1, 2, 3, 4, 5, 6, 7
 EPI_RELU, EPI_A_U8S8, EPI_ROUND_BF16, EPI_GELU = 1, 2, 4, 8
+DL_PLAIN, DL_LN, DL_ADD_LN = 0, 1, 2
 PAD_ZEROS, PAD_REFLECT, PAD_REPLICATE, PAD_CIRCULAR = 0, 1, 2, 3
 MERGE_ADD, MERGE_MUL, MERGE_ADD_SCALAR, MERGE_MUL_SCALAR, MERGE_COPY = 0, 1, 2, 3, 4
 ACT_SIGMOID, ACT_TANH, ACT_HARDSWISH, ACT_HARDSIGMOID, ACT_ELU, ACT_LEAKY_RELU = 0, 1, 2, 3, 4, 5
@@ -68,6 +69,7 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_memcpy_d2h": (_I, [_P, _P, _SZ, _P]),
     "lq_memcpy_d2d": (_I, [_P, _P, _SZ, _P]),
     "lq_fill_u32": (_I, [_P, ctypes.c_uint32, _SZ, _P]),
+    "lq_read_floor": (_I, [_P, _SZ, ctypes.c_uint32, _P, _P]),
     "lq_stream_create": (_I, [ctypes.POINTER(_P)]),
     "lq_stream_destroy": (_I, [_P]),
     "lq_stream_synchronize": (_I, [_P]),
@@ -134,6 +136,8 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_pack_weights_i8": (_I, [_P, _I64, _I64, _I64, _P, _P]),
     "lq_gemm_w8a8_packed": (_I, [_P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P, _I64, _P, _I64,
                                  _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _SZ, _P]),
+    "lq_dynamic_linear_packed_f32": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _P, _P, _F, _I64, _I64, _I, _I, _F,
+                                          _P, _P, _P, _P, _P, _I64, _P, _I64, _I, _P]),
     "lq_conv2d_weight_pack_size": (_SZ, [_I64, _I64, _I64, _I64]),
     "lq_conv2d_pack_weights_i8": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "lq_conv2d_i8_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I,

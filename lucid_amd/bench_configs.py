@@ -191,6 +191,25 @@ class DynLinear:
                 _C.U8S8, self.qmin, self.qmax, self.EPS, self.qp.data_ptr(), self.codes.data_ptr(), stream)
         return True
 
+    ONE_LAUNCH_MK, ONE_LAUNCH_MK_LN = 16384, 8192  # lq_dynamic_linear_packed_f32's limits
+
+    def one_launch(self, x: int, ldx: int, res, ldres: int, sum_, src: int, rows: int, y: int, stream,
+                   gelu: bool = False) -> bool:
+        """The whole forward in one launch (lq_dynamic_linear_packed_f32), the layer norm
+        before it folded in for ``src`` DL_LN / DL_ADD_LN (x + res stored to ``sum_``): the
+        bits of the norm, the input step and the product.  False (nothing launched) outside its
+        sizes (rows <= 16, K % 16 == 0, rows K <= 16384; with a norm K <= 2048, rows K <= 8192)."""
+        mk = self.ONE_LAUNCH_MK if src == _C.DL_PLAIN else self.ONE_LAUNCH_MK_LN
+        if (self.packed is None or rows > 16 or self.K % 16 or rows * self.K > mk
+                or (src != _C.DL_PLAIN and self.K > 2048)):
+            return False
+        _C.call("lq_dynamic_linear_packed_f32", x, ldx, res, ldres, sum_, self.K, src, None, None, np.float32(1e-5),
+                rows, self.K, self.qmin, self.qmax, self.EPS, self.qp.data_ptr(), self.packed.data_ptr(),
+                self.w.scale.data_ptr(), self.w.sums.data_ptr(),
+                self.bias.data_ptr() if self.bias is not None else None, self.N, y, self.N,
+                _C.EPI_GELU if gelu else 0, stream)
+        return True
+
     def gemm(self, rows: int, y: int, stream, gelu: bool = False) -> None:
         """The int8 product of the codes the last input step left, float32 out (with the tanh
         GELU of the following float module in its epilogue when ``gelu``)."""
@@ -218,8 +237,9 @@ class Int8Decoder:
     replayed (the position is the device counter ``self.pos``)."""
 
     def __init__(self, qdec, glue: dict, batch: int = BATCH, max_prompt: int = PREFILL,
-                 max_positions: int = PREFILL + DECODE) -> None:
+                 max_positions: int = PREFILL + DECODE, one_launch: bool = True) -> None:
         self.B, self.Tp, self.Tmax = batch, max_prompt, max_positions
+        self.one_launch = one_launch  # decode Linears as lq_dynamic_linear_packed_f32 where it applies
         self.D, self.H, self.hd = D_MODEL, HEADS, D_MODEL // HEADS
         rows = batch * max_prompt
         self.layers = [tuple(DynLinear(getattr(layer, n), rows) for n in ("qkv", "out", "up", "down"))
@@ -232,6 +252,7 @@ class Int8Decoder:
         self.npos = glue["pos"].shape[0]
         f32 = lambda *s: empty(s, np.float32, "gpu")  # noqa: E731
         self.h, self.hn, self.att, self.proj = f32(rows, self.D), f32(rows, self.D), f32(rows, self.D), f32(rows, self.D)
+        self.h2 = f32(batch, self.D)  # the residual stream's second buffer for one-launch decode steps
         self.qkv, self.up, self.hl = f32(rows, 3 * self.D), f32(rows, FFN), f32(batch, self.D)
         self.logits = f32(batch, self.V)
         self.q16 = empty((batch, self.H, max_prompt, self.hd), np.float16, "gpu")
@@ -251,15 +272,52 @@ class Int8Decoder:
         if key is None or key in self._streams:
             return
         self._streams.add(key)
-        bufs = [self.tok, self.posemb, self.h, self.hn, self.att, self.proj, self.qkv, self.up, self.hl,
+        bufs = [self.tok, self.posemb, self.h, self.h2, self.hn, self.att, self.proj, self.qkv, self.up, self.hl,
                 self.logits, self.q16, self.prompt, self.next, self.pos]
         bufs += [t for kv in self.cache for t in kv]
         bufs += [t for lins in self.layers for lin in lins for t in lin.tensors()] + self.head.tensors()
         for t in bufs:
             t.record_stream(stream)
 
+    def _decode_one_launch(self, stream) -> bool:
+        """A decode step whose Linears each run as one launch with the norm before them
+        (lq_dynamic_linear_packed_f32): the residual stream alternates between two buffers,
+        since the sum is stored while other workgroups still read the old one.  False when the
+        sizes fall outside that entry (nothing launched)."""
+        B, D, H, hd = self.B, self.D, self.H, self.hd
+        normed = [lin for (qkv, _, up, _) in self.layers for lin in (qkv, up)] + [self.head]
+        plain = [lin for (_, out, _, down) in self.layers for lin in (out, down)]
+        if B > 16 or any(lin.packed is None or lin.K % 16 for lin in normed + plain):
+            return False
+        if any(B * lin.K > lin.ONE_LAUNCH_MK_LN or lin.K > 2048 for lin in normed):
+            return False
+        if any(B * lin.K > lin.ONE_LAUNCH_MK for lin in plain):
+            return False
+        p = self.pos.data_ptr()
+        cur, nxt = self.h.data_ptr(), self.h2.data_ptr()
+        _C.call("lq_embedding_sum_f32", self.tok.data_ptr(), self.V, self.posemb.data_ptr(), self.npos, D,
+                self.next.data_ptr(), B, 1, 0, p, cur, stream)
+        proj = self.proj.data_ptr()
+        for li, ((qkv, out, up, down), (kc, vc)) in enumerate(zip(self.layers, self.cache)):
+            if li == 0:
+                qkv.one_launch(cur, D, None, D, None, _C.DL_LN, B, self.qkv.data_ptr(), stream)
+            else:
+                qkv.one_launch(cur, D, proj, D, nxt, _C.DL_ADD_LN, B, self.qkv.data_ptr(), stream)
+                cur, nxt = nxt, cur
+            _C.call("lq_kv_append_attention_f16", self.qkv.data_ptr(), B, H, hd, 0, p, self.Tmax, kc.data_ptr(),
+                    vc.data_ptr(), np.float32(self.scale), self.att.data_ptr(), stream)
+            out.one_launch(self.att.data_ptr(), D, None, D, None, _C.DL_PLAIN, B, proj, stream)
+            up.one_launch(cur, D, proj, D, nxt, _C.DL_ADD_LN, B, self.up.data_ptr(), stream, gelu=True)
+            cur, nxt = nxt, cur
+            down.one_launch(self.up.data_ptr(), FFN, None, FFN, None, _C.DL_PLAIN, B, proj, stream)
+        self.head.one_launch(cur, D, proj, D, None, _C.DL_ADD_LN, B, self.logits.data_ptr(), stream)
+        _C.call("lq_argmax_next_f32", self.logits.data_ptr(), B, self.V, self.next.data_ptr(), p, 1, stream)
+        return True
+
     def _step(self, tokens: int, n: int, stream) -> None:
         self._use_stream(stream)
+        if self.one_launch and n == 1 and tokens == self.next.data_ptr() and self._decode_one_launch(stream):
+            return
         B, D, H, hd = self.B, self.D, self.H, self.hd
         M = B * n
         p = self.pos.data_ptr()

@@ -1171,6 +1171,229 @@ static int launch_packed_skinny(const GemmArgs& a, hipStream_t st) {
     return launch_status("lq_gemm_w8a8_packed");
 }
 
+// ------------------------------------------ dynamic Linear at decode sizes, one launch
+//
+// nnqd.Linear's forward for M <= 16 rows in one launch (lq_dynamic_linear_packed_f32).  The
+// launches it replaces -- the layer norm of the float module before it (after its residual
+// add), lq_dynamic_quantize_f32 (live min / max, per-tensor affine qparams, codes c - 128)
+// and lq_gemm_w8a8_packed -- each wait for the one before, and at decode sizes each is a few
+// microseconds of latency around little work.  Here every workgroup builds the whole int8
+// input itself, in LDS: at most 16 rows, re-read from L2 by each workgroup, while the weight
+// -- the bytes that count -- is still read once.  A workgroup issues its first weight loads
+// before the input work, so their latency runs under it.  The norm is ln_row (the order of
+// the standalone norm), the extrema are order-free, the qparams and codes are dyn_qparams and
+// quant_one with the same reciprocal, and the products are exact int32 sums: the launches'
+// bits.
+//
+// WT: each of the 4 waves owns a 16-column tile and all of K (wide N, so fewer workgroups
+// repeat the input work); otherwise the waves split the K steps of one tile and meet in LDS
+// (gemm_i8_packed_skinny_kernel's split).
+enum { DL_PLAIN = 0, DL_LN = 1, DL_ADD_LN = 2 };  // LQ_DL_*
+constexpr int DL_MAX_MK = 16384;                   // input values (held in registers, 16 x 4 per lane)
+constexpr int DL_MAX_MK_LN = 8192;                 // normalized values staged in LDS (32 KB)
+constexpr int DL_MAX_K_LN = 32 * LN_T;             // row width ln_load<8> keeps in registers
+constexpr int DL_UNROLL = 8;
+constexpr int64_t DL_WT_MIN_TILES = 512;  // from here on, wave tiles (N >= 8192)
+
+struct DynLinArgs {
+    const float* x;
+    int64_t ldx;
+    const float* res;  // DL_ADD_LN
+    int64_t ldres;
+    float* sum;  // x + res out (workgroup 0), or null; never x itself (other workgroups read x)
+    int64_t ldsum;
+    const float* gamma;
+    const float* beta;
+    float ln_eps;
+    int qmin;
+    float eps, width_f;
+    Grid g;
+    float* qp;  // {min, max, scale, zero point} out (workgroup 0), or null
+    int KP;     // LDS row stride of the codes: the K steps' bytes + 16 (16 rows on distinct banks)
+};
+
+// Codes c - 128 of four values as one dword (byte e = value e).
+// (quant_store: the integer-domain form of Code::store(quant_one(...)), the same codes)
+__device__ __forceinline__ uint32_t dl_codes4(vf4 v, float inv, float z, const Grid& g) {
+    const uint32_t c0 = (uint8_t)quant_store<CodeU8S8>(v.x, inv, z, g);
+    const uint32_t c1 = (uint8_t)quant_store<CodeU8S8>(v.y, inv, z, g);
+    const uint32_t c2 = (uint8_t)quant_store<CodeU8S8>(v.z, inv, z, g);
+    const uint32_t c3 = (uint8_t)quant_store<CodeU8S8>(v.w, inv, z, g);
+    return c0 | (c1 << 8) | (c2 << 16) | (c3 << 24);
+}
+
+// MAXC: chunks per lane of a normalized row; RPW: rows per wave (M <= 4 RPW); both unused by
+// DL_PLAIN, whose M x K values stay in registers (16 float4 per lane).
+template <int SRC, bool WT, int MAXC, int RPW, int KIND>
+__global__ __launch_bounds__(256) void dyn_linear_skinny_kernel(DynLinArgs d, GemmArgs a) {
+    extern __shared__ __align__(16) uint8_t dl_lds[];
+    __shared__ int32_t smin[4], smax[4];
+    __shared__ v4i red[WT ? 1 : 4][64];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int M = a.M, K = a.K, KS = (K + 63) / 64, tiles = (a.N + 15) / 16;
+    int8_t* cs = reinterpret_cast<int8_t*>(dl_lds);  // codes c - 128, [M][KP]
+    float* ys = reinterpret_cast<float*>(dl_lds + ((M * d.KP + 15) & ~15));  // normalized rows [M][K]
+
+    // ---- everything that does not depend on the input, in flight first: this wave's first
+    // weight steps and its output columns' epilogue inputs
+    const int tile = WT ? blockIdx.x * 4 + wave : blockIdx.x;
+    const int per = WT ? KS : (KS + 3) / 4;
+    const int kb = WT ? 0 : wave * per, ke = min(KS, kb + per);
+    const int8_t* bt = a.B + (int64_t)min(tile, tiles - 1) * KS * PACK_TILE + lane * 16;
+    v4i bf[DL_UNROLL];
+#pragma unroll
+    for (int u = 0; u < DL_UNROLL; ++u)
+        bf[u] = kb + u < ke ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(bt + (int64_t)(kb + u) * PACK_TILE))
+                            : v4i{0, 0, 0, 0};
+    // the column inputs as loaded values only (a conversion here would wait for the weights):
+    // symmetric weights, no zero-point column
+    const int n = min(tile, tiles - 1) * 16 + (lane >> 4) * 4;
+    ColCtx cols;
+    cols.n = n;
+    cols.vec = vec_store_ok(a, n, OutTraits<KIND>::bytes);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        const int nn = min(n + r, a.N - 1);
+        cols.sb[r] = a.b_scale[nn];
+        cols.bias[r] = a.bias ? a.bias[nn] : 0.0f;
+        cols.bsum[r] = a.b_sums[nn];
+        cols.zb[r] = 0;
+    }
+
+    // ---- the input values and the keys of their extrema
+    int32_t kmin = KEY_POS_INF, kmax = KEY_NEG_INF;
+    const int K4 = K >> 2;
+    constexpr int XV = DL_MAX_MK / (4 * 256);
+    vf4 xv[SRC == DL_PLAIN ? XV : 1];
+    if constexpr (SRC == DL_PLAIN) {
+#pragma unroll
+        for (int j = 0; j < XV; ++j) {
+            const int i = tid + 256 * j;
+            if (i < M * K4) {
+                const int r = i / K4;
+                xv[j] = *reinterpret_cast<const vf4*>(d.x + (int64_t)r * d.ldx + 4 * (i - r * K4));
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < XV; ++j)
+            if (tid + 256 * j < M * K4) {
+                key_accum(kmin, kmax, xv[j].x);
+                key_accum(kmin, kmax, xv[j].y);
+                key_accum(kmin, kmax, xv[j].z);
+                key_accum(kmin, kmax, xv[j].w);
+            }
+    } else {
+        // rows wave, wave + 4, ...: every row of the wave loaded before any is normalized
+        float v[RPW][4 * MAXC], rv[RPW][4 * MAXC];
+#pragma unroll
+        for (int q = 0; q < RPW; ++q) {
+            const int r = wave + 4 * q;
+            const bool act = r < M;
+            const int rc = act ? r : 0;
+            ln_fetch<MAXC>(d.x + (int64_t)rc * d.ldx, SRC == DL_ADD_LN ? d.res + (int64_t)rc * d.ldres : nullptr, act,
+                           K, lane, v[q], rv[q]);
+        }
+#pragma unroll
+        for (int q = 0; q < RPW; ++q) {
+            const int r = wave + 4 * q;
+            const bool act = r < M;
+            float* wb = (SRC == DL_ADD_LN && d.sum && blockIdx.x == 0) ? d.sum + (int64_t)(act ? r : 0) * d.ldsum
+                                                                        : nullptr;
+            ln_add_store<MAXC>(v[q], rv[q], SRC == DL_ADD_LN, wb, act, K, lane);
+        }
+#pragma unroll
+        for (int q = 0; q < RPW; ++q) {
+            const int r = wave + 4 * q;
+            if (r >= M) continue;  // the whole wave: no row
+            ln_norm<MAXC>(v[q], true, K, lane, d.gamma, d.beta, d.ln_eps, ys + r * K);
+            {
+#pragma unroll
+                for (int j = 0; j < MAXC; ++j)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (4 * (lane + LN_T * j) + e < K) key_accum(kmin, kmax, v[q][4 * j + e]);
+            }
+        }
+    }
+    kmin = wave_min(kmin);
+    kmax = wave_max(kmax);
+    if (lane == 0) {
+        smin[wave] = kmin;
+        smax[wave] = kmax;
+    }
+    __syncthreads();  // also publishes ys
+    kmin = min(min(smin[0], smin[1]), min(smin[2], smin[3]));
+    kmax = max(max(smax[0], smax[1]), max(smax[2], smax[3]));
+    float o[4];
+    dyn_qparams(kmin, kmax, d.qmin, d.eps, d.width_f, d.g, o);
+    const float sc = o[2], z = o[3];
+    const float inv = 1.0f / sc;
+    if (d.qp && blockIdx.x == 0 && tid == 0) {
+        d.qp[0] = o[0];
+        d.qp[1] = o[1];
+        d.qp[2] = o[2];
+        d.qp[3] = o[3];
+    }
+
+    // ---- the codes, row-major in LDS with a zero tail up to whole K steps
+    if constexpr (SRC == DL_PLAIN) {
+#pragma unroll
+        for (int j = 0; j < XV; ++j) {
+            const int i = tid + 256 * j;
+            if (i < M * K4) {
+                const int r = i / K4, k = 4 * (i - r * K4);
+                *reinterpret_cast<uint32_t*>(cs + r * d.KP + k) = dl_codes4(xv[j], inv, z, d.g);
+            }
+        }
+    } else {
+        for (int i = tid; i < M * K4; i += 256) {
+            const int r = i / K4, k = 4 * (i - r * K4);
+            *reinterpret_cast<uint32_t*>(cs + r * d.KP + k) =
+                dl_codes4(*reinterpret_cast<const vf4*>(ys + r * K + k), inv, z, d.g);
+        }
+    }
+    const int tail4 = (KS * 64 - K) >> 2;
+    for (int i = tid; i < M * tail4; i += 256) {
+        const int r = i / tail4;
+        *reinterpret_cast<uint32_t*>(cs + r * d.KP + K + 4 * (i - r * tail4)) = 0u;
+    }
+    __syncthreads();
+
+    // ---- the product: weights from registers, code fragments from LDS (rows past M read the
+    // last row; their outputs are never stored)
+    const int8_t* arow = cs + min(lane & 15, M - 1) * d.KP + (lane >> 4) * 16;
+    v4i acc = v4i{0, 0, 0, 0};
+    for (int ks = kb; ks < ke; ks += DL_UNROLL) {
+#pragma unroll
+        for (int u = 0; u < DL_UNROLL; ++u)
+            if (ks + u < ke)
+                acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(bf[u], *reinterpret_cast<const v4i*>(arow + (ks + u) * 64),
+                                                            acc, 0, 0, 0);
+        if (ks + DL_UNROLL < ke) {
+#pragma unroll
+            for (int u = 0; u < DL_UNROLL; ++u) {
+                const int k2 = ks + DL_UNROLL + u;
+                bf[u] = k2 < ke ? __builtin_nontemporal_load(reinterpret_cast<const v4i*>(bt + (int64_t)k2 * PACK_TILE))
+                                : v4i{0, 0, 0, 0};
+            }
+        }
+    }
+    if constexpr (!WT) {
+        red[wave][lane] = acc;
+        __syncthreads();
+        if (wave != 0) return;
+        acc = red[0][lane] + red[1][lane] + red[2][lane] + red[3][lane];
+    }
+    if (tile >= tiles) return;
+    EpiParams p = epi_params(a);
+    p.za = (int)z - 128;  // the codes' zero point, in the stored c - 128 units
+    p.has_za = true;
+    RowCtx row;
+    row.sa = sc;
+    row.asum = 0;
+    epilogue4c<KIND>(a, p, row, cols, lane & 15, acc);
+}
+
 // ------------------------------------------------------------ generic kernel
 // Any K, alignment and leading dimensions (byte loads, dot4 on the fly): the fallback for
 // shapes the vector paths do not take.  One thread per output.
@@ -1507,6 +1730,87 @@ int lq_gemm_w8a8_packed(const int8_t* d_A, int64_t lda, const int8_t* d_B_packed
                       d_b_scale, b_scale_stride, d_a_zero_point, d_b_zero_point, d_b_sums, d_bias,
                       d_out_scale, d_out_zero_point, out_qmin, out_qmax, out_kind, flags, d_workspace,
                       workspace_bytes, stream);
+}
+
+int lq_dynamic_linear_packed_f32(const float* d_x, int64_t ldx, const float* d_res, int64_t ldres, float* d_sum,
+                                 int64_t ld_sum, int src, const float* d_gamma, const float* d_beta, float ln_eps,
+                                 int64_t M, int64_t K, int qmin, int qmax, float eps, float* d_qparams,
+                                 const int8_t* d_w_packed, const float* d_w_scale, const int32_t* d_w_sums,
+                                 const float* d_bias, int64_t N, float* d_y, int64_t ldy, int flags, void* stream) {
+    const char* fn = "lq_dynamic_linear_packed_f32";
+    LQ_REQUIRE(src == DL_PLAIN || src == DL_LN || src == DL_ADD_LN, std::string(fn) + ": bad src");
+    LQ_REQUIRE(M >= 1 && N >= 1 && K >= 16 && ldx >= K && ldy >= N, std::string(fn) + ": bad shape");
+    LQ_REQUIRE(d_x && d_w_packed && d_w_scale && d_w_sums && d_y, std::string(fn) + ": NULL pointer");
+    LQ_REQUIRE(src != DL_ADD_LN || (d_res && ldres >= K), std::string(fn) + ": DL_ADD_LN needs res");
+    LQ_REQUIRE(!d_sum || (src == DL_ADD_LN && ld_sum >= K), std::string(fn) + ": sum only with DL_ADD_LN");
+    LQ_REQUIRE(0 <= qmin && qmin < qmax && qmax <= 255, std::string(fn) + ": an unsigned 8-bit grid expected");
+    LQ_REQUIRE((flags & ~LQ_EPI_GELU) == 0, std::string(fn) + ": flags other than LQ_EPI_GELU");
+    if (M > 16 || K % 16 != 0 || M * K > DL_MAX_MK || (src != DL_PLAIN && (K > DL_MAX_K_LN || M * K > DL_MAX_MK_LN)))
+        return set_error(LQ_ERR_UNSUPPORTED, std::string(fn) + ": outside the one-launch sizes (M <= 16, K % 16 == 0, "
+                                                           "M K <= 16384, with a norm K <= 2048 and M K <= 8192)");
+    if (src == DL_PLAIN && (ldx % 4 != 0 || (reinterpret_cast<uintptr_t>(d_x) & 15) != 0))
+        return set_error(LQ_ERR_UNSUPPORTED, std::string(fn) + ": x rows must be 16-byte aligned");
+    GemmArgs a{};
+    a.B = d_w_packed;
+    a.C = d_y;
+    a.ldc = ldy;
+    a.M = (int)M;
+    a.N = (int)N;
+    a.K = (int)K;
+    a.b_scale = d_w_scale;
+    a.b_stride = 1;
+    a.b_sums = d_w_sums;
+    a.bias = d_bias;
+    a.out_kind = LQ_OUT_F32;
+    a.gelu = (flags & LQ_EPI_GELU) != 0;
+    a.a_u8s8 = 1;
+    a.splits = 1;
+    DynLinArgs dl;
+    dl.x = d_x;
+    dl.ldx = ldx;
+    dl.res = d_res;
+    dl.ldres = ldres;
+    dl.sum = d_sum;
+    dl.ldsum = ld_sum;
+    dl.gamma = d_gamma;
+    dl.beta = d_beta;
+    dl.ln_eps = ln_eps;
+    dl.qmin = qmin;
+    dl.eps = eps;
+    dl.width_f = (float)(qmax - qmin);
+    dl.g = make_grid(qmin, qmax);
+    dl.qp = d_qparams;
+    const int KS = (int)((K + 63) / 64);
+    dl.KP = KS * 64 + 16;
+    const size_t lds = (size_t)((M * dl.KP + 15) & ~15) + (src == DL_PLAIN ? 0 : (size_t)4 * M * K);
+    const int64_t tiles = (N + 15) / 16;
+    const bool wt = tiles >= DL_WT_MIN_TILES;
+    const dim3 grid((unsigned)(wt ? (tiles + 3) / 4 : tiles)), block(256);
+    const hipStream_t st = as_stream(stream);
+    auto go = [&](auto src_c, auto wt_c, auto maxc_c, auto rpw_c) {
+        constexpr int S = decltype(src_c)::value, C = decltype(maxc_c)::value, R = decltype(rpw_c)::value;
+        constexpr bool W = decltype(wt_c)::value;
+        hipLaunchKernelGGL((dyn_linear_skinny_kernel<S, W, C, R, LQ_OUT_F32>), grid, block, lds, st, dl, a);
+    };
+    auto by_src = [&](auto wt_c) {
+        using I = std::integral_constant<int, 1>;
+        using I2 = std::integral_constant<int, 2>;
+        using I4 = std::integral_constant<int, 4>;
+        using I8 = std::integral_constant<int, 8>;
+        // (chunks per lane, rows per wave): M <= 16, and M K <= 8192 keeps M <= 7 past K = 1024
+        auto normed = [&](auto src_c) {
+            if (K <= 2 * 4 * LN_T) go(src_c, wt_c, I2{}, I4{});
+            else if (K <= 4 * 4 * LN_T) go(src_c, wt_c, I4{}, I4{});
+            else go(src_c, wt_c, I8{}, I2{});
+        };
+        if (src == DL_PLAIN) go(std::integral_constant<int, DL_PLAIN>{}, wt_c, I{}, I{});
+        else if (src == DL_LN) normed(std::integral_constant<int, DL_LN>{});
+        else normed(std::integral_constant<int, DL_ADD_LN>{});
+    };
+    if (wt) by_src(std::true_type{});
+    else by_src(std::false_type{});
+    note_path(wt ? "dynamic linear one launch, wave tiles" : "dynamic linear one launch, split k");
+    return launch_status(fn);
 }
 
 }  // extern "C"

@@ -48,21 +48,27 @@ __global__ __launch_bounds__(256) void embedding_sum_kernel(const float* __restr
 }
 
 // y = (x - mean) / sqrt(var + eps) [* gamma + beta]: mean and biased variance in float32, one
-// workgroup of LN_T threads per row in ln_row's order (the order the fused norm + quantize
-// uses).  RES: the row is first replaced by x + res (the residual add, one rounding per
+// wave per row in ln_load / ln_norm's order (the order of every fused norm), four rows per
+// workgroup.  RES: the row is first replaced by x + res (the residual add, one rounding per
 // element), and the norm runs on the sums: the same bits as a separate add followed by the
-// norm, one launch instead of two.
-template <int MAXC, bool CACHED>
-__global__ __launch_bounds__(LN_T) void layer_norm_kernel(float* x, int64_t ldx, const float* __restrict__ res,
-                                                          int64_t ldres, float* __restrict__ y, int64_t ldy,
-                                                          int64_t rows, int64_t D, const float* __restrict__ gamma,
-                                                          const float* __restrict__ beta, float eps) {
-    __shared__ float part[2];
-    const int64_t r = blockIdx.x;
-    if (r >= rows) return;
-    float v[4 * MAXC];
-    ln_row<MAXC, CACHED>(x + r * ldx, res ? res + r * ldres : nullptr, true, (int)D, threadIdx.x, gamma, beta, eps, v,
-                         part, y + r * ldy);
+// norm, one launch instead of two.  MAXC 0: rows too wide for registers (ln_row_wide).
+constexpr int LN_ROWS_PER_WG = 4;
+template <int MAXC>
+__global__ __launch_bounds__(LN_T * LN_ROWS_PER_WG) void layer_norm_kernel(
+    float* x, int64_t ldx, const float* __restrict__ res, int64_t ldres, float* y, int64_t ldy, int64_t rows,
+    int64_t D, const float* __restrict__ gamma, const float* __restrict__ beta, float eps) {
+    const int64_t r = (int64_t)blockIdx.x * LN_ROWS_PER_WG + (threadIdx.x / LN_T);
+    const int t = threadIdx.x % LN_T;
+    if (r >= rows) return;  // a whole wave: no barrier follows
+    float* xr = x + r * ldx;
+    const float* rr = res ? res + r * ldres : nullptr;
+    if constexpr (MAXC == 0) {
+        ln_row_wide(xr, rr, true, (int)D, t, gamma, beta, eps, y + r * ldy);
+    } else {
+        float v[4 * MAXC];
+        ln_load<MAXC>(xr, rr, xr, true, (int)D, t, v);
+        ln_norm<MAXC>(v, true, (int)D, t, gamma, beta, eps, y + r * ldy);
+    }
 }
 
 // gelu, tanh form: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3)))
@@ -480,13 +486,16 @@ int lq_embedding_sum_f32(const float* d_tok_table, int64_t vocab, const float* d
 static int launch_layer_norm(float* x, int64_t ldx, const float* res, int64_t ldres, float* y, int64_t ldy,
                              int64_t rows, int64_t D, const float* gamma, const float* beta, float eps,
                              hipStream_t st) {
-    const dim3 grid((unsigned)rows), block(LN_T);
-    if (D <= 4 * LN_T) hipLaunchKernelGGL((layer_norm_kernel<1, true>), grid, block, 0, st, x, ldx, res, ldres, y, ldy,
-                                          rows, D, gamma, beta, eps);
-    else if (D <= 16 * LN_T) hipLaunchKernelGGL((layer_norm_kernel<4, true>), grid, block, 0, st, x, ldx, res, ldres,
-                                                y, ldy, rows, D, gamma, beta, eps);
-    else hipLaunchKernelGGL((layer_norm_kernel<1, false>), grid, block, 0, st, x, ldx, res, ldres, y, ldy, rows, D,
-                            gamma, beta, eps);
+    const dim3 grid((unsigned)((rows + LN_ROWS_PER_WG - 1) / LN_ROWS_PER_WG)), block(LN_T * LN_ROWS_PER_WG);
+    auto go = [&](auto c) {
+        hipLaunchKernelGGL((layer_norm_kernel<decltype(c)::value>), grid, block, 0, st, x, ldx, res, ldres, y, ldy,
+                           rows, D, gamma, beta, eps);
+    };
+    if (D <= 4 * LN_T) go(std::integral_constant<int, 1>{});
+    else if (D <= 8 * LN_T) go(std::integral_constant<int, 2>{});
+    else if (D <= 16 * LN_T) go(std::integral_constant<int, 4>{});
+    else if (D <= 32 * LN_T) go(std::integral_constant<int, 8>{});
+    else go(std::integral_constant<int, 0>{});
     return LQ_OK;
 }
 

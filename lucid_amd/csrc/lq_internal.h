@@ -110,84 +110,189 @@ __device__ __forceinline__ float gelu_tanh_f32(float v) {
     return 0.5f * v * (1.0f + tanhf(u));
 }
 
-// Layer norm of one row by a group of LN_T threads (two waves), in one fixed order shared by
-// the standalone norm (lq_layer_norm_f32) and the norm fused into a dynamic quantize, so the
-// two give the same bits: thread t owns the 4-element chunks c = t, t + LN_T, ... of the row
-// (elements 4c .. 4c + 3 below D); the row sum adds each thread's elements in index order,
-// then a shuffle tree over each wave, then the two wave sums in order; the variance sums the
-// squared deviations the same way.  CACHED keeps the thread's (at most 4 MAXC) values in
-// registers between the passes, otherwise they are read again from x.  Every thread of the
-// workgroup calls it (it holds barriers); `act` says whether this thread's row exists.  On
-// return v[] holds the normalized values of the thread's chunks (CACHED), and the row of x
-// holds x + res (res given).  part: 2 floats of LDS per row slot.
-constexpr int LN_T = 128;
+// Layer norm of one row by one wave (LN_T lanes), in one fixed order shared by every kernel
+// that normalizes -- the standalone lq_layer_norm_f32 / lq_add_layer_norm_f32, the norm fused
+// into a dynamic quantize, the norm folded into a one-launch dynamic Linear -- so all give the
+// same bits: lane t owns the 4-element chunks c = t, t + LN_T, ... of the row (elements
+// 4c .. 4c + 3 below D); the row sum adds a lane's elements in index order, then a shuffle
+// tree over the wave; the variance sums the squared deviations the same way;
+// inv = 1 / sqrt(var + eps) and y = ((v - mean) inv) gamma + beta.  A wave owns its row: no
+// barrier, so rows in flight are limited only by registers.
+constexpr int LN_T = 64;
 
-template <int MAXC, bool CACHED>
-__device__ __forceinline__ void ln_row(float* xr, const float* rr, bool act, int D, int t, const float* gamma,
-                                       const float* beta, float eps, float (&v)[4 * MAXC], float* part,
-                                       float* y) {
-    const int lane = t & 63, w = t >> 6;
-    const int nch = (D + 3) >> 2;
-    auto elem = [&](int j, int e) -> float {  // the current value of chunk j, element e
-        if constexpr (CACHED) return v[4 * j + e];
-        else return xr[4 * (t + LN_T * j) + e];
-    };
-    // the residual add, written back (each element by the thread that reads it again)
-    if constexpr (CACHED) {
+// The values of a row into v (MAXC chunks per lane) and, with res, its residual terms into rv;
+// positions past D, and every position of a row that is not `act`, hold 0.  Loads only, so a
+// caller can have several rows in flight before ln_add_store.
+template <int MAXC>
+__device__ __forceinline__ void ln_fetch(const float* xr, const float* rr, bool act, int D, int t,
+                                         float (&v)[4 * MAXC], float (&rv)[4 * MAXC]) {
+    // whole 16-byte chunks when D % 4 == 0 and the rows are 16-byte aligned
+    const bool vec = (D & 3) == 0 && ((reinterpret_cast<uintptr_t>(xr) | reinterpret_cast<uintptr_t>(rr)) & 15) == 0;
+    if (vec) {
+#pragma unroll
+        for (int j = 0; j < MAXC; ++j) {
+            const int idx = 4 * (t + LN_T * j);
+            const bool in = act && idx < D;
+            const vf4 a = in ? *reinterpret_cast<const vf4*>(xr + idx) : vf4{0.0f, 0.0f, 0.0f, 0.0f};
+            const vf4 b = (in && rr) ? *reinterpret_cast<const vf4*>(rr + idx) : vf4{0.0f, 0.0f, 0.0f, 0.0f};
+            v[4 * j] = a.x, v[4 * j + 1] = a.y, v[4 * j + 2] = a.z, v[4 * j + 3] = a.w;
+            rv[4 * j] = b.x, rv[4 * j + 1] = b.y, rv[4 * j + 2] = b.z, rv[4 * j + 3] = b.w;
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int idx = 4 * (t + LN_T * j) + e;
+            const bool in = act && idx < D;
+            v[4 * j + e] = in ? xr[idx] : 0.0f;
+            rv[4 * j + e] = (in && rr) ? rr[idx] : 0.0f;
+        }
+}
+
+// v = x + res (has_res), stored to wb when it is not NULL (the row of x itself for the in-place
+// callers: every load of the row came first).
+template <int MAXC>
+__device__ __forceinline__ void ln_add_store(float (&v)[4 * MAXC], const float (&rv)[4 * MAXC], bool has_res,
+                                             float* wb, bool act, int D, int t) {
+    if (!has_res) return;
+#pragma unroll
+    for (int k = 0; k < 4 * MAXC; ++k) v[k] = v[k] + rv[k];
+    if (wb && act) {
 #pragma unroll
         for (int j = 0; j < MAXC; ++j)
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const int idx = 4 * (t + LN_T * j) + e;
-                float a = 0.0f;
-                if (act && idx < D) {
-                    a = xr[idx];
-                    if (rr) {
-                        a = a + rr[idx];
-                        xr[idx] = a;
-                    }
-                }
-                v[4 * j + e] = a;
+                if (idx < D) wb[idx] = v[4 * j + e];
             }
-    } else if (rr && act) {
+    }
+}
+
+template <int MAXC>
+__device__ __forceinline__ void ln_load(const float* xr, const float* rr, float* wb, bool act, int D, int t,
+                                        float (&v)[4 * MAXC]) {
+    float rv[4 * MAXC];
+    ln_fetch<MAXC>(xr, rr, act, D, t, v, rv);
+    ln_add_store<MAXC>(v, rv, rr != nullptr, wb, act, D, t);
+}
+
+// Sum over the 64 lanes of a wave, the same value in every lane: partners at lane distance 1
+// and 2 (quad permutes), then the mirrored lane of each 8 and of each 16 (DPP row mirrors),
+// then the lane 16 and 32 away (permlane swaps) -- each step adds two partial sums that every
+// lane of the pair holds, so all lanes add the same values in the same order.  Register
+// permutes only: no LDS round trip per step.
+__device__ __forceinline__ float dpp_add(float s, int ctrl_sel) {
+    int b = __float_as_int(s), o;
+    switch (ctrl_sel) {  // the DPP control must be a constant
+    case 0: o = __builtin_amdgcn_update_dpp(b, b, 0xB1, 0xF, 0xF, true); break;   // quad_perm [1,0,3,2]
+    case 1: o = __builtin_amdgcn_update_dpp(b, b, 0x4E, 0xF, 0xF, true); break;   // quad_perm [2,3,0,1]
+    case 2: o = __builtin_amdgcn_update_dpp(b, b, 0x141, 0xF, 0xF, true); break;  // row_half_mirror
+    default: o = __builtin_amdgcn_update_dpp(b, b, 0x140, 0xF, 0xF, true); break; // row_mirror
+    }
+    return s + __int_as_float(o);
+}
+__device__ __forceinline__ float ln_wave_sum(float s) {
+    s = dpp_add(s, 0);
+    s = dpp_add(s, 1);
+    s = dpp_add(s, 2);
+    s = dpp_add(s, 3);
+    const int lane = __lane_id();
+    const uint32_t b = __float_as_uint(s);
+    auto p16 = __builtin_amdgcn_permlane16_swap(b, b, false, false);
+    s = s + __uint_as_float(((lane >> 4) & 1) ? p16[0] : p16[1]);
+    const uint32_t c = __float_as_uint(s);
+    auto p32 = __builtin_amdgcn_permlane32_swap(c, c, false, false);
+    s = s + __uint_as_float(lane >= 32 ? p32[0] : p32[1]);
+    return s;
+}
+
+// Normalizes the values ln_load left in v, in place, and stores them to y (when not NULL and
+// the row is `act`).  Every lane of the wave calls it (the sums are shuffles).
+template <int MAXC>
+__device__ __forceinline__ void ln_norm(float (&v)[4 * MAXC], bool act, int D, int t, const float* gamma,
+                                        const float* beta, float eps, float* y) {
+    float gv[4 * MAXC], bv[4 * MAXC];  // the affine terms, loaded under the reductions
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int idx = 4 * (t + LN_T * j) + e;
+            const bool in = act && idx < D;
+            gv[4 * j + e] = (in && gamma) ? gamma[idx] : 1.0f;
+            bv[4 * j + e] = (in && beta) ? beta[idx] : 0.0f;
+        }
+    float s = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (4 * (t + LN_T * j) + e < D) s += v[4 * j + e];
+    const float mean = ln_wave_sum(s) / (float)D;
+    float q = 0.0f;
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            if (4 * (t + LN_T * j) + e < D) {
+                const float c = v[4 * j + e] - mean;
+                q += c * c;
+            }
+    const float var = ln_wave_sum(q) / (float)D;
+    const float inv = 1.0f / sqrtf(var + eps);
+    if (!act) return;
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int idx = 4 * (t + LN_T * j) + e;
+            if (idx < D) {
+                float a = (v[4 * j + e] - mean) * inv;
+                if (gamma) a = a * gv[4 * j + e];
+                if (beta) a = a + bv[4 * j + e];
+                v[4 * j + e] = a;
+                if (y) y[idx] = a;
+            }
+        }
+}
+
+// A row too wide for registers: the same order, read from memory on each pass; x + res is
+// stored into the row itself first (in place).
+__device__ __forceinline__ void ln_row_wide(float* xr, const float* rr, bool act, int D, int t, const float* gamma,
+                                            const float* beta, float eps, float* y) {
+    const int nch = (D + 3) >> 2;
+    if (rr && act)
         for (int c = t; c < nch; c += LN_T)
             for (int e = 0; e < 4; ++e) {
                 const int idx = 4 * c + e;
                 if (idx < D) xr[idx] = xr[idx] + rr[idx];
             }
-    }
-    const int jn = CACHED ? MAXC : (nch + LN_T - 1) / LN_T;
-    auto row_sum = [&](auto term) -> float {
-        float s = 0.0f;
-        if (act)
-            for (int j = 0; j < jn; ++j)
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    if (4 * (t + LN_T * j) + e < D) s += term(elem(j, e));
-        for (int off = 32; off > 0; off >>= 1) s += __shfl_xor(s, off, 64);
-        if (lane == 0) part[w] = s;
-        __syncthreads();
-        const float tot = part[0] + part[1];
-        __syncthreads();
-        return tot;
-    };
-    const float mean = row_sum([](float a) { return a; }) / (float)D;
-    const float var = row_sum([&](float a) {
-                          const float c = a - mean;
-                          return c * c;
-                      }) / (float)D;
+    float s = 0.0f;
+    if (act)
+        for (int c = t; c < nch; c += LN_T)
+            for (int e = 0; e < 4; ++e)
+                if (4 * c + e < D) s += xr[4 * c + e];
+    const float mean = ln_wave_sum(s) / (float)D;
+    float q = 0.0f;
+    if (act)
+        for (int c = t; c < nch; c += LN_T)
+            for (int e = 0; e < 4; ++e)
+                if (4 * c + e < D) {
+                    const float d = xr[4 * c + e] - mean;
+                    q += d * d;
+                }
+    const float var = ln_wave_sum(q) / (float)D;
     const float inv = 1.0f / sqrtf(var + eps);
     if (!act) return;
-    for (int j = 0; j < jn; ++j)
-#pragma unroll
+    for (int c = t; c < nch; c += LN_T)
         for (int e = 0; e < 4; ++e) {
-            const int idx = 4 * (t + LN_T * j) + e;
+            const int idx = 4 * c + e;
             if (idx < D) {
-                float a = (elem(j, e) - mean) * inv;
+                float a = (xr[idx] - mean) * inv;
                 if (gamma) a = a * gamma[idx];
                 if (beta) a = a + beta[idx];
-                if constexpr (CACHED) v[4 * j + e] = a;
-                if (y) y[idx] = a;
+                y[idx] = a;
             }
         }
 }
@@ -319,6 +424,50 @@ __device__ __forceinline__ float extreme_min(float a, float b) {
 __device__ __forceinline__ float extreme_max(float a, float b) {
     if (a != a || b != b) return __int_as_float(0x7fc00000);
     return unkey(max(fkey(a), fkey(b)));
+}
+
+__device__ __forceinline__ void key_accum(int32_t& kmin, int32_t& kmax, float v) {
+    int32_t k = fkey(v);
+    kmin = min(kmin, k);
+    kmax = max(kmax, k);
+}
+
+// Extrema back from their keys; NaN for both when a NaN was seen (a key outside the range
+// of ordered floats).
+__device__ __forceinline__ void decode_keys(int32_t kmin, int32_t kmax, float& mn, float& mx) {
+    if (kmax > KEY_POS_INF || kmin < KEY_NEG_INF) {
+        mn = mx = __int_as_float(0x7fc00000);
+    } else {
+        mn = unkey(kmin);
+        mx = unkey(kmax);
+    }
+}
+
+// Code of x on grid g as a float: clip(rne(x * inv) + z) (the quantize formula).
+template <class Code>
+__device__ __forceinline__ float quant_one(float x, float inv, float z, const Grid& g) {
+    float t = x * inv;
+    float r = rne(t);
+    float u = r + z;
+    return clip_grid(u, g);
+}
+
+// Per-tensor affine qparams of a dynamic input from the keys of its extrema (the observer's
+// min / max, then calculate_qparams on the grid of width width_f = qmax - qmin):
+// out = {min, max, scale, zero point}.
+__device__ __forceinline__ void dyn_qparams(int32_t kmin, int32_t kmax, int qmin, float eps, float width_f,
+                                            const Grid& g, float (&out)[4]) {
+    float cmin, cmax;
+    decode_keys(kmin, kmax, cmin, cmax);
+    const float mn = extreme_min(cmin, 0.0f), mx = extreme_max(cmax, 0.0f);
+    const float wd = mx - mn;
+    const float qq = wd / width_f;
+    const float sc = extreme_max(qq, eps);
+    const float r = rne(mn / sc);
+    out[0] = cmin;
+    out[1] = cmax;
+    out[2] = sc;
+    out[3] = clip_grid((float)qmin - r, g);
 }
 
 // Wave64 reductions over int32.

@@ -44,11 +44,6 @@ struct PtParams {
 
 // ----------------------------------------------------------------- observers
 
-__device__ __forceinline__ void key_accum(int32_t& kmin, int32_t& kmax, float v) {
-    int32_t k = fkey(v);
-    kmin = min(kmin, k);
-    kmax = max(kmax, k);
-}
 
 // Block-wide min/max of keys; result valid in thread 0.
 __device__ __forceinline__ void block_reduce_keys(int32_t& kmin, int32_t& kmax) {
@@ -113,14 +108,6 @@ __global__ __launch_bounds__(kBlock) void minmax_partial_kernel(const float* __r
 }
 
 // Decode an extrema key pair: NaN in the data (keyed outside [-inf, +inf]) makes both NaN.
-__device__ __forceinline__ void decode_keys(int32_t kmin, int32_t kmax, float& mn, float& mx) {
-    if (kmax > KEY_POS_INF || kmin < KEY_NEG_INF) {
-        mn = mx = __int_as_float(0x7fc00000);
-    } else {
-        mn = unkey(kmin);
-        mx = unkey(kmax);
-    }
-}
 
 // Fold batch extrema into a running pair by mode (observer.py:408-414, 527-544).
 __device__ __forceinline__ void fold_running(float& rmin, float& rmax, float cmin, float cmax,
@@ -335,13 +322,6 @@ struct CodeVec {
     typename Code::T v[N];
 };
 
-template <class Code>
-__device__ __forceinline__ float quant_one(float x, float inv, float z, const Grid& g) {
-    float t = x * inv;
-    float r = rne(t);
-    float u = r + z;
-    return clip_grid(u, g);
-}
 
 template <class Code>
 __device__ __forceinline__ void store16(typename Code::T* dst, const float* c) {
@@ -904,20 +884,14 @@ __global__ __launch_bounds__(kDynBlock) void dyn_quant_small_kernel(const float*
             kmin = min(kmin, smin[w]);
             kmax = max(kmax, smax[w]);
         }
-        float cmin, cmax;
-        decode_keys(kmin, kmax, cmin, cmax);
-        qp[0] = cmin;
-        qp[1] = cmax;
-        const float mn = extreme_min(cmin, 0.0f), mx = extreme_max(cmax, 0.0f);
-        const float w = mx - mn;
-        const float qq = w / width_f;
-        const float sc = extreme_max(qq, eps);
-        const float r = rne(mn / sc);
-        const float z = clip_grid((float)qmin - r, g);
-        qp[2] = sc;
-        qp[3] = z;
-        s_sz[0] = sc;
-        s_sz[1] = z;
+        float o[4];
+        dyn_qparams(kmin, kmax, qmin, eps, width_f, g, o);
+        qp[0] = o[0];
+        qp[1] = o[1];
+        qp[2] = o[2];
+        qp[3] = o[3];
+        s_sz[0] = o[2];
+        s_sz[1] = o[3];
     }
     __syncthreads();
     const float sc = s_sz[0], z = s_sz[1];
@@ -937,14 +911,29 @@ struct DynQuantSmall {
 
 // The same step with the input produced in the launch: the layer norm of `rows` rows of D
 // (optionally after the residual add x += res, written back), as lq_layer_norm_f32 /
-// lq_add_layer_norm_f32 compute it -- ln_row, eight rows at a time on the workgroup's 1024
-// threads -- so the codes and qparams are the bits of that call followed by
-// lq_dynamic_quantize_f32.  The normalized rows wait in LDS.  (A GELU before the quantize
-// belongs in the producing GEMM's epilogue instead, LQ_EPI_GELU: one workgroup evaluating
-// tanh for a whole FFN row block was slower than the separate launches.)
+// lq_add_layer_norm_f32 compute it -- one wave per row (ln_load / ln_norm, or ln_row_wide),
+// sixteen rows at a time on the workgroup's 1024 threads -- so the codes and qparams are the
+// bits of that call followed by lq_dynamic_quantize_f32.  The normalized rows wait in LDS.
+// (A GELU before the quantize belongs in the producing GEMM's epilogue instead, LQ_EPI_GELU.)
 enum { DQ_LN = 2, DQ_LN_RES = 3 };
 constexpr int64_t DQ_LN_MAX = 12288;  // normalized values held in LDS (48 KB)
-constexpr int DQ_LN_MAXD = 16 * LN_T;  // widest row kept in registers by ln_row<4>
+
+template <int MAXC>
+__device__ __forceinline__ void dq_norm_rows(float* x, int64_t ldx, const float* res, int64_t ldres, int rows,
+                                             int D, const float* gamma, const float* beta, float ln_eps, float* ys) {
+    const int wave = threadIdx.x / LN_T, t = threadIdx.x % LN_T;
+    for (int r = wave; r < rows; r += kDynBlock / LN_T) {
+        float* xr = x + (int64_t)r * ldx;
+        const float* rr = res ? res + (int64_t)r * ldres : nullptr;
+        if constexpr (MAXC == 0) {
+            ln_row_wide(xr, rr, true, D, t, gamma, beta, ln_eps, ys + r * D);
+        } else {
+            float v[4 * MAXC];
+            ln_load<MAXC>(xr, rr, xr, true, D, t, v);
+            ln_norm<MAXC>(v, true, D, t, gamma, beta, ln_eps, ys + r * D);
+        }
+    }
+}
 
 template <class Code, int SRC>
 __global__ __launch_bounds__(kDynBlock) void dyn_quant_fused_kernel(float* x, int64_t ldx, const float* res,
@@ -955,28 +944,15 @@ __global__ __launch_bounds__(kDynBlock) void dyn_quant_fused_kernel(float* x, in
                                                                     float* __restrict__ qp, int qmin, float eps,
                                                                     float width_f, Grid g) {
     extern __shared__ float ys[];
-    __shared__ float part[kDynBlock / LN_T][2];
     __shared__ int32_t smin[kDynBlock / 64], smax[kDynBlock / 64];
     __shared__ float s_sz[2];
     const int tid = threadIdx.x;
     const int n = rows * D;
-    {
-        const int slot = tid / LN_T, t = tid % LN_T;
-        for (int r0 = 0; r0 < rows; r0 += kDynBlock / LN_T) {
-            const int r = r0 + slot;
-            const bool act = r < rows;
-            float* xr = x + (int64_t)(act ? r : 0) * ldx;
-            const float* rr = SRC == DQ_LN_RES ? res + (int64_t)(act ? r : 0) * ldres : nullptr;
-            if (D <= DQ_LN_MAXD) {
-                float v[16];
-                ln_row<4, true>(xr, rr, act, D, t, gamma, beta, ln_eps, v, part[slot], ys + (act ? r : 0) * D);
-            } else {  // wider rows are read from HBM again, as the standalone kernel does
-                float v[4];
-                ln_row<1, false>(xr, rr, act, D, t, gamma, beta, ln_eps, v, part[slot], ys + (act ? r : 0) * D);
-            }
-        }
-        __syncthreads();
-    }
+    const float* rs = SRC == DQ_LN_RES ? res : nullptr;
+    if (D <= 8 * LN_T) dq_norm_rows<2>(x, ldx, rs, ldres, rows, D, gamma, beta, ln_eps, ys);
+    else if (D <= 32 * LN_T) dq_norm_rows<8>(x, ldx, rs, ldres, rows, D, gamma, beta, ln_eps, ys);
+    else dq_norm_rows<0>(x, ldx, rs, ldres, rows, D, gamma, beta, ln_eps, ys);
+    __syncthreads();
     auto val = [&](int i) -> float { return ys[i]; };
     int32_t kmin = KEY_POS_INF, kmax = KEY_NEG_INF;
     for (int i = tid; i < n; i += kDynBlock) key_accum(kmin, kmax, val(i));
@@ -992,20 +968,14 @@ __global__ __launch_bounds__(kDynBlock) void dyn_quant_fused_kernel(float* x, in
             kmin = min(kmin, smin[w]);
             kmax = max(kmax, smax[w]);
         }
-        float cmin, cmax;
-        decode_keys(kmin, kmax, cmin, cmax);
-        qp[0] = cmin;
-        qp[1] = cmax;
-        const float mn = extreme_min(cmin, 0.0f), mx = extreme_max(cmax, 0.0f);
-        const float wd = mx - mn;
-        const float qq = wd / width_f;
-        const float sc = extreme_max(qq, eps);
-        const float r = rne(mn / sc);
-        const float z = clip_grid((float)qmin - r, g);
-        qp[2] = sc;
-        qp[3] = z;
-        s_sz[0] = sc;
-        s_sz[1] = z;
+        float o[4];
+        dyn_qparams(kmin, kmax, qmin, eps, width_f, g, o);
+        qp[0] = o[0];
+        qp[1] = o[1];
+        qp[2] = o[2];
+        qp[3] = o[3];
+        s_sz[0] = o[2];
+        s_sz[1] = o[3];
     }
     __syncthreads();
     const float sc = s_sz[0], z = s_sz[1];

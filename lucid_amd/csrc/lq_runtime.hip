@@ -234,6 +234,26 @@ __global__ void lq_fill_u32_kernel(uint32_t* __restrict__ dst, uint32_t value, s
     for (; i < count; i += stride) dst[i] = value;
 }
 
+// The streaming-read floor: every 16-byte chunk of src loaded once (4 per thread, 64 B
+// apart in a wave's 1 KB-per-load pattern), XOR-folded, and written only if it equals a value
+// the caller chooses never to match -- so the loads stay and nothing is stored.
+constexpr int RF_THREADS = 256, RF_PER = 4;
+typedef uint32_t rf_u32x4 __attribute__((ext_vector_type(4)));
+__global__ __launch_bounds__(RF_THREADS) void lq_read_floor_kernel(const rf_u32x4* __restrict__ src, size_t n16,
+                                                                    uint32_t never, uint32_t* sink) {
+    const size_t base = (size_t)blockIdx.x * RF_THREADS * RF_PER + threadIdx.x;
+    uint32_t acc = 0;
+#pragma unroll
+    for (int u = 0; u < RF_PER; ++u) {
+        const size_t i = base + (size_t)u * RF_THREADS;
+        if (i < n16) {
+            const rf_u32x4 v = __builtin_nontemporal_load(src + i);
+            acc ^= v.x ^ v.y ^ v.z ^ v.w;
+        }
+    }
+    if (acc == never) sink[threadIdx.x] = acc;
+}
+
 namespace lq {
 // A captured graph and its executable form, owned together by an lq_graph_* handle.
 struct CapturedGraph {
@@ -252,6 +272,19 @@ int lq_fill_u32(void* d_dst, uint32_t value, size_t count, void* stream) {
     hipLaunchKernelGGL(lq_fill_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, as_stream(stream),
                        (uint32_t*)d_dst, value, count);
     return launch_status("lq_fill_u32");
+}
+
+int lq_read_floor(const void* d_src, size_t bytes, uint32_t never, uint32_t* d_sink, void* stream) {
+    if (bytes == 0) return LQ_OK;
+    LQ_REQUIRE(d_src && d_sink, "lq_read_floor: NULL pointer");
+    LQ_REQUIRE(bytes % 16 == 0 && ((uintptr_t)d_src & 15) == 0,
+               "lq_read_floor: bytes and the source address must be multiples of 16");
+    const size_t n16 = bytes / 16, per = (size_t)RF_THREADS * RF_PER;
+    const size_t blocks = (n16 + per - 1) / per;
+    LQ_REQUIRE(blocks <= 0x7fffffff, "lq_read_floor: too many bytes for one launch");
+    hipLaunchKernelGGL(lq_read_floor_kernel, dim3((unsigned)blocks), dim3(RF_THREADS), 0, as_stream(stream),
+                       (const rf_u32x4*)d_src, n16, never, d_sink);
+    return launch_status("lq_read_floor");
 }
 
 int lq_stream_create(void** stream) {

@@ -29,7 +29,7 @@ from lucid_amd.quantization._qscheme import QDtype, per_channel_symmetric, qint8
 class _DynamicGates:
     """``x W^T + b`` with the int8 weight and its row scales (weight-only GEMV)."""
 
-    def _gates(self, name: str, x_ptr: int, ldx: int, M: int, K: int, y_ptr: int) -> None:
+    def _gates(self, name: str, x_ptr: int, ldx: int, M: int, K: int, y_ptr: int, ldy: int = 0) -> None:
         codes = self._buffers[f"weight_{name}_int8"]
         if codes.device != "gpu":
             codes = codes.to("gpu")
@@ -41,7 +41,7 @@ class _DynamicGates:
         self._alive = (scale, b)
         wsb = _C.lib().lq_gemv_w8_workspace_size(M, N, K)
         _C.call("lq_gemv_w8", x_ptr, _C.F32, ldx, codes.data_ptr(), K, scale.data_ptr(), None,
-                b.data_ptr() if b is not None else None, y_ptr, N, M, N, K, 0, workspace.get(wsb), wsb, None)
+                b.data_ptr() if b is not None else None, y_ptr, ldy or N, M, N, K, 0, workspace.get(wsb), wsb, None)
 
 
 def _quantize_into(qmod: Module, fmod: Module, dtype: QDtype) -> None:

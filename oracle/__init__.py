@@ -757,8 +757,9 @@ def _sig64(x):
 
 def rnn_cell(mode: str, gx: np.ndarray, gh: np.ndarray, h: np.ndarray, c=None):
     """One step from the two gate products (float64): ``mode`` RNN_TANH / RNN_RELU / LSTM
-    (gates i, f, g, o) / GRU (gates r, z, n) as lucid/nn/modules/rnn.py writes them."""
-    H = h.shape[-1]
+    (gates i, f, g, o) / GRU (gates r, z, n) as lucid/nn/modules/rnn.py writes them.  The
+    gate width sets H (a projected LSTM's h is narrower and unused here)."""
+    H = gx.shape[-1] // {"LSTM": 4, "GRU": 3}.get(mode, 1)
     if mode in ("RNN_TANH", "RNN_RELU"):
         pre = gx + gh
         return (np.tanh(pre) if mode == "RNN_TANH" else np.maximum(pre, 0.0)), None
@@ -777,27 +778,34 @@ def rnn_forward(mode: str, x: np.ndarray, weights: dict, num_layers: int = 1, bi
                 h0=None, c0=None):
     """A multi-layer (bi)directional recurrence over time-major ``x`` [T, B, I] in float64
     with ``weights[name]`` (``weight_ih_l{k}[_reverse]`` ..., biases optional): (output
-    [T, B, D H], h_n [L D, B, H], c_n or None)."""
+    [T, B, D R], h_n [L D, B, R], c_n [L D, B, H] or None).  An LSTM with ``weight_hr_l{k}``
+    [P, H] is the projected one (lucid/_C/backend/cpu/Lstm.h:90-164): the state carried and
+    emitted is h = (o tanh(c)) W_hr^T, R = P wide; otherwise R = H."""
     x = np.asarray(x, np.float64)
     T, B, _ = x.shape
     D = 2 if bidirectional else 1
-    H = weights["weight_hh_l0"].shape[1]
+    R = weights["weight_hh_l0"].shape[1]
+    Hc = weights["weight_hh_l0"].shape[0] // {"LSTM": 4, "GRU": 3}.get(mode, 1)
     h_n, c_n = [], []
     inp = x
     for layer in range(num_layers):
-        outs = np.zeros((T, B, D * H))
+        outs = np.zeros((T, B, D * R))
         for d in range(D):
             sfx = f"_l{layer}" + ("_reverse" if d else "")
             w_ih, w_hh = (np.asarray(weights[f"weight_{k}{sfx}"], np.float64) for k in ("ih", "hh"))
+            w_hr = weights.get(f"weight_hr{sfx}")
+            w_hr = None if w_hr is None else np.asarray(w_hr, np.float64)
             b_ih = np.asarray(weights.get(f"bias_ih{sfx}", np.zeros(w_ih.shape[0])), np.float64)
             b_hh = np.asarray(weights.get(f"bias_hh{sfx}", np.zeros(w_hh.shape[0])), np.float64)
             idx = layer * D + d
-            h = np.zeros((B, H)) if h0 is None else np.asarray(h0[idx], np.float64)
-            c = np.zeros((B, H)) if c0 is None else np.asarray(c0[idx], np.float64)
+            h = np.zeros((B, R)) if h0 is None else np.asarray(h0[idx], np.float64)
+            c = np.zeros((B, Hc)) if c0 is None else np.asarray(c0[idx], np.float64)
             for t in (range(T - 1, -1, -1) if d else range(T)):
                 h, cn = rnn_cell(mode, inp[t] @ w_ih.T + b_ih, h @ w_hh.T + b_hh, h, c)
+                if w_hr is not None:
+                    h = h @ w_hr.T
                 c = cn if cn is not None else c
-                outs[t, :, d * H:(d + 1) * H] = h
+                outs[t, :, d * R:(d + 1) * R] = h
             h_n.append(h)
             c_n.append(c)
         inp = outs

@@ -431,3 +431,35 @@ def test_int8_decoder_runtime(gpu, decoder_pair):
     agree = np.mean([(t == rf.argmax(-1)).mean() for t, rf in zip(toks, refs)])
     assert agree > 0.9, agree
     assert (nxt == logits0.argmax(-1)).mean() > 0.9
+
+
+def test_int8_decoder_one_launch_steps_bit_exact(gpu, decoder_pair):
+    """Decode steps whose Linears run as one launch each (norm, input step and product in
+    lq_dynamic_linear_packed_f32, the residual stream in two buffers) leave the same logits,
+    tokens and KV cache, bit for bit, as the same steps through the separate launches."""
+    import ctypes
+
+    from lucid_amd import _C
+    from lucid_amd.bench_configs import Int8Decoder
+
+    _, _, qdec, glue, tokens = decoder_pair
+    T, steps = 32, 6
+    st = ctypes.c_void_p()
+    _C.call("lq_stream_create", ctypes.byref(st))
+    out = []
+    for one in (False, True):
+        rt = Int8Decoder(qdec, glue, batch=BATCH, max_prompt=T, max_positions=T + steps, one_launch=one)
+        rt.set_prompt(tokens[:, :T])
+        rt.prefill(st)
+        rt.decode(st)  # the step's last product is the head's: its path note says which form ran
+        assert ("dynamic linear one launch" in _C.last_path()) == one
+        rt.prefill(st)
+        logits = []
+        for _ in range(steps):
+            rt.decode(st)
+            _C.call("lq_stream_synchronize", st)
+            logits.append(rt.logits.numpy().copy())
+        out.append((np.stack(logits), rt.next.numpy().copy(), rt.cache[-1][0].numpy().copy()))
+    _C.call("lq_stream_destroy", st)
+    for a, b in zip(out[0], out[1]):
+        np.testing.assert_array_equal(a.view(np.uint8), b.view(np.uint8))

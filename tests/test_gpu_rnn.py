@@ -283,3 +283,57 @@ def test_packed_sequence_recurrence(gpu, mode, layers, bidir, dynamic):
         np.testing.assert_allclose(h_n[:, b:b + 1], wh, atol=ATOL, rtol=0)
         if mode == "LSTM":
             np.testing.assert_allclose(state[1].numpy()[:, b:b + 1], wc, atol=ATOL, rtol=0)
+
+
+@pytest.mark.parametrize("layers,bidir,batch_first,packed", [(1, False, True, False), (2, True, False, False),
+                                                             (2, True, False, True), (1, False, False, True)])
+@pytest.mark.parametrize("dynamic", [False, True])
+def test_projected_lstm(gpu, layers, bidir, batch_first, packed, dynamic):
+    """LSTM with proj_size P (lucid/nn/modules/recurrent_base.py:138-192; the engine's projected
+    step, lucid/_C/backend/cpu/Lstm.h:90-164): weight_hr [P, H] after each layer's biases,
+    weight_hh [4H, P], outputs and h_n P wide, c_n H wide.  Float and dynamic int8 (weight_hr
+    quantized like every weight) against the oracle's float64 recurrence, 2e-5; dense and
+    unsorted packed input; h_n is the last step of the output (the reference's own check,
+    lucid/test/unit/nn/test_recurrent.py:54-66)."""
+    import lucid_amd.nn as nn
+    import lucid_amd.nn.quantized.dynamic as nnqd
+    from lucid_amd.nn.layers import manual_seed
+    from lucid_amd.nn.utils.rnn import pack_padded_sequence, pad_packed_sequence
+
+    manual_seed(40 + layers)
+    rng = np.random.default_rng(7 * layers + bidir)
+    T, B, I, H, P = 6, 4, 5, 12, 3
+    D = 2 if bidir else 1
+    m = nn.LSTM(I, H, num_layers=layers, bidirectional=bidir, batch_first=batch_first, proj_size=P).to("gpu")
+    names = [n for n, _ in m.named_parameters()]
+    assert names[:5] == ["weight_ih_l0", "weight_hh_l0", "bias_ih_l0", "bias_hh_l0", "weight_hr_l0"]
+    mod = nnqd.LSTM.from_float(m) if dynamic else m
+    if dynamic:
+        assert "weight_hr_l0_int8" in dict(mod.named_buffers())
+    weights = _deq_weights(mod) if dynamic else _float_weights(m)
+    x = rng.standard_normal((T, B, I)).astype(np.float32)
+    h0 = (rng.standard_normal((layers * D, B, P)) * 0.5).astype(np.float32)
+    c0 = (rng.standard_normal((layers * D, B, H)) * 0.5).astype(np.float32)
+    hx = (_dev(gpu, h0), _dev(gpu, c0))
+    if packed:
+        lens = [3, 6, 1, 5]
+        out, (h_n, c_n) = mod(pack_padded_sequence(_dev(gpu, x), lens, enforce_sorted=False), hx)
+        padded, _ = pad_packed_sequence(out)
+        got, h_n, c_n = padded.numpy(), h_n.numpy(), c_n.numpy()
+        for b, n in enumerate(lens):
+            want, wh, wc = O.rnn_forward("LSTM", x[:n, b:b + 1], weights, layers, bidir, h0[:, b:b + 1],
+                                         c0[:, b:b + 1])
+            np.testing.assert_allclose(got[:n, b:b + 1], want, atol=ATOL, rtol=0)
+            np.testing.assert_allclose(h_n[:, b:b + 1], wh, atol=ATOL, rtol=0)
+            np.testing.assert_allclose(c_n[:, b:b + 1], wc, atol=ATOL, rtol=0)
+        return
+    xin = x.transpose(1, 0, 2) if batch_first else x
+    out, (h_n, c_n) = mod(_dev(gpu, xin), hx)
+    assert tuple(out.shape) == ((B, T, D * P) if batch_first else (T, B, D * P))
+    assert tuple(h_n.shape) == (layers * D, B, P) and tuple(c_n.shape) == (layers * D, B, H)
+    got = out.numpy().transpose(1, 0, 2) if batch_first else out.numpy()
+    want, wh, wc = O.rnn_forward("LSTM", x, weights, layers, bidir, h0, c0)
+    np.testing.assert_allclose(got, want, atol=ATOL, rtol=0)
+    np.testing.assert_allclose(h_n.numpy(), wh, atol=ATOL, rtol=0)
+    np.testing.assert_allclose(c_n.numpy(), wc, atol=ATOL, rtol=0)
+    np.testing.assert_array_equal(h_n.numpy()[(layers - 1) * D], got[-1, :, :P])

@@ -403,3 +403,23 @@ def test_conv_size_arguments_refuse_wrong_lengths():
     with pytest.raises(ValueError, match="padding"):
         nnq.Conv3d(2, 2, 3, padding=(1, 1))
     assert nn.Conv3d(2, 2, 3, stride=[2]).stride == (2, 2, 2)
+
+
+def test_lstm_projection_parameters_and_refusals():
+    """proj_size registers weight_hr_l{k}[_reverse] [P, H] after each layer's biases, shrinks
+    weight_hh to [4H, P] and a deeper layer's weight_ih to [4H, D P], and is refused as the
+    reference refuses it (lucid/nn/modules/recurrent_base.py:138-145, 164-194)."""
+    import lucid_amd.nn as nn
+
+    m = nn.LSTM(4, 6, num_layers=2, bidirectional=True, proj_size=2)
+    shapes = {n: tuple(p.shape) for n, p in m.named_parameters()}
+    names = list(shapes)
+    assert names[:6] == ["weight_ih_l0", "weight_hh_l0", "bias_ih_l0", "bias_hh_l0", "weight_hr_l0",
+                         "weight_ih_l0_reverse"]
+    assert shapes["weight_hh_l0"] == (24, 2) and shapes["weight_hr_l1_reverse"] == (2, 6)
+    assert shapes["weight_ih_l1"] == (24, 4)
+    assert "proj_size=2" in repr(m)
+    assert "weight_hr_l0" not in dict(nn.LSTM(4, 6).named_parameters())
+    for bad in (6, 7, -1):
+        with pytest.raises(ValueError):
+            nn.LSTM(4, 6, proj_size=bad)

@@ -753,6 +753,57 @@ def test_rnn_forward_structure():
         np.testing.assert_allclose(o2, out)
 
 
+def test_rnn_forward_projection_reduces_to_a_plain_lstm():
+    """A projection W_hr = [I_P | 0] keeps the first P hidden units.  The projected LSTM (W_hh
+    [4H, P], layer-2 W_ih over the D P projected outputs) then equals an unprojected one whose
+    weights read only those units (zero columns elsewhere), restricted to them; c is the same
+    full-width cell state.  A projection applied to c, to the wrong side of the product, or
+    left out of the recurrent input fails it."""
+    rng = np.random.default_rng(21)
+    T, B, I, H, P, L, D = 5, 3, 4, 6, 2, 2, 2
+    x = rng.standard_normal((T, B, I))
+    sel = np.zeros((P, H))
+    sel[:, :P] = np.eye(P)
+    proj, plain = {}, {}
+    for layer in range(L):
+        for d in range(D):
+            sfx = f"_l{layer}" + ("_reverse" if d else "")
+            w_ih = rng.uniform(-0.5, 0.5, (4 * H, I if layer == 0 else D * P))
+            w_hh = rng.uniform(-0.5, 0.5, (4 * H, P))
+            proj[f"weight_ih{sfx}"], proj[f"weight_hh{sfx}"], proj[f"weight_hr{sfx}"] = w_ih, w_hh, sel
+            wide_hh = np.zeros((4 * H, H))
+            wide_hh[:, :P] = w_hh
+            if layer == 0:
+                wide_ih = w_ih
+            else:
+                wide_ih = np.zeros((4 * H, D * H))
+                for dd in range(D):
+                    wide_ih[:, dd * H:dd * H + P] = w_ih[:, dd * P:(dd + 1) * P]
+            plain[f"weight_ih{sfx}"], plain[f"weight_hh{sfx}"] = wide_ih, wide_hh
+            for k in ("bias_ih", "bias_hh"):
+                proj[k + sfx] = plain[k + sfx] = rng.uniform(-0.5, 0.5, 4 * H)
+    h0 = rng.standard_normal((L * D, B, P)) * 0.5
+    h0w = np.zeros((L * D, B, H))
+    h0w[:, :, :P] = h0
+    c0 = rng.standard_normal((L * D, B, H)) * 0.5
+    out, h_n, c_n = O.rnn_forward("LSTM", x, proj, L, True, h0, c0)
+    ow, hw, cw = O.rnn_forward("LSTM", x, plain, L, True, h0w, c0)
+    assert out.shape == (T, B, D * P) and h_n.shape == (L * D, B, P) and c_n.shape == (L * D, B, H)
+    for dd in range(D):
+        np.testing.assert_allclose(out[:, :, dd * P:(dd + 1) * P], ow[:, :, dd * H:dd * H + P], atol=1e-12)
+    np.testing.assert_allclose(h_n, hw[:, :, :P], atol=1e-12)
+    np.testing.assert_allclose(c_n, cw, atol=1e-12)
+    # a general projection is not the selector: the emitted state really is h_raw W_hr^T
+    one = {k: v for k, v in proj.items() if k.endswith("_l0")}
+    one["weight_hr_l0"] = rng.uniform(-1, 1, (P, H))
+    o1, h1, c1 = O.rnn_forward("LSTM", x[:1], one)
+    g = x[0] @ one["weight_ih_l0"].T + one["bias_ih_l0"] + one["bias_hh_l0"]
+    s = 1.0 / (1.0 + np.exp(-g))
+    c_ = s[:, :H] * np.tanh(g[:, 2 * H:3 * H])
+    np.testing.assert_allclose(c1[0], c_, atol=1e-12)
+    np.testing.assert_allclose(o1[0], (s[:, 3 * H:] * np.tanh(c_)) @ one["weight_hr_l0"].T, atol=1e-12)
+
+
 # ------------------------------------------------------------ transposed convolution
 
 
