@@ -716,6 +716,18 @@ def model_lines(L, C, gtimer, with_cpu: bool) -> dict:
         c5 = {"workload": "config 5: static int8 ResNet-18 (BN folded, per-channel int8 weights, uint8 "
                           "activations from 16 calibration batches), batch 32 at 224 x 224",
               "forward_ms": fwd, "images_per_s": round(32 / (fwd["median"] * 1e-3), 1)}
+        # the same forward replayed as one HIP graph (lucid_amd.graphs: the eager forward's
+        # launches on its buffers, Python dispatch and allocation out of the path)
+        from lucid_amd.graphs import CapturedForward
+
+        cap = CapturedForward(qnet, x)
+        for _ in range(3):
+            cap.replay()
+        cap.synchronize()
+        graph_ms = _event_ms(C, cap.stream, lambda: [cap.replay() for _ in range(20)]) / 20
+        c5.update({"graph_replay_ms": round(graph_ms, 4), "graph_launches": cap.launches,
+                   "graph_images_per_s": round(32 / (graph_ms * 1e-3), 1)})
+        del cap
         if with_cpu:
             import oracle.lucid_models as LM
 

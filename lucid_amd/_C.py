@@ -212,12 +212,17 @@ def check(rc: int, what: str = "") -> None:
 _entry_points: dict = {}
 
 
+_recording: list | None = None  # (name, args) of every call while a capture records (lucid_amd.graphs)
+
+
 def call(name: str, *args) -> None:
     """Call an int-status entry point and raise on failure (the ctypes function object is
     looked up once per name)."""
     f = _entry_points.get(name)
     if f is None:
         f = _entry_points[name] = getattr(lib(), name)
+    if _recording is not None:
+        _recording.append((name, args))
     rc = f(*args)
     if rc != OK:
         check(rc, name)

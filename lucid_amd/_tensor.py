@@ -83,6 +83,9 @@ def normalize_device(device: Any) -> str:
     return _DEVICE_ALIASES[d]
 
 
+_held: list | None = None  # every buffer allocated while a capture records (lucid_amd.graphs)
+
+
 class _DeviceBuffer:
     """An ``lq_malloc`` allocation, returned to the cache when collected."""
 
@@ -93,6 +96,8 @@ class _DeviceBuffer:
         _C.check(_C.lib().lq_malloc(ctypes.byref(p), max(int(nbytes), 1)), "lq_malloc")
         self.ptr = p.value
         self.nbytes = int(nbytes)
+        if _held is not None:
+            _held.append(self)
 
     def __del__(self) -> None:
         ptr = getattr(self, "ptr", None)
