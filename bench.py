@@ -728,6 +728,17 @@ def model_lines(L, C, gtimer, with_cpu: bool) -> dict:
         c5.update({"graph_replay_ms": round(graph_ms, 4), "graph_launches": cap.launches,
                    "graph_images_per_s": round(32 / (graph_ms * 1e-3), 1)})
         del cap
+        # the NHWC runtime (activations padded NHWC between block convolutions, residual adds
+        # fused into the second convolutions; the module forward's bits), replayed as a graph
+        rt = bc.Int8ResNet(qnet, 32)
+        cap = CapturedForward(rt, x)
+        for _ in range(3):
+            cap.replay()
+        cap.synchronize()
+        nhwc_ms = _event_ms(C, cap.stream, lambda: [cap.replay() for _ in range(20)]) / 20
+        c5.update({"nhwc_graph_replay_ms": round(nhwc_ms, 4), "nhwc_graph_launches": cap.launches,
+                   "nhwc_images_per_s": round(32 / (nhwc_ms * 1e-3), 1)})
+        del cap, rt
         if with_cpu:
             import oracle.lucid_models as LM
 

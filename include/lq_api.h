@@ -272,7 +272,10 @@ enum {
  * the kernel applies the 128 shift. */
 enum { LQ_EPI_RELU = 1, LQ_EPI_A_U8S8 = 2, LQ_EPI_ROUND_BF16 = 4 /* lq_group_matmul only */,
        LQ_EPI_GELU = 8 /* lq_gemm_w8a8(_packed), LQ_OUT_F32 only: y = gelu_tanh(y) after the bias,
-                          the bits of lq_gelu_tanh_f32 on the output (F.gelu after the Linear) */ };
+                          the bits of lq_gelu_tanh_f32 on the output (F.gelu after the Linear) */,
+       LQ_CONV_OUT_NHWC = 16 /* lq_conv2d_i8 only, byte codes out, groups 1, Cout a multiple of 16:
+                                y written [N][OH][OW][Cout] (the layout of lq_conv2d_i8_nhwc without a
+                                border), the same codes */ };
 
 /* C[m,n] epilogue of acc[m,n] = sum_k (A[m,k] - za) * (B[n,k] - zb[n])  (exact int32),
  * A int8 [M,K] row-major (lda), B int8 [N,K] row-major (ldb; Lucid's weight_int8 [out,in]).
@@ -599,6 +602,57 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
                  const float* d_a_zero_point, const float* d_w_scale, const float* d_bias,
                  const float* d_out_scale, const float* d_out_zero_point, int out_qmin, int out_qmax,
                  int out_kind, int flags, void* d_y, void* d_workspace, size_t workspace_bytes, void* stream);
+
+/* The same convolution (groups 1, zeros padding, no dilation) between activations held in the
+ * layout the implicit GEMM reads, for a network whose layers feed each other without
+ * repacking: x is [N][H + 2 x_pad][W + 2 x_pad][x_cs] codes (x_cs = C rounded up to 16; the
+ * border, x_pad >= pad, and the channel padding hold the activation zero point's code), and the
+ * output is written the same way, y [N][OH + 2 y_pad][OW + 2 y_pad][y_cs] (y_pad 0 or 1; the
+ * border filled with the output grid's zero-point code; Cout a multiple of 16), codes of
+ * out_kind LQ_OUT_Q8 / QU8 / QU8S8.  With d_skip (codes of skip_type, the output's layout and
+ * grid d_skip_scale / d_skip_zero_point) each output code c is then merged as lq_qmerge's
+ * LQ_MERGE_ADD computes it -- fl32((c - z) s) + fl32((skip - zs) ss), ReLU with merge_flags
+ * LQ_EPI_RELU, requantized to the merge grid (d_merge_scale / zero point, [merge_qmin,
+ * merge_qmax], merge_type) -- the residual add of a quantized block (QFunctional.add_relu,
+ * lucid/nn/quantized/functional_module.py:215-217) fused into its second convolution, and the
+ * border holds the merge grid's zero point.  The bits of lq_conv2d_i8 followed by lq_qmerge on
+ * the NCHW forms.  Workspace: lq_conv2d_i8_nhwc_workspace_size bytes (split-K sums; may be 0).
+ * No reference counterpart: a device layout between Lucid's NCHW modules. */
+size_t lq_conv2d_i8_nhwc_workspace_size(int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout, int64_t KH,
+                                        int64_t KW, int stride, int pad);
+int lq_conv2d_i8_nhwc(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64_t H, int64_t W, int x_pad,
+                      int64_t x_cs, const int8_t* d_w_packed, const int32_t* d_w_sums, int64_t Cout, int64_t KH,
+                      int64_t KW, int stride, int pad, const float* d_a_scale, const float* d_a_zero_point,
+                      const float* d_w_scale, const float* d_bias, const float* d_out_scale,
+                      const float* d_out_zero_point, int out_qmin, int out_qmax, int out_kind, int flags, int8_t* d_y,
+                      int y_pad, int64_t y_cs, const int8_t* d_skip, int skip_type, const float* d_skip_scale,
+                      const float* d_skip_zero_point, const float* d_merge_scale, const float* d_merge_zero_point,
+                      int merge_qmin, int merge_qmax, int merge_type, int merge_flags, void* d_workspace,
+                      size_t workspace_bytes, void* stream);
+
+/* Max pooling of byte codes (LQ_I8 / LQ_U8 / LQ_U8S8) from x[N, C, H, W] into the padded NHWC
+ * layout of lq_conv2d_i8_nhwc: y [N][OH + 2 y_pad][OW + 2 y_pad][C] (y_cs == C, C a multiple
+ * of 16, y_pad 0 or 1), the border filled with the code of *d_zero_point (the grid's zero
+ * point; pooling keeps the grid).  Windows up to 3 x 3 with lq_pool2d's rules; the codes are
+ * lq_pool2d's LQ_POOL_MAX.  Replaces max_pool2d over a quantized activation
+ * (lucid/_C/backend/cpu/Pool.cpp:27-80) where the next layer reads the NHWC layout. */
+int lq_maxpool2d_i8_to_nhwc(const int8_t* d_x, int x_type, const float* d_zero_point, int64_t N, int64_t C,
+                            int64_t H, int64_t W, int64_t OH, int64_t OW, int KH, int KW, int stride_h, int stride_w,
+                            int pad_h, int pad_w, int8_t* d_y, int y_pad, int64_t y_cs, void* stream);
+/* Max pooling within that layout: x [N][H + 2 x_pad][W + 2 x_pad][x_cs] to y [N][OH + 2 y_pad]
+ * [OW + 2 y_pad][y_cs] (C and both channel strides multiples of 16, windows up to 3 x 3, the
+ * input border never read, the output border filled with the code of *d_zero_point); the codes
+ * of lq_pool2d's LQ_POOL_MAX. */
+int lq_maxpool2d_i8_nhwc(const int8_t* d_x, int x_type, const float* d_zero_point, int64_t N, int64_t C, int64_t H,
+                         int64_t W, int x_pad, int64_t x_cs, int64_t OH, int64_t OW, int KH, int KW, int stride_h,
+                         int stride_w, int pad_h, int pad_w, int8_t* d_y, int y_pad, int64_t y_cs, void* stream);
+/* y[n, c] (float32 [N, C]) = the adaptive average pool to 1 x 1 of byte codes held in the padded
+ * NHWC layout (x_pad border, x_cs bytes per pixel): sum over h, then w, of
+ * fl32(fl32(float(c) - z) s), divided by H W -- lq_pool2d's LQ_POOL_AVG | LQ_POOL_ADAPTIVE bits
+ * (lucid/nn/functional/_pool_core.py:407-434). */
+int lq_avgpool2d_global_nhwc(const int8_t* d_x, int x_type, const float* d_scale, const float* d_zero_point,
+                             int64_t N, int64_t C, int64_t H, int64_t W, int x_pad, int64_t x_cs, float* d_y,
+                             void* stream);
 
 /* ---- float helpers around the quantized path ----------------------------------- */
 /* Float Conv2d y[N, Cout, OH, OW] (direct; the float model's conv during calibration,

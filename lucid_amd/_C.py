@@ -25,6 +25,7 @@ BF16 = 10
 OBS_MINMAX, OBS_EMA, OBS_REPLACE = 0, 1, 2
 OUT_I32, OUT_F32, OUT_F16, OUT_Q8, OUT_QU8, OUT_FQ32, OUT_Q16, OUT_QU8S8 = 0, 1, 2, 3, 4, 5, 6, 7
 EPI_RELU, EPI_A_U8S8, EPI_ROUND_BF16, EPI_GELU = 1, 2, 4, 8
+CONV_OUT_NHWC = 16
 DL_PLAIN, DL_LN, DL_ADD_LN = 0, 1, 2
 PAD_ZEROS, PAD_REFLECT, PAD_REPLICATE, PAD_CIRCULAR = 0, 1, 2, 3
 MERGE_ADD, MERGE_MUL, MERGE_ADD_SCALAR, MERGE_MUL_SCALAR, MERGE_COPY = 0, 1, 2, 3, 4
@@ -138,6 +139,15 @@ _SIGNATURES: dict[str, tuple] = {
                                  _P, _P, _P, _P, _P, _P, _I, _I, _I, _I, _P, _SZ, _P]),
     "lq_dynamic_linear_packed_f32": (_I, [_P, _I64, _P, _I64, _P, _I64, _I, _P, _P, _F, _I64, _I64, _I, _I, _F,
                                           _P, _P, _P, _P, _P, _I64, _P, _I64, _I, _P]),
+    "lq_conv2d_i8_nhwc_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I]),
+    "lq_conv2d_i8_nhwc": (_I, [_P, _I, _I64, _I64, _I64, _I64, _I, _I64, _P, _P, _I64, _I64, _I64, _I, _I, _P, _P,
+                               _P, _P, _P, _P, _I, _I, _I, _I, _P, _I, _I64, _P, _I, _P, _P, _P, _P, _I, _I, _I,
+                               _I, _P, _SZ, _P]),
+    "lq_maxpool2d_i8_to_nhwc": (_I, [_P, _I, _P, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _I, _I, _I, _I, _P, _I,
+                                     _I64, _P]),
+    "lq_avgpool2d_global_nhwc": (_I, [_P, _I, _P, _P, _I64, _I64, _I64, _I64, _I, _I64, _P, _P]),
+    "lq_maxpool2d_i8_nhwc": (_I, [_P, _I, _P, _I64, _I64, _I64, _I64, _I, _I64, _I64, _I64, _I, _I, _I, _I, _I, _I,
+                                  _P, _I, _I64, _P]),
     "lq_conv2d_weight_pack_size": (_SZ, [_I64, _I64, _I64, _I64]),
     "lq_conv2d_pack_weights_i8": (_I, [_P, _I64, _I64, _I64, _I64, _P, _P, _P]),
     "lq_conv2d_i8_workspace_size": (_SZ, [_I64, _I64, _I64, _I64, _I64, _I64, _I64, _I, _I, _I, _I, _I, _I, _I, _I,

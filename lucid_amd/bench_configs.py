@@ -463,7 +463,8 @@ def _main(argv: list[str]) -> None:
     """``python3 -m lucid_amd.bench_configs resnet18 [forwards]``: time the configuration-5
     forward (module dispatch included) after three warm-up forwards;
     ``python3 -m lucid_amd.bench_configs decoder [steps]``: configuration 4 launched eagerly
-    (two prefills, then greedy steps).  A profiler run wraps either."""
+    (two prefills, then greedy steps); ``resnet18_nhwc``: configuration 5 through
+    :class:`Int8ResNet`.  A profiler run wraps any of them."""
     import time
 
     import lucid_amd as L
@@ -472,11 +473,13 @@ def _main(argv: list[str]) -> None:
     if argv and argv[0] == "decoder":
         _decoder_eager(int(argv[1]) if len(argv) > 1 else 16)
         return
-    if not argv or argv[0] != "resnet18":
-        raise SystemExit("usage: python3 -m lucid_amd.bench_configs resnet18|decoder [count]")
+    if not argv or argv[0] not in ("resnet18", "resnet18_nhwc"):
+        raise SystemExit("usage: python3 -m lucid_amd.bench_configs resnet18|resnet18_nhwc|decoder [count]")
     n = int(argv[1]) if len(argv) > 1 else 10
     backends.quantized.engine = "reference"  # the per-channel int8 layers
     qnet, x = static_resnet18(calib_batches=4)
+    if argv[0] == "resnet18_nhwc":
+        qnet = Int8ResNet(qnet, 32)
     for _ in range(3):
         qnet(x)
     L.synchronize()
@@ -488,6 +491,148 @@ def _main(argv: list[str]) -> None:
         ts.append((time.perf_counter() - t0) * 1e3)
     ts.sort()
     print(f"resnet18 batch 32: forward median {ts[len(ts) // 2]:.3f} ms over {n}")
+
+
+
+class Int8ResNet:
+    """Configuration 5's converted network (:func:`static_resnet18`'s output) with its
+    activations kept, between the block convolutions, in the padded NHWC layout the int8
+    implicit GEMM reads: the stem (QuantStub, then the 7 x 7 convolution) as its modules run
+    it, the max pool into that layout (``lq_maxpool2d_i8_to_nhwc``), every block convolution
+    through ``lq_conv2d_i8_nhwc`` -- each writing the next one's input with its zero-point
+    border, the block's residual ``add_relu`` fused into its second convolution -- the global
+    average pool from the layout (``lq_avgpool2d_global_nhwc``), and the fc and DeQuantStub as
+    their modules run them.  The per-layer repacking of the input (NCHW to padded NHWC) and the
+    separate merge launches of the module forward are gone; the codes, and the result, are the
+    module forward's bits.  Buffers are allocated for one batch size; :meth:`forward` can be
+    recorded and replayed as one graph (``lucid_amd.graphs.CapturedForward``)."""
+
+    def __init__(self, qnet, batch: int, image: int = 224) -> None:
+        from lucid_amd.nn.quantized.linear import out_kind_for
+
+        self.qnet, self.N = qnet, batch
+        self.blocks = []
+        # the stem's output grid and geometry (7 x 7 / 2, then the 3 x 3 / 2 max pool)
+        stem = qnet.conv1
+        H = (image + 2 * 3 - 7) // 2 + 1
+        self.stem_hw, self.pool_hw = H, (H + 2 - 3) // 2 + 1
+        grid = (stem.scale, stem.zero_point, out_kind_for(stem.out_qdtype)[1])
+        C, H = stem.out_channels, self.pool_hw
+        self.stem_out = empty((batch, self.stem_hw, self.stem_hw, C), np.int8, "gpu")  # NHWC, no border
+        self.stem_ws_bytes = max(_C.lib().lq_conv2d_i8_workspace_size(batch, stem.in_channels, image, image, C, 7, 7,
+                                                                       2, 2, 3, 3, 3, 3, 1, 1, 1), 16)
+        self.stem_ws = empty((self.stem_ws_bytes,), np.uint8, "gpu")
+        self.pool_out = self._buffer(C, H)
+        cur = self.pool_out
+        for li in range(1, 5):
+            for blk in getattr(qnet, f"layer{li}"):
+                conv1, conv2 = blk.conv1, blk.conv2
+                st = conv1.stride[0]
+                Ho = (H + 2 - 3) // st + 1
+                mid = self._buffer(conv1.out_channels, Ho)
+                out = self._buffer(conv2.out_channels, Ho)
+                ds = None
+                if blk.downsample is not None:
+                    ds = (blk.downsample[0], self._buffer(blk.downsample[0].out_channels, Ho))
+                self.blocks.append(dict(conv1=conv1, conv2=conv2, skip=blk.skip, ds=ds, x=cur, mid=mid, out=out,
+                                        C=C, H=H, Ho=Ho, grid=grid))
+                grid = (blk.skip.scale, blk.skip.zero_point, _merge_code(blk.skip.qdtype))
+                cur, C, H = out, conv2.out_channels, Ho
+        self.final, self.final_c, self.final_hw, self.final_grid = cur, C, H, grid
+        self.pooled = empty((batch, C), np.float32, "gpu")
+        lib = _C.lib()
+        ws = 16
+        for b in self.blocks:
+            for conv, Cin, Hin in ((b["conv1"], b["C"], b["H"]), (b["conv2"], b["conv1"].out_channels, b["Ho"])):
+                k = conv.kernel_size[0]
+                ws = max(ws, lib.lq_conv2d_i8_nhwc_workspace_size(batch, Cin, Hin, Hin, conv.out_channels, k, k,
+                                                                  conv.stride[0], conv._pads()[0]))
+        self.ws_bytes = ws
+        self.ws = empty((ws,), np.uint8, "gpu")
+
+    def _buffer(self, C: int, H: int):
+        """A padded NHWC activation buffer (border 1) for this batch."""
+        return empty((self.N, H + 2, H + 2, C), np.int8, "gpu")
+
+    def _conv(self, conv, x, x_grid, Cin, Hin, y, skip=None, skip_grid=None, merge=None) -> None:
+        from lucid_amd.nn.quantized.linear import out_kind_for
+        from lucid_amd.quantization._device import on_device
+
+        ops = conv._operands()
+        s_in, z_in, code_in = x_grid
+        out_kind, _ = out_kind_for(conv.out_qdtype)
+        k = conv.kernel_size[0]
+        qd = conv.out_qdtype
+        b = on_device(conv.bias) if conv.bias is not None else None
+        if merge is not None:
+            ss, zs, st = skip_grid
+            ms, mz, mt = merge.scale, merge.zero_point, _merge_code(merge.qdtype)
+            mq = (merge.qdtype.quant_min, merge.qdtype.quant_max)
+            mflags = _C.EPI_RELU
+        _C.call("lq_conv2d_i8_nhwc", x.data_ptr(), code_in, self.N, Cin, Hin, Hin, 1, Cin, ops.packed.data_ptr(),
+                ops.sums.data_ptr(), conv.out_channels, k, k, conv.stride[0], conv._pads()[0], on_device(s_in).data_ptr(),
+                on_device(z_in).data_ptr(), ops.scale.data_ptr(), b.data_ptr() if b is not None else None,
+                on_device(conv.scale).data_ptr(), on_device(conv.zero_point).data_ptr(), qd.quant_min, qd.quant_max,
+                out_kind, _C.EPI_RELU if conv._relu else 0, y.data_ptr(), 1, conv.out_channels,
+                skip.data_ptr() if skip is not None else None, st if merge is not None else _C.U8S8,
+                on_device(ss).data_ptr() if merge is not None else None,
+                on_device(zs).data_ptr() if merge is not None else None,
+                on_device(ms).data_ptr() if merge is not None else None,
+                on_device(mz).data_ptr() if merge is not None else None,
+                mq[0] if merge is not None else 0, mq[1] if merge is not None else 255,
+                mt if merge is not None else _C.U8S8, mflags if merge is not None else 0, self.ws.data_ptr(),
+                self.ws_bytes, None)
+
+    def forward(self, x):
+        from lucid_amd.nn.quantized.linear import out_kind_for
+        from lucid_amd.quantization._device import on_device
+
+        qnet = self.qnet
+        q = qnet.quant(x).quant_source
+        stem = qnet.conv1
+        ops = stem._operands()
+        C, H = stem.out_channels, self.stem_hw
+        out_kind, code = out_kind_for(stem.out_qdtype)
+        qd = stem.out_qdtype
+        b = on_device(stem.bias) if stem.bias is not None else None
+        pt, pb, pl, pr = stem._pads()
+        # the stem convolution as its module runs it, its codes written NHWC
+        _C.call("lq_conv2d_i8", q.codes.data_ptr(), q.code_type, self.N, stem.in_channels, x.shape[2], x.shape[3],
+                ops.packed.data_ptr(), ops.sums.data_ptr(), C, stem.kernel_size[0], stem.kernel_size[1],
+                stem.stride[0], stem.stride[1], pt, pb, pl, pr, 1, 1, 1, 0,
+                q.scale.data_ptr(), q.zero_point.data_ptr(), ops.scale.data_ptr(),
+                b.data_ptr() if b is not None else None, on_device(stem.scale).data_ptr(),
+                on_device(stem.zero_point).data_ptr(), qd.quant_min, qd.quant_max, out_kind,
+                (_C.EPI_RELU if stem._relu else 0) | _C.CONV_OUT_NHWC, self.stem_out.data_ptr(),
+                self.stem_ws.data_ptr(), self.stem_ws_bytes, None)
+        _C.call("lq_maxpool2d_i8_nhwc", self.stem_out.data_ptr(), code, on_device(stem.zero_point).data_ptr(),
+                self.N, C, H, H, 0, C, self.pool_hw, self.pool_hw, 3, 3, 2, 2, 1, 1, self.pool_out.data_ptr(), 1, C,
+                None)
+        for b in self.blocks:
+            self._conv(b["conv1"], b["x"], b["grid"], b["C"], b["H"], b["mid"])
+            c1 = b["conv1"]
+            g1 = (c1.scale, c1.zero_point, out_kind_for(c1.out_qdtype)[1])
+            if b["ds"] is not None:
+                dconv, dbuf = b["ds"]
+                self._conv(dconv, b["x"], b["grid"], b["C"], b["H"], dbuf)
+                skip, skip_grid = dbuf, (dconv.scale, dconv.zero_point, out_kind_for(dconv.out_qdtype)[1])
+            else:
+                skip, skip_grid = b["x"], b["grid"]
+            self._conv(b["conv2"], b["mid"], g1, c1.out_channels, b["Ho"], b["out"], skip, skip_grid, b["skip"])
+        s_f, z_f, t_f = self.final_grid
+        _C.call("lq_avgpool2d_global_nhwc", self.final.data_ptr(), t_f, on_device(s_f).data_ptr(),
+                on_device(z_f).data_ptr(), self.N, self.final_c, self.final_hw, self.final_hw, 1, self.final_c,
+                self.pooled.data_ptr(), None)
+        return qnet.dequant(qnet.fc(qnet.flatten(self.pooled.reshape(self.N, self.final_c, 1, 1))))
+
+    __call__ = forward
+
+
+def _merge_code(qdtype) -> int:
+    """Code type a QFunctional of ``qdtype`` stores (the merge's _grid_codes choice)."""
+    if qdtype.quant_min >= -128 and qdtype.quant_max <= 127:
+        return _C.I8
+    return _C.U8S8
 
 
 if __name__ == "__main__":

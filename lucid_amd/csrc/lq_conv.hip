@@ -597,16 +597,49 @@ struct ConvDmaArgs {
     // them in split order and runs the epilogue
     int splits, phase;
     int32_t* part;
+    // NHWC output (lq_conv2d_i8_nhwc): y is pixel (0, 0) of a padded buffer -- ypad border
+    // pixels on each side, yrow bytes per padded row, yimg per image, ycs per pixel -- whose
+    // border this launch fills with the output grid's zero-point code
+    int out_nhwc, ypad, ycs;
+    int64_t yrow, yimg;
+    // residual merge into the NHWC output (QFunctional.add_relu of the conv's codes and a skip
+    // tensor of the same layout): the merge's grid, and the skip's codes and grid
+    const int8_t* skip;
+    int skip_type, m_type, m_relu;
+    const float* skip_scale;
+    const float* skip_zp;
+    const float* m_scale;
+    const float* m_zp;
+    int m_qmin, m_qmax;
 };
+
+// A stored byte code of an integer output kind / code type as its float code value.
+__device__ __forceinline__ float nhwc_code(uint32_t b, int type) {
+    if (type == LQ_I8) return (float)(int)(int8_t)(uint8_t)b;
+    if (type == LQ_U8) return (float)(int)(uint8_t)b;
+    return (float)((int)(int8_t)(uint8_t)b + 128);  // LQ_U8S8: c stored as c - 128
+}
+__device__ __forceinline__ uint32_t nhwc_store(float t, float inv, float z, const Grid& g, int type) {
+    if (type == LQ_I8) return (uint8_t)quant_store<CodeI8>(t, inv, z, g);
+    if (type == LQ_U8) return (uint8_t)quant_store<CodeU8>(t, inv, z, g);
+    return (uint8_t)quant_store<CodeU8S8>(t, inv, z, g);
+}
+__device__ __forceinline__ uint32_t nhwc_zero_code(float z, int type) {
+    const int zi = (int)z;  // an integral zero point
+    return (uint8_t)(type == LQ_U8S8 ? zi - 128 : zi);
+}
 
 // Epilogue of one wave's tile of 64 pixels x 16 FN channels: acc[i][j][r] is pixel
 // pb + 4 j + r of this lane's run (pb = the wave's first pixel + 16 (lane / 16)), channel
 // co_w + 16 i + lane % 16 of group g.  A lane owns 16 consecutive pixels of each of its FN
 // channels, stored as 16-byte NCHW runs when the run lies in one image and is aligned.
+constexpr int NH_ROW = 80;  // LDS bytes per channel row of the NHWC transpose (64 pixels + 16: no bank conflicts)
+
 template <int FN, int KIND>
 __device__ __forceinline__ void conv_epilogue(const ConvDmaArgs& a, v4i (&acc)[FN][4], const int pb, const int co_w,
                                               const int g, const int lane, const float* csb, const float* cbias,
-                                              const int32_t* cws, const float sa, const EpiParams& ep) {
+                                              const int32_t* cws, const float sa, const EpiParams& ep,
+                                              int8_t* nh = nullptr) {
     constexpr bool INT_CODES = KIND == LQ_OUT_Q8 || KIND == LQ_OUT_QU8 || KIND == LQ_OUT_Q16 || KIND == LQ_OUT_QU8S8;
     const int rho = lane & 15;
     const int OHW = a.OH * a.OW;
@@ -617,8 +650,91 @@ __device__ __forceinline__ void conv_epilogue(const ConvDmaArgs& a, v4i (&acc)[F
     const int pix0 = pb - nimg * OHW;
     constexpr int OB = OutTraits<KIND>::bytes;
     const bool vec = (OHW % 16 == 0) && (reinterpret_cast<uintptr_t>(a.y) % 16 == 0) && (pb + 15 < a.P);
+    // NHWC form (nh: this wave's LDS, a row of 64 pixel bytes per channel of its tile): each
+    // channel's 16-pixel run is staged as one 16-byte row segment; flush_nhwc then gives each
+    // lane one pixel and reads its channels back 16 at a time, so the global stores (and the
+    // skip loads of a fused residual merge) are 16 contiguous channel bytes of one pixel.
+    const int cbase = g * a.Cout_g + co_w;
+    auto stage_nhwc = [&](const int co, const uint32_t* out) __attribute__((always_inline)) {
+        v4i w;
+#pragma unroll
+        for (int d = 0; d < 4; ++d) w[d] = (int)pack_low_bytes(out + 4 * d);
+        *reinterpret_cast<v4i*>(nh + (co - cbase) * NH_ROW + (lane >> 4) * 16) = w;
+    };
+    auto flush_nhwc = [&]() __attribute__((always_inline)) {
+        constexpr int OT = KIND == LQ_OUT_Q8 ? LQ_I8 : KIND == LQ_OUT_QU8 ? LQ_U8 : LQ_U8S8;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        const int p = pb - (lane >> 4) * 16 + lane;  // this lane's pixel of the wave's 64
+        if (p >= a.P) return;
+        const int n = p / OHW, rem = p - n * OHW, oh = rem / a.OW, ow = rem - oh * a.OW;
+        int8_t* y = static_cast<int8_t*>(a.y);
+        const int64_t pix = n * a.yimg + (int64_t)(oh + a.ypad) * a.yrow + (int64_t)(ow + a.ypad) * a.ycs;
+        const bool merge = a.skip != nullptr;
+        float ss = 0.f, zs = 0.f, minv = 1.f, mz = 0.f;
+        Grid mg{};
+        if (merge) {
+            ss = a.skip_scale[0];
+            zs = a.skip_zp ? a.skip_zp[0] : 0.0f;
+            minv = 1.0f / a.m_scale[0];
+            mz = a.m_zp ? a.m_zp[0] : 0.0f;
+            mg = make_grid(a.m_qmin, a.m_qmax);
+        }
+        const uint32_t zc = merge ? nhwc_zero_code(mz, a.m_type) : nhwc_zero_code(ep.out_z, OT);
+        const v4i zc16 = v4i{(int)(zc * 0x01010101u), (int)(zc * 0x01010101u), (int)(zc * 0x01010101u),
+                             (int)(zc * 0x01010101u)};
+#pragma unroll
+        for (int k = 0; k < FN; ++k) {
+            if (co_w + 16 * k >= a.Cout_g) break;
+            const int64_t off = pix + cbase + 16 * k;
+            uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+            for (int j = 0; j < 16; ++j)
+                w[j >> 2] |= (uint32_t)(uint8_t)nh[(16 * k + j) * NH_ROW + (lane & 63)] << (8 * (j & 3));
+            if (merge) {  // merge_bytes16_kernel's arithmetic: dequantize both, add, ReLU, requantize
+                const v4i sk = *reinterpret_cast<const v4i*>(a.skip + off);
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    uint32_t o = 0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float av = (nhwc_code(w[d] >> (8 * e), OT) - ep.out_z) * ep.out_s;
+                        const float bv = (nhwc_code((uint32_t)sk[d] >> (8 * e), a.skip_type) - zs) * ss;
+                        float t = av + bv;
+                        if (a.m_relu) t = (t <= 0.0f) ? 0.0f : t;
+                        o |= nhwc_store(t, minv, mz, mg, a.m_type) << (8 * e);
+                    }
+                    w[d] = o;
+                }
+            }
+            *reinterpret_cast<v4i*>(y + off) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+            if (a.ypad) {
+                const bool l = ow == 0, r = ow == a.OW - 1;
+                const int64_t cs = a.ycs, rw = a.yrow;
+                if (l) *reinterpret_cast<v4i*>(y + off - cs) = zc16;
+                if (r) *reinterpret_cast<v4i*>(y + off + cs) = zc16;
+                if (oh == 0) {
+                    *reinterpret_cast<v4i*>(y + off - rw) = zc16;
+                    if (l) *reinterpret_cast<v4i*>(y + off - rw - cs) = zc16;
+                    if (r) *reinterpret_cast<v4i*>(y + off - rw + cs) = zc16;
+                }
+                if (oh == a.OH - 1) {
+                    *reinterpret_cast<v4i*>(y + off + rw) = zc16;
+                    if (l) *reinterpret_cast<v4i*>(y + off + rw - cs) = zc16;
+                    if (r) *reinterpret_cast<v4i*>(y + off + rw + cs) = zc16;
+                }
+            }
+        }
+    };
     // Stores of one channel's 16 consecutive pixels (out[] holds the output type's bits).
     auto store_col = [&](const int co, const uint32_t* out) __attribute__((always_inline)) {
+        if constexpr (OB == 1) {
+            if (nh) {
+                stage_nhwc(co, out);
+                return;
+            }
+        }
         if (vec) {
             const int64_t base = ((int64_t)nimg * Cout + co) * OHW + pix0;
             if (OB == 1) {
@@ -720,6 +836,9 @@ __device__ __forceinline__ void conv_epilogue(const ConvDmaArgs& a, v4i (&acc)[F
             };
             if (a.bias) cols_za(std::true_type{});
             else cols_za(std::false_type{});
+            if constexpr (OB == 1) {
+                if (nh) flush_nhwc();
+            }
             return;
         }
     }
@@ -747,6 +866,9 @@ __device__ __forceinline__ void conv_epilogue(const ConvDmaArgs& a, v4i (&acc)[F
             }
         }
         store_col(co, out);
+    }
+    if constexpr (OB == 1) {
+        if (nh) flush_nhwc();
     }
 }
 
@@ -1003,7 +1125,7 @@ int64_t halo_bytes_for(int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout,
 
 // Two waves per SIMD (<= 256 registers): the LDS ring leaves room for two workgroups per CU,
 // and their main loops and epilogues overlap.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int NBUF, int KIND>
+template <int BM, int BN, int WAVES_M, int WAVES_N, int NBUF, int KIND, bool NHWC = false>
 __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves_per_eu(2))) void conv_i8_dma_kernel(
     ConvDmaArgs a) {
     constexpr int BK = 128, NW = WAVES_M * WAVES_N, WM = BM / WAVES_M, WN = BN / WAVES_N;
@@ -1181,7 +1303,16 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves
         }
     }
 
-    conv_epilogue<FN, KIND>(a, acc, p0 + wm * 64 + c0 * 16, co0 + wn * WN, g, lane, csb, cbias, cws, sa, ep);
+    if constexpr (NHWC) {
+        // the transpose reuses the stage ring once every wave is done reading it (a separate
+        // array would cost the second workgroup per CU)
+        static_assert(NW * WN * NH_ROW <= NBUF * SB, "NHWC transpose in the stage ring");
+        block_barrier();
+        conv_epilogue<FN, KIND>(a, acc, p0 + wm * 64 + c0 * 16, co0 + wn * WN, g, lane, csb, cbias, cws, sa, ep,
+                                lds + wave * WN * NH_ROW);
+    } else {
+        conv_epilogue<FN, KIND>(a, acc, p0 + wm * 64 + c0 * 16, co0 + wn * WN, g, lane, csb, cbias, cws, sa, ep);
+    }
 }
 
 // ---------------------------------------------------------------- float helpers
@@ -1367,7 +1498,12 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
     LQ_REQUIRE(C % groups == 0 && Cout % groups == 0, "lq_conv2d_i8: channels must divide by groups");
     LQ_REQUIRE(x_code_type == LQ_I8 || x_code_type == LQ_U8S8, "lq_conv2d_i8: activation codes must be LQ_I8 or LQ_U8S8");
     LQ_REQUIRE(padding_mode >= LQ_PAD_ZEROS && padding_mode <= LQ_PAD_CIRCULAR, "lq_conv2d_i8: unknown padding mode");
-    LQ_REQUIRE((flags & ~LQ_EPI_RELU) == 0, "lq_conv2d_i8: unknown flags");
+    LQ_REQUIRE((flags & ~(LQ_EPI_RELU | LQ_CONV_OUT_NHWC)) == 0, "lq_conv2d_i8: unknown flags");
+    const bool out_nhwc = (flags & LQ_CONV_OUT_NHWC) != 0;
+    LQ_REQUIRE(!out_nhwc || ((out_kind == LQ_OUT_Q8 || out_kind == LQ_OUT_QU8 || out_kind == LQ_OUT_QU8S8) &&
+                             groups == 1 && Cout % 16 == 0 && aligned16(d_y)),
+               "lq_conv2d_i8: LQ_CONV_OUT_NHWC needs byte codes out, groups 1, Cout a multiple of 16 and a "
+               "16-byte aligned output");
     LQ_REQUIRE(out_kind >= LQ_OUT_I32 && out_kind <= LQ_OUT_QU8S8, "lq_conv2d_i8: unknown out_kind");
     int64_t OH = 0, OW = 0;
     LQ_REQUIRE(conv_geometry(H, W, (int)KH, (int)KW, stride_h, stride_w, pad_top, pad_bottom, pad_left, pad_right,
@@ -1396,13 +1532,16 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
     const ConvPlan plan = conv_plan(N, C, H, W, Cout, KH, KW, pad_top, pad_bottom, pad_left, pad_right, OH, OW, groups);
     LQ_REQUIRE(d_workspace && workspace_bytes >= plan.pack_bytes + plan.part_bytes,
                "lq_conv2d_i8: workspace smaller than lq_conv2d_i8_workspace_size");
+    if (out_nhwc && !plan.dma)
+        return set_error(LQ_ERR_UNSUPPORTED, "lq_conv2d_i8: LQ_CONV_OUT_NHWC needs the LDS-DMA plan");
     hipStream_t st = as_stream(stream);
 
     // halo-staged direct kernel: no padded copy of the input (the workspace goes unused)
     // (integer-code outputs only: the float kinds' epilogue does not fit this kernel's
     // register budget without spilling)
     const bool halo_kind = out_kind == LQ_OUT_Q8 || out_kind == LQ_OUT_QU8 || out_kind == LQ_OUT_QU8S8;
-    const int64_t halo = (halo_kind && (reinterpret_cast<uintptr_t>(d_x) & 15) == 0 && !plan.taps && plan.Cp == C)
+    const int64_t halo = (halo_kind && !out_nhwc && (reinterpret_cast<uintptr_t>(d_x) & 15) == 0 && !plan.taps &&
+                          plan.Cp == C)
                              ? halo_bytes_for(N, C, H, W, Cout, KH, KW, stride_h, stride_w, pad_top, pad_bottom,
                                               pad_left, pad_right, dilation_h, dilation_w, groups, padding_mode, OH, OW)
                              : 0;
@@ -1532,6 +1671,13 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
         d.qmin = out_qmin; d.qmax = out_qmax; d.relu = a.relu;
         d.splits = plan.splits;
         d.part = reinterpret_cast<int32_t*>(static_cast<int8_t*>(d_workspace) + plan.pack_bytes);
+        if (out_nhwc) {
+            d.out_nhwc = 1;
+            d.ypad = 0;
+            d.ycs = (int)Cout;
+            d.yrow = OW * Cout;
+            d.yimg = OH * OW * Cout;
+        }
         const bool big = plan.big;
         const dim3 grid((unsigned)plan.gx, (unsigned)plan.gy, (unsigned)groups);
         const dim3 grid0((unsigned)plan.gx, (unsigned)plan.gy, (unsigned)(groups * plan.splits));
@@ -1547,6 +1693,25 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
             hipLaunchKernelGGL((conv_i8_dma_kernel<128, 64, 2, 2, CV_SMALL_NBUF, K_>), grid, dim3(256), 0, st, d1); \
     }                                                                                                          \
     break;
+#define LQ_CONV_DMA_NHWC(K_)                                                                                   \
+    if (big) {                                                                                                 \
+        hipLaunchKernelGGL((conv_i8_dma_kernel<256, 64, 4, 1, 2, K_, true>), grid, dim3(256), 0, st, d);      \
+    } else {                                                                                                   \
+        hipLaunchKernelGGL((conv_i8_dma_kernel<128, 64, 2, 2, CV_SMALL_NBUF, K_, true>), grid0, dim3(256), 0, st, d); \
+        if (plan.splits > 1)                                                                                   \
+            hipLaunchKernelGGL((conv_i8_dma_kernel<128, 64, 2, 2, CV_SMALL_NBUF, K_, true>), grid, dim3(256), 0, st, d1); \
+    }                                                                                                          \
+    break;
+        if (out_nhwc) {
+            switch (out_kind) {
+                case LQ_OUT_Q8: LQ_CONV_DMA_NHWC(LQ_OUT_Q8)
+                case LQ_OUT_QU8: LQ_CONV_DMA_NHWC(LQ_OUT_QU8)
+                default: LQ_CONV_DMA_NHWC(LQ_OUT_QU8S8)
+            }
+            note_path(plan.taps ? "conv taps dma nhwc out" : "conv dma nhwc out");
+            return launch_status("lq_conv2d_i8");
+        }
+#undef LQ_CONV_DMA_NHWC
         switch (out_kind) {
             case LQ_OUT_I32: LQ_CONV_DMA(LQ_OUT_I32)
             case LQ_OUT_F32: LQ_CONV_DMA(LQ_OUT_F32)
@@ -1577,6 +1742,124 @@ int lq_conv2d_i8(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64
     }
     note_path(taps ? "conv taps staged 128x64" : "conv staged 128x64");
     return launch_status("lq_conv2d_i8");
+}
+
+size_t lq_conv2d_i8_nhwc_workspace_size(int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout, int64_t KH,
+                                        int64_t KW, int stride, int pad) {
+    if (N < 0 || C < 1 || H < 1 || W < 1 || Cout < 1) return 0;
+    int64_t OH = 0, OW = 0;
+    if (!conv_geometry(H, W, (int)KH, (int)KW, stride, stride, pad, pad, pad, pad, 1, 1, &OH, &OW)) return 0;
+    const ConvPlan pl = conv_plan(N, C, H, W, Cout, KH, KW, pad, pad, pad, pad, OH, OW, 1);
+    return pl.part_bytes;
+}
+
+int lq_conv2d_i8_nhwc(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, int64_t H, int64_t W, int x_pad,
+                      int64_t x_cs, const int8_t* d_w_packed, const int32_t* d_w_sums, int64_t Cout, int64_t KH,
+                      int64_t KW, int stride, int pad, const float* d_a_scale, const float* d_a_zero_point,
+                      const float* d_w_scale, const float* d_bias, const float* d_out_scale,
+                      const float* d_out_zero_point, int out_qmin, int out_qmax, int out_kind, int flags, int8_t* d_y,
+                      int y_pad, int64_t y_cs, const int8_t* d_skip, int skip_type, const float* d_skip_scale,
+                      const float* d_skip_zero_point, const float* d_merge_scale, const float* d_merge_zero_point,
+                      int merge_qmin, int merge_qmax, int merge_type, int merge_flags, void* d_workspace,
+                      size_t workspace_bytes, void* stream) {
+    const char* fn = "lq_conv2d_i8_nhwc";
+    LQ_REQUIRE(N >= 0 && C >= 1 && H >= 1 && W >= 1 && Cout >= 1 && KH >= 1 && KW >= 1 && stride >= 1 && pad >= 0,
+               std::string(fn) + ": bad shape");
+    LQ_REQUIRE(x_code_type == LQ_I8 || x_code_type == LQ_U8S8, std::string(fn) + ": activation codes must be LQ_I8 or LQ_U8S8");
+    LQ_REQUIRE(out_kind == LQ_OUT_Q8 || out_kind == LQ_OUT_QU8 || out_kind == LQ_OUT_QU8S8,
+               std::string(fn) + ": byte codes out (LQ_OUT_Q8 / QU8 / QU8S8)");
+    LQ_REQUIRE((flags & ~LQ_EPI_RELU) == 0 && (merge_flags & ~LQ_EPI_RELU) == 0, std::string(fn) + ": unknown flags");
+    LQ_REQUIRE(x_pad >= pad && y_pad >= 0 && y_pad <= 1, std::string(fn) + ": the input border must cover the padding; "
+                                                                            "an output border of 0 or 1");
+    LQ_REQUIRE(x_cs >= C && x_cs % 16 == 0 && y_cs >= Cout && Cout % 16 == 0,
+               std::string(fn) + ": channel strides: x_cs >= C, a multiple of 16; y_cs >= Cout; Cout a multiple of 16");
+    LQ_REQUIRE(!d_skip || ((skip_type == LQ_I8 || skip_type == LQ_U8 || skip_type == LQ_U8S8) &&
+                           (merge_type == LQ_I8 || merge_type == LQ_U8 || merge_type == LQ_U8S8) && d_skip_scale &&
+                           d_merge_scale),
+               std::string(fn) + ": a skip needs byte code types and its and the merge's scales");
+    int64_t OH = 0, OW = 0;
+    LQ_REQUIRE(conv_geometry(H, W, (int)KH, (int)KW, stride, stride, pad, pad, pad, pad, 1, 1, &OH, &OW),
+               std::string(fn) + ": kernel, stride or padding do not fit the input");
+    if (N == 0) return LQ_OK;
+    LQ_REQUIRE(d_x && d_w_packed && d_w_scale && d_y, std::string(fn) + ": NULL pointer");
+    const bool has_za = d_a_zero_point != nullptr || x_code_type == LQ_U8S8;
+    LQ_REQUIRE(!has_za || d_w_sums, std::string(fn) + ": an activation zero point needs the weight sums d_w_sums");
+    const int64_t Cp = (C + 15) / 16 * 16;
+    LQ_REQUIRE(!conv_taps_form(C, KW) && x_cs == Cp, std::string(fn) + ": the input's channel stride must be C rounded "
+                                                                       "up to 16 (and C above the tap-im2col form)");
+    const ConvPlan plan = conv_plan(N, C, H, W, Cout, KH, KW, pad, pad, pad, pad, OH, OW, 1);
+    if (!plan.dma) return set_error(LQ_ERR_UNSUPPORTED, std::string(fn) + ": this geometry has no LDS-DMA plan");
+    LQ_REQUIRE(plan.part_bytes == 0 || (d_workspace && aligned16(d_workspace) && workspace_bytes >= plan.part_bytes),
+               std::string(fn) + ": workspace smaller than lq_conv2d_i8_nhwc_workspace_size");
+    LQ_REQUIRE(aligned16(d_w_packed) && aligned16(d_x) && aligned16(d_y) && (!d_skip || aligned16(d_skip)) &&
+                   y_cs % 16 == 0,
+               std::string(fn) + ": 16-byte aligned buffers and an output channel stride that is a multiple of 16");
+    // the input buffer's geometry, and the origin the convolution's own padding starts at
+    const int64_t Hpb = H + 2 * x_pad, Wpb = W + 2 * x_pad;
+    const int64_t shift = x_pad - pad;
+    const int8_t* xo = d_x + (shift * Wpb + shift) * Cp;
+    const int64_t xbytes = N * Hpb * Wpb * Cp - (shift * Wpb + shift) * Cp;
+    const int64_t P = N * OH * OW;
+    LQ_REQUIRE(N * Hpb * Wpb * Cp < CV_MAX && P < CV_MAX && N * (OH + 2 * y_pad) * (OW + 2 * y_pad) * y_cs < CV_MAX,
+               std::string(fn) + ": tensors above 2^31 bytes are not supported");
+    const hipStream_t st = as_stream(stream);
+    ConvDmaArgs d{};
+    d.xp = xo;
+    d.wp = d_w_packed;
+    d.y = d_y;  // the padded buffer's first byte: the epilogue adds the border offsets
+    d.xp_bytes = (uint32_t)xbytes;
+    d.Hp = (int)Hpb; d.Wp = (int)Wpb; d.G = 1; d.Cp = (int)Cp;
+    const bool pow2 = Cp <= 128 && (Cp & (Cp - 1)) == 0;
+    d.cp_shift = pow2 ? __builtin_ctz((unsigned)Cp) : -1;
+    d.Cout_g = (int)Cout; d.KH = (int)KH; d.KW = (int)KW; d.sh = stride; d.sw = stride;
+    d.dh = 1; d.dw = 1; d.OH = (int)OH; d.OW = (int)OW; d.P = (int)P;
+    d.nk = (int)(plan.ldw / 128); d.ldw = (int)plan.ldw;
+    d.kw_magic = (int)((65536 + KW - 1) / KW);
+    d.kh_stride = (int)(Wpb * Cp);
+    d.kw_stride = (int)Cp;
+    d.a_scale = d_a_scale; d.a_zp = d_a_zero_point; d.a_u8s8 = x_code_type == LQ_U8S8;
+    d.w_scale = d_w_scale; d.w_sums = d_w_sums; d.bias = d_bias;
+    d.out_scale = d_out_scale; d.out_zp = d_out_zero_point;
+    d.qmin = out_qmin; d.qmax = out_qmax; d.relu = (flags & LQ_EPI_RELU) ? 1 : 0;
+    d.splits = plan.splits;
+    d.part = static_cast<int32_t*>(d_workspace);
+    d.out_nhwc = 1;
+    d.ypad = y_pad;
+    d.ycs = (int)y_cs;
+    d.yrow = (OW + 2 * y_pad) * y_cs;
+    d.yimg = (OH + 2 * y_pad) * d.yrow;
+    d.skip = d_skip;
+    d.skip_type = skip_type;
+    d.skip_scale = d_skip_scale;
+    d.skip_zp = d_skip_zero_point;
+    d.m_scale = d_merge_scale;
+    d.m_zp = d_merge_zero_point;
+    d.m_qmin = merge_qmin;
+    d.m_qmax = merge_qmax;
+    d.m_type = merge_type;
+    d.m_relu = (merge_flags & LQ_EPI_RELU) ? 1 : 0;
+    const dim3 grid((unsigned)plan.gx, (unsigned)plan.gy, 1u);
+    const dim3 grid0((unsigned)plan.gx, (unsigned)plan.gy, (unsigned)plan.splits);
+    ConvDmaArgs d1 = d;
+    d.phase = 0;
+    d1.phase = 1;
+#define LQ_CONV_NHWC(K_)                                                                                        \
+    if (plan.big) {                                                                                              \
+        hipLaunchKernelGGL((conv_i8_dma_kernel<256, 64, 4, 1, 2, K_, true>), grid, dim3(256), 0, st, d);        \
+    } else {                                                                                                     \
+        hipLaunchKernelGGL((conv_i8_dma_kernel<128, 64, 2, 2, CV_SMALL_NBUF, K_, true>), grid0, dim3(256), 0, st, d); \
+        if (plan.splits > 1)                                                                                     \
+            hipLaunchKernelGGL((conv_i8_dma_kernel<128, 64, 2, 2, CV_SMALL_NBUF, K_, true>), grid, dim3(256), 0, st, d1); \
+    }                                                                                                            \
+    break;
+    switch (out_kind) {
+        case LQ_OUT_Q8: LQ_CONV_NHWC(LQ_OUT_Q8)
+        case LQ_OUT_QU8: LQ_CONV_NHWC(LQ_OUT_QU8)
+        default: LQ_CONV_NHWC(LQ_OUT_QU8S8)
+    }
+#undef LQ_CONV_NHWC
+    note_path(plan.big ? "conv nhwc dma 256x64" : plan.splits > 1 ? "conv nhwc dma 128x64 split-k" : "conv nhwc dma 128x64");
+    return launch_status(fn);
 }
 
 int lq_conv2d_f32(const float* d_x, int64_t N, int64_t C, int64_t H, int64_t W, const float* d_w,

@@ -92,3 +92,22 @@ def test_unreplayable_calls_are_refused(gpu):
             CapturedForward(own_stream, warmup=0)
     finally:
         _C.call("lq_stream_destroy", cap_stream)
+
+
+@pytest.mark.parametrize("batch", [2, 32])
+def test_resnet18_nhwc_runtime_is_the_module_forward(gpu, reference_engine, batch):
+    """Int8ResNet (activations padded NHWC between the block convolutions, the residual adds
+    fused into the second convolutions) gives the module forward's bits, eagerly and replayed
+    as one graph, for two inputs."""
+    from lucid_amd.bench_configs import Int8ResNet, static_resnet18
+    from lucid_amd.graphs import CapturedForward
+
+    qnet, x = static_resnet18(batch=batch, calib_batches=2)
+    rt = Int8ResNet(qnet, batch)
+    _same(rt(x).numpy(), qnet(x).numpy())
+    cap = CapturedForward(rt, x)
+    rng = np.random.default_rng(batch)
+    for _ in range(2):
+        x2 = rng.standard_normal(tuple(x.shape)).astype(np.float32)
+        cap.load(x2)
+        _same(cap().numpy(), qnet(gpu.tensor(x2, device="gpu")).numpy())
