@@ -34,6 +34,9 @@ def test_record_stream_holds_a_freed_block_until_the_side_stream_is_done(gpu):
     st = ctypes.c_void_p()
     _C.call("lq_stream_create", ctypes.byref(st))
     try:
+        # blocks earlier tests left in the cache would compete for the same size
+        gpu.synchronize()
+        _C.call("lq_empty_cache")
         B = gpu.tensor(b, device="gpu")
         out = gpu.empty((N, N), np.int32, "gpu")
         # without record_stream: immediate same-size reuse on the null stream
