@@ -135,6 +135,40 @@ typedef _Float16 h4v __attribute__((ext_vector_type(4)));
 typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
+// The same copy, eight consecutive head dims per lane (hd % 8 == 0, 16-byte aligned buffers,
+// fewer than 2^31 vectors): two 16-byte float loads, the same per-element rounding, one
+// 16-byte fp16 store, and 32-bit index arithmetic (the element-wise form's 64-bit divisions
+// cost more than its memory traffic).
+__global__ __launch_bounds__(256) void kv_append_vec_kernel(const float* __restrict__ qkv, uint32_t rows, uint32_t n,
+                                                            uint32_t H, uint32_t hd, int64_t pos0,
+                                                            const int32_t* __restrict__ d_pos0, int64_t T_max,
+                                                            __half* __restrict__ q, __half* __restrict__ kc,
+                                                            __half* __restrict__ vc) {
+    pos0 = position(pos0, d_pos0, T_max - n);
+    const uint32_t hd8 = hd >> 3, hv = H * hd8, per_row = 3 * hv;
+    const uint32_t total = rows * per_row;
+    const f4v* src = reinterpret_cast<const f4v*>(qkv);
+    for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
+        const f4v a = __builtin_nontemporal_load(&src[2 * (size_t)e]);
+        const f4v c = __builtin_nontemporal_load(&src[2 * (size_t)e + 1]);
+        const uint32_t row = e / per_row, w = e - row * per_row;
+        const uint32_t which = w / hv, rem = w - which * hv;
+        const uint32_t h = rem / hd8, d = (rem - h * hd8) * 8;
+        const uint32_t b = row / n, i = row - b * n;
+        h8v o;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const __half lo = f32_to_f16_rn(a[j]), hi = f32_to_f16_rn(c[j]);
+            o[j] = __builtin_bit_cast(_Float16, lo);
+            o[j + 4] = __builtin_bit_cast(_Float16, hi);
+        }
+        const int64_t bh = (int64_t)b * H + h;
+        __half* dst = which == 0 ? q + (bh * n + i) * hd + d
+                                 : (which == 1 ? kc : vc) + (bh * T_max + pos0 + i) * hd + d;
+        *reinterpret_cast<h8v*>(dst) = o;
+    }
+}
+
 // Flash attention over blocks of FA_Q queries (4 waves x 16) on CDNA4 MFMA.  Per block of
 // FA_KB keys, staged in LDS (K rows, and V transposed), each wave computes the score tile
 // S^T = K Q^T with v_mfma_f32_16x16x32_f16 -- a lane then holds 4 keys (4g + i) of one query
@@ -564,6 +598,15 @@ int lq_kv_append_f16(const float* d_qkv, int64_t B, int64_t n, int64_t H, int64_
     if (B == 0 || n == 0) return LQ_OK;
     LQ_REQUIRE(d_qkv && d_q && d_k_cache && d_v_cache, "lq_kv_append_f16: NULL pointer");
     const int64_t total = B * n * 3 * H * hd;
+    const bool vec = hd % 8 == 0 && total / 8 < ((int64_t)1 << 31) && ((uintptr_t)d_qkv & 15) == 0 &&
+                     ((uintptr_t)d_q & 15) == 0 && ((uintptr_t)d_k_cache & 15) == 0 &&
+                     ((uintptr_t)d_v_cache & 15) == 0;
+    if (vec) {
+        hipLaunchKernelGGL(kv_append_vec_kernel, dim3(grid_for(total / 8)), dim3(256), 0, as_stream(stream), d_qkv,
+                           (uint32_t)(B * n), (uint32_t)n, (uint32_t)H, (uint32_t)hd, pos0, d_pos0, T_max,
+                           (__half*)d_q, (__half*)d_k_cache, (__half*)d_v_cache);
+        return launch_status("lq_kv_append_f16");
+    }
     hipLaunchKernelGGL(kv_append_kernel, dim3(grid_for(total)), dim3(256), 0, as_stream(stream), d_qkv, B, n, H, hd, pos0,
                        d_pos0, T_max, (__half*)d_q, (__half*)d_k_cache, (__half*)d_v_cache);
     return launch_status("lq_kv_append_f16");

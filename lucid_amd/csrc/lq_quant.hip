@@ -642,41 +642,48 @@ __device__ __forceinline__ BlockRun block_run(uint32_t n) {
     return BlockRun{b + threadIdx.x, min(n, b + chunk)};
 }
 
+// One group of four codes of quantize_g4_kernel.
 template <class Code, int MODE>
-__global__ __launch_bounds__(kBlock) void quantize_g4_kernel(const float* __restrict__ x,
-                                                             typename Code::T* __restrict__ q,
-                                                             uint32_t n, QArgs qa, Grid g) {
+__device__ __forceinline__ void quantize_group4(typename Group4<Code>::Raw* __restrict__ q4, uint32_t gi, vf4 v,
+                                                const QArgs& qa, Grid g, float t_inv, float t_s, float t_z) {
+    typename Group4<Code>::U o;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        float inv, s, z;
+        group_params<MODE>(qa, gi * 4, j, t_inv, t_s, t_z, inv, s, z);
+        o.v[j] = quant_store<Code>(v[j], inv, z, g);
+    }
+    q4[gi] = o.raw;
+}
+
+constexpr int kG4Inflight = 4 * kGrpUnroll;  // groups in flight per lane
+
+// The body of quantize_g4_kernel with the per-tensor parameters (t_inv, t_s, t_z) given; the
+// lane's first `skip` groups (0 or kG4Inflight) have been quantized by the caller.
+template <class Code, int MODE>
+__device__ __forceinline__ void quantize_g4_run(const float* __restrict__ x, typename Code::T* __restrict__ q,
+                                                uint32_t n, const QArgs& qa, Grid g, float t_inv, float t_s,
+                                                float t_z, uint32_t skip = 0) {
     typedef Group4<Code> G;
     const uint32_t ng = n >> 2;
-    float t_inv = 0.f, t_s = 0.f, t_z = 0.f;
-    if (MODE == PT) qa.tensor(t_inv, t_s, t_z);
     const vf4* x4 = reinterpret_cast<const vf4*>(x);
     typename G::Raw* q4 = reinterpret_cast<typename G::Raw*>(q);
-    auto one = [&](uint32_t gi, vf4 v) __attribute__((always_inline)) {
-        typename G::U o;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            float inv, s, z;
-            group_params<MODE>(qa, gi * 4, j, t_inv, t_s, t_z, inv, s, z);
-            o.v[j] = quant_store<Code>(v[j], inv, z, g);
-        }
-        q4[gi] = o.raw;
-    };
     // Streaming reads bypass the caches (nontemporal); the 4x smaller code stores do not.
     // Sixteen groups in flight per lane (with up to 8192 workgroups): the per-element rounding
     // and clipping would otherwise leave too few loads outstanding to cover HBM latency
     // (measured on 2^28 floats: 8 groups x 4096 workgroups 72-75%, 16 x 8192 77-79% of peak).
-    constexpr int U = 4 * kGrpUnroll;
+    constexpr int U = kG4Inflight;
     const BlockRun r = block_run(ng);
-    uint32_t i = r.i;
+    uint32_t i = r.i + skip * kBlock;
     for (; i + (U - 1) * kBlock < r.end; i += U * kBlock) {
         vf4 v[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(&x4[i + u * kBlock]);
 #pragma unroll
-        for (int u = 0; u < U; ++u) one(i + u * kBlock, v[u]);
+        for (int u = 0; u < U; ++u) quantize_group4<Code, MODE>(q4, i + u * kBlock, v[u], qa, g, t_inv, t_s, t_z);
     }
-    for (; i < r.end; i += kBlock) one(i, __builtin_nontemporal_load(&x4[i]));
+    for (; i < r.end; i += kBlock)
+        quantize_group4<Code, MODE>(q4, i, __builtin_nontemporal_load(&x4[i]), qa, g, t_inv, t_s, t_z);
     if (blockIdx.x == 0 && threadIdx.x < (n & 3)) {
         const uint32_t e = ng * 4 + threadIdx.x;
         float inv, s, z;
@@ -688,6 +695,15 @@ __global__ __launch_bounds__(kBlock) void quantize_g4_kernel(const float* __rest
         }
         q[e] = Code::store(quant_one<Code>(x[e], inv, z, g));
     }
+}
+
+template <class Code, int MODE>
+__global__ __launch_bounds__(kBlock) void quantize_g4_kernel(const float* __restrict__ x,
+                                                             typename Code::T* __restrict__ q,
+                                                             uint32_t n, QArgs qa, Grid g) {
+    float t_inv = 0.f, t_s = 0.f, t_z = 0.f;
+    if (MODE == PT) qa.tensor(t_inv, t_s, t_z);
+    quantize_g4_run<Code, MODE>(x, q, n, qa, g, t_inv, t_s, t_z);
 }
 
 template <class Code, typename Y, int MODE>
@@ -842,6 +858,17 @@ static bool g4_ok(const void* f, const void* c, int64_t n) {
     return aligned16(f) && ((reinterpret_cast<uintptr_t>(c) & ca) == 0) && n < ((int64_t)1 << 32);
 }
 
+static bool g4_ok_code(int q_dtype, const void* f, const void* c, int64_t n) {
+    switch (q_dtype) {
+    case LQ_I8: return g4_ok<CodeI8>(f, c, n);
+    case LQ_U8: return g4_ok<CodeU8>(f, c, n);
+    case LQ_I16: return g4_ok<CodeI16>(f, c, n);
+    case LQ_I32: return g4_ok<CodeI32>(f, c, n);
+    case LQ_U8S8: return g4_ok<CodeU8S8>(f, c, n);
+    default: return false;
+    }
+}
+
 // ------------------------------------------------- dynamic activation quantization
 //
 // The dynamic Linear's activation step (lucid/nn/quantized/dynamic/linear.py:85-92): the live
@@ -898,6 +925,87 @@ __global__ __launch_bounds__(kDynBlock) void dyn_quant_small_kernel(const float*
     const float inv = 1.0f / sc;
     for (int i = tid; i < n; i += kDynBlock) q[i] = Code::store(quant_one<Code>(x[i], inv, z, g));
 }
+
+// Above DYN_SMALL_MAX, with aligned float and code vectors: two launches.  minmax_partial_kernel
+// leaves at most DYN_PARTS_MAX extrema key pairs; every workgroup of dyn_quantize_g4_kernel
+// folds all of them (min / max of keys: any order gives the same pair), derives the qparams
+// with dyn_qparams and quantizes its run of groups as quantize_g4_kernel does with a device
+// scale (inv = 1.0f / s) -- the bits of minmax, calc_qparams and the per-tensor quantize.
+// Workgroup 0 stores {min, max, scale, zero point}.
+constexpr int DYN_PARTS_MAX = 4 * kBlock;
+
+template <class Code>
+__global__ __launch_bounds__(kBlock) void dyn_quantize_g4_kernel(const float* __restrict__ x,
+                                                                 typename Code::T* __restrict__ q, uint32_t n,
+                                                                 const int2* __restrict__ part, int nparts,
+                                                                 float* __restrict__ qp, int qmin, float eps,
+                                                                 float width_f, Grid g) {
+    typedef Group4<Code> G;
+    __shared__ float s_sz[2];
+    constexpr int U = kG4Inflight;
+    const BlockRun r = block_run(n >> 2);
+    const vf4* x4 = reinterpret_cast<const vf4*>(x);
+    // The lane's first U groups are read before the qparams exist: their loads and the
+    // partials' are in flight together, so the fold costs no extra memory round trip.
+    vf4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t i = r.i + u * kBlock;
+        if (i < r.end) v[u] = __builtin_nontemporal_load(&x4[i]);
+    }
+    int2 p[DYN_PARTS_MAX / kBlock];
+#pragma unroll
+    for (int u = 0; u < DYN_PARTS_MAX / kBlock; ++u) {
+        const int i = threadIdx.x + u * kBlock;
+        p[u] = i < nparts ? part[i] : make_int2(KEY_POS_INF, KEY_NEG_INF);
+    }
+    int32_t kmin = p[0].x, kmax = p[0].y;
+#pragma unroll
+    for (int u = 1; u < DYN_PARTS_MAX / kBlock; ++u) {
+        kmin = min(kmin, p[u].x);
+        kmax = max(kmax, p[u].y);
+    }
+    block_reduce_keys(kmin, kmax);
+    if (threadIdx.x == 0) {
+        float o[4];
+        dyn_qparams(kmin, kmax, qmin, eps, width_f, g, o);
+        if (blockIdx.x == 0) {
+            qp[0] = o[0];
+            qp[1] = o[1];
+            qp[2] = o[2];
+            qp[3] = o[3];
+        }
+        s_sz[0] = o[2];
+        s_sz[1] = o[3];
+    }
+    __syncthreads();
+    const float s = s_sz[0], z = s_sz[1], inv = 1.0f / s;
+    const QArgs qa{};
+    typename G::Raw* q4 = reinterpret_cast<typename G::Raw*>(q);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t i = r.i + u * kBlock;
+        if (i < r.end) quantize_group4<Code, PT>(q4, i, v[u], qa, g, inv, s, z);
+    }
+    quantize_g4_run<Code, PT>(x, q, n, qa, g, inv, s, z, U);
+}
+
+// At most 1024 workgroups (four per CU): each lane's first kG4Inflight groups, read before the
+// qparams, cover the whole tensor up to 2^24 elements.
+static dim3 dyn_g4_grid(int64_t n) {
+    const dim3 g = g4_quant_grid(n);
+    return dim3(g.x < 1024u ? g.x : 1024u);
+}
+
+template <class Code>
+struct DynQuantG4 {
+    static int run(const float* x, int64_t n, void* q, const int2* part, int nparts, float* qp, int qmin, float eps,
+                   float width_f, Grid g, hipStream_t st) {
+        hipLaunchKernelGGL(dyn_quantize_g4_kernel<Code>, dyn_g4_grid(n), dim3(kBlock), 0, st, x,
+                           (typename Code::T*)q, (uint32_t)n, part, nparts, qp, qmin, eps, width_f, g);
+        return launch_status("lq_dynamic_quantize_f32");
+    }
+};
 
 template <class Code>
 struct DynQuantSmall {
@@ -1235,6 +1343,17 @@ int lq_dynamic_quantize_f32(const float* d_x, int64_t n, int q_dtype, int qmin, 
     if (n > 0 && n <= DYN_SMALL_MAX) {
         note_path("dynamic quantize fused");
         return dispatch_code<DynQuantSmall>(q_dtype, d_x, n, d_q, d_qparams, qmin, eps, width_f, g, st);
+    }
+    const int parts = minmax_grid(n) < DYN_PARTS_MAX ? minmax_grid(n) : DYN_PARTS_MAX;
+    if (g4_ok_code(q_dtype, d_x, d_q, n)) {
+        LQ_REQUIRE(d_workspace && workspace_bytes >= sizeof(int2) * (size_t)parts,
+                   "lq_dynamic_quantize_f32: workspace too small");
+        note_path("dynamic quantize two-launch");
+        int2* part = static_cast<int2*>(d_workspace);
+        hipLaunchKernelGGL(minmax_partial_kernel, dim3(parts), dim3(kBlock), 0, st, d_x, n, part, true);
+        const int rc = launch_status("lq_dynamic_quantize_f32 extrema");
+        if (rc) return rc;
+        return dispatch_code<DynQuantG4>(q_dtype, d_x, n, d_q, part, parts, d_qparams, qmin, eps, width_f, g, st);
     }
     // the separate launches: observer (replace), qparams, quantize with the device scale
     note_path("dynamic quantize");

@@ -149,6 +149,32 @@ def test_kv_append_and_attention(gpu, B, H, n, pos0, T_max):
     _attention_case(gpu, B, H, n, pos0, T_max, device_pos=True)
 
 
+@pytest.mark.parametrize("hd,off", [(8, 0), (24, 0), (12, 0), (64, 1)])
+def test_kv_append_head_dims(gpu, hd, off):
+    """lq_kv_append_f16 at head dims other than attention's 64: eight dims per lane when hd % 8
+    == 0 and the buffers are 16-byte aligned, element by element otherwise (hd 12, or a qkv
+    buffer one float past alignment) -- the same fp16 bits either way."""
+    from lucid_amd import _C
+
+    B, n, H, T_max, pos0 = 2, 5, 3, 9, 4
+    rng = np.random.default_rng(hd)
+    qkv = (rng.standard_normal((B, n, 3, H, hd)) * 100).astype(np.float32)
+    qkv.flat[::7] = np.float32(65520.0)  # rounds to infinity in fp16
+    buf = _d(gpu, np.concatenate([np.zeros(off, np.float32), qkv.ravel()]))
+    kc = np.zeros((B, H, T_max, hd), np.float16)
+    vc = np.zeros((B, H, T_max, hd), np.float16)
+    dk, dv = _d(gpu, kc), _d(gpu, vc)
+    dq = gpu.empty((B, H, n, hd), np.float16, "gpu")
+    _C.call("lq_kv_append_f16", buf.data_ptr() + 4 * off, B, n, H, hd, pos0, None, T_max, dq.data_ptr(),
+            dk.data_ptr(), dv.data_ptr(), None)
+    q16 = qkv[:, :, 0].transpose(0, 2, 1, 3).astype(np.float16)
+    kc[:, :, pos0:pos0 + n] = qkv[:, :, 1].transpose(0, 2, 1, 3).astype(np.float16)
+    vc[:, :, pos0:pos0 + n] = qkv[:, :, 2].transpose(0, 2, 1, 3).astype(np.float16)
+    np.testing.assert_array_equal(dq.numpy().view(np.uint16), q16.view(np.uint16))
+    np.testing.assert_array_equal(dk.numpy().view(np.uint16), kc.view(np.uint16))
+    np.testing.assert_array_equal(dv.numpy().view(np.uint16), vc.view(np.uint16))
+
+
 def test_attention_rejects_unsupported(gpu):
     from lucid_amd import _C
 

@@ -296,36 +296,44 @@ def _dyn_inputs(n, seed):
     return x
 
 
-@pytest.mark.parametrize("n", [1, 5, 4096, 4097, 16384, 16385, 300000])
+@pytest.mark.parametrize("n", [1, 5, 4096, 4097, 16384, 16385, 300000, 8 * 2**20 + 3])
 @pytest.mark.parametrize("grid", [(0, 255, "U8S8"), (-128, 127, "I8")])
-def test_dynamic_quantize_matches_separate_calls(gpu, n, grid):
-    """lq_dynamic_quantize_f32 (one launch up to 16384 elements, three above) against the
+@pytest.mark.parametrize("offset", [0, 1])
+def test_dynamic_quantize_matches_separate_calls(gpu, n, grid, offset):
+    """lq_dynamic_quantize_f32 (one launch up to 16384 elements; above, two launches when the
+    float and code vectors are aligned -- offset 0 -- else the separate launches) against the
     observer -> qparams -> quantize launches it replaces, and against the oracle: the min, max,
-    scale, zero point and every code the same bits."""
+    scale, zero point and every code the same bits.  8 Mi + 3 elements folds the largest
+    number of extrema partials and quantizes a tail past the last group of four."""
     from lucid_amd import _C
 
+    if offset and n < 16385:
+        pytest.skip("the one-launch form has no alignment condition")
     qmin, qmax, ct = grid
     code_type = getattr(_C, ct)
     x = _dyn_inputs(n, n + abs(qmin))
-    xd = gpu.tensor(x, device="gpu")
+    xbuf = gpu.tensor(np.concatenate([np.zeros(offset, np.float32), x]), device="gpu")
+    xp = xbuf.data_ptr() + 4 * offset
     eps = float(np.float32(1e-8))
     qp = gpu.empty((4,), np.float32, "gpu")
     codes = gpu.empty((n,), np.int8, "gpu")
     ws_bytes = _C.lib().lq_dynamic_quantize_workspace_size(n)
     ws = gpu.empty((max(ws_bytes, 16),), np.uint8, "gpu")
-    _C.call("lq_dynamic_quantize_f32", xd.data_ptr(), n, code_type, qmin, qmax, eps, qp.data_ptr(),
+    _C.call("lq_dynamic_quantize_f32", xp, n, code_type, qmin, qmax, eps, qp.data_ptr(),
             codes.data_ptr(), ws.data_ptr(), ws_bytes, None)
     gpu.synchronize()
-    assert _C.last_path() == ("dynamic quantize fused" if n <= 16384 else "dynamic quantize")
+    want_path = ("dynamic quantize fused" if n <= 16384
+                 else "dynamic quantize" if offset else "dynamic quantize two-launch")
+    assert _C.last_path() == want_path
     # the separate launches
     qp2 = gpu.empty((4,), np.float32, "gpu")
     codes2 = gpu.empty((n,), np.int8, "gpu")
     mm_bytes = _C.lib().lq_minmax_workspace_size(n)
     mm = gpu.empty((mm_bytes,), np.uint8, "gpu")
     p = qp2.data_ptr()
-    _C.call("lq_minmax_f32", xd.data_ptr(), n, p, p + 4, _C.OBS_REPLACE, 0.0, mm.data_ptr(), mm_bytes, None)
+    _C.call("lq_minmax_f32", xp, n, p, p + 4, _C.OBS_REPLACE, 0.0, mm.data_ptr(), mm_bytes, None)
     _C.call("lq_calc_qparams_f32", p, p + 4, 1, 0, int(qmin < 0), qmin, qmax, eps, p + 8, p + 12, None)
-    _C.call("lq_quantize_per_tensor_f32", xd.data_ptr(), codes2.data_ptr(), n, code_type, p + 8, p + 12, 0.0, 0.0,
+    _C.call("lq_quantize_per_tensor_f32", xp, codes2.data_ptr(), n, code_type, p + 8, p + 12, 0.0, 0.0,
             qmin, qmax, None)
     a, b = qp.numpy(), qp2.numpy()
     np.testing.assert_array_equal(a.view(np.uint32), b.view(np.uint32))
@@ -340,13 +348,14 @@ def test_dynamic_quantize_matches_separate_calls(gpu, n, grid):
 
 
 def test_dynamic_quantize_edge_ranges(gpu):
-    """Zero range (all equal), negative-only, NaN and infinities: the fused launch against the
-    separate ones."""
+    """Zero range (all equal), negative-only, NaN and infinities: the fused launches against the
+    separate ones, at one-launch sizes and (tiled past 16384 elements) two-launch sizes."""
     from lucid_amd import _C
 
     eps = float(np.float32(1e-8))
     cases = [np.full(100, 1.5, np.float32), -np.abs(_dyn_inputs(777, 1)), np.zeros(64, np.float32),
              np.array([1.0, np.nan, -2.0, 3.0] * 50, np.float32), np.array([np.inf, -1.0, 2.0] * 30, np.float32)]
+    cases += [np.tile(c, 70000 // c.size + 1) for c in cases]
     for x in cases:
         n = x.size
         xd = gpu.tensor(x, device="gpu")
@@ -355,8 +364,11 @@ def test_dynamic_quantize_edge_ranges(gpu):
             qp = gpu.empty((4,), np.float32, "gpu")
             codes = gpu.empty((n,), np.int8, "gpu")
             if fused:
+                ws_bytes = _C.lib().lq_dynamic_quantize_workspace_size(n)
+                ws = gpu.empty((max(ws_bytes, 16),), np.uint8, "gpu")
                 _C.call("lq_dynamic_quantize_f32", xd.data_ptr(), n, _C.U8S8, 0, 255, eps, qp.data_ptr(),
-                        codes.data_ptr(), None, 0, None)
+                        codes.data_ptr(), ws.data_ptr() if ws_bytes else None, ws_bytes, None)
+                assert _C.last_path() == ("dynamic quantize fused" if n <= 16384 else "dynamic quantize two-launch")
             else:
                 mm_bytes = _C.lib().lq_minmax_workspace_size(n)
                 mm = gpu.empty((mm_bytes,), np.uint8, "gpu")
