@@ -179,10 +179,18 @@ __global__ __launch_bounds__(256) void kv_append_vec_kernel(const float* __restr
 // 4g + i of one dim, so the per-query rescale factors move there by lane shuffles.  Scores,
 // exponentials and the products accumulate in float32 over fp16 q / k / v.  Query i sees keys
 // 0 .. pos0 + i (causal); every query sees key 0, so the running max is finite after the
-// first block.  The next key block is loaded into registers while this one is computed.
-constexpr int FA_Q = 64, FA_KB = 32;
-constexpr int FA_KS = 72;  // K row stride in LDS (halves): 144 B keeps 16-byte rows, staggers banks
-constexpr int FA_VS = 40;  // V^T row stride (halves)
+// first block.  Keys are staged FA_STAGE at a time (four FA_KB blocks per pair of barriers)
+// and the next stage is loaded into registers while this one is computed.  A workgroup of
+// eight waves holds two query blocks, i and nqb - 1 - i (waves 0-3 and 4-7), so under the causal
+// mask every workgroup scores the same number of key blocks and each SIMD runs one wave of
+// each (with one block per workgroup the last blocks' waves did eight times the first's work
+// and set the kernel's time).  The weights are exp2 of scores pre-scaled by log2(e)
+// (v_exp_f32); the softmax's VALU work, not the MFMAs, bounds this kernel.
+constexpr int FA_Q = 64, FA_KB = 32, FA_STAGE = 128, FA_SUB = FA_STAGE / FA_KB;
+constexpr int FA_THREADS = 512;  // two query blocks of four waves
+constexpr int FA_CPT = FA_STAGE * ATT_HD / 8 / FA_THREADS;  // 16-byte K (and V) chunks per thread per stage
+constexpr int FA_KS = 72;   // K row stride in LDS (halves): 144 B keeps 16-byte rows, staggers banks
+constexpr int FA_VS = 136;  // V^T row stride (halves)
 
 __device__ __forceinline__ f4v mfma_16x16x32(h8v a, h8v b, f4v c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
@@ -191,55 +199,72 @@ __device__ __forceinline__ f4v mfma_16x16x16(h4v a, h4v b, f4v c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
-__global__ __launch_bounds__(256) void attention_mfma_kernel(const __half* __restrict__ q, const __half* __restrict__ kc,
+__global__ __launch_bounds__(FA_THREADS) void attention_mfma_kernel(const __half* __restrict__ q, const __half* __restrict__ kc,
                                                              const __half* __restrict__ vc, int64_t B, int64_t H,
                                                              int64_t n, int64_t pos0,
                                                              const int32_t* __restrict__ d_pos0, int64_t T_max,
                                                              float scale, float* __restrict__ out) {
-    __shared__ __attribute__((aligned(16))) _Float16 Ks[FA_KB * FA_KS];  // [key][dim]
-    __shared__ __attribute__((aligned(16))) _Float16 Vt[ATT_HD * FA_VS];  // [dim][key]
+    __shared__ __attribute__((aligned(16))) _Float16 Ks[FA_STAGE * FA_KS];  // [key][dim]
+    __shared__ __attribute__((aligned(16))) _Float16 Vt[ATT_HD * FA_VS];     // [dim][key]
     pos0 = position(pos0, d_pos0, T_max - n);
     const int b = blockIdx.z, h = blockIdx.y;
-    const int64_t q0 = (int64_t)blockIdx.x * FA_Q;
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g = lane >> 4, l16 = lane & 15;
+    const int nqb = (int)((n + FA_Q - 1) / FA_Q);
+    const int qb_hi = nqb - 1 - (int)blockIdx.x;  // >= blockIdx.x
+    const int qb = wave < 4 ? (int)blockIdx.x : qb_hi;
+    const bool active = wave < 4 || qb_hi != (int)blockIdx.x;  // an odd count's middle block once
+    const int64_t q0 = (int64_t)qb * FA_Q;
     const int64_t bh = (int64_t)b * H + h;
-    const int64_t qw = q0 + wave * 16;  // this wave's first query
+    const int64_t qw = q0 + (wave & 3) * 16;  // this wave's first query
     // B operand of S^T: query qw + l16, dims 8g .. 8g + 7 and 32 + 8g .. 32 + 8g + 7
     const _Float16* qrow = reinterpret_cast<const _Float16*>(q) + (bh * n + min(qw + l16, n - 1)) * ATT_HD;
     const h8v qf0 = *reinterpret_cast<const h8v*>(qrow + 8 * g);
     const h8v qf1 = *reinterpret_cast<const h8v*>(qrow + 32 + 8 * g);
     const int64_t qabs = pos0 + qw + l16;  // position of the query this lane scores
-    const int64_t kend = min(pos0 + q0 + FA_Q, pos0 + n);  // keys some query of the block sees
+    // keys some query of this wave's block sees (none for an idle wave), and of either block
+    const int64_t kend_w = active ? min(pos0 + q0 + FA_Q, pos0 + n) : 0;
+    const int64_t kend = min(pos0 + (int64_t)qb_hi * FA_Q + FA_Q, pos0 + n);
+    const float sl2 = scale * 1.44269504088896341f;  // scores in log2 units
     float m_run = -INFINITY, l_run = 0.0f;
     f4v o[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) o[c] = f4v{0.f, 0.f, 0.f, 0.f};
 
-    // staging: thread -> key kk of the block, dims c8 .. c8 + 7
+    // staging: thread -> keys kk + 64 u of the stage, dims c8 .. c8 + 7
     const int kk = tid >> 3, c8 = (tid & 7) * 8;
-    auto fetch = [&](int64_t kb, uint4& kv, uint4& vv) {
-        const int64_t key = kb + kk;
-        kv = uint4{0u, 0u, 0u, 0u};
-        vv = uint4{0u, 0u, 0u, 0u};
-        if (key < kend) {
-            kv = *reinterpret_cast<const uint4*>(kc + (bh * T_max + key) * ATT_HD + c8);
-            vv = *reinterpret_cast<const uint4*>(vc + (bh * T_max + key) * ATT_HD + c8);
+    constexpr int KSTEP = FA_THREADS / 8;
+    auto fetch = [&](int64_t kb, uint4 (&kv)[FA_CPT], uint4 (&vv)[FA_CPT]) __attribute__((always_inline)) {
+#pragma unroll
+        for (int u = 0; u < FA_CPT; ++u) {
+            const int64_t key = kb + kk + KSTEP * u;
+            kv[u] = uint4{0u, 0u, 0u, 0u};
+            vv[u] = uint4{0u, 0u, 0u, 0u};
+            if (key < kend) {
+                kv[u] = *reinterpret_cast<const uint4*>(kc + (bh * T_max + key) * ATT_HD + c8);
+                vv[u] = *reinterpret_cast<const uint4*>(vc + (bh * T_max + key) * ATT_HD + c8);
+            }
         }
     };
-    uint4 kv, vv;
+    uint4 kv[FA_CPT], vv[FA_CPT];
     fetch(0, kv, vv);
-    for (int64_t kb = 0; kb < kend; kb += FA_KB) {
-        *reinterpret_cast<uint4*>(Ks + kk * FA_KS + c8) = kv;
-        const _Float16* vh = reinterpret_cast<const _Float16*>(&vv);
+    for (int64_t kb0 = 0; kb0 < kend; kb0 += FA_STAGE) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) Vt[(c8 + j) * FA_VS + kk] = vh[j];
+        for (int u = 0; u < FA_CPT; ++u) {
+            const int key = kk + KSTEP * u;
+            *reinterpret_cast<uint4*>(Ks + key * FA_KS + c8) = kv[u];
+            const _Float16* vh = reinterpret_cast<const _Float16*>(&vv[u]);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) Vt[(c8 + j) * FA_VS + key] = vh[j];
+        }
         __syncthreads();
-        if (kb + FA_KB < kend) fetch(kb + FA_KB, kv, vv);  // in flight during this block
+        if (kb0 + FA_STAGE < kend) fetch(kb0 + FA_STAGE, kv, vv);  // in flight during this stage
+        for (int sb = 0; sb < FA_SUB && kb0 + FA_KB * sb < kend_w; ++sb) {
+        const int64_t kb = kb0 + FA_KB * sb;
         // S^T tiles: keys kb + 16 t + 4 g + i against query l16
         f4v sc[2];
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-            const _Float16* kr = Ks + (16 * t + l16) * FA_KS;
+            const _Float16* kr = Ks + (FA_KB * sb + 16 * t + l16) * FA_KS;
             f4v acc = f4v{0.f, 0.f, 0.f, 0.f};
             acc = mfma_16x16x32(*reinterpret_cast<const h8v*>(kr + 8 * g), qf0, acc);
             acc = mfma_16x16x32(*reinterpret_cast<const h8v*>(kr + 32 + 8 * g), qf1, acc);
@@ -251,21 +276,21 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const __half* __res
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int64_t key = kb + 16 * t + 4 * g + i;
-                const float v = (key <= qabs && key < kend) ? sc[t][i] * scale : -INFINITY;
+                const float v = (key <= qabs && key < kend_w) ? sc[t][i] * sl2 : -INFINITY;
                 sc[t][i] = v;
                 mb = fmaxf(mb, v);
             }
         mb = fmaxf(mb, __shfl_xor(mb, 16, 64));
         mb = fmaxf(mb, __shfl_xor(mb, 32, 64));
         const float m_new = fmaxf(m_run, mb);
-        const float corr = expf(m_run - m_new);
+        const float corr = __builtin_amdgcn_exp2f(m_run - m_new);
         float ps = 0.0f;
         h4v pa[2], pl[2];  // the weights as fp16 hi + lo: ~22 significant bits into the MFMA
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const float pv = expf(sc[t][i] - m_new);
+                const float pv = __builtin_amdgcn_exp2f(sc[t][i] - m_new);
                 ps += pv;
                 pa[t][i] = (_Float16)pv;
                 pl[t][i] = (_Float16)(pv - (float)pa[t][i]);
@@ -285,17 +310,19 @@ __global__ __launch_bounds__(256) void attention_mfma_kernel(const __half* __res
         for (int t = 0; t < 2; ++t)
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
-                const h4v vb = *reinterpret_cast<const h4v*>(Vt + (16 * c + l16) * FA_VS + 16 * t + 4 * g);
+                const h4v vb =
+                    *reinterpret_cast<const h4v*>(Vt + (16 * c + l16) * FA_VS + FA_KB * sb + 16 * t + 4 * g);
                 o[c] = mfma_16x16x16(pa[t], vb, o[c]);
                 o[c] = mfma_16x16x16(pl[t], vb, o[c]);
             }
+        }
         __syncthreads();
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const float li = __shfl(l_run, 4 * g + i, 64);
         const int64_t qi = qw + 4 * g + i;
-        if (qi < n) {
+        if (active && qi < n) {
             float* orow = out + (((int64_t)b * n + qi) * H + h) * ATT_HD + l16;
 #pragma unroll
             for (int c = 0; c < 4; ++c) orow[16 * c] = o[c][i] / li;
@@ -628,8 +655,9 @@ int lq_attention_f16(const void* d_q, const void* d_k_cache, const void* d_v_cac
         hipLaunchKernelGGL((attention_decode_kernel<false>), dim3((unsigned)H, (unsigned)B), dim3(DEC_THREADS), 0, st,
                            d_q, (__half*)d_k_cache, (__half*)d_v_cache, B, H, pos0, d_pos0, T_max, scale, d_out);
     } else {
-        hipLaunchKernelGGL(attention_mfma_kernel, dim3((unsigned)((n + FA_Q - 1) / FA_Q), (unsigned)H, (unsigned)B),
-                           dim3(256), 0, st, (const __half*)d_q, (const __half*)d_k_cache, (const __half*)d_v_cache,
+        const int64_t nqb = (n + FA_Q - 1) / FA_Q;
+        hipLaunchKernelGGL(attention_mfma_kernel, dim3((unsigned)((nqb + 1) / 2), (unsigned)H, (unsigned)B),
+                           dim3(FA_THREADS), 0, st, (const __half*)d_q, (const __half*)d_k_cache, (const __half*)d_v_cache,
                            B, H, n, pos0, d_pos0, T_max, scale, d_out);
     }
     return launch_status("lq_attention_f16");
