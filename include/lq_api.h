@@ -210,6 +210,20 @@ int lq_layer_norm_quantize_f32(float* d_x, int64_t ldx, const float* d_res, int6
 int lq_dynamic_quantize_f32(const float* d_x, int64_t n, int q_dtype, int qmin, int qmax, float eps,
                             float* d_qparams, void* d_q, void* d_workspace, size_t workspace_bytes,
                             void* stream);
+/* The same composition at any size, the normalized rows kept: lq_layer_norm_f32 (d_res NULL)
+ * or lq_add_layer_norm_f32 (x += res written back first) into y [rows, D] (contiguous), then
+ * lq_dynamic_quantize_f32 of y into codes q [rows, D] and d_qparams {min, max, scale, zero
+ * point} -- the same bits as those calls.  Above 16384 values with a 16-byte aligned y and
+ * codes aligned for four-code groups: two launches (the norm folds the extrema of what it
+ * stores, the quantize folds the workgroups' pairs); otherwise the separate calls.  The input
+ * step of a dynamic Linear after a LayerNorm (nn.LayerNorm -> lucid/nn/quantized/dynamic/
+ * linear.py:85-92) at prefill sizes.  Workspace: lq_layer_norm_dynamic_quantize_workspace_size
+ * bytes. */
+size_t lq_layer_norm_dynamic_quantize_workspace_size(int64_t rows, int64_t D);
+int lq_layer_norm_dynamic_quantize_f32(float* d_x, int64_t ldx, const float* d_res, int64_t ldres, int64_t rows,
+                                       int64_t D, const float* d_gamma, const float* d_beta, float ln_eps, float* d_y,
+                                       int q_dtype, int qmin, int qmax, float eps, float* d_qparams, void* d_q,
+                                       void* d_workspace, size_t workspace_bytes, void* stream);
 
 /* ---- quantize / dequantize / fake-quantize --------------------------------- */
 /* Per-tensor quantize of x[n] to codes q[n] of type q_dtype (LQ_I8, LQ_U8,

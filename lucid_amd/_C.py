@@ -108,6 +108,9 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_dynamic_quantize_workspace_size": (_SZ, [_I64]),
     "lq_dynamic_quantize_f32": (_I, [_P, _I64, _I, _I, _I, _F, _P, _P, _P, _SZ, _P]),
     "lq_layer_norm_quantize_f32": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P, _F, _I, _I, _I, _F, _P, _P, _P]),
+    "lq_layer_norm_dynamic_quantize_workspace_size": (_SZ, [_I64, _I64]),
+    "lq_layer_norm_dynamic_quantize_f32": (_I, [_P, _I64, _P, _I64, _I64, _I64, _P, _P, _F, _P, _I, _I, _I, _F, _P, _P,
+                                               _P, _SZ, _P]),
     "lq_quantize_per_channel_f32": (_I, [_P, _P, _I64, _I64, _I64, _I, _P, _P, _F, _I, _I, _P]),
     "lq_dequantize_per_tensor": (_I, [_P, _I, _P, _I, _I64, _P, _P, _F, _F, _P]),
     "lq_dequantize_per_channel": (_I, [_P, _I, _P, _I, _I64, _I64, _I64, _P, _P, _F, _P]),

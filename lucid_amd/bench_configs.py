@@ -165,12 +165,14 @@ class DynLinear:
         self.mm_ws = empty((self.mm_bytes,), np.uint8, "gpu")
         self.g_bytes = max(max(lib.lq_gemm_w8a8_workspace_size(m, self.N, self.K) for m in (1, max_rows)), 16)
         self.g_ws = empty((self.g_bytes,), np.uint8, "gpu")
+        self.ln_bytes = max(lib.lq_layer_norm_dynamic_quantize_workspace_size(max_rows, self.K), 16)
+        self.ln_ws = empty((self.ln_bytes,), np.uint8, "gpu")
 
     def tensors(self) -> list:
         """Every device tensor a call reads or writes."""
         w = self.w
-        return [t for t in (self.qp, self.codes, self.mm_ws, self.g_ws, self.packed, self.bias, w.codes, w.scale,
-                            w.sums) if t is not None]
+        return [t for t in (self.qp, self.codes, self.mm_ws, self.g_ws, self.ln_ws, self.packed, self.bias, w.codes,
+                            w.scale, w.sums) if t is not None]
 
     EPS = float(np.float32(1e-8))
     LN_FUSED_MAX = 12288  # one-workgroup limit of the fused layer norm + input step
@@ -190,6 +192,14 @@ class DynLinear:
         _C.call("lq_layer_norm_quantize_f32", x, ldx, res, ldres, rows, self.K, None, None, np.float32(1e-5),
                 _C.U8S8, self.qmin, self.qmax, self.EPS, self.qp.data_ptr(), self.codes.data_ptr(), stream)
         return True
+
+    def quantize_ln_rows(self, x: int, ldx: int, res, ldres: int, rows: int, y: int, stream) -> None:
+        """The same step at any row count, the normalized rows stored to ``y`` [rows, K]:
+        lq_layer_norm_dynamic_quantize_f32, the bits of lq_(add_)layer_norm_f32 then
+        lq_dynamic_quantize_f32 (two launches at prefill sizes)."""
+        _C.call("lq_layer_norm_dynamic_quantize_f32", x, ldx, res, ldres, rows, self.K, None, None, np.float32(1e-5),
+                y, _C.U8S8, self.qmin, self.qmax, self.EPS, self.qp.data_ptr(), self.codes.data_ptr(),
+                self.ln_ws.data_ptr(), self.ln_bytes, stream)
 
     ONE_LAUNCH_MK, ONE_LAUNCH_MK_LN = 16384, 8192  # lq_dynamic_linear_packed_f32's limits
 
@@ -330,12 +340,7 @@ class Int8Decoder:
             # sizes the norm runs inside the next Linear's input step (same bits either way)
             res = None if li == 0 else proj
             if not qkv.quantize_ln(h, D, res, D, M, stream):
-                if res is None:
-                    _C.call("lq_layer_norm_f32", h, D, hn, D, M, D, None, None, eps, stream)
-                else:
-                    _C.call("lq_add_layer_norm_f32", h, D, proj, D, hn, D, M, D, None, None, eps, stream)
-                _C.call("lq_dynamic_quantize_f32", hn, M * D, _C.U8S8, qkv.qmin, qkv.qmax, qkv.EPS,
-                        qkv.qp.data_ptr(), qkv.codes.data_ptr(), qkv.mm_ws.data_ptr(), qkv.mm_bytes, stream)
+                qkv.quantize_ln_rows(h, D, res, D, M, hn, stream)
             qkv.gemm(M, self.qkv.data_ptr(), stream)
             if n == 1:  # the step's k / v appended and attended in one launch
                 _C.call("lq_kv_append_attention_f16", self.qkv.data_ptr(), B, H, hd, 0, p, self.Tmax, kc.data_ptr(),
@@ -347,9 +352,7 @@ class Int8Decoder:
                         self.Tmax, np.float32(self.scale), self.att.data_ptr(), stream)
             out(self.att.data_ptr(), M, proj, stream)
             if not up.quantize_ln(h, D, proj, D, M, stream):
-                _C.call("lq_add_layer_norm_f32", h, D, proj, D, hn, D, M, D, None, None, eps, stream)
-                _C.call("lq_dynamic_quantize_f32", hn, M * D, _C.U8S8, up.qmin, up.qmax, up.EPS, up.qp.data_ptr(),
-                        up.codes.data_ptr(), up.mm_ws.data_ptr(), up.mm_bytes, stream)
+                up.quantize_ln_rows(h, D, proj, D, M, hn, stream)
             up.gemm(M, self.up.data_ptr(), stream, gelu=True)  # the GELU in the product's epilogue
             down(self.up.data_ptr(), M, proj, stream)
         # the last position of each sequence: the residual add and layer norm over rows n * D

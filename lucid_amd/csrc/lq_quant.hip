@@ -1007,6 +1007,49 @@ struct DynQuantG4 {
     }
 };
 
+// The norm before a dynamic Linear at prefill sizes, with the first half of its input step:
+// each wave normalizes rows (ln_load / ln_norm, or ln_row_wide past 2048 columns: the bits of
+// layer_norm_kernel, x replaced by x + res first when res is given), stores them to y and
+// folds the stored values into extrema keys; the workgroup's pair goes to part[blockIdx.x]
+// for dyn_quantize_g4_kernel.  At most DYN_PARTS_MAX workgroups, each walking rows
+// gridDim.x * 4 apart.
+template <int MAXC>
+__global__ __launch_bounds__(kBlock) void ln_extrema_kernel(float* x, int64_t ldx, const float* res, int64_t ldres,
+                                                            int rows, int D, const float* __restrict__ gamma,
+                                                            const float* __restrict__ beta, float ln_eps,
+                                                            float* y, int2* __restrict__ part) {
+    constexpr int RPW = kBlock / LN_T;  // rows per workgroup pass
+    const int wave = threadIdx.x / LN_T, t = threadIdx.x % LN_T;
+    int32_t kmin = KEY_POS_INF, kmax = KEY_NEG_INF;
+    for (int r = (int)blockIdx.x * RPW + wave; r < rows; r += (int)gridDim.x * RPW) {
+        float* xr = x + (int64_t)r * ldx;
+        const float* rr = res ? res + (int64_t)r * ldres : nullptr;
+        float* yr = y + (int64_t)r * D;
+        if constexpr (MAXC == 0) {
+            ln_row_wide(xr, rr, true, D, t, gamma, beta, ln_eps, yr);
+            for (int c = t; c < (D + 3) >> 2; c += LN_T)  // the lane's own stores, read back
+                for (int e = 0; e < 4; ++e)
+                    if (4 * c + e < D) key_accum(kmin, kmax, yr[4 * c + e]);
+        } else {
+            float v[4 * MAXC];
+            ln_load<MAXC>(xr, rr, xr, true, D, t, v);
+            ln_norm<MAXC>(v, true, D, t, gamma, beta, ln_eps, yr);
+#pragma unroll
+            for (int j = 0; j < MAXC; ++j)
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    if (4 * (t + LN_T * j) + e < D) key_accum(kmin, kmax, v[4 * j + e]);
+        }
+    }
+    block_reduce_keys(kmin, kmax);
+    if (threadIdx.x == 0) part[blockIdx.x] = make_int2(kmin, kmax);
+}
+
+static int ln_extrema_grid(int64_t rows) {
+    const int64_t g = (rows + kBlock / LN_T - 1) / (kBlock / LN_T);
+    return (int)(g < DYN_PARTS_MAX ? g : DYN_PARTS_MAX);
+}
+
 template <class Code>
 struct DynQuantSmall {
     static int run(const float* x, int64_t n, void* q, float* qp, int qmin, float eps, float width_f, Grid g,
@@ -1379,6 +1422,55 @@ int lq_layer_norm_quantize_f32(float* d_x, int64_t ldx, const float* d_res, int6
     return dispatch_code<DynQuantFused>(q_dtype, d_res ? (int)DQ_LN_RES : (int)DQ_LN, d_x, ldx, d_res, ldres,
                                         (int)rows, (int)D, d_gamma, d_beta, ln_eps, d_q, d_qparams, qmin, eps,
                                         (float)(qmax - qmin), make_grid(qmin, qmax), as_stream(stream));
+}
+
+size_t lq_layer_norm_dynamic_quantize_workspace_size(int64_t rows, int64_t D) {
+    if (rows <= 0 || D <= 0) return 0;
+    const size_t ln = sizeof(int2) * (size_t)ln_extrema_grid(rows);
+    const size_t dq = lq_dynamic_quantize_workspace_size(rows * D);
+    return ln > dq ? ln : dq;
+}
+
+int lq_layer_norm_dynamic_quantize_f32(float* d_x, int64_t ldx, const float* d_res, int64_t ldres, int64_t rows,
+                                       int64_t D, const float* d_gamma, const float* d_beta, float ln_eps, float* d_y,
+                                       int q_dtype, int qmin, int qmax, float eps, float* d_qparams, void* d_q,
+                                       void* d_workspace, size_t workspace_bytes, void* stream) {
+    const char* fn = "lq_layer_norm_dynamic_quantize_f32";
+    LQ_REQUIRE(rows > 0 && D > 0 && D < ((int64_t)1 << 30) && rows <= 0x7fffffff && ldx >= D &&
+                   (!d_res || ldres >= D),
+               std::string(fn) + ": bad shape");
+    LQ_REQUIRE(d_x && d_y && d_qparams && d_q, std::string(fn) + ": NULL pointer");
+    LQ_REQUIRE(valid_code(q_dtype), std::string(fn) + ": bad code dtype");
+    LQ_REQUIRE(qmax > qmin, std::string(fn) + ": qmax <= qmin");
+    LQ_REQUIRE(workspace_bytes >= lq_layer_norm_dynamic_quantize_workspace_size(rows, D) && d_workspace,
+               std::string(fn) + ": workspace too small");
+    const int64_t n = rows * D;
+    hipStream_t st = as_stream(stream);
+    if (n > DYN_SMALL_MAX && g4_ok_code(q_dtype, d_y, d_q, n)) {
+        note_path("layer norm dynamic quantize two-launch");
+        int2* part = static_cast<int2*>(d_workspace);
+        const int grid = ln_extrema_grid(rows);
+        auto go = [&](auto c) {
+            hipLaunchKernelGGL((ln_extrema_kernel<decltype(c)::value>), dim3((unsigned)grid), dim3(kBlock), 0, st, d_x,
+                               ldx, d_res, ldres, (int)rows, (int)D, d_gamma, d_beta, ln_eps, d_y, part);
+        };
+        if (D <= 4 * LN_T) go(std::integral_constant<int, 1>{});
+        else if (D <= 8 * LN_T) go(std::integral_constant<int, 2>{});
+        else if (D <= 16 * LN_T) go(std::integral_constant<int, 4>{});
+        else if (D <= 32 * LN_T) go(std::integral_constant<int, 8>{});
+        else go(std::integral_constant<int, 0>{});
+        const int rc = launch_status(fn);
+        if (rc) return rc;
+        return dispatch_code<DynQuantG4>(q_dtype, d_y, n, d_q, part, grid, d_qparams, qmin, (float)eps,
+                                         (float)(qmax - qmin), make_grid(qmin, qmax), st);
+    }
+    // the separate calls
+    note_path("layer norm dynamic quantize separate");
+    int rc = d_res ? lq_add_layer_norm_f32(d_x, ldx, d_res, ldres, d_y, D, rows, D, d_gamma, d_beta, ln_eps, stream)
+                   : lq_layer_norm_f32(d_x, ldx, d_y, D, rows, D, d_gamma, d_beta, ln_eps, stream);
+    if (rc) return rc;
+    return lq_dynamic_quantize_f32(d_y, n, q_dtype, qmin, qmax, eps, d_qparams, d_q, d_workspace, workspace_bytes,
+                                   stream);
 }
 
 int lq_quantize_per_channel_f32(const float* d_x, void* d_q, int64_t outer, int64_t C,

@@ -283,6 +283,59 @@ def test_layer_norm_quantize_equals_two_calls(gpu, rows, D, with_res):
     assert np.max(np.abs(deq - O.layer_norm(xr).ravel())) <= sc * 0.5 + 1e-4
 
 
+@pytest.mark.parametrize("rows,D,with_res,affine,qoff", [
+    (4096, 512, True, False, 0), (4096, 512, False, True, 0), (5000, 700, True, True, 0), (33, 2560, True, False, 0),
+    (4099, 256, False, False, 0), (8, 512, True, False, 0), (6, 3001, True, True, 1)])
+def test_layer_norm_dynamic_quantize_equals_calls(gpu, rows, D, with_res, affine, qoff):
+    """lq_layer_norm_dynamic_quantize_f32: x (after x += res), the normalized rows y, the codes and
+    the qparams bit for bit those of lq_(add_)layer_norm_f32 followed by lq_dynamic_quantize_f32
+    (two launches above 16384 values with aligned buffers -- 5000 rows fold more rows than
+    workgroups, D 2560 takes the wide norm -- else the separate calls: 4096 values, or codes one
+    byte past alignment)."""
+    from lucid_amd import _C
+
+    print(f"ln dynamic quantize rows={rows} D={D} res={with_res}", flush=True)
+    rng = np.random.default_rng(rows * 7 + D)
+    x = (rng.standard_normal((rows, D)) * 3 + 1).astype(np.float32)
+    x[rows // 2, D // 3] = np.float32(250.0)  # one outlier row sets the range
+    r = rng.standard_normal((rows, D)).astype(np.float32)
+    gam = (rng.standard_normal(D) * 0.5 + 1).astype(np.float32)
+    bet = (rng.standard_normal(D) * 0.1).astype(np.float32)
+    x1, x2, dr, dg, db = _d(gpu, x), _d(gpu, x), _d(gpu, r), _d(gpu, gam), _d(gpu, bet)
+    gp, bp = (dg.data_ptr(), db.data_ptr()) if affine else (None, None)
+    y1, y2 = gpu.empty((rows, D), np.float32, "gpu"), gpu.empty((rows, D), np.float32, "gpu")
+    q1, q2 = gpu.empty((rows * D,), np.int8, "gpu"), gpu.empty((rows * D + 16,), np.int8, "gpu")
+    qp1, qp2 = gpu.empty((4,), np.float32, "gpu"), gpu.empty((4,), np.float32, "gpu")
+    eps_ln, eps = np.float32(1e-5), np.float32(1e-8)
+    ws_n = _C.lib().lq_dynamic_quantize_workspace_size(rows * D)
+    ws = gpu.empty((max(ws_n, 16),), np.uint8, "gpu")
+    if with_res:
+        _C.call("lq_add_layer_norm_f32", x1.data_ptr(), D, dr.data_ptr(), D, y1.data_ptr(), D, rows, D, gp, bp,
+                eps_ln, None)
+    else:
+        _C.call("lq_layer_norm_f32", x1.data_ptr(), D, y1.data_ptr(), D, rows, D, gp, bp, eps_ln, None)
+    _C.call("lq_dynamic_quantize_f32", y1.data_ptr(), rows * D, _C.U8S8, 0, 255, eps, qp1.data_ptr(), q1.data_ptr(),
+            ws.data_ptr(), ws_n, None)
+    ws2_n = _C.lib().lq_layer_norm_dynamic_quantize_workspace_size(rows, D)
+    ws2 = gpu.empty((max(ws2_n, 16),), np.uint8, "gpu")
+    _C.call("lq_layer_norm_dynamic_quantize_f32", x2.data_ptr(), D, dr.data_ptr() if with_res else None, D, rows, D,
+            gp, bp, eps_ln, y2.data_ptr(), _C.U8S8, 0, 255, eps, qp2.data_ptr(), q2.data_ptr() + qoff, ws2.data_ptr(),
+            ws2_n, None)
+    n = rows * D
+    want_path = ("layer norm dynamic quantize two-launch" if n > 16384 and not qoff
+                 else "dynamic quantize fused" if n <= 16384 else "dynamic quantize")
+    assert _C.last_path() == want_path
+    np.testing.assert_array_equal(x1.numpy().view(np.uint32), x2.numpy().view(np.uint32))
+    np.testing.assert_array_equal(y1.numpy().view(np.uint32), y2.numpy().view(np.uint32))
+    np.testing.assert_array_equal(q1.numpy(), q2.numpy()[qoff:qoff + n])
+    np.testing.assert_array_equal(qp1.numpy().view(np.uint32), qp2.numpy().view(np.uint32))
+    # the range came from the data, and the norm matches float64
+    want_y = O.layer_norm(x + r if with_res else x, gam if affine else None, bet if affine else None)
+    assert_close_to_scale(y2.numpy(), want_y, 1e-5)
+    yv = y2.numpy()
+    np.testing.assert_array_equal(qp2.numpy()[:2], np.array([yv.min(), yv.max()], np.float32))
+
+
 def test_layer_norm_quantize_rejects_large(gpu):
     from lucid_amd import _C
 
