@@ -934,7 +934,9 @@ __global__ __launch_bounds__(kDynBlock) void dyn_quant_small_kernel(const float*
 // Workgroup 0 stores {min, max, scale, zero point}.
 constexpr int DYN_PARTS_MAX = 4 * kBlock;
 
-template <class Code>
+// U: groups per lane read ahead, the launch's groups per lane rounded up to a power of two
+// (at most kG4Inflight), so almost every early load is one the lane uses.
+template <class Code, int U>
 __global__ __launch_bounds__(kBlock) void dyn_quantize_g4_kernel(const float* __restrict__ x,
                                                                  typename Code::T* __restrict__ q, uint32_t n,
                                                                  const int2* __restrict__ part, int nparts,
@@ -942,22 +944,26 @@ __global__ __launch_bounds__(kBlock) void dyn_quantize_g4_kernel(const float* __
                                                                  float width_f, Grid g) {
     typedef Group4<Code> G;
     __shared__ float s_sz[2];
-    constexpr int U = kG4Inflight;
     const BlockRun r = block_run(n >> 2);
     const vf4* x4 = reinterpret_cast<const vf4*>(x);
-    // The lane's first U groups are read before the qparams exist: their loads and the
-    // partials' are in flight together, so the fold costs no extra memory round trip.
+    // The partials, then the lane's first U groups, are read before the qparams exist: all
+    // in flight together, so the fold costs no extra memory round trip.  Every load is
+    // unconditional, its index wrapped or clamped into range (a repeated partial changes no
+    // extremum, and wrapping spreads the repeats over the array instead of one hot line;
+    // groups past the run are loaded but not used): with no branch between them the wait for
+    // the partials leaves the group loads, issued after them, outstanding.
+    int2 p[DYN_PARTS_MAX / kBlock];
+#pragma unroll
+    for (int u = 0; u < DYN_PARTS_MAX / kBlock; ++u) {
+        const int i = (int)threadIdx.x + u * kBlock;
+        p[u] = part[i < nparts ? i : i % nparts];
+    }
+    const uint32_t last = (n >> 2) - 1;  // n >= 4 on this path
     vf4 v[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
         const uint32_t i = r.i + u * kBlock;
-        if (i < r.end) v[u] = __builtin_nontemporal_load(&x4[i]);
-    }
-    int2 p[DYN_PARTS_MAX / kBlock];
-#pragma unroll
-    for (int u = 0; u < DYN_PARTS_MAX / kBlock; ++u) {
-        const int i = threadIdx.x + u * kBlock;
-        p[u] = i < nparts ? part[i] : make_int2(KEY_POS_INF, KEY_NEG_INF);
+        v[u] = __builtin_nontemporal_load(&x4[i < last ? i : last]);
     }
     int32_t kmin = p[0].x, kmax = p[0].y;
 #pragma unroll
@@ -997,12 +1003,33 @@ static dim3 dyn_g4_grid(int64_t n) {
     return dim3(g.x < 1024u ? g.x : 1024u);
 }
 
+// Groups per lane of block_run's split over `grid` workgroups, rounded up to a power of two.
+static int dyn_g4_unroll(int64_t n, unsigned grid) {
+    const int64_t ng = n >> 2;
+    const int64_t chunk = ((ng + grid - 1) / grid + kBlock - 1) / kBlock * kBlock;
+    const int64_t per = chunk / kBlock;
+    int u = 1;
+    while (u < per && u < kG4Inflight) u *= 2;
+    return u;
+}
+
 template <class Code>
 struct DynQuantG4 {
     static int run(const float* x, int64_t n, void* q, const int2* part, int nparts, float* qp, int qmin, float eps,
                    float width_f, Grid g, hipStream_t st) {
-        hipLaunchKernelGGL(dyn_quantize_g4_kernel<Code>, dyn_g4_grid(n), dim3(kBlock), 0, st, x,
-                           (typename Code::T*)q, (uint32_t)n, part, nparts, qp, qmin, eps, width_f, g);
+        const dim3 grid = dyn_g4_grid(n);
+        auto go = [&](auto u_c) {
+            hipLaunchKernelGGL((dyn_quantize_g4_kernel<Code, decltype(u_c)::value>), grid, dim3(kBlock), 0, st, x,
+                               (typename Code::T*)q, (uint32_t)n, part, nparts, qp, qmin, eps, width_f, g);
+        };
+        static_assert(kG4Inflight == 16, "unroll choices");
+        switch (dyn_g4_unroll(n, grid.x)) {
+        case 1: go(std::integral_constant<int, 1>{}); break;
+        case 2: go(std::integral_constant<int, 2>{}); break;
+        case 4: go(std::integral_constant<int, 4>{}); break;
+        case 8: go(std::integral_constant<int, 8>{}); break;
+        default: go(std::integral_constant<int, 16>{}); break;
+        }
         return launch_status("lq_dynamic_quantize_f32");
     }
 };
