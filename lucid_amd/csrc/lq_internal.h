@@ -151,6 +151,28 @@ __device__ __forceinline__ void ln_fetch(const float* xr, const float* rr, bool 
         }
 }
 
+// The row's values from v to dst (positions below D): one 16-byte store per chunk when D % 4
+// == 0 and dst is 16-byte aligned, else element by element.
+template <int MAXC>
+__device__ __forceinline__ void ln_store(float* dst, const float (&v)[4 * MAXC], int D, int t) {
+    if ((D & 3) == 0 && (reinterpret_cast<uintptr_t>(dst) & 15) == 0) {
+#pragma unroll
+        for (int j = 0; j < MAXC; ++j) {
+            const int idx = 4 * (t + LN_T * j);
+            if (idx < D)
+                *reinterpret_cast<vf4*>(dst + idx) = vf4{v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]};
+        }
+        return;
+    }
+#pragma unroll
+    for (int j = 0; j < MAXC; ++j)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int idx = 4 * (t + LN_T * j) + e;
+            if (idx < D) dst[idx] = v[4 * j + e];
+        }
+}
+
 // v = x + res (has_res), stored to wb when it is not NULL (the row of x itself for the in-place
 // callers: every load of the row came first).
 template <int MAXC>
@@ -159,15 +181,7 @@ __device__ __forceinline__ void ln_add_store(float (&v)[4 * MAXC], const float (
     if (!has_res) return;
 #pragma unroll
     for (int k = 0; k < 4 * MAXC; ++k) v[k] = v[k] + rv[k];
-    if (wb && act) {
-#pragma unroll
-        for (int j = 0; j < MAXC; ++j)
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                const int idx = 4 * (t + LN_T * j) + e;
-                if (idx < D) wb[idx] = v[4 * j + e];
-            }
-    }
+    if (wb && act) ln_store<MAXC>(wb, v, D, t);
 }
 
 template <int MAXC>
@@ -252,9 +266,9 @@ __device__ __forceinline__ void ln_norm(float (&v)[4 * MAXC], bool act, int D, i
                 if (gamma) a = a * gv[4 * j + e];
                 if (beta) a = a + bv[4 * j + e];
                 v[4 * j + e] = a;
-                if (y) y[idx] = a;
             }
         }
+    if (y) ln_store<MAXC>(y, v, D, t);
 }
 
 // A row too wide for registers: the same order, read from memory on each pass; x + res is
