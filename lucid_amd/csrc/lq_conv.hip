@@ -655,6 +655,33 @@ __device__ __forceinline__ void conv_epilogue(const ConvDmaArgs& a, v4i (&acc)[F
     // lane one pixel and reads its channels back 16 at a time, so the global stores (and the
     // skip loads of a fused residual merge) are 16 contiguous channel bytes of one pixel.
     const int cbase = g * a.Cout_g + co_w;
+    // This lane's pixel of the wave's 64 in the NHWC flush, and (with a residual merge) its
+    // skip codes and the merge's scalars: loaded here, before the accumulators are converted,
+    // so the epilogue's arithmetic and LDS staging cover their one round trip (loaded inside
+    // the flush, each 16-channel group waited for its own).
+    const int fp = pb - (lane >> 4) * 16 + lane;
+    int64_t fpix = 0;
+    int fn = 0, foh = 0, fow = 0;
+    const bool fmerge = nh != nullptr && a.skip != nullptr && fp < a.P;
+    v4i sk[FN];
+    float ss = 0.f, zs = 0.f, mscale = 1.f, mz = 0.f;
+    if (nh != nullptr && fp < a.P) {
+        fn = fp / OHW;
+        const int rem = fp - fn * OHW;
+        foh = rem / a.OW;
+        fow = rem - foh * a.OW;
+        fpix = fn * a.yimg + (int64_t)(foh + a.ypad) * a.yrow + (int64_t)(fow + a.ypad) * a.ycs;
+    }
+    if (fmerge) {
+#pragma unroll
+        for (int k = 0; k < FN; ++k)
+            sk[k] = co_w + 16 * k < a.Cout_g ? *reinterpret_cast<const v4i*>(a.skip + fpix + cbase + 16 * k)
+                                             : v4i{0, 0, 0, 0};
+        ss = a.skip_scale[0];
+        zs = a.skip_zp ? a.skip_zp[0] : 0.0f;
+        mscale = a.m_scale[0];
+        mz = a.m_zp ? a.m_zp[0] : 0.0f;
+    }
     auto stage_nhwc = [&](const int co, const uint32_t* out) __attribute__((always_inline)) {
         v4i w;
 #pragma unroll
@@ -666,19 +693,15 @@ __device__ __forceinline__ void conv_epilogue(const ConvDmaArgs& a, v4i (&acc)[F
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-        const int p = pb - (lane >> 4) * 16 + lane;  // this lane's pixel of the wave's 64
-        if (p >= a.P) return;
-        const int n = p / OHW, rem = p - n * OHW, oh = rem / a.OW, ow = rem - oh * a.OW;
+        if (fp >= a.P) return;
+        const int oh = foh, ow = fow;
         int8_t* y = static_cast<int8_t*>(a.y);
-        const int64_t pix = n * a.yimg + (int64_t)(oh + a.ypad) * a.yrow + (int64_t)(ow + a.ypad) * a.ycs;
-        const bool merge = a.skip != nullptr;
-        float ss = 0.f, zs = 0.f, minv = 1.f, mz = 0.f;
+        const int64_t pix = fpix;
+        const bool merge = fmerge;
+        float minv = 1.f;
         Grid mg{};
         if (merge) {
-            ss = a.skip_scale[0];
-            zs = a.skip_zp ? a.skip_zp[0] : 0.0f;
-            minv = 1.0f / a.m_scale[0];
-            mz = a.m_zp ? a.m_zp[0] : 0.0f;
+            minv = 1.0f / mscale;
             mg = make_grid(a.m_qmin, a.m_qmax);
         }
         const uint32_t zc = merge ? nhwc_zero_code(mz, a.m_type) : nhwc_zero_code(ep.out_z, OT);
@@ -693,20 +716,32 @@ __device__ __forceinline__ void conv_epilogue(const ConvDmaArgs& a, v4i (&acc)[F
             for (int j = 0; j < 16; ++j)
                 w[j >> 2] |= (uint32_t)(uint8_t)nh[(16 * k + j) * NH_ROW + (lane & 63)] << (8 * (j & 3));
             if (merge) {  // merge_bytes16_kernel's arithmetic: dequantize both, add, ReLU, requantize
-                const v4i sk = *reinterpret_cast<const v4i*>(a.skip + off);
+                // the code types and the ReLU as constants for the common form (quint8 skip and
+                // merge with ReLU: 16 values per step without per-value type tests)
+                auto merge16 = [&](auto st_c, auto mt_c, auto relu_c) __attribute__((always_inline)) {
+                    constexpr int ST = decltype(st_c)::value, MT = decltype(mt_c)::value;
+                    constexpr int RELU = decltype(relu_c)::value;
 #pragma unroll
-                for (int d = 0; d < 4; ++d) {
-                    uint32_t o = 0;
+                    for (int d = 0; d < 4; ++d) {
+                        uint32_t o = 0;
 #pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float av = (nhwc_code(w[d] >> (8 * e), OT) - ep.out_z) * ep.out_s;
-                        const float bv = (nhwc_code((uint32_t)sk[d] >> (8 * e), a.skip_type) - zs) * ss;
-                        float t = av + bv;
-                        if (a.m_relu) t = (t <= 0.0f) ? 0.0f : t;
-                        o |= nhwc_store(t, minv, mz, mg, a.m_type) << (8 * e);
+                        for (int e = 0; e < 4; ++e) {
+                            const float av = (nhwc_code(w[d] >> (8 * e), OT) - ep.out_z) * ep.out_s;
+                            const int stype = ST >= 0 ? ST : a.skip_type, mtype = MT >= 0 ? MT : a.m_type;
+                            const float bv = (nhwc_code((uint32_t)sk[k][d] >> (8 * e), stype) - zs) * ss;
+                            float t = av + bv;
+                            if (RELU > 0 || (RELU < 0 && a.m_relu)) t = (t <= 0.0f) ? 0.0f : t;
+                            o |= nhwc_store(t, minv, mz, mg, mtype) << (8 * e);
+                        }
+                        w[d] = o;
                     }
-                    w[d] = o;
-                }
+                };
+                if (a.skip_type == LQ_U8S8 && a.m_type == LQ_U8S8 && a.m_relu)
+                    merge16(std::integral_constant<int, LQ_U8S8>{}, std::integral_constant<int, LQ_U8S8>{},
+                            std::integral_constant<int, 1>{});
+                else
+                    merge16(std::integral_constant<int, -1>{}, std::integral_constant<int, -1>{},
+                            std::integral_constant<int, -1>{});
             }
             *reinterpret_cast<v4i*>(y + off) = v4i{(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
             if (a.ypad) {
