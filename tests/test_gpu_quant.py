@@ -296,19 +296,20 @@ def _dyn_inputs(n, seed):
     return x
 
 
-@pytest.mark.parametrize("n", [1, 5, 4096, 4097, 16384, 16385, 300000, 8 * 2**20 + 3])
+_DYN_CASES = [(n, 0) for n in (1, 5, 4096, 4097, 16384, 16385, 300000, 8 * 2**20 + 3)] + [(16385, 1), (300000, 1)]
+
+
+@pytest.mark.parametrize("n,offset", _DYN_CASES)
 @pytest.mark.parametrize("grid", [(0, 255, "U8S8"), (-128, 127, "I8")])
-@pytest.mark.parametrize("offset", [0, 1])
 def test_dynamic_quantize_matches_separate_calls(gpu, n, grid, offset):
     """lq_dynamic_quantize_f32 (one launch up to 16384 elements; above, two launches when the
-    float and code vectors are aligned -- offset 0 -- else the separate launches) against the
+    float and code vectors are aligned -- offset 0 -- else the separate launches: offset 1
+    starts the input one float past alignment) against the
     observer -> qparams -> quantize launches it replaces, and against the oracle: the min, max,
     scale, zero point and every code the same bits.  8 Mi + 3 elements folds the largest
     number of extrema partials and quantizes a tail past the last group of four."""
     from lucid_amd import _C
 
-    if offset and n < 16385:
-        pytest.skip("the one-launch form has no alignment condition")
     qmin, qmax, ct = grid
     code_type = getattr(_C, ct)
     x = _dyn_inputs(n, n + abs(qmin))
