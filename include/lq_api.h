@@ -728,6 +728,12 @@ int lq_transpose_f32(const float* d_x, int64_t rows, int64_t cols, float* d_y, v
  * caches [B, H, T_max, hd] at positions pos .. pos + n - 1. */
 int lq_kv_append_f16(const float* d_qkv, int64_t B, int64_t n, int64_t H, int64_t hd, int64_t pos0,
                      const int32_t* d_pos0, int64_t T_max, void* d_q, void* d_k_cache, void* d_v_cache, void* stream);
+/* The same layout change from an fp16 qkv (the projection's LQ_OUT_F16 output: each value the
+ * fp16 rounding of the float32 one, so the caches and q hold the bits lq_kv_append_f16 writes
+ * from the float32 output) -- half the bytes read, no conversion.  hd % 8 == 0, 16-byte aligned
+ * buffers. */
+int lq_kv_append_h16(const void* d_qkv, int64_t B, int64_t n, int64_t H, int64_t hd, int64_t pos0,
+                     const int32_t* d_pos0, int64_t T_max, void* d_q, void* d_k_cache, void* d_v_cache, void* stream);
 /* Causal attention over the fp16 cache (F.scaled_dot_product_attention, is_causal): query i of
  * q [B, H, n, hd] sits at position pos + i and sees keys 0 .. pos + i; softmax(scale q.k) v
  * with fp32 scores and sums (fp16 MFMA products for n > 1); out [B, n, H, hd] float32.

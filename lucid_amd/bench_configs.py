@@ -220,15 +220,16 @@ class DynLinear:
                 _C.EPI_GELU if gelu else 0, stream)
         return True
 
-    def gemm(self, rows: int, y: int, stream, gelu: bool = False) -> None:
+    def gemm(self, rows: int, y: int, stream, gelu: bool = False, out_kind: int | None = None) -> None:
         """The int8 product of the codes the last input step left, float32 out (with the tanh
-        GELU of the following float module in its epilogue when ``gelu``)."""
+        GELU of the following float module in its epilogue when ``gelu``; ``out_kind``
+        ``_C.OUT_F16`` rounds the same float32 values to fp16 for a consumer that would)."""
         q = self.qp.data_ptr()
         sx, zx = q + 8, q + 12
         flags = _C.EPI_A_U8S8 | (_C.EPI_GELU if gelu else 0)
         common = (sx, 0, self.w.scale.data_ptr(), 1, zx, None, self.w.sums.data_ptr(),
-                  self.bias.data_ptr() if self.bias is not None else None, None, None, 0, 0, _C.OUT_F32,
-                  flags, self.g_ws.data_ptr(), self.g_bytes, stream)
+                  self.bias.data_ptr() if self.bias is not None else None, None, None, 0, 0,
+                  _C.OUT_F32 if out_kind is None else out_kind, flags, self.g_ws.data_ptr(), self.g_bytes, stream)
         if rows <= 128 and self.packed is not None:
             _C.call("lq_gemm_w8a8_packed", self.codes.data_ptr(), self.K, self.packed.data_ptr(), y, self.N, rows,
                     self.N, self.K, *common)
@@ -341,12 +342,15 @@ class Int8Decoder:
             res = None if li == 0 else proj
             if not qkv.quantize_ln(h, D, res, D, M, stream):
                 qkv.quantize_ln_rows(h, D, res, D, M, hn, stream)
-            qkv.gemm(M, self.qkv.data_ptr(), stream)
             if n == 1:  # the step's k / v appended and attended in one launch
+                qkv.gemm(M, self.qkv.data_ptr(), stream)
                 _C.call("lq_kv_append_attention_f16", self.qkv.data_ptr(), B, H, hd, 0, p, self.Tmax, kc.data_ptr(),
                         vc.data_ptr(), np.float32(self.scale), self.att.data_ptr(), stream)
             else:
-                _C.call("lq_kv_append_f16", self.qkv.data_ptr(), B, n, H, hd, 0, p, self.Tmax, self.q16.data_ptr(),
+                # q / k / v are only read as fp16: the product rounds them in its epilogue (the
+                # float32 values' fp16 bits) and the append moves half the bytes
+                qkv.gemm(M, self.qkv.data_ptr(), stream, out_kind=_C.OUT_F16)
+                _C.call("lq_kv_append_h16", self.qkv.data_ptr(), B, n, H, hd, 0, p, self.Tmax, self.q16.data_ptr(),
                         kc.data_ptr(), vc.data_ptr(), stream)
                 _C.call("lq_attention_f16", self.q16.data_ptr(), kc.data_ptr(), vc.data_ptr(), B, H, n, hd, 0, p,
                         self.Tmax, np.float32(self.scale), self.att.data_ptr(), stream)

@@ -136,10 +136,12 @@ typedef _Float16 h8v __attribute__((ext_vector_type(8)));
 typedef float f4v __attribute__((ext_vector_type(4)));
 
 // The same copy, eight consecutive head dims per lane (hd % 8 == 0, 16-byte aligned buffers,
-// fewer than 2^31 vectors): two 16-byte float loads, the same per-element rounding, one
-// 16-byte fp16 store, and 32-bit index arithmetic (the element-wise form's 64-bit divisions
-// cost more than its memory traffic).
-__global__ __launch_bounds__(256) void kv_append_vec_kernel(const float* __restrict__ qkv, uint32_t rows, uint32_t n,
+// fewer than 2^31 vectors) and 32-bit index arithmetic (the element-wise form's 64-bit
+// divisions cost more than its memory traffic).  F32SRC: two 16-byte float loads and the same
+// per-element rounding; otherwise qkv is already fp16 (the projection's epilogue rounded it
+// the same way) and the lane moves one 16-byte load to one 16-byte store.
+template <bool F32SRC>
+__global__ __launch_bounds__(256) void kv_append_vec_kernel(const void* __restrict__ qkv, uint32_t rows, uint32_t n,
                                                             uint32_t H, uint32_t hd, int64_t pos0,
                                                             const int32_t* __restrict__ d_pos0, int64_t T_max,
                                                             __half* __restrict__ q, __half* __restrict__ kc,
@@ -147,21 +149,25 @@ __global__ __launch_bounds__(256) void kv_append_vec_kernel(const float* __restr
     pos0 = position(pos0, d_pos0, T_max - n);
     const uint32_t hd8 = hd >> 3, hv = H * hd8, per_row = 3 * hv;
     const uint32_t total = rows * per_row;
-    const f4v* src = reinterpret_cast<const f4v*>(qkv);
     for (uint32_t e = blockIdx.x * blockDim.x + threadIdx.x; e < total; e += gridDim.x * blockDim.x) {
-        const f4v a = __builtin_nontemporal_load(&src[2 * (size_t)e]);
-        const f4v c = __builtin_nontemporal_load(&src[2 * (size_t)e + 1]);
+        h8v o;
+        if constexpr (F32SRC) {
+            const f4v* src = static_cast<const f4v*>(qkv);
+            const f4v a = __builtin_nontemporal_load(&src[2 * (size_t)e]);
+            const f4v c = __builtin_nontemporal_load(&src[2 * (size_t)e + 1]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const __half lo = f32_to_f16_rn(a[j]), hi = f32_to_f16_rn(c[j]);
+                o[j] = __builtin_bit_cast(_Float16, lo);
+                o[j + 4] = __builtin_bit_cast(_Float16, hi);
+            }
+        } else {
+            o = __builtin_nontemporal_load(&static_cast<const h8v*>(qkv)[e]);
+        }
         const uint32_t row = e / per_row, w = e - row * per_row;
         const uint32_t which = w / hv, rem = w - which * hv;
         const uint32_t h = rem / hd8, d = (rem - h * hd8) * 8;
         const uint32_t b = row / n, i = row - b * n;
-        h8v o;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const __half lo = f32_to_f16_rn(a[j]), hi = f32_to_f16_rn(c[j]);
-            o[j] = __builtin_bit_cast(_Float16, lo);
-            o[j + 4] = __builtin_bit_cast(_Float16, hi);
-        }
         const int64_t bh = (int64_t)b * H + h;
         __half* dst = which == 0 ? q + (bh * n + i) * hd + d
                                  : (which == 1 ? kc : vc) + (bh * T_max + pos0 + i) * hd + d;
@@ -629,7 +635,7 @@ int lq_kv_append_f16(const float* d_qkv, int64_t B, int64_t n, int64_t H, int64_
                      ((uintptr_t)d_q & 15) == 0 && ((uintptr_t)d_k_cache & 15) == 0 &&
                      ((uintptr_t)d_v_cache & 15) == 0;
     if (vec) {
-        hipLaunchKernelGGL(kv_append_vec_kernel, dim3(grid_for(total / 8)), dim3(256), 0, as_stream(stream), d_qkv,
+        hipLaunchKernelGGL(kv_append_vec_kernel<true>, dim3(grid_for(total / 8)), dim3(256), 0, as_stream(stream), d_qkv,
                            (uint32_t)(B * n), (uint32_t)n, (uint32_t)H, (uint32_t)hd, pos0, d_pos0, T_max,
                            (__half*)d_q, (__half*)d_k_cache, (__half*)d_v_cache);
         return launch_status("lq_kv_append_f16");
@@ -637,6 +643,23 @@ int lq_kv_append_f16(const float* d_qkv, int64_t B, int64_t n, int64_t H, int64_
     hipLaunchKernelGGL(kv_append_kernel, dim3(grid_for(total)), dim3(256), 0, as_stream(stream), d_qkv, B, n, H, hd, pos0,
                        d_pos0, T_max, (__half*)d_q, (__half*)d_k_cache, (__half*)d_v_cache);
     return launch_status("lq_kv_append_f16");
+}
+
+int lq_kv_append_h16(const void* d_qkv, int64_t B, int64_t n, int64_t H, int64_t hd, int64_t pos0,
+                     const int32_t* d_pos0, int64_t T_max, void* d_q, void* d_k_cache, void* d_v_cache, void* stream) {
+    LQ_REQUIRE(B >= 0 && n >= 0 && H > 0 && hd > 0 && pos0 >= 0 && n <= T_max && (d_pos0 || pos0 + n <= T_max),
+               "lq_kv_append_h16: bad shape");
+    if (B == 0 || n == 0) return LQ_OK;
+    LQ_REQUIRE(d_qkv && d_q && d_k_cache && d_v_cache, "lq_kv_append_h16: NULL pointer");
+    const int64_t total = B * n * 3 * H * hd;
+    LQ_REQUIRE(hd % 8 == 0 && total / 8 < ((int64_t)1 << 31) &&
+                   ((reinterpret_cast<uintptr_t>(d_qkv) | reinterpret_cast<uintptr_t>(d_q) |
+                     reinterpret_cast<uintptr_t>(d_k_cache) | reinterpret_cast<uintptr_t>(d_v_cache)) & 15) == 0,
+               "lq_kv_append_h16: hd must be a multiple of 8 and the buffers 16-byte aligned");
+    hipLaunchKernelGGL(kv_append_vec_kernel<false>, dim3(grid_for(total / 8)), dim3(256), 0, as_stream(stream), d_qkv,
+                       (uint32_t)(B * n), (uint32_t)n, (uint32_t)H, (uint32_t)hd, pos0, d_pos0, T_max, (__half*)d_q,
+                       (__half*)d_k_cache, (__half*)d_v_cache);
+    return launch_status("lq_kv_append_h16");
 }
 
 int lq_attention_f16(const void* d_q, const void* d_k_cache, const void* d_v_cache, int64_t B, int64_t H, int64_t n,

@@ -175,6 +175,32 @@ def test_kv_append_head_dims(gpu, hd, off):
     np.testing.assert_array_equal(dv.numpy().view(np.uint16), vc.view(np.uint16))
 
 
+@pytest.mark.parametrize("B,n,H,pos0,T_max", [(8, 512, 8, 0, 640), (2, 37, 3, 5, 64), (1, 1, 1, 10, 16)])
+def test_kv_append_from_fp16_equals_float(gpu, B, n, H, pos0, T_max):
+    """lq_kv_append_h16 on qkv rounded to fp16 writes q and the caches with the bits
+    lq_kv_append_f16 writes from the float32 qkv (the prefill's projection rounds in its
+    epilogue); a misaligned or hd % 8 != 0 call is refused."""
+    from lucid_amd import _C
+
+    hd = 64
+    rng = np.random.default_rng(B * 1000 + n)
+    qkv = (rng.standard_normal((B, n, 3, H, hd)) * 4).astype(np.float32)
+    qkv.flat[::11] = np.float32(70000.0)  # overflows fp16 to infinity in both routes
+    outs = []
+    for src in (qkv, qkv.astype(np.float16)):
+        kc = np.full((B, H, T_max, hd), 0.5, np.float16)
+        dk, dv = _d(gpu, kc), _d(gpu, kc)
+        dq = gpu.empty((B, H, n, hd), np.float16, "gpu")
+        fn = "lq_kv_append_f16" if src.dtype == np.float32 else "lq_kv_append_h16"
+        _C.call(fn, _d(gpu, src).data_ptr(), B, n, H, hd, pos0, None, T_max, dq.data_ptr(), dk.data_ptr(),
+                dv.data_ptr(), None)
+        outs.append([t.numpy().view(np.uint16) for t in (dq, dk, dv)])
+    for a, b in zip(*outs):
+        np.testing.assert_array_equal(a, b)
+    with pytest.raises(_C.LucidError, match="multiple of 8"):
+        _C.call("lq_kv_append_h16", 16, 1, 1, 1, 12, 0, None, 4, 16, 16, 16, None)
+
+
 def test_attention_rejects_unsupported(gpu):
     from lucid_amd import _C
 
