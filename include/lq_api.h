@@ -741,6 +741,18 @@ int lq_kv_append_h16(const void* d_qkv, int64_t B, int64_t n, int64_t H, int64_t
 int lq_attention_f16(const void* d_q, const void* d_k_cache, const void* d_v_cache, int64_t B, int64_t H, int64_t n,
                      int64_t hd, int64_t pos0, const int32_t* d_pos0, int64_t T_max, float scale, float* d_out,
                      void* stream);
+/* lq_attention_f16, then lq_dynamic_quantize_f32 of its output [B, n, H, hd] into codes and
+ * d_qparams {min, max, scale, zero point}: the input step of the dynamic out-projection after
+ * attention (lucid/nn/quantized/dynamic/linear.py:85-92), the same bits as the two calls.  For
+ * n > 1 (the flash kernel) above 16384 values with aligned output and codes, the attention folds
+ * the extrema of what it stores per workgroup and the quantize folds those pairs: two launches
+ * where the calls take three.  Workspace: lq_attention_dynamic_quantize_workspace_size bytes. */
+size_t lq_attention_dynamic_quantize_workspace_size(int64_t B, int64_t H, int64_t n, int64_t hd);
+int lq_attention_dynamic_quantize_f16(const void* d_q, const void* d_k_cache, const void* d_v_cache, int64_t B,
+                                      int64_t H, int64_t n, int64_t hd, int64_t pos0, const int32_t* d_pos0,
+                                      int64_t T_max, float scale, float* d_out, int q_dtype, int qmin, int qmax,
+                                      float eps, float* d_qparams, void* d_codes, void* d_workspace,
+                                      size_t workspace_bytes, void* stream);
 /* One decode step's lq_kv_append_f16 + lq_attention_f16 (n = 1) in one launch: qkv [B, 1, 3,
  * H, hd] float32; k / v rounded to fp16 into the caches at the position, q rounded to fp16,
  * then the attention of that query over keys 0 .. pos; out [B, 1, H, hd] float32.  Same

@@ -132,6 +132,9 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_transpose_f32": (_I, [_P, _I64, _I64, _P, _P]),
     "lq_kv_append_f16": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P]),
     "lq_kv_append_h16": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P]),
+    "lq_attention_dynamic_quantize_workspace_size": (_SZ, [_I64, _I64, _I64, _I64]),
+    "lq_attention_dynamic_quantize_f16": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _F, _P, _I, _I,
+                                               _I, _F, _P, _P, _P, _SZ, _P]),
     "lq_attention_f16": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _F, _P, _P]),
     "lq_increment_i32": (_I, [_P, ctypes.c_int32, _P]),
     "lq_argmax_f32": (_I, [_P, _I64, _I64, _P, _P]),

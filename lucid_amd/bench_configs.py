@@ -267,6 +267,9 @@ class Int8Decoder:
         self.qkv, self.up, self.hl = f32(rows, 3 * self.D), f32(rows, FFN), f32(batch, self.D)
         self.logits = f32(batch, self.V)
         self.q16 = empty((batch, self.H, max_prompt, self.hd), np.float16, "gpu")
+        self.att_bytes = max(_C.lib().lq_attention_dynamic_quantize_workspace_size(batch, self.H, max_prompt, self.hd),
+                             16)
+        self.att_ws = empty((self.att_bytes,), np.uint8, "gpu")  # attention's extrema pairs
         self.cache = [(empty((batch, self.H, self.Tmax, self.hd), np.float16, "gpu"),
                        empty((batch, self.H, self.Tmax, self.hd), np.float16, "gpu")) for _ in self.layers]
         self.prompt = empty((rows,), np.int32, "gpu")
@@ -284,7 +287,7 @@ class Int8Decoder:
             return
         self._streams.add(key)
         bufs = [self.tok, self.posemb, self.h, self.h2, self.hn, self.att, self.proj, self.qkv, self.up, self.hl,
-                self.logits, self.q16, self.prompt, self.next, self.pos]
+                self.logits, self.q16, self.att_ws, self.prompt, self.next, self.pos]
         bufs += [t for kv in self.cache for t in kv]
         bufs += [t for lins in self.layers for lin in lins for t in lin.tensors()] + self.head.tensors()
         for t in bufs:
@@ -352,9 +355,16 @@ class Int8Decoder:
                 qkv.gemm(M, self.qkv.data_ptr(), stream, out_kind=_C.OUT_F16)
                 _C.call("lq_kv_append_h16", self.qkv.data_ptr(), B, n, H, hd, 0, p, self.Tmax, self.q16.data_ptr(),
                         kc.data_ptr(), vc.data_ptr(), stream)
-                _C.call("lq_attention_f16", self.q16.data_ptr(), kc.data_ptr(), vc.data_ptr(), B, H, n, hd, 0, p,
-                        self.Tmax, np.float32(self.scale), self.att.data_ptr(), stream)
-            out(self.att.data_ptr(), M, proj, stream)
+            if n == 1:
+                out(self.att.data_ptr(), M, proj, stream)
+            else:
+                # the attention and the out-projection's input step (its extrema folded where the
+                # attention stores them), then the product
+                _C.call("lq_attention_dynamic_quantize_f16", self.q16.data_ptr(), kc.data_ptr(), vc.data_ptr(), B,
+                        H, n, hd, 0, p, self.Tmax, np.float32(self.scale), self.att.data_ptr(), _C.U8S8, out.qmin,
+                        out.qmax, out.EPS, out.qp.data_ptr(), out.codes.data_ptr(), self.att_ws.data_ptr(),
+                        self.att_bytes, stream)
+                out.gemm(M, proj, stream)
             if not up.quantize_ln(h, D, proj, D, M, stream):
                 up.quantize_ln_rows(h, D, proj, D, M, hn, stream)
             up.gemm(M, self.up.data_ptr(), stream, gelu=True)  # the GELU in the product's epilogue

@@ -205,11 +205,15 @@ __device__ __forceinline__ f4v mfma_16x16x16(h4v a, h4v b, f4v c) {
     return __builtin_amdgcn_mfma_f32_16x16x16f16(a, b, c, 0, 0, 0);
 }
 
+// EXT: also the extrema keys of every value the workgroup stores, one pair per workgroup in
+// part[] (grid order), for the dynamic quantize of the output that follows.
+template <bool EXT>
 __global__ __launch_bounds__(FA_THREADS) void attention_mfma_kernel(const __half* __restrict__ q, const __half* __restrict__ kc,
                                                              const __half* __restrict__ vc, int64_t B, int64_t H,
                                                              int64_t n, int64_t pos0,
                                                              const int32_t* __restrict__ d_pos0, int64_t T_max,
-                                                             float scale, float* __restrict__ out) {
+                                                             float scale, float* __restrict__ out,
+                                                             int2* __restrict__ part) {
     __shared__ __attribute__((aligned(16))) _Float16 Ks[FA_STAGE * FA_KS];  // [key][dim]
     __shared__ __attribute__((aligned(16))) _Float16 Vt[ATT_HD * FA_VS];     // [dim][key]
     pos0 = position(pos0, d_pos0, T_max - n);
@@ -324,6 +328,7 @@ __global__ __launch_bounds__(FA_THREADS) void attention_mfma_kernel(const __half
         }
         __syncthreads();
     }
+    int32_t kmin = KEY_POS_INF, kmax = KEY_NEG_INF;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         const float li = __shfl(l_run, 4 * g + i, 64);
@@ -331,7 +336,28 @@ __global__ __launch_bounds__(FA_THREADS) void attention_mfma_kernel(const __half
         if (active && qi < n) {
             float* orow = out + (((int64_t)b * n + qi) * H + h) * ATT_HD + l16;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) orow[16 * c] = o[c][i] / li;
+            for (int c = 0; c < 4; ++c) {
+                const float v = o[c][i] / li;
+                orow[16 * c] = v;
+                if constexpr (EXT) key_accum(kmin, kmax, v);
+            }
+        }
+    }
+    if constexpr (EXT) {
+        __shared__ int32_t smin[FA_THREADS / 64], smax[FA_THREADS / 64];
+        kmin = wave_min(kmin);
+        kmax = wave_max(kmax);
+        if (lane == 0) {
+            smin[wave] = kmin;
+            smax[wave] = kmax;
+        }
+        __syncthreads();
+        if (tid == 0) {
+            for (int w = 1; w < FA_THREADS / 64; ++w) {
+                kmin = min(kmin, smin[w]);
+                kmax = max(kmax, smax[w]);
+            }
+            part[((int64_t)blockIdx.z * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x] = make_int2(kmin, kmax);
         }
     }
 }
@@ -679,11 +705,56 @@ int lq_attention_f16(const void* d_q, const void* d_k_cache, const void* d_v_cac
                            d_q, (__half*)d_k_cache, (__half*)d_v_cache, B, H, pos0, d_pos0, T_max, scale, d_out);
     } else {
         const int64_t nqb = (n + FA_Q - 1) / FA_Q;
-        hipLaunchKernelGGL(attention_mfma_kernel, dim3((unsigned)((nqb + 1) / 2), (unsigned)H, (unsigned)B),
+        hipLaunchKernelGGL(attention_mfma_kernel<false>, dim3((unsigned)((nqb + 1) / 2), (unsigned)H, (unsigned)B),
                            dim3(FA_THREADS), 0, st, (const __half*)d_q, (const __half*)d_k_cache, (const __half*)d_v_cache,
-                           B, H, n, pos0, d_pos0, T_max, scale, d_out);
+                           B, H, n, pos0, d_pos0, T_max, scale, d_out, nullptr);
     }
     return launch_status("lq_attention_f16");
+}
+
+static int64_t attention_ext_parts(int64_t B, int64_t H, int64_t n) {
+    return ((n + FA_Q - 1) / FA_Q + 1) / 2 * H * B;
+}
+
+size_t lq_attention_dynamic_quantize_workspace_size(int64_t B, int64_t H, int64_t n, int64_t hd) {
+    if (B <= 0 || H <= 0 || n <= 0 || hd <= 0) return 0;
+    const size_t parts = sizeof(int2) * (size_t)attention_ext_parts(B, H, n);
+    const size_t dq = lq_dynamic_quantize_workspace_size(B * n * H * hd);
+    return parts > dq ? parts : dq;
+}
+
+int lq_attention_dynamic_quantize_f16(const void* d_q, const void* d_k_cache, const void* d_v_cache, int64_t B,
+                                      int64_t H, int64_t n, int64_t hd, int64_t pos0, const int32_t* d_pos0,
+                                      int64_t T_max, float scale, float* d_out, int q_dtype, int qmin, int qmax,
+                                      float eps, float* d_qparams, void* d_codes, void* d_workspace,
+                                      size_t workspace_bytes, void* stream) {
+    const char* fn = "lq_attention_dynamic_quantize_f16";
+    LQ_REQUIRE(d_qparams && d_codes && qmax > qmin, std::string(fn) + ": NULL output or qmax <= qmin");
+    LQ_REQUIRE(workspace_bytes >= lq_attention_dynamic_quantize_workspace_size(B, H, n, hd) && d_workspace,
+               std::string(fn) + ": workspace too small");
+    const int64_t total = B * n * H * hd;
+    const int64_t parts = attention_ext_parts(B, H, n);
+    if (n > 1 && hd == ATT_HD && total > 16384 && parts <= DYN_PARTS_MAX &&
+        dyn_parts_ok(q_dtype, d_out, d_codes, total, (int)parts)) {
+        LQ_REQUIRE(B >= 0 && H > 0 && pos0 >= 0 && n <= T_max && (d_pos0 || pos0 + n <= T_max) && B <= 65535 &&
+                       H <= 65535 && d_q && d_k_cache && d_v_cache,
+                   std::string(fn) + ": bad shape or NULL input");
+        note_path("attention dynamic quantize two-launch");
+        const hipStream_t st = as_stream(stream);
+        int2* part = static_cast<int2*>(d_workspace);
+        const int64_t nqb = (n + FA_Q - 1) / FA_Q;
+        hipLaunchKernelGGL(attention_mfma_kernel<true>, dim3((unsigned)((nqb + 1) / 2), (unsigned)H, (unsigned)B),
+                           dim3(FA_THREADS), 0, st, (const __half*)d_q, (const __half*)d_k_cache,
+                           (const __half*)d_v_cache, B, H, n, pos0, d_pos0, T_max, scale, d_out, part);
+        const int rc = launch_status(fn);
+        if (rc) return rc;
+        return dyn_quantize_parts(d_out, total, q_dtype, qmin, qmax, eps, part, (int)parts, d_qparams, d_codes, st);
+    }
+    // the separate calls
+    int rc = lq_attention_f16(d_q, d_k_cache, d_v_cache, B, H, n, hd, pos0, d_pos0, T_max, scale, d_out, stream);
+    if (rc) return rc;
+    return lq_dynamic_quantize_f32(d_out, total, q_dtype, qmin, qmax, eps, d_qparams, d_codes, d_workspace,
+                                   workspace_bytes, stream);
 }
 
 int lq_kv_append_attention_f16(const float* d_qkv, int64_t B, int64_t H, int64_t hd, int64_t pos0,

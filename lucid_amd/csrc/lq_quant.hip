@@ -932,7 +932,7 @@ __global__ __launch_bounds__(kDynBlock) void dyn_quant_small_kernel(const float*
 // with dyn_qparams and quantizes its run of groups as quantize_g4_kernel does with a device
 // scale (inv = 1.0f / s) -- the bits of minmax, calc_qparams and the per-tensor quantize.
 // Workgroup 0 stores {min, max, scale, zero point}.
-constexpr int DYN_PARTS_MAX = 4 * kBlock;
+static_assert(DYN_PARTS_MAX == 4 * kBlock, "four partials per lane in the fold");
 
 // U: groups per lane read ahead, the launch's groups per lane rounded up to a power of two
 // (at most kG4Inflight), so almost every early load is one the lane uses.
@@ -1290,6 +1290,16 @@ static void launch_fq(const float* x, float* y, float* mask, int64_t n, const QA
 static int check_ocl(int64_t outer, int64_t C, int64_t inner) {
     LQ_REQUIRE(outer >= 0 && C >= 1 && inner >= 0, "invalid [outer, C, inner] layout");
     return LQ_OK;
+}
+
+bool dyn_parts_ok(int q_dtype, const void* x, const void* q, int64_t n, int nparts) {
+    return n > 0 && nparts >= 1 && nparts <= DYN_PARTS_MAX && valid_code(q_dtype) && g4_ok_code(q_dtype, x, q, n);
+}
+
+int dyn_quantize_parts(const float* x, int64_t n, int q_dtype, int qmin, int qmax, float eps, const int2* parts,
+                       int nparts, float* qparams, void* q, hipStream_t st) {
+    return dispatch_code<DynQuantG4>(q_dtype, x, n, q, parts, nparts, qparams, qmin, eps, (float)(qmax - qmin),
+                                     make_grid(qmin, qmax), st);
 }
 
 }  // namespace lq

@@ -201,6 +201,50 @@ def test_kv_append_from_fp16_equals_float(gpu, B, n, H, pos0, T_max):
         _C.call("lq_kv_append_h16", 16, 1, 1, 1, 12, 0, None, 4, 16, 16, 16, None)
 
 
+@pytest.mark.parametrize("B,H,n,pos0,T_max,qoff", [(8, 8, 512, 0, 640, 0), (1, 2, 130, 3, 200, 0),
+                                                   (2, 3, 70, 5, 80, 0), (2, 3, 40, 0, 64, 0),
+                                                   (8, 8, 512, 0, 640, 1), (8, 8, 1, 511, 640, 0)])
+def test_attention_dynamic_quantize_equals_calls(gpu, B, H, n, pos0, T_max, qoff):
+    """lq_attention_dynamic_quantize_f16: the attention output, the codes and the qparams bit for
+    bit those of lq_attention_f16 followed by lq_dynamic_quantize_f32 (two launches for the
+    flash kernel above 16384 values with aligned codes; otherwise the calls: 15360 values, codes
+    one byte past alignment, a single query)."""
+    from lucid_amd import _C
+
+    print(f"attention dynamic quantize B={B} H={H} n={n} pos0={pos0} qoff={qoff}", flush=True)
+    hd = 64
+    rng = np.random.default_rng(B * 10 + n)
+    q = rng.standard_normal((B, H, n, hd)).astype(np.float16)
+    kc = rng.standard_normal((B, H, T_max, hd)).astype(np.float16)
+    vc = (rng.standard_normal((B, H, T_max, hd)) * 3).astype(np.float16)
+    dq, dk, dv = _d(gpu, q), _d(gpu, kc), _d(gpu, vc)
+    total = B * n * H * hd
+    scale, eps = np.float32(0.125), np.float32(1e-8)
+    o1, o2 = gpu.empty((B, n, H, hd), np.float32, "gpu"), gpu.empty((B, n, H, hd), np.float32, "gpu")
+    c1, c2 = gpu.empty((total,), np.int8, "gpu"), gpu.empty((total + 16,), np.int8, "gpu")
+    p1, p2 = gpu.empty((4,), np.float32, "gpu"), gpu.empty((4,), np.float32, "gpu")
+    ws1_n = max(_C.lib().lq_dynamic_quantize_workspace_size(total), 16)
+    ws1 = gpu.empty((ws1_n,), np.uint8, "gpu")
+    _C.call("lq_attention_f16", dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, H, n, hd, pos0, None, T_max, scale,
+            o1.data_ptr(), None)
+    _C.call("lq_dynamic_quantize_f32", o1.data_ptr(), total, _C.U8S8, 0, 255, eps, p1.data_ptr(), c1.data_ptr(),
+            ws1.data_ptr(), ws1_n, None)
+    ws2_n = _C.lib().lq_attention_dynamic_quantize_workspace_size(B, H, n, hd)
+    ws2 = gpu.empty((max(ws2_n, 16),), np.uint8, "gpu")
+    _C.call("lq_attention_dynamic_quantize_f16", dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), B, H, n, hd, pos0,
+            None, T_max, scale, o2.data_ptr(), _C.U8S8, 0, 255, eps, p2.data_ptr(), c2.data_ptr() + qoff,
+            ws2.data_ptr(), ws2_n, None)
+    two = n > 1 and total > 16384 and not qoff
+    want = ("attention dynamic quantize two-launch" if two
+            else "dynamic quantize fused" if total <= 16384 else "dynamic quantize")
+    assert _C.last_path() == want
+    np.testing.assert_array_equal(o1.numpy().view(np.uint32), o2.numpy().view(np.uint32))
+    np.testing.assert_array_equal(c1.numpy(), c2.numpy()[qoff:qoff + total])
+    np.testing.assert_array_equal(p1.numpy().view(np.uint32), p2.numpy().view(np.uint32))
+    ov = o2.numpy()
+    np.testing.assert_array_equal(p2.numpy()[:2], np.array([ov.min(), ov.max()], np.float32))
+
+
 def test_attention_rejects_unsupported(gpu):
     from lucid_amd import _C
 
