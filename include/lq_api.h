@@ -333,6 +333,21 @@ int lq_gemm_w8a8_noalloc(const int8_t* d_A, int64_t lda, const int8_t* d_B, int6
                          const int32_t* d_b_sums, const float* d_bias, const float* d_out_scale,
                          const float* d_out_zero_point, int out_qmin, int out_qmax, int out_kind,
                          int flags, void* stream);
+/* lq_gemm_w8a8 with float32 output y [M, N] (contiguous; bias, LQ_EPI_GELU / LQ_EPI_RELU /
+ * LQ_EPI_A_U8S8 as there), then lq_dynamic_quantize_f32 of y into codes [M N] and d_qparams
+ * {min, max, scale, zero point}: a dynamic Linear's product followed by the next dynamic
+ * Linear's input step (lucid/nn/quantized/dynamic/linear.py:85-92), the same bits as the two
+ * calls.  Where the product takes an LDS-DMA kernel with at most 1024 workgroups (and y and the
+ * codes are aligned), its epilogue folds the extrema of what it stores per workgroup and the
+ * quantize folds those pairs: two launches where the calls take three.  Workspace:
+ * lq_gemm_w8a8_dynamic_quantize_workspace_size bytes (the product's workspace first). */
+size_t lq_gemm_w8a8_dynamic_quantize_workspace_size(int64_t M, int64_t N, int64_t K);
+int lq_gemm_w8a8_dynamic_quantize(const int8_t* d_A, int64_t lda, const int8_t* d_B, int64_t ldb, float* d_y,
+                                  int64_t M, int64_t N, int64_t K, const float* d_a_scale, int64_t a_scale_stride,
+                                  const float* d_b_scale, int64_t b_scale_stride, const float* d_a_zero_point,
+                                  const float* d_b_zero_point, const int32_t* d_b_sums, const float* d_bias, int flags,
+                                  int q_dtype, int qmin, int qmax, float eps, float* d_qparams, void* d_codes,
+                                  void* d_workspace, size_t workspace_bytes, void* stream);
 /* ---- MFMA-packed weights for decode (M <= 128) ------------------------------ */
 /* Bytes of the packed form of an int8 weight B [N, K]: ceil(N/16) x ceil(K/64) tiles of
  * 1 KB.  Tile (t, s) sits at byte (t * ceil(K/64) + s) * 1024; its 16-byte chunk l holds

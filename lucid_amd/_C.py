@@ -133,6 +133,9 @@ _SIGNATURES: dict[str, tuple] = {
     "lq_kv_append_f16": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P]),
     "lq_kv_append_h16": (_I, [_P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _P, _P, _P, _P]),
     "lq_attention_dynamic_quantize_workspace_size": (_SZ, [_I64, _I64, _I64, _I64]),
+    "lq_gemm_w8a8_dynamic_quantize_workspace_size": (_SZ, [_I64, _I64, _I64]),
+    "lq_gemm_w8a8_dynamic_quantize": (_I, [_P, _I64, _P, _I64, _P, _I64, _I64, _I64, _P, _I64, _P, _I64, _P, _P, _P,
+                                           _P, _I, _I, _I, _I, _F, _P, _P, _P, _SZ, _P]),
     "lq_attention_dynamic_quantize_f16": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _F, _P, _I, _I,
                                                _I, _F, _P, _P, _P, _SZ, _P]),
     "lq_attention_f16": (_I, [_P, _P, _P, _I64, _I64, _I64, _I64, _I64, _P, _I64, _F, _P, _P]),

@@ -167,12 +167,14 @@ class DynLinear:
         self.g_ws = empty((self.g_bytes,), np.uint8, "gpu")
         self.ln_bytes = max(lib.lq_layer_norm_dynamic_quantize_workspace_size(max_rows, self.K), 16)
         self.ln_ws = empty((self.ln_bytes,), np.uint8, "gpu")
+        self.gq_bytes = max(lib.lq_gemm_w8a8_dynamic_quantize_workspace_size(max_rows, self.N, self.K), 16)
+        self.gq_ws = empty((self.gq_bytes,), np.uint8, "gpu")
 
     def tensors(self) -> list:
         """Every device tensor a call reads or writes."""
         w = self.w
-        return [t for t in (self.qp, self.codes, self.mm_ws, self.g_ws, self.ln_ws, self.packed, self.bias, w.codes,
-                            w.scale, w.sums) if t is not None]
+        return [t for t in (self.qp, self.codes, self.mm_ws, self.g_ws, self.ln_ws, self.gq_ws, self.packed, self.bias,
+                            w.codes, w.scale, w.sums) if t is not None]
 
     EPS = float(np.float32(1e-8))
     LN_FUSED_MAX = 12288  # one-workgroup limit of the fused layer norm + input step
@@ -219,6 +221,17 @@ class DynLinear:
                 self.bias.data_ptr() if self.bias is not None else None, self.N, y, self.N,
                 _C.EPI_GELU if gelu else 0, stream)
         return True
+
+    def gemm_quantize(self, rows: int, y: int, nxt: "DynLinear", stream, gelu: bool = False) -> None:
+        """The product into float32 ``y`` [rows, N] and, from it, ``nxt``'s input step (its codes
+        and qparams): lq_gemm_w8a8_dynamic_quantize, the bits of :meth:`gemm` followed by
+        ``lq_dynamic_quantize_f32`` on ``y``."""
+        q = self.qp.data_ptr()
+        _C.call("lq_gemm_w8a8_dynamic_quantize", self.codes.data_ptr(), self.K, self.w.codes.data_ptr(), self.K, y,
+                rows, self.N, self.K, q + 8, 0, self.w.scale.data_ptr(), 1, q + 12, None, self.w.sums.data_ptr(),
+                self.bias.data_ptr() if self.bias is not None else None,
+                _C.EPI_A_U8S8 | (_C.EPI_GELU if gelu else 0), _C.U8S8, nxt.qmin, nxt.qmax, nxt.EPS,
+                nxt.qp.data_ptr(), nxt.codes.data_ptr(), self.gq_ws.data_ptr(), self.gq_bytes, stream)
 
     def gemm(self, rows: int, y: int, stream, gelu: bool = False, out_kind: int | None = None) -> None:
         """The int8 product of the codes the last input step left, float32 out (with the tanh
@@ -367,8 +380,14 @@ class Int8Decoder:
                 out.gemm(M, proj, stream)
             if not up.quantize_ln(h, D, proj, D, M, stream):
                 up.quantize_ln_rows(h, D, proj, D, M, hn, stream)
-            up.gemm(M, self.up.data_ptr(), stream, gelu=True)  # the GELU in the product's epilogue
-            down(self.up.data_ptr(), M, proj, stream)
+            if n == 1:
+                up.gemm(M, self.up.data_ptr(), stream, gelu=True)  # the GELU in the product's epilogue
+                down(self.up.data_ptr(), M, proj, stream)
+            else:
+                # the up projection (GELU in its epilogue) folds its output's extrema for the down
+                # projection's input step
+                up.gemm_quantize(M, self.up.data_ptr(), down, stream, gelu=True)
+                down.gemm(M, proj, stream)
         # the last position of each sequence: the residual add and layer norm over rows n * D
         # apart (only those rows of h are read again), then the head
         hl, pl = h + (n - 1) * D * 4, proj + (n - 1) * D * 4

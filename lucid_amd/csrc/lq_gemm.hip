@@ -58,6 +58,7 @@ struct GemmArgs {
     int32_t* partial;        // split-K: [M,N] int32 accumulation buffer (zeroed)
     uint32_t* counters;      // split-K: one arrival counter per output tile (zeroed)
     int splits;              // split-K factor (1 = none)
+    int2* extrema;           // float32 out, LDS-DMA kernels: per-workgroup extrema keys of the stored values
 };
 
 // ------------------------------------------------------------------ epilogue
@@ -650,6 +651,7 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N >= 8 ? 2 : 1))) void gemm_i
 
     // One 64-column half HF of the wave tile at a time: acc[4 HF + i][j][r] is
     // C[mr0 + 16 j][nc0 + 4 i + r].
+    int32_t ext_min = KEY_POS_INF, ext_max = KEY_NEG_INF;  // float32 out with a.extrema
     auto epilogue_half = [&](auto h_c) __attribute__((always_inline)) {
         constexpr int HF = decltype(h_c)::value;
         const int ncw = n0 + wn * WN + HF * 64;  // first column of this 64-column half
@@ -828,6 +830,13 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N >= 8 ? 2 : 1))) void gemm_i
                                                a.gelu != 0);
                     }
                 }
+                if constexpr (KIND == LQ_OUT_F32) {
+                    if (a.extrema && m < a.M) {
+#pragma unroll
+                        for (int q = 0; q < 16; ++q)
+                            if (nc0 + q < a.N) key_accum(ext_min, ext_max, __uint_as_float(out[q]));
+                    }
+                }
                 store_row(j, out);
             });
         };
@@ -841,6 +850,25 @@ __attribute__((amdgpu_waves_per_eu(WAVES_M * WAVES_N >= 8 ? 2 : 1))) void gemm_i
     };
     epilogue_half(std::integral_constant<int, 0>());
     if constexpr (NH > 1) epilogue_half(std::integral_constant<int, 1>());
+    if constexpr (KIND == LQ_OUT_F32) {
+        if (a.extrema) {  // the workgroup's pair of keys, for a dynamic quantize of the output
+            __shared__ int32_t emin[NW], emax[NW];
+            ext_min = wave_min(ext_min);
+            ext_max = wave_max(ext_max);
+            if (lane == 0) {
+                emin[wave] = ext_min;
+                emax[wave] = ext_max;
+            }
+            __syncthreads();
+            if (threadIdx.x == 0) {
+                for (int w = 1; w < NW; ++w) {
+                    ext_min = min(ext_min, emin[w]);
+                    ext_max = max(ext_max, emax[w]);
+                }
+                a.extrema[blockIdx.x] = make_int2(ext_min, ext_max);
+            }
+        }
+    }
 }
 
 // ------------------------------------------------------ skinny-M (decode) kernel
@@ -1432,12 +1460,27 @@ __global__ __launch_bounds__(256) void row_sums_i8_kernel(const int8_t* __restri
 
 // ------------------------------------------------------------------- dispatch
 
+// With a.extrema (float32 out): only the LDS-DMA kernels fold their output's extrema, into at
+// most DYN_PARTS_MAX pairs; any other route returns LQ_ERR_UNSUPPORTED before launching
+// anything (the caller then runs the product and the dynamic quantize as separate calls), and
+// *ext_parts receives the number of pairs written.
+constexpr int GEMM_NO_EXTREMA = LQ_ERR_UNSUPPORTED;
+
 template <int KIND>
 struct GemmLaunch {
-    static int run(const GemmArgs& a0, hipStream_t st, int64_t workspace_split_bytes) {
+    static int run(const GemmArgs& a0, hipStream_t st, int64_t workspace_split_bytes, int* ext_parts = nullptr) {
         GemmArgs a = a0;
         const bool vec = aligned16(a.A) && aligned16(a.B) && (a.lda % 16 == 0) && (a.ldb % 16 == 0) &&
                          (a.K % 16 == 0);
+        const bool dma_ok = (a.K % 128 == 0) && ((int64_t)(a.M + 256) * a.lda < (int64_t)1 << 31) &&
+                            ((int64_t)(a.N + 256) * a.ldb < (int64_t)1 << 31);
+        const int64_t tiles128 = ((int64_t)(a.M + 127) / 128) * ((a.N + 127) / 128);
+        if (a.extrema) {
+            // the route must be one of the DMA kernels below, with few enough workgroups
+            if (KIND != LQ_OUT_F32 || !vec || a.M <= 64 || (a.M <= 128 && tiles128 < 128) || !dma_ok ||
+                tiles128 < 128 || tiles128 > DYN_PARTS_MAX)
+                return GEMM_NO_EXTREMA;
+        }
         if (!vec) {
             const int64_t total = (int64_t)a.M * a.N;
             hipLaunchKernelGGL(gemm_i8_generic_kernel<KIND>, dim3((unsigned)((total + 255) / 256)),
@@ -1463,28 +1506,27 @@ struct GemmLaunch {
             note_path("gemm skinny");
             return launch_status("lq_gemm_w8a8 (skinny)");
         }
-        const int64_t tiles128 = ((int64_t)(a.M + 127) / 128) * ((a.N + 127) / 128);
         if (a.M <= 128 && tiles128 < 128) {
             hipLaunchKernelGGL((gemm_i8_skinny_kernel<8, 8, KIND, 2>), dim3((unsigned)((a.N + 15) / 16)),
                                dim3(512), 0, st, a);
             note_path("gemm skinny");
             return launch_status("lq_gemm_w8a8 (skinny)");
         }
-        // LDS-DMA path: whole 128-byte K stages, 32-bit buffer offsets.
-        const bool dma_ok = (a.K % 128 == 0) && ((int64_t)(a.M + 256) * a.lda < (int64_t)1 << 31) &&
-                            ((int64_t)(a.N + 256) * a.ldb < (int64_t)1 << 31);
+        // LDS-DMA path: whole 128-byte K stages, 32-bit buffer offsets (dma_ok above).
         const int64_t dma_tiles = ((int64_t)(a.M + 255) / 256) * ((a.N + 127) / 128);
         // 256x256 tiles (8 waves of 128x64: a third fewer LDS fragment bytes per MFMA) take
         // ~15% less time per op than 256x128 tiles (waves of 64x64) but come in half as many
         // workgroups: compare the two in rounds of 256 workgroups (one per CU).
         const int64_t t256 = ((int64_t)(a.M + 255) / 256) * ((a.N + 255) / 256);
         if (dma_ok && t256 >= 256 && ((t256 + 255) / 256) * 100 <= ((dma_tiles + 255) / 256) * 57) {
+            if (ext_parts) *ext_parts = (int)t256;
             hipLaunchKernelGGL((gemm_i8_dma_kernel<256, 256, 2, 4, GEMM_NBUF, KIND>), dim3((unsigned)t256),
                                dim3(512), 0, st, a);
             note_path("gemm dma 256x256");
             return launch_status("lq_gemm_w8a8 (dma 256x256)");
         }
         if (dma_ok && dma_tiles >= 256) {
+            if (ext_parts) *ext_parts = (int)dma_tiles;
             hipLaunchKernelGGL((gemm_i8_dma_kernel<256, 128, 4, 2, GEMM_NBUF, KIND>), dim3((unsigned)dma_tiles),
                                dim3(512), 0, st, a);
             note_path("gemm dma 256x128");
@@ -1492,6 +1534,7 @@ struct GemmLaunch {
         }
         const int64_t dma_tiles_128 = ((int64_t)(a.M + 127) / 128) * ((a.N + 127) / 128);
         if (dma_ok && dma_tiles_128 >= 128) {
+            if (ext_parts) *ext_parts = (int)dma_tiles_128;
             hipLaunchKernelGGL((gemm_i8_dma_kernel<128, 128, 4, 2, GEMM_NBUF, KIND>), dim3((unsigned)dma_tiles_128),
                                dim3(512), 0, st, a);
             note_path("gemm dma 128x128");
@@ -1593,7 +1636,7 @@ static int gemm_entry(bool packed, const int8_t* d_A, int64_t lda, const int8_t*
                       const float* d_a_zero_point, const float* d_b_zero_point, const int32_t* d_b_sums,
                       const float* d_bias, const float* d_out_scale, const float* d_out_zero_point,
                       int out_qmin, int out_qmax, int out_kind, int flags, void* d_workspace,
-                      size_t workspace_bytes, void* stream) {
+                      size_t workspace_bytes, void* stream, int2* extrema = nullptr, int* ext_parts = nullptr) {
     LQ_REQUIRE(M >= 0 && N >= 0 && K >= 0, "lq_gemm_w8a8: negative size");
     LQ_REQUIRE(M <= 0x7fffffff && N <= 0x7fffffff && K <= 0x7fffffff, "lq_gemm_w8a8: size too large");
     if (M == 0 || N == 0) return LQ_OK;
@@ -1653,6 +1696,8 @@ static int gemm_entry(bool packed, const int8_t* d_A, int64_t lda, const int8_t*
     a.gelu = (flags & LQ_EPI_GELU) ? 1 : 0;
     a.a_u8s8 = (flags & LQ_EPI_A_U8S8) ? 1 : 0;
     a.splits = 1;
+    a.extrema = extrema;
+    if (extrema && (packed || out_kind != LQ_OUT_F32)) return GEMM_NO_EXTREMA;
     char* wsb = (char*)d_workspace;
     int rc;
     if (need_asums) {
@@ -1691,7 +1736,7 @@ static int gemm_entry(bool packed, const int8_t* d_A, int64_t lda, const int8_t*
     }
     switch (out_kind) {
     case LQ_OUT_I32: return GemmLaunch<LQ_OUT_I32>::run(a, st, split_bytes);
-    case LQ_OUT_F32: return GemmLaunch<LQ_OUT_F32>::run(a, st, split_bytes);
+    case LQ_OUT_F32: return GemmLaunch<LQ_OUT_F32>::run(a, st, split_bytes, ext_parts);
     case LQ_OUT_F16: return GemmLaunch<LQ_OUT_F16>::run(a, st, split_bytes);
     case LQ_OUT_Q8: return GemmLaunch<LQ_OUT_Q8>::run(a, st, split_bytes);
     case LQ_OUT_QU8: return GemmLaunch<LQ_OUT_QU8>::run(a, st, split_bytes);
@@ -1717,6 +1762,49 @@ int lq_gemm_w8a8(const int8_t* d_A, int64_t lda, const int8_t* d_B, int64_t ldb,
                       b_scale_stride, d_a_zero_point, d_b_zero_point, d_b_sums, d_bias, d_out_scale,
                       d_out_zero_point, out_qmin, out_qmax, out_kind, flags, d_workspace, workspace_bytes,
                       stream);
+}
+
+size_t lq_gemm_w8a8_dynamic_quantize_workspace_size(int64_t M, int64_t N, int64_t K) {
+    if (M <= 0 || N <= 0 || K < 0) return 0;
+    const size_t g = (lq_gemm_w8a8_workspace_size(M, N, K) + 255) & ~(size_t)255;
+    const size_t parts = sizeof(int2) * DYN_PARTS_MAX, dq = lq_dynamic_quantize_workspace_size(M * N);
+    return g + (parts > dq ? parts : dq);
+}
+
+int lq_gemm_w8a8_dynamic_quantize(const int8_t* d_A, int64_t lda, const int8_t* d_B, int64_t ldb, float* d_y,
+                                  int64_t M, int64_t N, int64_t K, const float* d_a_scale, int64_t a_scale_stride,
+                                  const float* d_b_scale, int64_t b_scale_stride, const float* d_a_zero_point,
+                                  const float* d_b_zero_point, const int32_t* d_b_sums, const float* d_bias, int flags,
+                                  int q_dtype, int qmin, int qmax, float eps, float* d_qparams, void* d_codes,
+                                  void* d_workspace, size_t workspace_bytes, void* stream) {
+    const char* fn = "lq_gemm_w8a8_dynamic_quantize";
+    LQ_REQUIRE(M > 0 && N > 0 && d_y && d_qparams && d_codes && qmax > qmin, std::string(fn) + ": bad arguments");
+    LQ_REQUIRE(d_workspace && workspace_bytes >= lq_gemm_w8a8_dynamic_quantize_workspace_size(M, N, K),
+               std::string(fn) + ": workspace too small");
+    const size_t g = (lq_gemm_w8a8_workspace_size(M, N, K) + 255) & ~(size_t)255;
+    void* tail = static_cast<char*>(d_workspace) + g;
+    const size_t tail_bytes = workspace_bytes - g;
+    int2* parts = static_cast<int2*>(tail);
+    if (dyn_parts_ok(q_dtype, d_y, d_codes, M * N, 1)) {
+        int nparts = 0;
+        const int rc = gemm_entry(false, d_A, lda, d_B, ldb, d_y, N, M, N, K, d_a_scale, a_scale_stride, d_b_scale,
+                                  b_scale_stride, d_a_zero_point, d_b_zero_point, d_b_sums, d_bias, nullptr, nullptr,
+                                  0, 0, LQ_OUT_F32, flags, d_workspace, g, stream, parts, &nparts);
+        if (rc == LQ_OK && nparts >= 1) {
+            const int rq = dyn_quantize_parts(d_y, M * N, q_dtype, qmin, qmax, eps, parts, nparts, d_qparams, d_codes,
+                                              as_stream(stream));
+            if (rq) return rq;
+            note_path("gemm dma with extrema + dynamic quantize");
+            return LQ_OK;
+        }
+        if (rc != GEMM_NO_EXTREMA) return rc;
+    }
+    // the separate calls
+    int rc = gemm_entry(false, d_A, lda, d_B, ldb, d_y, N, M, N, K, d_a_scale, a_scale_stride, d_b_scale,
+                        b_scale_stride, d_a_zero_point, d_b_zero_point, d_b_sums, d_bias, nullptr, nullptr, 0, 0,
+                        LQ_OUT_F32, flags, d_workspace, g, stream);
+    if (rc) return rc;
+    return lq_dynamic_quantize_f32(d_y, M * N, q_dtype, qmin, qmax, eps, d_qparams, d_codes, tail, tail_bytes, stream);
 }
 
 int lq_gemm_w8a8_packed(const int8_t* d_A, int64_t lda, const int8_t* d_B_packed, void* d_C, int64_t ldc,

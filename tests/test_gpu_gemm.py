@@ -408,3 +408,60 @@ def test_gemm_gelu_rejects(gpu):
         run_gemm(gpu, A, B, O.OUT_Q8, out_scale=1.0, flags=_C.EPI_GELU)
     with pytest.raises(_C.LucidError, match="GELU"):
         run_gemm(gpu, A, B, O.OUT_F32, relu=True, flags=_C.EPI_GELU)
+
+
+# ------------------------------------------- product followed by a dynamic input step
+
+
+@pytest.mark.parametrize("M,N,K,gelu,want", [
+    (4096, 2048, 512, True, "gemm dma with extrema + dynamic quantize"),
+    (4096, 4096, 256, False, "gemm dma with extrema + dynamic quantize"),
+    (3000, 1000, 384, True, "gemm dma with extrema + dynamic quantize"),
+    (100, 512, 512, False, "dynamic quantize two-launch"),
+    (4096, 8192, 256, False, "dynamic quantize two-launch"),
+    (512, 1024, 192, True, "dynamic quantize two-launch"),
+])
+def test_gemm_dynamic_quantize_equals_calls(gpu, M, N, K, gelu, want):
+    """lq_gemm_w8a8_dynamic_quantize: the float32 product (unsigned activation codes stored as
+    c - 128, bias, GELU) and the next Linear's input step -- codes and {min, max, scale, zero
+    point} -- bit for bit those of lq_gemm_w8a8 followed by lq_dynamic_quantize_f32.  The DMA
+    kernels fold the extrema in their epilogue (256x128, 256x256 and ragged 128x128 tiles,
+    whose rows and columns past the edge must not count); a skinny M, more than 1024 tiles and
+    K % 128 != 0 take the separate calls."""
+    from lucid_amd import _C
+
+    print(f"gemm dynamic quantize M={M} N={N} K={K} gelu={gelu}", flush=True)
+    rng = np.random.default_rng(M + N + K)
+    A = rng.integers(-128, 128, (M, K)).astype(np.int8)
+    B = rng.integers(-127, 128, (N, K)).astype(np.int8)
+    dA, dB = gpu.tensor(A, device="gpu"), gpu.tensor(B, device="gpu")
+    sa = gpu.tensor(np.array([0.02], np.float32), device="gpu")
+    za = gpu.tensor(np.array([131.0], np.float32), device="gpu")
+    sb = gpu.tensor(rng.uniform(1e-3, 1e-2, N).astype(np.float32), device="gpu")
+    bias = gpu.tensor(rng.standard_normal(N).astype(np.float32), device="gpu")
+    sums = gpu.tensor(B.astype(np.int32).sum(axis=1).astype(np.int32), device="gpu")
+    flags = _C.EPI_A_U8S8 | (_C.EPI_GELU if gelu else 0)
+    eps = np.float32(1e-8)
+    y1, y2 = gpu.empty((M, N), np.float32, "gpu"), gpu.empty((M, N), np.float32, "gpu")
+    c1, c2 = gpu.empty((M * N,), np.int8, "gpu"), gpu.empty((M * N,), np.int8, "gpu")
+    p1, p2 = gpu.empty((4,), np.float32, "gpu"), gpu.empty((4,), np.float32, "gpu")
+    g_n = max(_C.lib().lq_gemm_w8a8_workspace_size(M, N, K), 16)
+    gws = gpu.empty((g_n,), np.uint8, "gpu")
+    _C.call("lq_gemm_w8a8", dA.data_ptr(), K, dB.data_ptr(), K, y1.data_ptr(), N, M, N, K, sa.data_ptr(), 0,
+            sb.data_ptr(), 1, za.data_ptr(), None, sums.data_ptr(), bias.data_ptr(), None, None, 0, 0, _C.OUT_F32,
+            flags, gws.data_ptr(), g_n, None)
+    d_n = max(_C.lib().lq_dynamic_quantize_workspace_size(M * N), 16)
+    dws = gpu.empty((d_n,), np.uint8, "gpu")
+    _C.call("lq_dynamic_quantize_f32", y1.data_ptr(), M * N, _C.U8S8, 0, 255, eps, p1.data_ptr(), c1.data_ptr(),
+            dws.data_ptr(), d_n, None)
+    w_n = _C.lib().lq_gemm_w8a8_dynamic_quantize_workspace_size(M, N, K)
+    ws = gpu.empty((w_n,), np.uint8, "gpu")
+    _C.call("lq_gemm_w8a8_dynamic_quantize", dA.data_ptr(), K, dB.data_ptr(), K, y2.data_ptr(), M, N, K,
+            sa.data_ptr(), 0, sb.data_ptr(), 1, za.data_ptr(), None, sums.data_ptr(), bias.data_ptr(), flags,
+            _C.U8S8, 0, 255, eps, p2.data_ptr(), c2.data_ptr(), ws.data_ptr(), w_n, None)
+    assert _C.last_path() == want  # the separate calls end with lq_dynamic_quantize_f32's own path
+    np.testing.assert_array_equal(y1.numpy().view(np.uint32), y2.numpy().view(np.uint32))
+    np.testing.assert_array_equal(c1.numpy(), c2.numpy())
+    np.testing.assert_array_equal(p1.numpy().view(np.uint32), p2.numpy().view(np.uint32))
+    yv = y2.numpy()
+    np.testing.assert_array_equal(p2.numpy()[:2], np.array([yv.min(), yv.max()], np.float32))
