@@ -495,15 +495,25 @@ int dyn_quantize_parts(const float* x, int64_t n, int q_dtype, int qmin, int qma
                        int nparts, float* qparams, void* q, hipStream_t st);
 
 // Wave64 reductions over int32.
-__device__ __forceinline__ int32_t wave_min(int32_t v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = min(v, __shfl_xor(v, off, 64));
+// The same pairings as ln_wave_sum (quad permutes, row half-mirror and mirror, then the
+// permlane swaps of 16 and 32), with min / max in place of the add: register permutes only,
+// where a shuffle ladder waits on six LDS-crossbar round trips.  Min and max are order-free,
+// so every lane ends with the wave's extremum.
+template <bool MIN>
+__device__ __forceinline__ int32_t wave_extreme(int32_t v) {
+    auto pick = [](int32_t a, int32_t b) { return MIN ? min(a, b) : max(a, b); };
+    v = pick(v, __builtin_amdgcn_update_dpp(v, v, 0xB1, 0xF, 0xF, true));   // quad_perm [1,0,3,2]
+    v = pick(v, __builtin_amdgcn_update_dpp(v, v, 0x4E, 0xF, 0xF, true));   // quad_perm [2,3,0,1]
+    v = pick(v, __builtin_amdgcn_update_dpp(v, v, 0x141, 0xF, 0xF, true));  // row_half_mirror
+    v = pick(v, __builtin_amdgcn_update_dpp(v, v, 0x140, 0xF, 0xF, true));  // row_mirror
+    const int lane = __lane_id();
+    const auto p16 = __builtin_amdgcn_permlane16_swap((uint32_t)v, (uint32_t)v, false, false);
+    v = pick(v, (int32_t)(((lane >> 4) & 1) ? p16[0] : p16[1]));
+    const auto p32 = __builtin_amdgcn_permlane32_swap((uint32_t)v, (uint32_t)v, false, false);
+    v = pick(v, (int32_t)(lane >= 32 ? p32[0] : p32[1]));
     return v;
 }
-__device__ __forceinline__ int32_t wave_max(int32_t v) {
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) v = max(v, __shfl_xor(v, off, 64));
-    return v;
-}
+__device__ __forceinline__ int32_t wave_min(int32_t v) { return wave_extreme<true>(v); }
+__device__ __forceinline__ int32_t wave_max(int32_t v) { return wave_extreme<false>(v); }
 
 }  // namespace lq
