@@ -1034,6 +1034,54 @@ struct DynQuantG4 {
     }
 };
 
+// Per-tensor quantize at mid sizes (up to QUANT_AHEAD_MAX values): at most 1024 workgroups,
+// each lane's first U groups (the launch's groups per lane rounded up to a power of two) read
+// at once, the device scale with them -- one memory round trip where quantize_g4_kernel's
+// 4-8192 workgroups of one group per lane queue in waves of resident workgroups.  Same
+// arithmetic per group (quantize_group4).
+constexpr int64_t QUANT_AHEAD_MAX = (int64_t)1 << 24;
+
+template <class Code, int U>
+__global__ __launch_bounds__(kBlock) void quantize_g4_ahead_kernel(const float* __restrict__ x,
+                                                                   typename Code::T* __restrict__ q, uint32_t n,
+                                                                   QArgs qa, Grid g) {
+    typedef Group4<Code> G;
+    const BlockRun r = block_run(n >> 2);
+    const vf4* x4 = reinterpret_cast<const vf4*>(x);
+    const uint32_t last = (n >> 2) - 1;  // n >= 4 on this path
+    vf4 v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t i = r.i + u * kBlock;
+        v[u] = __builtin_nontemporal_load(&x4[i < last ? i : last]);
+    }
+    float t_inv, t_s, t_z;
+    qa.tensor(t_inv, t_s, t_z);
+    typename G::Raw* q4 = reinterpret_cast<typename G::Raw*>(q);
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t i = r.i + u * kBlock;
+        if (i < r.end) quantize_group4<Code, PT>(q4, i, v[u], qa, g, t_inv, t_s, t_z);
+    }
+    quantize_g4_run<Code, PT>(x, q, n, qa, g, t_inv, t_s, t_z, U);
+}
+
+template <class Code>
+static void launch_quantize_ahead(const float* x, void* q, int64_t n, const QArgs& qa, Grid g, hipStream_t st) {
+    const dim3 grid = dyn_g4_grid(n);
+    auto go = [&](auto u_c) {
+        hipLaunchKernelGGL((quantize_g4_ahead_kernel<Code, decltype(u_c)::value>), grid, dim3(kBlock), 0, st, x,
+                           (typename Code::T*)q, (uint32_t)n, qa, g);
+    };
+    switch (dyn_g4_unroll(n, grid.x)) {
+    case 1: go(std::integral_constant<int, 1>{}); break;
+    case 2: go(std::integral_constant<int, 2>{}); break;
+    case 4: go(std::integral_constant<int, 4>{}); break;
+    case 8: go(std::integral_constant<int, 8>{}); break;
+    default: go(std::integral_constant<int, 16>{}); break;
+    }
+}
+
 // The norm before a dynamic Linear at prefill sizes, with the first half of its input step:
 // each wave normalizes rows (ln_load / ln_norm, or ln_row_wide past 2048 columns: the bits of
 // layer_norm_kernel, x replaced by x + res first when res is given), stores them to y and
@@ -1184,8 +1232,11 @@ struct QuantPt {
         typedef typename Code::T T;
         if (g4_ok<Code>(x, q, n)) {
             QArgs qa{pp.d_scale, pp.d_zp, pp.inv_value, pp.scale_value, pp.zp_value, 1u, 1u};
-            hipLaunchKernelGGL((quantize_g4_kernel<Code, PT>), g4_quant_grid(n), dim3(kBlock), 0, st, x, (T*)q,
-                               (uint32_t)n, qa, g);
+            if (n >= 4 && n <= QUANT_AHEAD_MAX)
+                launch_quantize_ahead<Code>(x, q, n, qa, g, st);
+            else
+                hipLaunchKernelGGL((quantize_g4_kernel<Code, PT>), g4_quant_grid(n), dim3(kBlock), 0, st, x, (T*)q,
+                                   (uint32_t)n, qa, g);
         } else {
             hipLaunchKernelGGL(quantize_pt_kernel<Code>, scalar_grid(n), dim3(kBlock), 0, st, x, (T*)q, n,
                                pp, g, false);
