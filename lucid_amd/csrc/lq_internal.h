@@ -487,8 +487,9 @@ __device__ __forceinline__ void dyn_qparams(int32_t kmin, int32_t kmax, int qmin
 // The second launch of a dynamic quantize whose extrema were folded by the producing kernel:
 // nparts (<= DYN_PARTS_MAX) key pairs [min, max] per workgroup of the producer, then every
 // workgroup folds them, derives the per-tensor qparams of lq_dynamic_quantize_f32 and
-// quantizes x[n] (lq_quant.hip).  dyn_parts_ok: x, q aligned for the four-code groups and
-// n within 32 bits; otherwise the caller runs lq_dynamic_quantize_f32 itself.
+// quantizes x[n] (lq_quant.hip).  dyn_parts_ok: at least one group of four values, x and q
+// aligned for the four-code groups, n within 32 bits; otherwise the caller runs
+// lq_dynamic_quantize_f32 itself.
 constexpr int DYN_PARTS_MAX = 1024;
 bool dyn_parts_ok(int q_dtype, const void* x, const void* q, int64_t n, int nparts);
 int dyn_quantize_parts(const float* x, int64_t n, int q_dtype, int qmin, int qmax, float eps, const int2* parts,

@@ -1344,7 +1344,7 @@ static int check_ocl(int64_t outer, int64_t C, int64_t inner) {
 }
 
 bool dyn_parts_ok(int q_dtype, const void* x, const void* q, int64_t n, int nparts) {
-    return n > 0 && nparts >= 1 && nparts <= DYN_PARTS_MAX && valid_code(q_dtype) && g4_ok_code(q_dtype, x, q, n);
+    return n >= 4 && nparts >= 1 && nparts <= DYN_PARTS_MAX && valid_code(q_dtype) && g4_ok_code(q_dtype, x, q, n);
 }
 
 int dyn_quantize_parts(const float* x, int64_t n, int q_dtype, int qmin, int qmax, float eps, const int2* parts,
@@ -1476,7 +1476,7 @@ int lq_dynamic_quantize_f32(const float* d_x, int64_t n, int q_dtype, int qmin, 
         return dispatch_code<DynQuantSmall>(q_dtype, d_x, n, d_q, d_qparams, qmin, eps, width_f, g, st);
     }
     const int parts = minmax_grid(n) < DYN_PARTS_MAX ? minmax_grid(n) : DYN_PARTS_MAX;
-    if (g4_ok_code(q_dtype, d_x, d_q, n)) {
+    if (n > DYN_SMALL_MAX && g4_ok_code(q_dtype, d_x, d_q, n)) {
         LQ_REQUIRE(d_workspace && workspace_bytes >= sizeof(int2) * (size_t)parts,
                    "lq_dynamic_quantize_f32: workspace too small");
         note_path("dynamic quantize two-launch");

@@ -348,6 +348,21 @@ def test_dynamic_quantize_matches_separate_calls(gpu, n, grid, offset):
     np.testing.assert_array_equal(codes.numpy(), want.astype(np.int8))
 
 
+def test_dynamic_quantize_empty_input(gpu):
+    """n = 0 runs the separate launches (no element is read or written; the two-launch form's
+    read-ahead needs at least one group) and returns without error, as before the two-launch
+    form existed."""
+    from lucid_amd import _C
+
+    qp = gpu.empty((4,), np.float32, "gpu")
+    ws_n = _C.lib().lq_dynamic_quantize_workspace_size(0)
+    ws = gpu.empty((max(ws_n, 16),), np.uint8, "gpu")
+    _C.call("lq_dynamic_quantize_f32", None, 0, _C.U8S8, 0, 255, np.float32(1e-8), qp.data_ptr(), None,
+            ws.data_ptr(), ws_n, None)
+    gpu.synchronize()
+    assert _C.last_path() == "dynamic quantize"
+
+
 def test_dynamic_quantize_edge_ranges(gpu):
     """Zero range (all equal), negative-only, NaN and infinities: the fused launches against the
     separate ones, at one-launch sizes and (tiled past 16384 elements) two-launch sizes."""
