@@ -1160,8 +1160,12 @@ int64_t halo_bytes_for(int64_t N, int64_t C, int64_t H, int64_t W, int64_t Cout,
 
 // Two waves per SIMD (<= 256 registers): the LDS ring leaves room for two workgroups per CU,
 // and their main loops and epilogues overlap.
-template <int BM, int BN, int WAVES_M, int WAVES_N, int NBUF, int KIND, bool NHWC = false>
-__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves_per_eu(2))) void conv_i8_dma_kernel(
+// KSPLIT > 1 (NHWC, one K range per workgroup): KSPLIT groups of WAVES_M x WAVES_N waves, each
+// with its own stage ring, run equal shares of the K stages side by side; the groups' exact
+// int32 tile sums meet in LDS and group 0 runs the epilogue -- the waves of a cross-workgroup
+// split without its second launch.
+template <int BM, int BN, int WAVES_M, int WAVES_N, int NBUF, int KIND, bool NHWC = false, int KSPLIT = 1>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N * KSPLIT) __attribute__((amdgpu_waves_per_eu(2))) void conv_i8_dma_kernel(
     ConvDmaArgs a) {
     constexpr int BK = 128, NW = WAVES_M * WAVES_N, WM = BM / WAVES_M, WN = BN / WAVES_N;
     constexpr int FM = WM / 16, FN = WN / 16;
@@ -1169,19 +1173,25 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves
     static_assert(WM == 64, "a lane owns 16 consecutive pixels of a 64-pixel wave tile");
     static_assert(A_I * 8 * NW == BM && B_I * 8 * NW == BN && WN % 16 == 0, "copy split");
     static_assert(NBUF >= 2 && (NBUF - 1) * LPS < 64, "stage ring");
-    __shared__ __attribute__((aligned(1024))) int8_t lds[NBUF * SB];
+    static_assert(KSPLIT == 1 || NHWC, "the in-workgroup K split serves the NHWC form");
+    static_assert(KSPLIT * NBUF * SB <= 160 * 1024, "LDS budget");
+    __shared__ __attribute__((aligned(1024))) int8_t lds_all[KSPLIT * NBUF * SB];
 
     const int p0 = blockIdx.x * BM, co0 = blockIdx.y * BN;
     const int split = a.phase == 0 ? (int)blockIdx.z % a.splits : 0;
     const int g = a.phase == 0 ? (int)blockIdx.z / a.splits : (int)blockIdx.z;
     const int lane = threadIdx.x & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wave_all = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int kgrp = wave_all / NW;     // this wave's K group (0 when KSPLIT == 1)
+    const int wave = wave_all % NW;     // its wave within the group's tile layout
     const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+    int8_t* const lds = lds_all + kgrp * NBUF * SB;  // the group's stage ring
     const int GCp = a.G * a.Cp;
-    // K stages of this split: [kb, kb + nks)
+    // K stages of this split: [kb, kb + nks); with KSPLIT the group's equal share of them
+    // (the host takes KSPLIT > 1 only when it divides the stage count)
     const int per_split = (a.nk + a.splits - 1) / a.splits;
-    const int kb = split * per_split;
-    const int nks = min(a.nk - kb, per_split);
+    const int kb = split * per_split + kgrp * (min(a.nk - split * per_split, per_split) / KSPLIT);
+    const int nks = min(a.nk - split * per_split, per_split) / KSPLIT;
     // this tile's partial sums: splits x (FN x FM fragments) x (threads) int32x4, thread-minor
     constexpr int NFRAG = FN * FM;
     const int64_t tile_lin = ((int64_t)g * gridDim.y + blockIdx.y) * gridDim.x + blockIdx.x;
@@ -1343,8 +1353,34 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) __attribute__((amdgpu_waves
         // array would cost the second workgroup per CU)
         static_assert(NW * WN * NH_ROW <= NBUF * SB, "NHWC transpose in the stage ring");
         block_barrier();
+        if constexpr (KSPLIT > 1) {
+            // groups 1.. leave their tile sums past group 0's transpose rows; group 0 adds them
+            // (int32 wrap-around: any order gives the same bits) and runs the epilogue
+            constexpr int RED_OFF = (NW * WN * NH_ROW + 1023) / 1024 * 1024;
+            static_assert(RED_OFF + (KSPLIT - 1) * NFRAG * 64 * NW * 16 <= KSPLIT * NBUF * SB, "tile sums in LDS");
+            v4i* red = reinterpret_cast<v4i*>(lds_all + RED_OFF);
+            if (kgrp > 0) {
+#pragma unroll
+                for (int i = 0; i < FN; ++i)
+#pragma unroll
+                    for (int j = 0; j < FM; ++j)
+                        red[(((kgrp - 1) * NFRAG + i * FM + j) * NW + wave) * 64 + lane] = acc[i][j];
+            }
+            block_barrier();
+            if (kgrp > 0) return;  // no barrier follows
+#pragma unroll
+            for (int gq = 1; gq < KSPLIT; ++gq)
+#pragma unroll
+                for (int i = 0; i < FN; ++i)
+#pragma unroll
+                    for (int j = 0; j < FM; ++j) {
+                        const v4i v = red[(((gq - 1) * NFRAG + i * FM + j) * NW + wave) * 64 + lane];
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) acc[i][j][r] = (int)((uint32_t)acc[i][j][r] + (uint32_t)v[r]);
+                    }
+        }
         conv_epilogue<FN, KIND>(a, acc, p0 + wm * 64 + c0 * 16, co0 + wn * WN, g, lane, csb, cbias, cws, sa, ep,
-                                lds + wave * WN * NH_ROW);
+                                lds_all + wave * WN * NH_ROW);
     } else {
         conv_epilogue<FN, KIND>(a, acc, p0 + wm * 64 + c0 * 16, co0 + wn * WN, g, lane, csb, cbias, cws, sa, ep);
     }
@@ -1873,17 +1909,34 @@ int lq_conv2d_i8_nhwc(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, 
     d.m_qmax = merge_qmax;
     d.m_type = merge_type;
     d.m_relu = (merge_flags & LQ_EPI_RELU) ? 1 : 0;
+    // At most 256 tiles of 128 x 64 (at most one per CU): the tile's K stages split between
+    // two or three wave groups of one workgroup (their sums meet in LDS) in place of the
+    // cross-workgroup split and its second launch.  At most 128 such tiles and three groups:
+    // 64 x 64 tiles with three-stage rings (twice the workgroups, a deeper prefetch; the
+    // 144 KiB of LDS still fit one workgroup per CU).
+    const int64_t tiles = plan.gx * plan.gy;
+    const int ksplit = plan.big || tiles > 256 || d.nk < 6 ? 1 : d.nk % 3 == 0 ? 3 : d.nk % 2 == 0 ? 2 : 1;
+    const bool t64 = ksplit == 3 && tiles <= 128;
+    if (ksplit > 1) d.splits = 1;
+    const int splits = d.splits;
     const dim3 grid((unsigned)plan.gx, (unsigned)plan.gy, 1u);
-    const dim3 grid0((unsigned)plan.gx, (unsigned)plan.gy, (unsigned)plan.splits);
+    const dim3 grid0((unsigned)plan.gx, (unsigned)plan.gy, (unsigned)splits);
+    const dim3 grid64((unsigned)((P + 63) / 64), (unsigned)plan.gy, 1u);
     ConvDmaArgs d1 = d;
     d.phase = 0;
     d1.phase = 1;
 #define LQ_CONV_NHWC(K_)                                                                                        \
     if (plan.big) {                                                                                              \
         hipLaunchKernelGGL((conv_i8_dma_kernel<256, 64, 4, 1, 2, K_, true>), grid, dim3(256), 0, st, d);        \
+    } else if (t64) {                                                                                            \
+        hipLaunchKernelGGL((conv_i8_dma_kernel<64, 64, 1, 2, 3, K_, true, 3>), grid64, dim3(384), 0, st, d);    \
+    } else if (ksplit == 3) {                                                                                    \
+        hipLaunchKernelGGL((conv_i8_dma_kernel<128, 64, 2, 2, CV_SMALL_NBUF, K_, true, 3>), grid, dim3(768), 0, st, d); \
+    } else if (ksplit == 2) {                                                                                    \
+        hipLaunchKernelGGL((conv_i8_dma_kernel<128, 64, 2, 2, CV_SMALL_NBUF, K_, true, 2>), grid, dim3(512), 0, st, d); \
     } else {                                                                                                     \
         hipLaunchKernelGGL((conv_i8_dma_kernel<128, 64, 2, 2, CV_SMALL_NBUF, K_, true>), grid0, dim3(256), 0, st, d); \
-        if (plan.splits > 1)                                                                                     \
+        if (splits > 1)                                                                                          \
             hipLaunchKernelGGL((conv_i8_dma_kernel<128, 64, 2, 2, CV_SMALL_NBUF, K_, true>), grid, dim3(256), 0, st, d1); \
     }                                                                                                            \
     break;
@@ -1893,7 +1946,11 @@ int lq_conv2d_i8_nhwc(const int8_t* d_x, int x_code_type, int64_t N, int64_t C, 
         default: LQ_CONV_NHWC(LQ_OUT_QU8S8)
     }
 #undef LQ_CONV_NHWC
-    note_path(plan.big ? "conv nhwc dma 256x64" : plan.splits > 1 ? "conv nhwc dma 128x64 split-k" : "conv nhwc dma 128x64");
+    note_path(plan.big ? "conv nhwc dma 256x64"
+              : t64        ? "conv nhwc dma 64x64 wave-group split-k"
+              : ksplit > 1 ? "conv nhwc dma 128x64 wave-group split-k"
+              : splits > 1 ? "conv nhwc dma 128x64 split-k"
+                           : "conv nhwc dma 128x64");
     return launch_status(fn);
 }
 

@@ -2,8 +2,10 @@
 NHWC (the layout its implicit GEMM reads), output written the same way with its border, and
 the residual add_relu merge fused in -- against the NCHW path it stands for, bit for bit:
 lq_conv2d_i8 on the NCHW codes, then lq_qmerge (LQ_MERGE_ADD, ReLU) with the skip codes.
-Every ResNet-18 layer geometry at batch 2, including the split-K plans of the small late
-layers and a 1 x 1 stride-2 downsample reading a buffer bordered for a 3 x 3 consumer."""
+Every ResNet-18 layer geometry at batch 2 (the small late layers split their K stages between
+three wave groups of one workgroup, on 64 x 64 tiles), two and three groups on 128 x 64 tiles,
+a cross-workgroup split-K plan, and a 1 x 1 stride-2 downsample reading a buffer bordered for a
+3 x 3 consumer."""
 
 from __future__ import annotations
 
@@ -29,6 +31,9 @@ CASES = [  # (C, Cout, H, k, stride, pad, x_pad, residual)
     (64, 64, 56, 3, 1, 1, 1, False), (64, 64, 56, 3, 1, 1, 1, True), (64, 128, 56, 3, 2, 1, 1, False),
     (64, 128, 56, 1, 2, 0, 1, False), (128, 128, 28, 3, 1, 1, 1, True), (256, 256, 14, 3, 1, 1, 1, True),
     (256, 512, 14, 3, 2, 1, 1, False), (512, 512, 7, 3, 1, 1, 1, True), (32, 48, 9, 3, 1, 1, 2, True),
+    # K stages split between two wave groups (8 stages), three groups of 128 x 64 tiles (208
+    # tiles), and a cross-workgroup split (25 stages)
+    (1024, 64, 7, 1, 1, 0, 1, True), (128, 1024, 28, 3, 1, 1, 1, False), (128, 64, 9, 5, 1, 2, 2, True),
 ]
 
 
@@ -84,6 +89,13 @@ def test_nhwc_conv_equals_the_nchw_path(gpu, C, Cout, H, k, stride, pad, x_pad, 
             dzo.data_ptr(), 0, 255, _C.OUT_QU8S8, _C.EPI_RELU if not residual else 0, yp.data_ptr(), y_pad, Cout,
             dskip.data_ptr() if residual else None, _C.U8S8, ss.data_ptr(), dzs.data_ptr(), sm.data_ptr(),
             dzm.data_ptr(), 0, 255, _C.U8S8, _C.EPI_RELU, nw.data_ptr(), nws, None)
+    path = _C.last_path()
+    if (C, k) == (1024, 1) or Cout == 1024:
+        assert path == "conv nhwc dma 128x64 wave-group split-k", path
+    if (C, k) == (512, 3):
+        assert path == "conv nhwc dma 64x64 wave-group split-k", path
+    if (C, k) == (128, 5):
+        assert path == "conv nhwc dma 128x64 split-k", path
     got = yp.numpy()
     np.testing.assert_array_equal(got[:, y_pad:y_pad + OH, y_pad:y_pad + OH, :], want.transpose(0, 2, 3, 1))
     if y_pad:
