@@ -382,7 +382,7 @@ struct DmaTile {
 };
 
 // LDS stage buffers of the DMA main loop (a third buffer measured the same at 4096^3: the
-// copies land within one stage).
+// copies land within one stage; one round of 128x128 tiles takes three).
 constexpr int GEMM_NBUF = 2;
 
 // Scheduling pattern for one K step: R fragment reads (DS) spread over Q MFMAs, each read
@@ -1535,6 +1535,15 @@ struct GemmLaunch {
         const int64_t dma_tiles_128 = ((int64_t)(a.M + 127) / 128) * ((a.N + 127) / 128);
         if (dma_ok && dma_tiles_128 >= 128) {
             if (ext_parts) *ext_parts = (int)dma_tiles_128;
+            // One round of tiles (at most one per CU): the LDS a second workgroup per CU would
+            // use goes to a third ring stage (M = 1024, N = K = 4096: 26.6 -> 20.8 us; a fourth
+            // stage, or the K stages split between two wave groups of 8 waves, no better).
+            if (dma_tiles_128 <= 256) {
+                hipLaunchKernelGGL((gemm_i8_dma_kernel<128, 128, 4, 2, 3, KIND>), dim3((unsigned)dma_tiles_128),
+                                   dim3(512), 0, st, a);
+                note_path("gemm dma 128x128 3-stage");
+                return launch_status("lq_gemm_w8a8 (dma 128x128 3-stage)");
+            }
             hipLaunchKernelGGL((gemm_i8_dma_kernel<128, 128, 4, 2, GEMM_NBUF, KIND>), dim3((unsigned)dma_tiles_128),
                                dim3(512), 0, st, a);
             note_path("gemm dma 128x128");

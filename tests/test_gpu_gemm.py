@@ -147,23 +147,31 @@ def test_int32_accumulator_staged_many_tiles(gpu):
 
 @pytest.mark.parametrize("M,N,K", [(1500, 2900, 256), (2000, 6400, 384), (257, 16384, 128),
                                    (4096, 4100, 128), (1000, 2100, 256), (300, 7000, 128),
-                                   (3900, 8000, 128)])
+                                   (3900, 8000, 128), (1000, 2100, 1024), (1024, 2048, 2048)])
 def test_int32_accumulator_dma_path(gpu, M, N, K):
-    """The LDS-DMA 256x128 and 256x256 paths (K % 128 == 0, >= 128 / 256 tiles) with ragged M
-    and N: rows past M or N come in as zeros through the buffer bounds and are never stored."""
+    """The LDS-DMA 256x256, 256x128 and 128x128 paths (K % 128 == 0, >= 128 / 256 tiles; one
+    round of 128x128 tiles with a three-stage ring) with ragged M and N: rows past M or N come
+    in as zeros through the buffer bounds and are never stored."""
     rng = np.random.default_rng(M + N + K)
     A = _codes(rng, (M, K), -128, 127)
     B = _codes(rng, (N, K), -128, 127)
     print(f"gemm dma acc M={M} N={N} K={K}", flush=True)
     C = run_gemm(gpu, A, B)
+    from lucid_amd import _C
+
+    want = {(1000, 2100, 256): "gemm dma 128x128 3-stage", (1000, 2100, 1024): "gemm dma 128x128 3-stage",
+            (1024, 2048, 2048): "gemm dma 128x128 3-stage", (1500, 2900, 256): "gemm dma 128x128"}
+    if (M, N, K) in want:
+        assert _C.last_path() == want[M, N, K]
     np.testing.assert_array_equal(C, O.gemm_acc(A, B))
 
 
+@pytest.mark.parametrize("M,N,K", [(600, 8200, 128), (1000, 2100, 1024)])
 @pytest.mark.parametrize("kind", KINDS)
-def test_epilogue_kinds_dma_path(gpu, kind):
-    """Every output kind through the LDS-staged epilogue of the DMA path (ragged N)."""
+def test_epilogue_kinds_dma_path(gpu, kind, M, N, K):
+    """Every output kind through the LDS-staged epilogue of the DMA path (ragged N; the second
+    shape is one round of 128x128 tiles with a three-stage ring, ragged M too)."""
     rng = np.random.default_rng(1000 + kind)
-    M, N, K = 600, 8200, 128
     A = _codes(rng, (M, K), -128, 127)
     B = _codes(rng, (N, K), -127, 127)
     a_scale = rng.uniform(1e-3, 1e-1, M).astype(np.float32)

@@ -107,7 +107,7 @@ def test_gemm_headline_4096_full_exact(gpu):
 
 @pytest.mark.parametrize("M,N,K,path", [(4096, 11008, 4096, "gemm dma 256x256"),
                                         (4096, 4096, 11008, "gemm dma 256x256"),
-                                        (1024, 4096, 4096, "gemm dma 128x128")])
+                                        (1024, 4096, 4096, "gemm dma 128x128 3-stage")])
 def test_gemm_sweep_shapes_exact(gpu, M, N, K, path):
     """The sweep's large shapes: 64 sampled rows in full (4096-row shapes), every row at
     M = 1024; int8 and f16 outputs."""
