@@ -704,6 +704,27 @@ __device__ __forceinline__ void conv_epilogue(const ConvDmaArgs& a, v4i (&acc)[F
             minv = 1.0f / mscale;
             mg = make_grid(a.m_qmin, a.m_qmax);
         }
+        // The network's form (quint8 conv output, skip and merge, ReLU) with every scalar finite,
+        // the merge zero point integral and |t * minv| below 2^21 for every t the codes can give:
+        // the merge's requantize as one magic add and a med3 on the bits, as in the integer
+        // epilogue (ReLU folded into the lower bound), then the shift to the stored c - 128 --
+        // the same codes as quant_store.  (The shift stays a separate add: folded into the
+        // rounding constant, an odd shift would move the ties-to-even.)
+        bool fastm = false;
+        int32_t mLm = 0, mHm = 0, mshift = 0;
+        if (merge && OT == LQ_U8S8 && a.skip_type == LQ_U8S8 && a.m_type == LQ_U8S8 && a.m_relu) {
+            const float bound = ((255.0f + __builtin_fabsf(ep.out_z)) * __builtin_fabsf(ep.out_s) +
+                                 (255.0f + __builtin_fabsf(zs)) * __builtin_fabsf(ss)) * minv;
+            fastm = minv > 0.0f && bound < 2097152.0f && mz == __builtin_rintf(mz) && __builtin_fabsf(mz) < 1048576.0f;
+            if (fastm) {
+                const int mzi = (int)mz;
+                const int lo = min(max(mg.qlo, 0), 255), hi = max(min(mg.qhi, 255), 0);
+                const int H = hi - mzi, L = min(max(lo - mzi, 0), H);
+                mshift = mzi - 128;
+                mLm = RNE_MAGIC_BITS + L;
+                mHm = RNE_MAGIC_BITS + H;
+            }
+        }
         const uint32_t zc = merge ? nhwc_zero_code(mz, a.m_type) : nhwc_zero_code(ep.out_z, OT);
         const v4i zc16 = v4i{(int)(zc * 0x01010101u), (int)(zc * 0x01010101u), (int)(zc * 0x01010101u),
                              (int)(zc * 0x01010101u)};
@@ -736,7 +757,22 @@ __device__ __forceinline__ void conv_epilogue(const ConvDmaArgs& a, v4i (&acc)[F
                         w[d] = o;
                     }
                 };
-                if (a.skip_type == LQ_U8S8 && a.m_type == LQ_U8S8 && a.m_relu)
+                if (fastm) {
+#pragma unroll
+                    for (int d = 0; d < 4; ++d) {
+                        // codes c of both operands: the stored bytes c - 128 with the top bit flipped
+                        const uint32_t wa = w[d] ^ 0x80808080u, wb = (uint32_t)sk[k][d] ^ 0x80808080u;
+                        uint32_t o[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float av = ((float)((wa >> (8 * e)) & 0xffu) - ep.out_z) * ep.out_s;
+                            const float bv = ((float)((wb >> (8 * e)) & 0xffu) - zs) * ss;
+                            const float t = av + bv;
+                            o[e] = (uint32_t)(med3_i32(rne_bits(t * minv), mLm, mHm) + mshift);
+                        }
+                        w[d] = pack_low_bytes(o);
+                    }
+                } else if (a.skip_type == LQ_U8S8 && a.m_type == LQ_U8S8 && a.m_relu)
                     merge16(std::integral_constant<int, LQ_U8S8>{}, std::integral_constant<int, LQ_U8S8>{},
                             std::integral_constant<int, 1>{});
                 else

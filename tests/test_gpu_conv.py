@@ -189,6 +189,27 @@ def test_conv_halo_exact(gpu, case, kind):
         _check(got, want, kind)
 
 
+@pytest.mark.parametrize("case", [(2, 64, 16, 16, 64, 3, 3, (1, 1, 1, 1)), (2, 64, 14, 14, 128, 3, 3, (1, 1, 1, 1)),
+                                  (2, 256, 7, 7, 256, 3, 3, (1, 1, 1, 1))])
+@pytest.mark.parametrize("kind", [O.OUT_QU8S8, O.OUT_Q8, O.OUT_QU8])
+def test_conv_epilogue_ties_exact(gpu, case, kind):
+    # power-of-two scales, no bias and small codes put half the outputs on exact halves (ties
+    # of the round-to-nearest-even) with an odd output zero point; the halo kernel, the 128 x 64
+    # LDS-DMA tile and its split-K form against the oracle
+    N, C, H, W, Cout, KH, KW, pad = case
+    rng = np.random.default_rng(N * 1000 + C + H + Cout + kind + 17)
+    x = _codes(rng, (N, C, H, W), -3, 3)
+    w = _codes(rng, (Cout, C, KH, KW), -2, 2)
+    qmin, qmax = GRID.get(kind, (-128, 127))
+    zp = 127.0 if qmin == 0 else 3.0
+    kw = dict(stride=(1, 1), pad=pad, w_scale=np.ones(Cout, np.float32), out_kind=kind, qmin=qmin, qmax=qmax,
+              out_zp=zp, bias=None, a_scale=0.5, out_scale=1.0)
+    print(f"conv ties {case} kind={kind}", flush=True)
+    got = run_conv(gpu, x, w, **kw)
+    want = oracle_conv(x, w, **kw)
+    _check(got, want, kind)
+
+
 def test_conv_halo_declines(gpu):
     # shapes outside the halo kernel's reach keep the packed-input kernels
     from lucid_amd import _C

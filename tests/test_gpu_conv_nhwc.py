@@ -37,25 +37,42 @@ CASES = [  # (C, Cout, H, k, stride, pad, x_pad, residual)
 ]
 
 
-@pytest.mark.parametrize("C,Cout,H,k,stride,pad,x_pad,residual", CASES)
+# Power-of-two scales and small codes: the convolution's outputs and the merge's sums land on
+# exact halves (ties of the round-to-nearest-even), with odd zero points.
+TIE_CASES = [(64, 64, 56, 3, 1, 1, 1, True, True), (128, 128, 28, 3, 1, 1, 1, True, True),
+             (512, 512, 7, 3, 1, 1, 1, True, True)]
+
+
+@pytest.mark.parametrize("C,Cout,H,k,stride,pad,x_pad,residual,ties", [c + (False,) for c in CASES] + TIE_CASES)
 @pytest.mark.parametrize("y_pad", [1, 0])
-def test_nhwc_conv_equals_the_nchw_path(gpu, C, Cout, H, k, stride, pad, x_pad, residual, y_pad):
+def test_nhwc_conv_equals_the_nchw_path(gpu, C, Cout, H, k, stride, pad, x_pad, residual, ties, y_pad):
     from lucid_amd import _C
 
     lib = _C.lib()
-    rng = np.random.default_rng(C + 7 * Cout + H + k + 3 * residual)
+    rng = np.random.default_rng(C + 7 * Cout + H + k + 3 * residual + 5 * ties)
     N = 2
-    za, zo, zs, zm = 121.0, 9.0, 133.0, 4.0
-    x = rng.integers(-128, 128, (N, C, H, H)).astype(np.int8)  # U8S8: code c stored as c - 128
-    w = rng.integers(-127, 128, (Cout, C, k, k)).astype(np.int8)
+    za, zo, zs, zm = (121.0, 9.0, 133.0, 5.0) if ties else (121.0, 9.0, 133.0, 4.0)
+    if ties:
+        x = rng.integers(-9, -4, (N, C, H, H)).astype(np.int8)  # codes 119..123 about za
+        w = rng.integers(-2, 3, (Cout, C, k, k)).astype(np.int8)
+    else:
+        x = rng.integers(-128, 128, (N, C, H, H)).astype(np.int8)  # U8S8: code c stored as c - 128
+        w = rng.integers(-127, 128, (Cout, C, k, k)).astype(np.int8)
+    print(f"nhwc conv C={C} Cout={Cout} H={H} k={k} s={stride} residual={residual} ties={ties} y_pad={y_pad}",
+          flush=True)
     dw = _d(gpu, w)
     wp = gpu.empty((lib.lq_conv2d_weight_pack_size(Cout, C, k, k),), np.int8, "gpu")
     sums = gpu.empty((Cout,), np.int32, "gpu")
     _C.call("lq_conv2d_pack_weights_i8", dw.data_ptr(), Cout, C, k, k, wp.data_ptr(), sums.data_ptr(), None)
-    sa, sw = _d(gpu, np.float32(0.02)), _d(gpu, rng.uniform(2e-4, 2e-3, Cout).astype(np.float32))
+    if ties:
+        sa, sw = _d(gpu, np.float32(0.5)), _d(gpu, np.ones(Cout, np.float32))
+        bias = _d(gpu, np.zeros(Cout, np.float32))
+        so = _d(gpu, np.float32(1.0))
+    else:
+        sa, sw = _d(gpu, np.float32(0.02)), _d(gpu, rng.uniform(2e-4, 2e-3, Cout).astype(np.float32))
+        bias = _d(gpu, (rng.standard_normal(Cout) * 0.3).astype(np.float32))
+        so = _d(gpu, np.float32(0.03))
     dza, dzo = _d(gpu, np.float32(za)), _d(gpu, np.float32(zo))
-    bias = _d(gpu, (rng.standard_normal(Cout) * 0.3).astype(np.float32))
-    so = _d(gpu, np.float32(0.03))
     OH = (H + 2 * pad - k) // stride + 1
     # the NCHW path
     dx = _d(gpu, x)
@@ -68,7 +85,8 @@ def test_nhwc_conv_equals_the_nchw_path(gpu, C, Cout, H, k, stride, pad, x_pad, 
             ws.data_ptr(), ws_n, None)
     want = y_ref.numpy()
     skip = rng.integers(-128, 128, (N, Cout, OH, OH)).astype(np.int8)
-    ss, sm = _d(gpu, np.float32(0.025)), _d(gpu, np.float32(0.04))
+    ss, sm = (_d(gpu, np.float32(0.5)), _d(gpu, np.float32(1.0))) if ties else \
+        (_d(gpu, np.float32(0.025)), _d(gpu, np.float32(0.04)))
     dzs, dzm = _d(gpu, np.float32(zs)), _d(gpu, np.float32(zm))
     if residual:
         merged = gpu.empty((N * Cout * OH * OH,), np.int8, "gpu")
