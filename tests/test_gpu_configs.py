@@ -204,6 +204,86 @@ def test_resnet18_config5_block_exact(gpu, resnet_pipeline):
     np.testing.assert_array_equal(y.quant_source.codes.numpy(), want)
 
 
+def test_resnet18_config5_network_vs_oracle(gpu, resnet_pipeline):
+    # The whole converted network at batch 2 against the oracle's composition run end to end on
+    # its own outputs (no device value feeds it): the input codes, the stem, the max pool and
+    # every block's output codes bit for bit, the global average pool's float32 bits, then the
+    # fc (a float weight-only product, within its scale-aware tolerance, so its codes may move
+    # by one where a value sits on a rounding boundary) and the dequantized logits.
+    from tests.test_gpu_conv import oracle_conv
+
+    rng, _, q = resnet_pipeline
+    x = rng.standard_normal((2, 3, 224, 224)).astype(np.float32)
+
+    def grid(mod):
+        return np.float32(mod.scale.numpy().reshape(-1)[0]), np.float32(mod.zero_point.numpy().reshape(-1)[0])
+
+    def codes_of(t):
+        assert t.is_code_backed
+        return t.quant_source.codes.numpy()
+
+    def conv(mod, c, s, z, relu, pad, stride):
+        assert not mod.weight_zero_point.numpy().any()
+        so, zo = grid(mod)
+        out = oracle_conv(c, mod.weight_int8.numpy(), u8s8=True, za=float(z), stride=stride, pad=pad,
+                          a_scale=s, w_scale=mod.weight_scale.numpy(),
+                          bias=mod.bias.numpy() if mod.bias is not None else None, out_kind=O.OUT_QU8S8,
+                          out_scale=float(so), out_zp=float(zo), qmin=0, qmax=255, relu=relu)
+        return out, so, zo
+
+    # device forward, module by module (the forward's own sequence)
+    h = q.quant(_dev(gpu, x))
+    dev = {"quant": codes_of(h)}
+    h = q.conv1(h)
+    dev["conv1"] = codes_of(h)
+    h = q.maxpool(h)
+    dev["maxpool"] = codes_of(h)
+    blocks = [getattr(q, f"layer{i}")[j] for i in range(1, 5) for j in range(2)]
+    for n, blk in enumerate(blocks):
+        h = blk(h)
+        dev[f"block{n}"] = codes_of(h)
+    pooled_dev = q.avgpool(h)
+    fc_dev = q.fc(q.flatten(pooled_dev))
+    logits_dev = q.dequant(fc_dev).numpy()
+
+    # the oracle's chain
+    s0, z0 = grid(q.quant)
+    c = O.quantize(x, O.recip_tensor(np.atleast_1d(s0))[0], z0, 0, 255, O.U8S8)
+    np.testing.assert_array_equal(dev["quant"], c)
+    c, s, z = conv(q.conv1, c, s0, z0, True, (3, 3, 3, 3), (2, 2))
+    np.testing.assert_array_equal(dev["conv1"], c)
+    c = O.pool2d(c.astype(np.float32), "max", kernel=(3, 3), stride=(2, 2), pad=(1, 1)).astype(np.int8)
+    np.testing.assert_array_equal(dev["maxpool"], c)
+    for n, blk in enumerate(blocks):
+        st = tuple(blk.conv1.stride)
+        a, sa, za = conv(blk.conv1, c, s, z, True, (1, 1, 1, 1), st)
+        b, sb, zb = conv(blk.conv2, a, sa, za, False, (1, 1, 1, 1), (1, 1))
+        if blk.downsample is not None:
+            d, sd, zd = conv(blk.downsample[0], c, s, z, False, (0, 0, 0, 0), st)
+        else:
+            d, sd, zd = c, s, z
+        t = (O.dequantize(b, O.U8S8, sb, zb) + O.dequantize(d, O.U8S8, sd, zd)).astype(np.float32)
+        t = np.where(t <= 0, np.float32(0), t).astype(np.float32)
+        s, z = grid(blk.skip)
+        c = O.quantize(t, O.recip_tensor(np.atleast_1d(s))[0], z, 0, 255, O.U8S8)
+        np.testing.assert_array_equal(dev[f"block{n}"], c, err_msg=f"block {n}")
+    pooled = O.pool2d(O.dequantize(c, O.U8S8, s, z), "avg", adaptive=(1, 1))
+    np.testing.assert_array_equal(pooled_dev.numpy().view(np.uint32), pooled.view(np.uint32))
+    fc = q.fc
+    assert not fc.weight_zero_point.numpy().any()
+    y = O.gemv_w8(pooled.reshape(2, -1), fc.weight_int8.numpy(), fc.weight_scale.numpy(), None,
+                  fc.bias.numpy() if fc.bias is not None else None)
+    sf, zf = grid(fc)
+    lo, hi = fc.out_qdtype.quant_min, fc.out_qdtype.quant_max
+    ct = O.U8S8 if lo >= 0 else O.I8
+    want = O.quantize(y.astype(np.float32), O.recip_tensor(np.atleast_1d(sf))[0], zf, lo, hi, ct)
+    got = codes_of(fc_dev)
+    diff = got.astype(np.int32) - want.astype(np.int32)
+    print(f"fc codes off by one: {np.count_nonzero(diff)} of {diff.size}", flush=True)
+    assert np.abs(diff).max() <= 1 and np.count_nonzero(diff) <= diff.size // 1000 + 1
+    np.testing.assert_array_equal(logits_dev.view(np.uint32), O.dequantize(got, ct, sf, zf).view(np.uint32))
+
+
 def test_resnet18_config5_vs_float(gpu, resnet_pipeline):
     # the quantized network against its float original (BN folded) on a fresh batch of the
     # config's shape: a measured agreement, not a parity claim (int8 noise accumulates over
