@@ -121,6 +121,9 @@ CASES = [
     (1, 3, 9, 9, 5, 3, 7, (1, 1), (1, 1, 3, 3), (1, 1), 1, 3),          # circular, 21 taps x channels
     (1, 3, 5, 300, 8, 3, 3, (1, 2), (1, 1, 1, 1), (1, 1), 1, 0),        # 150 output columns: two blocks
     (3, 3, 1, 40, 12, 1, 5, (1, 1), (0, 0, 2, 2), (1, 1), 1, 0),        # a 1-D conv (height 1)
+    (1, 6, 8, 16, 8, 3, 3, (1, 1), (1, 1, 1, 1), (1, 1), 2, 0),         # Cg 3, two groups, zeros
+    (1, 2, 12, 32, 16, 5, 9, (2, 3), (2, 2, 4, 4), (1, 2), 1, 0),       # Cg 2, dilated row, zeros
+    (2, 3, 20, 260, 8, 7, 7, (2, 2), (3, 3, 3, 3), (1, 1), 1, 0),       # stem, 130 columns: two blocks
 ]
 
 
