@@ -403,29 +403,36 @@ __global__ __launch_bounds__(256) void maxpool_nhwc_kernel(MaxNhwc2Args a) {
 // y[n][c] = (sum over h, then w, of fl32(fl32(float(code) - z) s)) / (H W): the adaptive
 // average pool to 1 x 1 (lq_pool2d's order and rounding) from the padded NHWC layout.  One
 // thread per (n, c): consecutive threads read consecutive channel bytes of a pixel.
+// One thread per (n, c), 64 per workgroup (N C / 64 workgroups: 256 for ResNet-18 at batch 32,
+// one per CU, where 256-thread workgroups left three quarters of the CUs idle).
+constexpr int AVG_NHWC_THREADS = 64;
+constexpr int AVG_NHWC_BATCH = 64;  // pixel loads in flight per thread (7 x 7 in one round trip)
 template <int T>
-__global__ __launch_bounds__(256) void avgpool_global_nhwc_kernel(const int8_t* __restrict__ x, int64_t N, int C,
-                                                                  int H, int W, int xpad, int xcs, const float* scale,
-                                                                  const float* zp, float* __restrict__ y) {
-    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+__global__ __launch_bounds__(AVG_NHWC_THREADS) void avgpool_global_nhwc_kernel(const int8_t* __restrict__ x,
+                                                                               int64_t N, int C, int H, int W,
+                                                                               int xpad, int xcs, const float* scale,
+                                                                               const float* zp,
+                                                                               float* __restrict__ y) {
+    const int64_t i = (int64_t)blockIdx.x * AVG_NHWC_THREADS + threadIdx.x;
     if (i >= N * C) return;
     const int64_t n = i / C;
     const int c = (int)(i - n * C);
     const float s = scale[0], z = zp ? zp[0] : 0.0f;
     const int64_t wp = W + 2 * xpad;
     const int8_t* base = x + ((n * (H + 2 * xpad) + xpad) * wp + xpad) * xcs + c;
-    // the pixels' bytes in batches of 16 loads, then added in (h, w) order
+    // the pixels' bytes in batches of AVG_NHWC_BATCH loads, then added in (h, w) order
     float sum = 0.0f;
     const int HW = H * W;
-    for (int k0 = 0; k0 < HW; k0 += 16) {
-        int8_t b[16];
+    for (int k0 = 0; k0 < HW; k0 += AVG_NHWC_BATCH) {
+        int8_t b[AVG_NHWC_BATCH];
+        int h = k0 / W, w = k0 - h * W;  // pixel k0 + u, advanced without a division per load
 #pragma unroll
-        for (int u = 0; u < 16; ++u) {
-            const int k = min(k0 + u, HW - 1), h = k / W, w = k - h * W;
-            b[u] = base[((int64_t)h * wp + w) * xcs];
+        for (int u = 0; u < AVG_NHWC_BATCH; ++u) {
+            b[u] = base[((int64_t)min(h, H - 1) * wp + w) * xcs];
+            if (++w == W) w = 0, ++h;
         }
 #pragma unroll
-        for (int u = 0; u < 16; ++u)
+        for (int u = 0; u < AVG_NHWC_BATCH; ++u)
             if (k0 + u < HW) {
                 const float cv = T == LQ_U8S8 ? (float)((int)b[u] + 128) : T == LQ_U8 ? (float)(uint8_t)b[u] : (float)b[u];
                 const float d = cv - z;
@@ -563,9 +570,10 @@ int lq_avgpool2d_global_nhwc(const int8_t* d_x, int x_type, const float* d_scale
                std::string(fn) + ": bad shape");
     if (N == 0) return LQ_OK;
     LQ_REQUIRE(d_x && d_y && d_scale, std::string(fn) + ": NULL pointer");
-    const dim3 grid((unsigned)((N * C + 255) / 256));
+    const dim3 grid((unsigned)((N * C + AVG_NHWC_THREADS - 1) / AVG_NHWC_THREADS));
     const hipStream_t st = as_stream(stream);
-#define LQ_AVG_NHWC(T_) hipLaunchKernelGGL(avgpool_global_nhwc_kernel<T_>, grid, dim3(256), 0, st, d_x, N, (int)C, \
+#define LQ_AVG_NHWC(T_) hipLaunchKernelGGL(avgpool_global_nhwc_kernel<T_>, grid, dim3(AVG_NHWC_THREADS), 0, st, d_x, \
+                                           N, (int)C, \
                                            (int)H, (int)W, x_pad, (int)x_cs, d_scale, d_zero_point, d_y)
     if (x_type == LQ_I8) LQ_AVG_NHWC(LQ_I8);
     else if (x_type == LQ_U8) LQ_AVG_NHWC(LQ_U8);
