@@ -1537,7 +1537,17 @@ struct GemmLaunch {
             if (ext_parts) *ext_parts = (int)dma_tiles_128;
             // One round of tiles (at most one per CU): the LDS a second workgroup per CU would
             // use goes to a third ring stage (M = 1024, N = K = 4096: 26.6 -> 20.8 us; a fourth
-            // stage, or the K stages split between two wave groups of 8 waves, no better).
+            // stage, or the K stages split between two wave groups of 8 waves, no better).  At
+            // most half a round: 128x64 tiles of four waves with four-stage rings, twice the
+            // workgroups (M = 512, N = K = 4096: 16.7 -> 14.3 us).
+            if (dma_tiles_128 <= 128) {
+                const int64_t tiles64 = ((int64_t)(a.M + 127) / 128) * ((a.N + 63) / 64);
+                if (ext_parts) *ext_parts = (int)tiles64;
+                hipLaunchKernelGGL((gemm_i8_dma_kernel<128, 64, 4, 1, 4, KIND>), dim3((unsigned)tiles64),
+                                   dim3(256), 0, st, a);
+                note_path("gemm dma 128x64");
+                return launch_status("lq_gemm_w8a8 (dma 128x64)");
+            }
             if (dma_tiles_128 <= 256) {
                 hipLaunchKernelGGL((gemm_i8_dma_kernel<128, 128, 4, 2, 3, KIND>), dim3((unsigned)dma_tiles_128),
                                    dim3(512), 0, st, a);

@@ -147,11 +147,12 @@ def test_int32_accumulator_staged_many_tiles(gpu):
 
 @pytest.mark.parametrize("M,N,K", [(1500, 2900, 256), (2000, 6400, 384), (257, 16384, 128),
                                    (4096, 4100, 128), (1000, 2100, 256), (300, 7000, 128),
-                                   (3900, 8000, 128), (1000, 2100, 1024), (1024, 2048, 2048)])
+                                   (3900, 8000, 128), (1000, 2100, 1024), (1024, 2048, 2048), (512, 4096, 1024),
+                                   (500, 4000, 256)])
 def test_int32_accumulator_dma_path(gpu, M, N, K):
-    """The LDS-DMA 256x256, 256x128 and 128x128 paths (K % 128 == 0, >= 128 / 256 tiles; one
-    round of 128x128 tiles with a three-stage ring) with ragged M and N: rows past M or N come
-    in as zeros through the buffer bounds and are never stored."""
+    """The LDS-DMA 256x256, 256x128, 128x128 and 128x64 paths (K % 128 == 0, >= 128 / 256 tiles;
+    one round of 128x128 tiles with a three-stage ring, half a round as 128x64 tiles) with ragged
+    M and N: rows past M or N come in as zeros through the buffer bounds and are never stored."""
     rng = np.random.default_rng(M + N + K)
     A = _codes(rng, (M, K), -128, 127)
     B = _codes(rng, (N, K), -128, 127)
@@ -160,13 +161,14 @@ def test_int32_accumulator_dma_path(gpu, M, N, K):
     from lucid_amd import _C
 
     want = {(1000, 2100, 256): "gemm dma 128x128 3-stage", (1000, 2100, 1024): "gemm dma 128x128 3-stage",
-            (1024, 2048, 2048): "gemm dma 128x128 3-stage", (1500, 2900, 256): "gemm dma 128x128"}
+            (1024, 2048, 2048): "gemm dma 128x64", (1500, 2900, 256): "gemm dma 128x128",
+            (512, 4096, 1024): "gemm dma 128x64", (500, 4000, 256): "gemm dma 128x64"}
     if (M, N, K) in want:
         assert _C.last_path() == want[M, N, K]
     np.testing.assert_array_equal(C, O.gemm_acc(A, B))
 
 
-@pytest.mark.parametrize("M,N,K", [(600, 8200, 128), (1000, 2100, 1024)])
+@pytest.mark.parametrize("M,N,K", [(600, 8200, 128), (1000, 2100, 1024), (500, 4000, 256)])
 @pytest.mark.parametrize("kind", KINDS)
 def test_epilogue_kinds_dma_path(gpu, kind, M, N, K):
     """Every output kind through the LDS-staged epilogue of the DMA path (ragged N; the second
@@ -425,6 +427,7 @@ def test_gemm_gelu_rejects(gpu):
     (4096, 2048, 512, True, "gemm dma with extrema + dynamic quantize"),
     (4096, 4096, 256, False, "gemm dma with extrema + dynamic quantize"),
     (3000, 1000, 384, True, "gemm dma with extrema + dynamic quantize"),
+    (500, 4000, 256, False, "gemm dma with extrema + dynamic quantize"),
     (100, 512, 512, False, "dynamic quantize two-launch"),
     (4096, 8192, 256, False, "dynamic quantize two-launch"),
     (512, 1024, 192, True, "dynamic quantize two-launch"),
