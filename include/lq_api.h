@@ -729,7 +729,9 @@ int lq_layer_norm_f32(const float* d_x, int64_t ldx, float* d_y, int64_t ldy, in
 int lq_add_layer_norm_f32(float* d_x, int64_t ldx, const float* d_res, int64_t ldres, float* d_y, int64_t ldy,
                           int64_t rows, int64_t D, const float* d_gamma, const float* d_beta, float eps,
                           void* stream);
-/* y = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) (F.gelu, approximate="tanh"). */
+/* y = 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) (F.gelu, approximate="tanh"), evaluated as
+ * x / (1 + exp(-2 sqrt(2/pi) (x + 0.044715 x^3))) with the hardware exp2 and reciprocal (the same
+ * function, within a few float32 ulps). */
 int lq_gelu_tanh_f32(const float* d_x, float* d_y, int64_t n, void* stream);
 /* y = a + b elementwise (residual adds). */
 int lq_add_f32(const float* d_a, const float* d_b, float* d_y, int64_t n, void* stream);

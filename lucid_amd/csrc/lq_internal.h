@@ -102,12 +102,15 @@ __device__ __forceinline__ float round_result_to(float v, int mode) {
     return round_to(v, mode);
 }
 
-// gelu, tanh form: 0.5 x (1 + tanh(sqrt(2/pi) (x + 0.044715 x^3))) (F.gelu(approximate="tanh")),
-// one float32 rounding per operation in this order; shared so a fused kernel gives the same
-// bits as the standalone one.
+// gelu, tanh form: 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3) (F.gelu(approximate=
+// "tanh")), evaluated as x / (1 + e^{-2u}) -- the same function (1 + tanh u = 2 / (1 + e^{-2u}))
+// without the cancellation of 1 + tanh u where tanh u is near -1 -- with the hardware exp2 and
+// reciprocal (a few ulps; tanhf's libm call was most of a GELU epilogue's VALU work).  Shared
+// so a fused kernel gives the same bits as the standalone one.
 __device__ __forceinline__ float gelu_tanh_f32(float v) {
     const float u = 0.7978845608f * (v + 0.044715f * v * v * v);
-    return 0.5f * v * (1.0f + tanhf(u));
+    const float e = __builtin_amdgcn_exp2f(-2.8853900817779268f * u);  // e^{-2u} = 2^{-2u log2 e}
+    return v * __builtin_amdgcn_rcpf(1.0f + e);
 }
 
 // Layer norm of one row by one wave (LN_T lanes), in one fixed order shared by every kernel
